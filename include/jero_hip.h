@@ -1,0 +1,95 @@
+/*
+ * jero_hip.h -- C ABI of libjero_hip.so, the MI355X (gfx950) implementation of
+ * jero-engine's quantized-matmul hot path.
+ *
+ * The reference's hot path is the jero_kernels_rvv Rust API called by the recipes
+ * (src/gemma.rs:66-138, src/qwen_deepseek.rs:643-951, src/forward.rs:763-811).  Each entry
+ * point below names the reference interface it replaces.  All pointers named *_dev are
+ * device pointers; `stream` is a hipStream_t (NULL = the null stream).  Work is enqueued on
+ * the stream and the call returns; argument errors are reported before anything is enqueued.
+ *
+ * Status codes mirror the K3Error variants with the numbers the reference's CLI maps them
+ * to (src/bin/jero-diag/main.rs:595-605); JERO_ERR_DEVICE and JERO_ERR_INVALID_ARGUMENT have
+ * no K3Error counterpart (HIP runtime failure, null pointer).
+ */
+#ifndef JERO_HIP_H
+#define JERO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum jero_status {
+  JERO_OK = 0,
+  JERO_ERR_CAPABILITY_MISMATCH = 10, /* K3Error::CapabilityMismatch: unsupported quant / shape */
+  JERO_ERR_INSUFFICIENT_MEMORY = 11, /* K3Error::InsufficientLockableMemory: device allocation */
+  JERO_ERR_CONTEXT_LENGTH_EXCEEDED = 12, /* K3Error::ContextLengthExceeded */
+  JERO_ERR_TENSOR_BOUNDS = 14,       /* K3Error::TensorBoundsError: byte/shape mismatch, empty */
+  JERO_ERR_ROUTING_UNAVAILABLE = 15, /* K3Error::RoutingUnavailable: no expert selectable */
+  JERO_ERR_DEVICE = 20,              /* HIP runtime error */
+  JERO_ERR_INVALID_ARGUMENT = 21     /* null pointer or nonsensical argument */
+} jero_status;
+
+/* Quantization ids: GGUF/ggml type ids, plus the activation block formats. */
+typedef enum jero_quant {
+  JERO_F32 = 0,
+  JERO_F16 = 1,
+  JERO_Q4_0 = 2,
+  JERO_Q8_0 = 8,
+  JERO_Q4_K = 12, /* the reference's QuantType::Q4_K_M */
+  JERO_Q6_K = 14,
+  JERO_Q8_K = 15,  /* activation blocks for Q4_K / Q6_K weights: f32 d, i8 q[256], i16 bsums[16] */
+  JERO_ACT_Q8 = 100 /* activation blocks for Q8_0 / Q4_0 weights: f32 d, i8 q[32] (36 B) */
+} jero_quant;
+
+/* ---- runtime ---- */
+
+/* Selects the device for the calling thread and prepares per-device state. */
+int jero_hip_init(int device);
+/* Text of the last error raised on the calling thread ("" if none). */
+const char *jero_hip_last_error(void);
+const char *jero_hip_status_name(int status);
+/* Bytes of one row of n elements in `quant` (-1 if n is not a multiple of the block). */
+int64_t jero_hip_row_bytes(int quant, int64_t n);
+/* Activation format consumed by the dot product of `weight_quant` (-1 if unsupported). */
+int jero_hip_act_format(int weight_quant);
+
+/* ---- Q8 activation quantization ----
+ * Replaces repack::QuantizedActQ8::quantize(acts, m, k) (src/weights.rs:1416-1417) and the
+ * quantization implied inside vec_dot_* (src/gemma.rs:73-86).  x_dev: m rows of k f32;
+ * q_dev: m * jero_hip_row_bytes(act_quant, k) bytes.  act_quant is JERO_ACT_Q8 or JERO_Q8_K. */
+int jero_hip_quantize_act(int act_quant, const float *x_dev, int64_t m, int64_t k, void *q_dev, void *stream);
+
+/* ---- GEMV over GGUF weight bytes ----
+ * Replaces matvec_any (src/gemma.rs:100-138) -> matvec_any_slice (src/gemma.rs:66-95) ->
+ * vec_dot_q8_0 / vec_dot_q4_0 / BaselineKernel::vec_dot_q4_k_m / vec_dot_q6_k.
+ * w_dev: n_out rows of n_in elements in `quant` (GGUF tensor shape [n_in, n_out]);
+ * xq_dev: the activation already quantized to jero_hip_act_format(quant); y_dev: n_out f32. */
+int jero_hip_matvec(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
+                    const void *xq_dev, float *y_dev, void *stream);
+
+/* The reference signature vec_dot_*(out, &TensorView, &[f32]): quantizes x_dev first into
+ * `workspace_dev` (jero_hip_row_bytes(act, n_in) bytes).  A NULL workspace uses a
+ * library-owned per-device buffer: such calls must not overlap on one device. */
+int jero_hip_vec_dot(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
+                     const float *x_dev, float *y_dev, void *workspace_dev, size_t workspace_bytes,
+                     void *stream);
+
+/* The exact int32 partial sums of the same GEMV kernel: partials_dev[n_out][P] with P = n_in/32
+ * (Q8_0, Q4_0: per block; Q4_K: per 32-element sub-block) or n_in/16 (Q6_K).  Debug export for
+ * the bit-exact tests; y_dev receives the same outputs as jero_hip_matvec. */
+int jero_hip_matvec_partials(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
+                             const void *xq_dev, float *y_dev, int32_t *partials_dev, void *stream);
+
+/* dequantize_token_row (src/qwen_deepseek.rs:514,569): rows [row0, row0+n_rows) of a tensor
+ * with n_in elements per row, written as f32 to out_dev[n_rows][n_in]. */
+int jero_hip_dequantize_rows(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t row0,
+                             int64_t n_rows, float *out_dev, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* JERO_HIP_H */

@@ -1,0 +1,19 @@
+// gemv.h -- GEMV launchers shared by the entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace jero {
+
+// Largest n_in the register-resident activation layout supports for a weight format.
+int max_gemv_k(int quant);
+// Validates a matvec call (shape, bytes, alignment); records the error and returns its code.
+int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, int64_t n_out, const void* xq,
+                      const float* y);
+// Enqueues y = W xq (and the int32 partial sums when part != nullptr).
+int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, float* y, int32_t* part,
+                  hipStream_t s);
+
+}  // namespace jero

@@ -1,0 +1,295 @@
+// gemv_dot.h -- per-format "unit" dot products of the GEMV kernels.
+//
+// A unit is the slice of one weight row that one lane reduces per step:
+//   Q4_K : 64 elements = one (super-block b, 64-element group i): the 16-byte block header
+//          (d, dmin, 12 scale bytes) and the 32 bytes qs[32i, 32i+32) -> sub-blocks 2i, 2i+1
+//   Q6_K : 64 elements = (block b, half n, 16-lane group j): ql[64n+16j..+16], ql[64n+32+16j..+16],
+//          qh[32n+16j..+16], four int8 scales sc[8n+j+2t], d -> four 16-element groups
+//   Q8_0 : 32 elements = one block (f16 d + 32 int8)
+//   Q4_0 : 32 elements = one block (f16 d + 16 nibble bytes)
+// Act<F> holds the matching activation slice (ACT_Q8 or Q8_K) in registers; it is loaded
+// once per wave and reused for every row the wave reduces (activation-stationary GEMV).
+// Integer partial sums are exact (v_dot4_i32_i8); the float combine follows the block
+// formulas: Q4_K d_x (d sum sc S - dmin sum m bsum), Q6_K d_x d sum sc S, Q8_0/Q4_0 d_w d_x S.
+#pragma once
+
+#include "jero_common.h"
+
+namespace jero {
+
+template <int F>
+struct Unit;
+
+// ---------------------------------------------------------------- Q4_K x Q8_K
+template <>
+struct Unit<JERO_Q4_K> {
+  static constexpr int kElems = 64;
+  static constexpr int kPartials = 2;  // two 32-element sub-blocks
+  // index of partial t of unit u within the row's partial sums (one per 32 elements)
+  static __device__ __forceinline__ int part_index(int u, int t) { return 2 * u + t; }
+
+  struct Act {
+    uint32_t a[16];
+    float dx;
+    int bsa, bsb;
+    uint32_t jj0, hi;  // scale byte index of sub-block 2i (mod 4), and i >= 2
+  };
+  struct W {
+    u32x4 h, q0, q1;
+  };
+
+  static __device__ __forceinline__ void load_act(Act& A, const uint8_t* __restrict__ xq, int u) {
+    int b = u >> 2, i = u & 3;
+    const uint8_t* blk = xq + int64_t(b) * 292;
+    A.dx = *reinterpret_cast<const float*>(blk);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      u32x4 v = ld4(blk + 4 + 64 * i + 16 * t);
+      A.a[4 * t + 0] = v.x;
+      A.a[4 * t + 1] = v.y;
+      A.a[4 * t + 2] = v.z;
+      A.a[4 * t + 3] = v.w;
+    }
+    u32x2 bs = ld2(blk + 260 + 8 * i);
+    A.bsa = int(int16_t(bs.x & 0xFFFFu)) + int(int16_t(bs.x >> 16));
+    A.bsb = int(int16_t(bs.y & 0xFFFFu)) + int(int16_t(bs.y >> 16));
+    A.jj0 = uint32_t((2 * i) & 3);
+    A.hi = uint32_t(i >= 2);
+  }
+
+  static __device__ __forceinline__ void load_w(W& w, const uint8_t* __restrict__ row, int u) {
+    int b = u >> 2, i = u & 3;
+    const uint8_t* blk = row + int64_t(b) * 144;
+    w.h = ld4(blk);
+    w.q0 = ld4(blk + 16 + 32 * i);
+    w.q1 = ld4(blk + 32 + 32 * i);
+  }
+
+  // 6-bit scale and min of sub-block with scale byte index jj (see get_scale_min_k4).
+  static __device__ __forceinline__ void scale_min(const W& w, uint32_t jj, uint32_t hi, int& sc, int& m) {
+    uint32_t a = byte_of(w.h.y, jj), bb = byte_of(w.h.z, jj), c = byte_of(w.h.w, jj);
+    uint32_t sc_lo = a & 63u, m_lo = bb & 63u;
+    uint32_t sc_hi = (c & 15u) | ((a >> 6) << 4), m_hi = (c >> 4) | ((bb >> 6) << 4);
+    sc = int(hi ? sc_hi : sc_lo);
+    m = int(hi ? m_hi : m_lo);
+  }
+
+  static __device__ __forceinline__ float dot(const W& w, const Act& A, int32_t* part) {
+    uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+    int sa = 0, sb = 0;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      sa = dot4(q[t] & 0x0F0F0F0Fu, A.a[t], sa);
+      sb = dot4((q[t] >> 4) & 0x0F0F0F0Fu, A.a[8 + t], sb);
+    }
+    if (part) {
+      part[0] = sa;
+      part[1] = sb;
+    }
+    int sca, ma, scb, mb;
+    scale_min(w, A.jj0, A.hi, sca, ma);
+    scale_min(w, A.jj0 + 1u, A.hi, scb, mb);
+    int isum = sca * sa + scb * sb;
+    int msum = ma * A.bsa + mb * A.bsb;
+    float d = h2f(w.h.x), dmin = h2f(w.h.x >> 16);
+    return A.dx * (d * float(isum) - dmin * float(msum));
+  }
+};
+
+// ---------------------------------------------------------------- Q6_K x Q8_K
+template <>
+struct Unit<JERO_Q6_K> {
+  static constexpr int kElems = 64;
+  static constexpr int kPartials = 4;  // four 16-element groups
+  // group index (one per 16 elements) of partial t of unit u = 4b + 2n + j: 16b + 8n + j + 2t
+  static __device__ __forceinline__ int part_index(int u, int t) {
+    return 16 * (u >> 2) + 8 * ((u >> 1) & 1) + (u & 1) + 2 * t;
+  }
+
+  struct Act {
+    uint32_t a[16];  // a[4t + k]: q8 of group t, dword k
+    float dx;
+    int bs32[4];     // 32 * bsum of group t
+    uint32_t j;
+  };
+  struct W {
+    u32x4 lo, hi, qh;
+    u32x2 sc;
+    float d;
+  };
+
+  static __device__ __forceinline__ void load_act(Act& A, const uint8_t* __restrict__ xq, int u) {
+    int b = u >> 2, n = (u >> 1) & 1, j = u & 1;
+    const uint8_t* blk = xq + int64_t(b) * 292;
+    A.dx = *reinterpret_cast<const float*>(blk);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      u32x4 v = ld4(blk + 4 + 128 * n + 16 * j + 32 * t);
+      A.a[4 * t + 0] = v.x;
+      A.a[4 * t + 1] = v.y;
+      A.a[4 * t + 2] = v.z;
+      A.a[4 * t + 3] = v.w;
+    }
+    u32x4 bs = ld4(blk + 260 + 16 * n);  // bsums[8n .. 8n+8)
+    uint32_t dw[4] = {bs.x, bs.y, bs.z, bs.w};
+#pragma unroll
+    for (int t = 0; t < 4; t++) A.bs32[t] = 32 * int(int16_t((dw[t] >> (16 * j)) & 0xFFFFu));
+    A.j = uint32_t(j);
+  }
+
+  static __device__ __forceinline__ void load_w(W& w, const uint8_t* __restrict__ row, int u) {
+    int b = u >> 2, n = (u >> 1) & 1, j = u & 1;
+    const uint8_t* blk = row + int64_t(b) * 210;
+    w.lo = ld16_a2(blk + 64 * n + 16 * j);
+    w.hi = ld16_a2(blk + 64 * n + 32 + 16 * j);
+    w.qh = ld16_a2(blk + 128 + 32 * n + 16 * j);
+    w.sc = ld8_a2(blk + 192 + 8 * n);
+    w.d = ldh_a2(blk + 208);
+  }
+
+  static __device__ __forceinline__ float dot(const W& w, const Act& A, int32_t* part) {
+    uint32_t lo[4] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w};
+    uint32_t hi[4] = {w.hi.x, w.hi.y, w.hi.z, w.hi.w};
+    uint32_t qh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+    int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      uint32_t v0 = (lo[k] & 0x0F0F0F0Fu) | ((qh[k] & 0x03030303u) << 4);
+      uint32_t v1 = (hi[k] & 0x0F0F0F0Fu) | ((qh[k] & 0x0C0C0C0Cu) << 2);
+      uint32_t v2 = ((lo[k] >> 4) & 0x0F0F0F0Fu) | (qh[k] & 0x30303030u);
+      uint32_t v3 = ((hi[k] >> 4) & 0x0F0F0F0Fu) | ((qh[k] >> 2) & 0x30303030u);
+      s0 = dot4(v0, A.a[0 + k], s0);
+      s1 = dot4(v1, A.a[4 + k], s1);
+      s2 = dot4(v2, A.a[8 + k], s2);
+      s3 = dot4(v3, A.a[12 + k], s3);
+    }
+    s0 -= A.bs32[0];
+    s1 -= A.bs32[1];
+    s2 -= A.bs32[2];
+    s3 -= A.bs32[3];
+    if (part) {
+      part[0] = s0;
+      part[1] = s1;
+      part[2] = s2;
+      part[3] = s3;
+    }
+    uint32_t sh = 8u * A.j;
+    int c0 = int(int8_t(w.sc.x >> sh)), c1 = int(int8_t(w.sc.x >> (sh + 16u)));
+    int c2 = int(int8_t(w.sc.y >> sh)), c3 = int(int8_t(w.sc.y >> (sh + 16u)));
+    int isum = c0 * s0 + c1 * s1 + c2 * s2 + c3 * s3;
+    return A.dx * w.d * float(isum);
+  }
+};
+
+// ---------------------------------------------------------------- Q8_0 x ACT_Q8
+template <>
+struct Unit<JERO_Q8_0> {
+  static constexpr int kElems = 32;
+  static constexpr int kPartials = 1;
+  static __device__ __forceinline__ int part_index(int u, int) { return u; }
+
+  struct Act {
+    uint32_t a[8];
+    float dx;
+  };
+  struct W {
+    uint32_t D[9];
+    uint32_t s;  // byte offset of the block inside D[0] (0 or 2)
+  };
+
+  static __device__ __forceinline__ void load_act(Act& A, const uint8_t* __restrict__ xq, int u) {
+    const uint8_t* blk = xq + int64_t(u) * 36;
+    A.dx = *reinterpret_cast<const float*>(blk);
+    u32x4 v0 = ld4(blk + 4), v1 = ld4(blk + 20);
+    A.a[0] = v0.x; A.a[1] = v0.y; A.a[2] = v0.z; A.a[3] = v0.w;
+    A.a[4] = v1.x; A.a[5] = v1.y; A.a[6] = v1.z; A.a[7] = v1.w;
+  }
+
+  // The 34-byte block is read as the nine dwords from the dword-aligned address at or below
+  // it: each holds at least one byte of the block.
+  static __device__ __forceinline__ void load_w(W& w, const uint8_t* __restrict__ row, int u) {
+    uintptr_t a = reinterpret_cast<uintptr_t>(row + int64_t(u) * 34);
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
+    w.s = uint32_t(a & 3u);
+    u32x4 v0 = ld4(base), v1 = ld4(base + 16);
+    w.D[0] = v0.x; w.D[1] = v0.y; w.D[2] = v0.z; w.D[3] = v0.w;
+    w.D[4] = v1.x; w.D[5] = v1.y; w.D[6] = v1.z; w.D[7] = v1.w;
+    w.D[8] = ld1(base + 32);
+  }
+
+  static __device__ __forceinline__ float dot(const W& w, const Act& A, int32_t* part) {
+    int s = 0;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      uint32_t q = w.s ? w.D[t + 1] : funnel(w.D[t], w.D[t + 1], 2u);
+      s = dot4(q, A.a[t], s);
+    }
+    if (part) part[0] = s;
+    float d = h2f(w.D[0] >> (8u * w.s));
+    return d * A.dx * float(s);
+  }
+};
+
+// ---------------------------------------------------------------- Q4_0 x ACT_Q8
+template <>
+struct Unit<JERO_Q4_0> {
+  static constexpr int kElems = 32;
+  static constexpr int kPartials = 1;
+  static __device__ __forceinline__ int part_index(int u, int) { return u; }
+
+  struct Act {
+    uint32_t a[8];
+    float dx;
+    int asum8;  // 8 * sum of the block's q8
+  };
+  struct W {
+    uint32_t D[5];
+    uint32_t s;
+  };
+
+  static __device__ __forceinline__ void load_act(Act& A, const uint8_t* __restrict__ xq, int u) {
+    const uint8_t* blk = xq + int64_t(u) * 36;
+    A.dx = *reinterpret_cast<const float*>(blk);
+    u32x4 v0 = ld4(blk + 4), v1 = ld4(blk + 20);
+    A.a[0] = v0.x; A.a[1] = v0.y; A.a[2] = v0.z; A.a[3] = v0.w;
+    A.a[4] = v1.x; A.a[5] = v1.y; A.a[6] = v1.z; A.a[7] = v1.w;
+    int s = 0;
+#pragma unroll
+    for (int t = 0; t < 8; t++) s = dot4(A.a[t], 0x01010101u, s);
+    A.asum8 = 8 * s;
+  }
+
+  // The 18-byte block is read as the five dwords from the dword-aligned address at or below it.
+  static __device__ __forceinline__ void load_w(W& w, const uint8_t* __restrict__ row, int u) {
+    uintptr_t a = reinterpret_cast<uintptr_t>(row + int64_t(u) * 18);
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
+    w.s = uint32_t(a & 3u);
+    u32x4 v0 = ld4(base);
+    w.D[0] = v0.x; w.D[1] = v0.y; w.D[2] = v0.z; w.D[3] = v0.w;
+    w.D[4] = ld1(base + 16);
+  }
+
+  static __device__ __forceinline__ float dot(const W& w, const Act& A, int32_t* part) {
+    int s = 0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      uint32_t q = w.s ? w.D[t + 1] : funnel(w.D[t], w.D[t + 1], 2u);
+      s = dot4(q & 0x0F0F0F0Fu, A.a[t], s);
+      s = dot4((q >> 4) & 0x0F0F0F0Fu, A.a[4 + t], s);
+    }
+    s -= A.asum8;
+    if (part) part[0] = s;
+    float d = h2f(w.D[0] >> (8u * w.s));
+    return d * A.dx * float(s);
+  }
+};
+
+// Units per row and partial sums per row of a weight format.
+__host__ __device__ constexpr int units_per_row(int f, int64_t k) {
+  return int(k / ((f == JERO_Q4_K || f == JERO_Q6_K) ? 64 : 32));
+}
+__host__ __device__ constexpr int64_t partials_per_row(int f, int64_t k) {
+  return f == JERO_Q6_K ? k / 16 : k / 32;
+}
+
+}  // namespace jero

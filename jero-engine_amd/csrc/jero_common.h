@@ -1,0 +1,134 @@
+// jero_common.h -- device-side helpers shared by the gfx950 kernels of libjero_hip.
+//
+// Block formats (GGUF/ggml, little endian) read by the kernels:
+//   Q8_0   34 B : f16 d | i8 q[32]
+//   Q4_0   18 B : f16 d | u8 qs[16]            (q - 8, low nibbles first)
+//   Q4_K  144 B : f16 d | f16 dmin | u8 sc[12] | u8 qs[128]
+//   Q6_K  210 B : u8 ql[128] | u8 qh[64] | i8 sc[16] | f16 d
+//   Q8_K  292 B : f32 d | i8 q[256] | i16 bsums[16]      (activation for Q4_K / Q6_K)
+//   ACT_Q8 36 B : f32 d | i8 q[32]                       (activation for Q8_0 / Q4_0)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "jero_hip.h"
+
+namespace jero {
+
+constexpr int kWave = 64;
+
+struct FmtInfo {
+  int block_elems;
+  int block_bytes;
+};
+
+__host__ __device__ constexpr FmtInfo fmt_info(int q) {
+  return q == JERO_Q8_0     ? FmtInfo{32, 34}
+         : q == JERO_Q4_0   ? FmtInfo{32, 18}
+         : q == JERO_Q4_K   ? FmtInfo{256, 144}
+         : q == JERO_Q6_K   ? FmtInfo{256, 210}
+         : q == JERO_Q8_K   ? FmtInfo{256, 292}
+         : q == JERO_ACT_Q8 ? FmtInfo{32, 36}
+         : q == JERO_F32    ? FmtInfo{1, 4}
+         : q == JERO_F16    ? FmtInfo{1, 2}
+                            : FmtInfo{0, 0};
+}
+
+// 16-byte vector with 4-byte alignment: selects global_load_dwordx4 on any dword address.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2), aligned(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ u32x4 ld4(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x2 ld2(const uint8_t* p) { return *reinterpret_cast<const u32x2*>(p); }
+__device__ __forceinline__ uint32_t ld1(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+// Bytes [s, s+4) of the 8-byte little-endian pair (lo, hi), s in 0..3.
+__device__ __forceinline__ uint32_t funnel(uint32_t lo, uint32_t hi, uint32_t s) {
+  return __builtin_amdgcn_alignbyte(hi, lo, s);
+}
+
+// 16 bytes starting at an address that is only 2-byte aligned.  Reads the five dwords that
+// cover them from the dword-aligned address below: every dword read holds at least one byte
+// of [p, p+16), so the read never leaves the pages that hold the requested bytes.
+__device__ __forceinline__ u32x4 ld16_a2(const uint8_t* p) {
+  uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
+  uint32_t s = uint32_t(a & 3u);
+  u32x4 w = ld4(base);
+  uint32_t w4 = (s != 0u) ? ld1(base + 16) : 0u;
+  u32x4 r;
+  r.x = funnel(w.x, w.y, s);
+  r.y = funnel(w.y, w.z, s);
+  r.z = funnel(w.z, w.w, s);
+  r.w = funnel(w.w, w4, s);
+  return r;
+}
+
+// 4 bytes at a 2-byte aligned address (same page argument as ld16_a2).
+__device__ __forceinline__ uint32_t ld4_a2(const uint8_t* p) {
+  uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
+  uint32_t s = uint32_t(a & 3u);
+  uint32_t w0 = ld1(base);
+  uint32_t w1 = (s != 0u) ? ld1(base + 4) : 0u;
+  return funnel(w0, w1, s);
+}
+
+// 8 bytes at a 2-byte aligned address.
+__device__ __forceinline__ u32x2 ld8_a2(const uint8_t* p) {
+  uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
+  uint32_t s = uint32_t(a & 3u);
+  u32x2 w = ld2(base);
+  uint32_t w2 = (s != 0u) ? ld1(base + 8) : 0u;
+  u32x2 r;
+  r.x = funnel(w.x, w.y, s);
+  r.y = funnel(w.y, w2, s);
+  return r;
+}
+
+// 2-byte f16 at a 2-byte aligned address -> f32.
+__device__ __forceinline__ float ldh_a2(const uint8_t* p) {
+  uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  uint32_t w = ld1(reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3)));
+  uint16_t h = uint16_t(w >> (8u * uint32_t(a & 3u)));
+  return float(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return float(__builtin_bit_cast(_Float16, uint16_t(bits16 & 0xFFFFu)));
+}
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4(int(a), int(b), c, false);
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, uint32_t i) { return __builtin_amdgcn_ubfe(w, 8u * i, 8u); }
+
+// Sum over groups of `width` consecutive lanes (width a power of two <= 64).
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+template <int WIDTH>
+__device__ __forceinline__ int group_sum_i(int v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+}  // namespace jero

@@ -1,0 +1,207 @@
+"""Python front end of libjero_hip.so (ctypes over the C ABI in include/jero_hip.h).
+
+The names mirror the jero_kernels_rvv entry points the reference's recipes call
+(src/gemma.rs:66-138, src/qwen_deepseek.rs:643-951): ``vec_dot_q8_0(out, weights, input)``,
+``matvec_any``, ``QuantizedActQ8.quantize`` ...  Device buffers are torch tensors (torch is
+used for device memory and streams only); every computation runs in the HIP library.
+Errors come back as :class:`K3Error` carrying the reference's variant name.
+
+The library must have been built (``make -C jero-engine_amd`` or ``__graft_entry__.build()``);
+importing this module on a box without it raises instead of falling back to anything.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.normpath(os.path.join(HERE, "..", "libjero_hip.so"))
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, ACT_Q8 = 0, 1, 2, 8, 12, 14, 15, 100
+Q4_K_M = Q4_K  # the reference's QuantType::Q4_K_M names the Q4_K block format
+QUANT_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_K: "Q8_K",
+               ACT_Q8: "ACT_Q8"}
+KV_F32, KV_F16 = 0, 1
+
+OK = 0
+STATUS_NAMES = {10: "CapabilityMismatch", 11: "InsufficientLockableMemory", 12: "ContextLengthExceeded",
+                14: "TensorBoundsError", 15: "RoutingUnavailable", 20: "DeviceError", 21: "InvalidArgument"}
+
+
+class K3Error(RuntimeError):
+    """A non-zero jero_status; ``variant`` is the K3Error variant name it mirrors."""
+
+    def __init__(self, status, message):
+        self.status = status
+        self.variant = STATUS_NAMES.get(status, "Unknown")
+        super().__init__(f"{self.variant}({status}): {message}")
+
+
+_lib = None
+_P, _I64, _I32, _SZ, _F = C.c_void_p, C.c_int64, C.c_int, C.c_size_t, C.c_float
+_SIGS = {
+    "jero_hip_init": (_I32, [_I32]),
+    "jero_hip_last_error": (C.c_char_p, []),
+    "jero_hip_status_name": (C.c_char_p, [_I32]),
+    "jero_hip_row_bytes": (_I64, [_I32, _I64]),
+    "jero_hip_act_format": (_I32, [_I32]),
+    "jero_hip_quantize_act": (_I32, [_I32, _P, _I64, _I64, _P, _P]),
+    "jero_hip_matvec": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P]),
+    "jero_hip_vec_dot": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _SZ, _P]),
+    "jero_hip_matvec_partials": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _P]),
+    "jero_hip_dequantize_rows": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, _P]),
+}
+
+
+def lib():
+    """Loads libjero_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C jero-engine_amd`")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name, None)
+            if fn is None:
+                continue
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def declared_symbols():
+    """The entry points include/jero_hip.h declares (parsed from the header)."""
+    import re
+    hdr = os.path.normpath(os.path.join(HERE, "..", "..", "include", "jero_hip.h"))
+    text = open(hdr).read()
+    return sorted(set(re.findall(r"\b(jero_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def check(status):
+    if status != OK:
+        msg = lib().jero_hip_last_error().decode(errors="replace")
+        raise K3Error(status, msg)
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def _ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def init(device=0):
+    check(lib().jero_hip_init(device))
+
+
+def row_bytes(quant, n):
+    return lib().jero_hip_row_bytes(quant, n)
+
+
+def act_format(weight_quant):
+    return lib().jero_hip_act_format(weight_quant)
+
+
+class TensorView:
+    """A device-resident GGUF tensor: ``quant``, GGUF ``shape`` [n_in, n_out] and its bytes
+    (a uint8 torch tensor on the device), as jero_core::TensorView is for the reference."""
+
+    def __init__(self, name, quant, shape, data):
+        self.name, self.quant, self.shape, self.data = name, quant, list(shape), data
+
+    @property
+    def n_in(self):
+        return self.shape[0]
+
+    @property
+    def n_out(self):
+        return self.shape[1] if len(self.shape) > 1 else 1
+
+    def nbytes(self):
+        return self.data.numel() * self.data.element_size()
+
+    def slice_rows(self, start, count):
+        rb = row_bytes(self.quant, self.n_in)
+        if start < 0 or count <= 0 or start + count > self.n_out:
+            raise K3Error(14, f"slice_rows [{start}, {start + count}) beyond {self.n_out} rows of '{self.name}'")
+        return TensorView(self.name, self.quant, [self.n_in, count], self.data[start * rb:(start + count) * rb])
+
+    def slice_expert(self, expert, num_experts):
+        """Expert `expert` of a stacked [n_in, n_out, num_experts] tensor (src/qwen_deepseek.rs:739)."""
+        rows = self.n_out
+        return TensorView(f"{self.name}[{expert}]", self.quant, [self.n_in, rows],
+                          self.data.view(num_experts, -1)[expert])
+
+
+def quantize_act(act_quant, x, out=None, stream=None):
+    """QuantizedActQ8::quantize(acts, m, k) (src/weights.rs:1416): x [m, k] or [k] f32 on device."""
+    import torch
+    m, k = (1, x.shape[0]) if x.dim() == 1 else x.shape
+    nb = row_bytes(act_quant, k)
+    if nb < 0:
+        raise K3Error(14, f"k={k} is not a multiple of the {QUANT_NAMES.get(act_quant)} block")
+    if out is None:
+        out = torch.empty(m * nb, dtype=torch.uint8, device=x.device)
+    check(lib().jero_hip_quantize_act(act_quant, _ptr(x), m, k, _ptr(out), _stream(stream)))
+    return out
+
+
+def matvec(weights, xq, out, stream=None):
+    """y = W . x with x already in the weight format's activation blocks."""
+    check(lib().jero_hip_matvec(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in,
+                                out.numel(), _ptr(xq), _ptr(out), _stream(stream)))
+    return out
+
+
+def matvec_partials(weights, xq, out, partials, stream=None):
+    check(lib().jero_hip_matvec_partials(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in,
+                                         out.numel(), _ptr(xq), _ptr(out), _ptr(partials), _stream(stream)))
+    return out, partials
+
+
+def _vec_dot(expect_quant, out, weights, inp, workspace=None, stream=None):
+    if weights.quant != expect_quant:
+        raise K3Error(10, f"tensor '{weights.name}' is {QUANT_NAMES.get(weights.quant)}, "
+                          f"expected {QUANT_NAMES.get(expect_quant)}")
+    return matvec_any(out, weights, inp, workspace, stream)
+
+
+def matvec_any(out, weights, inp, workspace=None, stream=None):
+    """matvec_any (src/gemma.rs:100-138): dispatch on the tensor's quantization."""
+    if out.numel() == 0 or inp.numel() == 0:
+        raise K3Error(14, "matvec output and input slices cannot be empty")
+    ws_p = _ptr(workspace) if workspace is not None else None
+    ws_n = workspace.numel() if workspace is not None else 0
+    check(lib().jero_hip_vec_dot(weights.quant, _ptr(weights.data), weights.nbytes(), inp.numel(), out.numel(),
+                                 _ptr(inp), _ptr(out), ws_p, ws_n, _stream(stream)))
+    return out
+
+
+def vec_dot_q8_0(out, weights, inp, **kw):
+    return _vec_dot(Q8_0, out, weights, inp, **kw)
+
+
+def vec_dot_q4_0(out, weights, inp, **kw):
+    return _vec_dot(Q4_0, out, weights, inp, **kw)
+
+
+def vec_dot_q4_k_m(out, weights, inp, **kw):
+    """BaselineKernel::vec_dot_q4_k_m (src/gemma.rs:82)."""
+    return _vec_dot(Q4_K, out, weights, inp, **kw)
+
+
+def vec_dot_q6_k(out, weights, inp, **kw):
+    return _vec_dot(Q6_K, out, weights, inp, **kw)
+
+
+def dequantize_rows(weights, row0, n_rows, out, stream=None):
+    """dequantize_token_row for rows [row0, row0 + n_rows)."""
+    check(lib().jero_hip_dequantize_rows(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in, row0,
+                                         n_rows, _ptr(out), _stream(stream)))
+    return out
+
+
+def dequantize_token_row(weights, row, out, stream=None):
+    return dequantize_rows(weights, row, 1, out, stream)

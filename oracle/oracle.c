@@ -1,0 +1,777 @@
+/*
+ * oracle.c -- CPU restatement of jero-engine's quantized-matmul hot path.
+ * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py; the product library never links it.
+ * The functions, their reference citations and their pins are listed in oracle.h.
+ *
+ * Plain C99 + pthreads, scalar, no intrinsics: built -O3 -march=native it is also the
+ * "C restatement of the reference's portable CPU path" that bench.py times.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ fp16 */
+
+float jo_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1Fu;
+  uint32_t mant = h & 0x3FFu;
+  uint32_t bits;
+  if (exp == 0) {
+    if (mant == 0) {
+      bits = sign;
+    } else { /* subnormal: normalise */
+      int e = -1;
+      do {
+        e++;
+        mant <<= 1;
+      } while ((mant & 0x400u) == 0);
+      mant &= 0x3FFu;
+      bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (mant << 13);
+    }
+  } else if (exp == 31) {
+    bits = sign | 0x7F800000u | (mant << 13);
+  } else {
+    bits = sign | ((exp + 127 - 15) << 23) | (mant << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+/* Round-to-nearest-even float -> half (IEEE 754 conversion). */
+uint16_t jo_f32_to_f16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  uint32_t absx = x & 0x7FFFFFFFu;
+  if (absx >= 0x7F800000u) { /* inf or nan */
+    return (uint16_t)(sign | 0x7C00u | (absx > 0x7F800000u ? 0x200u : 0u));
+  }
+  if (absx >= 0x477FF000u) { /* rounds to >= 65520 -> inf */
+    return (uint16_t)(sign | 0x7C00u);
+  }
+  if (absx < 0x38800000u) { /* result is subnormal or zero in half */
+    /* value = absx as float; half subnormal unit = 2^-24 */
+    float af;
+    memcpy(&af, &absx, 4);
+    float scaled = af * 16777216.0f; /* exact: multiply by 2^24 */
+    /* rint with round-half-even in the default FP environment */
+    uint32_t m = (uint32_t)nearbyintf(scaled);
+    return (uint16_t)(sign | m);
+  }
+  uint32_t mant = absx & 0x7FFFFFu;
+  uint32_t exp = (absx >> 23) - 127 + 15;
+  uint32_t h = (exp << 10) | (mant >> 13);
+  uint32_t rem = mant & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1; /* carries into exponent correctly */
+  return (uint16_t)(sign | h);
+}
+
+/* ------------------------------------------------------------------ formats */
+
+int64_t jo_block_elems(int quant) {
+  switch (quant) {
+    case JO_F32:
+    case JO_F16: return 1;
+    case JO_Q4_0:
+    case JO_Q8_0:
+    case JO_ACT_Q8: return 32;
+    case JO_Q4_K:
+    case JO_Q6_K:
+    case JO_Q8_K: return 256;
+    default: return 0;
+  }
+}
+
+int64_t jo_block_bytes(int quant) {
+  switch (quant) {
+    case JO_F32: return 4;
+    case JO_F16: return 2;
+    case JO_Q4_0: return 18;
+    case JO_Q8_0: return 34;
+    case JO_ACT_Q8: return 36;
+    case JO_Q4_K: return 144;
+    case JO_Q6_K: return 210;
+    case JO_Q8_K: return 292;
+    default: return 0;
+  }
+}
+
+int64_t jo_row_bytes(int quant, int64_t n) {
+  int64_t be = jo_block_elems(quant);
+  if (be <= 0 || n < 0 || n % be) return -1;
+  return (n / be) * jo_block_bytes(quant);
+}
+
+int jo_act_format(int weight_quant) {
+  switch (weight_quant) {
+    case JO_Q4_0:
+    case JO_Q8_0: return JO_ACT_Q8;
+    case JO_Q4_K:
+    case JO_Q6_K: return JO_Q8_K;
+    default: return -1;
+  }
+}
+
+static inline uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static inline float rdf32(const uint8_t *p) {
+  float f;
+  memcpy(&f, p, 4);
+  return f;
+}
+static inline int16_t rdi16(const uint8_t *p) { return (int16_t)rd16(p); }
+
+/* Q4_K 6-bit scale/min of sub-block j (ggml get_scale_min_k4). */
+static inline void q4k_scale_min(int j, const uint8_t *s, int *sc, int *m) {
+  if (j < 4) {
+    *sc = s[j] & 63;
+    *m = s[j + 4] & 63;
+  } else {
+    *sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+    *m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+  }
+}
+
+/* Unpack one Q6_K block to 256 signed values in [-32, 31] and return the 16 scales. */
+static void q6k_unpack(const uint8_t *b, int8_t q[256], int8_t sc[16]) {
+  const uint8_t *ql = b, *qh = b + 128;
+  for (int n = 0; n < 2; n++) {
+    for (int l = 0; l < 32; l++) {
+      q[128 * n + l] = (int8_t)(((ql[64 * n + l] & 0xF) | (((qh[32 * n + l] >> 0) & 3) << 4)) - 32);
+      q[128 * n + l + 32] = (int8_t)(((ql[64 * n + l + 32] & 0xF) | (((qh[32 * n + l] >> 2) & 3) << 4)) - 32);
+      q[128 * n + l + 64] = (int8_t)(((ql[64 * n + l] >> 4) | (((qh[32 * n + l] >> 4) & 3) << 4)) - 32);
+      q[128 * n + l + 96] = (int8_t)(((ql[64 * n + l + 32] >> 4) | (((qh[32 * n + l] >> 6) & 3) << 4)) - 32);
+    }
+  }
+  memcpy(sc, b + 192, 16);
+}
+
+int jo_dequantize_row(int quant, const void *row, int64_t n, float *out) {
+  const uint8_t *p = (const uint8_t *)row;
+  int64_t be = jo_block_elems(quant), bb = jo_block_bytes(quant);
+  if (be <= 0 || n % be) return -1;
+  int64_t nb = n / be;
+  for (int64_t b = 0; b < nb; b++) {
+    const uint8_t *blk = p + b * bb;
+    float *y = out + b * be;
+    switch (quant) {
+      case JO_F32: y[0] = rdf32(blk); break;
+      case JO_F16: y[0] = jo_f16_to_f32(rd16(blk)); break;
+      case JO_Q8_0: {
+        float d = jo_f16_to_f32(rd16(blk));
+        for (int j = 0; j < 32; j++) y[j] = d * (float)(int8_t)blk[2 + j];
+      } break;
+      case JO_Q4_0: {
+        float d = jo_f16_to_f32(rd16(blk));
+        for (int j = 0; j < 16; j++) {
+          y[j] = d * (float)((blk[2 + j] & 0xF) - 8);
+          y[j + 16] = d * (float)((blk[2 + j] >> 4) - 8);
+        }
+      } break;
+      case JO_ACT_Q8: {
+        float d = rdf32(blk);
+        for (int j = 0; j < 32; j++) y[j] = d * (float)(int8_t)blk[4 + j];
+      } break;
+      case JO_Q4_K: {
+        float d = jo_f16_to_f32(rd16(blk)), dmin = jo_f16_to_f32(rd16(blk + 2));
+        const uint8_t *s = blk + 4, *qs = blk + 16;
+        for (int i = 0; i < 4; i++) {
+          int sc1, m1, sc2, m2;
+          q4k_scale_min(2 * i, s, &sc1, &m1);
+          q4k_scale_min(2 * i + 1, s, &sc2, &m2);
+          float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
+          float d2 = d * (float)sc2, mm2 = dmin * (float)m2;
+          for (int l = 0; l < 32; l++) {
+            y[64 * i + l] = d1 * (float)(qs[32 * i + l] & 0xF) - mm1;
+            y[64 * i + 32 + l] = d2 * (float)(qs[32 * i + l] >> 4) - mm2;
+          }
+        }
+      } break;
+      case JO_Q6_K: {
+        int8_t q[256], sc[16];
+        q6k_unpack(blk, q, sc);
+        float d = jo_f16_to_f32(rd16(blk + 208));
+        for (int l = 0; l < 256; l++) y[l] = d * (float)sc[l / 16] * (float)q[l];
+      } break;
+      case JO_Q8_K: {
+        float d = rdf32(blk);
+        for (int j = 0; j < 256; j++) y[j] = d * (float)(int8_t)blk[4 + j];
+      } break;
+      default: return -1;
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------ activation quantizers */
+
+/* QuantizedActQ8 block: {f32 d; i8 q[32]}.  d = amax/127 stays f32 (an f16 d misses the
+ * golden llama logits by 0.19; the f32 d matches them to 8e-7).  q = round-half-even(x * (1/d)). */
+void jo_quantize_act_q8(const float *x, int64_t m, int64_t k, void *out) {
+  uint8_t *o = (uint8_t *)out;
+  int64_t nb = k / 32;
+  for (int64_t r = 0; r < m; r++) {
+    for (int64_t b = 0; b < nb; b++) {
+      const float *xb = x + r * k + b * 32;
+      uint8_t *ob = o + (r * nb + b) * 36;
+      float amax = 0.0f;
+      for (int j = 0; j < 32; j++) {
+        float a = fabsf(xb[j]);
+        if (a > amax) amax = a;
+      }
+      float d = amax / 127.0f;
+      float id = d != 0.0f ? 1.0f / d : 0.0f;
+      memcpy(ob, &d, 4);
+      for (int j = 0; j < 32; j++) {
+        float v = xb[j] * id;
+        ob[4 + j] = (uint8_t)(int8_t)(int)nearbyintf(v);
+      }
+    }
+  }
+}
+
+/* Q8_K block: {f32 d; i8 qs[256]; i16 bsums[16]} (ggml quantize_row_q8_K_ref). The signed
+ * element of largest magnitude (first one on ties) sets iscale = -127/max; q = min(127,
+ * round-half-even(iscale*x)); d = 1/iscale; bsums are sums of 16 consecutive q. */
+void jo_quantize_q8_k(const float *x, int64_t m, int64_t k, void *out) {
+  uint8_t *o = (uint8_t *)out;
+  int64_t nb = k / 256;
+  for (int64_t r = 0; r < m; r++) {
+    for (int64_t b = 0; b < nb; b++) {
+      const float *xb = x + r * k + b * 256;
+      uint8_t *ob = o + (r * nb + b) * 292;
+      float amax = 0.0f, mx = 0.0f;
+      for (int j = 0; j < 256; j++) {
+        float a = fabsf(xb[j]);
+        if (a > amax) {
+          amax = a;
+          mx = xb[j];
+        }
+      }
+      if (amax == 0.0f) {
+        memset(ob, 0, 292);
+        continue;
+      }
+      float iscale = -127.0f / mx;
+      int8_t q[256];
+      for (int j = 0; j < 256; j++) {
+        int v = (int)nearbyintf(iscale * xb[j]);
+        q[j] = (int8_t)(v < 127 ? v : 127);
+      }
+      float d = 1.0f / iscale;
+      memcpy(ob, &d, 4);
+      memcpy(ob + 4, q, 256);
+      for (int g = 0; g < 16; g++) {
+        int s = 0;
+        for (int l = 0; l < 16; l++) s += q[16 * g + l];
+        int16_t s16 = (int16_t)s;
+        memcpy(ob + 260 + 2 * g, &s16, 2);
+      }
+    }
+  }
+}
+
+void jo_quantize_act(int act_quant, const float *x, int64_t m, int64_t k, void *out) {
+  if (act_quant == JO_Q8_K)
+    jo_quantize_q8_k(x, m, k, out);
+  else
+    jo_quantize_act_q8(x, m, k, out);
+}
+
+/* ------------------------------------------------------------------ dot products */
+
+int64_t jo_partials_per_row(int quant, int64_t k) {
+  switch (quant) {
+    case JO_Q8_0:
+    case JO_Q4_0: return k / 32;
+    case JO_Q4_K: return k / 32;
+    case JO_Q6_K: return k / 16;
+    default: return 0;
+  }
+}
+
+double jo_vec_dot_row(int quant, const void *wrow, int64_t k, const void *xq, int32_t *partials) {
+  const uint8_t *w = (const uint8_t *)wrow, *a = (const uint8_t *)xq;
+  double acc = 0.0;
+  switch (quant) {
+    case JO_Q8_0: /* y = sum_b f16(d_w) * d_x * sum_32 q_w q_x */
+      for (int64_t b = 0; b < k / 32; b++) {
+        const uint8_t *wb = w + b * 34, *ab = a + b * 36;
+        int32_t s = 0;
+        for (int j = 0; j < 32; j++) s += (int32_t)(int8_t)wb[2 + j] * (int32_t)(int8_t)ab[4 + j];
+        if (partials) partials[b] = s;
+        acc += (double)jo_f16_to_f32(rd16(wb)) * (double)rdf32(ab) * (double)s;
+      }
+      break;
+    case JO_Q4_0: /* y = sum_b f16(d_w) * d_x * sum_32 (q4 - 8) q_x */
+      for (int64_t b = 0; b < k / 32; b++) {
+        const uint8_t *wb = w + b * 18, *ab = a + b * 36;
+        int32_t s = 0;
+        for (int j = 0; j < 16; j++) {
+          s += ((wb[2 + j] & 0xF) - 8) * (int32_t)(int8_t)ab[4 + j];
+          s += ((wb[2 + j] >> 4) - 8) * (int32_t)(int8_t)ab[4 + j + 16];
+        }
+        if (partials) partials[b] = s;
+        acc += (double)jo_f16_to_f32(rd16(wb)) * (double)rdf32(ab) * (double)s;
+      }
+      break;
+    case JO_Q4_K: /* y = sum_b d_x (d sum_j sc_j S_j - dmin sum_j m_j sum(q8 in j)) */
+      for (int64_t b = 0; b < k / 256; b++) {
+        const uint8_t *wb = w + b * 144, *ab = a + b * 292;
+        const uint8_t *s = wb + 4, *qs = wb + 16;
+        const int8_t *q8 = (const int8_t *)(ab + 4);
+        int64_t isum = 0, msum = 0;
+        for (int j = 0; j < 8; j++) {
+          int sc, mn;
+          q4k_scale_min(j, s, &sc, &mn);
+          int i = j / 2, hi = j & 1;
+          int32_t S = 0, qsum = 0;
+          for (int l = 0; l < 32; l++) {
+            int q4 = hi ? (qs[32 * i + l] >> 4) : (qs[32 * i + l] & 0xF);
+            S += q4 * q8[32 * j + l];
+            qsum += q8[32 * j + l];
+          }
+          if (partials) partials[b * 8 + j] = S;
+          isum += (int64_t)sc * S;
+          msum += (int64_t)mn * qsum;
+        }
+        double dx = rdf32(ab);
+        acc += dx * ((double)jo_f16_to_f32(rd16(wb)) * (double)isum -
+                     (double)jo_f16_to_f32(rd16(wb + 2)) * (double)msum);
+      }
+      break;
+    case JO_Q6_K: /* y = sum_b d_x d sum_i sc_i sum_16 (q6 - 32) q8 */
+      for (int64_t b = 0; b < k / 256; b++) {
+        const uint8_t *wb = w + b * 210, *ab = a + b * 292;
+        const int8_t *q8 = (const int8_t *)(ab + 4);
+        int8_t q[256], sc[16];
+        q6k_unpack(wb, q, sc);
+        int64_t isum = 0;
+        for (int g = 0; g < 16; g++) {
+          int32_t S = 0;
+          for (int l = 0; l < 16; l++) S += q[16 * g + l] * q8[16 * g + l];
+          if (partials) partials[b * 16 + g] = S;
+          isum += (int64_t)sc[g] * S;
+        }
+        acc += (double)rdf32(ab) * (double)jo_f16_to_f32(rd16(wb + 208)) * (double)isum;
+      }
+      break;
+    default: break;
+  }
+  return acc;
+}
+
+/* ------------------------------------------------------------------ threaded row loops */
+
+typedef struct {
+  int quant;
+  const uint8_t *w;
+  int64_t k, n, row_bytes, act_row_bytes, chunk;
+  const uint8_t *xq;
+  int64_t m; /* activation rows (GEMM) */
+  float *y;
+  int tid, threads;
+} jo_job;
+
+static void *jo_worker(void *arg) {
+  jo_job *j = (jo_job *)arg;
+  int64_t nchunks = (j->n + j->chunk - 1) / j->chunk;
+  for (int64_t c = j->tid; c < nchunks; c += j->threads) {
+    int64_t r0 = c * j->chunk, r1 = r0 + j->chunk < j->n ? r0 + j->chunk : j->n;
+    for (int64_t mm = 0; mm < j->m; mm++)
+      for (int64_t r = r0; r < r1; r++)
+        j->y[mm * j->n + r] =
+            (float)jo_vec_dot_row(j->quant, j->w + r * j->row_bytes, j->k, j->xq + mm * j->act_row_bytes, NULL);
+  }
+  return NULL;
+}
+
+static int jo_run_rows(int quant, const void *w, int64_t k, int64_t n, const void *xq, int64_t m, float *y,
+                       int threads) {
+  int act = jo_act_format(quant);
+  if (act < 0 || k <= 0 || n <= 0 || jo_row_bytes(quant, k) < 0) return -1;
+  if (threads < 1) threads = 1;
+  if (n < 64) threads = 1; /* matvec_any runs short outputs on the caller thread */
+  int64_t chunk = (n + threads - 1) / threads;
+  if (chunk < 16) chunk = 16;
+  if (chunk > 2048) chunk = 2048;
+  jo_job jobs[256];
+  pthread_t th[256];
+  if (threads > 256) threads = 256;
+  for (int t = 0; t < threads; t++) {
+    jobs[t] = (jo_job){quant, (const uint8_t *)w, k, n, jo_row_bytes(quant, k), jo_row_bytes(act, k), chunk,
+                       (const uint8_t *)xq, m, y, t, threads};
+  }
+  if (threads == 1) {
+    jo_worker(&jobs[0]);
+    return 0;
+  }
+  for (int t = 0; t < threads; t++) pthread_create(&th[t], NULL, jo_worker, &jobs[t]);
+  for (int t = 0; t < threads; t++) pthread_join(th[t], NULL);
+  return 0;
+}
+
+int jo_matvec(int quant, const void *w, int64_t k, int64_t n, const void *xq, float *y, int threads) {
+  return jo_run_rows(quant, w, k, n, xq, 1, y, threads);
+}
+
+int jo_gemm(int quant, const void *w, int64_t k, int64_t n, const void *xq, int64_t m, float *y, int threads) {
+  return jo_run_rows(quant, w, k, n, xq, m, y, threads);
+}
+
+int jo_vec_dot(int quant, const void *w, int64_t k, int64_t n, const float *x, float *y, int threads) {
+  int act = jo_act_format(quant);
+  if (act < 0 || jo_row_bytes(act, k) < 0) return -1;
+  void *xq = malloc((size_t)jo_row_bytes(act, k));
+  if (!xq) return -1;
+  jo_quantize_act(act, x, 1, k, xq);
+  int rc = jo_matvec(quant, w, k, n, xq, y, threads);
+  free(xq);
+  return rc;
+}
+
+int jo_matvec_dequant_f64(int quant, const void *w, int64_t k, int64_t n, const void *xq, double *y) {
+  int act = jo_act_format(quant);
+  int64_t rb = jo_row_bytes(quant, k);
+  if (act < 0 || rb < 0) return -1;
+  float *wr = (float *)malloc((size_t)k * 4), *xr = (float *)malloc((size_t)k * 4);
+  if (!wr || !xr) {
+    free(wr);
+    free(xr);
+    return -1;
+  }
+  jo_dequantize_row(act, xq, k, xr);
+  for (int64_t r = 0; r < n; r++) {
+    jo_dequantize_row(quant, (const uint8_t *)w + r * rb, k, wr);
+    double s = 0.0;
+    for (int64_t i = 0; i < k; i++) s += (double)wr[i] * (double)xr[i];
+    y[r] = s;
+  }
+  free(wr);
+  free(xr);
+  return 0;
+}
+
+int jo_matvec_partials(int quant, const void *w, int64_t k, int64_t n, const void *xq, int32_t *partials) {
+  int64_t rb = jo_row_bytes(quant, k), pp = jo_partials_per_row(quant, k);
+  if (rb < 0 || pp <= 0) return -1;
+  for (int64_t r = 0; r < n; r++) jo_vec_dot_row(quant, (const uint8_t *)w + r * rb, k, xq, partials + r * pp);
+  return 0;
+}
+
+void jo_gemm_i8(const int8_t *x, int64_t m, const int8_t *w, int64_t n, int64_t k, int32_t *out) {
+  for (int64_t i = 0; i < m; i++)
+    for (int64_t j = 0; j < n; j++) {
+      int32_t s = 0;
+      for (int64_t t = 0; t < k; t++) s += (int32_t)x[i * k + t] * (int32_t)w[j * k + t];
+      out[i * n + j] = s;
+    }
+}
+
+/* ------------------------------------------------------------------ elementwise + attention */
+
+void jo_rmsnorm(float *out, const float *x, const float *w, int64_t n, float eps) {
+  double ss = 0.0;
+  for (int64_t i = 0; i < n; i++) ss += (double)x[i] * (double)x[i];
+  double scale = 1.0 / sqrt(ss / (double)n + (double)eps);
+  for (int64_t i = 0; i < n; i++) out[i] = (float)((double)x[i] * scale * (double)w[i]);
+}
+
+void jo_rope_inplace(float *x, int64_t len, int hd, int64_t pos, float theta) {
+  for (int64_t h = 0; h < len / hd; h++) {
+    float *v = x + h * hd;
+    for (int i = 0; i < hd / 2; i++) {
+      float expo = (float)(2 * i) / (float)hd;
+      float angle = (float)pos / powf(theta, expo); /* f32 angle, as the scalar reference */
+      double c = cos((double)angle), s = sin((double)angle);
+      double x0 = v[2 * i], x1 = v[2 * i + 1];
+      v[2 * i] = (float)(x0 * c - x1 * s);
+      v[2 * i + 1] = (float)(x0 * s + x1 * c);
+    }
+  }
+}
+
+void jo_swiglu(float *out, const float *gate, const float *up, int64_t n) {
+  for (int64_t i = 0; i < n; i++) {
+    double g = gate[i];
+    out[i] = (float)(g / (1.0 + exp(-g)) * (double)up[i]);
+  }
+}
+
+int64_t jo_argmax(const float *x, int64_t n) {
+  int64_t best = -1;
+  float bv = -INFINITY;
+  for (int64_t i = 0; i < n; i++) {
+    if (isnan(x[i])) continue;
+    if (best < 0 || x[i] > bv) {
+      bv = x[i];
+      best = i;
+    }
+  }
+  return best;
+}
+
+int jo_gqa_attention(float *out, const float *q, const float *k, const float *v, int nq, int nkv, int hd,
+                     int64_t seq_len, float scale) {
+  if (nq <= 0 || nkv <= 0 || hd <= 0 || nq % nkv || seq_len <= 0) return -1;
+  int group = nq / nkv;
+  int64_t kvd = (int64_t)nkv * hd;
+  double *sc = (double *)malloc((size_t)seq_len * sizeof(double));
+  double *acc = (double *)malloc((size_t)hd * sizeof(double));
+  if (!sc || !acc) {
+    free(sc);
+    free(acc);
+    return -1;
+  }
+  for (int h = 0; h < nq; h++) {
+    int kh = h / group;
+    const float *qh = q + (int64_t)h * hd;
+    double mx = -INFINITY;
+    for (int64_t t = 0; t < seq_len; t++) {
+      const float *kt = k + t * kvd + (int64_t)kh * hd;
+      double s = 0.0;
+      for (int d = 0; d < hd; d++) s += (double)qh[d] * (double)kt[d];
+      s *= (double)scale;
+      sc[t] = s;
+      if (s > mx) mx = s;
+    }
+    double sum = 0.0;
+    for (int64_t t = 0; t < seq_len; t++) {
+      sc[t] = exp(sc[t] - mx);
+      sum += sc[t];
+    }
+    for (int d = 0; d < hd; d++) acc[d] = 0.0;
+    for (int64_t t = 0; t < seq_len; t++) {
+      const float *vt = v + t * kvd + (int64_t)kh * hd;
+      double p = sc[t] / sum;
+      for (int d = 0; d < hd; d++) acc[d] += p * (double)vt[d];
+    }
+    for (int d = 0; d < hd; d++) out[(int64_t)h * hd + d] = (float)acc[d];
+  }
+  free(sc);
+  free(acc);
+  return 0;
+}
+
+/* select_top_k_experts (src/gemma.rs:362-442): f32 softmax over all experts, stable order
+ * by logit descending (non-finite logits rank as -inf) with the lower index first, take k,
+ * renormalise the chosen probabilities when normalize != 0. */
+int jo_select_top_k(const float *logits, int64_t n, int top_k, int normalize, int32_t *idx, float *w) {
+  if (n <= 0 || top_k <= 0) return 0;
+  float mx = -INFINITY;
+  for (int64_t i = 0; i < n; i++)
+    if (isfinite(logits[i]) && logits[i] > mx) mx = logits[i];
+  float *p = (float *)malloc((size_t)n * 4);
+  int64_t *ord = (int64_t *)malloc((size_t)n * 8);
+  if (!p || !ord) {
+    free(p);
+    free(ord);
+    return 0;
+  }
+  float sum = 0.0f;
+  for (int64_t i = 0; i < n; i++) {
+    p[i] = (isfinite(logits[i]) && isfinite(mx)) ? expf(logits[i] - mx) : 0.0f;
+    sum += p[i];
+  }
+  if (sum > 0.0f && isfinite(sum)) {
+    for (int64_t i = 0; i < n; i++) p[i] /= sum;
+  } else {
+    for (int64_t i = 0; i < n; i++) p[i] = 1.0f / (float)n;
+  }
+  /* insertion order by (logit desc, index asc) */
+  for (int64_t i = 0; i < n; i++) ord[i] = i;
+  for (int64_t i = 1; i < n; i++) {
+    int64_t cur = ord[i];
+    float lc = isfinite(logits[cur]) ? logits[cur] : -INFINITY;
+    int64_t j = i - 1;
+    while (j >= 0) {
+      float lj = isfinite(logits[ord[j]]) ? logits[ord[j]] : -INFINITY;
+      if (lj < lc) {
+        ord[j + 1] = ord[j];
+        j--;
+      } else {
+        break;
+      }
+    }
+    ord[j + 1] = cur;
+  }
+  int k = top_k < n ? top_k : (int)n;
+  float ssum = 0.0f;
+  for (int i = 0; i < k; i++) {
+    idx[i] = (int32_t)ord[i];
+    w[i] = p[ord[i]];
+    ssum += w[i];
+  }
+  if (normalize) {
+    if (ssum > 0.0f && isfinite(ssum)) {
+      for (int i = 0; i < k; i++) w[i] /= ssum;
+    } else {
+      for (int i = 0; i < k; i++) w[i] = 1.0f / (float)k;
+    }
+  }
+  free(p);
+  free(ord);
+  return k;
+}
+
+/* ------------------------------------------------------------------ MoE */
+
+static int jo_matvec_f32in(int quant, const void *w, int64_t k, int64_t n, const float *x, float *y, int threads) {
+  return jo_vec_dot(quant, w, k, n, x, y, threads);
+}
+
+int jo_swiglu_expert(int gate_quant, const void *gate, int up_quant, const void *up, int down_quant,
+                     const void *down, int64_t hidden, int64_t ffn, const float *x, float *y) {
+  float *g = (float *)malloc((size_t)ffn * 4), *u = (float *)malloc((size_t)ffn * 4);
+  float *a = (float *)malloc((size_t)ffn * 4);
+  int rc = (!g || !u || !a) ? -1 : 0;
+  if (!rc) rc = jo_matvec_f32in(gate_quant, gate, hidden, ffn, x, g, 1);
+  if (!rc) rc = jo_matvec_f32in(up_quant, up, hidden, ffn, x, u, 1);
+  if (!rc) {
+    jo_swiglu(a, g, u, ffn);
+    rc = jo_matvec_f32in(down_quant, down, ffn, hidden, a, y, 1);
+  }
+  free(g);
+  free(u);
+  free(a);
+  return rc;
+}
+
+typedef struct {
+  const float *router_logits;
+  int64_t t0, t1, n_experts;
+  int top_k, gq, uq, dq;
+  const uint8_t *gate, *up, *down;
+  int64_t hidden, ffn;
+  const float *x;
+  float *y;
+  int32_t *sel_idx;
+  float *sel_w;
+  int rc;
+} jo_moe_job;
+
+static void *jo_moe_worker(void *arg) {
+  jo_moe_job *j = (jo_moe_job *)arg;
+  int64_t gstride = jo_row_bytes(j->gq, j->hidden) * j->ffn;
+  int64_t ustride = jo_row_bytes(j->uq, j->hidden) * j->ffn;
+  int64_t dstride = jo_row_bytes(j->dq, j->ffn) * j->hidden;
+  float *tmp = (float *)malloc((size_t)j->hidden * 4);
+  if (!tmp) {
+    j->rc = -1;
+    return NULL;
+  }
+  for (int64_t t = j->t0; t < j->t1; t++) {
+    int32_t *idx = j->sel_idx + t * j->top_k;
+    float *w = j->sel_w + t * j->top_k;
+    int k = jo_select_top_k(j->router_logits + t * j->n_experts, j->n_experts, j->top_k, 1, idx, w);
+    float *yt = j->y + t * j->hidden;
+    for (int64_t i = 0; i < j->hidden; i++) yt[i] = 0.0f;
+    for (int s = 0; s < k; s++) {
+      int64_t e = idx[s];
+      if (jo_swiglu_expert(j->gq, j->gate + e * gstride, j->uq, j->up + e * ustride, j->dq, j->down + e * dstride,
+                           j->hidden, j->ffn, j->x + t * j->hidden, tmp)) {
+        j->rc = -1;
+        break;
+      }
+      for (int64_t i = 0; i < j->hidden; i++) yt[i] += w[s] * tmp[i];
+    }
+  }
+  free(tmp);
+  return NULL;
+}
+
+int jo_moe_ffn(const float *router_logits, int64_t t, int64_t n_experts, int top_k, int gate_quant,
+               const void *gate, int up_quant, const void *up, int down_quant, const void *down, int64_t hidden,
+               int64_t ffn, const float *x, float *y, int32_t *sel_idx, float *sel_w, int threads) {
+  if (t <= 0 || n_experts <= 0 || top_k <= 0 || top_k > n_experts) return -1;
+  if (threads < 1) threads = 1;
+  if (threads > t) threads = (int)t;
+  if (threads > 256) threads = 256;
+  jo_moe_job jobs[256];
+  pthread_t th[256];
+  int64_t per = (t + threads - 1) / threads;
+  for (int i = 0; i < threads; i++) {
+    int64_t t0 = i * per, t1 = t0 + per < t ? t0 + per : t;
+    jobs[i] = (jo_moe_job){router_logits, t0, t1, n_experts, top_k, gate_quant, up_quant, down_quant,
+                           (const uint8_t *)gate, (const uint8_t *)up, (const uint8_t *)down, hidden, ffn, x, y,
+                           sel_idx, sel_w, 0};
+  }
+  for (int i = 0; i < threads; i++) pthread_create(&th[i], NULL, jo_moe_worker, &jobs[i]);
+  int rc = 0;
+  for (int i = 0; i < threads; i++) {
+    pthread_join(th[i], NULL);
+    if (jobs[i].rc) rc = jobs[i].rc;
+  }
+  return rc;
+}
+
+/* ------------------------------------------------------------------ decode step */
+
+static void jo_head_rmsnorm(float *x, int64_t len, int hd, const float *w, float eps) {
+  float *tmp = (float *)malloc((size_t)hd * 4);
+  for (int64_t h = 0; h < len / hd; h++) {
+    jo_rmsnorm(tmp, x + h * hd, w, hd, eps);
+    memcpy(x + h * hd, tmp, (size_t)hd * 4);
+  }
+  free(tmp);
+}
+
+int jo_decode_step(const jo_model *M, float *kv, int32_t token, int64_t pos, float *logits, int threads) {
+  int64_t H = M->hidden, F = M->ffn, qd = (int64_t)M->nq * M->hd, kvd = (int64_t)M->nkv * M->hd;
+  int64_t cap = M->kv_capacity;
+  if (token < 0 || token >= M->vocab || cap <= 0) return -1;
+  float *x = (float *)malloc((size_t)H * 4), *xn = (float *)malloc((size_t)H * 4);
+  float *q = (float *)malloc((size_t)qd * 4), *k = (float *)malloc((size_t)kvd * 4);
+  float *v = (float *)malloc((size_t)kvd * 4), *att = (float *)malloc((size_t)qd * 4);
+  float *proj = (float *)malloc((size_t)H * 4), *g = (float *)malloc((size_t)F * 4);
+  float *u = (float *)malloc((size_t)F * 4), *a = (float *)malloc((size_t)F * 4);
+  int rc = 0;
+  if (!x || !xn || !q || !k || !v || !att || !proj || !g || !u || !a) rc = -1;
+  if (!rc) rc = jo_dequantize_row(M->tok_embd.quant, (const uint8_t *)M->tok_embd.data +
+                                                         token * jo_row_bytes(M->tok_embd.quant, H),
+                                  H, x);
+  for (int64_t L = 0; L < M->n_layers && !rc; L++) {
+    const jo_layer *ly = &M->layers[L];
+    jo_rmsnorm(xn, x, ly->attn_norm, H, M->eps);
+    rc |= jo_vec_dot(ly->wq.quant, ly->wq.data, H, qd, xn, q, threads);
+    rc |= jo_vec_dot(ly->wk.quant, ly->wk.data, H, kvd, xn, k, threads);
+    rc |= jo_vec_dot(ly->wv.quant, ly->wv.data, H, kvd, xn, v, threads);
+    if (ly->q_norm) jo_head_rmsnorm(q, qd, M->hd, ly->q_norm, M->eps);
+    if (ly->k_norm) jo_head_rmsnorm(k, kvd, M->hd, ly->k_norm, M->eps);
+    jo_rope_inplace(q, qd, M->hd, pos, M->theta);
+    jo_rope_inplace(k, kvd, M->hd, pos, M->theta);
+    float *kring = kv + L * 2 * cap * kvd, *vring = kring + cap * kvd;
+    int64_t slot = pos % cap, active = pos + 1 < cap ? pos + 1 : cap;
+    memcpy(kring + slot * kvd, k, (size_t)kvd * 4);
+    memcpy(vring + slot * kvd, v, (size_t)kvd * 4);
+    rc |= jo_gqa_attention(att, q, kring, vring, M->nq, M->nkv, M->hd, active, 1.0f / sqrtf((float)M->hd));
+    rc |= jo_vec_dot(ly->wo.quant, ly->wo.data, qd, H, att, proj, threads);
+    for (int64_t i = 0; i < H; i++) x[i] += proj[i];
+    jo_rmsnorm(xn, x, ly->ffn_norm, H, M->eps);
+    rc |= jo_vec_dot(ly->w_gate.quant, ly->w_gate.data, H, F, xn, g, threads);
+    rc |= jo_vec_dot(ly->w_up.quant, ly->w_up.data, H, F, xn, u, threads);
+    jo_swiglu(a, g, u, F);
+    rc |= jo_vec_dot(ly->w_down.quant, ly->w_down.data, F, H, a, proj, threads);
+    for (int64_t i = 0; i < H; i++) x[i] += proj[i];
+  }
+  if (!rc) {
+    jo_rmsnorm(xn, x, M->output_norm, H, M->eps);
+    rc = jo_vec_dot(M->output.quant, M->output.data, H, M->vocab, xn, logits, threads);
+  }
+  free(x);
+  free(xn);
+  free(q);
+  free(k);
+  free(v);
+  free(att);
+  free(proj);
+  free(g);
+  free(u);
+  free(a);
+  return rc;
+}

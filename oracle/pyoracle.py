@@ -1,0 +1,262 @@
+"""ctypes front end of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker or the timed CPU baseline.
+The function list, the reference citations and the parity pins are in oracle.h.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, ACT_Q8 = 0, 1, 2, 8, 12, 14, 15, 100
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle` (or __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        P, I64, I32, F = C.c_void_p, C.c_int64, C.c_int, C.c_float
+        sig = {
+            "jo_f16_to_f32": (F, [C.c_uint16]),
+            "jo_f32_to_f16": (C.c_uint16, [F]),
+            "jo_block_elems": (I64, [I32]),
+            "jo_block_bytes": (I64, [I32]),
+            "jo_row_bytes": (I64, [I32, I64]),
+            "jo_act_format": (I32, [I32]),
+            "jo_dequantize_row": (I32, [I32, P, I64, P]),
+            "jo_quantize_act_q8": (None, [P, I64, I64, P]),
+            "jo_quantize_q8_k": (None, [P, I64, I64, P]),
+            "jo_quantize_act": (None, [I32, P, I64, I64, P]),
+            "jo_partials_per_row": (I64, [I32, I64]),
+            "jo_vec_dot_row": (C.c_double, [I32, P, I64, P, P]),
+            "jo_matvec": (I32, [I32, P, I64, I64, P, P, I32]),
+            "jo_vec_dot": (I32, [I32, P, I64, I64, P, P, I32]),
+            "jo_matvec_dequant_f64": (I32, [I32, P, I64, I64, P, P]),
+            "jo_matvec_partials": (I32, [I32, P, I64, I64, P, P]),
+            "jo_gemm": (I32, [I32, P, I64, I64, P, I64, P, I32]),
+            "jo_gemm_i8": (None, [P, I64, P, I64, I64, P]),
+            "jo_gqa_attention": (I32, [P, P, P, P, I32, I32, I32, I64, F]),
+            "jo_rmsnorm": (None, [P, P, P, I64, F]),
+            "jo_rope_inplace": (None, [P, I64, I32, I64, F]),
+            "jo_swiglu": (None, [P, P, P, I64]),
+            "jo_argmax": (I64, [P, I64]),
+            "jo_select_top_k": (I32, [P, I64, I32, I32, P, P]),
+            "jo_swiglu_expert": (I32, [I32, P, I32, P, I32, P, I64, I64, P, P]),
+            "jo_moe_ffn": (I32, [P, I64, I64, I32, I32, P, I32, P, I32, P, I64, I64, P, P, P, P, I32]),
+            "jo_decode_step": (I32, [P, P, I32, I64, P, I32]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p) if a is not None else None
+
+
+def act_format(weight_quant):
+    return lib().jo_act_format(weight_quant)
+
+
+def row_bytes(quant, n):
+    return lib().jo_row_bytes(quant, n)
+
+
+def dequantize(quant, data, rows, k):
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty((rows, k), np.float32)
+    rb = row_bytes(quant, k)
+    for r in range(rows):
+        rc = lib().jo_dequantize_row(quant, C.c_void_p(data.ctypes.data + r * rb), k, _p(out[r]))
+        assert rc == 0
+    return out
+
+
+def quantize_act(act_quant, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = (1, x.shape[0]) if x.ndim == 1 else x.shape
+    out = np.empty(m * row_bytes(act_quant, k), np.uint8)
+    lib().jo_quantize_act(act_quant, _p(x), m, k, _p(out))
+    return out
+
+
+def matvec(quant, w, k, n, xq, threads=1):
+    y = np.empty(n, np.float32)
+    rc = lib().jo_matvec(quant, _p(w), k, n, _p(xq), _p(y), threads)
+    assert rc == 0
+    return y
+
+
+def vec_dot(quant, w, k, n, x, threads=1):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(n, np.float32)
+    rc = lib().jo_vec_dot(quant, _p(w), k, n, _p(x), _p(y), threads)
+    assert rc == 0
+    return y
+
+
+def matvec_f64(quant, w, k, n, xq):
+    y = np.empty(n, np.float64)
+    rc = lib().jo_matvec_dequant_f64(quant, _p(w), k, n, _p(xq), _p(y))
+    assert rc == 0
+    return y
+
+
+def partials(quant, w, k, n, xq):
+    pp = lib().jo_partials_per_row(quant, k)
+    out = np.empty((n, pp), np.int32)
+    rc = lib().jo_matvec_partials(quant, _p(w), k, n, _p(xq), _p(out))
+    assert rc == 0
+    return out
+
+
+def gemm(quant, w, k, n, xq, m, threads=1):
+    y = np.empty((m, n), np.float32)
+    rc = lib().jo_gemm(quant, _p(w), k, n, _p(xq), m, _p(y), threads)
+    assert rc == 0
+    return y
+
+
+def gemm_i8(x, w):
+    x = np.ascontiguousarray(x, dtype=np.int8)
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    m, k = x.shape
+    n = w.shape[0]
+    out = np.empty((m, n), np.int32)
+    lib().jo_gemm_i8(_p(x), m, _p(w), n, k, _p(out))
+    return out
+
+
+def gqa_attention(q, k, v, nq, nkv, hd, seq_len, scale):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.empty(nq * hd, np.float32)
+    rc = lib().jo_gqa_attention(_p(out), _p(q), _p(k), _p(v), nq, nkv, hd, seq_len, scale)
+    assert rc == 0
+    return out
+
+
+def rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().jo_rmsnorm(_p(out), _p(x), _p(w), x.size, eps)
+    return out
+
+
+def rope(x, hd, pos, theta):
+    x = np.array(x, dtype=np.float32, copy=True)
+    lib().jo_rope_inplace(_p(x), x.size, hd, pos, theta)
+    return x
+
+
+def swiglu(g, u):
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    out = np.empty_like(g)
+    lib().jo_swiglu(_p(out), _p(g), _p(u), g.size)
+    return out
+
+
+def argmax(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    r = lib().jo_argmax(_p(x), x.size)
+    return None if r < 0 else int(r)
+
+
+def select_top_k(logits, k, normalize=True):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    idx = np.zeros(max(k, 1), np.int32)
+    w = np.zeros(max(k, 1), np.float32)
+    n = lib().jo_select_top_k(_p(logits), logits.size, k, 1 if normalize else 0, _p(idx), _p(w))
+    return [(int(idx[i]), float(w[i])) for i in range(n)]
+
+
+def moe_ffn(router_logits, top_k, gate, up, down, gq, uq, dq, hidden, ffn, x, threads=1):
+    router_logits = np.ascontiguousarray(router_logits, dtype=np.float32)
+    t, E = router_logits.shape
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(t, hidden)
+    y = np.empty((t, hidden), np.float32)
+    si = np.empty((t, top_k), np.int32)
+    sw = np.empty((t, top_k), np.float32)
+    rc = lib().jo_moe_ffn(_p(router_logits), t, E, top_k, gq, _p(gate), uq, _p(up), dq, _p(down), hidden, ffn,
+                          _p(x), _p(y), _p(si), _p(sw), threads)
+    assert rc == 0
+    return y, si, sw
+
+
+# ---- decode model (jo_model / jo_layer structs) ----
+
+class JoTensor(C.Structure):
+    _fields_ = [("quant", C.c_int), ("data", C.c_void_p)]
+
+
+class JoLayer(C.Structure):
+    _fields_ = [("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p), ("q_norm", C.c_void_p),
+                ("k_norm", C.c_void_p), ("wq", JoTensor), ("wk", JoTensor), ("wv", JoTensor), ("wo", JoTensor),
+                ("w_gate", JoTensor), ("w_up", JoTensor), ("w_down", JoTensor)]
+
+
+class JoModel(C.Structure):
+    _fields_ = [("hidden", C.c_int64), ("ffn", C.c_int64), ("n_layers", C.c_int64), ("vocab", C.c_int64),
+                ("nq", C.c_int), ("nkv", C.c_int), ("hd", C.c_int), ("eps", C.c_float), ("theta", C.c_float),
+                ("kv_capacity", C.c_int64), ("tok_embd", JoTensor), ("output", JoTensor),
+                ("output_norm", C.c_void_p), ("layers", C.c_void_p)]
+
+
+class DecodeModel:
+    """Holds a jo_model over numpy-owned tensors (see tests/model_spec.py for the dict layout)."""
+
+    def __init__(self, spec, tensors, kv_capacity):
+        self._keep = []
+        s = spec
+        nl = s["n_layers"]
+        self.layers = (JoLayer * nl)()
+
+        def t(name):
+            quant, arr = tensors[name]
+            arr = np.ascontiguousarray(arr)
+            self._keep.append(arr)
+            return JoTensor(quant, arr.ctypes.data)
+
+        def f(name):
+            if name not in tensors:
+                return None
+            arr = np.ascontiguousarray(tensors[name][1], dtype=np.float32)
+            self._keep.append(arr)
+            return arr.ctypes.data
+
+        for L in range(nl):
+            p = f"blk.{L}."
+            self.layers[L] = JoLayer(f(p + "attn_norm.weight"), f(p + "ffn_norm.weight"),
+                                     f(p + "attn_q_norm.weight"), f(p + "attn_k_norm.weight"),
+                                     t(p + "attn_q.weight"), t(p + "attn_k.weight"), t(p + "attn_v.weight"),
+                                     t(p + "attn_output.weight"), t(p + "ffn_gate.weight"), t(p + "ffn_up.weight"),
+                                     t(p + "ffn_down.weight"))
+        self.model = JoModel(s["hidden"], s["ffn"], nl, s["vocab"], s["nq"], s["nkv"], s["hd"], s["eps"],
+                             s["theta"], kv_capacity, t("token_embd.weight"), t("output.weight"),
+                             f("output_norm.weight"), C.cast(self.layers, C.c_void_p))
+        self.kv_capacity = kv_capacity
+        self.kvd = s["nkv"] * s["hd"]
+        self.spec = s
+
+    def new_kv(self):
+        return np.zeros((self.spec["n_layers"], 2, self.kv_capacity, self.kvd), np.float32)
+
+    def step(self, kv, token, pos, threads=1):
+        logits = np.empty(self.spec["vocab"], np.float32)
+        rc = lib().jo_decode_step(C.byref(self.model), _p(kv), token, pos, _p(logits), threads)
+        assert rc == 0
+        return logits

@@ -1,0 +1,67 @@
+"""The C ABI without a GPU: the library loads, exports every declared entry point, and
+rejects bad arguments with the K3Error-mirroring status before touching the device."""
+import ctypes as C
+
+import pytest
+
+import jero_hip as J
+
+
+def test_library_exports_every_declared_symbol():
+    lib = J.lib()
+    declared = J.declared_symbols()
+    assert len(declared) >= 8
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert missing == []
+
+
+def test_status_names_mirror_k3error():
+    lib = J.lib()
+    names = {s: lib.jero_hip_status_name(s).decode() for s in (0, 10, 11, 12, 14, 15, 20, 21)}
+    assert names[10] == "CapabilityMismatch"
+    assert names[14] == "TensorBoundsError"
+    assert names[11] == "InsufficientLockableMemory"
+    assert names[15] == "RoutingUnavailable"
+
+
+def test_row_bytes_and_act_formats():
+    assert J.row_bytes(J.Q4_K, 4096) == 16 * 144
+    assert J.row_bytes(J.Q6_K, 4096) == 16 * 210
+    assert J.row_bytes(J.Q8_0, 4096) == 128 * 34
+    assert J.row_bytes(J.Q8_K, 4096) == 16 * 292
+    assert J.row_bytes(J.ACT_Q8, 4096) == 128 * 36
+    assert J.row_bytes(J.Q4_K, 100) == -1
+    assert J.act_format(J.Q4_K) == J.Q8_K and J.act_format(J.Q6_K) == J.Q8_K
+    assert J.act_format(J.Q8_0) == J.ACT_Q8 and J.act_format(J.Q4_0) == J.ACT_Q8
+    assert J.act_format(J.F32) == -1
+
+
+def _matvec(quant, w, nbytes, n_in, n_out, xq, y):
+    return J.lib().jero_hip_matvec(quant, w, nbytes, n_in, n_out, xq, y, None)
+
+
+def test_matvec_argument_errors_before_launch():
+    fake = C.c_void_p(0x10000)  # never dereferenced: every call below fails validation first
+    assert _matvec(J.Q4_K, None, 1 << 20, 256, 4, fake, fake) == 21             # null weights
+    assert _matvec(J.Q4_K, fake, 1 << 20, 0, 4, fake, fake) == 14               # empty input
+    assert _matvec(J.Q4_K, fake, 1 << 20, 256, 0, fake, fake) == 14             # empty output
+    assert _matvec(J.Q4_K, fake, 1 << 20, 100, 4, fake, fake) == 14             # not a block multiple
+    assert _matvec(J.Q4_K, fake, 144 * 4 - 1, 256, 4, fake, fake) == 14         # tensor too small
+    assert _matvec(J.F16, fake, 1 << 20, 256, 4, fake, fake) == 10              # unsupported quant
+    assert _matvec(J.Q4_K, fake, 1 << 30, 256 * 129, 1, fake, fake) == 10       # above the K limit
+    assert _matvec(J.Q4_K, C.c_void_p(0x10002), 1 << 20, 256, 4, fake, fake) == 21  # misaligned
+
+
+def test_k3error_carries_variant_and_message():
+    with pytest.raises(J.K3Error) as ei:
+        J.check(_matvec(J.Q4_K, C.c_void_p(0x10000), 10, 256, 4, C.c_void_p(0x10000), C.c_void_p(0x10000)))
+    assert ei.value.variant == "TensorBoundsError"
+    assert "bytes" in str(ei.value)
+
+
+def test_quantize_argument_errors():
+    lib = J.lib()
+    fake = C.c_void_p(0x10000)
+    assert lib.jero_hip_quantize_act(J.Q4_K, fake, 1, 256, fake, None) == 10
+    assert lib.jero_hip_quantize_act(J.Q8_K, fake, 1, 100, fake, None) == 14
+    assert lib.jero_hip_quantize_act(J.Q8_K, None, 1, 256, fake, None) == 21

@@ -1,0 +1,132 @@
+"""GPU parity of the Q8 activation quantizers and the GEMV family against the oracle.
+
+Bar: activation bytes and int32 partial sums bit-exact; f32 outputs within 1e-5 relative
+to the oracle's f64 result, relative meaning |y - y_ref| / max(|y_ref|, rms(y_ref)).
+"""
+import numpy as np
+import pytest
+import torch
+
+import jero_hip as J
+import pyoracle as O
+from qdata import rand_act, rand_weights
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-5
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def rel_err(y, ref):
+    ref = np.asarray(ref, np.float64)
+    scale = max(float(np.sqrt(np.mean(ref ** 2))), 1e-30)
+    return float(np.max(np.abs(np.asarray(y, np.float64) - ref) / np.maximum(np.abs(ref), scale)))
+
+
+@pytest.mark.parametrize("act,k,m", [(J.ACT_Q8, 32, 1), (J.ACT_Q8, 4096, 1), (J.ACT_Q8, 4096, 7),
+                                     (J.Q8_K, 256, 1), (J.Q8_K, 4096, 1), (J.Q8_K, 12288, 1),
+                                     (J.Q8_K, 4096, 512)])
+def test_quantize_act_bit_exact(dev, act, k, m):
+    print(f"quantize act={act} k={k} m={m}", flush=True)
+    x = rand_act(k, 100 + k + m, m=m)
+    x[0, :32] = 0.0                      # zero block (ACT_Q8) / partly zero (Q8_K)
+    if act == J.Q8_K and m > 1:
+        x[1, :256] = 0.0                 # all-zero Q8_K block
+        x[1, 256 + 5], x[1, 256 + 9] = -3.0, 3.0  # tie of opposite signs: first one wins
+    xd = to_dev(x, dev)
+    q = J.quantize_act(act, xd)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(q.cpu().numpy(), O.quantize_act(act, x))
+
+
+SHAPES = [  # (quant, n_in, n_out)
+    (J.Q4_K, 4096, 4096), (J.Q4_K, 4096, 12288), (J.Q4_K, 12288, 4096), (J.Q4_K, 2048, 768),
+    (J.Q4_K, 256, 77), (J.Q4_K, 768, 33), (J.Q4_K, 32768, 5),
+    (J.Q6_K, 4096, 4096), (J.Q6_K, 768, 2048), (J.Q6_K, 12288, 100), (J.Q6_K, 256, 9), (J.Q6_K, 1280, 3),
+    (J.Q8_0, 4096, 4096), (J.Q8_0, 128, 16), (J.Q8_0, 96, 5), (J.Q8_0, 16384, 7),
+    (J.Q4_0, 4096, 1000), (J.Q4_0, 160, 3),
+]
+
+
+@pytest.mark.parametrize("quant,n_in,n_out", SHAPES)
+def test_matvec_parity(dev, quant, n_in, n_out):
+    print(f"matvec quant={quant} n_in={n_in} n_out={n_out}", flush=True)
+    w = rand_weights(quant, n_out, n_in, quant * 1000 + n_in + n_out, full_range=True)
+    act = J.act_format(quant)
+    x = rand_act(n_in, n_in + n_out)
+    xq = O.quantize_act(act, x)
+    W = J.TensorView("w", quant, [n_in, n_out], to_dev(w, dev))
+    y = torch.empty(n_out, dtype=torch.float32, device=dev)
+    pp = O.lib().jo_partials_per_row(quant, n_in)
+    part = torch.empty((n_out, pp), dtype=torch.int32, device=dev)
+    J.matvec_partials(W, to_dev(xq, dev), y, part)
+    y2 = torch.empty_like(y)
+    J.matvec(W, to_dev(xq, dev), y2)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(part.cpu().numpy(), O.partials(quant, w, n_in, n_out, xq))
+    ref = O.matvec_f64(quant, w, n_in, n_out, xq)
+    assert rel_err(y.cpu().numpy(), ref) < REL_TOL
+    # the partials instantiation and the plain one reduce in the same order
+    assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("quant", [J.Q4_K, J.Q6_K, J.Q8_0, J.Q4_0])
+def test_vec_dot_f32_input_equals_quantize_then_matvec(dev, quant):
+    print(f"vec_dot quant={quant}", flush=True)
+    n_in, n_out = 4096, 300
+    w = rand_weights(quant, n_out, n_in, 7 + quant)
+    x = rand_act(n_in, 8 + quant)
+    W = J.TensorView("w", quant, [n_in, n_out], to_dev(w, dev))
+    xd = to_dev(x, dev)
+    y = torch.empty(n_out, dtype=torch.float32, device=dev)
+    {J.Q4_K: J.vec_dot_q4_k_m, J.Q6_K: J.vec_dot_q6_k, J.Q8_0: J.vec_dot_q8_0, J.Q4_0: J.vec_dot_q4_0}[quant](y, W, xd)
+    ws = torch.empty(J.row_bytes(J.act_format(quant), n_in), dtype=torch.uint8, device=dev)
+    y2 = torch.empty_like(y)
+    J.matvec_any(y2, W, xd, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    ref = O.vec_dot(quant, w, n_in, n_out, x)
+    assert rel_err(y.cpu().numpy(), ref) < REL_TOL
+
+
+def test_row_slices_are_bitwise_identical(dev):
+    """Partition invariance: any row slice reproduces the full GEMV bit for bit
+    (tests/wave1_engine_regression_test.rs:1286-1295)."""
+    n_in, n_out = 4096, 12288
+    w = rand_weights(J.Q4_K, n_out, n_in, 77)
+    W = J.TensorView("w", J.Q4_K, [n_in, n_out], to_dev(w, dev))
+    xq = to_dev(O.quantize_act(J.Q8_K, rand_act(n_in, 78)), dev)
+    y = torch.empty(n_out, dtype=torch.float32, device=dev)
+    J.matvec(W, xq, y)
+    for start, cnt in [(0, 16), (5, 2048), (4096, 1), (12000, 288)]:
+        ys = torch.empty(cnt, dtype=torch.float32, device=dev)
+        J.matvec(W.slice_rows(start, cnt), xq, ys)
+        torch.cuda.synchronize()
+        assert torch.equal(ys, y[start:start + cnt])
+
+
+def test_wrong_quant_and_empty_raise(dev):
+    W = J.TensorView("blk.0.attn_q.weight", J.Q6_K, [256, 4],
+                     torch.zeros(4 * 210, dtype=torch.uint8, device=dev))
+    x = torch.zeros(256, dtype=torch.float32, device=dev)
+    with pytest.raises(J.K3Error) as ei:
+        J.vec_dot_q4_k_m(torch.empty(4, device=dev), W, x)
+    assert ei.value.variant == "CapabilityMismatch"
+    with pytest.raises(J.K3Error) as ei:
+        J.matvec_any(torch.empty(0, device=dev), W, x)
+    assert ei.value.variant == "TensorBoundsError"
+
+
+def test_dequantize_rows_matches_oracle(dev):
+    for quant, k in [(J.Q4_K, 512), (J.Q6_K, 768), (J.Q8_0, 96), (J.Q4_0, 64)]:
+        print(f"dequant quant={quant}", flush=True)
+        w = rand_weights(quant, 6, k, 300 + quant)
+        W = J.TensorView("w", quant, [k, 6], to_dev(w, dev))
+        out = torch.empty((3, k), dtype=torch.float32, device=dev)
+        J.dequantize_rows(W, 2, 3, out)
+        torch.cuda.synchronize()
+        ref = O.dequantize(quant, w, 6, k)[2:5]
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-6, atol=1e-7)

@@ -1,0 +1,377 @@
+"""Pins the CPU oracle (oracle/liboracle.so) before it is trusted as the checker.
+
+Each function of the oracle is held here to something other than its own formula:
+the reference's known-answer tests, the reference's golden llama logits, an independent
+numpy restatement (oracle/ref_numpy.py), f64/brute-force evaluation and closed-form
+invariants.  Reference citations are given per test.
+"""
+import math
+import struct
+
+import numpy as np
+import pytest
+
+import pyoracle as O
+import ref_numpy as R
+from qdata import rand_act, rand_weights
+
+WEIGHT_FORMATS = [O.Q8_0, O.Q4_0, O.Q4_K, O.Q6_K]
+
+
+# ---------------------------------------------------------------- f16 conversion
+
+def test_f16_to_f32_all_halves():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([O.lib().jo_f16_to_f32(int(b)) for b in bits[::7]], np.float32)
+    r = ref[::7]
+    same = (got == r) | (np.isnan(got) & np.isnan(r))
+    assert same.all()
+
+
+def test_f32_to_f16_round_to_nearest_even():
+    rng = np.random.default_rng(3)
+    vals = np.concatenate([rng.standard_normal(4000) * 10.0 ** rng.integers(-9, 5, 4000),
+                           np.array([65504.0, 65520.0, 65519.99, 6e-8, 3e-8, 2.98e-8, 0.0, -0.0])]).astype(np.float32)
+    # exact ties: half-way between two halves
+    ties = (np.arange(1, 200, dtype=np.float32) * 2 + 1) * np.float32(2.0 ** -11)
+    vals = np.concatenate([vals, ties, -ties])
+    got = np.array([O.lib().jo_f32_to_f16(float(v)) for v in vals], np.uint16)
+    with np.errstate(over="ignore"):
+        ref = vals.astype(np.float16).view(np.uint16)
+    assert (got == ref).all()
+
+
+# ---------------------------------------------------------------- formats: reference KATs
+
+def test_q8_0_row_kat():
+    """src/gemma.rs:1627-1645: Q8_0 row of q=2 with f16 scale 1.0 (0x3C00) dequantizes to 2.0."""
+    row = bytes([0x00, 0x3C]) + bytes([2] * 32) + bytes([0x00, 0x3C]) + bytes([2] * 32)
+    out = O.dequantize(O.Q8_0, np.frombuffer(row, np.uint8), 1, 64)
+    assert np.all(np.abs(out - 2.0) < 1e-5)
+
+
+def test_q4_0_row_kat():
+    """src/gemma.rs:1647-1662: Q4_0 scale 0.5 (0x3800), nibbles 0xAA -> (10 - 8) * 0.5 = 1.0."""
+    row = bytes([0x00, 0x38]) + bytes([0xAA] * 16)
+    out = O.dequantize(O.Q4_0, np.frombuffer(row, np.uint8), 1, 32)
+    assert np.all(np.abs(out - 1.0) < 1e-5)
+
+
+def test_block_byte_sizes():
+    """Q4_K [256, 2] is 288 B (src/weights.rs:1208); Q6_K 210 B; Q8_0 34 B; Q8_K 292 B."""
+    assert O.row_bytes(O.Q4_K, 256) * 2 == 288
+    assert O.row_bytes(O.Q6_K, 256) == 210
+    assert O.row_bytes(O.Q8_0, 32) == 34
+    assert O.row_bytes(O.Q8_K, 256) == 292
+    assert O.row_bytes(O.ACT_Q8, 32) == 36
+    assert O.row_bytes(O.Q4_K, 100) == -1
+
+
+def test_q4_k_header_and_q6_k_scale_positions():
+    """Q4_K d/dmin at bytes 0-3 and Q6_K d at bytes 208-209
+    (tests/wave1_engine_regression_test.rs:250-282): zeroing exactly those bytes zeroes the row
+    (Q4_K) / the whole block (Q6_K)."""
+    w = rand_weights(O.Q4_K, 1, 256, 1)
+    w[0:4] = 0
+    assert np.all(O.dequantize(O.Q4_K, w, 1, 256) == 0)
+    w = rand_weights(O.Q4_K, 1, 256, 1)
+    w[2:4] = 0  # dmin = 0: values are d*sc*q >= 0
+    assert np.all(O.dequantize(O.Q4_K, w, 1, 256) >= 0)
+    w = rand_weights(O.Q6_K, 1, 256, 2)
+    w[208:210] = 0
+    assert np.all(O.dequantize(O.Q6_K, w, 1, 256) == 0)
+
+
+@pytest.mark.parametrize("quant", WEIGHT_FORMATS)
+def test_dequant_matches_numpy_restatement(quant):
+    k, rows = 512, 9
+    w = rand_weights(quant, rows, k, 10 + quant, full_range=True)
+    a = O.dequantize(quant, w, rows, k)
+    b = R.dequantize(quant, w, rows, k)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_q4_k_single_element_closed_form():
+    """One hand-built Q4_K block: sub-block 5 (j >= 4 path of the 6-bit packing)."""
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    # sub-block 5: sc = (s[9] & 15) | ((s[1] >> 6) << 4), m = (s[9] >> 4) | ((s[5] >> 6) << 4)
+    blk[4 + 9] = 0x3A     # sc low 4 = 10, m low 4 = 3
+    blk[4 + 1] = 0x80     # sc high 2 bits = 2  -> sc = 10 | 32 = 42
+    blk[4 + 5] = 0x40     # m high 2 bits = 1   -> m = 3 | 16 = 19
+    # element 64*2 + 32 + 7 = 167 is the high nibble of qs[32*2 + 7]
+    blk[16 + 64 + 7] = 0xB0  # high nibble 11
+    y = O.dequantize(O.Q4_K, blk, 1, 256)[0]
+    assert y[167] == pytest.approx(0.5 * 42 * 11 - 0.25 * 19)
+    assert y[160] == pytest.approx(-0.25 * 19)  # same sub-block, q = 0
+
+
+def test_q6_k_single_element_closed_form():
+    blk = np.zeros(210, np.uint8)
+    blk[208:210] = np.frombuffer(np.float16(0.125).tobytes(), np.uint8)
+    # element 128 + 64 + 5 (half 1, third quarter): ql[64 + 5] >> 4, qh[32 + 5] bits 4-5, scale 8 + 4 + 0
+    blk[64 + 5] = 0x90        # high nibble 9
+    blk[128 + 32 + 5] = 0x20  # bits 4-5 = 2 -> q = 9 | 32 = 41 -> 41 - 32 = 9
+    blk[192 + 12] = np.uint8(np.int8(-3).view(np.uint8))
+    y = O.dequantize(O.Q6_K, blk, 1, 256)[0]
+    assert y[197] == pytest.approx(0.125 * -3 * 9)
+
+
+# ---------------------------------------------------------------- activation quantizers
+
+@pytest.mark.parametrize("k", [32, 256, 4096])
+def test_act_q8_matches_numpy(k):
+    x = rand_act(k, 5, m=3)
+    x[0, :32] = 0.0  # an all-zero block
+    a = O.quantize_act(O.ACT_Q8, x)
+    b = np.concatenate([R.quantize_act_q8(r) for r in x])
+    np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("k", [256, 4096, 12288])
+def test_q8_k_matches_numpy(k):
+    x = rand_act(k, 6, m=2)
+    x[1, :256] = 0.0
+    a = O.quantize_act(O.Q8_K, x)
+    b = np.concatenate([R.quantize_q8_k(r) for r in x])
+    np.testing.assert_array_equal(a, b)
+
+
+def test_q8_k_invariants():
+    x = rand_act(4096, 7)
+    q = O.quantize_act(O.Q8_K, x).reshape(16, 292)
+    qs = q[:, 4:260].view(np.int8).astype(np.int32)
+    bs = q[:, 260:].copy().view(np.int16).astype(np.int32)
+    d = q[:, :4].copy().view(np.float32).reshape(-1)
+    assert np.all(bs == qs.reshape(16, 16, 16).sum(axis=2))
+    assert np.all(np.abs(qs) <= 127)
+    assert np.all(np.abs(qs).max(axis=1) == 127)
+    err = np.abs(qs * d[:, None] - x.reshape(16, 256))
+    assert np.all(err <= np.abs(d)[:, None] * 0.5 + 1e-6)
+
+
+def test_q8_k_tie_takes_first_index_sign():
+    """Equal magnitudes of opposite sign: the first one sets the sign of d (ggml strict >)."""
+    # iscale = -127 / max maps the chosen element to -127, so d has the opposite sign of it
+    x = np.zeros(256, np.float32)
+    x[3], x[10] = -2.0, 2.0
+    q = O.quantize_act(O.Q8_K, x)
+    d = q[:4].copy().view(np.float32)[0]
+    qs = q[4:260].view(np.int8)
+    assert d > 0 and qs[3] == -127 and qs[10] == 127
+    x[3], x[10] = 2.0, -2.0
+    q = O.quantize_act(O.Q8_K, x)
+    d = q[:4].copy().view(np.float32)[0]
+    qs = q[4:260].view(np.int8)
+    assert d < 0 and qs[3] == -127 and qs[10] == 127
+
+
+def test_act_q8_round_half_even():
+    """ACT_Q8 rounds ties to even: 127 * (k + 0.5) / 127 lands exactly half-way."""
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1], x[2], x[3] = 2.5, 3.5, -2.5
+    q = O.quantize_act(O.ACT_Q8, x)
+    assert q[:4].copy().view(np.float32)[0] == np.float32(1.0)
+    assert list(q[4:8].view(np.int8)) == [127, 2, 4, -2]
+
+
+# ---------------------------------------------------------------- dot products
+
+@pytest.mark.parametrize("quant", WEIGHT_FORMATS)
+def test_partials_match_integer_brute_force(quant):
+    k, rows = 1024, 7
+    w = rand_weights(quant, rows, k, 20 + quant, full_range=True)
+    act = O.act_format(quant)
+    xq = O.quantize_act(act, rand_act(k, 21))
+    got = O.partials(quant, w, k, rows, xq)
+    ref = R.partials(quant, w, rows, k, act, xq)
+    np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("quant", WEIGHT_FORMATS)
+def test_matvec_matches_dequant_f64(quant):
+    k, rows = 2048, 33
+    w = rand_weights(quant, rows, k, 30 + quant)
+    act = O.act_format(quant)
+    xq = O.quantize_act(act, rand_act(k, 31))
+    y = O.matvec(quant, w, k, rows, xq, threads=4)
+    # independent: numpy dequantization of both operands, f64 dot
+    wd = R.dequantize(quant, w, rows, k).astype(np.float64)
+    xd = R.dequantize(act, xq, 1, k)[0].astype(np.float64)
+    ref = wd @ xd
+    scale = max(np.sqrt(np.mean(ref ** 2)), 1e-30)
+    assert np.max(np.abs(y - ref) / np.maximum(np.abs(ref), scale)) < 1e-6
+
+
+def test_matvec_partition_invariance():
+    """Row results do not depend on the thread partition (src/gemma.rs:114-134,
+    tests/wave1_engine_regression_test.rs:1286-1295)."""
+    k, rows = 1024, 300
+    w = rand_weights(O.Q4_K, rows, k, 40)
+    xq = O.quantize_act(O.Q8_K, rand_act(k, 41))
+    ys = [O.matvec(O.Q4_K, w, k, rows, xq, threads=t) for t in (1, 3, 8)]
+    for y in ys[1:]:
+        np.testing.assert_array_equal(ys[0], y)
+
+
+def test_zero_scale_rows_are_exact_zero():
+    """Rows with d = 0 give exactly 0.0 (the golden logits 0..4 are exactly 0.0)."""
+    k = 256
+    w = rand_weights(O.Q8_0, 2, k, 50).reshape(2, -1)
+    w[0].reshape(-1, 34)[:, 0:2] = 0
+    xq = O.quantize_act(O.ACT_Q8, rand_act(k, 51))
+    y = O.matvec(O.Q8_0, w.reshape(-1), k, 2, xq)
+    assert y[0] == 0.0 and y[1] != 0.0
+
+
+def test_gemm_i8_brute_force():
+    rng = np.random.default_rng(60)
+    x = rng.integers(-128, 128, (17, 96)).astype(np.int8)
+    w = rng.integers(-128, 128, (23, 96)).astype(np.int8)
+    np.testing.assert_array_equal(O.gemm_i8(x, w), x.astype(np.int32) @ w.astype(np.int32).T)
+
+
+def test_gemm_rows_equal_gemv():
+    k, n, m = 512, 40, 5
+    w = rand_weights(O.Q6_K, n, k, 61)
+    x = rand_act(k, 62, m=m)
+    xq = O.quantize_act(O.Q8_K, x)
+    y = O.gemm(O.Q6_K, w, k, n, xq, m)
+    rb = O.row_bytes(O.Q8_K, k)
+    for i in range(m):
+        np.testing.assert_array_equal(y[i], O.matvec(O.Q6_K, w, k, n, xq[i * rb:(i + 1) * rb]))
+
+
+# ---------------------------------------------------------------- elementwise, attention
+
+def test_dot_product_kat():
+    """kernels_rvv_wired KAT [2] . [3] = 6 (src/lib.rs:380-387), through an F32-free path:
+    a Q8_0 row with d=1 and q=2 against activations 3 quantized to ACT_Q8."""
+    row = np.frombuffer(bytes([0x00, 0x3C]) + bytes([2] + [0] * 31), np.uint8)
+    x = np.zeros(32, np.float32)
+    x[0] = 3.0
+    xq = O.quantize_act(O.ACT_Q8, x)
+    assert O.matvec(O.Q8_0, row, 32, 1, xq)[0] == pytest.approx(6.0, rel=1e-6)
+
+
+def test_rmsnorm_closed_form():
+    x = np.array([3.0, 4.0], np.float32)
+    w = np.array([1.0, 2.0], np.float32)
+    y = O.rmsnorm(x, w, 0.0)
+    s = 1.0 / math.sqrt((9 + 16) / 2)
+    np.testing.assert_allclose(y, [3 * s, 8 * s], rtol=1e-6)
+
+
+def test_rope_interleaved_pairs():
+    """Interleaved pairs (2i, 2i+1) rotated by pos / theta^(2i/hd)
+    (tests/wave1_engine_regression_test.rs:698-712); pos 0 is the identity; norms kept."""
+    rng = np.random.default_rng(70)
+    x = rng.standard_normal(2 * 8).astype(np.float32)
+    np.testing.assert_array_equal(O.rope(x, 8, 0, 10000.0), x)
+    y = O.rope(x, 8, 5, 10000.0)
+    xp, yp = x.reshape(-1, 2), y.reshape(-1, 2)
+    np.testing.assert_allclose(np.linalg.norm(yp, axis=1), np.linalg.norm(xp, axis=1), rtol=1e-5)
+    # pair 1 of head 0: angle = 5 / 10000^(2/8)
+    a = 5.0 / 10000.0 ** 0.25
+    c, s = math.cos(a), math.sin(a)
+    assert y[2] == pytest.approx(x[2] * c - x[3] * s, rel=1e-5)
+    assert y[3] == pytest.approx(x[2] * s + x[3] * c, rel=1e-5)
+
+
+def test_swiglu_closed_form():
+    g = np.array([0.0, 1.0, -2.0], np.float32)
+    u = np.array([5.0, 2.0, 3.0], np.float32)
+    ref = [0.0, 2.0 / (1 + math.exp(-1.0)), 3.0 * -2.0 / (1 + math.exp(2.0))]
+    np.testing.assert_allclose(O.swiglu(g, u), ref, rtol=1e-6)
+
+
+def test_attention_brute_force_and_special_cases():
+    rng = np.random.default_rng(80)
+    nq, nkv, hd, T = 8, 2, 16, 37
+    q = rng.standard_normal(nq * hd).astype(np.float32)
+    k = rng.standard_normal((T, nkv * hd)).astype(np.float32)
+    v = rng.standard_normal((T, nkv * hd)).astype(np.float32)
+    out = O.gqa_attention(q, k, v, nq, nkv, hd, T, 0.25)
+    ref = np.zeros(nq * hd)
+    for h in range(nq):
+        kh = h // (nq // nkv)
+        s = k[:, kh * hd:(kh + 1) * hd].astype(np.float64) @ q[h * hd:(h + 1) * hd] * 0.25
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        ref[h * hd:(h + 1) * hd] = p @ v[:, kh * hd:(kh + 1) * hd]
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+    # one position: output equals that V row; identical keys: output is the mean of V
+    out1 = O.gqa_attention(q, k[:1], v[:1], nq, nkv, hd, 1, 0.25)
+    np.testing.assert_allclose(out1.reshape(nq, hd), np.repeat(v[0].reshape(nkv, hd), nq // nkv, axis=0), rtol=1e-6)
+    ksame = np.repeat(k[:1], T, axis=0)
+    outm = O.gqa_attention(q, ksame, v, nq, nkv, hd, T, 0.25)
+    np.testing.assert_allclose(outm.reshape(nq, hd),
+                               np.repeat(v.mean(axis=0).reshape(nkv, hd), nq // nkv, axis=0), rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- argmax, routing KATs
+
+def test_argmax_kats():
+    """src/engine.rs:2677-2727."""
+    nan, ninf = float("nan"), float("-inf")
+    assert O.argmax(np.array([], np.float32)) is None
+    assert O.argmax(np.full(1024, nan, np.float32)) is None
+    assert O.argmax(np.array([nan, 3.5, nan, 2.0], np.float32)) == 1
+    assert O.argmax(np.array([ninf, ninf], np.float32)) == 0
+    for n in (32768, 65537, 256000):
+        x = np.array([-100.0 - (i % 97) for i in range(n)], np.float32)
+        x[n - 17] = -0.25
+        x[0] = ninf
+        assert O.argmax(x) == n - 17
+        t = np.full(n, 1.25, np.float32)
+        t[0] = nan
+        t[103] = 42.5
+        t[n // 2 + 11] = 42.5
+        t[n - 1] = nan
+        assert O.argmax(t) == 103
+
+
+def test_select_top_k_kats():
+    """src/gemma.rs:1722-1740."""
+    tied = np.array([0.1, 3.0, 0.5, 1.0, 3.0, 2.0], np.float32)
+    top2 = O.select_top_k(tied, 2, True)
+    assert [i for i, _ in top2] == [1, 4]
+    assert abs(top2[0][1] - 0.5) < 1e-6 and abs(top2[1][1] - 0.5) < 1e-6
+    raw = O.select_top_k(tied, 2, False)
+    assert raw[0][1] + raw[1][1] < 0.99
+    assert O.select_top_k(np.array([], np.float32), 2, True) == []
+    assert O.select_top_k(tied, 0, True) == []
+
+
+def test_select_top_k_softmax_values_and_nonfinite():
+    logits = np.array([1.0, float("nan"), 2.0, float("inf"), 0.5], np.float32)
+    sel = O.select_top_k(logits, 3, False)
+    fin = np.array([1.0, 2.0, 0.5])
+    p = np.exp(fin - fin.max()) / np.exp(fin - fin.max()).sum()
+    assert [i for i, _ in sel] == [2, 0, 4]
+    np.testing.assert_allclose([w for _, w in sel], [p[1], p[0], p[2]], rtol=1e-6)
+
+
+def test_moe_ffn_matches_dense_composition():
+    """dispatch_qwen3_moe_ffn (src/qwen_deepseek.rs:847-951): y = sum_k w_k expert_k(x)."""
+    H, F, E, K = 256, 512, 6, 2
+    gate = rand_weights(O.Q4_K, E * F, H, 90)
+    up = rand_weights(O.Q4_K, E * F, H, 91)
+    down = rand_weights(O.Q6_K, E * H, F, 92)
+    x = rand_act(H, 93, m=2)
+    logits = rand_act(E, 94, m=2)
+    y, si, sw = O.moe_ffn(logits, K, gate, up, down, O.Q4_K, O.Q4_K, O.Q6_K, H, F, x, threads=2)
+    for t in range(2):
+        sel = O.select_top_k(logits[t], K, True)
+        ref = np.zeros(H, np.float32)
+        for e, wgt in sel:
+            g = O.vec_dot(O.Q4_K, gate[e * F * 144:(e + 1) * F * 144], H, F, x[t])
+            u = O.vec_dot(O.Q4_K, up[e * F * 144:(e + 1) * F * 144], H, F, x[t])
+            a = O.swiglu(g, u)
+            rb = O.row_bytes(O.Q6_K, F)
+            ref += np.float32(wgt) * O.vec_dot(O.Q6_K, down[e * H * rb:(e + 1) * H * rb], F, H, a)
+        np.testing.assert_allclose(y[t], ref, rtol=1e-6, atol=1e-7)
+        assert list(si[t]) == [e for e, _ in sel]

@@ -42,6 +42,7 @@ typedef enum jero_quant {
   JERO_Q4_K = 12, /* the reference's QuantType::Q4_K_M */
   JERO_Q6_K = 14,
   JERO_Q8_K = 15,  /* activation blocks for Q4_K / Q6_K weights: f32 d, i8 q[256], i16 bsums[16] */
+  JERO_Q6_K_R = 114, /* Q6_K bytes re-laid out by jero_hip_repack into aligned planes (same size) */
   JERO_ACT_Q8 = 100 /* activation blocks for Q8_0 / Q4_0 weights: f32 d, i8 q[32] (36 B) */
 } jero_quant;
 
@@ -83,6 +84,15 @@ int jero_hip_vec_dot(int quant, const void *w_dev, size_t w_bytes, int64_t n_in,
  * the bit-exact tests; y_dev receives the same outputs as jero_hip_matvec. */
 int jero_hip_matvec_partials(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
                              const void *xq_dev, float *y_dev, int32_t *partials_dev, void *stream);
+
+/* Load-time re-layout of a weight tensor for the GEMV kernels; replaces repack_tensor_parallel
+ * (src/weights.rs:914-955) -> RepackedWeight.  Q6_K -> JERO_Q6_K_R: the n_out x n_in tensor's
+ * bytes are regrouped into 16-byte aligned planes of the same total size (src and dst may not
+ * overlap).  The result is passed to jero_hip_matvec / _partials / _vec_dot as quant
+ * JERO_Q6_K_R with the same n_in and n_out; it must be used whole (its rows are not contiguous).
+ * Other formats: CapabilityMismatch. */
+int jero_hip_repack(int quant, const void *src_dev, size_t src_bytes, int64_t n_in, int64_t n_out,
+                    void *dst_dev, int *dst_quant, void *stream);
 
 /* dequantize_token_row (src/qwen_deepseek.rs:514,569): rows [row0, row0+n_rows) of a tensor
  * with n_in elements per row, written as f32 to out_dev[n_rows][n_in]. */

@@ -6,12 +6,15 @@
 //     units c, c+LPR, ..., up to UPL of them, and keeps their activation slice in registers
 //     for the whole kernel, so the activation is read once per wave, never per row.
 //   * 64/LPR rows are reduced side by side (one per lane group) and R such row groups per
-//     wave: all R*UPL weight loads (16-byte, dword-aligned) are issued before any math so a
-//     lane has R*UPL*48 bytes in flight.
+//     wave: all R*UPL weight loads (16-byte, dword-aligned) are issued before any math.
+//   * For long rows (>= 8192 elements) the workgroup first copies the quantized activation
+//     into LDS with 16-byte loads issued ahead of the weight loads, and each lane takes its
+//     slice from LDS: one activation read per workgroup instead of one per wave.
 //   * Integer partial sums per sub-block are exact (v_dot4_i32_i8); each lane folds its
-//     units to one f32 and the row total is a butterfly over the LPR lanes.
-// Each row is reduced by exactly one lane group: the result is independent of the grid, as
-// matvec_any's results are independent of its row partitioning.
+//     units to one f32 and the row total is a DPP butterfly over the LPR lanes.
+// Each row is reduced by exactly one lane group in a fixed order that depends only on n_in:
+// the result is independent of the grid, as matvec_any's results are independent of its row
+// partitioning.
 #include "gemv.h"
 
 #include "gemv_dot.h"
@@ -20,37 +23,77 @@
 
 namespace jero {
 
-template <int F, int LPR, int UPL, int R, bool PART>
-__global__ void __launch_bounds__(256) gemv_kernel(const uint8_t* __restrict__ w, int64_t rb, int U, int64_t N,
-                                                   const uint8_t* __restrict__ xq, float* __restrict__ y,
-                                                   int32_t* __restrict__ part, int64_t ppr) {
+constexpr int kGemvThreads = 256;
+
+template <int F, int LPR, int UPL, int R, bool PART, bool LDS_ACT>
+__global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const uint8_t* __restrict__ w, int64_t rb, int U,
+                                                             int64_t N, const uint8_t* __restrict__ xq,
+                                                             int act_bytes, float* __restrict__ y,
+                                                             int32_t* __restrict__ part, int64_t ppr) {
   using Ut = Unit<F>;
   constexpr int G = kWave / LPR;
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_act[];
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t wave = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
   const int g = lane / LPR, c = lane % LPR;
   const int64_t row0 = wave * (G * R);
-  if (row0 >= N) return;
 
+  // 1. activation copy into registers first (its loads retire before the weight loads)
+  constexpr int kMaxChunks = 10;  // 16-byte chunks per thread: up to 40 KB of activation
+  u32x4 av[LDS_ACT ? kMaxChunks : 1];
+  const int n16 = act_bytes >> 4;
+  if constexpr (LDS_ACT) {
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; i++) {
+      const int ch = threadIdx.x + kGemvThreads * i;
+      if (ch < n16) av[i] = ld4(xq + 16 * ch);
+    }
+  } else {
+    if (row0 >= N) return;
+  }
+
+  // 2. weight loads for all rows of the wave
   typename Ut::W wt[R][UPL];
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int64_t row = row0 + r * G + g;
-    const uint8_t* rp = w + (row < N ? row : 0) * rb;
 #pragma unroll
     for (int t = 0; t < UPL; t++) {
       const int u = c + LPR * t;
-      if (row < N && u < U) Ut::load_w(wt[r][t], rp, u);
+      if (row < N && u < U) {
+        if constexpr (F == JERO_Q6_K_R)
+          Ut::load_w_planar(wt[r][t], w, N, U, row, u);
+        else
+          Ut::load_w(wt[r][t], w + row * rb, u);
+      }
     }
   }
 
+  // 3. activation slice: from LDS (staged once per workgroup) or straight from global
+  const uint8_t* act_src = xq;
+  if constexpr (LDS_ACT) {
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; i++) {
+      const int ch = threadIdx.x + kGemvThreads * i;
+      if (ch < n16) *reinterpret_cast<u32x4*>(s_act + 16 * ch) = av[i];
+    }
+    for (int d = 4 * n16 + threadIdx.x; d < act_bytes / 4; d += kGemvThreads)
+      reinterpret_cast<uint32_t*>(s_act)[d] = reinterpret_cast<const uint32_t*>(xq)[d];
+    // Wait for this wave's LDS writes only (not its weight loads), then the workgroup barrier.
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt untouched
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (row0 >= N) return;
+    act_src = s_act;
+  }
   typename Ut::Act act[UPL];
 #pragma unroll
   for (int t = 0; t < UPL; t++) {
     const int u = c + LPR * t;
-    if (u < U) Ut::load_act(act[t], xq, u);
+    if (u < U) Ut::load_act(act[t], act_src, u);
   }
 
+  // 4. per-row dot products, DPP reduction over the row's lanes
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int64_t row = row0 + r * G + g;
@@ -69,79 +112,132 @@ __global__ void __launch_bounds__(256) gemv_kernel(const uint8_t* __restrict__ w
         }
       }
     }
-    acc = group_sum<LPR>(acc);
-    if (c == 0 && row < N) y[row] = acc;
+    acc = group_sum_last<LPR>(acc);
+    if (c == LPR - 1 && row < N) y[row] = acc;
   }
 }
 
 namespace {
 
-template <int F, int LPR, int UPL, int R, bool PART>
-void launch_one(const uint8_t* w, int64_t rb, int U, int64_t N, const uint8_t* xq, float* y, int32_t* part,
-                int64_t ppr, hipStream_t stream) {
+struct Launch {
+  const uint8_t* w;
+  int64_t rb;
+  int U;
+  int64_t N;
+  const uint8_t* xq;
+  int act_bytes;
+  float* y;
+  int32_t* part;
+  int64_t ppr;
+  hipStream_t s;
+};
+
+template <int F, int LPR, int UPL, int R, bool PART, bool LDS>
+void launch_one(const Launch& L) {
   constexpr int G = kWave / LPR;
-  int64_t waves = (N + G * R - 1) / (G * R);
-  int64_t blocks = (waves + 3) / 4;
-  hipLaunchKernelGGL((gemv_kernel<F, LPR, UPL, R, PART>), dim3(unsigned(blocks)), dim3(256), 0, stream, w, rb, U,
-                     N, xq, y, part, ppr);
+  int64_t waves = (L.N + G * R - 1) / (G * R);
+  int64_t blocks = (waves + kGemvThreads / kWave - 1) / (kGemvThreads / kWave);
+  size_t shm = LDS ? size_t((L.act_bytes + 15) & ~15) : 0;
+  hipLaunchKernelGGL((gemv_kernel<F, LPR, UPL, R, PART, LDS>), dim3(unsigned(blocks)), dim3(kGemvThreads), shm, L.s,
+                     L.w, L.rb, L.U, L.N, L.xq, L.act_bytes, L.y, L.part, L.ppr);
 }
 
-template <int F, int LPR, int UPL, bool PART>
-void launch_r(int R, const uint8_t* w, int64_t rb, int U, int64_t N, const uint8_t* xq, float* y, int32_t* part,
-              int64_t ppr, hipStream_t s) {
+template <int F, int LPR, int UPL, bool PART, bool LDS>
+void launch_r(int R, const Launch& L) {
   if constexpr (PART) {
-    launch_one<F, LPR, UPL, 1, true>(w, rb, U, N, xq, y, part, ppr, s);
+    launch_one<F, LPR, UPL, 1, true, LDS>(L);
   } else {
     if (R >= 4)
-      launch_one<F, LPR, UPL, 4, false>(w, rb, U, N, xq, y, part, ppr, s);
+      launch_one<F, LPR, UPL, 4, false, LDS>(L);
     else if (R == 2)
-      launch_one<F, LPR, UPL, 2, false>(w, rb, U, N, xq, y, part, ppr, s);
+      launch_one<F, LPR, UPL, 2, false, LDS>(L);
     else
-      launch_one<F, LPR, UPL, 1, false>(w, rb, U, N, xq, y, part, ppr, s);
+      launch_one<F, LPR, UPL, 1, false, LDS>(L);
   }
 }
 
+template <int F, int UPL, bool PART>
+void launch_upl(int R, bool lds, const Launch& L) {
+  if (lds)
+    launch_r<F, 64, UPL, PART, true>(R, L);
+  else
+    launch_r<F, 64, UPL, PART, false>(R, L);
+}
+
 template <int F, bool PART>
-int launch_fmt(const uint8_t* w, int64_t k, int64_t N, const uint8_t* xq, float* y, int32_t* part,
-               hipStream_t s) {
-  const int64_t rb = row_bytes(F, k);
-  const int U = units_per_row(F, k);
-  const int64_t ppr = partials_per_row(F, k);
+int launch_fmt(const uint8_t* w, int64_t k, int64_t N, const uint8_t* xq, float* y, int32_t* part, hipStream_t s) {
+  Launch L{w, row_bytes(F, k), units_per_row(F, k), N, xq, int(row_bytes(act_format(F), k)), y, part,
+           partials_per_row(F, k), s};
+  const int U = L.U;
   int lpr = U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4;
   int upl = (U + lpr - 1) / lpr;
   int G = kWave / lpr;
-  // Rows per wave: enough waves to cover ~8 per CU first, then deepen the per-lane queue.
+  // Rows per wave: measured on MI355X, two rows per wave is best up to ~12K rows of 4096
+  // and four for the 150K-row output head; long rows (K >= 8192) run one row per wave with
+  // the activation staged in LDS.
   const int cus = device_info().cus;
   int64_t groups = (N + G - 1) / G;
-  int R = groups >= int64_t(cus) * 8 * 4 ? 4 : groups >= int64_t(cus) * 8 * 2 ? 2 : 1;
+  int R = groups >= int64_t(cus) * 64 ? 4 : groups >= int64_t(cus) * 8 ? 2 : 1;
+  bool lds = k >= 8192;
+  if (lds) R = 1;
   if (lpr == 4) {
-    launch_r<F, 4, 1, PART>(R, w, rb, U, N, xq, y, part, ppr, s);
+    launch_r<F, 4, 1, PART, false>(R, L);
   } else if (lpr == 16) {
-    launch_r<F, 16, 1, PART>(R, w, rb, U, N, xq, y, part, ppr, s);
+    launch_r<F, 16, 1, PART, false>(R, L);
   } else if (lpr == 32) {
-    launch_r<F, 32, 1, PART>(R, w, rb, U, N, xq, y, part, ppr, s);
+    launch_r<F, 32, 1, PART, false>(R, L);
   } else {
     switch (upl) {
-      case 1: launch_r<F, 64, 1, PART>(R, w, rb, U, N, xq, y, part, ppr, s); break;
-      case 2: launch_r<F, 64, 2, PART>(R, w, rb, U, N, xq, y, part, ppr, s); break;
-      case 3: launch_r<F, 64, 3, PART>(R, w, rb, U, N, xq, y, part, ppr, s); break;
-      case 4: launch_r<F, 64, 4, PART>(R, w, rb, U, N, xq, y, part, ppr, s); break;
+      case 1: launch_upl<F, 1, PART>(R, lds, L); break;
+      case 2: launch_upl<F, 2, PART>(R, lds, L); break;
+      case 3: launch_upl<F, 3, PART>(R, lds, L); break;
+      case 4: launch_upl<F, 4, PART>(R, lds, L); break;
       case 5:
-      case 6: launch_r<F, 64, 6, PART>(R, w, rb, U, N, xq, y, part, ppr, s); break;
+      case 6: launch_upl<F, 6, PART>(R, lds, L); break;
       case 7:
-      case 8: launch_r<F, 64, 8, PART>(R, w, rb, U, N, xq, y, part, ppr, s); break;
+      case 8: launch_upl<F, 8, PART>(R, lds, L); break;
       default:
-        return fail(JERO_ERR_CAPABILITY_MISMATCH,
-                    "matvec: n_in=" + std::to_string(k) + " exceeds the register-resident activation limit (" +
-                        std::to_string(64 * 8) + " units per row)");
+        return fail(JERO_ERR_CAPABILITY_MISMATCH, "matvec: n_in=" + std::to_string(k) +
+                                                      " exceeds the register-resident activation limit");
     }
   }
   return check_launch("matvec");
 }
 
+// Regroups Q6_K blocks into the JERO_Q6_K_R planes (one thread per block).
+__global__ void __launch_bounds__(256) repack_q6k_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                         int64_t N, int nb) {
+  int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= N * nb) return;
+  const int64_t r = t / nb;
+  const int b = int(t % nb);
+  const int U = 4 * nb;
+  const int64_t plane = N * int64_t(U) * 16;
+  const uint8_t* s = src + t * 210;
+  uint8_t* lo = dst;
+  uint8_t* hi = dst + plane;
+  uint8_t* qh = dst + 2 * plane;
+  uint8_t* sc = dst + 3 * plane;
+  uint8_t* dd = sc + N * int64_t(U) * 4;
+  for (int q = 0; q < 4; q++) {
+    const int n = q >> 1, j = q & 1;
+    const int64_t u = r * U + 4 * b + q;
+    for (int i = 0; i < 16; i++) {
+      lo[u * 16 + i] = s[64 * n + 16 * j + i];
+      hi[u * 16 + i] = s[64 * n + 32 + 16 * j + i];
+      qh[u * 16 + i] = s[128 + 32 * n + 16 * j + i];
+    }
+    for (int k = 0; k < 4; k++) sc[u * 4 + k] = s[192 + 8 * n + j + 2 * k];
+  }
+  dd[t * 2] = s[208];
+  dd[t * 2 + 1] = s[209];
+}
+
 }  // namespace
 
-int max_gemv_k(int quant) { return 64 * 8 * ((quant == JERO_Q4_K || quant == JERO_Q6_K) ? 64 : 32); }
+int max_gemv_k(int quant) {
+  return 64 * 8 * ((quant == JERO_Q4_K || quant == JERO_Q6_K || quant == JERO_Q6_K_R) ? 64 : 32);
+}
 
 int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, int64_t n_out, const void* xq,
                       const float* y) {
@@ -160,17 +256,20 @@ int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, in
                                                   std::to_string(max_gemv_k(quant)));
   if (!aligned4(w) || !aligned4(xq) || !aligned4(y))
     return fail(JERO_ERR_INVALID_ARGUMENT, "matvec: weights, activations and output must be 4-byte aligned");
+  if (quant == JERO_Q6_K_R && (reinterpret_cast<uintptr_t>(w) & 15u))
+    return fail(JERO_ERR_INVALID_ARGUMENT, "matvec: Q6_K_R planes must be 16-byte aligned");
   return JERO_OK;
 }
 
-int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, float* y,
-                  int32_t* part, hipStream_t s) {
+int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, float* y, int32_t* part,
+                  hipStream_t s) {
   const uint8_t* wb = static_cast<const uint8_t*>(w);
   const uint8_t* xb = static_cast<const uint8_t*>(xq);
   if (part) {
     switch (quant) {
       case JERO_Q4_K: return launch_fmt<JERO_Q4_K, true>(wb, n_in, n_out, xb, y, part, s);
       case JERO_Q6_K: return launch_fmt<JERO_Q6_K, true>(wb, n_in, n_out, xb, y, part, s);
+      case JERO_Q6_K_R: return launch_fmt<JERO_Q6_K_R, true>(wb, n_in, n_out, xb, y, part, s);
       case JERO_Q8_0: return launch_fmt<JERO_Q8_0, true>(wb, n_in, n_out, xb, y, part, s);
       case JERO_Q4_0: return launch_fmt<JERO_Q4_0, true>(wb, n_in, n_out, xb, y, part, s);
     }
@@ -178,11 +277,25 @@ int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const v
     switch (quant) {
       case JERO_Q4_K: return launch_fmt<JERO_Q4_K, false>(wb, n_in, n_out, xb, y, nullptr, s);
       case JERO_Q6_K: return launch_fmt<JERO_Q6_K, false>(wb, n_in, n_out, xb, y, nullptr, s);
+      case JERO_Q6_K_R: return launch_fmt<JERO_Q6_K_R, false>(wb, n_in, n_out, xb, y, nullptr, s);
       case JERO_Q8_0: return launch_fmt<JERO_Q8_0, false>(wb, n_in, n_out, xb, y, nullptr, s);
       case JERO_Q4_0: return launch_fmt<JERO_Q4_0, false>(wb, n_in, n_out, xb, y, nullptr, s);
     }
   }
   return fail(JERO_ERR_CAPABILITY_MISMATCH, "unsupported weight quantization " + std::to_string(quant));
+}
+
+int launch_repack(int quant, const void* src, int64_t n_in, int64_t n_out, void* dst, int* dst_quant,
+                  hipStream_t s) {
+  if (quant != JERO_Q6_K)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "repack: only Q6_K has a device layout (got " +
+                                                  std::to_string(quant) + ")");
+  int nb = int(n_in / 256);
+  int64_t blocks = n_out * nb;
+  hipLaunchKernelGGL(repack_q6k_kernel, dim3(unsigned((blocks + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), n_out, nb);
+  if (dst_quant) *dst_quant = JERO_Q6_K_R;
+  return check_launch("repack");
 }
 
 }  // namespace jero
@@ -227,4 +340,22 @@ extern "C" int jero_hip_vec_dot(int quant, const void* w_dev, size_t w_bytes, in
   rc = launch_quantize_act(act, x_dev, 1, n_in, ws, s);
   if (rc) return rc;
   return launch_matvec(quant, w_dev, n_in, n_out, ws, y_dev, nullptr, s);
+}
+
+extern "C" int jero_hip_repack(int quant, const void* src_dev, size_t src_bytes, int64_t n_in, int64_t n_out,
+                               void* dst_dev, int* dst_quant, void* stream) {
+  if (!src_dev || !dst_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "repack: null pointer");
+  if (n_in <= 0 || n_out <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "repack: empty tensor");
+  int64_t rb = row_bytes(quant, n_in);
+  if (rb < 0) return fail(JERO_ERR_TENSOR_BOUNDS, "repack: n_in is not a multiple of the block");
+  if (uint64_t(rb) * uint64_t(n_out) > src_bytes)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "repack: tensor holds " + std::to_string(src_bytes) + " bytes, shape needs " +
+                                            std::to_string(rb * n_out));
+  if (reinterpret_cast<uintptr_t>(dst_dev) & 15u)
+    return fail(JERO_ERR_INVALID_ARGUMENT, "repack: destination must be 16-byte aligned");
+  const uint8_t* s0 = static_cast<const uint8_t*>(src_dev);
+  const uint8_t* d0 = static_cast<const uint8_t*>(dst_dev);
+  size_t n = size_t(rb) * size_t(n_out);
+  if (s0 < d0 + n && d0 < s0 + n) return fail(JERO_ERR_INVALID_ARGUMENT, "repack: source and destination overlap");
+  return launch_repack(quant, src_dev, n_in, n_out, dst_dev, dst_quant, static_cast<hipStream_t>(stream));
 }

@@ -110,11 +110,10 @@ struct Unit<JERO_Q6_K> {
     uint32_t a[16];  // a[4t + k]: q8 of group t, dword k
     float dx;
     int bs32[4];     // 32 * bsum of group t
-    uint32_t j;
   };
   struct W {
     u32x4 lo, hi, qh;
-    u32x2 sc;
+    uint32_t sc;  // the unit's four int8 scales sc[8n+j+2t], t = 0..3, one per byte
     float d;
   };
 
@@ -134,16 +133,19 @@ struct Unit<JERO_Q6_K> {
     uint32_t dw[4] = {bs.x, bs.y, bs.z, bs.w};
 #pragma unroll
     for (int t = 0; t < 4; t++) A.bs32[t] = 32 * int(int16_t((dw[t] >> (16 * j)) & 0xFFFFu));
-    A.j = uint32_t(j);
   }
 
+  // Raw GGUF layout: block b of the row, pieces of unit (n, j); 2-byte aligned reads.
   static __device__ __forceinline__ void load_w(W& w, const uint8_t* __restrict__ row, int u) {
     int b = u >> 2, n = (u >> 1) & 1, j = u & 1;
     const uint8_t* blk = row + int64_t(b) * 210;
     w.lo = ld16_a2(blk + 64 * n + 16 * j);
     w.hi = ld16_a2(blk + 64 * n + 32 + 16 * j);
     w.qh = ld16_a2(blk + 128 + 32 * n + 16 * j);
-    w.sc = ld8_a2(blk + 192 + 8 * n);
+    u32x2 sc = ld8_a2(blk + 192 + 8 * n);
+    uint32_t sh = 8u * uint32_t(j);
+    w.sc = ((sc.x >> sh) & 0xFFu) | (((sc.x >> (sh + 16u)) & 0xFFu) << 8) | (((sc.y >> sh) & 0xFFu) << 16) |
+           (((sc.y >> (sh + 16u)) & 0xFFu) << 24);
     w.d = ldh_a2(blk + 208);
   }
 
@@ -173,11 +175,32 @@ struct Unit<JERO_Q6_K> {
       part[2] = s2;
       part[3] = s3;
     }
-    uint32_t sh = 8u * A.j;
-    int c0 = int(int8_t(w.sc.x >> sh)), c1 = int(int8_t(w.sc.x >> (sh + 16u)));
-    int c2 = int(int8_t(w.sc.y >> sh)), c3 = int(int8_t(w.sc.y >> (sh + 16u)));
+    int c0 = int(int8_t(w.sc)), c1 = int(int8_t(w.sc >> 8));
+    int c2 = int(int8_t(w.sc >> 16)), c3 = int(int8_t(w.sc >> 24));
     int isum = c0 * s0 + c1 * s1 + c2 * s2 + c3 * s3;
     return A.dx * w.d * float(isum);
+  }
+};
+
+// ---------------------------------------------------------------- Q6_K, planar device layout
+// JERO_Q6_K_R holds the bytes of a Q6_K tensor of N rows and nb blocks per row (U = 4 nb
+// units per row) as five planes, so that every load is 16-byte aligned and consecutive lanes
+// read consecutive bytes:
+//   lo [N][U][16] = ql[64n+16j .. +16]      hi [N][U][16] = ql[64n+32+16j .. +16]
+//   qh [N][U][16] = qh[32n+16j .. +16]      sc [N][U][4]  = sc[8n+j+2t], t = 0..3
+//   d  [N][nb] f16
+// Same size as the GGUF tensor (210 bytes per block); the dot product is Unit<Q6_K>'s.
+template <>
+struct Unit<JERO_Q6_K_R> : Unit<JERO_Q6_K> {
+  static __device__ __forceinline__ void load_w_planar(W& w, const uint8_t* __restrict__ base, int64_t N, int U,
+                                                       int64_t row, int u) {
+    const int64_t plane = N * int64_t(U) * 16;
+    const int64_t gu = row * U + u;
+    w.lo = ld4(base + gu * 16);
+    w.hi = ld4(base + plane + gu * 16);
+    w.qh = ld4(base + 2 * plane + gu * 16);
+    w.sc = ld1(base + 3 * plane + gu * 4);
+    w.d = ldh_a2(base + 3 * plane + N * int64_t(U) * 4 + (row * (U / 4) + (u >> 2)) * 2);
   }
 };
 
@@ -286,10 +309,10 @@ struct Unit<JERO_Q4_0> {
 
 // Units per row and partial sums per row of a weight format.
 __host__ __device__ constexpr int units_per_row(int f, int64_t k) {
-  return int(k / ((f == JERO_Q4_K || f == JERO_Q6_K) ? 64 : 32));
+  return int(k / ((f == JERO_Q4_K || f == JERO_Q6_K || f == JERO_Q6_K_R) ? 64 : 32));
 }
 __host__ __device__ constexpr int64_t partials_per_row(int f, int64_t k) {
-  return f == JERO_Q6_K ? k / 16 : k / 32;
+  return (f == JERO_Q6_K || f == JERO_Q6_K_R) ? k / 16 : k / 32;
 }
 
 }  // namespace jero

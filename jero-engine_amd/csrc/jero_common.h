@@ -28,6 +28,7 @@ __host__ __device__ constexpr FmtInfo fmt_info(int q) {
          : q == JERO_Q4_0   ? FmtInfo{32, 18}
          : q == JERO_Q4_K   ? FmtInfo{256, 144}
          : q == JERO_Q6_K   ? FmtInfo{256, 210}
+         : q == JERO_Q6_K_R ? FmtInfo{256, 210}
          : q == JERO_Q8_K   ? FmtInfo{256, 292}
          : q == JERO_ACT_Q8 ? FmtInfo{32, 36}
          : q == JERO_F32    ? FmtInfo{1, 4}
@@ -120,6 +121,30 @@ template <int WIDTH>
 __device__ __forceinline__ int group_sum_i(int v) {
 #pragma unroll
   for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// DPP add of a lane permutation (quad_perm / row_ror / row_bcast controls); lanes outside
+// row_mask add 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+  int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false);
+  return v + __builtin_bit_cast(float, o);
+}
+
+// Sum over groups of WIDTH (4, 16, 32 or 64) consecutive lanes with DPP; the group total
+// lands in the group's last lane (lane % WIDTH == WIDTH - 1).
+template <int WIDTH>
+__device__ __forceinline__ float group_sum_last(float v) {
+  static_assert(WIDTH == 4 || WIDTH == 16 || WIDTH == 32 || WIDTH == 64, "group width");
+  v = dpp_add<0xB1, 0xF>(v);  // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E, 0xF>(v);  // quad_perm [2,3,0,1]
+  if constexpr (WIDTH >= 16) {
+    v = dpp_add<0x124, 0xF>(v);  // row_ror:4
+    v = dpp_add<0x128, 0xF>(v);  // row_ror:8
+  }
+  if constexpr (WIDTH >= 32) v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+  if constexpr (WIDTH >= 64) v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
   return v;
 }
 

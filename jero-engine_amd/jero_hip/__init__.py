@@ -15,10 +15,10 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.normpath(os.path.join(HERE, "..", "libjero_hip.so"))
 
-F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, ACT_Q8 = 0, 1, 2, 8, 12, 14, 15, 100
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, ACT_Q8, Q6_K_R = 0, 1, 2, 8, 12, 14, 15, 100, 114
 Q4_K_M = Q4_K  # the reference's QuantType::Q4_K_M names the Q4_K block format
 QUANT_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_K: "Q8_K",
-               ACT_Q8: "ACT_Q8"}
+               ACT_Q8: "ACT_Q8", Q6_K_R: "Q6_K_R"}
 KV_F32, KV_F16 = 0, 1
 
 OK = 0
@@ -48,6 +48,7 @@ _SIGS = {
     "jero_hip_vec_dot": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "jero_hip_matvec_partials": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _P]),
     "jero_hip_dequantize_rows": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, _P]),
+    "jero_hip_repack": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, C.POINTER(C.c_int), _P]),
 }
 
 
@@ -194,6 +195,17 @@ def vec_dot_q4_k_m(out, weights, inp, **kw):
 
 def vec_dot_q6_k(out, weights, inp, **kw):
     return _vec_dot(Q6_K, out, weights, inp, **kw)
+
+
+def repack(weights, stream=None):
+    """Load-time re-layout (repack_tensor_parallel, src/weights.rs:914-955): returns a new
+    TensorView in the device layout (Q6_K -> Q6_K_R, same byte count)."""
+    import torch
+    dst = torch.empty(weights.nbytes(), dtype=torch.uint8, device=weights.data.device)
+    q = C.c_int(0)
+    check(lib().jero_hip_repack(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in, weights.n_out,
+                                _ptr(dst), C.byref(q), _stream(stream)))
+    return TensorView(weights.name, q.value, weights.shape, dst)
 
 
 def dequantize_rows(weights, row0, n_rows, out, stream=None):

@@ -130,3 +130,35 @@ def test_dequantize_rows_matches_oracle(dev):
         torch.cuda.synchronize()
         ref = O.dequantize(quant, w, 6, k)[2:5]
         np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("n_in,n_out", [(4096, 4096), (768, 2048), (12288, 300), (1280, 7), (4096, 151936)])
+def test_q6_k_repacked_layout_is_bitwise_identical(dev, n_in, n_out):
+    """The planar Q6_K_R layout computes exactly what the raw GGUF Q6_K path computes."""
+    print(f"q6k_r n_in={n_in} n_out={n_out}", flush=True)
+    w = rand_weights(J.Q6_K, n_out, n_in, 500 + n_in + n_out, full_range=True)
+    W = J.TensorView("output.weight", J.Q6_K, [n_in, n_out], to_dev(w, dev))
+    Wr = J.repack(W)
+    assert Wr.quant == J.Q6_K_R and Wr.nbytes() == W.nbytes()
+    x = rand_act(n_in, 501)
+    xq = to_dev(O.quantize_act(J.Q8_K, x), dev)
+    y, yr = (torch.empty(n_out, dtype=torch.float32, device=dev) for _ in range(2))
+    J.matvec(W, xq, y)
+    J.matvec(Wr, xq, yr)
+    if n_out <= 4096:
+        pp = n_in // 16
+        part = torch.empty((n_out, pp), dtype=torch.int32, device=dev)
+        J.matvec_partials(Wr, xq, torch.empty_like(yr), part)
+    torch.cuda.synchronize()
+    assert torch.equal(y, yr)
+    if n_out <= 4096:
+        np.testing.assert_array_equal(part.cpu().numpy(), O.partials(J.Q6_K, w, n_in, n_out, O.quantize_act(J.Q8_K, x)))
+        ref = O.matvec_f64(J.Q6_K, w, n_in, n_out, O.quantize_act(J.Q8_K, x))
+        assert rel_err(yr.cpu().numpy(), ref) < REL_TOL
+
+
+def test_repack_rejects_other_formats(dev):
+    W = J.TensorView("w", J.Q4_K, [256, 4], torch.zeros(4 * 144, dtype=torch.uint8, device=dev))
+    with pytest.raises(J.K3Error) as ei:
+        J.repack(W)
+    assert ei.value.variant == "CapabilityMismatch"

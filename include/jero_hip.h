@@ -46,6 +46,9 @@ typedef enum jero_quant {
   JERO_ACT_Q8 = 100 /* activation blocks for Q8_0 / Q4_0 weights: f32 d, i8 q[32] (36 B) */
 } jero_quant;
 
+/* Element type of the K/V rings. */
+typedef enum jero_kv_dtype { JERO_KV_F32 = 0, JERO_KV_F16 = 1 } jero_kv_dtype;
+
 /* ---- runtime ---- */
 
 /* Selects the device for the calling thread and prepares per-device state. */
@@ -93,6 +96,18 @@ int jero_hip_matvec_partials(int quant, const void *w_dev, size_t w_bytes, int64
  * Other formats: CapabilityMismatch. */
 int jero_hip_repack(int quant, const void *src_dev, size_t src_bytes, int64_t n_in, int64_t n_out,
                     void *dst_dev, int *dst_quant, void *stream);
+
+/* ---- attention ----
+ * gqa_causal_attention_f32(out, q, k, v, n_heads_q, n_heads_kv, head_dim, seq_len, scale)
+ * (called at src/qwen_deepseek.rs:669-691): softmax(q . k_t * scale) . v over t < seq_len for
+ * each q head h, kv head h / (n_heads_q / n_heads_kv).  q_dev: [n_heads_q][head_dim] f32;
+ * k_dev, v_dev: [seq_len][n_heads_kv * head_dim] of kv_dtype (16-byte aligned); out_dev:
+ * [n_heads_q][head_dim] f32.  head_dim in {32, 64, 128}; at most 8 q heads per kv head.
+ * Workspace: n_heads_q * ceil(seq_len/128) * (head_dim + 2) floats (NULL: library-owned, calls
+ * must not overlap on one device). */
+int jero_hip_gqa_attention(float *out_dev, const float *q_dev, const void *k_dev, const void *v_dev, int kv_dtype,
+                           int n_heads_q, int n_heads_kv, int head_dim, int64_t seq_len, float scale,
+                           void *workspace_dev, size_t workspace_bytes, void *stream);
 
 /* dequantize_token_row (src/qwen_deepseek.rs:514,569): rows [row0, row0+n_rows) of a tensor
  * with n_in elements per row, written as f32 to out_dev[n_rows][n_in]. */

@@ -1,0 +1,39 @@
+// attention.h -- decode attention launchers shared by the entry points and the decode step.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace jero {
+
+struct AttnParams {
+  const float* q;        // [nq][hd] f32 (fused: before QK-norm and RoPE)
+  const void* k;         // K ring of the layer, [capacity][nkv*hd] of kv_dtype
+  const void* v;         // V ring of the layer
+  int kv_dtype;          // JERO_KV_F32 / JERO_KV_F16
+  int nkv, group, hd;
+  int active;            // slots attended: [0, active)
+  float scale;
+  float* part_o;         // workspace: [nq][S][hd] then [nq][S][2] (set by launch_attention)
+  float* part_ml;
+  // fused decode-step mode
+  const float* k_new;    // [nkv][hd] f32 before QK-norm and RoPE
+  const float* v_new;    // [nkv][hd] f32
+  const float* q_norm;   // [hd] or null
+  const float* k_norm;   // [hd] or null
+  float eps;
+  int64_t pos;
+  float theta;
+  int slot;              // ring slot of the new token (-1: none)
+  void* k_write;         // same rings, writable
+  void* v_write;
+};
+
+int attn_splits(int active);
+size_t attn_workspace_bytes(int nq, int hd, int active);
+int check_attention_shape(int nq, int nkv, int hd, int64_t seq_len);
+// Enqueues the split-K kernel and the merge; out: [nq][hd] f32.
+int launch_attention(const AttnParams& p, bool fused, float* out, hipStream_t s);
+
+}  // namespace jero

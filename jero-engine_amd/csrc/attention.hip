@@ -1,0 +1,379 @@
+// attention.hip -- GQA softmax attention of one decode token over the KV ring, gfx950.
+//
+// Replaces gqa_causal_attention_f32 (called at src/qwen_deepseek.rs:669-691) and, in its
+// fused form, the rest of run_gqa_causal_with_cache_scaled (src/qwen_deepseek.rs:643-694) plus
+// the QK-norm and RoPE of run_dense_attention_sublayer_scaled (:1039-1071).
+//
+// KV layout (the recipes' flat ring, src/qwen_deepseek.rs:643-694): per layer a K ring then a
+// V ring, each [capacity][n_kv * head_dim], f32 (as the reference) or f16 (half the bytes).
+//
+// Split-K ("flash decoding"): workgroup (split s, kv head h) owns positions
+// [s*128, s*128+128) of the active slots and all q heads of h's group.  It issues its K and V
+// loads (16 bytes per lane, consecutive lanes on consecutive bytes) before anything else, so
+// a workgroup has its whole 2 x 128 x head_dim tile in flight; then it scores, exponentiates
+// against its local max and accumulates P V.  A second kernel merges the splits with the
+// usual max/sum rescaling.  Fused mode: every workgroup rebuilds its q heads (per-head RMSNorm,
+// interleaved RoPE, scale folded in); the workgroup whose range holds the new slot also
+// normalises/rotates k, writes k and v into the ring and uses them for that slot.
+#include "attention.h"
+
+#include "jero_common.h"
+#include "runtime.h"
+
+namespace jero {
+
+constexpr int kAttnThreads = 256;
+constexpr int kAttnChunk = 128;  // positions per workgroup
+constexpr int kMaxGroup = 8;     // q heads per kv head
+
+template <typename T>
+__device__ __forceinline__ void widen16(const u32x4 v, float* out);
+template <>
+__device__ __forceinline__ void widen16<_Float16>(const u32x4 v, float* out) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    out[2 * i] = float(__builtin_bit_cast(_Float16, uint16_t(w[i] & 0xFFFFu)));
+    out[2 * i + 1] = float(__builtin_bit_cast(_Float16, uint16_t(w[i] >> 16)));
+  }
+}
+template <>
+__device__ __forceinline__ void widen16<float>(const u32x4 v, float* out) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) out[i] = __uint_as_float(w[i]);
+}
+
+template <typename T>
+__device__ __forceinline__ T narrow(float x) {
+  return T(x);
+}
+
+// RoPE angle of pair i at position pos: pos / theta^(2i/hd), in f32 as the reference computes it.
+__device__ __forceinline__ float rope_angle(int i, int hd, int64_t pos, float theta) {
+  float expo = float(2 * i) / float(hd);
+  return float(pos) / powf(theta, expo);
+}
+
+// Per-head RMSNorm (optional weight) + interleaved RoPE of one head held as one pair per lane
+// in a group of HD/2 lanes; returns the rotated pair.
+template <int HD>
+__device__ __forceinline__ float2 norm_rope_pair(float x0, float x1, int pair, const float* __restrict__ nw,
+                                                 float eps, int64_t pos, float theta, bool rope) {
+  if (nw) {
+    float ss = x0 * x0 + x1 * x1;
+#pragma unroll
+    for (int off = HD / 4; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    float inv = 1.0f / sqrtf(ss / float(HD) + eps);
+    x0 = x0 * inv * nw[2 * pair];
+    x1 = x1 * inv * nw[2 * pair + 1];
+  }
+  if (!rope) return make_float2(x0, x1);
+  float a = rope_angle(pair, HD, pos, theta);
+  float s, c;
+  sincosf(a, &s, &c);
+  return make_float2(x0 * c - x1 * s, x0 * s + x1 * c);
+}
+
+template <int HD, typename KV, bool FUSED>
+__global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p) {
+  constexpr int EPL = 16 / int(sizeof(KV));     // elements per 16-byte load
+  constexpr int LPP = HD / EPL;                 // lanes per position (K rows)
+  constexpr int PPW = kWave / LPP;              // positions per wave per step
+  constexpr int KSTEPS = kAttnChunk / (PPW * (kAttnThreads / kWave));
+  constexpr int DPT = HD / EPL;                 // dim chunks per V row
+  constexpr int NPS = kAttnThreads / DPT;       // position subsets in the PV phase
+  constexpr int VSTEPS = kAttnChunk / NPS;
+  static_assert(KSTEPS >= 1 && VSTEPS >= 1, "tile shape");
+
+  __shared__ float s_q[kMaxGroup][HD];
+  __shared__ float s_knew[HD];
+  __shared__ float s_vnew[HD];
+  __shared__ float s_p[kMaxGroup][kAttnChunk];
+  __shared__ float s_red[kAttnThreads / kWave][kMaxGroup * HD];
+  __shared__ float s_m[kMaxGroup], s_l[kMaxGroup];
+
+  const int split = blockIdx.x, kh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int group = p.group;
+  const int64_t kvd = int64_t(p.nkv) * HD;
+  const int p0 = split * kAttnChunk;
+  const int p1 = min(p0 + kAttnChunk, p.active);
+  const KV* kb = static_cast<const KV*>(p.k) + kh * HD;
+  const KV* vb = static_cast<const KV*>(p.v) + kh * HD;
+
+  // 1. K and V tiles into registers
+  u32x4 kreg[KSTEPS], vreg[VSTEPS];
+  const int kc = lane % LPP;
+#pragma unroll
+  for (int i = 0; i < KSTEPS; i++) {
+    const int pos = p0 + (i * (kAttnThreads / kWave) + wv) * PPW + lane / LPP;
+    if (pos < p1) kreg[i] = ld4(reinterpret_cast<const uint8_t*>(kb + int64_t(pos) * kvd + kc * EPL));
+  }
+  const int dc = tid % DPT, ps = tid / DPT;
+#pragma unroll
+  for (int i = 0; i < VSTEPS; i++) {
+    const int pos = p0 + i * NPS + ps;
+    if (pos < p1) vreg[i] = ld4(reinterpret_cast<const uint8_t*>(vb + int64_t(pos) * kvd + dc * EPL));
+  }
+
+  // 2. q heads of this group (and, fused, the new k/v) into LDS
+  const bool own_slot = FUSED && p.slot >= p0 && p.slot < p1;
+  {
+    constexpr int HPW = 128 / HD;  // heads per wave pass (HD/2 lanes per head)
+    const int pair = lane % (HD / 2), sub = lane / (HD / 2);
+    for (int h0 = wv * HPW; h0 < group + (FUSED ? 1 : 0); h0 += (kAttnThreads / kWave) * HPW) {
+      const int gi = h0 + sub;
+      const bool is_k = FUSED && gi == group;
+      const bool ok = gi <= group && (gi < group || is_k);
+      float x0 = 0.f, x1 = 0.f;
+      if (ok) {
+        const float* src = is_k ? p.k_new + kh * HD : p.q + (int64_t(kh) * group + gi) * HD;
+        x0 = src[2 * pair];
+        x1 = src[2 * pair + 1];
+      }
+      float2 r;
+      if constexpr (FUSED)
+        r = norm_rope_pair<HD>(x0, x1, pair, is_k ? p.k_norm : p.q_norm, p.eps, p.pos, p.theta, true);
+      else
+        r = make_float2(x0, x1);
+      if (ok) {
+        if (is_k) {
+          s_knew[2 * pair] = r.x;
+          s_knew[2 * pair + 1] = r.y;
+        } else {
+          s_q[gi][2 * pair] = r.x * p.scale;
+          s_q[gi][2 * pair + 1] = r.y * p.scale;
+        }
+      }
+    }
+    if (own_slot) {
+      for (int d = tid; d < HD; d += kAttnThreads) s_vnew[d] = p.v_new[kh * HD + d];
+    }
+  }
+  __syncthreads();
+  if (own_slot) {  // append the new token's k, v to the ring
+    KV* kw = static_cast<KV*>(p.k_write) + int64_t(p.slot) * kvd + kh * HD;
+    KV* vw = static_cast<KV*>(p.v_write) + int64_t(p.slot) * kvd + kh * HD;
+    for (int d = tid; d < HD; d += kAttnThreads) {
+      kw[d] = narrow<KV>(s_knew[d]);
+      vw[d] = narrow<KV>(s_vnew[d]);
+    }
+  }
+
+  // 3. scores: 16-byte K slices against every q head of the group, reduced over LPP lanes
+#pragma unroll
+  for (int i = 0; i < KSTEPS; i++) {
+    const int pos = p0 + (i * (kAttnThreads / kWave) + wv) * PPW + lane / LPP;
+    float kf[EPL];
+    if (pos < p1) {
+      if (FUSED && pos == p.slot) {
+#pragma unroll
+        for (int e = 0; e < EPL; e++) kf[e] = s_knew[kc * EPL + e];
+      } else {
+        widen16<KV>(kreg[i], kf);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPL; e++) kf[e] = 0.f;
+    }
+    for (int gi = 0; gi < group; gi++) {
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; e++) s += s_q[gi][kc * EPL + e] * kf[e];
+#pragma unroll
+      for (int off = LPP / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, kWave);
+      if (kc == 0 && pos < p1) s_p[gi][pos - p0] = s;
+    }
+  }
+  __syncthreads();
+
+  // 4. local softmax numerators per head (one wave per head)
+  const int n = p1 - p0;
+  for (int gi = wv; gi < group; gi += kAttnThreads / kWave) {
+    float m = -INFINITY;
+    for (int j = lane; j < n; j += kWave) m = fmaxf(m, s_p[gi][j]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int j = lane; j < n; j += kWave) {
+      float e = expf(s_p[gi][j] - m);
+      s_p[gi][j] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      s_m[gi] = m;
+      s_l[gi] = l;
+    }
+  }
+  __syncthreads();
+
+  // 5. P V over this thread's position subset, then across subsets
+  float acc[kMaxGroup][EPL];
+#pragma unroll
+  for (int gi = 0; gi < kMaxGroup; gi++)
+#pragma unroll
+    for (int e = 0; e < EPL; e++) acc[gi][e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < VSTEPS; i++) {
+    const int pos = p0 + i * NPS + ps;
+    if (pos < p1) {
+      float vf[EPL];
+      if (FUSED && pos == p.slot) {
+#pragma unroll
+        for (int e = 0; e < EPL; e++) vf[e] = s_vnew[dc * EPL + e];
+      } else {
+        widen16<KV>(vreg[i], vf);
+      }
+#pragma unroll
+      for (int gi = 0; gi < kMaxGroup; gi++) {
+        if (gi < group) {
+          const float pr = s_p[gi][pos - p0];
+#pragma unroll
+          for (int e = 0; e < EPL; e++) acc[gi][e] += pr * vf[e];
+        }
+      }
+    }
+  }
+  // subsets of one wave sit DPT lanes apart
+#pragma unroll
+  for (int gi = 0; gi < kMaxGroup; gi++) {
+    if (gi < group) {
+#pragma unroll
+      for (int e = 0; e < EPL; e++) {
+        float v = acc[gi][e];
+#pragma unroll
+        for (int off = DPT; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
+        acc[gi][e] = v;
+      }
+    }
+  }
+  if (lane < DPT) {
+#pragma unroll
+    for (int gi = 0; gi < kMaxGroup; gi++)
+      if (gi < group)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) s_red[wv][gi * HD + dc * EPL + e] = acc[gi][e];
+  }
+  __syncthreads();
+  const int S = gridDim.x;
+  for (int idx = tid; idx < group * HD; idx += kAttnThreads) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnThreads / kWave; w++) v += s_red[w][idx];
+    const int gi = idx / HD, d = idx % HD;
+    const int h = kh * group + gi;
+    p.part_o[(int64_t(h) * S + split) * HD + d] = v;
+  }
+  if (tid < group) {
+    const int h = kh * group + tid;
+    p.part_ml[(int64_t(h) * S + split) * 2 + 0] = s_m[tid];
+    p.part_ml[(int64_t(h) * S + split) * 2 + 1] = s_l[tid];
+  }
+}
+
+// Merge of the splits: one workgroup per q head, one thread per output dim.
+__global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restrict__ part_o,
+                                                           const float* __restrict__ part_ml, int S, int hd,
+                                                           float* __restrict__ out) {
+  const int h = blockIdx.x;
+  const int d = threadIdx.x;
+  float M = -INFINITY;
+  for (int s = 0; s < S; s++) M = fmaxf(M, part_ml[(int64_t(h) * S + s) * 2]);
+  float L = 0.f, o = 0.f;
+  for (int s = 0; s < S; s++) {
+    const float w = expf(part_ml[(int64_t(h) * S + s) * 2] - M);
+    L += w * part_ml[(int64_t(h) * S + s) * 2 + 1];
+    if (d < hd) o += w * part_o[(int64_t(h) * S + s) * hd + d];
+  }
+  if (d < hd) out[int64_t(h) * hd + d] = o / L;
+}
+
+int attn_splits(int active) { return (active + kAttnChunk - 1) / kAttnChunk; }
+
+size_t attn_workspace_bytes(int nq, int hd, int active) {
+  const size_t S = size_t(attn_splits(active));
+  return size_t(nq) * S * (size_t(hd) + 2) * sizeof(float);
+}
+
+template <int HD, typename KV, bool FUSED>
+static void launch_partial(const AttnParams& p, int S, hipStream_t s) {
+  hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED>), dim3(S, p.nkv), dim3(kAttnThreads), 0, s, p);
+}
+
+int launch_attention(const AttnParams& p0, bool fused, float* out, hipStream_t s) {
+  AttnParams p = p0;
+  const int S = attn_splits(p.active);
+  p.part_ml = p.part_o + size_t(p.nkv) * p.group * S * p.hd;
+#define JERO_ATTN_CASE(HDV)                                                                     \
+  if (p.hd == HDV) {                                                                            \
+    if (p.kv_dtype == JERO_KV_F16) {                                                            \
+      if (fused) launch_partial<HDV, _Float16, true>(p, S, s);                                  \
+      else launch_partial<HDV, _Float16, false>(p, S, s);                                       \
+    } else {                                                                                    \
+      if (fused) launch_partial<HDV, float, true>(p, S, s);                                     \
+      else launch_partial<HDV, float, false>(p, S, s);                                          \
+    }                                                                                           \
+  }
+  JERO_ATTN_CASE(32) else JERO_ATTN_CASE(64) else JERO_ATTN_CASE(128) else return fail(
+      JERO_ERR_CAPABILITY_MISMATCH, "attention: head_dim " + std::to_string(p.hd) + " not in {32, 64, 128}");
+#undef JERO_ATTN_CASE
+  int rc = check_launch("attention partial");
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(p.nkv * p.group), dim3(p.hd < 64 ? 64 : p.hd), 0, s, p.part_o,
+                     p.part_ml, S, p.hd, out);
+  return check_launch("attention combine");
+}
+
+int check_attention_shape(int nq, int nkv, int hd, int64_t seq_len) {
+  if (nq <= 0 || nkv <= 0 || hd <= 0 || seq_len <= 0)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "attention: empty heads or sequence");
+  if (nq % nkv) return fail(JERO_ERR_TENSOR_BOUNDS, "attention: n_heads_q not a multiple of n_heads_kv");
+  if (nq / nkv > kMaxGroup)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: more than " + std::to_string(kMaxGroup) +
+                                                  " q heads per kv head");
+  if (hd != 32 && hd != 64 && hd != 128)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: head_dim " + std::to_string(hd) + " not in {32, 64, 128}");
+  if (seq_len > (int64_t(1) << 24)) return fail(JERO_ERR_CONTEXT_LENGTH_EXCEEDED, "attention: sequence too long");
+  return JERO_OK;
+}
+
+}  // namespace jero
+
+using namespace jero;
+
+extern "C" int jero_hip_gqa_attention(float* out_dev, const float* q_dev, const void* k_dev, const void* v_dev,
+                                      int kv_dtype, int n_heads_q, int n_heads_kv, int head_dim, int64_t seq_len,
+                                      float scale, void* workspace_dev, size_t workspace_bytes, void* stream) {
+  int rc = check_attention_shape(n_heads_q, n_heads_kv, head_dim, seq_len);
+  if (rc) return rc;
+  if (!out_dev || !q_dev || !k_dev || !v_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "attention: null pointer");
+  if (kv_dtype != JERO_KV_F32 && kv_dtype != JERO_KV_F16)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: kv_dtype must be JERO_KV_F32 or JERO_KV_F16");
+  if ((reinterpret_cast<uintptr_t>(k_dev) | reinterpret_cast<uintptr_t>(v_dev)) & 15u)
+    return fail(JERO_ERR_INVALID_ARGUMENT, "attention: K and V must be 16-byte aligned");
+  size_t need = attn_workspace_bytes(n_heads_q, head_dim, int(seq_len));
+  void* ws = workspace_dev;
+  if (ws) {
+    if (workspace_bytes < need)
+      return fail(JERO_ERR_TENSOR_BOUNDS, "attention: workspace of " + std::to_string(workspace_bytes) +
+                                              " bytes, need " + std::to_string(need));
+    if (!aligned4(ws)) return fail(JERO_ERR_INVALID_ARGUMENT, "attention: workspace must be 4-byte aligned");
+  } else {
+    rc = workspace(need, &ws);
+    if (rc) return rc;
+  }
+  AttnParams p{};
+  p.q = q_dev;
+  p.k = k_dev;
+  p.v = v_dev;
+  p.kv_dtype = kv_dtype;
+  p.nkv = n_heads_kv;
+  p.group = n_heads_q / n_heads_kv;
+  p.hd = head_dim;
+  p.active = int(seq_len);
+  p.scale = scale;
+  p.slot = -1;
+  p.part_o = static_cast<float*>(ws);
+  return launch_attention(p, false, out_dev, static_cast<hipStream_t>(stream));
+}

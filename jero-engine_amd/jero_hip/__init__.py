@@ -49,6 +49,7 @@ _SIGS = {
     "jero_hip_matvec_partials": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _P]),
     "jero_hip_dequantize_rows": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, _P]),
     "jero_hip_repack": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, C.POINTER(C.c_int), _P]),
+    "jero_hip_gqa_attention": (_I32, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I64, _F, _P, _SZ, _P]),
 }
 
 
@@ -206,6 +207,18 @@ def repack(weights, stream=None):
     check(lib().jero_hip_repack(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in, weights.n_out,
                                 _ptr(dst), C.byref(q), _stream(stream)))
     return TensorView(weights.name, q.value, weights.shape, dst)
+
+
+def gqa_causal_attention_f32(out, q, k, v, n_heads_q, n_heads_kv, head_dim, seq_len, scale, workspace=None,
+                             stream=None):
+    """gqa_causal_attention_f32 (src/qwen_deepseek.rs:669-691); k, v: [seq][n_kv*hd] f32 or f16."""
+    import torch
+    kv_dtype = KV_F16 if k.dtype == torch.float16 else KV_F32
+    ws_p = _ptr(workspace) if workspace is not None else None
+    ws_n = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    check(lib().jero_hip_gqa_attention(_ptr(out), _ptr(q), _ptr(k), _ptr(v), kv_dtype, n_heads_q, n_heads_kv,
+                                       head_dim, seq_len, scale, ws_p, ws_n, _stream(stream)))
+    return out
 
 
 def dequantize_rows(weights, row0, n_rows, out, stream=None):

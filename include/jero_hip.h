@@ -109,6 +109,24 @@ int jero_hip_gqa_attention(float *out_dev, const float *q_dev, const void *k_dev
                            int n_heads_q, int n_heads_kv, int head_dim, int64_t seq_len, float scale,
                            void *workspace_dev, size_t workspace_bytes, void *stream);
 
+/* ---- routed experts ----
+ * dispatch_qwen3_moe_ffn (src/qwen_deepseek.rs:847-951) from router logits, with
+ * select_top_k_experts(logits, top_k, normalize = true) (src/gemma.rs:362-442) and
+ * run_single_swiglu_expert (:748-771) per selected expert:
+ *   y[t] = sum_j w[t][j] * down_e(silu(gate_e x_t) * up_e x_t),  e = sel_idx[t][j].
+ * x_dev [n_tokens][hidden] f32 (16-byte aligned); router_logits_dev [n_tokens][n_experts] f32;
+ * gate/up: stacked [n_experts][ffn rows][hidden] in one K-quant; down: [n_experts][hidden rows][ffn]
+ * in Q4_K or Q6_K (GGUF stacked [hidden, ffn, n_experts] tensors, expert e = rows e*ffn..).
+ * Outputs y_dev [n_tokens][hidden], sel_idx_dev / sel_w_dev [n_tokens][top_k].
+ * hidden <= 2048 for the gate/up pairing; top_k <= 16; n_experts <= 1024.  Workspace:
+ * jero_hip_moe_workspace_bytes(...) bytes, 256-byte aligned (NULL: library-owned). */
+int jero_hip_moe_ffn(const float *x_dev, const float *router_logits_dev, int64_t n_tokens, int64_t n_experts,
+                     int top_k, int gate_quant, const void *gate_dev, size_t gate_bytes, int up_quant,
+                     const void *up_dev, size_t up_bytes, int down_quant, const void *down_dev, size_t down_bytes,
+                     int64_t hidden, int64_t ffn, float *y_dev, int32_t *sel_idx_dev, float *sel_w_dev,
+                     void *workspace_dev, size_t workspace_bytes, void *stream);
+size_t jero_hip_moe_workspace_bytes(int64_t n_tokens, int64_t n_experts, int top_k, int64_t hidden, int64_t ffn);
+
 /* dequantize_token_row (src/qwen_deepseek.rs:514,569): rows [row0, row0+n_rows) of a tensor
  * with n_in elements per row, written as f32 to out_dev[n_rows][n_in]. */
 int jero_hip_dequantize_rows(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t row0,

@@ -1,0 +1,44 @@
+// moe.h -- routed expert FFN launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace jero {
+
+// Expert grouping produced by the routing kernel (device arrays).
+struct MoeLists {
+  int32_t* offset;    // [E+1] first list position of each expert
+  int32_t* active;    // [E] ascending ids of experts with at least one (token, slot)
+  int32_t* n_active;  // [1]
+  int32_t* entry;     // [T*k] (token*k + slot), grouped by expert, ascending within an expert
+  int32_t* inv;       // [T*k] list position of (token*k + slot)
+};
+
+struct MoeArgs {
+  const float* x;       // [T][hidden]
+  const float* logits;  // [T][E]
+  int64_t T, E;
+  int top_k;
+  int gate_quant, up_quant, down_quant;
+  const void* gate;  // stacked [E][ffn rows][hidden]
+  const void* up;
+  const void* down;  // stacked [E][hidden rows][ffn]
+  int64_t hidden, ffn;
+  float* y;          // [T][hidden]
+  int32_t* sel_idx;  // [T][k]
+  float* sel_w;      // [T][k]
+  // workspace carve-out (set by launch_moe)
+  uint8_t* xq;
+  float* act;
+  const uint8_t* aq;
+  float* yd;
+  int max_active;
+};
+
+size_t moe_workspace_bytes(int64_t T, int64_t E, int top_k, int64_t hidden, int64_t ffn);
+int check_moe_args(const MoeArgs& a, size_t gate_bytes, size_t up_bytes, size_t down_bytes);
+int launch_moe(MoeArgs a, void* ws, hipStream_t s);
+
+}  // namespace jero

@@ -50,6 +50,9 @@ _SIGS = {
     "jero_hip_dequantize_rows": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, _P]),
     "jero_hip_repack": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, C.POINTER(C.c_int), _P]),
     "jero_hip_gqa_attention": (_I32, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I64, _F, _P, _SZ, _P]),
+    "jero_hip_moe_ffn": (_I32, [_P, _P, _I64, _I64, _I32, _I32, _P, _SZ, _I32, _P, _SZ, _I32, _P, _SZ, _I64, _I64,
+                                _P, _P, _P, _P, _SZ, _P]),
+    "jero_hip_moe_workspace_bytes": (_SZ, [_I64, _I64, _I32, _I64, _I64]),
 }
 
 
@@ -219,6 +222,26 @@ def gqa_causal_attention_f32(out, q, k, v, n_heads_q, n_heads_kv, head_dim, seq_
     check(lib().jero_hip_gqa_attention(_ptr(out), _ptr(q), _ptr(k), _ptr(v), kv_dtype, n_heads_q, n_heads_kv,
                                        head_dim, seq_len, scale, ws_p, ws_n, _stream(stream)))
     return out
+
+
+def dispatch_qwen3_moe_ffn(out, norm_ffn_in, router_logits, top_k, gate, up, down, workspace=None, stream=None):
+    """dispatch_qwen3_moe_ffn (src/qwen_deepseek.rs:847-951) from router logits.
+    gate/up/down: stacked TensorViews with shape [n_in, rows_per_expert, n_experts].
+    Returns (sel_idx [T, k] int32, sel_w [T, k] f32) device tensors."""
+    import torch
+    T = router_logits.shape[0] if router_logits.dim() == 2 else 1
+    E = router_logits.shape[-1]
+    hidden, ffn = gate.shape[0], gate.shape[1]
+    sel_idx = torch.empty((T, top_k), dtype=torch.int32, device=out.device)
+    sel_w = torch.empty((T, top_k), dtype=torch.float32, device=out.device)
+    if workspace is None:
+        need = lib().jero_hip_moe_workspace_bytes(T, E, top_k, hidden, ffn)
+        workspace = torch.empty(need, dtype=torch.uint8, device=out.device)
+    check(lib().jero_hip_moe_ffn(_ptr(norm_ffn_in), _ptr(router_logits), T, E, top_k, gate.quant, _ptr(gate.data),
+                                 gate.nbytes(), up.quant, _ptr(up.data), up.nbytes(), down.quant, _ptr(down.data),
+                                 down.nbytes(), hidden, ffn, _ptr(out), _ptr(sel_idx), _ptr(sel_w), _ptr(workspace),
+                                 workspace.numel(), _stream(stream)))
+    return sel_idx, sel_w
 
 
 def dequantize_rows(weights, row0, n_rows, out, stream=None):

@@ -1,0 +1,72 @@
+"""GPU parity of the routed-expert FFN against the oracle's dispatch_qwen3_moe_ffn.
+
+Routing (selected experts and their order) must match exactly; weights within 1e-6; outputs
+within 1e-3 of max(|ref|, rms(ref)): the expert hidden activations are re-quantized to Q8_K
+between gate/up and down, so a last-bit difference in silu(g)*u can move one int8 by one.
+"""
+import numpy as np
+import pytest
+import torch
+
+import jero_hip as J
+import pyoracle as O
+from qdata import rand_act, rand_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(dev, T, E, H, F, K, gq, dq, seed, logits=None):
+    gate = rand_weights(gq, E * F, H, seed)
+    up = rand_weights(gq, E * F, H, seed + 1)
+    down = rand_weights(dq, E * H, F, seed + 2)
+    x = rand_act(H, seed + 3, m=T)
+    if logits is None:
+        logits = rand_act(E, seed + 4, m=T)
+    y_ref, si_ref, sw_ref = O.moe_ffn(logits, K, gate, up, down, gq, gq, dq, H, F, x, threads=8)
+    td = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    G = J.TensorView("blk.0.ffn_gate_exps.weight", gq, [H, F, E], td(gate))
+    U = J.TensorView("blk.0.ffn_up_exps.weight", gq, [H, F, E], td(up))
+    D = J.TensorView("blk.0.ffn_down_exps.weight", dq, [F, H, E], td(down))
+    y = torch.empty((T, H), dtype=torch.float32, device=dev)
+    si, sw = J.dispatch_qwen3_moe_ffn(y, td(x), td(logits), K, G, U, D)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(si.cpu().numpy(), si_ref)
+    np.testing.assert_allclose(sw.cpu().numpy(), sw_ref, rtol=1e-6, atol=1e-7)
+    ref = y_ref.astype(np.float64)
+    scale = np.sqrt(np.mean(ref ** 2, axis=1, keepdims=True))
+    err = np.max(np.abs(y.cpu().numpy() - ref) / np.maximum(np.abs(ref), scale))
+    assert err < 1e-3, err
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_moe_qwen3_shape(dev, T):
+    """Hidden 2048, 128 experts of 768, top-8; gate/up Q4_K, down Q6_K."""
+    print(f"moe qwen3 T={T}", flush=True)
+    run_case(dev, T, 128, 2048, 768, 8, J.Q4_K, J.Q6_K, 900 + T)
+
+
+def test_moe_small_and_q4k_down(dev):
+    print("moe small", flush=True)
+    run_case(dev, 5, 6, 256, 512, 2, J.Q4_K, J.Q4_K, 40)
+    run_case(dev, 3, 16, 512, 256, 4, J.Q6_K, J.Q6_K, 41)
+
+
+def test_moe_routing_ties_and_nonfinite(dev):
+    """Ties pick the lower expert id; NaN/inf logits rank last with zero probability."""
+    print("moe ties", flush=True)
+    E = 8
+    logits = np.array([[0.1, 3.0, 0.5, 1.0, 3.0, 2.0, -1.0, 0.0],
+                       [np.nan, 1.0, np.inf, 1.0, -np.inf, 0.5, 0.5, 2.0]], np.float32)
+    run_case(dev, 2, E, 256, 256, 3, J.Q4_K, J.Q6_K, 60, logits=logits)
+
+
+def test_moe_argument_errors(dev):
+    z = torch.zeros(4096, dtype=torch.float32, device=dev)
+    G = J.TensorView("g", J.Q4_K, [256, 256, 4], torch.zeros(4 * 256 * 144, dtype=torch.uint8, device=dev))
+    D = J.TensorView("d", J.Q6_K, [256, 256, 4], torch.zeros(4 * 256 * 210, dtype=torch.uint8, device=dev))
+    with pytest.raises(J.K3Error) as ei:
+        J.dispatch_qwen3_moe_ffn(z[:256].view(1, 256), z[:256], z[:4].view(1, 4), 5, G, G, D)
+    assert ei.value.variant == "CapabilityMismatch"
+    with pytest.raises(J.K3Error) as ei:
+        J.dispatch_qwen3_moe_ffn(z[:256].view(1, 256), z[:256], z[:4].view(1, 4), 0, G, G, D)
+    assert ei.value.variant == "RoutingUnavailable"

@@ -132,6 +132,45 @@ size_t jero_hip_moe_workspace_bytes(int64_t n_tokens, int64_t n_experts, int top
 int jero_hip_dequantize_rows(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t row0,
                              int64_t n_rows, float *out_dev, void *stream);
 
+/* ---- device-resident decoder (batch-1 decode step) ----
+ * The Qwen3/Llama dense decode path: embed_token -> n_layers x [RMSNorm -> Q|K|V -> (QK-norm)
+ * -> interleaved RoPE -> KV-ring append + GQA attention -> Wo + residual -> RMSNorm -> SwiGLU
+ * FFN + residual] -> RMSNorm -> LM head -> greedy argmax.  Replaces
+ * execute_token_standard_with_hidden (src/qwen_deepseek.rs:1239-1314) as called by
+ * Qwen3Recipe::decode_step (:1441-1460) and sample_greedy_argmax (src/engine.rs:1873-1895).
+ * Tensors are given by GGUF name (ModelWeights::tensor): token_embd.weight, output.weight,
+ * output_norm.weight, blk.N.{attn_norm, attn_q, attn_k, attn_v, attn_output, attn_q_norm,
+ * attn_k_norm, ffn_norm, ffn_gate, ffn_up, ffn_down}.weight; norms F32, matrices in
+ * Q8_0/Q4_0/Q4_K/Q6_K with GGUF shape [n_in, n_out].  The KV arena is one device buffer of
+ * [n_layers][K ring, V ring][kv_capacity][n_heads_kv * head_dim] (the recipes' flat layout). */
+typedef struct jero_model_config {
+  int64_t hidden, ffn, n_layers, vocab;
+  int n_heads_q, n_heads_kv, head_dim;
+  float rms_eps, rope_theta;
+  int64_t kv_capacity; /* ring slots per layer (n_ctx) */
+  int kv_dtype;        /* JERO_KV_F16 or JERO_KV_F32 */
+  int qk_norm;         /* nonzero: per-head RMSNorm of q and k (Qwen3) */
+} jero_model_config;
+typedef struct jero_model jero_model;
+
+int jero_hip_model_create(const jero_model_config *cfg, jero_model **model);
+int jero_hip_model_destroy(jero_model *model);
+/* Copies one tensor to the device (src host memory, or device memory if src_on_device). */
+int jero_hip_model_set_tensor(jero_model *model, const char *name, int quant, const void *src, size_t nbytes,
+                              int64_t n_in, int64_t n_out, int src_on_device);
+/* Checks every tensor is present and builds the device layout (fused Q|K|V and gate|up rows,
+ * Q6_K_R planes).  Required before the first decode step. */
+int jero_hip_model_finalize(jero_model *model);
+/* Device addresses of layer `layer`'s K and V rings (to pre-fill or inspect the cache). */
+int jero_hip_model_kv(jero_model *model, int64_t layer, void **k_ring_dev, void **v_ring_dev);
+/* Device addresses of the current token, the position and the last step's logits [vocab]. */
+int jero_hip_model_state(jero_model *model, int32_t **token_dev, int64_t **pos_dev, float **logits_dev);
+/* Enqueues: token and position of the next decode step. */
+int jero_hip_model_set_position(jero_model *model, int32_t token, int64_t pos, void *stream);
+/* Enqueues one decode step at the device position: writes logits, replaces the token with the
+ * greedy next token and advances the position.  Enqueues kernels only (graph-capturable). */
+int jero_hip_decode_step(jero_model *model, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

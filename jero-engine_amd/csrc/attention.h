@@ -28,6 +28,8 @@ struct AttnParams {
   int slot;              // ring slot of the new token (-1: none)
   void* k_write;         // same rings, writable
   void* v_write;
+  const int64_t* pos_dev;  // if set: pos = *pos_dev, slot = pos % capacity, active = min(pos+1, capacity)
+  int64_t capacity;        // ring slots (grid is sized for all of them when pos_dev is set)
 };
 
 int attn_splits(int active);

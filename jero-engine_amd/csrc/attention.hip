@@ -97,8 +97,24 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int group = p.group;
   const int64_t kvd = int64_t(p.nkv) * HD;
+  int active = p.active, slot = p.slot;
+  int64_t pos_now = p.pos;
+  if (p.pos_dev) {  // position kept on the device (graph-replayed decode)
+    pos_now = *p.pos_dev;
+    slot = int(pos_now % p.capacity);
+    active = int(pos_now + 1 < p.capacity ? pos_now + 1 : p.capacity);
+  }
+  const int S = gridDim.x;
   const int p0 = split * kAttnChunk;
-  const int p1 = min(p0 + kAttnChunk, p.active);
+  if (p0 >= active) {  // empty split: contributes nothing to the merge
+    if (tid < group) {
+      const int h = kh * group + tid;
+      p.part_ml[(int64_t(h) * S + split) * 2 + 0] = -INFINITY;
+      p.part_ml[(int64_t(h) * S + split) * 2 + 1] = 0.f;
+    }
+    return;
+  }
+  const int p1 = min(p0 + kAttnChunk, active);
   const KV* kb = static_cast<const KV*>(p.k) + kh * HD;
   const KV* vb = static_cast<const KV*>(p.v) + kh * HD;
 
@@ -118,7 +134,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   }
 
   // 2. q heads of this group (and, fused, the new k/v) into LDS
-  const bool own_slot = FUSED && p.slot >= p0 && p.slot < p1;
+  const bool own_slot = FUSED && slot >= p0 && slot < p1;
   {
     constexpr int HPW = 128 / HD;  // heads per wave pass (HD/2 lanes per head)
     const int pair = lane % (HD / 2), sub = lane / (HD / 2);
@@ -134,7 +150,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
       }
       float2 r;
       if constexpr (FUSED)
-        r = norm_rope_pair<HD>(x0, x1, pair, is_k ? p.k_norm : p.q_norm, p.eps, p.pos, p.theta, true);
+        r = norm_rope_pair<HD>(x0, x1, pair, is_k ? p.k_norm : p.q_norm, p.eps, pos_now, p.theta, true);
       else
         r = make_float2(x0, x1);
       if (ok) {
@@ -153,8 +169,8 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   }
   __syncthreads();
   if (own_slot) {  // append the new token's k, v to the ring
-    KV* kw = static_cast<KV*>(p.k_write) + int64_t(p.slot) * kvd + kh * HD;
-    KV* vw = static_cast<KV*>(p.v_write) + int64_t(p.slot) * kvd + kh * HD;
+    KV* kw = static_cast<KV*>(p.k_write) + int64_t(slot) * kvd + kh * HD;
+    KV* vw = static_cast<KV*>(p.v_write) + int64_t(slot) * kvd + kh * HD;
     for (int d = tid; d < HD; d += kAttnThreads) {
       kw[d] = narrow<KV>(s_knew[d]);
       vw[d] = narrow<KV>(s_vnew[d]);
@@ -167,7 +183,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
     const int pos = p0 + (i * (kAttnThreads / kWave) + wv) * PPW + lane / LPP;
     float kf[EPL];
     if (pos < p1) {
-      if (FUSED && pos == p.slot) {
+      if (FUSED && pos == slot) {
 #pragma unroll
         for (int e = 0; e < EPL; e++) kf[e] = s_knew[kc * EPL + e];
       } else {
@@ -219,7 +235,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
     const int pos = p0 + i * NPS + ps;
     if (pos < p1) {
       float vf[EPL];
-      if (FUSED && pos == p.slot) {
+      if (FUSED && pos == slot) {
 #pragma unroll
         for (int e = 0; e < EPL; e++) vf[e] = s_vnew[dc * EPL + e];
       } else {
@@ -256,7 +272,6 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
         for (int e = 0; e < EPL; e++) s_red[wv][gi * HD + dc * EPL + e] = acc[gi][e];
   }
   __syncthreads();
-  const int S = gridDim.x;
   for (int idx = tid; idx < group * HD; idx += kAttnThreads) {
     float v = 0.f;
 #pragma unroll
@@ -279,9 +294,11 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restri
   const int h = blockIdx.x;
   const int d = threadIdx.x;
   float M = -INFINITY;
-  for (int s = 0; s < S; s++) M = fmaxf(M, part_ml[(int64_t(h) * S + s) * 2]);
+  for (int s = 0; s < S; s++)
+    if (part_ml[(int64_t(h) * S + s) * 2 + 1] > 0.f) M = fmaxf(M, part_ml[(int64_t(h) * S + s) * 2]);
   float L = 0.f, o = 0.f;
   for (int s = 0; s < S; s++) {
+    if (!(part_ml[(int64_t(h) * S + s) * 2 + 1] > 0.f)) continue;  // empty split
     const float w = expf(part_ml[(int64_t(h) * S + s) * 2] - M);
     L += w * part_ml[(int64_t(h) * S + s) * 2 + 1];
     if (d < hd) o += w * part_o[(int64_t(h) * S + s) * hd + d];
@@ -303,7 +320,7 @@ static void launch_partial(const AttnParams& p, int S, hipStream_t s) {
 
 int launch_attention(const AttnParams& p0, bool fused, float* out, hipStream_t s) {
   AttnParams p = p0;
-  const int S = attn_splits(p.active);
+  const int S = attn_splits(p.pos_dev ? int(p.capacity) : p.active);
   p.part_ml = p.part_o + size_t(p.nkv) * p.group * S * p.hd;
 #define JERO_ATTN_CASE(HDV)                                                                     \
   if (p.hd == HDV) {                                                                            \

@@ -1,0 +1,43 @@
+// decode.h -- fused decode-step kernels and their launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace jero {
+
+constexpr int kDecodeThreads = 512;     // 8 waves per workgroup
+constexpr int kDecodeBlocksPerCU = 2;   // persistent grid: workgroups per CU
+constexpr int kDecodeMaxActBlocks = 8;  // activation blocks per wave in the prologue
+
+enum { kOutStore = 0, kOutResid = 1, kOutSwiglu = 2, kOutArgmax = 3 };
+
+struct DGemvArgs {
+  const uint8_t* w;   // weight rows (GGUF layout, or Q6_K_R planes)
+  int64_t rb;         // bytes per row (GGUF layouts)
+  int U;              // units per row
+  int64_t N;          // rows of the tensor
+  int64_t n_groups;   // row groups (set by the launcher)
+  const float* x;     // f32 input [K] (16-byte aligned)
+  const float* norm_w;  // RMSNorm weight [K] or null
+  float eps;
+  int K;
+  float* y;           // output (store / residual target / SwiGLU act / logits)
+  int64_t half;       // SwiGLU: rows [0, half) gate, [half, 2 half) up
+  float* amax_v;      // argmax partials per workgroup
+  int64_t* amax_i;
+  int max_blocks;     // 0: grid capped at kDecodeBlocksPerCU workgroups per CU
+};
+
+int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s);
+// Workgroups launch_dgemv uses for an n_in = K, N-row tensor (the argmax partial count).
+int dgemv_blocks(int quant, int64_t K, int64_t N, int out_mode);
+// Longest row the fused decode GEMV takes for a weight format.
+int dgemv_max_k(int quant);
+int launch_embed(int quant, const void* w, int64_t rb, int H, int64_t vocab, const int32_t* token, float* out,
+                 hipStream_t s);
+int launch_argmax_final(const float* v, const int64_t* idx, int n, int32_t* token, int64_t* pos, hipStream_t s);
+int launch_set_state(int32_t* token, int64_t* pos, int32_t t, int64_t p, hipStream_t s);
+
+}  // namespace jero

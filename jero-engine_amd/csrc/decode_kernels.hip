@@ -1,0 +1,505 @@
+// decode_kernels.hip -- fused kernels of the batch-1 decode step (gfx950).
+//
+// The decode step of execute_token_standard_with_hidden (src/qwen_deepseek.rs:1239-1314) is
+// a chain of GEMVs separated by small vector ops.  Here each GEMV absorbs its neighbours:
+//   prologue: the workgroup turns the f32 input into the activation blocks the weight format
+//             needs (ACT_Q8 or Q8_K) directly in LDS, optionally after RMSNorm
+//             (rmsnorm_standard, :521-528) -- the weight loads of the first rows are already
+//             in flight while it does so;
+//   epilogue: plain store, residual add into the hidden state (:1086-1095, :1304-1306),
+//             SwiGLU of paired gate/up rows (run_dense_swiglu_ffn, :696-727), or, for the
+//             LM head, a per-workgroup (max, first index) for sample_greedy_argmax
+//             (src/engine.rs:1873-1895).
+// Token id and position are read from device memory, so one captured graph of the step can be
+// replayed for consecutive tokens; the last kernel writes the greedy token and advances the
+// position.
+#include "decode.h"
+
+#include "dequant.h"
+#include "gemv_dot.h"
+#include "jero_common.h"
+#include "runtime.h"
+
+namespace jero {
+
+// ---------------------------------------------------------------- prologue: f32 -> blocks in LDS
+
+__device__ __forceinline__ float block_sum(float v, float* s_tmp) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (lane == 0) s_tmp[wv] = v;
+  lds_barrier();
+  float t = 0.f;
+  for (int i = 0; i < nw; i++) t += s_tmp[i];
+  return t;
+}
+
+// Q8_K block of 256 elements from one wave (4 elements per lane) into LDS (ggml rule, as the
+// standalone quantizer).
+__device__ __forceinline__ void q8k_block_lds(const float e[4], int lane, uint8_t* ob) {
+  float am = 0.0f;
+  int ai = 0x7fffffff;
+  float mxv = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    float a = fabsf(e[t]);
+    if (a > am) {
+      am = a;
+      ai = 4 * lane + t;
+      mxv = e[t];
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    float oa = __shfl_xor(am, off, kWave);
+    int oi = __shfl_xor(ai, off, kWave);
+    float ov = __shfl_xor(mxv, off, kWave);
+    if (oa > am || (oa == am && oi < ai)) {
+      am = oa;
+      ai = oi;
+      mxv = ov;
+    }
+  }
+  if (am == 0.0f) {
+    reinterpret_cast<uint32_t*>(ob + 4)[lane] = 0u;
+    if (lane < 16) reinterpret_cast<int16_t*>(ob + 260)[lane] = 0;
+    if (lane == 0) *reinterpret_cast<float*>(ob) = 0.0f;
+    return;
+  }
+  float iscale = -127.0f / mxv;
+  int s = 0;
+  uint32_t packed = 0;
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    int qv = int(__builtin_rintf(iscale * e[t]));
+    qv = qv < 127 ? qv : 127;
+    s += qv;
+    packed |= (uint32_t(qv) & 0xFFu) << (8 * t);
+  }
+  reinterpret_cast<uint32_t*>(ob + 4)[lane] = packed;
+  s += __shfl_xor(s, 1, kWave);
+  s += __shfl_xor(s, 2, kWave);
+  if ((lane & 3) == 0) reinterpret_cast<int16_t*>(ob + 260)[lane >> 2] = int16_t(s);
+  if (lane == 0) *reinterpret_cast<float*>(ob) = 1.0f / iscale;
+}
+
+// The workgroup's share of the f32 input, loaded before the weight rows so that the prologue
+// only waits for these loads.  Q8_K: wave w takes blocks w, w+nw, ... (4 elements per lane,
+// the quantizer's layout); ACT_Q8: half-wave h takes 32-element blocks h, h+2nw, ...
+template <int ACT>
+struct XRegs {
+  float4 v[kDecodeMaxActBlocks];
+  float4 g[kDecodeMaxActBlocks];
+};
+
+template <int ACT>
+__device__ __forceinline__ void load_x(XRegs<ACT>& X, const float* __restrict__ x, const float* __restrict__ nw,
+                                       int K) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+#pragma unroll
+  for (int i = 0; i < kDecodeMaxActBlocks; i++) {
+    if constexpr (ACT == JERO_Q8_K) {
+      const int b = wv + nwv * i;
+      if (b < K / 256) {
+        X.v[i] = reinterpret_cast<const float4*>(x + b * 256)[lane];
+        if (nw) X.g[i] = reinterpret_cast<const float4*>(nw + b * 256)[lane];
+      }
+    } else {
+      const int b = 2 * wv + (lane >> 5) + 2 * nwv * i;
+      if (b < K / 32) {
+        X.v[i].x = x[b * 32 + (lane & 31)];
+        if (nw) X.g[i].x = nw[b * 32 + (lane & 31)];
+      }
+    }
+  }
+}
+
+// Builds the activation blocks of x (or of rmsnorm(x) * nw) in LDS from the registers.
+template <int ACT>
+__device__ void build_act_lds(XRegs<ACT>& X, bool has_norm, float eps, int K, uint8_t* s_act, float* s_tmp) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  float scale = 1.0f;
+  if (has_norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kDecodeMaxActBlocks; i++) {
+      if constexpr (ACT == JERO_Q8_K) {
+        if (wv + nwv * i < K / 256)
+          ss += X.v[i].x * X.v[i].x + X.v[i].y * X.v[i].y + X.v[i].z * X.v[i].z + X.v[i].w * X.v[i].w;
+      } else {
+        if (2 * wv + (lane >> 5) + 2 * nwv * i < K / 32) ss += X.v[i].x * X.v[i].x;
+      }
+    }
+    ss = block_sum(ss, s_tmp);
+    scale = 1.0f / sqrtf(ss / float(K) + eps);
+  }
+#pragma unroll
+  for (int i = 0; i < kDecodeMaxActBlocks; i++) {
+    if constexpr (ACT == JERO_Q8_K) {
+      const int b = wv + nwv * i;
+      if (b < K / 256) {
+        float e[4] = {X.v[i].x, X.v[i].y, X.v[i].z, X.v[i].w};
+        if (has_norm) {
+          e[0] = e[0] * scale * X.g[i].x;
+          e[1] = e[1] * scale * X.g[i].y;
+          e[2] = e[2] * scale * X.g[i].z;
+          e[3] = e[3] * scale * X.g[i].w;
+        }
+        q8k_block_lds(e, lane, s_act + b * 292);
+      }
+    } else {
+      const int b = 2 * wv + (lane >> 5) + 2 * nwv * i;
+      if (b < K / 32) {
+        const int l = lane & 31;
+        float v = X.v[i].x;
+        if (has_norm) v = v * scale * X.g[i].x;
+        float a = fabsf(v);
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, kWave));
+        float d = a / 127.0f;
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint8_t* ob = s_act + b * 36;
+        ob[4 + l] = uint8_t(int8_t(int(__builtin_rintf(v * id))));
+        if (l == 0) *reinterpret_cast<float*>(ob) = d;
+      }
+    }
+  }
+  lds_barrier();
+}
+
+// ---------------------------------------------------------------- fused GEMV
+
+template <int F, int LPR, int UPL, int R, int OUT>
+__global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
+  using Ut = Unit<F>;
+  constexpr int ACT = (F == JERO_Q8_0 || F == JERO_Q4_0) ? JERO_ACT_Q8 : JERO_Q8_K;
+  constexpr int G = kWave / LPR;
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_mem[];
+  float* s_tmp = reinterpret_cast<float*>(s_mem);  // 64 floats of scratch
+  uint8_t* s_act = s_mem + 256;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t wave0 = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  const int64_t stride = int64_t(gridDim.x) * (blockDim.x / kWave);
+  const int g = lane / LPR, c = lane % LPR;
+  const int U = a.U;
+  const int64_t N = a.N;
+  const int64_t n_groups = a.n_groups;
+
+  // row of (row group rg, row slot r, lane group g); SWIGLU pairs gate row f with up row half+f
+  auto row_of = [&](int64_t rg, int r) -> int64_t {
+    if constexpr (OUT == kOutSwiglu) {
+      if constexpr (G == 1) {
+        const int64_t f = rg * (R / 2) + r / 2;
+        return (r & 1) ? a.half + f : f;
+      } else {
+        const int64_t f = (rg * R + r) * (G / 2) + g / 2;
+        return (g & 1) ? a.half + f : f;
+      }
+    } else {
+      return rg * (G * R) + int64_t(r) * G + g;
+    }
+  };
+  auto row_valid = [&](int64_t rg, int r) -> bool {
+    if constexpr (OUT == kOutSwiglu) {
+      if constexpr (G == 1) {
+        return rg * (R / 2) + r / 2 < a.half;
+      } else {
+        return (rg * R + r) * (G / 2) + g / 2 < a.half;
+      }
+    } else {
+      return row_of(rg, r) < N;
+    }
+  };
+  auto load_rows = [&](int64_t rg, typename Ut::W (&wt)[R][UPL]) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const bool ok = rg < n_groups && row_valid(rg, r);
+      const int64_t row = ok ? row_of(rg, r) : 0;
+#pragma unroll
+      for (int t = 0; t < UPL; t++) {
+        const int u = c + LPR * t;
+        if (ok && u < U) {
+          if constexpr (F == JERO_Q6_K_R)
+            Ut::load_w_planar(wt[r][t], a.w, N, U, row, u);
+          else
+            Ut::load_w(wt[r][t], a.w + row * a.rb, u);
+        }
+      }
+    }
+  };
+
+  // 1. input loads, then the first row group's weight loads, then the prologue
+  XRegs<ACT> X;
+  load_x<ACT>(X, a.x, a.norm_w, a.K);
+  typename Ut::W cur[R][UPL], nxt[R][UPL];
+  load_rows(wave0, cur);
+  // 2. activation blocks in LDS (every thread takes part)
+  build_act_lds<ACT>(X, a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp);
+  typename Ut::Act act[UPL];
+#pragma unroll
+  for (int t = 0; t < UPL; t++) {
+    const int u = c + LPR * t;
+    if (u < U) Ut::load_act(act[t], s_act, u);
+  }
+  const bool last = c == LPR - 1;
+  float best_v = -INFINITY;
+  int64_t best_i = -1;
+  // 3. row groups: prefetch the next group, reduce the current one
+  for (int64_t rg = wave0; rg < n_groups; rg += stride) {
+    load_rows(rg + stride, nxt);
+    float vals[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const bool ok = row_valid(rg, r);
+      float acc = 0.f;
+#pragma unroll
+      for (int t = 0; t < UPL; t++) {
+        const int u = c + LPR * t;
+        if (ok && u < U) acc += Ut::dot(cur[r][t], act[t], nullptr);
+      }
+      vals[r] = group_sum_last<LPR>(acc);
+    }
+    if constexpr (OUT == kOutSwiglu) {
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        if constexpr (G == 1) {
+          if ((r & 1) && last && row_valid(rg, r)) {
+            const float gv = vals[r - 1], uv = vals[r];
+            a.y[row_of(rg, r) - a.half] = gv / (1.0f + expf(-gv)) * uv;
+          }
+        } else {
+          const float gv = __shfl(vals[r], lane - LPR, kWave);
+          if ((g & 1) && last && row_valid(rg, r)) a.y[row_of(rg, r) - a.half] = gv / (1.0f + expf(-gv)) * vals[r];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int64_t row = row_of(rg, r);
+        if (last && row < N) {
+          if constexpr (OUT == kOutResid) {
+            a.y[row] += vals[r];
+          } else {
+            a.y[row] = vals[r];
+            if constexpr (OUT == kOutArgmax) {
+              const float v = vals[r];
+              if (!isnan(v) && (best_i < 0 || v > best_v)) {  // rows ascend: strict > keeps the first
+                best_v = v;
+                best_i = row;
+              }
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+      for (int t = 0; t < UPL; t++) cur[r][t] = nxt[r][t];
+  }
+  if constexpr (OUT == kOutArgmax) {
+    // (max, first index) over the workgroup's rows, NaN skipped
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      float ov = __shfl_xor(best_v, off, kWave);
+      int64_t oi = __shfl_xor(best_i, off, kWave);
+      if (oi >= 0 && (best_i < 0 || ov > best_v || (ov == best_v && oi < best_i))) {
+        best_v = ov;
+        best_i = oi;
+      }
+    }
+    __shared__ float s_bv[kDecodeThreads / 64];
+    __shared__ int64_t s_bi[kDecodeThreads / 64];
+    if (lane == 0) {
+      s_bv[wv] = best_v;
+      s_bi[wv] = best_i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int i = 1; i < int(blockDim.x >> 6); i++) {
+        if (s_bi[i] >= 0 && (best_i < 0 || s_bv[i] > best_v || (s_bv[i] == best_v && s_bi[i] < best_i))) {
+          best_v = s_bv[i];
+          best_i = s_bi[i];
+        }
+      }
+      a.amax_v[blockIdx.x] = best_v;
+      a.amax_i[blockIdx.x] = best_i;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- small kernels
+
+// hidden = dequantize_token_row(token_embd, *token) (embed_token, src/qwen_deepseek.rs:558-582)
+// A token outside the vocabulary (the greedy token of all-NaN logits is -1) embeds as zeros.
+__global__ void __launch_bounds__(256) embed_kernel(int quant, const uint8_t* __restrict__ w, int64_t rb, int H,
+                                                    int64_t vocab, const int32_t* __restrict__ token,
+                                                    float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= H) return;
+  const int64_t t = *token;
+  out[i] = (t >= 0 && t < vocab) ? dequant_elem(quant, w + t * rb, i) : 0.0f;
+}
+
+// Greedy token from the head's per-workgroup (max, index) pairs; advances the position.
+__global__ void __launch_bounds__(1024) argmax_final_kernel(const float* __restrict__ v, const int64_t* __restrict__ idx,
+                                                            int n, int32_t* __restrict__ token,
+                                                            int64_t* __restrict__ pos) {
+  float bv = -INFINITY;
+  int64_t bi = -1;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    if (idx[i] >= 0 && (bi < 0 || v[i] > bv || (v[i] == bv && idx[i] < bi))) {
+      bv = v[i];
+      bi = idx[i];
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    float ov = __shfl_xor(bv, off, kWave);
+    int64_t oi = __shfl_xor(bi, off, kWave);
+    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  __shared__ float s_bv[16];
+  __shared__ int64_t s_bi[16];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) {
+    s_bv[wv] = bv;
+    s_bi[wv] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < int(blockDim.x >> 6); i++) {
+      if (s_bi[i] >= 0 && (bi < 0 || s_bv[i] > bv || (s_bv[i] == bv && s_bi[i] < bi))) {
+        bv = s_bv[i];
+        bi = s_bi[i];
+      }
+    }
+    *token = bi >= 0 ? int32_t(bi) : -1;
+    *pos += 1;
+  }
+}
+
+__global__ void set_state_kernel(int32_t* token, int64_t* pos, int32_t t, int64_t p) {
+  *token = t;
+  *pos = p;
+}
+
+// ---------------------------------------------------------------- launchers
+
+namespace {
+
+template <int F, int LPR, int UPL, int R, int OUT>
+void dgemv_one(DGemvArgs a, int64_t rows_or_pairs, hipStream_t s) {
+  constexpr int G = kWave / LPR;
+  if constexpr (OUT == kOutSwiglu) {
+    const int64_t per = G == 1 ? R / 2 : R * (G / 2);
+    a.n_groups = (rows_or_pairs + per - 1) / per;
+  } else {
+    a.n_groups = (rows_or_pairs + G * R - 1) / (G * R);
+  }
+  const int64_t wpb = kDecodeThreads / kWave;
+  int64_t blocks = (a.n_groups + wpb - 1) / wpb;
+  const int64_t cap = int64_t(device_info().cus) * kDecodeBlocksPerCU;
+  if (blocks > cap) blocks = cap;
+  if (a.max_blocks > 0 && blocks > a.max_blocks) blocks = a.max_blocks;
+  const size_t shm = 256 + size_t(row_bytes((F == JERO_Q8_0 || F == JERO_Q4_0) ? JERO_ACT_Q8 : JERO_Q8_K, a.K));
+  hipLaunchKernelGGL((dgemv_kernel<F, LPR, UPL, R, OUT>), dim3(unsigned(blocks)), dim3(kDecodeThreads),
+                     (shm + 15) & ~size_t(15), s, a);
+}
+
+template <int F, int OUT>
+int dgemv_fmt(const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t s) {
+  const int U = a.U;
+  const int lpr = U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4;
+  const int upl = (U + lpr - 1) / lpr;
+  if (lpr == 4) {
+    dgemv_one<F, 4, 1, 2, OUT>(a, rows_or_pairs, s);
+  } else if (lpr == 16) {
+    dgemv_one<F, 16, 1, 2, OUT>(a, rows_or_pairs, s);
+  } else if (lpr == 32) {
+    dgemv_one<F, 32, 1, 2, OUT>(a, rows_or_pairs, s);
+  } else if (upl == 1) {
+    dgemv_one<F, 64, 1, 2, OUT>(a, rows_or_pairs, s);
+  } else if (upl == 2) {
+    dgemv_one<F, 64, 2, 2, OUT>(a, rows_or_pairs, s);
+  } else if (upl <= 3) {
+    dgemv_one<F, 64, 3, 2, OUT>(a, rows_or_pairs, s);
+  } else if (upl <= 4) {
+    dgemv_one<F, 64, 4, 2, OUT>(a, rows_or_pairs, s);
+  } else {
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: row of " + std::to_string(a.K) + " elements too long");
+  }
+  return JERO_OK;
+}
+
+template <int OUT>
+int dgemv_out(int quant, const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t s) {
+  switch (quant) {
+    case JERO_Q4_K: return dgemv_fmt<JERO_Q4_K, OUT>(a, rows_or_pairs, s);
+    case JERO_Q6_K: return dgemv_fmt<JERO_Q6_K, OUT>(a, rows_or_pairs, s);
+    case JERO_Q6_K_R: return dgemv_fmt<JERO_Q6_K_R, OUT>(a, rows_or_pairs, s);
+    case JERO_Q8_0: return dgemv_fmt<JERO_Q8_0, OUT>(a, rows_or_pairs, s);
+    case JERO_Q4_0: return dgemv_fmt<JERO_Q4_0, OUT>(a, rows_or_pairs, s);
+  }
+  return fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: unsupported weight quantization " + std::to_string(quant));
+}
+
+}  // namespace
+
+int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s) {
+  int rc;
+  switch (out_mode) {
+    case kOutStore: rc = dgemv_out<kOutStore>(quant, a, a.N, s); break;
+    case kOutResid: rc = dgemv_out<kOutResid>(quant, a, a.N, s); break;
+    case kOutSwiglu: rc = dgemv_out<kOutSwiglu>(quant, a, a.half, s); break;
+    case kOutArgmax: rc = dgemv_out<kOutArgmax>(quant, a, a.N, s); break;
+    default: return fail(JERO_ERR_INVALID_ARGUMENT, "decode: bad output mode");
+  }
+  if (rc) return rc;
+  return check_launch("decode gemv");
+}
+
+int dgemv_blocks(int quant, int64_t K, int64_t N, int out_mode) {
+  const int U = units_per_row(quant, K);
+  const int lpr = U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4;
+  const int64_t G = kWave / lpr, R = 2;
+  int64_t n_groups;
+  if (out_mode == kOutSwiglu) {
+    const int64_t per = G == 1 ? R / 2 : R * (G / 2);
+    n_groups = (N / 2 + per - 1) / per;
+  } else {
+    n_groups = (N + G * R - 1) / (G * R);
+  }
+  const int64_t wpb = kDecodeThreads / kWave;
+  int64_t blocks = (n_groups + wpb - 1) / wpb;
+  const int64_t cap = int64_t(device_info().cus) * kDecodeBlocksPerCU;
+  return int(blocks < cap ? blocks : cap);
+}
+
+int dgemv_max_k(int quant) {
+  // UPL <= 4 units per lane, and the prologue's kDecodeMaxActBlocks blocks per wave
+  return (quant == JERO_Q8_0 || quant == JERO_Q4_0) ? 32 * 2 * (kDecodeThreads / kWave) * kDecodeMaxActBlocks
+                                                    : 256 * (kDecodeThreads / kWave) * kDecodeMaxActBlocks;
+}
+
+int launch_embed(int quant, const void* w, int64_t rb, int H, int64_t vocab, const int32_t* token, float* out,
+                 hipStream_t s) {
+  hipLaunchKernelGGL(embed_kernel, dim3(unsigned((H + 255) / 256)), dim3(256), 0, s, quant,
+                     static_cast<const uint8_t*>(w), rb, H, vocab, token, out);
+  return check_launch("embed");
+}
+
+int launch_argmax_final(const float* v, const int64_t* idx, int n, int32_t* token, int64_t* pos, hipStream_t s) {
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1024), 0, s, v, idx, n, token, pos);
+  return check_launch("argmax");
+}
+
+int launch_set_state(int32_t* token, int64_t* pos, int32_t t, int64_t p, hipStream_t s) {
+  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, s, token, pos, t, p);
+  return check_launch("set state");
+}
+
+}  // namespace jero

@@ -79,10 +79,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const uint8_t* __res
     }
     for (int d = 4 * n16 + threadIdx.x; d < act_bytes / 4; d += kGemvThreads)
       reinterpret_cast<uint32_t*>(s_act)[d] = reinterpret_cast<const uint32_t*>(xq)[d];
-    // Wait for this wave's LDS writes only (not its weight loads), then the workgroup barrier.
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt untouched
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+    lds_barrier();  // this wave's LDS writes only, not its weight loads
     if (row0 >= N) return;
     act_src = s_act;
   }

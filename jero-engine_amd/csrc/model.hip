@@ -1,0 +1,444 @@
+// model.hip -- device-resident dense decoder and its decode step (host orchestration).
+//
+// Mirrors the Qwen/Llama decode path of the reference: ModelWeights::tensor(name) lookups of
+// GGUF tensor names, the KV arena (src/kv.rs:43-122; used by the recipes as flat per-layer
+// K/V rings, src/qwen_deepseek.rs:643-694) and execute_token_standard_with_hidden
+// (src/qwen_deepseek.rs:1239-1314) followed by sample_greedy_argmax (src/engine.rs:1873-1895).
+//
+// Weights are uploaded once (set_tensor) and regrouped once (finalize): Q|K|V rows become one
+// tensor when they share a format, gate and up rows one tensor (rows [0, ffn) gate, [ffn, 2ffn)
+// up) so one kernel produces silu(gate) * up, and every Q6_K matrix is re-laid out as Q6_K_R.
+// The step itself only enqueues kernels -- no allocation, copy or memset -- so it can be captured
+// in a HIP graph.  Token and position live in device memory: the step reads them, and its last
+// kernel stores the greedy token and advances the position, so replaying the graph decodes
+// consecutive tokens.
+#include <map>
+#include <string>
+#include <vector>
+
+#include "attention.h"
+#include "decode.h"
+#include "gemv.h"
+#include "jero_common.h"
+#include "runtime.h"
+
+namespace jero {
+
+struct DevTensor {
+  int quant = -1;
+  void* dev = nullptr;
+  size_t bytes = 0;
+  int64_t n_in = 0, n_out = 0;
+  bool present() const { return dev != nullptr; }
+};
+
+struct LayerW {
+  DevTensor attn_norm, ffn_norm, q_norm, k_norm;
+  DevTensor wq, wk, wv, wo, gate, up, down;
+  DevTensor qkv;      // fused Q|K|V (or Q|K when V's format differs)
+  bool v_separate = false;
+  DevTensor gate_up;  // fused gate|up
+};
+
+}  // namespace jero
+
+struct jero_model {
+  jero_model_config cfg{};
+  jero::DevTensor tok_embd, output, output_norm;
+  std::vector<jero::LayerW> layers;
+  bool finalized = false;
+  // device state
+  float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
+  float* attn_ws = nullptr;
+  float* amax_v = nullptr;
+  int64_t* amax_i = nullptr;
+  int32_t* token = nullptr;
+  int64_t* pos = nullptr;
+  void* kv = nullptr;
+  size_t kv_bytes = 0;
+  std::vector<void*> owned;
+};
+
+namespace jero {
+
+static int dev_alloc(jero_model* m, size_t bytes, void** p) {
+  if (hipMalloc(p, bytes < 256 ? 256 : bytes) != hipSuccess)
+    return fail(JERO_ERR_INSUFFICIENT_MEMORY, "model: hipMalloc of " + std::to_string(bytes) + " bytes failed");
+  m->owned.push_back(*p);
+  return JERO_OK;
+}
+
+static void dev_free(jero_model* m, void* p) {
+  for (auto& q : m->owned)
+    if (q == p) {
+      (void)hipFree(q);
+      q = nullptr;
+    }
+}
+
+static int64_t q_dim(const jero_model_config& c) { return int64_t(c.n_heads_q) * c.head_dim; }
+static int64_t kv_dim(const jero_model_config& c) { return int64_t(c.n_heads_kv) * c.head_dim; }
+
+// Expected (n_in, n_out) of a named tensor; returns false if the name is unknown.
+static bool expected_shape(const jero_model_config& c, const std::string& base, int64_t& n_in, int64_t& n_out) {
+  const int64_t H = c.hidden, F = c.ffn, Q = q_dim(c), KV = kv_dim(c);
+  static const std::map<std::string, int> kinds = {
+      {"attn_norm.weight", 0}, {"ffn_norm.weight", 1}, {"attn_q_norm.weight", 2}, {"attn_k_norm.weight", 3},
+      {"attn_q.weight", 4},    {"attn_k.weight", 5},   {"attn_v.weight", 6},      {"attn_output.weight", 7},
+      {"ffn_gate.weight", 8},  {"ffn_up.weight", 9},   {"ffn_down.weight", 10}};
+  auto it = kinds.find(base);
+  if (it == kinds.end()) return false;
+  switch (it->second) {
+    case 0:
+    case 1: n_in = H, n_out = 1; break;
+    case 2:
+    case 3: n_in = c.head_dim, n_out = 1; break;
+    case 4: n_in = H, n_out = Q; break;
+    case 5:
+    case 6: n_in = H, n_out = KV; break;
+    case 7: n_in = Q, n_out = H; break;
+    case 8:
+    case 9: n_in = H, n_out = F; break;
+    case 10: n_in = F, n_out = H; break;
+  }
+  return true;
+}
+
+static DevTensor* find_slot(jero_model* m, const std::string& name, int64_t& n_in, int64_t& n_out) {
+  const auto& c = m->cfg;
+  if (name == "token_embd.weight") {
+    n_in = c.hidden, n_out = c.vocab;
+    return &m->tok_embd;
+  }
+  if (name == "output.weight") {
+    n_in = c.hidden, n_out = c.vocab;
+    return &m->output;
+  }
+  if (name == "output_norm.weight") {
+    n_in = c.hidden, n_out = 1;
+    return &m->output_norm;
+  }
+  if (name.rfind("blk.", 0) != 0) return nullptr;
+  size_t dot = name.find('.', 4);
+  if (dot == std::string::npos) return nullptr;
+  int64_t L = -1;
+  try {
+    L = std::stoll(name.substr(4, dot - 4));
+  } catch (...) {
+    return nullptr;
+  }
+  if (L < 0 || L >= c.n_layers) return nullptr;
+  std::string base = name.substr(dot + 1);
+  if (!expected_shape(c, base, n_in, n_out)) return nullptr;
+  LayerW& l = m->layers[size_t(L)];
+  static const std::map<std::string, DevTensor LayerW::*> slots = {
+      {"attn_norm.weight", &LayerW::attn_norm}, {"ffn_norm.weight", &LayerW::ffn_norm},
+      {"attn_q_norm.weight", &LayerW::q_norm},  {"attn_k_norm.weight", &LayerW::k_norm},
+      {"attn_q.weight", &LayerW::wq},           {"attn_k.weight", &LayerW::wk},
+      {"attn_v.weight", &LayerW::wv},           {"attn_output.weight", &LayerW::wo},
+      {"ffn_gate.weight", &LayerW::gate},       {"ffn_up.weight", &LayerW::up},
+      {"ffn_down.weight", &LayerW::down}};
+  return &(l.*(slots.at(base)));
+}
+
+static bool is_norm(const std::string& name) {
+  return name.size() >= 12 && name.compare(name.size() - 12, 12, "_norm.weight") == 0;
+}
+
+// Rows of a and b stacked into one new tensor (same format and n_in).
+static int concat_rows(jero_model* m, std::vector<DevTensor*> parts, DevTensor& out) {
+  size_t total = 0;
+  for (auto* t : parts) total += t->bytes;
+  void* p = nullptr;
+  int rc = dev_alloc(m, total, &p);
+  if (rc) return rc;
+  size_t off = 0;
+  int64_t rows = 0;
+  for (auto* t : parts) {
+    rc = check_hip(hipMemcpy(static_cast<uint8_t*>(p) + off, t->dev, t->bytes, hipMemcpyDeviceToDevice), "concat");
+    if (rc) return rc;
+    off += t->bytes;
+    rows += t->n_out;
+  }
+  out = {parts[0]->quant, p, total, parts[0]->n_in, rows};
+  for (auto* t : parts) {
+    dev_free(m, t->dev);
+    t->dev = nullptr;
+  }
+  return JERO_OK;
+}
+
+// Q6_K tensors become Q6_K_R (same bytes, aligned planes).
+static int repack_if_q6k(jero_model* m, DevTensor& t) {
+  if (t.quant != JERO_Q6_K) return JERO_OK;
+  void* p = nullptr;
+  int rc = dev_alloc(m, t.bytes, &p);
+  if (rc) return rc;
+  int q = 0;
+  rc = launch_repack(JERO_Q6_K, t.dev, t.n_in, t.n_out, p, &q, nullptr);
+  if (rc) return rc;
+  rc = check_hip(hipDeviceSynchronize(), "repack");
+  if (rc) return rc;
+  dev_free(m, t.dev);
+  t.dev = p;
+  t.quant = q;
+  return JERO_OK;
+}
+
+static int gemv(jero_model* m, const DevTensor& w, const float* x, const float* norm, float eps, int out_mode,
+                float* y, int64_t half, hipStream_t s) {
+  (void)m;
+  DGemvArgs a{};
+  a.w = static_cast<const uint8_t*>(w.dev);
+  a.rb = row_bytes(w.quant, w.n_in);
+  a.U = int(w.n_in / ((w.quant == JERO_Q8_0 || w.quant == JERO_Q4_0) ? 32 : 64));
+  a.N = w.n_out;
+  a.x = x;
+  a.norm_w = norm;
+  a.eps = eps;
+  a.K = int(w.n_in);
+  a.y = y;
+  a.half = half;
+  a.amax_v = m->amax_v;
+  a.amax_i = m->amax_i;
+  return launch_dgemv(w.quant, out_mode, a, s);
+}
+
+}  // namespace jero
+
+using namespace jero;
+
+extern "C" int jero_hip_model_create(const jero_model_config* cfg, jero_model** out) {
+  if (!cfg || !out) return fail(JERO_ERR_INVALID_ARGUMENT, "model_create: null pointer");
+  *out = nullptr;
+  const auto& c = *cfg;
+  if (c.hidden <= 0 || c.ffn <= 0 || c.n_layers <= 0 || c.vocab <= 0 || c.kv_capacity <= 0)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "model_create: empty dimension");
+  int rc = check_attention_shape(c.n_heads_q, c.n_heads_kv, c.head_dim, c.kv_capacity);
+  if (rc) return rc;
+  if (c.kv_dtype != JERO_KV_F16 && c.kv_dtype != JERO_KV_F32)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "model_create: kv_dtype must be JERO_KV_F16 or JERO_KV_F32");
+  if (c.hidden % 32 || c.ffn % 32 || q_dim(c) % 32)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "model_create: hidden, ffn and q dims must be multiples of 32");
+  auto* m = new jero_model();
+  m->cfg = c;
+  m->layers.resize(size_t(c.n_layers));
+  const int64_t Q = q_dim(c), KV = kv_dim(c);
+  const size_t es = c.kv_dtype == JERO_KV_F16 ? 2 : 4;
+  m->kv_bytes = size_t(c.n_layers) * 2 * size_t(c.kv_capacity) * size_t(KV) * es;
+  const int max_blocks = 1024 * 4;
+  void* p;
+  if ((rc = dev_alloc(m, m->kv_bytes, &m->kv)) ||
+      (rc = check_hip(hipMemset(m->kv, 0, m->kv_bytes), "kv zero")) ||
+      (rc = dev_alloc(m, sizeof(float) * size_t(c.hidden), &p)) || ((m->hidden = static_cast<float*>(p)), false) ||
+      (rc = dev_alloc(m, sizeof(float) * size_t(Q + 2 * KV), &p)) || ((m->qkv = static_cast<float*>(p)), false) ||
+      (rc = dev_alloc(m, sizeof(float) * size_t(Q), &p)) || ((m->attn = static_cast<float*>(p)), false) ||
+      (rc = dev_alloc(m, sizeof(float) * size_t(c.ffn), &p)) || ((m->act = static_cast<float*>(p)), false) ||
+      (rc = dev_alloc(m, sizeof(float) * size_t(c.vocab), &p)) || ((m->logits = static_cast<float*>(p)), false) ||
+      (rc = dev_alloc(m, attn_workspace_bytes(c.n_heads_q, c.head_dim, int(c.kv_capacity)), &p)) ||
+      ((m->attn_ws = static_cast<float*>(p)), false) ||
+      (rc = dev_alloc(m, sizeof(float) * max_blocks, &p)) || ((m->amax_v = static_cast<float*>(p)), false) ||
+      (rc = dev_alloc(m, sizeof(int64_t) * max_blocks, &p)) || ((m->amax_i = static_cast<int64_t*>(p)), false) ||
+      (rc = dev_alloc(m, sizeof(int32_t), &p)) || ((m->token = static_cast<int32_t*>(p)), false) ||
+      (rc = dev_alloc(m, sizeof(int64_t), &p)) || ((m->pos = static_cast<int64_t*>(p)), false)) {
+    for (void* q : m->owned)
+      if (q) (void)hipFree(q);
+    delete m;
+    return rc;
+  }
+  if ((rc = check_hip(hipMemset(m->token, 0, sizeof(int32_t)), "state")) ||
+      (rc = check_hip(hipMemset(m->pos, 0, sizeof(int64_t)), "state"))) {
+    for (void* q : m->owned)
+      if (q) (void)hipFree(q);
+    delete m;
+    return rc;
+  }
+  *out = m;
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_model_destroy(jero_model* m) {
+  if (!m) return JERO_OK;
+  (void)hipDeviceSynchronize();
+  for (void* q : m->owned)
+    if (q) (void)hipFree(q);
+  delete m;
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_model_set_tensor(jero_model* m, const char* name, int quant, const void* src, size_t nbytes,
+                                         int64_t n_in, int64_t n_out, int src_on_device) {
+  if (!m || !name || !src) return fail(JERO_ERR_INVALID_ARGUMENT, "set_tensor: null pointer");
+  if (m->finalized) return fail(JERO_ERR_INVALID_ARGUMENT, "set_tensor: model already finalized");
+  int64_t ein = 0, eout = 0;
+  DevTensor* slot = find_slot(m, name, ein, eout);
+  if (!slot) return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string("set_tensor: unknown tensor '") + name + "'");
+  if (n_in != ein || n_out != eout)
+    return fail(JERO_ERR_TENSOR_BOUNDS, std::string("set_tensor: '") + name + "' has shape [" + std::to_string(n_in) +
+                                            ", " + std::to_string(n_out) + "], expected [" + std::to_string(ein) +
+                                            ", " + std::to_string(eout) + "]");
+  const bool norm = is_norm(name);
+  if (norm && quant != JERO_F32)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string("set_tensor: norm '") + name + "' must be F32");
+  if (!norm && !is_weight_quant(quant))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH,
+                std::string("set_tensor: '") + name + "' quantization " + std::to_string(quant) + " unsupported");
+  const int64_t rb = row_bytes(quant, n_in);
+  if (rb < 0 || size_t(rb) * size_t(n_out) != nbytes)
+    return fail(JERO_ERR_TENSOR_BOUNDS, std::string("set_tensor: '") + name + "' byte size " + std::to_string(nbytes) +
+                                            " does not match its shape");
+  if (!norm && std::string(name) != "token_embd.weight" && n_in > dgemv_max_k(quant))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string("set_tensor: '") + name + "' rows of " +
+                                                  std::to_string(n_in) + " elements exceed the decode limit " +
+                                                  std::to_string(dgemv_max_k(quant)));
+  if (slot->dev) dev_free(m, slot->dev);
+  void* p = nullptr;
+  int rc = dev_alloc(m, nbytes, &p);
+  if (rc) return rc;
+  rc = check_hip(hipMemcpy(p, src, nbytes, src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice),
+                 "set_tensor upload");
+  if (rc) return rc;
+  *slot = {quant, p, nbytes, n_in, n_out};
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_model_finalize(jero_model* m) {
+  if (!m) return fail(JERO_ERR_INVALID_ARGUMENT, "finalize: null model");
+  if (m->finalized) return JERO_OK;
+  const auto& c = m->cfg;
+  auto need = [&](const DevTensor& t, const std::string& n) -> int {
+    if (!t.present()) return fail(JERO_ERR_CAPABILITY_MISMATCH, "finalize: tensor '" + n + "' missing");
+    return JERO_OK;
+  };
+  int rc;
+  if ((rc = need(m->tok_embd, "token_embd.weight")) || (rc = need(m->output, "output.weight")) ||
+      (rc = need(m->output_norm, "output_norm.weight")))
+    return rc;
+  for (int64_t L = 0; L < c.n_layers; L++) {
+    LayerW& l = m->layers[size_t(L)];
+    const std::string p = "blk." + std::to_string(L) + ".";
+    if ((rc = need(l.attn_norm, p + "attn_norm.weight")) || (rc = need(l.ffn_norm, p + "ffn_norm.weight")) ||
+        (rc = need(l.wq, p + "attn_q.weight")) || (rc = need(l.wk, p + "attn_k.weight")) ||
+        (rc = need(l.wv, p + "attn_v.weight")) || (rc = need(l.wo, p + "attn_output.weight")) ||
+        (rc = need(l.gate, p + "ffn_gate.weight")) || (rc = need(l.up, p + "ffn_up.weight")) ||
+        (rc = need(l.down, p + "ffn_down.weight")))
+      return rc;
+    if (c.qk_norm && ((rc = need(l.q_norm, p + "attn_q_norm.weight")) || (rc = need(l.k_norm, p + "attn_k_norm.weight"))))
+      return rc;
+    if (l.wq.quant != l.wk.quant)
+      return fail(JERO_ERR_CAPABILITY_MISMATCH, "finalize: attn_q and attn_k of layer " + std::to_string(L) +
+                                                    " must share a format");
+    if (l.gate.quant != l.up.quant)
+      return fail(JERO_ERR_CAPABILITY_MISMATCH, "finalize: ffn_gate and ffn_up of layer " + std::to_string(L) +
+                                                    " must share a format");
+    l.v_separate = l.wv.quant != l.wq.quant;
+    if (l.v_separate) {
+      if ((rc = concat_rows(m, {&l.wq, &l.wk}, l.qkv))) return rc;
+      if ((rc = repack_if_q6k(m, l.wv))) return rc;
+    } else {
+      if ((rc = concat_rows(m, {&l.wq, &l.wk, &l.wv}, l.qkv))) return rc;
+    }
+    if ((rc = repack_if_q6k(m, l.qkv))) return rc;
+    if ((rc = concat_rows(m, {&l.gate, &l.up}, l.gate_up))) return rc;
+    if ((rc = repack_if_q6k(m, l.gate_up))) return rc;
+    if ((rc = repack_if_q6k(m, l.wo))) return rc;
+    if ((rc = repack_if_q6k(m, l.down))) return rc;
+  }
+  if ((rc = repack_if_q6k(m, m->output))) return rc;
+  m->finalized = true;
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_model_kv(jero_model* m, int64_t layer, void** k_ring, void** v_ring) {
+  if (!m || !k_ring || !v_ring) return fail(JERO_ERR_INVALID_ARGUMENT, "model_kv: null pointer");
+  if (layer < 0 || layer >= m->cfg.n_layers) return fail(JERO_ERR_TENSOR_BOUNDS, "model_kv: layer out of range");
+  const size_t es = m->cfg.kv_dtype == JERO_KV_F16 ? 2 : 4;
+  const size_t ring = size_t(m->cfg.kv_capacity) * size_t(kv_dim(m->cfg)) * es;
+  uint8_t* base = static_cast<uint8_t*>(m->kv) + size_t(layer) * 2 * ring;
+  *k_ring = base;
+  *v_ring = base + ring;
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_model_state(jero_model* m, int32_t** token_dev, int64_t** pos_dev, float** logits_dev) {
+  if (!m) return fail(JERO_ERR_INVALID_ARGUMENT, "model_state: null model");
+  if (token_dev) *token_dev = m->token;
+  if (pos_dev) *pos_dev = m->pos;
+  if (logits_dev) *logits_dev = m->logits;
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_model_set_position(jero_model* m, int32_t token, int64_t pos, void* stream) {
+  if (!m) return fail(JERO_ERR_INVALID_ARGUMENT, "set_position: null model");
+  if (token < 0 || token >= m->cfg.vocab)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "set_position: token " + std::to_string(token) + " outside the vocabulary");
+  if (pos < 0) return fail(JERO_ERR_CONTEXT_LENGTH_EXCEEDED, "set_position: negative position");
+  return launch_set_state(m->token, m->pos, token, pos, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
+  if (!m) return fail(JERO_ERR_INVALID_ARGUMENT, "decode_step: null model");
+  if (!m->finalized) return fail(JERO_ERR_INVALID_ARGUMENT, "decode_step: call jero_hip_model_finalize first");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const auto& c = m->cfg;
+  const int64_t Q = q_dim(c), KV = kv_dim(c);
+  const float eps_attn = c.rms_eps;
+  const float eps_ffn = c.rms_eps > 1e-6f ? c.rms_eps : 1e-6f;  // rms_eps.max(1e-6), :1250
+  int rc = launch_embed(m->tok_embd.quant, m->tok_embd.dev, row_bytes(m->tok_embd.quant, c.hidden), int(c.hidden),
+                        c.vocab, m->token, m->hidden, s);
+  if (rc) return rc;
+  const size_t es = c.kv_dtype == JERO_KV_F16 ? 2 : 4;
+  const size_t ring = size_t(c.kv_capacity) * size_t(KV) * es;
+  for (int64_t L = 0; L < c.n_layers; L++) {
+    const LayerW& l = m->layers[size_t(L)];
+    // attention sublayer: RMSNorm -> Q|K|V
+    rc = gemv(m, l.qkv, m->hidden, static_cast<const float*>(l.attn_norm.dev), eps_attn, kOutStore, m->qkv, 0, s);
+    if (rc) return rc;
+    if (l.v_separate) {
+      rc = gemv(m, l.wv, m->hidden, static_cast<const float*>(l.attn_norm.dev), eps_attn, kOutStore,
+                m->qkv + Q + KV, 0, s);
+      if (rc) return rc;
+    }
+    // QK-norm, RoPE, KV append, attention over the ring
+    AttnParams p{};
+    uint8_t* base = static_cast<uint8_t*>(m->kv) + size_t(L) * 2 * ring;
+    p.q = m->qkv;
+    p.k = base;
+    p.v = base + ring;
+    p.kv_dtype = c.kv_dtype;
+    p.nkv = c.n_heads_kv;
+    p.group = c.n_heads_q / c.n_heads_kv;
+    p.hd = c.head_dim;
+    p.active = int(c.kv_capacity);
+    p.scale = 1.0f / sqrtf(float(c.head_dim));
+    p.part_o = m->attn_ws;
+    p.k_new = m->qkv + Q;
+    p.v_new = m->qkv + Q + KV;
+    p.q_norm = c.qk_norm ? static_cast<const float*>(l.q_norm.dev) : nullptr;
+    p.k_norm = c.qk_norm ? static_cast<const float*>(l.k_norm.dev) : nullptr;
+    p.eps = eps_attn;
+    p.theta = c.rope_theta;
+    p.slot = -1;
+    p.k_write = base;
+    p.v_write = base + ring;
+    p.pos_dev = m->pos;
+    p.capacity = c.kv_capacity;
+    rc = launch_attention(p, true, m->attn, s);
+    if (rc) return rc;
+    // output projection + residual
+    rc = gemv(m, l.wo, m->attn, nullptr, 0.f, kOutResid, m->hidden, 0, s);
+    if (rc) return rc;
+    // FFN: RMSNorm -> gate|up -> SwiGLU -> down + residual
+    rc = gemv(m, l.gate_up, m->hidden, static_cast<const float*>(l.ffn_norm.dev), eps_ffn, kOutSwiglu, m->act,
+              c.ffn, s);
+    if (rc) return rc;
+    rc = gemv(m, l.down, m->act, nullptr, 0.f, kOutResid, m->hidden, 0, s);
+    if (rc) return rc;
+  }
+  // final norm -> LM head -> greedy token
+  rc = gemv(m, m->output, m->hidden, static_cast<const float*>(m->output_norm.dev), eps_ffn, kOutArgmax, m->logits, 0,
+            s);
+  if (rc) return rc;
+  return launch_argmax_final(m->amax_v, m->amax_i, dgemv_blocks(m->output.quant, c.hidden, c.vocab, kOutArgmax),
+                             m->token, m->pos, s);
+}

@@ -53,6 +53,14 @@ _SIGS = {
     "jero_hip_moe_ffn": (_I32, [_P, _P, _I64, _I64, _I32, _I32, _P, _SZ, _I32, _P, _SZ, _I32, _P, _SZ, _I64, _I64,
                                 _P, _P, _P, _P, _SZ, _P]),
     "jero_hip_moe_workspace_bytes": (_SZ, [_I64, _I64, _I32, _I64, _I64]),
+    "jero_hip_model_create": (_I32, [_P, C.POINTER(_P)]),
+    "jero_hip_model_destroy": (_I32, [_P]),
+    "jero_hip_model_set_tensor": (_I32, [_P, C.c_char_p, _I32, _P, _SZ, _I64, _I64, _I32]),
+    "jero_hip_model_finalize": (_I32, [_P]),
+    "jero_hip_model_kv": (_I32, [_P, _I64, C.POINTER(_P), C.POINTER(_P)]),
+    "jero_hip_model_state": (_I32, [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_P)]),
+    "jero_hip_model_set_position": (_I32, [_P, _I32, _I64, _P]),
+    "jero_hip_decode_step": (_I32, [_P, _P]),
 }
 
 
@@ -253,3 +261,102 @@ def dequantize_rows(weights, row0, n_rows, out, stream=None):
 
 def dequantize_token_row(weights, row, out, stream=None):
     return dequantize_rows(weights, row, 1, out, stream)
+
+
+# ---------------------------------------------------------------- device-resident decoder
+
+class ModelConfig(C.Structure):
+    """jero_model_config."""
+    _fields_ = [("hidden", C.c_int64), ("ffn", C.c_int64), ("n_layers", C.c_int64), ("vocab", C.c_int64),
+                ("n_heads_q", C.c_int), ("n_heads_kv", C.c_int), ("head_dim", C.c_int), ("rms_eps", C.c_float),
+                ("rope_theta", C.c_float), ("kv_capacity", C.c_int64), ("kv_dtype", C.c_int), ("qk_norm", C.c_int)]
+
+
+_hip = None
+
+
+def _memcpy(dst_ptr, src_ptr, nbytes):
+    """Synchronous device/host copy through the HIP runtime (hipMemcpyDefault)."""
+    global _hip
+    if _hip is None:
+        _hip = C.CDLL("libamdhip64.so")
+        _hip.hipMemcpy.argtypes = [_P, _P, _SZ, C.c_int]
+        _hip.hipMemcpy.restype = C.c_int
+    rc = _hip.hipMemcpy(C.c_void_p(dst_ptr), C.c_void_p(src_ptr), nbytes, 4)
+    if rc != 0:
+        raise K3Error(20, f"hipMemcpy failed ({rc})")
+
+
+class DecodeModel:
+    """A device-resident dense decoder (Qwen3 / Llama layout): the ArchRecipe::decode_step path
+    of the reference (src/qwen_deepseek.rs:1441-1460) with ctx state (token, position, logits)
+    held on the device."""
+
+    def __init__(self, hidden, ffn, n_layers, vocab, n_heads_q, n_heads_kv, head_dim, rms_eps, rope_theta,
+                 kv_capacity, kv_dtype=KV_F16, qk_norm=True):
+        self.cfg = ModelConfig(hidden, ffn, n_layers, vocab, n_heads_q, n_heads_kv, head_dim, rms_eps, rope_theta,
+                               kv_capacity, kv_dtype, 1 if qk_norm else 0)
+        h = C.c_void_p()
+        check(lib().jero_hip_model_create(C.byref(self.cfg), C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().jero_hip_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_tensor(self, name, quant, data, n_in, n_out):
+        """data: a numpy array (host) or a torch tensor (host or device) holding the GGUF bytes."""
+        import numpy as np
+        if isinstance(data, np.ndarray):
+            arr = np.ascontiguousarray(data)
+            ptr, nbytes, on_dev = arr.ctypes.data, arr.nbytes, 0
+        else:
+            ptr, nbytes, on_dev = data.data_ptr(), data.numel() * data.element_size(), 1 if data.is_cuda else 0
+        check(lib().jero_hip_model_set_tensor(self.h, name.encode(), quant, C.c_void_p(ptr), nbytes, n_in, n_out,
+                                              on_dev))
+
+    def finalize(self):
+        check(lib().jero_hip_model_finalize(self.h))
+
+    def kv_ptrs(self, layer):
+        k, v = C.c_void_p(), C.c_void_p()
+        check(lib().jero_hip_model_kv(self.h, layer, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+    def write_kv(self, layer, k, v):
+        """Copies torch tensors k, v ([capacity][n_kv*hd] in the cache dtype) into layer's rings."""
+        kp, vp = self.kv_ptrs(layer)
+        _memcpy(kp, k.data_ptr(), k.numel() * k.element_size())
+        _memcpy(vp, v.data_ptr(), v.numel() * v.element_size())
+
+    def state_ptrs(self):
+        t, p, l = C.c_void_p(), C.c_void_p(), C.c_void_p()
+        check(lib().jero_hip_model_state(self.h, C.byref(t), C.byref(p), C.byref(l)))
+        return t.value, p.value, l.value
+
+    def set_position(self, token, pos, stream=None):
+        check(lib().jero_hip_model_set_position(self.h, token, pos, _stream(stream)))
+
+    def decode_step(self, stream=None):
+        check(lib().jero_hip_decode_step(self.h, _stream(stream)))
+
+    def read_logits(self, out):
+        _, _, lp = self.state_ptrs()
+        _memcpy(out.data_ptr(), lp, self.cfg.vocab * 4)
+        return out
+
+    def read_token_pos(self):
+        import numpy as np
+        tp, pp, _ = self.state_ptrs()
+        t = np.zeros(1, np.int32)
+        p = np.zeros(1, np.int64)
+        _memcpy(t.ctypes.data, tp, 4)
+        _memcpy(p.ctypes.data, pp, 8)
+        return int(t[0]), int(p[0])

@@ -1,0 +1,52 @@
+"""Random-init dense decoder weights (Qwen3 layout) for the decode parity tests.
+
+Quantized matrices are uniform random payload bytes with N(0, 0.02)-scale fields (qdata);
+norm weights are 1 + 0.1 N(0, 1).  The Q4_K_M mix follows llama.cpp's public recipe:
+Q6_K for attn_v / ffn_down on layers i < n/8, i >= 7n/8 or (i - n/8) % 3 == 2; Q6_K head.
+"""
+import numpy as np
+
+from qdata import Q4_K, Q6_K, Q8_0, F32, rand_weights
+
+
+def q6k_layers(n):
+    return [i for i in range(n) if i < n // 8 or i >= 7 * n // 8 or (i - n // 8) % 3 == 2]
+
+
+def build(spec, seed=0, mix="q4_k_m"):
+    H, F, L, V = spec["hidden"], spec["ffn"], spec["n_layers"], spec["vocab"]
+    Q, KV, hd = spec["nq"] * spec["hd"], spec["nkv"] * spec["hd"], spec["hd"]
+    rng = np.random.default_rng(seed)
+    hi = set(q6k_layers(L)) if mix == "q4_k_m" else set()
+    t = {}
+    s = [seed * 100]
+
+    def mat(name, quant, n_in, n_out):
+        s[0] += 1
+        t[name] = (quant, rand_weights(quant, n_out, n_in, s[0]), n_in, n_out)
+
+    def norm(name, n):
+        t[name] = (F32, (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32), n, 1)
+
+    mat("token_embd.weight", Q4_K, H, V)
+    mat("output.weight", Q6_K, H, V)
+    norm("output_norm.weight", H)
+    for i in range(L):
+        p = f"blk.{i}."
+        norm(p + "attn_norm.weight", H)
+        norm(p + "ffn_norm.weight", H)
+        norm(p + "attn_q_norm.weight", hd)
+        norm(p + "attn_k_norm.weight", hd)
+        mat(p + "attn_q.weight", Q4_K, H, Q)
+        mat(p + "attn_k.weight", Q4_K, H, KV)
+        mat(p + "attn_v.weight", Q6_K if i in hi else Q4_K, H, KV)
+        mat(p + "attn_output.weight", Q4_K, Q, H)
+        mat(p + "ffn_gate.weight", Q4_K, H, F)
+        mat(p + "ffn_up.weight", Q4_K, H, F)
+        mat(p + "ffn_down.weight", Q6_K if i in hi else Q4_K, F, H)
+    return t
+
+
+def oracle_tensors(t):
+    """{name: (quant, array)} for pyoracle.DecodeModel."""
+    return {k: (v[0], v[1]) for k, v in t.items()}

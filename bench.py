@@ -13,7 +13,15 @@ average launch duration measured with events; peak = 8 TB/s HBM.
 cpu_baseline: the CPU oracle's GEMV (C restatement of the reference's matvec_any row-chunk
 path, scalar, pthreads over all host cores) on the same three shapes.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--copy-probe MB]
+Second part ("decode"): the full batch-1 decode step of a random-init Qwen3-8B-shaped model
+in Q4_K_M (36 layers, hidden 4096, 32/8 heads of 128, FFN 12288, vocab 151936; Q6_K head and
+Q6_K attn_v/ffn_down on 18 layers), f16 KV ring of 4096 slots pre-filled with N(0,1) values,
+greedy next token.  One step is captured in a HIP graph; each replay decodes the next token
+(the token and position advance on the device).  Reported as tokens/s and as fractions of the
+weight-only (4.671 GB/token) and weights+KV (+0.604 GB) HBM rooflines, next to the oracle's
+C decode step timed on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--copy-probe MB]
 """
 import argparse
 import json
@@ -28,6 +36,8 @@ HBM_PEAK_GBS = 8000.0
 SHAPES = [(4096, 4096), (4096, 12288), (12288, 4096)]  # (n_in, n_out), Q4_K
 HEAD = (4096, 151936)  # Q6_K output head
 ROTATE_BYTES = 768e6
+QWEN3_8B = dict(hidden=4096, ffn=12288, n_layers=36, vocab=151936, nq=32, nkv=8, hd=128, eps=1e-6, theta=1e6)
+KV_CAP = 4096
 
 
 def synth_weights(torch, J, quant, n_in, n_out, copies, dev, seed):
@@ -76,6 +86,112 @@ def time_graph(torch, fn, steps, warmup, stream):
     return s.elapsed_time(e) / 1e3 / steps
 
 
+def q6k_layers(n):
+    """llama.cpp's Q4_K_M rule: Q6_K attn_v / ffn_down on these layers."""
+    return [i for i in range(n) if i < n // 8 or i >= 7 * n // 8 or (i - n // 8) % 3 == 2]
+
+
+def decode_tensors(spec):
+    """(name, quant, n_in, n_out) of the Q4_K_M Qwen3 model."""
+    H, F, L, V = spec["hidden"], spec["ffn"], spec["n_layers"], spec["vocab"]
+    Q, KV, hd = spec["nq"] * spec["hd"], spec["nkv"] * spec["hd"], spec["hd"]
+    hi = set(q6k_layers(L))
+    out = [("token_embd.weight", 12, H, V), ("output.weight", 14, H, V), ("output_norm.weight", 0, H, 1)]
+    for i in range(L):
+        p = f"blk.{i}."
+        out += [(p + "attn_norm.weight", 0, H, 1), (p + "ffn_norm.weight", 0, H, 1),
+                (p + "attn_q_norm.weight", 0, hd, 1), (p + "attn_k_norm.weight", 0, hd, 1),
+                (p + "attn_q.weight", 12, H, Q), (p + "attn_k.weight", 12, H, KV),
+                (p + "attn_v.weight", 14 if i in hi else 12, H, KV), (p + "attn_output.weight", 12, Q, H),
+                (p + "ffn_gate.weight", 12, H, F), (p + "ffn_up.weight", 12, H, F),
+                (p + "ffn_down.weight", 14 if i in hi else 12, F, H)]
+    return out
+
+
+def bench_decode(torch, J, dev, stream, steps, warmup, keep_host):
+    """Builds the model on the device, times graph-replayed decode steps; optionally returns
+    host copies of every tensor and of the KV rings for the CPU baseline."""
+    spec = QWEN3_8B
+    m = J.DecodeModel(spec["hidden"], spec["ffn"], spec["n_layers"], spec["vocab"], spec["nq"], spec["nkv"],
+                      spec["hd"], spec["eps"], spec["theta"], KV_CAP, J.KV_F16, True)
+    host = {}
+    weight_bytes = 0
+    g = torch.Generator(device=dev)
+    g.manual_seed(4242)
+    for i, (name, quant, n_in, n_out) in enumerate(decode_tensors(spec)):
+        if quant == 0:
+            t = (1.0 + 0.1 * torch.randn(n_in, generator=g, device=dev)).float()
+        else:
+            t = synth_weights(torch, J, quant, n_in, n_out, 1, dev, 5000 + i)[0]
+            if name != "token_embd.weight":
+                weight_bytes += t.numel()
+        m.set_tensor(name, quant, t, n_in, n_out)
+        if keep_host:
+            host[name] = (quant, t.cpu().numpy())
+        del t
+    m.finalize()
+    kvd = spec["nkv"] * spec["hd"]
+    host_kv = None
+    if keep_host:
+        import numpy as np
+        host_kv = np.empty((spec["n_layers"], 2, KV_CAP, kvd), np.float32)
+    for L in range(spec["n_layers"]):
+        k = torch.randn(KV_CAP, kvd, generator=g, device=dev).half()
+        v = torch.randn(KV_CAP, kvd, generator=g, device=dev).half()
+        m.write_kv(L, k, v)
+        if keep_host:
+            host_kv[L, 0] = k.float().cpu().numpy()
+            host_kv[L, 1] = v.float().cpu().numpy()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        m.set_position(1, KV_CAP - 1, stream=stream)
+        for _ in range(max(1, warmup)):
+            m.decode_step(stream=stream)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            m.decode_step(stream=stream)
+        graph.replay()
+        stream.synchronize()
+        s0, e0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        e0.record(stream)
+    e0.synchronize()
+    t_tok = s0.elapsed_time(e0) / 1e3 / steps
+    tok, pos = m.read_token_pos()
+    kv_bytes = spec["n_layers"] * 2 * KV_CAP * kvd * 2
+    res = {"workload": "Qwen3-8B-shape Q4_K_M batch-1 greedy decode, 36 layers, f16 KV ring 4096 slots full",
+           "tok_s": round(1.0 / t_tok, 1), "ms_per_token": round(t_tok * 1e3, 4), "steps": steps,
+           "weight_bytes_per_token": weight_bytes, "kv_bytes_per_token": kv_bytes,
+           "frac_weight_roofline": round(weight_bytes / t_tok / 1e9 / HBM_PEAK_GBS, 4),
+           "frac_weights_kv_roofline": round((weight_bytes + kv_bytes) / t_tok / 1e9 / HBM_PEAK_GBS, 4),
+           "last_token": tok, "position": pos, "graph": "one decode step captured, replayed per token"}
+    m.close()
+    return res, host, host_kv
+
+
+def cpu_decode_baseline(O, host, host_kv, budget_s=10.0):
+    """The oracle's decode step (execute_token_standard_with_hidden restated in C, scalar,
+    pthreads over all host cores) on the same weights and KV values (widened to f32)."""
+    spec = QWEN3_8B
+    threads = len(os.sched_getaffinity(0))
+    om = O.DecodeModel(spec, host, KV_CAP)
+    done, t0, tok = 0, time.perf_counter(), 1
+    pos = KV_CAP - 1
+    while True:
+        logits = om.step(host_kv, tok, pos, threads=threads)
+        tok = int(logits.argmax())
+        pos += 1
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return done / el, threads, done, el
+
+
 def cpu_baseline(O, host_w, host_xq, budget_s=12.0):
     """Times the oracle's threaded GEMV on the same shapes; returns GB/s and the sample."""
     threads = len(os.sched_getaffinity(0))
@@ -86,7 +202,7 @@ def cpu_baseline(O, host_w, host_xq, budget_s=12.0):
             O.matvec(O.Q4_K, w, n_in, n_out, xq, threads=threads)
         done += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or done >= 2000:
+        if el >= budget_s:
             break
     return per_step * done / el / 1e9, threads, done, el
 
@@ -97,6 +213,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=50)
     ap.add_argument("--copy-probe", type=float, default=0.0,
                     help="also run one device copy of this many MB (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -195,6 +313,20 @@ def main():
                "sample": f"{reps} passes over the three Q4_K shapes (66.2 MB of weights, full size), "
                          f"{el:.1f} s, C restatement of matvec_any row chunks, scalar, pthreads"}
 
+    # ---- full decode step (extra)
+    decode = None
+    if not args.no_decode:
+        del bufs, views
+        torch.cuda.empty_cache()
+        decode, host, host_kv = bench_decode(torch, J, dev, stream, args.decode_steps, 3, not args.no_cpu)
+        if not args.no_cpu:
+            import pyoracle as O
+            tps, threads, reps, el = cpu_decode_baseline(O, host, host_kv)
+            decode["cpu_baseline"] = {"value": round(tps, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+                                      "sample": f"{reps} greedy steps of the same model from position {KV_CAP - 1}, "
+                                                f"{el:.1f} s, f32 KV ring"}
+            del host, host_kv
+
     out = {
         "metric": "Q4_K GEMV GB/s (% HBM peak); decode tok/s, 8B-shape Q4_K_M, 1 GPU",
         "value": round(value, 1),
@@ -215,6 +347,7 @@ def main():
         "cpu_baseline": cpu,
         "per_shape": per_shape,
         "q6k_head": head,
+        "decode": decode,
     }
     print(json.dumps(out))
 

@@ -29,6 +29,7 @@ struct AttnParams {
   void* k_write;         // same rings, writable
   void* v_write;
   const int64_t* pos_dev;  // if set: pos = *pos_dev, slot = pos % capacity, active = min(pos+1, capacity)
+  const float* rope_cs;    // if set: [hd/2][cos, sin] of this step's RoPE angles
   int64_t capacity;        // ring slots (grid is sized for all of them when pos_dev is set)
 };
 

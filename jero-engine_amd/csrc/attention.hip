@@ -8,7 +8,7 @@
 // V ring, each [capacity][n_kv * head_dim], f32 (as the reference) or f16 (half the bytes).
 //
 // Split-K ("flash decoding"): workgroup (split s, kv head h) owns positions
-// [s*128, s*128+128) of the active slots and all q heads of h's group.  It issues its K and V
+// [s*64, s*64+64) of the active slots and all q heads of h's group.  It issues its K and V
 // loads (16 bytes per lane, consecutive lanes on consecutive bytes) before anything else, so
 // a workgroup has its whole 2 x 128 x head_dim tile in flight; then it scores, exponentiates
 // against its local max and accumulates P V.  A second kernel merges the splits with the
@@ -23,8 +23,8 @@
 namespace jero {
 
 constexpr int kAttnThreads = 256;
-constexpr int kAttnChunk = 128;  // positions per workgroup
-constexpr int kMaxGroup = 8;     // q heads per kv head
+constexpr int kAttnChunk = 64;  // positions per workgroup
+constexpr int kMaxGroup = 8;    // q heads per kv head
 
 template <typename T>
 __device__ __forceinline__ void widen16(const u32x4 v, float* out);
@@ -59,7 +59,8 @@ __device__ __forceinline__ float rope_angle(int i, int hd, int64_t pos, float th
 // in a group of HD/2 lanes; returns the rotated pair.
 template <int HD>
 __device__ __forceinline__ float2 norm_rope_pair(float x0, float x1, int pair, const float* __restrict__ nw,
-                                                 float eps, int64_t pos, float theta, bool rope) {
+                                                 float eps, int64_t pos, float theta, bool rope,
+                                                 const float* __restrict__ rope_cs) {
   if (nw) {
     float ss = x0 * x0 + x1 * x1;
 #pragma unroll
@@ -69,13 +70,17 @@ __device__ __forceinline__ float2 norm_rope_pair(float x0, float x1, int pair, c
     x1 = x1 * inv * nw[2 * pair + 1];
   }
   if (!rope) return make_float2(x0, x1);
-  float a = rope_angle(pair, HD, pos, theta);
   float s, c;
-  sincosf(a, &s, &c);
+  if (rope_cs) {  // (cos, sin) of this step's angles, computed once per step
+    c = rope_cs[2 * pair];
+    s = rope_cs[2 * pair + 1];
+  } else {
+    sincosf(rope_angle(pair, HD, pos, theta), &s, &c);
+  }
   return make_float2(x0 * c - x1 * s, x0 * s + x1 * c);
 }
 
-template <int HD, typename KV, bool FUSED>
+template <int HD, typename KV, bool FUSED, int MAXG>
 __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p) {
   constexpr int EPL = 16 / int(sizeof(KV));     // elements per 16-byte load
   constexpr int LPP = HD / EPL;                 // lanes per position (K rows)
@@ -86,12 +91,12 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   constexpr int VSTEPS = kAttnChunk / NPS;
   static_assert(KSTEPS >= 1 && VSTEPS >= 1, "tile shape");
 
-  __shared__ float s_q[kMaxGroup][HD];
+  __shared__ float s_q[MAXG][HD];
   __shared__ float s_knew[HD];
   __shared__ float s_vnew[HD];
-  __shared__ float s_p[kMaxGroup][kAttnChunk];
-  __shared__ float s_red[kAttnThreads / kWave][kMaxGroup * HD];
-  __shared__ float s_m[kMaxGroup], s_l[kMaxGroup];
+  __shared__ float s_p[MAXG][kAttnChunk];
+  __shared__ float s_red[kAttnThreads / kWave][MAXG * HD];
+  __shared__ float s_m[MAXG], s_l[MAXG];
 
   const int split = blockIdx.x, kh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -150,7 +155,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
       }
       float2 r;
       if constexpr (FUSED)
-        r = norm_rope_pair<HD>(x0, x1, pair, is_k ? p.k_norm : p.q_norm, p.eps, pos_now, p.theta, true);
+        r = norm_rope_pair<HD>(x0, x1, pair, is_k ? p.k_norm : p.q_norm, p.eps, pos_now, p.theta, true, p.rope_cs);
       else
         r = make_float2(x0, x1);
       if (ok) {
@@ -193,13 +198,20 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
 #pragma unroll
       for (int e = 0; e < EPL; e++) kf[e] = 0.f;
     }
-    for (int gi = 0; gi < group; gi++) {
-      float s = 0.f;
 #pragma unroll
-      for (int e = 0; e < EPL; e++) s += s_q[gi][kc * EPL + e] * kf[e];
+    for (int gi = 0; gi < MAXG; gi++) {
+      if (gi < group) {
+        float s = 0.f;
 #pragma unroll
-      for (int off = LPP / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, kWave);
-      if (kc == 0 && pos < p1) s_p[gi][pos - p0] = s;
+        for (int e = 0; e < EPL; e++) s += s_q[gi][kc * EPL + e] * kf[e];
+        if constexpr (LPP <= 16) {
+          s = group_sum_all<LPP>(s);  // DPP within a row of 16 lanes
+          if (kc == 0 && pos < p1) s_p[gi][pos - p0] = s;
+        } else {
+          s = group_sum_last<LPP>(s);
+          if (kc == LPP - 1 && pos < p1) s_p[gi][pos - p0] = s;
+        }
+      }
     }
   }
   __syncthreads();
@@ -209,14 +221,14 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   for (int gi = wv; gi < group; gi += kAttnThreads / kWave) {
     float m = -INFINITY;
     for (int j = lane; j < n; j += kWave) m = fmaxf(m, s_p[gi][j]);
-    m = wave_max(m);
+    m = wave_max_dpp(m);
     float l = 0.f;
     for (int j = lane; j < n; j += kWave) {
       float e = expf(s_p[gi][j] - m);
       s_p[gi][j] = e;
       l += e;
     }
-    l = wave_sum(l);
+    l = wave_sum_dpp(l);
     if (lane == 0) {
       s_m[gi] = m;
       s_l[gi] = l;
@@ -225,9 +237,9 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   __syncthreads();
 
   // 5. P V over this thread's position subset, then across subsets
-  float acc[kMaxGroup][EPL];
+  float acc[MAXG][EPL];
 #pragma unroll
-  for (int gi = 0; gi < kMaxGroup; gi++)
+  for (int gi = 0; gi < MAXG; gi++)
 #pragma unroll
     for (int e = 0; e < EPL; e++) acc[gi][e] = 0.f;
 #pragma unroll
@@ -242,7 +254,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
         widen16<KV>(vreg[i], vf);
       }
 #pragma unroll
-      for (int gi = 0; gi < kMaxGroup; gi++) {
+      for (int gi = 0; gi < MAXG; gi++) {
         if (gi < group) {
           const float pr = s_p[gi][pos - p0];
 #pragma unroll
@@ -253,7 +265,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   }
   // subsets of one wave sit DPT lanes apart
 #pragma unroll
-  for (int gi = 0; gi < kMaxGroup; gi++) {
+  for (int gi = 0; gi < MAXG; gi++) {
     if (gi < group) {
 #pragma unroll
       for (int e = 0; e < EPL; e++) {
@@ -266,7 +278,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   }
   if (lane < DPT) {
 #pragma unroll
-    for (int gi = 0; gi < kMaxGroup; gi++)
+    for (int gi = 0; gi < MAXG; gi++)
       if (gi < group)
 #pragma unroll
         for (int e = 0; e < EPL; e++) s_red[wv][gi * HD + dc * EPL + e] = acc[gi][e];
@@ -287,23 +299,58 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   }
 }
 
-// Merge of the splits: one workgroup per q head, one thread per output dim.
+// Merge of the splits: one workgroup per q head.  The split weights w_s = exp(m_s - M)
+// go to LDS first; then thread (d, g) accumulates w_s o_s[d] over splits s = g (mod 256/HD)
+// with independent loads, and the groups are summed through LDS.
+constexpr int kMaxSplits = 2048;
+
+template <int HD>
 __global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restrict__ part_o,
-                                                           const float* __restrict__ part_ml, int S, int hd,
+                                                           const float* __restrict__ part_ml, int S,
                                                            float* __restrict__ out) {
-  const int h = blockIdx.x;
-  const int d = threadIdx.x;
-  float M = -INFINITY;
-  for (int s = 0; s < S; s++)
-    if (part_ml[(int64_t(h) * S + s) * 2 + 1] > 0.f) M = fmaxf(M, part_ml[(int64_t(h) * S + s) * 2]);
-  float L = 0.f, o = 0.f;
-  for (int s = 0; s < S; s++) {
-    if (!(part_ml[(int64_t(h) * S + s) * 2 + 1] > 0.f)) continue;  // empty split
-    const float w = expf(part_ml[(int64_t(h) * S + s) * 2] - M);
-    L += w * part_ml[(int64_t(h) * S + s) * 2 + 1];
-    if (d < hd) o += w * part_o[(int64_t(h) * S + s) * hd + d];
+  constexpr int NG = 256 / HD;
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_red[256];
+  __shared__ float s_ml[2 * 4];
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float* ml = part_ml + int64_t(h) * S * 2;
+  float m = -INFINITY;
+  for (int s = tid; s < S; s += 256)
+    if (ml[2 * s + 1] > 0.f) m = fmaxf(m, ml[2 * s]);
+  m = wave_max_dpp(m);
+  if (lane == 0) s_ml[wv] = m;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(s_ml[0], s_ml[1]), fmaxf(s_ml[2], s_ml[3]));
+  float l = 0.f;
+  for (int s = tid; s < S; s += 256) {
+    const float w = ml[2 * s + 1] > 0.f ? expf(ml[2 * s] - M) : 0.f;
+    s_w[s] = w;
+    l += w * ml[2 * s + 1];
   }
-  if (d < hd) out[int64_t(h) * hd + d] = o / L;
+  l = wave_sum_dpp(l);
+  __syncthreads();
+  if (lane == 0) s_ml[4 + wv] = l;
+  __syncthreads();
+  const float L = s_ml[4] + s_ml[5] + s_ml[6] + s_ml[7];
+  const int d = tid % HD, g = tid / HD;
+  const float* po = part_o + int64_t(h) * S * HD + d;
+  float o0 = 0.f, o1 = 0.f;
+  int s = g;
+  // empty splits (w = 0) never wrote their rows: skip them rather than multiply by 0
+  for (; s + NG < S; s += 2 * NG) {
+    const float w0 = s_w[s], w1 = s_w[s + NG];
+    if (w0 != 0.f) o0 += w0 * po[int64_t(s) * HD];
+    if (w1 != 0.f) o1 += w1 * po[int64_t(s + NG) * HD];
+  }
+  if (s < S && s_w[s] != 0.f) o0 += s_w[s] * po[int64_t(s) * HD];
+  s_red[tid] = o0 + o1;
+  __syncthreads();
+  if (tid < HD) {
+    float o = 0.f;
+#pragma unroll
+    for (int j = 0; j < NG; j++) o += s_red[j * HD + tid];
+    out[int64_t(h) * HD + tid] = o / L;
+  }
 }
 
 int attn_splits(int active) { return (active + kAttnChunk - 1) / kAttnChunk; }
@@ -315,7 +362,20 @@ size_t attn_workspace_bytes(int nq, int hd, int active) {
 
 template <int HD, typename KV, bool FUSED>
 static void launch_partial(const AttnParams& p, int S, hipStream_t s) {
-  hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED>), dim3(S, p.nkv), dim3(kAttnThreads), 0, s, p);
+  if (p.group <= 1)
+    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 1>), dim3(S, p.nkv), dim3(kAttnThreads), 0, s, p);
+  else if (p.group <= 2)
+    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 2>), dim3(S, p.nkv), dim3(kAttnThreads), 0, s, p);
+  else if (p.group <= 4)
+    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 4>), dim3(S, p.nkv), dim3(kAttnThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 8>), dim3(S, p.nkv), dim3(kAttnThreads), 0, s, p);
+}
+
+template <int HD>
+static void launch_combine(const AttnParams& p, int S, float* out, hipStream_t s) {
+  const int nq = p.nkv * p.group;
+  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(nq), dim3(256), 0, s, p.part_o, p.part_ml, S, out);
 }
 
 int launch_attention(const AttnParams& p0, bool fused, float* out, hipStream_t s) {
@@ -337,8 +397,9 @@ int launch_attention(const AttnParams& p0, bool fused, float* out, hipStream_t s
 #undef JERO_ATTN_CASE
   int rc = check_launch("attention partial");
   if (rc) return rc;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(p.nkv * p.group), dim3(p.hd < 64 ? 64 : p.hd), 0, s, p.part_o,
-                     p.part_ml, S, p.hd, out);
+  if (p.hd == 32) launch_combine<32>(p, S, out, s);
+  else if (p.hd == 64) launch_combine<64>(p, S, out, s);
+  else launch_combine<128>(p, S, out, s);
   return check_launch("attention combine");
 }
 
@@ -351,7 +412,9 @@ int check_attention_shape(int nq, int nkv, int hd, int64_t seq_len) {
                                                   " q heads per kv head");
   if (hd != 32 && hd != 64 && hd != 128)
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: head_dim " + std::to_string(hd) + " not in {32, 64, 128}");
-  if (seq_len > (int64_t(1) << 24)) return fail(JERO_ERR_CONTEXT_LENGTH_EXCEEDED, "attention: sequence too long");
+  if (seq_len > int64_t(kMaxSplits) * kAttnChunk)
+    return fail(JERO_ERR_CONTEXT_LENGTH_EXCEEDED, "attention: more than " +
+                                                      std::to_string(int64_t(kMaxSplits) * kAttnChunk) + " positions");
   return JERO_OK;
 }
 

@@ -35,8 +35,9 @@ int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s);
 int dgemv_blocks(int quant, int64_t K, int64_t N, int out_mode);
 // Longest row the fused decode GEMV takes for a weight format.
 int dgemv_max_k(int quant);
+// hidden = embedding row of *token; also the step's RoPE table rope_cs[hd/2][cos, sin].
 int launch_embed(int quant, const void* w, int64_t rb, int H, int64_t vocab, const int32_t* token, float* out,
-                 hipStream_t s);
+                 const int64_t* pos, float theta, int hd, float* rope_cs, hipStream_t s);
 int launch_argmax_final(const float* v, const int64_t* idx, int n, int32_t* token, int64_t* pos, hipStream_t s);
 int launch_set_state(int32_t* token, int64_t* pos, int32_t t, int64_t p, hipStream_t s);
 

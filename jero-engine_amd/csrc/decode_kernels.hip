@@ -25,7 +25,7 @@ namespace jero {
 // ---------------------------------------------------------------- prologue: f32 -> blocks in LDS
 
 __device__ __forceinline__ float block_sum(float v, float* s_tmp) {
-  v = wave_sum(v);
+  v = wave_sum_dpp(v);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
   if (lane == 0) s_tmp[wv] = v;
   lds_barrier();
@@ -38,34 +38,27 @@ __device__ __forceinline__ float block_sum(float v, float* s_tmp) {
 // standalone quantizer).
 __device__ __forceinline__ void q8k_block_lds(const float e[4], int lane, uint8_t* ob) {
   float am = 0.0f;
-  int ai = 0x7fffffff;
-  float mxv = 0.0f;
 #pragma unroll
-  for (int t = 0; t < 4; t++) {
-    float a = fabsf(e[t]);
-    if (a > am) {
-      am = a;
-      ai = 4 * lane + t;
-      mxv = e[t];
-    }
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    float oa = __shfl_xor(am, off, kWave);
-    int oi = __shfl_xor(ai, off, kWave);
-    float ov = __shfl_xor(mxv, off, kWave);
-    if (oa > am || (oa == am && oi < ai)) {
-      am = oa;
-      ai = oi;
-      mxv = ov;
-    }
-  }
+  for (int t = 0; t < 4; t++) am = fmaxf(am, fabsf(e[t]));
+  am = wave_max_dpp(am);  // uniform block max |x|
   if (am == 0.0f) {
     reinterpret_cast<uint32_t*>(ob + 4)[lane] = 0u;
     if (lane < 16) reinterpret_cast<int16_t*>(ob + 260)[lane] = 0;
     if (lane == 0) *reinterpret_cast<float*>(ob) = 0.0f;
     return;
   }
+  // the first element (lowest index) with |x| == max sets the sign: lowest lane, lowest t
+  int mine = 4;
+#pragma unroll
+  for (int t = 3; t >= 0; t--)
+    if (fabsf(e[t]) == am) mine = t;
+  const uint64_t hit = __ballot(mine < 4);
+  const int src = __builtin_ctzll(hit);
+  const int t_src = __builtin_amdgcn_readlane(mine, src);
+  const float mxv = __builtin_bit_cast(
+      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t_src == 0 ? e[0] : t_src == 1 ? e[1]
+                                                               : t_src == 2 ? e[2] : e[3]),
+                                       src));
   float iscale = -127.0f / mxv;
   int s = 0;
   uint32_t packed = 0;
@@ -77,8 +70,7 @@ __device__ __forceinline__ void q8k_block_lds(const float e[4], int lane, uint8_
     packed |= (uint32_t(qv) & 0xFFu) << (8 * t);
   }
   reinterpret_cast<uint32_t*>(ob + 4)[lane] = packed;
-  s += __shfl_xor(s, 1, kWave);
-  s += __shfl_xor(s, 2, kWave);
+  s = int(group_sum_all<4>(float(s)));  // |s| <= 508: exact in f32
   if ((lane & 3) == 0) reinterpret_cast<int16_t*>(ob + 260)[lane >> 2] = int16_t(s);
   if (lane == 0) *reinterpret_cast<float*>(ob) = 1.0f / iscale;
 }
@@ -86,18 +78,18 @@ __device__ __forceinline__ void q8k_block_lds(const float e[4], int lane, uint8_
 // The workgroup's share of the f32 input, loaded before the weight rows so that the prologue
 // only waits for these loads.  Q8_K: wave w takes blocks w, w+nw, ... (4 elements per lane,
 // the quantizer's layout); ACT_Q8: half-wave h takes 32-element blocks h, h+2nw, ...
-template <int ACT>
+template <int ACT, int XB>
 struct XRegs {
-  float4 v[kDecodeMaxActBlocks];
-  float4 g[kDecodeMaxActBlocks];
+  float4 v[XB];
+  float4 g[XB];
 };
 
-template <int ACT>
-__device__ __forceinline__ void load_x(XRegs<ACT>& X, const float* __restrict__ x, const float* __restrict__ nw,
+template <int ACT, int XB>
+__device__ __forceinline__ void load_x(XRegs<ACT, XB>& X, const float* __restrict__ x, const float* __restrict__ nw,
                                        int K) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
 #pragma unroll
-  for (int i = 0; i < kDecodeMaxActBlocks; i++) {
+  for (int i = 0; i < XB; i++) {
     if constexpr (ACT == JERO_Q8_K) {
       const int b = wv + nwv * i;
       if (b < K / 256) {
@@ -115,14 +107,14 @@ __device__ __forceinline__ void load_x(XRegs<ACT>& X, const float* __restrict__ 
 }
 
 // Builds the activation blocks of x (or of rmsnorm(x) * nw) in LDS from the registers.
-template <int ACT>
-__device__ void build_act_lds(XRegs<ACT>& X, bool has_norm, float eps, int K, uint8_t* s_act, float* s_tmp) {
+template <int ACT, int XB>
+__device__ void build_act_lds(XRegs<ACT, XB>& X, bool has_norm, float eps, int K, uint8_t* s_act, float* s_tmp) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
   float scale = 1.0f;
   if (has_norm) {
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < kDecodeMaxActBlocks; i++) {
+    for (int i = 0; i < XB; i++) {
       if constexpr (ACT == JERO_Q8_K) {
         if (wv + nwv * i < K / 256)
           ss += X.v[i].x * X.v[i].x + X.v[i].y * X.v[i].y + X.v[i].z * X.v[i].z + X.v[i].w * X.v[i].w;
@@ -134,7 +126,7 @@ __device__ void build_act_lds(XRegs<ACT>& X, bool has_norm, float eps, int K, ui
     scale = 1.0f / sqrtf(ss / float(K) + eps);
   }
 #pragma unroll
-  for (int i = 0; i < kDecodeMaxActBlocks; i++) {
+  for (int i = 0; i < XB; i++) {
     if constexpr (ACT == JERO_Q8_K) {
       const int b = wv + nwv * i;
       if (b < K / 256) {
@@ -169,7 +161,7 @@ __device__ void build_act_lds(XRegs<ACT>& X, bool has_norm, float eps, int K, ui
 
 // ---------------------------------------------------------------- fused GEMV
 
-template <int F, int LPR, int UPL, int R, int OUT>
+template <int F, int LPR, int UPL, int R, int OUT, int XB>
 __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
   using Ut = Unit<F>;
   constexpr int ACT = (F == JERO_Q8_0 || F == JERO_Q4_0) ? JERO_ACT_Q8 : JERO_Q8_K;
@@ -229,12 +221,12 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
   };
 
   // 1. input loads, then the first row group's weight loads, then the prologue
-  XRegs<ACT> X;
-  load_x<ACT>(X, a.x, a.norm_w, a.K);
+  XRegs<ACT, XB> X;
+  load_x<ACT, XB>(X, a.x, a.norm_w, a.K);
   typename Ut::W cur[R][UPL], nxt[R][UPL];
   load_rows(wave0, cur);
   // 2. activation blocks in LDS (every thread takes part)
-  build_act_lds<ACT>(X, a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp);
+  build_act_lds<ACT, XB>(X, a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp);
   typename Ut::Act act[UPL];
 #pragma unroll
   for (int t = 0; t < UPL; t++) {
@@ -332,10 +324,21 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
 
 // hidden = dequantize_token_row(token_embd, *token) (embed_token, src/qwen_deepseek.rs:558-582)
 // A token outside the vocabulary (the greedy token of all-NaN logits is -1) embeds as zeros.
+// Block 0 also writes the step's RoPE table: (cos, sin) of pos / theta^(2i/hd), the f32 angle
+// of the reference's apply_rope_inplace (src/qwen_deepseek.rs:1056-1071).
 __global__ void __launch_bounds__(256) embed_kernel(int quant, const uint8_t* __restrict__ w, int64_t rb, int H,
                                                     int64_t vocab, const int32_t* __restrict__ token,
-                                                    float* __restrict__ out) {
+                                                    float* __restrict__ out, const int64_t* __restrict__ pos,
+                                                    float theta, int hd, float* __restrict__ rope_cs) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (blockIdx.x == 0 && threadIdx.x < hd / 2) {
+    const float expo = float(2 * threadIdx.x) / float(hd);
+    const float angle = float(*pos) / powf(theta, expo);
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
+    rope_cs[2 * threadIdx.x] = cs;
+    rope_cs[2 * threadIdx.x + 1] = sn;
+  }
   if (i >= H) return;
   const int64_t t = *token;
   out[i] = (t >= 0 && t < vocab) ? dequant_elem(quant, w + t * rb, i) : 0.0f;
@@ -391,7 +394,7 @@ __global__ void set_state_kernel(int32_t* token, int64_t* pos, int32_t t, int64_
 
 namespace {
 
-template <int F, int LPR, int UPL, int R, int OUT>
+template <int F, int LPR, int UPL, int R, int OUT, int XB>
 void dgemv_one(DGemvArgs a, int64_t rows_or_pairs, hipStream_t s) {
   constexpr int G = kWave / LPR;
   if constexpr (OUT == kOutSwiglu) {
@@ -406,8 +409,29 @@ void dgemv_one(DGemvArgs a, int64_t rows_or_pairs, hipStream_t s) {
   if (blocks > cap) blocks = cap;
   if (a.max_blocks > 0 && blocks > a.max_blocks) blocks = a.max_blocks;
   const size_t shm = 256 + size_t(row_bytes((F == JERO_Q8_0 || F == JERO_Q4_0) ? JERO_ACT_Q8 : JERO_Q8_K, a.K));
-  hipLaunchKernelGGL((dgemv_kernel<F, LPR, UPL, R, OUT>), dim3(unsigned(blocks)), dim3(kDecodeThreads),
+  hipLaunchKernelGGL((dgemv_kernel<F, LPR, UPL, R, OUT, XB>), dim3(unsigned(blocks)), dim3(kDecodeThreads),
                      (shm + 15) & ~size_t(15), s, a);
+}
+
+// Activation blocks each wave builds in the prologue.
+inline int xb_for(int F, int K) {
+  const int waves = kDecodeThreads / kWave;
+  const int per = (F == JERO_Q8_0 || F == JERO_Q4_0) ? (K / 32 + 2 * waves - 1) / (2 * waves)
+                                                      : (K / 256 + waves - 1) / waves;
+  return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 6 ? 6 : 8;
+}
+
+template <int F, int LPR, int UPL, int OUT>
+void dgemv_xb(const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t s) {
+  // one row per wave slot; SwiGLU with one row group per wave needs its gate/up pair in-wave
+  constexpr int R = (OUT == kOutSwiglu && LPR == 64) ? 2 : 1;
+  switch (xb_for(F, a.K)) {
+    case 1: dgemv_one<F, LPR, UPL, R, OUT, 1>(a, rows_or_pairs, s); break;
+    case 2: dgemv_one<F, LPR, UPL, R, OUT, 2>(a, rows_or_pairs, s); break;
+    case 4: dgemv_one<F, LPR, UPL, R, OUT, 4>(a, rows_or_pairs, s); break;
+    case 6: dgemv_one<F, LPR, UPL, R, OUT, 6>(a, rows_or_pairs, s); break;
+    default: dgemv_one<F, LPR, UPL, R, OUT, 8>(a, rows_or_pairs, s); break;
+  }
 }
 
 template <int F, int OUT>
@@ -416,19 +440,19 @@ int dgemv_fmt(const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t s) {
   const int lpr = U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4;
   const int upl = (U + lpr - 1) / lpr;
   if (lpr == 4) {
-    dgemv_one<F, 4, 1, 2, OUT>(a, rows_or_pairs, s);
+    dgemv_xb<F, 4, 1, OUT>(a, rows_or_pairs, s);
   } else if (lpr == 16) {
-    dgemv_one<F, 16, 1, 2, OUT>(a, rows_or_pairs, s);
+    dgemv_xb<F, 16, 1, OUT>(a, rows_or_pairs, s);
   } else if (lpr == 32) {
-    dgemv_one<F, 32, 1, 2, OUT>(a, rows_or_pairs, s);
+    dgemv_xb<F, 32, 1, OUT>(a, rows_or_pairs, s);
   } else if (upl == 1) {
-    dgemv_one<F, 64, 1, 2, OUT>(a, rows_or_pairs, s);
+    dgemv_xb<F, 64, 1, OUT>(a, rows_or_pairs, s);
   } else if (upl == 2) {
-    dgemv_one<F, 64, 2, 2, OUT>(a, rows_or_pairs, s);
+    dgemv_xb<F, 64, 2, OUT>(a, rows_or_pairs, s);
   } else if (upl <= 3) {
-    dgemv_one<F, 64, 3, 2, OUT>(a, rows_or_pairs, s);
+    dgemv_xb<F, 64, 3, OUT>(a, rows_or_pairs, s);
   } else if (upl <= 4) {
-    dgemv_one<F, 64, 4, 2, OUT>(a, rows_or_pairs, s);
+    dgemv_xb<F, 64, 4, OUT>(a, rows_or_pairs, s);
   } else {
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: row of " + std::to_string(a.K) + " elements too long");
   }
@@ -465,7 +489,7 @@ int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s) {
 int dgemv_blocks(int quant, int64_t K, int64_t N, int out_mode) {
   const int U = units_per_row(quant, K);
   const int lpr = U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4;
-  const int64_t G = kWave / lpr, R = 2;
+  const int64_t G = kWave / lpr, R = (out_mode == kOutSwiglu && lpr == 64) ? 2 : 1;
   int64_t n_groups;
   if (out_mode == kOutSwiglu) {
     const int64_t per = G == 1 ? R / 2 : R * (G / 2);
@@ -486,9 +510,9 @@ int dgemv_max_k(int quant) {
 }
 
 int launch_embed(int quant, const void* w, int64_t rb, int H, int64_t vocab, const int32_t* token, float* out,
-                 hipStream_t s) {
+                 const int64_t* pos, float theta, int hd, float* rope_cs, hipStream_t s) {
   hipLaunchKernelGGL(embed_kernel, dim3(unsigned((H + 255) / 256)), dim3(256), 0, s, quant,
-                     static_cast<const uint8_t*>(w), rb, H, vocab, token, out);
+                     static_cast<const uint8_t*>(w), rb, H, vocab, token, out, pos, theta, hd, rope_cs);
   return check_launch("embed");
 }
 

@@ -152,6 +152,39 @@ __device__ __forceinline__ float group_sum_last(float v) {
 // outstanding global loads (which __syncthreads' fence would also drain).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Sum over aligned groups of WIDTH (4, 8 or 16) lanes; every lane of a group gets the total.
+template <int WIDTH>
+__device__ __forceinline__ float group_sum_all(float v) {
+  static_assert(WIDTH == 4 || WIDTH == 8 || WIDTH == 16, "group width");
+  v = dpp_add<0xB1, 0xF>(v);                            // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E, 0xF>(v);                            // quad_perm [2,3,0,1]
+  if constexpr (WIDTH >= 8) v = dpp_add<0x141, 0xF>(v);   // row_half_mirror
+  if constexpr (WIDTH >= 16) v = dpp_add<0x140, 0xF>(v);  // row_mirror
+  return v;
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max(float v) {
+  int o = __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -INFINITY), __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                      0xF, false);
+  return fmaxf(v, __builtin_bit_cast(float, o));
+}
+
+// Whole-wave reductions with DPP; the result is returned uniformly (read from lane 63).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = group_sum_last<64>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = dpp_max<0xB1, 0xF>(v);
+  v = dpp_max<0x4E, 0xF>(v);
+  v = dpp_max<0x124, 0xF>(v);
+  v = dpp_max<0x128, 0xF>(v);
+  v = dpp_max<0x142, 0xA>(v);
+  v = dpp_max<0x143, 0xC>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));

@@ -54,6 +54,7 @@ struct jero_model {
   int64_t* amax_i = nullptr;
   int32_t* token = nullptr;
   int64_t* pos = nullptr;
+  float* rope_cs = nullptr;
   void* kv = nullptr;
   size_t kv_bytes = 0;
   std::vector<void*> owned;
@@ -240,7 +241,8 @@ extern "C" int jero_hip_model_create(const jero_model_config* cfg, jero_model** 
       (rc = dev_alloc(m, sizeof(float) * max_blocks, &p)) || ((m->amax_v = static_cast<float*>(p)), false) ||
       (rc = dev_alloc(m, sizeof(int64_t) * max_blocks, &p)) || ((m->amax_i = static_cast<int64_t*>(p)), false) ||
       (rc = dev_alloc(m, sizeof(int32_t), &p)) || ((m->token = static_cast<int32_t*>(p)), false) ||
-      (rc = dev_alloc(m, sizeof(int64_t), &p)) || ((m->pos = static_cast<int64_t*>(p)), false)) {
+      (rc = dev_alloc(m, sizeof(int64_t), &p)) || ((m->pos = static_cast<int64_t*>(p)), false) ||
+      (rc = dev_alloc(m, sizeof(float) * size_t(c.head_dim), &p)) || ((m->rope_cs = static_cast<float*>(p)), false)) {
     for (void* q : m->owned)
       if (q) (void)hipFree(q);
     delete m;
@@ -385,7 +387,7 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
   const float eps_attn = c.rms_eps;
   const float eps_ffn = c.rms_eps > 1e-6f ? c.rms_eps : 1e-6f;  // rms_eps.max(1e-6), :1250
   int rc = launch_embed(m->tok_embd.quant, m->tok_embd.dev, row_bytes(m->tok_embd.quant, c.hidden), int(c.hidden),
-                        c.vocab, m->token, m->hidden, s);
+                        c.vocab, m->token, m->hidden, m->pos, c.rope_theta, c.head_dim, m->rope_cs, s);
   if (rc) return rc;
   const size_t es = c.kv_dtype == JERO_KV_F16 ? 2 : 4;
   const size_t ring = size_t(c.kv_capacity) * size_t(KV) * es;
@@ -422,6 +424,7 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
     p.k_write = base;
     p.v_write = base + ring;
     p.pos_dev = m->pos;
+    p.rope_cs = m->rope_cs;
     p.capacity = c.kv_capacity;
     rc = launch_attention(p, true, m->attn, s);
     if (rc) return rc;

@@ -100,11 +100,12 @@ int jero_hip_repack(int quant, const void *src_dev, size_t src_bytes, int64_t n_
 /* ---- attention ----
  * gqa_causal_attention_f32(out, q, k, v, n_heads_q, n_heads_kv, head_dim, seq_len, scale)
  * (called at src/qwen_deepseek.rs:669-691): softmax(q . k_t * scale) . v over t < seq_len for
- * each q head h, kv head h / (n_heads_q / n_heads_kv).  q_dev: [n_heads_q][head_dim] f32;
+ * each q head h, kv head h / (n_heads_q / n_heads_kv).  q_dev: [n_heads_q][head_dim] f32 (8-byte
+ * aligned);
  * k_dev, v_dev: [seq_len][n_heads_kv * head_dim] of kv_dtype (16-byte aligned); out_dev:
  * [n_heads_q][head_dim] f32.  head_dim in {32, 64, 128}; at most 8 q heads per kv head.
- * Workspace: n_heads_q * ceil(seq_len/128) * (head_dim + 2) floats (NULL: library-owned, calls
- * must not overlap on one device). */
+ * seq_len <= 131072.  Workspace: n_heads_q * ceil(seq_len/64) * (head_dim + 2) floats, 16-byte
+ * aligned (NULL: library-owned, calls must not overlap on one device). */
 int jero_hip_gqa_attention(float *out_dev, const float *q_dev, const void *k_dev, const void *v_dev, int kv_dtype,
                            int n_heads_q, int n_heads_kv, int head_dim, int64_t seq_len, float scale,
                            void *workspace_dev, size_t workspace_bytes, void *stream);

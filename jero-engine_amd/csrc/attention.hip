@@ -55,29 +55,19 @@ __device__ __forceinline__ float rope_angle(int i, int hd, int64_t pos, float th
   return float(pos) / powf(theta, expo);
 }
 
-// Per-head RMSNorm (optional weight) + interleaved RoPE of one head held as one pair per lane
-// in a group of HD/2 lanes; returns the rotated pair.
+// Per-head RMSNorm (weight pair nw, if has_norm) + interleaved RoPE of one head held as one
+// pair per lane in a group of HD/2 lanes; cs = (cos, sin) of the pair's angle.
 template <int HD>
-__device__ __forceinline__ float2 norm_rope_pair(float x0, float x1, int pair, const float* __restrict__ nw,
-                                                 float eps, int64_t pos, float theta, bool rope,
-                                                 const float* __restrict__ rope_cs) {
-  if (nw) {
+__device__ __forceinline__ float2 norm_rope_pair(float x0, float x1, bool has_norm, float2 nw, float eps, float2 cs) {
+  if (has_norm) {
     float ss = x0 * x0 + x1 * x1;
 #pragma unroll
     for (int off = HD / 4; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
     float inv = 1.0f / sqrtf(ss / float(HD) + eps);
-    x0 = x0 * inv * nw[2 * pair];
-    x1 = x1 * inv * nw[2 * pair + 1];
+    x0 = x0 * inv * nw.x;
+    x1 = x1 * inv * nw.y;
   }
-  if (!rope) return make_float2(x0, x1);
-  float s, c;
-  if (rope_cs) {  // (cos, sin) of this step's angles, computed once per step
-    c = rope_cs[2 * pair];
-    s = rope_cs[2 * pair + 1];
-  } else {
-    sincosf(rope_angle(pair, HD, pos, theta), &s, &c);
-  }
-  return make_float2(x0 * c - x1 * s, x0 * s + x1 * c);
+  return make_float2(x0 * cs.x - x1 * cs.y, x0 * cs.y + x1 * cs.x);
 }
 
 template <int HD, typename KV, bool FUSED, int MAXG>
@@ -102,15 +92,70 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int group = p.group;
   const int64_t kvd = int64_t(p.nkv) * HD;
+  const int S = gridDim.x;
+  const int p0 = split * kAttnChunk;
+
+  // 0. this thread's q pairs (fused: also the new k), issued first so that waiting for them
+  //    does not wait for the K/V tile behind them
+  constexpr int HPW = 128 / HD;                         // heads per wave pass (HD/2 lanes per head)
+  constexpr int HPP = (kAttnThreads / kWave) * HPW;     // heads per pass of the workgroup
+  constexpr int NPASS = (MAXG + (FUSED ? 1 : 0) + HPP - 1) / HPP;
+  const int pair = lane % (HD / 2), sub = lane / (HD / 2);
+  float2 qx[NPASS];
+  // Loads are unconditional, from clamped in-bounds addresses: a load under a branch gets its
+  // own wait for completion, which would serialise the tile's round trips.
+#pragma unroll
+  for (int it = 0; it < NPASS; it++) {
+    const int gi = wv * HPW + it * HPP + sub;
+    const bool is_k = FUSED && gi == group;
+    const float* src = is_k ? p.k_new + kh * HD : p.q + (int64_t(kh) * group + (gi < group ? gi : 0)) * HD;
+    const float2 v = *reinterpret_cast<const float2*>(src + 2 * pair);
+    qx[it] = (gi < group || is_k) ? v : make_float2(0.f, 0.f);
+  }
+
+  // Fused mode: the rest of what the prologue reads (position, RoPE table, norm weights, the
+  // new v) goes out in the same batch.  A null pointer reads a valid stand-in (the q vector)
+  // whose value is then ignored.
+  const float* dummy = p.q;
+  float2 cs_pre = make_float2(1.f, 0.f), qn_pre = cs_pre, kn_pre = cs_pre;
+  float vnew_pre = 0.f;
+  int64_t pos_pre = p.pos;
+  if constexpr (FUSED) {
+    pos_pre = *(p.pos_dev ? p.pos_dev : reinterpret_cast<const int64_t*>(p.k));
+    cs_pre = *reinterpret_cast<const float2*>((p.rope_cs ? p.rope_cs : dummy) + 2 * pair);
+    qn_pre = *reinterpret_cast<const float2*>((p.q_norm ? p.q_norm : dummy) + 2 * pair);
+    kn_pre = *reinterpret_cast<const float2*>((p.k_norm ? p.k_norm : dummy) + 2 * pair);
+    vnew_pre = p.v_new[kh * HD + tid % HD];
+  }
+
+  // 1. K and V tiles into registers.  With the position on the device the grid covers every
+  //    ring slot, so slots [p0, p0 + 64) are inside the ring whatever the position; slots past
+  //    the active range are loaded and then ignored.
+  const int bound = p.pos_dev ? int(p.capacity) : p.active;
+  const int pl = min(p0 + kAttnChunk, bound);
+  const KV* kb = static_cast<const KV*>(p.k) + kh * HD;
+  const KV* vb = static_cast<const KV*>(p.v) + kh * HD;
+  u32x4 kreg[KSTEPS], vreg[VSTEPS];
+  const int kc = lane % LPP;
+#pragma unroll
+  for (int i = 0; i < KSTEPS; i++) {
+    const int pos = min(p0 + (i * (kAttnThreads / kWave) + wv) * PPW + lane / LPP, pl - 1);
+    kreg[i] = ld4(reinterpret_cast<const uint8_t*>(kb + int64_t(pos) * kvd + kc * EPL));
+  }
+  const int dc = tid % DPT, ps = tid / DPT;
+#pragma unroll
+  for (int i = 0; i < VSTEPS; i++) {
+    const int pos = min(p0 + i * NPS + ps, pl - 1);
+    vreg[i] = ld4(reinterpret_cast<const uint8_t*>(vb + int64_t(pos) * kvd + dc * EPL));
+  }
+
   int active = p.active, slot = p.slot;
   int64_t pos_now = p.pos;
   if (p.pos_dev) {  // position kept on the device (graph-replayed decode)
-    pos_now = *p.pos_dev;
+    pos_now = pos_pre;
     slot = int(pos_now % p.capacity);
     active = int(pos_now + 1 < p.capacity ? pos_now + 1 : p.capacity);
   }
-  const int S = gridDim.x;
-  const int p0 = split * kAttnChunk;
   if (p0 >= active) {  // empty split: contributes nothing to the merge
     if (tid < group) {
       const int h = kh * group + tid;
@@ -120,44 +165,23 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
     return;
   }
   const int p1 = min(p0 + kAttnChunk, active);
-  const KV* kb = static_cast<const KV*>(p.k) + kh * HD;
-  const KV* vb = static_cast<const KV*>(p.v) + kh * HD;
-
-  // 1. K and V tiles into registers
-  u32x4 kreg[KSTEPS], vreg[VSTEPS];
-  const int kc = lane % LPP;
-#pragma unroll
-  for (int i = 0; i < KSTEPS; i++) {
-    const int pos = p0 + (i * (kAttnThreads / kWave) + wv) * PPW + lane / LPP;
-    if (pos < p1) kreg[i] = ld4(reinterpret_cast<const uint8_t*>(kb + int64_t(pos) * kvd + kc * EPL));
-  }
-  const int dc = tid % DPT, ps = tid / DPT;
-#pragma unroll
-  for (int i = 0; i < VSTEPS; i++) {
-    const int pos = p0 + i * NPS + ps;
-    if (pos < p1) vreg[i] = ld4(reinterpret_cast<const uint8_t*>(vb + int64_t(pos) * kvd + dc * EPL));
-  }
 
   // 2. q heads of this group (and, fused, the new k/v) into LDS
   const bool own_slot = FUSED && slot >= p0 && slot < p1;
   {
-    constexpr int HPW = 128 / HD;  // heads per wave pass (HD/2 lanes per head)
-    const int pair = lane % (HD / 2), sub = lane / (HD / 2);
-    for (int h0 = wv * HPW; h0 < group + (FUSED ? 1 : 0); h0 += (kAttnThreads / kWave) * HPW) {
-      const int gi = h0 + sub;
+    float2 cs = cs_pre;
+    if (FUSED && !p.rope_cs) sincosf(rope_angle(pair, HD, pos_now, p.theta), &cs.y, &cs.x);
+#pragma unroll
+    for (int it = 0; it < NPASS; it++) {
+      const int gi = wv * HPW + it * HPP + sub;
       const bool is_k = FUSED && gi == group;
-      const bool ok = gi <= group && (gi < group || is_k);
-      float x0 = 0.f, x1 = 0.f;
-      if (ok) {
-        const float* src = is_k ? p.k_new + kh * HD : p.q + (int64_t(kh) * group + gi) * HD;
-        x0 = src[2 * pair];
-        x1 = src[2 * pair + 1];
-      }
+      const bool ok = gi < group || is_k;
       float2 r;
       if constexpr (FUSED)
-        r = norm_rope_pair<HD>(x0, x1, pair, is_k ? p.k_norm : p.q_norm, p.eps, pos_now, p.theta, true, p.rope_cs);
+        r = norm_rope_pair<HD>(qx[it].x, qx[it].y, (is_k ? p.k_norm : p.q_norm) != nullptr, is_k ? kn_pre : qn_pre,
+                               p.eps, cs);
       else
-        r = make_float2(x0, x1);
+        r = qx[it];
       if (ok) {
         if (is_k) {
           s_knew[2 * pair] = r.x;
@@ -168,9 +192,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
         }
       }
     }
-    if (own_slot) {
-      for (int d = tid; d < HD; d += kAttnThreads) s_vnew[d] = p.v_new[kh * HD + d];
-    }
+    if (own_slot && tid < HD) s_vnew[tid] = vnew_pre;
   }
   __syncthreads();
   if (own_slot) {  // append the new token's k, v to the ring
@@ -299,57 +321,91 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   }
 }
 
-// Merge of the splits: one workgroup per q head.  The split weights w_s = exp(m_s - M)
-// go to LDS first; then thread (d, g) accumulates w_s o_s[d] over splits s = g (mod 256/HD)
-// with independent loads, and the groups are summed through LDS.
+// Merge of the splits: one workgroup per q head.  Thread (q, g) owns float4 column q of the
+// head and splits s = g (mod SG).  Its first CH partial rows are loaded at entry, before the
+// split weights w_s = exp(m_s - M) are known, so the whole merge costs one round trip to the
+// partials for up to SG * CH splits.  Empty splits (l = 0) never wrote their rows: their
+// weight is 0 and the select keeps whatever those rows hold out of the sum.
 constexpr int kMaxSplits = 2048;
 
 template <int HD>
 __global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restrict__ part_o,
                                                            const float* __restrict__ part_ml, int S,
                                                            float* __restrict__ out) {
-  constexpr int NG = 256 / HD;
+  constexpr int Q = HD / 4;    // float4 columns of a row
+  constexpr int SG = 256 / Q;  // split groups
+  constexpr int CH = 8;        // rows per thread per pass
   __shared__ float s_w[kMaxSplits];
-  __shared__ float s_red[256];
-  __shared__ float s_ml[2 * 4];
+  __shared__ float4 s_red[256];
+  __shared__ float s_ml[8];
   const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const float* ml = part_ml + int64_t(h) * S * 2;
+  const int q = tid % Q, g = tid / Q;
+  const float2* ml = reinterpret_cast<const float2*>(part_ml) + int64_t(h) * S;
+  const float4* po = reinterpret_cast<const float4*>(part_o + int64_t(h) * S * HD) + q;
+  // every load below is unconditional (clamped to split S - 1): a load under a branch would
+  // wait for its own completion and serialise the round trips
+  float4 ov[CH];
+#pragma unroll
+  for (int i = 0; i < CH; i++) ov[i] = po[int64_t(min(g + SG * i, S - 1)) * Q];
+  constexpr int MLPT = kMaxSplits / 256;
+  float2 e[MLPT];
+#pragma unroll
+  for (int i = 0; i < MLPT; i++) e[i] = ml[min(tid + 256 * i, S - 1)];
   float m = -INFINITY;
-  for (int s = tid; s < S; s += 256)
-    if (ml[2 * s + 1] > 0.f) m = fmaxf(m, ml[2 * s]);
+#pragma unroll
+  for (int i = 0; i < MLPT; i++)
+    if (tid + 256 * i < S && e[i].y > 0.f) m = fmaxf(m, e[i].x);
   m = wave_max_dpp(m);
   if (lane == 0) s_ml[wv] = m;
   __syncthreads();
   const float M = fmaxf(fmaxf(s_ml[0], s_ml[1]), fmaxf(s_ml[2], s_ml[3]));
   float l = 0.f;
-  for (int s = tid; s < S; s += 256) {
-    const float w = ml[2 * s + 1] > 0.f ? expf(ml[2 * s] - M) : 0.f;
-    s_w[s] = w;
-    l += w * ml[2 * s + 1];
+#pragma unroll
+  for (int i = 0; i < MLPT; i++) {
+    const int s = tid + 256 * i;
+    const float w = (s < S && e[i].y > 0.f) ? expf(e[i].x - M) : 0.f;
+    if (s < S) s_w[s] = w;
+    l += w * e[i].y;
   }
   l = wave_sum_dpp(l);
-  __syncthreads();
   if (lane == 0) s_ml[4 + wv] = l;
   __syncthreads();
   const float L = s_ml[4] + s_ml[5] + s_ml[6] + s_ml[7];
-  const int d = tid % HD, g = tid / HD;
-  const float* po = part_o + int64_t(h) * S * HD + d;
-  float o0 = 0.f, o1 = 0.f;
-  int s = g;
-  // empty splits (w = 0) never wrote their rows: skip them rather than multiply by 0
-  for (; s + NG < S; s += 2 * NG) {
-    const float w0 = s_w[s], w1 = s_w[s + NG];
-    if (w0 != 0.f) o0 += w0 * po[int64_t(s) * HD];
-    if (w1 != 0.f) o1 += w1 * po[int64_t(s + NG) * HD];
-  }
-  if (s < S && s_w[s] != 0.f) o0 += s_w[s] * po[int64_t(s) * HD];
-  s_red[tid] = o0 + o1;
-  __syncthreads();
-  if (tid < HD) {
-    float o = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int base = 0;;) {
 #pragma unroll
-    for (int j = 0; j < NG; j++) o += s_red[j * HD + tid];
-    out[int64_t(h) * HD + tid] = o / L;
+    for (int i = 0; i < CH; i++) {
+      const int s = base + g + SG * i;
+      const float w = s < S ? s_w[s] : 0.f;
+      const bool on = w != 0.f;
+      acc.x += on ? w * ov[i].x : 0.f;
+      acc.y += on ? w * ov[i].y : 0.f;
+      acc.z += on ? w * ov[i].z : 0.f;
+      acc.w += on ? w * ov[i].w : 0.f;
+    }
+    base += SG * CH;
+    if (base >= S) break;
+#pragma unroll
+    for (int i = 0; i < CH; i++) ov[i] = po[int64_t(min(base + g + SG * i, S - 1)) * Q];
+  }
+  s_red[tid] = acc;
+  __syncthreads();
+  if (tid < Q) {
+    float4 o = s_red[tid];
+#pragma unroll
+    for (int j = 1; j < SG; j++) {
+      const float4 r = s_red[j * Q + tid];
+      o.x += r.x;
+      o.y += r.y;
+      o.z += r.z;
+      o.w += r.w;
+    }
+    const float inv = 1.0f / L;
+    float* oh = out + int64_t(h) * HD + 4 * tid;
+    oh[0] = o.x * inv;
+    oh[1] = o.y * inv;
+    oh[2] = o.z * inv;
+    oh[3] = o.w * inv;
   }
 }
 
@@ -432,13 +488,15 @@ extern "C" int jero_hip_gqa_attention(float* out_dev, const float* q_dev, const 
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: kv_dtype must be JERO_KV_F32 or JERO_KV_F16");
   if ((reinterpret_cast<uintptr_t>(k_dev) | reinterpret_cast<uintptr_t>(v_dev)) & 15u)
     return fail(JERO_ERR_INVALID_ARGUMENT, "attention: K and V must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(q_dev) & 7u) return fail(JERO_ERR_INVALID_ARGUMENT, "attention: q must be 8-byte aligned");
   size_t need = attn_workspace_bytes(n_heads_q, head_dim, int(seq_len));
   void* ws = workspace_dev;
   if (ws) {
     if (workspace_bytes < need)
       return fail(JERO_ERR_TENSOR_BOUNDS, "attention: workspace of " + std::to_string(workspace_bytes) +
                                               " bytes, need " + std::to_string(need));
-    if (!aligned4(ws)) return fail(JERO_ERR_INVALID_ARGUMENT, "attention: workspace must be 4-byte aligned");
+    if (reinterpret_cast<uintptr_t>(ws) & 15u)
+      return fail(JERO_ERR_INVALID_ARGUMENT, "attention: workspace must be 16-byte aligned");
   } else {
     rc = workspace(need, &ws);
     if (rc) return rc;

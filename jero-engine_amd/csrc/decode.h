@@ -30,9 +30,9 @@ struct DGemvArgs {
   int max_blocks;     // 0: grid capped at kDecodeBlocksPerCU workgroups per CU
 };
 
-int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s);
-// Workgroups launch_dgemv uses for an n_in = K, N-row tensor (the argmax partial count).
-int dgemv_blocks(int quant, int64_t K, int64_t N, int out_mode);
+// Enqueues the fused GEMV; *blocks (if given) receives the workgroups launched, which is the
+// number of argmax partials an argmax launch leaves in amax_v / amax_i.
+int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s, int* blocks = nullptr);
 // Longest row the fused decode GEMV takes for a weight format.
 int dgemv_max_k(int quant);
 // hidden = embedding row of *token; also the step's RoPE table rope_cs[hd/2][cos, sin].

@@ -15,6 +15,8 @@
 // position.
 #include "decode.h"
 
+#include <algorithm>
+
 #include "dequant.h"
 #include "gemv_dot.h"
 #include "jero_common.h"
@@ -394,8 +396,24 @@ __global__ void set_state_kernel(int32_t* token, int64_t* pos, int32_t t, int64_
 
 namespace {
 
+// Workgroups of one dgemv instance that fit on a CU at once (registers and LDS); the
+// persistent grid never exceeds what is resident, or a second batch of workgroups would
+// start only after the first one drained.
 template <int F, int LPR, int UPL, int R, int OUT, int XB>
-void dgemv_one(DGemvArgs a, int64_t rows_or_pairs, hipStream_t s) {
+int dgemv_fit() {
+  static const int fit = [] {
+    int nb = 0;
+    const size_t shm = 256 + size_t(XB) * (kDecodeThreads / kWave) * 292 + 16;  // prologue LDS bound
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, dgemv_kernel<F, LPR, UPL, R, OUT, XB>, kDecodeThreads,
+                                                     shm) != hipSuccess || nb < 1)
+      nb = 1;
+    return nb;
+  }();
+  return fit;
+}
+
+template <int F, int LPR, int UPL, int R, int OUT, int XB>
+int dgemv_one(DGemvArgs a, int64_t rows_or_pairs, hipStream_t s) {
   constexpr int G = kWave / LPR;
   if constexpr (OUT == kOutSwiglu) {
     const int64_t per = G == 1 ? R / 2 : R * (G / 2);
@@ -405,12 +423,14 @@ void dgemv_one(DGemvArgs a, int64_t rows_or_pairs, hipStream_t s) {
   }
   const int64_t wpb = kDecodeThreads / kWave;
   int64_t blocks = (a.n_groups + wpb - 1) / wpb;
-  const int64_t cap = int64_t(device_info().cus) * kDecodeBlocksPerCU;
+  const int per_cu = std::min(kDecodeBlocksPerCU, dgemv_fit<F, LPR, UPL, R, OUT, XB>());
+  const int64_t cap = int64_t(device_info().cus) * per_cu;
   if (blocks > cap) blocks = cap;
   if (a.max_blocks > 0 && blocks > a.max_blocks) blocks = a.max_blocks;
   const size_t shm = 256 + size_t(row_bytes((F == JERO_Q8_0 || F == JERO_Q4_0) ? JERO_ACT_Q8 : JERO_Q8_K, a.K));
   hipLaunchKernelGGL((dgemv_kernel<F, LPR, UPL, R, OUT, XB>), dim3(unsigned(blocks)), dim3(kDecodeThreads),
                      (shm + 15) & ~size_t(15), s, a);
+  return int(blocks);
 }
 
 // Activation blocks each wave builds in the prologue.
@@ -422,41 +442,32 @@ inline int xb_for(int F, int K) {
 }
 
 template <int F, int LPR, int UPL, int OUT>
-void dgemv_xb(const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t s) {
+int dgemv_xb(const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t s) {
   // one row per wave slot; SwiGLU with one row group per wave needs its gate/up pair in-wave
   constexpr int R = (OUT == kOutSwiglu && LPR == 64) ? 2 : 1;
   switch (xb_for(F, a.K)) {
-    case 1: dgemv_one<F, LPR, UPL, R, OUT, 1>(a, rows_or_pairs, s); break;
-    case 2: dgemv_one<F, LPR, UPL, R, OUT, 2>(a, rows_or_pairs, s); break;
-    case 4: dgemv_one<F, LPR, UPL, R, OUT, 4>(a, rows_or_pairs, s); break;
-    case 6: dgemv_one<F, LPR, UPL, R, OUT, 6>(a, rows_or_pairs, s); break;
-    default: dgemv_one<F, LPR, UPL, R, OUT, 8>(a, rows_or_pairs, s); break;
+    case 1: return dgemv_one<F, LPR, UPL, R, OUT, 1>(a, rows_or_pairs, s);
+    case 2: return dgemv_one<F, LPR, UPL, R, OUT, 2>(a, rows_or_pairs, s);
+    case 4: return dgemv_one<F, LPR, UPL, R, OUT, 4>(a, rows_or_pairs, s);
+    case 6: return dgemv_one<F, LPR, UPL, R, OUT, 6>(a, rows_or_pairs, s);
+    default: return dgemv_one<F, LPR, UPL, R, OUT, 8>(a, rows_or_pairs, s);
   }
 }
 
+// Returns the workgroups launched (> 0) or a negated status.
 template <int F, int OUT>
 int dgemv_fmt(const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t s) {
   const int U = a.U;
   const int lpr = U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4;
   const int upl = (U + lpr - 1) / lpr;
-  if (lpr == 4) {
-    dgemv_xb<F, 4, 1, OUT>(a, rows_or_pairs, s);
-  } else if (lpr == 16) {
-    dgemv_xb<F, 16, 1, OUT>(a, rows_or_pairs, s);
-  } else if (lpr == 32) {
-    dgemv_xb<F, 32, 1, OUT>(a, rows_or_pairs, s);
-  } else if (upl == 1) {
-    dgemv_xb<F, 64, 1, OUT>(a, rows_or_pairs, s);
-  } else if (upl == 2) {
-    dgemv_xb<F, 64, 2, OUT>(a, rows_or_pairs, s);
-  } else if (upl <= 3) {
-    dgemv_xb<F, 64, 3, OUT>(a, rows_or_pairs, s);
-  } else if (upl <= 4) {
-    dgemv_xb<F, 64, 4, OUT>(a, rows_or_pairs, s);
-  } else {
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: row of " + std::to_string(a.K) + " elements too long");
-  }
-  return JERO_OK;
+  if (lpr == 4) return dgemv_xb<F, 4, 1, OUT>(a, rows_or_pairs, s);
+  if (lpr == 16) return dgemv_xb<F, 16, 1, OUT>(a, rows_or_pairs, s);
+  if (lpr == 32) return dgemv_xb<F, 32, 1, OUT>(a, rows_or_pairs, s);
+  if (upl == 1) return dgemv_xb<F, 64, 1, OUT>(a, rows_or_pairs, s);
+  if (upl == 2) return dgemv_xb<F, 64, 2, OUT>(a, rows_or_pairs, s);
+  if (upl <= 3) return dgemv_xb<F, 64, 3, OUT>(a, rows_or_pairs, s);
+  if (upl <= 4) return dgemv_xb<F, 64, 4, OUT>(a, rows_or_pairs, s);
+  return -fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: row of " + std::to_string(a.K) + " elements too long");
 }
 
 template <int OUT>
@@ -468,12 +479,12 @@ int dgemv_out(int quant, const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t 
     case JERO_Q8_0: return dgemv_fmt<JERO_Q8_0, OUT>(a, rows_or_pairs, s);
     case JERO_Q4_0: return dgemv_fmt<JERO_Q4_0, OUT>(a, rows_or_pairs, s);
   }
-  return fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: unsupported weight quantization " + std::to_string(quant));
+  return -fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: unsupported weight quantization " + std::to_string(quant));
 }
 
 }  // namespace
 
-int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s) {
+int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s, int* blocks) {
   int rc;
   switch (out_mode) {
     case kOutStore: rc = dgemv_out<kOutStore>(quant, a, a.N, s); break;
@@ -482,25 +493,9 @@ int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s) {
     case kOutArgmax: rc = dgemv_out<kOutArgmax>(quant, a, a.N, s); break;
     default: return fail(JERO_ERR_INVALID_ARGUMENT, "decode: bad output mode");
   }
-  if (rc) return rc;
+  if (rc < 0) return -rc;
+  if (blocks) *blocks = rc;
   return check_launch("decode gemv");
-}
-
-int dgemv_blocks(int quant, int64_t K, int64_t N, int out_mode) {
-  const int U = units_per_row(quant, K);
-  const int lpr = U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4;
-  const int64_t G = kWave / lpr, R = (out_mode == kOutSwiglu && lpr == 64) ? 2 : 1;
-  int64_t n_groups;
-  if (out_mode == kOutSwiglu) {
-    const int64_t per = G == 1 ? R / 2 : R * (G / 2);
-    n_groups = (N / 2 + per - 1) / per;
-  } else {
-    n_groups = (N + G * R - 1) / (G * R);
-  }
-  const int64_t wpb = kDecodeThreads / kWave;
-  int64_t blocks = (n_groups + wpb - 1) / wpb;
-  const int64_t cap = int64_t(device_info().cus) * kDecodeBlocksPerCU;
-  return int(blocks < cap ? blocks : cap);
 }
 
 int dgemv_max_k(int quant) {

@@ -186,9 +186,10 @@ static int repack_if_q6k(jero_model* m, DevTensor& t) {
   return JERO_OK;
 }
 
+constexpr int kArgmaxSlots = 4096;
+
 static int gemv(jero_model* m, const DevTensor& w, const float* x, const float* norm, float eps, int out_mode,
-                float* y, int64_t half, hipStream_t s) {
-  (void)m;
+                float* y, int64_t half, hipStream_t s, int* blocks = nullptr) {
   DGemvArgs a{};
   a.w = static_cast<const uint8_t*>(w.dev);
   a.rb = row_bytes(w.quant, w.n_in);
@@ -202,7 +203,8 @@ static int gemv(jero_model* m, const DevTensor& w, const float* x, const float* 
   a.half = half;
   a.amax_v = m->amax_v;
   a.amax_i = m->amax_i;
-  return launch_dgemv(w.quant, out_mode, a, s);
+  a.max_blocks = kArgmaxSlots;  // one argmax partial slot per workgroup
+  return launch_dgemv(w.quant, out_mode, a, s, blocks);
 }
 
 }  // namespace jero
@@ -227,7 +229,7 @@ extern "C" int jero_hip_model_create(const jero_model_config* cfg, jero_model** 
   const int64_t Q = q_dim(c), KV = kv_dim(c);
   const size_t es = c.kv_dtype == JERO_KV_F16 ? 2 : 4;
   m->kv_bytes = size_t(c.n_layers) * 2 * size_t(c.kv_capacity) * size_t(KV) * es;
-  const int max_blocks = 1024 * 4;
+  const int max_blocks = kArgmaxSlots;
   void* p;
   if ((rc = dev_alloc(m, m->kv_bytes, &m->kv)) ||
       (rc = check_hip(hipMemset(m->kv, 0, m->kv_bytes), "kv zero")) ||
@@ -439,9 +441,9 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
     if (rc) return rc;
   }
   // final norm -> LM head -> greedy token
+  int head_blocks = 0;
   rc = gemv(m, m->output, m->hidden, static_cast<const float*>(m->output_norm.dev), eps_ffn, kOutArgmax, m->logits, 0,
-            s);
+            s, &head_blocks);
   if (rc) return rc;
-  return launch_argmax_final(m->amax_v, m->amax_i, dgemv_blocks(m->output.quant, c.hidden, c.vocab, kOutArgmax),
-                             m->token, m->pos, s);
+  return launch_argmax_final(m->amax_v, m->amax_i, head_blocks, m->token, m->pos, s);
 }

@@ -88,6 +88,22 @@ int jero_hip_vec_dot(int quant, const void *w_dev, size_t w_bytes, int64_t n_in,
 int jero_hip_matvec_partials(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
                              const void *xq_dev, float *y_dev, int32_t *partials_dev, void *stream);
 
+/* ---- GEMM over GGUF weight bytes (m activation rows at once) ----
+ * Row r of the result is jero_hip_matvec of activation row r: it replaces the prefill token loop
+ * (src/qwen_deepseek.rs:2298-2312, one matvec_any per token) and PackedNibbleMatrix::gemm(out,
+ * &QuantizedActQ8) (src/weights.rs:1416-1426).  xq_dev: m rows of jero_hip_row_bytes(act, n_in)
+ * bytes (jero_hip_quantize_act with m rows); y_dev: [m][n_out] f32.  Q4_K with n_out a multiple
+ * of 128 runs the int8-MFMA kernel; other formats and shapes run one GEMV per row. */
+int jero_hip_gemm(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
+                  const void *xq_dev, int64_t m, float *y_dev, void *stream);
+
+/* The exact integer product of ForwardExec::matmul (src/forward.rs:555-655) -> matmul_rows
+ * (:763-811) -> gemm_i8_ime / gemm_i8_vector: out[m][n] = sum_k x[m][k] * w[n][k] in int32.
+ * x_dev [m][k] and w_dev [n][k] int8 row-major, out_dev [m][n] int32; k <= 131071 so no sum
+ * can overflow.  k a multiple of 16 (and 4-byte aligned operands) runs the MFMA kernel. */
+int jero_hip_gemm_i8(const int8_t *x_dev, int64_t m, int64_t k, const int8_t *w_dev, int64_t n, int32_t *out_dev,
+                     void *stream);
+
 /* Load-time re-layout of a weight tensor for the GEMV kernels; replaces repack_tensor_parallel
  * (src/weights.rs:914-955) -> RepackedWeight.  Q6_K -> JERO_Q6_K_R: the n_out x n_in tensor's
  * bytes are regrouped into 16-byte aligned planes of the same total size (src and dst may not

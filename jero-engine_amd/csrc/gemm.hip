@@ -1,0 +1,433 @@
+// gemm.hip -- prefill GEMM over GGUF Q4_K weights and the exact int8 GEMM, on gfx950 int8 MFMA.
+//
+// Q4_K x Q8_K (many tokens at once).  Row m of Y is the GEMV of x_m (the reference's prefill runs
+// matvec_any token by token, src/qwen_deepseek.rs:2298-2312), so per 256-element block b:
+//   y[m][n] += d_x[m,b] * (d_w[n,b] * T - dmin[n,b] * Mn),
+//   T  = sum_k sc_{j(k)}[n] * q4[n][k] * q8[m][k]      (j = 32-element sub-block)
+//   Mn = sum_{i<16} m_{i/2}[n] * bsum16[m][i]
+// T needs the 6-bit sub-block scale inside the sum.  sc = 8a + b with a, b in 0..7 splits it
+// into two int8 planes a*q4 and b*q4 (both <= 105), so T = 8 * (plane-a product) + (plane-b
+// product): 16 v_mfma_i32_32x32x32_i8 per 32x32 tile and block, accumulated in one int32
+// register set (shifted left by 3 between the planes), exact.  Mn is one
+// v_mfma_f32_32x32x16_f16 over the 16 bsums (|bsum| <= 2032 and m <= 63 are exact in f16, the
+// sums stay below 2^24).  The scales are applied once per block in f32.
+//
+// Tiling: a workgroup of 4 waves owns a 128 (tokens) x 128 (weight rows) tile; each wave a
+// 64 x 64 quadrant of 2 x 2 MFMA tiles.  Per block, the 128 activation rows (int8 + bsums + d)
+// and the 128 weight rows (expanded to the two planes, mins and scales) are staged in LDS; the
+// global loads of block b+1 are in flight while block b runs.  Workgroups are mapped so that
+// the ones sharing a weight tile run on one XCD (one L2).
+//
+// int8 x int8 -> int32 (ForwardExec::matmul, src/forward.rs:555-655, 763-811): the same
+// 128 x 128 workgroup tile, 256-wide K steps, one v_mfma_i32_32x32x32_i8 per 32 K.
+#include <algorithm>
+#include <string>
+
+#include "gemv.h"
+#include "jero_common.h"
+#include "runtime.h"
+
+namespace jero {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kGemmThreads = 256;
+constexpr int kGemmBM = 128;   // tokens per workgroup tile
+constexpr int kGemmBN = 128;   // weight rows per workgroup tile
+constexpr int kPlaneStride = 272;  // LDS bytes per 256-byte row: 16-byte reads of 16 rows hit distinct banks
+
+struct Q4kStage {
+  int8_t a[kGemmBM][kPlaneStride];   // q8 of the activation block
+  int8_t pa[kGemmBN][kPlaneStride];  // (sc >> 3) * q4
+  int8_t pb[kGemmBN][kPlaneStride];  // (sc & 7) * q4
+  _Float16 bs[kGemmBM][16];          // activation bsums
+  _Float16 mn[kGemmBN][16];          // weight mins, m_{i/2} at i
+  float dx[kGemmBM];
+  float dw[kGemmBN];
+  float dmin[kGemmBN];
+};
+
+// Global data of one block for this thread: activation row half and weight row half.
+struct Q4kRegs {
+  u32x4 aq[8];   // 128 bytes of the activation row's q8
+  u32x4 aext[2]; // half 0: d in .x; half 1: the 16 bsums
+  u32x4 wh;      // weight block header: d, dmin, scales[12]
+  u32x4 wq[4];   // 64 bytes of the weight row's qs
+};
+
+// Workgroup -> (weight tile, token tile): consecutive workgroups go to consecutive XCDs, so
+// workgroup w runs on XCD w % 8; each XCD takes a contiguous range of weight tiles and runs
+// every token tile of one weight tile back to back.
+__device__ __forceinline__ void gemm_tile_of(int wg, int n_wg, int n_tiles_m, int& tm, int& tn) {
+  int l = wg;
+  if ((n_wg & 7) == 0) l = (wg & 7) * (n_wg >> 3) + (wg >> 3);  // a bijection when 8 divides the grid
+  tn = l / n_tiles_m;
+  tm = l % n_tiles_m;
+}
+
+__device__ __forceinline__ void q4k_load(Q4kRegs& R, const uint8_t* __restrict__ x, int64_t xrb, int m0, int M,
+                                         const uint8_t* __restrict__ w, int64_t wrb, int n0, int b) {
+  const int t = threadIdx.x, r = t >> 1, h = t & 1;
+  const int m = min(m0 + r, M - 1);  // rows past M read row M-1 and are never stored
+  const uint8_t* xa = x + int64_t(m) * xrb + int64_t(b) * 292;
+#pragma unroll
+  for (int i = 0; i < 8; i++) R.aq[i] = ld4(xa + 4 + 128 * h + 16 * i);
+  // half 0: bytes 0..15 (d first); half 1: the 32 bytes of bsums at 260
+  R.aext[0] = ld4(xa + (h ? 260 : 0));
+  R.aext[1] = ld4(xa + (h ? 276 : 0));
+  const uint8_t* wb = w + int64_t(n0 + r) * wrb + int64_t(b) * 144;
+  R.wh = ld4(wb);
+#pragma unroll
+  for (int i = 0; i < 4; i++) R.wq[i] = ld4(wb + 16 + 64 * h + 16 * i);
+}
+
+__device__ __forceinline__ uint32_t byte_at(const u32x4& v, int i) {
+  const uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
+  return (w >> (8 * (i & 3))) & 0xFFu;
+}
+
+__device__ __forceinline__ uint32_t pk_mul(uint32_t x, uint32_t s) {
+  // four bytes times s (<= 7): per 16-bit half b0*s + (b1*s << 8), no carry since b*s <= 105
+  const u16x2 r = __builtin_bit_cast(u16x2, x) * u16x2{uint16_t(s), uint16_t(s)};
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ void q4k_store(const Q4kRegs& R, Q4kStage& S) {
+  const int t = threadIdx.x, r = t >> 1, h = t & 1;
+  // activation
+#pragma unroll
+  for (int i = 0; i < 8; i++) *reinterpret_cast<u32x4*>(&S.a[r][128 * h + 16 * i]) = R.aq[i];
+  if (h == 0) {
+    S.dx[r] = __uint_as_float(R.aext[0].x);
+  } else {
+    v8h lo, hi;
+    const uint32_t w[8] = {R.aext[0].x, R.aext[0].y, R.aext[0].z, R.aext[0].w,
+                           R.aext[1].x, R.aext[1].y, R.aext[1].z, R.aext[1].w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      lo[2 * i] = _Float16(float(int16_t(w[i] & 0xFFFFu)));
+      lo[2 * i + 1] = _Float16(float(int16_t(w[i] >> 16)));
+      hi[2 * i] = _Float16(float(int16_t(w[4 + i] & 0xFFFFu)));
+      hi[2 * i + 1] = _Float16(float(int16_t(w[4 + i] >> 16)));
+    }
+    *reinterpret_cast<v8h*>(&S.bs[r][0]) = lo;
+    *reinterpret_cast<v8h*>(&S.bs[r][8]) = hi;
+  }
+  // weight: scales and mins of this half's four sub-blocks j = 4h .. 4h+3 (GGUF 6-bit packing)
+  const uint32_t dd = R.wh.x;
+  if (h == 0) {
+    S.dw[r] = float(__builtin_bit_cast(_Float16, uint16_t(dd & 0xFFFFu)));
+    S.dmin[r] = float(__builtin_bit_cast(_Float16, uint16_t(dd >> 16)));
+  }
+  uint32_t sc[4], mv[4];
+#pragma unroll
+  for (int jj = 0; jj < 4; jj++) {
+    const int j = 4 * h + jj;
+    // scales[i] is header byte 4 + i
+    if (j < 4) {
+      sc[jj] = byte_at(R.wh, 4 + j) & 63u;
+      mv[jj] = byte_at(R.wh, 4 + j + 4) & 63u;
+    } else {
+      sc[jj] = (byte_at(R.wh, 4 + j + 4) & 15u) | ((byte_at(R.wh, 4 + j - 4) >> 6) << 4);
+      mv[jj] = (byte_at(R.wh, 4 + j + 4) >> 4) | ((byte_at(R.wh, 4 + j) >> 6) << 4);
+    }
+  }
+  v8h mins;
+#pragma unroll
+  for (int i = 0; i < 8; i++) mins[i] = _Float16(float(mv[i >> 1]));
+  *reinterpret_cast<v8h*>(&S.mn[r][8 * h]) = mins;
+  // qs chunk c (bytes 64h + 16c of qs): pair p = 2h + c/2, elements l0 = 16 (c & 1) .. +16;
+  // low nibbles -> sub-block 2p, high nibbles -> 2p + 1
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const int p = 2 * h + (c >> 1), l0 = 16 * (c & 1);
+    const uint32_t s_lo = sc[2 * (c >> 1)], s_hi = sc[2 * (c >> 1) + 1];
+    const uint32_t xw[4] = {R.wq[c].x, R.wq[c].y, R.wq[c].z, R.wq[c].w};
+    u32x4 a_lo, b_lo, a_hi, b_hi;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t ql = xw[i] & 0x0F0F0F0Fu, qh = (xw[i] >> 4) & 0x0F0F0F0Fu;
+      a_lo[i] = pk_mul(ql, s_lo >> 3);
+      b_lo[i] = pk_mul(ql, s_lo & 7u);
+      a_hi[i] = pk_mul(qh, s_hi >> 3);
+      b_hi[i] = pk_mul(qh, s_hi & 7u);
+    }
+    *reinterpret_cast<u32x4*>(&S.pa[r][64 * p + l0]) = a_lo;
+    *reinterpret_cast<u32x4*>(&S.pb[r][64 * p + l0]) = b_lo;
+    *reinterpret_cast<u32x4*>(&S.pa[r][64 * p + 32 + l0]) = a_hi;
+    *reinterpret_cast<u32x4*>(&S.pb[r][64 * p + 32 + l0]) = b_hi;
+  }
+}
+
+__global__ void __launch_bounds__(kGemmThreads) gemm_q4k_kernel(const uint8_t* __restrict__ w, int64_t wrb,
+                                                                 const uint8_t* __restrict__ x, int64_t xrb, int M,
+                                                                 int N, int nb, float* __restrict__ y) {
+  __shared__ Q4kStage S;
+  const int n_tiles_m = (M + kGemmBM - 1) / kGemmBM;
+  int tm, tn;
+  gemm_tile_of(blockIdx.x, gridDim.x, n_tiles_m, tm, tn);
+  const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+
+  v16f acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+
+  Q4kRegs R;
+  q4k_load(R, x, xrb, m0, M, w, wrb, n0, 0);
+  q4k_store(R, S);
+  __syncthreads();
+  for (int b = 0; b < nb; b++) {
+    if (b + 1 < nb) q4k_load(R, x, xrb, m0, M, w, wrb, n0, b + 1);
+    // plane a (scaled by 8 afterwards), then plane b, into one int32 accumulator per tile
+    v16i C[2][2];
+#pragma unroll
+    for (int pl = 0; pl < 2; pl++) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        v4i af[2], bf[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+          af[i] = *reinterpret_cast<const v4i*>(&S.a[64 * wm + 32 * i + lr][32 * j + 16 * lh]);
+          bf[i] = *reinterpret_cast<const v4i*>(pl == 0 ? &S.pa[64 * wn + 32 * i + lr][32 * j + 16 * lh]
+                                                        : &S.pb[64 * wn + 32 * i + lr][32 * j + 16 * lh]);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+          for (int k = 0; k < 2; k++) {
+            if (pl == 0 && j == 0) {
+              const v16i z = {};
+              C[i][k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[k], z, 0, 0, 0);
+            } else {
+              C[i][k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[k], C[i][k], 0, 0, 0);
+            }
+          }
+      }
+      if (pl == 0) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+          for (int k = 0; k < 2; k++) C[i][k] = C[i][k] << 3;
+      }
+    }
+    // mins: Mn = bsums . m over the 16 bsum groups
+    v16f Mn[2][2];
+    {
+      v8h bsf[2], mnf[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        bsf[i] = *reinterpret_cast<const v8h*>(&S.bs[64 * wm + 32 * i + lr][8 * lh]);
+        mnf[i] = *reinterpret_cast<const v8h*>(&S.mn[64 * wn + 32 * i + lr][8 * lh]);
+      }
+      const v16f z = {};
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int k = 0; k < 2; k++) Mn[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bsf[i], mnf[k], z, 0, 0, 0);
+    }
+    // scales: column n = lane % 32 of each tile, rows (v/4)*8 + (lane/32)*4 + v%4
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int nl = 64 * wn + 32 * k + lr;
+      const float dw = S.dw[nl], dm = S.dmin[nl];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float4 dx = *reinterpret_cast<const float4*>(&S.dx[64 * wm + 32 * i + 8 * g + 4 * lh]);
+          const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int v = 4 * g + e;
+            const float tb = dw * float(C[i][k][v]) - dm * Mn[i][k][v];
+            acc[i][k][v] = fmaf(dxv[e], tb, acc[i][k][v]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (b + 1 < nb) {
+      q4k_store(R, S);
+      __syncthreads();
+    }
+  }
+  // store: for each v, the 32 lanes of a half-wave write 32 consecutive floats of one row
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int n = n0 + 64 * wn + 32 * k + lr;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int m = m0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
+        if (m < M) y[int64_t(m) * N + n] = acc[i][k][v];
+      }
+    }
+}
+
+// ---------------------------------------------------------------- int8 x int8 -> int32
+
+struct I8Stage {
+  int8_t a[kGemmBM][kPlaneStride];
+  int8_t b[kGemmBN][kPlaneStride];
+};
+
+// 256 K-bytes of a row of 128 rows, 2 threads per row: 8 loads of 16 bytes each.  Chunks at or
+// past k are zero; rows past `rows` read row rows-1.
+__device__ __forceinline__ void i8_load(u32x4 (&r)[8], const int8_t* __restrict__ p, int64_t ld, int row0, int rows,
+                                        int k0, int K) {
+  const int t = threadIdx.x, rr = t >> 1, h = t & 1;
+  const int row = min(row0 + rr, rows - 1);
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(p) + int64_t(row) * ld;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int kk = k0 + 128 * h + 16 * i;
+    const u32x4 v = ld4(base + min(kk, K - 16));
+    r[i] = kk < K ? v : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+__device__ __forceinline__ void i8_store(const u32x4 (&r)[8], int8_t (*dst)[kPlaneStride]) {
+  const int t = threadIdx.x, rr = t >> 1, h = t & 1;
+#pragma unroll
+  for (int i = 0; i < 8; i++) *reinterpret_cast<u32x4*>(&dst[rr][128 * h + 16 * i]) = r[i];
+}
+
+__global__ void __launch_bounds__(kGemmThreads) gemm_i8_kernel(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
+                                                                int M, int N, int K, int32_t* __restrict__ out) {
+  __shared__ I8Stage S;
+  const int n_tiles_m = (M + kGemmBM - 1) / kGemmBM;
+  int tm, tn;
+  gemm_tile_of(blockIdx.x, gridDim.x, n_tiles_m, tm, tn);
+  const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+  v16i C[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) C[i][k][v] = 0;
+  u32x4 ra[8], rb[8];
+  i8_load(ra, x, K, m0, M, 0, K);
+  i8_load(rb, w, K, n0, N, 0, K);
+  i8_store(ra, S.a);
+  i8_store(rb, S.b);
+  __syncthreads();
+  for (int k0 = 0; k0 < K; k0 += 256) {
+    const bool more = k0 + 256 < K;
+    if (more) {
+      i8_load(ra, x, K, m0, M, k0 + 256, K);
+      i8_load(rb, w, K, n0, N, k0 + 256, K);
+    }
+    const int steps = min(8, (K - k0 + 31) / 32);
+    for (int j = 0; j < steps; j++) {
+      v4i af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        af[i] = *reinterpret_cast<const v4i*>(&S.a[64 * wm + 32 * i + lr][32 * j + 16 * lh]);
+        bf[i] = *reinterpret_cast<const v4i*>(&S.b[64 * wn + 32 * i + lr][32 * j + 16 * lh]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int k = 0; k < 2; k++) C[i][k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[k], C[i][k], 0, 0, 0);
+    }
+    __syncthreads();
+    if (more) {
+      i8_store(ra, S.a);
+      i8_store(rb, S.b);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int n = n0 + 64 * wn + 32 * k + lr;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int m = m0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
+        if (m < M && n < N) out[int64_t(m) * N + n] = C[i][k][v];
+      }
+    }
+}
+
+// K not a multiple of 16: one output per thread, byte loads.
+__global__ void __launch_bounds__(256) gemm_i8_small_kernel(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
+                                                             int M, int N, int K, int32_t* __restrict__ out) {
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= int64_t(M) * N) return;
+  const int m = int(idx / N), n = int(idx % N);
+  const int8_t* xa = x + int64_t(m) * K;
+  const int8_t* wb = w + int64_t(n) * K;
+  int32_t s = 0;
+  for (int k = 0; k < K; k++) s += int32_t(xa[k]) * int32_t(wb[k]);
+  out[idx] = s;
+}
+
+int gemm_tiles(int64_t M, int64_t N) { return int(((M + kGemmBM - 1) / kGemmBM) * ((N + kGemmBN - 1) / kGemmBN)); }
+
+}  // namespace jero
+
+using namespace jero;
+
+extern "C" int jero_hip_gemm(int quant, const void* w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
+                             const void* xq_dev, int64_t m, float* y_dev, void* stream) {
+  int rc = check_matvec_args(quant, w_dev, w_bytes, n_in, n_out, xq_dev, y_dev);
+  if (rc) return rc;
+  if (m <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "gemm: no activation rows");
+  if (m > (int64_t(1) << 24) || n_out > (int64_t(1) << 30))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "gemm: m or n_out beyond the 32-bit tile indexing");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int act = act_format(quant);
+  const int64_t xrb = row_bytes(act, n_in);
+  if (quant == JERO_Q4_K && n_out % kGemmBN == 0) {
+    const int tiles = gemm_tiles(m, n_out);
+    hipLaunchKernelGGL(gemm_q4k_kernel, dim3(unsigned(tiles)), dim3(kGemmThreads), 0, s,
+                       static_cast<const uint8_t*>(w_dev), row_bytes(quant, n_in),
+                       static_cast<const uint8_t*>(xq_dev), xrb, int(m), int(n_out), int(n_in / 256), y_dev);
+    return check_launch("gemm q4_k");
+  }
+  // other formats and shapes: one GEMV per activation row (each row is matvec_any of x_m)
+  for (int64_t r = 0; r < m; r++) {
+    rc = launch_matvec(quant, w_dev, n_in, n_out, static_cast<const uint8_t*>(xq_dev) + r * xrb, y_dev + r * n_out,
+                       nullptr, s);
+    if (rc) return rc;
+  }
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_gemm_i8(const int8_t* x_dev, int64_t m, int64_t k, const int8_t* w_dev, int64_t n,
+                                int32_t* out_dev, void* stream) {
+  if (!x_dev || !w_dev || !out_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "gemm_i8: null pointer");
+  if (m <= 0 || n <= 0 || k <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "gemm_i8: empty operand");
+  if (m > (int64_t(1) << 24) || n > (int64_t(1) << 24) || k > (int64_t(1) << 24))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "gemm_i8: m, n, k above 2^24");
+  if (k * 128 * 128 > INT32_MAX)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "gemm_i8: k=" + std::to_string(k) + " could overflow int32 sums");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (k % 16 == 0 && !(reinterpret_cast<uintptr_t>(x_dev) & 3u) && !(reinterpret_cast<uintptr_t>(w_dev) & 3u)) {
+    const int tiles = gemm_tiles(m, n);
+    hipLaunchKernelGGL(gemm_i8_kernel, dim3(unsigned(tiles)), dim3(kGemmThreads), 0, s, x_dev, w_dev, int(m), int(n),
+                       int(k), out_dev);
+    return check_launch("gemm i8");
+  }
+  const int64_t total = m * n;
+  hipLaunchKernelGGL(gemm_i8_small_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, x_dev, w_dev, int(m),
+                     int(n), int(k), out_dev);
+  return check_launch("gemm i8 (small k)");
+}

@@ -47,6 +47,8 @@ _SIGS = {
     "jero_hip_matvec": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P]),
     "jero_hip_vec_dot": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "jero_hip_matvec_partials": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _P]),
+    "jero_hip_gemm": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _I64, _P, _P]),
+    "jero_hip_gemm_i8": (_I32, [_P, _I64, _I64, _P, _I64, _P, _P]),
     "jero_hip_dequantize_rows": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, _P]),
     "jero_hip_repack": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, C.POINTER(C.c_int), _P]),
     "jero_hip_gqa_attention": (_I32, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I64, _F, _P, _SZ, _P]),
@@ -165,6 +167,29 @@ def matvec(weights, xq, out, stream=None):
     """y = W . x with x already in the weight format's activation blocks."""
     check(lib().jero_hip_matvec(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in,
                                 out.numel(), _ptr(xq), _ptr(out), _stream(stream)))
+    return out
+
+
+def gemm(weights, xq, m, out, stream=None):
+    """Y[m, n_out] = rows of the m quantized activation rows `xq` times W: row r is matvec of
+    x_r (the prefill token loop, src/qwen_deepseek.rs:2298-2312, and PackedNibbleMatrix::gemm,
+    src/weights.rs:1416-1426)."""
+    check(lib().jero_hip_gemm(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in, weights.n_out,
+                              _ptr(xq), m, _ptr(out), _stream(stream)))
+    return out
+
+
+def gemm_i8(x, w, out=None, stream=None):
+    """Exact int8 product of ForwardExec::matmul (src/forward.rs:763-811): out[m, n] =
+    sum_k x[m, k] * w[n, k] in int32; x [m, k], w [n, k] int8 device tensors."""
+    import torch
+    m, k = x.shape
+    n = w.shape[0]
+    if w.shape[1] != k:
+        raise K3Error(14, f"gemm_i8: x has k={k}, w has k={w.shape[1]}")
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.int32, device=x.device)
+    check(lib().jero_hip_gemm_i8(_ptr(x), m, k, _ptr(w), n, _ptr(out), _stream(stream)))
     return out
 
 

@@ -61,6 +61,22 @@ int64_t jero_hip_row_bytes(int quant, int64_t n);
 /* Activation format consumed by the dot product of `weight_quant` (-1 if unsupported). */
 int jero_hip_act_format(int weight_quant);
 
+/* ---- device copies of host weight tensors ----
+ * The device-side RepackedTensorStore (src/weights.rs:189-277): the reference's kernels read
+ * weights from mmaped host bytes (LockedModelWeights, src/weights.rs:729-734); a binding
+ * registers each tensor once and then passes the device address to the entry points below.
+ * Registering [host, host + nbytes) copies it to the current device on first use; registering
+ * it again, or any sub-range of it, returns the matching device address without copying.
+ * Partially overlapping ranges are rejected (TensorBoundsError). */
+int jero_hip_weights_register(const void *host, size_t nbytes, const void **dev_out);
+/* Device address of [host, host + nbytes), which must lie inside a registered tensor
+ * (slice_rows / slice_expert views of it). */
+int jero_hip_weights_lookup(const void *host, size_t nbytes, const void **dev_out);
+/* Frees every tensor registered on the current device (after a device synchronize). */
+int jero_hip_weights_release_all(void);
+/* Waits for the work enqueued on `stream`. */
+int jero_hip_sync(void *stream);
+
 /* ---- Q8 activation quantization ----
  * Replaces repack::QuantizedActQ8::quantize(acts, m, k) (src/weights.rs:1416-1417) and the
  * quantization implied inside vec_dot_* (src/gemma.rs:73-86).  x_dev: m rows of k f32;

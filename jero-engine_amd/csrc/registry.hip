@@ -1,0 +1,120 @@
+// registry.hip -- device copies of host (mmaped) weight tensors, uploaded once.
+//
+// The reference's kernels read weights straight from the mmaped GGUF bytes that
+// LockedModelWeights owns (src/weights.rs:729-734), and repacked copies are cached per tensor
+// by RepackedTensorStore (src/weights.rs:189-277).  Here a tensor's bytes are copied to HBM on
+// its first registration and found again by host address: registering the same range again is
+// free, and any sub-range (a slice_rows / slice_expert view) of a registered tensor maps to the
+// matching device address, so a binding can hand the GPU the view the reference's callers pass.
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "jero_common.h"
+#include "runtime.h"
+
+namespace jero {
+namespace {
+
+struct Region {
+  size_t nbytes;
+  int device;
+  void* dev;
+};
+
+std::mutex g_mu;
+// keyed by (device, host start address)
+std::map<std::pair<int, uintptr_t>, Region> g_regions;
+
+int current_device(int* dev) { return check_hip(hipGetDevice(dev), "hipGetDevice"); }
+
+// Registered region of `device` holding [p, p + n), or nullptr.
+const Region* find_region(int device, uintptr_t p, size_t n, uintptr_t* start) {
+  auto it = g_regions.upper_bound({device, p});
+  if (it == g_regions.begin()) return nullptr;
+  --it;
+  if (it->first.first != device) return nullptr;
+  const uintptr_t s = it->first.second;
+  if (p < s || p + n > s + it->second.nbytes) return nullptr;
+  *start = s;
+  return &it->second;
+}
+
+}  // namespace
+}  // namespace jero
+
+using namespace jero;
+
+extern "C" int jero_hip_weights_register(const void* host, size_t nbytes, const void** dev_out) {
+  if (!host || !dev_out) return fail(JERO_ERR_INVALID_ARGUMENT, "weights_register: null pointer");
+  if (nbytes == 0) return fail(JERO_ERR_TENSOR_BOUNDS, "weights_register: empty tensor");
+  int device = 0;
+  int rc = current_device(&device);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lock(g_mu);
+  const uintptr_t p = reinterpret_cast<uintptr_t>(host);
+  uintptr_t start = 0;
+  if (const Region* r = find_region(device, p, nbytes, &start)) {
+    *dev_out = static_cast<const uint8_t*>(r->dev) + (p - start);
+    return JERO_OK;
+  }
+  // a new range must not overlap an existing one partially
+  auto it = g_regions.lower_bound({device, p});
+  if (it != g_regions.end() && it->first.first == device && it->first.second < p + nbytes)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "weights_register: range overlaps a registered tensor");
+  if (it != g_regions.begin()) {
+    auto pr = std::prev(it);
+    if (pr->first.first == device && pr->first.second + pr->second.nbytes > p)
+      return fail(JERO_ERR_TENSOR_BOUNDS, "weights_register: range overlaps a registered tensor");
+  }
+  void* dev = nullptr;
+  if (hipMalloc(&dev, nbytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(JERO_ERR_INSUFFICIENT_MEMORY, "weights_register: no device memory for " + std::to_string(nbytes) +
+                                                  " bytes");
+  }
+  rc = check_hip(hipMemcpy(dev, host, nbytes, hipMemcpyHostToDevice), "weights_register upload");
+  if (rc) {
+    (void)hipFree(dev);
+    return rc;
+  }
+  g_regions[{device, p}] = Region{nbytes, device, dev};
+  *dev_out = dev;
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_weights_lookup(const void* host, size_t nbytes, const void** dev_out) {
+  if (!host || !dev_out) return fail(JERO_ERR_INVALID_ARGUMENT, "weights_lookup: null pointer");
+  int device = 0;
+  int rc = current_device(&device);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lock(g_mu);
+  const uintptr_t p = reinterpret_cast<uintptr_t>(host);
+  uintptr_t start = 0;
+  const Region* r = find_region(device, p, nbytes, &start);
+  if (!r) return fail(JERO_ERR_TENSOR_BOUNDS, "weights_lookup: range is not inside a registered tensor");
+  *dev_out = static_cast<const uint8_t*>(r->dev) + (p - start);
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_weights_release_all(void) {
+  int device = 0;
+  int rc = current_device(&device);
+  if (rc) return rc;
+  rc = check_hip(hipDeviceSynchronize(), "weights_release_all sync");
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lock(g_mu);
+  for (auto it = g_regions.begin(); it != g_regions.end();) {
+    if (it->first.first == device) {
+      (void)hipFree(it->second.dev);
+      it = g_regions.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_sync(void* stream) {
+  return check_hip(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "stream synchronize");
+}

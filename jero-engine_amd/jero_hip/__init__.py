@@ -47,6 +47,10 @@ _SIGS = {
     "jero_hip_matvec": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P]),
     "jero_hip_vec_dot": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "jero_hip_matvec_partials": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _P]),
+    "jero_hip_weights_register": (_I32, [_P, _SZ, C.POINTER(_P)]),
+    "jero_hip_weights_lookup": (_I32, [_P, _SZ, C.POINTER(_P)]),
+    "jero_hip_weights_release_all": (_I32, []),
+    "jero_hip_sync": (_I32, [_P]),
     "jero_hip_gemm": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _I64, _P, _P]),
     "jero_hip_gemm_i8": (_I32, [_P, _I64, _I64, _P, _I64, _P, _P]),
     "jero_hip_dequantize_rows": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, _P]),
@@ -168,6 +172,27 @@ def matvec(weights, xq, out, stream=None):
     check(lib().jero_hip_matvec(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in,
                                 out.numel(), _ptr(xq), _ptr(out), _stream(stream)))
     return out
+
+
+def weights_register(host_array):
+    """Device address of a host numpy buffer's bytes (uploaded on first registration)."""
+    dev = _P()
+    check(lib().jero_hip_weights_register(host_array.ctypes.data, host_array.nbytes, C.byref(dev)))
+    return dev.value
+
+
+def weights_lookup(host_array):
+    dev = _P()
+    check(lib().jero_hip_weights_lookup(host_array.ctypes.data, host_array.nbytes, C.byref(dev)))
+    return dev.value
+
+
+def weights_release_all():
+    check(lib().jero_hip_weights_release_all())
+
+
+def sync(stream=None):
+    check(lib().jero_hip_sync(_stream(stream)))
 
 
 def gemm(weights, xq, m, out, stream=None):

@@ -35,33 +35,31 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kGemmThreads = 256;
-constexpr int kGemmBM = 128;   // tokens per workgroup tile
-constexpr int kGemmBN = 128;   // weight rows per workgroup tile
+constexpr int kGemmThreads = 256;  // int8 kernel
+constexpr int kGemmBM = 128;       // tokens (rows of x) per workgroup tile
+constexpr int kGemmBN = 128;       // weight rows per workgroup tile
 constexpr int kPlaneStride = 272;  // LDS bytes per 256-byte row: 16-byte reads of 16 rows hit distinct banks
+constexpr int kQ4Threads = 512;    // Q4_K kernel: 8 waves, two per SIMD
 
-struct Q4kStage {
-  int8_t a[kGemmBM][kPlaneStride];   // q8 of the activation block
-  int8_t pa[kGemmBN][kPlaneStride];  // (sc >> 3) * q4
-  int8_t pb[kGemmBN][kPlaneStride];  // (sc & 7) * q4
-  _Float16 bs[kGemmBM][16];          // activation bsums
-  _Float16 mn[kGemmBN][16];          // weight mins, m_{i/2} at i
+// One block (256 K-elements) of the workgroup's 128 activation rows and 128 weight rows, as
+// plain copies: the weight rows stay raw Q4_K (each lane expands its fragments to the int8
+// planes and decodes its row's scale fields in registers).
+struct __attribute__((aligned(16))) Q4kStage {
+  int8_t a[kGemmBM][kPlaneStride];  // q8 of the activation block
+  uint8_t w[kGemmBN][144];          // raw Q4_K blocks (144 = 9 x 16: rows stay 16-byte aligned)
+  int16_t bs[kGemmBM][16];          // activation bsums (raw)
   float dx[kGemmBM];
-  float dw[kGemmBN];
-  float dmin[kGemmBN];
 };
 
-// Global data of one block for this thread: activation row half and weight row half.
+// Global data of one block for this thread: a quarter of an activation row and of a weight row.
 struct Q4kRegs {
-  u32x4 aq[8];   // 128 bytes of the activation row's q8
-  u32x4 aext[2]; // half 0: d in .x; half 1: the 16 bsums
-  u32x4 wh;      // weight block header: d, dmin, scales[12]
-  u32x4 wq[4];   // 64 bytes of the weight row's qs
+  u32x4 aq[4];  // 64 bytes of the activation row's q8
+  u32x4 ax;     // quarter 0: d in .x; quarters 1, 2: bsums 0..7, 8..15
+  u32x4 wc[3];  // weight row chunks q, q + 4 and (quarter 0) chunk 8
 };
 
-// Workgroup -> (weight tile, token tile): consecutive workgroups go to consecutive XCDs, so
-// workgroup w runs on XCD w % 8; each XCD takes a contiguous range of weight tiles and runs
-// every token tile of one weight tile back to back.
+// Workgroup -> (weight tile, token tile): workgroup w runs on XCD w % 8; each XCD takes a
+// contiguous range of tiles, which runs every token tile of one weight tile back to back.
 __device__ __forceinline__ void gemm_tile_of(int wg, int n_wg, int n_tiles_m, int& tm, int& tn) {
   int l = wg;
   if ((n_wg & 7) == 0) l = (wg & 7) * (n_wg >> 3) + (wg >> 3);  // a bijection when 8 divides the grid
@@ -69,24 +67,36 @@ __device__ __forceinline__ void gemm_tile_of(int wg, int n_wg, int n_tiles_m, in
   tm = l % n_tiles_m;
 }
 
+// Every load is unconditional (rows past M read row M-1 and are never stored).
 __device__ __forceinline__ void q4k_load(Q4kRegs& R, const uint8_t* __restrict__ x, int64_t xrb, int m0, int M,
                                          const uint8_t* __restrict__ w, int64_t wrb, int n0, int b) {
-  const int t = threadIdx.x, r = t >> 1, h = t & 1;
-  const int m = min(m0 + r, M - 1);  // rows past M read row M-1 and are never stored
+  const int t = threadIdx.x, r = t >> 2, q = t & 3;
+  const int m = min(m0 + r, M - 1);
   const uint8_t* xa = x + int64_t(m) * xrb + int64_t(b) * 292;
 #pragma unroll
-  for (int i = 0; i < 8; i++) R.aq[i] = ld4(xa + 4 + 128 * h + 16 * i);
-  // half 0: bytes 0..15 (d first); half 1: the 32 bytes of bsums at 260
-  R.aext[0] = ld4(xa + (h ? 260 : 0));
-  R.aext[1] = ld4(xa + (h ? 276 : 0));
+  for (int i = 0; i < 4; i++) R.aq[i] = ld4(xa + 4 + 64 * q + 16 * i);
+  R.ax = ld4(xa + (q == 1 ? 260 : q == 2 ? 276 : 0));
   const uint8_t* wb = w + int64_t(n0 + r) * wrb + int64_t(b) * 144;
-  R.wh = ld4(wb);
-#pragma unroll
-  for (int i = 0; i < 4; i++) R.wq[i] = ld4(wb + 16 + 64 * h + 16 * i);
+  R.wc[0] = ld4(wb + 16 * q);
+  R.wc[1] = ld4(wb + 16 * (q + 4));
+  R.wc[2] = ld4(wb + (q == 0 ? 128 : 16 * q));
 }
 
-__device__ __forceinline__ uint32_t byte_at(const u32x4& v, int i) {
-  const uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
+__device__ __forceinline__ void q4k_store(const Q4kRegs& R, Q4kStage& S) {
+  const int t = threadIdx.x, r = t >> 2, q = t & 3;
+#pragma unroll
+  for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(&S.a[r][64 * q + 16 * i]) = R.aq[i];
+  *reinterpret_cast<u32x4*>(&S.w[r][16 * q]) = R.wc[0];
+  *reinterpret_cast<u32x4*>(&S.w[r][16 * (q + 4)]) = R.wc[1];
+  // quarter 0 writes chunk 8; the others rewrite their chunk q with the same bytes
+  *reinterpret_cast<u32x4*>(&S.w[r][q == 0 ? 128 : 16 * q]) = R.wc[2];
+  if (q == 0) S.dx[r] = __uint_as_float(R.ax.x);
+  if (q == 1 || q == 2) *reinterpret_cast<u32x4*>(&S.bs[r][8 * (q - 1)]) = R.ax;
+}
+
+// Byte i (0..11) of the 12 packed scale bytes held in three dwords.
+__device__ __forceinline__ uint32_t sbyte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+  const uint32_t w = i < 4 ? s0 : i < 8 ? s1 : s2;
   return (w >> (8 * (i & 3))) & 0xFFu;
 }
 
@@ -96,189 +106,126 @@ __device__ __forceinline__ uint32_t pk_mul(uint32_t x, uint32_t s) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
-__device__ __forceinline__ void q4k_store(const Q4kRegs& R, Q4kStage& S) {
-  const int t = threadIdx.x, r = t >> 1, h = t & 1;
-  // activation
-#pragma unroll
-  for (int i = 0; i < 8; i++) *reinterpret_cast<u32x4*>(&S.a[r][128 * h + 16 * i]) = R.aq[i];
-  if (h == 0) {
-    S.dx[r] = __uint_as_float(R.aext[0].x);
-  } else {
-    v8h lo, hi;
-    const uint32_t w[8] = {R.aext[0].x, R.aext[0].y, R.aext[0].z, R.aext[0].w,
-                           R.aext[1].x, R.aext[1].y, R.aext[1].z, R.aext[1].w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      lo[2 * i] = _Float16(float(int16_t(w[i] & 0xFFFFu)));
-      lo[2 * i + 1] = _Float16(float(int16_t(w[i] >> 16)));
-      hi[2 * i] = _Float16(float(int16_t(w[4 + i] & 0xFFFFu)));
-      hi[2 * i + 1] = _Float16(float(int16_t(w[4 + i] >> 16)));
-    }
-    *reinterpret_cast<v8h*>(&S.bs[r][0]) = lo;
-    *reinterpret_cast<v8h*>(&S.bs[r][8]) = hi;
-  }
-  // weight: scales and mins of this half's four sub-blocks j = 4h .. 4h+3 (GGUF 6-bit packing)
-  const uint32_t dd = R.wh.x;
-  if (h == 0) {
-    S.dw[r] = float(__builtin_bit_cast(_Float16, uint16_t(dd & 0xFFFFu)));
-    S.dmin[r] = float(__builtin_bit_cast(_Float16, uint16_t(dd >> 16)));
-  }
-  uint32_t sc[4], mv[4];
-#pragma unroll
-  for (int jj = 0; jj < 4; jj++) {
-    const int j = 4 * h + jj;
-    // scales[i] is header byte 4 + i
-    if (j < 4) {
-      sc[jj] = byte_at(R.wh, 4 + j) & 63u;
-      mv[jj] = byte_at(R.wh, 4 + j + 4) & 63u;
-    } else {
-      sc[jj] = (byte_at(R.wh, 4 + j + 4) & 15u) | ((byte_at(R.wh, 4 + j - 4) >> 6) << 4);
-      mv[jj] = (byte_at(R.wh, 4 + j + 4) >> 4) | ((byte_at(R.wh, 4 + j) >> 6) << 4);
-    }
-  }
-  v8h mins;
-#pragma unroll
-  for (int i = 0; i < 8; i++) mins[i] = _Float16(float(mv[i >> 1]));
-  *reinterpret_cast<v8h*>(&S.mn[r][8 * h]) = mins;
-  // qs chunk c (bytes 64h + 16c of qs): pair p = 2h + c/2, elements l0 = 16 (c & 1) .. +16;
-  // low nibbles -> sub-block 2p, high nibbles -> 2p + 1
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    const int p = 2 * h + (c >> 1), l0 = 16 * (c & 1);
-    const uint32_t s_lo = sc[2 * (c >> 1)], s_hi = sc[2 * (c >> 1) + 1];
-    const uint32_t xw[4] = {R.wq[c].x, R.wq[c].y, R.wq[c].z, R.wq[c].w};
-    u32x4 a_lo, b_lo, a_hi, b_hi;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t ql = xw[i] & 0x0F0F0F0Fu, qh = (xw[i] >> 4) & 0x0F0F0F0Fu;
-      a_lo[i] = pk_mul(ql, s_lo >> 3);
-      b_lo[i] = pk_mul(ql, s_lo & 7u);
-      a_hi[i] = pk_mul(qh, s_hi >> 3);
-      b_hi[i] = pk_mul(qh, s_hi & 7u);
-    }
-    *reinterpret_cast<u32x4*>(&S.pa[r][64 * p + l0]) = a_lo;
-    *reinterpret_cast<u32x4*>(&S.pb[r][64 * p + l0]) = b_lo;
-    *reinterpret_cast<u32x4*>(&S.pa[r][64 * p + 32 + l0]) = a_hi;
-    *reinterpret_cast<u32x4*>(&S.pb[r][64 * p + 32 + l0]) = b_hi;
-  }
-}
-
-__global__ void __launch_bounds__(kGemmThreads) gemm_q4k_kernel(const uint8_t* __restrict__ w, int64_t wrb,
-                                                                 const uint8_t* __restrict__ x, int64_t xrb, int M,
-                                                                 int N, int nb, float* __restrict__ y) {
-  __shared__ Q4kStage S;
+__global__ void __launch_bounds__(kQ4Threads) gemm_q4k_kernel(const uint8_t* __restrict__ w, int64_t wrb,
+                                                               const uint8_t* __restrict__ x, int64_t xrb, int M,
+                                                               int N, int nb, float* __restrict__ y) {
+  __shared__ Q4kStage S[2];
   const int n_tiles_m = (M + kGemmBM - 1) / kGemmBM;
   int tm, tn;
   gemm_tile_of(blockIdx.x, gridDim.x, n_tiles_m, tm, tn);
   const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int wm = wv >> 1, wn = wv & 1;
+  const int wm = wv >> 2, wn = wv & 3;  // wave tile: rows 64 wm .. +64, weight rows 32 wn .. +32
   const int lr = lane & 31, lh = lane >> 5;
+  const int nl = 32 * wn + lr;
 
-  v16f acc[2][2];
+  v16f acc[2];
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+    for (int v = 0; v < 16; v++) acc[i][v] = 0.f;
 
   Q4kRegs R;
   q4k_load(R, x, xrb, m0, M, w, wrb, n0, 0);
-  q4k_store(R, S);
+  q4k_store(R, S[0]);
   __syncthreads();
   for (int b = 0; b < nb; b++) {
+    const Q4kStage& T = S[b & 1];
     if (b + 1 < nb) q4k_load(R, x, xrb, m0, M, w, wrb, n0, b + 1);
-    // plane a (scaled by 8 afterwards), then plane b, into one int32 accumulator per tile
-    v16i C[2][2];
+    // this lane's weight row: header d, dmin and the 6-bit scales / mins (GGUF Q4_K packing)
+    const u32x4 hd = *reinterpret_cast<const u32x4*>(&T.w[nl][0]);
+    uint32_t scv[8], mvv[4];
 #pragma unroll
-    for (int pl = 0; pl < 2; pl++) {
+    for (int j = 0; j < 8; j++) {
+      scv[j] = j < 4 ? sbyte(hd.y, hd.z, hd.w, j) & 63u
+                     : (sbyte(hd.y, hd.z, hd.w, j + 4) & 15u) | ((sbyte(hd.y, hd.z, hd.w, j - 4) >> 6) << 4);
+    }
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        v4i af[2], bf[2];
+    for (int jj = 0; jj < 4; jj++) {  // mins of sub-blocks 4 lh + jj (this lane's half of the bsums)
+      const int j = 4 * lh + jj;
+      mvv[jj] = j < 4 ? sbyte(hd.y, hd.z, hd.w, j + 4) & 63u
+                      : (sbyte(hd.y, hd.z, hd.w, j + 4) >> 4) | ((sbyte(hd.y, hd.z, hd.w, j) >> 6) << 4);
+    }
+    v16i Ca[2], Cb[2];  // plane a (sc >> 3) and plane b (sc & 7) products
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-          af[i] = *reinterpret_cast<const v4i*>(&S.a[64 * wm + 32 * i + lr][32 * j + 16 * lh]);
-          bf[i] = *reinterpret_cast<const v4i*>(pl == 0 ? &S.pa[64 * wn + 32 * i + lr][32 * j + 16 * lh]
-                                                        : &S.pb[64 * wn + 32 * i + lr][32 * j + 16 * lh]);
-        }
+    for (int i = 0; i < 4; i++) {
+      // qs bytes 32 i + 16 lh .. +16: low nibbles are sub-block 2i, high nibbles 2i + 1, at
+      // K-elements 16 lh .. +16 of each (the MFMA fragment of this lane)
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(&T.w[nl][16 + 32 * i + 16 * lh]);
+      const uint32_t s0 = scv[2 * i], s1 = scv[2 * i + 1];
+      v4i pa0, pb0, pa1, pb1;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-          for (int k = 0; k < 2; k++) {
-            if (pl == 0 && j == 0) {
-              const v16i z = {};
-              C[i][k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[k], z, 0, 0, 0);
-            } else {
-              C[i][k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[k], C[i][k], 0, 0, 0);
-            }
-          }
+      for (int e = 0; e < 4; e++) {
+        const uint32_t ql = raw[e] & 0x0F0F0F0Fu, qh = (raw[e] >> 4) & 0x0F0F0F0Fu;
+        pa0[e] = int(pk_mul(ql, s0 >> 3));
+        pb0[e] = int(pk_mul(ql, s0 & 7u));
+        pa1[e] = int(pk_mul(qh, s1 >> 3));
+        pb1[e] = int(pk_mul(qh, s1 & 7u));
       }
-      if (pl == 0) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-          for (int k = 0; k < 2; k++) C[i][k] = C[i][k] << 3;
+      for (int mt = 0; mt < 2; mt++) {
+        const v4i af0 = *reinterpret_cast<const v4i*>(&T.a[64 * wm + 32 * mt + lr][64 * i + 16 * lh]);
+        const v4i af1 = *reinterpret_cast<const v4i*>(&T.a[64 * wm + 32 * mt + lr][64 * i + 32 + 16 * lh]);
+        if (i == 0) {
+          const v16i z = {};
+          Ca[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af0, pa0, z, 0, 0, 0);
+          Cb[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af0, pb0, z, 0, 0, 0);
+        } else {
+          Ca[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af0, pa0, Ca[mt], 0, 0, 0);
+          Cb[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af0, pb0, Cb[mt], 0, 0, 0);
+        }
+        Ca[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af1, pa1, Ca[mt], 0, 0, 0);
+        Cb[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af1, pb1, Cb[mt], 0, 0, 0);
       }
     }
-    // mins: Mn = bsums . m over the 16 bsum groups
-    v16f Mn[2][2];
-    {
-      v8h bsf[2], mnf[2];
+    // mins (bsums . m over the 16 bsum groups), then the block's scales:
+    // column n = lane % 32 of the tile, rows (v/4)*8 + (lane/32)*4 + v%4
+    v8h mnf;
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        bsf[i] = *reinterpret_cast<const v8h*>(&S.bs[64 * wm + 32 * i + lr][8 * lh]);
-        mnf[i] = *reinterpret_cast<const v8h*>(&S.mn[64 * wn + 32 * i + lr][8 * lh]);
+    for (int i = 0; i < 8; i++) mnf[i] = _Float16(float(mvv[i >> 1]));
+    const float dw = float(__builtin_bit_cast(_Float16, uint16_t(hd.x & 0xFFFFu)));
+    const float dm = float(__builtin_bit_cast(_Float16, uint16_t(hd.x >> 16)));
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+      const u32x4 braw = *reinterpret_cast<const u32x4*>(&T.bs[64 * wm + 32 * mt + lr][8 * lh]);
+      v8h bsf;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        bsf[2 * i] = _Float16(float(int16_t(braw[i] & 0xFFFFu)));
+        bsf[2 * i + 1] = _Float16(float(int16_t(braw[i] >> 16)));
       }
       const v16f z = {};
+      const v16f Mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(bsf, mnf, z, 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int g = 0; g < 4; g++) {
+        const float4 dx = *reinterpret_cast<const float4*>(&T.dx[64 * wm + 32 * mt + 8 * g + 4 * lh]);
+        const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
 #pragma unroll
-        for (int k = 0; k < 2; k++) Mn[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bsf[i], mnf[k], z, 0, 0, 0);
-    }
-    // scales: column n = lane % 32 of each tile, rows (v/4)*8 + (lane/32)*4 + v%4
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const int nl = 64 * wn + 32 * k + lr;
-      const float dw = S.dw[nl], dm = S.dmin[nl];
-#pragma unroll
-      for (int i = 0; i < 2; i++) {
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const float4 dx = *reinterpret_cast<const float4*>(&S.dx[64 * wm + 32 * i + 8 * g + 4 * lh]);
-          const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const int v = 4 * g + e;
-            const float tb = dw * float(C[i][k][v]) - dm * Mn[i][k][v];
-            acc[i][k][v] = fmaf(dxv[e], tb, acc[i][k][v]);
-          }
+        for (int e = 0; e < 4; e++) {
+          const int v = 4 * g + e;
+          const int tv = (Ca[mt][v] << 3) + Cb[mt][v];
+          acc[mt][v] = fmaf(dxv[e], dw * float(tv) - dm * Mn[v], acc[mt][v]);
         }
       }
     }
+    // stage b + 1 goes to the buffer every wave finished reading before the last barrier
+    if (b + 1 < nb) q4k_store(R, S[(b + 1) & 1]);
     __syncthreads();
-    if (b + 1 < nb) {
-      q4k_store(R, S);
-      __syncthreads();
-    }
   }
   // store: for each v, the 32 lanes of a half-wave write 32 consecutive floats of one row
+  const int n = n0 + nl;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const int n = n0 + 64 * wn + 32 * k + lr;
-#pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
-        if (m < M) y[int64_t(m) * N + n] = acc[i][k][v];
-      }
+    for (int v = 0; v < 16; v++) {
+      const int m = m0 + 64 * wm + 32 * mt + 8 * (v >> 2) + 4 * lh + (v & 3);
+      if (m < M) y[int64_t(m) * N + n] = acc[mt][v];
     }
 }
 
 // ---------------------------------------------------------------- int8 x int8 -> int32
 
-struct I8Stage {
+struct __attribute__((aligned(16))) I8Stage {
   int8_t a[kGemmBM][kPlaneStride];
   int8_t b[kGemmBN][kPlaneStride];
 };
@@ -397,7 +344,7 @@ extern "C" int jero_hip_gemm(int quant, const void* w_dev, size_t w_bytes, int64
   const int64_t xrb = row_bytes(act, n_in);
   if (quant == JERO_Q4_K && n_out % kGemmBN == 0) {
     const int tiles = gemm_tiles(m, n_out);
-    hipLaunchKernelGGL(gemm_q4k_kernel, dim3(unsigned(tiles)), dim3(kGemmThreads), 0, s,
+    hipLaunchKernelGGL(gemm_q4k_kernel, dim3(unsigned(tiles)), dim3(kQ4Threads), 0, s,
                        static_cast<const uint8_t*>(w_dev), row_bytes(quant, n_in),
                        static_cast<const uint8_t*>(xq_dev), xrb, int(m), int(n_out), int(n_in / 256), y_dev);
     return check_launch("gemm q4_k");

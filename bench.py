@@ -21,7 +21,12 @@ greedy next token.  One step is captured in a HIP graph; each replay decodes the
 weight-only (4.671 GB/token) and weights+KV (+0.604 GB) HBM rooflines, next to the oracle's
 C decode step timed on the host cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--copy-probe MB]
+Third and fourth parts: the Q4_K x Q8_K prefill GEMM (M=512, K=4096, N=14336) on int8 MFMA, as
+TOP/s and fractions of the int8 peak, next to the oracle's per-token GEMV; and the Qwen3-MoE expert
+layer (H=2048, 128 experts, FFN 768, top-8) at 1 and 64 tokens, as GB/s over the routed experts.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-gemm]
+                       [--no-moe] [--copy-probe MB]
 """
 import argparse
 import json
@@ -173,6 +178,107 @@ def bench_decode(torch, J, dev, stream, steps, warmup, keep_host):
     return res, host, host_kv
 
 
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+GEMM_SHAPE = (512, 4096, 14336)  # (tokens M, n_in K, n_out N), Q4_K weights
+
+
+def bench_gemm(torch, J, dev, stream, steps, keep_host):
+    """Prefill GEMM: Y[512, 14336] = X[512, 4096] (Q8_K) . W (Q4_K), int8 MFMA kernel.  Weights
+    rotate over 4 copies.  `mfma_issue_frac`: the MFMA work the kernel issues (two int8 planes
+    of 2MNK ops each, plus the f16 mins product of 2MN*16 per block) over the time at peak."""
+    M, K, N = GEMM_SHAPE
+    copies = 4
+    buf = synth_weights(torch, J, J.Q4_K, K, N, copies, dev, 3000)
+    views = [J.TensorView("ffn_up", J.Q4_K, [K, N], buf[c]) for c in range(copies)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(3001)
+    x = torch.randn(M, K, generator=g, device=dev)
+    xq = J.quantize_act(J.Q8_K, x)
+    y = torch.empty(M, N, device=dev)
+    cnt = [0]
+
+    def one():
+        J.gemm(views[cnt[0] % copies], xq, M, y, stream=stream)
+        cnt[0] += 1
+
+    t = time_graph(torch, one, steps, 3, stream)
+    ops = 2.0 * M * N * K
+    issued_s = 2 * ops / (INT8_PEAK_TOPS * 1e12) + 2.0 * M * N * 16 * (K // 256) / (F16_PEAK_TFLOPS * 1e12)
+    res = {"workload": f"Q4_K x Q8_K prefill GEMM M={M} K={K} N={N}, int8 MFMA", "us": round(t * 1e6, 2),
+           "tops": round(ops / t / 1e12, 1), "unit": "TOP/s", "peak": INT8_PEAK_TOPS,
+           "frac_int8_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS, 4),
+           "mfma_issue_frac": round(issued_s / t, 4), "tokens_per_s": round(M / t, 1)}
+    host = None
+    if keep_host:
+        host = (buf[0].cpu().numpy(), xq.cpu().numpy())
+    del buf, views
+    return res, host
+
+
+def cpu_gemm_baseline(O, host, budget_s=8.0):
+    """The oracle's GEMM (prefill = one matvec_any per token, C restatement, scalar, pthreads over
+    all host cores) on the same weights, a bounded number of token rows."""
+    M, K, N = GEMM_SHAPE
+    w, xq = host
+    threads = len(os.sched_getaffinity(0))
+    rb = len(xq) // M
+    t0 = time.perf_counter()
+    rows = 0
+    while time.perf_counter() - t0 < budget_s and rows < M:
+        O.matvec(12, w, K, N, xq[rows * rb:(rows + 1) * rb], threads=threads)
+        rows += 1
+    el = time.perf_counter() - t0
+    return rows / el, threads, rows, el
+
+
+MOE = dict(hidden=2048, experts=128, ffn=768, top_k=8)
+
+
+def bench_moe(torch, J, dev, stream, steps):
+    """Qwen3-MoE expert layer: H=2048, 128 experts of FFN 768 (gate/up Q4_K, down Q6_K), router
+    logits N(0,1), top-8; T=1 (decode) and T=64.  Two weight copies and 8 logit sets rotate, so the
+    experts read differ between launches.  Algorithmic bytes: the distinct routed experts' weights
+    (3.06 MB each) + activations."""
+    H, E, F, k = MOE["hidden"], MOE["experts"], MOE["ffn"], MOE["top_k"]
+    copies = 2
+    gate = synth_weights(torch, J, J.Q4_K, H, E * F, copies, dev, 3100)
+    up = synth_weights(torch, J, J.Q4_K, H, E * F, copies, dev, 3101)
+    down = synth_weights(torch, J, J.Q6_K, F, E * H, copies, dev, 3102)
+    gv = [J.TensorView("ffn_gate_exps", J.Q4_K, [H, F, E], gate[c]) for c in range(copies)]
+    uv = [J.TensorView("ffn_up_exps", J.Q4_K, [H, F, E], up[c]) for c in range(copies)]
+    dv = [J.TensorView("ffn_down_exps", J.Q6_K, [F, H, E], down[c]) for c in range(copies)]
+    per_expert = (J.row_bytes(J.Q4_K, H) * F * 2 + J.row_bytes(J.Q6_K, F) * H)
+    g = torch.Generator(device=dev)
+    g.manual_seed(3103)
+    out = {}
+    for T in (1, 64):
+        x = torch.randn(T, H, generator=g, device=dev)
+        logits = [torch.randn(T, E, generator=g, device=dev) for _ in range(8)]
+        y = torch.empty(T, H, device=dev)
+        ws = torch.empty(J.lib().jero_hip_moe_workspace_bytes(T, E, k, H, F), dtype=torch.uint8, device=dev)
+        cnt = [0]
+        sels = []
+
+        def one():
+            c = cnt[0]
+            sel, _ = J.dispatch_qwen3_moe_ffn(y, x, logits[c % 8], k, gv[c % copies], uv[c % copies],
+                                             dv[c % copies], workspace=ws, stream=stream)
+            if len(sels) < 8:
+                sels.append(sel)
+            cnt[0] += 1
+
+        t = time_graph(torch, one, steps, 1, stream)
+        distinct = sum(len(set(s.cpu().numpy().reshape(-1).tolist())) for s in sels[:8]) / len(sels[:8])
+        algo = distinct * per_expert + T * H * 4 * 2 + T * E * 4
+        out[f"T{T}"] = {"us": round(t * 1e6, 2), "distinct_experts": round(distinct, 1),
+                        "bytes": int(algo), "GB_s": round(algo / t / 1e9, 1),
+                        "frac_hbm": round(algo / t / 1e9 / HBM_PEAK_GBS, 4)}
+    out["workload"] = "Qwen3-MoE expert layer H=2048, E=128, F=768, top-8, gate/up Q4_K, down Q6_K"
+    del gate, up, down
+    return out
+
+
 def cpu_decode_baseline(O, host, host_kv, budget_s=10.0):
     """The oracle's decode step (execute_token_standard_with_hidden restated in C, scalar,
     pthreads over all host cores) on the same weights and KV values (widened to f32)."""
@@ -207,6 +313,18 @@ def cpu_baseline(O, host_w, host_xq, budget_s=12.0):
     return per_step * done / el / 1e9, threads, done, el
 
 
+def measured_traffic():
+    """HBM bytes per Q4_K GEMV launch (mean of the three shapes) from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes, each scaled by the counter's reading for a 512 MB copy; None if
+    the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "gemv_q4k_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["q4k_gemv_traffic_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -214,6 +332,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=50)
     ap.add_argument("--copy-probe", type=float, default=0.0,
                     help="also run one device copy of this many MB (PMC byte-counter calibration)")
@@ -313,6 +433,23 @@ def main():
                "sample": f"{reps} passes over the three Q4_K shapes (66.2 MB of weights, full size), "
                          f"{el:.1f} s, C restatement of matvec_any row chunks, scalar, pthreads"}
 
+    # ---- prefill GEMM (extra)
+    gemm = None
+    if not args.no_gemm:
+        gemm, ghost = bench_gemm(torch, J, dev, stream, max(10, args.steps // 10), not args.no_cpu)
+        torch.cuda.empty_cache()
+        if ghost is not None:
+            import pyoracle as O
+            tps, threads, rows, el = cpu_gemm_baseline(O, ghost)
+            gemm["cpu_baseline"] = {"value": round(tps, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+                                    "sample": f"{rows} of the 512 token rows (matvec_any per token), {el:.1f} s"}
+
+    # ---- routed experts (extra)
+    moe = None
+    if not args.no_moe:
+        moe = bench_moe(torch, J, dev, stream, max(20, args.steps // 5))
+        torch.cuda.empty_cache()
+
     # ---- full decode step (extra)
     decode = None
     if not args.no_decode:
@@ -343,10 +480,12 @@ def main():
         "config": {"workload": "Q4_K x Q8_K decode GEMV, batch 1: 4096->4096, 4096->12288, 12288->4096",
                    "rotated_weight_bytes": int(ROTATE_BYTES), "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "per_shape": per_shape,
         "q6k_head": head,
+        "prefill_gemm": gemm,
+        "moe": moe,
         "decode": decode,
     }
     print(json.dumps(out))

@@ -20,6 +20,8 @@
 // All integer partial sums are exact; every output element is reduced in a fixed order.
 #include "moe.h"
 
+#include <algorithm>
+
 #include "gemv_dot.h"
 #include "quantize.h"
 #include "runtime.h"
@@ -29,6 +31,7 @@ namespace jero {
 constexpr int kRouteThreads = 1024;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 16;
+constexpr int kRouteLdsPairs = 8192;  // (token, slot) pairs grouped from LDS
 
 __device__ __forceinline__ bool better(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
 
@@ -38,20 +41,26 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = kRouteThreads / 64;
   constexpr int PER = kMaxExperts / 64;
   __shared__ int s_count[kMaxExperts];
+  __shared__ int s_off[kMaxExperts];
+  __shared__ int s_wsum[2 * (kRouteThreads / 64)];
+  __shared__ __attribute__((aligned(16))) int s_sel[kRouteLdsPairs + 4];  // the selections, when they fit
   // 1. routing, one wave per token
   for (int t = wv; t < T; t += nw) {
     const float* lt = logits + int64_t(t) * E;
     float key[PER], prob[PER];
+    // all loads first, unconditional (clamped), then branch-free selects: a branch on a loaded
+    // value makes the load wait by itself
+    float lv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) lv[i] = lt[min(lane + 64 * i, E - 1)];
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-      const int e = lane + 64 * i;
-      float l = e < E ? lt[e] : -INFINITY;
-      bool fin = e < E && isfinite(l);
-      key[i] = fin ? l : -INFINITY;
-      if (fin) mx = fmaxf(mx, l);
+      const bool fin = (lane + 64 * i < E) & (fabsf(lv[i]) <= 3.402823466e38f);  // finite, not NaN
+      key[i] = fin ? lv[i] : -INFINITY;
+      mx = fmaxf(mx, key[i]);
     }
-    mx = wave_max(mx);
+    mx = wave_max_dpp(mx);
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
@@ -60,176 +69,271 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
       prob[i] = (fin && isfinite(mx)) ? expf(key[i] - mx) : 0.f;
       sum += prob[i];
     }
-    sum = wave_sum(sum);
+    sum = wave_sum_dpp(sum);
     const bool ok = sum > 0.f && isfinite(sum);
 #pragma unroll
     for (int i = 0; i < PER; i++) prob[i] = ok ? prob[i] / sum : 1.0f / float(E);
-    // top-k rounds; taken entries drop below every remaining key
+    // top-k rounds: the wave-wide best remaining key (DPP max), then its lowest expert index
+    // (the first column i, then the lowest lane, whose entry holds it); taken entries drop out
     float ssum = 0.f;
-    float wsel[kMaxTopK];
-    int isel[kMaxTopK];
+    int my_i = 0;      // lane j keeps selection j
+    float my_w = 0.f;
     bool taken[PER];
 #pragma unroll
     for (int i = 0; i < PER; i++) taken[i] = !(lane + 64 * i < E);
     for (int j = 0; j < k; j++) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
+      float lb = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < PER; i++)
+        if (!taken[i]) lb = fmaxf(lb, key[i]);
+      const float best = wave_max_dpp(lb);
+      int bi = -1;
       float bp = 0.f;
 #pragma unroll
       for (int i = 0; i < PER; i++) {
-        const int e = lane + 64 * i;
-        if (!taken[i] && better(key[i], e, bv, bi)) {
-          bv = key[i];
-          bi = e;
-          bp = prob[i];
+        const uint64_t hit = __ballot(!taken[i] && key[i] == best);
+        if (bi < 0 && hit != 0) {
+          const int src = __builtin_ctzll(hit);
+          bi = src + 64 * i;
+          bp = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, prob[i]), src));
+          if (lane == src) taken[i] = true;
         }
       }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        float ov = __shfl_xor(bv, off, kWave);
-        int oi = __shfl_xor(bi, off, kWave);
-        float op = __shfl_xor(bp, off, kWave);
-        if (better(ov, oi, bv, bi)) {
-          bv = ov;
-          bi = oi;
-          bp = op;
-        }
+      if (lane == j) {
+        my_i = bi;
+        my_w = bp;
       }
-#pragma unroll
-      for (int i = 0; i < PER; i++)
-        if (lane + 64 * i == bi) taken[i] = true;
-      isel[j] = bi;
-      wsel[j] = bp;
       ssum += bp;
     }
     const bool sok = ssum > 0.f && isfinite(ssum);
-    if (lane == 0) {
-      for (int j = 0; j < k; j++) {
-        sel_idx[t * k + j] = isel[j];
-        sel_w[t * k + j] = sok ? wsel[j] / ssum : 1.0f / float(k);
-      }
+    if (lane < k) {
+      sel_idx[t * k + lane] = my_i;
+      sel_w[t * k + lane] = sok ? my_w / ssum : 1.0f / float(k);
+      if (t * k + lane < kRouteLdsPairs) s_sel[t * k + lane] = my_i;
     }
   }
   // 2. group the (token, slot) pairs by expert
   for (int e = threadIdx.x; e < E; e += kRouteThreads) s_count[e] = 0;
-  __threadfence_block();
-  __syncthreads();
   const int n = T * k;
-  for (int i = threadIdx.x; i < n; i += kRouteThreads) atomicAdd(&s_count[sel_idx[i]], 1);
+  if (threadIdx.x < 4 && n + int(threadIdx.x) < kRouteLdsPairs + 4) s_sel[n + threadIdx.x] = -1;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int off = 0, na = 0;
-    for (int e = 0; e < E; e++) {
-      lists.offset[e] = off;
-      if (s_count[e] > 0) lists.active[na++] = e;
-      off += s_count[e];
+  const bool in_lds = n <= kRouteLdsPairs;
+  for (int i = threadIdx.x; i < n; i += kRouteThreads) atomicAdd(&s_count[in_lds ? s_sel[i] : sel_idx[i]], 1);
+  __syncthreads();
+  {
+    // exclusive scans of the counts (offsets) and of the active flags (active list), one thread
+    // per expert: wave scans, then the 16 wave totals
+    const int e = threadIdx.x;
+    const int c = e < E ? s_count[e] : 0, f = c > 0 ? 1 : 0;
+    int ic = c, jf = f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int oc = __shfl_up(ic, off, kWave), of = __shfl_up(jf, off, kWave);
+      if (lane >= off) {
+        ic += oc;
+        jf += of;
+      }
     }
-    lists.offset[E] = off;
-    *lists.n_active = na;
+    if (lane == 63) {
+      s_wsum[wv] = ic;
+      s_wsum[nw + wv] = jf;
+    }
+    __syncthreads();
+    int bc = 0, bf = 0;
+    for (int w = 0; w < wv; w++) {
+      bc += s_wsum[w];
+      bf += s_wsum[nw + w];
+    }
+    if (e < E) {
+      const int off_e = bc + ic - c;
+      s_off[e] = off_e;
+      lists.offset[e] = off_e;
+      if (f) lists.active[bf + jf - 1] = e;
+      if (e == E - 1) {
+        lists.offset[E] = off_e + c;
+        *lists.n_active = bf + jf;
+      }
+    }
   }
   __syncthreads();
   // stable placement: thread e walks the pairs in order and keeps those routed to e
   for (int e = threadIdx.x; e < E; e += kRouteThreads) {
     if (s_count[e] == 0) continue;
-    int pos = lists.offset[e];
-    for (int i = 0; i < n; i++) {
-      if (sel_idx[i] == e) {
-        lists.entry[pos] = i;
-        lists.inv[i] = pos;
-        pos++;
+    int pos = s_off[e];
+    if (in_lds) {  // four selections per LDS read (s_sel is padded with -1 past n)
+      for (int i = 0; i < n; i += 4) {
+        const int4 v = *reinterpret_cast<const int4*>(&s_sel[i]);
+        const int vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          if (vv[q] == e) {
+            lists.entry[pos] = i + q;
+            lists.inv[i + q] = pos;
+            pos++;
+          }
+        }
+      }
+    } else {
+      for (int i = 0; i < n; i++) {
+        if (sel_idx[i] == e) {
+          lists.entry[pos] = i;
+          lists.inv[i] = pos;
+          pos++;
+        }
       }
     }
   }
 }
 
-// gate/up + SwiGLU.  LPR <= 32: lane groups (2p, 2p+1) hold gate row and up row f0 + p.
+constexpr int kMoeTokChunk = 16;         // activation rows of one expert staged in LDS per pass
+constexpr int64_t kMoeStageBytes = 49152;  // LDS for them
+
+// Copies `n` activation rows of `rb` bytes (dword multiples) into LDS: row j comes from
+// src + rows[j] * rb, with rows[] already in LDS.  Eight unconditional (clamped) loads per thread
+// are in flight at a time.  Ends with a barrier.
+__device__ __forceinline__ void stage_rows(uint32_t* __restrict__ dst, const uint8_t* __restrict__ src, int64_t rb,
+                                           int n, const int* __restrict__ rows) {
+  const int words = int(rb / 4), total = n * words;
+  for (int idx0 = threadIdx.x; idx0 < total; idx0 += 8 * int(blockDim.x)) {
+    uint32_t v[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const int idx = min(idx0 + q * int(blockDim.x), total - 1);
+      const int j = idx / words, w = idx - j * words;
+      v[q] = reinterpret_cast<const uint32_t*>(src + int64_t(rows[j]) * rb)[w];
+    }
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const int idx = idx0 + q * int(blockDim.x);
+      if (idx < total) dst[idx] = v[q];
+    }
+  }
+  __syncthreads();
+}
+
+// gate/up + SwiGLU.  A workgroup takes one active expert and 4 * ppw * P of its (gate, up) row
+// pairs: lane groups (2p, 2p+1) of a wave hold gate row and up row f.  The expert's token
+// activations are staged in LDS (kMoeTokChunk rows per pass), so each weight row is read from
+// HBM once and each activation once per workgroup; the next row pair's weights are in flight
+// while the current one is reduced over the tokens.
 template <int F, int LPR, int UPL>
 __global__ void __launch_bounds__(256) moe_gate_up_kernel(const uint8_t* __restrict__ gate,
                                                           const uint8_t* __restrict__ up, int64_t rb, int U, int Fdim,
                                                           int k, const uint8_t* __restrict__ xq, int64_t xq_rb,
-                                                          MoeLists lists, float* __restrict__ act) {
+                                                          MoeLists lists, float* __restrict__ act, int ppw,
+                                                          int wg_per_expert, int chunk) {
   using Ut = Unit<F>;
   constexpr int G = kWave / LPR;
-  constexpr int P = G / 2;  // (gate, up) row pairs per wave
+  constexpr int P = G / 2;  // (gate, up) row pairs per wave pass
   static_assert(P >= 1, "gate/up pairing needs two lane groups per wave");
-  const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-  const int waves_per_expert = (Fdim + P - 1) / P;
-  const int slot = int(wave / waves_per_expert);
-  if (slot >= *lists.n_active) return;
+  extern __shared__ uint32_t s_x[];
+  const int slot = int(blockIdx.x) / wg_per_expert, part = int(blockIdx.x) % wg_per_expert;
+  if (slot >= *lists.n_active) return;  // uniform over the workgroup
   const int e = lists.active[slot];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane / LPR, c = lane % LPR;
-  const int f = int(wave % waves_per_expert) * P + g / 2;
   const bool is_up = g & 1;
-  const bool row_ok = f < Fdim;
-  const uint8_t* row = (is_up ? up : gate) + (int64_t(e) * Fdim + (row_ok ? f : 0)) * rb;
-  typename Ut::W wt[UPL];
+  const int i0 = lists.offset[e], cnt = lists.offset[e + 1] - i0;
+  const int f0 = (part * 4 + wv) * ppw * P + g / 2;  // this lane group's first row pair
+  auto load_pair = [&](int it, typename Ut::W (&wt)[UPL]) {
+    const int f = min(f0 + it * P, Fdim - 1);
+    const uint8_t* row = (is_up ? up : gate) + (int64_t(e) * Fdim + f) * rb;
 #pragma unroll
-  for (int t = 0; t < UPL; t++) {
-    const int u = c + LPR * t;
-    if (row_ok && u < U) Ut::load_w(wt[t], row, u);
-  }
-  const int i0 = lists.offset[e], i1 = lists.offset[e + 1];
-  for (int i = i0; i < i1; i++) {
-    const int tok = lists.entry[i] / k;
-    const uint8_t* xt = xq + int64_t(tok) * xq_rb;
-    float acc = 0.f;
+    for (int t = 0; t < UPL; t++) Ut::load_w(wt[t], row, min(c + LPR * t, U - 1));
+  };
+  __shared__ int s_rows[kMoeTokChunk];
+  typename Ut::W cur[UPL], nxt[UPL];
+  load_pair(0, cur);  // in flight while the activations are staged
+  for (int base = 0; base < cnt; base += chunk) {
+    const int nch = min(chunk, cnt - base);
+    if (base > 0) load_pair(0, cur);
+    __syncthreads();  // the previous pass's readers are done
+    if (int(threadIdx.x) < nch) s_rows[threadIdx.x] = lists.entry[i0 + base + threadIdx.x] / k;
+    __syncthreads();
+    stage_rows(s_x, xq, xq_rb, nch, s_rows);
+    for (int it = 0; it < ppw; it++) {
+      load_pair(min(it + 1, ppw - 1), nxt);
+      const int f = f0 + it * P;
+      const bool row_ok = f < Fdim;
+      for (int j = 0; j < nch; j++) {
+        const uint8_t* xt = reinterpret_cast<const uint8_t*>(s_x) + int64_t(j) * xq_rb;
+        float accv = 0.f;
 #pragma unroll
-    for (int t = 0; t < UPL; t++) {
-      const int u = c + LPR * t;
-      if (row_ok && u < U) {
-        typename Ut::Act a;
-        Ut::load_act(a, xt, u);
-        acc += Ut::dot(wt[t], a, nullptr);
+        for (int t = 0; t < UPL; t++) {
+          const int u = c + LPR * t;
+          if (u < U) {
+            typename Ut::Act a;
+            Ut::load_act(a, xt, u);
+            accv += Ut::dot(cur[t], a, nullptr);
+          }
+        }
+        accv = group_sum_last<LPR>(accv);
+        const float gv = __shfl(accv, lane - LPR, kWave);  // gate total, from the group below
+        if (is_up && c == LPR - 1 && row_ok) {
+          const float silu = gv / (1.0f + expf(-gv));
+          act[int64_t(i0 + base + j) * Fdim + f] = silu * accv;
+        }
       }
-    }
-    acc = group_sum_last<LPR>(acc);
-    const float gv = __shfl(acc, lane - LPR, kWave);  // gate total, from the group below
-    if (is_up && c == LPR - 1 && row_ok) {
-      const float silu = gv / (1.0f + expf(-gv));
-      act[int64_t(i) * Fdim + f] = silu * acc;
+#pragma unroll
+      for (int t = 0; t < UPL; t++) cur[t] = nxt[t];
     }
   }
 }
 
-// down: one lane group per row h of the expert's down matrix, over the expert's entries.
+// down: a workgroup takes one active expert and 4 * rpw * G rows h of its down matrix (one lane
+// group per row); the expert's act rows (contiguous, entries i0 .. i1) are staged in LDS.
 template <int F, int LPR, int UPL>
 __global__ void __launch_bounds__(256) moe_down_kernel(const uint8_t* __restrict__ down, int64_t rb, int U, int H,
                                                        const uint8_t* __restrict__ aq, int64_t aq_rb, MoeLists lists,
-                                                       float* __restrict__ yd) {
+                                                       float* __restrict__ yd, int rpw, int wg_per_expert,
+                                                       int chunk) {
   using Ut = Unit<F>;
   constexpr int G = kWave / LPR;
-  const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-  const int waves_per_expert = (H + G - 1) / G;
-  const int slot = int(wave / waves_per_expert);
+  extern __shared__ uint32_t s_x[];
+  const int slot = int(blockIdx.x) / wg_per_expert, part = int(blockIdx.x) % wg_per_expert;
   if (slot >= *lists.n_active) return;
   const int e = lists.active[slot];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane / LPR, c = lane % LPR;
-  const int h = int(wave % waves_per_expert) * G + g;
-  const bool row_ok = h < H;
-  const uint8_t* row = down + (int64_t(e) * H + (row_ok ? h : 0)) * rb;
-  typename Ut::W wt[UPL];
+  const int i0 = lists.offset[e], cnt = lists.offset[e + 1] - i0;
+  const int h0 = (part * 4 + wv) * rpw * G + g;
+  auto load_row = [&](int it, typename Ut::W (&wt)[UPL]) {
+    const int h = min(h0 + it * G, H - 1);
+    const uint8_t* row = down + (int64_t(e) * H + h) * rb;
 #pragma unroll
-  for (int t = 0; t < UPL; t++) {
-    const int u = c + LPR * t;
-    if (row_ok && u < U) Ut::load_w(wt[t], row, u);
-  }
-  const int i0 = lists.offset[e], i1 = lists.offset[e + 1];
-  for (int i = i0; i < i1; i++) {
-    const uint8_t* at = aq + int64_t(i) * aq_rb;
-    float acc = 0.f;
+    for (int t = 0; t < UPL; t++) Ut::load_w(wt[t], row, min(c + LPR * t, U - 1));
+  };
+  __shared__ int s_rows[kMoeTokChunk];
+  typename Ut::W cur[UPL], nxt[UPL];
+  load_row(0, cur);  // in flight while the activations are staged
+  for (int base = 0; base < cnt; base += chunk) {
+    const int nch = min(chunk, cnt - base);
+    if (base > 0) load_row(0, cur);
+    __syncthreads();
+    if (int(threadIdx.x) < nch) s_rows[threadIdx.x] = i0 + base + threadIdx.x;
+    __syncthreads();
+    stage_rows(s_x, aq, aq_rb, nch, s_rows);
+    for (int it = 0; it < rpw; it++) {
+      load_row(min(it + 1, rpw - 1), nxt);
+      const int h = h0 + it * G;
+      for (int j = 0; j < nch; j++) {
+        const uint8_t* at = reinterpret_cast<const uint8_t*>(s_x) + int64_t(j) * aq_rb;
+        float accv = 0.f;
 #pragma unroll
-    for (int t = 0; t < UPL; t++) {
-      const int u = c + LPR * t;
-      if (row_ok && u < U) {
-        typename Ut::Act a;
-        Ut::load_act(a, at, u);
-        acc += Ut::dot(wt[t], a, nullptr);
+        for (int t = 0; t < UPL; t++) {
+          const int u = c + LPR * t;
+          if (u < U) {
+            typename Ut::Act a;
+            Ut::load_act(a, at, u);
+            accv += Ut::dot(cur[t], a, nullptr);
+          }
+        }
+        accv = group_sum_last<LPR>(accv);
+        if (c == LPR - 1 && h < H) yd[int64_t(i0 + base + j) * H + h] = accv;
       }
+#pragma unroll
+      for (int t = 0; t < UPL; t++) cur[t] = nxt[t];
     }
-    acc = group_sum_last<LPR>(acc);
-    if (c == LPR - 1 && row_ok) yd[int64_t(i) * H + h] = acc;
   }
 }
 
@@ -250,14 +354,20 @@ namespace {
 
 int lpr_for(int U) { return U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4; }
 
+// Work per wave: enough row pairs that the grid is about 4096 waves (at least one pair, at most 16).
 template <int F, int LPR, int UPL>
 void gate_up_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
   constexpr int P = (kWave / LPR) / 2;
   const int U = units_per_row(F, a.hidden);
-  int64_t waves = int64_t(a.max_active) * ((a.ffn + P - 1) / P);
-  hipLaunchKernelGGL((moe_gate_up_kernel<F, LPR, UPL>), dim3(unsigned((waves + 3) / 4)), dim3(256), 0, s,
-                     static_cast<const uint8_t*>(a.gate), static_cast<const uint8_t*>(a.up),
-                     row_bytes(F, a.hidden), U, int(a.ffn), a.top_k, a.xq, row_bytes(JERO_Q8_K, a.hidden), L, a.act);
+  const int64_t pairs = int64_t(a.max_active) * a.ffn;
+  const int ppw = int(std::min<int64_t>(16, std::max<int64_t>(1, pairs / (int64_t(P) * 4096))));
+  const int wg_per_expert = int((a.ffn + 4 * P * ppw - 1) / (4 * P * ppw));
+  const int64_t xrb = row_bytes(JERO_Q8_K, a.hidden);
+  const int chunk = int(std::max<int64_t>(1, std::min<int64_t>(kMoeTokChunk, kMoeStageBytes / xrb)));
+  hipLaunchKernelGGL((moe_gate_up_kernel<F, LPR, UPL>), dim3(unsigned(int64_t(a.max_active) * wg_per_expert)),
+                     dim3(256), size_t(chunk) * size_t(xrb), s, static_cast<const uint8_t*>(a.gate),
+                     static_cast<const uint8_t*>(a.up), row_bytes(F, a.hidden), U, int(a.ffn), a.top_k, a.xq, xrb, L,
+                     a.act, ppw, wg_per_expert, chunk);
 }
 
 template <int F>
@@ -277,10 +387,14 @@ template <int F, int LPR, int UPL>
 void down_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
   constexpr int G = kWave / LPR;
   const int U = units_per_row(F, a.ffn);
-  int64_t waves = int64_t(a.max_active) * ((a.hidden + G - 1) / G);
-  hipLaunchKernelGGL((moe_down_kernel<F, LPR, UPL>), dim3(unsigned((waves + 3) / 4)), dim3(256), 0, s,
-                     static_cast<const uint8_t*>(a.down), row_bytes(F, a.ffn), U, int(a.hidden), a.aq,
-                     row_bytes(JERO_Q8_K, a.ffn), L, a.yd);
+  const int64_t rows = int64_t(a.max_active) * a.hidden;
+  const int rpw = int(std::min<int64_t>(16, std::max<int64_t>(1, rows / (int64_t(G) * 4096))));
+  const int wg_per_expert = int((a.hidden + 4 * G * rpw - 1) / (4 * G * rpw));
+  const int64_t arb = row_bytes(JERO_Q8_K, a.ffn);
+  const int chunk = int(std::max<int64_t>(1, std::min<int64_t>(kMoeTokChunk, kMoeStageBytes / arb)));
+  hipLaunchKernelGGL((moe_down_kernel<F, LPR, UPL>), dim3(unsigned(int64_t(a.max_active) * wg_per_expert)),
+                     dim3(256), size_t(chunk) * size_t(arb), s, static_cast<const uint8_t*>(a.down), row_bytes(F, a.ffn),
+                     U, int(a.hidden), a.aq, arb, L, a.yd, rpw, wg_per_expert, chunk);
 }
 
 template <int F>

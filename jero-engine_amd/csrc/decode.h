@@ -28,11 +28,18 @@ struct DGemvArgs {
   float* amax_v;      // argmax partials per workgroup
   int64_t* amax_i;
   int max_blocks;     // 0: grid capped at kDecodeBlocksPerCU workgroups per CU
+  // second tensor of a two-tensor launch (launch_dgemv_dual)
+  const uint8_t* w2;
+  int64_t rb2;
+  int64_t N2;
 };
 
 // Enqueues the fused GEMV; *blocks (if given) receives the workgroups launched, which is the
 // number of argmax partials an argmax launch leaves in amax_v / amax_i.
 int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s, int* blocks = nullptr);
+// rmsnorm(x) . [W1; W2] into y[0, N + N2) for two K-quant tensors of different formats sharing
+// n_in = K <= 4096 (Q4_K with Q6_K_R, either order): one launch, one prologue.
+int launch_dgemv_dual(int quant1, int quant2, const DGemvArgs& a, hipStream_t s);
 // Longest row the fused decode GEMV takes for a weight format.
 int dgemv_max_k(int quant);
 // hidden = embedding row of *token; also the step's RoPE table rope_cs[hd/2][cos, sin].

@@ -335,6 +335,99 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- two tensors, one launch
+
+// Rows of one store segment for this wave: rows r_begin, r_begin + stride, ... below N of a
+// K-quant tensor, one row per wave (64 lanes), dotted with the activation blocks in LDS.  `cur`
+// holds the first row's weights, already loaded.
+template <int F, int UPL>
+__device__ __forceinline__ void store_segment(const uint8_t* __restrict__ w, int64_t rb, int U, int64_t N,
+                                              int64_t r_begin, int64_t stride, const uint8_t* s_act, float* y,
+                                              typename Unit<F>::W (&cur)[UPL]) {
+  using Ut = Unit<F>;
+  const int c = threadIdx.x & 63;
+  auto load_row = [&](int64_t r, typename Ut::W (&wt)[UPL]) {
+#pragma unroll
+    for (int t = 0; t < UPL; t++) {
+      const int u = c + 64 * t;
+      if (r < N && u < U) {
+        if constexpr (F == JERO_Q6_K_R)
+          Ut::load_w_planar(wt[t], w, N, U, r, u);
+        else
+          Ut::load_w(wt[t], w + r * rb, u);
+      }
+    }
+  };
+  typename Ut::Act act[UPL];
+#pragma unroll
+  for (int t = 0; t < UPL; t++) {
+    const int u = c + 64 * t;
+    if (u < U) Ut::load_act(act[t], s_act, u);
+  }
+  typename Ut::W nxt[UPL];
+  for (int64_t r = r_begin; r < N; r += stride) {
+    load_row(r + stride, nxt);
+    float acc = 0.f;
+#pragma unroll
+    for (int t = 0; t < UPL; t++) {
+      const int u = c + 64 * t;
+      if (u < U) acc += Ut::dot(cur[t], act[t], nullptr);
+    }
+    acc = group_sum_last<64>(acc);
+    if (c == 63) y[r] = acc;
+#pragma unroll
+    for (int t = 0; t < UPL; t++) cur[t] = nxt[t];
+  }
+}
+
+// rmsnorm(x) . [W1; W2] for two K-quant tensors of different formats (the Q|K and V projections
+// of a layer whose attn_v is Q6_K): rows [0, N) of W1 then rows [0, N2) of W2 into y[0, N + N2).
+// One prologue (RMSNorm + Q8_K blocks in LDS) serves both; each wave runs its W1 rows, then its
+// W2 rows, in the order of one persistent row index over both tensors.
+template <int F1, int F2, int UPL, int XB>
+__global__ void __launch_bounds__(kDecodeThreads) dgemv_dual_kernel(DGemvArgs a) {
+  static_assert(F1 != JERO_Q8_0 && F1 != JERO_Q4_0 && F2 != JERO_Q8_0 && F2 != JERO_Q4_0, "K-quants only");
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_mem[];
+  float* s_tmp = reinterpret_cast<float*>(s_mem);
+  uint8_t* s_act = s_mem + 256;
+  const int c = threadIdx.x & 63;
+  const int64_t wave0 = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  const int64_t stride = int64_t(gridDim.x) * (blockDim.x / kWave);
+  const int64_t N1 = a.N, total = a.N + a.N2;
+  // first row index of the wave in each segment (the persistent index runs over N1 + N2 rows)
+  const int64_t r1 = wave0;
+  const int64_t r2 = (wave0 >= N1 ? wave0 : wave0 + ((N1 - wave0 + stride - 1) / stride) * stride) - N1;
+  XRegs<JERO_Q8_K, XB, true> X;
+  load_x<JERO_Q8_K, XB, true>(X, a.x, a.norm_w, a.K);
+  typename Unit<F1>::W c1[UPL];
+  typename Unit<F2>::W c2[UPL];
+#pragma unroll
+  for (int t = 0; t < UPL; t++) {
+    const int u = c + 64 * t;
+    if (r1 < N1 && u < a.U) {
+      if constexpr (F1 == JERO_Q6_K_R)
+        Unit<F1>::load_w_planar(c1[t], a.w, N1, a.U, r1, u);
+      else
+        Unit<F1>::load_w(c1[t], a.w + r1 * a.rb, u);
+    }
+  }
+  build_act_lds<JERO_Q8_K, XB, true>(X, a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp);
+  store_segment<F1, UPL>(a.w, a.rb, a.U, N1, r1, stride, s_act, a.y, c1);
+  if (r2 + N1 < total) {
+#pragma unroll
+    for (int t = 0; t < UPL; t++) {
+      const int u = c + 64 * t;
+      if (u < a.U) {
+        if constexpr (F2 == JERO_Q6_K_R)
+          Unit<F2>::load_w_planar(c2[t], a.w2, a.N2, a.U, r2, u);
+        else
+          Unit<F2>::load_w(c2[t], a.w2 + r2 * a.rb2, u);
+      }
+    }
+    store_segment<F2, UPL>(a.w2, a.rb2, a.U, a.N2, r2, stride, s_act, a.y + N1, c2);
+  }
+}
+
 // ---------------------------------------------------------------- small kernels
 
 // hidden = dequantize_token_row(token_embd, *token) (embed_token, src/qwen_deepseek.rs:558-582)
@@ -509,6 +602,31 @@ int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s, int
   if (rc < 0) return -rc;
   if (blocks) *blocks = rc;
   return check_launch("decode gemv");
+}
+
+int launch_dgemv_dual(int quant1, int quant2, const DGemvArgs& a0, hipStream_t s) {
+  if (a0.U > 64 || a0.K % 256 != 0)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: two-tensor GEMV takes rows of at most 4096 K-quant elements");
+  DGemvArgs a = a0;
+  const int64_t wpb = kDecodeThreads / kWave;
+  int64_t blocks = (a.N + a.N2 + wpb - 1) / wpb;
+  const int64_t cap = int64_t(device_info().cus) * kDecodeBlocksPerCU;
+  if (blocks > cap) blocks = cap;
+  const size_t shm = (256 + size_t(row_bytes(JERO_Q8_K, a.K)) + 15) & ~size_t(15);
+  const int xb = xb_for(JERO_Q4_K, a.K);
+#define JERO_DUAL(Q1, Q2, XBV)                                                                            \
+  hipLaunchKernelGGL((dgemv_dual_kernel<Q1, Q2, 1, XBV>), dim3(unsigned(blocks)), dim3(kDecodeThreads), shm, s, a)
+  if (quant1 == JERO_Q4_K && quant2 == JERO_Q6_K_R) {
+    if (xb <= 1) JERO_DUAL(JERO_Q4_K, JERO_Q6_K_R, 1);
+    else JERO_DUAL(JERO_Q4_K, JERO_Q6_K_R, 2);
+  } else if (quant1 == JERO_Q6_K_R && quant2 == JERO_Q4_K) {
+    if (xb <= 1) JERO_DUAL(JERO_Q6_K_R, JERO_Q4_K, 1);
+    else JERO_DUAL(JERO_Q6_K_R, JERO_Q4_K, 2);
+  } else {
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: no two-tensor GEMV for this format pair");
+  }
+#undef JERO_DUAL
+  return check_launch("decode two-tensor gemv");
 }
 
 int dgemv_max_k(int quant) {

@@ -396,12 +396,33 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
   for (int64_t L = 0; L < c.n_layers; L++) {
     const LayerW& l = m->layers[size_t(L)];
     // attention sublayer: RMSNorm -> Q|K|V
-    rc = gemv(m, l.qkv, m->hidden, static_cast<const float*>(l.attn_norm.dev), eps_attn, kOutStore, m->qkv, 0, s);
-    if (rc) return rc;
-    if (l.v_separate) {
-      rc = gemv(m, l.wv, m->hidden, static_cast<const float*>(l.attn_norm.dev), eps_attn, kOutStore,
-                m->qkv + Q + KV, 0, s);
+    const bool dual = l.v_separate && l.qkv.n_in <= 4096 &&
+                      ((l.qkv.quant == JERO_Q4_K && l.wv.quant == JERO_Q6_K_R) ||
+                       (l.qkv.quant == JERO_Q6_K_R && l.wv.quant == JERO_Q4_K));
+    if (dual) {  // Q|K and V of different formats in one launch
+      DGemvArgs a{};
+      a.w = static_cast<const uint8_t*>(l.qkv.dev);
+      a.rb = row_bytes(l.qkv.quant, l.qkv.n_in);
+      a.U = int(l.qkv.n_in / 64);
+      a.N = l.qkv.n_out;
+      a.w2 = static_cast<const uint8_t*>(l.wv.dev);
+      a.rb2 = row_bytes(l.wv.quant, l.wv.n_in);
+      a.N2 = l.wv.n_out;
+      a.x = m->hidden;
+      a.norm_w = static_cast<const float*>(l.attn_norm.dev);
+      a.eps = eps_attn;
+      a.K = int(l.qkv.n_in);
+      a.y = m->qkv;
+      rc = launch_dgemv_dual(l.qkv.quant, l.wv.quant, a, s);
       if (rc) return rc;
+    } else {
+      rc = gemv(m, l.qkv, m->hidden, static_cast<const float*>(l.attn_norm.dev), eps_attn, kOutStore, m->qkv, 0, s);
+      if (rc) return rc;
+      if (l.v_separate) {
+        rc = gemv(m, l.wv, m->hidden, static_cast<const float*>(l.attn_norm.dev), eps_attn, kOutStore,
+                  m->qkv + Q + KV, 0, s);
+        if (rc) return rc;
+      }
     }
     // QK-norm, RoPE, KV append, attention over the ring
     AttnParams p{};

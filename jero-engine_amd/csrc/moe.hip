@@ -35,11 +35,12 @@ constexpr int kRouteLdsPairs = 8192;  // (token, slot) pairs grouped from LDS
 
 __device__ __forceinline__ bool better(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
 
+// PER = expert columns per lane (E <= 64 * PER).
+template <int PER>
 __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits, int T, int E,
                                                                   int k, int32_t* __restrict__ sel_idx,
                                                                   float* __restrict__ sel_w, MoeLists lists) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = kRouteThreads / 64;
-  constexpr int PER = kMaxExperts / 64;
   __shared__ int s_count[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
   __shared__ int s_wsum[2 * (kRouteThreads / 64)];
@@ -453,8 +454,17 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
 
   int rc = launch_quantize_act(JERO_Q8_K, a.x, a.T, a.hidden, a.xq, s);
   if (rc) return rc;
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), 0, s, a.logits, int(a.T), int(a.E), a.top_k,
-                     a.sel_idx, a.sel_w, L);
+  {
+    const int per = a.E <= 128 ? 2 : a.E <= 256 ? 4 : a.E <= 512 ? 8 : 16;
+#define JERO_ROUTE(P)                                                                                         \
+  hipLaunchKernelGGL(moe_route_kernel<P>, dim3(1), dim3(kRouteThreads), 0, s, a.logits, int(a.T), int(a.E), \
+                     a.top_k, a.sel_idx, a.sel_w, L)
+    if (per == 2) JERO_ROUTE(2);
+    else if (per == 4) JERO_ROUTE(4);
+    else if (per == 8) JERO_ROUTE(8);
+    else JERO_ROUTE(16);
+#undef JERO_ROUTE
+  }
   rc = check_launch("moe route");
   if (rc) return rc;
   rc = a.gate_quant == JERO_Q4_K ? gate_up_fmt<JERO_Q4_K>(a, L, s) : gate_up_fmt<JERO_Q6_K>(a, L, s);

@@ -51,6 +51,13 @@ def test_moe_small_and_q4k_down(dev):
     run_case(dev, 3, 16, 512, 256, 4, J.Q6_K, J.Q6_K, 41)
 
 
+@pytest.mark.parametrize("E,K", [(200, 6), (300, 8), (700, 16)])
+def test_moe_many_experts(dev, E, K):
+    """Router widths above 128 experts (4, 8 and 16 expert columns per lane), top-k up to 16."""
+    print(f"moe E={E} k={K}", flush=True)
+    run_case(dev, 3, E, 256, 256, K, J.Q4_K, J.Q6_K, 70 + E)
+
+
 def test_moe_routing_ties_and_nonfinite(dev):
     """Ties pick the lower expert id; NaN/inf logits rank last with zero probability."""
     print("moe ties", flush=True)

@@ -36,47 +36,6 @@ __device__ __forceinline__ float block_sum(float v, float* s_tmp) {
   return t;
 }
 
-// Q8_K block of 256 elements from one wave (4 elements per lane) into LDS (ggml rule, as the
-// standalone quantizer).
-__device__ __forceinline__ void q8k_block_lds(const float e[4], int lane, uint8_t* ob) {
-  float am = 0.0f;
-#pragma unroll
-  for (int t = 0; t < 4; t++) am = fmaxf(am, fabsf(e[t]));
-  am = wave_max_dpp(am);  // uniform block max |x|
-  if (am == 0.0f) {
-    reinterpret_cast<uint32_t*>(ob + 4)[lane] = 0u;
-    if (lane < 16) reinterpret_cast<int16_t*>(ob + 260)[lane] = 0;
-    if (lane == 0) *reinterpret_cast<float*>(ob) = 0.0f;
-    return;
-  }
-  // the first element (lowest index) with |x| == max sets the sign: lowest lane, lowest t
-  int mine = 4;
-#pragma unroll
-  for (int t = 3; t >= 0; t--)
-    if (fabsf(e[t]) == am) mine = t;
-  const uint64_t hit = __ballot(mine < 4);
-  const int src = __builtin_ctzll(hit);
-  const int t_src = __builtin_amdgcn_readlane(mine, src);
-  const float mxv = __builtin_bit_cast(
-      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t_src == 0 ? e[0] : t_src == 1 ? e[1]
-                                                               : t_src == 2 ? e[2] : e[3]),
-                                       src));
-  float iscale = -127.0f / mxv;
-  int s = 0;
-  uint32_t packed = 0;
-#pragma unroll
-  for (int t = 0; t < 4; t++) {
-    int qv = int(__builtin_rintf(iscale * e[t]));
-    qv = qv < 127 ? qv : 127;
-    s += qv;
-    packed |= (uint32_t(qv) & 0xFFu) << (8 * t);
-  }
-  reinterpret_cast<uint32_t*>(ob + 4)[lane] = packed;
-  s = int(group_sum_all<4>(float(s)));  // |s| <= 508: exact in f32
-  if ((lane & 3) == 0) reinterpret_cast<int16_t*>(ob + 260)[lane >> 2] = int16_t(s);
-  if (lane == 0) *reinterpret_cast<float*>(ob) = 1.0f / iscale;
-}
-
 // The workgroup's share of the f32 input, loaded before the weight rows so that the prologue
 // only waits for these loads.  Q8_K: wave w takes blocks w, w+nw, ... (4 elements per lane,
 // the quantizer's layout); ACT_Q8: half-wave h takes 32-element blocks h, h+2nw, ...
@@ -145,7 +104,7 @@ __device__ void build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps,
             e[3] = e[3] * scale * X.g[i].w;
           }
         }
-        q8k_block_lds(e, lane, s_act + b * 292);
+        q8k_block_wave(e, lane, s_act + b * 292);
       }
     } else {
       const int b = 2 * wv + (lane >> 5) + 2 * nwv * i;

@@ -185,6 +185,49 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Q8_K block of 256 elements from one wave, four consecutive elements per lane, written to `ob`
+// (LDS or global memory, 4-byte aligned).  ggml's rule: the first element (lowest index) of
+// largest magnitude is `max`; iscale = -127 / max, q = min(127, rint(iscale * x)), d = 1 / iscale,
+// bsums over 16-element groups; an all-zero block stores zeros.
+__device__ __forceinline__ void q8k_block_wave(const float e[4], int lane, uint8_t* ob) {
+  float am = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 4; t++) am = fmaxf(am, fabsf(e[t]));
+  am = wave_max_dpp(am);  // uniform block max |x|
+  if (am == 0.0f) {
+    reinterpret_cast<uint32_t*>(ob + 4)[lane] = 0u;
+    if (lane < 16) reinterpret_cast<int16_t*>(ob + 260)[lane] = 0;
+    if (lane == 0) *reinterpret_cast<float*>(ob) = 0.0f;
+    return;
+  }
+  // the first element (lowest index) with |x| == max sets the sign: lowest lane, lowest t
+  int mine = 4;
+#pragma unroll
+  for (int t = 3; t >= 0; t--)
+    if (fabsf(e[t]) == am) mine = t;
+  const uint64_t hit = __ballot(mine < 4);
+  const int src = __builtin_ctzll(hit);
+  const int t_src = __builtin_amdgcn_readlane(mine, src);
+  const float mxv = __builtin_bit_cast(
+      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t_src == 0 ? e[0] : t_src == 1 ? e[1]
+                                                               : t_src == 2 ? e[2] : e[3]),
+                                       src));
+  float iscale = -127.0f / mxv;
+  int s = 0;
+  uint32_t packed = 0;
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    int qv = int(__builtin_rintf(iscale * e[t]));
+    qv = qv < 127 ? qv : 127;
+    s += qv;
+    packed |= (uint32_t(qv) & 0xFFu) << (8 * t);
+  }
+  reinterpret_cast<uint32_t*>(ob + 4)[lane] = packed;
+  s = int(group_sum_all<4>(float(s)));  // |s| <= 508: exact in f32
+  if ((lane & 3) == 0) reinterpret_cast<int16_t*>(ob + 260)[lane >> 2] = int16_t(s);
+  if (lane == 0) *reinterpret_cast<float*>(ob) = 1.0f / iscale;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));

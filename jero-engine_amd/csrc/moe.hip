@@ -39,12 +39,25 @@ __device__ __forceinline__ bool better(float a, int ia, float b, int ib) { retur
 template <int PER>
 __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits, int T, int E,
                                                                   int k, int32_t* __restrict__ sel_idx,
-                                                                  float* __restrict__ sel_w, MoeLists lists) {
+                                                                  float* __restrict__ sel_w, MoeLists lists,
+                                                                  const float* __restrict__ x, int H,
+                                                                  uint8_t* __restrict__ xq) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = kRouteThreads / 64;
   __shared__ int s_count[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
   __shared__ int s_wsum[2 * (kRouteThreads / 64)];
   __shared__ __attribute__((aligned(16))) int s_sel[kRouteLdsPairs + 4];  // the selections, when they fit
+  // 0. the T hidden vectors to Q8_K (the gate/up input), one wave per 256-element block, when the
+  //    launcher passes xq (a few blocks; many tokens go through the parallel quantizer instead)
+  if (xq) {
+    const int bpr = H / 256, nblk = T * bpr;
+    for (int blk = wv; blk < nblk; blk += nw) {
+      const int t = blk / bpr, j = blk - t * bpr;
+      const float4 v = reinterpret_cast<const float4*>(x + int64_t(t) * H + int64_t(j) * 256)[lane];
+      const float e[4] = {v.x, v.y, v.z, v.w};
+      q8k_block_wave(e, lane, xq + int64_t(t) * bpr * 292 + int64_t(j) * 292);
+    }
+  }
   // 1. routing, one wave per token
   for (int t = wv; t < T; t += nw) {
     const float* lt = logits + int64_t(t) * E;
@@ -452,13 +465,18 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   a.yd = reinterpret_cast<float*>(take(sizeof(float) * size_t(n) * size_t(a.hidden)));
   a.max_active = int(n < a.E ? n : a.E);
 
-  int rc = launch_quantize_act(JERO_Q8_K, a.x, a.T, a.hidden, a.xq, s);
-  if (rc) return rc;
+  // a few tokens are quantized inside the routing workgroup (one launch less); many in parallel
+  const bool quant_in_route = a.T * (a.hidden / 256) <= 2 * (kRouteThreads / kWave);
+  int rc;
+  if (!quant_in_route) {
+    rc = launch_quantize_act(JERO_Q8_K, a.x, a.T, a.hidden, a.xq, s);
+    if (rc) return rc;
+  }
   {
     const int per = a.E <= 128 ? 2 : a.E <= 256 ? 4 : a.E <= 512 ? 8 : 16;
 #define JERO_ROUTE(P)                                                                                         \
   hipLaunchKernelGGL(moe_route_kernel<P>, dim3(1), dim3(kRouteThreads), 0, s, a.logits, int(a.T), int(a.E), \
-                     a.top_k, a.sel_idx, a.sel_w, L)
+                     a.top_k, a.sel_idx, a.sel_w, L, a.x, int(a.hidden), quant_in_route ? a.xq : nullptr)
     if (per == 2) JERO_ROUTE(2);
     else if (per == 4) JERO_ROUTE(4);
     else if (per == 8) JERO_ROUTE(8);

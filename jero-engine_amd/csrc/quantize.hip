@@ -36,61 +36,14 @@ __global__ void __launch_bounds__(256) quant_act_q8_kernel(const float* __restri
   if (l == 0) *reinterpret_cast<float*>(ob) = d;
 }
 
-// One wave per 256-element block, four consecutive elements per lane.
-__device__ __forceinline__ void quant_q8k_block(const float4 v, int lane, const float* __restrict__ xb,
-                                                uint8_t* __restrict__ ob) {
-  float e[4] = {v.x, v.y, v.z, v.w};
-  float am = 0.0f;
-  int ai = 0x7fffffff;
-#pragma unroll
-  for (int t = 0; t < 4; t++) {
-    float a = fabsf(e[t]);
-    if (a > am) {
-      am = a;
-      ai = 4 * lane + t;
-    }
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    float oa = __shfl_xor(am, off, kWave);
-    int oi = __shfl_xor(ai, off, kWave);
-    if (oa > am || (oa == am && oi < ai)) {
-      am = oa;
-      ai = oi;
-    }
-  }
-  if (am == 0.0f) {
-    reinterpret_cast<uint32_t*>(ob + 4)[lane] = 0u;
-    if (lane < 16) reinterpret_cast<int16_t*>(ob + 260)[lane] = 0;
-    if (lane == 0) *reinterpret_cast<float*>(ob) = 0.0f;
-    return;
-  }
-  float mx = xb[ai];
-  float iscale = -127.0f / mx;
-  int s = 0;
-  uint32_t packed = 0;
-#pragma unroll
-  for (int t = 0; t < 4; t++) {
-    int qv = int(__builtin_rintf(iscale * e[t]));
-    qv = qv < 127 ? qv : 127;
-    s += qv;
-    packed |= (uint32_t(qv) & 0xFFu) << (8 * t);
-  }
-  reinterpret_cast<uint32_t*>(ob + 4)[lane] = packed;
-  s += __shfl_xor(s, 1, kWave);
-  s += __shfl_xor(s, 2, kWave);
-  if ((lane & 3) == 0) reinterpret_cast<int16_t*>(ob + 260)[lane >> 2] = int16_t(s);
-  if (lane == 0) *reinterpret_cast<float*>(ob) = 1.0f / iscale;
-}
-
 __global__ void __launch_bounds__(256) quant_q8k_kernel(const float* __restrict__ x, int64_t nblocks,
                                                         uint8_t* __restrict__ q) {
   int64_t blk = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
   int lane = threadIdx.x & 63;
   if (blk >= nblocks) return;
-  const float* xb = x + blk * 256;
-  float4 v = reinterpret_cast<const float4*>(xb)[lane];
-  quant_q8k_block(v, lane, xb, q + blk * 292);
+  const float4 v = reinterpret_cast<const float4*>(x + blk * 256)[lane];
+  const float e[4] = {v.x, v.y, v.z, v.w};
+  q8k_block_wave(e, lane, q + blk * 292);
 }
 
 int launch_quantize_act(int act_quant, const float* x, int64_t m, int64_t k, void* q, hipStream_t stream) {

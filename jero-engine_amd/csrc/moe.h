@@ -32,7 +32,6 @@ struct MoeArgs {
   // workspace carve-out (set by launch_moe)
   uint8_t* xq;
   float* act;
-  const uint8_t* aq;
   float* yd;
   int max_active;
 };

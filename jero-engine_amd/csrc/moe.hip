@@ -225,6 +225,33 @@ __device__ __forceinline__ void stage_rows(uint32_t* __restrict__ dst, const uin
   __syncthreads();
 }
 
+// Quantizes n consecutive f32 rows (src rows row0 .. row0 + n, `cols` floats each) to Q8_K rows of
+// `qrb` bytes in LDS, one wave per 256-element block; each wave loads four blocks before
+// quantizing them.  Ends with a barrier.
+__device__ __forceinline__ void stage_quant_rows(uint8_t* __restrict__ dst, const float* __restrict__ src, int cols,
+                                                 int64_t qrb, int n, int row0) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = int(blockDim.x) >> 6;
+  const int bpr = cols / 256, total = n * bpr;
+  for (int b0 = wv; b0 < total; b0 += 4 * nw) {
+    float4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int b = min(b0 + q * nw, total - 1), j = b / bpr, jb = b - j * bpr;
+      v[q] = reinterpret_cast<const float4*>(src + int64_t(row0 + j) * cols + int64_t(jb) * 256)[lane];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int b = b0 + q * nw;  // uniform over the wave
+      if (b < total) {
+        const int j = b / bpr, jb = b - j * bpr;
+        const float e[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+        q8k_block_wave(e, lane, dst + int64_t(j) * qrb + int64_t(jb) * 292);
+      }
+    }
+  }
+  __syncthreads();
+}
+
 // gate/up + SwiGLU.  A workgroup takes one active expert and 4 * ppw * P of its (gate, up) row
 // pairs: lane groups (2p, 2p+1) of a wave hold gate row and up row f.  The expert's token
 // activations are staged in LDS (kMoeTokChunk rows per pass), so each weight row is read from
@@ -295,10 +322,12 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(const uint8_t* __restr
 }
 
 // down: a workgroup takes one active expert and 4 * rpw * G rows h of its down matrix (one lane
-// group per row); the expert's act rows (contiguous, entries i0 .. i1) are staged in LDS.
+// group per row); the expert's act rows (contiguous, entries i0 .. i1, f32) are quantized to Q8_K
+// straight into LDS.
 template <int F, int LPR, int UPL>
 __global__ void __launch_bounds__(256) moe_down_kernel(const uint8_t* __restrict__ down, int64_t rb, int U, int H,
-                                                       const uint8_t* __restrict__ aq, int64_t aq_rb, MoeLists lists,
+                                                       const float* __restrict__ act, int ffn, int64_t aq_rb,
+                                                       MoeLists lists,
                                                        float* __restrict__ yd, int rpw, int wg_per_expert,
                                                        int chunk) {
   using Ut = Unit<F>;
@@ -317,16 +346,13 @@ __global__ void __launch_bounds__(256) moe_down_kernel(const uint8_t* __restrict
 #pragma unroll
     for (int t = 0; t < UPL; t++) Ut::load_w(wt[t], row, min(c + LPR * t, U - 1));
   };
-  __shared__ int s_rows[kMoeTokChunk];
   typename Ut::W cur[UPL], nxt[UPL];
   load_row(0, cur);  // in flight while the activations are staged
   for (int base = 0; base < cnt; base += chunk) {
     const int nch = min(chunk, cnt - base);
     if (base > 0) load_row(0, cur);
-    __syncthreads();
-    if (int(threadIdx.x) < nch) s_rows[threadIdx.x] = i0 + base + threadIdx.x;
-    __syncthreads();
-    stage_rows(s_x, aq, aq_rb, nch, s_rows);
+    __syncthreads();  // the previous pass's readers are done
+    stage_quant_rows(reinterpret_cast<uint8_t*>(s_x), act, ffn, aq_rb, nch, i0 + base);
     for (int it = 0; it < rpw; it++) {
       load_row(min(it + 1, rpw - 1), nxt);
       const int h = h0 + it * G;
@@ -408,7 +434,7 @@ void down_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
   const int chunk = int(std::max<int64_t>(1, std::min<int64_t>(kMoeTokChunk, kMoeStageBytes / arb)));
   hipLaunchKernelGGL((moe_down_kernel<F, LPR, UPL>), dim3(unsigned(int64_t(a.max_active) * wg_per_expert)),
                      dim3(256), size_t(chunk) * size_t(arb), s, static_cast<const uint8_t*>(a.down), row_bytes(F, a.ffn),
-                     U, int(a.hidden), a.aq, arb, L, a.yd, rpw, wg_per_expert, chunk);
+                     U, int(a.hidden), a.act, int(a.ffn), arb, L, a.yd, rpw, wg_per_expert, chunk);
 }
 
 template <int F>
@@ -439,7 +465,6 @@ size_t moe_workspace_bytes(int64_t T, int64_t E, int top_k, int64_t hidden, int6
   add(sizeof(int32_t));                                    // n_active
   add(sizeof(int32_t) * size_t(n) * 2);                    // entry, inv
   add(sizeof(float) * size_t(n) * size_t(ffn));            // act
-  add(size_t(n) * size_t(row_bytes(JERO_Q8_K, ffn)));      // act_q
   add(sizeof(float) * size_t(n) * size_t(hidden));         // per-slot down outputs
   return b;
 }
@@ -461,7 +486,6 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   L.entry = ei;
   L.inv = ei + n;
   a.act = reinterpret_cast<float*>(take(sizeof(float) * size_t(n) * size_t(a.ffn)));
-  a.aq = take(size_t(n) * size_t(row_bytes(JERO_Q8_K, a.ffn)));
   a.yd = reinterpret_cast<float*>(take(sizeof(float) * size_t(n) * size_t(a.hidden)));
   a.max_active = int(n < a.E ? n : a.E);
 
@@ -488,8 +512,6 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   rc = a.gate_quant == JERO_Q4_K ? gate_up_fmt<JERO_Q4_K>(a, L, s) : gate_up_fmt<JERO_Q6_K>(a, L, s);
   if (rc) return rc;
   rc = check_launch("moe gate/up");
-  if (rc) return rc;
-  rc = launch_quantize_act(JERO_Q8_K, a.act, n, a.ffn, const_cast<uint8_t*>(a.aq), s);
   if (rc) return rc;
   rc = a.down_quant == JERO_Q4_K ? down_fmt<JERO_Q4_K>(a, L, s) : down_fmt<JERO_Q6_K>(a, L, s);
   if (rc) return rc;

@@ -39,6 +39,9 @@ __device__ __forceinline__ float block_sum(float v, float* s_tmp) {
 // The workgroup's share of the f32 input, loaded before the weight rows so that the prologue
 // only waits for these loads.  Q8_K: wave w takes blocks w, w+nw, ... (4 elements per lane,
 // the quantizer's layout); ACT_Q8: half-wave h takes 32-element blocks h, h+2nw, ...
+// Every load here and in the weight loads that follow is unconditional (block index clamped,
+// a null norm pointer replaced by x): with a load under a branch the compiler cannot count
+// the loads issued after the input, and the prologue would wait for the weights as well.
 template <int ACT, int XB, bool NORM>
 struct XRegs {
   float4 v[XB];
@@ -49,25 +52,35 @@ template <int ACT, int XB, bool NORM>
 __device__ __forceinline__ void load_x(XRegs<ACT, XB, NORM>& X, const float* __restrict__ x, const float* __restrict__ nw,
                                        int K) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  const float* g = nw ? nw : x;
 #pragma unroll
   for (int i = 0; i < XB; i++) {
     if constexpr (ACT == JERO_Q8_K) {
-      const int b = wv + nwv * i;
-      if (b < K / 256) {
-        X.v[i] = reinterpret_cast<const float4*>(x + b * 256)[lane];
-        if constexpr (NORM) {
-          if (nw) X.g[i] = reinterpret_cast<const float4*>(nw + b * 256)[lane];
-        }
-      }
+      const int b = min(wv + nwv * i, K / 256 - 1);
+      X.v[i] = reinterpret_cast<const float4*>(x + b * 256)[lane];
+      if constexpr (NORM) X.g[i] = reinterpret_cast<const float4*>(g + b * 256)[lane];
     } else {
-      const int b = 2 * wv + (lane >> 5) + 2 * nwv * i;
-      if (b < K / 32) {
-        X.v[i].x = x[b * 32 + (lane & 31)];
-        if constexpr (NORM) {
-          if (nw) X.g[i].x = nw[b * 32 + (lane & 31)];
-        }
-      }
+      const int b = min(2 * wv + (lane >> 5) + 2 * nwv * i, K / 32 - 1);
+      X.v[i].x = x[b * 32 + (lane & 31)];
+      if constexpr (NORM) X.g[i].x = g[b * 32 + (lane & 31)];
     }
+  }
+}
+
+// Marks the input registers as used here.  Placed after the first weight loads: the compiler
+// then cannot sink an input load into the prologue's per-block branch (where it would wait for
+// every load in flight), and the wait for the input lands after the weight loads are issued.
+__device__ __forceinline__ void pin4(float4& v) {
+  float a = v.x, b = v.y, c = v.z, d = v.w;
+  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+  v = make_float4(a, b, c, d);
+}
+template <int ACT, int XB, bool NORM>
+__device__ __forceinline__ void pin_x(XRegs<ACT, XB, NORM>& X) {
+#pragma unroll
+  for (int i = 0; i < XB; i++) {
+    pin4(X.v[i]);
+    if constexpr (NORM) pin4(X.g[i]);
   }
 }
 
@@ -171,20 +184,24 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
       return row_of(rg, r) < N;
     }
   };
-  auto load_rows = [&](int64_t rg, typename Ut::W (&wt)[R][UPL]) {
+  // Unconditional loads: a row past the end reads row 0, a unit past the row end reads the
+  // row's last unit; neither reaches a result (row_valid and u < U mask them below).  The
+  // residual epilogue's read of y rides with the weights: issued after them, a load of y would
+  // make the wait for it a wait for everything issued before (loads complete in order).  Each
+  // row of y is read and then written by the one wave that owns it.
+  auto load_rows = [&](int64_t rg, typename Ut::W (&wt)[R][UPL], float (&yr)[R]) {
 #pragma unroll
     for (int r = 0; r < R; r++) {
       const bool ok = rg < n_groups && row_valid(rg, r);
       const int64_t row = ok ? row_of(rg, r) : 0;
+      if constexpr (OUT == kOutResid) yr[r] = a.y[row];
 #pragma unroll
       for (int t = 0; t < UPL; t++) {
-        const int u = c + LPR * t;
-        if (ok && u < U) {
-          if constexpr (F == JERO_Q6_K_R)
-            Ut::load_w_planar(wt[r][t], a.w, N, U, row, u);
-          else
-            Ut::load_w(wt[r][t], a.w + row * a.rb, u);
-        }
+        const int u = min(c + LPR * t, U - 1);
+        if constexpr (F == JERO_Q6_K_R)
+          Ut::load_w_planar(wt[r][t], a.w, N, U, row, u);
+        else
+          Ut::load_w(wt[r][t], a.w + row * a.rb, u);
       }
     }
   };
@@ -193,35 +210,33 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
   constexpr bool NORM = OUT != kOutResid;  // residual epilogues (Wo, down) take un-normalised input
   XRegs<ACT, XB, NORM> X;
   load_x<ACT, XB, NORM>(X, a.x, NORM ? a.norm_w : nullptr, a.K);
-  // The next row group's weights are prefetched (reloading in place instead, to fit two
-  // workgroups per CU on long rows, measured slower).
-  typename Ut::W cur[R][UPL], nxt[R][UPL];
-  load_rows(wave0, cur);
+  // The next row group's weights are prefetched into the other of two register buffers, so
+  // the wait before a group's math covers only that group's loads (reloading in place
+  // instead, to fit two workgroups per CU on long rows, measured slower).
+  typename Ut::W wa[R][UPL], wb[R][UPL];
+  float ya[R], yb[R];
+  load_rows(wave0, wa, ya);
+  pin_x(X);
   // 2. activation blocks in LDS (every thread takes part)
   build_act_lds<ACT, XB, NORM>(X, NORM && a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp);
   // The activation units stay in registers for all rows (re-reading them from LDS per row, to
   // fit two workgroups per CU on long rows, measured slower).
   typename Ut::Act act[UPL];
 #pragma unroll
-  for (int t = 0; t < UPL; t++) {
-    const int u = c + LPR * t;
-    if (u < U) Ut::load_act(act[t], s_act, u);
-  }
+  for (int t = 0; t < UPL; t++) Ut::load_act(act[t], s_act, min(c + LPR * t, U - 1));
   const bool last = c == LPR - 1;
   float best_v = -INFINITY;
   int64_t best_i = -1;
-  // 3. row groups: prefetch the next group, reduce the current one
-  for (int64_t rg = wave0; rg < n_groups; rg += stride) {
-    load_rows(rg + stride, nxt);
+  // 3. row groups: reduce one group while the next one's loads are in flight
+  auto process = [&](int64_t rg, const typename Ut::W (&cur)[R][UPL], const float (&yres)[R]) {
     float vals[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-      const bool ok = row_valid(rg, r);
       float acc = 0.f;
 #pragma unroll
       for (int t = 0; t < UPL; t++) {
-        const int u = c + LPR * t;
-        if (ok && u < U) acc += Ut::dot(cur[r][t], act[t], nullptr);
+        const float d = Ut::dot(cur[r][t], act[t], nullptr);
+        acc += (c + LPR * t < U) ? d : 0.f;
       }
       vals[r] = group_sum_last<LPR>(acc);
     }
@@ -244,7 +259,7 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
         const int64_t row = row_of(rg, r);
         if (last && row < N) {
           if constexpr (OUT == kOutResid) {
-            a.y[row] += vals[r];
+            a.y[row] = yres[r] + vals[r];
           } else {
             a.y[row] = vals[r];
             if constexpr (OUT == kOutArgmax) {
@@ -258,10 +273,16 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
         }
       }
     }
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-      for (int t = 0; t < UPL; t++) cur[r][t] = nxt[r][t];
+  };
+  // (sched_barrier: all of the next group's loads are issued before this group's math)
+  for (int64_t rg = wave0; rg < n_groups; rg += 2 * stride) {
+    load_rows(rg + stride, wb, yb);
+    __builtin_amdgcn_sched_barrier(0);
+    process(rg, wa, ya);
+    if (rg + stride >= n_groups) break;
+    load_rows(rg + 2 * stride, wa, ya);
+    __builtin_amdgcn_sched_barrier(0);
+    process(rg + stride, wb, yb);
   }
   if constexpr (OUT == kOutArgmax) {
     // (max, first index) over the workgroup's rows, NaN skipped
@@ -296,46 +317,55 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
 
 // ---------------------------------------------------------------- two tensors, one launch
 
+// Loads of row r of a K-quant tensor for one wave (64 lanes), unconditional: a row past the end
+// reads row 0 and a unit past the row end reads the row's last unit (masked in the dot).
+template <int F, int UPL>
+__device__ __forceinline__ void load_row_units(const uint8_t* __restrict__ w, int64_t rb, int U, int64_t N, int64_t r,
+                                               typename Unit<F>::W (&wt)[UPL]) {
+  const int c = threadIdx.x & 63;
+  const int64_t row = r < N ? r : 0;
+#pragma unroll
+  for (int t = 0; t < UPL; t++) {
+    const int u = min(c + 64 * t, U - 1);
+    if constexpr (F == JERO_Q6_K_R)
+      Unit<F>::load_w_planar(wt[t], w, N, U, row, u);
+    else
+      Unit<F>::load_w(wt[t], w + row * rb, u);
+  }
+}
+
 // Rows of one store segment for this wave: rows r_begin, r_begin + stride, ... below N of a
-// K-quant tensor, one row per wave (64 lanes), dotted with the activation blocks in LDS.  `cur`
-// holds the first row's weights, already loaded.
+// K-quant tensor, one row per wave (64 lanes), dotted with the activation blocks in LDS.  `wa`
+// holds the first row's weights, already issued; the next row's loads go into the other
+// buffer before each row's math.
 template <int F, int UPL>
 __device__ __forceinline__ void store_segment(const uint8_t* __restrict__ w, int64_t rb, int U, int64_t N,
                                               int64_t r_begin, int64_t stride, const uint8_t* s_act, float* y,
-                                              typename Unit<F>::W (&cur)[UPL]) {
+                                              typename Unit<F>::W (&wa)[UPL]) {
   using Ut = Unit<F>;
   const int c = threadIdx.x & 63;
-  auto load_row = [&](int64_t r, typename Ut::W (&wt)[UPL]) {
-#pragma unroll
-    for (int t = 0; t < UPL; t++) {
-      const int u = c + 64 * t;
-      if (r < N && u < U) {
-        if constexpr (F == JERO_Q6_K_R)
-          Ut::load_w_planar(wt[t], w, N, U, r, u);
-        else
-          Ut::load_w(wt[t], w + r * rb, u);
-      }
-    }
-  };
   typename Ut::Act act[UPL];
 #pragma unroll
-  for (int t = 0; t < UPL; t++) {
-    const int u = c + 64 * t;
-    if (u < U) Ut::load_act(act[t], s_act, u);
-  }
-  typename Ut::W nxt[UPL];
-  for (int64_t r = r_begin; r < N; r += stride) {
-    load_row(r + stride, nxt);
+  for (int t = 0; t < UPL; t++) Ut::load_act(act[t], s_act, min(c + 64 * t, U - 1));
+  auto process = [&](int64_t r, const typename Ut::W (&cur)[UPL]) {
     float acc = 0.f;
 #pragma unroll
     for (int t = 0; t < UPL; t++) {
-      const int u = c + 64 * t;
-      if (u < U) acc += Ut::dot(cur[t], act[t], nullptr);
+      const float d = Ut::dot(cur[t], act[t], nullptr);
+      acc += (c + 64 * t < U) ? d : 0.f;
     }
     acc = group_sum_last<64>(acc);
     if (c == 63) y[r] = acc;
-#pragma unroll
-    for (int t = 0; t < UPL; t++) cur[t] = nxt[t];
+  };
+  typename Ut::W wb[UPL];
+  for (int64_t r = r_begin; r < N; r += 2 * stride) {
+    load_row_units<F, UPL>(w, rb, U, N, r + stride, wb);
+    __builtin_amdgcn_sched_barrier(0);
+    process(r, wa);
+    if (r + stride >= N) break;
+    load_row_units<F, UPL>(w, rb, U, N, r + 2 * stride, wa);
+    __builtin_amdgcn_sched_barrier(0);
+    process(r + stride, wb);
   }
 }
 
@@ -349,7 +379,6 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_dual_kernel(DGemvArgs a)
   extern __shared__ __attribute__((aligned(16))) uint8_t s_mem[];
   float* s_tmp = reinterpret_cast<float*>(s_mem);
   uint8_t* s_act = s_mem + 256;
-  const int c = threadIdx.x & 63;
   const int64_t wave0 = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
   const int64_t stride = int64_t(gridDim.x) * (blockDim.x / kWave);
   const int64_t N1 = a.N, total = a.N + a.N2;
@@ -360,29 +389,12 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_dual_kernel(DGemvArgs a)
   load_x<JERO_Q8_K, XB, true>(X, a.x, a.norm_w, a.K);
   typename Unit<F1>::W c1[UPL];
   typename Unit<F2>::W c2[UPL];
-#pragma unroll
-  for (int t = 0; t < UPL; t++) {
-    const int u = c + 64 * t;
-    if (r1 < N1 && u < a.U) {
-      if constexpr (F1 == JERO_Q6_K_R)
-        Unit<F1>::load_w_planar(c1[t], a.w, N1, a.U, r1, u);
-      else
-        Unit<F1>::load_w(c1[t], a.w + r1 * a.rb, u);
-    }
-  }
+  load_row_units<F1, UPL>(a.w, a.rb, a.U, N1, r1, c1);
+  pin_x(X);
   build_act_lds<JERO_Q8_K, XB, true>(X, a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp);
   store_segment<F1, UPL>(a.w, a.rb, a.U, N1, r1, stride, s_act, a.y, c1);
   if (r2 + N1 < total) {
-#pragma unroll
-    for (int t = 0; t < UPL; t++) {
-      const int u = c + 64 * t;
-      if (u < a.U) {
-        if constexpr (F2 == JERO_Q6_K_R)
-          Unit<F2>::load_w_planar(c2[t], a.w2, a.N2, a.U, r2, u);
-        else
-          Unit<F2>::load_w(c2[t], a.w2 + r2 * a.rb2, u);
-      }
-    }
+    load_row_units<F2, UPL>(a.w2, a.rb2, a.U, a.N2, r2, c2);
     store_segment<F2, UPL>(a.w2, a.rb2, a.U, a.N2, r2, stride, s_act, a.y + N1, c2);
   }
 }

@@ -44,28 +44,25 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const uint8_t* __res
   const int n16 = act_bytes >> 4;
   if constexpr (LDS_ACT) {
 #pragma unroll
-    for (int i = 0; i < kMaxChunks; i++) {
-      const int ch = threadIdx.x + kGemvThreads * i;
-      if (ch < n16) av[i] = ld4(xq + 16 * ch);
-    }
+    for (int i = 0; i < kMaxChunks; i++) av[i] = ld4(xq + 16 * min(int(threadIdx.x) + kGemvThreads * i, n16 - 1));
   } else {
     if (row0 >= N) return;
   }
 
-  // 2. weight loads for all rows of the wave
+  // 2. weight loads for all rows of the wave, unconditional (row and unit clamped into the
+  //    matrix, results of clamped lanes masked below): a load under a branch gets a wait of
+  //    its own, and the activation's wait would become a wait for the weights as well
   typename Ut::W wt[R][UPL];
 #pragma unroll
   for (int r = 0; r < R; r++) {
-    const int64_t row = row0 + r * G + g;
+    const int64_t row = min(row0 + r * G + g, N - 1);
 #pragma unroll
     for (int t = 0; t < UPL; t++) {
-      const int u = c + LPR * t;
-      if (row < N && u < U) {
-        if constexpr (F == JERO_Q6_K_R)
-          Ut::load_w_planar(wt[r][t], w, N, U, row, u);
-        else
-          Ut::load_w(wt[r][t], w + row * rb, u);
-      }
+      const int u = min(c + LPR * t, U - 1);
+      if constexpr (F == JERO_Q6_K_R)
+        Ut::load_w_planar(wt[r][t], w, N, U, row, u);
+      else
+        Ut::load_w(wt[r][t], w + row * rb, u);
     }
   }
 
@@ -85,10 +82,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const uint8_t* __res
   }
   typename Ut::Act act[UPL];
 #pragma unroll
-  for (int t = 0; t < UPL; t++) {
-    const int u = c + LPR * t;
-    if (u < U) Ut::load_act(act[t], act_src, u);
-  }
+  for (int t = 0; t < UPL; t++) Ut::load_act(act[t], act_src, min(c + LPR * t, U - 1));
 
   // 4. per-row dot products, DPP reduction over the row's lanes
 #pragma unroll
@@ -98,15 +92,18 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const uint8_t* __res
 #pragma unroll
     for (int t = 0; t < UPL; t++) {
       const int u = c + LPR * t;
-      if (row < N && u < U) {
-        if constexpr (PART) {
-          int32_t p[Ut::kPartials];
-          acc += Ut::dot(wt[r][t], act[t], p);
+      const bool ok = row < N && u < U;
+      if constexpr (PART) {
+        int32_t p[Ut::kPartials];
+        const float d = Ut::dot(wt[r][t], act[t], p);
+        acc += ok ? d : 0.0f;
+        if (ok) {
 #pragma unroll
           for (int k = 0; k < Ut::kPartials; k++) part[row * ppr + Ut::part_index(u, k)] = p[k];
-        } else {
-          acc += Ut::dot(wt[r][t], act[t], nullptr);
         }
+      } else {
+        const float d = Ut::dot(wt[r][t], act[t], nullptr);
+        acc += ok ? d : 0.0f;
       }
     }
     acc = group_sum_last<LPR>(acc);

@@ -111,11 +111,19 @@ struct Unit<JERO_Q6_K> {
     float dx;
     int bs32[4];     // 32 * bsum of group t
   };
+  // d stays as the loaded dword and the shift of its f16 (converted in dot): converting at
+  // the load would make the compiler wait for the load wherever it places the conversion.
   struct W {
     u32x4 lo, hi, qh;
     uint32_t sc;  // the unit's four int8 scales sc[8n+j+2t], t = 0..3, one per byte
-    float d;
+    uint32_t dw, dsh;
   };
+  // f16 at a 2-byte aligned address: the dword holding it and its bit shift.
+  static __device__ __forceinline__ void load_d(W& w, const uint8_t* __restrict__ p) {
+    const uint32_t s = uint32_t(reinterpret_cast<uintptr_t>(p) & 3u);
+    w.dw = ld1(p - s);
+    w.dsh = 8u * s;
+  }
 
   static __device__ __forceinline__ void load_act(Act& A, const uint8_t* __restrict__ xq, int u) {
     int b = u >> 2, n = (u >> 1) & 1, j = u & 1;
@@ -146,7 +154,7 @@ struct Unit<JERO_Q6_K> {
     uint32_t sh = 8u * uint32_t(j);
     w.sc = ((sc.x >> sh) & 0xFFu) | (((sc.x >> (sh + 16u)) & 0xFFu) << 8) | (((sc.y >> sh) & 0xFFu) << 16) |
            (((sc.y >> (sh + 16u)) & 0xFFu) << 24);
-    w.d = ldh_a2(blk + 208);
+    load_d(w, blk + 208);
   }
 
   static __device__ __forceinline__ float dot(const W& w, const Act& A, int32_t* part) {
@@ -178,7 +186,7 @@ struct Unit<JERO_Q6_K> {
     int c0 = int(int8_t(w.sc)), c1 = int(int8_t(w.sc >> 8));
     int c2 = int(int8_t(w.sc >> 16)), c3 = int(int8_t(w.sc >> 24));
     int isum = c0 * s0 + c1 * s1 + c2 * s2 + c3 * s3;
-    return A.dx * w.d * float(isum);
+    return A.dx * h2f(w.dw >> w.dsh) * float(isum);
   }
 };
 
@@ -200,7 +208,7 @@ struct Unit<JERO_Q6_K_R> : Unit<JERO_Q6_K> {
     w.hi = ld4(base + plane + gu * 16);
     w.qh = ld4(base + 2 * plane + gu * 16);
     w.sc = ld1(base + 3 * plane + gu * 4);
-    w.d = ldh_a2(base + 3 * plane + N * int64_t(U) * 4 + (row * (U / 4) + (u >> 2)) * 2);
+    load_d(w, base + 3 * plane + N * int64_t(U) * 4 + (row * (U / 4) + (u >> 2)) * 2);
   }
 };
 
@@ -231,9 +239,9 @@ struct Unit<JERO_Q8_0> {
   // The 34-byte block is read as the nine dwords from the dword-aligned address at or below
   // it: each holds at least one byte of the block.
   static __device__ __forceinline__ void load_w(W& w, const uint8_t* __restrict__ row, int u) {
-    uintptr_t a = reinterpret_cast<uintptr_t>(row + int64_t(u) * 34);
-    const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
-    w.s = uint32_t(a & 3u);
+    const uint8_t* p = row + int64_t(u) * 34;
+    w.s = uint32_t(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint8_t* base = p - w.s;  // pointer arithmetic keeps the global address space
     u32x4 v0 = ld4(base), v1 = ld4(base + 16);
     w.D[0] = v0.x; w.D[1] = v0.y; w.D[2] = v0.z; w.D[3] = v0.w;
     w.D[4] = v1.x; w.D[5] = v1.y; w.D[6] = v1.z; w.D[7] = v1.w;
@@ -284,9 +292,9 @@ struct Unit<JERO_Q4_0> {
 
   // The 18-byte block is read as the five dwords from the dword-aligned address at or below it.
   static __device__ __forceinline__ void load_w(W& w, const uint8_t* __restrict__ row, int u) {
-    uintptr_t a = reinterpret_cast<uintptr_t>(row + int64_t(u) * 18);
-    const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
-    w.s = uint32_t(a & 3u);
+    const uint8_t* p = row + int64_t(u) * 18;
+    w.s = uint32_t(reinterpret_cast<uintptr_t>(p) & 3u);
+    const uint8_t* base = p - w.s;  // pointer arithmetic keeps the global address space
     u32x4 v0 = ld4(base);
     w.D[0] = v0.x; w.D[1] = v0.y; w.D[2] = v0.z; w.D[3] = v0.w;
     w.D[4] = ld1(base + 16);

@@ -53,13 +53,14 @@ __device__ __forceinline__ uint32_t funnel(uint32_t lo, uint32_t hi, uint32_t s)
 
 // 16 bytes starting at an address that is only 2-byte aligned.  Reads the five dwords that
 // cover them from the dword-aligned address below: every dword read holds at least one byte
-// of [p, p+16), so the read never leaves the pages that hold the requested bytes.
+// of [p, p+16), so the read never leaves the pages that hold the requested bytes.  At an
+// aligned address the fifth read repeats the fourth dword (funnel ignores it): every load is
+// issued unconditionally, since a load under a branch gets a wait for completion of its own.
 __device__ __forceinline__ u32x4 ld16_a2(const uint8_t* p) {
-  uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
-  uint32_t s = uint32_t(a & 3u);
+  const uint32_t s = uint32_t(reinterpret_cast<uintptr_t>(p) & 3u);
+  const uint8_t* base = p - s;  // pointer arithmetic keeps the global address space
   u32x4 w = ld4(base);
-  uint32_t w4 = (s != 0u) ? ld1(base + 16) : 0u;
+  uint32_t w4 = ld1(base + (s != 0u ? 16 : 12));
   u32x4 r;
   r.x = funnel(w.x, w.y, s);
   r.y = funnel(w.y, w.z, s);
@@ -70,21 +71,19 @@ __device__ __forceinline__ u32x4 ld16_a2(const uint8_t* p) {
 
 // 4 bytes at a 2-byte aligned address (same page argument as ld16_a2).
 __device__ __forceinline__ uint32_t ld4_a2(const uint8_t* p) {
-  uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
-  uint32_t s = uint32_t(a & 3u);
+  const uint32_t s = uint32_t(reinterpret_cast<uintptr_t>(p) & 3u);
+  const uint8_t* base = p - s;  // pointer arithmetic keeps the global address space
   uint32_t w0 = ld1(base);
-  uint32_t w1 = (s != 0u) ? ld1(base + 4) : 0u;
+  uint32_t w1 = ld1(base + (s != 0u ? 4 : 0));
   return funnel(w0, w1, s);
 }
 
 // 8 bytes at a 2-byte aligned address.
 __device__ __forceinline__ u32x2 ld8_a2(const uint8_t* p) {
-  uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint8_t* base = reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3));
-  uint32_t s = uint32_t(a & 3u);
+  const uint32_t s = uint32_t(reinterpret_cast<uintptr_t>(p) & 3u);
+  const uint8_t* base = p - s;  // pointer arithmetic keeps the global address space
   u32x2 w = ld2(base);
-  uint32_t w2 = (s != 0u) ? ld1(base + 8) : 0u;
+  uint32_t w2 = ld1(base + (s != 0u ? 8 : 4));
   u32x2 r;
   r.x = funnel(w.x, w.y, s);
   r.y = funnel(w.y, w2, s);
@@ -93,9 +92,9 @@ __device__ __forceinline__ u32x2 ld8_a2(const uint8_t* p) {
 
 // 2-byte f16 at a 2-byte aligned address -> f32.
 __device__ __forceinline__ float ldh_a2(const uint8_t* p) {
-  uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  uint32_t w = ld1(reinterpret_cast<const uint8_t*>(a & ~uintptr_t(3)));
-  uint16_t h = uint16_t(w >> (8u * uint32_t(a & 3u)));
+  const uint32_t s = uint32_t(reinterpret_cast<uintptr_t>(p) & 3u);
+  uint32_t w = ld1(p - s);
+  uint16_t h = uint16_t(w >> (8u * s));
   return float(__builtin_bit_cast(_Float16, h));
 }
 

@@ -8,11 +8,11 @@
 // V ring, each [capacity][n_kv * head_dim], f32 (as the reference) or f16 (half the bytes).
 //
 // Split-K ("flash decoding"): workgroup (split s, kv head h) owns positions
-// [s*64, s*64+64) of the active slots and all q heads of h's group.  It issues its K and V
-// loads (16 bytes per lane, consecutive lanes on consecutive bytes) before anything else, so
-// a workgroup has its whole 2 x 128 x head_dim tile in flight; then it scores, exponentiates
-// against its local max and accumulates P V.  A second kernel merges the splits with the
-// usual max/sum rescaling.  Fused mode: every workgroup rebuilds its q heads (per-head RMSNorm,
+// [s*64, s*64+64) of the active slots and all q heads of h's group, each of its four waves 16
+// of them.  A wave issues all its loads first (its 2 x 16 x head_dim K/V rows, 16 bytes per
+// lane), then scores, exponentiates against its own max and accumulates P V with DPP
+// reductions only; one barrier merges the four waves.  A second kernel merges the splits with
+// the usual max/sum rescaling.  Fused mode: every wave rebuilds its q heads (per-head RMSNorm,
 // interleaved RoPE, scale folded in); the workgroup whose range holds the new slot also
 // normalises/rotates k, writes k and v into the ring and uses them for that slot.
 #include "attention.h"
@@ -57,39 +57,80 @@ __device__ __forceinline__ float rope_angle(int i, int hd, int64_t pos, float th
   return float(pos) / powf(theta, expo);
 }
 
-// Per-head RMSNorm (weight pair nw, if has_norm) + interleaved RoPE of one head held as one
-// pair per lane in a group of HD/2 lanes; cs = (cos, sin) of the pair's angle.
-template <int HD>
-__device__ __forceinline__ float2 norm_rope_pair(float x0, float x1, bool has_norm, float2 nw, float eps, float2 cs) {
-  if (has_norm) {
-    float ss = x0 * x0 + x1 * x1;
-#pragma unroll
-    for (int off = HD / 4; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
-    float inv = 1.0f / sqrtf(ss / float(HD) + eps);
-    x0 = x0 * inv * nw.x;
-    x1 = x1 * inv * nw.y;
-  }
-  return make_float2(x0 * cs.x - x1 * cs.y, x0 * cs.y + x1 * cs.x);
+// Sum over aligned groups of W consecutive lanes (W a power of two up to 32); every lane of a
+// group gets the total.  DPP within a row of 16 lanes, one swizzle across rows for W = 32.
+template <int W>
+__device__ __forceinline__ float lanes_sum(float v) {
+  if constexpr (W >= 2) v = dpp_add<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+  if constexpr (W >= 4) v = dpp_add<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+  if constexpr (W >= 8) v = dpp_add<0x141, 0xF>(v);   // row_half_mirror
+  if constexpr (W >= 16) v = dpp_add<0x140, 0xF>(v);  // row_mirror
+  if constexpr (W >= 32) v += __shfl_xor(v, 16, kWave);
+  return v;
 }
 
+// Per-head RMSNorm (weights nw, if has_norm) + interleaved RoPE of one head held as E
+// consecutive elements per lane in a group of HD/E lanes; cs[j] = (cos, sin) of pair j.
+template <int HD, int E>
+__device__ __forceinline__ void norm_rope_chunk(float (&x)[E], bool has_norm, const float (&nw)[E], float eps,
+                                                const float2 (&cs)[E / 2]) {
+  if (has_norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; e++) ss += x[e] * x[e];
+    ss = lanes_sum<HD / E>(ss);
+    const float inv = 1.0f / sqrtf(ss / float(HD) + eps);
+#pragma unroll
+    for (int e = 0; e < E; e++) x[e] = x[e] * inv * nw[e];
+  }
+#pragma unroll
+  for (int j = 0; j < E / 2; j++) {
+    const float x0 = x[2 * j], x1 = x[2 * j + 1];
+    x[2 * j] = x0 * cs[j].x - x1 * cs[j].y;
+    x[2 * j + 1] = x0 * cs[j].y + x1 * cs[j].x;
+  }
+}
+
+// n floats at an 8-byte aligned address (n even), as float2 loads.
+template <int N>
+__device__ __forceinline__ void ld_floats(float (&dst)[N], const float* __restrict__ src) {
+#pragma unroll
+  for (int j = 0; j < N / 2; j++) {
+    const float2 v = reinterpret_cast<const float2*>(src)[j];
+    dst[2 * j] = v.x;
+    dst[2 * j + 1] = v.y;
+  }
+}
+
+// Split-K partial of one decode token's attention.  Workgroup (split s, kv head h) owns the
+// 64 slots [64 s, 64 s + 64) and every q head of h's group; each of its four waves treats 16 of
+// those slots as a sub-split of its own and the workgroup merges the four at the end, so the
+// whole pipeline has one workgroup barrier.
+//   * All global loads go out first, unconditionally (clamped in-bounds addresses): the q
+//     heads, the fused-mode extras and the wave's K and V rows, 16 bytes per lane.
+//   * K layout: lane = (position kp, chunk kc); each position's CPR chunk lanes hold the q heads'
+//     matching chunks, so scores are a DPP sum over CPR consecutive lanes.  q is normalised
+//     and rotated in registers by the same lanes (the head's sum of squares is the same sum).
+//   * The wave's softmax (max, exp, sum over its 16 positions) is a whole-wave DPP reduction.
+//   * V layout: lane = (chunk vc, position vp) with the PPL positions of a load in consecutive
+//     lanes, so P V sums over positions with DPP as well; the numerators move from the K
+//     layout to the V layout through the wave's own LDS rows (no barrier).
+//   * The four sub-splits merge with the usual max rescaling through LDS, one barrier.
 template <int HD, typename KV, bool FUSED, int MAXG>
 __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p) {
-  constexpr int EPL = 16 / int(sizeof(KV));     // elements per 16-byte load
-  constexpr int LPP = HD / EPL;                 // lanes per position (K rows)
-  constexpr int PPW = kWave / LPP;              // positions per wave per step
-  constexpr int CH = attn_chunk(HD);
-  constexpr int KSTEPS = CH / (PPW * (kAttnThreads / kWave));
-  constexpr int DPT = HD / EPL;                 // dim chunks per V row
-  constexpr int NPS = kAttnThreads / DPT;       // position subsets in the PV phase
-  constexpr int VSTEPS = CH / NPS;
-  static_assert(KSTEPS >= 1 && VSTEPS >= 1, "tile shape");
+  constexpr int EPL = 16 / int(sizeof(KV));  // KV elements per 16-byte load
+  constexpr int CPR = HD / EPL;              // 16-byte chunks per K/V row
+  constexpr int PPL = kWave / CPR;           // positions per wave-wide load
+  constexpr int NW = kAttnThreads / kWave;   // waves = sub-splits
+  constexpr int CH = attn_chunk(HD);         // positions per workgroup
+  constexpr int WPOS = CH / NW;              // positions per wave
+  constexpr int NL = WPOS / PPL;             // K loads and V loads per lane
+  constexpr int G4 = (MAXG + 3) / 4;         // float4s per position row of numerators
+  static_assert(NL >= 1 && NL * PPL == WPOS && CPR <= 32, "tile shape");
 
-  __shared__ float s_q[MAXG][HD];
-  __shared__ float s_knew[HD];
-  __shared__ float s_vnew[HD];
-  __shared__ float s_p[MAXG][CH];
-  __shared__ float s_red[kAttnThreads / kWave][MAXG * HD];
-  __shared__ float s_m[MAXG], s_l[MAXG];
+  __shared__ float4 s_p[NW][WPOS][G4];
+  __shared__ float s_o[NW][MAXG][HD];
+  __shared__ float s_m[NW][MAXG], s_l[NW][MAXG];
 
   const int split = blockIdx.x, kh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -97,60 +138,40 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   const int64_t kvd = int64_t(p.nkv) * HD;
   const int S = gridDim.x;
   const int p0 = split * CH;
+  const int w0 = p0 + wv * WPOS;
+  const int kc = lane % CPR, kp = lane / CPR;
+  const int vp = lane % PPL, vc = lane / PPL;
 
-  // 0. this thread's q pairs (fused: also the new k), issued first so that waiting for them
-  //    does not wait for the K/V tile behind them
-  constexpr int HPW = 128 / HD;                         // heads per wave pass (HD/2 lanes per head)
-  constexpr int HPP = (kAttnThreads / kWave) * HPW;     // heads per pass of the workgroup
-  constexpr int NPASS = (MAXG + (FUSED ? 1 : 0) + HPP - 1) / HPP;
-  const int pair = lane % (HD / 2), sub = lane / (HD / 2);
-  float2 qx[NPASS];
-  // Loads are unconditional, from clamped in-bounds addresses: a load under a branch gets its
-  // own wait for completion, which would serialise the tile's round trips.
+  // 0. loads
+  float q[MAXG][EPL];
 #pragma unroll
-  for (int it = 0; it < NPASS; it++) {
-    const int gi = wv * HPW + it * HPP + sub;
-    const bool is_k = FUSED && gi == group;
-    const float* src = is_k ? p.k_new + kh * HD : p.q + (int64_t(kh) * group + (gi < group ? gi : 0)) * HD;
-    const float2 v = *reinterpret_cast<const float2*>(src + 2 * pair);
-    qx[it] = (gi < group || is_k) ? v : make_float2(0.f, 0.f);
-  }
-
-  // Fused mode: the rest of what the prologue reads (position, RoPE table, norm weights, the
-  // new v) goes out in the same batch.  A null pointer reads a valid stand-in (the q vector)
-  // whose value is then ignored.
-  const float* dummy = p.q;
-  float2 cs_pre = make_float2(1.f, 0.f), qn_pre = cs_pre, kn_pre = cs_pre;
-  float vnew_pre = 0.f;
+  for (int h = 0; h < MAXG; h++)
+    ld_floats<EPL>(q[h], p.q + (int64_t(kh) * group + min(h, group - 1)) * HD + kc * EPL);
   int64_t pos_pre = p.pos;
+  float kn[EPL], vn[EPL], qnw[EPL], knw[EPL], csr[EPL];
   if constexpr (FUSED) {
+    // a null pointer reads a valid stand-in (the q vector) whose value is then ignored
     pos_pre = *(p.pos_dev ? p.pos_dev : reinterpret_cast<const int64_t*>(p.k));
-    cs_pre = *reinterpret_cast<const float2*>((p.rope_cs ? p.rope_cs : dummy) + 2 * pair);
-    qn_pre = *reinterpret_cast<const float2*>((p.q_norm ? p.q_norm : dummy) + 2 * pair);
-    kn_pre = *reinterpret_cast<const float2*>((p.k_norm ? p.k_norm : dummy) + 2 * pair);
-    vnew_pre = p.v_new[kh * HD + tid % HD];
+    ld_floats<EPL>(kn, p.k_new + kh * HD + kc * EPL);
+    ld_floats<EPL>(vn, p.v_new + kh * HD + vc * EPL);
+    ld_floats<EPL>(qnw, (p.q_norm ? p.q_norm : p.q) + kc * EPL);
+    ld_floats<EPL>(knw, (p.k_norm ? p.k_norm : p.q) + kc * EPL);
+    ld_floats<EPL>(csr, (p.rope_cs ? p.rope_cs : p.q) + kc * EPL);
   }
-
-  // 1. K and V tiles into registers.  With the position on the device the grid covers every
-  //    ring slot, so slots [p0, p0 + 64) are inside the ring whatever the position; slots past
-  //    the active range are loaded and then ignored.
+  // With the position on the device the grid covers every ring slot, so slots [p0, p0 + 64)
+  // are inside the ring whatever the position; slots past the active range are loaded and
+  // then ignored.
   const int bound = p.pos_dev ? int(p.capacity) : p.active;
   const int pl = min(p0 + CH, bound);
   const KV* kb = static_cast<const KV*>(p.k) + kh * HD;
   const KV* vb = static_cast<const KV*>(p.v) + kh * HD;
-  u32x4 kreg[KSTEPS], vreg[VSTEPS];
-  const int kc = lane % LPP;
+  u32x4 kreg[NL], vreg[NL];
 #pragma unroll
-  for (int i = 0; i < KSTEPS; i++) {
-    const int pos = min(p0 + (i * (kAttnThreads / kWave) + wv) * PPW + lane / LPP, pl - 1);
-    kreg[i] = ld4(reinterpret_cast<const uint8_t*>(kb + int64_t(pos) * kvd + kc * EPL));
-  }
-  const int dc = tid % DPT, ps = tid / DPT;
+  for (int i = 0; i < NL; i++)
+    kreg[i] = ld4(reinterpret_cast<const uint8_t*>(kb + int64_t(min(w0 + i * PPL + kp, pl - 1)) * kvd + kc * EPL));
 #pragma unroll
-  for (int i = 0; i < VSTEPS; i++) {
-    const int pos = min(p0 + i * NPS + ps, pl - 1);
-    vreg[i] = ld4(reinterpret_cast<const uint8_t*>(vb + int64_t(pos) * kvd + dc * EPL));
-  }
+  for (int i = 0; i < NL; i++)
+    vreg[i] = ld4(reinterpret_cast<const uint8_t*>(vb + int64_t(min(w0 + i * PPL + vp, pl - 1)) * kvd + vc * EPL));
 
   int active = p.active, slot = p.slot;
   int64_t pos_now = p.pos;
@@ -169,158 +190,164 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   }
   const int p1 = min(p0 + CH, active);
 
-  // 2. q heads of this group (and, fused, the new k/v) into LDS
-  const bool own_slot = FUSED && slot >= p0 && slot < p1;
-  {
-    float2 cs = cs_pre;
-    if (FUSED && !p.rope_cs) sincosf(rope_angle(pair, HD, pos_now, p.theta), &cs.y, &cs.x);
+  // 1. q heads (fused: QK-norm and RoPE, also of the new k), scale folded into q
+  if constexpr (FUSED) {
+    float2 cs[EPL / 2];
 #pragma unroll
-    for (int it = 0; it < NPASS; it++) {
-      const int gi = wv * HPW + it * HPP + sub;
-      const bool is_k = FUSED && gi == group;
-      const bool ok = gi < group || is_k;
-      float2 r;
-      if constexpr (FUSED)
-        r = norm_rope_pair<HD>(qx[it].x, qx[it].y, (is_k ? p.k_norm : p.q_norm) != nullptr, is_k ? kn_pre : qn_pre,
-                               p.eps, cs);
-      else
-        r = qx[it];
-      if (ok) {
-        if (is_k) {
-          s_knew[2 * pair] = r.x;
-          s_knew[2 * pair + 1] = r.y;
-        } else {
-          s_q[gi][2 * pair] = r.x * p.scale;
-          s_q[gi][2 * pair + 1] = r.y * p.scale;
-        }
-      }
-    }
-    if (own_slot && tid < HD) s_vnew[tid] = vnew_pre;
-  }
-  __syncthreads();
-  if (own_slot) {  // append the new token's k, v to the ring
-    KV* kw = static_cast<KV*>(p.k_write) + int64_t(slot) * kvd + kh * HD;
-    KV* vw = static_cast<KV*>(p.v_write) + int64_t(slot) * kvd + kh * HD;
-    for (int d = tid; d < HD; d += kAttnThreads) {
-      kw[d] = narrow<KV>(s_knew[d]);
-      vw[d] = narrow<KV>(s_vnew[d]);
-    }
-  }
-
-  // 3. scores: 16-byte K slices against every q head of the group, reduced over LPP lanes
-#pragma unroll
-  for (int i = 0; i < KSTEPS; i++) {
-    const int pos = p0 + (i * (kAttnThreads / kWave) + wv) * PPW + lane / LPP;
-    float kf[EPL];
-    if (pos < p1) {
-      if (FUSED && pos == slot) {
-#pragma unroll
-        for (int e = 0; e < EPL; e++) kf[e] = s_knew[kc * EPL + e];
+    for (int j = 0; j < EPL / 2; j++) {
+      if (p.rope_cs) {
+        cs[j] = make_float2(csr[2 * j], csr[2 * j + 1]);
       } else {
-        widen16<KV>(kreg[i], kf);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPL; e++) kf[e] = 0.f;
-    }
-#pragma unroll
-    for (int gi = 0; gi < MAXG; gi++) {
-      if (gi < group) {
-        float s = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; e++) s += s_q[gi][kc * EPL + e] * kf[e];
-        if constexpr (LPP <= 16) {
-          s = group_sum_all<LPP>(s);  // DPP within a row of 16 lanes
-          if (kc == 0 && pos < p1) s_p[gi][pos - p0] = s;
-        } else {
-          s = group_sum_last<LPP>(s);
-          if (kc == LPP - 1 && pos < p1) s_p[gi][pos - p0] = s;
-        }
+        float sn, cn;
+        sincosf(rope_angle(kc * (EPL / 2) + j, HD, pos_now, p.theta), &sn, &cn);
+        cs[j] = make_float2(cn, sn);
       }
     }
+#pragma unroll
+    for (int h = 0; h < MAXG; h++) norm_rope_chunk<HD, EPL>(q[h], p.q_norm != nullptr, qnw, p.eps, cs);
+    norm_rope_chunk<HD, EPL>(kn, p.k_norm != nullptr, knw, p.eps, cs);
   }
-  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < MAXG; h++)
+#pragma unroll
+    for (int e = 0; e < EPL; e++) q[h][e] *= p.scale;
 
-  // 4. local softmax numerators per head (one wave per head)
-  const int n = p1 - p0;
-  for (int gi = wv; gi < group; gi += kAttnThreads / kWave) {
-    float m = -INFINITY;
-    for (int j = lane; j < n; j += kWave) m = fmaxf(m, s_p[gi][j]);
-    m = wave_max_dpp(m);
-    float l = 0.f;
-    for (int j = lane; j < n; j += kWave) {
-      float e = expf(s_p[gi][j] - m);
-      s_p[gi][j] = e;
-      l += e;
+  // 2. scores of the wave's positions (K layout); masked slots score -inf
+  float sc[NL][MAXG];
+#pragma unroll
+  for (int i = 0; i < NL; i++) {
+    const int pos = w0 + i * PPL + kp;
+    float kf[EPL];
+    widen16<KV>(kreg[i], kf);
+    if constexpr (FUSED) {
+#pragma unroll
+      for (int e = 0; e < EPL; e++) kf[e] = pos == slot ? kn[e] : kf[e];
     }
-    l = wave_sum_dpp(l);
-    if (lane == 0) {
-      s_m[gi] = m;
-      s_l[gi] = l;
+#pragma unroll
+    for (int h = 0; h < MAXG; h++) {
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; e++) s += q[h][e] * kf[e];
+      s = lanes_sum<CPR>(s);
+      sc[i][h] = pos < p1 ? s : -INFINITY;
     }
   }
-  __syncthreads();
 
-  // 5. P V over this thread's position subset, then across subsets
+  // 3. the wave's softmax numerators, max and sum per head (uniform across the wave)
+  float m[MAXG], l[MAXG];
+#pragma unroll
+  for (int h = 0; h < MAXG; h++) {
+    float mx = sc[0][h];
+#pragma unroll
+    for (int i = 1; i < NL; i++) mx = fmaxf(mx, sc[i][h]);
+    mx = wave_max_dpp(mx);
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+      const float e = mx == -INFINITY ? 0.f : expf(sc[i][h] - mx);
+      sc[i][h] = e;
+      sum += e;
+    }
+    m[h] = mx;
+    l[h] = wave_sum_dpp(kc == 0 ? sum : 0.f);  // one lane per position
+  }
+  if (kc == 0) {
+#pragma unroll
+    for (int i = 0; i < NL; i++)
+#pragma unroll
+      for (int g4 = 0; g4 < G4; g4++) {
+        float t[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) t[k] = 4 * g4 + k < MAXG ? sc[i][4 * g4 + k] : 0.f;
+        s_p[wv][i * PPL + kp][g4] = make_float4(t[0], t[1], t[2], t[3]);
+      }
+  }
+
+  // 4. P V over the wave's positions (V layout), summed over the PPL position lanes
   float acc[MAXG][EPL];
 #pragma unroll
-  for (int gi = 0; gi < MAXG; gi++)
+  for (int h = 0; h < MAXG; h++)
 #pragma unroll
-    for (int e = 0; e < EPL; e++) acc[gi][e] = 0.f;
+    for (int e = 0; e < EPL; e++) acc[h][e] = 0.f;
 #pragma unroll
-  for (int i = 0; i < VSTEPS; i++) {
-    const int pos = p0 + i * NPS + ps;
-    if (pos < p1) {
-      float vf[EPL];
-      if (FUSED && pos == slot) {
+  for (int i = 0; i < NL; i++) {
+    const int pos = w0 + i * PPL + vp;
+    float pr[G4 * 4];
 #pragma unroll
-        for (int e = 0; e < EPL; e++) vf[e] = s_vnew[dc * EPL + e];
-      } else {
-        widen16<KV>(vreg[i], vf);
-      }
+    for (int g4 = 0; g4 < G4; g4++) {
+      const float4 t = s_p[wv][i * PPL + vp][g4];  // written by this wave above
+      pr[4 * g4] = t.x;
+      pr[4 * g4 + 1] = t.y;
+      pr[4 * g4 + 2] = t.z;
+      pr[4 * g4 + 3] = t.w;
+    }
+    float vf[EPL];
+    widen16<KV>(vreg[i], vf);
 #pragma unroll
-      for (int gi = 0; gi < MAXG; gi++) {
-        if (gi < group) {
-          const float pr = s_p[gi][pos - p0];
+    for (int e = 0; e < EPL; e++) {
+      if constexpr (FUSED) vf[e] = pos == slot ? vn[e] : vf[e];
+      vf[e] = pos < p1 ? vf[e] : 0.f;  // a stale slot past the active range may hold anything
+    }
 #pragma unroll
-          for (int e = 0; e < EPL; e++) acc[gi][e] += pr * vf[e];
-        }
+    for (int h = 0; h < MAXG; h++)
+#pragma unroll
+      for (int e = 0; e < EPL; e++) acc[h][e] += pr[h] * vf[e];
+  }
+#pragma unroll
+  for (int h = 0; h < MAXG; h++)
+#pragma unroll
+    for (int e = 0; e < EPL; e++) acc[h][e] = lanes_sum<PPL>(acc[h][e]);
+
+  // fused: the workgroup holding the new slot appends k, v to the ring
+  if constexpr (FUSED) {
+    if (slot >= p0 && slot < p1) {
+      KV* kw = static_cast<KV*>(p.k_write) + int64_t(slot) * kvd + kh * HD;
+      KV* vw = static_cast<KV*>(p.v_write) + int64_t(slot) * kvd + kh * HD;
+#pragma unroll
+      for (int i = 0; i < NL; i++) {
+        if (w0 + i * PPL + kp == slot)
+#pragma unroll
+          for (int e = 0; e < EPL; e++) kw[kc * EPL + e] = narrow<KV>(kn[e]);
+        if (w0 + i * PPL + vp == slot)
+#pragma unroll
+          for (int e = 0; e < EPL; e++) vw[vc * EPL + e] = narrow<KV>(vn[e]);
       }
     }
   }
-  // subsets of one wave sit DPT lanes apart
+
+  // 5. merge of the four sub-splits
+  if (vp == 0) {
 #pragma unroll
-  for (int gi = 0; gi < MAXG; gi++) {
-    if (gi < group) {
+    for (int h = 0; h < MAXG; h++)
 #pragma unroll
-      for (int e = 0; e < EPL; e++) {
-        float v = acc[gi][e];
-#pragma unroll
-        for (int off = DPT; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
-        acc[gi][e] = v;
-      }
-    }
+      for (int e = 0; e < EPL; e++) s_o[wv][h][vc * EPL + e] = acc[h][e];
   }
-  if (lane < DPT) {
+  if (lane == 0) {
 #pragma unroll
-    for (int gi = 0; gi < MAXG; gi++)
-      if (gi < group)
-#pragma unroll
-        for (int e = 0; e < EPL; e++) s_red[wv][gi * HD + dc * EPL + e] = acc[gi][e];
+    for (int h = 0; h < MAXG; h++) {
+      s_m[wv][h] = m[h];
+      s_l[wv][h] = l[h];
+    }
   }
   __syncthreads();
   for (int idx = tid; idx < group * HD; idx += kAttnThreads) {
-    float v = 0.f;
+    const int h = idx / HD, d = idx % HD;
+    float M = s_m[0][h];
 #pragma unroll
-    for (int w = 0; w < kAttnThreads / kWave; w++) v += s_red[w][idx];
-    const int gi = idx / HD, d = idx % HD;
-    const int h = kh * group + gi;
-    p.part_o[(int64_t(h) * S + split) * HD + d] = v;
-  }
-  if (tid < group) {
-    const int h = kh * group + tid;
-    p.part_ml[(int64_t(h) * S + split) * 2 + 0] = s_m[tid];
-    p.part_ml[(int64_t(h) * S + split) * 2 + 1] = s_l[tid];
+    for (int w = 1; w < NW; w++) M = fmaxf(M, s_m[w][h]);
+    float o = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+      const float wt = s_m[w][h] == -INFINITY ? 0.f : expf(s_m[w][h] - M);
+      o += wt * s_o[w][h][d];
+      L += wt * s_l[w][h];
+    }
+    const int64_t row = int64_t(kh * group + h) * S + split;
+    p.part_o[row * HD + d] = o;
+    if (d == 0) {
+      p.part_ml[row * 2 + 0] = M;
+      p.part_ml[row * 2 + 1] = L;
+    }
   }
 }
 

@@ -3,6 +3,9 @@
 Default workload (one "step"): the Q4_K x Q8_K decode GEMV shapes at batch 1 --
 4096->4096, 4096->12288 and 12288->4096 -- each launch reading its own copy of the weights
 (copies rotate over >= 768 MB so the 256 MB Infinity Cache never serves a repeat).  The
+weights are GGUF Q4_K tensors re-laid out once at load into the planar Q4_K_R device layout
+(jero_hip_repack, the layout the decode step runs on; same bytes); per_shape_gguf times the
+same GEMV straight on the GGUF layout.  The
 step is captured once in a HIP graph and replayed; HIP events on the replay stream time
 the K steps.  `value` is algorithmic bytes (weights + Q8_K activation + f32 output) per
 second over the whole step.  Extra fields: the Q6_K 4096->151936 output head, and the
@@ -358,14 +361,16 @@ def main():
         torch.cuda.synchronize()
         del a, b
 
-    # ---- Q4_K decode shapes
-    bufs, xqs, ys, views, algo = [], [], [], [], []
+    # ---- Q4_K decode shapes: the GGUF tensors re-laid out once at load (Q4_K -> Q4_K_R, the
+    # layout the decode step runs on); the GGUF-layout kernel is timed too (per_shape_gguf)
+    bufs, xqs, ys, views, raw_views, algo = [], [], [], [], [], []
     for i, (n_in, n_out) in enumerate(SHAPES):
         nbytes = J.row_bytes(J.Q4_K, n_in) * n_out
         copies = max(2, int(np.ceil(ROTATE_BYTES / nbytes)))
         buf = synth_weights(torch, J, J.Q4_K, n_in, n_out, copies, dev, 1000 + i)
         bufs.append(buf)
-        views.append([J.TensorView(f"w{i}", J.Q4_K, [n_in, n_out], buf[c]) for c in range(copies)])
+        raw_views.append([J.TensorView(f"w{i}", J.Q4_K, [n_in, n_out], buf[c]) for c in range(copies)])
+        views.append([J.repack(v) for v in raw_views[-1]])
         x = torch.randn(n_in, generator=torch.Generator(device=dev).manual_seed(7 + i), device=dev)
         xqs.append(J.quantize_act(J.Q8_K, x))
         ys.append(torch.empty(n_out, dtype=torch.float32, device=dev))
@@ -385,18 +390,19 @@ def main():
     step_bytes = sum(algo)
     value = step_bytes / t_step / 1e9
 
-    # per-shape kernel averages (same method, one shape per graph)
-    per_shape = {}
-    for i, (n_in, n_out) in enumerate(SHAPES):
-        cnt = [0]
+    # per-shape kernel averages (same method, one shape per graph), planar and GGUF layouts
+    per_shape, per_shape_gguf = {}, {}
+    for table, vlist in ((per_shape, views), (per_shape_gguf, raw_views)):
+        for i, (n_in, n_out) in enumerate(SHAPES):
+            cnt = [0]
 
-        def one(i=i, cnt=cnt):
-            vv = views[i]
-            J.matvec(vv[cnt[0] % len(vv)], xqs[i], ys[i], stream=stream)
-            cnt[0] += 1
+            def one(i=i, cnt=cnt, vlist=vlist):
+                vv = vlist[i]
+                J.matvec(vv[cnt[0] % len(vv)], xqs[i], ys[i], stream=stream)
+                cnt[0] += 1
 
-        t = time_graph(torch, one, args.steps, args.warmup, stream)
-        per_shape[f"{n_in}x{n_out}"] = {"us": round(t * 1e6, 3), "GB_s": round(algo[i] / t / 1e9, 1),
+            t = time_graph(torch, one, args.steps, args.warmup, stream)
+            table[f"{n_in}x{n_out}"] = {"us": round(t * 1e6, 3), "GB_s": round(algo[i] / t / 1e9, 1),
                                         "bytes": algo[i]}
     gemv_launch_us = t_step * 1e6 / len(SHAPES)
     achieved = (step_bytes / len(SHAPES)) / (gemv_launch_us * 1e-6) / 1e9
@@ -478,11 +484,13 @@ def main():
         "dtype": "int8",
         "data": "synthetic: random-init Q4_K weights (uniform payload, N(0,0.02)-scale fields), N(0,1) activations",
         "config": {"workload": "Q4_K x Q8_K decode GEMV, batch 1: 4096->4096, 4096->12288, 12288->4096",
+                   "weight_layout": "Q4_K_R (GGUF Q4_K bytes re-laid out once at load by jero_hip_repack)",
                    "rotated_weight_bytes": int(ROTATE_BYTES), "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "per_shape": per_shape,
+        "per_shape_gguf": per_shape_gguf,
         "q6k_head": head,
         "prefill_gemm": gemm,
         "moe": moe,

@@ -42,6 +42,7 @@ typedef enum jero_quant {
   JERO_Q4_K = 12, /* the reference's QuantType::Q4_K_M */
   JERO_Q6_K = 14,
   JERO_Q8_K = 15,  /* activation blocks for Q4_K / Q6_K weights: f32 d, i8 q[256], i16 bsums[16] */
+  JERO_Q4_K_R = 112, /* Q4_K bytes re-laid out by jero_hip_repack into aligned planes (same size) */
   JERO_Q6_K_R = 114, /* Q6_K bytes re-laid out by jero_hip_repack into aligned planes (same size) */
   JERO_ACT_Q8 = 100 /* activation blocks for Q8_0 / Q4_0 weights: f32 d, i8 q[32] (36 B) */
 } jero_quant;
@@ -121,10 +122,11 @@ int jero_hip_gemm_i8(const int8_t *x_dev, int64_t m, int64_t k, const int8_t *w_
                      void *stream);
 
 /* Load-time re-layout of a weight tensor for the GEMV kernels; replaces repack_tensor_parallel
- * (src/weights.rs:914-955) -> RepackedWeight.  Q6_K -> JERO_Q6_K_R: the n_out x n_in tensor's
- * bytes are regrouped into 16-byte aligned planes of the same total size (src and dst may not
- * overlap).  The result is passed to jero_hip_matvec / _partials / _vec_dot as quant
- * JERO_Q6_K_R with the same n_in and n_out; it must be used whole (its rows are not contiguous).
+ * (src/weights.rs:914-955) -> RepackedWeight.  Q4_K -> JERO_Q4_K_R and Q6_K -> JERO_Q6_K_R:
+ * the n_out x n_in tensor's bytes are regrouped into 16-byte aligned planes of the same total
+ * size (src and dst may not overlap).  The result is passed to jero_hip_matvec / _partials /
+ * _vec_dot as the returned quant with the same n_in and n_out and computes exactly what the
+ * GGUF tensor computes; it must be used whole (its rows are not contiguous).
  * Other formats: CapabilityMismatch. */
 int jero_hip_repack(int quant, const void *src_dev, size_t src_bytes, int64_t n_in, int64_t n_out,
                     void *dst_dev, int *dst_quant, void *stream);

@@ -14,7 +14,7 @@ constexpr int kDecodeMaxActBlocks = 8;  // activation blocks per wave in the pro
 enum { kOutStore = 0, kOutResid = 1, kOutSwiglu = 2, kOutArgmax = 3 };
 
 struct DGemvArgs {
-  const uint8_t* w;   // weight rows (GGUF layout, or Q6_K_R planes)
+  const uint8_t* w;   // weight rows (GGUF layout, or Q4_K_R / Q6_K_R planes)
   int64_t rb;         // bytes per row (GGUF layouts)
   int U;              // units per row
   int64_t N;          // rows of the tensor
@@ -38,7 +38,7 @@ struct DGemvArgs {
 // number of argmax partials an argmax launch leaves in amax_v / amax_i.
 int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s, int* blocks = nullptr);
 // rmsnorm(x) . [W1; W2] into y[0, N + N2) for two K-quant tensors of different formats sharing
-// n_in = K <= 4096 (Q4_K with Q6_K_R, either order): one launch, one prologue.
+// n_in = K <= 4096 (Q4_K_R with Q6_K_R, either order): one launch, one prologue.
 int launch_dgemv_dual(int quant1, int quant2, const DGemvArgs& a, hipStream_t s);
 // Longest row the fused decode GEMV takes for a weight format.
 int dgemv_max_k(int quant);

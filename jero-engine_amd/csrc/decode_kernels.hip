@@ -198,7 +198,7 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
 #pragma unroll
       for (int t = 0; t < UPL; t++) {
         const int u = min(c + LPR * t, U - 1);
-        if constexpr (F == JERO_Q6_K_R)
+        if constexpr (is_planar(F))
           Ut::load_w_planar(wt[r][t], a.w, N, U, row, u);
         else
           Ut::load_w(wt[r][t], a.w + row * a.rb, u);
@@ -327,7 +327,7 @@ __device__ __forceinline__ void load_row_units(const uint8_t* __restrict__ w, in
 #pragma unroll
   for (int t = 0; t < UPL; t++) {
     const int u = min(c + 64 * t, U - 1);
-    if constexpr (F == JERO_Q6_K_R)
+    if constexpr (is_planar(F))
       Unit<F>::load_w_planar(wt[t], w, N, U, row, u);
     else
       Unit<F>::load_w(wt[t], w + row * rb, u);
@@ -549,8 +549,10 @@ int dgemv_fmt(const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t s) {
 
 template <int OUT>
 int dgemv_out(int quant, const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t s) {
+  // K-quant matrices reach the decode step in their planar layouts (the model re-lays them out
+  // at finalize); raw Q6_K remains for tensors the caller hands over unconverted
   switch (quant) {
-    case JERO_Q4_K: return dgemv_fmt<JERO_Q4_K, OUT>(a, rows_or_pairs, s);
+    case JERO_Q4_K_R: return dgemv_fmt<JERO_Q4_K_R, OUT>(a, rows_or_pairs, s);
     case JERO_Q6_K: return dgemv_fmt<JERO_Q6_K, OUT>(a, rows_or_pairs, s);
     case JERO_Q6_K_R: return dgemv_fmt<JERO_Q6_K_R, OUT>(a, rows_or_pairs, s);
     case JERO_Q8_0: return dgemv_fmt<JERO_Q8_0, OUT>(a, rows_or_pairs, s);
@@ -587,12 +589,12 @@ int launch_dgemv_dual(int quant1, int quant2, const DGemvArgs& a0, hipStream_t s
   const int xb = xb_for(JERO_Q4_K, a.K);
 #define JERO_DUAL(Q1, Q2, XBV)                                                                            \
   hipLaunchKernelGGL((dgemv_dual_kernel<Q1, Q2, 1, XBV>), dim3(unsigned(blocks)), dim3(kDecodeThreads), shm, s, a)
-  if (quant1 == JERO_Q4_K && quant2 == JERO_Q6_K_R) {
-    if (xb <= 1) JERO_DUAL(JERO_Q4_K, JERO_Q6_K_R, 1);
-    else JERO_DUAL(JERO_Q4_K, JERO_Q6_K_R, 2);
-  } else if (quant1 == JERO_Q6_K_R && quant2 == JERO_Q4_K) {
-    if (xb <= 1) JERO_DUAL(JERO_Q6_K_R, JERO_Q4_K, 1);
-    else JERO_DUAL(JERO_Q6_K_R, JERO_Q4_K, 2);
+  if (quant1 == JERO_Q4_K_R && quant2 == JERO_Q6_K_R) {
+    if (xb <= 1) JERO_DUAL(JERO_Q4_K_R, JERO_Q6_K_R, 1);
+    else JERO_DUAL(JERO_Q4_K_R, JERO_Q6_K_R, 2);
+  } else if (quant1 == JERO_Q6_K_R && quant2 == JERO_Q4_K_R) {
+    if (xb <= 1) JERO_DUAL(JERO_Q6_K_R, JERO_Q4_K_R, 1);
+    else JERO_DUAL(JERO_Q6_K_R, JERO_Q4_K_R, 2);
   } else {
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: no two-tensor GEMV for this format pair");
   }

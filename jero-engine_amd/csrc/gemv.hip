@@ -59,7 +59,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const uint8_t* __res
 #pragma unroll
     for (int t = 0; t < UPL; t++) {
       const int u = min(c + LPR * t, U - 1);
-      if constexpr (F == JERO_Q6_K_R)
+      if constexpr (is_planar(F))
         Ut::load_w_planar(wt[r][t], w, N, U, row, u);
       else
         Ut::load_w(wt[r][t], w + row * rb, u);
@@ -198,6 +198,25 @@ int launch_fmt(const uint8_t* w, int64_t k, int64_t N, const uint8_t* xq, float*
   return check_launch("matvec");
 }
 
+// Regroups Q4_K blocks into the JERO_Q4_K_R row runs (one thread per block).
+__global__ void __launch_bounds__(256) repack_q4k_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                         int64_t N, int nb) {
+  int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= N * nb) return;
+  const int U = 4 * nb;
+  const int b = int(t % nb);
+  const uint8_t* s = src + t * 144;
+  uint8_t* row = dst + (t / nb) * (int64_t(nb) * 144);
+  for (int i = 0; i < 16; i++) row[U * 32 + b * 16 + i] = s[i];
+  for (int q = 0; q < 4; q++) {
+    const int u = 4 * b + q;
+    for (int i = 0; i < 16; i++) {
+      row[u * 16 + i] = s[16 + 32 * q + i];
+      row[U * 16 + u * 16 + i] = s[32 + 32 * q + i];
+    }
+  }
+}
+
 // Regroups Q6_K blocks into the JERO_Q6_K_R planes (one thread per block).
 __global__ void __launch_bounds__(256) repack_q6k_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
                                                          int64_t N, int nb) {
@@ -230,7 +249,7 @@ __global__ void __launch_bounds__(256) repack_q6k_kernel(const uint8_t* __restri
 }  // namespace
 
 int max_gemv_k(int quant) {
-  return 64 * 8 * ((quant == JERO_Q4_K || quant == JERO_Q6_K || quant == JERO_Q6_K_R) ? 64 : 32);
+  return 64 * 8 * int(64 / units_per_row(quant, 64));  // 64 lanes x 8 units of 64 or 32 elements
 }
 
 int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, int64_t n_out, const void* xq,
@@ -250,8 +269,8 @@ int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, in
                                                   std::to_string(max_gemv_k(quant)));
   if (!aligned4(w) || !aligned4(xq) || !aligned4(y))
     return fail(JERO_ERR_INVALID_ARGUMENT, "matvec: weights, activations and output must be 4-byte aligned");
-  if (quant == JERO_Q6_K_R && (reinterpret_cast<uintptr_t>(w) & 15u))
-    return fail(JERO_ERR_INVALID_ARGUMENT, "matvec: Q6_K_R planes must be 16-byte aligned");
+  if (is_planar(quant) && (reinterpret_cast<uintptr_t>(w) & 15u))
+    return fail(JERO_ERR_INVALID_ARGUMENT, "matvec: Q4_K_R / Q6_K_R planes must be 16-byte aligned");
   return JERO_OK;
 }
 
@@ -262,6 +281,7 @@ int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const v
   if (part) {
     switch (quant) {
       case JERO_Q4_K: return launch_fmt<JERO_Q4_K, true>(wb, n_in, n_out, xb, y, part, s);
+      case JERO_Q4_K_R: return launch_fmt<JERO_Q4_K_R, true>(wb, n_in, n_out, xb, y, part, s);
       case JERO_Q6_K: return launch_fmt<JERO_Q6_K, true>(wb, n_in, n_out, xb, y, part, s);
       case JERO_Q6_K_R: return launch_fmt<JERO_Q6_K_R, true>(wb, n_in, n_out, xb, y, part, s);
       case JERO_Q8_0: return launch_fmt<JERO_Q8_0, true>(wb, n_in, n_out, xb, y, part, s);
@@ -270,6 +290,7 @@ int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const v
   } else {
     switch (quant) {
       case JERO_Q4_K: return launch_fmt<JERO_Q4_K, false>(wb, n_in, n_out, xb, y, nullptr, s);
+      case JERO_Q4_K_R: return launch_fmt<JERO_Q4_K_R, false>(wb, n_in, n_out, xb, y, nullptr, s);
       case JERO_Q6_K: return launch_fmt<JERO_Q6_K, false>(wb, n_in, n_out, xb, y, nullptr, s);
       case JERO_Q6_K_R: return launch_fmt<JERO_Q6_K_R, false>(wb, n_in, n_out, xb, y, nullptr, s);
       case JERO_Q8_0: return launch_fmt<JERO_Q8_0, false>(wb, n_in, n_out, xb, y, nullptr, s);
@@ -281,14 +302,19 @@ int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const v
 
 int launch_repack(int quant, const void* src, int64_t n_in, int64_t n_out, void* dst, int* dst_quant,
                   hipStream_t s) {
-  if (quant != JERO_Q6_K)
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, "repack: only Q6_K has a device layout (got " +
+  if (quant != JERO_Q4_K && quant != JERO_Q6_K)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "repack: only Q4_K and Q6_K have a device layout (got " +
                                                   std::to_string(quant) + ")");
   int nb = int(n_in / 256);
   int64_t blocks = n_out * nb;
-  hipLaunchKernelGGL(repack_q6k_kernel, dim3(unsigned((blocks + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), n_out, nb);
-  if (dst_quant) *dst_quant = JERO_Q6_K_R;
+  const dim3 grid(unsigned((blocks + 255) / 256));
+  if (quant == JERO_Q4_K)
+    hipLaunchKernelGGL(repack_q4k_kernel, grid, dim3(256), 0, s, static_cast<const uint8_t*>(src),
+                       static_cast<uint8_t*>(dst), n_out, nb);
+  else
+    hipLaunchKernelGGL(repack_q6k_kernel, grid, dim3(256), 0, s, static_cast<const uint8_t*>(src),
+                       static_cast<uint8_t*>(dst), n_out, nb);
+  if (dst_quant) *dst_quant = quant == JERO_Q4_K ? JERO_Q4_K_R : JERO_Q6_K_R;
   return check_launch("repack");
 }
 

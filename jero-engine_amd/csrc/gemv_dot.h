@@ -96,6 +96,26 @@ struct Unit<JERO_Q4_K> {
   }
 };
 
+// ---------------------------------------------------------------- Q4_K, planar device layout
+// JERO_Q4_K_R keeps each row of a Q4_K tensor (nb blocks, U = 4 nb units of 64 elements) in
+// its own 144 nb bytes, regrouped into three runs, so that each 16-byte load instruction of a
+// wave reads one contiguous kilobyte (the GGUF layout spreads a wave's loads over every line
+// of its blocks) while a row stays one contiguous range:
+//   row = q0 [U][16] | q1 [U][16] | h [nb][16]
+//   q0[u] = qs[32i .. 32i+16), q1[u] = qs[32i+16 .. 32i+32) of block b (unit u = 4b+i);
+//   h[b] = d, dmin, scales[12] (the block's first 16 bytes).
+// Same size as the GGUF tensor; the dot product is Unit<Q4_K>'s.
+template <>
+struct Unit<JERO_Q4_K_R> : Unit<JERO_Q4_K> {
+  static __device__ __forceinline__ void load_w_planar(W& w, const uint8_t* __restrict__ base, int64_t /*N*/, int U,
+                                                       int64_t row, int u) {
+    const uint8_t* rp = base + row * (int64_t(U) * 36);
+    w.q0 = ld4(rp + u * 16);
+    w.q1 = ld4(rp + U * 16 + u * 16);
+    w.h = ld4(rp + U * 32 + (u >> 2) * 16);
+  }
+};
+
 // ---------------------------------------------------------------- Q6_K x Q8_K
 template <>
 struct Unit<JERO_Q6_K> {
@@ -316,8 +336,9 @@ struct Unit<JERO_Q4_0> {
 };
 
 // Units per row and partial sums per row of a weight format.
+__host__ __device__ constexpr bool is_planar(int f) { return f == JERO_Q4_K_R || f == JERO_Q6_K_R; }
 __host__ __device__ constexpr int units_per_row(int f, int64_t k) {
-  return int(k / ((f == JERO_Q4_K || f == JERO_Q6_K || f == JERO_Q6_K_R) ? 64 : 32));
+  return int(k / ((f == JERO_Q4_K || f == JERO_Q4_K_R || f == JERO_Q6_K || f == JERO_Q6_K_R) ? 64 : 32));
 }
 __host__ __device__ constexpr int64_t partials_per_row(int f, int64_t k) {
   return (f == JERO_Q6_K || f == JERO_Q6_K_R) ? k / 16 : k / 32;

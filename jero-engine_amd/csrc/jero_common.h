@@ -27,6 +27,7 @@ __host__ __device__ constexpr FmtInfo fmt_info(int q) {
   return q == JERO_Q8_0     ? FmtInfo{32, 34}
          : q == JERO_Q4_0   ? FmtInfo{32, 18}
          : q == JERO_Q4_K   ? FmtInfo{256, 144}
+         : q == JERO_Q4_K_R ? FmtInfo{256, 144}
          : q == JERO_Q6_K   ? FmtInfo{256, 210}
          : q == JERO_Q6_K_R ? FmtInfo{256, 210}
          : q == JERO_Q8_K   ? FmtInfo{256, 292}

@@ -7,7 +7,8 @@
 //
 // Weights are uploaded once (set_tensor) and regrouped once (finalize): Q|K|V rows become one
 // tensor when they share a format, gate and up rows one tensor (rows [0, ffn) gate, [ffn, 2ffn)
-// up) so one kernel produces silu(gate) * up, and every Q6_K matrix is re-laid out as Q6_K_R.
+// up) so one kernel produces silu(gate) * up, and every Q4_K / Q6_K matrix is re-laid out in
+// its planar device layout (Q4_K_R / Q6_K_R).
 // The step itself only enqueues kernels -- no allocation, copy or memset -- so it can be captured
 // in a HIP graph.  Token and position live in device memory: the step reads them, and its last
 // kernel stores the greedy token and advances the position, so replaying the graph decodes
@@ -169,14 +170,14 @@ static int concat_rows(jero_model* m, std::vector<DevTensor*> parts, DevTensor& 
   return JERO_OK;
 }
 
-// Q6_K tensors become Q6_K_R (same bytes, aligned planes).
-static int repack_if_q6k(jero_model* m, DevTensor& t) {
-  if (t.quant != JERO_Q6_K) return JERO_OK;
+// Q4_K / Q6_K tensors become Q4_K_R / Q6_K_R (same bytes, aligned planes).
+static int repack_planar(jero_model* m, DevTensor& t) {
+  if (t.quant != JERO_Q4_K && t.quant != JERO_Q6_K) return JERO_OK;
   void* p = nullptr;
   int rc = dev_alloc(m, t.bytes, &p);
   if (rc) return rc;
   int q = 0;
-  rc = launch_repack(JERO_Q6_K, t.dev, t.n_in, t.n_out, p, &q, nullptr);
+  rc = launch_repack(t.quant, t.dev, t.n_in, t.n_out, p, &q, nullptr);
   if (rc) return rc;
   rc = check_hip(hipDeviceSynchronize(), "repack");
   if (rc) return rc;
@@ -338,17 +339,17 @@ extern "C" int jero_hip_model_finalize(jero_model* m) {
     l.v_separate = l.wv.quant != l.wq.quant;
     if (l.v_separate) {
       if ((rc = concat_rows(m, {&l.wq, &l.wk}, l.qkv))) return rc;
-      if ((rc = repack_if_q6k(m, l.wv))) return rc;
+      if ((rc = repack_planar(m, l.wv))) return rc;
     } else {
       if ((rc = concat_rows(m, {&l.wq, &l.wk, &l.wv}, l.qkv))) return rc;
     }
-    if ((rc = repack_if_q6k(m, l.qkv))) return rc;
+    if ((rc = repack_planar(m, l.qkv))) return rc;
     if ((rc = concat_rows(m, {&l.gate, &l.up}, l.gate_up))) return rc;
-    if ((rc = repack_if_q6k(m, l.gate_up))) return rc;
-    if ((rc = repack_if_q6k(m, l.wo))) return rc;
-    if ((rc = repack_if_q6k(m, l.down))) return rc;
+    if ((rc = repack_planar(m, l.gate_up))) return rc;
+    if ((rc = repack_planar(m, l.wo))) return rc;
+    if ((rc = repack_planar(m, l.down))) return rc;
   }
-  if ((rc = repack_if_q6k(m, m->output))) return rc;
+  if ((rc = repack_planar(m, m->output))) return rc;
   m->finalized = true;
   return JERO_OK;
 }
@@ -397,8 +398,8 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
     const LayerW& l = m->layers[size_t(L)];
     // attention sublayer: RMSNorm -> Q|K|V
     const bool dual = l.v_separate && l.qkv.n_in <= 4096 &&
-                      ((l.qkv.quant == JERO_Q4_K && l.wv.quant == JERO_Q6_K_R) ||
-                       (l.qkv.quant == JERO_Q6_K_R && l.wv.quant == JERO_Q4_K));
+                      ((l.qkv.quant == JERO_Q4_K_R && l.wv.quant == JERO_Q6_K_R) ||
+                       (l.qkv.quant == JERO_Q6_K_R && l.wv.quant == JERO_Q4_K_R));
     if (dual) {  // Q|K and V of different formats in one launch
       DGemvArgs a{};
       a.w = static_cast<const uint8_t*>(l.qkv.dev);

@@ -33,6 +33,7 @@ int act_format(int weight_quant) {
     case JERO_Q8_0:
     case JERO_Q4_0: return JERO_ACT_Q8;
     case JERO_Q4_K:
+    case JERO_Q4_K_R:
     case JERO_Q6_K:
     case JERO_Q6_K_R: return JERO_Q8_K;
     default: return -1;

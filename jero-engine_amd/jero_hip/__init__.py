@@ -15,10 +15,10 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.normpath(os.path.join(HERE, "..", "libjero_hip.so"))
 
-F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, ACT_Q8, Q6_K_R = 0, 1, 2, 8, 12, 14, 15, 100, 114
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, ACT_Q8, Q4_K_R, Q6_K_R = 0, 1, 2, 8, 12, 14, 15, 100, 112, 114
 Q4_K_M = Q4_K  # the reference's QuantType::Q4_K_M names the Q4_K block format
 QUANT_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_K: "Q8_K",
-               ACT_Q8: "ACT_Q8", Q6_K_R: "Q6_K_R"}
+               ACT_Q8: "ACT_Q8", Q4_K_R: "Q4_K_R", Q6_K_R: "Q6_K_R"}
 KV_F32, KV_F16 = 0, 1
 
 OK = 0
@@ -261,7 +261,7 @@ def vec_dot_q6_k(out, weights, inp, **kw):
 
 def repack(weights, stream=None):
     """Load-time re-layout (repack_tensor_parallel, src/weights.rs:914-955): returns a new
-    TensorView in the device layout (Q6_K -> Q6_K_R, same byte count)."""
+    TensorView in the device layout (Q4_K -> Q4_K_R, Q6_K -> Q6_K_R, same byte count)."""
     import torch
     dst = torch.empty(weights.nbytes(), dtype=torch.uint8, device=weights.data.device)
     q = C.c_int(0)

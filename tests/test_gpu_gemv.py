@@ -157,8 +157,34 @@ def test_q6_k_repacked_layout_is_bitwise_identical(dev, n_in, n_out):
         assert rel_err(yr.cpu().numpy(), ref) < REL_TOL
 
 
+@pytest.mark.parametrize("n_in,n_out", [(4096, 4096), (4096, 12288), (12288, 4096), (768, 2048), (2304, 7),
+                                        (256, 1)])
+def test_q4_k_repacked_layout_is_bitwise_identical(dev, n_in, n_out):
+    """The planar Q4_K_R layout computes exactly what the raw GGUF Q4_K path computes."""
+    print(f"q4k_r n_in={n_in} n_out={n_out}", flush=True)
+    w = rand_weights(J.Q4_K, n_out, n_in, 700 + n_in + n_out, full_range=True)
+    W = J.TensorView("blk.0.ffn_up.weight", J.Q4_K, [n_in, n_out], to_dev(w, dev))
+    Wr = J.repack(W)
+    assert Wr.quant == J.Q4_K_R and Wr.nbytes() == W.nbytes()
+    x = rand_act(n_in, 701)
+    xq = to_dev(O.quantize_act(J.Q8_K, x), dev)
+    y, yr = (torch.empty(n_out, dtype=torch.float32, device=dev) for _ in range(2))
+    J.matvec(W, xq, y)
+    J.matvec(Wr, xq, yr)
+    if n_out <= 4096:
+        pp = n_in // 32
+        part = torch.empty((n_out, pp), dtype=torch.int32, device=dev)
+        J.matvec_partials(Wr, xq, torch.empty_like(yr), part)
+    torch.cuda.synchronize()
+    assert torch.equal(y, yr)
+    if n_out <= 4096:
+        np.testing.assert_array_equal(part.cpu().numpy(), O.partials(J.Q4_K, w, n_in, n_out, O.quantize_act(J.Q8_K, x)))
+        ref = O.matvec_f64(J.Q4_K, w, n_in, n_out, O.quantize_act(J.Q8_K, x))
+        assert rel_err(yr.cpu().numpy(), ref) < REL_TOL
+
+
 def test_repack_rejects_other_formats(dev):
-    W = J.TensorView("w", J.Q4_K, [256, 4], torch.zeros(4 * 144, dtype=torch.uint8, device=dev))
+    W = J.TensorView("w", J.Q8_0, [256, 4], torch.zeros(4 * 8 * 34, dtype=torch.uint8, device=dev))
     with pytest.raises(J.K3Error) as ei:
         J.repack(W)
     assert ei.value.variant == "CapabilityMismatch"

@@ -4,8 +4,9 @@ Golden llama Q8_0 fixture: first-token logits within 1e-4 and the greedy ids, as
 reference's own certification (tests/architecture_certification_gate.rs:305).
 
 Random Qwen3-shaped models against the oracle's decode step, per step:
-  * cosine similarity of the logit vectors >= 0.99999 (the reference certifies at 0.9999,
-    src/certification.rs:240-318);
+  * cosine similarity of the logit vectors >= 0.9999, the reference's certification floor
+    (verify_parity_against_golden, src/certification.rs:240-318, exercised at 0.9999 in :950),
+    and >= 0.99999 on average over the steps;
   * the greedy token equals the oracle's argmax whenever the oracle's top-2 gap exceeds
     1e-2 of the logits' rms;
   * max elementwise error <= 2e-2 of max(|ref|, rms(ref)), and <= 1e-3 on at least 3/4 of the
@@ -111,6 +112,7 @@ def test_decode_matches_oracle(dev, kv_name, cap, prefill, steps):
 def run_steps(m, om, kv, spec, cap, prefill, steps, kv_dtype, dev, tok=17, strict_fraction=True):
     logits = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
     over = 0
+    coss = []
     m.set_position(tok, prefill)
     for i in range(steps):
         pos = prefill + i
@@ -123,7 +125,8 @@ def run_steps(m, om, kv, spec, cap, prefill, steps, kv_dtype, dev, tok=17, stric
         got = logits.cpu().numpy()
         err, cs = rel_err(got, ref), cosine(got, ref)
         print(f"  pos {pos}: rel err {err:.2e} cos {cs:.8f}", flush=True)
-        assert cs >= 0.99999, (pos, cs)
+        assert cs >= 0.9999, (pos, cs)
+        coss.append(cs)
         assert err < 2e-2, (pos, err)
         over += err >= 1e-3
         gtok, gpos = m.read_token_pos()
@@ -133,7 +136,8 @@ def run_steps(m, om, kv, spec, cap, prefill, steps, kv_dtype, dev, tok=17, stric
         if top2[1] - top2[0] > 1e-2 * scale:
             assert gtok == int(np.argmax(ref)), (pos, gtok, int(np.argmax(ref)))
         tok = gtok if gtok >= 0 else 0  # the oracle follows the device's token
-    print(f"  steps above 1e-3: {over} of {steps}", flush=True)
+    print(f"  steps above 1e-3: {over} of {steps}; mean cos {np.mean(coss):.8f}", flush=True)
+    assert np.mean(coss) >= 0.99999, np.mean(coss)
     if strict_fraction:
         assert over <= max(2, steps // 5), over
 

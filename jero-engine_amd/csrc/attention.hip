@@ -110,14 +110,16 @@ __device__ __forceinline__ void ld_floats(float (&dst)[N], const float* __restri
 
 // Split-K partial of one decode token's attention.  Workgroup (split s, kv head h) owns the
 // 64 slots [64 s, 64 s + 64) and every q head of h's group; each of its four waves treats 16 of
-// those slots as a sub-split of its own and the workgroup merges the four at the end, so the
-// whole pipeline has one workgroup barrier.
+// those slots as a sub-split of its own and the workgroup merges the four at the end.
 //   * All global loads go out first, unconditionally (clamped in-bounds addresses): the q
 //     heads, the fused-mode extras and the wave's K and V rows, 16 bytes per lane.
 //   * K layout: lane = (position kp, chunk kc); each position's CPR chunk lanes hold the q heads'
-//     matching chunks, so scores are a DPP sum over CPR consecutive lanes.  q is normalised
-//     and rotated in registers by the same lanes (the head's sum of squares is the same sum).
-//   * The wave's softmax (max, exp, sum over its 16 positions) is a whole-wave DPP reduction.
+//     matching chunks, so scores are a DPP sum over CPR consecutive lanes.  In fused mode each q
+//     head is normalised and rotated once per workgroup, by one wave in the same layout (the head's sum
+//     of squares is the same DPP sum), and shared through LDS; that barrier waits for LDS only,
+//     so the K/V rows stay in flight.
+//   * The wave's softmax (max, exp, sum over its 16 positions) reduces across the position
+//     groups only: a position's score is already in all of its chunk lanes.
 //   * V layout: lane = (chunk vc, position vp) with the PPL positions of a load in consecutive
 //     lanes, so P V sums over positions with DPP as well; the numerators move from the K
 //     layout to the V layout through the wave's own LDS rows (no barrier).
@@ -134,6 +136,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   constexpr int G4 = (MAXG + 3) / 4;         // float4s per position row of numerators
   static_assert(NL >= 1 && NL * PPL == WPOS && CPR <= 32, "tile shape");
 
+  __shared__ float s_q[MAXG][HD];
   __shared__ float4 s_p[NW][WPOS][G4];
   __shared__ float s_o[NW][MAXG][HD];
   __shared__ float s_m[NW][MAXG], s_l[NW][MAXG];
@@ -148,11 +151,15 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   const int kc = lane % CPR, kp = lane / CPR;
   const int vp = lane % PPL, vc = lane / PPL;
 
-  // 0. loads
-  float q[MAXG][EPL];
+  // 0. loads.  Fused: wave w prepares q heads w, w + NW, ... and the workgroup shares them
+  //    through LDS; otherwise every wave loads all of its q heads (only the scale to apply).
+  constexpr int HPW = FUSED ? (MAXG + NW - 1) / NW : MAXG;
+  float qw[HPW][EPL];
 #pragma unroll
-  for (int h = 0; h < MAXG; h++)
-    ld_floats<EPL>(q[h], p.q + (int64_t(kh) * group + min(h, group - 1)) * HD + kc * EPL);
+  for (int j = 0; j < HPW; j++) {
+    const int h = FUSED ? wv + NW * j : j;
+    ld_floats<EPL>(qw[j], p.q + (int64_t(kh) * group + min(h, group - 1)) * HD + kc * EPL);
+  }
   int64_t pos_pre = p.pos;
   float kn[EPL], vn[EPL], qnw[EPL], knw[EPL], csr[EPL];
   if constexpr (FUSED) {
@@ -196,7 +203,8 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   }
   const int p1 = min(p0 + CH, active);
 
-  // 1. q heads (fused: QK-norm and RoPE, also of the new k), scale folded into q
+  // 1. q heads (fused: QK-norm and RoPE, also of the new k in the workgroup that holds its
+  //    slot), scale folded into q; each head is prepared by one wave and shared through LDS
   if constexpr (FUSED) {
     float2 cs[EPL / 2];
 #pragma unroll
@@ -210,13 +218,30 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
       }
     }
 #pragma unroll
-    for (int h = 0; h < MAXG; h++) norm_rope_chunk<HD, EPL>(q[h], p.q_norm != nullptr, qnw, p.eps, cs);
-    norm_rope_chunk<HD, EPL>(kn, p.k_norm != nullptr, knw, p.eps, cs);
+    for (int j = 0; j < HPW; j++) norm_rope_chunk<HD, EPL>(qw[j], p.q_norm != nullptr, qnw, p.eps, cs);
+    if (slot >= p0 && slot < p1) norm_rope_chunk<HD, EPL>(kn, p.k_norm != nullptr, knw, p.eps, cs);
   }
+  float q[MAXG][EPL];
+  if constexpr (FUSED) {
 #pragma unroll
-  for (int h = 0; h < MAXG; h++)
+    for (int j = 0; j < HPW; j++) {
+      const int h = wv + NW * j;
+      if (h < MAXG && kp == 0) {
 #pragma unroll
-    for (int e = 0; e < EPL; e++) q[h][e] *= p.scale;
+        for (int e = 0; e < EPL; e++) s_q[h][kc * EPL + e] = qw[j][e] * p.scale;
+      }
+    }
+    lds_barrier();  // LDS only: the K/V loads stay in flight
+#pragma unroll
+    for (int h = 0; h < MAXG; h++)
+#pragma unroll
+      for (int e = 0; e < EPL; e++) q[h][e] = s_q[h][kc * EPL + e];
+  } else {
+#pragma unroll
+    for (int h = 0; h < MAXG; h++)
+#pragma unroll
+      for (int e = 0; e < EPL; e++) q[h][e] = qw[h][e] * p.scale;
+  }
 
   // 2. scores of the wave's positions (K layout); masked slots score -inf
   float sc[NL][MAXG];
@@ -239,14 +264,17 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
     }
   }
 
-  // 3. the wave's softmax numerators, max and sum per head (uniform across the wave)
+  // 3. the wave's softmax numerators, max and sum per head (uniform across the wave).  A
+  //    position's score is already in all CPR of its lanes, so only the position groups
+  //    (lanes CPR apart) are reduced.
   float m[MAXG], l[MAXG];
 #pragma unroll
   for (int h = 0; h < MAXG; h++) {
     float mx = sc[0][h];
 #pragma unroll
     for (int i = 1; i < NL; i++) mx = fmaxf(mx, sc[i][h]);
-    mx = wave_max_dpp(mx);
+#pragma unroll
+    for (int off = CPR; off < kWave; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < NL; i++) {
@@ -254,8 +282,10 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
       sc[i][h] = e;
       sum += e;
     }
+#pragma unroll
+    for (int off = CPR; off < kWave; off <<= 1) sum += __shfl_xor(sum, off, kWave);
     m[h] = mx;
-    l[h] = wave_sum_dpp(kc == 0 ? sum : 0.f);  // one lane per position
+    l[h] = sum;
   }
   if (kc == 0) {
 #pragma unroll

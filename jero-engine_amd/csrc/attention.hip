@@ -475,6 +475,84 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restri
   }
 }
 
+// Merge for up to 256 splits (decode up to 16384 positions): one workgroup per q head, wave w
+// takes splits w, w + 4, ... (at most 64, one per lane).  Every load goes out at entry -- the
+// lane's (m, l) and, for each of the wave's splits, the partial rows' elements of the lane's
+// dims -- so the merge costs one round trip; the wave's max and sum are DPP reductions, the
+// split weights are broadcast with readlane, and one barrier merges the four waves.
+constexpr int kCombineSmallSplits = 256;
+
+template <int HD>
+__global__ void __launch_bounds__(256) attn_combine_small_kernel(const float* __restrict__ part_o,
+                                                                 const float* __restrict__ part_ml, int S,
+                                                                 float* __restrict__ out) {
+  constexpr int DPL = HD >= 64 ? HD / 64 : 1;  // dims per lane
+  constexpr int CHUNK = 16;                    // splits per batch of loads
+  __shared__ float s_o[4][HD];
+  __shared__ float s_ml[4][2];
+  const int h = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int ns = (S - wv + 3) / 4;  // splits of this wave
+  const float2* ml = reinterpret_cast<const float2*>(part_ml) + int64_t(h) * S;
+  const float* po = part_o + int64_t(h) * S * HD;
+  const int s_lane = min(wv + 4 * lane, S - 1);
+  const float2 e = ml[s_lane];
+  float o[DPL];
+#pragma unroll
+  for (int t = 0; t < DPL; t++) o[t] = 0.f;
+  // first batch of partial-row loads, issued before the (m, l) arithmetic
+  float v[CHUNK][DPL];
+#pragma unroll
+  for (int jj = 0; jj < CHUNK; jj++)
+#pragma unroll
+    for (int t = 0; t < DPL; t++)
+      v[jj][t] = po[int64_t(min(wv + 4 * jj, S - 1)) * HD + min(lane + 64 * t, HD - 1)];
+  const bool ok = lane < ns && e.y > 0.f;
+  const float M = wave_max_dpp(ok ? e.x : -INFINITY);
+  const float wgt = ok ? exp_fast(e.x - M) : 0.f;
+  const float L = wave_sum_dpp(wgt * e.y);
+  for (int j0 = 0; j0 < ns; j0 += CHUNK) {
+    if (j0 > 0) {
+#pragma unroll
+      for (int jj = 0; jj < CHUNK; jj++)
+#pragma unroll
+        for (int t = 0; t < DPL; t++)
+          v[jj][t] = po[int64_t(min(wv + 4 * (j0 + jj), S - 1)) * HD + min(lane + 64 * t, HD - 1)];
+    }
+    // Empty splits never wrote their rows (the workspace holds whatever was there, possibly
+    // NaN): their zero weight selects the row out of the sum instead of multiplying it.
+#pragma unroll
+    for (int jj = 0; jj < CHUNK; jj++) {
+      const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), j0 + jj));
+      const bool use = j0 + jj < ns && w != 0.f;
+#pragma unroll
+      for (int t = 0; t < DPL; t++) o[t] += use ? w * v[jj][t] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < DPL; t++)
+    if (lane + 64 * t < HD) s_o[wv][lane + 64 * t] = o[t];
+  if (lane == 0) {
+    s_ml[wv][0] = M;
+    s_ml[wv][1] = L;
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < HD; d += 256) {
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; w++)
+      if (s_ml[w][1] > 0.f) Mx = fmaxf(Mx, s_ml[w][0]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const bool live = s_ml[w][1] > 0.f;
+      const float c = live ? exp_fast(s_ml[w][0] - Mx) : 0.f;
+      num += live ? c * s_o[w][d] : 0.f;
+      den += c * s_ml[w][1];
+    }
+    out[int64_t(h) * HD + d] = num / den;
+  }
+}
+
 int attn_splits(int active, int hd) { return (active + attn_chunk(hd) - 1) / attn_chunk(hd); }
 
 size_t attn_workspace_bytes(int nq, int hd, int active) {
@@ -497,7 +575,10 @@ static void launch_partial(const AttnParams& p, int S, hipStream_t s) {
 template <int HD>
 static void launch_combine(const AttnParams& p, int S, float* out, hipStream_t s) {
   const int nq = p.nkv * p.group;
-  hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(nq), dim3(256), 0, s, p.part_o, p.part_ml, S, out);
+  if (S <= kCombineSmallSplits)
+    hipLaunchKernelGGL((attn_combine_small_kernel<HD>), dim3(nq), dim3(256), 0, s, p.part_o, p.part_ml, S, out);
+  else
+    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(nq), dim3(256), 0, s, p.part_o, p.part_ml, S, out);
 }
 
 int launch_attention(const AttnParams& p0, bool fused, float* out, hipStream_t s) {

@@ -239,18 +239,19 @@ MOE = dict(hidden=2048, experts=128, ffn=768, top_k=8)
 
 
 def bench_moe(torch, J, dev, stream, steps):
-    """Qwen3-MoE expert layer: H=2048, 128 experts of FFN 768 (gate/up Q4_K, down Q6_K), router
-    logits N(0,1), top-8; T=1 (decode) and T=64.  Two weight copies and 8 logit sets rotate, so the
-    experts read differ between launches.  Algorithmic bytes: the distinct routed experts' weights
-    (3.06 MB each) + activations."""
+    """Qwen3-MoE expert layer: H=2048, 128 experts of FFN 768 (gate/up Q4_K, down Q6_K, repacked
+    at load time), router logits N(0,1), top-8; T=1 (decode) and T=64.  Two weight copies and 8
+    logit sets rotate, so the experts read differ between launches.  Algorithmic bytes: the
+    distinct routed experts' weights (3.06 MB each) + activations."""
     H, E, F, k = MOE["hidden"], MOE["experts"], MOE["ffn"], MOE["top_k"]
     copies = 2
     gate = synth_weights(torch, J, J.Q4_K, H, E * F, copies, dev, 3100)
     up = synth_weights(torch, J, J.Q4_K, H, E * F, copies, dev, 3101)
     down = synth_weights(torch, J, J.Q6_K, F, E * H, copies, dev, 3102)
-    gv = [J.TensorView("ffn_gate_exps", J.Q4_K, [H, F, E], gate[c]) for c in range(copies)]
-    uv = [J.TensorView("ffn_up_exps", J.Q4_K, [H, F, E], up[c]) for c in range(copies)]
-    dv = [J.TensorView("ffn_down_exps", J.Q6_K, [F, H, E], down[c]) for c in range(copies)]
+    # the expert tensors in the load-time device layouts (Q4_K_R / Q6_K_R over all experts' rows)
+    gv = [J.repack(J.TensorView("ffn_gate_exps", J.Q4_K, [H, F, E], gate[c])) for c in range(copies)]
+    uv = [J.repack(J.TensorView("ffn_up_exps", J.Q4_K, [H, F, E], up[c])) for c in range(copies)]
+    dv = [J.repack(J.TensorView("ffn_down_exps", J.Q6_K, [F, H, E], down[c])) for c in range(copies)]
     per_expert = (J.row_bytes(J.Q4_K, H) * F * 2 + J.row_bytes(J.Q6_K, F) * H)
     g = torch.Generator(device=dev)
     g.manual_seed(3103)
@@ -278,7 +279,8 @@ def bench_moe(torch, J, dev, stream, steps):
                         "bytes": int(algo), "GB_s": round(algo / t / 1e9, 1),
                         "frac_hbm": round(algo / t / 1e9 / HBM_PEAK_GBS, 4)}
     out["workload"] = "Qwen3-MoE expert layer H=2048, E=128, F=768, top-8, gate/up Q4_K, down Q6_K"
-    del gate, up, down
+    out["weight_layout"] = "Q4_K_R / Q6_K_R (load-time repack of the GGUF expert tensors)"
+    del gate, up, down, gv, uv, dv
     return out
 
 

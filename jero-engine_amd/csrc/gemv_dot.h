@@ -94,6 +94,38 @@ struct Unit<JERO_Q4_K> {
     float d = h2f(w.h.x), dmin = h2f(w.h.x >> 16);
     return A.dx * (d * float(isum) - dmin * float(msum));
   }
+
+  // The unit unpacked once for dot products with several activation vectors (the same integer
+  // sums and float operations as dot, so the same bits).
+  struct Prep {
+    uint32_t v[16];  // nibbles of sub-block 2i (v[0..8)) and 2i+1 (v[8..16))
+    int sca, scb, ma, mb;
+    float d, dmin;
+  };
+  static __device__ __forceinline__ void prep(Prep& p, const W& w, int u) {
+    const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      p.v[t] = q[t] & 0x0F0F0F0Fu;
+      p.v[8 + t] = (q[t] >> 4) & 0x0F0F0F0Fu;
+    }
+    const int i = u & 3;
+    scale_min(w, uint32_t((2 * i) & 3), uint32_t(i >= 2), p.sca, p.ma);
+    scale_min(w, uint32_t((2 * i) & 3) + 1u, uint32_t(i >= 2), p.scb, p.mb);
+    p.d = h2f(w.h.x);
+    p.dmin = h2f(w.h.x >> 16);
+  }
+  static __device__ __forceinline__ float dot_prep(const Prep& p, const Act& A) {
+    int sa = 0, sb = 0;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      sa = dot4(p.v[t], A.a[t], sa);
+      sb = dot4(p.v[8 + t], A.a[8 + t], sb);
+    }
+    const int isum = p.sca * sa + p.scb * sb;
+    const int msum = p.ma * A.bsa + p.mb * A.bsb;
+    return A.dx * (p.d * float(isum) - p.dmin * float(msum));
+  }
 };
 
 // ---------------------------------------------------------------- Q4_K, planar device layout
@@ -207,6 +239,39 @@ struct Unit<JERO_Q6_K> {
     int c2 = int(int8_t(w.sc >> 16)), c3 = int(int8_t(w.sc >> 24));
     int isum = c0 * s0 + c1 * s1 + c2 * s2 + c3 * s3;
     return A.dx * h2f(w.dw >> w.dsh) * float(isum);
+  }
+
+  // The unit unpacked once for dot products with several activation vectors (same bits as dot).
+  struct Prep {
+    uint32_t v[16];  // v[4g + k]: 6-bit values of group g, dword k
+    int c[4];
+    float d;
+  };
+  static __device__ __forceinline__ void prep(Prep& p, const W& w, int /*u*/) {
+    const uint32_t lo[4] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w};
+    const uint32_t hi[4] = {w.hi.x, w.hi.y, w.hi.z, w.hi.w};
+    const uint32_t qh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      p.v[0 + k] = (lo[k] & 0x0F0F0F0Fu) | ((qh[k] & 0x03030303u) << 4);
+      p.v[4 + k] = (hi[k] & 0x0F0F0F0Fu) | ((qh[k] & 0x0C0C0C0Cu) << 2);
+      p.v[8 + k] = ((lo[k] >> 4) & 0x0F0F0F0Fu) | (qh[k] & 0x30303030u);
+      p.v[12 + k] = ((hi[k] >> 4) & 0x0F0F0F0Fu) | ((qh[k] >> 2) & 0x30303030u);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; g++) p.c[g] = int(int8_t(w.sc >> (8 * g)));
+    p.d = h2f(w.dw >> w.dsh);
+  }
+  static __device__ __forceinline__ float dot_prep(const Prep& p, const Act& A) {
+    int sg[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) sg[g] = dot4(p.v[4 * g + k], A.a[4 * g + k], sg[g]);
+    int isum = 0;
+#pragma unroll
+    for (int g = 0; g < 4; g++) isum += p.c[g] * (sg[g] - A.bs32[g]);
+    return A.dx * p.d * float(isum);
   }
 };
 

@@ -5,11 +5,12 @@
 // stacked [hidden, ffn, n_experts] tensors (:729-746) and run_single_swiglu_expert (:748-771).
 // The reference loops token by token and expert by expert; here the work is regrouped by
 // expert so that each selected expert's weights stream from HBM once for all of its tokens:
-//   1. route   (one workgroup): per token f32 softmax over all experts, top-k by (logit desc,
-//              index asc) with non-finite logits ranked last, renormalised weights; then the
-//              (token, slot) pairs are grouped by expert in ascending (token, slot) order, and
-//              the ascending list of active experts is written.
-//   2. quantize the T hidden vectors to Q8_K.
+//   1. route:  per token (one wave) f32 softmax over all experts, top-k by (logit desc, index
+//              asc) with non-finite logits ranked last, renormalised weights; the T hidden
+//              vectors are quantized to Q8_K alongside.
+//   2. group:  the (token, slot) pairs are grouped by expert in ascending (token, slot) order and
+//              the ascending list of active experts is written (one workgroup).  Few tokens run
+//              1 and 2 in one workgroup; many spread 1 over the GPU and group in a second launch.
 //   3. gate/up: one lane group per weight row; gate row f and up row f of an active expert
 //              sit side by side in one wave, loaded once, and are dotted with every token routed
 //              to that expert; act = silu(g) * u.
@@ -35,110 +36,109 @@ constexpr int kRouteLdsPairs = 8192;  // (token, slot) pairs grouped from LDS
 
 __device__ __forceinline__ bool better(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
 
-// PER = expert columns per lane (E <= 64 * PER).
+// Routes token t in one wave (PER = expert columns per lane, E <= 64 * PER): f32 softmax over
+// all experts, top-k by (logit desc, index asc) with non-finite logits last, renormalised
+// weights -> sel_idx / sel_w (and s_sel when given).
 template <int PER>
-__global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits, int T, int E,
-                                                                  int k, int32_t* __restrict__ sel_idx,
-                                                                  float* __restrict__ sel_w, MoeLists lists,
-                                                                  const float* __restrict__ x, int H,
-                                                                  uint8_t* __restrict__ xq) {
+__device__ __forceinline__ void route_token(const float* __restrict__ logits, int t, int E, int k,
+                                            int32_t* __restrict__ sel_idx, float* __restrict__ sel_w, int* s_sel) {
+  const int lane = threadIdx.x & 63;
+  const float* lt = logits + int64_t(t) * E;
+  float key[PER], prob[PER];
+  // all loads first, unconditional (clamped), then branch-free selects: a branch on a loaded
+  // value makes the load wait by itself
+  float lv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++) lv[i] = lt[min(lane + 64 * i, E - 1)];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const bool fin = (lane + 64 * i < E) & (fabsf(lv[i]) <= 3.402823466e38f);  // finite, not NaN
+    key[i] = fin ? lv[i] : -INFINITY;
+    mx = fmaxf(mx, key[i]);
+  }
+  mx = wave_max_dpp(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const bool fin = lane + 64 * i < E && key[i] != -INFINITY;
+    prob[i] = (fin && isfinite(mx)) ? expf(key[i] - mx) : 0.f;
+    sum += prob[i];
+  }
+  sum = wave_sum_dpp(sum);
+  const bool ok = sum > 0.f && isfinite(sum);
+#pragma unroll
+  for (int i = 0; i < PER; i++) prob[i] = ok ? prob[i] / sum : 1.0f / float(E);
+  // top-k rounds: the wave-wide best remaining key (DPP max), then its lowest expert index
+  // (the first column i, then the lowest lane, whose entry holds it); taken entries drop out
+  float ssum = 0.f;
+  int my_i = 0;  // lane j keeps selection j
+  float my_w = 0.f;
+  bool taken[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++) taken[i] = !(lane + 64 * i < E);
+  for (int j = 0; j < k; j++) {
+    float lb = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; i++) lb = taken[i] ? lb : fmaxf(lb, key[i]);
+    const float best = wave_max_dpp(lb);
+    int bi = -1;
+    float bp = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const uint64_t hit = __ballot(!taken[i] && key[i] == best);
+      if (bi < 0 && hit != 0) {
+        const int src = __builtin_ctzll(hit);
+        bi = src + 64 * i;
+        bp = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, prob[i]), src));
+        taken[i] = taken[i] || lane == src;
+      }
+    }
+    my_i = lane == j ? bi : my_i;
+    my_w = lane == j ? bp : my_w;
+    ssum += bp;
+  }
+  const bool sok = ssum > 0.f && isfinite(ssum);
+  if (lane < k) {
+    sel_idx[t * k + lane] = my_i;
+    sel_w[t * k + lane] = sok ? my_w / ssum : 1.0f / float(k);
+    if (s_sel && t * k + lane < kRouteLdsPairs) s_sel[t * k + lane] = my_i;
+  }
+}
+
+// LDS of the grouping step.
+struct GroupLds {
+  int count[kMaxExperts];
+  int off[kMaxExperts];
+  int fill[kMaxExperts];
+  int wsum[2 * (kRouteThreads / 64)];
+  __attribute__((aligned(16))) int sel[kRouteLdsPairs + 4];  // the selections, when they fit
+  int list[kRouteLdsPairs];                                   // pairs grouped by expert, atomic order
+};
+
+// Zeroes the per-expert counters (before a barrier that precedes group_pairs).
+__device__ __forceinline__ void group_init(GroupLds& g, int E) {
+  for (int e = threadIdx.x; e < E; e += kRouteThreads) {
+    g.count[e] = 0;
+    g.fill[e] = 0;
+  }
+}
+
+// Groups the n (token, slot) pairs by expert, in ascending pair order within an expert, and
+// writes the ascending list of active experts.  The selections are in g.sel when n fits, else in
+// sel_idx.  One workgroup of kRouteThreads threads; starts and ends with a barrier.
+__device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, int n, int E, MoeLists lists) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = kRouteThreads / 64;
-  __shared__ int s_count[kMaxExperts];
-  __shared__ int s_off[kMaxExperts];
-  __shared__ int s_wsum[2 * (kRouteThreads / 64)];
-  __shared__ __attribute__((aligned(16))) int s_sel[kRouteLdsPairs + 4];  // the selections, when they fit
-  // 0. the T hidden vectors to Q8_K (the gate/up input), one wave per 256-element block, when the
-  //    launcher passes xq (a few blocks; many tokens go through the parallel quantizer instead)
-  if (xq) {
-    const int bpr = H / 256, nblk = T * bpr;
-    for (int blk = wv; blk < nblk; blk += nw) {
-      const int t = blk / bpr, j = blk - t * bpr;
-      const float4 v = reinterpret_cast<const float4*>(x + int64_t(t) * H + int64_t(j) * 256)[lane];
-      const float e[4] = {v.x, v.y, v.z, v.w};
-      q8k_block_wave(e, lane, xq + int64_t(t) * bpr * 292 + int64_t(j) * 292);
-    }
-  }
-  // 1. routing, one wave per token
-  for (int t = wv; t < T; t += nw) {
-    const float* lt = logits + int64_t(t) * E;
-    float key[PER], prob[PER];
-    // all loads first, unconditional (clamped), then branch-free selects: a branch on a loaded
-    // value makes the load wait by itself
-    float lv[PER];
-#pragma unroll
-    for (int i = 0; i < PER; i++) lv[i] = lt[min(lane + 64 * i, E - 1)];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const bool fin = (lane + 64 * i < E) & (fabsf(lv[i]) <= 3.402823466e38f);  // finite, not NaN
-      key[i] = fin ? lv[i] : -INFINITY;
-      mx = fmaxf(mx, key[i]);
-    }
-    mx = wave_max_dpp(mx);
-    float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int e = lane + 64 * i;
-      bool fin = e < E && key[i] != -INFINITY;
-      prob[i] = (fin && isfinite(mx)) ? expf(key[i] - mx) : 0.f;
-      sum += prob[i];
-    }
-    sum = wave_sum_dpp(sum);
-    const bool ok = sum > 0.f && isfinite(sum);
-#pragma unroll
-    for (int i = 0; i < PER; i++) prob[i] = ok ? prob[i] / sum : 1.0f / float(E);
-    // top-k rounds: the wave-wide best remaining key (DPP max), then its lowest expert index
-    // (the first column i, then the lowest lane, whose entry holds it); taken entries drop out
-    float ssum = 0.f;
-    int my_i = 0;      // lane j keeps selection j
-    float my_w = 0.f;
-    bool taken[PER];
-#pragma unroll
-    for (int i = 0; i < PER; i++) taken[i] = !(lane + 64 * i < E);
-    for (int j = 0; j < k; j++) {
-      float lb = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < PER; i++)
-        if (!taken[i]) lb = fmaxf(lb, key[i]);
-      const float best = wave_max_dpp(lb);
-      int bi = -1;
-      float bp = 0.f;
-#pragma unroll
-      for (int i = 0; i < PER; i++) {
-        const uint64_t hit = __ballot(!taken[i] && key[i] == best);
-        if (bi < 0 && hit != 0) {
-          const int src = __builtin_ctzll(hit);
-          bi = src + 64 * i;
-          bp = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, prob[i]), src));
-          if (lane == src) taken[i] = true;
-        }
-      }
-      if (lane == j) {
-        my_i = bi;
-        my_w = bp;
-      }
-      ssum += bp;
-    }
-    const bool sok = ssum > 0.f && isfinite(ssum);
-    if (lane < k) {
-      sel_idx[t * k + lane] = my_i;
-      sel_w[t * k + lane] = sok ? my_w / ssum : 1.0f / float(k);
-      if (t * k + lane < kRouteLdsPairs) s_sel[t * k + lane] = my_i;
-    }
-  }
-  // 2. group the (token, slot) pairs by expert
-  for (int e = threadIdx.x; e < E; e += kRouteThreads) s_count[e] = 0;
-  const int n = T * k;
-  if (threadIdx.x < 4 && n + int(threadIdx.x) < kRouteLdsPairs + 4) s_sel[n + threadIdx.x] = -1;
+  if (threadIdx.x < 4 && n + int(threadIdx.x) < kRouteLdsPairs + 4) g.sel[n + threadIdx.x] = -1;
   __syncthreads();
   const bool in_lds = n <= kRouteLdsPairs;
-  for (int i = threadIdx.x; i < n; i += kRouteThreads) atomicAdd(&s_count[in_lds ? s_sel[i] : sel_idx[i]], 1);
+  for (int i = threadIdx.x; i < n; i += kRouteThreads) atomicAdd(&g.count[in_lds ? g.sel[i] : sel_idx[i]], 1);
   __syncthreads();
   {
     // exclusive scans of the counts (offsets) and of the active flags (active list), one thread
     // per expert: wave scans, then the 16 wave totals
     const int e = threadIdx.x;
-    const int c = e < E ? s_count[e] : 0, f = c > 0 ? 1 : 0;
+    const int c = e < E ? g.count[e] : 0, f = c > 0 ? 1 : 0;
     int ic = c, jf = f;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -149,18 +149,18 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
       }
     }
     if (lane == 63) {
-      s_wsum[wv] = ic;
-      s_wsum[nw + wv] = jf;
+      g.wsum[wv] = ic;
+      g.wsum[nw + wv] = jf;
     }
     __syncthreads();
     int bc = 0, bf = 0;
     for (int w = 0; w < wv; w++) {
-      bc += s_wsum[w];
-      bf += s_wsum[nw + w];
+      bc += g.wsum[w];
+      bf += g.wsum[nw + w];
     }
     if (e < E) {
       const int off_e = bc + ic - c;
-      s_off[e] = off_e;
+      g.off[e] = off_e;
       lists.offset[e] = off_e;
       if (f) lists.active[bf + jf - 1] = e;
       if (e == E - 1) {
@@ -170,24 +170,25 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
     }
   }
   __syncthreads();
-  // stable placement: thread e walks the pairs in order and keeps those routed to e
-  for (int e = threadIdx.x; e < E; e += kRouteThreads) {
-    if (s_count[e] == 0) continue;
-    int pos = s_off[e];
-    if (in_lds) {  // four selections per LDS read (s_sel is padded with -1 past n)
-      for (int i = 0; i < n; i += 4) {
-        const int4 v = *reinterpret_cast<const int4*>(&s_sel[i]);
-        const int vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          if (vv[q] == e) {
-            lists.entry[pos] = i + q;
-            lists.inv[i + q] = pos;
-            pos++;
-          }
-        }
-      }
-    } else {
+  if (in_lds) {
+    // stable placement in two parallel steps: each pair takes a slot of its expert's segment by
+    // an LDS atomic, then its final place is its rank among the segment's pairs (pairs ascend)
+    for (int i = threadIdx.x; i < n; i += kRouteThreads) {
+      const int e = g.sel[i];
+      g.list[g.off[e] + atomicAdd(&g.fill[e], 1)] = i;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kRouteThreads) {
+      const int e = g.sel[i], o = g.off[e], c = g.count[e];
+      int r = 0;
+      for (int q = 0; q < c; q++) r += g.list[o + q] < i ? 1 : 0;
+      lists.entry[o + r] = i;
+      lists.inv[i] = o + r;
+    }
+  } else {
+    // more pairs than LDS holds: thread e walks the selections in order and keeps those routed to e
+    for (int e = threadIdx.x; e < E; e += kRouteThreads) {
+      int pos = g.off[e];
       for (int i = 0; i < n; i++) {
         if (sel_idx[i] == e) {
           lists.entry[pos] = i;
@@ -199,12 +200,87 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
   }
 }
 
-constexpr int kMoeTokChunk = 16;         // activation rows of one expert staged in LDS per pass
+// Few tokens: one workgroup quantizes the hidden vectors to Q8_K (when xq is given; one wave per
+// 256-element block), routes (one wave per token) and groups.
+template <int PER>
+__global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits, int T, int E,
+                                                                  int k, int32_t* __restrict__ sel_idx,
+                                                                  float* __restrict__ sel_w, MoeLists lists,
+                                                                  const float* __restrict__ x, int H,
+                                                                  uint8_t* __restrict__ xq) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = kRouteThreads / 64;
+  __shared__ GroupLds g;
+  if (xq) {
+    const int bpr = H / 256, nblk = T * bpr;
+    for (int blk = wv; blk < nblk; blk += nw) {
+      const int t = blk / bpr, j = blk - t * bpr;
+      const float4 v = reinterpret_cast<const float4*>(x + int64_t(t) * H + int64_t(j) * 256)[lane];
+      const float e[4] = {v.x, v.y, v.z, v.w};
+      q8k_block_wave(e, lane, xq + int64_t(t) * bpr * 292 + int64_t(j) * 292);
+    }
+  }
+  group_init(g, E);
+  for (int t = wv; t < T; t += nw) route_token<PER>(logits, t, E, k, sel_idx, sel_w, g.sel);
+  group_pairs(g, sel_idx, T * k, E, lists);
+}
+
+// Many tokens, first step: workgroups [0, n_quant_wg) quantize the hidden vectors to Q8_K (one
+// wave per 256-element block), the others route one token per wave.  Spreading the routing over
+// many CUs matters: a single workgroup is bound by one CU's VALU issue at a few dozen tokens.
+template <int PER>
+__global__ void __launch_bounds__(256) moe_prep_kernel(const float* __restrict__ logits, int T, int E, int k,
+                                                       int32_t* __restrict__ sel_idx, float* __restrict__ sel_w,
+                                                       const float* __restrict__ x, int H, uint8_t* __restrict__ xq,
+                                                       int n_quant_wg) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (int(blockIdx.x) < n_quant_wg) {
+    const int bpr = H / 256, nblk = T * bpr;
+    for (int blk = int(blockIdx.x) * 4 + wv; blk < nblk; blk += n_quant_wg * 4) {
+      const int t = blk / bpr, j = blk - t * bpr;
+      const float4 v = reinterpret_cast<const float4*>(x + int64_t(t) * H + int64_t(j) * 256)[lane];
+      const float e[4] = {v.x, v.y, v.z, v.w};
+      q8k_block_wave(e, lane, xq + int64_t(t) * bpr * 292 + int64_t(j) * 292);
+    }
+  } else {
+    const int t = (int(blockIdx.x) - n_quant_wg) * 4 + wv;
+    if (t < T) route_token<PER>(logits, t, E, k, sel_idx, sel_w, nullptr);
+  }
+}
+
+// Many tokens, second step: one workgroup groups the selections.
+__global__ void __launch_bounds__(kRouteThreads) moe_group_kernel(const int32_t* __restrict__ sel_idx, int n, int E,
+                                                                  MoeLists lists) {
+  __shared__ GroupLds g;
+  group_init(g, E);
+  if (n <= kRouteLdsPairs)
+    for (int i = threadIdx.x; i < n; i += kRouteThreads) g.sel[i] = sel_idx[i];
+  group_pairs(g, sel_idx, n, E, lists);
+}
+
+constexpr int kMoeTokChunk = 8;          // activation rows of one expert staged in LDS per pass
 constexpr int64_t kMoeStageBytes = 49152;  // LDS for them
+
+// Waits for every global load in flight.  Ends a staging loop whose last LDS writes sit under a
+// lane condition: without it the loads feeding them look outstanding to the compiler on the path
+// that skips those writes, and it then waits at the next reuse of their registers (inside the
+// weight pipeline) instead.
+__device__ __forceinline__ void vm_settle() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// Unit u of row `row` of a stacked expert tensor of n_rows rows: GGUF bytes (rb per row) or a
+// planar layout (Q4_K_R / Q6_K_R, as written by jero_hip_repack over all n_rows rows).
+template <int F>
+__device__ __forceinline__ void load_unit(typename Unit<F>::W& w, const uint8_t* __restrict__ base, int64_t n_rows,
+                                          int U, int64_t rb, int64_t row, int u) {
+  if constexpr (is_planar(F))
+    Unit<F>::load_w_planar(w, base, n_rows, U, row, u);
+  else
+    Unit<F>::load_w(w, base + row * rb, u);
+}
 
 // Copies `n` activation rows of `rb` bytes (dword multiples) into LDS: row j comes from
 // src + rows[j] * rb, with rows[] already in LDS.  Eight unconditional (clamped) loads per thread
-// are in flight at a time.  Ends with a barrier.
+// are in flight at a time.  Ends with a barrier on LDS traffic (global loads issued before
+// the staging complete first anyway: their counter drains in order).
 __device__ __forceinline__ void stage_rows(uint32_t* __restrict__ dst, const uint8_t* __restrict__ src, int64_t rb,
                                            int n, const int* __restrict__ rows) {
   const int words = int(rb / 4), total = n * words;
@@ -222,12 +298,13 @@ __device__ __forceinline__ void stage_rows(uint32_t* __restrict__ dst, const uin
       if (idx < total) dst[idx] = v[q];
     }
   }
-  __syncthreads();
+  vm_settle();
+  lds_barrier();
 }
 
 // Quantizes n consecutive f32 rows (src rows row0 .. row0 + n, `cols` floats each) to Q8_K rows of
 // `qrb` bytes in LDS, one wave per 256-element block; each wave loads four blocks before
-// quantizing them.  Ends with a barrier.
+// quantizing them.  Ends with a barrier on LDS traffic.
 __device__ __forceinline__ void stage_quant_rows(uint8_t* __restrict__ dst, const float* __restrict__ src, int cols,
                                                  int64_t qrb, int n, int row0) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = int(blockDim.x) >> 6;
@@ -249,25 +326,33 @@ __device__ __forceinline__ void stage_quant_rows(uint8_t* __restrict__ dst, cons
       }
     }
   }
-  __syncthreads();
+  vm_settle();
+  lds_barrier();
 }
 
 // gate/up + SwiGLU.  A workgroup takes one active expert and 4 * ppw * P of its (gate, up) row
 // pairs: lane groups (2p, 2p+1) of a wave hold gate row and up row f.  The expert's token
-// activations are staged in LDS (kMoeTokChunk rows per pass), so each weight row is read from
-// HBM once and each activation once per workgroup; the next row pair's weights are in flight
-// while the current one is reduced over the tokens.
+// activations are staged in LDS (`chunk` rows per pass), so each weight row is read from HBM once
+// and each activation once per workgroup.  Two register buffers alternate: the next row pair's
+// weights are in flight while the current one is reduced over the tokens.  The loads are kept
+// where they are issued by three rules: no buffer is copied into the other (a copy waits for the
+// load), every path through the token loop uses the weights (the loop runs at least once, and
+// units past the row end are dotted clamped and then dropped by a select, never skipped by a
+// branch), and barriers wait on LDS only.
 template <int F, int LPR, int UPL>
 __global__ void __launch_bounds__(256) moe_gate_up_kernel(const uint8_t* __restrict__ gate,
-                                                          const uint8_t* __restrict__ up, int64_t rb, int U, int Fdim,
+                                                          const uint8_t* __restrict__ up, int64_t n_rows, int64_t rb,
+                                                          int U, int Fdim,
                                                           int k, const uint8_t* __restrict__ xq, int64_t xq_rb,
                                                           MoeLists lists, float* __restrict__ act, int ppw,
                                                           int wg_per_expert, int chunk) {
   using Ut = Unit<F>;
+  using W = typename Ut::W;
   constexpr int G = kWave / LPR;
   constexpr int P = G / 2;  // (gate, up) row pairs per wave pass
   static_assert(P >= 1, "gate/up pairing needs two lane groups per wave");
   extern __shared__ uint32_t s_x[];
+  __shared__ int s_rows[kMoeTokChunk];
   const int slot = int(blockIdx.x) / wg_per_expert, part = int(blockIdx.x) % wg_per_expert;
   if (slot >= *lists.n_active) return;  // uniform over the workgroup
   const int e = lists.active[slot];
@@ -275,62 +360,79 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(const uint8_t* __restr
   const int g = lane / LPR, c = lane % LPR;
   const bool is_up = g & 1;
   const int i0 = lists.offset[e], cnt = lists.offset[e + 1] - i0;
-  const int f0 = (part * 4 + wv) * ppw * P + g / 2;  // this lane group's first row pair
-  auto load_pair = [&](int it, typename Ut::W (&wt)[UPL]) {
+  const int rows_wg = 4 * ppw * P, fbase = part * rows_wg;  // the workgroup's row pairs
+  const int r0 = wv * ppw * P + g / 2;                       // this lane group's first, in them
+  const int f0 = fbase + r0;
+  // results go to LDS and leave in one coalesced pass per token chunk: a global store inside the
+  // pipeline would count with the weight loads, and waiting for the weights would wait for it
+  float* s_out = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(s_x) + int64_t(chunk) * xq_rb);
+  auto load_pair = [&](int it, W (&wt)[UPL]) {
     const int f = min(f0 + it * P, Fdim - 1);
-    const uint8_t* row = (is_up ? up : gate) + (int64_t(e) * Fdim + f) * rb;
 #pragma unroll
-    for (int t = 0; t < UPL; t++) Ut::load_w(wt[t], row, min(c + LPR * t, U - 1));
+    for (int t = 0; t < UPL; t++)
+      load_unit<F>(wt[t], is_up ? up : gate, n_rows, U, rb, int64_t(e) * Fdim + f, min(c + LPR * t, U - 1));
   };
-  __shared__ int s_rows[kMoeTokChunk];
-  typename Ut::W cur[UPL], nxt[UPL];
-  load_pair(0, cur);  // in flight while the activations are staged
+  auto process = [&](int it, W (&wt)[UPL], int nch) {
+    typename Ut::Prep pr[UPL];  // unpacked once for all the tokens
+#pragma unroll
+    for (int t = 0; t < UPL; t++) Ut::prep(pr[t], wt[t], min(c + LPR * t, U - 1));
+    int j = 0;
+    do {  // nch >= 1
+      const uint8_t* xt = reinterpret_cast<const uint8_t*>(s_x) + int64_t(j) * xq_rb;
+      float accv = 0.f;
+#pragma unroll
+      for (int t = 0; t < UPL; t++) {
+        const int u = c + LPR * t;
+        typename Ut::Act a;
+        Ut::load_act(a, xt, min(u, U - 1));
+        const float d = Ut::dot_prep(pr[t], a);
+        accv += u < U ? d : 0.f;
+      }
+      accv = group_sum_last<LPR>(accv);
+      const float gv = __shfl(accv, lane - LPR, kWave);  // gate total, from the group below
+      if (is_up && c == LPR - 1) {
+        const float silu = gv / (1.0f + expf(-gv));
+        s_out[j * rows_wg + r0 + it * P] = silu * accv;
+      }
+    } while (++j < nch);
+  };
+  W wa[UPL], wb[UPL];
   for (int base = 0; base < cnt; base += chunk) {
     const int nch = min(chunk, cnt - base);
-    if (base > 0) load_pair(0, cur);
-    __syncthreads();  // the previous pass's readers are done
+    load_pair(0, wa);  // in flight while the activations are staged
+    lds_barrier();     // the previous pass's readers are done
     if (int(threadIdx.x) < nch) s_rows[threadIdx.x] = lists.entry[i0 + base + threadIdx.x] / k;
-    __syncthreads();
+    lds_barrier();
     stage_rows(s_x, xq, xq_rb, nch, s_rows);
-    for (int it = 0; it < ppw; it++) {
-      load_pair(min(it + 1, ppw - 1), nxt);
-      const int f = f0 + it * P;
-      const bool row_ok = f < Fdim;
-      for (int j = 0; j < nch; j++) {
-        const uint8_t* xt = reinterpret_cast<const uint8_t*>(s_x) + int64_t(j) * xq_rb;
-        float accv = 0.f;
-#pragma unroll
-        for (int t = 0; t < UPL; t++) {
-          const int u = c + LPR * t;
-          if (u < U) {
-            typename Ut::Act a;
-            Ut::load_act(a, xt, u);
-            accv += Ut::dot(cur[t], a, nullptr);
-          }
-        }
-        accv = group_sum_last<LPR>(accv);
-        const float gv = __shfl(accv, lane - LPR, kWave);  // gate total, from the group below
-        if (is_up && c == LPR - 1 && row_ok) {
-          const float silu = gv / (1.0f + expf(-gv));
-          act[int64_t(i0 + base + j) * Fdim + f] = silu * accv;
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < UPL; t++) cur[t] = nxt[t];
+    // ppw is even: the loop's only exit is at the bottom, so no path leaves wb in flight
+    for (int it = 0;; it += 2) {
+      load_pair(it + 1, wb);
+      __builtin_amdgcn_sched_barrier(0);
+      process(it, wa, nch);
+      load_pair(min(it + 2, ppw - 1), wa);  // the last one is redundant
+      __builtin_amdgcn_sched_barrier(0);
+      process(it + 1, wb, nch);
+      if (it + 2 >= ppw) break;
+    }
+    lds_barrier();
+    for (int idx = threadIdx.x; idx < nch * rows_wg; idx += 256) {
+      const int j = idx / rows_wg, r = idx - j * rows_wg;
+      if (fbase + r < Fdim) act[int64_t(i0 + base + j) * Fdim + fbase + r] = s_out[idx];
     }
   }
 }
 
 // down: a workgroup takes one active expert and 4 * rpw * G rows h of its down matrix (one lane
 // group per row); the expert's act rows (contiguous, entries i0 .. i1, f32) are quantized to Q8_K
-// straight into LDS.
+// straight into LDS.  Weights alternate between two register buffers under the rules of gate/up.
 template <int F, int LPR, int UPL>
-__global__ void __launch_bounds__(256) moe_down_kernel(const uint8_t* __restrict__ down, int64_t rb, int U, int H,
+__global__ void __launch_bounds__(256) moe_down_kernel(const uint8_t* __restrict__ down, int64_t n_rows, int64_t rb,
+                                                       int U, int H,
                                                        const float* __restrict__ act, int ffn, int64_t aq_rb,
-                                                       MoeLists lists,
-                                                       float* __restrict__ yd, int rpw, int wg_per_expert,
-                                                       int chunk) {
+                                                       MoeLists lists, float* __restrict__ yd, int rpw,
+                                                       int wg_per_expert, int chunk) {
   using Ut = Unit<F>;
+  using W = typename Ut::W;
   constexpr int G = kWave / LPR;
   extern __shared__ uint32_t s_x[];
   const int slot = int(blockIdx.x) / wg_per_expert, part = int(blockIdx.x) % wg_per_expert;
@@ -339,40 +441,56 @@ __global__ void __launch_bounds__(256) moe_down_kernel(const uint8_t* __restrict
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane / LPR, c = lane % LPR;
   const int i0 = lists.offset[e], cnt = lists.offset[e + 1] - i0;
-  const int h0 = (part * 4 + wv) * rpw * G + g;
-  auto load_row = [&](int it, typename Ut::W (&wt)[UPL]) {
+  const int rows_wg = 4 * rpw * G, hbase = part * rows_wg;  // the workgroup's rows
+  const int r0 = wv * rpw * G + g;                          // this lane group's first, in them
+  const int h0 = hbase + r0;
+  // results leave through LDS, as in gate/up
+  float* s_out = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(s_x) + int64_t(chunk) * aq_rb);
+  auto load_row = [&](int it, W (&wt)[UPL]) {
     const int h = min(h0 + it * G, H - 1);
-    const uint8_t* row = down + (int64_t(e) * H + h) * rb;
 #pragma unroll
-    for (int t = 0; t < UPL; t++) Ut::load_w(wt[t], row, min(c + LPR * t, U - 1));
+    for (int t = 0; t < UPL; t++)
+      load_unit<F>(wt[t], down, n_rows, U, rb, int64_t(e) * H + h, min(c + LPR * t, U - 1));
   };
-  typename Ut::W cur[UPL], nxt[UPL];
-  load_row(0, cur);  // in flight while the activations are staged
+  auto process = [&](int it, W (&wt)[UPL], int nch) {
+    typename Ut::Prep pr[UPL];  // unpacked once for all the tokens
+#pragma unroll
+    for (int t = 0; t < UPL; t++) Ut::prep(pr[t], wt[t], min(c + LPR * t, U - 1));
+    int j = 0;
+    do {  // nch >= 1
+      const uint8_t* at = reinterpret_cast<const uint8_t*>(s_x) + int64_t(j) * aq_rb;
+      float accv = 0.f;
+#pragma unroll
+      for (int t = 0; t < UPL; t++) {
+        const int u = c + LPR * t;
+        typename Ut::Act a;
+        Ut::load_act(a, at, min(u, U - 1));
+        const float d = Ut::dot_prep(pr[t], a);
+        accv += u < U ? d : 0.f;
+      }
+      accv = group_sum_last<LPR>(accv);
+      if (c == LPR - 1) s_out[j * rows_wg + r0 + it * G] = accv;
+    } while (++j < nch);
+  };
+  W wa[UPL], wb[UPL];
   for (int base = 0; base < cnt; base += chunk) {
     const int nch = min(chunk, cnt - base);
-    if (base > 0) load_row(0, cur);
-    __syncthreads();  // the previous pass's readers are done
+    load_row(0, wa);  // in flight while the activations are staged
+    lds_barrier();    // the previous pass's readers are done
     stage_quant_rows(reinterpret_cast<uint8_t*>(s_x), act, ffn, aq_rb, nch, i0 + base);
-    for (int it = 0; it < rpw; it++) {
-      load_row(min(it + 1, rpw - 1), nxt);
-      const int h = h0 + it * G;
-      for (int j = 0; j < nch; j++) {
-        const uint8_t* at = reinterpret_cast<const uint8_t*>(s_x) + int64_t(j) * aq_rb;
-        float accv = 0.f;
-#pragma unroll
-        for (int t = 0; t < UPL; t++) {
-          const int u = c + LPR * t;
-          if (u < U) {
-            typename Ut::Act a;
-            Ut::load_act(a, at, u);
-            accv += Ut::dot(cur[t], a, nullptr);
-          }
-        }
-        accv = group_sum_last<LPR>(accv);
-        if (c == LPR - 1 && h < H) yd[int64_t(i0 + base + j) * H + h] = accv;
-      }
-#pragma unroll
-      for (int t = 0; t < UPL; t++) cur[t] = nxt[t];
+    for (int it = 0;; it += 2) {  // rpw is even, as ppw in gate/up
+      load_row(it + 1, wb);
+      __builtin_amdgcn_sched_barrier(0);
+      process(it, wa, nch);
+      load_row(min(it + 2, rpw - 1), wa);
+      __builtin_amdgcn_sched_barrier(0);
+      process(it + 1, wb, nch);
+      if (it + 2 >= rpw) break;
+    }
+    lds_barrier();
+    for (int idx = threadIdx.x; idx < nch * rows_wg; idx += 256) {
+      const int j = idx / rows_wg, r = idx - j * rows_wg;
+      if (hbase + r < H) yd[int64_t(i0 + base + j) * H + hbase + r] = s_out[idx];
     }
   }
 }
@@ -394,20 +512,21 @@ namespace {
 
 int lpr_for(int U) { return U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4; }
 
-// Work per wave: enough row pairs that the grid is about 4096 waves (at least one pair, at most 16).
+// Work per wave: an even number of row pairs (2 .. 16), enough that the grid is about 4096 waves.
 template <int F, int LPR, int UPL>
 void gate_up_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
   constexpr int P = (kWave / LPR) / 2;
   const int U = units_per_row(F, a.hidden);
   const int64_t pairs = int64_t(a.max_active) * a.ffn;
-  const int ppw = int(std::min<int64_t>(16, std::max<int64_t>(1, pairs / (int64_t(P) * 4096))));
+  const int ppw = 2 * int(std::min<int64_t>(8, std::max<int64_t>(1, pairs / (int64_t(P) * 8192))));  // even
   const int wg_per_expert = int((a.ffn + 4 * P * ppw - 1) / (4 * P * ppw));
   const int64_t xrb = row_bytes(JERO_Q8_K, a.hidden);
-  const int chunk = int(std::max<int64_t>(1, std::min<int64_t>(kMoeTokChunk, kMoeStageBytes / xrb)));
+  // an expert holds at most T of the (token, slot) pairs: size the LDS stage for no more
+  const int chunk = int(std::max<int64_t>(1, std::min<int64_t>({kMoeTokChunk, kMoeStageBytes / xrb, a.T})));
   hipLaunchKernelGGL((moe_gate_up_kernel<F, LPR, UPL>), dim3(unsigned(int64_t(a.max_active) * wg_per_expert)),
-                     dim3(256), size_t(chunk) * size_t(xrb), s, static_cast<const uint8_t*>(a.gate),
-                     static_cast<const uint8_t*>(a.up), row_bytes(F, a.hidden), U, int(a.ffn), a.top_k, a.xq, xrb, L,
-                     a.act, ppw, wg_per_expert, chunk);
+                     dim3(256), size_t(chunk) * size_t(xrb + 4 * 4 * P * ppw), s, static_cast<const uint8_t*>(a.gate),
+                     static_cast<const uint8_t*>(a.up), a.E * a.ffn, row_bytes(F, a.hidden), U, int(a.ffn), a.top_k,
+                     a.xq, xrb, L, a.act, ppw, wg_per_expert, chunk);
 }
 
 template <int F>
@@ -428,13 +547,14 @@ void down_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
   constexpr int G = kWave / LPR;
   const int U = units_per_row(F, a.ffn);
   const int64_t rows = int64_t(a.max_active) * a.hidden;
-  const int rpw = int(std::min<int64_t>(16, std::max<int64_t>(1, rows / (int64_t(G) * 4096))));
+  const int rpw = 2 * int(std::min<int64_t>(8, std::max<int64_t>(1, rows / (int64_t(G) * 8192))));  // even
   const int wg_per_expert = int((a.hidden + 4 * G * rpw - 1) / (4 * G * rpw));
   const int64_t arb = row_bytes(JERO_Q8_K, a.ffn);
-  const int chunk = int(std::max<int64_t>(1, std::min<int64_t>(kMoeTokChunk, kMoeStageBytes / arb)));
+  const int chunk = int(std::max<int64_t>(1, std::min<int64_t>({kMoeTokChunk, kMoeStageBytes / arb, a.T})));
   hipLaunchKernelGGL((moe_down_kernel<F, LPR, UPL>), dim3(unsigned(int64_t(a.max_active) * wg_per_expert)),
-                     dim3(256), size_t(chunk) * size_t(arb), s, static_cast<const uint8_t*>(a.down), row_bytes(F, a.ffn),
-                     U, int(a.hidden), a.act, int(a.ffn), arb, L, a.yd, rpw, wg_per_expert, chunk);
+                     dim3(256), size_t(chunk) * size_t(arb + 4 * 4 * G * rpw), s, static_cast<const uint8_t*>(a.down),
+                     a.E * a.hidden,
+                     row_bytes(F, a.ffn), U, int(a.hidden), a.act, int(a.ffn), arb, L, a.yd, rpw, wg_per_expert, chunk);
 }
 
 template <int F>
@@ -489,31 +609,48 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   a.yd = reinterpret_cast<float*>(take(sizeof(float) * size_t(n) * size_t(a.hidden)));
   a.max_active = int(n < a.E ? n : a.E);
 
-  // a few tokens are quantized inside the routing workgroup (one launch less); many in parallel
-  const bool quant_in_route = a.T * (a.hidden / 256) <= 2 * (kRouteThreads / kWave);
-  int rc;
-  if (!quant_in_route) {
-    rc = launch_quantize_act(JERO_Q8_K, a.x, a.T, a.hidden, a.xq, s);
+  // few tokens: one workgroup quantizes, routes and groups; many: quantize and route over many
+  // workgroups, then group in one
+  const bool single = a.T * (a.hidden / 256) <= 2 * (kRouteThreads / kWave);
+  const int per = a.E <= 128 ? 2 : a.E <= 256 ? 4 : a.E <= 512 ? 8 : 16;
+  const int n_quant_wg = int(std::min<int64_t>(1024, (a.T * (a.hidden / 256) + 3) / 4));
+  const unsigned prep_grid = unsigned(n_quant_wg + (a.T + 3) / 4);
+#define JERO_ROUTE(P)                                                                                            \
+  do {                                                                                                           \
+    if (single)                                                                                                  \
+      hipLaunchKernelGGL(moe_route_kernel<P>, dim3(1), dim3(kRouteThreads), 0, s, a.logits, int(a.T), int(a.E),  \
+                         a.top_k, a.sel_idx, a.sel_w, L, a.x, int(a.hidden), a.xq);                             \
+    else                                                                                                         \
+      hipLaunchKernelGGL(moe_prep_kernel<P>, dim3(prep_grid), dim3(256), 0, s, a.logits, int(a.T), int(a.E),     \
+                         a.top_k, a.sel_idx, a.sel_w, a.x, int(a.hidden), a.xq, n_quant_wg);                    \
+  } while (0)
+  if (per == 2) JERO_ROUTE(2);
+  else if (per == 4) JERO_ROUTE(4);
+  else if (per == 8) JERO_ROUTE(8);
+  else JERO_ROUTE(16);
+#undef JERO_ROUTE
+  int rc = check_launch("moe route");
+  if (rc) return rc;
+  if (!single) {
+    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(kRouteThreads), 0, s, a.sel_idx, int(n), int(a.E), L);
+    rc = check_launch("moe group");
     if (rc) return rc;
   }
-  {
-    const int per = a.E <= 128 ? 2 : a.E <= 256 ? 4 : a.E <= 512 ? 8 : 16;
-#define JERO_ROUTE(P)                                                                                         \
-  hipLaunchKernelGGL(moe_route_kernel<P>, dim3(1), dim3(kRouteThreads), 0, s, a.logits, int(a.T), int(a.E), \
-                     a.top_k, a.sel_idx, a.sel_w, L, a.x, int(a.hidden), quant_in_route ? a.xq : nullptr)
-    if (per == 2) JERO_ROUTE(2);
-    else if (per == 4) JERO_ROUTE(4);
-    else if (per == 8) JERO_ROUTE(8);
-    else JERO_ROUTE(16);
-#undef JERO_ROUTE
+  switch (a.gate_quant) {
+    case JERO_Q4_K: rc = gate_up_fmt<JERO_Q4_K>(a, L, s); break;
+    case JERO_Q4_K_R: rc = gate_up_fmt<JERO_Q4_K_R>(a, L, s); break;
+    case JERO_Q6_K: rc = gate_up_fmt<JERO_Q6_K>(a, L, s); break;
+    default: rc = gate_up_fmt<JERO_Q6_K_R>(a, L, s); break;
   }
-  rc = check_launch("moe route");
-  if (rc) return rc;
-  rc = a.gate_quant == JERO_Q4_K ? gate_up_fmt<JERO_Q4_K>(a, L, s) : gate_up_fmt<JERO_Q6_K>(a, L, s);
   if (rc) return rc;
   rc = check_launch("moe gate/up");
   if (rc) return rc;
-  rc = a.down_quant == JERO_Q4_K ? down_fmt<JERO_Q4_K>(a, L, s) : down_fmt<JERO_Q6_K>(a, L, s);
+  switch (a.down_quant) {
+    case JERO_Q4_K: rc = down_fmt<JERO_Q4_K>(a, L, s); break;
+    case JERO_Q4_K_R: rc = down_fmt<JERO_Q4_K_R>(a, L, s); break;
+    case JERO_Q6_K: rc = down_fmt<JERO_Q6_K>(a, L, s); break;
+    default: rc = down_fmt<JERO_Q6_K_R>(a, L, s); break;
+  }
   if (rc) return rc;
   rc = check_launch("moe down");
   if (rc) return rc;
@@ -530,9 +667,10 @@ int check_moe_args(const MoeArgs& a, size_t gate_bytes, size_t up_bytes, size_t 
   if (a.T <= 0 || a.hidden <= 0 || a.ffn <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "moe: empty input");
   if (a.top_k > a.E || a.top_k > kMaxTopK || a.E > kMaxExperts)
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "moe: top_k must be <= min(n_experts, 16), n_experts <= 1024");
-  if (a.gate_quant != a.up_quant || (a.gate_quant != JERO_Q4_K && a.gate_quant != JERO_Q6_K) ||
-      (a.down_quant != JERO_Q4_K && a.down_quant != JERO_Q6_K))
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, "moe: gate/up must share a K-quant format; down Q4_K or Q6_K");
+  auto kquant = [](int q) { return q == JERO_Q4_K || q == JERO_Q6_K || q == JERO_Q4_K_R || q == JERO_Q6_K_R; };
+  if (a.gate_quant != a.up_quant || !kquant(a.gate_quant) || !kquant(a.down_quant))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH,
+                "moe: gate/up must share a K-quant format; down Q4_K or Q6_K (GGUF or repacked _R layouts)");
   int64_t rg = row_bytes(a.gate_quant, a.hidden), rd = row_bytes(a.down_quant, a.ffn);
   if (rg < 0 || rd < 0) return fail(JERO_ERR_TENSOR_BOUNDS, "moe: hidden/ffn not multiples of 256");
   if (uint64_t(rg) * a.ffn * a.E > gate_bytes || uint64_t(rg) * a.ffn * a.E > up_bytes ||
@@ -540,6 +678,9 @@ int check_moe_args(const MoeArgs& a, size_t gate_bytes, size_t up_bytes, size_t 
     return fail(JERO_ERR_TENSOR_BOUNDS, "moe: stacked expert tensors smaller than [E][rows][cols]");
   if (!aligned4(a.gate) || !aligned4(a.up) || !aligned4(a.down) || (reinterpret_cast<uintptr_t>(a.x) & 15u))
     return fail(JERO_ERR_INVALID_ARGUMENT, "moe: weights 4-byte and x 16-byte aligned");
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if ((is_planar(a.gate_quant) && (!a16(a.gate) || !a16(a.up))) || (is_planar(a.down_quant) && !a16(a.down)))
+    return fail(JERO_ERR_INVALID_ARGUMENT, "moe: repacked (_R) expert tensors must be 16-byte aligned");
   return JERO_OK;
 }
 

@@ -261,11 +261,15 @@ def vec_dot_q6_k(out, weights, inp, **kw):
 
 def repack(weights, stream=None):
     """Load-time re-layout (repack_tensor_parallel, src/weights.rs:914-955): returns a new
-    TensorView in the device layout (Q4_K -> Q4_K_R, Q6_K -> Q6_K_R, same byte count)."""
+    TensorView in the device layout (Q4_K -> Q4_K_R, Q6_K -> Q6_K_R, same byte count).  A stacked
+    expert tensor [n_in, rows, n_experts] is repacked as its rows * n_experts rows."""
     import torch
     dst = torch.empty(weights.nbytes(), dtype=torch.uint8, device=weights.data.device)
     q = C.c_int(0)
-    check(lib().jero_hip_repack(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in, weights.n_out,
+    rows = 1
+    for d in weights.shape[1:]:
+        rows *= d
+    check(lib().jero_hip_repack(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in, rows,
                                 _ptr(dst), C.byref(q), _stream(stream)))
     return TensorView(weights.name, q.value, weights.shape, dst)
 

@@ -15,7 +15,7 @@ from qdata import rand_act, rand_weights
 pytestmark = pytest.mark.gpu
 
 
-def run_case(dev, T, E, H, F, K, gq, dq, seed, logits=None):
+def run_case(dev, T, E, H, F, K, gq, dq, seed, logits=None, repacked=False):
     gate = rand_weights(gq, E * F, H, seed)
     up = rand_weights(gq, E * F, H, seed + 1)
     down = rand_weights(dq, E * H, F, seed + 2)
@@ -30,6 +30,12 @@ def run_case(dev, T, E, H, F, K, gq, dq, seed, logits=None):
     y = torch.empty((T, H), dtype=torch.float32, device=dev)
     si, sw = J.dispatch_qwen3_moe_ffn(y, td(x), td(logits), K, G, U, D)
     torch.cuda.synchronize()
+    if repacked:  # the load-time layouts (Q4_K_R / Q6_K_R over all experts' rows) give the same bits
+        yr = torch.empty_like(y)
+        sir, swr = J.dispatch_qwen3_moe_ffn(yr, td(x), td(logits), K, J.repack(G), J.repack(U), J.repack(D))
+        torch.cuda.synchronize()
+        assert torch.equal(sir, si) and torch.equal(swr, sw)
+        assert torch.equal(yr, y)
     np.testing.assert_array_equal(si.cpu().numpy(), si_ref)
     np.testing.assert_allclose(sw.cpu().numpy(), sw_ref, rtol=1e-6, atol=1e-7)
     ref = y_ref.astype(np.float64)
@@ -42,13 +48,19 @@ def run_case(dev, T, E, H, F, K, gq, dq, seed, logits=None):
 def test_moe_qwen3_shape(dev, T):
     """Hidden 2048, 128 experts of 768, top-8; gate/up Q4_K, down Q6_K."""
     print(f"moe qwen3 T={T}", flush=True)
-    run_case(dev, T, 128, 2048, 768, 8, J.Q4_K, J.Q6_K, 900 + T)
+    run_case(dev, T, 128, 2048, 768, 8, J.Q4_K, J.Q6_K, 900 + T, repacked=True)
 
 
 def test_moe_small_and_q4k_down(dev):
     print("moe small", flush=True)
-    run_case(dev, 5, 6, 256, 512, 2, J.Q4_K, J.Q4_K, 40)
-    run_case(dev, 3, 16, 512, 256, 4, J.Q6_K, J.Q6_K, 41)
+    run_case(dev, 5, 6, 256, 512, 2, J.Q4_K, J.Q4_K, 40, repacked=True)
+    run_case(dev, 3, 16, 512, 256, 4, J.Q6_K, J.Q6_K, 41, repacked=True)
+
+
+def test_moe_many_tokens_per_expert(dev):
+    """Four experts for 40 tokens at top-2: each expert sees ~20 tokens, several LDS passes."""
+    print("moe many tokens per expert", flush=True)
+    run_case(dev, 40, 4, 512, 512, 2, J.Q4_K, J.Q6_K, 42, repacked=True)
 
 
 @pytest.mark.parametrize("E,K", [(200, 6), (300, 8), (700, 16)])

@@ -185,19 +185,20 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-// Q8_K block of 256 elements from one wave, four consecutive elements per lane, written to `ob`
-// (LDS or global memory, 4-byte aligned).  ggml's rule: the first element (lowest index) of
-// largest magnitude is `max`; iscale = -127 / max, q = min(127, rint(iscale * x)), d = 1 / iscale,
-// bsums over 16-element groups; an all-zero block stores zeros.
-__device__ __forceinline__ void q8k_block_wave(const float e[4], int lane, uint8_t* ob) {
+// Q8_K block of 256 elements from one wave, four consecutive elements per lane, written as its
+// three fields: 256 int8 at qs, 16 int16 bsums at bs, the f32 scale at d (LDS or global memory,
+// 4-byte aligned).  ggml's rule: the first element (lowest index) of largest magnitude is `max`;
+// iscale = -127 / max, q = min(127, rint(iscale * x)), d = 1 / iscale, bsums over 16-element
+// groups; an all-zero block stores zeros.
+__device__ __forceinline__ void q8k_block_wave_split(const float e[4], int lane, uint8_t* qs, uint8_t* bs, uint8_t* d) {
   float am = 0.0f;
 #pragma unroll
   for (int t = 0; t < 4; t++) am = fmaxf(am, fabsf(e[t]));
   am = wave_max_dpp(am);  // uniform block max |x|
   if (am == 0.0f) {
-    reinterpret_cast<uint32_t*>(ob + 4)[lane] = 0u;
-    if (lane < 16) reinterpret_cast<int16_t*>(ob + 260)[lane] = 0;
-    if (lane == 0) *reinterpret_cast<float*>(ob) = 0.0f;
+    reinterpret_cast<uint32_t*>(qs)[lane] = 0u;
+    if (lane < 16) reinterpret_cast<int16_t*>(bs)[lane] = 0;
+    if (lane == 0) *reinterpret_cast<float*>(d) = 0.0f;
     return;
   }
   // the first element (lowest index) with |x| == max sets the sign: lowest lane, lowest t
@@ -222,10 +223,15 @@ __device__ __forceinline__ void q8k_block_wave(const float e[4], int lane, uint8
     s += qv;
     packed |= (uint32_t(qv) & 0xFFu) << (8 * t);
   }
-  reinterpret_cast<uint32_t*>(ob + 4)[lane] = packed;
+  reinterpret_cast<uint32_t*>(qs)[lane] = packed;
   s = int(group_sum_all<4>(float(s)));  // |s| <= 508: exact in f32
-  if ((lane & 3) == 0) reinterpret_cast<int16_t*>(ob + 260)[lane >> 2] = int16_t(s);
-  if (lane == 0) *reinterpret_cast<float*>(ob) = 1.0f / iscale;
+  if ((lane & 3) == 0) reinterpret_cast<int16_t*>(bs)[lane >> 2] = int16_t(s);
+  if (lane == 0) *reinterpret_cast<float*>(d) = 1.0f / iscale;
+}
+
+// The same block written as one 292-byte Q8_K block at ob.
+__device__ __forceinline__ void q8k_block_wave(const float e[4], int lane, uint8_t* ob) {
+  q8k_block_wave_split(e, lane, ob + 4, ob + 260, ob);
 }
 
 __device__ __forceinline__ float wave_max(float v) {

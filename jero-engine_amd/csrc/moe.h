@@ -14,7 +14,12 @@ struct MoeLists {
   int32_t* n_active;  // [1]
   int32_t* entry;     // [T*k] (token*k + slot), grouped by expert, ascending within an expert
   int32_t* inv;       // [T*k] list position of (token*k + slot)
+  int32_t* desc;      // [E][kMoeDescInts] per active slot: expert, first list position, count, 0,
+                      // then the tokens of its first kMoeDescTokens list entries (or null)
 };
+
+constexpr int kMoeDescInts = 16;
+constexpr int kMoeDescTokens = kMoeDescInts - 4;
 
 struct MoeArgs {
   const float* x;       // [T][hidden]

@@ -111,9 +111,12 @@ struct GroupLds {
   int count[kMaxExperts];
   int off[kMaxExperts];
   int fill[kMaxExperts];
+  int active[kMaxExperts];
   int wsum[2 * (kRouteThreads / 64)];
+  int n_active;
   __attribute__((aligned(16))) int sel[kRouteLdsPairs + 4];  // the selections, when they fit
   int list[kRouteLdsPairs];                                   // pairs grouped by expert, atomic order
+  int entry[kRouteLdsPairs];                                  // the final list (descriptors' tokens)
 };
 
 // Zeroes the per-expert counters (before a barrier that precedes group_pairs).
@@ -127,7 +130,7 @@ __device__ __forceinline__ void group_init(GroupLds& g, int E) {
 // Groups the n (token, slot) pairs by expert, in ascending pair order within an expert, and
 // writes the ascending list of active experts.  The selections are in g.sel when n fits, else in
 // sel_idx.  One workgroup of kRouteThreads threads; starts and ends with a barrier.
-__device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, int n, int E, MoeLists lists) {
+__device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, int n, int E, int k, MoeLists lists) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = kRouteThreads / 64;
   if (threadIdx.x < 4 && n + int(threadIdx.x) < kRouteLdsPairs + 4) g.sel[n + threadIdx.x] = -1;
   __syncthreads();
@@ -162,10 +165,14 @@ __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, in
       const int off_e = bc + ic - c;
       g.off[e] = off_e;
       lists.offset[e] = off_e;
-      if (f) lists.active[bf + jf - 1] = e;
+      if (f) {
+        lists.active[bf + jf - 1] = e;
+        g.active[bf + jf - 1] = e;
+      }
       if (e == E - 1) {
         lists.offset[E] = off_e + c;
         *lists.n_active = bf + jf;
+        g.n_active = bf + jf;
       }
     }
   }
@@ -184,6 +191,18 @@ __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, in
       for (int q = 0; q < c; q++) r += g.list[o + q] < i ? 1 : 0;
       lists.entry[o + r] = i;
       lists.inv[i] = o + r;
+      g.entry[o + r] = i;
+    }
+    if (lists.desc) {
+      // per active slot: expert, first list position, count, and its first tokens
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < g.n_active * kMoeDescInts; idx += kRouteThreads) {
+        const int sl = idx / kMoeDescInts, q = idx - sl * kMoeDescInts;
+        const int e = g.active[sl], o = g.off[e], c = g.count[e];
+        int v = q == 0 ? e : q == 1 ? o : q == 2 ? c : 0;
+        if (q >= 4) v = g.entry[o + min(q - 4, c - 1)] / k;
+        lists.desc[idx] = v;
+      }
     }
   } else {
     // more pairs than LDS holds: thread e walks the selections in order and keeps those routed to e
@@ -221,7 +240,7 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
   }
   group_init(g, E);
   for (int t = wv; t < T; t += nw) route_token<PER>(logits, t, E, k, sel_idx, sel_w, g.sel);
-  group_pairs(g, sel_idx, T * k, E, lists);
+  group_pairs(g, sel_idx, T * k, E, k, lists);
 }
 
 // Many tokens, first step: workgroups [0, n_quant_wg) quantize the hidden vectors to Q8_K (one
@@ -249,12 +268,12 @@ __global__ void __launch_bounds__(256) moe_prep_kernel(const float* __restrict__
 
 // Many tokens, second step: one workgroup groups the selections.
 __global__ void __launch_bounds__(kRouteThreads) moe_group_kernel(const int32_t* __restrict__ sel_idx, int n, int E,
-                                                                  MoeLists lists) {
+                                                                  int k, MoeLists lists) {
   __shared__ GroupLds g;
   group_init(g, E);
   if (n <= kRouteLdsPairs)
     for (int i = threadIdx.x; i < n; i += kRouteThreads) g.sel[i] = sel_idx[i];
-  group_pairs(g, sel_idx, n, E, lists);
+  group_pairs(g, sel_idx, n, E, k, lists);
 }
 
 constexpr int kMoeTokChunk = 8;          // activation rows of one expert staged in LDS per pass
@@ -495,6 +514,287 @@ __global__ void __launch_bounds__(256) moe_down_kernel(const uint8_t* __restrict
   }
 }
 
+// ---------------------------------------------------------------- expert GEMMs on MFMA
+// Several tokens per expert: v_mfma_i32_16x16x64_i8 over one 64-weight unit at a time.  A unit
+// has SEG integer-scaled segments (Q4_K: 2 sub-blocks of 32 weights; Q6_K: 4 groups of 16).  The
+// 16 rows of the A operand are (token, segment) pairs, each holding its token's activations only
+// in the K range of its segment (zeros elsewhere), so one MFMA yields the exact integer partial
+// sum of every segment for TPT = 16 / SEG tokens and 16 weight rows (the B operand, columns).
+// Lane l supplies A row l % 16 and B column l % 16 over K [16 (l / 16), +16) and receives C rows
+// 4 (l / 16) .. +4 of column l % 16: all segments of 4 / SEG tokens for one weight row, so the
+// segment scales, mins and block scales come from the lane's own weight row and are applied
+// in-lane, per unit, with the GEMV's float formula.  Activations are staged in LDS as Q8_K rows.
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__host__ __device__ constexpr int mfma_seg(int f) { return f == JERO_Q6_K || f == JERO_Q6_K_R ? 4 : 2; }
+__host__ __device__ inline int act_row_stride(int nb) { return ((nb * 292 + 15) & ~15) + 16; }
+constexpr int kMfmaTokens = 8;  // tokens staged per pass (NT = kMfmaTokens / TPT token tiles)
+
+// The weights of block b (units 4b .. 4b + 3: one step) of one weight row for lane group kg, as
+// loaded.  A step takes a whole block so that every cache line it fetches is used up within
+// the step: lines shared between steps were evicted from L2 between their uses (the step
+// working set of all resident waves exceeds an XCD's L2), costing 1.45x the HBM bytes.
+template <int F>
+struct MfmaPiece;
+template <>
+struct MfmaPiece<JERO_Q4_K_R> {
+  u32x4 q[4];  // q0 (kg even) or q1 (kg odd) run of each unit: 16 bytes of qs
+  u32x4 h;     // the block header (d, dmin, 12 scale bytes)
+  static __device__ __forceinline__ void load(MfmaPiece& p, const uint8_t* __restrict__ base, int64_t /*n_rows*/,
+                                              int U, int64_t /*rb*/, int64_t row, int b, int kg) {
+    const uint8_t* rp = base + row * (int64_t(U) * 36);
+#pragma unroll
+    for (int x = 0; x < 4; x++) p.q[x] = ld4(rp + (kg & 1) * U * 16 + (4 * b + x) * 16);
+    p.h = ld4(rp + U * 32 + b * 16);
+  }
+};
+template <>
+struct MfmaPiece<JERO_Q4_K> : MfmaPiece<JERO_Q4_K_R> {
+  static __device__ __forceinline__ void load(MfmaPiece& p, const uint8_t* __restrict__ base, int64_t /*n_rows*/,
+                                              int /*U*/, int64_t rb, int64_t row, int b, int kg) {
+    const uint8_t* blk = base + row * rb + int64_t(b) * 144;
+#pragma unroll
+    for (int x = 0; x < 4; x++) p.q[x] = ld4(blk + 16 + 32 * x + 16 * (kg & 1));
+    p.h = ld4(blk);
+  }
+};
+template <>
+struct MfmaPiece<JERO_Q6_K_R> {
+  u32x4 x[4], qh[4];  // ql run (lo for even kg, hi for odd) and qh run of each unit
+  u32x4 sc;           // the units' int8 group scales, one dword per unit
+  uint32_t dw, dsh;   // the block's f16 d: its dword and shift
+  static __device__ __forceinline__ void load(MfmaPiece& p, const uint8_t* __restrict__ base, int64_t n_rows, int U,
+                                              int64_t /*rb*/, int64_t row, int b, int kg) {
+    const int64_t plane = n_rows * int64_t(U) * 16, gu = row * U + 4 * b;
+#pragma unroll
+    for (int x = 0; x < 4; x++) {
+      p.x[x] = ld4(base + (kg & 1) * plane + (gu + x) * 16);
+      p.qh[x] = ld4(base + 2 * plane + (gu + x) * 16);
+    }
+    p.sc = ld4(base + 3 * plane + gu * 4);
+    const uint8_t* dp = base + 3 * plane + n_rows * int64_t(U) * 4 + (row * (U / 4) + b) * 2;
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(dp) & 3u);
+    p.dw = ld1(dp - sh);
+    p.dsh = 8u * sh;
+  }
+};
+
+// 6-bit scale and min of Q4_K sub-block `sb` (0..7) from the block header h.
+__device__ __forceinline__ void q4k_scale_min(const u32x4& h, int sb, int& sc, int& m) {
+  const uint32_t jj = uint32_t(sb & 3);
+  const uint32_t a = byte_of(h.y, jj), bb = byte_of(h.z, jj), c = byte_of(h.w, jj);
+  sc = int(sb < 4 ? a & 63u : (c & 15u) | ((a >> 6) << 4));
+  m = int(sb < 4 ? bb & 63u : (c >> 4) | ((bb >> 6) << 4));
+}
+
+constexpr int kStageChunks = 8;  // Q8_K staging: 16-byte chunks per thread in its one batch
+constexpr int kStageBlocks = 8;  // f32 staging: 256-element blocks per wave in its one batch
+
+// One workgroup: an active expert, 64 TILES of its weight rows (TILES tiles of 16 per wave, one
+// after the other), every token of the expert (kMfmaTokens per pass).  Several tiles per wave
+// amortize the workgroup's start (descriptor, activation staging) over more weight bytes; each
+// tile's results go to LDS when its last block is done and leave in one coalesced pass.  GU: gate (w0) and up (w1) rows from the tokens' Q8_K rows, out =
+// silu(gate) * up per (list entry, row); else down (w0) rows from the f32 act rows (quantized here),
+// out = the dot per (list entry, row).  A workgroup makes two dependent trips to memory before
+// its first MFMA: the slot descriptor, then the activations (in one batch) with the first
+// weights behind them; the load counter drains in order, so nothing small waits behind weights.
+template <int F, bool GU, int TILES>
+__global__ void __launch_bounds__(256) moe_mfma_kernel(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
+                                                       int64_t n_rows, int64_t rb, int U, int R, int k,
+                                                       const uint8_t* __restrict__ xq, int64_t xq_rb,
+                                                       const float* __restrict__ act_in, MoeLists lists,
+                                                       float* __restrict__ out, int wg_per_expert) {
+  constexpr int SEG = mfma_seg(F), TPT = 16 / SEG, NT = kMfmaTokens / TPT, LT = 4 / SEG;
+  constexpr int NW = GU ? 2 : 1;  // weight tensors per wave
+  using Piece = MfmaPiece<F>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_act[];
+  __shared__ int s_tok[kMfmaTokens];
+  const int slot = int(blockIdx.x) / wg_per_expert, part = int(blockIdx.x) % wg_per_expert;
+  // the descriptor (slot < E, always in bounds) and the active count in one trip
+  const int n_act = *lists.n_active;
+  const int32_t* dsc = lists.desc + slot * kMoeDescInts;
+  const int e = dsc[0], i0 = dsc[1], cnt = dsc[2];
+  if (slot >= n_act) return;  // uniform over the workgroup
+  int tk = dsc[4 + min(int(threadIdx.x), kMfmaTokens - 1)];  // thread j < kMfmaTokens: token j
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int c = lane & 15, kg = lane >> 4;
+  const int nb = U / 4, stride = act_row_stride(nb), dummy = kMfmaTokens * stride;
+  const int row0 = (part * 4 + wv) * TILES * 16 + c;  // this lane's weight row (B column) in tile 0
+  const int steps = TILES * nb;
+  float* s_out = reinterpret_cast<float*>(s_act + dummy + 304);  // [TILES][kMfmaTokens][64 rows]
+  const uint8_t* wt[2] = {w0, GU ? w1 : w0};
+  // A operand lanes: virtual row vr = (token, segment); K group kg belongs to segment kg / (4 / SEG)
+  const int vr = lane & 15, a_tok = vr / SEG, a_seg = vr % SEG, kg_seg = kg / (4 / SEG);
+  // step s: block s % nb of tile s / nb (steps past the end clamp to the last)
+  auto load = [&](int s_, Piece (&p)[NW]) {
+    const int sc = min(s_, steps - 1), tile = sc / nb;
+    const int64_t grow = int64_t(e) * R + min(row0 + 16 * tile, R - 1);
+#pragma unroll
+    for (int t = 0; t < NW; t++) Piece::load(p[t], wt[t], n_rows, U, rb, grow, sc - tile * nb, kg);
+  };
+  for (int base = 0; base < cnt; base += kMfmaTokens) {
+    const int nch = min(kMfmaTokens, cnt - base);
+    if (base > 0)  // later passes (more than kMfmaTokens tokens): their tokens from the list
+      tk = lists.entry[i0 + base + min(int(threadIdx.x) % kMfmaTokens, nch - 1)] / k;
+    if (threadIdx.x < kMfmaTokens) s_tok[threadIdx.x] = tk;
+    lds_barrier();  // the previous pass's readers are done; s_tok
+    Piece pa[NW], pb[NW];
+    // staging in one batch: every load issued, then the first weights, then the LDS writes
+    // (out-of-range slots write a dummy area: no branch may skip a wait)
+    if constexpr (GU) {
+      const int chunks = nb * 73 / 4, total = nch * chunks;  // 16-byte chunks of a Q8_K row (nb % 4 == 0)
+      u32x4 v[kStageChunks];
+#pragma unroll
+      for (int q = 0; q < kStageChunks; q++) {
+        const int idx = min(int(threadIdx.x) + 256 * q, total - 1), j = idx / chunks;
+        v[q] = ld4(xq + int64_t(s_tok[j]) * xq_rb + (idx - j * chunks) * 16);
+      }
+      load(0, pa);
+#pragma unroll
+      for (int q = 0; q < kStageChunks; q++) {
+        const int idx = int(threadIdx.x) + 256 * q, j = idx / chunks;
+        *reinterpret_cast<u32x4*>(s_act + (idx < total ? j * stride + (idx - j * chunks) * 16 : dummy)) = v[q];
+      }
+    } else {
+      const int cols = U * 64, total = nch * nb;
+      float4 v[kStageBlocks];
+#pragma unroll
+      for (int q = 0; q < kStageBlocks; q++) {
+        const int b = min(wv + 4 * q, total - 1), j = b / nb, jb = b - j * nb;
+        v[q] = reinterpret_cast<const float4*>(act_in + int64_t(i0 + base + j) * cols + int64_t(jb) * 256)[lane];
+      }
+      load(0, pa);
+#pragma unroll
+      for (int q = 0; q < kStageBlocks; q++) {
+        const int b = wv + 4 * q, j = b / nb, jb = b - j * nb;
+        const float ev[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+        q8k_block_wave(ev, lane, s_act + (b < total ? j * stride + 292 * jb : dummy));
+      }
+    }
+    lds_barrier();
+    float acc[NW][NT][LT];
+#pragma unroll
+    for (int t = 0; t < NW; t++)
+#pragma unroll
+      for (int tl = 0; tl < NT; tl++)
+#pragma unroll
+        for (int q = 0; q < LT; q++) acc[t][tl][q] = 0.f;
+    // one step: block b (units 4b .. 4b + 3) of one tile; a step past the last (steps odd) is a
+    // padding step: clamped loads, nothing accumulated
+    auto process = [&](int s_, Piece (&p)[NW]) {
+      const bool live = s_ < steps;
+      const int sc = min(s_, steps - 1), tile = sc / nb, b = sc - tile * nb;
+#pragma unroll
+      for (int x = 0; x < 4; x++) {
+        const int u = 4 * b + x;
+        // A: this lane's (token, segment) row over K group kg, zero outside its segment
+        int a_off;
+        if constexpr (SEG == 2) a_off = 292 * b + 4 + 64 * (u & 3) + 16 * kg;
+        else a_off = 292 * b + 4 + 128 * ((u >> 1) & 1) + 16 * (u & 1) + 32 * kg;
+        v4i A[NT];
+#pragma unroll
+        for (int tl = 0; tl < NT; tl++) {
+          const int t = min(tl * TPT + a_tok, nch - 1);
+          const uint32_t* ap = reinterpret_cast<const uint32_t*>(s_act + t * stride + a_off);  // 4-byte aligned
+          const v4i v = {int(ap[0]), int(ap[1]), int(ap[2]), int(ap[3])};
+          const bool on = a_seg == kg_seg;
+          A[tl] = on ? v : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int t = 0; t < NW; t++) {
+          // B: this lane's weight row over K group kg, as non-negative int8
+          v4i B;
+          float d, dmin = 0.f;
+          int sc[SEG], mn[SEG];
+          if constexpr (SEG == 2) {
+            const u32x4 q = p[t].q[x];
+            const uint32_t qd[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int w = 0; w < 4; w++) B[w] = int(kg < 2 ? qd[w] & 0x0F0F0F0Fu : (qd[w] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+            for (int sg = 0; sg < 2; sg++) q4k_scale_min(p[t].h, 2 * (u & 3) + sg, sc[sg], mn[sg]);
+            d = h2f(p[t].h.x);
+            dmin = h2f(p[t].h.x >> 16);
+          } else {
+            const uint32_t xd[4] = {p[t].x[x].x, p[t].x[x].y, p[t].x[x].z, p[t].x[x].w};
+            const uint32_t hd[4] = {p[t].qh[x].x, p[t].qh[x].y, p[t].qh[x].z, p[t].qh[x].w};
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+              const uint32_t nib = kg & 2 ? (xd[w] >> 4) & 0x0F0F0F0Fu : xd[w] & 0x0F0F0F0Fu;
+              B[w] = int(nib | (((hd[w] >> (2 * kg)) & 0x03030303u) << 4));
+            }
+            const uint32_t scd[4] = {p[t].sc.x, p[t].sc.y, p[t].sc.z, p[t].sc.w};
+#pragma unroll
+            for (int g = 0; g < 4; g++) sc[g] = int(int8_t(scd[x] >> (8 * g)));
+            d = h2f(p[t].dw >> p[t].dsh);
+          }
+#pragma unroll
+          for (int tl = 0; tl < NT; tl++) {
+            const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tl], B, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < LT; q++) {
+              const int t_loc = tl * TPT + kg * LT + q;        // staged token of C rows 4kg + SEG q ..
+              const uint8_t* blk = s_act + min(t_loc, nch - 1) * stride + 292 * b;
+              const float dx = *reinterpret_cast<const float*>(blk);
+              const int16_t* bs = reinterpret_cast<const int16_t*>(blk + 260);
+              float term;
+              if constexpr (SEG == 2) {
+                const int i = u & 3;
+                const int bsa = int(bs[4 * i]) + int(bs[4 * i + 1]), bsb = int(bs[4 * i + 2]) + int(bs[4 * i + 3]);
+                const int isum = sc[0] * C[SEG * q] + sc[1] * C[SEG * q + 1];
+                const int msum = mn[0] * bsa + mn[1] * bsb;
+                term = dx * (d * float(isum) - dmin * float(msum));
+              } else {
+                const int g0 = 8 * ((u >> 1) & 1) + (u & 1);  // bsum index of the unit's group 0
+                int isum = 0;
+#pragma unroll
+                for (int g = 0; g < 4; g++) isum += sc[g] * (C[g] - 32 * int(bs[g0 + 2 * g]));
+                term = dx * d * float(isum);
+              }
+              acc[t][tl][q] += live ? term : 0.f;
+            }
+          }
+        }
+      }
+      if (b == nb - 1) {  // the tile's last block: its results to LDS, accumulators reset
+#pragma unroll
+        for (int tl = 0; tl < NT; tl++)
+#pragma unroll
+          for (int q = 0; q < LT; q++) {
+            float v;
+            if constexpr (GU) {
+              const float g = acc[0][tl][q];
+              v = g / (1.0f + expf(-g)) * acc[1][tl][q];
+            } else {
+              v = acc[0][tl][q];
+            }
+            const int t_loc = tl * TPT + kg * LT + q;  // < kMfmaTokens
+            if (live) s_out[(tile * kMfmaTokens + t_loc) * 64 + 16 * wv + c] = v;
+#pragma unroll
+            for (int t = 0; t < NW; t++) acc[t][tl][q] = 0.f;
+          }
+      }
+    };
+    // an even number of steps (a padding step when odd): the loop's only exit is at the bottom
+    for (int s_ = 0;; s_ += 2) {
+      load(s_ + 1, pb);
+      __builtin_amdgcn_sched_barrier(0);
+      process(s_, pa);
+      load(s_ + 2, pa);  // the last one is redundant (clamped)
+      __builtin_amdgcn_sched_barrier(0);
+      process(s_ + 1, pb);
+      if (s_ + 2 >= steps) break;
+    }
+    lds_barrier();
+    for (int idx = threadIdx.x; idx < TILES * nch * 64; idx += 256) {
+      const int tile = idx / (nch * 64), rem = idx - tile * nch * 64, t = rem / 64, w = (rem / 16) & 3, cc = rem & 15;
+      const int row = (part * 4 + w) * TILES * 16 + 16 * tile + cc;
+      if (row < R) out[int64_t(i0 + base + t) * R + row] = s_out[(tile * kMfmaTokens + t) * 64 + 16 * w + cc];
+    }
+  }
+}
+
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ yd, const float* __restrict__ w,
                                                           const int32_t* __restrict__ inv, int T, int k, int H,
                                                           float* __restrict__ y) {
@@ -573,6 +873,34 @@ int down_fmt(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
   return JERO_OK;
 }
 
+// Expert GEMMs on MFMA (several tokens per expert): formats with a piece loader.
+bool mfma_format(int f) { return f == JERO_Q4_K || f == JERO_Q4_K_R || f == JERO_Q6_K_R; }
+
+template <int F, bool GU>
+void mfma_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
+  constexpr int TILES = GU ? 2 : 4;  // 16-row tiles per wave: K = hidden (long) vs K = ffn (short)
+  const int64_t K = GU ? a.hidden : a.ffn, R = GU ? a.ffn : a.hidden;
+  const int U = units_per_row(F, K), nb = U / 4;
+  const int wg_per_expert = int((R + 64 * TILES - 1) / (64 * TILES));
+  const size_t lds = size_t(kMfmaTokens) * size_t(act_row_stride(nb)) + 304 +  // + the dummy area
+                     sizeof(float) * TILES * kMfmaTokens * 64;                   // + the results
+  const uint8_t* w0 = static_cast<const uint8_t*>(GU ? a.gate : a.down);
+  const uint8_t* w1 = static_cast<const uint8_t*>(GU ? a.up : a.down);
+  hipLaunchKernelGGL((moe_mfma_kernel<F, GU, TILES>), dim3(unsigned(int64_t(a.max_active) * wg_per_expert)), dim3(256),
+                     lds, s,
+                     w0, w1, a.E * R, row_bytes(F, K), U, int(R), a.top_k, a.xq, row_bytes(JERO_Q8_K, a.hidden), a.act,
+                     L, GU ? a.act : a.yd, wg_per_expert);
+}
+
+template <bool GU>
+void mfma_fmt(int f, const MoeArgs& a, const MoeLists& L, hipStream_t s) {
+  switch (f) {
+    case JERO_Q4_K: mfma_one<JERO_Q4_K, GU>(a, L, s); break;
+    case JERO_Q4_K_R: mfma_one<JERO_Q4_K_R, GU>(a, L, s); break;
+    default: mfma_one<JERO_Q6_K_R, GU>(a, L, s); break;
+  }
+}
+
 }  // namespace
 
 size_t moe_workspace_bytes(int64_t T, int64_t E, int top_k, int64_t hidden, int64_t ffn) {
@@ -584,6 +912,7 @@ size_t moe_workspace_bytes(int64_t T, int64_t E, int top_k, int64_t hidden, int6
   add(sizeof(int32_t) * size_t(E));                        // active
   add(sizeof(int32_t));                                    // n_active
   add(sizeof(int32_t) * size_t(n) * 2);                    // entry, inv
+  add(sizeof(int32_t) * size_t(E) * kMoeDescInts);         // slot descriptors
   add(sizeof(float) * size_t(n) * size_t(ffn));            // act
   add(sizeof(float) * size_t(n) * size_t(hidden));         // per-slot down outputs
   return b;
@@ -605,9 +934,18 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   int32_t* ei = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(n) * 2));
   L.entry = ei;
   L.inv = ei + n;
-  a.act = reinterpret_cast<float*>(take(sizeof(float) * size_t(n) * size_t(a.ffn)));
+  int32_t* desc = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(a.E) * kMoeDescInts));
+  a.act = reinterpret_cast<float*>(take(sizeof(float) * size_t(a.ffn) * size_t(n)));
   a.yd = reinterpret_cast<float*>(take(sizeof(float) * size_t(n) * size_t(a.hidden)));
   a.max_active = int(n < a.E ? n : a.E);
+  // several tokens per expert on average: the MFMA expert GEMMs (a token's dot products come
+  // out of the matrix cores instead of one cross-lane reduction per token and row); they start
+  // from the per-slot descriptors, written by the grouping step
+  const bool mfma = a.T * a.top_k >= 2 * a.E && n <= kRouteLdsPairs && mfma_format(a.gate_quant) &&
+                    mfma_format(a.down_quant) && (a.hidden / 256) % 4 == 0 &&
+                    kMfmaTokens * (a.hidden / 256) * 73 / 4 <= kStageChunks * 256 &&
+                    kMfmaTokens * (a.ffn / 256) <= 4 * kStageBlocks;
+  L.desc = mfma ? desc : nullptr;
 
   // few tokens: one workgroup quantizes, routes and groups; many: quantize and route over many
   // workgroups, then group in one
@@ -632,10 +970,18 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   int rc = check_launch("moe route");
   if (rc) return rc;
   if (!single) {
-    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(kRouteThreads), 0, s, a.sel_idx, int(n), int(a.E), L);
+    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(kRouteThreads), 0, s, a.sel_idx, int(n), int(a.E), a.top_k, L);
     rc = check_launch("moe group");
     if (rc) return rc;
   }
+  if (mfma) {
+    mfma_fmt<true>(a.gate_quant, a, L, s);
+    rc = check_launch("moe gate/up");
+    if (rc) return rc;
+    mfma_fmt<false>(a.down_quant, a, L, s);
+    rc = check_launch("moe down");
+    if (rc) return rc;
+  } else {
   switch (a.gate_quant) {
     case JERO_Q4_K: rc = gate_up_fmt<JERO_Q4_K>(a, L, s); break;
     case JERO_Q4_K_R: rc = gate_up_fmt<JERO_Q4_K_R>(a, L, s); break;
@@ -654,6 +1000,7 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   if (rc) return rc;
   rc = check_launch("moe down");
   if (rc) return rc;
+  }
   const int64_t total = a.T * a.hidden;
   hipLaunchKernelGGL(moe_combine_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, a.yd, a.sel_w, L.inv,
                      int(a.T), a.top_k, int(a.hidden), a.y);

@@ -1,8 +1,12 @@
 """GPU parity of the routed-expert FFN against the oracle's dispatch_qwen3_moe_ffn.
 
 Routing (selected experts and their order) must match exactly; weights within 1e-6; outputs
-within 1e-3 of max(|ref|, rms(ref)): the expert hidden activations are re-quantized to Q8_K
-between gate/up and down, so a last-bit difference in silu(g)*u can move one int8 by one.
+within 1e-3 of max(|ref|, rms(ref)) per token row.  The expert hidden activations are
+re-quantized to Q8_K between gate/up and down, so a last-bit difference in silu(g)*u (summation
+order) can move one int8 by one; that shifts the token's whole output row by ~1e-3 of its rms,
+up to a few 1e-3 where |ref| is small.  Such rows (at most a tenth of the rows, and one) must
+still hold cosine >= 0.9999, the reference's certification floor (src/certification.rs:240-318),
+and 2e-2.  Without a flip the kernels sit at ~1e-6.
 """
 import numpy as np
 import pytest
@@ -30,18 +34,28 @@ def run_case(dev, T, E, H, F, K, gq, dq, seed, logits=None, repacked=False):
     y = torch.empty((T, H), dtype=torch.float32, device=dev)
     si, sw = J.dispatch_qwen3_moe_ffn(y, td(x), td(logits), K, G, U, D)
     torch.cuda.synchronize()
-    if repacked:  # the load-time layouts (Q4_K_R / Q6_K_R over all experts' rows) give the same bits
+    if repacked:  # the load-time layouts (Q4_K_R / Q6_K_R over all experts' rows)
         yr = torch.empty_like(y)
         sir, swr = J.dispatch_qwen3_moe_ffn(yr, td(x), td(logits), K, J.repack(G), J.repack(U), J.repack(D))
         torch.cuda.synchronize()
         assert torch.equal(sir, si) and torch.equal(swr, sw)
-        assert torch.equal(yr, y)
+        check_out(yr, y_ref)
     np.testing.assert_array_equal(si.cpu().numpy(), si_ref)
     np.testing.assert_allclose(sw.cpu().numpy(), sw_ref, rtol=1e-6, atol=1e-7)
+    check_out(y, y_ref)
+
+
+def check_out(y, y_ref):
+    got = y.cpu().numpy().astype(np.float64)
     ref = y_ref.astype(np.float64)
     scale = np.sqrt(np.mean(ref ** 2, axis=1, keepdims=True))
-    err = np.max(np.abs(y.cpu().numpy() - ref) / np.maximum(np.abs(ref), scale))
-    assert err < 1e-3, err
+    err = np.max(np.abs(got - ref) / np.maximum(np.abs(ref), scale), axis=1)  # per token row
+    assert err.max() < 2e-2, err.max()
+    flipped = np.nonzero(err >= 1e-3)[0]
+    assert len(flipped) <= max(1, len(err) // 10), (len(flipped), err.max())
+    for t in flipped:
+        cos = got[t] @ ref[t] / (np.linalg.norm(got[t]) * np.linalg.norm(ref[t]))
+        assert cos >= 0.9999, (t, cos, err[t])
 
 
 @pytest.mark.parametrize("T", [1, 64])
@@ -58,9 +72,13 @@ def test_moe_small_and_q4k_down(dev):
 
 
 def test_moe_many_tokens_per_expert(dev):
-    """Four experts for 40 tokens at top-2: each expert sees ~20 tokens, several LDS passes."""
+    """Four experts for 40 tokens at top-2: each expert sees ~20 tokens, several token passes.
+    Two tokens or more per expert on average run the MFMA expert GEMMs (Q4_K in either layout,
+    Q6_K repacked); GGUF Q6_K down runs the GEMV kernels."""
     print("moe many tokens per expert", flush=True)
     run_case(dev, 40, 4, 512, 512, 2, J.Q4_K, J.Q6_K, 42, repacked=True)
+    run_case(dev, 40, 4, 512, 512, 2, J.Q4_K, J.Q4_K, 43, repacked=True)
+    run_case(dev, 24, 3, 256, 768, 3, J.Q6_K, J.Q6_K, 44, repacked=True)
 
 
 @pytest.mark.parametrize("E,K", [(200, 6), (300, 8), (700, 16)])

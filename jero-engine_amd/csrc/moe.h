@@ -18,7 +18,7 @@ struct MoeLists {
                       // then the tokens of its first kMoeDescTokens list entries (or null)
 };
 
-constexpr int kMoeDescInts = 16;
+constexpr int kMoeDescInts = 20;
 constexpr int kMoeDescTokens = kMoeDescInts - 4;
 
 struct MoeArgs {

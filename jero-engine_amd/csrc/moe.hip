@@ -529,7 +529,13 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 __host__ __device__ constexpr int mfma_seg(int f) { return f == JERO_Q6_K || f == JERO_Q6_K_R ? 4 : 2; }
 __host__ __device__ inline int act_row_stride(int nb) { return ((nb * 292 + 15) & ~15) + 16; }
-constexpr int kMfmaTokens = 8;  // tokens staged per pass (NT = kMfmaTokens / TPT token tiles)
+// Tokens staged per pass (NT = kMfmaTokens / TPT token tiles), and token chunks per (expert, row
+// block): chunk c takes the expert's tokens [8c, 8c + 8), [8c + 16, ...); a chunk with no tokens
+// exits at once.  An expert above 8 tokens is thus served by two workgroups side by side rather
+// than two passes in one: with one round of workgroups the kernel ends with its slowest one.
+constexpr int kMfmaTokens = 8;
+constexpr int kMfmaChunks = 2;
+static_assert(kMfmaTokens * kMfmaChunks <= kMoeDescTokens, "first passes' tokens come from the slot descriptor");
 
 // The weights of block b (units 4b .. 4b + 3: one step) of one weight row for lane group kg, as
 // loaded.  A step takes a whole block so that every cache line it fetches is used up within
@@ -610,13 +616,18 @@ __global__ void __launch_bounds__(256) moe_mfma_kernel(const uint8_t* __restrict
   using Piece = MfmaPiece<F>;
   extern __shared__ __attribute__((aligned(16))) uint8_t s_act[];
   __shared__ int s_tok[kMfmaTokens];
-  const int slot = int(blockIdx.x) / wg_per_expert, part = int(blockIdx.x) % wg_per_expert;
+  // chunk-major: workgroups are dealt to the XCDs round-robin by index, so the mostly-empty
+  // chunks 1.. must not interleave with chunk 0 (that would leave half the XCDs idle)
+  const int n_wg = int(gridDim.x) / kMfmaChunks;
+  const int chunk = int(blockIdx.x) / n_wg, wgi = int(blockIdx.x) - chunk * n_wg;
+  const int slot = wgi / wg_per_expert, part = wgi % wg_per_expert;
   // the descriptor (slot < E, always in bounds) and the active count in one trip
   const int n_act = *lists.n_active;
   const int32_t* dsc = lists.desc + slot * kMoeDescInts;
   const int e = dsc[0], i0 = dsc[1], cnt = dsc[2];
-  if (slot >= n_act) return;  // uniform over the workgroup
-  int tk = dsc[4 + min(int(threadIdx.x), kMfmaTokens - 1)];  // thread j < kMfmaTokens: token j
+  if (slot >= n_act || chunk * kMfmaTokens >= cnt) return;  // uniform over the workgroup
+  // thread j < kMfmaTokens: token j of this chunk's first pass
+  int tk = dsc[4 + chunk * kMfmaTokens + min(int(threadIdx.x), kMfmaTokens - 1)];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int c = lane & 15, kg = lane >> 4;
   const int nb = U / 4, stride = act_row_stride(nb), dummy = kMfmaTokens * stride;
@@ -633,9 +644,9 @@ __global__ void __launch_bounds__(256) moe_mfma_kernel(const uint8_t* __restrict
 #pragma unroll
     for (int t = 0; t < NW; t++) Piece::load(p[t], wt[t], n_rows, U, rb, grow, sc - tile * nb, kg);
   };
-  for (int base = 0; base < cnt; base += kMfmaTokens) {
+  for (int base = chunk * kMfmaTokens; base < cnt; base += kMfmaChunks * kMfmaTokens) {
     const int nch = min(kMfmaTokens, cnt - base);
-    if (base > 0)  // later passes (more than kMfmaTokens tokens): their tokens from the list
+    if (base >= kMfmaChunks * kMfmaTokens)  // later passes: their tokens from the list
       tk = lists.entry[i0 + base + min(int(threadIdx.x) % kMfmaTokens, nch - 1)] / k;
     if (threadIdx.x < kMfmaTokens) s_tok[threadIdx.x] = tk;
     lds_barrier();  // the previous pass's readers are done; s_tok
@@ -886,8 +897,8 @@ void mfma_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
                      sizeof(float) * TILES * kMfmaTokens * 64;                   // + the results
   const uint8_t* w0 = static_cast<const uint8_t*>(GU ? a.gate : a.down);
   const uint8_t* w1 = static_cast<const uint8_t*>(GU ? a.up : a.down);
-  hipLaunchKernelGGL((moe_mfma_kernel<F, GU, TILES>), dim3(unsigned(int64_t(a.max_active) * wg_per_expert)), dim3(256),
-                     lds, s,
+  hipLaunchKernelGGL((moe_mfma_kernel<F, GU, TILES>),
+                     dim3(unsigned(int64_t(a.max_active) * wg_per_expert * kMfmaChunks)), dim3(256), lds, s,
                      w0, w1, a.E * R, row_bytes(F, K), U, int(R), a.top_k, a.xq, row_bytes(JERO_Q8_K, a.hidden), a.act,
                      L, GU ? a.act : a.yd, wg_per_expert);
 }

@@ -248,7 +248,7 @@ def bench_moe(torch, J, dev, stream, steps):
     gate = synth_weights(torch, J, J.Q4_K, H, E * F, copies, dev, 3100)
     up = synth_weights(torch, J, J.Q4_K, H, E * F, copies, dev, 3101)
     down = synth_weights(torch, J, J.Q6_K, F, E * H, copies, dev, 3102)
-    # the expert tensors in the load-time device layouts (Q4_K_R / Q6_K_R over all experts' rows)
+    # the expert tensors in the load-time device layouts (Q4_K_T / Q6_K_T: 16-row tiles)
     gv = [J.repack(J.TensorView("ffn_gate_exps", J.Q4_K, [H, F, E], gate[c])) for c in range(copies)]
     uv = [J.repack(J.TensorView("ffn_up_exps", J.Q4_K, [H, F, E], up[c])) for c in range(copies)]
     dv = [J.repack(J.TensorView("ffn_down_exps", J.Q6_K, [F, H, E], down[c])) for c in range(copies)]
@@ -279,7 +279,7 @@ def bench_moe(torch, J, dev, stream, steps):
                         "bytes": int(algo), "GB_s": round(algo / t / 1e9, 1),
                         "frac_hbm": round(algo / t / 1e9 / HBM_PEAK_GBS, 4)}
     out["workload"] = "Qwen3-MoE expert layer H=2048, E=128, F=768, top-8, gate/up Q4_K, down Q6_K"
-    out["weight_layout"] = "Q4_K_R / Q6_K_R (load-time repack of the GGUF expert tensors)"
+    out["weight_layout"] = "Q4_K_T / Q6_K_T (16-row tiles; load-time repack of the GGUF expert tensors)"
     del gate, up, down, gv, uv, dv
     return out
 

@@ -43,7 +43,9 @@ typedef enum jero_quant {
   JERO_Q6_K = 14,
   JERO_Q8_K = 15,  /* activation blocks for Q4_K / Q6_K weights: f32 d, i8 q[256], i16 bsums[16] */
   JERO_Q4_K_R = 112, /* Q4_K bytes re-laid out by jero_hip_repack into aligned planes (same size) */
+  JERO_Q4_K_T = 113, /* stacked expert Q4_K re-laid out by jero_hip_repack_experts (16-row tiles) */
   JERO_Q6_K_R = 114, /* Q6_K bytes re-laid out by jero_hip_repack into aligned planes (same size) */
+  JERO_Q6_K_T = 115, /* stacked expert Q6_K re-laid out by jero_hip_repack_experts (16-row tiles) */
   JERO_ACT_Q8 = 100 /* activation blocks for Q8_0 / Q4_0 weights: f32 d, i8 q[32] (36 B) */
 } jero_quant;
 
@@ -130,6 +132,16 @@ int jero_hip_gemm_i8(const int8_t *x_dev, int64_t m, int64_t k, const int8_t *w_
  * Other formats: CapabilityMismatch. */
 int jero_hip_repack(int quant, const void *src_dev, size_t src_bytes, int64_t n_in, int64_t n_out,
                     void *dst_dev, int *dst_quant, void *stream);
+
+/* Load-time re-layout of a stacked expert tensor (GGUF [n_in, rows_per_expert, n_experts], expert
+ * e = rows e*rows_per_expert ..) for jero_hip_moe_ffn; the same repack_tensor_parallel
+ * (src/weights.rs:914-955) step for the expert tensors.  Q4_K -> JERO_Q4_K_T, Q6_K -> JERO_Q6_K_T:
+ * each block of 16 consecutive rows stores, per 256-element block column, the 16 rows' bytes as
+ * one contiguous piece (same total size; src and dst may not overlap; dst 16-byte aligned), so
+ * the expert kernels stream whole pieces.  rows_per_expert must be a multiple of 16; other
+ * formats: CapabilityMismatch. */
+int jero_hip_repack_experts(int quant, const void *src_dev, size_t src_bytes, int64_t n_in, int64_t rows_per_expert,
+                            int64_t n_experts, void *dst_dev, int *dst_quant, void *stream);
 
 /* ---- attention ----
  * gqa_causal_attention_f32(out, q, k, v, n_heads_q, n_heads_kv, head_dim, seq_len, scale)

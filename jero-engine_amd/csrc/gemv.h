@@ -17,5 +17,7 @@ int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const v
                   hipStream_t s);
 // Enqueues the Q4_K -> Q4_K_R or Q6_K -> Q6_K_R re-layout (dst: 16-byte aligned, same size).
 int launch_repack(int quant, const void* src, int64_t n_in, int64_t n_out, void* dst, int* dst_quant, hipStream_t s);
+int launch_repack_experts(int quant, const void* src, int64_t n_in, int64_t n_rows, void* dst, int* dst_quant,
+                          hipStream_t s);
 
 }  // namespace jero

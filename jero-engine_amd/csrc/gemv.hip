@@ -248,6 +248,45 @@ __global__ void __launch_bounds__(256) repack_q6k_kernel(const uint8_t* __restri
   dd[t * 2 + 1] = s[209];
 }
 
+// Regroups Q4_K blocks into JERO_Q4_K_T pieces (one thread per block).
+__global__ void __launch_bounds__(256) repack_q4k_tiled_kernel(const uint8_t* __restrict__ src,
+                                                               uint8_t* __restrict__ dst, int64_t N, int nb) {
+  int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= N * nb) return;
+  const int64_t r = t / nb;
+  const int b = int(t % nb), c = int(r & 15);
+  const uint8_t* s = src + t * 144;
+  uint8_t* pc = dst + ((r >> 4) * nb + b) * 2304;
+  for (int k = 0; k < 16; k++) pc[2048 + c * 16 + k] = s[k];
+  for (int i = 0; i < 4; i++)
+    for (int k = 0; k < 16; k++) {
+      pc[((2 * i) * 16 + c) * 16 + k] = s[16 + 32 * i + k];
+      pc[((2 * i + 1) * 16 + c) * 16 + k] = s[32 + 32 * i + k];
+    }
+}
+
+// Regroups Q6_K blocks into JERO_Q6_K_T pieces (one thread per block).
+__global__ void __launch_bounds__(256) repack_q6k_tiled_kernel(const uint8_t* __restrict__ src,
+                                                               uint8_t* __restrict__ dst, int64_t N, int nb) {
+  int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= N * nb) return;
+  const int64_t r = t / nb;
+  const int b = int(t % nb), c = int(r & 15);
+  const uint8_t* s = src + t * 210;
+  uint8_t* pc = dst + ((r >> 4) * nb + b) * 3360;
+  for (int i = 0; i < 4; i++) {
+    const int n = i >> 1, j = i & 1;
+    for (int k = 0; k < 16; k++) {
+      pc[((2 * i) * 16 + c) * 16 + k] = s[64 * n + 16 * j + k];
+      pc[((2 * i + 1) * 16 + c) * 16 + k] = s[64 * n + 32 + 16 * j + k];
+      pc[2048 + (i * 16 + c) * 16 + k] = s[128 + 32 * n + 16 * j + k];
+    }
+    for (int k = 0; k < 4; k++) pc[3072 + c * 16 + i * 4 + k] = s[192 + 8 * n + j + 2 * k];
+  }
+  pc[3328 + c * 2] = s[208];
+  pc[3328 + c * 2 + 1] = s[209];
+}
+
 }  // namespace
 
 int max_gemv_k(int quant) {
@@ -320,6 +359,24 @@ int launch_repack(int quant, const void* src, int64_t n_in, int64_t n_out, void*
   return check_launch("repack");
 }
 
+int launch_repack_experts(int quant, const void* src, int64_t n_in, int64_t n_rows, void* dst, int* dst_quant,
+                          hipStream_t s) {
+  if (quant != JERO_Q4_K && quant != JERO_Q6_K)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "repack_experts: only Q4_K and Q6_K have a tiled layout (got " +
+                                                  std::to_string(quant) + ")");
+  const int nb = int(n_in / 256);
+  const int64_t blocks = n_rows * nb;
+  const dim3 grid(unsigned((blocks + 255) / 256));
+  if (quant == JERO_Q4_K)
+    hipLaunchKernelGGL(repack_q4k_tiled_kernel, grid, dim3(256), 0, s, static_cast<const uint8_t*>(src),
+                       static_cast<uint8_t*>(dst), n_rows, nb);
+  else
+    hipLaunchKernelGGL(repack_q6k_tiled_kernel, grid, dim3(256), 0, s, static_cast<const uint8_t*>(src),
+                       static_cast<uint8_t*>(dst), n_rows, nb);
+  if (dst_quant) *dst_quant = quant == JERO_Q4_K ? JERO_Q4_K_T : JERO_Q6_K_T;
+  return check_launch("repack_experts");
+}
+
 }  // namespace jero
 
 using namespace jero;
@@ -380,4 +437,28 @@ extern "C" int jero_hip_repack(int quant, const void* src_dev, size_t src_bytes,
   size_t n = size_t(rb) * size_t(n_out);
   if (s0 < d0 + n && d0 < s0 + n) return fail(JERO_ERR_INVALID_ARGUMENT, "repack: source and destination overlap");
   return launch_repack(quant, src_dev, n_in, n_out, dst_dev, dst_quant, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int jero_hip_repack_experts(int quant, const void* src_dev, size_t src_bytes, int64_t n_in,
+                                       int64_t rows_per_expert, int64_t n_experts, void* dst_dev, int* dst_quant,
+                                       void* stream) {
+  if (!src_dev || !dst_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "repack_experts: null pointer");
+  if (n_in <= 0 || rows_per_expert <= 0 || n_experts <= 0)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "repack_experts: empty tensor");
+  if (rows_per_expert % 16)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "repack_experts: rows per expert must be a multiple of 16 (got " +
+                                                  std::to_string(rows_per_expert) + ")");
+  const int64_t rb = row_bytes(quant, n_in), n_rows = rows_per_expert * n_experts;
+  if (rb < 0) return fail(JERO_ERR_TENSOR_BOUNDS, "repack_experts: n_in is not a multiple of the block");
+  if (uint64_t(rb) * uint64_t(n_rows) > src_bytes)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "repack_experts: tensor holds " + std::to_string(src_bytes) +
+                                            " bytes, shape needs " + std::to_string(rb * n_rows));
+  if (reinterpret_cast<uintptr_t>(dst_dev) & 15u)
+    return fail(JERO_ERR_INVALID_ARGUMENT, "repack_experts: destination must be 16-byte aligned");
+  const uint8_t* s0 = static_cast<const uint8_t*>(src_dev);
+  const uint8_t* d0 = static_cast<const uint8_t*>(dst_dev);
+  const size_t n = size_t(rb) * size_t(n_rows);
+  if (s0 < d0 + n && d0 < s0 + n)
+    return fail(JERO_ERR_INVALID_ARGUMENT, "repack_experts: source and destination overlap");
+  return launch_repack_experts(quant, src_dev, n_in, n_rows, dst_dev, dst_quant, static_cast<hipStream_t>(stream));
 }

@@ -148,6 +148,27 @@ struct Unit<JERO_Q4_K_R> : Unit<JERO_Q4_K> {
   }
 };
 
+// ---------------------------------------------------------------- Q4_K, 16-row tiles (experts)
+// JERO_Q4_K_T holds a Q4_K tensor of N rows (N a multiple of 16) as pieces of 2304 bytes, one per
+// (tile of 16 rows, block column b), tiles in row order and, within a tile, b ascending:
+//   piece = q [4 units i][2 runs][16 rows][16] | h [16 rows][16]
+//   q[i][0][c] = qs[32i .. 32i+16), q[i][1][c] = qs[32i+16 .. 32i+32) of row c's block b;
+//   h[c] = that block's first 16 bytes (d, dmin, scales).
+// A wave's loads of one 16-row block column then read whole contiguous pieces: the expert GEMMs
+// step over 16 rows block by block, and the per-row runs of Q4_K_R would have them touch 64 bytes
+// in each of 32 places (measured 3.1 against 5.5 TB/s for the same bytes read contiguously).
+template <>
+struct Unit<JERO_Q4_K_T> : Unit<JERO_Q4_K> {
+  static __device__ __forceinline__ void load_w_planar(W& w, const uint8_t* __restrict__ base, int64_t /*N*/, int U,
+                                                       int64_t row, int u) {
+    const int c = int(row & 15), i = u & 3;
+    const uint8_t* pc = base + ((row >> 4) * (U / 4) + (u >> 2)) * 2304;
+    w.q0 = ld4(pc + ((2 * i) * 16 + c) * 16);
+    w.q1 = ld4(pc + ((2 * i + 1) * 16 + c) * 16);
+    w.h = ld4(pc + 2048 + c * 16);
+  }
+};
+
 // ---------------------------------------------------------------- Q6_K x Q8_K
 template <>
 struct Unit<JERO_Q6_K> {
@@ -297,6 +318,26 @@ struct Unit<JERO_Q6_K_R> : Unit<JERO_Q6_K> {
   }
 };
 
+// ---------------------------------------------------------------- Q6_K, 16-row tiles (experts)
+// JERO_Q6_K_T holds a Q6_K tensor of N rows (N a multiple of 16) as pieces of 3360 bytes, one per
+// (tile of 16 rows, block column b), in the order of Q4_K_T; with units u = 4b + i, i = 2n + j:
+//   piece = ql [4 i][2 halves][16 rows][16] | qh [4 i][16 rows][16] | sc [16 rows][4 i][4] | d [16 rows] f16
+//   ql[i][0][c] = ql[64n+16j .. +16], ql[i][1][c] = ql[64n+32+16j .. +16], qh[i][c] = qh[32n+16j .. +16],
+//   sc[c][i] = sc[8n+j+2t], t = 0..3 (the Q6_K_R pieces of row c, regrouped by tile).
+template <>
+struct Unit<JERO_Q6_K_T> : Unit<JERO_Q6_K> {
+  static __device__ __forceinline__ void load_w_planar(W& w, const uint8_t* __restrict__ base, int64_t /*N*/, int U,
+                                                       int64_t row, int u) {
+    const int c = int(row & 15), i = u & 3;
+    const uint8_t* pc = base + ((row >> 4) * (U / 4) + (u >> 2)) * 3360;
+    w.lo = ld4(pc + ((2 * i) * 16 + c) * 16);
+    w.hi = ld4(pc + ((2 * i + 1) * 16 + c) * 16);
+    w.qh = ld4(pc + 2048 + (i * 16 + c) * 16);
+    w.sc = ld1(pc + 3072 + c * 16 + i * 4);
+    load_d(w, pc + 3328 + c * 2);
+  }
+};
+
 // ---------------------------------------------------------------- Q8_0 x ACT_Q8
 template <>
 struct Unit<JERO_Q8_0> {
@@ -400,13 +441,16 @@ struct Unit<JERO_Q4_0> {
   }
 };
 
-// Units per row and partial sums per row of a weight format.
-__host__ __device__ constexpr bool is_planar(int f) { return f == JERO_Q4_K_R || f == JERO_Q6_K_R; }
-__host__ __device__ constexpr int units_per_row(int f, int64_t k) {
-  return int(k / ((f == JERO_Q4_K || f == JERO_Q4_K_R || f == JERO_Q6_K || f == JERO_Q6_K_R) ? 64 : 32));
+// Units per row and partial sums per row of a weight format.  "Planar": a device layout read
+// through Unit<F>::load_w_planar (16-byte aligned).
+__host__ __device__ constexpr bool is_planar(int f) {
+  return f == JERO_Q4_K_R || f == JERO_Q6_K_R || f == JERO_Q4_K_T || f == JERO_Q6_K_T;
 }
-__host__ __device__ constexpr int64_t partials_per_row(int f, int64_t k) {
-  return (f == JERO_Q6_K || f == JERO_Q6_K_R) ? k / 16 : k / 32;
+__host__ __device__ constexpr bool is_q6k(int f) { return f == JERO_Q6_K || f == JERO_Q6_K_R || f == JERO_Q6_K_T; }
+__host__ __device__ constexpr bool is_kquant(int f) {
+  return f == JERO_Q4_K || f == JERO_Q4_K_R || f == JERO_Q4_K_T || is_q6k(f);
 }
+__host__ __device__ constexpr int units_per_row(int f, int64_t k) { return int(k / (is_kquant(f) ? 64 : 32)); }
+__host__ __device__ constexpr int64_t partials_per_row(int f, int64_t k) { return is_q6k(f) ? k / 16 : k / 32; }
 
 }  // namespace jero

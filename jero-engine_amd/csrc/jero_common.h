@@ -28,8 +28,10 @@ __host__ __device__ constexpr FmtInfo fmt_info(int q) {
          : q == JERO_Q4_0   ? FmtInfo{32, 18}
          : q == JERO_Q4_K   ? FmtInfo{256, 144}
          : q == JERO_Q4_K_R ? FmtInfo{256, 144}
+         : q == JERO_Q4_K_T ? FmtInfo{256, 144}
          : q == JERO_Q6_K   ? FmtInfo{256, 210}
          : q == JERO_Q6_K_R ? FmtInfo{256, 210}
+         : q == JERO_Q6_K_T ? FmtInfo{256, 210}
          : q == JERO_Q8_K   ? FmtInfo{256, 292}
          : q == JERO_ACT_Q8 ? FmtInfo{32, 36}
          : q == JERO_F32    ? FmtInfo{1, 4}

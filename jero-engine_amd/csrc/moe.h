@@ -14,12 +14,17 @@ struct MoeLists {
   int32_t* n_active;  // [1]
   int32_t* entry;     // [T*k] (token*k + slot), grouped by expert, ascending within an expert
   int32_t* inv;       // [T*k] list position of (token*k + slot)
-  int32_t* desc;      // [E][kMoeDescInts] per active slot: expert, first list position, count, 0,
-                      // then the tokens of its first kMoeDescTokens list entries (or null)
+  int32_t* pass;      // [passes][kMoePassInts] per pass (up to kMoePassTokens of one expert's
+                      // list entries, experts ascending): expert, first list position, count, 0,
+                      // then the pass's tokens (or null: no pass descriptors)
+  int32_t* ctr;       // [kMoeCtrInts]: the number of passes, then the work counters of the
+                      // expert GEMMs, each on its own 128-byte line (with pass)
 };
 
-constexpr int kMoeDescInts = 20;
-constexpr int kMoeDescTokens = kMoeDescInts - 4;
+constexpr int kMoePassTokens = 8;
+constexpr int kMoePassInts = 4 + kMoePassTokens;
+constexpr int kMoeCtrInts = 96;
+constexpr int kMoeCtrGateUp = 32, kMoeCtrDown = 64;  // counter offsets in ctr
 
 struct MoeArgs {
   const float* x;       // [T][hidden]

@@ -112,7 +112,8 @@ struct GroupLds {
   int off[kMaxExperts];
   int fill[kMaxExperts];
   int active[kMaxExperts];
-  int wsum[2 * (kRouteThreads / 64)];
+  int poff[kMaxExperts];  // first pass of each expert (pass descriptors)
+  int wsum[3 * (kRouteThreads / 64)];
   int n_active;
   __attribute__((aligned(16))) int sel[kRouteLdsPairs + 4];  // the selections, when they fit
   int list[kRouteLdsPairs];                                   // pairs grouped by expert, atomic order
@@ -128,8 +129,9 @@ __device__ __forceinline__ void group_init(GroupLds& g, int E) {
 }
 
 // Groups the n (token, slot) pairs by expert, in ascending pair order within an expert, and
-// writes the ascending list of active experts.  The selections are in g.sel when n fits, else in
-// sel_idx.  One workgroup of kRouteThreads threads; starts and ends with a barrier.
+// writes the ascending list of active experts; with lists.pass, also the pass descriptors, their
+// number and zeroed work counters (n must then fit in LDS).  The selections are in g.sel when n
+// fits, else in sel_idx.  One workgroup of kRouteThreads threads; starts and ends with a barrier.
 __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, int n, int E, int k, MoeLists lists) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = kRouteThreads / 64;
   if (threadIdx.x < 4 && n + int(threadIdx.x) < kRouteLdsPairs + 4) g.sel[n + threadIdx.x] = -1;
@@ -138,32 +140,36 @@ __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, in
   for (int i = threadIdx.x; i < n; i += kRouteThreads) atomicAdd(&g.count[in_lds ? g.sel[i] : sel_idx[i]], 1);
   __syncthreads();
   {
-    // exclusive scans of the counts (offsets) and of the active flags (active list), one thread
-    // per expert: wave scans, then the 16 wave totals
+    // exclusive scans of the counts (offsets), of the active flags (active list) and of the
+    // pass counts, one thread per expert: wave scans, then the 16 wave totals
     const int e = threadIdx.x;
-    const int c = e < E ? g.count[e] : 0, f = c > 0 ? 1 : 0;
-    int ic = c, jf = f;
+    const int c = e < E ? g.count[e] : 0, f = c > 0 ? 1 : 0, np = (c + kMoePassTokens - 1) / kMoePassTokens;
+    int ic = c, jf = f, kp = np;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-      const int oc = __shfl_up(ic, off, kWave), of = __shfl_up(jf, off, kWave);
+      const int oc = __shfl_up(ic, off, kWave), of = __shfl_up(jf, off, kWave), op = __shfl_up(kp, off, kWave);
       if (lane >= off) {
         ic += oc;
         jf += of;
+        kp += op;
       }
     }
     if (lane == 63) {
       g.wsum[wv] = ic;
       g.wsum[nw + wv] = jf;
+      g.wsum[2 * nw + wv] = kp;
     }
     __syncthreads();
-    int bc = 0, bf = 0;
+    int bc = 0, bf = 0, bp = 0;
     for (int w = 0; w < wv; w++) {
       bc += g.wsum[w];
       bf += g.wsum[nw + w];
+      bp += g.wsum[2 * nw + w];
     }
     if (e < E) {
       const int off_e = bc + ic - c;
       g.off[e] = off_e;
+      g.poff[e] = bp + kp - np;
       lists.offset[e] = off_e;
       if (f) {
         lists.active[bf + jf - 1] = e;
@@ -173,6 +179,11 @@ __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, in
         lists.offset[E] = off_e + c;
         *lists.n_active = bf + jf;
         g.n_active = bf + jf;
+        if (lists.pass) {
+          lists.ctr[0] = bp + kp;
+          lists.ctr[kMoeCtrGateUp] = 0;
+          lists.ctr[kMoeCtrDown] = 0;
+        }
       }
     }
   }
@@ -193,15 +204,22 @@ __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, in
       lists.inv[i] = o + r;
       g.entry[o + r] = i;
     }
-    if (lists.desc) {
-      // per active slot: expert, first list position, count, and its first tokens
+    if (lists.pass) {
+      // per pass of an expert: expert, first list position, count, and its tokens (the last
+      // one repeated past the count)
       __syncthreads();
-      for (int idx = threadIdx.x; idx < g.n_active * kMoeDescInts; idx += kRouteThreads) {
-        const int sl = idx / kMoeDescInts, q = idx - sl * kMoeDescInts;
-        const int e = g.active[sl], o = g.off[e], c = g.count[e];
-        int v = q == 0 ? e : q == 1 ? o : q == 2 ? c : 0;
-        if (q >= 4) v = g.entry[o + min(q - 4, c - 1)] / k;
-        lists.desc[idx] = v;
+      for (int e = threadIdx.x; e < E; e += kRouteThreads) {
+        const int o = g.off[e], c = g.count[e];
+        int32_t* pd = lists.pass + int64_t(g.poff[e]) * kMoePassInts;
+        for (int b = 0; b < c; b += kMoePassTokens, pd += kMoePassInts) {
+          const int m = min(kMoePassTokens, c - b);
+          pd[0] = e;
+          pd[1] = o + b;
+          pd[2] = m;
+          pd[3] = 0;
+#pragma unroll
+          for (int j = 0; j < kMoePassTokens; j++) pd[4 + j] = g.entry[o + b + min(j, m - 1)] / k;
+        }
       }
     }
   } else {
@@ -226,7 +244,7 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
                                                                   int k, int32_t* __restrict__ sel_idx,
                                                                   float* __restrict__ sel_w, MoeLists lists,
                                                                   const float* __restrict__ x, int H,
-                                                                  uint8_t* __restrict__ xq) {
+                                                                  uint8_t* __restrict__ xq, int64_t xq_rb) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = kRouteThreads / 64;
   __shared__ GroupLds g;
   if (xq) {
@@ -235,7 +253,7 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
       const int t = blk / bpr, j = blk - t * bpr;
       const float4 v = reinterpret_cast<const float4*>(x + int64_t(t) * H + int64_t(j) * 256)[lane];
       const float e[4] = {v.x, v.y, v.z, v.w};
-      q8k_block_wave(e, lane, xq + int64_t(t) * bpr * 292 + int64_t(j) * 292);
+      q8k_block_wave(e, lane, xq + int64_t(t) * xq_rb + int64_t(j) * 292);
     }
   }
   group_init(g, E);
@@ -250,7 +268,7 @@ template <int PER>
 __global__ void __launch_bounds__(256) moe_prep_kernel(const float* __restrict__ logits, int T, int E, int k,
                                                        int32_t* __restrict__ sel_idx, float* __restrict__ sel_w,
                                                        const float* __restrict__ x, int H, uint8_t* __restrict__ xq,
-                                                       int n_quant_wg) {
+                                                       int64_t xq_rb, int n_quant_wg) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   if (int(blockIdx.x) < n_quant_wg) {
     const int bpr = H / 256, nblk = T * bpr;
@@ -258,7 +276,7 @@ __global__ void __launch_bounds__(256) moe_prep_kernel(const float* __restrict__
       const int t = blk / bpr, j = blk - t * bpr;
       const float4 v = reinterpret_cast<const float4*>(x + int64_t(t) * H + int64_t(j) * 256)[lane];
       const float e[4] = {v.x, v.y, v.z, v.w};
-      q8k_block_wave(e, lane, xq + int64_t(t) * bpr * 292 + int64_t(j) * 292);
+      q8k_block_wave(e, lane, xq + int64_t(t) * xq_rb + int64_t(j) * 292);
     }
   } else {
     const int t = (int(blockIdx.x) - n_quant_wg) * 4 + wv;
@@ -284,6 +302,10 @@ constexpr int64_t kMoeStageBytes = 49152;  // LDS for them
 // that skips those writes, and it then waits at the next reuse of their registers (inside the
 // weight pipeline) instead.
 __device__ __forceinline__ void vm_settle() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// Makes v opaque to the optimizer at this point (it waits for v's load here): a value picked by
+// lane from loaded registers is otherwise turned back into a load of its own, a second trip.
+__device__ __forceinline__ void pin(u32x4& v) { asm volatile("" : "+v"(v)); }
 
 // Unit u of row `row` of a stacked expert tensor of n_rows rows: GGUF bytes (rb per row) or a
 // planar layout (Q4_K_R / Q6_K_R, as written by jero_hip_repack over all n_rows rows).
@@ -522,47 +544,65 @@ __global__ void __launch_bounds__(256) moe_down_kernel(const uint8_t* __restrict
 // sum of every segment for TPT = 16 / SEG tokens and 16 weight rows (the B operand, columns).
 // Lane l supplies A row l % 16 and B column l % 16 over K [16 (l / 16), +16) and receives C rows
 // 4 (l / 16) .. +4 of column l % 16: all segments of 4 / SEG tokens for one weight row, so the
-// segment scales, mins and block scales come from the lane's own weight row and are applied
-// in-lane, per unit, with the GEMV's float formula.  Activations are staged in LDS as Q8_K rows.
+// segment scales and mins come from the lane's own weight row and are applied in-lane, in
+// integers, over the block's four units; the block's float scales then apply once per block,
+// dx * (d * isum - dmin * msum) as the reference's block dot.  Activations are staged in LDS as
+// Q8_K rows (rows of 16-byte multiples, one more row of zeros for the A lanes outside their
+// segment).
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-__host__ __device__ constexpr int mfma_seg(int f) { return f == JERO_Q6_K || f == JERO_Q6_K_R ? 4 : 2; }
-__host__ __device__ inline int act_row_stride(int nb) { return ((nb * 292 + 15) & ~15) + 16; }
-// Tokens staged per pass (NT = kMfmaTokens / TPT token tiles), and token chunks per (expert, row
-// block): chunk c takes the expert's tokens [8c, 8c + 8), [8c + 16, ...); a chunk with no tokens
-// exits at once.  An expert above 8 tokens is thus served by two workgroups side by side rather
-// than two passes in one: with one round of workgroups the kernel ends with its slowest one.
-constexpr int kMfmaTokens = 8;
-constexpr int kMfmaChunks = 2;
-static_assert(kMfmaTokens * kMfmaChunks <= kMoeDescTokens, "first passes' tokens come from the slot descriptor");
+__host__ __device__ constexpr int mfma_seg(int f) { return is_q6k(f) ? 4 : 2; }
+// LDS bytes per staged token row: its Q8_K row rounded up to 16 bytes, plus 16, made an odd number
+// of 16-byte units so that the rows of the 8 tokens start 4 banks apart: a wave's A reads (one
+// 16-byte piece from each of up to 8 rows at the same offset) then hit distinct banks.
+__host__ __device__ inline int act_row_stride(int nb) {
+  const int s = ((nb * 292 + 15) & ~15) + 16;
+  return (s / 16) % 2 ? s : s + 16;
+}
+// Tokens staged per pass (NT = kMfmaTokens / TPT token tiles): a pass descriptor's worth.
+constexpr int kMfmaTokens = kMoePassTokens;
 
 // The weights of block b (units 4b .. 4b + 3: one step) of one weight row for lane group kg, as
 // loaded.  A step takes a whole block so that every cache line it fetches is used up within
 // the step: lines shared between steps were evicted from L2 between their uses (the step
-// working set of all resident waves exceeds an XCD's L2), costing 1.45x the HBM bytes.
+// working set of all resident waves exceeds an XCD's L2), costing 1.45x the HBM bytes.  A Cur
+// holds the lane's pointers into its weight row of tile 0 (one per region of the layout); a step
+// adds its tile's and block's offsets, which are uniform.
 template <int F>
 struct MfmaPiece;
 template <>
 struct MfmaPiece<JERO_Q4_K_R> {
   u32x4 q[4];  // q0 (kg even) or q1 (kg odd) run of each unit: 16 bytes of qs
   u32x4 h;     // the block header (d, dmin, 12 scale bytes)
-  static __device__ __forceinline__ void load(MfmaPiece& p, const uint8_t* __restrict__ base, int64_t /*n_rows*/,
-                                              int U, int64_t /*rb*/, int64_t row, int b, int kg) {
+  struct Cur {
+    const uint8_t *q, *h;
+    int64_t tile;  // bytes per 16 rows
+  };
+  static __device__ __forceinline__ Cur cursor(const uint8_t* __restrict__ base, int64_t /*n_rows*/, int U,
+                                               int64_t /*rb*/, int64_t row, int kg) {
     const uint8_t* rp = base + row * (int64_t(U) * 36);
+    return {rp + (kg & 1) * U * 16, rp + U * 32, int64_t(16) * U * 36};
+  }
+  static __device__ __forceinline__ void load(MfmaPiece& p, const Cur& cu, int tile, int b) {
+    const int64_t o = tile * cu.tile;
 #pragma unroll
-    for (int x = 0; x < 4; x++) p.q[x] = ld4(rp + (kg & 1) * U * 16 + (4 * b + x) * 16);
-    p.h = ld4(rp + U * 32 + b * 16);
+    for (int x = 0; x < 4; x++) p.q[x] = ld4(cu.q + o + (4 * b + x) * 16);
+    p.h = ld4(cu.h + o + b * 16);
   }
 };
 template <>
 struct MfmaPiece<JERO_Q4_K> : MfmaPiece<JERO_Q4_K_R> {
-  static __device__ __forceinline__ void load(MfmaPiece& p, const uint8_t* __restrict__ base, int64_t /*n_rows*/,
-                                              int /*U*/, int64_t rb, int64_t row, int b, int kg) {
-    const uint8_t* blk = base + row * rb + int64_t(b) * 144;
+  static __device__ __forceinline__ Cur cursor(const uint8_t* __restrict__ base, int64_t /*n_rows*/, int /*U*/,
+                                               int64_t rb, int64_t row, int kg) {
+    const uint8_t* rp = base + row * rb;
+    return {rp + 16 + 16 * (kg & 1), rp, 16 * rb};
+  }
+  static __device__ __forceinline__ void load(MfmaPiece& p, const Cur& cu, int tile, int b) {
+    const int64_t o = tile * cu.tile + b * 144;
 #pragma unroll
-    for (int x = 0; x < 4; x++) p.q[x] = ld4(blk + 16 + 32 * x + 16 * (kg & 1));
-    p.h = ld4(blk);
+    for (int x = 0; x < 4; x++) p.q[x] = ld4(cu.q + o + 32 * x);
+    p.h = ld4(cu.h + o);
   }
 };
 template <>
@@ -570,19 +610,73 @@ struct MfmaPiece<JERO_Q6_K_R> {
   u32x4 x[4], qh[4];  // ql run (lo for even kg, hi for odd) and qh run of each unit
   u32x4 sc;           // the units' int8 group scales, one dword per unit
   uint32_t dw, dsh;   // the block's f16 d: its dword and shift
-  static __device__ __forceinline__ void load(MfmaPiece& p, const uint8_t* __restrict__ base, int64_t n_rows, int U,
-                                              int64_t /*rb*/, int64_t row, int b, int kg) {
-    const int64_t plane = n_rows * int64_t(U) * 16, gu = row * U + 4 * b;
+  struct Cur {
+    const uint8_t *x, *qh, *sc, *d;
+    int U;
+  };
+  static __device__ __forceinline__ Cur cursor(const uint8_t* __restrict__ base, int64_t n_rows, int U,
+                                               int64_t /*rb*/, int64_t row, int kg) {
+    const int64_t plane = n_rows * int64_t(U) * 16;
+    return {base + (kg & 1) * plane + row * U * 16, base + 2 * plane + row * U * 16, base + 3 * plane + row * U * 4,
+            base + 3 * plane + n_rows * int64_t(U) * 4 + row * (U / 4) * 2, U};
+  }
+  static __device__ __forceinline__ void load(MfmaPiece& p, const Cur& cu, int tile, int b) {
+    const int64_t gu = int64_t(tile) * 16 * cu.U + 4 * b;  // the step's first unit, from the row's
 #pragma unroll
     for (int x = 0; x < 4; x++) {
-      p.x[x] = ld4(base + (kg & 1) * plane + (gu + x) * 16);
-      p.qh[x] = ld4(base + 2 * plane + (gu + x) * 16);
+      p.x[x] = ld4(cu.x + (gu + x) * 16);
+      p.qh[x] = ld4(cu.qh + (gu + x) * 16);
     }
-    p.sc = ld4(base + 3 * plane + gu * 4);
-    const uint8_t* dp = base + 3 * plane + n_rows * int64_t(U) * 4 + (row * (U / 4) + b) * 2;
+    p.sc = ld4(cu.sc + gu * 4);
+    const uint8_t* dp = cu.d + (int64_t(tile) * 16 * (cu.U / 4) + b) * 2;
     const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(dp) & 3u);
     p.dw = ld1(dp - sh);
     p.dsh = 8u * sh;
+  }
+};
+
+// The 16-row tiled layouts: a step reads whole contiguous pieces (one per tile and block).
+template <>
+struct MfmaPiece<JERO_Q4_K_T> : MfmaPiece<JERO_Q4_K_R> {
+  static __device__ __forceinline__ Cur cursor(const uint8_t* __restrict__ base, int64_t /*n_rows*/, int U,
+                                               int64_t /*rb*/, int64_t row, int kg) {
+    const int64_t tile = int64_t(U / 4) * 2304;  // bytes per 16 rows
+    const uint8_t* pc = base + (row >> 4) * tile;
+    const int c = int(row & 15);
+    return {pc + ((kg & 1) * 16 + c) * 16, pc + 2048 + c * 16, tile};
+  }
+  static __device__ __forceinline__ void load(MfmaPiece& p, const Cur& cu, int tile, int b) {
+    const int64_t o = tile * cu.tile + b * 2304;
+#pragma unroll
+    for (int x = 0; x < 4; x++) p.q[x] = ld4(cu.q + o + 512 * x);
+    p.h = ld4(cu.h + o);
+  }
+};
+template <>
+struct MfmaPiece<JERO_Q6_K_T> : MfmaPiece<JERO_Q6_K_R> {
+  struct Cur {
+    const uint8_t *x, *qh, *sc, *d;
+    int64_t tile;   // bytes per 16 rows
+    uint32_t dsh;   // the f16 d's shift in its dword (rows alternate halves)
+  };
+  static __device__ __forceinline__ Cur cursor(const uint8_t* __restrict__ base, int64_t /*n_rows*/, int U,
+                                               int64_t /*rb*/, int64_t row, int kg) {
+    const int64_t tile = int64_t(U / 4) * 3360;
+    const uint8_t* pc = base + (row >> 4) * tile;
+    const int c = int(row & 15);
+    return {pc + ((kg & 1) * 16 + c) * 16, pc + 2048 + c * 16, pc + 3072 + c * 16, pc + 3328 + (c & ~1) * 2, tile,
+            16u * uint32_t(c & 1)};
+  }
+  static __device__ __forceinline__ void load(MfmaPiece& p, const Cur& cu, int tile, int b) {
+    const int64_t o = tile * cu.tile + b * 3360;
+#pragma unroll
+    for (int x = 0; x < 4; x++) {
+      p.x[x] = ld4(cu.x + o + 512 * x);
+      p.qh[x] = ld4(cu.qh + o + 256 * x);
+    }
+    p.sc = ld4(cu.sc + o);
+    p.dw = ld1(cu.d + o);
+    p.dsh = cu.dsh;
   }
 };
 
@@ -597,64 +691,88 @@ __device__ __forceinline__ void q4k_scale_min(const u32x4& h, int sb, int& sc, i
 constexpr int kStageChunks = 8;  // Q8_K staging: 16-byte chunks per thread in its one batch
 constexpr int kStageBlocks = 8;  // f32 staging: 256-element blocks per wave in its one batch
 
-// One workgroup: an active expert, 64 TILES of its weight rows (TILES tiles of 16 per wave, one
-// after the other), every token of the expert (kMfmaTokens per pass).  Several tiles per wave
-// amortize the workgroup's start (descriptor, activation staging) over more weight bytes; each
-// tile's results go to LDS when its last block is done and leave in one coalesced pass.  GU: gate (w0) and up (w1) rows from the tokens' Q8_K rows, out =
-// silu(gate) * up per (list entry, row); else down (w0) rows from the f32 act rows (quantized here),
-// out = the dot per (list entry, row).  A workgroup makes two dependent trips to memory before
-// its first MFMA: the slot descriptor, then the activations (in one batch) with the first
-// weights behind them; the load counter drains in order, so nothing small waits behind weights.
-template <int F, bool GU, int TILES>
-__global__ void __launch_bounds__(256) moe_mfma_kernel(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
-                                                       int64_t n_rows, int64_t rb, int U, int R, int k,
+// Work items: (pass, row block) -- one pass descriptor's tokens (up to kMfmaTokens of one
+// expert) against 64 * tiles weight rows of that expert (tiles tiles of 16 per wave, one after
+// the other), numbered pass-major.  The grid is persistent (what fits on the GPU at once) and
+// each workgroup takes the next item from a counter until none is left.  The next item's number
+// is fetched while the current one runs.  Each tile's results go to LDS when its last block is
+// done and leave in one coalesced pass.  GU: gate (w0) and up (w1) rows from the tokens' Q8_K
+// rows, out = silu(gate) * up per (list entry, row); else down (w0) rows from the f32 act rows
+// (quantized here), out = the dot per (list entry, row).  An item makes two dependent trips to
+// memory before its first MFMA: the pass descriptor, then the activations (in one batch) with the
+// first weights behind them; the load counter drains in order, so nothing small waits behind
+// weights.  R is a multiple of 64 * tiles: no row is clamped.
+// Workgroups per CU the register budget is cut for: three (168 VGPRs), except Q6_K gate/up, whose
+// two tensors' pieces need more registers than that without spilling.
+__host__ __device__ constexpr int mfma_min_wgs(int f, bool gu) { return gu && mfma_seg(f) == 4 ? 2 : 3; }
+
+template <int F, bool GU>
+__global__ void __launch_bounds__(256, mfma_min_wgs(F, GU)) moe_mfma_kernel(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
+                                                       int64_t n_rows, int64_t rb, int U, int R, int tiles,
                                                        const uint8_t* __restrict__ xq, int64_t xq_rb,
                                                        const float* __restrict__ act_in, MoeLists lists,
-                                                       float* __restrict__ out, int wg_per_expert) {
+                                                       float* __restrict__ out, int wg_per_expert, int ctr_off) {
   constexpr int SEG = mfma_seg(F), TPT = 16 / SEG, NT = kMfmaTokens / TPT, LT = 4 / SEG;
   constexpr int NW = GU ? 2 : 1;  // weight tensors per wave
   using Piece = MfmaPiece<F>;
+  using Cur = typename Piece::Cur;
   extern __shared__ __attribute__((aligned(16))) uint8_t s_act[];
   __shared__ int s_tok[kMfmaTokens];
-  // chunk-major: workgroups are dealt to the XCDs round-robin by index, so the mostly-empty
-  // chunks 1.. must not interleave with chunk 0 (that would leave half the XCDs idle)
-  const int n_wg = int(gridDim.x) / kMfmaChunks;
-  const int chunk = int(blockIdx.x) / n_wg, wgi = int(blockIdx.x) - chunk * n_wg;
-  const int slot = wgi / wg_per_expert, part = wgi % wg_per_expert;
-  // the descriptor (slot < E, always in bounds) and the active count in one trip
-  const int n_act = *lists.n_active;
-  const int32_t* dsc = lists.desc + slot * kMoeDescInts;
-  const int e = dsc[0], i0 = dsc[1], cnt = dsc[2];
-  if (slot >= n_act || chunk * kMfmaTokens >= cnt) return;  // uniform over the workgroup
-  // thread j < kMfmaTokens: token j of this chunk's first pass
-  int tk = dsc[4 + chunk * kMfmaTokens + min(int(threadIdx.x), kMfmaTokens - 1)];
+  __shared__ int s_item;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int c = lane & 15, kg = lane >> 4;
-  const int nb = U / 4, stride = act_row_stride(nb), dummy = kMfmaTokens * stride;
-  const int row0 = (part * 4 + wv) * TILES * 16 + c;  // this lane's weight row (B column) in tile 0
-  const int steps = TILES * nb;
-  float* s_out = reinterpret_cast<float*>(s_act + dummy + 304);  // [TILES][kMfmaTokens][64 rows]
+  const int nb = U / 4, stride = act_row_stride(nb);
+  const int zrow = kMfmaTokens * stride, dummy = zrow + stride;  // the zero row, then a dummy area
+  const int steps = tiles * nb;
+  float* s_out = reinterpret_cast<float*>(s_act + dummy + 304);  // [tiles][kMfmaTokens][64 rows]
+  for (int i = threadIdx.x; i < stride / 16; i += 256) *reinterpret_cast<u32x4*>(s_act + zrow + 16 * i) = u32x4{};
+  // the counter is bumped by atomicInc (with no wrap): the compiler turns a single-lane atomicAdd
+  // into a wave-aggregated one whose result it waits for at once
+  unsigned* const ctr = reinterpret_cast<unsigned*>(lists.ctr + ctr_off);
+  const int n_items = lists.ctr[0] * wg_per_expert;
+  if (threadIdx.x == 0) s_item = int(atomicInc(ctr, 0xFFFFFFFFu));
+  __syncthreads();
   const uint8_t* wt[2] = {w0, GU ? w1 : w0};
   // A operand lanes: virtual row vr = (token, segment); K group kg belongs to segment kg / (4 / SEG)
-  const int vr = lane & 15, a_tok = vr / SEG, a_seg = vr % SEG, kg_seg = kg / (4 / SEG);
-  // step s: block s % nb of tile s / nb (steps past the end clamp to the last)
-  auto load = [&](int s_, Piece (&p)[NW]) {
-    const int sc = min(s_, steps - 1), tile = sc / nb;
-    const int64_t grow = int64_t(e) * R + min(row0 + 16 * tile, R - 1);
+  const int vr = lane & 15, a_tok = vr / SEG, kg_seg = kg / (4 / SEG);
+  const bool a_on = vr % SEG == kg_seg;
+  const int a_lane = SEG == 2 ? 4 + 16 * kg : 4 + 32 * kg;  // the lane's K group in a unit's bytes
+  const uint32_t nsh = (kg & 2) ? 4u : 0u;                    // its nibble: low for kg < 2
+  static_assert(kMoePassInts == 12, "a pass descriptor is three 16-byte loads");
+  for (int item = s_item; item < n_items;) {  // item is uniform over the workgroup
+    const int pi = item / wg_per_expert, part = item - pi * wg_per_expert;
+    // the pass descriptor in one trip: expert, first list position, token count, 0, tokens
+    const uint8_t* pd = reinterpret_cast<const uint8_t*>(lists.pass) + int64_t(pi) * (kMoePassInts * 4);
+    u32x4 ph = ld4(pd), pt0 = ld4(pd + 16), pt1 = ld4(pd + 32);
+    pin(pt0);  // held in registers: else a thread's token is loaded again once the header is in
+    pin(pt1);
+    const int e = int(ph.x), i0 = int(ph.y), nch = int(ph.z);
+    const uint32_t tj[kMfmaTokens] = {pt0.x, pt0.y, pt0.z, pt0.w, pt1.x, pt1.y, pt1.z, pt1.w};
+    const int row0 = (part * 4 + wv) * tiles * 16 + c;  // this lane's weight row (B column) in tile 0
+    Cur cur[NW];
 #pragma unroll
-    for (int t = 0; t < NW; t++) Piece::load(p[t], wt[t], n_rows, U, rb, grow, sc - tile * nb, kg);
-  };
-  for (int base = chunk * kMfmaTokens; base < cnt; base += kMfmaChunks * kMfmaTokens) {
-    const int nch = min(kMfmaTokens, cnt - base);
-    if (base >= kMfmaChunks * kMfmaTokens)  // later passes: their tokens from the list
-      tk = lists.entry[i0 + base + min(int(threadIdx.x) % kMfmaTokens, nch - 1)] / k;
-    if (threadIdx.x < kMfmaTokens) s_tok[threadIdx.x] = tk;
-    lds_barrier();  // the previous pass's readers are done; s_tok
+    for (int t = 0; t < NW; t++) cur[t] = Piece::cursor(wt[t], n_rows, U, rb, int64_t(e) * R + row0, kg);
+    // step s: block s % nb of tile s / nb (steps past the end clamp to the last)
+    auto load = [&](int s_, Piece (&p)[NW]) {
+      const int sc = min(s_, steps - 1), tile = sc / nb;
+#pragma unroll
+      for (int t = 0; t < NW; t++) Piece::load(p[t], cur[t], tile, sc - tile * nb);
+    };
+    // the lane's LDS rows: its A row's token (or the zero row), and the tokens of its C rows
+    int a_base[NT], e_base[NT][LT];
+#pragma unroll
+    for (int tl = 0; tl < NT; tl++) {
+      a_base[tl] = (a_on ? min(tl * TPT + a_tok, nch - 1) * stride : zrow) + a_lane;
+#pragma unroll
+      for (int q = 0; q < LT; q++) e_base[tl][q] = min(tl * TPT + kg * LT + q, nch - 1) * stride;
+    }
+    if (threadIdx.x < kMfmaTokens) s_tok[threadIdx.x] = int(tj[threadIdx.x]);
+    lds_barrier();  // s_tok
     Piece pa[NW], pb[NW];
     // staging in one batch: every load issued, then the first weights, then the LDS writes
     // (out-of-range slots write a dummy area: no branch may skip a wait)
     if constexpr (GU) {
-      const int chunks = nb * 73 / 4, total = nch * chunks;  // 16-byte chunks of a Q8_K row (nb % 4 == 0)
+      const int chunks = int(xq_rb / 16), total = nch * chunks;  // 16-byte chunks of a (padded) Q8_K row
       u32x4 v[kStageChunks];
 #pragma unroll
       for (int q = 0; q < kStageChunks; q++) {
@@ -673,7 +791,7 @@ __global__ void __launch_bounds__(256) moe_mfma_kernel(const uint8_t* __restrict
 #pragma unroll
       for (int q = 0; q < kStageBlocks; q++) {
         const int b = min(wv + 4 * q, total - 1), j = b / nb, jb = b - j * nb;
-        v[q] = reinterpret_cast<const float4*>(act_in + int64_t(i0 + base + j) * cols + int64_t(jb) * 256)[lane];
+        v[q] = reinterpret_cast<const float4*>(act_in + int64_t(i0 + j) * cols + int64_t(jb) * 256)[lane];
       }
       load(0, pa);
 #pragma unroll
@@ -684,6 +802,9 @@ __global__ void __launch_bounds__(256) moe_mfma_kernel(const uint8_t* __restrict
       }
     }
     lds_barrier();
+    // the next item's number, fetched behind the first weights: its wait comes after the K loop
+    unsigned nxt = 0;
+    if (threadIdx.x == 0) nxt = atomicInc(ctr, 0xFFFFFFFFu);
     float acc[NW][NT][LT];
 #pragma unroll
     for (int t = 0; t < NW; t++)
@@ -695,79 +816,78 @@ __global__ void __launch_bounds__(256) moe_mfma_kernel(const uint8_t* __restrict
     // padding step: clamped loads, nothing accumulated
     auto process = [&](int s_, Piece (&p)[NW]) {
       const bool live = s_ < steps;
-      const int sc = min(s_, steps - 1), tile = sc / nb, b = sc - tile * nb;
+      const int sc_ = min(s_, steps - 1), tile = sc_ / nb, b = sc_ - tile * nb, bo = 292 * b;
+      int isum[NW][NT][LT], msum[NW][NT][LT];  // the block's integer sums (msum: Q4_K mins)
 #pragma unroll
       for (int x = 0; x < 4; x++) {
-        const int u = 4 * b + x;
-        // A: this lane's (token, segment) row over K group kg, zero outside its segment
-        int a_off;
-        if constexpr (SEG == 2) a_off = 292 * b + 4 + 64 * (u & 3) + 16 * kg;
-        else a_off = 292 * b + 4 + 128 * ((u >> 1) & 1) + 16 * (u & 1) + 32 * kg;
         v4i A[NT];
 #pragma unroll
         for (int tl = 0; tl < NT; tl++) {
-          const int t = min(tl * TPT + a_tok, nch - 1);
-          const uint32_t* ap = reinterpret_cast<const uint32_t*>(s_act + t * stride + a_off);  // 4-byte aligned
-          const v4i v = {int(ap[0]), int(ap[1]), int(ap[2]), int(ap[3])};
-          const bool on = a_seg == kg_seg;
-          A[tl] = on ? v : v4i{0, 0, 0, 0};
+          const int xo = SEG == 2 ? 64 * x : 128 * (x >> 1) + 16 * (x & 1);
+          const uint32_t* ap = reinterpret_cast<const uint32_t*>(s_act + a_base[tl] + bo + xo);  // 4-byte aligned
+          A[tl] = v4i{int(ap[0]), int(ap[1]), int(ap[2]), int(ap[3])};
         }
 #pragma unroll
         for (int t = 0; t < NW; t++) {
           // B: this lane's weight row over K group kg, as non-negative int8
           v4i B;
-          float d, dmin = 0.f;
           int sc[SEG], mn[SEG];
           if constexpr (SEG == 2) {
             const u32x4 q = p[t].q[x];
             const uint32_t qd[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-            for (int w = 0; w < 4; w++) B[w] = int(kg < 2 ? qd[w] & 0x0F0F0F0Fu : (qd[w] >> 4) & 0x0F0F0F0Fu);
+            for (int w = 0; w < 4; w++) B[w] = int((qd[w] >> nsh) & 0x0F0F0F0Fu);
 #pragma unroll
-            for (int sg = 0; sg < 2; sg++) q4k_scale_min(p[t].h, 2 * (u & 3) + sg, sc[sg], mn[sg]);
-            d = h2f(p[t].h.x);
-            dmin = h2f(p[t].h.x >> 16);
+            for (int sg = 0; sg < 2; sg++) q4k_scale_min(p[t].h, 2 * x + sg, sc[sg], mn[sg]);
           } else {
             const uint32_t xd[4] = {p[t].x[x].x, p[t].x[x].y, p[t].x[x].z, p[t].x[x].w};
             const uint32_t hd[4] = {p[t].qh[x].x, p[t].qh[x].y, p[t].qh[x].z, p[t].qh[x].w};
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
-              const uint32_t nib = kg & 2 ? (xd[w] >> 4) & 0x0F0F0F0Fu : xd[w] & 0x0F0F0F0Fu;
-              B[w] = int(nib | (((hd[w] >> (2 * kg)) & 0x03030303u) << 4));
-            }
+            for (int w = 0; w < 4; w++)
+              B[w] = int(((xd[w] >> nsh) & 0x0F0F0F0Fu) | (((hd[w] >> (2 * kg)) & 0x03030303u) << 4));
             const uint32_t scd[4] = {p[t].sc.x, p[t].sc.y, p[t].sc.z, p[t].sc.w};
 #pragma unroll
             for (int g = 0; g < 4; g++) sc[g] = int(int8_t(scd[x] >> (8 * g)));
-            d = h2f(p[t].dw >> p[t].dsh);
           }
 #pragma unroll
           for (int tl = 0; tl < NT; tl++) {
             const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tl], B, v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
             for (int q = 0; q < LT; q++) {
-              const int t_loc = tl * TPT + kg * LT + q;        // staged token of C rows 4kg + SEG q ..
-              const uint8_t* blk = s_act + min(t_loc, nch - 1) * stride + 292 * b;
-              const float dx = *reinterpret_cast<const float*>(blk);
-              const int16_t* bs = reinterpret_cast<const int16_t*>(blk + 260);
-              float term;
+              const int16_t* bs = reinterpret_cast<const int16_t*>(s_act + e_base[tl][q] + bo + 260);
               if constexpr (SEG == 2) {
-                const int i = u & 3;
-                const int bsa = int(bs[4 * i]) + int(bs[4 * i + 1]), bsb = int(bs[4 * i + 2]) + int(bs[4 * i + 3]);
-                const int isum = sc[0] * C[SEG * q] + sc[1] * C[SEG * q + 1];
-                const int msum = mn[0] * bsa + mn[1] * bsb;
-                term = dx * (d * float(isum) - dmin * float(msum));
+                const int bsa = int(bs[4 * x]) + int(bs[4 * x + 1]), bsb = int(bs[4 * x + 2]) + int(bs[4 * x + 3]);
+                // 24-bit products: |C| < 2^16 for a 32-weight sub-block, scales and mins < 64
+                const int is = __mul24(sc[0], C[SEG * q]) + __mul24(sc[1], C[SEG * q + 1]);
+                const int ms = __mul24(mn[0], bsa) + __mul24(mn[1], bsb);
+                isum[t][tl][q] = x == 0 ? is : isum[t][tl][q] + is;
+                msum[t][tl][q] = x == 0 ? ms : msum[t][tl][q] + ms;
               } else {
-                const int g0 = 8 * ((u >> 1) & 1) + (u & 1);  // bsum index of the unit's group 0
-                int isum = 0;
+                const int g0 = 8 * (x >> 1) + (x & 1);  // bsum index of the unit's group 0
+                int is = 0;
 #pragma unroll
-                for (int g = 0; g < 4; g++) isum += sc[g] * (C[g] - 32 * int(bs[g0 + 2 * g]));
-                term = dx * d * float(isum);
+                for (int g = 0; g < 4; g++) is += __mul24(sc[g], C[g] - 32 * int(bs[g0 + 2 * g]));  // |.| < 2^17
+                isum[t][tl][q] = x == 0 ? is : isum[t][tl][q] + is;
               }
-              acc[t][tl][q] += live ? term : 0.f;
             }
           }
         }
       }
+      // the block's float scales, once per (tensor, token)
+#pragma unroll
+      for (int t = 0; t < NW; t++)
+#pragma unroll
+        for (int tl = 0; tl < NT; tl++)
+#pragma unroll
+          for (int q = 0; q < LT; q++) {
+            const float dx = *reinterpret_cast<const float*>(s_act + e_base[tl][q] + bo);
+            float term;
+            if constexpr (SEG == 2)
+              term = dx * (h2f(p[t].h.x) * float(isum[t][tl][q]) - h2f(p[t].h.x >> 16) * float(msum[t][tl][q]));
+            else
+              term = dx * (h2f(p[t].dw >> p[t].dsh) * float(isum[t][tl][q]));
+            acc[t][tl][q] += live ? term : 0.f;
+          }
       if (b == nb - 1) {  // the tile's last block: its results to LDS, accumulators reset
 #pragma unroll
         for (int tl = 0; tl < NT; tl++)
@@ -797,11 +917,16 @@ __global__ void __launch_bounds__(256) moe_mfma_kernel(const uint8_t* __restrict
       process(s_ + 1, pb);
       if (s_ + 2 >= steps) break;
     }
-    lds_barrier();
-    for (int idx = threadIdx.x; idx < TILES * nch * 64; idx += 256) {
+    // the next item's number goes out before the flush's stores: its wait then waits for no store
+    if (threadIdx.x == 0) s_item = int(nxt);
+    lds_barrier();  // s_out and s_item; every thread read the item's s_tok and s_item long ago
+    item = s_item;
+    // no barrier after the flush: the next item writes s_tok and s_act before its staging
+    // barrier and s_out only after it, and nobody reads those here
+    for (int idx = threadIdx.x; idx < tiles * nch * 64; idx += 256) {
       const int tile = idx / (nch * 64), rem = idx - tile * nch * 64, t = rem / 64, w = (rem / 16) & 3, cc = rem & 15;
-      const int row = (part * 4 + w) * TILES * 16 + 16 * tile + cc;
-      if (row < R) out[int64_t(i0 + base + t) * R + row] = s_out[(tile * kMfmaTokens + t) * 64 + 16 * w + cc];
+      const int row = (part * 4 + w) * tiles * 16 + 16 * tile + cc;
+      out[int64_t(i0 + t) * R + row] = s_out[(tile * kMfmaTokens + t) * 64 + 16 * w + cc];
     }
   }
 }
@@ -819,6 +944,13 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restric
 
 // ---------------------------------------------------------------- launch plumbing
 
+// Passes over n (token, slot) pairs among E experts: at most one partial pass per active expert.
+int64_t moe_max_passes(int64_t n, int64_t E) { return (n + (kMoePassTokens - 1) * std::min(n, E)) / kMoePassTokens; }
+
+// Bytes between the tokens' Q8_K rows in the workspace: a row rounded up to 16 bytes, so that the
+// expert GEMMs stage them in 16-byte pieces.
+int64_t moe_xq_rb(int64_t hidden) { return (row_bytes(JERO_Q8_K, hidden) + 15) & ~int64_t(15); }
+
 namespace {
 
 int lpr_for(int U) { return U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4; }
@@ -831,7 +963,7 @@ void gate_up_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
   const int64_t pairs = int64_t(a.max_active) * a.ffn;
   const int ppw = 2 * int(std::min<int64_t>(8, std::max<int64_t>(1, pairs / (int64_t(P) * 8192))));  // even
   const int wg_per_expert = int((a.ffn + 4 * P * ppw - 1) / (4 * P * ppw));
-  const int64_t xrb = row_bytes(JERO_Q8_K, a.hidden);
+  const int64_t xrb = moe_xq_rb(a.hidden);
   // an expert holds at most T of the (token, slot) pairs: size the LDS stage for no more
   const int chunk = int(std::max<int64_t>(1, std::min<int64_t>({kMoeTokChunk, kMoeStageBytes / xrb, a.T})));
   hipLaunchKernelGGL((moe_gate_up_kernel<F, LPR, UPL>), dim3(unsigned(int64_t(a.max_active) * wg_per_expert)),
@@ -885,22 +1017,37 @@ int down_fmt(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
 }
 
 // Expert GEMMs on MFMA (several tokens per expert): formats with a piece loader.
-bool mfma_format(int f) { return f == JERO_Q4_K || f == JERO_Q4_K_R || f == JERO_Q6_K_R; }
+bool mfma_format(int f) { return f == JERO_Q4_K || f == JERO_Q4_K_R || f == JERO_Q4_K_T || f == JERO_Q6_K_R || f == JERO_Q6_K_T; }
+
+// Workgroups of the persistent expert-GEMM grid per CU, at most (fewer when registers or LDS
+// allow fewer): enough waves to keep each CU's share of HBM busy, few enough that each item is
+// short, as the kernel's tail is about one item long.
+constexpr int kMfmaWgPerCu = 3;
+
+// 16-row tiles per wave of an expert GEMM item (R, the weight rows per expert, a multiple of 64):
+// gate/up (K = hidden, long rows) two, down (K = ffn, short rows) four, where they divide R.
+int mfma_tiles(bool gu, int64_t R) {
+  if (R % 256 == 0 && !gu) return 4;
+  return R % 128 == 0 ? 2 : 1;
+}
 
 template <int F, bool GU>
 void mfma_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
-  constexpr int TILES = GU ? 2 : 4;  // 16-row tiles per wave: K = hidden (long) vs K = ffn (short)
   const int64_t K = GU ? a.hidden : a.ffn, R = GU ? a.ffn : a.hidden;
-  const int U = units_per_row(F, K), nb = U / 4;
-  const int wg_per_expert = int((R + 64 * TILES - 1) / (64 * TILES));
-  const size_t lds = size_t(kMfmaTokens) * size_t(act_row_stride(nb)) + 304 +  // + the dummy area
-                     sizeof(float) * TILES * kMfmaTokens * 64;                   // + the results
+  const int U = units_per_row(F, K), nb = U / 4, tiles = mfma_tiles(GU, R);
+  const int wg_per_expert = int(R / (64 * tiles));
+  const size_t lds = size_t(kMfmaTokens + 1) * size_t(act_row_stride(nb)) + 304 +  // + zero row, dummy area
+                     sizeof(float) * size_t(tiles) * kMfmaTokens * 64;               // + the results
+  int fit = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, moe_mfma_kernel<F, GU>, 256, lds) != hipSuccess || fit < 1)
+    fit = 1;
+  const int64_t items = moe_max_passes(a.T * a.top_k, a.E) * wg_per_expert;
+  const int64_t grid = std::min<int64_t>(items, int64_t(std::min(fit, kMfmaWgPerCu)) * device_info().cus);
   const uint8_t* w0 = static_cast<const uint8_t*>(GU ? a.gate : a.down);
   const uint8_t* w1 = static_cast<const uint8_t*>(GU ? a.up : a.down);
-  hipLaunchKernelGGL((moe_mfma_kernel<F, GU, TILES>),
-                     dim3(unsigned(int64_t(a.max_active) * wg_per_expert * kMfmaChunks)), dim3(256), lds, s,
-                     w0, w1, a.E * R, row_bytes(F, K), U, int(R), a.top_k, a.xq, row_bytes(JERO_Q8_K, a.hidden), a.act,
-                     L, GU ? a.act : a.yd, wg_per_expert);
+  hipLaunchKernelGGL((moe_mfma_kernel<F, GU>), dim3(unsigned(grid)), dim3(256), lds, s, w0, w1, a.E * R,
+                     row_bytes(F, K), U, int(R), tiles, a.xq, moe_xq_rb(a.hidden), a.act, L, GU ? a.act : a.yd,
+                     wg_per_expert, GU ? kMoeCtrGateUp : kMoeCtrDown);
 }
 
 template <bool GU>
@@ -908,6 +1055,8 @@ void mfma_fmt(int f, const MoeArgs& a, const MoeLists& L, hipStream_t s) {
   switch (f) {
     case JERO_Q4_K: mfma_one<JERO_Q4_K, GU>(a, L, s); break;
     case JERO_Q4_K_R: mfma_one<JERO_Q4_K_R, GU>(a, L, s); break;
+    case JERO_Q4_K_T: mfma_one<JERO_Q4_K_T, GU>(a, L, s); break;
+    case JERO_Q6_K_T: mfma_one<JERO_Q6_K_T, GU>(a, L, s); break;
     default: mfma_one<JERO_Q6_K_R, GU>(a, L, s); break;
   }
 }
@@ -918,12 +1067,13 @@ size_t moe_workspace_bytes(int64_t T, int64_t E, int top_k, int64_t hidden, int6
   const int64_t n = T * top_k;
   size_t b = 0;
   auto add = [&](size_t x) { b += (x + 255) & ~size_t(255); };
-  add(size_t(T) * size_t(row_bytes(JERO_Q8_K, hidden)));  // xq
+  add(size_t(T) * size_t(moe_xq_rb(hidden)));             // xq
   add(sizeof(int32_t) * size_t(E + 1));                    // offset
   add(sizeof(int32_t) * size_t(E));                        // active
   add(sizeof(int32_t));                                    // n_active
   add(sizeof(int32_t) * size_t(n) * 2);                    // entry, inv
-  add(sizeof(int32_t) * size_t(E) * kMoeDescInts);         // slot descriptors
+  add(sizeof(int32_t) * size_t(moe_max_passes(n, E)) * kMoePassInts);  // pass descriptors
+  add(sizeof(int32_t) * kMoeCtrInts);                                   // pass count, work counters
   add(sizeof(float) * size_t(n) * size_t(ffn));            // act
   add(sizeof(float) * size_t(n) * size_t(hidden));         // per-slot down outputs
   return b;
@@ -937,7 +1087,8 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
     p += (x + 255) & ~size_t(255);
     return r;
   };
-  a.xq = take(size_t(a.T) * size_t(row_bytes(JERO_Q8_K, a.hidden)));
+  const int64_t xq_rb = moe_xq_rb(a.hidden);
+  a.xq = take(size_t(a.T) * size_t(xq_rb));
   MoeLists L;
   L.offset = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(a.E + 1)));
   L.active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(a.E)));
@@ -945,18 +1096,20 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   int32_t* ei = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(n) * 2));
   L.entry = ei;
   L.inv = ei + n;
-  int32_t* desc = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(a.E) * kMoeDescInts));
+  int32_t* pass = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(moe_max_passes(n, a.E)) * kMoePassInts));
+  int32_t* ctr = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * kMoeCtrInts));
   a.act = reinterpret_cast<float*>(take(sizeof(float) * size_t(a.ffn) * size_t(n)));
   a.yd = reinterpret_cast<float*>(take(sizeof(float) * size_t(n) * size_t(a.hidden)));
   a.max_active = int(n < a.E ? n : a.E);
   // several tokens per expert on average: the MFMA expert GEMMs (a token's dot products come
   // out of the matrix cores instead of one cross-lane reduction per token and row); they start
-  // from the per-slot descriptors, written by the grouping step
+  // from the pass descriptors and work counters, written by the grouping step
   const bool mfma = a.T * a.top_k >= 2 * a.E && n <= kRouteLdsPairs && mfma_format(a.gate_quant) &&
-                    mfma_format(a.down_quant) && (a.hidden / 256) % 4 == 0 &&
-                    kMfmaTokens * (a.hidden / 256) * 73 / 4 <= kStageChunks * 256 &&
+                    mfma_format(a.down_quant) && a.hidden % 64 == 0 && a.ffn % 64 == 0 &&  // whole 64-row items
+                    kMfmaTokens * (xq_rb / 16) <= kStageChunks * 256 &&                      // one staging batch
                     kMfmaTokens * (a.ffn / 256) <= 4 * kStageBlocks;
-  L.desc = mfma ? desc : nullptr;
+  L.pass = mfma ? pass : nullptr;
+  L.ctr = ctr;
 
   // few tokens: one workgroup quantizes, routes and groups; many: quantize and route over many
   // workgroups, then group in one
@@ -968,10 +1121,10 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   do {                                                                                                           \
     if (single)                                                                                                  \
       hipLaunchKernelGGL(moe_route_kernel<P>, dim3(1), dim3(kRouteThreads), 0, s, a.logits, int(a.T), int(a.E),  \
-                         a.top_k, a.sel_idx, a.sel_w, L, a.x, int(a.hidden), a.xq);                             \
+                         a.top_k, a.sel_idx, a.sel_w, L, a.x, int(a.hidden), a.xq, xq_rb);                      \
     else                                                                                                         \
       hipLaunchKernelGGL(moe_prep_kernel<P>, dim3(prep_grid), dim3(256), 0, s, a.logits, int(a.T), int(a.E),     \
-                         a.top_k, a.sel_idx, a.sel_w, a.x, int(a.hidden), a.xq, n_quant_wg);                    \
+                         a.top_k, a.sel_idx, a.sel_w, a.x, int(a.hidden), a.xq, xq_rb, n_quant_wg);             \
   } while (0)
   if (per == 2) JERO_ROUTE(2);
   else if (per == 4) JERO_ROUTE(4);
@@ -996,6 +1149,8 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   switch (a.gate_quant) {
     case JERO_Q4_K: rc = gate_up_fmt<JERO_Q4_K>(a, L, s); break;
     case JERO_Q4_K_R: rc = gate_up_fmt<JERO_Q4_K_R>(a, L, s); break;
+    case JERO_Q4_K_T: rc = gate_up_fmt<JERO_Q4_K_T>(a, L, s); break;
+    case JERO_Q6_K_T: rc = gate_up_fmt<JERO_Q6_K_T>(a, L, s); break;
     case JERO_Q6_K: rc = gate_up_fmt<JERO_Q6_K>(a, L, s); break;
     default: rc = gate_up_fmt<JERO_Q6_K_R>(a, L, s); break;
   }
@@ -1005,6 +1160,8 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   switch (a.down_quant) {
     case JERO_Q4_K: rc = down_fmt<JERO_Q4_K>(a, L, s); break;
     case JERO_Q4_K_R: rc = down_fmt<JERO_Q4_K_R>(a, L, s); break;
+    case JERO_Q4_K_T: rc = down_fmt<JERO_Q4_K_T>(a, L, s); break;
+    case JERO_Q6_K_T: rc = down_fmt<JERO_Q6_K_T>(a, L, s); break;
     case JERO_Q6_K: rc = down_fmt<JERO_Q6_K>(a, L, s); break;
     default: rc = down_fmt<JERO_Q6_K_R>(a, L, s); break;
   }
@@ -1025,10 +1182,9 @@ int check_moe_args(const MoeArgs& a, size_t gate_bytes, size_t up_bytes, size_t 
   if (a.T <= 0 || a.hidden <= 0 || a.ffn <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "moe: empty input");
   if (a.top_k > a.E || a.top_k > kMaxTopK || a.E > kMaxExperts)
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "moe: top_k must be <= min(n_experts, 16), n_experts <= 1024");
-  auto kquant = [](int q) { return q == JERO_Q4_K || q == JERO_Q6_K || q == JERO_Q4_K_R || q == JERO_Q6_K_R; };
-  if (a.gate_quant != a.up_quant || !kquant(a.gate_quant) || !kquant(a.down_quant))
-    return fail(JERO_ERR_CAPABILITY_MISMATCH,
-                "moe: gate/up must share a K-quant format; down Q4_K or Q6_K (GGUF or repacked _R layouts)");
+  if (a.gate_quant != a.up_quant || !is_kquant(a.gate_quant) || !is_kquant(a.down_quant))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "moe: gate/up must share a K-quant format; down Q4_K or Q6_K (GGUF, "
+                                              "repacked _R or tiled _T layouts)");
   int64_t rg = row_bytes(a.gate_quant, a.hidden), rd = row_bytes(a.down_quant, a.ffn);
   if (rg < 0 || rd < 0) return fail(JERO_ERR_TENSOR_BOUNDS, "moe: hidden/ffn not multiples of 256");
   if (uint64_t(rg) * a.ffn * a.E > gate_bytes || uint64_t(rg) * a.ffn * a.E > up_bytes ||
@@ -1038,7 +1194,7 @@ int check_moe_args(const MoeArgs& a, size_t gate_bytes, size_t up_bytes, size_t 
     return fail(JERO_ERR_INVALID_ARGUMENT, "moe: weights 4-byte and x 16-byte aligned");
   auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   if ((is_planar(a.gate_quant) && (!a16(a.gate) || !a16(a.up))) || (is_planar(a.down_quant) && !a16(a.down)))
-    return fail(JERO_ERR_INVALID_ARGUMENT, "moe: repacked (_R) expert tensors must be 16-byte aligned");
+    return fail(JERO_ERR_INVALID_ARGUMENT, "moe: repacked (_R, _T) expert tensors must be 16-byte aligned");
   return JERO_OK;
 }
 

@@ -16,6 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.normpath(os.path.join(HERE, "..", "libjero_hip.so"))
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, ACT_Q8, Q4_K_R, Q6_K_R = 0, 1, 2, 8, 12, 14, 15, 100, 112, 114
+Q4_K_T, Q6_K_T = 113, 115  # stacked expert tensors in 16-row tiles (repack of a 3-D tensor)
 Q4_K_M = Q4_K  # the reference's QuantType::Q4_K_M names the Q4_K block format
 QUANT_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_K: "Q8_K",
                ACT_Q8: "ACT_Q8", Q4_K_R: "Q4_K_R", Q6_K_R: "Q6_K_R"}
@@ -55,6 +56,7 @@ _SIGS = {
     "jero_hip_gemm_i8": (_I32, [_P, _I64, _I64, _P, _I64, _P, _P]),
     "jero_hip_dequantize_rows": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, _P]),
     "jero_hip_repack": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, C.POINTER(C.c_int), _P]),
+    "jero_hip_repack_experts": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, C.POINTER(C.c_int), _P]),
     "jero_hip_gqa_attention": (_I32, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I64, _F, _P, _SZ, _P]),
     "jero_hip_moe_ffn": (_I32, [_P, _P, _I64, _I64, _I32, _I32, _P, _SZ, _I32, _P, _SZ, _I32, _P, _SZ, _I64, _I64,
                                 _P, _P, _P, _P, _SZ, _P]),
@@ -259,18 +261,27 @@ def vec_dot_q6_k(out, weights, inp, **kw):
     return _vec_dot(Q6_K, out, weights, inp, **kw)
 
 
-def repack(weights, stream=None):
+def repack(weights, stream=None, experts=None):
     """Load-time re-layout (repack_tensor_parallel, src/weights.rs:914-955): returns a new
-    TensorView in the device layout (Q4_K -> Q4_K_R, Q6_K -> Q6_K_R, same byte count).  A stacked
-    expert tensor [n_in, rows, n_experts] is repacked as its rows * n_experts rows."""
+    TensorView in a device layout of the same byte count.  A 2-D tensor: Q4_K -> Q4_K_R,
+    Q6_K -> Q6_K_R (the GEMV layouts).  A stacked expert tensor [n_in, rows, n_experts] with rows a
+    multiple of 16: Q4_K -> Q4_K_T, Q6_K -> Q6_K_T (16-row tiles, for dispatch_qwen3_moe_ffn);
+    experts=False repacks it as rows * n_experts rows of the 2-D layout instead."""
     import torch
     dst = torch.empty(weights.nbytes(), dtype=torch.uint8, device=weights.data.device)
     q = C.c_int(0)
     rows = 1
     for d in weights.shape[1:]:
         rows *= d
-    check(lib().jero_hip_repack(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in, rows,
-                                _ptr(dst), C.byref(q), _stream(stream)))
+    if experts is None:
+        experts = len(weights.shape) == 3 and weights.shape[1] % 16 == 0
+    if experts:
+        check(lib().jero_hip_repack_experts(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in,
+                                            weights.shape[1], weights.shape[2], _ptr(dst), C.byref(q),
+                                            _stream(stream)))
+    else:
+        check(lib().jero_hip_repack(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in, rows,
+                                    _ptr(dst), C.byref(q), _stream(stream)))
     return TensorView(weights.name, q.value, weights.shape, dst)
 
 

@@ -183,6 +183,44 @@ def test_q4_k_repacked_layout_is_bitwise_identical(dev, n_in, n_out):
         assert rel_err(yr.cpu().numpy(), ref) < REL_TOL
 
 
+def tile_q4k(w, n_rows, nb):
+    """Q4_K_T pieces from GGUF Q4_K bytes: per (16-row tile, block) q [4][2][16 rows][16] | h [16 rows][16]."""
+    t = n_rows // 16
+    blk = w.reshape(t, 16, nb, 144)
+    q = blk[..., 16:].reshape(t, 16, nb, 4, 2, 16).transpose(0, 2, 3, 4, 1, 5).reshape(t, nb, 2048)
+    h = blk[..., :16].transpose(0, 2, 1, 3).reshape(t, nb, 256)
+    return np.concatenate([q, h], axis=2).reshape(-1)
+
+
+def tile_q6k(w, n_rows, nb):
+    """Q6_K_T pieces: ql [4 units][2 halves][16 rows][16] | qh [4][16 rows][16] | sc [16 rows][4][4] | d [16 rows]."""
+    t = n_rows // 16
+    blk = w.reshape(t, 16, nb, 210)
+    ql = blk[..., :128].reshape(t, 16, nb, 2, 2, 2, 16).transpose(0, 2, 3, 5, 4, 1, 6).reshape(t, nb, 2048)
+    qh = blk[..., 128:192].reshape(t, 16, nb, 2, 2, 16).transpose(0, 2, 3, 4, 1, 5).reshape(t, nb, 1024)
+    sc = blk[..., 192:208].reshape(t, 16, nb, 2, 4, 2).transpose(0, 2, 1, 3, 5, 4).reshape(t, nb, 256)
+    d = blk[..., 208:].transpose(0, 2, 1, 3).reshape(t, nb, 32)
+    return np.concatenate([ql, qh, sc, d], axis=2).reshape(-1)
+
+
+@pytest.mark.parametrize("quant", [J.Q4_K, J.Q6_K])
+def test_repack_experts_tiled_layout(dev, quant):
+    """jero_hip_repack_experts writes the 16-row tiled pieces, byte for byte."""
+    print(f"repack experts quant={quant}", flush=True)
+    n_in, rows, experts = 768, 48, 3
+    w = rand_weights(quant, rows * experts, n_in, 900 + quant, full_range=True)
+    W = J.TensorView("blk.0.ffn_gate_exps.weight", quant, [n_in, rows, experts], to_dev(w, dev))
+    Wt = J.repack(W)
+    torch.cuda.synchronize()
+    assert Wt.quant == (J.Q4_K_T if quant == J.Q4_K else J.Q6_K_T) and Wt.nbytes() == W.nbytes()
+    tile = tile_q4k if quant == J.Q4_K else tile_q6k
+    np.testing.assert_array_equal(Wt.data.cpu().numpy(), tile(np.frombuffer(w.tobytes(), np.uint8), rows * experts,
+                                                              n_in // 256))
+    with pytest.raises(J.K3Error) as ei:  # rows per expert not a multiple of 16
+        J.repack(J.TensorView("e", quant, [n_in, 24, 2], W.data), experts=True)
+    assert ei.value.variant == "CapabilityMismatch"
+
+
 def test_repack_rejects_other_formats(dev):
     W = J.TensorView("w", J.Q8_0, [256, 4], torch.zeros(4 * 8 * 34, dtype=torch.uint8, device=dev))
     with pytest.raises(J.K3Error) as ei:

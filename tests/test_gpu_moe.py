@@ -34,12 +34,16 @@ def run_case(dev, T, E, H, F, K, gq, dq, seed, logits=None, repacked=False):
     y = torch.empty((T, H), dtype=torch.float32, device=dev)
     si, sw = J.dispatch_qwen3_moe_ffn(y, td(x), td(logits), K, G, U, D)
     torch.cuda.synchronize()
-    if repacked:  # the load-time layouts (Q4_K_R / Q6_K_R over all experts' rows)
-        yr = torch.empty_like(y)
-        sir, swr = J.dispatch_qwen3_moe_ffn(yr, td(x), td(logits), K, J.repack(G), J.repack(U), J.repack(D))
-        torch.cuda.synchronize()
-        assert torch.equal(sir, si) and torch.equal(swr, sw)
-        check_out(yr, y_ref)
+    if repacked:  # the load-time layouts: 16-row tiles (_T), and the GEMV planes over all rows (_R)
+        for experts, gl, dl in ((True, (J.Q4_K_T, J.Q6_K_T), (J.Q4_K_T, J.Q6_K_T)),
+                                (False, (J.Q4_K_R, J.Q6_K_R), (J.Q4_K_R, J.Q6_K_R))):
+            Gr, Ur, Dr = (J.repack(t, experts=experts) for t in (G, U, D))
+            assert Gr.quant == gl[gq == J.Q6_K] and Dr.quant == dl[dq == J.Q6_K]
+            yr = torch.empty_like(y)
+            sir, swr = J.dispatch_qwen3_moe_ffn(yr, td(x), td(logits), K, Gr, Ur, Dr)
+            torch.cuda.synchronize()
+            assert torch.equal(sir, si) and torch.equal(swr, sw)
+            check_out(yr, y_ref)
     np.testing.assert_array_equal(si.cpu().numpy(), si_ref)
     np.testing.assert_allclose(sw.cpu().numpy(), sw_ref, rtol=1e-6, atol=1e-7)
     check_out(y, y_ref)

@@ -22,6 +22,7 @@
 #include "moe.h"
 
 #include <algorithm>
+#include <type_traits>
 
 #include "gemv_dot.h"
 #include "quantize.h"
@@ -768,157 +769,190 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU)) moe_mfma_kernel(cons
     }
     if (threadIdx.x < kMfmaTokens) s_tok[threadIdx.x] = int(tj[threadIdx.x]);
     lds_barrier();  // s_tok
-    Piece pa[NW], pb[NW];
-    // staging in one batch: every load issued, then the first weights, then the LDS writes
-    // (out-of-range slots write a dummy area: no branch may skip a wait)
-    if constexpr (GU) {
-      const int chunks = int(xq_rb / 16), total = nch * chunks;  // 16-byte chunks of a (padded) Q8_K row
-      u32x4 v[kStageChunks];
+    // Q6_K: the block's sum over its 16 groups of scale x bsum, per (token, row), comes from one f16
+    // MFMA (exact: |sum| < 2^23): K slot 4 kg' + t is group 8n + j + 2t of unit kg' = 2n + j (the
+    // unit's scale byte t), and A row 4 kg + i holds token 4 i + kg, so that C[tl] of lane (c, kg)
+    // is token 4 tl + kg, as in the int8 MFMA.  The lane's A row: its token's bsums of groups 8n + j
+    // + 2t, t = 0..3, the halves j of four dwords.
+    const int fb_base = min((vr & 3) * 4 + (vr >> 2), nch - 1) * stride + 260 + 16 * (kg >> 1);
+    const uint32_t fb_sh = 16u * uint32_t(kg & 1);
+    const uint32_t qh_rot = uint32_t(2 * kg - 4) & 31u;  // rotates the lane's 2 high bits to bits 4..5
+    // the K loop over NTA token tiles (NTA = NT; one instance: a second one for passes of at most
+    // TPT tokens, whose buffers and staging would have to be its own, spilled registers)
+    auto kloop = [&](auto nta) {
+      constexpr int NTA = decltype(nta)::value;
+      Piece pa[NW], pb[NW];
+      // staging in one batch: every load issued, then the first weights, then the LDS writes
+      // (out-of-range slots write a dummy area: no branch may skip a wait)
+      if constexpr (GU) {
+        const int chunks = int(xq_rb / 16), total = nch * chunks;  // 16-byte chunks of a (padded) Q8_K row
+        u32x4 v[kStageChunks];
 #pragma unroll
-      for (int q = 0; q < kStageChunks; q++) {
-        const int idx = min(int(threadIdx.x) + 256 * q, total - 1), j = idx / chunks;
-        v[q] = ld4(xq + int64_t(s_tok[j]) * xq_rb + (idx - j * chunks) * 16);
-      }
-      load(0, pa);
-#pragma unroll
-      for (int q = 0; q < kStageChunks; q++) {
-        const int idx = int(threadIdx.x) + 256 * q, j = idx / chunks;
-        *reinterpret_cast<u32x4*>(s_act + (idx < total ? j * stride + (idx - j * chunks) * 16 : dummy)) = v[q];
-      }
-    } else {
-      const int cols = U * 64, total = nch * nb;
-      float4 v[kStageBlocks];
-#pragma unroll
-      for (int q = 0; q < kStageBlocks; q++) {
-        const int b = min(wv + 4 * q, total - 1), j = b / nb, jb = b - j * nb;
-        v[q] = reinterpret_cast<const float4*>(act_in + int64_t(i0 + j) * cols + int64_t(jb) * 256)[lane];
-      }
-      load(0, pa);
-#pragma unroll
-      for (int q = 0; q < kStageBlocks; q++) {
-        const int b = wv + 4 * q, j = b / nb, jb = b - j * nb;
-        const float ev[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
-        q8k_block_wave(ev, lane, s_act + (b < total ? j * stride + 292 * jb : dummy));
-      }
-    }
-    lds_barrier();
-    // the next item's number, fetched behind the first weights: its wait comes after the K loop
-    unsigned nxt = 0;
-    if (threadIdx.x == 0) nxt = atomicInc(ctr, 0xFFFFFFFFu);
-    float acc[NW][NT][LT];
-#pragma unroll
-    for (int t = 0; t < NW; t++)
-#pragma unroll
-      for (int tl = 0; tl < NT; tl++)
-#pragma unroll
-        for (int q = 0; q < LT; q++) acc[t][tl][q] = 0.f;
-    // one step: block b (units 4b .. 4b + 3) of one tile; a step past the last (steps odd) is a
-    // padding step: clamped loads, nothing accumulated
-    auto process = [&](int s_, Piece (&p)[NW]) {
-      const bool live = s_ < steps;
-      const int sc_ = min(s_, steps - 1), tile = sc_ / nb, b = sc_ - tile * nb, bo = 292 * b;
-      int isum[NW][NT][LT], msum[NW][NT][LT];  // the block's integer sums (msum: Q4_K mins)
-#pragma unroll
-      for (int x = 0; x < 4; x++) {
-        v4i A[NT];
-#pragma unroll
-        for (int tl = 0; tl < NT; tl++) {
-          const int xo = SEG == 2 ? 64 * x : 128 * (x >> 1) + 16 * (x & 1);
-          const uint32_t* ap = reinterpret_cast<const uint32_t*>(s_act + a_base[tl] + bo + xo);  // 4-byte aligned
-          A[tl] = v4i{int(ap[0]), int(ap[1]), int(ap[2]), int(ap[3])};
+        for (int q = 0; q < kStageChunks; q++) {
+          const int idx = min(int(threadIdx.x) + 256 * q, total - 1), j = idx / chunks;
+          v[q] = ld4(xq + int64_t(s_tok[j]) * xq_rb + (idx - j * chunks) * 16);
         }
+        load(0, pa);
 #pragma unroll
-        for (int t = 0; t < NW; t++) {
-          // B: this lane's weight row over K group kg, as non-negative int8
-          v4i B;
-          int sc[SEG], mn[SEG];
-          if constexpr (SEG == 2) {
-            const u32x4 q = p[t].q[x];
-            const uint32_t qd[4] = {q.x, q.y, q.z, q.w};
+        for (int q = 0; q < kStageChunks; q++) {
+          const int idx = int(threadIdx.x) + 256 * q, j = idx / chunks;
+          *reinterpret_cast<u32x4*>(s_act + (idx < total ? j * stride + (idx - j * chunks) * 16 : dummy)) = v[q];
+        }
+      } else {
+        const int cols = U * 64, total = nch * nb;
+        float4 v[kStageBlocks];
 #pragma unroll
-            for (int w = 0; w < 4; w++) B[w] = int((qd[w] >> nsh) & 0x0F0F0F0Fu);
+        for (int q = 0; q < kStageBlocks; q++) {
+          const int b = min(wv + 4 * q, total - 1), j = b / nb, jb = b - j * nb;
+          v[q] = reinterpret_cast<const float4*>(act_in + int64_t(i0 + j) * cols + int64_t(jb) * 256)[lane];
+        }
+        load(0, pa);
 #pragma unroll
-            for (int sg = 0; sg < 2; sg++) q4k_scale_min(p[t].h, 2 * x + sg, sc[sg], mn[sg]);
-          } else {
-            const uint32_t xd[4] = {p[t].x[x].x, p[t].x[x].y, p[t].x[x].z, p[t].x[x].w};
-            const uint32_t hd[4] = {p[t].qh[x].x, p[t].qh[x].y, p[t].qh[x].z, p[t].qh[x].w};
-#pragma unroll
-            for (int w = 0; w < 4; w++)
-              B[w] = int(((xd[w] >> nsh) & 0x0F0F0F0Fu) | (((hd[w] >> (2 * kg)) & 0x03030303u) << 4));
-            const uint32_t scd[4] = {p[t].sc.x, p[t].sc.y, p[t].sc.z, p[t].sc.w};
-#pragma unroll
-            for (int g = 0; g < 4; g++) sc[g] = int(int8_t(scd[x] >> (8 * g)));
-          }
-#pragma unroll
-          for (int tl = 0; tl < NT; tl++) {
-            const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tl], B, v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-            for (int q = 0; q < LT; q++) {
-              const int16_t* bs = reinterpret_cast<const int16_t*>(s_act + e_base[tl][q] + bo + 260);
-              if constexpr (SEG == 2) {
-                const int bsa = int(bs[4 * x]) + int(bs[4 * x + 1]), bsb = int(bs[4 * x + 2]) + int(bs[4 * x + 3]);
-                // 24-bit products: |C| < 2^16 for a 32-weight sub-block, scales and mins < 64
-                const int is = __mul24(sc[0], C[SEG * q]) + __mul24(sc[1], C[SEG * q + 1]);
-                const int ms = __mul24(mn[0], bsa) + __mul24(mn[1], bsb);
-                isum[t][tl][q] = x == 0 ? is : isum[t][tl][q] + is;
-                msum[t][tl][q] = x == 0 ? ms : msum[t][tl][q] + ms;
-              } else {
-                const int g0 = 8 * (x >> 1) + (x & 1);  // bsum index of the unit's group 0
-                int is = 0;
-#pragma unroll
-                for (int g = 0; g < 4; g++) is += __mul24(sc[g], C[g] - 32 * int(bs[g0 + 2 * g]));  // |.| < 2^17
-                isum[t][tl][q] = x == 0 ? is : isum[t][tl][q] + is;
-              }
-            }
-          }
+        for (int q = 0; q < kStageBlocks; q++) {
+          const int b = wv + 4 * q, j = b / nb, jb = b - j * nb;
+          const float ev[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+          q8k_block_wave(ev, lane, s_act + (b < total ? j * stride + 292 * jb : dummy));
         }
       }
-      // the block's float scales, once per (tensor, token)
+      lds_barrier();
+      // the next item's number, fetched behind the first weights: its wait comes after the K loop
+      unsigned nxt = 0;
+      if (threadIdx.x == 0) nxt = atomicInc(ctr, 0xFFFFFFFFu);
+      float acc[NW][NT][LT];
 #pragma unroll
       for (int t = 0; t < NW; t++)
 #pragma unroll
         for (int tl = 0; tl < NT; tl++)
 #pragma unroll
-          for (int q = 0; q < LT; q++) {
-            const float dx = *reinterpret_cast<const float*>(s_act + e_base[tl][q] + bo);
-            float term;
-            if constexpr (SEG == 2)
-              term = dx * (h2f(p[t].h.x) * float(isum[t][tl][q]) - h2f(p[t].h.x >> 16) * float(msum[t][tl][q]));
-            else
-              term = dx * (h2f(p[t].dw >> p[t].dsh) * float(isum[t][tl][q]));
-            acc[t][tl][q] += live ? term : 0.f;
+          for (int q = 0; q < LT; q++) acc[t][tl][q] = 0.f;
+      // one step: block b (units 4b .. 4b + 3) of one tile; a step past the last (steps odd) is a
+      // padding step: clamped loads, nothing accumulated
+      auto process = [&](int s_, Piece (&p)[NW]) {
+        const bool live = s_ < steps;
+        const int sc_ = min(s_, steps - 1), tile = sc_ / nb, b = sc_ - tile * nb, bo = 292 * b;
+        int isum[NW][NT][LT], msum[NW][NT][LT];  // the block's integer sums (msum: Q4_K mins)
+#pragma unroll
+        for (int x = 0; x < 4; x++) {
+          v4i A[NTA];
+#pragma unroll
+          for (int tl = 0; tl < NTA; tl++) {
+            const int xo = SEG == 2 ? 64 * x : 128 * (x >> 1) + 16 * (x & 1);
+            const uint32_t* ap = reinterpret_cast<const uint32_t*>(s_act + a_base[tl] + bo + xo);  // 4-byte aligned
+            A[tl] = v4i{int(ap[0]), int(ap[1]), int(ap[2]), int(ap[3])};
           }
-      if (b == nb - 1) {  // the tile's last block: its results to LDS, accumulators reset
 #pragma unroll
-        for (int tl = 0; tl < NT; tl++)
+          for (int t = 0; t < NW; t++) {
+            // B: this lane's weight row over K group kg, as non-negative int8
+            v4i B;
+            int sc[SEG], mn[SEG];
+            if constexpr (SEG == 2) {
+              const u32x4 q = p[t].q[x];
+              const uint32_t qd[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-          for (int q = 0; q < LT; q++) {
-            float v;
-            if constexpr (GU) {
-              const float g = acc[0][tl][q];
-              v = g / (1.0f + expf(-g)) * acc[1][tl][q];
+              for (int w = 0; w < 4; w++) B[w] = int((qd[w] >> nsh) & 0x0F0F0F0Fu);
+#pragma unroll
+              for (int sg = 0; sg < 2; sg++) q4k_scale_min(p[t].h, 2 * x + sg, sc[sg], mn[sg]);
             } else {
-              v = acc[0][tl][q];
-            }
-            const int t_loc = tl * TPT + kg * LT + q;  // < kMfmaTokens
-            if (live) s_out[(tile * kMfmaTokens + t_loc) * 64 + 16 * wv + c] = v;
+              const uint32_t xd[4] = {p[t].x[x].x, p[t].x[x].y, p[t].x[x].z, p[t].x[x].w};
+              const uint32_t hd[4] = {p[t].qh[x].x, p[t].qh[x].y, p[t].qh[x].z, p[t].qh[x].w};
 #pragma unroll
-            for (int t = 0; t < NW; t++) acc[t][tl][q] = 0.f;
+              for (int w = 0; w < 4; w++)
+                B[w] = int(((xd[w] >> nsh) & 0x0F0F0F0Fu) |
+                           (__builtin_amdgcn_alignbit(hd[w], hd[w], qh_rot) & 0x30303030u));
+              const uint32_t scd[4] = {p[t].sc.x, p[t].sc.y, p[t].sc.z, p[t].sc.w};
+#pragma unroll
+              for (int g = 0; g < 4; g++) sc[g] = int(int8_t(scd[x] >> (8 * g)));
+            }
+#pragma unroll
+            for (int tl = 0; tl < NTA; tl++) {
+              const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tl], B, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+              for (int q = 0; q < LT; q++) {
+                if constexpr (SEG == 2) {
+                  const int16_t* bs = reinterpret_cast<const int16_t*>(s_act + e_base[tl][q] + bo + 260);
+                  const int bsa = int(bs[4 * x]) + int(bs[4 * x + 1]), bsb = int(bs[4 * x + 2]) + int(bs[4 * x + 3]);
+                  // 24-bit products: |C| < 2^16 for a 32-weight sub-block, scales and mins < 64
+                  const int is = __mul24(sc[0], C[SEG * q]) + __mul24(sc[1], C[SEG * q + 1]);
+                  const int ms = __mul24(mn[0], bsa) + __mul24(mn[1], bsb);
+                  isum[t][tl][q] = x == 0 ? is : isum[t][tl][q] + is;
+                  msum[t][tl][q] = x == 0 ? ms : msum[t][tl][q] + ms;
+                } else {
+                  int is = 0;  // the q6 offset of 32 is taken off once per block, below
+#pragma unroll
+                  for (int g = 0; g < 4; g++) is += __mul24(sc[g], C[g]);  // |C| < 2^17
+                  isum[t][tl][q] = x == 0 ? is : isum[t][tl][q] + is;
+                }
+              }
+            }
           }
+        }
+        if constexpr (SEG == 4) {
+          typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+          typedef float f4 __attribute__((ext_vector_type(4)));
+          const uint32_t* bp = reinterpret_cast<const uint32_t*>(s_act + fb_base + bo);
+          h4 Ab;
+#pragma unroll
+          for (int t4 = 0; t4 < 4; t4++) Ab[t4] = _Float16(int(int16_t(bp[t4] >> fb_sh)));
+#pragma unroll
+          for (int t = 0; t < NW; t++) {
+            pin(p[t].sc);  // in registers already: else the lane's pick becomes a load of its own
+            const uint32_t sdw = kg == 0 ? p[t].sc.x : kg == 1 ? p[t].sc.y : kg == 2 ? p[t].sc.z : p[t].sc.w;
+            h4 Bb;
+#pragma unroll
+            for (int t4 = 0; t4 < 4; t4++) Bb[t4] = _Float16(int(int8_t(sdw >> (8 * t4))));
+            const f4 Cb = __builtin_amdgcn_mfma_f32_16x16x16f16(Ab, Bb, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int tl = 0; tl < NTA; tl++) isum[t][tl][0] -= 32 * int(Cb[tl]);
+          }
+        }
+        // the block's float scales, once per (tensor, token)
+#pragma unroll
+        for (int t = 0; t < NW; t++)
+#pragma unroll
+          for (int tl = 0; tl < NTA; tl++)
+#pragma unroll
+            for (int q = 0; q < LT; q++) {
+              const float dx = *reinterpret_cast<const float*>(s_act + e_base[tl][q] + bo);
+              float term;
+              if constexpr (SEG == 2)
+                term = dx * (h2f(p[t].h.x) * float(isum[t][tl][q]) - h2f(p[t].h.x >> 16) * float(msum[t][tl][q]));
+              else
+                term = dx * (h2f(p[t].dw >> p[t].dsh) * float(isum[t][tl][q]));
+              acc[t][tl][q] += live ? term : 0.f;
+            }
+        if (b == nb - 1) {  // the tile's last block: its results to LDS, accumulators reset
+#pragma unroll
+          for (int tl = 0; tl < NTA; tl++)
+#pragma unroll
+            for (int q = 0; q < LT; q++) {
+              float v;
+              if constexpr (GU) {
+                const float g = acc[0][tl][q];
+                v = g / (1.0f + expf(-g)) * acc[1][tl][q];
+              } else {
+                v = acc[0][tl][q];
+              }
+              const int t_loc = tl * TPT + kg * LT + q;  // < kMfmaTokens
+              if (live) s_out[(tile * kMfmaTokens + t_loc) * 64 + 16 * wv + c] = v;
+#pragma unroll
+              for (int t = 0; t < NW; t++) acc[t][tl][q] = 0.f;
+            }
+        }
+      };
+      // an even number of steps (a padding step when odd): the loop's only exit is at the bottom
+      for (int s_ = 0;; s_ += 2) {
+        load(s_ + 1, pb);
+        __builtin_amdgcn_sched_barrier(0);
+        process(s_, pa);
+        load(s_ + 2, pa);  // the last one is redundant (clamped)
+        __builtin_amdgcn_sched_barrier(0);
+        process(s_ + 1, pb);
+        if (s_ + 2 >= steps) break;
       }
+      // the next item's number goes out before the flush's stores: its wait then waits for no store
+      if (threadIdx.x == 0) s_item = int(nxt);
     };
-    // an even number of steps (a padding step when odd): the loop's only exit is at the bottom
-    for (int s_ = 0;; s_ += 2) {
-      load(s_ + 1, pb);
-      __builtin_amdgcn_sched_barrier(0);
-      process(s_, pa);
-      load(s_ + 2, pa);  // the last one is redundant (clamped)
-      __builtin_amdgcn_sched_barrier(0);
-      process(s_ + 1, pb);
-      if (s_ + 2 >= steps) break;
-    }
-    // the next item's number goes out before the flush's stores: its wait then waits for no store
-    if (threadIdx.x == 0) s_item = int(nxt);
+    kloop(std::integral_constant<int, NT>{});
     lds_barrier();  // s_out and s_item; every thread read the item's s_tok and s_item long ago
     item = s_item;
     // no barrier after the flush: the next item writes s_tok and s_act before its staging

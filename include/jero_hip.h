@@ -164,8 +164,9 @@ int jero_hip_gqa_attention(float *out_dev, const float *q_dev, const void *k_dev
  * x_dev [n_tokens][hidden] f32 (16-byte aligned); router_logits_dev [n_tokens][n_experts] f32;
  * gate/up: stacked [n_experts][ffn rows][hidden] in one K-quant; down: [n_experts][hidden rows][ffn]
  * in Q4_K or Q6_K (GGUF stacked [hidden, ffn, n_experts] tensors, expert e = rows e*ffn..), or the
- * same tensors after jero_hip_repack over all their rows (JERO_Q4_K_R / JERO_Q6_K_R, 16-byte
- * aligned; the layouts the expert GEMMs read fastest).
+ * same tensors after jero_hip_repack_experts (JERO_Q4_K_T / JERO_Q6_K_T, the layouts the expert
+ * GEMMs read fastest) or jero_hip_repack over all their rows (JERO_Q4_K_R / JERO_Q6_K_R); repacked
+ * tensors 16-byte aligned.
  * Outputs y_dev [n_tokens][hidden], sel_idx_dev / sel_w_dev [n_tokens][top_k].
  * hidden <= 2048 for the gate/up pairing; top_k <= 16; n_experts <= 1024.  Workspace:
  * jero_hip_moe_workspace_bytes(...) bytes, 256-byte aligned (NULL: library-owned). */

@@ -94,6 +94,31 @@ def time_graph(torch, fn, steps, warmup, stream):
     return s.elapsed_time(e) / 1e3 / steps
 
 
+def time_graph_dist(torch, fn, chunk, reps, stream):
+    """Per-step time distribution: one graph of `chunk` steps (chunk covers every rotated weight
+    copy, so no replay re-reads what the previous one left in the Infinity Cache), replayed `reps`
+    times with events around each replay; returns the p10 / p50 / p90 of the per-step mean (us)."""
+    import numpy as np
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fn()
+        stream.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(chunk):
+                fn()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    with torch.cuda.stream(stream):
+        g.replay()  # warm replay
+        ev[0].record(stream)
+        for r in range(reps):
+            g.replay()
+            ev[r + 1].record(stream)
+    ev[-1].synchronize()
+    t = np.array([ev[r].elapsed_time(ev[r + 1]) * 1e3 / chunk for r in range(reps)])
+    return {"p10_us": round(float(np.percentile(t, 10)), 3), "p50_us": round(float(np.median(t)), 3),
+            "p90_us": round(float(np.percentile(t, 90)), 3), "replays": reps, "steps_per_replay": chunk}
+
+
 def q6k_layers(n):
     """llama.cpp's Q4_K_M rule: Q6_K attn_v / ffn_down on these layers."""
     return [i for i in range(n) if i < n // 8 or i >= 7 * n // 8 or (i - n // 8) % 3 == 2]
@@ -391,6 +416,8 @@ def main():
     t_step = time_graph(torch, step, args.steps, args.warmup, stream)
     step_bytes = sum(algo)
     value = step_bytes / t_step / 1e9
+    max_copies = max(len(v) for v in views)
+    step_dist = time_graph_dist(torch, step, max_copies, 21, stream)
 
     # per-shape kernel averages (same method, one shape per graph), planar and GGUF layouts
     per_shape, per_shape_gguf = {}, {}
@@ -405,7 +432,8 @@ def main():
 
             t = time_graph(torch, one, args.steps, args.warmup, stream)
             table[f"{n_in}x{n_out}"] = {"us": round(t * 1e6, 3), "GB_s": round(algo[i] / t / 1e9, 1),
-                                        "bytes": algo[i]}
+                                        "bytes": algo[i],
+                                        "dist": time_graph_dist(torch, one, len(vlist[i]), 21, stream)}
     gemv_launch_us = t_step * 1e6 / len(SHAPES)
     achieved = (step_bytes / len(SHAPES)) / (gemv_launch_us * 1e-6) / 1e9
 
@@ -480,6 +508,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(t_step * 1e3, 5),
+        "step_dist": step_dist,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

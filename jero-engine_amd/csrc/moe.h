@@ -26,6 +26,15 @@ constexpr int kMoePassInts = 4 + kMoePassTokens;
 constexpr int kMoeCtrInts = 96;
 constexpr int kMoeCtrGateUp = 32, kMoeCtrDown = 64;  // counter offsets in ctr
 
+// The single-token path's extra inputs (the gate/up kernel routes and quantizes the token itself).
+struct MoeSingle {
+  const float* logits;  // [E]
+  const float* x;       // [H]
+  int E, H;
+  int32_t* sel_idx;     // [k]
+  float* sel_w;         // [k]
+};
+
 struct MoeArgs {
   const float* x;       // [T][hidden]
   const float* logits;  // [T][E]

@@ -381,13 +381,13 @@ __device__ __forceinline__ void stage_quant_rows(uint8_t* __restrict__ dst, cons
 // load), every path through the token loop uses the weights (the loop runs at least once, and
 // units past the row end are dotted clamped and then dropped by a select, never skipped by a
 // branch), and barriers wait on LDS only.
-template <int F, int LPR, int UPL>
+template <int F, int LPR, int UPL, int SPER>
 __global__ void __launch_bounds__(256) moe_gate_up_kernel(const uint8_t* __restrict__ gate,
                                                           const uint8_t* __restrict__ up, int64_t n_rows, int64_t rb,
                                                           int U, int Fdim,
                                                           int k, const uint8_t* __restrict__ xq, int64_t xq_rb,
                                                           MoeLists lists, float* __restrict__ act, int ppw,
-                                                          int wg_per_expert, int chunk) {
+                                                          int wg_per_expert, int chunk, MoeSingle one) {
   using Ut = Unit<F>;
   using W = typename Ut::W;
   constexpr int G = kWave / LPR;
@@ -395,13 +395,35 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(const uint8_t* __restr
   static_assert(P >= 1, "gate/up pairing needs two lane groups per wave");
   extern __shared__ uint32_t s_x[];
   __shared__ int s_rows[kMoeTokChunk];
+  __shared__ int s_sel[kMaxTopK];
   const int slot = int(blockIdx.x) / wg_per_expert, part = int(blockIdx.x) % wg_per_expert;
-  if (slot >= *lists.n_active) return;  // uniform over the workgroup
-  const int e = lists.active[slot];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int e, i0, cnt;
+  if constexpr (SPER > 0) {
+    // one token (SPER expert columns per lane): every workgroup routes it (wave 0; the selections
+    // are written out too, by all workgroups alike) and quantizes it to a Q8_K row in LDS (the
+    // other waves); slot j is the token's j-th selection, its act row j
+    if (wv == 0) {
+      route_token<SPER>(one.logits, 0, one.E, k, one.sel_idx, one.sel_w, s_sel);
+    } else {
+      for (int blk = wv - 1; blk < one.H / 256; blk += 3) {
+        const float4 v = reinterpret_cast<const float4*>(one.x + int64_t(blk) * 256)[lane];
+        const float ev[4] = {v.x, v.y, v.z, v.w};
+        q8k_block_wave(ev, lane, reinterpret_cast<uint8_t*>(s_x) + blk * 292);
+      }
+    }
+    __syncthreads();
+    e = s_sel[slot];
+    i0 = slot;
+    cnt = 1;
+  } else {
+    if (slot >= *lists.n_active) return;  // uniform over the workgroup
+    e = lists.active[slot];
+    i0 = lists.offset[e];
+    cnt = lists.offset[e + 1] - i0;
+  }
   const int g = lane / LPR, c = lane % LPR;
   const bool is_up = g & 1;
-  const int i0 = lists.offset[e], cnt = lists.offset[e + 1] - i0;
   const int rows_wg = 4 * ppw * P, fbase = part * rows_wg;  // the workgroup's row pairs
   const int r0 = wv * ppw * P + g / 2;                       // this lane group's first, in them
   const int f0 = fbase + r0;
@@ -442,10 +464,12 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(const uint8_t* __restr
   for (int base = 0; base < cnt; base += chunk) {
     const int nch = min(chunk, cnt - base);
     load_pair(0, wa);  // in flight while the activations are staged
-    lds_barrier();     // the previous pass's readers are done
-    if (int(threadIdx.x) < nch) s_rows[threadIdx.x] = lists.entry[i0 + base + threadIdx.x] / k;
-    lds_barrier();
-    stage_rows(s_x, xq, xq_rb, nch, s_rows);
+    if constexpr (SPER == 0) {  // (one token: its row is in LDS already)
+      lds_barrier();            // the previous pass's readers are done
+      if (int(threadIdx.x) < nch) s_rows[threadIdx.x] = lists.entry[i0 + base + threadIdx.x] / k;
+      lds_barrier();
+      stage_rows(s_x, xq, xq_rb, nch, s_rows);
+    }
     // ppw is even: the loop's only exit is at the bottom, so no path leaves wb in flight
     for (int it = 0;; it += 2) {
       load_pair(it + 1, wb);
@@ -534,6 +558,86 @@ __global__ void __launch_bounds__(256) moe_down_kernel(const uint8_t* __restrict
       const int j = idx / rows_wg, r = idx - j * rows_wg;
       if (hbase + r < H) yd[int64_t(i0 + base + j) * H + hbase + r] = s_out[idx];
     }
+  }
+}
+
+// One token, down and combine in one: a workgroup takes RW rows h of the output, and for each its
+// k selected experts' down rows (units (slot j, row r), lane group per unit); the token's act rows
+// (act row j = selection j) are quantized to Q8_K in LDS.  The dots land in LDS and the workgroup
+// then writes y[h] = sum over j ascending of w_j * dot_j, the reference's combine order.
+template <int F, int LPR, int UPL>
+__global__ void __launch_bounds__(256) moe1_down_kernel(const uint8_t* __restrict__ down, int64_t n_rows, int64_t rb,
+                                                        int U, int H, const float* __restrict__ act, int ffn,
+                                                        int64_t aq_rb, int k, const int32_t* __restrict__ sel_idx,
+                                                        const float* __restrict__ sel_w, float* __restrict__ y, int RW,
+                                                        int upg) {
+  using Ut = Unit<F>;
+  using W = typename Ut::W;
+  constexpr int G = kWave / LPR;
+  extern __shared__ uint32_t s_x[];  // k Q8_K act rows, then dots [k][RW]
+  __shared__ int s_sel[kMaxTopK];
+  __shared__ float s_w[kMaxTopK];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int g = lane / LPR, c = lane % LPR;
+  const int lg = wv * G + g, n_lg = 4 * G;  // lane group and their number
+  const int hbase = int(blockIdx.x) * RW, n_units = RW * k;
+  float* s_dot = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(s_x) + int64_t(k) * aq_rb);
+  if (threadIdx.x < kMaxTopK) {
+    const int j = min(int(threadIdx.x), k - 1);
+    s_sel[threadIdx.x] = sel_idx[j];
+    s_w[threadIdx.x] = sel_w[j];
+  }
+  __syncthreads();
+  // unit i of this lane group: q = lg + n_lg * i -> (slot j, row r), clamped past the end
+  auto unit = [&](int i, int& j, int& r) {
+    const int q = min(lg + n_lg * i, n_units - 1);
+    j = q / RW;
+    r = q - j * RW;
+  };
+  auto load_unit_w = [&](int i, W (&wt)[UPL]) {
+    int j, r;
+    unit(i, j, r);
+    const int h = min(hbase + r, H - 1);
+#pragma unroll
+    for (int t = 0; t < UPL; t++)
+      load_unit<F>(wt[t], down, n_rows, U, rb, int64_t(s_sel[j]) * H + h, min(c + LPR * t, U - 1));
+  };
+  auto process = [&](int i, W (&wt)[UPL]) {
+    int j, r;
+    unit(i, j, r);
+    typename Ut::Prep pr[UPL];
+#pragma unroll
+    for (int t = 0; t < UPL; t++) Ut::prep(pr[t], wt[t], min(c + LPR * t, U - 1));
+    const uint8_t* at = reinterpret_cast<const uint8_t*>(s_x) + int64_t(j) * aq_rb;
+    float accv = 0.f;
+#pragma unroll
+    for (int t = 0; t < UPL; t++) {
+      const int u = c + LPR * t;
+      typename Ut::Act a;
+      Ut::load_act(a, at, min(u, U - 1));
+      const float d = Ut::dot_prep(pr[t], a);
+      accv += u < U ? d : 0.f;
+    }
+    accv = group_sum_last<LPR>(accv);
+    if (c == LPR - 1 && lg + n_lg * i < n_units) s_dot[j * RW + r] = accv;
+  };
+  W wa[UPL], wb[UPL];
+  load_unit_w(0, wa);  // in flight while the act rows are quantized
+  stage_quant_rows(reinterpret_cast<uint8_t*>(s_x), act, ffn, aq_rb, k, 0);
+  for (int i = 0;; i += 2) {  // upg is even: the loop's only exit is at the bottom
+    load_unit_w(i + 1, wb);
+    __builtin_amdgcn_sched_barrier(0);
+    process(i, wa);
+    load_unit_w(min(i + 2, upg - 1), wa);  // the last one is redundant
+    __builtin_amdgcn_sched_barrier(0);
+    process(i + 1, wb);
+    if (i + 2 >= upg) break;
+  }
+  lds_barrier();
+  for (int r = threadIdx.x; r < RW; r += 256) {
+    float acc = 0.f;
+    for (int j = 0; j < k; j++) acc += s_w[j] * s_dot[j * RW + r];
+    if (hbase + r < H) y[hbase + r] = acc;
   }
 }
 
@@ -990,8 +1094,8 @@ namespace {
 int lpr_for(int U) { return U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4; }
 
 // Work per wave: an even number of row pairs (2 .. 16), enough that the grid is about 4096 waves.
-template <int F, int LPR, int UPL>
-void gate_up_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
+template <int F, int LPR, int UPL, int SPER>
+void gate_up_one(const MoeArgs& a, const MoeLists& L, const MoeSingle& one, hipStream_t s) {
   constexpr int P = (kWave / LPR) / 2;
   const int U = units_per_row(F, a.hidden);
   const int64_t pairs = int64_t(a.max_active) * a.ffn;
@@ -1000,19 +1104,20 @@ void gate_up_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
   const int64_t xrb = moe_xq_rb(a.hidden);
   // an expert holds at most T of the (token, slot) pairs: size the LDS stage for no more
   const int chunk = int(std::max<int64_t>(1, std::min<int64_t>({kMoeTokChunk, kMoeStageBytes / xrb, a.T})));
-  hipLaunchKernelGGL((moe_gate_up_kernel<F, LPR, UPL>), dim3(unsigned(int64_t(a.max_active) * wg_per_expert)),
+  hipLaunchKernelGGL((moe_gate_up_kernel<F, LPR, UPL, SPER>), dim3(unsigned(int64_t(a.max_active) * wg_per_expert)),
                      dim3(256), size_t(chunk) * size_t(xrb + 4 * 4 * P * ppw), s, static_cast<const uint8_t*>(a.gate),
                      static_cast<const uint8_t*>(a.up), a.E * a.ffn, row_bytes(F, a.hidden), U, int(a.ffn), a.top_k,
-                     a.xq, xrb, L, a.act, ppw, wg_per_expert, chunk);
+                     a.xq, xrb, L, a.act, ppw, wg_per_expert, chunk, one);
 }
 
-template <int F>
-int gate_up_fmt(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
+// SPER > 0: the single-token path (the kernel routes with SPER expert columns per lane).
+template <int F, int SPER = 0>
+int gate_up_fmt(const MoeArgs& a, const MoeLists& L, hipStream_t s, const MoeSingle& one = MoeSingle{}) {
   const int U = units_per_row(F, a.hidden);
   switch (lpr_for(U)) {
-    case 4: gate_up_one<F, 4, 1>(a, L, s); return JERO_OK;
-    case 16: gate_up_one<F, 16, 1>(a, L, s); return JERO_OK;
-    case 32: gate_up_one<F, 32, 1>(a, L, s); return JERO_OK;
+    case 4: gate_up_one<F, 4, 1, SPER>(a, L, one, s); return JERO_OK;
+    case 16: gate_up_one<F, 16, 1, SPER>(a, L, one, s); return JERO_OK;
+    case 32: gate_up_one<F, 32, 1, SPER>(a, L, one, s); return JERO_OK;
     default:
       return fail(JERO_ERR_CAPABILITY_MISMATCH,
                   "moe: hidden " + std::to_string(a.hidden) + " above the gate/up pairing limit (2048 for K-quants)");
@@ -1045,6 +1150,36 @@ int down_fmt(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
   else if (upl == 1) down_one<F, 64, 1>(a, L, s);
   else if (upl == 2) down_one<F, 64, 2>(a, L, s);
   else if (upl <= 4) down_one<F, 64, 4>(a, L, s);
+  else
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "moe: ffn " + std::to_string(a.ffn) + " above the down-proj limit");
+  return JERO_OK;
+}
+
+// One token: down rows of all k selected experts per workgroup, combined in selection order.
+// Each lane group takes an even number (2) of (slot, row) units; RW rows per workgroup.
+template <int F, int LPR, int UPL>
+void down1_one(const MoeArgs& a, hipStream_t s) {
+  constexpr int G = kWave / LPR;
+  const int U = units_per_row(F, a.ffn), upg = 2;
+  const int RW = std::max(1, 4 * G * upg / a.top_k);
+  const int64_t arb = row_bytes(JERO_Q8_K, a.ffn);
+  const size_t lds = size_t(a.top_k) * size_t(arb) + sizeof(float) * size_t(a.top_k) * RW;
+  hipLaunchKernelGGL((moe1_down_kernel<F, LPR, UPL>), dim3(unsigned((a.hidden + RW - 1) / RW)), dim3(256), lds, s,
+                     static_cast<const uint8_t*>(a.down), a.E * a.hidden, row_bytes(F, a.ffn), U, int(a.hidden), a.act,
+                     int(a.ffn), arb, a.top_k, a.sel_idx, a.sel_w, a.y, RW, upg);
+}
+
+template <int F>
+int down1_fmt(const MoeArgs& a, hipStream_t s) {
+  const int U = units_per_row(F, a.ffn);
+  const int lpr = lpr_for(U);
+  const int upl = (U + lpr - 1) / lpr;
+  if (lpr == 4) down1_one<F, 4, 1>(a, s);
+  else if (lpr == 16) down1_one<F, 16, 1>(a, s);
+  else if (lpr == 32) down1_one<F, 32, 1>(a, s);
+  else if (upl == 1) down1_one<F, 64, 1>(a, s);
+  else if (upl == 2) down1_one<F, 64, 2>(a, s);
+  else if (upl <= 4) down1_one<F, 64, 4>(a, s);
   else
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "moe: ffn " + std::to_string(a.ffn) + " above the down-proj limit");
   return JERO_OK;
@@ -1144,6 +1279,35 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
                     kMfmaTokens * (a.ffn / 256) <= 4 * kStageBlocks;
   L.pass = mfma ? pass : nullptr;
   L.ctr = ctr;
+
+  // one token among at most 128 experts: two launches.  Gate/up routes and quantizes the token
+  // itself (every workgroup alike), down takes all k selected experts' rows per workgroup and
+  // sums them in selection order: no grouping, no combine.
+  if (a.T == 1 && a.E <= 128) {
+    const MoeSingle one{a.logits, a.x, int(a.E), int(a.hidden), a.sel_idx, a.sel_w};
+    int rc;
+    switch (a.gate_quant) {
+      case JERO_Q4_K: rc = gate_up_fmt<JERO_Q4_K, 2>(a, L, s, one); break;
+      case JERO_Q4_K_R: rc = gate_up_fmt<JERO_Q4_K_R, 2>(a, L, s, one); break;
+      case JERO_Q4_K_T: rc = gate_up_fmt<JERO_Q4_K_T, 2>(a, L, s, one); break;
+      case JERO_Q6_K_T: rc = gate_up_fmt<JERO_Q6_K_T, 2>(a, L, s, one); break;
+      case JERO_Q6_K: rc = gate_up_fmt<JERO_Q6_K, 2>(a, L, s, one); break;
+      default: rc = gate_up_fmt<JERO_Q6_K_R, 2>(a, L, s, one); break;
+    }
+    if (rc) return rc;
+    rc = check_launch("moe gate/up");
+    if (rc) return rc;
+    switch (a.down_quant) {
+      case JERO_Q4_K: rc = down1_fmt<JERO_Q4_K>(a, s); break;
+      case JERO_Q4_K_R: rc = down1_fmt<JERO_Q4_K_R>(a, s); break;
+      case JERO_Q4_K_T: rc = down1_fmt<JERO_Q4_K_T>(a, s); break;
+      case JERO_Q6_K_T: rc = down1_fmt<JERO_Q6_K_T>(a, s); break;
+      case JERO_Q6_K: rc = down1_fmt<JERO_Q6_K>(a, s); break;
+      default: rc = down1_fmt<JERO_Q6_K_R>(a, s); break;
+    }
+    if (rc) return rc;
+    return check_launch("moe down");
+  }
 
   // few tokens: one workgroup quantizes, routes and groups; many: quantize and route over many
   // workgroups, then group in one

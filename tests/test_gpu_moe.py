@@ -75,6 +75,17 @@ def test_moe_small_and_q4k_down(dev):
     run_case(dev, 3, 16, 512, 256, 4, J.Q6_K, J.Q6_K, 41, repacked=True)
 
 
+def test_moe_single_token(dev):
+    """One token (two launches: gate/up routes the token itself, down sums the experts in selection
+    order): Q4_K and Q6_K throughout, GGUF and repacked layouts, and the tie / NaN routing rules."""
+    print("moe single token", flush=True)
+    run_case(dev, 1, 6, 256, 512, 2, J.Q4_K, J.Q4_K, 45, repacked=True)
+    run_case(dev, 1, 16, 512, 256, 4, J.Q6_K, J.Q6_K, 46, repacked=True)
+    run_case(dev, 1, 128, 1024, 768, 16, J.Q4_K, J.Q6_K, 47)
+    logits = np.array([[np.nan, 1.0, np.inf, 1.0, -np.inf, 0.5, 0.5, 2.0]], np.float32)
+    run_case(dev, 1, 8, 256, 256, 3, J.Q4_K, J.Q6_K, 61, logits=logits)
+
+
 def test_moe_many_tokens_per_expert(dev):
     """Four experts for 40 tokens at top-2: each expert sees ~20 tokens, several token passes.
     Two tokens or more per expert on average run the MFMA expert GEMMs (Q4_K in either layout,

@@ -221,6 +221,35 @@ int jero_hip_model_set_position(jero_model *model, int32_t token, int64_t pos, v
  * greedy next token and advances the position.  Enqueues kernels only (graph-capturable). */
 int jero_hip_decode_step(jero_model *model, void *stream);
 
+/* ---- GGUF v3 model files ----
+ * The weight source of LockedModelWeights (src/weights.rs:338-570): the file is mapped
+ * read-only and its header, metadata and tensor descriptors parsed (GGUF v2/v3, little-endian,
+ * data section aligned to general.alignment, default 32).  A malformed or truncated file, a
+ * misaligned tensor or one that runs past the end is TensorBoundsError.  flock/mlock residency
+ * policy is the host's and is not done here. */
+typedef struct jero_gguf jero_gguf;
+int jero_hip_gguf_open(const char *path, jero_gguf **out);
+void jero_hip_gguf_close(jero_gguf *g);
+/* Number of tensors and general.architecture ("" if absent); strings live until close. */
+int jero_hip_gguf_info(const jero_gguf *g, int64_t *n_tensors, const char **arch);
+/* Metadata by key (ModelWeights metadata accessors): integers (any integer or bool type),
+ * numbers (integer or float types) and strings.  A missing key or another type is
+ * JERO_ERR_INVALID_ARGUMENT. */
+int jero_hip_gguf_meta_int(const jero_gguf *g, const char *key, int64_t *v);
+int jero_hip_gguf_meta_float(const jero_gguf *g, const char *key, double *v);
+int jero_hip_gguf_meta_str(const jero_gguf *g, const char *key, const char **v);
+/* Name of the i-th tensor in file order. */
+int jero_hip_gguf_tensor_name(const jero_gguf *g, int64_t i, const char **name);
+/* ModelWeights::tensor (src/weights.rs:1097-1144): ggml type, dims (dims[0] = row length, unused
+ * dims 1), mapped host bytes and their size.  A missing output.weight of a non-BitNet model is
+ * token_embd.weight (tied embeddings, :1110-1126); any other missing name is TensorBoundsError.
+ * A ggml type with no row size here is CapabilityMismatch (descriptor outputs still filled). */
+int jero_hip_gguf_tensor(const jero_gguf *g, const char *name, int *quant, int *n_dims, int64_t *dims,
+                         const void **host, size_t *nbytes);
+/* The tensor's bytes registered on the current device (jero_hip_weights_register): copied to HBM
+ * once, the device address returned. */
+int jero_hip_gguf_upload(const jero_gguf *g, const char *name, const void **dev_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -69,6 +69,16 @@ _SIGS = {
     "jero_hip_model_state": (_I32, [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_P)]),
     "jero_hip_model_set_position": (_I32, [_P, _I32, _I64, _P]),
     "jero_hip_decode_step": (_I32, [_P, _P]),
+    "jero_hip_gguf_open": (_I32, [C.c_char_p, C.POINTER(_P)]),
+    "jero_hip_gguf_close": (None, [_P]),
+    "jero_hip_gguf_info": (_I32, [_P, C.POINTER(_I64), C.POINTER(C.c_char_p)]),
+    "jero_hip_gguf_meta_int": (_I32, [_P, C.c_char_p, C.POINTER(_I64)]),
+    "jero_hip_gguf_meta_float": (_I32, [_P, C.c_char_p, C.POINTER(C.c_double)]),
+    "jero_hip_gguf_meta_str": (_I32, [_P, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "jero_hip_gguf_tensor_name": (_I32, [_P, _I64, C.POINTER(C.c_char_p)]),
+    "jero_hip_gguf_tensor": (_I32, [_P, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(_I64),
+                                    C.POINTER(_P), C.POINTER(_SZ)]),
+    "jero_hip_gguf_upload": (_I32, [_P, C.c_char_p, C.POINTER(_P)]),
 }
 
 
@@ -376,6 +386,30 @@ class DecodeModel:
         except Exception:
             pass
 
+    @classmethod
+    def from_gguf(cls, path, kv_capacity, kv_dtype=KV_F16):
+        """Builds and finalizes a model from a GGUF file: hyperparameters by
+        GGUFFile.hyperparams, every tensor copied from the mapped file."""
+        g = path if isinstance(path, GGUFFile) else GGUFFile(path)
+        try:
+            hp = g.hyperparams()
+            m = cls(hp["hidden"], hp["ffn"], hp["n_layers"], hp["vocab"], hp["n_heads_q"], hp["n_heads_kv"],
+                    hp["head_dim"], hp["rms_eps"], hp["rope_theta"], kv_capacity, kv_dtype, hp["qk_norm"])
+            names = ["token_embd.weight", "output.weight", "output_norm.weight"]
+            per = ["attn_norm", "ffn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up",
+                   "ffn_down"] + (["attn_q_norm", "attn_k_norm"] if hp["qk_norm"] else [])
+            names += [f"blk.{i}.{b}.weight" for i in range(hp["n_layers"]) for b in per]
+            for name in names:
+                t = g.tensor(name)
+                n_out = t["dims"][1] if t["n_dims"] > 1 else 1
+                check(lib().jero_hip_model_set_tensor(m.h, name.encode(), t["quant"], C.c_void_p(t["host"]),
+                                                      t["nbytes"], t["dims"][0], n_out, 0))
+            m.finalize()
+            return m
+        finally:
+            if g is not path:
+                g.close()
+
     def set_tensor(self, name, quant, data, n_in, n_out):
         """data: a numpy array (host) or a torch tensor (host or device) holding the GGUF bytes."""
         import numpy as np
@@ -425,3 +459,109 @@ class DecodeModel:
         _memcpy(t.ctypes.data, tp, 4)
         _memcpy(p.ctypes.data, pp, 8)
         return int(t[0]), int(p[0])
+
+
+class GGUFFile:
+    """A mapped GGUF v2/v3 model file (LockedModelWeights' weight source, src/weights.rs:338-570)."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        check(lib().jero_hip_gguf_open(os.fsencode(path), C.byref(h)))
+        self.h = h
+        n, a = _I64(), C.c_char_p()
+        check(lib().jero_hip_gguf_info(h, C.byref(n), C.byref(a)))
+        self.n_tensors, self.arch = n.value, a.value.decode()
+
+    def close(self):
+        if self.h:
+            lib().jero_hip_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def meta_int(self, key, default=None):
+        v = _I64()
+        rc = lib().jero_hip_gguf_meta_int(self.h, key.encode(), C.byref(v))
+        if rc and default is not None:
+            return default
+        check(rc)
+        return v.value
+
+    def meta_float(self, key, default=None):
+        v = C.c_double()
+        rc = lib().jero_hip_gguf_meta_float(self.h, key.encode(), C.byref(v))
+        if rc and default is not None:
+            return default
+        check(rc)
+        return v.value
+
+    def meta_str(self, key):
+        v = C.c_char_p()
+        check(lib().jero_hip_gguf_meta_str(self.h, key.encode(), C.byref(v)))
+        return v.value.decode()
+
+    def tensor_names(self):
+        out = []
+        for i in range(self.n_tensors):
+            v = C.c_char_p()
+            check(lib().jero_hip_gguf_tensor_name(self.h, i, C.byref(v)))
+            out.append(v.value.decode())
+        return out
+
+    def tensor(self, name):
+        """ModelWeights::tensor (src/weights.rs:1097-1144), with the tied output.weight fallback:
+        {quant, n_dims, dims (4, row length first), host (mapped address), nbytes}."""
+        q, nd, dims, host, nb = C.c_int(), C.c_int(), (_I64 * 4)(), C.c_void_p(), _SZ()
+        check(lib().jero_hip_gguf_tensor(self.h, name.encode(), C.byref(q), C.byref(nd), dims, C.byref(host),
+                                         C.byref(nb)))
+        return dict(quant=q.value, n_dims=nd.value, dims=list(dims), host=host.value, nbytes=nb.value)
+
+    def tensor_bytes(self, name):
+        """The tensor's bytes as a read-only numpy view of the mapping (valid until close)."""
+        import numpy as np
+        t = self.tensor(name)
+        buf = (C.c_uint8 * t["nbytes"]).from_address(t["host"])
+        a = np.frombuffer(buf, np.uint8)
+        a.flags.writeable = False
+        return a
+
+    def upload(self, name):
+        """Device address of the tensor, copied to HBM once through the weight registry."""
+        dev = C.c_void_p()
+        check(lib().jero_hip_gguf_upload(self.h, name.encode(), C.byref(dev)))
+        return dev.value
+
+    def hyperparams(self):
+        """GgufHyperparams::from_metadata (src/capability.rs:212-285) for the dense decoder:
+        metadata first, tensor shapes where a key is absent (block count from the highest
+        blk.N, head_count_kv = head_count, key_length from blk.0.attn_k's width, vocab from the
+        LM head / embedding rows)."""
+        a = self.arch
+        names = set(self.tensor_names())
+        emb = self.tensor("token_embd.weight")
+        hidden = self.meta_int(f"{a}.embedding_length", 0) or emb["dims"][0]
+        n_layers = self.meta_int(f"{a}.block_count", 0)
+        if not n_layers:
+            n_layers = 1 + max([int(n.split(".")[1]) for n in names if n.startswith("blk.")], default=-1)
+        nq = self.meta_int(f"{a}.attention.head_count")
+        nkv = self.meta_int(f"{a}.attention.head_count_kv", 0) or nq
+        hd = self.meta_int(f"{a}.attention.key_length", 0)
+        if not hd:
+            k = self.tensor("blk.0.attn_k.weight")
+            hd = k["dims"][1] // nkv if k["dims"][1] % nkv == 0 else hidden // nq
+        ffn = self.meta_int(f"{a}.feed_forward_length", 0) or self.tensor("blk.0.ffn_gate.weight")["dims"][1]
+        vocab = self.meta_int(f"{a}.vocab_size", 0) or self.tensor("output.weight")["dims"][1]
+        eps = self.meta_float(f"{a}.attention.layer_norm_rms_epsilon", 1e-6)
+        theta = self.meta_float(f"{a}.rope.freq_base", 10000.0)
+        return dict(hidden=hidden, ffn=ffn, n_layers=n_layers, vocab=vocab, n_heads_q=nq, n_heads_kv=nkv,
+                    head_dim=hd, rms_eps=eps, rope_theta=theta, qk_norm="blk.0.attn_q_norm.weight" in names)

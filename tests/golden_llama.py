@@ -87,3 +87,21 @@ def build():
 def golden():
     with open(os.path.join(HERE, "golden", "llama_authentic_q8_0.json")) as f:
         return json.load(f)
+
+
+def gguf_kvs():
+    """The metadata of build_authentic_llama_q8_0_gguf (architecture_certification_gate.rs:90-106)."""
+    from gguf_writer import U32, F32 as GF32
+    return [("llama.block_count", U32, 2), ("llama.embedding_length", U32, 128),
+            ("llama.feed_forward_length", U32, 256), ("llama.attention.head_count", U32, 4),
+            ("llama.attention.head_count_kv", U32, 2), ("llama.attention.key_length", U32, 32),
+            ("llama.rope.freq_base", GF32, 500000.0), ("llama.attention.layer_norm_rms_epsilon", GF32, 1.0e-5),
+            ("llama.context_length", U32, 128), ("llama.vocab_size", U32, 16),
+            ("tokenizer.ggml.eos_token_id", U32, 2)]
+
+
+def gguf_file_bytes():
+    """The golden model as the GGUF v3 file the reference's test builds (alignment 32)."""
+    from gguf_writer import as_bytes, gguf_bytes
+    t = build()
+    return gguf_bytes("llama", gguf_kvs(), [(n, q, shp, as_bytes(t[n][1])) for n, q, shp in tensor_specs()])

@@ -63,6 +63,22 @@ def test_golden_llama_on_device(dev):
         shp = shapes[name]
         tensors[name] = (quant, arr, shp[0], shp[1] if len(shp) > 1 else 1)
     m = make_gpu_model(s, tensors, 128, J.KV_F32, False)
+    check_golden(m, g, s, dev)
+
+
+def test_golden_llama_from_gguf_file(dev, tmp_path):
+    """The same golden model read from the GGUF v3 file the reference's test builds
+    (architecture_certification_gate.rs:82-176): hyperparameters from its metadata, tensors
+    from the mapped file."""
+    print("golden llama from gguf", flush=True)
+    path = tmp_path / "llama_authentic_q8_0.gguf"
+    path.write_bytes(GL.gguf_file_bytes())
+    m = J.DecodeModel.from_gguf(str(path), 128, J.KV_F32)
+    assert (m.cfg.hidden, m.cfg.n_layers, m.cfg.head_dim, m.cfg.qk_norm) == (128, 2, 32, 0)
+    check_golden(m, GL.golden(), GL.SPEC, dev)
+
+
+def check_golden(m, g, s, dev):
     logits = torch.empty(s["vocab"], dtype=torch.float32, device=dev)
     for pos, tok in enumerate(g["prompt_token_ids"]):
         m.set_position(tok, pos)
@@ -79,6 +95,61 @@ def test_golden_llama_on_device(dev):
         greedy.append(m.read_token_pos()[0])
     assert greedy == g["greedy_token_ids"]
     assert m.read_token_pos()[1] == len(g["prompt_token_ids"]) + len(g["greedy_token_ids"]) - 1
+
+
+def write_model_gguf(path, arch, spec, tensors):
+    """A GGUF v3 file holding `tensors` ({name: (quant, bytes, n_in, n_out)}) and the spec's
+    hyperparameters under {arch}.* keys."""
+    import gguf_writer as W
+    kvs = [(f"{arch}.block_count", W.U32, spec["n_layers"]), (f"{arch}.embedding_length", W.U32, spec["hidden"]),
+           (f"{arch}.feed_forward_length", W.U32, spec["ffn"]), (f"{arch}.attention.head_count", W.U32, spec["nq"]),
+           (f"{arch}.attention.head_count_kv", W.U32, spec["nkv"]),
+           (f"{arch}.attention.key_length", W.U32, spec["hd"]), (f"{arch}.rope.freq_base", W.F32, spec["theta"]),
+           (f"{arch}.attention.layer_norm_rms_epsilon", W.F32, spec["eps"])]
+    ts = [(n, q, (n_in, n_out) if n_out > 1 else (n_in,), W.as_bytes(a)) for n, (q, a, n_in, n_out) in tensors.items()]
+    path.write_bytes(W.gguf_bytes(arch, kvs, ts))
+
+
+def test_qwen3_from_gguf_matches_set_tensor(dev, tmp_path):
+    """Q4_K_M-mix Qwen3-shaped model (tied output: no output.weight in the file) from a GGUF file
+    against the same tensors given one by one: logits bit-equal over several steps."""
+    print("qwen3 from gguf", flush=True)
+    spec = dict(QWEN_SMALL)
+    t = MS.build(spec, seed=11)
+    tied = dict(t)
+    tied["output.weight"] = t["token_embd.weight"]
+    path = tmp_path / "qwen3.gguf"
+    write_model_gguf(path, "qwen3", spec, {k: v for k, v in t.items() if k != "output.weight"})
+    a = make_gpu_model(spec, tied, 64, J.KV_F16, True)
+    b = J.DecodeModel.from_gguf(str(path), 64, J.KV_F16)
+    assert b.cfg.qk_norm == 1 and b.cfg.vocab == spec["vocab"] and b.cfg.ffn == spec["ffn"]
+    la = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
+    lb = torch.empty_like(la)
+    for m in (a, b):
+        m.set_position(17, 0)
+    for step in range(6):
+        a.decode_step()
+        b.decode_step()
+        torch.cuda.synchronize()
+        a.read_logits(la)
+        b.read_logits(lb)
+        assert torch.equal(la, lb), step
+        assert a.read_token_pos() == b.read_token_pos()
+
+
+def test_gguf_upload_registers_once(dev, tmp_path):
+    """gguf_upload copies a tensor's mapped bytes to HBM once; later calls return that address."""
+    print("gguf upload", flush=True)
+    path = tmp_path / "g.gguf"
+    path.write_bytes(GL.gguf_file_bytes())
+    with J.GGUFFile(str(path)) as g:
+        for name in ("blk.1.attn_q.weight", "output_norm.weight"):
+            host = g.tensor_bytes(name)
+            d0 = g.upload(name)
+            assert g.upload(name) == d0
+            back = np.zeros_like(host)
+            J._memcpy(back.ctypes.data, d0, host.nbytes)
+            np.testing.assert_array_equal(back, host)
 
 
 QWEN_SMALL = dict(hidden=512, ffn=1024, n_layers=4, vocab=1000, nq=8, nkv=2, hd=64, eps=1e-6, theta=1e6)

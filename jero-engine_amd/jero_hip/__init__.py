@@ -535,6 +535,21 @@ class GGUFFile:
         a.flags.writeable = False
         return a
 
+    def tensor_view(self, name, device="cuda", repack_layout=False):
+        """The tensor copied to a device TensorView (shape as in the file, row length first).
+        repack_layout: Q4_K / Q6_K re-laid out on the device like a load-time repack
+        (src/weights.rs:914-955): 2-D tensors to Q4_K_R / Q6_K_R, stacked expert tensors
+        [n_in, rows, n_experts] with rows a multiple of 16 to Q4_K_T / Q6_K_T."""
+        import torch
+        t = self.tensor(name)
+        dst = torch.empty(t["nbytes"], dtype=torch.uint8, device=device)
+        _memcpy(dst.data_ptr(), t["host"], t["nbytes"])
+        v = TensorView(name, t["quant"], t["dims"][:t["n_dims"]], dst)
+        if repack_layout and v.quant in (Q4_K, Q6_K):
+            v = repack(v)
+            torch.cuda.synchronize(dst.device)
+        return v
+
     def upload(self, name):
         """Device address of the tensor, copied to HBM once through the weight registry."""
         dev = C.c_void_p()

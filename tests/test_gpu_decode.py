@@ -152,6 +152,32 @@ def test_gguf_upload_registers_once(dev, tmp_path):
             np.testing.assert_array_equal(back, host)
 
 
+def test_gguf_tensor_view_repacks_on_device(dev, tmp_path):
+    """GGUF tensors to device views in the kernels' layouts: a stacked Q4_K expert tensor to
+    16-row tiles, a 2-D Q6_K matrix to the planar layout, byte-equal to repacking the same bytes
+    given directly."""
+    import gguf_writer as W
+    import qdata
+    print("gguf tensor_view repack", flush=True)
+    n_in, rows, E = 512, 32, 3
+    exps = qdata.rand_weights(J.Q4_K, rows * E, n_in, 5)
+    head = qdata.rand_weights(J.Q6_K, 40, n_in, 6)
+    path = tmp_path / "e.gguf"
+    path.write_bytes(W.gguf_bytes("qwen3moe", [], [("blk.0.ffn_gate_exps.weight", J.Q4_K, (n_in, rows, E), exps.tobytes()),
+                                                   ("output.weight", J.Q6_K, (n_in, 40), head.tobytes())]))
+    with J.GGUFFile(str(path)) as g:
+        for name, arr, shape, want in (("blk.0.ffn_gate_exps.weight", exps, [n_in, rows, E], J.Q4_K_T),
+                                       ("output.weight", head, [n_in, 40], J.Q6_K_R)):
+            v = g.tensor_view(name, dev, repack_layout=True)
+            assert v.quant == want and v.shape == shape
+            raw = g.tensor_view(name, dev)
+            assert raw.quant in (J.Q4_K, J.Q6_K)
+            assert torch.equal(raw.data.cpu(), torch.from_numpy(np.ascontiguousarray(arr).view(np.uint8).reshape(-1)))
+            ref = J.repack(J.TensorView(name, raw.quant, shape, raw.data.clone()))
+            torch.cuda.synchronize()
+            assert ref.quant == want and torch.equal(v.data, ref.data)
+
+
 QWEN_SMALL = dict(hidden=512, ffn=1024, n_layers=4, vocab=1000, nq=8, nkv=2, hd=64, eps=1e-6, theta=1e6)
 
 

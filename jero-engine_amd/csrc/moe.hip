@@ -372,18 +372,6 @@ __device__ __forceinline__ void stage_quant_rows(uint8_t* __restrict__ dst, cons
   lds_barrier();
 }
 
-// Logical workgroup of physical workgroup b (of n) when groups of m consecutive logical
-// workgroups read the same 128-byte lines (the rows of one 16-row tile).  Workgroups go to the 8
-// XCDs round-robin and each XCD has its own L2, so in every run of 8m physical workgroups the m
-// members of a group are given physical indices 8 apart (one XCD), and the lines are fetched
-// from HBM once instead of once per XCD.  A tail shorter than 8m keeps the identity order.
-__device__ __forceinline__ int xcd_grouped(int b, int n, int m) {
-  const int chunk = 8 * m;
-  if (m <= 1 || b >= n / chunk * chunk) return b;
-  const int c = b / chunk, r = b - c * chunk;
-  return c * chunk + (r & 7) * m + (r >> 3);
-}
-
 // gate/up + SwiGLU.  A workgroup takes one active expert and 4 * ppw * P of its (gate, up) row
 // pairs: lane groups (2p, 2p+1) of a wave hold gate row and up row f.  The expert's token
 // activations are staged in LDS (`chunk` rows per pass), so each weight row is read from HBM once
@@ -408,15 +396,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(const uint8_t* __restr
   extern __shared__ uint32_t s_x[];
   __shared__ int s_rows[kMoeTokChunk];
   __shared__ int s_sel[kMaxTopK];
-  // Q4_K_T rows come in 16-row tiles: the workgroups of an expert that share a tile's lines run
-  // on one XCD (xcd_grouped)
-  constexpr bool kTiled = F == JERO_Q4_K_T || F == JERO_Q6_K_T;
-  const int rows_per_wg = 4 * ppw * ((kWave / LPR) / 2);
-  const int share = kTiled && rows_per_wg < 16 && 16 % rows_per_wg == 0 && wg_per_expert % (16 / rows_per_wg) == 0
-                        ? 16 / rows_per_wg
-                        : 1;
-  const int wg = xcd_grouped(int(blockIdx.x), int(gridDim.x), share);
-  const int slot = wg / wg_per_expert, part = wg % wg_per_expert;
+  const int slot = int(blockIdx.x) / wg_per_expert, part = int(blockIdx.x) % wg_per_expert;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   int e, i0, cnt;
   if constexpr (SPER > 0) {
@@ -579,6 +559,18 @@ __global__ void __launch_bounds__(256) moe_down_kernel(const uint8_t* __restrict
       if (hbase + r < H) yd[int64_t(i0 + base + j) * H + hbase + r] = s_out[idx];
     }
   }
+}
+
+// Logical workgroup of physical workgroup b (of n) when groups of m consecutive logical
+// workgroups read the same 128-byte lines (the rows of one 16-row tile).  Workgroups go to the 8
+// XCDs round-robin and each XCD has its own L2, so in every run of 8m physical workgroups the m
+// members of a group are given physical indices 8 apart (one XCD), and the lines are fetched
+// from HBM once instead of once per XCD.  A tail shorter than 8m keeps the identity order.
+__device__ __forceinline__ int xcd_grouped(int b, int n, int m) {
+  const int chunk = 8 * m;
+  if (m <= 1 || b >= n / chunk * chunk) return b;
+  const int c = b / chunk, r = b - c * chunk;
+  return c * chunk + (r & 7) * m + (r >> 3);
 }
 
 // One token, down and combine in one: a workgroup takes RW rows h of the output, and for each its

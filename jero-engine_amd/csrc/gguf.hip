@@ -45,6 +45,31 @@ int scalar_size(uint32_t t) {
   }
 }
 
+// Well-formed UTF-8 (RFC 3629: shortest forms only, no surrogates, at most U+10FFFF).  GGUF
+// strings are UTF-8; the reference's parser builds Rust Strings from them, which rejects the rest.
+bool valid_utf8(const uint8_t* s, size_t n) {
+  size_t i = 0;
+  while (i < n) {
+    const uint8_t c = s[i];
+    int len;
+    uint32_t cp;
+    if (c < 0x80) { i++; continue; }
+    if ((c & 0xE0) == 0xC0) { len = 2; cp = c & 0x1F; }
+    else if ((c & 0xF0) == 0xE0) { len = 3; cp = c & 0x0F; }
+    else if ((c & 0xF8) == 0xF0) { len = 4; cp = c & 0x07; }
+    else return false;
+    if (n - i < size_t(len)) return false;
+    for (int k = 1; k < len; k++) {
+      if ((s[i + k] & 0xC0) != 0x80) return false;
+      cp = (cp << 6) | (s[i + k] & 0x3F);
+    }
+    static const uint32_t kMin[5] = {0, 0, 0x80, 0x800, 0x10000};
+    if (cp < kMin[len] || cp > 0x10FFFF || (cp >= 0xD800 && cp <= 0xDFFF)) return false;
+    i += size_t(len);
+  }
+  return true;
+}
+
 struct Reader {
   const uint8_t* p;
   size_t n, pos = 0;
@@ -62,7 +87,7 @@ struct Reader {
   }
   std::string str() {
     const uint64_t len = get<uint64_t>();
-    if (!ok || len > n - pos) {
+    if (!ok || len > n - pos || !valid_utf8(p + pos, size_t(len))) {
       ok = false;
       return {};
     }
@@ -177,7 +202,11 @@ int parse(jero_gguf& g) {
         return fail(JERO_ERR_TENSOR_BOUNDS, "gguf: bad dims of tensor '" + name + "'");
       rows *= t.dims[d];
     }
+    if (t.dims[0] <= 0 || t.dims[0] > (int64_t(1) << 40))
+      return fail(JERO_ERR_TENSOR_BOUNDS, "gguf: bad row length of tensor '" + name + "'");
     const int64_t rb = jero::row_bytes(t.quant, t.dims[0]);
+    if (rb > 0 && rows > INT64_MAX / rb)
+      return fail(JERO_ERR_TENSOR_BOUNDS, "gguf: tensor '" + name + "' too large");
     // tensors in other formats are listed with no byte size and cannot be fetched
     t.nbytes = rb > 0 ? size_t(rb) * size_t(rows) : 0;
     if (g.tensors.count(name)) return fail(JERO_ERR_TENSOR_BOUNDS, "gguf: tensor '" + name + "' listed twice");

@@ -146,8 +146,19 @@ def test_malformed_files_are_rejected(tmp_path):
     assert _status(tmp_path, W.gguf_bytes("t", [], t, offsets=[0, 1 << 40]), "past.gguf") == 14
     assert _status(tmp_path, W.gguf_bytes("t", [], [("x", 0, (8,), bytes(32))] * 2), "dup.gguf") == 14
     assert _status(tmp_path, W.gguf_bytes("t", [], t, alignment=48), "align48.gguf") == 14
+    huge = [("x", 8, (1 << 39, 1 << 39), bytes(34))]
+    assert _status(tmp_path, W.gguf_bytes("t", [], huge), "huge.gguf") == 14
+    assert _status(tmp_path, W.gguf_bytes("t", [], [("x", 0, (2 ** 64 - 32,), bytes(32))]), "neg.gguf") == 14
     with pytest.raises(J.K3Error):
         J.GGUFFile(str(tmp_path / "does-not-exist.gguf"))
+    # strings must be well-formed UTF-8: a bad continuation, an overlong form, a surrogate
+    for i, bad in enumerate((b"\xc3(", b"\xc0\xaf", b"\xed\xa0\x80")):
+        name = b"blk." + bad + b".weight"
+        data = W.gguf_bytes("t", [], [("x" * len(name), 0, (8,), bytes(32))]).replace(b"x" * len(name), name)
+        assert _status(tmp_path, data, f"utf8{i}.gguf") == 14
+    ok = W.gguf_bytes("t", [("t.s", W.STRING, "€ 𝄞 ü")], [("ß", 0, (8,), bytes(32))])
+    with open_bytes(tmp_path, ok, "utf8ok.gguf") as g:
+        assert g.tensor_names() == ["ß"] and g.meta_str("t.s") == "€ 𝄞 ü"
 
 
 def test_unsupported_tensor_type_is_listed_but_not_fetched(tmp_path):
@@ -157,3 +168,29 @@ def test_unsupported_tensor_type_is_listed_but_not_fetched(tmp_path):
         with pytest.raises(J.K3Error) as e:
             g.tensor("bf16")
         assert e.value.status == 10
+
+
+def test_corrupted_headers_never_read_out_of_bounds(tmp_path):
+    """Seeded byte corruptions of the golden file's header: each open either succeeds or raises
+    K3Error; every tensor a successful open reports lies inside the file."""
+    good = bytearray(GL.gguf_file_bytes())
+    head_end = good.index(b"output.weight") + 40
+    rng = np.random.default_rng(123)
+    p = tmp_path / "fuzz.gguf"
+    for case in range(400):
+        bad = bytearray(good)
+        for _ in range(int(rng.integers(1, 4))):
+            bad[int(rng.integers(0, head_end))] = int(rng.integers(0, 256))
+        p.write_bytes(bytes(bad))
+        try:
+            g = J.GGUFFile(str(p))
+        except J.K3Error:
+            continue
+        with g:
+            for name in g.tensor_names():
+                try:
+                    t = g.tensor(name)
+                except J.K3Error:
+                    continue
+                b = g.tensor_bytes(name)
+                assert b.size == t["nbytes"] and t["nbytes"] <= len(bad), (case, name)

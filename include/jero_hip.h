@@ -77,6 +77,11 @@ int jero_hip_weights_register(const void *host, size_t nbytes, const void **dev_
 int jero_hip_weights_lookup(const void *host, size_t nbytes, const void **dev_out);
 /* Frees every tensor registered on the current device (after a device synchronize). */
 int jero_hip_weights_release_all(void);
+/* Frees, on every device, the registered tensors that lie inside [host, host + nbytes) (after a
+ * synchronize of each such device), so that a new mapping at the same host addresses registers
+ * its own bytes.  The owner of an mmaped weight file calls it before unmapping (munmap of
+ * LockedModelWeights, src/weights.rs:729-734); jero_hip_gguf_close does so itself. */
+int jero_hip_weights_release(const void *host, size_t nbytes);
 /* Waits for the work enqueued on `stream`. */
 int jero_hip_sync(void *stream);
 
@@ -218,8 +223,22 @@ int jero_hip_model_state(jero_model *model, int32_t **token_dev, int64_t **pos_d
 /* Enqueues: token and position of the next decode step. */
 int jero_hip_model_set_position(jero_model *model, int32_t token, int64_t pos, void *stream);
 /* Enqueues one decode step at the device position: writes logits, replaces the token with the
- * greedy next token and advances the position.  Enqueues kernels only (graph-capturable). */
+ * greedy next token and advances the position.  Enqueues kernels only (graph-capturable).
+ * Logits with no argmax (all NaN) fail closed as the reference's engine does
+ * (src/engine.rs:636-641): the step stores token -1, keeps the position and sets a sticky device
+ * status; later steps then store -1 and leave the position until jero_hip_model_set_position. */
 int jero_hip_decode_step(jero_model *model, void *stream);
+/* Waits for `stream` and returns the model's status: JERO_OK, or CapabilityMismatch ("empty
+ * logits buffer after decode step (or all-NaN)") once a step has failed closed. */
+int jero_hip_model_status(jero_model *model, void *stream);
+
+/* sample_greedy_argmax -> argmax_f32 (src/engine.rs:1873-1895): the first index of the largest
+ * non-NaN value of x_dev[n] into *idx_dev (int64, device), -1 when n == 0 or every value is NaN
+ * (Option::None).  The same (max, first index) reduction as the decode step's LM-head epilogue.
+ * Workspace: 12304 bytes, 8-byte aligned (NULL: library-owned, calls must not overlap on one
+ * device). */
+int jero_hip_argmax(const float *x_dev, int64_t n, int64_t *idx_dev, void *workspace_dev, size_t workspace_bytes,
+                    void *stream);
 
 /* ---- GGUF v3 model files ----
  * The weight source of LockedModelWeights (src/weights.rs:338-570): the file is mapped
@@ -229,6 +248,8 @@ int jero_hip_decode_step(jero_model *model, void *stream);
  * policy is the host's and is not done here. */
 typedef struct jero_gguf jero_gguf;
 int jero_hip_gguf_open(const char *path, jero_gguf **out);
+/* Releases the device copies jero_hip_gguf_upload made of the file's tensors
+ * (jero_hip_weights_release over the mapping), then unmaps the file. */
 void jero_hip_gguf_close(jero_gguf *g);
 /* Number of tensors and general.architecture ("" if absent); strings live until close. */
 int jero_hip_gguf_info(const jero_gguf *g, int64_t *n_tensors, const char **arch);
@@ -241,8 +262,9 @@ int jero_hip_gguf_meta_str(const jero_gguf *g, const char *key, const char **v);
 /* Name of the i-th tensor in file order. */
 int jero_hip_gguf_tensor_name(const jero_gguf *g, int64_t i, const char **name);
 /* ModelWeights::tensor (src/weights.rs:1097-1144): ggml type, dims (dims[0] = row length, unused
- * dims 1), mapped host bytes and their size.  A missing output.weight of a non-BitNet model is
- * token_embd.weight (tied embeddings, :1110-1126); any other missing name is TensorBoundsError.
+ * dims 1), mapped host bytes and their size.  A missing output.weight of an autoregressive
+ * (architecture_requires_kv_cache, src/memory.rs:863-868), non-BitNet model is token_embd.weight
+ * (tied embeddings, src/weights.rs:1110-1126); any other missing name is TensorBoundsError.
  * A ggml type with no row size here is CapabilityMismatch (descriptor outputs still filled). */
 int jero_hip_gguf_tensor(const jero_gguf *g, const char *name, int *quant, int *n_dims, int64_t *dims,
                          const void **host, size_t *nbytes);

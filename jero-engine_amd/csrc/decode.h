@@ -45,7 +45,14 @@ int dgemv_max_k(int quant);
 // hidden = embedding row of *token; also the step's RoPE table rope_cs[hd/2][cos, sin].
 int launch_embed(int quant, const void* w, int64_t rb, int H, int64_t vocab, const int32_t* token, float* out,
                  const int64_t* pos, float theta, int hd, float* rope_cs, hipStream_t s);
-int launch_argmax_final(const float* v, const int64_t* idx, int n, int32_t* token, int64_t* pos, hipStream_t s);
-int launch_set_state(int32_t* token, int64_t* pos, int32_t t, int64_t p, hipStream_t s);
+// The greedy token from the head's per-workgroup partials; all-NaN logits set the sticky *status
+// (token -1, position kept) instead of producing a token.
+int launch_argmax_final(const float* v, const int64_t* idx, int n, int32_t* token, int64_t* pos, int32_t* status,
+                        hipStream_t s);
+// Standalone argmax_f32 of n floats into *out_idx (-1: empty or all NaN); pv / pi hold
+// argmax_partials(n) partial pairs.
+int argmax_partials(int64_t n);
+int launch_argmax(const float* x, int64_t n, int64_t* out_idx, float* pv, int64_t* pi, hipStream_t s);
+int launch_set_state(int32_t* token, int64_t* pos, int32_t* status, int32_t t, int64_t p, hipStream_t s);
 
 }  // namespace jero

@@ -423,26 +423,22 @@ __global__ void __launch_bounds__(256) embed_kernel(int quant, const uint8_t* __
   out[i] = (t >= 0 && t < vocab) ? dequant_elem(quant, w + t * rb, i) : 0.0f;
 }
 
-// Greedy token from the head's per-workgroup (max, index) pairs; advances the position.
-__global__ void __launch_bounds__(1024) argmax_final_kernel(const float* __restrict__ v, const int64_t* __restrict__ idx,
-                                                            int n, int32_t* __restrict__ token,
-                                                            int64_t* __restrict__ pos) {
-  float bv = -INFINITY;
-  int64_t bi = -1;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    if (idx[i] >= 0 && (bi < 0 || v[i] > bv || (v[i] == bv && idx[i] < bi))) {
-      bv = v[i];
-      bi = idx[i];
-    }
+// (max, first index) merge of sample_greedy_argmax (src/engine.rs:1873-1895): NaN never wins,
+// a larger value wins, an equal value keeps the lower index.  idx < 0 marks "no value yet".
+__device__ __forceinline__ void argmax_merge(float& bv, int64_t& bi, float ov, int64_t oi) {
+  if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+    bv = ov;
+    bi = oi;
   }
+}
+
+// Workgroup-wide (max, first index) of per-thread candidates; the result is in thread 0.
+__device__ __forceinline__ void argmax_block(float& bv, int64_t& bi) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
-    float ov = __shfl_xor(bv, off, kWave);
-    int64_t oi = __shfl_xor(bi, off, kWave);
-    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
-      bv = ov;
-      bi = oi;
-    }
+    const float ov = __shfl_xor(bv, off, kWave);
+    const int64_t oi = __shfl_xor(bi, off, kWave);
+    argmax_merge(bv, bi, ov, oi);
   }
   __shared__ float s_bv[16];
   __shared__ int64_t s_bi[16];
@@ -452,21 +448,65 @@ __global__ void __launch_bounds__(1024) argmax_final_kernel(const float* __restr
     s_bi[wv] = bi;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int i = 1; i < int(blockDim.x >> 6); i++) {
-      if (s_bi[i] >= 0 && (bi < 0 || s_bv[i] > bv || (s_bv[i] == bv && s_bi[i] < bi))) {
-        bv = s_bv[i];
-        bi = s_bi[i];
-      }
+  if (threadIdx.x == 0)
+    for (int i = 1; i < int(blockDim.x >> 6); i++) argmax_merge(bv, bi, s_bv[i], s_bi[i]);
+}
+
+// Per-workgroup (max, first index) of a contiguous chunk of x (the standalone argmax_f32).
+__global__ void __launch_bounds__(1024) argmax_partial_kernel(const float* __restrict__ x, int64_t n, int64_t chunk,
+                                                              float* __restrict__ pv, int64_t* __restrict__ pi) {
+  const int64_t b0 = int64_t(blockIdx.x) * chunk;
+  const int64_t b1 = b0 + chunk < n ? b0 + chunk : n;
+  float bv = -INFINITY;
+  int64_t bi = -1;
+  for (int64_t i = b0 + threadIdx.x; i < b1; i += blockDim.x) {  // ascending per thread
+    const float v = x[i];
+    if (!isnan(v) && (bi < 0 || v > bv)) {
+      bv = v;
+      bi = i;
     }
-    *token = bi >= 0 ? int32_t(bi) : -1;
-    *pos += 1;
+  }
+  argmax_block(bv, bi);
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x] = bv;
+    pi[blockIdx.x] = bi;
   }
 }
 
-__global__ void set_state_kernel(int32_t* token, int64_t* pos, int32_t t, int64_t p) {
+// The greedy token from n per-workgroup (max, index) pairs.
+//   Decode step (pos != null): *token = the index and the position advances.  Logits that are
+//   all NaN (or empty) leave no index: the reference's engine then fails closed
+//   (src/engine.rs:636-641), so the step sets the sticky *status, stores token -1 and keeps the
+//   position; while *status is set later steps store -1 and leave the position alone (the
+//   host reads the status and must set a new position to go on).
+//   Standalone argmax (pos == null): *out_idx = the index, -1 for none (Option::None).
+__global__ void __launch_bounds__(1024) argmax_final_kernel(const float* __restrict__ v, const int64_t* __restrict__ idx,
+                                                            int n, int32_t* __restrict__ token,
+                                                            int64_t* __restrict__ pos, int32_t* __restrict__ status,
+                                                            int64_t* __restrict__ out_idx) {
+  float bv = -INFINITY;
+  int64_t bi = -1;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) argmax_merge(bv, bi, v[i], idx[i]);
+  argmax_block(bv, bi);
+  if (threadIdx.x == 0) {
+    if (pos == nullptr) {
+      *out_idx = bi;
+    } else if (*status != 0) {
+      *token = -1;
+    } else if (bi < 0) {
+      *status = 1;
+      *token = -1;
+    } else {
+      *token = int32_t(bi);
+      *pos += 1;
+    }
+  }
+}
+
+__global__ void set_state_kernel(int32_t* token, int64_t* pos, int32_t* status, int32_t t, int64_t p) {
   *token = t;
   *pos = p;
+  *status = 0;
 }
 
 // ---------------------------------------------------------------- launchers
@@ -615,14 +655,52 @@ int launch_embed(int quant, const void* w, int64_t rb, int H, int64_t vocab, con
   return check_launch("embed");
 }
 
-int launch_argmax_final(const float* v, const int64_t* idx, int n, int32_t* token, int64_t* pos, hipStream_t s) {
-  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1024), 0, s, v, idx, n, token, pos);
+int launch_argmax_final(const float* v, const int64_t* idx, int n, int32_t* token, int64_t* pos, int32_t* status,
+                        hipStream_t s) {
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1024), 0, s, v, idx, n, token, pos, status, nullptr);
   return check_launch("argmax");
 }
 
-int launch_set_state(int32_t* token, int64_t* pos, int32_t t, int64_t p, hipStream_t s) {
-  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, s, token, pos, t, p);
+int argmax_partials(int64_t n) { return n <= 0 ? 0 : int(std::min<int64_t>(1024, (n + 8191) / 8192)); }
+
+int launch_argmax(const float* x, int64_t n, int64_t* out_idx, float* pv, int64_t* pi, hipStream_t s) {
+  const int nb = argmax_partials(n);
+  if (nb > 0) {
+    const int64_t chunk = (n + nb - 1) / nb;
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(unsigned(nb)), dim3(1024), 0, s, x, n, chunk, pv, pi);
+  }
+  hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1024), 0, s, pv, pi, nb, nullptr, nullptr, nullptr, out_idx);
+  return check_launch("argmax");
+}
+
+int launch_set_state(int32_t* token, int64_t* pos, int32_t* status, int32_t t, int64_t p, hipStream_t s) {
+  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, s, token, pos, status, t, p);
   return check_launch("set state");
 }
 
 }  // namespace jero
+
+using namespace jero;
+
+extern "C" int jero_hip_argmax(const float* x_dev, int64_t n, int64_t* idx_dev, void* workspace_dev,
+                               size_t workspace_bytes, void* stream) {
+  if (!idx_dev || (n > 0 && !x_dev)) return fail(JERO_ERR_INVALID_ARGUMENT, "argmax: null pointer");
+  if (n < 0) return fail(JERO_ERR_TENSOR_BOUNDS, "argmax: negative length");
+  if (reinterpret_cast<uintptr_t>(idx_dev) & 7u) return fail(JERO_ERR_INVALID_ARGUMENT, "argmax: index not 8-byte aligned");
+  const int nb = argmax_partials(n);
+  const size_t need = size_t(nb) * (sizeof(float) + sizeof(int64_t)) + 16;
+  void* ws = workspace_dev;
+  if (ws) {
+    if (workspace_bytes < need)
+      return fail(JERO_ERR_TENSOR_BOUNDS, "argmax: workspace of " + std::to_string(workspace_bytes) +
+                                              " bytes, need " + std::to_string(need));
+    if (reinterpret_cast<uintptr_t>(ws) & 7u)
+      return fail(JERO_ERR_INVALID_ARGUMENT, "argmax: workspace must be 8-byte aligned");
+  } else {
+    const int rc = workspace(need, &ws);
+    if (rc) return rc;
+  }
+  int64_t* pi = static_cast<int64_t*>(ws);
+  float* pv = reinterpret_cast<float*>(pi + nb);
+  return launch_argmax(x_dev, n, idx_dev, pv, pi, static_cast<hipStream_t>(stream));
+}

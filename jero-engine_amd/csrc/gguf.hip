@@ -228,11 +228,20 @@ int parse(jero_gguf& g) {
   return JERO_OK;
 }
 
+// Encoder-style architectures keep no KV cache and get no tied LM head
+// (architecture_requires_kv_cache, src/memory.rs:863-868).
+bool architecture_requires_kv_cache(const std::string& arch) {
+  static const char* const kNoCache[] = {"modernbert", "bert", "deberta-v3", "ttm", "ft-transformer", "tabpfn-v2"};
+  for (const char* a : kNoCache)
+    if (arch == a) return false;
+  return true;
+}
+
 // The descriptor of `name`, with the tied-embedding fallback of the reference.
 const Tensor* find_tensor(const jero_gguf* g, const std::string& name) {
   auto it = g->tensors.find(name);
   if (it != g->tensors.end()) return &it->second;
-  if (name == "output.weight" && g->arch.rfind("bitnet", 0) != 0) {
+  if (name == "output.weight" && architecture_requires_kv_cache(g->arch) && g->arch.rfind("bitnet", 0) != 0) {
     auto e = g->tensors.find("token_embd.weight");
     if (e != g->tensors.end()) return &e->second;
   }
@@ -277,6 +286,7 @@ extern "C" int jero_hip_gguf_open(const char* path, jero_gguf** out) {
 
 extern "C" void jero_hip_gguf_close(jero_gguf* g) {
   if (!g) return;
+  (void)jero_hip_weights_release(g->map, g->len);
   munmap(g->map, g->len);
   delete g;
 }

@@ -172,7 +172,29 @@ __device__ __forceinline__ float dpp_max(float v) {
   return fmaxf(v, __builtin_bit_cast(float, o));
 }
 
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_max_i32(int v) {
+  const int o = __builtin_amdgcn_update_dpp(int(0x80000000u), v, CTRL, ROW_MASK, 0xF, false);
+  return max(v, o);
+}
+
+// f32::total_cmp as a signed integer key: a negative float has every bit but the sign flipped,
+// so the keys order -inf < ... < -0.0 < +0.0 < ... < +inf (NaNs at the two ends by sign).
+__host__ __device__ __forceinline__ int total_order_key(float f) {
+  const int b = __builtin_bit_cast(int, f);
+  return b ^ int(uint32_t(b >> 31) >> 1);
+}
+
 // Whole-wave reductions with DPP; the result is returned uniformly (read from lane 63).
+__device__ __forceinline__ int wave_max_i32_dpp(int v) {
+  v = dpp_max_i32<0xB1, 0xF>(v);
+  v = dpp_max_i32<0x4E, 0xF>(v);
+  v = dpp_max_i32<0x124, 0xF>(v);
+  v = dpp_max_i32<0x128, 0xF>(v);
+  v = dpp_max_i32<0x142, 0xA>(v);
+  v = dpp_max_i32<0x143, 0xC>(v);
+  return __builtin_amdgcn_readlane(v, 63);
+}
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v = group_sum_last<64>(v);
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));

@@ -55,6 +55,7 @@ struct jero_model {
   int64_t* amax_i = nullptr;
   int32_t* token = nullptr;
   int64_t* pos = nullptr;
+  int32_t* status = nullptr;  // sticky: nonzero after a step whose logits held no argmax
   float* rope_cs = nullptr;
   void* kv = nullptr;
   size_t kv_bytes = 0;
@@ -245,6 +246,7 @@ extern "C" int jero_hip_model_create(const jero_model_config* cfg, jero_model** 
       (rc = dev_alloc(m, sizeof(int64_t) * max_blocks, &p)) || ((m->amax_i = static_cast<int64_t*>(p)), false) ||
       (rc = dev_alloc(m, sizeof(int32_t), &p)) || ((m->token = static_cast<int32_t*>(p)), false) ||
       (rc = dev_alloc(m, sizeof(int64_t), &p)) || ((m->pos = static_cast<int64_t*>(p)), false) ||
+      (rc = dev_alloc(m, sizeof(int32_t), &p)) || ((m->status = static_cast<int32_t*>(p)), false) ||
       (rc = dev_alloc(m, sizeof(float) * size_t(c.head_dim), &p)) || ((m->rope_cs = static_cast<float*>(p)), false)) {
     for (void* q : m->owned)
       if (q) (void)hipFree(q);
@@ -252,7 +254,8 @@ extern "C" int jero_hip_model_create(const jero_model_config* cfg, jero_model** 
     return rc;
   }
   if ((rc = check_hip(hipMemset(m->token, 0, sizeof(int32_t)), "state")) ||
-      (rc = check_hip(hipMemset(m->pos, 0, sizeof(int64_t)), "state"))) {
+      (rc = check_hip(hipMemset(m->pos, 0, sizeof(int64_t)), "state")) ||
+      (rc = check_hip(hipMemset(m->status, 0, sizeof(int32_t)), "state"))) {
     for (void* q : m->owned)
       if (q) (void)hipFree(q);
     delete m;
@@ -378,7 +381,20 @@ extern "C" int jero_hip_model_set_position(jero_model* m, int32_t token, int64_t
   if (token < 0 || token >= m->cfg.vocab)
     return fail(JERO_ERR_TENSOR_BOUNDS, "set_position: token " + std::to_string(token) + " outside the vocabulary");
   if (pos < 0) return fail(JERO_ERR_CONTEXT_LENGTH_EXCEEDED, "set_position: negative position");
-  return launch_set_state(m->token, m->pos, token, pos, static_cast<hipStream_t>(stream));
+  return launch_set_state(m->token, m->pos, m->status, token, pos, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int jero_hip_model_status(jero_model* m, void* stream) {
+  if (!m) return fail(JERO_ERR_INVALID_ARGUMENT, "model_status: null model");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int32_t st = 0;
+  int rc = check_hip(hipStreamSynchronize(s), "model_status sync");
+  if (rc) return rc;
+  rc = check_hip(hipMemcpy(&st, m->status, sizeof(st), hipMemcpyDeviceToHost), "model_status read");
+  if (rc) return rc;
+  if (st != 0)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "empty logits buffer after decode step (or all-NaN)");
+  return JERO_OK;
 }
 
 extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
@@ -467,5 +483,5 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
   rc = gemv(m, m->output, m->hidden, static_cast<const float*>(m->output_norm.dev), eps_ffn, kOutArgmax, m->logits, 0,
             s, &head_blocks);
   if (rc) return rc;
-  return launch_argmax_final(m->amax_v, m->amax_i, head_blocks, m->token, m->pos, s);
+  return launch_argmax_final(m->amax_v, m->amax_i, head_blocks, m->token, m->pos, m->status, s);
 }

@@ -35,8 +35,6 @@ constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 16;
 constexpr int kRouteLdsPairs = 8192;  // (token, slot) pairs grouped from LDS
 
-__device__ __forceinline__ bool better(float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); }
-
 // Routes token t in one wave (PER = expert columns per lane, E <= 64 * PER): f32 softmax over
 // all experts, top-k by (logit desc, index asc) with non-finite logits last, renormalised
 // weights -> sel_idx / sel_w (and s_sel when given).
@@ -71,7 +69,12 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, in
 #pragma unroll
   for (int i = 0; i < PER; i++) prob[i] = ok ? prob[i] / sum : 1.0f / float(E);
   // top-k rounds: the wave-wide best remaining key (DPP max), then its lowest expert index
-  // (the first column i, then the lowest lane, whose entry holds it); taken entries drop out
+  // (the first column i, then the lowest lane, whose entry holds it); taken entries drop out.
+  // Keys are compared as f32::total_cmp orders them (src/gemma.rs:417), i.e. as signed integers
+  // of the sign-folded bits, so +0.0 ranks above -0.0.
+  int tkey[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++) tkey[i] = total_order_key(key[i]);
   float ssum = 0.f;
   int my_i = 0;  // lane j keeps selection j
   float my_w = 0.f;
@@ -79,15 +82,15 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, in
 #pragma unroll
   for (int i = 0; i < PER; i++) taken[i] = !(lane + 64 * i < E);
   for (int j = 0; j < k; j++) {
-    float lb = -INFINITY;
+    int lb = int(0x80000000u);
 #pragma unroll
-    for (int i = 0; i < PER; i++) lb = taken[i] ? lb : fmaxf(lb, key[i]);
-    const float best = wave_max_dpp(lb);
+    for (int i = 0; i < PER; i++) lb = taken[i] ? lb : max(lb, tkey[i]);
+    const int best = wave_max_i32_dpp(lb);
     int bi = -1;
     float bp = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-      const uint64_t hit = __ballot(!taken[i] && key[i] == best);
+      const uint64_t hit = __ballot(!taken[i] && tkey[i] == best);
       if (bi < 0 && hit != 0) {
         const int src = __builtin_ctzll(hit);
         bi = src + 64 * i;

@@ -6,9 +6,11 @@
 // its first registration and found again by host address: registering the same range again is
 // free, and any sub-range (a slice_rows / slice_expert view) of a registered tensor maps to the
 // matching device address, so a binding can hand the GPU the view the reference's callers pass.
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "jero_common.h"
 #include "runtime.h"
@@ -111,6 +113,35 @@ extern "C" int jero_hip_weights_release_all(void) {
     } else {
       ++it;
     }
+  }
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_weights_release(const void* host, size_t nbytes) {
+  if (!host) return fail(JERO_ERR_INVALID_ARGUMENT, "weights_release: null pointer");
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(host), hi = lo + nbytes;
+  int cur = 0;
+  int rc = current_device(&cur);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lock(g_mu);
+  std::vector<int> synced;
+  for (auto it = g_regions.begin(); it != g_regions.end();) {
+    const uintptr_t s = it->first.second;
+    if (s < lo || s + it->second.nbytes > hi) {
+      ++it;
+      continue;
+    }
+    const int d = it->first.first;
+    // enqueued work on that device may still read the copy
+    if (std::find(synced.begin(), synced.end(), d) == synced.end()) {
+      if (d != cur) (void)hipSetDevice(d);
+      rc = check_hip(hipDeviceSynchronize(), "weights_release sync");
+      if (d != cur) (void)hipSetDevice(cur);
+      if (rc) return rc;
+      synced.push_back(d);
+    }
+    (void)hipFree(it->second.dev);
+    it = g_regions.erase(it);
   }
   return JERO_OK;
 }

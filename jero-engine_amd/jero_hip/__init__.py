@@ -51,6 +51,9 @@ _SIGS = {
     "jero_hip_weights_register": (_I32, [_P, _SZ, C.POINTER(_P)]),
     "jero_hip_weights_lookup": (_I32, [_P, _SZ, C.POINTER(_P)]),
     "jero_hip_weights_release_all": (_I32, []),
+    "jero_hip_weights_release": (_I32, [_P, _SZ]),
+    "jero_hip_argmax": (_I32, [_P, _I64, _P, _P, _SZ, _P]),
+    "jero_hip_model_status": (_I32, [_P, _P]),
     "jero_hip_sync": (_I32, [_P]),
     "jero_hip_gemm": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _I64, _P, _P]),
     "jero_hip_gemm_i8": (_I32, [_P, _I64, _I64, _P, _I64, _P, _P]),
@@ -201,6 +204,30 @@ def weights_lookup(host_array):
 
 def weights_release_all():
     check(lib().jero_hip_weights_release_all())
+
+
+def weights_release(host_array):
+    """Frees the device copies registered inside the host buffer's range (before it is unmapped)."""
+    check(lib().jero_hip_weights_release(host_array.ctypes.data, host_array.nbytes))
+
+
+def argmax_f32(x, out=None, workspace=None, stream=None):
+    """argmax_f32 behind sample_greedy_argmax (src/engine.rs:1873-1895) on a device f32 tensor:
+    returns a device int64 tensor of one element holding the first index of the largest non-NaN
+    value, or -1 (None) for an empty or all-NaN input."""
+    import torch
+    if out is None:
+        out = torch.empty(1, dtype=torch.int64, device=x.device)
+    ws_p = _ptr(workspace) if workspace is not None else None
+    ws_n = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    check(lib().jero_hip_argmax(_ptr(x) if x.numel() else None, x.numel(), _ptr(out), ws_p, ws_n, _stream(stream)))
+    return out
+
+
+def sample_greedy_argmax(logits, stream=None):
+    """sample_greedy_argmax (src/engine.rs:1873-1895): the token id, or None."""
+    idx = int(argmax_f32(logits, stream=stream).item())
+    return None if idx < 0 else idx
 
 
 def sync(stream=None):
@@ -445,6 +472,11 @@ class DecodeModel:
 
     def decode_step(self, stream=None):
         check(lib().jero_hip_decode_step(self.h, _stream(stream)))
+
+    def status(self, stream=None):
+        """Waits for the stream; raises K3Error CapabilityMismatch once a step found no argmax
+        (all-NaN logits), as the reference's engine fails closed (src/engine.rs:636-641)."""
+        check(lib().jero_hip_model_status(self.h, _stream(stream)))
 
     def read_logits(self, out):
         _, _, lp = self.state_ptrs()

@@ -558,9 +558,18 @@ int jo_gqa_attention(float *out, const float *q, const float *k, const float *v,
   return 0;
 }
 
+/* f32::total_cmp as a signed integer key: for a negative float every bit but the sign is
+ * flipped, so the keys order -inf < ... < -0.0 < +0.0 < ... < +inf as signed integers. */
+static int32_t jo_total_key(float f) {
+  int32_t b;
+  memcpy(&b, &f, 4);
+  return b ^ (int32_t)((uint32_t)(b >> 31) >> 1);
+}
+
 /* select_top_k_experts (src/gemma.rs:362-442): f32 softmax over all experts, stable order
- * by logit descending (non-finite logits rank as -inf) with the lower index first, take k,
- * renormalise the chosen probabilities when normalize != 0. */
+ * by logit descending under f32::total_cmp (:417; non-finite logits rank as -inf, +0.0 above
+ * -0.0) with the lower index first, take k, renormalise the chosen probabilities when
+ * normalize != 0. */
 int jo_select_top_k(const float *logits, int64_t n, int top_k, int normalize, int32_t *idx, float *w) {
   if (n <= 0 || top_k <= 0) return 0;
   float mx = -INFINITY;
@@ -587,10 +596,10 @@ int jo_select_top_k(const float *logits, int64_t n, int top_k, int normalize, in
   for (int64_t i = 0; i < n; i++) ord[i] = i;
   for (int64_t i = 1; i < n; i++) {
     int64_t cur = ord[i];
-    float lc = isfinite(logits[cur]) ? logits[cur] : -INFINITY;
+    int32_t lc = jo_total_key(isfinite(logits[cur]) ? logits[cur] : -INFINITY);
     int64_t j = i - 1;
     while (j >= 0) {
-      float lj = isfinite(logits[ord[j]]) ? logits[ord[j]] : -INFINITY;
+      int32_t lj = jo_total_key(isfinite(logits[ord[j]]) ? logits[ord[j]] : -INFINITY);
       if (lj < lc) {
         ord[j + 1] = ord[j];
         j--;

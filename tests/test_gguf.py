@@ -58,6 +58,15 @@ def test_tied_output_falls_back_to_embedding(tmp_path):
         with pytest.raises(J.K3Error) as e:
             g.tensor("output.weight")
         assert e.value.status == 14
+    # architectures without a KV cache (architecture_requires_kv_cache, src/memory.rs:863-868)
+    # get no tied head either; a name that only starts like one ("bert-like") does
+    for i, arch in enumerate(("bert", "modernbert", "deberta-v3", "ttm", "ft-transformer", "tabpfn-v2")):
+        with open_bytes(tmp_path, W.gguf_bytes(arch, [], tensors), f"e{i}.gguf") as g:
+            with pytest.raises(J.K3Error) as e:
+                g.tensor("output.weight")
+            assert e.value.status == 14, arch
+    with open_bytes(tmp_path, W.gguf_bytes("bert-like", [], tensors), "bl.gguf") as g:
+        np.testing.assert_array_equal(g.tensor_bytes("output.weight"), emb)
 
 
 def test_metadata_value_types(tmp_path):

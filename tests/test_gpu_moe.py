@@ -112,6 +112,18 @@ def test_moe_routing_ties_and_nonfinite(dev):
     run_case(dev, 2, E, 256, 256, 3, J.Q4_K, J.Q6_K, 60, logits=logits)
 
 
+def test_moe_routing_signed_zero_total_order(dev):
+    """The router ranks by f32::total_cmp (src/gemma.rs:417): +0.0 above -0.0, ties by index,
+    on both the one-token path and the many-token routing."""
+    print("moe signed zero", flush=True)
+    nz = np.float32(-0.0)
+    one = np.array([[nz, 0.0, nz, nz, 0.0, -1.0, nz, nz]], np.float32)
+    run_case(dev, 1, 8, 256, 256, 3, J.Q4_K, J.Q6_K, 62, logits=one)
+    two = np.array([[nz, 0.0, -2.0, -3.0, -4.0, -5.0, -6.0, -7.0], [0.0, nz, -2.0, -3.0, -4.0, -5.0, -6.0, -7.0]],
+                   np.float32)
+    run_case(dev, 2, 8, 256, 256, 1, J.Q4_K, J.Q6_K, 63, logits=two)
+
+
 def test_moe_argument_errors(dev):
     z = torch.zeros(4096, dtype=torch.float32, device=dev)
     G = J.TensorView("g", J.Q4_K, [256, 256, 4], torch.zeros(4 * 256 * 144, dtype=torch.uint8, device=dev))

@@ -51,3 +51,37 @@ def test_register_slice_and_release(dev):
     with pytest.raises(J.K3Error):
         J.weights_lookup(w)
     J.sync()
+
+
+def test_release_range_and_gguf_close(dev, tmp_path):
+    """jero_hip_weights_release frees the copies inside a host range; gguf_close does it for the
+    mapping, so a second file mapped at the same addresses uploads its own bytes, never the
+    first file's stale copy."""
+    import gguf_writer as W
+    a = rand_weights(J.Q4_K, 8, 512, 77)
+    b = rand_weights(J.Q4_K, 8, 512, 78)
+    assert not np.array_equal(a, b)
+    d = J.weights_register(a)
+    J.weights_release(a)
+    with pytest.raises(J.K3Error):
+        J.weights_lookup(a)
+    assert J.weights_register(a) is not None
+    J.weights_release(a)
+    paths = []
+    for i, arr in enumerate((a, b)):
+        p = tmp_path / f"m{i}.gguf"
+        p.write_bytes(W.gguf_bytes("llama", [], [("w", J.Q4_K, (512, 8), arr.tobytes())]))
+        paths.append(p)
+    assert paths[0].stat().st_size == paths[1].stat().st_size
+    for p, arr in zip(paths, (a, b)):
+        g = J.GGUFFile(str(p))
+        host = g.tensor_bytes("w")
+        dv = g.upload("w")
+        back = np.zeros(arr.nbytes, np.uint8)
+        J._memcpy(back.ctypes.data, dv, arr.nbytes)
+        np.testing.assert_array_equal(back, arr)
+        g.close()
+        with pytest.raises(J.K3Error):
+            J.weights_lookup(host)  # released with the mapping
+    J.sync()
+    del d

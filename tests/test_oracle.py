@@ -346,6 +346,17 @@ def test_select_top_k_kats():
     assert O.select_top_k(tied, 0, True) == []
 
 
+def test_select_top_k_total_order_of_signed_zero():
+    """select_top_k_experts sorts with f32::total_cmp (src/gemma.rs:417), which ranks +0.0 above
+    -0.0: [-0.0, +0.0] at k = 1 selects expert 1, its mirror expert 0; equal zeros keep index
+    order.  A comparison with `<` would tie them and take the lower index both times."""
+    nz, pz = np.float32(-0.0), np.float32(0.0)
+    assert [i for i, _ in O.select_top_k(np.array([nz, pz], np.float32), 1, True)] == [1]
+    assert [i for i, _ in O.select_top_k(np.array([pz, nz], np.float32), 1, True)] == [0]
+    mixed = np.array([nz, nz, pz, -1.0, pz, nz], np.float32)
+    assert [i for i, _ in O.select_top_k(mixed, 5, True)] == [2, 4, 0, 1, 5]
+
+
 def test_select_top_k_softmax_values_and_nonfinite():
     logits = np.array([1.0, float("nan"), 2.0, float("inf"), 0.5], np.float32)
     sel = O.select_top_k(logits, 3, False)

@@ -232,6 +232,25 @@ int jero_hip_decode_step(jero_model *model, void *stream);
  * logits buffer after decode step (or all-NaN)") once a step has failed closed. */
 int jero_hip_model_status(jero_model *model, void *stream);
 
+/* Debug trace of the decode step, for the layer-by-layer parity tests (no counterpart in the
+ * reference; the reference's intermediate vectors are locals of
+ * execute_token_standard_with_hidden, src/qwen_deepseek.rs:1239-1314).  While a buffer is set,
+ * every decode step overwrites it with its intermediate values; NULL turns tracing off.  The
+ * buffer (device, 16-byte aligned, jero_hip_model_trace_bytes bytes) holds per layer, each field
+ * starting on a 16-byte boundary, with A(n) = the larger of the Q8_K and ACT_Q8 block sizes of
+ * n elements rounded up to 16:
+ *   x_in f32[H]  xn_attn f32[H]  q8_attn u8[A(H)]  qkv f32[Q+2KV]  q_rope f32[Q]  k_rope f32[KV]
+ *   attn f32[Q]  q8_wo u8[A(Q)]  x_mid f32[H]  xn_ffn f32[H]  q8_ffn u8[A(H)]  gu f32[2F]
+ *   act f32[F]  q8_down u8[A(F)]
+ * then x_final f32[H]  xn_head f32[H]  q8_head u8[A(H)]  rope_cs f32[hd] (the step's RoPE table,
+ * (cos, sin) of pos / theta^(2i/hd) for pair i).  xn_* are the f32 values a GEMV's
+ * prologue quantized (after RMSNorm), q8_* the activation blocks it built (the format of the
+ * tensor it feeds: attn_q, attn_output, ffn_gate, ffn_down, output), qkv and gu the raw
+ * projections, q_rope / k_rope q and the new k after QK-norm and RoPE (before the softmax
+ * scale), attn the attention output, act silu(gate) * up. */
+int jero_hip_model_trace(jero_model *model, void *trace_dev, size_t trace_bytes);
+int64_t jero_hip_model_trace_bytes(const jero_model *model);
+
 /* sample_greedy_argmax -> argmax_f32 (src/engine.rs:1873-1895): the first index of the largest
  * non-NaN value of x_dev[n] into *idx_dev (int64, device), -1 when n == 0 or every value is NaN
  * (Option::None).  The same (max, first index) reduction as the decode step's LM-head epilogue.

@@ -31,6 +31,10 @@ struct AttnParams {
   const int64_t* pos_dev;  // if set: pos = *pos_dev, slot = pos % capacity, active = min(pos+1, capacity)
   const float* rope_cs;    // if set: [hd/2][cos, sin] of this step's RoPE angles
   int64_t capacity;        // ring slots (grid is sized for all of them when pos_dev is set)
+  // fused mode debug trace (null: off): q [nq][hd] and the new k [nkv][hd] after QK-norm and
+  // RoPE, before the softmax scale
+  float* tr_q;
+  float* tr_k;
 };
 
 int attn_splits(int active, int hd);

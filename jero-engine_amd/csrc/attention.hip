@@ -220,6 +220,20 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
 #pragma unroll
     for (int j = 0; j < HPW; j++) norm_rope_chunk<HD, EPL>(qw[j], p.q_norm != nullptr, qnw, p.eps, cs);
     if (slot >= p0 && slot < p1) norm_rope_chunk<HD, EPL>(kn, p.k_norm != nullptr, knw, p.eps, cs);
+    if (p.tr_q != nullptr && kp == 0) {  // debug trace
+      if (split == 0) {
+#pragma unroll
+        for (int j = 0; j < HPW; j++) {
+          const int h = wv + NW * j;
+          if (h < group)
+#pragma unroll
+            for (int e = 0; e < EPL; e++) p.tr_q[(int64_t(kh) * group + h) * HD + kc * EPL + e] = qw[j][e];
+        }
+      }
+      if (wv == 0 && slot >= p0 && slot < p1)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) p.tr_k[int64_t(kh) * HD + kc * EPL + e] = kn[e];
+    }
   }
   float q[MAXG][EPL];
   if constexpr (FUSED) {

@@ -32,6 +32,11 @@ struct DGemvArgs {
   const uint8_t* w2;
   int64_t rb2;
   int64_t N2;
+  // debug trace (null: off), written by workgroup 0: the f32 values the prologue quantized
+  // (after RMSNorm), the activation blocks it built, and the raw gate|up outputs of SwiGLU
+  float* tr_xn;
+  uint8_t* tr_q8;
+  float* tr_gu;
 };
 
 // Enqueues the fused GEMV; *blocks (if given) receives the workgroups launched, which is the

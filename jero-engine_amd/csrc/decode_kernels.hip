@@ -84,9 +84,11 @@ __device__ __forceinline__ void pin_x(XRegs<ACT, XB, NORM>& X) {
   }
 }
 
-// Builds the activation blocks of x (or of rmsnorm(x) * nw) in LDS from the registers.
+// Builds the activation blocks of x (or of rmsnorm(x) * nw) in LDS from the registers; tr_xn
+// (debug trace, or null) receives the f32 values that are quantized.
 template <int ACT, int XB, bool NORM>
-__device__ void build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps, int K, uint8_t* s_act, float* s_tmp) {
+__device__ void build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps, int K, uint8_t* s_act, float* s_tmp,
+                              float* tr_xn) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
   float scale = 1.0f;
   if (has_norm) {
@@ -117,6 +119,7 @@ __device__ void build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps,
             e[3] = e[3] * scale * X.g[i].w;
           }
         }
+        if (tr_xn) reinterpret_cast<float4*>(tr_xn + b * 256)[lane] = make_float4(e[0], e[1], e[2], e[3]);
         q8k_block_wave(e, lane, s_act + b * 292);
       }
     } else {
@@ -127,6 +130,7 @@ __device__ void build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps,
         if constexpr (NORM) {
           if (has_norm) v = v * scale * X.g[i].x;
         }
+        if (tr_xn) tr_xn[b * 32 + l] = v;
         float a = fabsf(v);
 #pragma unroll
         for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, kWave));
@@ -139,6 +143,12 @@ __device__ void build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps,
     }
   }
   lds_barrier();
+}
+
+// Debug trace: the workgroup copies the activation blocks it built in LDS to global memory.
+__device__ __forceinline__ void trace_act(uint8_t* dst, const uint8_t* s_act, int bytes) {
+  for (int i = threadIdx.x; i < bytes / 4; i += blockDim.x)
+    reinterpret_cast<uint32_t*>(dst)[i] = reinterpret_cast<const uint32_t*>(s_act)[i];
 }
 
 // ---------------------------------------------------------------- fused GEMV
@@ -218,7 +228,10 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
   load_rows(wave0, wa, ya);
   pin_x(X);
   // 2. activation blocks in LDS (every thread takes part)
-  build_act_lds<ACT, XB, NORM>(X, NORM && a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp);
+  const bool tracing = blockIdx.x == 0 && a.tr_q8 != nullptr;
+  build_act_lds<ACT, XB, NORM>(X, NORM && a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp,
+                               tracing ? a.tr_xn : nullptr);
+  if (tracing) trace_act(a.tr_q8, s_act, int(ACT == JERO_Q8_K ? a.K / 256 * 292 : a.K / 32 * 36));
   // The activation units stay in registers for all rows (re-reading them from LDS per row, to
   // fit two workgroups per CU on long rows, measured slower).
   typename Ut::Act act[UPL];
@@ -246,11 +259,23 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
         if constexpr (G == 1) {
           if ((r & 1) && last && row_valid(rg, r)) {
             const float gv = vals[r - 1], uv = vals[r];
-            a.y[row_of(rg, r) - a.half] = gv / (1.0f + expf(-gv)) * uv;
+            const int64_t f = row_of(rg, r) - a.half;
+            a.y[f] = gv / (1.0f + expf(-gv)) * uv;
+            if (a.tr_gu) {
+              a.tr_gu[f] = gv;
+              a.tr_gu[a.half + f] = uv;
+            }
           }
         } else {
           const float gv = __shfl(vals[r], lane - LPR, kWave);
-          if ((g & 1) && last && row_valid(rg, r)) a.y[row_of(rg, r) - a.half] = gv / (1.0f + expf(-gv)) * vals[r];
+          if ((g & 1) && last && row_valid(rg, r)) {
+            const int64_t f = row_of(rg, r) - a.half;
+            a.y[f] = gv / (1.0f + expf(-gv)) * vals[r];
+            if (a.tr_gu) {
+              a.tr_gu[f] = gv;
+              a.tr_gu[a.half + f] = vals[r];
+            }
+          }
         }
       }
     } else {
@@ -391,7 +416,9 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_dual_kernel(DGemvArgs a)
   typename Unit<F2>::W c2[UPL];
   load_row_units<F1, UPL>(a.w, a.rb, a.U, N1, r1, c1);
   pin_x(X);
-  build_act_lds<JERO_Q8_K, XB, true>(X, a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp);
+  const bool tracing = blockIdx.x == 0 && a.tr_q8 != nullptr;
+  build_act_lds<JERO_Q8_K, XB, true>(X, a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp, tracing ? a.tr_xn : nullptr);
+  if (tracing) trace_act(a.tr_q8, s_act, a.K / 256 * 292);
   store_segment<F1, UPL>(a.w, a.rb, a.U, N1, r1, stride, s_act, a.y, c1);
   if (r2 + N1 < total) {
     load_row_units<F2, UPL>(a.w2, a.rb2, a.U, a.N2, r2, c2);

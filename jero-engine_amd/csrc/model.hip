@@ -60,6 +60,7 @@ struct jero_model {
   void* kv = nullptr;
   size_t kv_bytes = 0;
   std::vector<void*> owned;
+  uint8_t* trace = nullptr;  // debug trace buffer of the caller (jero_hip_model_trace), or null
 };
 
 namespace jero {
@@ -190,8 +191,47 @@ static int repack_planar(jero_model* m, DevTensor& t) {
 
 constexpr int kArgmaxSlots = 4096;
 
+// Byte offsets of the debug trace of one decode step (the layout include/jero_hip.h documents):
+// per layer the fields below in this order, each starting on a 16-byte boundary, then the
+// head's fields.  act_bytes(n) is the larger of the Q8_K and ACT_Q8 block sizes of n elements.
+struct TraceLayout {
+  enum { kXIn, kXnAttn, kQ8Attn, kQkv, kQRope, kKRope, kAttn, kQ8Wo, kXMid, kXnFfn, kQ8Ffn, kGu, kAct, kQ8Down, kFields };
+  size_t field[kFields];
+  size_t layer_bytes, x_final, xn_head, q8_head, rope_cs, total;
+};
+
+static size_t round16(size_t n) { return (n + 15) & ~size_t(15); }
+static size_t trace_act_bytes(int64_t n) {
+  const size_t a = size_t(n / 32) * 36, b = n % 256 == 0 ? size_t(n / 256) * 292 : 0;
+  return round16(a > b ? a : b);
+}
+
+static TraceLayout trace_layout(const jero_model_config& c) {
+  const int64_t H = c.hidden, F = c.ffn, Q = q_dim(c), KV = kv_dim(c);
+  const size_t sizes[TraceLayout::kFields] = {
+      round16(4 * size_t(H)),  round16(4 * size_t(H)), trace_act_bytes(H),     round16(4 * size_t(Q + 2 * KV)),
+      round16(4 * size_t(Q)),  round16(4 * size_t(KV)), round16(4 * size_t(Q)), trace_act_bytes(Q),
+      round16(4 * size_t(H)),  round16(4 * size_t(H)), trace_act_bytes(H),     round16(8 * size_t(F)),
+      round16(4 * size_t(F)),  trace_act_bytes(F)};
+  TraceLayout t{};
+  size_t off = 0;
+  for (int i = 0; i < TraceLayout::kFields; i++) {
+    t.field[i] = off;
+    off += sizes[i];
+  }
+  t.layer_bytes = off;
+  const size_t tail = t.layer_bytes * size_t(c.n_layers);
+  t.x_final = tail;
+  t.xn_head = tail + round16(4 * size_t(H));
+  t.q8_head = t.xn_head + round16(4 * size_t(H));
+  t.rope_cs = t.q8_head + trace_act_bytes(H);
+  t.total = t.rope_cs + round16(4 * size_t(c.head_dim));
+  return t;
+}
+
 static int gemv(jero_model* m, const DevTensor& w, const float* x, const float* norm, float eps, int out_mode,
-                float* y, int64_t half, hipStream_t s, int* blocks = nullptr) {
+                float* y, int64_t half, hipStream_t s, int* blocks = nullptr, float* tr_xn = nullptr,
+                uint8_t* tr_q8 = nullptr, float* tr_gu = nullptr) {
   DGemvArgs a{};
   a.w = static_cast<const uint8_t*>(w.dev);
   a.rb = row_bytes(w.quant, w.n_in);
@@ -206,6 +246,9 @@ static int gemv(jero_model* m, const DevTensor& w, const float* x, const float* 
   a.amax_v = m->amax_v;
   a.amax_i = m->amax_i;
   a.max_blocks = kArgmaxSlots;  // one argmax partial slot per workgroup
+  a.tr_xn = tr_xn;
+  a.tr_q8 = tr_q8;
+  a.tr_gu = tr_gu;
   return launch_dgemv(w.quant, out_mode, a, s, blocks);
 }
 
@@ -384,6 +427,26 @@ extern "C" int jero_hip_model_set_position(jero_model* m, int32_t token, int64_t
   return launch_set_state(m->token, m->pos, m->status, token, pos, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int64_t jero_hip_model_trace_bytes(const jero_model* m) {
+  return m ? int64_t(trace_layout(m->cfg).total) : -1;
+}
+
+extern "C" int jero_hip_model_trace(jero_model* m, void* trace_dev, size_t trace_bytes) {
+  if (!m) return fail(JERO_ERR_INVALID_ARGUMENT, "model_trace: null model");
+  if (!trace_dev) {
+    m->trace = nullptr;
+    return JERO_OK;
+  }
+  const size_t need = trace_layout(m->cfg).total;
+  if (trace_bytes < need)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "model_trace: buffer of " + std::to_string(trace_bytes) + " bytes, need " +
+                                            std::to_string(need));
+  if (reinterpret_cast<uintptr_t>(trace_dev) & 15u)
+    return fail(JERO_ERR_INVALID_ARGUMENT, "model_trace: buffer must be 16-byte aligned");
+  m->trace = static_cast<uint8_t*>(trace_dev);
+  return JERO_OK;
+}
+
 extern "C" int jero_hip_model_status(jero_model* m, void* stream) {
   if (!m) return fail(JERO_ERR_INVALID_ARGUMENT, "model_status: null model");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -410,8 +473,20 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
   if (rc) return rc;
   const size_t es = c.kv_dtype == JERO_KV_F16 ? 2 : 4;
   const size_t ring = size_t(c.kv_capacity) * size_t(KV) * es;
+  const TraceLayout tl = trace_layout(c);
+  // debug trace: field f of layer L (null when tracing is off)
+  auto tr = [&](int64_t L, int f) -> uint8_t* {
+    return m->trace ? m->trace + size_t(L) * tl.layer_bytes + tl.field[f] : nullptr;
+  };
+  auto trf = [&](int64_t L, int f) -> float* { return reinterpret_cast<float*>(tr(L, f)); };
+  auto snap = [&](uint8_t* dst, const void* src, size_t bytes) -> int {
+    if (!dst) return JERO_OK;
+    return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s), "decode trace copy");
+  };
+  if (m->trace && (rc = snap(m->trace + tl.rope_cs, m->rope_cs, 4 * size_t(c.head_dim)))) return rc;
   for (int64_t L = 0; L < c.n_layers; L++) {
     const LayerW& l = m->layers[size_t(L)];
+    if ((rc = snap(tr(L, TraceLayout::kXIn), m->hidden, 4 * size_t(c.hidden)))) return rc;
     // attention sublayer: RMSNorm -> Q|K|V
     const bool dual = l.v_separate && l.qkv.n_in <= 4096 &&
                       ((l.qkv.quant == JERO_Q4_K_R && l.wv.quant == JERO_Q6_K_R) ||
@@ -430,10 +505,13 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
       a.eps = eps_attn;
       a.K = int(l.qkv.n_in);
       a.y = m->qkv;
+      a.tr_xn = trf(L, TraceLayout::kXnAttn);
+      a.tr_q8 = tr(L, TraceLayout::kQ8Attn);
       rc = launch_dgemv_dual(l.qkv.quant, l.wv.quant, a, s);
       if (rc) return rc;
     } else {
-      rc = gemv(m, l.qkv, m->hidden, static_cast<const float*>(l.attn_norm.dev), eps_attn, kOutStore, m->qkv, 0, s);
+      rc = gemv(m, l.qkv, m->hidden, static_cast<const float*>(l.attn_norm.dev), eps_attn, kOutStore, m->qkv, 0, s,
+                nullptr, trf(L, TraceLayout::kXnAttn), tr(L, TraceLayout::kQ8Attn));
       if (rc) return rc;
       if (l.v_separate) {
         rc = gemv(m, l.wv, m->hidden, static_cast<const float*>(l.attn_norm.dev), eps_attn, kOutStore,
@@ -466,22 +544,33 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
     p.pos_dev = m->pos;
     p.rope_cs = m->rope_cs;
     p.capacity = c.kv_capacity;
+    p.tr_q = trf(L, TraceLayout::kQRope);
+    p.tr_k = trf(L, TraceLayout::kKRope);
+    if ((rc = snap(tr(L, TraceLayout::kQkv), m->qkv, 4 * size_t(Q + 2 * KV)))) return rc;
     rc = launch_attention(p, true, m->attn, s);
     if (rc) return rc;
+    if ((rc = snap(tr(L, TraceLayout::kAttn), m->attn, 4 * size_t(Q)))) return rc;
     // output projection + residual
-    rc = gemv(m, l.wo, m->attn, nullptr, 0.f, kOutResid, m->hidden, 0, s);
+    rc = gemv(m, l.wo, m->attn, nullptr, 0.f, kOutResid, m->hidden, 0, s, nullptr, nullptr,
+              tr(L, TraceLayout::kQ8Wo));
     if (rc) return rc;
+    if ((rc = snap(tr(L, TraceLayout::kXMid), m->hidden, 4 * size_t(c.hidden)))) return rc;
     // FFN: RMSNorm -> gate|up -> SwiGLU -> down + residual
     rc = gemv(m, l.gate_up, m->hidden, static_cast<const float*>(l.ffn_norm.dev), eps_ffn, kOutSwiglu, m->act,
-              c.ffn, s);
+              c.ffn, s, nullptr, trf(L, TraceLayout::kXnFfn), tr(L, TraceLayout::kQ8Ffn), trf(L, TraceLayout::kGu));
     if (rc) return rc;
-    rc = gemv(m, l.down, m->act, nullptr, 0.f, kOutResid, m->hidden, 0, s);
+    if ((rc = snap(tr(L, TraceLayout::kAct), m->act, 4 * size_t(c.ffn)))) return rc;
+    rc = gemv(m, l.down, m->act, nullptr, 0.f, kOutResid, m->hidden, 0, s, nullptr, nullptr,
+              tr(L, TraceLayout::kQ8Down));
     if (rc) return rc;
   }
   // final norm -> LM head -> greedy token
   int head_blocks = 0;
+  uint8_t* tr_tail = m->trace;
+  if (tr_tail && (rc = snap(tr_tail + tl.x_final, m->hidden, 4 * size_t(c.hidden)))) return rc;
   rc = gemv(m, m->output, m->hidden, static_cast<const float*>(m->output_norm.dev), eps_ffn, kOutArgmax, m->logits, 0,
-            s, &head_blocks);
+            s, &head_blocks, tr_tail ? reinterpret_cast<float*>(tr_tail + tl.xn_head) : nullptr,
+            tr_tail ? tr_tail + tl.q8_head : nullptr);
   if (rc) return rc;
   return launch_argmax_final(m->amax_v, m->amax_i, head_blocks, m->token, m->pos, m->status, s);
 }

@@ -54,6 +54,8 @@ _SIGS = {
     "jero_hip_weights_release": (_I32, [_P, _SZ]),
     "jero_hip_argmax": (_I32, [_P, _I64, _P, _P, _SZ, _P]),
     "jero_hip_model_status": (_I32, [_P, _P]),
+    "jero_hip_model_trace": (_I32, [_P, _P, _SZ]),
+    "jero_hip_model_trace_bytes": (_I64, [_P]),
     "jero_hip_sync": (_I32, [_P]),
     "jero_hip_gemm": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _I64, _P, _P]),
     "jero_hip_gemm_i8": (_I32, [_P, _I64, _I64, _P, _I64, _P, _P]),
@@ -472,6 +474,53 @@ class DecodeModel:
 
     def decode_step(self, stream=None):
         check(lib().jero_hip_decode_step(self.h, _stream(stream)))
+
+    TRACE_FIELDS = ("x_in", "xn_attn", "q8_attn", "qkv", "q_rope", "k_rope", "attn", "q8_wo", "x_mid", "xn_ffn",
+                    "q8_ffn", "gu", "act", "q8_down")
+
+    def trace_layout(self):
+        """{field: (byte offset in a layer record, numpy dtype, count)}, the layer record size
+        and the head fields' offsets, as jero_hip_model_trace documents them."""
+        import numpy as np
+        c = self.cfg
+        H, F, Q, KV = c.hidden, c.ffn, c.n_heads_q * c.head_dim, c.n_heads_kv * c.head_dim
+        r16 = lambda n: (n + 15) // 16 * 16
+        A = lambda n: r16(max(n // 32 * 36, n // 256 * 292 if n % 256 == 0 else 0))
+        f4, u8 = np.float32, np.uint8
+        spec = [(f4, H), (f4, H), (u8, A(H)), (f4, Q + 2 * KV), (f4, Q), (f4, KV), (f4, Q), (u8, A(Q)), (f4, H),
+                (f4, H), (u8, A(H)), (f4, 2 * F), (f4, F), (u8, A(F))]
+        out, off = {}, 0
+        for name, (dt, n) in zip(self.TRACE_FIELDS, spec):
+            nb = r16(n * np.dtype(dt).itemsize)
+            out[name] = (off, dt, n if dt is f4 else nb)
+            off += nb
+        tail = off * c.n_layers
+        head = {"x_final": (tail, f4, H), "xn_head": (tail + r16(4 * H), f4, H),
+                "q8_head": (tail + 2 * r16(4 * H), u8, A(H)), "rope_cs": (tail + 2 * r16(4 * H) + A(H), f4, c.head_dim)}
+        total = tail + 2 * r16(4 * H) + A(H) + r16(4 * c.head_dim)
+        assert total == lib().jero_hip_model_trace_bytes(self.h), "trace layout disagrees with the library"
+        return out, off, head, total
+
+    def set_trace(self, buf):
+        """Records every later decode step's intermediate values into the uint8 device tensor
+        `buf` (None: off)."""
+        if buf is None:
+            check(lib().jero_hip_model_trace(self.h, None, 0))
+        else:
+            check(lib().jero_hip_model_trace(self.h, _ptr(buf), buf.numel()))
+
+    def read_trace(self, buf):
+        """The trace in `buf` as ([per-layer dict of numpy arrays], head dict)."""
+        import numpy as np
+        fields, layer_bytes, head, total = self.trace_layout()
+        raw = buf[:total].cpu().numpy()
+
+        def view(off, dt, n):
+            return raw[off:off + n * np.dtype(dt).itemsize].view(dt).copy()
+
+        layers = [{k: view(L * layer_bytes + o, dt, n) for k, (o, dt, n) in fields.items()}
+                  for L in range(self.cfg.n_layers)]
+        return layers, {k: view(o, dt, n) for k, (o, dt, n) in head.items()}
 
     def status(self, stream=None):
         """Waits for the stream; raises K3Error CapabilityMismatch once a step found no argmax

@@ -730,57 +730,106 @@ static void jo_head_rmsnorm(float *x, int64_t len, int hd, const float *w, float
   free(tmp);
 }
 
-int jo_decode_step(const jo_model *M, float *kv, int32_t token, int64_t pos, float *logits, int threads) {
-  int64_t H = M->hidden, F = M->ffn, qd = (int64_t)M->nq * M->hd, kvd = (int64_t)M->nkv * M->hd;
-  int64_t cap = M->kv_capacity;
-  if (token < 0 || token >= M->vocab || cap <= 0) return -1;
-  float *x = (float *)malloc((size_t)H * 4), *xn = (float *)malloc((size_t)H * 4);
-  float *q = (float *)malloc((size_t)qd * 4), *k = (float *)malloc((size_t)kvd * 4);
-  float *v = (float *)malloc((size_t)kvd * 4), *att = (float *)malloc((size_t)qd * 4);
-  float *proj = (float *)malloc((size_t)H * 4), *g = (float *)malloc((size_t)F * 4);
-  float *u = (float *)malloc((size_t)F * 4), *a = (float *)malloc((size_t)F * 4);
-  int rc = 0;
-  if (!x || !xn || !q || !k || !v || !att || !proj || !g || !u || !a) rc = -1;
-  if (!rc) rc = jo_dequantize_row(M->tok_embd.quant, (const uint8_t *)M->tok_embd.data +
-                                                         token * jo_row_bytes(M->tok_embd.quant, H),
-                                  H, x);
-  for (int64_t L = 0; L < M->n_layers && !rc; L++) {
-    const jo_layer *ly = &M->layers[L];
-    jo_rmsnorm(xn, x, ly->attn_norm, H, M->eps);
-    rc |= jo_vec_dot(ly->wq.quant, ly->wq.data, H, qd, xn, q, threads);
-    rc |= jo_vec_dot(ly->wk.quant, ly->wk.data, H, kvd, xn, k, threads);
-    rc |= jo_vec_dot(ly->wv.quant, ly->wv.data, H, kvd, xn, v, threads);
-    if (ly->q_norm) jo_head_rmsnorm(q, qd, M->hd, ly->q_norm, M->eps);
-    if (ly->k_norm) jo_head_rmsnorm(k, kvd, M->hd, ly->k_norm, M->eps);
+/* y = W . x for an f32 x: x quantized to W's activation format (written to q8 when given),
+ * then jo_matvec. */
+static int jo_matvec_q(int quant, const void *w, int64_t k, int64_t n, const float *x, float *y, int threads,
+                       void *q8) {
+  int act = jo_act_format(quant);
+  int64_t qb = jo_row_bytes(act, k);
+  if (act < 0 || qb < 0) return -1;
+  void *xq = malloc((size_t)qb);
+  if (!xq) return -1;
+  jo_quantize_act(act, x, 1, k, xq);
+  if (q8) memcpy(q8, xq, (size_t)qb);
+  int rc = jo_matvec(quant, w, k, n, xq, y, threads);
+  free(xq);
+  return rc;
+}
+
+int jo_decode_layer(const jo_model *M, float *kv, int64_t L, float *x, int64_t pos, int threads,
+                    const jo_layer_trace *tr) {
+  const int64_t H = M->hidden, F = M->ffn, qd = (int64_t)M->nq * M->hd, kvd = (int64_t)M->nkv * M->hd;
+  const int64_t cap = M->kv_capacity;
+  /* the attention sublayer and QK-norm use rms_eps as given; the FFN norm rms_eps.max(1e-6) (:1251) */
+  const float eps_attn = M->eps, eps_ffn = M->eps > 1e-6f ? M->eps : 1e-6f;
+  static const jo_layer_trace none;
+  if (!tr) tr = &none;
+  if (L < 0 || L >= M->n_layers || cap <= 0 || pos < 0) return -1;
+  const jo_layer *ly = &M->layers[L];
+  float *xn = (float *)malloc((size_t)H * 4), *qkv = (float *)malloc((size_t)(qd + 2 * kvd) * 4);
+  float *att = (float *)malloc((size_t)qd * 4), *proj = (float *)malloc((size_t)H * 4);
+  float *gu = (float *)malloc((size_t)F * 8), *a = (float *)malloc((size_t)F * 4);
+  int rc = (!xn || !qkv || !att || !proj || !gu || !a) ? -1 : 0;
+  float *q = qkv, *k = qkv + qd, *v = qkv + qd + kvd;
+  if (!rc) {
+    jo_rmsnorm(xn, x, ly->attn_norm, H, eps_attn);
+    if (tr->xn_attn) memcpy(tr->xn_attn, xn, (size_t)H * 4);
+    rc |= jo_matvec_q(ly->wq.quant, ly->wq.data, H, qd, xn, q, threads, tr->q8_attn);
+    rc |= jo_matvec_q(ly->wk.quant, ly->wk.data, H, kvd, xn, k, threads, NULL);
+    rc |= jo_matvec_q(ly->wv.quant, ly->wv.data, H, kvd, xn, v, threads, NULL);
+  }
+  if (!rc) {
+    if (tr->qkv) memcpy(tr->qkv, qkv, (size_t)(qd + 2 * kvd) * 4);
+    /* QK-norm before RoPE (:1039-1071) */
+    if (ly->q_norm) jo_head_rmsnorm(q, qd, M->hd, ly->q_norm, eps_attn);
+    if (ly->k_norm) jo_head_rmsnorm(k, kvd, M->hd, ly->k_norm, eps_attn);
     jo_rope_inplace(q, qd, M->hd, pos, M->theta);
     jo_rope_inplace(k, kvd, M->hd, pos, M->theta);
+    if (tr->q_rope) memcpy(tr->q_rope, q, (size_t)qd * 4);
+    if (tr->k_rope) memcpy(tr->k_rope, k, (size_t)kvd * 4);
     float *kring = kv + L * 2 * cap * kvd, *vring = kring + cap * kvd;
     int64_t slot = pos % cap, active = pos + 1 < cap ? pos + 1 : cap;
     memcpy(kring + slot * kvd, k, (size_t)kvd * 4);
     memcpy(vring + slot * kvd, v, (size_t)kvd * 4);
     rc |= jo_gqa_attention(att, q, kring, vring, M->nq, M->nkv, M->hd, active, 1.0f / sqrtf((float)M->hd));
-    rc |= jo_vec_dot(ly->wo.quant, ly->wo.data, qd, H, att, proj, threads);
-    for (int64_t i = 0; i < H; i++) x[i] += proj[i];
-    jo_rmsnorm(xn, x, ly->ffn_norm, H, M->eps);
-    rc |= jo_vec_dot(ly->w_gate.quant, ly->w_gate.data, H, F, xn, g, threads);
-    rc |= jo_vec_dot(ly->w_up.quant, ly->w_up.data, H, F, xn, u, threads);
-    jo_swiglu(a, g, u, F);
-    rc |= jo_vec_dot(ly->w_down.quant, ly->w_down.data, F, H, a, proj, threads);
-    for (int64_t i = 0; i < H; i++) x[i] += proj[i];
   }
   if (!rc) {
-    jo_rmsnorm(xn, x, M->output_norm, H, M->eps);
-    rc = jo_vec_dot(M->output.quant, M->output.data, H, M->vocab, xn, logits, threads);
+    if (tr->attn) memcpy(tr->attn, att, (size_t)qd * 4);
+    rc |= jo_matvec_q(ly->wo.quant, ly->wo.data, qd, H, att, proj, threads, tr->q8_wo);
+    for (int64_t i = 0; i < H; i++) x[i] += proj[i];
+    if (tr->x_mid) memcpy(tr->x_mid, x, (size_t)H * 4);
+    jo_rmsnorm(xn, x, ly->ffn_norm, H, eps_ffn);
+    if (tr->xn_ffn) memcpy(tr->xn_ffn, xn, (size_t)H * 4);
+    rc |= jo_matvec_q(ly->w_gate.quant, ly->w_gate.data, H, F, xn, gu, threads, tr->q8_ffn);
+    rc |= jo_matvec_q(ly->w_up.quant, ly->w_up.data, H, F, xn, gu + F, threads, NULL);
   }
-  free(x);
+  if (!rc) {
+    if (tr->gu) memcpy(tr->gu, gu, (size_t)F * 8);
+    jo_swiglu(a, gu, gu + F, F);
+    if (tr->act) memcpy(tr->act, a, (size_t)F * 4);
+    rc |= jo_matvec_q(ly->w_down.quant, ly->w_down.data, F, H, a, proj, threads, tr->q8_down);
+    for (int64_t i = 0; i < H; i++) x[i] += proj[i];
+  }
   free(xn);
-  free(q);
-  free(k);
-  free(v);
+  free(qkv);
   free(att);
   free(proj);
-  free(g);
-  free(u);
+  free(gu);
   free(a);
+  return rc;
+}
+
+int jo_decode_head(const jo_model *M, const float *x, float *logits, int threads, float *xn_head, void *q8_head) {
+  const int64_t H = M->hidden;
+  const float eps = M->eps > 1e-6f ? M->eps : 1e-6f; /* :1305-1306 */
+  float *xn = (float *)malloc((size_t)H * 4);
+  if (!xn) return -1;
+  jo_rmsnorm(xn, x, M->output_norm, H, eps);
+  if (xn_head) memcpy(xn_head, xn, (size_t)H * 4);
+  int rc = jo_matvec_q(M->output.quant, M->output.data, H, M->vocab, xn, logits, threads, q8_head);
+  free(xn);
+  return rc;
+}
+
+int jo_decode_step(const jo_model *M, float *kv, int32_t token, int64_t pos, float *logits, int threads) {
+  const int64_t H = M->hidden;
+  if (token < 0 || token >= M->vocab || M->kv_capacity <= 0) return -1;
+  float *x = (float *)malloc((size_t)H * 4);
+  if (!x) return -1;
+  int rc = jo_dequantize_row(M->tok_embd.quant,
+                             (const uint8_t *)M->tok_embd.data + token * jo_row_bytes(M->tok_embd.quant, H), H, x);
+  for (int64_t L = 0; L < M->n_layers && !rc; L++) rc = jo_decode_layer(M, kv, L, x, pos, threads, NULL);
+  if (!rc) rc = jo_decode_head(M, x, logits, threads, NULL, NULL);
+  free(x);
   return rc;
 }

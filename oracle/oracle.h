@@ -143,6 +143,35 @@ typedef struct jo_model {
   const jo_layer *layers;
 } jo_model;
 
+/* Intermediate values of one layer of the decode step (every pointer optional):
+ *   xn_attn  rmsnorm(x) * attn_norm, the f32 input of the Q|K|V projections [hidden]
+ *   q8_attn  its activation blocks in attn_q's activation format (Q8_K or ACT_Q8)
+ *   qkv      the raw projections q | k | v [q_dim + 2 kv_dim]
+ *   q_rope, k_rope   q and k after QK-norm and RoPE [q_dim], [kv_dim]
+ *   attn     the attention output [q_dim];  q8_wo its activation blocks (attn_output's format)
+ *   x_mid    the hidden state after the attention residual [hidden]
+ *   xn_ffn, q8_ffn   the FFN input after RMSNorm and its activation blocks (ffn_gate's format)
+ *   gu       the raw gate | up projections [2 ffn];  act  silu(gate) * up [ffn]
+ *   q8_down  act's activation blocks (ffn_down's format) */
+typedef struct jo_layer_trace {
+  float *xn_attn;
+  void *q8_attn;
+  float *qkv, *q_rope, *k_rope, *attn;
+  void *q8_wo;
+  float *x_mid, *xn_ffn;
+  void *q8_ffn;
+  float *gu, *act;
+  void *q8_down;
+} jo_layer_trace;
+
+/* Layer L of execute_token_standard_with_hidden (src/qwen_deepseek.rs:1262-1302, with
+ * run_dense_attention_sublayer_scaled :984-1097 and run_dense_swiglu_ffn :696-727): x [hidden]
+ * in, the layer's output out (in place); writes K/V of `pos` into layer L's rings of kv. */
+int jo_decode_layer(const jo_model *mdl, float *kv, int64_t layer, float *x, int64_t pos, int threads,
+                    const jo_layer_trace *tr);
+/* Final RMSNorm and LM head (:1305-1312): logits [vocab] from the last hidden state; xn_head /
+ * q8_head (optional) receive the normalised input and its activation blocks. */
+int jo_decode_head(const jo_model *mdl, const float *x, float *logits, int threads, float *xn_head, void *q8_head);
 /* kv: f32 [n_layers][2][kv_capacity][nkv*hd].  logits [vocab]. */
 int jo_decode_step(const jo_model *mdl, float *kv, int32_t token, int64_t pos, float *logits,
                    int threads);

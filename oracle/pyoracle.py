@@ -52,6 +52,8 @@ def lib():
             "jo_swiglu_expert": (I32, [I32, P, I32, P, I32, P, I64, I64, P, P]),
             "jo_moe_ffn": (I32, [P, I64, I64, I32, I32, P, I32, P, I32, P, I64, I64, P, P, P, P, I32]),
             "jo_decode_step": (I32, [P, P, I32, I64, P, I32]),
+            "jo_decode_layer": (I32, [P, P, I64, P, I64, I32, P]),
+            "jo_decode_head": (I32, [P, P, P, I32, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -216,6 +218,15 @@ class JoModel(C.Structure):
                 ("output_norm", C.c_void_p), ("layers", C.c_void_p)]
 
 
+class JoLayerTrace(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("xn_attn", "q8_attn", "qkv", "q_rope", "k_rope", "attn", "q8_wo", "x_mid",
+                                          "xn_ffn", "q8_ffn", "gu", "act", "q8_down")]
+
+
+def act_row_bytes(weight_quant, k):
+    return row_bytes(lib().jo_act_format(weight_quant), k)
+
+
 class DecodeModel:
     """Holds a jo_model over numpy-owned tensors (see tests/model_spec.py for the dict layout)."""
 
@@ -260,3 +271,44 @@ class DecodeModel:
         rc = lib().jo_decode_step(C.byref(self.model), _p(kv), token, pos, _p(logits), threads)
         assert rc == 0
         return logits
+
+    def embed(self, token):
+        H = self.spec["hidden"]
+        q = self.model.tok_embd.quant
+        rb = row_bytes(q, H)
+        raw = (C.c_uint8 * rb).from_address(self.model.tok_embd.data + token * rb)
+        return dequantize(q, np.frombuffer(raw, np.uint8), 1, H)[0]
+
+    def layer(self, kv, L, x, pos, threads=1, trace=True):
+        """jo_decode_layer: returns (x_out, trace dict of the layer's intermediate values)."""
+        s = self.spec
+        H, F = s["hidden"], s["ffn"]
+        qd, kvd = s["nq"] * s["hd"], s["nkv"] * s["hd"]
+        ly = self.layers[L]
+        x = np.array(x, np.float32, copy=True)
+        tr = None
+        out = {}
+        if trace:
+            out = dict(xn_attn=np.empty(H, np.float32), q8_attn=np.empty(act_row_bytes(ly.wq.quant, H), np.uint8),
+                       qkv=np.empty(qd + 2 * kvd, np.float32), q_rope=np.empty(qd, np.float32),
+                       k_rope=np.empty(kvd, np.float32), attn=np.empty(qd, np.float32),
+                       q8_wo=np.empty(act_row_bytes(ly.wo.quant, qd), np.uint8), x_mid=np.empty(H, np.float32),
+                       xn_ffn=np.empty(H, np.float32), q8_ffn=np.empty(act_row_bytes(ly.w_gate.quant, H), np.uint8),
+                       gu=np.empty(2 * F, np.float32), act=np.empty(F, np.float32),
+                       q8_down=np.empty(act_row_bytes(ly.w_down.quant, F), np.uint8))
+            tr = JoLayerTrace(*[out[n].ctypes.data for n, _ in JoLayerTrace._fields_])
+        rc = lib().jo_decode_layer(C.byref(self.model), _p(kv), L, _p(x), pos, threads,
+                                   C.byref(tr) if tr is not None else None)
+        assert rc == 0
+        return x, out
+
+    def head(self, x, threads=1):
+        """jo_decode_head: (logits, xn_head, q8_head)."""
+        s = self.spec
+        x = np.ascontiguousarray(x, np.float32)
+        logits = np.empty(s["vocab"], np.float32)
+        xn = np.empty(s["hidden"], np.float32)
+        q8 = np.empty(act_row_bytes(self.model.output.quant, s["hidden"]), np.uint8)
+        rc = lib().jo_decode_head(C.byref(self.model), _p(x), _p(logits), threads, _p(xn), _p(q8))
+        assert rc == 0
+        return logits, xn, q8

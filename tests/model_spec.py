@@ -50,3 +50,64 @@ def build(spec, seed=0, mix="q4_k_m"):
 def oracle_tensors(t):
     """{name: (quant, array)} for pyoracle.DecodeModel."""
     return {k: (v[0], v[1]) for k, v in t.items()}
+
+
+def _dev_weights(torch, quant, rows, k, gen, dev):
+    """rows x k random blocks of `quant` generated on the device: uniform payload bytes, scale
+    fields at the magnitudes rand_weights uses."""
+    from qdata import BLOCK
+    be, bb = BLOCK[quant]
+    nb = rows * (k // be)
+    b = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, device=dev, generator=gen)
+    u = lambda lo, hi: (torch.rand(nb, device=dev, generator=gen) * (hi - lo) + lo).half().view(torch.uint8).view(nb, 2)
+    if quant == Q4_K:
+        b[:, 0:2] = u(1e-4, 4e-4)
+        b[:, 2:4] = u(5e-4, 2e-3)
+    elif quant == Q6_K:
+        b[:, 192:208] = torch.randint(-64, 64, (nb, 16), dtype=torch.int8, device=dev, generator=gen).view(torch.uint8)
+        b[:, 208:210] = u(1e-4, 3e-4)
+    elif quant == Q8_0:
+        b[:, 0:2] = u(2e-4, 6e-4)
+        b[:, 2:] = torch.randint(-127, 128, (nb, 32), dtype=torch.int8, device=dev, generator=gen).view(torch.uint8)
+    else:
+        raise ValueError(quant)
+    return b.reshape(-1)
+
+
+def build_device(spec, dev, seed=0, mix="q4_k_m"):
+    """The same model layout as build(), with the quantized matrices generated on the GPU (fast at
+    the 8B shape): {name: (quant, host numpy array, n_in, n_out)} plus {name: device tensor}."""
+    import torch
+    H, F, L, V = spec["hidden"], spec["ffn"], spec["n_layers"], spec["vocab"]
+    Q, KV, hd = spec["nq"] * spec["hd"], spec["nkv"] * spec["hd"], spec["hd"]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    hi = set(q6k_layers(L)) if mix == "q4_k_m" else set()
+    host, on_dev = {}, {}
+
+    def mat(name, quant, n_in, n_out):
+        d = _dev_weights(torch, quant, n_out, n_in, gen, dev)
+        on_dev[name] = d
+        host[name] = (quant, d.cpu().numpy(), n_in, n_out)
+
+    def norm(name, n):
+        host[name] = (F32, (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32), n, 1)
+
+    mat("token_embd.weight", Q4_K, H, V)
+    mat("output.weight", Q6_K, H, V)
+    norm("output_norm.weight", H)
+    for i in range(L):
+        p = f"blk.{i}."
+        norm(p + "attn_norm.weight", H)
+        norm(p + "ffn_norm.weight", H)
+        norm(p + "attn_q_norm.weight", hd)
+        norm(p + "attn_k_norm.weight", hd)
+        mat(p + "attn_q.weight", Q4_K, H, Q)
+        mat(p + "attn_k.weight", Q4_K, H, KV)
+        mat(p + "attn_v.weight", Q6_K if i in hi else Q4_K, H, KV)
+        mat(p + "attn_output.weight", Q4_K, Q, H)
+        mat(p + "ffn_gate.weight", Q4_K, H, F)
+        mat(p + "ffn_up.weight", Q4_K, H, F)
+        mat(p + "ffn_down.weight", Q6_K if i in hi else Q4_K, F, H)
+    return host, on_dev

@@ -3,24 +3,25 @@
 Golden llama Q8_0 fixture: first-token logits within 1e-4 and the greedy ids, as the
 reference's own certification (tests/architecture_certification_gate.rs:305).
 
-Random Qwen3-shaped models against the oracle's decode step, per step:
-  * cosine similarity of the logit vectors >= 0.9999, the reference's certification floor
-    (verify_parity_against_golden, src/certification.rs:240-318, exercised at 0.9999 in :950),
-    and >= 0.99999 on average over the steps;
-  * the greedy token equals the oracle's argmax whenever the oracle's top-2 gap exceeds
-    1e-2 of the logits' rms;
-  * max elementwise error <= 2e-2 of max(|ref|, rms(ref)), and <= 1e-3 on at least 3/4 of the
-    steps.
-Why not 1e-3 on every step: activations are re-quantized to int8 before every GEMV, so two
-correct implementations whose f32 hidden states differ in the last ulp can round an element
-to neighbouring int8 values; inside a layer that moves the hidden state by ~1e-4, which moves
-several int8 values of the LM-head input at once and the logits by ~1e-2 on that step only.
-The steps above 1e-3 are counted and printed.
+Random Qwen3-shaped models against the oracle, every step traced (decode_parity.run_traced):
+  * teacher-forced, layer by layer: the device's activation blocks bit-exact, every GEMV within
+    1e-5, attention within 1e-3, RMSNorm / QK-norm / RoPE / SwiGLU at f32
+    precision, each stage recomputed by the oracle from the device's own input to it;
+  * free-running (device and oracle each from their own state): the int8 flips between the two
+    runs are counted at every quantization point and each must be a +-1 flip whose two
+    pre-rounding values differ by less than half a quantum; a step without flips must match the
+    oracle's logits within 1e-3, a step with flips within 2e-2 at cosine >= 0.9999 (the
+    reference's certification floor, src/certification.rs:240-318).
+Why flips happen at all: activations are re-quantized to int8 before every GEMV, and the device
+(f32, its own summation order) and the oracle (f64 accumulation) round an element lying within
+~1e-6 of a rounding boundary to neighbouring int8 values; one flip moves the hidden state by
+~1e-4 and the logits by up to ~1e-2 on that step.
 """
 import numpy as np
 import pytest
 import torch
 
+import decode_parity as DP
 import golden_llama as GL
 import jero_hip as J
 import model_spec as MS
@@ -38,18 +39,6 @@ def make_gpu_model(spec, tensors, cap, kv_dtype, qk_norm):
         m.set_tensor(name, quant, arr, n_in, n_out)
     m.finalize()
     return m
-
-
-def cosine(a, b):
-    a = np.asarray(a, np.float64)
-    b = np.asarray(b, np.float64)
-    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
-
-
-def rel_err(y, ref):
-    ref = np.asarray(ref, np.float64)
-    scale = max(float(np.sqrt(np.mean(ref ** 2))), 1e-30)
-    return float(np.max(np.abs(np.asarray(y, np.float64) - ref) / np.maximum(np.abs(ref), scale)))
 
 
 def test_golden_llama_on_device(dev):
@@ -95,6 +84,25 @@ def check_golden(m, g, s, dev):
         greedy.append(m.read_token_pos()[0])
     assert greedy == g["greedy_token_ids"]
     assert m.read_token_pos()[1] == len(g["prompt_token_ids"]) + len(g["greedy_token_ids"]) - 1
+
+
+def test_golden_llama_traced_against_oracle(dev):
+    """The golden llama (Q8_0 weights, ACT_Q8 activations, no QK-norm) decoded with the trace on:
+    the same layer-by-layer checks as the Qwen3 models, over the prompt and four more steps."""
+    print("golden llama traced", flush=True)
+    s = dict(GL.SPEC)
+    tensors = {}
+    shapes = {n: shp for n, _, shp in GL.tensor_specs()}
+    for name, (quant, arr) in GL.build().items():
+        shp = shapes[name]
+        tensors[name] = (quant, arr, shp[0], shp[1] if len(shp) > 1 else 1)
+    spec = dict(hidden=s["hidden"], ffn=s["ffn"], n_layers=s["n_layers"], vocab=s["vocab"], nq=s["nq"], nkv=s["nkv"],
+                hd=s["hd"], eps=s["eps"], theta=s["theta"])
+    m = make_gpu_model(spec, tensors, 128, J.KV_F32, False)
+    om = O.DecodeModel(spec, MS.oracle_tensors(tensors), 128)
+    kv = om.new_kv()
+    DP.run_traced(m, om, tensors, spec, kv, 128, 0, 8, False, dev, 1, qk_norm=False)
+    m.close()
 
 
 def write_model_gguf(path, arch, spec, tensors):
@@ -191,9 +199,16 @@ def test_decode_matches_oracle(dev, kv_name, cap, prefill, steps):
     kv_dtype = J.KV_F32 if kv_name == "f32" else J.KV_F16
     m = make_gpu_model(spec, t, cap, kv_dtype, True)
     om = O.DecodeModel(spec, MS.oracle_tensors(t), cap)
+    kv = prefill_kv(m, om, spec, cap, prefill, 7, dev, kv_dtype == J.KV_F16)
+    DP.run_traced(m, om, t, spec, kv, cap, prefill, steps, kv_dtype == J.KV_F16, dev, 17)
+
+
+def prefill_kv(m, om, spec, cap, prefill, seed, dev, kv_f16=True):
+    """Both rings (device and oracle) pre-filled with the same N(0, 1) values, f16-exact, for
+    positions [0, prefill)."""
     kv = om.new_kv()
     kvd = spec["nkv"] * spec["hd"]
-    rng = np.random.default_rng(7)
+    rng = np.random.default_rng(seed)
     for L in range(spec["n_layers"]):
         k = rng.standard_normal((cap, kvd)).astype(np.float16)
         v = rng.standard_normal((cap, kvd)).astype(np.float16)
@@ -201,65 +216,52 @@ def test_decode_matches_oracle(dev, kv_name, cap, prefill, steps):
         v[prefill:] = 0
         kv[L, 0] = k.astype(np.float32)
         kv[L, 1] = v.astype(np.float32)
-        tdt = torch.float16 if kv_dtype == J.KV_F16 else torch.float32
+        tdt = torch.float16 if kv_f16 else torch.float32
         m.write_kv(L, torch.from_numpy(k).to(tdt).to(dev), torch.from_numpy(v).to(tdt).to(dev))
-    run_steps(m, om, kv, spec, cap, prefill, steps, kv_dtype, dev)
+    return kv
 
 
-def run_steps(m, om, kv, spec, cap, prefill, steps, kv_dtype, dev, tok=17, strict_fraction=True):
-    logits = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
-    over = 0
-    coss = []
-    m.set_position(tok, prefill)
-    for i in range(steps):
-        pos = prefill + i
-        m.decode_step()
-        torch.cuda.synchronize()
-        m.read_logits(logits)
-        ref = om.step(kv, tok, pos, threads=16)
-        if kv_dtype == J.KV_F16:  # the device ring stores the new row in f16: so does the oracle's
-            kv[:, :, pos % cap] = kv[:, :, pos % cap].astype(np.float16).astype(np.float32)
-        got = logits.cpu().numpy()
-        err, cs = rel_err(got, ref), cosine(got, ref)
-        print(f"  pos {pos}: rel err {err:.2e} cos {cs:.8f}", flush=True)
-        assert cs >= 0.9999, (pos, cs)
-        coss.append(cs)
-        assert err < 2e-2, (pos, err)
-        over += err >= 1e-3
-        gtok, gpos = m.read_token_pos()
-        assert gpos == pos + 1
-        top2 = np.sort(ref.astype(np.float64))[-2:]
-        scale = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
-        if top2[1] - top2[0] > 1e-2 * scale:
-            assert gtok == int(np.argmax(ref)), (pos, gtok, int(np.argmax(ref)))
-        tok = gtok if gtok >= 0 else 0  # the oracle follows the device's token
-    print(f"  steps above 1e-3: {over} of {steps}; mean cos {np.mean(coss):.8f}", flush=True)
-    assert np.mean(coss) >= 0.99999, np.mean(coss)
-    if strict_fraction:
-        assert over <= max(2, steps // 5), over
+QWEN3_8B = dict(hidden=4096, ffn=12288, n_layers=36, vocab=151936, nq=32, nkv=8, hd=128, eps=1e-6, theta=1e6)
 
 
 def test_decode_qwen3_8b_layer_shape(dev):
     """Two layers of the Qwen3-8B shape (hidden 4096, 32/8 heads of 128, FFN 12288, vocab
-    151936), Q4_K_M mix, f16 cache of 4096 slots pre-filled to 4095, then decode.  At this
-    width a step re-quantizes ~28K activations, so int8 flips land on most steps (measured
-    2-5e-3 elementwise, cosine 0.9999995): the per-step bars apply, the 1e-3 fraction does not."""
+    151936), Q4_K_M mix, f16 cache of 4096 slots pre-filled to 4094, then decode."""
     print("decode qwen3-8b layer shape", flush=True)
-    spec = dict(hidden=4096, ffn=12288, n_layers=2, vocab=151936, nq=32, nkv=8, hd=128, eps=1e-6, theta=1e6)
+    spec = dict(QWEN3_8B, n_layers=2)
     cap, prefill = 4096, 4094
     t = MS.build(spec, seed=8)
     m = make_gpu_model(spec, t, cap, J.KV_F16, True)
     om = O.DecodeModel(spec, MS.oracle_tensors(t), cap)
-    kv = om.new_kv()
-    kvd = spec["nkv"] * spec["hd"]
-    rng = np.random.default_rng(9)
-    for L in range(spec["n_layers"]):
-        k = rng.standard_normal((cap, kvd)).astype(np.float16)
-        v = rng.standard_normal((cap, kvd)).astype(np.float16)
-        kv[L, 0] = k.astype(np.float32)
-        kv[L, 1] = v.astype(np.float32)
-        m.write_kv(L, torch.from_numpy(k).to(dev), torch.from_numpy(v).to(dev))
-    run_steps(m, om, kv, spec, cap, prefill, 3, J.KV_F16, dev, tok=1234, strict_fraction=False)
+    kv = prefill_kv(m, om, spec, cap, prefill, 9, dev)
+    DP.run_traced(m, om, t, spec, kv, cap, prefill, 2, True, dev, 1234)
+    m.close()
+
+
+def test_decode_qwen3_8b_full_depth(dev):
+    """The benchmark's decode model at its full depth: a random-init Qwen3-8B-shaped model in
+    Q4_K_M (36 layers; Q6_K head, Q6_K attn_v / ffn_down on 18 layers), f16 KV ring of 4096
+    slots pre-filled with N(0, 1) values to position 4094, three greedy steps (the last one at
+    position 4096 wraps the ring), every layer of every step checked teacher-forced and the
+    free-running flips accounted for."""
+    import time
+    print("decode qwen3-8b full depth: building weights on the device", flush=True)
+    t0 = time.time()
+    spec = dict(QWEN3_8B)
+    cap, prefill = 4096, 4094
+    t, on_dev = MS.build_device(spec, dev, seed=40)
+    m = J.DecodeModel(spec["hidden"], spec["ffn"], spec["n_layers"], spec["vocab"], spec["nq"], spec["nkv"],
+                      spec["hd"], spec["eps"], spec["theta"], cap, J.KV_F16, True)
+    for name, (quant, arr, n_in, n_out) in t.items():
+        m.set_tensor(name, quant, on_dev.get(name, arr), n_in, n_out)
+    del on_dev
+    m.finalize()
+    torch.cuda.empty_cache()
+    om = O.DecodeModel(spec, MS.oracle_tensors(t), cap)
+    kv = prefill_kv(m, om, spec, cap, prefill, 41, dev)
+    print(f"  model ready in {time.time() - t0:.0f} s", flush=True)
+    res = DP.run_traced(m, om, t, spec, kv, cap, prefill, 3, True, dev, 4321)
+    print(f"  flips per step {[r[0] for r in res]}", flush=True)
     m.close()
 
 

@@ -181,6 +181,14 @@ int jero_hip_moe_ffn(const float *x_dev, const float *router_logits_dev, int64_t
                      int64_t hidden, int64_t ffn, float *y_dev, int32_t *sel_idx_dev, float *sel_w_dev,
                      void *workspace_dev, size_t workspace_bytes, void *stream);
 size_t jero_hip_moe_workspace_bytes(int64_t n_tokens, int64_t n_experts, int top_k, int64_t hidden, int64_t ffn);
+/* Debug view of a workspace after jero_hip_moe_ffn returned and its stream was synchronized, for
+ * the per-expert parity tests (no counterpart in the reference, where the expert's SwiGLU
+ * vector is a local of run_single_swiglu_expert, src/qwen_deepseek.rs:748-771): *act_dev holds the
+ * f32 rows silu(gate_e x_t) * up_e x_t [ffn] that the down projections quantized to Q8_K, one per
+ * (token t, slot j); the row of (t, j) is t * top_k + j when *identity, else the int32 at
+ * (*pair_row_dev)[t * top_k + j] (device memory). */
+int jero_hip_moe_trace_view(void *workspace_dev, int64_t n_tokens, int64_t n_experts, int top_k, int64_t hidden,
+                            int64_t ffn, float **act_dev, int32_t **pair_row_dev, int *identity);
 
 /* dequantize_token_row (src/qwen_deepseek.rs:514,569): rows [row0, row0+n_rows) of a tensor
  * with n_in elements per row, written as f32 to out_dev[n_rows][n_in]. */

@@ -1458,6 +1458,34 @@ extern "C" int jero_hip_moe_ffn(const float* x_dev, const float* router_logits_d
   return launch_moe(a, ws, static_cast<hipStream_t>(stream));
 }
 
+extern "C" int jero_hip_moe_trace_view(void* workspace_dev, int64_t n_tokens, int64_t n_experts, int top_k,
+                                       int64_t hidden, int64_t ffn, float** act_dev, int32_t** pair_row_dev,
+                                       int* identity) {
+  if (!workspace_dev || !act_dev || !pair_row_dev || !identity)
+    return fail(JERO_ERR_INVALID_ARGUMENT, "moe_trace_view: null pointer");
+  if (n_tokens <= 0 || n_experts <= 0 || top_k <= 0 || hidden <= 0 || ffn <= 0)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "moe_trace_view: empty shape");
+  // the carve-out of launch_moe, in the same order
+  const int64_t n = n_tokens * top_k;
+  uint8_t* p = static_cast<uint8_t*>(workspace_dev);
+  auto take = [&](size_t x) {
+    uint8_t* r = p;
+    p += (x + 255) & ~size_t(255);
+    return r;
+  };
+  take(size_t(n_tokens) * size_t(moe_xq_rb(hidden)));
+  take(sizeof(int32_t) * size_t(n_experts + 1));
+  take(sizeof(int32_t) * size_t(n_experts));
+  take(sizeof(int32_t));
+  int32_t* ei = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(n) * 2));
+  take(sizeof(int32_t) * size_t(moe_max_passes(n, n_experts)) * kMoePassInts);
+  take(sizeof(int32_t) * kMoeCtrInts);
+  *act_dev = reinterpret_cast<float*>(take(sizeof(float) * size_t(ffn) * size_t(n)));
+  *pair_row_dev = ei + n;
+  *identity = (n_tokens == 1 && n_experts <= 128) ? 1 : 0;  // the one-token path keeps rows in selection order
+  return JERO_OK;
+}
+
 extern "C" size_t jero_hip_moe_workspace_bytes(int64_t n_tokens, int64_t n_experts, int top_k, int64_t hidden,
                                                int64_t ffn) {
   return moe_workspace_bytes(n_tokens, n_experts, top_k, hidden, ffn);

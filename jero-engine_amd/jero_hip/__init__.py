@@ -66,6 +66,8 @@ _SIGS = {
     "jero_hip_moe_ffn": (_I32, [_P, _P, _I64, _I64, _I32, _I32, _P, _SZ, _I32, _P, _SZ, _I32, _P, _SZ, _I64, _I64,
                                 _P, _P, _P, _P, _SZ, _P]),
     "jero_hip_moe_workspace_bytes": (_SZ, [_I64, _I64, _I32, _I64, _I64]),
+    "jero_hip_moe_trace_view": (_I32, [_P, _I64, _I64, _I32, _I64, _I64, C.POINTER(_P), C.POINTER(_P),
+                                       C.POINTER(C.c_int)]),
     "jero_hip_model_create": (_I32, [_P, C.POINTER(_P)]),
     "jero_hip_model_destroy": (_I32, [_P]),
     "jero_hip_model_set_tensor": (_I32, [_P, C.c_char_p, _I32, _P, _SZ, _I64, _I64, _I32]),
@@ -354,6 +356,30 @@ def dispatch_qwen3_moe_ffn(out, norm_ffn_in, router_logits, top_k, gate, up, dow
                                  down.nbytes(), hidden, ffn, _ptr(out), _ptr(sel_idx), _ptr(sel_w), _ptr(workspace),
                                  workspace.numel(), _stream(stream)))
     return sel_idx, sel_w
+
+
+def moe_workspace(n_tokens, n_experts, top_k, hidden, ffn, device="cuda"):
+    import torch
+    need = lib().jero_hip_moe_workspace_bytes(n_tokens, n_experts, top_k, hidden, ffn)
+    return torch.empty(need, dtype=torch.uint8, device=device)
+
+
+def moe_trace_act(workspace, n_tokens, n_experts, top_k, hidden, ffn):
+    """The f32 SwiGLU rows of the last jero_hip_moe_ffn call on `workspace` (synchronize first), as
+    a numpy array [n_tokens, top_k, ffn] in (token, slot) order (jero_hip_moe_trace_view)."""
+    import numpy as np
+    act, rows, ident = _P(), _P(), C.c_int()
+    check(lib().jero_hip_moe_trace_view(_ptr(workspace), n_tokens, n_experts, top_k, hidden, ffn, C.byref(act),
+                                        C.byref(rows), C.byref(ident)))
+    n = n_tokens * top_k
+    a = np.empty((n, ffn), np.float32)
+    _memcpy(a.ctypes.data, act.value, a.nbytes)
+    if ident.value:
+        order = np.arange(n)
+    else:
+        order = np.empty(n, np.int32)
+        _memcpy(order.ctypes.data, rows.value, order.nbytes)
+    return a[order].reshape(n_tokens, top_k, ffn)
 
 
 def dequantize_rows(weights, row0, n_rows, out, stream=None):

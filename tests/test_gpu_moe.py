@@ -1,22 +1,28 @@
 """GPU parity of the routed-expert FFN against the oracle's dispatch_qwen3_moe_ffn.
 
-Routing (selected experts and their order) must match exactly; weights within 1e-6; outputs
-within 1e-3 of max(|ref|, rms(ref)) per token row.  The expert hidden activations are
-re-quantized to Q8_K between gate/up and down, so a last-bit difference in silu(g)*u (summation
-order) can move one int8 by one; that shifts the token's whole output row by ~1e-3 of its rms,
-up to a few 1e-3 where |ref| is small.  Such rows (at most a tenth of the rows, and one) must
-still hold cosine >= 0.9999, the reference's certification floor (src/certification.rs:240-318),
-and 2e-2.  Without a flip the kernels sit at ~1e-6.
+Routing (selected experts and their order) must match exactly and the weights within 1e-6.
+Outputs are checked per expert, as the decode step is (decode_parity): the oracle quantizes
+each token, runs each selected expert's gate/up from those (bit-identical) activation blocks and
+forms silu(g) * u; the device's f32 SwiGLU rows (jero_hip_moe_trace_view) must match within
+1e-5 of their rms, and the two rows' Q8_K quantizations may differ only by tie flips
+(decode_parity.tie_flips: pre-rounding values within 0.05 quantum everywhere, each flip a +-1
+crossing of a rounding boundary between them).  The oracle then runs the expert's down
+projection on the device's activation blocks and combines the experts in selection order in
+f32, as the reference accumulates (src/qwen_deepseek.rs:847-951); the device's outputs must
+match within the north-star 1e-5 of max(|ref|, rms(ref)) per token.
 """
 import numpy as np
 import pytest
 import torch
 
+import decode_parity as DP
 import jero_hip as J
 import pyoracle as O
 from qdata import rand_act, rand_weights
 
 pytestmark = pytest.mark.gpu
+
+MOE_TOL = 1e-5
 
 
 def run_case(dev, T, E, H, F, K, gq, dq, seed, logits=None, repacked=False):
@@ -26,40 +32,55 @@ def run_case(dev, T, E, H, F, K, gq, dq, seed, logits=None, repacked=False):
     x = rand_act(H, seed + 3, m=T)
     if logits is None:
         logits = rand_act(E, seed + 4, m=T)
-    y_ref, si_ref, sw_ref = O.moe_ffn(logits, K, gate, up, down, gq, gq, dq, H, F, x, threads=8)
+    _, si_ref, sw_ref = O.moe_ffn(logits, K, gate, up, down, gq, gq, dq, H, F, x, threads=8)
     td = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
     G = J.TensorView("blk.0.ffn_gate_exps.weight", gq, [H, F, E], td(gate))
     U = J.TensorView("blk.0.ffn_up_exps.weight", gq, [H, F, E], td(up))
     D = J.TensorView("blk.0.ffn_down_exps.weight", dq, [F, H, E], td(down))
-    y = torch.empty((T, H), dtype=torch.float32, device=dev)
-    si, sw = J.dispatch_qwen3_moe_ffn(y, td(x), td(logits), K, G, U, D)
-    torch.cuda.synchronize()
+    runs = [(G, U, D)]
     if repacked:  # the load-time layouts: 16-row tiles (_T), and the GEMV planes over all rows (_R)
         for experts, gl, dl in ((True, (J.Q4_K_T, J.Q6_K_T), (J.Q4_K_T, J.Q6_K_T)),
                                 (False, (J.Q4_K_R, J.Q6_K_R), (J.Q4_K_R, J.Q6_K_R))):
             Gr, Ur, Dr = (J.repack(t, experts=experts) for t in (G, U, D))
             assert Gr.quant == gl[gq == J.Q6_K] and Dr.quant == dl[dq == J.Q6_K]
-            yr = torch.empty_like(y)
-            sir, swr = J.dispatch_qwen3_moe_ffn(yr, td(x), td(logits), K, Gr, Ur, Dr)
-            torch.cuda.synchronize()
-            assert torch.equal(sir, si) and torch.equal(swr, sw)
-            check_out(yr, y_ref)
-    np.testing.assert_array_equal(si.cpu().numpy(), si_ref)
-    np.testing.assert_allclose(sw.cpu().numpy(), sw_ref, rtol=1e-6, atol=1e-7)
-    check_out(y, y_ref)
+            runs.append((Gr, Ur, Dr))
+    first = None
+    for Gx, Ux, Dx in runs:
+        ws = J.moe_workspace(T, E, K, H, F, dev)
+        y = torch.empty((T, H), dtype=torch.float32, device=dev)
+        si, sw = J.dispatch_qwen3_moe_ffn(y, td(x), td(logits), K, Gx, Ux, Dx, workspace=ws)
+        torch.cuda.synchronize()
+        if first is None:
+            first = (si, sw)
+            np.testing.assert_array_equal(si.cpu().numpy(), si_ref)
+            np.testing.assert_allclose(sw.cpu().numpy(), sw_ref, rtol=1e-6, atol=1e-7)
+        else:
+            assert torch.equal(si, first[0]) and torch.equal(sw, first[1])
+        act = J.moe_trace_act(ws, T, E, K, H, F)
+        check_experts(y.cpu().numpy(), act, x, si_ref, sw_ref, gate, up, down, gq, dq, H, F)
 
 
-def check_out(y, y_ref):
-    got = y.cpu().numpy().astype(np.float64)
-    ref = y_ref.astype(np.float64)
-    scale = np.sqrt(np.mean(ref ** 2, axis=1, keepdims=True))
-    err = np.max(np.abs(got - ref) / np.maximum(np.abs(ref), scale), axis=1)  # per token row
-    assert err.max() < 2e-2, err.max()
-    flipped = np.nonzero(err >= 1e-3)[0]
-    assert len(flipped) <= max(1, len(err) // 10), (len(flipped), err.max())
-    for t in flipped:
-        cos = got[t] @ ref[t] / (np.linalg.norm(got[t]) * np.linalg.norm(ref[t]))
-        assert cos >= 0.9999, (t, cos, err[t])
+def check_experts(y, act, x, si, sw, gate, up, down, gq, dq, H, F):
+    gb, db = O.row_bytes(gq, H) * F, O.row_bytes(dq, F) * H
+    st = DP.FlipStats()
+    act_err = 0.0
+    for t in range(x.shape[0]):
+        xq = O.quantize_act(DP.Q8_K, x[t])
+        ref = np.zeros(H, np.float32)
+        for j, e in enumerate(si[t]):
+            g = O.matvec(gq, gate[e * gb:(e + 1) * gb], H, F, xq)
+            u = O.matvec(gq, up[e * gb:(e + 1) * gb], H, F, xq)
+            a_or = O.swiglu(g, u)
+            a_dev = act[t, j]
+            act_err = max(act_err, DP.rel(a_dev, a_or))
+            q_dev = O.quantize_act(DP.Q8_K, a_dev)
+            st.add(DP.tie_flips(f"token {t} slot {j}", DP.Q8_K, F, a_or, O.quantize_act(DP.Q8_K, a_or), a_dev, q_dev))
+            ref += np.float32(sw[t, j]) * O.matvec(dq, down[e * db:(e + 1) * db], F, H, q_dev)
+        err = DP.rel(y[t], ref)
+        assert err <= MOE_TOL, (t, err)
+    print(f"  SwiGLU rows within {act_err:.1e}; {st.flips} tie flips (farthest {st.tie_dist:.1e} quanta from its "
+          f"boundary, largest pre-rounding difference {st.pre_diff:.1e})", flush=True)
+    assert act_err <= MOE_TOL, act_err
 
 
 @pytest.mark.parametrize("T", [1, 64])

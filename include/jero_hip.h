@@ -106,6 +106,16 @@ int jero_hip_vec_dot(int quant, const void *w_dev, size_t w_bytes, int64_t n_in,
                      const float *x_dev, float *y_dev, void *workspace_dev, size_t workspace_bytes,
                      void *stream);
 
+/* jero_hip_vec_dot without allocation.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  The quantized activation is staged in a static device array of 128 KiB
+ * held by each device the library runs on, so the call never allocates; n_in whose activation
+ * blocks exceed it (above 114688 elements for Q4_K / Q6_K, 116508 for Q8_0 / Q4_0) is
+ * CapabilityMismatch.  Every call on a device shares that array: calls that overlap on one
+ * device (other streams, other threads) race and must be serialized by the caller. */
+int jero_hip_vec_dot_noalloc(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
+                             const float *x_dev, float *y_dev, void *stream);
+
 /* The exact int32 partial sums of the same GEMV kernel: partials_dev[n_out][P] with P = n_in/32
  * (Q8_0, Q4_0: per block; Q4_K: per 32-element sub-block) or n_in/16 (Q6_K).  Debug export for
  * the bit-exact tests; y_dev receives the same outputs as jero_hip_matvec. */

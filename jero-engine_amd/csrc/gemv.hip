@@ -17,6 +17,9 @@
 // partitioning.
 #include "gemv.h"
 
+#include <mutex>
+#include <vector>
+
 #include "gemv_dot.h"
 #include "quantize.h"
 #include "runtime.h"
@@ -415,6 +418,57 @@ extern "C" int jero_hip_vec_dot(int quant, const void* w_dev, size_t w_bytes, in
     rc = workspace(need, &ws);
     if (rc) return rc;
   }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = launch_quantize_act(act, x_dev, 1, n_in, ws, s);
+  if (rc) return rc;
+  return launch_matvec(quant, w_dev, n_in, n_out, ws, y_dev, nullptr, s);
+}
+
+// ---- the allocation-free vec_dot: activation staging in a static device array ----
+// Every device holding the library holds its own copy of `scratch` until the process ends.  In
+// host code the array's name is only a stand-in for it: its device address, per device, comes
+// from hipGetSymbolAddress, taken once per device with that device current and kept here.
+namespace {
+constexpr size_t kVecDotScratchBytes = 128 * 1024;
+}  // namespace
+static __device__ __align__(256) uint8_t scratch[kVecDotScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // per device: the device address of `scratch`
+
+int scratch_ptr(void** out) {
+  int dev = 0;
+  int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (int(g_scratch_ptr.size()) <= dev) g_scratch_ptr.resize(size_t(dev) + 1, nullptr);
+  if (!g_scratch_ptr[size_t(dev)]) {
+    void* p = nullptr;
+    rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "vec_dot_noalloc: hipGetSymbolAddress");
+    if (rc) return rc;
+    g_scratch_ptr[size_t(dev)] = p;
+  }
+  *out = g_scratch_ptr[size_t(dev)];
+  return JERO_OK;
+}
+}  // namespace
+
+extern "C" int jero_hip_vec_dot_noalloc(int quant, const void* w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
+                                        const float* x_dev, float* y_dev, void* stream) {
+  const int act = act_format(quant);
+  int rc = check_matvec_args(quant, w_dev, w_bytes, n_in, n_out, x_dev, y_dev);
+  if (rc) return rc;
+  if (reinterpret_cast<uintptr_t>(x_dev) & 15u)
+    return fail(JERO_ERR_INVALID_ARGUMENT, "vec_dot_noalloc: input must be 16-byte aligned");
+  const size_t need = size_t(row_bytes(act, n_in));
+  if (need > kVecDotScratchBytes)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "vec_dot_noalloc: n_in=" + std::to_string(n_in) + " needs " +
+                                                  std::to_string(need) + " bytes of activation staging, above its " +
+                                                  std::to_string(kVecDotScratchBytes) + "-byte static buffer");
+  void* ws = nullptr;
+  rc = scratch_ptr(&ws);
+  if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   rc = launch_quantize_act(act, x_dev, 1, n_in, ws, s);
   if (rc) return rc;

@@ -48,6 +48,7 @@ _SIGS = {
     "jero_hip_matvec": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P]),
     "jero_hip_vec_dot": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "jero_hip_matvec_partials": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _P]),
+    "jero_hip_vec_dot_noalloc": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P]),
     "jero_hip_weights_register": (_I32, [_P, _SZ, C.POINTER(_P)]),
     "jero_hip_weights_lookup": (_I32, [_P, _SZ, C.POINTER(_P)]),
     "jero_hip_weights_release_all": (_I32, []),
@@ -282,6 +283,14 @@ def matvec_any(out, weights, inp, workspace=None, stream=None):
     ws_n = workspace.numel() if workspace is not None else 0
     check(lib().jero_hip_vec_dot(weights.quant, _ptr(weights.data), weights.nbytes(), inp.numel(), out.numel(),
                                  _ptr(inp), _ptr(out), ws_p, ws_n, _stream(stream)))
+    return out
+
+
+def vec_dot_noalloc(out, weights, inp, stream=None):
+    """matvec_any staged through the library's static device buffer (jero_hip_vec_dot_noalloc): no
+    allocation; calls on one device must not overlap."""
+    check(lib().jero_hip_vec_dot_noalloc(weights.quant, _ptr(weights.data), weights.nbytes(), inp.numel(),
+                                         out.numel(), _ptr(inp), _ptr(out), _stream(stream)))
     return out
 
 

@@ -37,6 +37,7 @@ typedef enum jero_status {
 typedef enum jero_quant {
   JERO_F32 = 0,
   JERO_F16 = 1,
+  JERO_BF16 = 30,
   JERO_Q4_0 = 2,
   JERO_Q8_0 = 8,
   JERO_Q4_K = 12, /* the reference's QuantType::Q4_K_M */
@@ -61,7 +62,8 @@ const char *jero_hip_last_error(void);
 const char *jero_hip_status_name(int status);
 /* Bytes of one row of n elements in `quant` (-1 if n is not a multiple of the block). */
 int64_t jero_hip_row_bytes(int quant, int64_t n);
-/* Activation format consumed by the dot product of `weight_quant` (-1 if unsupported). */
+/* Activation format consumed by the dot product of `weight_quant` (-1 if unsupported): Q8_K for
+ * Q4_K / Q6_K, ACT_Q8 for Q8_0 / Q4_0, JERO_F32 (the f32 vector itself) for F32 / F16 / BF16. */
 int jero_hip_act_format(int weight_quant);
 
 /* ---- device copies of host weight tensors ----
@@ -93,7 +95,9 @@ int jero_hip_quantize_act(int act_quant, const float *x_dev, int64_t m, int64_t 
 
 /* ---- GEMV over GGUF weight bytes ----
  * Replaces matvec_any (src/gemma.rs:100-138) -> matvec_any_slice (src/gemma.rs:66-95) ->
- * vec_dot_q8_0 / vec_dot_q4_0 / BaselineKernel::vec_dot_q4_k_m / vec_dot_q6_k.
+ * vec_dot_q8_0 / vec_dot_q4_0 / BaselineKernel::vec_dot_q4_k_m / vec_dot_q6_k, and matvec_f32 /
+ * vec_dot_f16 / vec_dot_bf16 (src/gemma.rs:72-74,140-189) for unquantized rows, whose
+ * "activation" is the f32 input itself (any n_in; rows need only their element alignment).
  * w_dev: n_out rows of n_in elements in `quant` (GGUF tensor shape [n_in, n_out]);
  * xq_dev: the activation already quantized to jero_hip_act_format(quant); y_dev: n_out f32. */
 int jero_hip_matvec(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,

@@ -13,6 +13,11 @@ __device__ __forceinline__ float dequant_elem(int quant, const uint8_t* __restri
   switch (quant) {
     case JERO_F32: return reinterpret_cast<const float*>(row)[col];
     case JERO_F16: return ldh_a2(row + 2 * col);
+    case JERO_BF16: {
+      const uint8_t* p = row + 2 * col;
+      const uint32_t s = uint32_t(reinterpret_cast<uintptr_t>(p) & 3u);
+      return __uint_as_float(((ld1(p - s) >> (8u * s)) & 0xFFFFu) << 16);
+    }
     case JERO_Q8_0: {
       const uint8_t* b = row + (col / 32) * 34;
       return ldh_a2(b) * float(int8_t(b[2 + col % 32]));

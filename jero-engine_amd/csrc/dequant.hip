@@ -30,7 +30,7 @@ using namespace jero;
 
 extern "C" int jero_hip_dequantize_rows(int quant, const void* w_dev, size_t w_bytes, int64_t n_in, int64_t row0,
                                         int64_t n_rows, float* out_dev, void* stream) {
-  if (!(is_weight_quant(quant) || quant == JERO_F32 || quant == JERO_F16))
+  if (!is_weight_quant(quant))
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "dequantize_rows: unsupported quantization " + std::to_string(quant));
   if (!w_dev || !out_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "dequantize_rows: null pointer");
   if (n_in <= 0 || n_rows <= 0 || row0 < 0) return fail(JERO_ERR_TENSOR_BOUNDS, "dequantize_rows: empty range");

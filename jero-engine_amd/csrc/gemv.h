@@ -7,6 +7,11 @@
 
 namespace jero {
 
+// F32 / F16 / BF16 weight rows (their "activation" is the f32 input itself).
+bool is_float_weight(int quant);
+// Enqueues y = W x for unquantized weight rows (any n_in).
+int launch_matvec_float(int quant, const void* w, int64_t n_in, int64_t n_out, const float* x, float* y,
+                        hipStream_t s);
 // Largest n_in the register-resident activation layout supports for a weight format.
 int max_gemv_k(int quant);
 // Validates a matvec call (shape, bytes, alignment); records the error and returns its code.

@@ -308,7 +308,7 @@ int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, in
   if (uint64_t(rb) * uint64_t(n_out) > w_bytes)
     return fail(JERO_ERR_TENSOR_BOUNDS, "matvec: tensor holds " + std::to_string(w_bytes) + " bytes, shape needs " +
                                             std::to_string(rb * n_out));
-  if (n_in > max_gemv_k(quant))
+  if (!is_float_weight(quant) && n_in > max_gemv_k(quant))
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "matvec: n_in=" + std::to_string(n_in) + " above the supported " +
                                                   std::to_string(max_gemv_k(quant)));
   if (!aligned4(w) || !aligned4(xq) || !aligned4(y))
@@ -320,6 +320,10 @@ int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, in
 
 int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, float* y, int32_t* part,
                   hipStream_t s) {
+  if (is_float_weight(quant)) {
+    if (part) return fail(JERO_ERR_CAPABILITY_MISMATCH, "matvec_partials: float weights have no integer partial sums");
+    return launch_matvec_float(quant, w, n_in, n_out, static_cast<const float*>(xq), y, s);
+  }
   const uint8_t* wb = static_cast<const uint8_t*>(w);
   const uint8_t* xb = static_cast<const uint8_t*>(xq);
   if (part) {
@@ -407,6 +411,8 @@ extern "C" int jero_hip_vec_dot(int quant, const void* w_dev, size_t w_bytes, in
   if (rc) return rc;
   if (reinterpret_cast<uintptr_t>(x_dev) & 15u)
     return fail(JERO_ERR_INVALID_ARGUMENT, "vec_dot: input must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (act == JERO_F32) return launch_matvec(quant, w_dev, n_in, n_out, x_dev, y_dev, nullptr, s);  // unquantized
   size_t need = size_t(row_bytes(act, n_in));
   void* ws = workspace_dev;
   if (ws) {
@@ -418,7 +424,6 @@ extern "C" int jero_hip_vec_dot(int quant, const void* w_dev, size_t w_bytes, in
     rc = workspace(need, &ws);
     if (rc) return rc;
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
   rc = launch_quantize_act(act, x_dev, 1, n_in, ws, s);
   if (rc) return rc;
   return launch_matvec(quant, w_dev, n_in, n_out, ws, y_dev, nullptr, s);
@@ -461,6 +466,8 @@ extern "C" int jero_hip_vec_dot_noalloc(int quant, const void* w_dev, size_t w_b
   if (rc) return rc;
   if (reinterpret_cast<uintptr_t>(x_dev) & 15u)
     return fail(JERO_ERR_INVALID_ARGUMENT, "vec_dot_noalloc: input must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (act == JERO_F32) return launch_matvec(quant, w_dev, n_in, n_out, x_dev, y_dev, nullptr, s);  // no staging
   const size_t need = size_t(row_bytes(act, n_in));
   if (need > kVecDotScratchBytes)
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "vec_dot_noalloc: n_in=" + std::to_string(n_in) + " needs " +
@@ -469,7 +476,6 @@ extern "C" int jero_hip_vec_dot_noalloc(int quant, const void* w_dev, size_t w_b
   void* ws = nullptr;
   rc = scratch_ptr(&ws);
   if (rc) return rc;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   rc = launch_quantize_act(act, x_dev, 1, n_in, ws, s);
   if (rc) return rc;
   return launch_matvec(quant, w_dev, n_in, n_out, ws, y_dev, nullptr, s);

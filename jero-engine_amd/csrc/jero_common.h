@@ -36,6 +36,7 @@ __host__ __device__ constexpr FmtInfo fmt_info(int q) {
          : q == JERO_ACT_Q8 ? FmtInfo{32, 36}
          : q == JERO_F32    ? FmtInfo{1, 4}
          : q == JERO_F16    ? FmtInfo{1, 2}
+         : q == JERO_BF16   ? FmtInfo{1, 2}
                             : FmtInfo{0, 0};
 }
 

@@ -331,14 +331,18 @@ extern "C" int jero_hip_model_set_tensor(jero_model* m, const char* name, int qu
   const bool norm = is_norm(name);
   if (norm && quant != JERO_F32)
     return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string("set_tensor: norm '") + name + "' must be F32");
-  if (!norm && !is_weight_quant(quant))
+  const bool embd = std::string(name) == "token_embd.weight";
+  const bool float_w = quant == JERO_F32 || quant == JERO_F16 || quant == JERO_BF16;
+  if (!norm && (!is_weight_quant(quant) || (float_w && !embd)))
     return fail(JERO_ERR_CAPABILITY_MISMATCH,
-                std::string("set_tensor: '") + name + "' quantization " + std::to_string(quant) + " unsupported");
+                std::string("set_tensor: '") + name + "' quantization " + std::to_string(quant) +
+                    " unsupported by the decode step (projections: Q8_0, Q4_0, Q4_K, Q6_K; the embedding also F32, "
+                    "F16, BF16)");
   const int64_t rb = row_bytes(quant, n_in);
   if (rb < 0 || size_t(rb) * size_t(n_out) != nbytes)
     return fail(JERO_ERR_TENSOR_BOUNDS, std::string("set_tensor: '") + name + "' byte size " + std::to_string(nbytes) +
                                             " does not match its shape");
-  if (!norm && std::string(name) != "token_embd.weight" && n_in > dgemv_max_k(quant))
+  if (!norm && !embd && n_in > dgemv_max_k(quant))
     return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string("set_tensor: '") + name + "' rows of " +
                                                   std::to_string(n_in) + " elements exceed the decode limit " +
                                                   std::to_string(dgemv_max_k(quant)));

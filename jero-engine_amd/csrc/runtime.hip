@@ -36,6 +36,9 @@ int act_format(int weight_quant) {
     case JERO_Q4_K_R:
     case JERO_Q6_K:
     case JERO_Q6_K_R: return JERO_Q8_K;
+    case JERO_F32:
+    case JERO_F16:
+    case JERO_BF16: return JERO_F32;  // the f32 input, unquantized
     default: return -1;
   }
 }

@@ -17,8 +17,9 @@ LIB_PATH = os.path.normpath(os.path.join(HERE, "..", "libjero_hip.so"))
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, ACT_Q8, Q4_K_R, Q6_K_R = 0, 1, 2, 8, 12, 14, 15, 100, 112, 114
 Q4_K_T, Q6_K_T = 113, 115  # stacked expert tensors in 16-row tiles (repack of a 3-D tensor)
+BF16 = 30
 Q4_K_M = Q4_K  # the reference's QuantType::Q4_K_M names the Q4_K block format
-QUANT_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_K: "Q8_K",
+QUANT_NAMES = {F32: "F32", F16: "F16", BF16: "BF16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_K: "Q8_K",
                ACT_Q8: "ACT_Q8", Q4_K_R: "Q4_K_R", Q6_K_R: "Q6_K_R"}
 KV_F32, KV_F16 = 0, 1
 
@@ -292,6 +293,19 @@ def vec_dot_noalloc(out, weights, inp, stream=None):
     check(lib().jero_hip_vec_dot_noalloc(weights.quant, _ptr(weights.data), weights.nbytes(), inp.numel(),
                                          out.numel(), _ptr(inp), _ptr(out), _stream(stream)))
     return out
+
+
+def matvec_f32(out, weights, inp, **kw):
+    """matvec_f32 (src/gemma.rs:140-189): F32 weight rows dotted with the f32 input."""
+    return _vec_dot(F32, out, weights, inp, **kw)
+
+
+def vec_dot_f16(out, weights, inp, **kw):
+    return _vec_dot(F16, out, weights, inp, **kw)
+
+
+def vec_dot_bf16(out, weights, inp, **kw):
+    return _vec_dot(BF16, out, weights, inp, **kw)
 
 
 def vec_dot_q8_0(out, weights, inp, **kw):

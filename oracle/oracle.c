@@ -77,7 +77,8 @@ uint16_t jo_f32_to_f16(float f) {
 int64_t jo_block_elems(int quant) {
   switch (quant) {
     case JO_F32:
-    case JO_F16: return 1;
+    case JO_F16:
+    case JO_BF16: return 1;
     case JO_Q4_0:
     case JO_Q8_0:
     case JO_ACT_Q8: return 32;
@@ -91,7 +92,8 @@ int64_t jo_block_elems(int quant) {
 int64_t jo_block_bytes(int quant) {
   switch (quant) {
     case JO_F32: return 4;
-    case JO_F16: return 2;
+    case JO_F16:
+    case JO_BF16: return 2;
     case JO_Q4_0: return 18;
     case JO_Q8_0: return 34;
     case JO_ACT_Q8: return 36;
@@ -114,6 +116,9 @@ int jo_act_format(int weight_quant) {
     case JO_Q8_0: return JO_ACT_Q8;
     case JO_Q4_K:
     case JO_Q6_K: return JO_Q8_K;
+    case JO_F32:
+    case JO_F16:
+    case JO_BF16: return JO_F32; /* the f32 input itself (matvec_f32, vec_dot_f16/bf16) */
     default: return -1;
   }
 }
@@ -162,6 +167,10 @@ int jo_dequantize_row(int quant, const void *row, int64_t n, float *out) {
     switch (quant) {
       case JO_F32: y[0] = rdf32(blk); break;
       case JO_F16: y[0] = jo_f16_to_f32(rd16(blk)); break;
+      case JO_BF16: {
+        uint32_t bits = (uint32_t)rd16(blk) << 16;
+        memcpy(&y[0], &bits, 4);
+      } break;
       case JO_Q8_0: {
         float d = jo_f16_to_f32(rd16(blk));
         for (int j = 0; j < 32; j++) y[j] = d * (float)(int8_t)blk[2 + j];
@@ -277,6 +286,10 @@ void jo_quantize_q8_k(const float *x, int64_t m, int64_t k, void *out) {
 }
 
 void jo_quantize_act(int act_quant, const float *x, int64_t m, int64_t k, void *out) {
+  if (act_quant == JO_F32) { /* unquantized input of the float weight formats */
+    memcpy(out, x, (size_t)(m * k) * 4);
+    return;
+  }
   if (act_quant == JO_Q8_K)
     jo_quantize_q8_k(x, m, k, out);
   else
@@ -343,6 +356,16 @@ double jo_vec_dot_row(int quant, const void *wrow, int64_t k, const void *xq, in
         double dx = rdf32(ab);
         acc += dx * ((double)jo_f16_to_f32(rd16(wb)) * (double)isum -
                      (double)jo_f16_to_f32(rd16(wb + 2)) * (double)msum);
+      }
+      break;
+    case JO_F32:
+    case JO_F16:
+    case JO_BF16: /* matvec_f32 / vec_dot_f16 / vec_dot_bf16 (src/gemma.rs:72-74,140-189): the row
+                     widened to f32 dotted with the f32 input, accumulated in f64 here */
+      for (int64_t i = 0; i < k; i++) {
+        float wv;
+        jo_dequantize_row(quant, w + i * jo_block_bytes(quant), 1, &wv);
+        acc += (double)wv * (double)rdf32(a + 4 * i);
       }
       break;
     case JO_Q6_K: /* y = sum_b d_x d sum_i sc_i sum_16 (q6 - 32) q8 */

@@ -48,6 +48,7 @@ extern "C" {
 enum {
   JO_F32 = 0,
   JO_F16 = 1,
+  JO_BF16 = 30,
   JO_Q4_0 = 2,
   JO_Q8_0 = 8,
   JO_Q4_K = 12,

@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, ACT_Q8 = 0, 1, 2, 8, 12, 14, 15, 100
+BF16 = 30
 
 _lib = None
 

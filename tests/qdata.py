@@ -45,3 +45,31 @@ def rand_act(k, seed, m=None):
 def row_bytes(quant, k):
     be, bb = BLOCK[quant]
     return (k // be) * bb
+
+
+BF16 = 30
+FLOAT_BYTES = {F32: 4, F16: 2, BF16: 2}
+
+
+def rand_float_weights(quant, rows, k, seed, scale=0.02):
+    """rows x k N(0, scale) weights stored as F32, F16 or BF16 (rounded to nearest even), as a flat
+    uint8 array."""
+    rng = np.random.default_rng(seed)
+    w = (scale * rng.standard_normal((rows, k))).astype(np.float32)
+    if quant == F32:
+        return w.view(np.uint8).reshape(-1)
+    if quant == F16:
+        return w.astype(np.float16).view(np.uint8).reshape(-1)
+    b = w.view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16  # round to nearest even on the upper 16 bits
+    return b.astype(np.uint16).view(np.uint8).reshape(-1)
+
+
+def float_values(quant, data, rows, k):
+    """The f32 values of rand_float_weights' bytes."""
+    data = np.ascontiguousarray(data, np.uint8)
+    if quant == F32:
+        return data.view(np.float32).reshape(rows, k)
+    if quant == F16:
+        return data.view(np.float16).astype(np.float32).reshape(rows, k)
+    return (data.view(np.uint16).astype(np.uint32) << 16).view(np.float32).reshape(rows, k)

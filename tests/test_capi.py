@@ -33,7 +33,8 @@ def test_row_bytes_and_act_formats():
     assert J.row_bytes(J.Q4_K, 100) == -1
     assert J.act_format(J.Q4_K) == J.Q8_K and J.act_format(J.Q6_K) == J.Q8_K
     assert J.act_format(J.Q8_0) == J.ACT_Q8 and J.act_format(J.Q4_0) == J.ACT_Q8
-    assert J.act_format(J.F32) == -1
+    assert J.act_format(J.F32) == J.F32 and J.act_format(J.F16) == J.F32 and J.act_format(J.BF16) == J.F32
+    assert J.act_format(J.Q8_K) == -1
 
 
 def _matvec(quant, w, nbytes, n_in, n_out, xq, y):
@@ -47,7 +48,7 @@ def test_matvec_argument_errors_before_launch():
     assert _matvec(J.Q4_K, fake, 1 << 20, 256, 0, fake, fake) == 14             # empty output
     assert _matvec(J.Q4_K, fake, 1 << 20, 100, 4, fake, fake) == 14             # not a block multiple
     assert _matvec(J.Q4_K, fake, 144 * 4 - 1, 256, 4, fake, fake) == 14         # tensor too small
-    assert _matvec(J.F16, fake, 1 << 20, 256, 4, fake, fake) == 10              # unsupported quant
+    assert _matvec(3, fake, 1 << 20, 256, 4, fake, fake) == 10                  # unsupported quant (Q4_1)
     assert _matvec(J.Q4_K, fake, 1 << 30, 256 * 129, 1, fake, fake) == 10       # above the K limit
     assert _matvec(J.Q4_K, C.c_void_p(0x10002), 1 << 20, 256, 4, fake, fake) == 21  # misaligned
 

@@ -226,3 +226,52 @@ def test_repack_rejects_other_formats(dev):
     with pytest.raises(J.K3Error) as ei:
         J.repack(W)
     assert ei.value.variant == "CapabilityMismatch"
+
+
+@pytest.mark.parametrize("quant", [0, 1, 30])
+@pytest.mark.parametrize("n_in,n_out", [(2048, 128), (4096, 4096), (1000, 77), (130, 3), (65536, 40)])
+def test_float_weights_matvec(dev, quant, n_in, n_out):
+    """matvec_f32 / vec_dot_f16 / vec_dot_bf16 (src/gemma.rs:72-74,140-189): the Qwen3-MoE router
+    shape (F32 ffn_gate_inp 2048 x 128), a square matrix, rows that are not 16-byte aligned, tiny
+    rows and a 65536-long row, against the oracle within 1e-5."""
+    from qdata import rand_float_weights
+    print(f"float matvec quant={quant} {n_in}x{n_out}", flush=True)
+    w = rand_float_weights(quant, n_out, n_in, 17)
+    x = rand_act(n_in, 18)
+    W = J.TensorView("blk.0.ffn_gate_inp.weight", quant, [n_in, n_out], torch.from_numpy(w).to(dev))
+    y = torch.empty(n_out, dtype=torch.float32, device=dev)
+    J.matvec_any(y, W, torch.from_numpy(x).to(dev))
+    y2 = torch.empty_like(y)
+    J.vec_dot_noalloc(y2, W, torch.from_numpy(x).to(dev))
+    torch.cuda.synchronize()
+    ref = O.vec_dot(quant, w, n_in, n_out, x, threads=8)
+    got = y.cpu().numpy()
+    scale = max(np.sqrt(np.mean(ref.astype(np.float64) ** 2)), 1e-30)
+    err = np.max(np.abs(got - ref) / np.maximum(np.abs(ref), scale))
+    assert err <= 1e-5, err
+    assert torch.equal(y, y2)
+
+
+def test_float_weights_kat_and_gemm(dev):
+    """dot_product_f32([2], [3]) = 6 (src/lib.rs:380-387) on the device, F32 rows through
+    jero_hip_gemm for several token rows (the router of a batch), each row equal to its matvec,
+    and F32 weights rejected where integer partial sums are asked for."""
+    from qdata import rand_float_weights
+    W = J.TensorView("w", J.F32, [1, 1], torch.tensor([2.0], device=dev).view(torch.uint8))
+    y = torch.empty(1, dtype=torch.float32, device=dev)
+    J.matvec_f32(y, W, torch.tensor([3.0], device=dev))
+    assert y.item() == 6.0
+    w = rand_float_weights(J.F32, 128, 2048, 19)
+    x = rand_act(2048, 20, m=5)
+    Wt = J.TensorView("router", J.F32, [2048, 128], torch.from_numpy(w).to(dev))
+    xt = torch.from_numpy(x).to(dev)
+    Y = torch.empty((5, 128), dtype=torch.float32, device=dev)
+    J.gemm(Wt, xt, 5, Y)
+    for r in range(5):
+        yr = torch.empty(128, dtype=torch.float32, device=dev)
+        J.matvec_any(yr, Wt, xt[r].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(Y[r], yr), r
+    with pytest.raises(J.K3Error) as ei:
+        J.matvec_partials(Wt, xt[0], torch.empty(128, device=dev), torch.empty(128, dtype=torch.int32, device=dev))
+    assert ei.value.variant == "CapabilityMismatch"

@@ -386,3 +386,18 @@ def test_moe_ffn_matches_dense_composition():
             ref += np.float32(wgt) * O.vec_dot(O.Q6_K, down[e * H * rb:(e + 1) * H * rb], F, H, a)
         np.testing.assert_allclose(y[t], ref, rtol=1e-6, atol=1e-7)
         assert list(si[t]) == [e for e, _ in sel]
+
+
+def test_float_weight_dot_kat_and_brute_force():
+    """dot_product_f32 [2] . [3] = 6 (src/lib.rs:380-387) through the F32 row path; F16/BF16 rows
+    widened to f32 and dotted in f64 equal a numpy f64 product of the same values."""
+    from qdata import BF16, F16, F32, float_values, rand_float_weights
+    w = np.array([2.0], np.float32).view(np.uint8)
+    assert O.vec_dot(F32, w, 1, 1, np.array([3.0], np.float32))[0] == 6.0
+    x = rand_act(333, 5)
+    for q in (F32, F16, BF16):
+        w = rand_float_weights(q, 7, 333, 6)
+        ref = float_values(q, w, 7, 333).astype(np.float64) @ x.astype(np.float64)
+        np.testing.assert_allclose(O.vec_dot(q, w, 333, 7, x), ref, rtol=1e-6, atol=1e-9)
+    # BF16 is the upper half of the f32 bits: 1.0 = 0x3F80
+    assert O.dequantize(BF16, np.array([0x80, 0x3F], np.uint8), 1, 1)[0, 0] == 1.0

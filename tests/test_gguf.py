@@ -171,12 +171,14 @@ def test_malformed_files_are_rejected(tmp_path):
 
 
 def test_unsupported_tensor_type_is_listed_but_not_fetched(tmp_path):
-    t = [("bf16", 30, (8, 2), bytes(32)), ("x", 0, (8,), bytes(32))]
+    t = [("q5_0", 6, (32, 2), bytes(44)), ("bf16", 30, (8, 2), bytes(32)), ("x", 0, (8,), bytes(32))]
     with open_bytes(tmp_path, W.gguf_bytes("t", [], t)) as g:
-        assert g.tensor_names() == ["bf16", "x"]
+        assert g.tensor_names() == ["q5_0", "bf16", "x"]
         with pytest.raises(J.K3Error) as e:
-            g.tensor("bf16")
+            g.tensor("q5_0")
         assert e.value.status == 10
+        bf = g.tensor("bf16")  # BF16 rows have a size (2 bytes per element)
+        assert bf["quant"] == 30 and bf["nbytes"] == 32
 
 
 def test_corrupted_headers_never_read_out_of_bounds(tmp_path):

@@ -99,7 +99,9 @@ int jero_hip_quantize_act(int act_quant, const float *x_dev, int64_t m, int64_t 
  * vec_dot_f16 / vec_dot_bf16 (src/gemma.rs:72-74,140-189) for unquantized rows, whose
  * "activation" is the f32 input itself (any n_in; rows need only their element alignment).
  * w_dev: n_out rows of n_in elements in `quant` (GGUF tensor shape [n_in, n_out]);
- * xq_dev: the activation already quantized to jero_hip_act_format(quant); y_dev: n_out f32. */
+ * xq_dev: the activation already quantized to jero_hip_act_format(quant); y_dev: n_out f32.
+ * Any row length up to 2^30 elements: rows longer than 16384 (Q8_0 / Q4_0) or 32768 (K-quants)
+ * elements run a K-looped kernel that stages the activation through LDS. */
 int jero_hip_matvec(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
                     const void *xq_dev, float *y_dev, void *stream);
 

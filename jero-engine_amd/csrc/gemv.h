@@ -12,7 +12,8 @@ bool is_float_weight(int quant);
 // Enqueues y = W x for unquantized weight rows (any n_in).
 int launch_matvec_float(int quant, const void* w, int64_t n_in, int64_t n_out, const float* x, float* y,
                         hipStream_t s);
-// Largest n_in the register-resident activation layout supports for a weight format.
+// Largest n_in the register-resident activation layout supports for a weight format (longer
+// rows run the K-looped kernel).
 int max_gemv_k(int quant);
 // Validates a matvec call (shape, bytes, alignment); records the error and returns its code.
 int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, int64_t n_out, const void* xq,

@@ -114,6 +114,71 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const uint8_t* __res
   }
 }
 
+// Rows longer than the register-resident activation allows (no row-length limit): each wave
+// reduces R rows, one per 64 lanes in turn; the workgroup stages the activation through LDS in
+// chunks of whole blocks (kLongChunkBytes), every lane walks the chunk's units c, c + 64, ...
+// with all R rows' loads of a step issued together, and the f32 accumulators carry across
+// chunks.  Each row is reduced in an order that depends only on n_in.
+constexpr int kLongChunkBytes = 32 * 1024;
+
+template <int F, int R, bool PART>
+__global__ void __launch_bounds__(kGemvThreads) gemv_long_kernel(const uint8_t* __restrict__ w, int64_t rb, int U,
+                                                                  int64_t N, const uint8_t* __restrict__ xq,
+                                                                  int64_t act_bytes, int act_block, int units_per_block,
+                                                                  int chunk_blocks, float* __restrict__ y,
+                                                                  int32_t* __restrict__ part, int64_t ppr) {
+  using Ut = Unit<F>;
+  __shared__ __attribute__((aligned(16))) uint8_t s_act[kLongChunkBytes];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  const int64_t row0 = wave * R;
+  const int64_t n_blocks = act_bytes / act_block;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) acc[r] = 0.f;
+  for (int64_t b0 = 0; b0 < n_blocks; b0 += chunk_blocks) {
+    const int nb = int(n_blocks - b0 < chunk_blocks ? n_blocks - b0 : chunk_blocks);
+    const int bytes = nb * act_block;  // a multiple of 4
+    __syncthreads();                   // the previous chunk is no longer read
+    for (int i = threadIdx.x; i < bytes / 4; i += kGemvThreads)
+      reinterpret_cast<uint32_t*>(s_act)[i] = reinterpret_cast<const uint32_t*>(xq + b0 * act_block)[i];
+    __syncthreads();
+    const int u_first = int(b0) * units_per_block, u_count = nb * units_per_block;
+    for (int j = lane; j < u_count; j += kWave) {
+      const int u = u_first + j;
+      typename Ut::W wt[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int64_t row = row0 + r < N ? row0 + r : N - 1;
+        if constexpr (is_planar(F))
+          Ut::load_w_planar(wt[r], w, N, U, row, u);
+        else
+          Ut::load_w(wt[r], w + row * rb, u);
+      }
+      typename Ut::Act a;
+      Ut::load_act(a, s_act, j);  // chunks start on block boundaries: unit j of the chunk
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        if constexpr (PART) {
+          int32_t p[Ut::kPartials];
+          acc[r] += Ut::dot(wt[r], a, p);
+          if (row0 + r < N) {
+#pragma unroll
+            for (int k = 0; k < Ut::kPartials; k++) part[(row0 + r) * ppr + Ut::part_index(u, k)] = p[k];
+          }
+        } else {
+          acc[r] += Ut::dot(wt[r], a, nullptr);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const float v = group_sum_last<64>(acc[r]);
+    if (lane == 63 && row0 + r < N) y[row0 + r] = v;
+  }
+}
+
 namespace {
 
 struct Launch {
@@ -195,9 +260,17 @@ int launch_fmt(const uint8_t* w, int64_t k, int64_t N, const uint8_t* xq, float*
       case 6: launch_upl<F, 6, PART>(R, lds, L); break;
       case 7:
       case 8: launch_upl<F, 8, PART>(R, lds, L); break;
-      default:
-        return fail(JERO_ERR_CAPABILITY_MISMATCH, "matvec: n_in=" + std::to_string(k) +
-                                                      " exceeds the register-resident activation limit");
+      default: {
+        // rows beyond the register-resident activation: the K-looped kernel
+        constexpr int act = (F == JERO_Q8_0 || F == JERO_Q4_0) ? JERO_ACT_Q8 : JERO_Q8_K;
+        constexpr int ab = act == JERO_Q8_K ? 292 : 36;
+        constexpr int upb = act == JERO_Q8_K ? 4 : 1;
+        constexpr int RL = PART ? 1 : 2;
+        const int64_t waves = (N + RL - 1) / RL;
+        const int64_t blocks = (waves + kGemvThreads / kWave - 1) / (kGemvThreads / kWave);
+        hipLaunchKernelGGL((gemv_long_kernel<F, RL, PART>), dim3(unsigned(blocks)), dim3(kGemvThreads), 0, s, w,
+                           L.rb, U, N, xq, row_bytes(act, k), ab, upb, kLongChunkBytes / ab, y, part, L.ppr);
+      }
     }
   }
   return check_launch("matvec");
@@ -308,9 +381,8 @@ int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, in
   if (uint64_t(rb) * uint64_t(n_out) > w_bytes)
     return fail(JERO_ERR_TENSOR_BOUNDS, "matvec: tensor holds " + std::to_string(w_bytes) + " bytes, shape needs " +
                                             std::to_string(rb * n_out));
-  if (!is_float_weight(quant) && n_in > max_gemv_k(quant))
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, "matvec: n_in=" + std::to_string(n_in) + " above the supported " +
-                                                  std::to_string(max_gemv_k(quant)));
+  if (n_in > (int64_t(1) << 30) || n_out > (int64_t(1) << 40))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "matvec: n_in above 2^30 or n_out above 2^40");
   if (!aligned4(w) || !aligned4(xq) || !aligned4(y))
     return fail(JERO_ERR_INVALID_ARGUMENT, "matvec: weights, activations and output must be 4-byte aligned");
   if (is_planar(quant) && (reinterpret_cast<uintptr_t>(w) & 15u))

@@ -49,7 +49,7 @@ def test_matvec_argument_errors_before_launch():
     assert _matvec(J.Q4_K, fake, 1 << 20, 100, 4, fake, fake) == 14             # not a block multiple
     assert _matvec(J.Q4_K, fake, 144 * 4 - 1, 256, 4, fake, fake) == 14         # tensor too small
     assert _matvec(3, fake, 1 << 20, 256, 4, fake, fake) == 10                  # unsupported quant (Q4_1)
-    assert _matvec(J.Q4_K, fake, 1 << 30, 256 * 129, 1, fake, fake) == 10       # above the K limit
+    assert _matvec(J.Q4_K, fake, 1 << 62, 256 * ((1 << 22) + 1), 1, fake, fake) == 10  # n_in above 2^30
     assert _matvec(J.Q4_K, C.c_void_p(0x10002), 1 << 20, 256, 4, fake, fake) == 21  # misaligned
 
 

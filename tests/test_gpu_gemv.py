@@ -275,3 +275,35 @@ def test_float_weights_kat_and_gemm(dev):
     with pytest.raises(J.K3Error) as ei:
         J.matvec_partials(Wt, xt[0], torch.empty(128, device=dev), torch.empty(128, dtype=torch.int32, device=dev))
     assert ei.value.variant == "CapabilityMismatch"
+
+
+@pytest.mark.parametrize("quant,n_in,n_out", [(8, 28672, 512), (2, 20480, 300), (12, 65536, 200), (14, 40960, 130),
+                                              (112, 49152, 96), (114, 36864, 64)])
+def test_long_rows(dev, quant, n_in, n_out):
+    """Rows longer than the register-resident activation (the reference's vec_dot_* has no
+    row-length limit, src/gemma.rs:66-138): Q8_0 at 28672 (a 70B-class ffn_down), Q4_0, Q4_K,
+    Q6_K and the planar layouts, with the int32 partial sums bit-exact on the first case."""
+    print(f"long rows quant={quant} {n_in}x{n_out}", flush=True)
+    base = {112: J.Q4_K, 114: J.Q6_K}.get(quant, quant)
+    w = rand_weights(base, n_out, n_in, 71)
+    x = rand_act(n_in, 72)
+    xq = J.quantize_act(J.act_format(base), torch.from_numpy(x).to(dev))
+    W = J.TensorView("long", base, [n_in, n_out], torch.from_numpy(w).to(dev))
+    if quant != base:
+        W = J.repack(W)
+        assert W.quant == quant
+    y = torch.empty(n_out, dtype=torch.float32, device=dev)
+    J.matvec(W, xq, y)
+    torch.cuda.synchronize()
+    ref = O.matvec(base, w, n_in, n_out, xq.cpu().numpy(), threads=8)
+    scale = max(np.sqrt(np.mean(ref.astype(np.float64) ** 2)), 1e-30)
+    err = np.max(np.abs(y.cpu().numpy() - ref) / np.maximum(np.abs(ref), scale))
+    assert err <= 1e-5, err
+    if quant == 8:
+        pp = O.partials(base, w, n_in, n_out, xq.cpu().numpy())
+        part = torch.empty(pp.shape, dtype=torch.int32, device=dev)
+        y2 = torch.empty_like(y)
+        J.matvec_partials(W, xq, y2, part)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(part.cpu().numpy(), pp)
+        assert torch.equal(y, y2)

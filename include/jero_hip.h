@@ -220,7 +220,8 @@ int jero_hip_dequantize_rows(int quant, const void *w_dev, size_t w_bytes, int64
  * Tensors are given by GGUF name (ModelWeights::tensor): token_embd.weight, output.weight,
  * output_norm.weight, blk.N.{attn_norm, attn_q, attn_k, attn_v, attn_output, attn_q_norm,
  * attn_k_norm, ffn_norm, ffn_gate, ffn_up, ffn_down}.weight; norms F32, matrices in
- * Q8_0/Q4_0/Q4_K/Q6_K with GGUF shape [n_in, n_out].  The KV arena is one device buffer of
+ * Q8_0/Q4_0/Q4_K/Q6_K with GGUF shape [n_in, n_out] (rows of up to 54592 elements for Q8_0/Q4_0,
+ * 53760 for Q4_K/Q6_K: the activation of a row is held in LDS), token_embd also F32/F16/BF16.  The KV arena is one device buffer of
  * [n_layers][K ring, V ring][kv_capacity][n_heads_kv * head_dim] (the recipes' flat layout). */
 typedef struct jero_model_config {
   int64_t hidden, ffn, n_layers, vocab;

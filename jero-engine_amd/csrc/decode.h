@@ -10,6 +10,7 @@ namespace jero {
 constexpr int kDecodeThreads = 512;     // 8 waves per workgroup
 constexpr int kDecodeBlocksPerCU = 2;   // persistent grid: workgroups per CU
 constexpr int kDecodeMaxActBlocks = 8;  // activation blocks per wave in the prologue
+constexpr int kDecodeMaxLongActBytes = 60 * 1024;  // LDS activation of the long-row kernel
 
 enum { kOutStore = 0, kOutResid = 1, kOutSwiglu = 2, kOutArgmax = 3 };
 
@@ -45,8 +46,10 @@ int launch_dgemv(int quant, int out_mode, const DGemvArgs& a, hipStream_t s, int
 // rmsnorm(x) . [W1; W2] into y[0, N + N2) for two K-quant tensors of different formats sharing
 // n_in = K <= 4096 (Q4_K_R with Q6_K_R, either order): one launch, one prologue.
 int launch_dgemv_dual(int quant1, int quant2, const DGemvArgs& a, hipStream_t s);
-// Longest row the fused decode GEMV takes for a weight format.
+// Longest row the register-resident fused decode GEMV takes for a weight format; rows up to
+// dgemv_long_max_k run the long-row variant.
 int dgemv_max_k(int quant);
+int dgemv_long_max_k(int quant);
 // hidden = embedding row of *token; also the step's RoPE table rope_cs[hd/2][cos, sin].
 int launch_embed(int quant, const void* w, int64_t rb, int H, int64_t vocab, const int32_t* token, float* out,
                  const int64_t* pos, float theta, int hd, float* rope_cs, hipStream_t s);

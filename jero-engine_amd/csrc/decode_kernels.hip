@@ -530,6 +530,141 @@ __global__ void __launch_bounds__(1024) argmax_final_kernel(const float* __restr
   }
 }
 
+// ---------------------------------------------------------------- long rows
+
+// The fused decode GEMV for rows longer than the register-resident path takes (dgemv_max_k):
+// the prologue loops over the activation blocks, building them in LDS (after RMSNorm: a first
+// pass sums the squares), and each wave then reduces one row (SwiGLU: a gate row and its up
+// row) at a time, loading UPL units per lane per step and the activation units from LDS.  The
+// epilogues and the debug trace are the register-resident kernel's.
+template <int F, int OUT>
+__global__ void __launch_bounds__(kDecodeThreads) dgemv_long_kernel(DGemvArgs a) {
+  using Ut = Unit<F>;
+  constexpr int ACT = (F == JERO_Q8_0 || F == JERO_Q4_0) ? JERO_ACT_Q8 : JERO_Q8_K;
+  constexpr int R = OUT == kOutSwiglu ? 2 : 1;
+  constexpr int UPL = 4;
+  constexpr bool NORM = OUT != kOutResid;
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_mem[];
+  float* s_tmp = reinterpret_cast<float*>(s_mem);
+  uint8_t* s_act = s_mem + 256;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  const int K = a.K, U = a.U;
+  const bool has_norm = NORM && a.norm_w != nullptr;
+  const bool tracing = blockIdx.x == 0 && a.tr_q8 != nullptr;
+  float* tr_xn = tracing ? a.tr_xn : nullptr;
+  // 1. prologue
+  float scale = 1.0f;
+  if (has_norm) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < K; i += blockDim.x) ss += a.x[i] * a.x[i];
+    ss = block_sum(ss, s_tmp);
+    scale = 1.0f / sqrtf(ss / float(K) + a.eps);
+  }
+  if constexpr (ACT == JERO_Q8_K) {
+    for (int b = wv; b < K / 256; b += nwv) {
+      const float4 xv = reinterpret_cast<const float4*>(a.x + b * 256)[lane];
+      float e[4] = {xv.x, xv.y, xv.z, xv.w};
+      if (has_norm) {
+        const float4 g = reinterpret_cast<const float4*>(a.norm_w + b * 256)[lane];
+        e[0] = e[0] * scale * g.x;
+        e[1] = e[1] * scale * g.y;
+        e[2] = e[2] * scale * g.z;
+        e[3] = e[3] * scale * g.w;
+      }
+      if (tr_xn) reinterpret_cast<float4*>(tr_xn + b * 256)[lane] = make_float4(e[0], e[1], e[2], e[3]);
+      q8k_block_wave(e, lane, s_act + b * 292);
+    }
+  } else {
+    const int nb = K / 32, l = lane & 31;
+    for (int p = wv; 2 * p < nb; p += nwv) {  // both half-waves take the same number of steps
+      const int b = 2 * p + (lane >> 5);
+      const bool ok = b < nb;
+      const int bb = ok ? b : nb - 1;
+      float v = a.x[bb * 32 + l];
+      if (has_norm) v = v * scale * a.norm_w[bb * 32 + l];
+      if (tr_xn && ok) tr_xn[b * 32 + l] = v;
+      float am = fabsf(v);
+#pragma unroll
+      for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, kWave));
+      const float d = am / 127.0f;
+      const float id = d != 0.0f ? 1.0f / d : 0.0f;
+      if (ok) {
+        s_act[b * 36 + 4 + l] = uint8_t(int8_t(int(__builtin_rintf(v * id))));
+        if (l == 0) *reinterpret_cast<float*>(s_act + b * 36) = d;
+      }
+    }
+  }
+  lds_barrier();
+  if (tracing) trace_act(a.tr_q8, s_act, int(ACT == JERO_Q8_K ? K / 256 * 292 : K / 32 * 36));
+  // 2. rows
+  const int64_t wave0 = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  const int64_t stride = int64_t(gridDim.x) * nwv;
+  const int64_t items = OUT == kOutSwiglu ? a.half : a.N;
+  float best_v = -INFINITY;
+  int64_t best_i = -1;
+  for (int64_t it = wave0; it < items; it += stride) {
+    int64_t rows[R];
+    rows[0] = it;
+    if constexpr (R == 2) rows[1] = a.half + it;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    for (int u0 = 0; u0 < U; u0 += 64 * UPL) {
+      typename Ut::W wt[R][UPL];
+#pragma unroll
+      for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int t = 0; t < UPL; t++) {
+          const int u = min(u0 + lane + 64 * t, U - 1);
+          if constexpr (is_planar(F))
+            Ut::load_w_planar(wt[r][t], a.w, a.N, U, rows[r], u);
+          else
+            Ut::load_w(wt[r][t], a.w + rows[r] * a.rb, u);
+        }
+#pragma unroll
+      for (int t = 0; t < UPL; t++) {
+        const int u = u0 + lane + 64 * t;
+        typename Ut::Act act;
+        Ut::load_act(act, s_act, min(u, U - 1));
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const float d = Ut::dot(wt[r][t], act, nullptr);
+          acc[r] += u < U ? d : 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = group_sum_last<64>(acc[r]);
+    if (lane == 63) {
+      if constexpr (OUT == kOutSwiglu) {
+        const float gv = acc[0], uv = acc[1];
+        a.y[it] = gv / (1.0f + expf(-gv)) * uv;
+        if (a.tr_gu) {
+          a.tr_gu[it] = gv;
+          a.tr_gu[a.half + it] = uv;
+        }
+      } else if constexpr (OUT == kOutResid) {
+        a.y[it] = a.y[it] + acc[0];
+      } else {
+        a.y[it] = acc[0];
+        if constexpr (OUT == kOutArgmax) {
+          if (!isnan(acc[0]) && (best_i < 0 || acc[0] > best_v)) {  // rows ascend per wave
+            best_v = acc[0];
+            best_i = it;
+          }
+        }
+      }
+    }
+  }
+  if constexpr (OUT == kOutArgmax) {
+    argmax_block(best_v, best_i);
+    if (threadIdx.x == 0) {
+      a.amax_v[blockIdx.x] = best_v;
+      a.amax_i[blockIdx.x] = best_i;
+    }
+  }
+}
+
 __global__ void set_state_kernel(int32_t* token, int64_t* pos, int32_t* status, int32_t t, int64_t p) {
   *token = t;
   *pos = p;
@@ -614,8 +749,31 @@ int dgemv_fmt(const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t s) {
   return -fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: row of " + std::to_string(a.K) + " elements too long");
 }
 
+template <int F, int OUT>
+int dgemv_long(DGemvArgs a, hipStream_t s) {
+  const int64_t items = OUT == kOutSwiglu ? a.half : a.N;
+  int64_t blocks = (items + kDecodeThreads / kWave - 1) / (kDecodeThreads / kWave);
+  const int64_t cap = int64_t(device_info().cus) * kDecodeBlocksPerCU;
+  if (blocks > cap) blocks = cap;
+  if (a.max_blocks > 0 && blocks > a.max_blocks) blocks = a.max_blocks;
+  const size_t shm = 256 + size_t(row_bytes((F == JERO_Q8_0 || F == JERO_Q4_0) ? JERO_ACT_Q8 : JERO_Q8_K, a.K));
+  hipLaunchKernelGGL((dgemv_long_kernel<F, OUT>), dim3(unsigned(blocks)), dim3(kDecodeThreads), (shm + 15) & ~size_t(15),
+                     s, a);
+  return int(blocks);
+}
+
 template <int OUT>
 int dgemv_out(int quant, const DGemvArgs& a, int64_t rows_or_pairs, hipStream_t s) {
+  if (a.K > dgemv_max_k(quant)) {  // rows beyond the register-resident path
+    switch (quant) {
+      case JERO_Q4_K_R: return dgemv_long<JERO_Q4_K_R, OUT>(a, s);
+      case JERO_Q6_K: return dgemv_long<JERO_Q6_K, OUT>(a, s);
+      case JERO_Q6_K_R: return dgemv_long<JERO_Q6_K_R, OUT>(a, s);
+      case JERO_Q8_0: return dgemv_long<JERO_Q8_0, OUT>(a, s);
+      case JERO_Q4_0: return dgemv_long<JERO_Q4_0, OUT>(a, s);
+    }
+    return -fail(JERO_ERR_CAPABILITY_MISMATCH, "decode: unsupported weight quantization " + std::to_string(quant));
+  }
   // K-quant matrices reach the decode step in their planar layouts (the model re-lays them out
   // at finalize); raw Q6_K remains for tensors the caller hands over unconverted
   switch (quant) {
@@ -667,6 +825,12 @@ int launch_dgemv_dual(int quant1, int quant2, const DGemvArgs& a0, hipStream_t s
   }
 #undef JERO_DUAL
   return check_launch("decode two-tensor gemv");
+}
+
+int dgemv_long_max_k(int quant) {
+  // the activation blocks of a row live in LDS
+  return (quant == JERO_Q8_0 || quant == JERO_Q4_0) ? (kDecodeMaxLongActBytes / 36) * 32
+                                                    : (kDecodeMaxLongActBytes / 292) * 256;
 }
 
 int dgemv_max_k(int quant) {

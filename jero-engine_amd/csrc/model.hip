@@ -342,10 +342,10 @@ extern "C" int jero_hip_model_set_tensor(jero_model* m, const char* name, int qu
   if (rb < 0 || size_t(rb) * size_t(n_out) != nbytes)
     return fail(JERO_ERR_TENSOR_BOUNDS, std::string("set_tensor: '") + name + "' byte size " + std::to_string(nbytes) +
                                             " does not match its shape");
-  if (!norm && !embd && n_in > dgemv_max_k(quant))
+  if (!norm && !embd && n_in > dgemv_long_max_k(quant))
     return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string("set_tensor: '") + name + "' rows of " +
                                                   std::to_string(n_in) + " elements exceed the decode limit " +
-                                                  std::to_string(dgemv_max_k(quant)));
+                                                  std::to_string(dgemv_long_max_k(quant)));
   if (slot->dev) dev_free(m, slot->dev);
   void* p = nullptr;
   int rc = dev_alloc(m, nbytes, &p);

@@ -76,7 +76,8 @@ def _dev_weights(torch, quant, rows, k, gen, dev):
 
 def build_device(spec, dev, seed=0, mix="q4_k_m"):
     """The same model layout as build(), with the quantized matrices generated on the GPU (fast at
-    the 8B shape): {name: (quant, host numpy array, n_in, n_out)} plus {name: device tensor}."""
+    the 8B shape): {name: (quant, host numpy array, n_in, n_out)} plus {name: device tensor}.
+    mix "q8_0": every matrix Q8_0."""
     import torch
     H, F, L, V = spec["hidden"], spec["ffn"], spec["n_layers"], spec["vocab"]
     Q, KV, hd = spec["nq"] * spec["hd"], spec["nkv"] * spec["hd"], spec["hd"]
@@ -87,6 +88,8 @@ def build_device(spec, dev, seed=0, mix="q4_k_m"):
     host, on_dev = {}, {}
 
     def mat(name, quant, n_in, n_out):
+        if mix == "q8_0":
+            quant = Q8_0
         d = _dev_weights(torch, quant, n_out, n_in, gen, dev)
         on_dev[name] = d
         host[name] = (quant, d.cpu().numpy(), n_in, n_out)

@@ -318,3 +318,24 @@ def test_model_errors(dev):
     with pytest.raises(J.K3Error) as ei:
         J.DecodeModel(512, 1024, 1, 100, 8, 3, 64, 1e-6, 1e6, 64)
     assert ei.value.variant == "TensorBoundsError"
+
+
+@pytest.mark.parametrize("mix,spec", [
+    ("q8_0", dict(hidden=5120, ffn=13824, n_layers=2, vocab=1000, nq=40, nkv=8, hd=128, eps=1e-6, theta=1e6)),
+    ("q4_k_m", dict(hidden=512, ffn=20480, n_layers=2, vocab=700, nq=8, nkv=2, hd=64, eps=1e-6, theta=1e6))])
+def test_decode_long_rows(dev, mix, spec):
+    """Projections whose rows are longer than the register-resident decode GEMV takes: a Q8_0
+    model at hidden 5120 / FFN 13824 (every Q8_0 matrix is longer than 4096 elements: the Q|K|V
+    store, SwiGLU, residual and LM-head argmax epilogues all run the long-row kernel), and a Q4_K_M
+    model whose ffn_down rows hold 20480 elements; every layer checked as the other models are."""
+    print(f"decode long rows {mix}", flush=True)
+    t, on_dev = MS.build_device(spec, dev, seed=77, mix=mix)
+    m = J.DecodeModel(spec["hidden"], spec["ffn"], spec["n_layers"], spec["vocab"], spec["nq"], spec["nkv"],
+                      spec["hd"], spec["eps"], spec["theta"], 256, J.KV_F16, True)
+    for name, (quant, arr, n_in, n_out) in t.items():
+        m.set_tensor(name, quant, on_dev.get(name, arr), n_in, n_out)
+    m.finalize()
+    om = O.DecodeModel(spec, MS.oracle_tensors(t), 256)
+    kv = prefill_kv(m, om, spec, 256, 100, 78, dev)
+    DP.run_traced(m, om, t, spec, kv, 256, 100, 3, True, dev, 11)
+    m.close()

@@ -189,7 +189,7 @@ int jero_hip_gqa_attention(float *out_dev, const float *q_dev, const void *k_dev
  * GEMMs read fastest) or jero_hip_repack over all their rows (JERO_Q4_K_R / JERO_Q6_K_R); repacked
  * tensors 16-byte aligned.
  * Outputs y_dev [n_tokens][hidden], sel_idx_dev / sel_w_dev [n_tokens][top_k].
- * hidden <= 2048 for the gate/up pairing; top_k <= 16; n_experts <= 1024.  Workspace:
+ * hidden <= 8192 for the gate/up pairing; top_k <= 16; n_experts <= 1024.  Workspace:
  * jero_hip_moe_workspace_bytes(...) bytes, 256-byte aligned (NULL: library-owned). */
 int jero_hip_moe_ffn(const float *x_dev, const float *router_logits_dev, int64_t n_tokens, int64_t n_experts,
                      int top_k, int gate_quant, const void *gate_dev, size_t gate_bytes, int up_quant,

@@ -1132,13 +1132,22 @@ void gate_up_one(const MoeArgs& a, const MoeLists& L, const MoeSingle& one, hipS
 template <int F, int SPER = 0>
 int gate_up_fmt(const MoeArgs& a, const MoeLists& L, hipStream_t s, const MoeSingle& one = MoeSingle{}) {
   const int U = units_per_row(F, a.hidden);
+  // a gate row and its up row share a wave: at most 32 lanes per row, more units per lane beyond
   switch (lpr_for(U)) {
     case 4: gate_up_one<F, 4, 1, SPER>(a, L, one, s); return JERO_OK;
     case 16: gate_up_one<F, 16, 1, SPER>(a, L, one, s); return JERO_OK;
     case 32: gate_up_one<F, 32, 1, SPER>(a, L, one, s); return JERO_OK;
     default:
+      if (U <= 64) {
+        gate_up_one<F, 32, 2, SPER>(a, L, one, s);
+        return JERO_OK;
+      }
+      if (U <= 128) {
+        gate_up_one<F, 32, 4, SPER>(a, L, one, s);
+        return JERO_OK;
+      }
       return fail(JERO_ERR_CAPABILITY_MISMATCH,
-                  "moe: hidden " + std::to_string(a.hidden) + " above the gate/up pairing limit (2048 for K-quants)");
+                  "moe: hidden " + std::to_string(a.hidden) + " above the gate/up pairing limit (8192 for K-quants)");
   }
 }
 

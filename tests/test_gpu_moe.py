@@ -90,6 +90,20 @@ def test_moe_qwen3_shape(dev, T):
     run_case(dev, T, 128, 2048, 768, 8, J.Q4_K, J.Q6_K, 900 + T, repacked=True)
 
 
+@pytest.mark.parametrize("T", [1, 64])
+def test_moe_hidden_4096(dev, T):
+    """The Qwen3-235B-A22B expert shape: hidden 4096, 128 experts of 1536, top-8 (gate/up rows of
+    64 units: two units per lane of a 32-lane row group)."""
+    print(f"moe hidden 4096 T={T}", flush=True)
+    run_case(dev, T, 128, 4096, 1536, 8, J.Q4_K, J.Q6_K, 950 + T, repacked=True)
+
+
+def test_moe_hidden_8192_small(dev):
+    """Four units per lane (hidden 8192), few experts."""
+    print("moe hidden 8192", flush=True)
+    run_case(dev, 3, 4, 8192, 256, 2, J.Q4_K, J.Q4_K, 960)
+
+
 def test_moe_small_and_q4k_down(dev):
     print("moe small", flush=True)
     run_case(dev, 5, 6, 256, 512, 2, J.Q4_K, J.Q4_K, 40, repacked=True)

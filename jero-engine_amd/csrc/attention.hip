@@ -401,6 +401,284 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
   }
 }
 
+// ---------------------------------------------------------------- f16 rings on MFMA
+
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ h4_t h4_of(uint32_t lo, uint32_t hi) {
+  return __builtin_bit_cast(h4_t, (uint64_t(hi) << 32) | lo);
+}
+
+// The split-K partial for f16 rings on the matrix cores (v_mfma_f32_16x16x16_f16).  Workgroup
+// (split s, kv head h) owns slots [64 s, 64 s + 64) and all (up to 16) q heads of h's group; wave w
+// owns the 16 slots [64 s + 16 w, +16), one MFMA tile.
+//   * Lane l loads 16-byte chunks 4j + l/16 (j < HD/32) of the K row and of the V row of slot
+//     l % 16: a row's chunks come from four consecutive lanes, 64 contiguous bytes per load.
+//   * Scores S^T[slot][head] = sum_d K[slot][d] q[head][d]: A = the K chunks as loaded (16-dim
+//     tile i takes the lane's halves 4i .. 4i+3, i.e. dims 8(4(i/2) + l/16) + 4(i%2) + t), B = q in
+//     the same dim order.  q is split into f16 hi + lo parts (q = hi + lo to 2^-22) and the K
+//     values are exact f16, so two MFMAs per tile give the f32 scores.
+//   * The result lands as lane l: head l % 16, slots 4(l/16) + r -- exactly the A layout of P V
+//     (rows = heads, k = slots), so the softmax numerators p (split hi + lo as q) feed P V with no
+//     data movement.  V needs the k = slot layout: one MFMA against the identity (A = the V chunks
+//     as loaded, B = I) returns V^T tile by tile in that layout, exactly (one non-zero product).
+//   * Slots past the active range score -inf and their V is zeroed before any product (a stale
+//     slot may hold anything).  The softmax max and sum reduce over the 4 lanes of a head.
+//   * Fused (decode step): the q heads are normalised and rotated once per workgroup into LDS (one
+//     wave per head); the workgroup holding the new slot does the same for k, attends to the new
+//     k and v rounded to f16 (the values the ring then holds) and appends them to the ring.
+template <int HD, int MAXG, bool FUSED>
+__global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
+  constexpr int NCH = HD / 32;  // 16-byte chunks per lane per row
+  constexpr int NT = HD / 16;   // 16-dim MFMA tiles
+  constexpr int NW = kAttnThreads / kWave;
+  constexpr int CH = 16 * NW;   // slots per workgroup
+  static_assert(MAXG <= 16 && (HD == 64 || HD == 128), "tile shape");
+  __shared__ __attribute__((aligned(16))) float s_q[16][HD];
+  __shared__ __attribute__((aligned(16))) float s_kn[HD];
+  __shared__ float s_o[NW][MAXG][HD];
+  __shared__ float s_m[NW][16], s_l[NW][16];
+
+  const int split = blockIdx.x, kh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int group = p.group;
+  const int64_t kvd = int64_t(p.nkv) * HD;
+  const int S = gridDim.x;
+  const int p0 = split * CH, w0 = p0 + wv * 16;
+  const int kq = lane >> 4, col = lane & 15;
+
+  // 0. small loads first (they complete before the K/V loads issued after them)
+  int64_t pos_pre = p.pos;
+  if constexpr (FUSED) pos_pre = *(p.pos_dev ? p.pos_dev : reinterpret_cast<const int64_t*>(p.k));
+  // fused: wave w prepares heads w, w + NW, ... as one pair of dims per lane (lanes < HD / 2)
+  constexpr int HPW = (MAXG + NW - 1) / NW;
+  const int pr = lane < HD / 2 ? lane : HD / 2 - 1;
+  float2 qv[HPW];
+#pragma unroll
+  for (int j = 0; j < HPW; j++) {
+    const int h = min(wv + NW * j, group - 1);
+    qv[j] = reinterpret_cast<const float2*>(p.q + (int64_t(kh) * group + h) * HD)[pr];
+  }
+  float2 knv = make_float2(0.f, 0.f), qnw = knv, knw = knv, csv = knv;
+  if constexpr (FUSED) {
+    knv = reinterpret_cast<const float2*>(p.k_new + kh * HD)[pr];
+    qnw = reinterpret_cast<const float2*>(p.q_norm ? p.q_norm : p.q)[pr];
+    knw = reinterpret_cast<const float2*>(p.k_norm ? p.k_norm : p.q)[pr];
+    csv = reinterpret_cast<const float2*>(p.rope_cs ? p.rope_cs : p.q)[pr];
+  }
+  // 1. K and V loads: slot w0 + col, chunks 4j + kq (clamped in-bounds; masked below)
+  const int bound = p.pos_dev ? int(p.capacity) : p.active;
+  const int pl = min(p0 + CH, bound);
+  const int ps = min(w0 + col, pl - 1);
+  const _Float16* kb = static_cast<const _Float16*>(p.k) + int64_t(kh) * HD + int64_t(ps) * kvd;
+  const _Float16* vb = static_cast<const _Float16*>(p.v) + int64_t(kh) * HD + int64_t(ps) * kvd;
+  u32x4 kr[NCH], vr[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; j++) kr[j] = ld4(reinterpret_cast<const uint8_t*>(kb + 8 * (4 * j + kq)));
+#pragma unroll
+  for (int j = 0; j < NCH; j++) vr[j] = ld4(reinterpret_cast<const uint8_t*>(vb + 8 * (4 * j + kq)));
+
+  int active = p.active, slot = p.slot;
+  int64_t pos_now = p.pos;
+  if (p.pos_dev) {
+    pos_now = pos_pre;
+    slot = int(pos_now % p.capacity);
+    active = int(pos_now + 1 < p.capacity ? pos_now + 1 : p.capacity);
+  }
+  if (p0 >= active) {  // empty split: contributes nothing to the merge
+    if (tid < group) {
+      const int h = kh * group + tid;
+      p.part_ml[(int64_t(h) * S + split) * 2 + 0] = -INFINITY;
+      p.part_ml[(int64_t(h) * S + split) * 2 + 1] = 0.f;
+    }
+    return;
+  }
+  const int p1 = min(p0 + CH, active);
+  const bool has_slot = FUSED && slot >= p0 && slot < p1;
+
+  // 2. q heads (fused: QK-norm, RoPE), scaled, into LDS; rows past the group are zero
+  float2 cs = csv;
+  if constexpr (FUSED) {
+    if (!p.rope_cs) {
+      float sn, cn;
+      sincosf(rope_angle(pr, HD, pos_now, p.theta), &sn, &cn);
+      cs = make_float2(cn, sn);
+    }
+  }
+  auto norm_rope = [&](float2 x, bool has_norm, float2 nw) -> float2 {
+    if (has_norm) {
+      const float ss = wave_sum_dpp(lane < HD / 2 ? x.x * x.x + x.y * x.y : 0.f);
+      const float inv = 1.0f / sqrtf(ss / float(HD) + p.eps);
+      x.x = x.x * inv * nw.x;
+      x.y = x.y * inv * nw.y;
+    }
+    return make_float2(x.x * cs.x - x.y * cs.y, x.x * cs.y + x.y * cs.x);
+  };
+#pragma unroll
+  for (int j = 0; j < HPW; j++) {
+    const int h = wv + NW * j;
+    float2 x = qv[j];
+    if constexpr (FUSED) x = norm_rope(x, p.q_norm != nullptr, qnw);
+    if (h < 16 && lane < HD / 2) {
+      const bool real = h < group;
+      reinterpret_cast<float2*>(s_q[h])[lane] = real ? make_float2(x.x * p.scale, x.y * p.scale) : make_float2(0.f, 0.f);
+      if constexpr (FUSED) {
+        if (real && split == 0 && p.tr_q) reinterpret_cast<float2*>(p.tr_q + (int64_t(kh) * group + h) * HD)[lane] = x;
+      }
+    }
+  }
+  for (int h = wv + NW * HPW; h < 16; h += NW)  // rows no wave prepared (MAXG < 16)
+    if (lane < HD / 2) reinterpret_cast<float2*>(s_q[h])[lane] = make_float2(0.f, 0.f);
+  if constexpr (FUSED) {
+    if (has_slot && wv == 0) {
+      const float2 k = norm_rope(knv, p.k_norm != nullptr, knw);
+      if (lane < HD / 2) {
+        reinterpret_cast<float2*>(s_kn)[lane] = k;
+        if (p.tr_k) reinterpret_cast<float2*>(p.tr_k + int64_t(kh) * HD)[lane] = k;
+      }
+    }
+  }
+  lds_barrier();  // LDS only: the K/V loads stay in flight
+
+  // 3. B operands of the scores: q hi / lo in the lanes' dim order
+  h4_t qhi[NT], qlo[NT];
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    const int d = 8 * (4 * (i / 2) + kq) + 4 * (i % 2);
+    const float4 q = *reinterpret_cast<const float4*>(&s_q[col][d]);
+    const float qa[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const _Float16 hi = _Float16(qa[t]);
+      qhi[i][t] = hi;
+      qlo[i][t] = _Float16(qa[t] - float(hi));
+    }
+  }
+  // the new slot's k and v, as f16, replace the ring values in the lane that holds that slot
+  const bool mine = has_slot && w0 + col == slot;
+  if constexpr (FUSED) {
+    if (mine) {
+#pragma unroll
+      for (int j = 0; j < NCH; j++) {
+        const int d = 8 * (4 * j + kq);
+        const float* vn = p.v_new + int64_t(kh) * HD + d;
+        uint32_t kw[4], vw[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          kw[t] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(s_kn[d + 2 * t]))) |
+                  (uint32_t(__builtin_bit_cast(uint16_t, _Float16(s_kn[d + 2 * t + 1]))) << 16);
+          vw[t] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(vn[2 * t]))) |
+                  (uint32_t(__builtin_bit_cast(uint16_t, _Float16(vn[2 * t + 1]))) << 16);
+        }
+        kr[j] = u32x4{kw[0], kw[1], kw[2], kw[3]};
+        vr[j] = u32x4{vw[0], vw[1], vw[2], vw[3]};
+      }
+    }
+  }
+  // a slot past the active range may hold anything: its V row becomes zeros
+  if (w0 + col >= p1) {
+#pragma unroll
+    for (int j = 0; j < NCH; j++) vr[j] = u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // 4. scores: lane holds head col, slots w0 + 4 kq + r
+  f4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    const u32x4 c = kr[i / 2];
+    const h4_t a = (i & 1) ? h4_of(c.z, c.w) : h4_of(c.x, c.y);
+    sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qhi[i], sc, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qlo[i], sc, 0, 0, 0);
+  }
+  float s[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) s[r] = w0 + 4 * kq + r < p1 ? sc[r] : -INFINITY;
+  // 5. the wave's softmax per head: the 4 lanes col, col + 16, col + 32, col + 48
+  float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  float e[4], sum = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    e[r] = mx == -INFINITY ? 0.f : exp_fast(s[r] - mx);
+    sum += e[r];
+  }
+  sum += __shfl_xor(sum, 16, kWave);
+  sum += __shfl_xor(sum, 32, kWave);
+  h4_t phi, plo;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const _Float16 hi = _Float16(e[r]);
+    phi[r] = hi;
+    plo[r] = _Float16(e[r] - float(hi));
+  }
+  // 6. P V: V^T tiles through the identity, then two MFMAs per tile
+  h4_t ident;
+#pragma unroll
+  for (int t = 0; t < 4; t++) ident[t] = _Float16(4 * kq + t == col ? 1.0f : 0.0f);
+  f4_t o[NT];
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    const u32x4 c = vr[i / 2];
+    const h4_t a = (i & 1) ? h4_of(c.z, c.w) : h4_of(c.x, c.y);
+    const f4_t vt = __builtin_amdgcn_mfma_f32_16x16x16f16(a, ident, f4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    h4_t b;
+#pragma unroll
+    for (int t = 0; t < 4; t++) b[t] = _Float16(vt[t]);  // exact: the values are f16
+    o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, b, f4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, b, o[i], 0, 0, 0);
+  }
+  // o[i]: lane holds heads 4 kq + r, the dim of column col of tile i
+  // 7. fused: the workgroup holding the new slot appends k and v to the ring (as f16)
+  if constexpr (FUSED) {
+    if (mine) {
+      _Float16* kw = static_cast<_Float16*>(p.k_write) + int64_t(slot) * kvd + kh * HD;
+      _Float16* vw = static_cast<_Float16*>(p.v_write) + int64_t(slot) * kvd + kh * HD;
+#pragma unroll
+      for (int j = 0; j < NCH; j++) {
+        *reinterpret_cast<u32x4*>(kw + 8 * (4 * j + kq)) = kr[j];
+        *reinterpret_cast<u32x4*>(vw + 8 * (4 * j + kq)) = vr[j];
+      }
+    }
+  }
+  // 8. merge of the four waves
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    // column col of tile i holds dim 8 (4 (i/2) + col/4) + 4 (i%2) + col%4
+    const int d = 8 * (4 * (i / 2) + (col >> 2)) + 4 * (i & 1) + (col & 3);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int h = 4 * kq + r;
+      if (h < MAXG && h < group) s_o[wv][h][d] = o[i][r];
+    }
+  }
+  if (lane < 16) {
+    s_m[wv][lane] = mx;
+    s_l[wv][lane] = sum;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < group * HD; idx += kAttnThreads) {
+    const int h = idx / HD, d = idx % HD;
+    float M = s_m[0][h];
+#pragma unroll
+    for (int w = 1; w < NW; w++) M = fmaxf(M, s_m[w][h]);
+    float ov = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+      const float wt = s_m[w][h] == -INFINITY ? 0.f : exp_fast(s_m[w][h] - M);
+      ov += wt * s_o[w][h][d];
+      L += wt * s_l[w][h];
+    }
+    const int64_t row = int64_t(kh * group + h) * S + split;
+    p.part_o[row * HD + d] = ov;
+    if (d == 0) {
+      p.part_ml[row * 2 + 0] = M;
+      p.part_ml[row * 2 + 1] = L;
+    }
+  }
+}
+
 // Merge of the splits: one workgroup per q head.  Thread (q, g) owns float4 column q of the
 // head and splits s = g (mod SG).  Its first CH partial rows are loaded at entry, before the
 // split weights w_s = exp(m_s - M) are known, so the whole merge costs one round trip to the
@@ -586,6 +864,19 @@ static void launch_partial(const AttnParams& p, int S, hipStream_t s) {
     hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 8>), dim3(S, p.nkv), dim3(kAttnThreads), 0, s, p);
 }
 
+template <int HD, bool FUSED>
+static void launch_mfma(const AttnParams& p, int S, hipStream_t s) {
+  const dim3 grid(S, p.nkv);
+  if (p.group <= 1)
+    hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, FUSED>), grid, dim3(kAttnThreads), 0, s, p);
+  else if (p.group <= 2)
+    hipLaunchKernelGGL((attn_mfma_kernel<HD, 2, FUSED>), grid, dim3(kAttnThreads), 0, s, p);
+  else if (p.group <= 4)
+    hipLaunchKernelGGL((attn_mfma_kernel<HD, 4, FUSED>), grid, dim3(kAttnThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((attn_mfma_kernel<HD, 8, FUSED>), grid, dim3(kAttnThreads), 0, s, p);
+}
+
 template <int HD>
 static void launch_combine(const AttnParams& p, int S, float* out, hipStream_t s) {
   const int nq = p.nkv * p.group;
@@ -601,7 +892,10 @@ int launch_attention(const AttnParams& p0, bool fused, float* out, hipStream_t s
   p.part_ml = p.part_o + size_t(p.nkv) * p.group * S * p.hd;
 #define JERO_ATTN_CASE(HDV)                                                                     \
   if (p.hd == HDV) {                                                                            \
-    if (p.kv_dtype == JERO_KV_F16) {                                                            \
+    if (p.kv_dtype == JERO_KV_F16 && HDV >= 64) {                                               \
+      if (fused) launch_mfma<(HDV >= 64 ? HDV : 64), true>(p, S, s);                            \
+      else launch_mfma<(HDV >= 64 ? HDV : 64), false>(p, S, s);                                 \
+    } else if (p.kv_dtype == JERO_KV_F16) {                                                     \
       if (fused) launch_partial<HDV, _Float16, true>(p, S, s);                                  \
       else launch_partial<HDV, _Float16, false>(p, S, s);                                       \
     } else {                                                                                    \

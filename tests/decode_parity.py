@@ -9,8 +9,9 @@ oracle from the device's own input to that stage, as the device's debug trace re
     the oracle reading the device's activation bytes; residual adds are checked through the GEMV
     (x_out - x_in against the oracle's projection, allowing the f32 rounding of the add);
   * attention within ATTN_TOL = 1e-3, the oracle attending with the device's q over the device's
-    ring (its current slot replaced by the device's f32 k and v, which the kernel attends to
-    before they are rounded into an f16 ring); the ring slot itself must equal the rounded k/v;
+    ring as it stands after the step (the new slot holds the device's k and v, rounded to f16 in
+    an f16 ring: the values the kernel attends to); that slot must equal the device's f32 k and
+    v rounded to the ring's type;
   * RMSNorm (attention, FFN, head) within NORM_TOL of the oracle's f64-accumulated norm, SwiGLU
     within SWIGLU_TOL (f32 against f64 arithmetic);
   * RoPE in two parts: the step's table of (cos, sin) must hold the f32 angles pos / theta^(2i/hd)
@@ -161,9 +162,8 @@ def check_layer(t, spec, D, L, pos, x_next, ring_k, ring_v, kv_f16, qk_norm=True
     rnd = (lambda a: a.astype(np.float16).astype(np.float32)) if kv_f16 else (lambda a: a.astype(np.float32))
     assert np.array_equal(ring_k[slot], rnd(D["k_rope"])), f"layer {L}: K ring slot {slot} is not the new k"
     assert np.array_equal(ring_v[slot], rnd(v_new)), f"layer {L}: V ring slot {slot} is not the new v"
-    kr, vr = ring_k[:active].copy(), ring_v[:active].copy()
-    kr[slot], vr[slot] = D["k_rope"], v_new
-    ref_attn = O.gqa_attention(D["q_rope"], kr, vr, nq, nkv, hd, active, 1.0 / np.sqrt(np.float32(hd)))
+    ref_attn = O.gqa_attention(D["q_rope"], ring_k[:active], ring_v[:active], nq, nkv, hd, active,
+                               1.0 / np.sqrt(np.float32(hd)))
     err["attn"] = rel(D["attn"], ref_attn)
     # Wo + residual
     wq_ = t[p + "attn_output.weight"][0]
@@ -300,12 +300,15 @@ def _adopt(stats, tag, fmt, n, x_or, dev_q8, dev_x):
     return q8_bytes(fmt, n, dev_q8)
 
 
-def oracle_step_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True, threads=16):
+def oracle_step_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True, threads=16, dev_rows=None):
     """The oracle's decode step from hidden state x (the embedding row) and its f32 rings kv,
     adopting the device's activation bytes at each quantization point after tie_flips has
     accounted for every difference, and rotating by the device's RoPE table (check_rope_table
     has bounded its angles by two ulps; the oracle's own powf may differ in the last bit, which
-    at position p moves the rotation by up to ~p * 2.4e-7).  Returns (logits, FlipStats)."""
+    at position p moves the rotation by up to ~p * 2.4e-7).  dev_rows (f16 rings): per layer
+    the device's new (k, v) ring rows; the oracle's own rows, rounded to f16, are accounted
+    against them by f16_tie_flips and the device's rows are attended to.  Returns (logits,
+    FlipStats, f16 flips)."""
     H, F = spec["hidden"], spec["ffn"]
     nq, nkv, hd = spec["nq"], spec["nkv"], spec["hd"]
     Q, KV = nq * hd, nkv * hd
@@ -313,6 +316,7 @@ def oracle_step_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True
     cap = kv.shape[2]
     slot, active = pos % cap, min(pos + 1, cap)
     st = FlipStats()
+    f16_flips = 0
     x = np.asarray(x, np.float32).copy()
     for L, D in enumerate(dev_layers):
         p = f"blk.{L}."
@@ -334,6 +338,10 @@ def oracle_step_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True
         else:
             q = O.rope(q, hd, pos, spec["theta"])
             k = O.rope(k, hd, pos, spec["theta"])
+        if dev_rows is not None:
+            for w, (mine, dev32) in enumerate(((k, D["k_rope"]), (v, D["qkv"][Q + KV:]))):
+                f16_flips += f16_tie_flips(f"layer {L} {'KV'[w]} row", mine, dev32, dev_rows[L][w])[0]
+            k, v = dev_rows[L]
         kv[L, 0, slot], kv[L, 1, slot] = k, v
         att = O.gqa_attention(q, kv[L, 0, :active], kv[L, 1, :active], nq, nkv, hd, active,
                               1.0 / np.sqrt(np.float32(hd)))
@@ -350,7 +358,7 @@ def oracle_step_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True
     xn = O.rmsnorm(x, t["output_norm.weight"][1], eps_ffn)
     fh = act_fmt(t["output.weight"][0])
     hq = _adopt(st, "head input", fh, H, xn, dev_head["q8_head"], dev_head["xn_head"])
-    return _mv(t, "output.weight", hq, threads), st
+    return _mv(t, "output.weight", hq, threads), st, f16_flips
 
 
 def read_ring(m, L, cap, kvd, kv_f16):
@@ -419,21 +427,11 @@ def run_traced(m, om, t, spec, kv, cap, pos0, steps, kv_f16, dev, tok, qk_norm=T
                     worst[k_] = max(worst.get(k_, 0.0), v_)
             eh = check_head(t, spec, dh, got, gtok, threads)
             worst["head_gemv"] = eh["gemv"]
-            ref, st = oracle_step_adopting(t, spec, kv, pos, x0, dl, dh, qk_norm, threads)
+            ref, st, f16_flips = oracle_step_adopting(t, spec, kv, pos, x0, dl, dh, qk_norm, threads,
+                                                      dev_rows if kv_f16 else None)
             free = om.step(kv_free, tok, pos, threads=threads)
-            f16_flips = 0
-            if kv_f16:
-                # the device ring holds the new row in f16: the plain oracle rounds its own; the
-                # adopting oracle takes the device's row once its own rounding is accounted for
+            if kv_f16:  # the device ring holds the new row in f16: so does the plain oracle's
                 kv_free[:, :, pos % cap] = kv_free[:, :, pos % cap].astype(np.float16).astype(np.float32)
-                Q, KV = spec["nq"] * spec["hd"], kvd
-                for L in range(L_n):
-                    dev32 = (dl[L]["k_rope"], dl[L]["qkv"][Q + KV:])
-                    for w in (0, 1):
-                        n16, _ = f16_tie_flips(f"layer {L} {'KV'[w]} row", kv[L, w, pos % cap], dev32[w],
-                                               dev_rows[L][w])
-                        f16_flips += n16
-                        kv[L, w, pos % cap] = dev_rows[L][w]
             err, cs = rel(got, ref), cosine(got, ref)
             ferr, fcs = rel(got, free), cosine(got, free)
             print(f"  pos {pos}: teacher-forced max errors " +

@@ -93,7 +93,7 @@ def test_adopting_step_on_a_faithful_trace():
     # rebuild the pre-step rings: the trace run wrote slot POS
     t2, om2, kv, layers2, head2, logits2 = oracle_trace()
     kv[:, :, POS] = 0
-    ref, st = DP.oracle_step_adopting(t, SPEC, kv, POS, om.embed(17), layers, head, True, threads=4)
+    ref, st, f16 = DP.oracle_step_adopting(t, SPEC, kv, POS, om.embed(17), layers, head, True, threads=4)
     assert st.flips == 0 and st.pre_diff == 0.0
     np.testing.assert_array_equal(ref, logits)
 

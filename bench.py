@@ -8,8 +8,10 @@ weights are GGUF Q4_K tensors re-laid out once at load into the planar Q4_K_R de
 same GEMV straight on the GGUF layout.  The
 step is captured once in a HIP graph and replayed; HIP events on the replay stream time
 the K steps.  `value` is algorithmic bytes (weights + Q8_K activation + f32 output) per
-second over the whole step.  Extra fields: the Q6_K 4096->151936 output head, and the
-per-shape kernel averages.
+second over the whole step.  Extra fields: the Q6_K 4096->151936 output head, the per-shape
+kernel averages, the pure-read ceiling of each shape (one launch that reads the same rotated
+weight bytes and nothing else, jero_hip_read_probe) with the GEMV's ratio to it, and the Q8_0 x Q8_0
+4096x4096 GEMV with its own ceiling and CPU line.
 
 roofline: the Q4_K GEMV kernel (all three shapes): algorithmic bytes per launch over the
 average launch duration measured with events; peak = 8 TB/s HBM.
@@ -70,6 +72,23 @@ def synth_weights(torch, J, quant, n_in, n_out, copies, dev, seed):
         sc = torch.randint(-64, 64, (copies, nb, 16), dtype=torch.int8, device=dev, generator=g)
         v[:, :, 192:208] = sc.view(torch.uint8)
     return buf
+
+
+def q8_0_weights(torch, n_in, n_out, copies, dev, seed):
+    """Q8_0 weights quantized from N(0, 0.02) floats (32-element blocks: f16 d = max|x|/127, int8
+    round-to-nearest of x/d); 4 distinct matrices, their bytes repeated over `copies` buffers."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    mats = []
+    for _ in range(min(4, copies)):
+        x = (0.02 * torch.randn(n_out, n_in // 32, 32, generator=g, device=dev)).float()
+        d = (x.abs().amax(dim=2, keepdim=True) / 127.0).half()
+        q = torch.where(d.float() > 0, torch.round(x / d.float()), torch.zeros_like(x)).clamp(-127, 127)
+        blk = torch.cat([d.view(torch.uint8).view(n_out, n_in // 32, 2),
+                         q.to(torch.int8).view(torch.uint8)], dim=2)
+        mats.append(blk.reshape(-1))
+        del x, d, q
+    return [mats[c % len(mats)].clone() for c in range(copies)]
 
 
 def time_graph(torch, fn, steps, warmup, stream):
@@ -309,6 +328,54 @@ def bench_moe(torch, J, dev, stream, steps):
     return out
 
 
+def bench_q8_0(torch, J, dev, stream, steps, warmup, keep_host):
+    """Q8_0 x Q8_0 GEMV 4096x4096, batch 1 (weights N(0,0.02) quantized to Q8_0, activation N(0,1)
+    quantized to the 32-element Q8 activation blocks), copies rotating over >= 768 MB; with the
+    pure-read ceiling over the same buffers."""
+    n_in = n_out = 4096
+    nbytes = J.row_bytes(J.Q8_0, n_in) * n_out
+    copies = max(2, int(-(-ROTATE_BYTES // nbytes)))
+    bufs = q8_0_weights(torch, n_in, n_out, copies, dev, 4000)
+    views = [J.TensorView("w", J.Q8_0, [n_in, n_out], b) for b in bufs]
+    x = torch.randn(n_in, generator=torch.Generator(device=dev).manual_seed(4001), device=dev)
+    xq = J.quantize_act(J.ACT_Q8, x)
+    y = torch.empty(n_out, dtype=torch.float32, device=dev)
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    cnt = [0]
+
+    def one():
+        J.matvec(views[cnt[0] % copies], xq, y, stream=stream)
+        cnt[0] += 1
+
+    def probe():
+        J.read_probe(bufs[cnt[0] % copies], sink, stream=stream)
+        cnt[0] += 1
+
+    t = time_graph(torch, one, steps, warmup, stream)
+    tc = time_graph(torch, probe, steps, warmup, stream)
+    algo = nbytes + J.row_bytes(J.ACT_Q8, n_in) + 4 * n_out
+    res = {"workload": "Q8_0 x Q8_0 GEMV 4096x4096, batch 1", "us": round(t * 1e6, 3),
+           "GB_s": round(algo / t / 1e9, 1), "bytes": algo, "frac_hbm": round(algo / t / 1e9 / HBM_PEAK_GBS, 4),
+           "read_ceiling_us": round(tc * 1e6, 3), "gemv_over_ceiling": round(tc / t, 4)}
+    host = (bufs[0].cpu().numpy(), xq.cpu().numpy()) if keep_host else None
+    del bufs, views
+    return res, host
+
+
+def cpu_q8_0_baseline(O, host, budget_s=5.0):
+    """The oracle's Q8_0 GEMV (matvec_any row chunks, scalar, pthreads over all host cores)."""
+    w, xq = host
+    threads = len(os.sched_getaffinity(0))
+    done, t0 = 0, time.perf_counter()
+    while True:
+        O.matvec(O.Q8_0, w, 4096, 4096, xq, threads=threads)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return (w.size + xq.size + 4 * 4096) * done / el / 1e9, threads, done, el
+
+
 def cpu_decode_baseline(O, host, host_kv, budget_s=10.0):
     """The oracle's decode step (execute_token_standard_with_hidden restated in C, scalar,
     pthreads over all host cores) on the same weights and KV values (widened to f32)."""
@@ -434,6 +501,22 @@ def main():
             table[f"{n_in}x{n_out}"] = {"us": round(t * 1e6, 3), "GB_s": round(algo[i] / t / 1e9, 1),
                                         "bytes": algo[i],
                                         "dist": time_graph_dist(torch, one, len(vlist[i]), 21, stream)}
+    # pure-read ceiling: one launch per shape reading the same rotated buffers and nothing else
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    ceiling = {}
+    for i, (n_in, n_out) in enumerate(SHAPES):
+        cnt = [0]
+
+        def probe(i=i, cnt=cnt):
+            vv = views[i]
+            J.read_probe(vv[cnt[0] % len(vv)].data, sink, stream=stream)
+            cnt[0] += 1
+
+        tc = time_graph(torch, probe, args.steps, args.warmup, stream)
+        key = f"{n_in}x{n_out}"
+        per_shape[key]["read_ceiling_us"] = round(tc * 1e6, 3)
+        per_shape[key]["gemv_over_ceiling"] = round(tc * 1e6 / per_shape[key]["us"], 4)
+        ceiling[key] = tc
     gemv_launch_us = t_step * 1e6 / len(SHAPES)
     achieved = (step_bytes / len(SHAPES)) / (gemv_launch_us * 1e-6) / 1e9
 
@@ -458,6 +541,10 @@ def main():
             "frac_hbm": round(h_algo / th / 1e9 / HBM_PEAK_GBS, 4)}
     del hv
 
+    # ---- Q8_0 4096x4096 (the reference's CPU-runnable case; extra)
+    q8_0, q8host = bench_q8_0(torch, J, dev, stream, args.steps, args.warmup, not args.no_cpu)
+    torch.cuda.empty_cache()
+
     # ---- CPU baseline: the oracle's GEMV on the same three shapes
     cpu = None
     if not args.no_cpu:
@@ -468,6 +555,12 @@ def main():
         cpu = {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
                "sample": f"{reps} passes over the three Q4_K shapes (66.2 MB of weights, full size), "
                          f"{el:.1f} s, C restatement of matvec_any row chunks, scalar, pthreads"}
+
+    if q8host is not None:
+        import pyoracle as O
+        gbs, threads, reps, el = cpu_q8_0_baseline(O, q8host)
+        q8_0["cpu_baseline"] = {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+                                "sample": f"{reps} full GEMVs, {el:.1f} s, C restatement of matvec_any row chunks"}
 
     # ---- prefill GEMM (extra)
     gemm = None
@@ -522,6 +615,11 @@ def main():
         "cpu_baseline": cpu,
         "per_shape": per_shape,
         "per_shape_gguf": per_shape_gguf,
+        "read_ceiling": {"what": "one launch per shape that only reads the same rotated weight bytes "
+                                 "(jero_hip_read_probe); per_shape[...].gemv_over_ceiling = ceiling / GEMV time",
+                         "step_us": round(sum(ceiling.values()) * 1e6, 3),
+                         "gemv_step_over_ceiling": round(sum(ceiling.values()) / t_step, 4)},
+        "q8_0_4096": q8_0,
         "q6k_head": head,
         "prefill_gemm": gemm,
         "moe": moe,

@@ -12,14 +12,16 @@
 // v_mfma_f32_32x32x16_f16 over the 16 bsums (|bsum| <= 2032 and m <= 63 are exact in f16, the
 // sums stay below 2^24).  The scales are applied once per block in f32.
 //
-// Tiling: a workgroup of 4 waves owns a 128 (tokens) x 128 (weight rows) tile; each wave a
-// 64 x 64 quadrant of 2 x 2 MFMA tiles.  Per block, the 128 activation rows (int8 + bsums + d)
-// and the 128 weight rows (expanded to the two planes, mins and scales) are staged in LDS; the
-// global loads of block b+1 are in flight while block b runs.  Workgroups are mapped so that
-// the ones sharing a weight tile run on one XCD (one L2).
+// Tiling: a workgroup of 8 waves (two per SIMD) owns a 128 (tokens) x 128 (weight rows) tile;
+// each wave a 64 x 32 piece of 2 x 1 MFMA tiles.  Per block, the 128 activation rows (int8 +
+// bsums + d) and the 128 weight rows as raw Q4_K bytes are staged in LDS, double-buffered: the
+// global loads of block b+1 are in flight while block b runs.  Each lane expands its own weight
+// fragments to the two int8 planes and decodes its row's scales in registers.  Workgroups are
+// mapped so that the ones sharing a weight tile run on one XCD (one L2).
 //
-// int8 x int8 -> int32 (ForwardExec::matmul, src/forward.rs:555-655, 763-811): the same
-// 128 x 128 workgroup tile, 256-wide K steps, one v_mfma_i32_32x32x32_i8 per 32 K.
+// int8 x int8 -> int32 (ForwardExec::matmul, src/forward.rs:555-655, 763-811): a workgroup of
+// 4 waves on the same 128 x 128 tile (each wave a 64 x 64 quadrant of 2 x 2 MFMA tiles),
+// 256-wide K steps, one v_mfma_i32_32x32x32_i8 per 32 K.
 #include <algorithm>
 #include <string>
 

@@ -1,0 +1,44 @@
+// probe.hip -- measurement probe: the bandwidth ceiling of one launch that only reads.
+//
+// Not part of the hot path.  A GEMV launch of B weight bytes cannot finish faster than a kernel
+// that reads the same B bytes with the same launch cost and nothing else to do; this kernel is
+// that reader, so a benchmark can report each GEMV against it.  Two 16-byte loads per thread
+// (a workgroup reads 8 KiB: threads t and t + 256 of its chunk; one, four, eight or sixteen loads
+// per thread measured 2-10 % slower at 9-28 MB), 256-thread workgroups covering the buffer; the
+// loaded words are folded by XOR over the wave and written only when they equal a value no weight
+// buffer holds in practice, so the loads stay but no bytes are written.
+#include "jero_common.h"
+#include "runtime.h"
+
+namespace jero {
+
+namespace {
+
+__global__ void __launch_bounds__(256) read_probe_kernel(const u32x4* __restrict__ src, int64_t n16,
+                                                         uint32_t* __restrict__ sink) {
+  const int64_t i = int64_t(blockIdx.x) * 512 + threadIdx.x;
+  const u32x4 v = src[i < n16 ? i : n16 - 1];
+  const u32x4 u = src[i + 256 < n16 ? i + 256 : n16 - 1];
+  uint32_t h = v.x ^ v.y ^ v.z ^ v.w ^ u.x ^ u.y ^ u.z ^ u.w;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) h ^= __shfl_xor(h, off, kWave);
+  if (h == 0x9E3779B9u && (threadIdx.x & 63) == 0) sink[blockIdx.x & 255] = h;
+}
+
+}  // namespace
+
+}  // namespace jero
+
+using namespace jero;
+
+extern "C" int jero_hip_read_probe(const void* src_dev, size_t bytes, uint32_t* sink_dev, void* stream) {
+  if (!src_dev || !sink_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "read_probe: null pointer");
+  if ((reinterpret_cast<uintptr_t>(src_dev) & 15u) || bytes % 16 || bytes == 0)
+    return fail(JERO_ERR_INVALID_ARGUMENT, "read_probe: buffer must be 16-byte aligned, a non-zero multiple of 16");
+  const int64_t n16 = int64_t(bytes / 16);
+  const int64_t blocks = (n16 + 511) / 512;
+  if (blocks > INT32_MAX) return fail(JERO_ERR_TENSOR_BOUNDS, "read_probe: buffer too large");
+  hipLaunchKernelGGL(read_probe_kernel, dim3(unsigned(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4*>(src_dev), n16, sink_dev);
+  return check_launch("read_probe");
+}

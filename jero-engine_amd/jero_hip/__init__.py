@@ -50,6 +50,7 @@ _SIGS = {
     "jero_hip_vec_dot": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _SZ, _P]),
     "jero_hip_matvec_partials": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P, _P]),
     "jero_hip_vec_dot_noalloc": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _P, _P]),
+    "jero_hip_read_probe": (_I32, [_P, _SZ, _P, _P]),
     "jero_hip_weights_register": (_I32, [_P, _SZ, C.POINTER(_P)]),
     "jero_hip_weights_lookup": (_I32, [_P, _SZ, C.POINTER(_P)]),
     "jero_hip_weights_release_all": (_I32, []),
@@ -293,6 +294,13 @@ def vec_dot_noalloc(out, weights, inp, stream=None):
     check(lib().jero_hip_vec_dot_noalloc(weights.quant, _ptr(weights.data), weights.nbytes(), inp.numel(),
                                          out.numel(), _ptr(inp), _ptr(out), _stream(stream)))
     return out
+
+
+def read_probe(buf, sink, stream=None):
+    """One launch that only reads buf's bytes (jero_hip_read_probe): the bandwidth ceiling of a
+    kernel over the same bytes.  sink: >= 1 KiB device tensor."""
+    assert sink.numel() * sink.element_size() >= 1024
+    check(lib().jero_hip_read_probe(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink), _stream(stream)))
 
 
 def matvec_f32(out, weights, inp, **kw):

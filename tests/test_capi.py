@@ -66,3 +66,13 @@ def test_quantize_argument_errors():
     assert lib.jero_hip_quantize_act(J.Q4_K, fake, 1, 256, fake, None) == 10
     assert lib.jero_hip_quantize_act(J.Q8_K, fake, 1, 100, fake, None) == 14
     assert lib.jero_hip_quantize_act(J.Q8_K, None, 1, 256, fake, None) == 21
+
+
+def test_read_probe_argument_errors():
+    lib = J.lib()
+    fake = C.c_void_p(0x10000)
+    assert lib.jero_hip_read_probe(None, 1024, fake, None) == 21
+    assert lib.jero_hip_read_probe(fake, 1024, None, None) == 21
+    assert lib.jero_hip_read_probe(C.c_void_p(0x10008), 1024, fake, None) == 21  # misaligned
+    assert lib.jero_hip_read_probe(fake, 1000, fake, None) == 21  # not a multiple of 16
+    assert lib.jero_hip_read_probe(fake, 0, fake, None) == 21

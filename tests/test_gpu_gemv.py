@@ -307,3 +307,14 @@ def test_long_rows(dev, quant, n_in, n_out):
         torch.cuda.synchronize()
         np.testing.assert_array_equal(part.cpu().numpy(), pp)
         assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("nbytes", [16, 8192, 8192 + 48, 9458240])
+def test_read_probe_reads_and_leaves_sink(dev, nbytes):
+    """The bandwidth probe runs over any 16-byte multiple (partial last workgroup included) and
+    writes nothing for data whose wave XOR is not its sentinel."""
+    buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    sink = torch.full((256,), 7, dtype=torch.int32, device=dev)
+    J.read_probe(buf, sink)
+    torch.cuda.synchronize()
+    assert bool((sink == 7).all())

@@ -144,6 +144,39 @@ int jero_hip_gemm(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, in
 int jero_hip_gemm_i8(const int8_t *x_dev, int64_t m, int64_t k, const int8_t *w_dev, int64_t n, int32_t *out_dev,
                      void *stream);
 
+/* requant_all(&ForwardExec::matmul(..), shift) (src/forward.rs:813-815, called at :957-970) in one
+ * launch: jero_hip_gemm_i8's int32 sums requantized as forward.rs's requant (:345-350) does,
+ * out[m][n] = clamp((acc + 2^(shift-1)) >> shift, -127, 127) as int8 row-major; the add wraps as
+ * two's complement (the reference's release build), the shift is arithmetic.  shift in 1..31. */
+int jero_hip_gemm_i8_requant(const int8_t *x_dev, int64_t m, int64_t k, const int8_t *w_dev, int64_t n, int shift,
+                             int8_t *out_dev, void *stream);
+/* requant_all (src/forward.rs:813-815) alone: n int32 -> int8, as above. */
+int jero_hip_requant_i8(const int32_t *raw_dev, int64_t n, int shift, int8_t *out_dev, void *stream);
+
+/* The packed-tile form of the int8 product, the ime::{TILE_*, tile_count, pack_tiles,
+ * gemm_i8_ime} names forward.rs imports (src/forward.rs:26-29, used at :365-372, :569, :779-796).
+ * Tiles of JERO_TILE_N rows (weights) or JERO_TILE_M rows (activations), K in chunks of
+ * JERO_TILE_K.  Packed layout: element (r, c) of a [rows][k] matrix, rows padded with zero rows
+ * to jero_hip_tile_count(rows) whole tiles, sits at byte
+ *   ((r / 8 * (k / 32) + c / 32) * 8 + r % 8) * 32 + c % 32. */
+#define JERO_TILE_M 8
+#define JERO_TILE_N 8
+#define JERO_TILE_K 32
+#define JERO_TILE_C 64
+/* ime::tile_count: whole tiles covering `rows` rows. */
+int64_t jero_hip_tile_count(int64_t rows);
+/* ime::pack_tiles: src_dev [rows][k] int8 row-major -> dst_dev, jero_hip_tile_count(rows) * 8 * k
+ * bytes in the packed layout; k a multiple of 32. */
+int jero_hip_pack_tiles(const int8_t *src_dev, int64_t rows, int64_t k, int8_t *dst_dev, void *stream);
+/* ime::gemm_i8_ime(a, m_tiles, packed_w, tile_begin..tile_end, k_chunks, |mt, nt, &[i32; TILE_C]|):
+ * the C block of every activation tile mt < m_tiles and weight tile nt in [tile_begin, tile_end),
+ * C[i * 8 + j] = sum_k a[8 mt + i][k] * w[8 nt + j][k] (exact int32), written to c_dev as
+ * [m_tiles][tile_end - tile_begin][JERO_TILE_C]; the callback then reads block (mt, nt) at
+ * (mt * (tile_end - tile_begin) + nt - tile_begin) * 64.  Both operands packed (4-byte aligned),
+ * k = 32 * k_chunks <= 131071. */
+int jero_hip_gemm_i8_tiles(const int8_t *a_packed_dev, int64_t m_tiles, const int8_t *w_packed_dev, int64_t tile_begin,
+                           int64_t tile_end, int64_t k_chunks, int32_t *c_dev, void *stream);
+
 /* Load-time re-layout of a weight tensor for the GEMV kernels; replaces repack_tensor_parallel
  * (src/weights.rs:914-955) -> RepackedWeight.  Q4_K -> JERO_Q4_K_R and Q6_K -> JERO_Q6_K_R:
  * the n_out x n_in tensor's bytes are regrouped into 16-byte aligned planes of the same total
@@ -171,8 +204,9 @@ int jero_hip_repack_experts(int quant, const void *src_dev, size_t src_bytes, in
  * aligned);
  * k_dev, v_dev: [seq_len][n_heads_kv * head_dim] of kv_dtype (16-byte aligned); out_dev:
  * [n_heads_q][head_dim] f32.  head_dim in {32, 64, 128}; at most 8 q heads per kv head.
- * seq_len <= 131072.  Workspace: n_heads_q * ceil(seq_len/64) * (head_dim + 2) floats, 16-byte
+ * seq_len <= JERO_MAX_ATTENTION_POSITIONS, else ContextLengthExceeded.  Workspace: n_heads_q * ceil(seq_len/64) * (head_dim + 2) floats, 16-byte
  * aligned (NULL: library-owned, calls must not overlap on one device). */
+#define JERO_MAX_ATTENTION_POSITIONS 131072
 int jero_hip_gqa_attention(float *out_dev, const float *q_dev, const void *k_dev, const void *v_dev, int kv_dtype,
                            int n_heads_q, int n_heads_kv, int head_dim, int64_t seq_len, float scale,
                            void *workspace_dev, size_t workspace_bytes, void *stream);

@@ -914,6 +914,8 @@ int launch_attention(const AttnParams& p0, bool fused, float* out, hipStream_t s
   return check_launch("attention combine");
 }
 
+static_assert(int64_t(kMaxSplits) * attn_chunk(64) == JERO_MAX_ATTENTION_POSITIONS, "attention position limit");
+
 int check_attention_shape(int nq, int nkv, int hd, int64_t seq_len) {
   if (nq <= 0 || nkv <= 0 || hd <= 0 || seq_len <= 0)
     return fail(JERO_ERR_TENSOR_BOUNDS, "attention: empty heads or sequence");

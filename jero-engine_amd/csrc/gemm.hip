@@ -21,7 +21,10 @@
 //
 // int8 x int8 -> int32 (ForwardExec::matmul, src/forward.rs:555-655, 763-811): a workgroup of
 // 4 waves on the same 128 x 128 tile (each wave a 64 x 64 quadrant of 2 x 2 MFMA tiles),
-// 256-wide K steps, one v_mfma_i32_32x32x32_i8 per 32 K.
+// 256-wide K steps, one v_mfma_i32_32x32x32_i8 per 32 K.  The operands are row-major or in the
+// packed tile layout of jero_hip_pack_tiles (read in place: the loader computes each 16-byte
+// piece's address); the epilogue writes int32 rows, int8 rows requantized as forward.rs's
+// `requant` (:345-350) does, or tile-major 8 x 8 blocks for gemm_i8_ime's callback (:779-796).
 #include <algorithm>
 #include <string>
 
@@ -232,20 +235,41 @@ struct __attribute__((aligned(16))) I8Stage {
   int8_t b[kGemmBN][kPlaneStride];
 };
 
+// Packed tile layout (jero_hip_pack_tiles): element (r, c) of a [rows][K] int8 matrix, rows
+// padded with zero rows to whole tiles of kTileRows, K a multiple of kTileK, sits at byte
+//   ((r / kTileRows * (K / kTileK) + c / kTileK) * kTileRows + r % kTileRows) * kTileK + c % kTileK
+// i.e. tile by tile, each tile's K chunks in order, each chunk its rows' kTileK bytes in order.
+constexpr int kTileRows = 8, kTileK = 32;
+
+__device__ __forceinline__ int64_t packed_offset(int r, int c, int K) {
+  return ((int64_t(r / kTileRows) * (K / kTileK) + c / kTileK) * kTileRows + r % kTileRows) * kTileK + c % kTileK;
+}
+
 // 256 K-bytes of a row of 128 rows, 2 threads per row: 8 loads of 16 bytes each.  Chunks at or
 // past k are zero; rows past `rows` read row rows-1.
+template <bool PACKED>
 __device__ __forceinline__ void i8_load(u32x4 (&r)[8], const int8_t* __restrict__ p, int64_t ld, int row0, int rows,
                                         int k0, int K) {
   const int t = threadIdx.x, rr = t >> 1, h = t & 1;
   const int row = min(row0 + rr, rows - 1);
-  const uint8_t* base = reinterpret_cast<const uint8_t*>(p) + int64_t(row) * ld;
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(p) + (PACKED ? 0 : int64_t(row) * ld);
 #pragma unroll
   for (int i = 0; i < 8; i++) {
     const int kk = k0 + 128 * h + 16 * i;
-    const u32x4 v = ld4(base + min(kk, K - 16));
+    const int kc = min(kk, K - 16);
+    const u32x4 v = ld4(base + (PACKED ? packed_offset(row, kc, K) : kc));
     r[i] = kk < K ? v : u32x4{0u, 0u, 0u, 0u};
   }
 }
+
+// forward.rs's requant (:345-350): (v + 2^(shift-1)) >> shift, clamped to [-127, 127]; the add
+// wraps as two's complement (the reference's release build), the shift is arithmetic.
+__device__ __forceinline__ int8_t requant_i8(int32_t v, int shift) {
+  const int32_t r = int32_t(uint32_t(v) + (uint32_t(1) << (shift - 1))) >> shift;
+  return int8_t(r < -127 ? -127 : r > 127 ? 127 : r);
+}
+
+enum { kI8OutI32 = 0, kI8OutRequant = 1, kI8OutTiles = 2 };
 
 __device__ __forceinline__ void i8_store(const u32x4 (&r)[8], int8_t (*dst)[kPlaneStride]) {
   const int t = threadIdx.x, rr = t >> 1, h = t & 1;
@@ -253,8 +277,11 @@ __device__ __forceinline__ void i8_store(const u32x4 (&r)[8], int8_t (*dst)[kPla
   for (int i = 0; i < 8; i++) *reinterpret_cast<u32x4*>(&dst[rr][128 * h + 16 * i]) = r[i];
 }
 
+// EPI kI8OutI32: out int32 [M][N]; kI8OutRequant: out int8 [M][N], requant_i8(., shift);
+// kI8OutTiles: out int32 blocks [M / 8][N / 8][8 * 8], block (m / 8, n / 8) element (m % 8) * 8 + n % 8.
+template <bool PACKED, int EPI>
 __global__ void __launch_bounds__(kGemmThreads) gemm_i8_kernel(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
-                                                                int M, int N, int K, int32_t* __restrict__ out) {
+                                                                int M, int N, int K, void* __restrict__ out, int shift) {
   __shared__ I8Stage S;
   const int n_tiles_m = (M + kGemmBM - 1) / kGemmBM;
   int tm, tn;
@@ -271,16 +298,16 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_i8_kernel(const int8_t* __r
 #pragma unroll
       for (int v = 0; v < 16; v++) C[i][k][v] = 0;
   u32x4 ra[8], rb[8];
-  i8_load(ra, x, K, m0, M, 0, K);
-  i8_load(rb, w, K, n0, N, 0, K);
+  i8_load<PACKED>(ra, x, K, m0, M, 0, K);
+  i8_load<PACKED>(rb, w, K, n0, N, 0, K);
   i8_store(ra, S.a);
   i8_store(rb, S.b);
   __syncthreads();
   for (int k0 = 0; k0 < K; k0 += 256) {
     const bool more = k0 + 256 < K;
     if (more) {
-      i8_load(ra, x, K, m0, M, k0 + 256, K);
-      i8_load(rb, w, K, n0, N, k0 + 256, K);
+      i8_load<PACKED>(ra, x, K, m0, M, k0 + 256, K);
+      i8_load<PACKED>(rb, w, K, n0, N, k0 + 256, K);
     }
     const int steps = min(8, (K - k0 + 31) / 32);
     for (int j = 0; j < steps; j++) {
@@ -310,14 +337,25 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_i8_kernel(const int8_t* __r
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int m = m0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
-        if (m < M && n < N) out[int64_t(m) * N + n] = C[i][k][v];
+        if (m < M && n < N) {
+          if constexpr (EPI == kI8OutI32) {
+            static_cast<int32_t*>(out)[int64_t(m) * N + n] = C[i][k][v];
+          } else if constexpr (EPI == kI8OutRequant) {
+            static_cast<int8_t*>(out)[int64_t(m) * N + n] = requant_i8(C[i][k][v], shift);
+          } else {
+            const int64_t blk = int64_t(m / kTileRows) * (N / kTileRows) + n / kTileRows;
+            static_cast<int32_t*>(out)[blk * kTileRows * kTileRows + (m % kTileRows) * kTileRows + n % kTileRows] =
+                C[i][k][v];
+          }
+        }
       }
     }
 }
 
-// K not a multiple of 16: one output per thread, byte loads.
+// K not a multiple of 16: one output per thread, byte loads (EPI: kI8OutI32 or kI8OutRequant).
+template <int EPI>
 __global__ void __launch_bounds__(256) gemm_i8_small_kernel(const int8_t* __restrict__ x, const int8_t* __restrict__ w,
-                                                             int M, int N, int K, int32_t* __restrict__ out) {
+                                                             int M, int N, int K, void* __restrict__ out, int shift) {
   const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= int64_t(M) * N) return;
   const int m = int(idx / N), n = int(idx % N);
@@ -325,10 +363,60 @@ __global__ void __launch_bounds__(256) gemm_i8_small_kernel(const int8_t* __rest
   const int8_t* wb = w + int64_t(n) * K;
   int32_t s = 0;
   for (int k = 0; k < K; k++) s += int32_t(xa[k]) * int32_t(wb[k]);
-  out[idx] = s;
+  if constexpr (EPI == kI8OutI32) static_cast<int32_t*>(out)[idx] = s;
+  else static_cast<int8_t*>(out)[idx] = requant_i8(s, shift);
+}
+
+__global__ void __launch_bounds__(256) requant_kernel(const int32_t* __restrict__ raw, int64_t n, int shift,
+                                                       int8_t* __restrict__ out) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = requant_i8(raw[i], shift);
+}
+
+// One thread per byte of the packed matrix: the byte of element (r, c), or 0 for padding rows.
+__global__ void __launch_bounds__(256) pack_tiles_kernel(const int8_t* __restrict__ src, int64_t rows, int K,
+                                                          int64_t total, int8_t* __restrict__ dst) {
+  const int64_t o = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (o >= total) return;
+  const int kk = int(o % kTileK);
+  const int64_t q = o / kTileK;
+  const int i = int(q % kTileRows);
+  const int64_t tc = q / kTileRows;
+  const int kc = int(tc % (K / kTileK));
+  const int64_t r = (tc / (K / kTileK)) * kTileRows + i;
+  dst[o] = r < rows ? src[r * K + int64_t(kc) * kTileK + kk] : int8_t(0);
 }
 
 int gemm_tiles(int64_t M, int64_t N) { return int(((M + kGemmBM - 1) / kGemmBM) * ((N + kGemmBN - 1) / kGemmBN)); }
+
+// Shared argument checks of the int8 products: sizes within 32-bit tile indexing and no int32
+// sum able to overflow (|x w| <= 128 * 128 per term).
+static int check_i8_args(const void* x, int64_t m, int64_t k, const void* w, int64_t n, const void* out,
+                         const char* who) {
+  if (!x || !w || !out) return fail(JERO_ERR_INVALID_ARGUMENT, std::string(who) + ": null pointer");
+  if (m <= 0 || n <= 0 || k <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, std::string(who) + ": empty operand");
+  if (m > (int64_t(1) << 24) || n > (int64_t(1) << 24) || k > (int64_t(1) << 24))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string(who) + ": m, n, k above 2^24");
+  if (k * 128 * 128 > INT32_MAX)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string(who) + ": k=" + std::to_string(k) + " could overflow int32 sums");
+  return JERO_OK;
+}
+
+template <int EPI>
+static int launch_gemm_i8(const int8_t* x, int64_t m, int64_t k, const int8_t* w, int64_t n, void* out, int shift,
+                          hipStream_t s) {
+  int rc = check_i8_args(x, m, k, w, n, out, "gemm_i8");
+  if (rc) return rc;
+  if (k % 16 == 0 && aligned4(x) && aligned4(w)) {
+    hipLaunchKernelGGL((gemm_i8_kernel<false, EPI>), dim3(unsigned(gemm_tiles(m, n))), dim3(kGemmThreads), 0, s, x, w,
+                       int(m), int(n), int(k), out, shift);
+    return check_launch("gemm i8");
+  }
+  const int64_t total = m * n;
+  hipLaunchKernelGGL((gemm_i8_small_kernel<EPI>), dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, x, w, int(m),
+                     int(n), int(k), out, shift);
+  return check_launch("gemm i8 (small k)");
+}
 
 }  // namespace jero
 
@@ -362,21 +450,52 @@ extern "C" int jero_hip_gemm(int quant, const void* w_dev, size_t w_bytes, int64
 
 extern "C" int jero_hip_gemm_i8(const int8_t* x_dev, int64_t m, int64_t k, const int8_t* w_dev, int64_t n,
                                 int32_t* out_dev, void* stream) {
-  if (!x_dev || !w_dev || !out_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "gemm_i8: null pointer");
-  if (m <= 0 || n <= 0 || k <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "gemm_i8: empty operand");
-  if (m > (int64_t(1) << 24) || n > (int64_t(1) << 24) || k > (int64_t(1) << 24))
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, "gemm_i8: m, n, k above 2^24");
-  if (k * 128 * 128 > INT32_MAX)
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, "gemm_i8: k=" + std::to_string(k) + " could overflow int32 sums");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (k % 16 == 0 && !(reinterpret_cast<uintptr_t>(x_dev) & 3u) && !(reinterpret_cast<uintptr_t>(w_dev) & 3u)) {
-    const int tiles = gemm_tiles(m, n);
-    hipLaunchKernelGGL(gemm_i8_kernel, dim3(unsigned(tiles)), dim3(kGemmThreads), 0, s, x_dev, w_dev, int(m), int(n),
-                       int(k), out_dev);
-    return check_launch("gemm i8");
-  }
-  const int64_t total = m * n;
-  hipLaunchKernelGGL(gemm_i8_small_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, x_dev, w_dev, int(m),
-                     int(n), int(k), out_dev);
-  return check_launch("gemm i8 (small k)");
+  return launch_gemm_i8<kI8OutI32>(x_dev, m, k, w_dev, n, out_dev, 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int jero_hip_gemm_i8_requant(const int8_t* x_dev, int64_t m, int64_t k, const int8_t* w_dev, int64_t n,
+                                        int shift, int8_t* out_dev, void* stream) {
+  if (shift < 1 || shift > 31) return fail(JERO_ERR_INVALID_ARGUMENT, "gemm_i8_requant: shift must be in 1..31");
+  return launch_gemm_i8<kI8OutRequant>(x_dev, m, k, w_dev, n, out_dev, shift, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int jero_hip_requant_i8(const int32_t* raw_dev, int64_t n, int shift, int8_t* out_dev, void* stream) {
+  if (!raw_dev || !out_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "requant_i8: null pointer");
+  if (shift < 1 || shift > 31) return fail(JERO_ERR_INVALID_ARGUMENT, "requant_i8: shift must be in 1..31");
+  if (n <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "requant_i8: empty input");
+  hipLaunchKernelGGL(requant_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     raw_dev, n, shift, out_dev);
+  return check_launch("requant_i8");
+}
+
+extern "C" int64_t jero_hip_tile_count(int64_t rows) { return rows <= 0 ? 0 : (rows + kTileRows - 1) / kTileRows; }
+
+extern "C" int jero_hip_pack_tiles(const int8_t* src_dev, int64_t rows, int64_t k, int8_t* dst_dev, void* stream) {
+  if (!src_dev || !dst_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "pack_tiles: null pointer");
+  if (rows <= 0 || k <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "pack_tiles: empty matrix");
+  if (k % kTileK) return fail(JERO_ERR_TENSOR_BOUNDS, "pack_tiles: k not a multiple of " + std::to_string(kTileK));
+  if (rows > (int64_t(1) << 24) || k > (int64_t(1) << 24))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "pack_tiles: rows or k above 2^24");
+  const int64_t total = jero_hip_tile_count(rows) * kTileRows * k;
+  hipLaunchKernelGGL(pack_tiles_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), src_dev, rows, int(k), total, dst_dev);
+  return check_launch("pack_tiles");
+}
+
+extern "C" int jero_hip_gemm_i8_tiles(const int8_t* a_packed_dev, int64_t m_tiles, const int8_t* w_packed_dev,
+                                      int64_t tile_begin, int64_t tile_end, int64_t k_chunks, int32_t* c_dev,
+                                      void* stream) {
+  if (!a_packed_dev || !w_packed_dev || !c_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "gemm_i8_tiles: null pointer");
+  if (m_tiles <= 0 || k_chunks <= 0 || tile_begin < 0 || tile_end <= tile_begin)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "gemm_i8_tiles: empty tile range");
+  if (!aligned4(a_packed_dev) || !aligned4(w_packed_dev))
+    return fail(JERO_ERR_INVALID_ARGUMENT, "gemm_i8_tiles: packed operands must be 4-byte aligned");
+  const int64_t m = m_tiles * kTileRows, n = (tile_end - tile_begin) * kTileRows, k = k_chunks * kTileK;
+  int rc = check_i8_args(a_packed_dev, m, k, w_packed_dev, n, c_dev, "gemm_i8_tiles");
+  if (rc) return rc;
+  const int8_t* w0 = w_packed_dev + tile_begin * k_chunks * kTileRows * kTileK;
+  hipLaunchKernelGGL((gemm_i8_kernel<true, kI8OutTiles>), dim3(unsigned(gemm_tiles(m, n))), dim3(kGemmThreads), 0,
+                     static_cast<hipStream_t>(stream), a_packed_dev, w0, int(m), int(n), int(k),
+                     static_cast<void*>(c_dev), 0);
+  return check_launch("gemm_i8_tiles");
 }

@@ -62,6 +62,11 @@ _SIGS = {
     "jero_hip_sync": (_I32, [_P]),
     "jero_hip_gemm": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _I64, _P, _P]),
     "jero_hip_gemm_i8": (_I32, [_P, _I64, _I64, _P, _I64, _P, _P]),
+    "jero_hip_gemm_i8_requant": (_I32, [_P, _I64, _I64, _P, _I64, _I32, _P, _P]),
+    "jero_hip_requant_i8": (_I32, [_P, _I64, _I32, _P, _P]),
+    "jero_hip_tile_count": (_I64, [_I64]),
+    "jero_hip_pack_tiles": (_I32, [_P, _I64, _I64, _P, _P]),
+    "jero_hip_gemm_i8_tiles": (_I32, [_P, _I64, _P, _I64, _I64, _I64, _P, _P]),
     "jero_hip_dequantize_rows": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, _P]),
     "jero_hip_repack": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, C.POINTER(C.c_int), _P]),
     "jero_hip_repack_experts": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, C.POINTER(C.c_int), _P]),
@@ -262,6 +267,70 @@ def gemm_i8(x, w, out=None, stream=None):
         out = torch.empty((m, n), dtype=torch.int32, device=x.device)
     check(lib().jero_hip_gemm_i8(_ptr(x), m, k, _ptr(w), n, _ptr(out), _stream(stream)))
     return out
+
+
+def gemm_i8_requant(x, w, shift, out=None, stream=None):
+    """requant_all(&ForwardExec::matmul(x, w), shift) (src/forward.rs:813-815, :957-970) in one
+    launch: int8 [m, n] of the int32 product requantized as forward.rs's requant (:345-350)."""
+    import torch
+    m, k = x.shape
+    n = w.shape[0]
+    if w.shape[1] != k:
+        raise K3Error(14, f"gemm_i8_requant: x has k={k}, w has k={w.shape[1]}")
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.int8, device=x.device)
+    check(lib().jero_hip_gemm_i8_requant(_ptr(x), m, k, _ptr(w), n, shift, _ptr(out), _stream(stream)))
+    return out
+
+
+def requant_all(raw, shift, out=None, stream=None):
+    """requant_all (src/forward.rs:813-815) on a device int32 tensor."""
+    import torch
+    if out is None:
+        out = torch.empty(raw.shape, dtype=torch.int8, device=raw.device)
+    check(lib().jero_hip_requant_i8(_ptr(raw), raw.numel(), shift, _ptr(out), _stream(stream)))
+    return out
+
+
+class ime:
+    """The ime names forward.rs imports (src/forward.rs:26-29): TILE_*, tile_count, pack_tiles,
+    gemm_i8_ime, gemm_i8_vector, over this library's packed layout (jero_hip_pack_tiles)."""
+    TILE_M, TILE_N, TILE_K, TILE_C = 8, 8, 32, 64
+
+    @staticmethod
+    def tile_count(rows):
+        return int(lib().jero_hip_tile_count(rows))
+
+    @staticmethod
+    def pack_tiles(x, rows, k, stream=None):
+        """x: [rows, k] int8 device tensor -> packed bytes (tile_count(rows) * 8 * k)."""
+        import torch
+        out = torch.empty(ime.tile_count(rows) * ime.TILE_N * k, dtype=torch.int8, device=x.device)
+        check(lib().jero_hip_pack_tiles(_ptr(x), rows, k, _ptr(out), _stream(stream)))
+        return out
+
+    @staticmethod
+    def gemm_i8_ime(a, m_tiles, packed_w, tile_range, k_chunks, emit, stream=None):
+        """gemm_i8_ime (src/forward.rs:779-796): emit(mt, nt, c) for every activation tile mt and
+        weight tile nt in tile_range, c the TILE_C int32 values of the 8 x 8 block (row-major)."""
+        import torch
+        nt0, nt1 = tile_range.start, tile_range.stop
+        c = torch.empty((m_tiles, nt1 - nt0, ime.TILE_C), dtype=torch.int32, device=a.device)
+        check(lib().jero_hip_gemm_i8_tiles(_ptr(a), m_tiles, _ptr(packed_w), nt0, nt1, k_chunks, _ptr(c),
+                                           _stream(stream)))
+        host = c.cpu().numpy()
+        for mt in range(m_tiles):
+            for nt in range(nt0, nt1):
+                emit(mt, nt, host[mt, nt - nt0])
+
+    @staticmethod
+    def gemm_i8_vector(x, m, rows, row_range, k, emit, stream=None):
+        """gemm_i8_vector (src/forward.rs:797-806): emit(row, col, v) for row < m, col in
+        row_range; x [m, k] and rows [n, k] int8 device tensors."""
+        out = gemm_i8(x[:m], rows[row_range.start:row_range.stop], stream=stream).cpu().numpy()
+        for r in range(m):
+            for j, col in enumerate(row_range):
+                emit(r, col, int(out[r, j]))
 
 
 def matvec_partials(weights, xq, out, partials, stream=None):

@@ -141,6 +141,23 @@ def gemm_i8(x, w):
     return out
 
 
+def requant(v, shift):
+    """requant (src/forward.rs:345-350): (v + 2^(shift-1)) >> shift, clamped to [-127, 127], as int8.
+    The i32 add wraps as two's complement (the reference's release build); >> is arithmetic."""
+    v = np.asarray(v, np.int64)
+    t = (v + (1 << (shift - 1)) + (1 << 31)) % (1 << 32) - (1 << 31)
+    return np.clip(t >> shift, -127, 127).astype(np.int8)
+
+
+def pack_tiles(x, rows, k, tile_rows=8, tile_k=32):
+    """This library's ime::pack_tiles layout: element (r, c) at
+    ((r // 8 * (k // 32) + c // 32) * 8 + r % 8) * 32 + c % 32, rows padded with zero rows."""
+    t = -(-rows // tile_rows)
+    p = np.zeros((t * tile_rows, k), np.int8)
+    p[:rows] = np.asarray(x, np.int8).reshape(rows, k)
+    return p.reshape(t, tile_rows, k // tile_k, tile_k).transpose(0, 2, 1, 3).reshape(-1).copy()
+
+
 def gqa_attention(q, k, v, nq, nkv, hd, seq_len, scale):
     q = np.ascontiguousarray(q, dtype=np.float32)
     k = np.ascontiguousarray(k, dtype=np.float32)

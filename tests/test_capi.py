@@ -76,3 +76,20 @@ def test_read_probe_argument_errors():
     assert lib.jero_hip_read_probe(C.c_void_p(0x10008), 1024, fake, None) == 21  # misaligned
     assert lib.jero_hip_read_probe(fake, 1000, fake, None) == 21  # not a multiple of 16
     assert lib.jero_hip_read_probe(fake, 0, fake, None) == 21
+
+
+def test_int8_entry_argument_errors():
+    lib = J.lib()
+    fake = C.c_void_p(0x10000)
+    assert lib.jero_hip_requant_i8(fake, 16, 0, fake, None) == 21      # shift 0
+    assert lib.jero_hip_requant_i8(fake, 16, 32, fake, None) == 21     # shift above 31
+    assert lib.jero_hip_requant_i8(None, 16, 7, fake, None) == 21
+    assert lib.jero_hip_requant_i8(fake, 0, 7, fake, None) == 14
+    assert lib.jero_hip_gemm_i8_requant(fake, 4, 64, fake, 4, 0, fake, None) == 21
+    assert lib.jero_hip_gemm_i8_requant(fake, 0, 64, fake, 4, 7, fake, None) == 14
+    assert lib.jero_hip_pack_tiles(fake, 8, 48, fake, None) == 14      # k not a multiple of 32
+    assert lib.jero_hip_pack_tiles(fake, 0, 64, fake, None) == 14
+    assert lib.jero_hip_gemm_i8_tiles(fake, 1, fake, 2, 2, 2, fake, None) == 14   # empty tile range
+    assert lib.jero_hip_gemm_i8_tiles(C.c_void_p(0x10002), 1, fake, 0, 1, 2, fake, None) == 21  # misaligned
+    assert lib.jero_hip_gemm_i8_tiles(fake, 1, fake, 0, 1, 1 << 13, fake, None) == 10  # k = 2^18: int32 overflow
+    assert [lib.jero_hip_tile_count(r) for r in (0, 1, 8, 9, 512)] == [0, 1, 1, 2, 64]

@@ -401,3 +401,27 @@ def test_float_weight_dot_kat_and_brute_force():
         np.testing.assert_allclose(O.vec_dot(q, w, 333, 7, x), ref, rtol=1e-6, atol=1e-9)
     # BF16 is the upper half of the f32 bits: 1.0 = 0x3F80
     assert O.dequantize(BF16, np.array([0x80, 0x3F], np.uint8), 1, 1)[0, 0] == 1.0
+
+
+def test_requant_kats():
+    """forward.rs's requant (:345-350) on hand-computed cases: the rounding term, floor shifts of
+    negatives, the [-127, 127] clamp (not -128), and the wrapping i32 add at the top of the range."""
+    cases = [((5, 1), 3), ((-5, 1), -2), ((4, 1), 2), ((-4, 1), -2), ((-6, 2), -1), ((1000, 2), 127),
+             ((-1000, 2), -127), ((255, 1), 127), ((253, 1), 127), ((-255, 1), -127), ((-256, 1), -127),
+             ((100, 31), 0), ((-100, 31), 0), ((1 << 30, 31), -1), ((2147483647, 1), -127), ((0, 7), 0),
+             ((63, 7), 0), ((64, 7), 1), ((-64, 7), 0), ((-65, 7), -1)]
+    for (v, s), want in cases:
+        assert int(O.requant(v, s)) == want, (v, s)
+
+
+def test_pack_tiles_layout():
+    """Packed bytes follow the documented offset formula, element by element; padding rows are 0."""
+    rng = np.random.default_rng(3)
+    rows, k = 13, 64
+    x = rng.integers(-128, 128, size=(rows, k)).astype(np.int8)
+    p = O.pack_tiles(x, rows, k)
+    assert p.size == 16 * k
+    for r in range(16):
+        for c in range(k):
+            off = ((r // 8 * (k // 32) + c // 32) * 8 + r % 8) * 32 + c % 32
+            assert p[off] == (x[r, c] if r < rows else 0)

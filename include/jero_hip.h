@@ -269,11 +269,19 @@ typedef struct jero_model jero_model;
 
 int jero_hip_model_create(const jero_model_config *cfg, jero_model **model);
 int jero_hip_model_destroy(jero_model *model);
-/* Copies one tensor to the device (src host memory, or device memory if src_on_device). */
+/* Copies one tensor to the device (src host memory, or device memory if src_on_device).  A layer
+ * projection (blk.N.attn_q/attn_k/attn_v/attn_output/ffn_gate/ffn_up/ffn_down.weight) whose
+ * element count differs from its expected shape is ignored, as project_or_deterministic_slice
+ * (src/gemma.rs:841-860) ignores it: the step then takes that projection's fallback. */
 int jero_hip_model_set_tensor(jero_model *model, const char *name, int quant, const void *src, size_t nbytes,
                               int64_t n_in, int64_t n_out, int src_on_device);
-/* Checks every tensor is present and builds the device layout (fused Q|K|V and gate|up rows,
- * Q6_K_R planes).  Required before the first decode step. */
+/* Checks the required tensors (embedding, head, norms) are present and builds the device layout
+ * (fused Q|K|V and gate|up rows, Q6_K_R planes).  Required before the first decode step.  A
+ * projection left out takes project_or_deterministic_slice's fallback (src/gemma.rs:841-860):
+ * out[i] = in[i % in_len] * scale with the Qwen3 call sites' scales (Q 0.5, K 0.25, V 0.125 of the
+ * normalised input, src/qwen_deepseek.rs:1011-1031; Wo 0.25 of the attention output, :1086-1092;
+ * gate 0.5, up 0.25 of the normalised input and down 0.125 of the SwiGLU vector, :696-725); the
+ * layer's present projections then run unfused. */
 int jero_hip_model_finalize(jero_model *model);
 /* Device addresses of layer `layer`'s K and V rings (to pre-fill or inspect the cache). */
 int jero_hip_model_kv(jero_model *model, int64_t layer, void **k_ring_dev, void **v_ring_dev);

@@ -864,6 +864,52 @@ int launch_argmax(const float* x, int64_t n, int64_t* out_idx, float* pv, int64_
   return check_launch("argmax");
 }
 
+// project_or_deterministic_slice's fallback (src/gemma.rs:841-860): y[i] = in[i % len] * scale for
+// i < out_len, in = x, or RMSNorm(x) * norm_w when norm_w is set (each workgroup reduces the norm
+// itself: len is a hidden size); RESID adds into y.  1024 outputs per workgroup.
+__global__ void __launch_bounds__(256) det_proj_kernel(const float* __restrict__ x, int64_t len,
+                                                        const float* __restrict__ norm_w, float eps, float scale,
+                                                        float* __restrict__ y, int64_t out_len, int resid) {
+  __shared__ float s_tmp[4];
+  float inv = 1.0f;
+  if (norm_w) {
+    float ss = 0.f;
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) ss += x[i] * x[i];
+    ss = block_sum(ss, s_tmp);
+    inv = 1.0f / sqrtf(ss / float(len) + eps);
+  }
+  const int64_t end = min(out_len, int64_t(blockIdx.x + 1) * 1024);
+  for (int64_t i = int64_t(blockIdx.x) * 1024 + threadIdx.x; i < end; i += blockDim.x) {
+    const int64_t j = i % len;
+    float v = x[j];
+    if (norm_w) v = v * inv * norm_w[j];
+    v *= scale;
+    if (resid) y[i] += v;
+    else y[i] = v;
+  }
+}
+
+// SwiGLU of separately computed gate | up rows (the fused epilogue's formula): act[i] =
+// silu(gu[i]) * gu[F + i].
+__global__ void __launch_bounds__(256) swiglu_kernel(const float* __restrict__ gu, int64_t F, float* __restrict__ act) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= F) return;
+  const float gv = gu[i], uv = gu[F + i];
+  act[i] = gv / (1.0f + expf(-gv)) * uv;
+}
+
+int launch_det_proj(const float* x, int64_t len, const float* norm_w, float eps, float scale, float* y,
+                    int64_t out_len, bool resid, hipStream_t s) {
+  hipLaunchKernelGGL(det_proj_kernel, dim3(unsigned((out_len + 1023) / 1024)), dim3(256), 0, s, x, len, norm_w, eps,
+                     scale, y, out_len, resid ? 1 : 0);
+  return check_launch("deterministic projection");
+}
+
+int launch_swiglu(const float* gu, int64_t F, float* act, hipStream_t s) {
+  hipLaunchKernelGGL(swiglu_kernel, dim3(unsigned((F + 255) / 256)), dim3(256), 0, s, gu, F, act);
+  return check_launch("swiglu");
+}
+
 int launch_set_state(int32_t* token, int64_t* pos, int32_t* status, int32_t t, int64_t p, hipStream_t s) {
   hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, s, token, pos, status, t, p);
   return check_launch("set state");

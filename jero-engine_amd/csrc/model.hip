@@ -13,6 +13,7 @@
 // in a HIP graph.  Token and position live in device memory: the step reads them, and its last
 // kernel stores the greedy token and advances the position, so replaying the graph decodes
 // consecutive tokens.
+#include <cstring>
 #include <map>
 #include <string>
 #include <vector>
@@ -39,6 +40,9 @@ struct LayerW {
   DevTensor qkv;      // fused Q|K|V (or Q|K when V's format differs)
   bool v_separate = false;
   DevTensor gate_up;  // fused gate|up
+  // a projection tensor absent (or Q, K / gate, up in different formats): the present ones run
+  // unfused, the absent ones as project_or_deterministic_slice's fallback
+  bool qkv_split = false, gu_split = false;
 };
 
 }  // namespace jero
@@ -51,6 +55,7 @@ struct jero_model {
   // device state
   float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr;
   float* attn_ws = nullptr;
+  float* gu = nullptr;  // gate | up rows of layers that compute them apart [2 ffn]
   float* amax_v = nullptr;
   int64_t* amax_i = nullptr;
   int32_t* token = nullptr;
@@ -147,6 +152,18 @@ static DevTensor* find_slot(jero_model* m, const std::string& name, int64_t& n_i
 
 static bool is_norm(const std::string& name) {
   return name.size() >= 12 && name.compare(name.size() - 12, 12, "_norm.weight") == 0;
+}
+
+// The layer projections that project_or_deterministic_slice computes (src/gemma.rs:841-860).
+static bool is_projection(const std::string& name) {
+  static const char* const kinds[] = {".attn_q.weight", ".attn_k.weight", ".attn_v.weight", ".attn_output.weight",
+                                      ".ffn_gate.weight", ".ffn_up.weight", ".ffn_down.weight"};
+  if (name.compare(0, 4, "blk.") != 0) return false;
+  for (const char* k : kinds) {
+    const size_t n = strlen(k);
+    if (name.size() > n && name.compare(name.size() - n, n, k) == 0) return true;
+  }
+  return false;
 }
 
 // Rows of a and b stacked into one new tensor (same format and n_in).
@@ -324,6 +341,13 @@ extern "C" int jero_hip_model_set_tensor(jero_model* m, const char* name, int qu
   int64_t ein = 0, eout = 0;
   DevTensor* slot = find_slot(m, name, ein, eout);
   if (!slot) return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string("set_tensor: unknown tensor '") + name + "'");
+  if (is_projection(name) && n_in * n_out != ein * eout) {
+    // project_or_deterministic_slice (src/gemma.rs:841-860) uses a tensor only when its element count
+    // is out_len * in_len; any other takes the deterministic fallback, as if it were absent
+    if (slot->dev) dev_free(m, slot->dev);
+    *slot = DevTensor{};
+    return JERO_OK;
+  }
   if (n_in != ein || n_out != eout)
     return fail(JERO_ERR_TENSOR_BOUNDS, std::string("set_tensor: '") + name + "' has shape [" + std::to_string(n_in) +
                                             ", " + std::to_string(n_out) + "], expected [" + std::to_string(ein) +
@@ -372,32 +396,40 @@ extern "C" int jero_hip_model_finalize(jero_model* m) {
   for (int64_t L = 0; L < c.n_layers; L++) {
     LayerW& l = m->layers[size_t(L)];
     const std::string p = "blk." + std::to_string(L) + ".";
-    if ((rc = need(l.attn_norm, p + "attn_norm.weight")) || (rc = need(l.ffn_norm, p + "ffn_norm.weight")) ||
-        (rc = need(l.wq, p + "attn_q.weight")) || (rc = need(l.wk, p + "attn_k.weight")) ||
-        (rc = need(l.wv, p + "attn_v.weight")) || (rc = need(l.wo, p + "attn_output.weight")) ||
-        (rc = need(l.gate, p + "ffn_gate.weight")) || (rc = need(l.up, p + "ffn_up.weight")) ||
-        (rc = need(l.down, p + "ffn_down.weight")))
+    // the projections may be absent (project_or_deterministic_slice's fallback); the norms may not
+    if ((rc = need(l.attn_norm, p + "attn_norm.weight")) || (rc = need(l.ffn_norm, p + "ffn_norm.weight")))
       return rc;
     if (c.qk_norm && ((rc = need(l.q_norm, p + "attn_q_norm.weight")) || (rc = need(l.k_norm, p + "attn_k_norm.weight"))))
       return rc;
-    if (l.wq.quant != l.wk.quant)
-      return fail(JERO_ERR_CAPABILITY_MISMATCH, "finalize: attn_q and attn_k of layer " + std::to_string(L) +
-                                                    " must share a format");
-    if (l.gate.quant != l.up.quant)
-      return fail(JERO_ERR_CAPABILITY_MISMATCH, "finalize: ffn_gate and ffn_up of layer " + std::to_string(L) +
-                                                    " must share a format");
-    l.v_separate = l.wv.quant != l.wq.quant;
-    if (l.v_separate) {
-      if ((rc = concat_rows(m, {&l.wq, &l.wk}, l.qkv))) return rc;
-      if ((rc = repack_planar(m, l.wv))) return rc;
+    l.qkv_split = !l.wq.present() || !l.wk.present() || !l.wv.present() || l.wq.quant != l.wk.quant;
+    l.gu_split = !l.gate.present() || !l.up.present() || l.gate.quant != l.up.quant;
+    if (l.qkv_split) {
+      for (DevTensor* t : {&l.wq, &l.wk, &l.wv})
+        if (t->present() && (rc = repack_planar(m, *t))) return rc;
     } else {
-      if ((rc = concat_rows(m, {&l.wq, &l.wk, &l.wv}, l.qkv))) return rc;
+      l.v_separate = l.wv.quant != l.wq.quant;
+      if (l.v_separate) {
+        if ((rc = concat_rows(m, {&l.wq, &l.wk}, l.qkv))) return rc;
+        if ((rc = repack_planar(m, l.wv))) return rc;
+      } else {
+        if ((rc = concat_rows(m, {&l.wq, &l.wk, &l.wv}, l.qkv))) return rc;
+      }
+      if ((rc = repack_planar(m, l.qkv))) return rc;
     }
-    if ((rc = repack_planar(m, l.qkv))) return rc;
-    if ((rc = concat_rows(m, {&l.gate, &l.up}, l.gate_up))) return rc;
-    if ((rc = repack_planar(m, l.gate_up))) return rc;
-    if ((rc = repack_planar(m, l.wo))) return rc;
-    if ((rc = repack_planar(m, l.down))) return rc;
+    if (l.gu_split) {
+      for (DevTensor* t : {&l.gate, &l.up})
+        if (t->present() && (rc = repack_planar(m, *t))) return rc;
+      if (!m->gu) {
+        void* g = nullptr;
+        if ((rc = dev_alloc(m, sizeof(float) * 2 * size_t(c.ffn), &g))) return rc;
+        m->gu = static_cast<float*>(g);
+      }
+    } else {
+      if ((rc = concat_rows(m, {&l.gate, &l.up}, l.gate_up))) return rc;
+      if ((rc = repack_planar(m, l.gate_up))) return rc;
+    }
+    if (l.wo.present() && (rc = repack_planar(m, l.wo))) return rc;
+    if (l.down.present() && (rc = repack_planar(m, l.down))) return rc;
   }
   if ((rc = repack_planar(m, m->output))) return rc;
   m->finalized = true;
@@ -492,7 +524,7 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
     const LayerW& l = m->layers[size_t(L)];
     if ((rc = snap(tr(L, TraceLayout::kXIn), m->hidden, 4 * size_t(c.hidden)))) return rc;
     // attention sublayer: RMSNorm -> Q|K|V
-    const bool dual = l.v_separate && l.qkv.n_in <= 4096 &&
+    const bool dual = !l.qkv_split && l.v_separate && l.qkv.n_in <= 4096 &&
                       ((l.qkv.quant == JERO_Q4_K_R && l.wv.quant == JERO_Q6_K_R) ||
                        (l.qkv.quant == JERO_Q6_K_R && l.wv.quant == JERO_Q4_K_R));
     if (dual) {  // Q|K and V of different formats in one launch
@@ -513,6 +545,24 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
       a.tr_q8 = tr(L, TraceLayout::kQ8Attn);
       rc = launch_dgemv_dual(l.qkv.quant, l.wv.quant, a, s);
       if (rc) return rc;
+    } else if (l.qkv_split) {
+      // each of Q, K, V projected on its own or, absent, the fallback slice of the normalised input
+      // (scales 0.5, 0.25, 0.125: src/qwen_deepseek.rs:1011-1031)
+      const float* nw = static_cast<const float*>(l.attn_norm.dev);
+      const DevTensor* w3[3] = {&l.wq, &l.wk, &l.wv};
+      const int64_t off[3] = {0, Q, Q + KV}, len[3] = {Q, KV, KV};
+      const float sc[3] = {0.5f, 0.25f, 0.125f};
+      bool traced = false;
+      for (int j = 0; j < 3; j++) {
+        if (w3[j]->present()) {
+          rc = gemv(m, *w3[j], m->hidden, nw, eps_attn, kOutStore, m->qkv + off[j], 0, s, nullptr,
+                    traced ? nullptr : trf(L, TraceLayout::kXnAttn), traced ? nullptr : tr(L, TraceLayout::kQ8Attn));
+          traced = true;
+        } else {
+          rc = launch_det_proj(m->hidden, c.hidden, nw, eps_attn, sc[j], m->qkv + off[j], len[j], false, s);
+        }
+        if (rc) return rc;
+      }
     } else {
       rc = gemv(m, l.qkv, m->hidden, static_cast<const float*>(l.attn_norm.dev), eps_attn, kOutStore, m->qkv, 0, s,
                 nullptr, trf(L, TraceLayout::kXnAttn), tr(L, TraceLayout::kQ8Attn));
@@ -554,18 +604,45 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
     rc = launch_attention(p, true, m->attn, s);
     if (rc) return rc;
     if ((rc = snap(tr(L, TraceLayout::kAttn), m->attn, 4 * size_t(Q)))) return rc;
-    // output projection + residual
-    rc = gemv(m, l.wo, m->attn, nullptr, 0.f, kOutResid, m->hidden, 0, s, nullptr, nullptr,
-              tr(L, TraceLayout::kQ8Wo));
+    // output projection + residual (absent: the fallback slice of the attention output, scale 0.25)
+    if (l.wo.present())
+      rc = gemv(m, l.wo, m->attn, nullptr, 0.f, kOutResid, m->hidden, 0, s, nullptr, nullptr,
+                tr(L, TraceLayout::kQ8Wo));
+    else
+      rc = launch_det_proj(m->attn, Q, nullptr, 0.f, 0.25f, m->hidden, c.hidden, true, s);
     if (rc) return rc;
     if ((rc = snap(tr(L, TraceLayout::kXMid), m->hidden, 4 * size_t(c.hidden)))) return rc;
     // FFN: RMSNorm -> gate|up -> SwiGLU -> down + residual
-    rc = gemv(m, l.gate_up, m->hidden, static_cast<const float*>(l.ffn_norm.dev), eps_ffn, kOutSwiglu, m->act,
-              c.ffn, s, nullptr, trf(L, TraceLayout::kXnFfn), tr(L, TraceLayout::kQ8Ffn), trf(L, TraceLayout::kGu));
-    if (rc) return rc;
+    if (l.gu_split) {
+      // gate and up apart (absent: fallback slices of the normalised input, scales 0.5 and 0.25,
+      // run_dense_swiglu_ffn src/qwen_deepseek.rs:696-725), then SwiGLU
+      const float* nw = static_cast<const float*>(l.ffn_norm.dev);
+      const DevTensor* w2[2] = {&l.gate, &l.up};
+      const float sc[2] = {0.5f, 0.25f};
+      bool traced = false;
+      for (int j = 0; j < 2; j++) {
+        if (w2[j]->present()) {
+          rc = gemv(m, *w2[j], m->hidden, nw, eps_ffn, kOutStore, m->gu + j * c.ffn, 0, s, nullptr,
+                    traced ? nullptr : trf(L, TraceLayout::kXnFfn), traced ? nullptr : tr(L, TraceLayout::kQ8Ffn));
+          traced = true;
+        } else {
+          rc = launch_det_proj(m->hidden, c.hidden, nw, eps_ffn, sc[j], m->gu + j * c.ffn, c.ffn, false, s);
+        }
+        if (rc) return rc;
+      }
+      if ((rc = launch_swiglu(m->gu, c.ffn, m->act, s))) return rc;
+      if ((rc = snap(tr(L, TraceLayout::kGu), m->gu, 8 * size_t(c.ffn)))) return rc;
+    } else {
+      rc = gemv(m, l.gate_up, m->hidden, static_cast<const float*>(l.ffn_norm.dev), eps_ffn, kOutSwiglu, m->act,
+                c.ffn, s, nullptr, trf(L, TraceLayout::kXnFfn), tr(L, TraceLayout::kQ8Ffn), trf(L, TraceLayout::kGu));
+      if (rc) return rc;
+    }
     if ((rc = snap(tr(L, TraceLayout::kAct), m->act, 4 * size_t(c.ffn)))) return rc;
-    rc = gemv(m, l.down, m->act, nullptr, 0.f, kOutResid, m->hidden, 0, s, nullptr, nullptr,
-              tr(L, TraceLayout::kQ8Down));
+    if (l.down.present())
+      rc = gemv(m, l.down, m->act, nullptr, 0.f, kOutResid, m->hidden, 0, s, nullptr, nullptr,
+                tr(L, TraceLayout::kQ8Down));
+    else  // the fallback slice of the SwiGLU vector, scale 0.125
+      rc = launch_det_proj(m->act, c.ffn, nullptr, 0.f, 0.125f, m->hidden, c.hidden, true, s);
     if (rc) return rc;
   }
   // final norm -> LM head -> greedy token

@@ -769,6 +769,18 @@ static int jo_matvec_q(int quant, const void *w, int64_t k, int64_t n, const flo
   return rc;
 }
 
+/* project_or_deterministic_slice (src/gemma.rs:841-860): the projection when the tensor is present
+ * (its element count out_len * in_len is checked when the model is built), else the deterministic
+ * slice out[i] = in[i % in_len] * scale.  A fallback leaves the activation-block trace untouched. */
+static int proj_or_det(const jo_tensor *w, int64_t in_len, int64_t out_len, const float *in, float *out, float scale,
+                       int threads, void *q8_trace) {
+  if (!w->data) {
+    for (int64_t i = 0; i < out_len; i++) out[i] = in[i % in_len] * scale;
+    return 0;
+  }
+  return jo_matvec_q(w->quant, w->data, in_len, out_len, in, out, threads, q8_trace);
+}
+
 int jo_decode_layer(const jo_model *M, float *kv, int64_t L, float *x, int64_t pos, int threads,
                     const jo_layer_trace *tr) {
   const int64_t H = M->hidden, F = M->ffn, qd = (int64_t)M->nq * M->hd, kvd = (int64_t)M->nkv * M->hd;
@@ -787,9 +799,10 @@ int jo_decode_layer(const jo_model *M, float *kv, int64_t L, float *x, int64_t p
   if (!rc) {
     jo_rmsnorm(xn, x, ly->attn_norm, H, eps_attn);
     if (tr->xn_attn) memcpy(tr->xn_attn, xn, (size_t)H * 4);
-    rc |= jo_matvec_q(ly->wq.quant, ly->wq.data, H, qd, xn, q, threads, tr->q8_attn);
-    rc |= jo_matvec_q(ly->wk.quant, ly->wk.data, H, kvd, xn, k, threads, NULL);
-    rc |= jo_matvec_q(ly->wv.quant, ly->wv.data, H, kvd, xn, v, threads, NULL);
+    /* scales of the fallback: q 0.5, k 0.25, v 0.125 (src/qwen_deepseek.rs:1011-1031) */
+    rc |= proj_or_det(&ly->wq, H, qd, xn, q, 0.5f, threads, tr->q8_attn);
+    rc |= proj_or_det(&ly->wk, H, kvd, xn, k, 0.25f, threads, NULL);
+    rc |= proj_or_det(&ly->wv, H, kvd, xn, v, 0.125f, threads, NULL);
   }
   if (!rc) {
     if (tr->qkv) memcpy(tr->qkv, qkv, (size_t)(qd + 2 * kvd) * 4);
@@ -808,19 +821,20 @@ int jo_decode_layer(const jo_model *M, float *kv, int64_t L, float *x, int64_t p
   }
   if (!rc) {
     if (tr->attn) memcpy(tr->attn, att, (size_t)qd * 4);
-    rc |= jo_matvec_q(ly->wo.quant, ly->wo.data, qd, H, att, proj, threads, tr->q8_wo);
+    rc |= proj_or_det(&ly->wo, qd, H, att, proj, 0.25f, threads, tr->q8_wo); /* :1086-1092 */
     for (int64_t i = 0; i < H; i++) x[i] += proj[i];
     if (tr->x_mid) memcpy(tr->x_mid, x, (size_t)H * 4);
     jo_rmsnorm(xn, x, ly->ffn_norm, H, eps_ffn);
     if (tr->xn_ffn) memcpy(tr->xn_ffn, xn, (size_t)H * 4);
-    rc |= jo_matvec_q(ly->w_gate.quant, ly->w_gate.data, H, F, xn, gu, threads, tr->q8_ffn);
-    rc |= jo_matvec_q(ly->w_up.quant, ly->w_up.data, H, F, xn, gu + F, threads, NULL);
+    /* run_dense_swiglu_ffn (:696-725): gate 0.5, up 0.25, down 0.125 */
+    rc |= proj_or_det(&ly->w_gate, H, F, xn, gu, 0.5f, threads, tr->q8_ffn);
+    rc |= proj_or_det(&ly->w_up, H, F, xn, gu + F, 0.25f, threads, NULL);
   }
   if (!rc) {
     if (tr->gu) memcpy(tr->gu, gu, (size_t)F * 8);
     jo_swiglu(a, gu, gu + F, F);
     if (tr->act) memcpy(tr->act, a, (size_t)F * 4);
-    rc |= jo_matvec_q(ly->w_down.quant, ly->w_down.data, F, H, a, proj, threads, tr->q8_down);
+    rc |= proj_or_det(&ly->w_down, F, H, a, proj, 0.125f, threads, tr->q8_down);
     for (int64_t i = 0; i < H; i++) x[i] += proj[i];
   }
   free(xn);

@@ -255,6 +255,8 @@ class DecodeModel:
         self.layers = (JoLayer * nl)()
 
         def t(name):
+            if name not in tensors:  # a projection left out: the deterministic slice (gemma.rs:841-860)
+                return JoTensor(0, None)
             quant, arr = tensors[name]
             arr = np.ascontiguousarray(arr)
             self._keep.append(arr)

@@ -339,3 +339,38 @@ def test_decode_long_rows(dev, mix, spec):
     kv = prefill_kv(m, om, spec, 256, 100, 78, dev)
     DP.run_traced(m, om, t, spec, kv, 256, 100, 3, True, dev, 11)
     m.close()
+
+
+def test_deterministic_projection_fallback(dev):
+    """project_or_deterministic_slice (src/gemma.rs:841-860) in the decode step: projections left
+    out, and one passed with the wrong element count (ignored, as the reference ignores it), take
+    the fallback slice with the Qwen3 call sites' scales; the present ones run unfused.  Device
+    logits against the oracle's over three greedy steps, within 1e-3."""
+    from qdata import rand_weights
+    spec = dict(hidden=512, ffn=1024, n_layers=2, vocab=300, nq=8, nkv=2, hd=64, eps=1e-6, theta=1e6)
+    H, KV = spec["hidden"], spec["nkv"] * spec["hd"]
+    print("decode with absent projections", flush=True)
+    t = MS.build(spec, seed=21)
+    absent = ["blk.0.attn_q.weight", "blk.0.attn_v.weight", "blk.0.ffn_up.weight", "blk.1.attn_output.weight",
+              "blk.1.ffn_gate.weight", "blk.1.ffn_down.weight"]
+    dev_t = {k: v for k, v in t.items() if k not in absent and k != "blk.1.attn_k.weight"}
+    dev_t["blk.1.attn_k.weight"] = (J.Q4_K, rand_weights(J.Q4_K, 2 * KV, H, 77), H, 2 * KV)  # wrong count
+    m = make_gpu_model(spec, dev_t, 64, J.KV_F32, True)
+    host = {k: v for k, v in MS.oracle_tensors(t).items() if k not in absent and k != "blk.1.attn_k.weight"}
+    om = O.DecodeModel(spec, host, 64)
+    kv = om.new_kv()
+    lg = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
+    tok = 5
+    m.set_position(tok, 0)
+    for pos in range(3):
+        m.decode_step()
+        torch.cuda.synchronize()
+        m.read_logits(lg)
+        ref = om.step(kv, tok, pos, threads=4)
+        got = lg.cpu().numpy()
+        err = DP.rel(got, ref)
+        print(f"pos {pos}: rel err {err:.2e}", flush=True)
+        assert err <= 1e-3, (pos, err)
+        tok = int(O.argmax(ref))
+        assert m.read_token_pos() == (tok, pos + 1)
+    m.close()

@@ -425,3 +425,42 @@ def test_pack_tiles_layout():
         for c in range(k):
             off = ((r // 8 * (k // 32) + c // 32) * 8 + r % 8) * 32 + c % 32
             assert p[off] == (x[r, c] if r < rows else 0)
+
+
+def test_deterministic_projection_fallback_equals_selection_matrices():
+    """project_or_deterministic_slice (src/gemma.rs:841-860) with the Qwen3 call sites' scales: a
+    model whose projections are absent gives the logits of the same model carrying F32 selection
+    matrices S[i][i % in_len] = scale (an exact product: one power-of-two term per row); a wrong
+    scale on one of them (v at 0.25 instead of 0.125) does not."""
+    import model_spec as MS
+    spec = dict(hidden=256, ffn=512, n_layers=2, vocab=40, nq=4, nkv=2, hd=64, eps=1e-6, theta=1e6)
+    H, F, Q, KV = 256, 512, 256, 128
+    t = MS.oracle_tensors(MS.build(spec, seed=3))
+    absent = {"blk.0.attn_v.weight": (H, KV, 0.125), "blk.0.ffn_up.weight": (H, F, 0.25),
+              "blk.0.attn_q.weight": (H, Q, 0.5), "blk.1.attn_k.weight": (H, KV, 0.25),
+              "blk.1.attn_output.weight": (Q, H, 0.25), "blk.1.ffn_gate.weight": (H, F, 0.5),
+              "blk.1.ffn_down.weight": (F, H, 0.125)}
+
+    def selection(n_in, n_out, s):
+        S = np.zeros((n_out, n_in), np.float32)
+        S[np.arange(n_out), np.arange(n_out) % n_in] = s
+        return (O.F32, S.reshape(-1))
+
+    a = {k: v for k, v in t.items() if k not in absent}
+    b = dict(t, **{k: selection(*v) for k, v in absent.items()})
+    c = dict(b)
+    c["blk.0.attn_v.weight"] = selection(H, KV, 0.25)
+
+    def run(tensors):
+        om = O.DecodeModel(spec, tensors, 16)
+        kv = om.new_kv()
+        out, tok = [], 3
+        for pos in range(3):
+            lg = om.step(kv, tok, pos, threads=2)
+            out.append(lg)
+            tok = int(np.argmax(lg))
+        return np.stack(out)
+
+    la, lb, lc = run(a), run(b), run(c)
+    assert np.array_equal(la, lb)
+    assert not np.allclose(la, lc, rtol=1e-3, atol=1e-3)

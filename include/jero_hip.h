@@ -298,6 +298,17 @@ int jero_hip_decode_step(jero_model *model, void *stream);
 /* Waits for `stream` and returns the model's status: JERO_OK, or CapabilityMismatch ("empty
  * logits buffer after decode step (or all-NaN)") once a step has failed closed. */
 int jero_hip_model_status(jero_model *model, void *stream);
+/* run_prefill_with_hidden (src/qwen_deepseek.rs:2217-2316) without its token loop: the n prompt
+ * tokens (host array) at positions pos0 .. pos0 + n - 1 go through each layer at once -- every
+ * projection one GEMM over the n activation rows (jero_hip_gemm's kernels), every token's
+ * attention causal over the ring up to its own position -- and leave the state n decode steps
+ * would leave: the n K/V rows in the ring, the last token's logits, its greedy next token and
+ * position pos0 + n.  pos0 + n <= kv_capacity, else ContextLengthExceeded (as engine.rs:727
+ * rejects a prompt past n_ctx).  Allocates its row buffers on first use (held by the model).
+ * With a trace set (jero_hip_model_trace, n * jero_hip_model_trace_bytes bytes or more), token t's
+ * trace in the decode step's layout lands at t * jero_hip_model_trace_bytes; the head's fields
+ * only for the last token. */
+int jero_hip_model_prefill(jero_model *model, const int32_t *tokens, int64_t n, int64_t pos0, void *stream);
 
 /* Debug trace of the decode step, for the layer-by-layer parity tests (no counterpart in the
  * reference; the reference's intermediate vectors are locals of

@@ -35,6 +35,10 @@ struct AttnParams {
   // RoPE, before the softmax scale
   float* tr_q;
   float* tr_k;
+  // a batch of queries (prefill, not fused): grid z is the token t, whose q row starts t *
+  // q_stride floats on, which attends to active + t slots, and whose partials start t * part_tok
+  // (part_o) and t * part_tok_ml (part_ml) floats on; all zero for one query
+  int64_t q_stride, part_tok, part_tok_ml;
 };
 
 int attn_splits(int active, int hd);
@@ -42,5 +46,10 @@ size_t attn_workspace_bytes(int nq, int hd, int active);
 int check_attention_shape(int nq, int nkv, int hd, int64_t seq_len);
 // Enqueues the split-K kernel and the merge; out: [nq][hd] f32.
 int launch_attention(const AttnParams& p, bool fused, float* out, hipStream_t s);
+// Causal attention of n_tok consecutive queries (prefill): token t's q heads at p.q + t *
+// q_stride, attending to the first p.active + t slots of the rings; out row t at out + t *
+// out_stride.  Workspace: attn_workspace_bytes(nq, hd, p.active + n_tok - 1) * n_tok bytes.
+int launch_attention_tokens(const AttnParams& p, int n_tok, int64_t q_stride, float* out, int64_t out_stride,
+                            hipStream_t s);
 
 }  // namespace jero

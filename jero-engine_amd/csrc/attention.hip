@@ -126,6 +126,13 @@ __device__ __forceinline__ void ld_floats(float (&dst)[N], const float* __restri
 //   * The four sub-splits merge with the usual max rescaling through LDS, one barrier.
 template <int HD, typename KV, bool FUSED, int MAXG>
 __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p) {
+  {  // token of a batch of queries (zero offsets for one query)
+    const int t = blockIdx.z;
+    p.q += t * p.q_stride;
+    p.active += t;
+    p.part_o += t * p.part_tok;
+    p.part_ml += t * p.part_tok_ml;
+  }
   constexpr int EPL = 16 / int(sizeof(KV));  // KV elements per 16-byte load
   constexpr int CPR = HD / EPL;              // 16-byte chunks per K/V row
   constexpr int PPL = kWave / CPR;           // positions per wave-wide load
@@ -430,6 +437,13 @@ __device__ __forceinline__ h4_t h4_of(uint32_t lo, uint32_t hi) {
 //     k and v rounded to f16 (the values the ring then holds) and appends them to the ring.
 template <int HD, int MAXG, bool FUSED>
 __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
+  {  // token of a batch of queries (zero offsets for one query)
+    const int t = blockIdx.z;
+    p.q += t * p.q_stride;
+    p.active += t;
+    p.part_o += t * p.part_tok;
+    p.part_ml += t * p.part_tok_ml;
+  }
   constexpr int NCH = HD / 32;  // 16-byte chunks per lane per row
   constexpr int NT = HD / 16;   // 16-dim MFMA tiles
   constexpr int NW = kAttnThreads / kWave;
@@ -689,7 +703,11 @@ constexpr int kMaxSplits = 2048;
 template <int HD>
 __global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restrict__ part_o,
                                                            const float* __restrict__ part_ml, int S,
-                                                           float* __restrict__ out) {
+                                                           float* __restrict__ out, int64_t tok_o, int64_t tok_ml,
+                                                           int64_t tok_out) {
+  part_o += blockIdx.y * tok_o;  // token of a batch of queries
+  part_ml += blockIdx.y * tok_ml;
+  out += blockIdx.y * tok_out;
   constexpr int Q = HD / 4;    // float4 columns of a row
   constexpr int SG = 256 / Q;  // split groups
   constexpr int CH = 8;        // rows per thread per pass
@@ -777,7 +795,11 @@ constexpr int kCombineSmallSplits = 256;
 template <int HD>
 __global__ void __launch_bounds__(256) attn_combine_small_kernel(const float* __restrict__ part_o,
                                                                  const float* __restrict__ part_ml, int S,
-                                                                 float* __restrict__ out) {
+                                                                 float* __restrict__ out, int64_t tok_o,
+                                                                 int64_t tok_ml, int64_t tok_out) {
+  part_o += blockIdx.y * tok_o;  // token of a batch of queries
+  part_ml += blockIdx.y * tok_ml;
+  out += blockIdx.y * tok_out;
   constexpr int DPL = HD >= 64 ? HD / 64 : 1;  // dims per lane
   constexpr int CHUNK = 16;                    // splits per batch of loads
   __shared__ float s_o[4][HD];
@@ -853,20 +875,21 @@ size_t attn_workspace_bytes(int nq, int hd, int active) {
 }
 
 template <int HD, typename KV, bool FUSED>
-static void launch_partial(const AttnParams& p, int S, hipStream_t s) {
+static void launch_partial(const AttnParams& p, int S, int T, hipStream_t s) {
+  const dim3 grid(S, p.nkv, T);
   if (p.group <= 1)
-    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 1>), dim3(S, p.nkv), dim3(kAttnThreads), 0, s, p);
+    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 1>), grid, dim3(kAttnThreads), 0, s, p);
   else if (p.group <= 2)
-    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 2>), dim3(S, p.nkv), dim3(kAttnThreads), 0, s, p);
+    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 2>), grid, dim3(kAttnThreads), 0, s, p);
   else if (p.group <= 4)
-    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 4>), dim3(S, p.nkv), dim3(kAttnThreads), 0, s, p);
+    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 4>), grid, dim3(kAttnThreads), 0, s, p);
   else
-    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 8>), dim3(S, p.nkv), dim3(kAttnThreads), 0, s, p);
+    hipLaunchKernelGGL((attn_partial_kernel<HD, KV, FUSED, 8>), grid, dim3(kAttnThreads), 0, s, p);
 }
 
 template <int HD, bool FUSED>
-static void launch_mfma(const AttnParams& p, int S, hipStream_t s) {
-  const dim3 grid(S, p.nkv);
+static void launch_mfma(const AttnParams& p, int S, int T, hipStream_t s) {
+  const dim3 grid(S, p.nkv, T);
   if (p.group <= 1)
     hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, FUSED>), grid, dim3(kAttnThreads), 0, s, p);
   else if (p.group <= 2)
@@ -878,29 +901,34 @@ static void launch_mfma(const AttnParams& p, int S, hipStream_t s) {
 }
 
 template <int HD>
-static void launch_combine(const AttnParams& p, int S, float* out, hipStream_t s) {
+static void launch_combine(const AttnParams& p, int S, int T, float* out, int64_t out_stride, hipStream_t s) {
   const int nq = p.nkv * p.group;
+  const dim3 grid(nq, T);
   if (S <= kCombineSmallSplits)
-    hipLaunchKernelGGL((attn_combine_small_kernel<HD>), dim3(nq), dim3(256), 0, s, p.part_o, p.part_ml, S, out);
+    hipLaunchKernelGGL((attn_combine_small_kernel<HD>), grid, dim3(256), 0, s, p.part_o, p.part_ml, S, out,
+                       p.part_tok, p.part_tok_ml, out_stride);
   else
-    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3(nq), dim3(256), 0, s, p.part_o, p.part_ml, S, out);
+    hipLaunchKernelGGL((attn_combine_kernel<HD>), grid, dim3(256), 0, s, p.part_o, p.part_ml, S, out, p.part_tok,
+                       p.part_tok_ml, out_stride);
 }
 
-int launch_attention(const AttnParams& p0, bool fused, float* out, hipStream_t s) {
-  AttnParams p = p0;
-  const int S = attn_splits(p.pos_dev ? int(p.capacity) : p.active, p.hd);
-  p.part_ml = p.part_o + size_t(p.nkv) * p.group * S * p.hd;
+// The split-K partial kernel over S splits for T queries, then the merge.
+static int attention_impl(AttnParams p, bool fused, int S, int T, float* out, int64_t out_stride, hipStream_t s) {
+  const int64_t nq = int64_t(p.nkv) * p.group;
+  p.part_tok = T > 1 ? nq * S * p.hd : 0;
+  p.part_tok_ml = T > 1 ? nq * S * 2 : 0;
+  p.part_ml = p.part_o + int64_t(T) * nq * S * p.hd;
 #define JERO_ATTN_CASE(HDV)                                                                     \
   if (p.hd == HDV) {                                                                            \
     if (p.kv_dtype == JERO_KV_F16 && HDV >= 64) {                                               \
-      if (fused) launch_mfma<(HDV >= 64 ? HDV : 64), true>(p, S, s);                            \
-      else launch_mfma<(HDV >= 64 ? HDV : 64), false>(p, S, s);                                 \
+      if (fused) launch_mfma<(HDV >= 64 ? HDV : 64), true>(p, S, T, s);                         \
+      else launch_mfma<(HDV >= 64 ? HDV : 64), false>(p, S, T, s);                              \
     } else if (p.kv_dtype == JERO_KV_F16) {                                                     \
-      if (fused) launch_partial<HDV, _Float16, true>(p, S, s);                                  \
-      else launch_partial<HDV, _Float16, false>(p, S, s);                                       \
+      if (fused) launch_partial<HDV, _Float16, true>(p, S, T, s);                               \
+      else launch_partial<HDV, _Float16, false>(p, S, T, s);                                    \
     } else {                                                                                    \
-      if (fused) launch_partial<HDV, float, true>(p, S, s);                                     \
-      else launch_partial<HDV, float, false>(p, S, s);                                          \
+      if (fused) launch_partial<HDV, float, true>(p, S, T, s);                                  \
+      else launch_partial<HDV, float, false>(p, S, T, s);                                       \
     }                                                                                           \
   }
   JERO_ATTN_CASE(32) else JERO_ATTN_CASE(64) else JERO_ATTN_CASE(128) else return fail(
@@ -908,10 +936,22 @@ int launch_attention(const AttnParams& p0, bool fused, float* out, hipStream_t s
 #undef JERO_ATTN_CASE
   int rc = check_launch("attention partial");
   if (rc) return rc;
-  if (p.hd == 32) launch_combine<32>(p, S, out, s);
-  else if (p.hd == 64) launch_combine<64>(p, S, out, s);
-  else launch_combine<128>(p, S, out, s);
+  if (p.hd == 32) launch_combine<32>(p, S, T, out, out_stride, s);
+  else if (p.hd == 64) launch_combine<64>(p, S, T, out, out_stride, s);
+  else launch_combine<128>(p, S, T, out, out_stride, s);
   return check_launch("attention combine");
+}
+
+int launch_attention(const AttnParams& p, bool fused, float* out, hipStream_t s) {
+  return attention_impl(p, fused, attn_splits(p.pos_dev ? int(p.capacity) : p.active, p.hd), 1, out, 0, s);
+}
+
+int launch_attention_tokens(const AttnParams& p0, int n_tok, int64_t q_stride, float* out, int64_t out_stride,
+                            hipStream_t s) {
+  if (n_tok <= 0 || n_tok > 65535) return fail(JERO_ERR_TENSOR_BOUNDS, "attention: query batch of 1..65535 tokens");
+  AttnParams p = p0;
+  p.q_stride = q_stride;
+  return attention_impl(p, false, attn_splits(p.active + n_tok - 1, p.hd), n_tok, out, out_stride, s);
 }
 
 static_assert(int64_t(kMaxSplits) * attn_chunk(64) == JERO_MAX_ATTENTION_POSITIONS, "attention position limit");

@@ -64,8 +64,10 @@ int launch_argmax(const float* x, int64_t n, int64_t* out_idx, float* pv, int64_
 int launch_set_state(int32_t* token, int64_t* pos, int32_t* status, int32_t t, int64_t p, hipStream_t s);
 // A projection whose tensor the model lacks (project_or_deterministic_slice, src/gemma.rs:841-860):
 // y[i] (+)= in[i % len] * scale, in = x or RMSNorm(x) * norm_w.
+// rows > 1: a batch of rows x_stride / y_stride floats apart.
 int launch_det_proj(const float* x, int64_t len, const float* norm_w, float eps, float scale, float* y,
-                    int64_t out_len, bool resid, hipStream_t s);
+                    int64_t out_len, bool resid, hipStream_t s, int64_t rows = 1, int64_t x_stride = 0,
+                    int64_t y_stride = 0);
 // act[i] = silu(gu[i]) * gu[F + i] for gate | up rows computed apart.
 int launch_swiglu(const float* gu, int64_t F, float* act, hipStream_t s);
 

@@ -866,11 +866,15 @@ int launch_argmax(const float* x, int64_t n, int64_t* out_idx, float* pv, int64_
 
 // project_or_deterministic_slice's fallback (src/gemma.rs:841-860): y[i] = in[i % len] * scale for
 // i < out_len, in = x, or RMSNorm(x) * norm_w when norm_w is set (each workgroup reduces the norm
-// itself: len is a hidden size); RESID adds into y.  1024 outputs per workgroup.
+// itself: len is a hidden size); RESID adds into y.  1024 outputs per workgroup; grid y is the
+// row of a batch (x and y rows x_stride and y_stride floats apart).
 __global__ void __launch_bounds__(256) det_proj_kernel(const float* __restrict__ x, int64_t len,
                                                         const float* __restrict__ norm_w, float eps, float scale,
-                                                        float* __restrict__ y, int64_t out_len, int resid) {
+                                                        float* __restrict__ y, int64_t out_len, int resid,
+                                                        int64_t x_stride, int64_t y_stride) {
   __shared__ float s_tmp[4];
+  x += blockIdx.y * x_stride;
+  y += blockIdx.y * y_stride;
   float inv = 1.0f;
   if (norm_w) {
     float ss = 0.f;
@@ -899,9 +903,9 @@ __global__ void __launch_bounds__(256) swiglu_kernel(const float* __restrict__ g
 }
 
 int launch_det_proj(const float* x, int64_t len, const float* norm_w, float eps, float scale, float* y,
-                    int64_t out_len, bool resid, hipStream_t s) {
-  hipLaunchKernelGGL(det_proj_kernel, dim3(unsigned((out_len + 1023) / 1024)), dim3(256), 0, s, x, len, norm_w, eps,
-                     scale, y, out_len, resid ? 1 : 0);
+                    int64_t out_len, bool resid, hipStream_t s, int64_t rows, int64_t x_stride, int64_t y_stride) {
+  hipLaunchKernelGGL(det_proj_kernel, dim3(unsigned((out_len + 1023) / 1024), unsigned(rows)), dim3(256), 0, s, x, len,
+                     norm_w, eps, scale, y, out_len, resid ? 1 : 0, x_stride, y_stride);
   return check_launch("deterministic projection");
 }
 

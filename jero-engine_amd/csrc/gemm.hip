@@ -72,19 +72,32 @@ __device__ __forceinline__ void gemm_tile_of(int wg, int n_wg, int n_tiles_m, in
   tm = l % n_tiles_m;
 }
 
-// Every load is unconditional (rows past M read row M-1 and are never stored).
+// Every load is unconditional (rows past M read row M-1 and are never stored).  PLANAR: the weight
+// rows are in the Q4_K_R layout (each row's q0 run of U = 4 nb 16-byte pieces, its q1 run, then
+// its nb block headers); the chunks land in LDS as the same raw Q4_K block, so the rest of the
+// kernel, and its results, do not depend on the layout.
+template <bool PLANAR>
 __device__ __forceinline__ void q4k_load(Q4kRegs& R, const uint8_t* __restrict__ x, int64_t xrb, int m0, int M,
-                                         const uint8_t* __restrict__ w, int64_t wrb, int n0, int b) {
+                                         const uint8_t* __restrict__ w, int64_t wrb, int n0, int b, int nb) {
   const int t = threadIdx.x, r = t >> 2, q = t & 3;
   const int m = min(m0 + r, M - 1);
   const uint8_t* xa = x + int64_t(m) * xrb + int64_t(b) * 292;
 #pragma unroll
   for (int i = 0; i < 4; i++) R.aq[i] = ld4(xa + 4 + 64 * q + 16 * i);
   R.ax = ld4(xa + (q == 1 ? 260 : q == 2 ? 276 : 0));
-  const uint8_t* wb = w + int64_t(n0 + r) * wrb + int64_t(b) * 144;
-  R.wc[0] = ld4(wb + 16 * q);
-  R.wc[1] = ld4(wb + 16 * (q + 4));
-  R.wc[2] = ld4(wb + (q == 0 ? 128 : 16 * q));
+  const uint8_t* rp = w + int64_t(n0 + r) * wrb;
+  // 16-byte chunk c of the row's block b: 0 = header, 1 + i = qs bytes [16 i, 16 i + 16)
+  auto chunk = [&](int c) -> const uint8_t* {
+    if constexpr (!PLANAR) {
+      return rp + int64_t(b) * 144 + 16 * c;
+    } else {
+      const int U = 4 * nb, i = c - 1;
+      return c == 0 ? rp + U * 32 + b * 16 : rp + (i & 1) * U * 16 + (4 * b + (i >> 1)) * 16;
+    }
+  };
+  R.wc[0] = ld4(chunk(q));
+  R.wc[1] = ld4(chunk(q + 4));
+  R.wc[2] = ld4(chunk(q == 0 ? 8 : q));
 }
 
 __device__ __forceinline__ void q4k_store(const Q4kRegs& R, Q4kStage& S) {
@@ -111,6 +124,7 @@ __device__ __forceinline__ uint32_t pk_mul(uint32_t x, uint32_t s) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+template <bool PLANAR>
 __global__ void __launch_bounds__(kQ4Threads) gemm_q4k_kernel(const uint8_t* __restrict__ w, int64_t wrb,
                                                                const uint8_t* __restrict__ x, int64_t xrb, int M,
                                                                int N, int nb, float* __restrict__ y) {
@@ -131,12 +145,12 @@ __global__ void __launch_bounds__(kQ4Threads) gemm_q4k_kernel(const uint8_t* __r
     for (int v = 0; v < 16; v++) acc[i][v] = 0.f;
 
   Q4kRegs R;
-  q4k_load(R, x, xrb, m0, M, w, wrb, n0, 0);
+  q4k_load<PLANAR>(R, x, xrb, m0, M, w, wrb, n0, 0, nb);
   q4k_store(R, S[0]);
   __syncthreads();
   for (int b = 0; b < nb; b++) {
     const Q4kStage& T = S[b & 1];
-    if (b + 1 < nb) q4k_load(R, x, xrb, m0, M, w, wrb, n0, b + 1);
+    if (b + 1 < nb) q4k_load<PLANAR>(R, x, xrb, m0, M, w, wrb, n0, b + 1, nb);
     // this lane's weight row: header d, dmin and the 6-bit scales / mins (GGUF Q4_K packing)
     const u32x4 hd = *reinterpret_cast<const u32x4*>(&T.w[nl][0]);
     uint32_t scv[8], mvv[4];
@@ -422,6 +436,35 @@ static int launch_gemm_i8(const int8_t* x, int64_t m, int64_t k, const int8_t* w
 
 using namespace jero;
 
+namespace jero {
+
+int launch_gemm(int quant, const void* w_dev, int64_t n_in, int64_t n_out, const void* xq_dev, int64_t m, float* y_dev,
+                hipStream_t s) {
+  const int act = act_format(quant);
+  const int64_t xrb = row_bytes(act, n_in);
+  if ((quant == JERO_Q4_K || quant == JERO_Q4_K_R) && n_out % kGemmBN == 0) {
+    const int tiles = gemm_tiles(m, n_out);
+    if (quant == JERO_Q4_K)
+      hipLaunchKernelGGL(gemm_q4k_kernel<false>, dim3(unsigned(tiles)), dim3(kQ4Threads), 0, s,
+                         static_cast<const uint8_t*>(w_dev), row_bytes(quant, n_in),
+                         static_cast<const uint8_t*>(xq_dev), xrb, int(m), int(n_out), int(n_in / 256), y_dev);
+    else
+      hipLaunchKernelGGL(gemm_q4k_kernel<true>, dim3(unsigned(tiles)), dim3(kQ4Threads), 0, s,
+                         static_cast<const uint8_t*>(w_dev), row_bytes(quant, n_in),
+                         static_cast<const uint8_t*>(xq_dev), xrb, int(m), int(n_out), int(n_in / 256), y_dev);
+    return check_launch("gemm q4_k");
+  }
+  // other formats and shapes: one GEMV per activation row (each row is matvec_any of x_m)
+  for (int64_t r = 0; r < m; r++) {
+    const int rc = launch_matvec(quant, w_dev, n_in, n_out, static_cast<const uint8_t*>(xq_dev) + r * xrb,
+                                 y_dev + r * n_out, nullptr, s);
+    if (rc) return rc;
+  }
+  return JERO_OK;
+}
+
+}  // namespace jero
+
 extern "C" int jero_hip_gemm(int quant, const void* w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
                              const void* xq_dev, int64_t m, float* y_dev, void* stream) {
   int rc = check_matvec_args(quant, w_dev, w_bytes, n_in, n_out, xq_dev, y_dev);
@@ -429,23 +472,7 @@ extern "C" int jero_hip_gemm(int quant, const void* w_dev, size_t w_bytes, int64
   if (m <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "gemm: no activation rows");
   if (m > (int64_t(1) << 24) || n_out > (int64_t(1) << 30))
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "gemm: m or n_out beyond the 32-bit tile indexing");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int act = act_format(quant);
-  const int64_t xrb = row_bytes(act, n_in);
-  if (quant == JERO_Q4_K && n_out % kGemmBN == 0) {
-    const int tiles = gemm_tiles(m, n_out);
-    hipLaunchKernelGGL(gemm_q4k_kernel, dim3(unsigned(tiles)), dim3(kQ4Threads), 0, s,
-                       static_cast<const uint8_t*>(w_dev), row_bytes(quant, n_in),
-                       static_cast<const uint8_t*>(xq_dev), xrb, int(m), int(n_out), int(n_in / 256), y_dev);
-    return check_launch("gemm q4_k");
-  }
-  // other formats and shapes: one GEMV per activation row (each row is matvec_any of x_m)
-  for (int64_t r = 0; r < m; r++) {
-    rc = launch_matvec(quant, w_dev, n_in, n_out, static_cast<const uint8_t*>(xq_dev) + r * xrb, y_dev + r * n_out,
-                       nullptr, s);
-    if (rc) return rc;
-  }
-  return JERO_OK;
+  return launch_gemm(quant, w_dev, n_in, n_out, xq_dev, m, y_dev, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int jero_hip_gemm_i8(const int8_t* x_dev, int64_t m, int64_t k, const int8_t* w_dev, int64_t n,

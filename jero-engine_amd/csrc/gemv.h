@@ -21,6 +21,10 @@ int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, in
 // Enqueues y = W xq (and the int32 partial sums when part != nullptr).
 int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, float* y, int32_t* part,
                   hipStream_t s);
+// Y[m][n_out] for m activation rows (jero_hip_gemm after its checks): the int8-MFMA kernel for
+// Q4_K and Q4_K_R with n_out a multiple of 128, one GEMV per row otherwise.
+int launch_gemm(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, int64_t m, float* y,
+                hipStream_t s);
 // Enqueues the Q4_K -> Q4_K_R or Q6_K -> Q6_K_R re-layout (dst: 16-byte aligned, same size).
 int launch_repack(int quant, const void* src, int64_t n_in, int64_t n_out, void* dst, int* dst_quant, hipStream_t s);
 int launch_repack_experts(int quant, const void* src, int64_t n_in, int64_t n_rows, void* dst, int* dst_quant,

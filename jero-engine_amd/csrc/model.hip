@@ -22,6 +22,8 @@
 #include "decode.h"
 #include "gemv.h"
 #include "jero_common.h"
+#include "prefill.h"
+#include "quantize.h"
 #include "runtime.h"
 
 namespace jero {
@@ -45,6 +47,16 @@ struct LayerW {
   bool qkv_split = false, gu_split = false;
 };
 
+// Row buffers of the batched prefill, grown on demand (rows tokens at a time).
+struct PrefillBufs {
+  int64_t rows = 0;
+  size_t ws_bytes = 0;
+  int32_t* tok = nullptr;
+  float *X = nullptr, *XN = nullptr, *T = nullptr, *QKV = nullptr, *ATT = nullptr, *GU = nullptr, *ACT = nullptr,
+        *RC = nullptr, *ws = nullptr;
+  uint8_t* XQ = nullptr;
+};
+
 }  // namespace jero
 
 struct jero_model {
@@ -66,6 +78,8 @@ struct jero_model {
   size_t kv_bytes = 0;
   std::vector<void*> owned;
   uint8_t* trace = nullptr;  // debug trace buffer of the caller (jero_hip_model_trace), or null
+  size_t trace_bytes = 0;
+  jero::PrefillBufs pf;
 };
 
 namespace jero {
@@ -480,6 +494,7 @@ extern "C" int jero_hip_model_trace(jero_model* m, void* trace_dev, size_t trace
   if (reinterpret_cast<uintptr_t>(trace_dev) & 15u)
     return fail(JERO_ERR_INVALID_ARGUMENT, "model_trace: buffer must be 16-byte aligned");
   m->trace = static_cast<uint8_t*>(trace_dev);
+  m->trace_bytes = trace_bytes;
   return JERO_OK;
 }
 
@@ -652,6 +667,232 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
   rc = gemv(m, m->output, m->hidden, static_cast<const float*>(m->output_norm.dev), eps_ffn, kOutArgmax, m->logits, 0,
             s, &head_blocks, tr_tail ? reinterpret_cast<float*>(tr_tail + tl.xn_head) : nullptr,
             tr_tail ? tr_tail + tl.q8_head : nullptr);
+  if (rc) return rc;
+  return launch_argmax_final(m->amax_v, m->amax_i, head_blocks, m->token, m->pos, m->status, s);
+}
+
+namespace jero {
+
+// Attention queries per launch of the batched prefill: bounds its split workspace.
+constexpr int64_t kPrefillAttnTokens = 256;
+
+static int prefill_buffers(jero_model* m, int64_t n, int64_t pos0) {
+  const auto& c = m->cfg;
+  const int64_t H = c.hidden, F = c.ffn, Q = q_dim(c), KV = kv_dim(c);
+  const int64_t tq = std::min(n, kPrefillAttnTokens);
+  const size_t ws = size_t(tq) * attn_workspace_bytes(c.n_heads_q, c.head_dim, int(pos0 + n));
+  PrefillBufs& b = m->pf;
+  if (n <= b.rows && ws <= b.ws_bytes) return JERO_OK;
+  const int64_t rows = std::max(n, b.rows);
+  for (void* p : {static_cast<void*>(b.tok), static_cast<void*>(b.X), static_cast<void*>(b.XN),
+                  static_cast<void*>(b.T), static_cast<void*>(b.QKV), static_cast<void*>(b.ATT),
+                  static_cast<void*>(b.GU), static_cast<void*>(b.ACT), static_cast<void*>(b.RC),
+                  static_cast<void*>(b.ws), static_cast<void*>(b.XQ)})
+    if (p) dev_free(m, p);
+  b = PrefillBufs{};
+  auto act_row = [](int64_t k) { return std::max(k / 32 * 36, k / 256 * 292); };
+  const size_t xq_row = size_t(std::max({act_row(H), act_row(Q), act_row(F)}));
+  void* p = nullptr;
+  int rc;
+  auto f32 = [&](int64_t count, float** out) -> int {
+    int r = dev_alloc(m, sizeof(float) * size_t(count), &p);
+    if (!r) *out = static_cast<float*>(p);
+    return r;
+  };
+  if ((rc = dev_alloc(m, sizeof(int32_t) * size_t(rows), &p))) return rc;
+  b.tok = static_cast<int32_t*>(p);
+  if ((rc = f32(rows * H, &b.X)) || (rc = f32(rows * H, &b.XN)) || (rc = f32(rows * H, &b.T)) ||
+      (rc = f32(rows * (Q + 2 * KV), &b.QKV)) || (rc = f32(rows * Q, &b.ATT)) || (rc = f32(rows * 2 * F, &b.GU)) ||
+      (rc = f32(rows * F, &b.ACT)) || (rc = f32(rows * c.head_dim, &b.RC)))
+    return rc;
+  if ((rc = dev_alloc(m, ws, &p))) return rc;
+  b.ws = static_cast<float*>(p);
+  if ((rc = dev_alloc(m, xq_row * size_t(rows), &p))) return rc;
+  b.XQ = static_cast<uint8_t*>(p);
+  b.rows = rows;
+  b.ws_bytes = ws;
+  return JERO_OK;
+}
+
+}  // namespace jero
+
+extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int64_t n, int64_t pos0, void* stream) {
+  if (!m || !tokens) return fail(JERO_ERR_INVALID_ARGUMENT, "prefill: null pointer");
+  if (!m->finalized) return fail(JERO_ERR_INVALID_ARGUMENT, "prefill: model not finalized");
+  const auto& c = m->cfg;
+  if (n <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "prefill: no tokens");
+  if (pos0 < 0 || pos0 + n > c.kv_capacity)
+    return fail(JERO_ERR_CONTEXT_LENGTH_EXCEEDED, "prefill: positions " + std::to_string(pos0) + " .. " +
+                                                      std::to_string(pos0 + n - 1) + " exceed the ring of " +
+                                                      std::to_string(c.kv_capacity));
+  for (int64_t t = 0; t < n; t++)
+    if (tokens[t] < 0 || tokens[t] >= c.vocab)
+      return fail(JERO_ERR_TENSOR_BOUNDS, "prefill: token " + std::to_string(tokens[t]) + " outside the vocabulary");
+  const TraceLayout tl = trace_layout(c);
+  if (m->trace && m->trace_bytes < size_t(n) * tl.total)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "prefill: the trace buffer holds fewer than " + std::to_string(n) + " steps");
+  int rc = prefill_buffers(m, n, pos0);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  PrefillBufs& b = m->pf;
+  const int64_t H = c.hidden, F = c.ffn, Q = q_dim(c), KV = kv_dim(c);
+  const float eps_attn = c.rms_eps;
+  const float eps_ffn = c.rms_eps > 1e-6f ? c.rms_eps : 1e-6f;
+  const size_t es = c.kv_dtype == JERO_KV_F16 ? 2 : 4;
+  const size_t ring = size_t(c.kv_capacity) * size_t(KV) * es;
+  if ((rc = check_hip(hipMemcpyAsync(b.tok, tokens, sizeof(int32_t) * size_t(n), hipMemcpyHostToDevice, s),
+                      "prefill tokens")))
+    return rc;
+  // token t's trace (the decode step's layout) at t * tl.total: one strided copy per field
+  auto snap = [&](size_t off, const void* src, size_t pitch, size_t width) -> int {
+    if (!m->trace) return JERO_OK;
+    return check_hip(hipMemcpy2DAsync(m->trace + off, tl.total, src, pitch, width, size_t(n), hipMemcpyDeviceToDevice, s),
+                     "prefill trace copy");
+  };
+  auto fld = [&](int64_t L, int f) { return size_t(L) * tl.layer_bytes + tl.field[f]; };
+  // quantizes n rows of k floats into b.XQ in `fmt`; returns its row bytes
+  auto quant_rows = [&](int fmt, const float* x, int64_t k, int64_t* xrb) -> int {
+    *xrb = row_bytes(fmt, k);
+    return launch_quantize_act(fmt, x, n, k, b.XQ, s);
+  };
+  if ((rc = launch_embed_rows(m->tok_embd.quant, m->tok_embd.dev, row_bytes(m->tok_embd.quant, H), int(H), b.tok, n,
+                              b.X, s)))
+    return rc;
+  for (int64_t L = 0; L < c.n_layers; L++) {
+    const LayerW& l = m->layers[size_t(L)];
+    const float* anw = static_cast<const float*>(l.attn_norm.dev);
+    if ((rc = snap(fld(L, TraceLayout::kXIn), b.X, 4 * H, 4 * H))) return rc;
+    // attention sublayer: RMSNorm rows -> Q, K, V rows
+    if ((rc = launch_rmsnorm_rows(b.X, n, H, anw, eps_attn, b.XN, s))) return rc;
+    if ((rc = snap(fld(L, TraceLayout::kXnAttn), b.XN, 4 * H, 4 * H))) return rc;
+    float *qp, *kp, *vp;
+    int64_t qs, ks, vs;
+    int64_t xrb = 0;
+    int have_fmt = -1;
+    auto project = [&](const DevTensor& w, const float* in, int64_t k, float* out, int trace_field) -> int {
+      const int fmt = act_format(w.quant);
+      int r = JERO_OK;
+      if (fmt != have_fmt) {
+        if ((r = quant_rows(fmt, in, k, &xrb))) return r;
+        have_fmt = fmt;
+        if (trace_field >= 0 && (r = snap(fld(L, trace_field), b.XQ, size_t(xrb), size_t(xrb)))) return r;
+      }
+      return launch_gemm(w.quant, w.dev, k, w.n_out, b.XQ, n, out, s);
+    };
+    if (!l.qkv_split) {
+      const int64_t w1 = l.qkv.n_out;  // Q + 2 KV, or Q + KV with V apart
+      qp = b.QKV, qs = w1, kp = b.QKV + Q, ks = w1;
+      if ((rc = project(l.qkv, b.XN, H, b.QKV, TraceLayout::kQ8Attn))) return rc;
+      if (l.v_separate) {
+        vp = b.QKV + n * w1, vs = KV;
+        if ((rc = project(l.wv, b.XN, H, vp, -1))) return rc;
+      } else {
+        vp = b.QKV + Q + KV, vs = w1;
+      }
+    } else {
+      qp = b.QKV, qs = Q, kp = b.QKV + n * Q, ks = KV, vp = b.QKV + n * (Q + KV), vs = KV;
+      const DevTensor* w3[3] = {&l.wq, &l.wk, &l.wv};
+      float* o3[3] = {qp, kp, vp};
+      const int64_t len[3] = {Q, KV, KV};
+      const float sc[3] = {0.5f, 0.25f, 0.125f};
+      bool first = true;  // the trace holds the first present projection's activation rows
+      for (int j = 0; j < 3; j++) {
+        if (w3[j]->present()) {
+          rc = project(*w3[j], b.XN, H, o3[j], first ? TraceLayout::kQ8Attn : -1);
+          first = false;
+        } else {  // project_or_deterministic_slice's fallback of the normalised rows
+          rc = launch_det_proj(b.X, H, anw, eps_attn, sc[j], o3[j], len[j], false, s, n, H, len[j]);
+        }
+        if (rc) return rc;
+      }
+    }
+    const size_t fq = fld(L, TraceLayout::kQkv);
+    if ((rc = snap(fq, qp, 4 * qs, 4 * Q)) || (rc = snap(fq + 4 * Q, kp, 4 * ks, 4 * KV)) ||
+        (rc = snap(fq + 4 * (Q + KV), vp, 4 * vs, 4 * KV)))
+      return rc;
+    // QK-norm, RoPE, the K/V rows into the ring, causal attention of every token
+    uint8_t* base = static_cast<uint8_t*>(m->kv) + size_t(L) * 2 * ring;
+    if ((rc = launch_qk_rope_rows(qp, qs, kp, ks, vp, vs, n, c.n_heads_q, c.n_heads_kv, c.head_dim,
+                                  c.qk_norm ? static_cast<const float*>(l.q_norm.dev) : nullptr,
+                                  c.qk_norm ? static_cast<const float*>(l.k_norm.dev) : nullptr, eps_attn, pos0,
+                                  c.rope_theta, b.RC, base, base + ring, c.kv_dtype == JERO_KV_F16, c.kv_capacity, s)))
+      return rc;
+    if ((rc = snap(fld(L, TraceLayout::kQRope), qp, 4 * qs, 4 * Q)) ||
+        (rc = snap(fld(L, TraceLayout::kKRope), kp, 4 * ks, 4 * KV)))
+      return rc;
+    for (int64_t t0 = 0; t0 < n; t0 += kPrefillAttnTokens) {
+      const int64_t nt = std::min(kPrefillAttnTokens, n - t0);
+      AttnParams p{};
+      p.q = qp + t0 * qs;
+      p.k = base;
+      p.v = base + ring;
+      p.kv_dtype = c.kv_dtype;
+      p.nkv = c.n_heads_kv;
+      p.group = c.n_heads_q / c.n_heads_kv;
+      p.hd = c.head_dim;
+      p.active = int(pos0 + t0 + 1);
+      p.scale = 1.0f / sqrtf(float(c.head_dim));
+      p.part_o = b.ws;
+      p.slot = -1;
+      if ((rc = launch_attention_tokens(p, int(nt), qs, b.ATT + t0 * Q, Q, s))) return rc;
+    }
+    if ((rc = snap(fld(L, TraceLayout::kAttn), b.ATT, 4 * Q, 4 * Q))) return rc;
+    // output projection + residual
+    have_fmt = -1;
+    if (l.wo.present()) {
+      if ((rc = project(l.wo, b.ATT, Q, b.T, TraceLayout::kQ8Wo)) || (rc = launch_add_rows(b.X, b.T, n * H, s)))
+        return rc;
+    } else if ((rc = launch_det_proj(b.ATT, Q, nullptr, 0.f, 0.25f, b.X, H, true, s, n, Q, H))) {
+      return rc;
+    }
+    if ((rc = snap(fld(L, TraceLayout::kXMid), b.X, 4 * H, 4 * H))) return rc;
+    // FFN: RMSNorm rows -> gate | up -> SwiGLU -> down + residual
+    const float* fnw = static_cast<const float*>(l.ffn_norm.dev);
+    if ((rc = launch_rmsnorm_rows(b.X, n, H, fnw, eps_ffn, b.XN, s))) return rc;
+    if ((rc = snap(fld(L, TraceLayout::kXnFfn), b.XN, 4 * H, 4 * H))) return rc;
+    have_fmt = -1;
+    const size_t fg = fld(L, TraceLayout::kGu);
+    if (!l.gu_split) {
+      if ((rc = project(l.gate_up, b.XN, H, b.GU, TraceLayout::kQ8Ffn)) ||
+          (rc = launch_swiglu_rows(b.GU, 2 * F, b.GU + F, 2 * F, b.ACT, n, F, s)) ||
+          (rc = snap(fg, b.GU, 8 * F, 8 * F)))
+        return rc;
+    } else {
+      float* g2[2] = {b.GU, b.GU + n * F};
+      const DevTensor* w2[2] = {&l.gate, &l.up};
+      const float sc[2] = {0.5f, 0.25f};
+      bool first = true;
+      for (int j = 0; j < 2; j++) {
+        if (w2[j]->present()) {
+          rc = project(*w2[j], b.XN, H, g2[j], first ? TraceLayout::kQ8Ffn : -1);
+          first = false;
+        } else {
+          rc = launch_det_proj(b.X, H, fnw, eps_ffn, sc[j], g2[j], F, false, s, n, H, F);
+        }
+        if (rc) return rc;
+      }
+      if ((rc = launch_swiglu_rows(g2[0], F, g2[1], F, b.ACT, n, F, s)) || (rc = snap(fg, g2[0], 4 * F, 4 * F)) ||
+          (rc = snap(fg + 4 * F, g2[1], 4 * F, 4 * F)))
+        return rc;
+    }
+    if ((rc = snap(fld(L, TraceLayout::kAct), b.ACT, 4 * F, 4 * F))) return rc;
+    have_fmt = -1;
+    if (l.down.present()) {
+      if ((rc = project(l.down, b.ACT, F, b.T, TraceLayout::kQ8Down)) || (rc = launch_add_rows(b.X, b.T, n * H, s)))
+        return rc;
+    } else if ((rc = launch_det_proj(b.ACT, F, nullptr, 0.f, 0.125f, b.X, H, true, s, n, F, H))) {
+      return rc;
+    }
+  }
+  // every token's final hidden state and RoPE table; the head on the last token only
+  if ((rc = snap(tl.x_final, b.X, 4 * H, 4 * H)) || (rc = snap(tl.rope_cs, b.RC, 4 * size_t(c.head_dim), 4 * size_t(c.head_dim))))
+    return rc;
+  if ((rc = launch_set_state(m->token, m->pos, m->status, tokens[n - 1], pos0 + n - 1, s))) return rc;
+  uint8_t* tr_last = m->trace ? m->trace + size_t(n - 1) * tl.total : nullptr;
+  int head_blocks = 0;
+  rc = gemv(m, m->output, b.X + (n - 1) * H, static_cast<const float*>(m->output_norm.dev), eps_ffn, kOutArgmax,
+            m->logits, 0, s, &head_blocks, tr_last ? reinterpret_cast<float*>(tr_last + tl.xn_head) : nullptr,
+            tr_last ? tr_last + tl.q8_head : nullptr);
   if (rc) return rc;
   return launch_argmax_final(m->amax_v, m->amax_i, head_blocks, m->token, m->pos, m->status, s);
 }

@@ -1,0 +1,27 @@
+// prefill.h -- row kernels of the batched prefill (jero_hip_model_prefill).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace jero {
+
+// X[t] = embedding row of tokens[t] (device array), t < n.
+int launch_embed_rows(int quant, const void* w, int64_t rb, int H, const int32_t* tokens, int64_t n, float* X,
+                      hipStream_t s);
+// XN[t] = RMSNorm(X[t]) * w, rows of H floats.
+int launch_rmsnorm_rows(const float* X, int64_t n, int64_t H, const float* w, float eps, float* XN, hipStream_t s);
+// Per token t < n (position pos0 + t): QK-norm (when given) and RoPE of its q heads (row t at q +
+// t q_stride) and k heads (k + t k_stride), in place, the k and v heads (v + t v_stride) appended
+// to ring slot (pos0 + t) % capacity, and the RoPE table of the token into rope_cs[t][hd].
+int launch_qk_rope_rows(float* q, int64_t q_stride, float* k, int64_t k_stride, const float* v, int64_t v_stride,
+                        int64_t n, int nq, int nkv, int hd, const float* q_norm, const float* k_norm, float eps,
+                        int64_t pos0, float theta, float* rope_cs, void* k_ring, void* v_ring, bool kv_f16,
+                        int64_t capacity, hipStream_t s);
+// act[t][i] = silu(g[t][i]) * u[t][i], act rows of F floats.
+int launch_swiglu_rows(const float* g, int64_t g_stride, const float* u, int64_t u_stride, float* act, int64_t n,
+                       int64_t F, hipStream_t s);
+// x[i] += d[i], i < count.
+int launch_add_rows(float* x, const float* d, int64_t count, hipStream_t s);
+
+}  // namespace jero

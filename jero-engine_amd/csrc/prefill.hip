@@ -1,0 +1,165 @@
+// prefill.hip -- the row kernels of the batched prefill (jero_hip_model_prefill): the n prompt
+// tokens go through each layer at once, as GEMMs over n activation rows, instead of
+// run_prefill_with_hidden's token loop (src/qwen_deepseek.rs:2217-2316, loop :2298-2312).  Each
+// kernel is the per-token arithmetic of the decode step applied to every row: the embedding row,
+// RMSNorm, QK-norm and RoPE (the fused attention prologue's formulas), the K/V ring append,
+// SwiGLU and the residual add.
+#include "prefill.h"
+
+#include "dequant.h"
+#include "jero_common.h"
+#include "runtime.h"
+
+namespace jero {
+
+namespace {
+
+// X[t][i] = embedding row tokens[t]; grid (ceil(H / 256), n).
+__global__ void __launch_bounds__(256) embed_rows_kernel(int quant, const uint8_t* __restrict__ w, int64_t rb, int H,
+                                                         const int32_t* __restrict__ tokens, float* __restrict__ X) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= H) return;
+  X[int64_t(blockIdx.y) * H + i] = dequant_elem(quant, w + int64_t(tokens[blockIdx.y]) * rb, i);
+}
+
+__device__ __forceinline__ float block_sum256(float v, float* s_tmp) {
+  v = wave_sum_dpp(v);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) s_tmp[wv] = v;
+  __syncthreads();
+  return s_tmp[0] + s_tmp[1] + s_tmp[2] + s_tmp[3];
+}
+
+// XN[t] = RMSNorm(X[t]) * w: x * (1 / sqrt(mean(x^2) + eps)) * w; one workgroup per row.
+__global__ void __launch_bounds__(256) rmsnorm_rows_kernel(const float* __restrict__ X, int64_t H,
+                                                           const float* __restrict__ w, float eps,
+                                                           float* __restrict__ XN) {
+  __shared__ float s_tmp[4];
+  const float* x = X + int64_t(blockIdx.x) * H;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < H; i += 256) ss += x[i] * x[i];
+  ss = block_sum256(ss, s_tmp);
+  const float inv = 1.0f / sqrtf(ss / float(H) + eps);
+  float* y = XN + int64_t(blockIdx.x) * H;
+  for (int64_t i = threadIdx.x; i < H; i += 256) y[i] = x[i] * inv * w[i];
+}
+
+// One wave per (token t = blockIdx.x, head y = blockIdx.y): y < nq a q head, y < nq + nkv a k
+// head (both: per-head RMSNorm when a norm is given, then RoPE at position pos0 + t with the
+// decode step's table cos / sin of pos / theta^(2i / hd), written back in place; k also into its
+// ring slot), otherwise a v head (into its ring slot).  Lane l < hd / 2 holds pair (2l, 2l + 1).
+// Token t's table also goes to rope_cs[t][hd] (the trace of its step).
+template <typename KV>
+__global__ void __launch_bounds__(64) qk_rope_rows_kernel(float* __restrict__ q, int64_t q_stride, float* __restrict__ k,
+                                                          int64_t k_stride, const float* __restrict__ v,
+                                                          int64_t v_stride, int nq, int nkv, int hd,
+                                                          const float* __restrict__ q_norm,
+                                                          const float* __restrict__ k_norm, float eps, int64_t pos0,
+                                                          float theta, float* __restrict__ rope_cs,
+                                                          KV* __restrict__ k_ring, KV* __restrict__ v_ring,
+                                                          int64_t capacity) {
+  const int t = blockIdx.x, y = blockIdx.y, lane = threadIdx.x;
+  const int64_t pos = pos0 + t;
+  const int64_t slot = pos % capacity;
+  const int64_t kvd = int64_t(nkv) * hd;
+  const bool on = lane < hd / 2;
+  const int pr = on ? lane : hd / 2 - 1;
+  if (y >= nq + nkv) {  // v head: ring append only
+    const int h = y - nq - nkv;
+    const float2 x = reinterpret_cast<const float2*>(v + t * v_stride + int64_t(h) * hd)[pr];
+    if (on) {
+      KV* dst = v_ring + slot * kvd + int64_t(h) * hd + 2 * lane;
+      dst[0] = KV(x.x);
+      dst[1] = KV(x.y);
+    }
+    return;
+  }
+  const float expo = float(2 * pr) / float(hd);
+  float sn, cn;
+  sincosf(float(pos) / powf(theta, expo), &sn, &cn);
+  if (y == 0 && on) {
+    rope_cs[int64_t(t) * hd + 2 * lane] = cn;
+    rope_cs[int64_t(t) * hd + 2 * lane + 1] = sn;
+  }
+  const bool isq = y < nq;
+  float* row = isq ? q + t * q_stride + int64_t(y) * hd : k + t * k_stride + int64_t(y - nq) * hd;
+  const float* nw = isq ? q_norm : k_norm;
+  float2 x = reinterpret_cast<const float2*>(row)[pr];
+  if (nw) {
+    const float ss = wave_sum_dpp(on ? x.x * x.x + x.y * x.y : 0.f);
+    const float inv = 1.0f / sqrtf(ss / float(hd) + eps);
+    const float2 g = reinterpret_cast<const float2*>(nw)[pr];
+    x.x = x.x * inv * g.x;
+    x.y = x.y * inv * g.y;
+  }
+  const float2 r = make_float2(x.x * cn - x.y * sn, x.x * sn + x.y * cn);
+  if (on) {
+    reinterpret_cast<float2*>(row)[lane] = r;
+    if (!isq) {
+      KV* dst = k_ring + slot * kvd + int64_t(y - nq) * hd + 2 * lane;
+      dst[0] = KV(r.x);
+      dst[1] = KV(r.y);
+    }
+  }
+}
+
+// act[t][i] = silu(g[t][i]) * u[t][i] (the decode step's SwiGLU formula); grid (ceil(F / 256), n).
+__global__ void __launch_bounds__(256) swiglu_rows_kernel(const float* __restrict__ g, int64_t g_stride,
+                                                          const float* __restrict__ u, int64_t u_stride,
+                                                          float* __restrict__ act, int64_t F) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= F) return;
+  const int64_t t = blockIdx.y;
+  const float gv = g[t * g_stride + i], uv = u[t * u_stride + i];
+  act[t * F + i] = gv / (1.0f + expf(-gv)) * uv;
+}
+
+// x[i] += d[i] (the residual of Wo and down).
+__global__ void __launch_bounds__(256) add_rows_kernel(float* __restrict__ x, const float* __restrict__ d, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) x[i] += d[i];
+}
+
+}  // namespace
+
+int launch_embed_rows(int quant, const void* w, int64_t rb, int H, const int32_t* tokens, int64_t n, float* X,
+                      hipStream_t s) {
+  hipLaunchKernelGGL(embed_rows_kernel, dim3(unsigned((H + 255) / 256), unsigned(n)), dim3(256), 0, s, quant,
+                     static_cast<const uint8_t*>(w), rb, H, tokens, X);
+  return check_launch("prefill embed");
+}
+
+int launch_rmsnorm_rows(const float* X, int64_t n, int64_t H, const float* w, float eps, float* XN, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(unsigned(n)), dim3(256), 0, s, X, H, w, eps, XN);
+  return check_launch("prefill rmsnorm");
+}
+
+int launch_qk_rope_rows(float* q, int64_t q_stride, float* k, int64_t k_stride, const float* v, int64_t v_stride,
+                        int64_t n, int nq, int nkv, int hd, const float* q_norm, const float* k_norm, float eps,
+                        int64_t pos0, float theta, float* rope_cs, void* k_ring, void* v_ring, bool kv_f16,
+                        int64_t capacity, hipStream_t s) {
+  const dim3 grid(unsigned(n), unsigned(nq + 2 * nkv));
+  if (kv_f16)
+    hipLaunchKernelGGL(qk_rope_rows_kernel<_Float16>, grid, dim3(64), 0, s, q, q_stride, k, k_stride, v, v_stride, nq,
+                       nkv, hd, q_norm, k_norm, eps, pos0, theta, rope_cs, static_cast<_Float16*>(k_ring),
+                       static_cast<_Float16*>(v_ring), capacity);
+  else
+    hipLaunchKernelGGL(qk_rope_rows_kernel<float>, grid, dim3(64), 0, s, q, q_stride, k, k_stride, v, v_stride, nq,
+                       nkv, hd, q_norm, k_norm, eps, pos0, theta, rope_cs, static_cast<float*>(k_ring),
+                       static_cast<float*>(v_ring), capacity);
+  return check_launch("prefill qk-norm / rope");
+}
+
+int launch_swiglu_rows(const float* g, int64_t g_stride, const float* u, int64_t u_stride, float* act, int64_t n,
+                       int64_t F, hipStream_t s) {
+  hipLaunchKernelGGL(swiglu_rows_kernel, dim3(unsigned((F + 255) / 256), unsigned(n)), dim3(256), 0, s, g, g_stride,
+                     u, u_stride, act, F);
+  return check_launch("prefill swiglu");
+}
+
+int launch_add_rows(float* x, const float* d, int64_t count, hipStream_t s) {
+  hipLaunchKernelGGL(add_rows_kernel, dim3(unsigned((count + 255) / 256)), dim3(256), 0, s, x, d, count);
+  return check_launch("prefill residual");
+}
+
+}  // namespace jero

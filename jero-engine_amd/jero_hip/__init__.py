@@ -84,6 +84,7 @@ _SIGS = {
     "jero_hip_model_state": (_I32, [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_P)]),
     "jero_hip_model_set_position": (_I32, [_P, _I32, _I64, _P]),
     "jero_hip_decode_step": (_I32, [_P, _P]),
+    "jero_hip_model_prefill": (_I32, [_P, _P, _I64, _I64, _P]),
     "jero_hip_gguf_open": (_I32, [C.c_char_p, C.POINTER(_P)]),
     "jero_hip_gguf_close": (None, [_P]),
     "jero_hip_gguf_info": (_I32, [_P, C.POINTER(_I64), C.POINTER(C.c_char_p)]),
@@ -597,6 +598,14 @@ class DecodeModel:
 
     def set_position(self, token, pos, stream=None):
         check(lib().jero_hip_model_set_position(self.h, token, pos, _stream(stream)))
+
+    def prefill(self, tokens, pos0, stream=None):
+        """run_prefill_with_hidden over `tokens` from position pos0 in one pass
+        (jero_hip_model_prefill): leaves the last token's logits, the greedy next token and
+        position pos0 + len(tokens)."""
+        import numpy as np
+        t = np.ascontiguousarray(np.asarray(tokens, np.int32))
+        check(lib().jero_hip_model_prefill(self.h, t.ctypes.data, t.size, pos0, _stream(stream)))
 
     def decode_step(self, stream=None):
         check(lib().jero_hip_decode_step(self.h, _stream(stream)))

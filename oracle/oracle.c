@@ -817,6 +817,11 @@ int jo_decode_layer(const jo_model *M, float *kv, int64_t L, float *x, int64_t p
     int64_t slot = pos % cap, active = pos + 1 < cap ? pos + 1 : cap;
     memcpy(kring + slot * kvd, k, (size_t)kvd * 4);
     memcpy(vring + slot * kvd, v, (size_t)kvd * 4);
+    if (M->kv_f16) /* an f16 ring: the new row as the ring holds it, before it is attended */
+      for (int64_t i = 0; i < kvd; i++) {
+        kring[slot * kvd + i] = jo_f16_to_f32(jo_f32_to_f16(kring[slot * kvd + i]));
+        vring[slot * kvd + i] = jo_f16_to_f32(jo_f32_to_f16(vring[slot * kvd + i]));
+      }
     rc |= jo_gqa_attention(att, q, kring, vring, M->nq, M->nkv, M->hd, active, 1.0f / sqrtf((float)M->hd));
   }
   if (!rc) {

@@ -142,6 +142,7 @@ typedef struct jo_model {
   jo_tensor tok_embd, output;
   const float *output_norm;
   const jo_layer *layers;
+  int kv_f16; /* nonzero: the rings hold f16 values (each new K/V row rounded before it is attended) */
 } jo_model;
 
 /* Intermediate values of one layer of the decode step (every pointer optional):

@@ -233,7 +233,7 @@ class JoModel(C.Structure):
     _fields_ = [("hidden", C.c_int64), ("ffn", C.c_int64), ("n_layers", C.c_int64), ("vocab", C.c_int64),
                 ("nq", C.c_int), ("nkv", C.c_int), ("hd", C.c_int), ("eps", C.c_float), ("theta", C.c_float),
                 ("kv_capacity", C.c_int64), ("tok_embd", JoTensor), ("output", JoTensor),
-                ("output_norm", C.c_void_p), ("layers", C.c_void_p)]
+                ("output_norm", C.c_void_p), ("layers", C.c_void_p), ("kv_f16", C.c_int)]
 
 
 class JoLayerTrace(C.Structure):

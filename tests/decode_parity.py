@@ -301,6 +301,17 @@ def _adopt(stats, tag, fmt, n, x_or, dev_q8, dev_x):
 
 
 def oracle_step_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True, threads=16, dev_rows=None):
+    """The step's layers (oracle_layers_adopting), then the head adopting the device's head input
+    bytes the same way.  Returns (logits, FlipStats, f16 flips)."""
+    x, st, f16_flips = oracle_layers_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm, threads, dev_rows)
+    eps_ffn = max(spec["eps"], 1e-6)
+    xn = O.rmsnorm(x, t["output_norm.weight"][1], eps_ffn)
+    fh = act_fmt(t["output.weight"][0])
+    hq = _adopt(st, "head input", fh, spec["hidden"], xn, dev_head["q8_head"], dev_head["xn_head"])
+    return _mv(t, "output.weight", hq, threads), st, f16_flips
+
+
+def oracle_layers_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True, threads=16, dev_rows=None):
     """The oracle's decode step from hidden state x (the embedding row) and its f32 rings kv,
     adopting the device's activation bytes at each quantization point after tie_flips has
     accounted for every difference, and rotating by the device's RoPE table (check_rope_table
@@ -308,7 +319,7 @@ def oracle_step_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True
     at position p moves the rotation by up to ~p * 2.4e-7).  dev_rows (f16 rings): per layer
     the device's new (k, v) ring rows; the oracle's own rows, rounded to f16, are accounted
     against them by f16_tie_flips and the device's rows are attended to.  Returns (logits,
-    FlipStats, f16 flips)."""
+    FlipStats, f16 flips) -- here the hidden state after the last layer in place of the logits."""
     H, F = spec["hidden"], spec["ffn"]
     nq, nkv, hd = spec["nq"], spec["nkv"], spec["hd"]
     Q, KV = nq * hd, nkv * hd
@@ -355,10 +366,7 @@ def oracle_step_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True
         fd = act_fmt(t[p + "ffn_down.weight"][0])
         dq8 = _adopt(st, f"layer {L} down input", fd, F, a, D["q8_down"], D["act"])
         x = (x + _mv(t, p + "ffn_down.weight", dq8, threads)).astype(np.float32)
-    xn = O.rmsnorm(x, t["output_norm.weight"][1], eps_ffn)
-    fh = act_fmt(t["output.weight"][0])
-    hq = _adopt(st, "head input", fh, H, xn, dev_head["q8_head"], dev_head["xn_head"])
-    return _mv(t, "output.weight", hq, threads), st, f16_flips
+    return x, st, f16_flips
 
 
 def read_ring(m, L, cap, kvd, kv_f16):
@@ -401,6 +409,7 @@ def run_traced(m, om, t, spec, kv, cap, pos0, steps, kv_f16, dev, tok, qk_norm=T
     logits = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
     m.set_position(tok, pos0)
     kv_free = kv.copy()
+    om.model.kv_f16 = 1 if kv_f16 else 0  # the plain oracle's rings hold what the device's hold
     flips_so_far = 0
     out = []
     try:
@@ -430,8 +439,6 @@ def run_traced(m, om, t, spec, kv, cap, pos0, steps, kv_f16, dev, tok, qk_norm=T
             ref, st, f16_flips = oracle_step_adopting(t, spec, kv, pos, x0, dl, dh, qk_norm, threads,
                                                       dev_rows if kv_f16 else None)
             free = om.step(kv_free, tok, pos, threads=threads)
-            if kv_f16:  # the device ring holds the new row in f16: so does the plain oracle's
-                kv_free[:, :, pos % cap] = kv_free[:, :, pos % cap].astype(np.float16).astype(np.float32)
             err, cs = rel(got, ref), cosine(got, ref)
             ferr, fcs = rel(got, free), cosine(got, free)
             print(f"  pos {pos}: teacher-forced max errors " +
@@ -452,3 +459,68 @@ def run_traced(m, om, t, spec, kv, cap, pos0, steps, kv_f16, dev, tok, qk_norm=T
     finally:
         m.set_trace(None)
     return out
+
+
+def run_prefill_traced(m, om, t, spec, kv, cap, pos0, tokens, kv_f16, dev, qk_norm=True, threads=16):
+    """jero_hip_model_prefill of `tokens` from position pos0 with the trace on.  Prefill writes
+    token i's trace in the decode step's layout, so every prompt token is held to the decode
+    step's bars: teacher-forced checks of every layer (check_layer, attention over the ring up to
+    its own position); end to end, the oracle's token loop (run_prefill_with_hidden) adopting the
+    device's activation bytes only at accounted tie flips, each token's final hidden state within
+    1e-3 and, on the last token, the head checks and the logits within 1e-3.  kv: the oracle's f32
+    rings, advanced in step.  Returns (greedy token, per-token (tie flips, hidden/logits error))."""
+    import torch
+    L_n = spec["n_layers"]
+    kvd = spec["nkv"] * spec["hd"]
+    n = len(tokens)
+    _, _, _, total = m.trace_layout()
+    buf = torch.zeros(n * total, dtype=torch.uint8, device=dev)
+    m.set_trace(buf)
+    try:
+        m.prefill(tokens, pos0)
+        m.status()
+    finally:
+        m.set_trace(None)
+    logits = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
+    m.read_logits(logits)
+    got = logits.cpu().numpy()
+    gtok, gpos = m.read_token_pos()
+    assert gpos == pos0 + n
+    rings = [read_ring(m, L, cap, kvd, kv_f16) for L in range(L_n)]
+    out = []
+    for i, tok in enumerate(tokens):
+        pos = pos0 + i
+        dl, dh = m.read_trace(buf[i * total:(i + 1) * total])
+        x0 = om.embed(tok)
+        assert np.array_equal(dl[0]["x_in"], x0), ("embedding row differs", i)
+        check_rope_table(spec, pos, dh["rope_cs"])
+        dev_rows = []
+        worst = {}
+        for L in range(L_n):
+            rk, rv = rings[L]
+            dev_rows.append((rk[pos % cap].copy(), rv[pos % cap].copy()))
+            x_next = dl[L + 1]["x_in"] if L + 1 < L_n else dh["x_final"]
+            e = check_layer(t, spec, dl[L], L, pos, x_next, rk, rv, kv_f16, qk_norm, threads, dh["rope_cs"])
+            for k_, v_ in e.items():
+                worst[k_] = max(worst.get(k_, 0.0), v_)
+        last = i == n - 1
+        if last:
+            eh = check_head(t, spec, dh, got, gtok, threads)
+            worst["head_gemv"] = eh["gemv"]
+            ref, st, f16_flips = oracle_step_adopting(t, spec, kv, pos, x0, dl, dh, qk_norm, threads,
+                                                      dev_rows if kv_f16 else None)
+            err = rel(got, ref)
+        else:
+            xo, st, f16_flips = oracle_layers_adopting(t, spec, kv, pos, x0, dl, dh, qk_norm, threads,
+                                                       dev_rows if kv_f16 else None)
+            err = rel(dh["x_final"], xo)
+        print(f"  prefill token {i} (pos {pos}): teacher-forced max errors " +
+              " ".join(f"{k_} {v_:.1e}" for k_, v_ in sorted(worst.items())) +
+              f" | end to end: {st.flips} int8 + {f16_flips} f16 tie flips, "
+              f"{'logits' if last else 'hidden state'} rel err {err:.2e}", flush=True)
+        assert err <= 1e-3, (i, err)
+        out.append((st.flips + f16_flips, err))
+    ref_top = np.sort(ref.astype(np.float64))[-2:]
+    if ref_top[1] - ref_top[0] > 1e-2 * np.sqrt(np.mean(ref.astype(np.float64) ** 2)):
+        assert gtok == O.argmax(ref), (gtok, O.argmax(ref))
+    return gtok, out

@@ -464,3 +464,22 @@ def test_deterministic_projection_fallback_equals_selection_matrices():
     la, lb, lc = run(a), run(b), run(c)
     assert np.array_equal(la, lb)
     assert not np.allclose(la, lc, rtol=1e-3, atol=1e-3)
+
+
+def test_f16_ring_mode_rounds_the_new_row_before_attending():
+    """kv_f16: the step writes its new K/V rows as f16 values (the device's f16 ring), and the
+    step's attention sees them rounded: its logits differ from the f32 ring's, while a ring that
+    already holds f16-exact rows gives the same logits either way at the next position."""
+    import model_spec as MS
+    spec = dict(hidden=256, ffn=512, n_layers=2, vocab=40, nq=4, nkv=2, hd=64, eps=1e-6, theta=1e6)
+    om = O.DecodeModel(spec, MS.oracle_tensors(MS.build(spec, seed=4)), 8)
+    kv32, kv16 = om.new_kv(), om.new_kv()
+    l32 = om.step(kv32, 3, 0, threads=2)
+    om.model.kv_f16 = 1
+    l16 = om.step(kv16, 3, 0, threads=2)
+    row = kv16[:, :, 0]
+    assert np.array_equal(row, row.astype(np.float16).astype(np.float32))
+    assert not np.array_equal(kv32[:, :, 0], kv32[:, :, 0].astype(np.float16).astype(np.float32))
+    # layer 0's rows come from the same input; later layers see the rounded attention
+    assert np.array_equal(kv16[0, :, 0], kv32[0, :, 0].astype(np.float16).astype(np.float32))
+    assert not np.array_equal(l16, l32)

@@ -370,7 +370,8 @@ int jero_hip_gguf_tensor(const jero_gguf *g, const char *name, int *quant, int *
 int jero_hip_gguf_upload(const jero_gguf *g, const char *name, const void **dev_out);
 
 /* Measurement probe, no counterpart in the reference: one launch that reads `bytes` (a non-zero
- * multiple of 16) at the 16-byte aligned src_dev and nothing else, two 16-byte loads per thread.
+ * multiple of 16) at the 16-byte aligned src_dev and nothing else, two non-temporal 16-byte loads
+ * per thread.
  * Timed over the same buffers as a GEMV, it is the bandwidth ceiling that launch could reach.
  * sink_dev: 1 KiB of device memory it may write. */
 int jero_hip_read_probe(const void *src_dev, size_t bytes, uint32_t *sink_dev, void *stream);

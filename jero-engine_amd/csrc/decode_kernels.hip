@@ -168,6 +168,8 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
   const int U = a.U;
   const int64_t N = a.N;
   const int64_t n_groups = a.n_groups;
+  // the LM head streams its weights once; the layer GEMVs measured faster with the default policy
+  constexpr bool NT = OUT == kOutArgmax && nt_capable(F);
 
   // row of (row group rg, row slot r, lane group g); SWIGLU pairs gate row f with up row half+f
   auto row_of = [&](int64_t rg, int r) -> int64_t {
@@ -206,13 +208,7 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
       const int64_t row = ok ? row_of(rg, r) : 0;
       if constexpr (OUT == kOutResid) yr[r] = a.y[row];
 #pragma unroll
-      for (int t = 0; t < UPL; t++) {
-        const int u = min(c + LPR * t, U - 1);
-        if constexpr (is_planar(F))
-          Ut::load_w_planar(wt[r][t], a.w, N, U, row, u);
-        else
-          Ut::load_w(wt[r][t], a.w + row * a.rb, u);
-      }
+      for (int t = 0; t < UPL; t++) load_unit<F, NT>(wt[r][t], a.w, a.rb, N, U, row, min(c + LPR * t, U - 1));
     }
   };
 

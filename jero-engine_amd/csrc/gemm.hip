@@ -457,7 +457,7 @@ int launch_gemm(int quant, const void* w_dev, int64_t n_in, int64_t n_out, const
   // other formats and shapes: one GEMV per activation row (each row is matvec_any of x_m)
   for (int64_t r = 0; r < m; r++) {
     const int rc = launch_matvec(quant, w_dev, n_in, n_out, static_cast<const uint8_t*>(xq_dev) + r * xrb,
-                                 y_dev + r * n_out, nullptr, s);
+                                 y_dev + r * n_out, nullptr, s, false);  // every row re-reads the matrix
     if (rc) return rc;
   }
   return JERO_OK;

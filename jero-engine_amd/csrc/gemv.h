@@ -18,9 +18,11 @@ int max_gemv_k(int quant);
 // Validates a matvec call (shape, bytes, alignment); records the error and returns its code.
 int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, int64_t n_out, const void* xq,
                       const float* y);
-// Enqueues y = W xq (and the int32 partial sums when part != nullptr).
+// Enqueues y = W xq (and the int32 partial sums when part != nullptr).  once: the launch is the
+// only reader of these weights for a while (a single GEMV, not one of a batch of rows over the
+// same matrix), so its weight loads may bypass the caches (non-temporal).
 int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, float* y, int32_t* part,
-                  hipStream_t s);
+                  hipStream_t s, bool once = true);
 // Y[m][n_out] for m activation rows (jero_hip_gemm after its checks): the int8-MFMA kernel for
 // Q4_K and Q4_K_R with n_out a multiple of 128, one GEMV per row otherwise.
 int launch_gemm(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, int64_t m, float* y,

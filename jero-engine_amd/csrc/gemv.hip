@@ -28,7 +28,8 @@ namespace jero {
 
 constexpr int kGemvThreads = 256;
 
-template <int F, int LPR, int UPL, int R, bool PART, bool LDS_ACT>
+// NT: the launch reads every weight byte once (non-temporal weight loads).
+template <int F, int LPR, int UPL, int R, bool PART, bool LDS_ACT, bool NT>
 __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const uint8_t* __restrict__ w, int64_t rb, int U,
                                                              int64_t N, const uint8_t* __restrict__ xq,
                                                              int act_bytes, float* __restrict__ y,
@@ -60,13 +61,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const uint8_t* __res
   for (int r = 0; r < R; r++) {
     const int64_t row = min(row0 + r * G + g, N - 1);
 #pragma unroll
-    for (int t = 0; t < UPL; t++) {
-      const int u = min(c + LPR * t, U - 1);
-      if constexpr (is_planar(F))
-        Ut::load_w_planar(wt[r][t], w, N, U, row, u);
-      else
-        Ut::load_w(wt[r][t], w + row * rb, u);
-    }
+    for (int t = 0; t < UPL; t++) load_unit<F, NT>(wt[r][t], w, rb, N, U, row, min(c + LPR * t, U - 1));
   }
 
   // 3. activation slice: from LDS (staged once per workgroup) or straight from global
@@ -192,6 +187,7 @@ struct Launch {
   int32_t* part;
   int64_t ppr;
   hipStream_t s;
+  bool nt;  // every weight byte read once: non-temporal loads where the format has them
 };
 
 template <int F, int LPR, int UPL, int R, bool PART, bool LDS>
@@ -200,8 +196,15 @@ void launch_one(const Launch& L) {
   int64_t waves = (L.N + G * R - 1) / (G * R);
   int64_t blocks = (waves + kGemvThreads / kWave - 1) / (kGemvThreads / kWave);
   size_t shm = LDS ? size_t((L.act_bytes + 15) & ~15) : 0;
-  hipLaunchKernelGGL((gemv_kernel<F, LPR, UPL, R, PART, LDS>), dim3(unsigned(blocks)), dim3(kGemvThreads), shm, L.s,
-                     L.w, L.rb, L.U, L.N, L.xq, L.act_bytes, L.y, L.part, L.ppr);
+  if constexpr (nt_capable(F)) {
+    if (L.nt) {
+      hipLaunchKernelGGL((gemv_kernel<F, LPR, UPL, R, PART, LDS, true>), dim3(unsigned(blocks)), dim3(kGemvThreads),
+                         shm, L.s, L.w, L.rb, L.U, L.N, L.xq, L.act_bytes, L.y, L.part, L.ppr);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((gemv_kernel<F, LPR, UPL, R, PART, LDS, false>), dim3(unsigned(blocks)), dim3(kGemvThreads), shm,
+                     L.s, L.w, L.rb, L.U, L.N, L.xq, L.act_bytes, L.y, L.part, L.ppr);
 }
 
 template <int F, int LPR, int UPL, bool PART, bool LDS>
@@ -227,9 +230,10 @@ void launch_upl(int R, bool lds, const Launch& L) {
 }
 
 template <int F, bool PART>
-int launch_fmt(const uint8_t* w, int64_t k, int64_t N, const uint8_t* xq, float* y, int32_t* part, hipStream_t s) {
+int launch_fmt(const uint8_t* w, int64_t k, int64_t N, const uint8_t* xq, float* y, int32_t* part, hipStream_t s,
+               bool once) {
   Launch L{w, row_bytes(F, k), units_per_row(F, k), N, xq, int(row_bytes(act_format(F), k)), y, part,
-           partials_per_row(F, k), s};
+           partials_per_row(F, k), s, once};
   const int U = L.U;
   int lpr = U > 32 ? 64 : U > 16 ? 32 : U > 4 ? 16 : 4;
   int upl = (U + lpr - 1) / lpr;
@@ -391,7 +395,7 @@ int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, in
 }
 
 int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, float* y, int32_t* part,
-                  hipStream_t s) {
+                  hipStream_t s, bool once) {
   if (is_float_weight(quant)) {
     if (part) return fail(JERO_ERR_CAPABILITY_MISMATCH, "matvec_partials: float weights have no integer partial sums");
     return launch_matvec_float(quant, w, n_in, n_out, static_cast<const float*>(xq), y, s);
@@ -400,21 +404,21 @@ int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const v
   const uint8_t* xb = static_cast<const uint8_t*>(xq);
   if (part) {
     switch (quant) {
-      case JERO_Q4_K: return launch_fmt<JERO_Q4_K, true>(wb, n_in, n_out, xb, y, part, s);
-      case JERO_Q4_K_R: return launch_fmt<JERO_Q4_K_R, true>(wb, n_in, n_out, xb, y, part, s);
-      case JERO_Q6_K: return launch_fmt<JERO_Q6_K, true>(wb, n_in, n_out, xb, y, part, s);
-      case JERO_Q6_K_R: return launch_fmt<JERO_Q6_K_R, true>(wb, n_in, n_out, xb, y, part, s);
-      case JERO_Q8_0: return launch_fmt<JERO_Q8_0, true>(wb, n_in, n_out, xb, y, part, s);
-      case JERO_Q4_0: return launch_fmt<JERO_Q4_0, true>(wb, n_in, n_out, xb, y, part, s);
+      case JERO_Q4_K: return launch_fmt<JERO_Q4_K, true>(wb, n_in, n_out, xb, y, part, s, once);
+      case JERO_Q4_K_R: return launch_fmt<JERO_Q4_K_R, true>(wb, n_in, n_out, xb, y, part, s, once);
+      case JERO_Q6_K: return launch_fmt<JERO_Q6_K, true>(wb, n_in, n_out, xb, y, part, s, once);
+      case JERO_Q6_K_R: return launch_fmt<JERO_Q6_K_R, true>(wb, n_in, n_out, xb, y, part, s, once);
+      case JERO_Q8_0: return launch_fmt<JERO_Q8_0, true>(wb, n_in, n_out, xb, y, part, s, once);
+      case JERO_Q4_0: return launch_fmt<JERO_Q4_0, true>(wb, n_in, n_out, xb, y, part, s, once);
     }
   } else {
     switch (quant) {
-      case JERO_Q4_K: return launch_fmt<JERO_Q4_K, false>(wb, n_in, n_out, xb, y, nullptr, s);
-      case JERO_Q4_K_R: return launch_fmt<JERO_Q4_K_R, false>(wb, n_in, n_out, xb, y, nullptr, s);
-      case JERO_Q6_K: return launch_fmt<JERO_Q6_K, false>(wb, n_in, n_out, xb, y, nullptr, s);
-      case JERO_Q6_K_R: return launch_fmt<JERO_Q6_K_R, false>(wb, n_in, n_out, xb, y, nullptr, s);
-      case JERO_Q8_0: return launch_fmt<JERO_Q8_0, false>(wb, n_in, n_out, xb, y, nullptr, s);
-      case JERO_Q4_0: return launch_fmt<JERO_Q4_0, false>(wb, n_in, n_out, xb, y, nullptr, s);
+      case JERO_Q4_K: return launch_fmt<JERO_Q4_K, false>(wb, n_in, n_out, xb, y, nullptr, s, once);
+      case JERO_Q4_K_R: return launch_fmt<JERO_Q4_K_R, false>(wb, n_in, n_out, xb, y, nullptr, s, once);
+      case JERO_Q6_K: return launch_fmt<JERO_Q6_K, false>(wb, n_in, n_out, xb, y, nullptr, s, once);
+      case JERO_Q6_K_R: return launch_fmt<JERO_Q6_K_R, false>(wb, n_in, n_out, xb, y, nullptr, s, once);
+      case JERO_Q8_0: return launch_fmt<JERO_Q8_0, false>(wb, n_in, n_out, xb, y, nullptr, s, once);
+      case JERO_Q4_0: return launch_fmt<JERO_Q4_0, false>(wb, n_in, n_out, xb, y, nullptr, s, once);
     }
   }
   return fail(JERO_ERR_CAPABILITY_MISMATCH, "unsupported weight quantization " + std::to_string(quant));

@@ -57,12 +57,13 @@ struct Unit<JERO_Q4_K> {
     A.hi = uint32_t(i >= 2);
   }
 
+  template <bool NT = false>  // NT: non-temporal loads (the weights of a single-pass GEMV)
   static __device__ __forceinline__ void load_w(W& w, const uint8_t* __restrict__ row, int u) {
     int b = u >> 2, i = u & 3;
     const uint8_t* blk = row + int64_t(b) * 144;
-    w.h = ld4(blk);
-    w.q0 = ld4(blk + 16 + 32 * i);
-    w.q1 = ld4(blk + 32 + 32 * i);
+    w.h = ldx4<NT>(blk);
+    w.q0 = ldx4<NT>(blk + 16 + 32 * i);
+    w.q1 = ldx4<NT>(blk + 32 + 32 * i);
   }
 
   // 6-bit scale and min of sub-block with scale byte index jj (see get_scale_min_k4).
@@ -139,12 +140,13 @@ struct Unit<JERO_Q4_K> {
 // Same size as the GGUF tensor; the dot product is Unit<Q4_K>'s.
 template <>
 struct Unit<JERO_Q4_K_R> : Unit<JERO_Q4_K> {
+  template <bool NT = false>
   static __device__ __forceinline__ void load_w_planar(W& w, const uint8_t* __restrict__ base, int64_t /*N*/, int U,
                                                        int64_t row, int u) {
     const uint8_t* rp = base + row * (int64_t(U) * 36);
-    w.q0 = ld4(rp + u * 16);
-    w.q1 = ld4(rp + U * 16 + u * 16);
-    w.h = ld4(rp + U * 32 + (u >> 2) * 16);
+    w.q0 = ldx4<NT>(rp + u * 16);
+    w.q1 = ldx4<NT>(rp + U * 16 + u * 16);
+    w.h = ldx4<NT>(rp + U * 32 + (u >> 2) * 16);
   }
 };
 
@@ -306,14 +308,15 @@ struct Unit<JERO_Q6_K> {
 // Same size as the GGUF tensor (210 bytes per block); the dot product is Unit<Q6_K>'s.
 template <>
 struct Unit<JERO_Q6_K_R> : Unit<JERO_Q6_K> {
+  template <bool NT = false>
   static __device__ __forceinline__ void load_w_planar(W& w, const uint8_t* __restrict__ base, int64_t N, int U,
                                                        int64_t row, int u) {
     const int64_t plane = N * int64_t(U) * 16;
     const int64_t gu = row * U + u;
-    w.lo = ld4(base + gu * 16);
-    w.hi = ld4(base + plane + gu * 16);
-    w.qh = ld4(base + 2 * plane + gu * 16);
-    w.sc = ld1(base + 3 * plane + gu * 4);
+    w.lo = ldx4<NT>(base + gu * 16);
+    w.hi = ldx4<NT>(base + plane + gu * 16);
+    w.qh = ldx4<NT>(base + 2 * plane + gu * 16);
+    w.sc = ldx1<NT>(base + 3 * plane + gu * 4);
     load_d(w, base + 3 * plane + N * int64_t(U) * 4 + (row * (U / 4) + (u >> 2)) * 2);
   }
 };
@@ -446,6 +449,24 @@ struct Unit<JERO_Q4_0> {
 __host__ __device__ constexpr bool is_planar(int f) {
   return f == JERO_Q4_K_R || f == JERO_Q6_K_R || f == JERO_Q4_K_T || f == JERO_Q6_K_T;
 }
+// Formats whose weight loads have a non-temporal variant (16-byte pieces that no other load of
+// the launch touches).
+__host__ __device__ constexpr bool nt_capable(int f) { return f == JERO_Q4_K || f == JERO_Q4_K_R || f == JERO_Q6_K_R; }
+
+// Loads the weights of unit u of a row through Unit<F>'s loader (non-temporal when NT).
+template <int F, bool NT>
+__device__ __forceinline__ void load_unit(typename Unit<F>::W& w, const uint8_t* __restrict__ base, int64_t rb,
+                                          int64_t N, int U, int64_t row, int u) {
+  static_assert(!NT || nt_capable(F), "no non-temporal loader for this format");
+  if constexpr (is_planar(F)) {
+    if constexpr (NT) Unit<F>::template load_w_planar<true>(w, base, N, U, row, u);
+    else Unit<F>::load_w_planar(w, base, N, U, row, u);
+  } else {
+    if constexpr (NT) Unit<F>::template load_w<true>(w, base + row * rb, u);
+    else Unit<F>::load_w(w, base + row * rb, u);
+  }
+}
+
 __host__ __device__ constexpr bool is_q6k(int f) { return f == JERO_Q6_K || f == JERO_Q6_K_R || f == JERO_Q6_K_T; }
 __host__ __device__ constexpr bool is_kquant(int f) {
   return f == JERO_Q4_K || f == JERO_Q4_K_R || f == JERO_Q4_K_T || is_q6k(f);

@@ -2,11 +2,13 @@
 //
 // Not part of the hot path.  A GEMV launch of B weight bytes cannot finish faster than a kernel
 // that reads the same B bytes with the same launch cost and nothing else to do; this kernel is
-// that reader, so a benchmark can report each GEMV against it.  Two 16-byte loads per thread
-// (a workgroup reads 8 KiB: threads t and t + 256 of its chunk; one, four, eight or sixteen loads
-// per thread measured 2-10 % slower at 9-28 MB), 256-thread workgroups covering the buffer; the
-// loaded words are folded by XOR over the wave and written only when they equal a value no weight
-// buffer holds in practice, so the loads stay but no bytes are written.
+// that reader, so a benchmark can report each GEMV against it.  Two non-temporal 16-byte loads
+// per thread (a workgroup reads 8 KiB: threads t and t + 256 of its chunk), 256-thread workgroups
+// covering the buffer: the fastest of the variants measured at 9-28 MB (non-temporal loads 8-11 %
+// faster than the default policy; one, four, eight or sixteen loads per thread, or 512- and
+// 1024-thread workgroups, 2-15 % slower).  The loaded words are folded by XOR over the wave and
+// written only when they equal a value no weight buffer holds in practice, so the loads stay but
+// no bytes are written.
 #include "jero_common.h"
 #include "runtime.h"
 
@@ -17,8 +19,8 @@ namespace {
 __global__ void __launch_bounds__(256) read_probe_kernel(const u32x4* __restrict__ src, int64_t n16,
                                                          uint32_t* __restrict__ sink) {
   const int64_t i = int64_t(blockIdx.x) * 512 + threadIdx.x;
-  const u32x4 v = src[i < n16 ? i : n16 - 1];
-  const u32x4 u = src[i + 256 < n16 ? i + 256 : n16 - 1];
+  const u32x4 v = __builtin_nontemporal_load(src + (i < n16 ? i : n16 - 1));
+  const u32x4 u = __builtin_nontemporal_load(src + (i + 256 < n16 ? i + 256 : n16 - 1));
   uint32_t h = v.x ^ v.y ^ v.z ^ v.w ^ u.x ^ u.y ^ u.z ^ u.w;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) h ^= __shfl_xor(h, off, kWave);

@@ -177,6 +177,42 @@ int jero_hip_pack_tiles(const int8_t *src_dev, int64_t rows, int64_t k, int8_t *
 int jero_hip_gemm_i8_tiles(const int8_t *a_packed_dev, int64_t m_tiles, const int8_t *w_packed_dev, int64_t tile_begin,
                            int64_t tile_end, int64_t k_chunks, int32_t *c_dev, void *stream);
 
+/* The synthetic all-int8 transformer the reference benchmarks its int8 GEMM with: ForwardModel
+ * (src/forward.rs:834-1075), 4 layers of width 512, FFN 1024, one 512-wide attention head, every
+ * value an exact integer, so results are bit-identical to the reference.  The device holds the
+ * weights (generated from seed, as ForwardModel::new does, src/forward.rs:879-903), a K/V cache of
+ * max_positions positions per layer and the activation rows of max_positions tokens. */
+typedef struct jero_forward_model jero_forward_model;
+/* ForwardModel::new(seed, vocab) (src/forward.rs:879-903) on the current device; vocab in
+ * 0..2^24, max_positions in 1..2^22 (TensorBounds otherwise).  Synchronous. */
+int jero_hip_forward_model_create(uint64_t seed, int64_t vocab, int64_t max_positions, jero_forward_model **out);
+int jero_hip_forward_model_destroy(jero_forward_model *model);
+/* Logit rows of the LM head: max(vocab, 1) rounded up to whole 8-row tiles (Matrix::random,
+ * src/forward.rs:364-377); -1 for a null model. */
+int64_t jero_hip_forward_model_head_rows(const jero_forward_model *model);
+/* Positions held in the K/V cache (the KvState's length); -1 for a null model. */
+int64_t jero_hip_forward_model_positions(const jero_forward_model *model);
+/* Empties the K/V cache (a fresh KvState, src/forward.rs:1010-1013). */
+int jero_hip_forward_model_reset(jero_forward_model *model);
+/* Device address and shape of a matrix: layer 0..3 with which 0..5 = wq wk wv wo up down, or
+ * layer -1 for the LM head (which ignored); row-major int8 [n][k] and its requant shift. */
+int jero_hip_forward_model_weight(const jero_forward_model *model, int layer, int which, const int8_t **w_dev,
+                                  int64_t *n, int64_t *k, int *shift);
+/* ForwardModel::forward (src/forward.rs:930-976): the m >= 1 host tokens at positions
+ * start_pos.., which must be the cached position count (InvalidArgument otherwise), appended to
+ * the cache (ContextLengthExceeded past max_positions); logits_dev (device, int32
+ * [jero_hip_forward_model_head_rows]) receives the last token's logits.  Enqueued on stream. */
+int jero_hip_forward_model_forward(jero_forward_model *model, const uint32_t *tokens, int64_t m, int64_t start_pos,
+                                   int32_t *logits_dev, void *stream);
+/* ForwardModel::evaluate's token loop (src/forward.rs:995-1043): empties the cache, runs the
+ * prompt's forward, then greedy steps (ForwardModel::sample, :978-986) until max_tokens tokens;
+ * each step's token stays on the device for the next step.  generated (host) receives max_tokens
+ * ids; timing_ms (host, 2 floats, or NULL) the device time of the prefill (through the first
+ * sample) and of the decode steps.  An empty prompt is CapabilityMismatch, as in the reference;
+ * n + max_tokens - 1 positions past max_positions ContextLengthExceeded.  Synchronous. */
+int jero_hip_forward_model_evaluate(jero_forward_model *model, const uint32_t *prompt, int64_t n, int64_t max_tokens,
+                                    uint32_t *generated, float *timing_ms, void *stream);
+
 /* Load-time re-layout of a weight tensor for the GEMV kernels; replaces repack_tensor_parallel
  * (src/weights.rs:914-955) -> RepackedWeight.  Q4_K -> JERO_Q4_K_R and Q6_K -> JERO_Q6_K_R:
  * the n_out x n_in tensor's bytes are regrouped into 16-byte aligned planes of the same total

@@ -1,0 +1,551 @@
+// forward.hip -- ForwardModel (src/forward.rs:834-1075), the synthetic all-int8 transformer, on gfx950.
+//
+// Exact integer arithmetic throughout, so the device pass is bit-identical to the reference:
+// int32 dot products (v_dot4_i32_i8), requant (:345-350), the integer RMSNorm (:672-699, isqrt
+// :747-758), the integer-weighted attention (:702-744), the i8 saturating residual adds (:817-821)
+// and the greedy sample (:978-986).
+//
+// HBM layout: every matrix row-major int8 [n][k] (Matrix::rows, n padded to whole 8-row tiles with
+// zero rows), generated on the device from the seed (splitmix / fill_small are integer hashes, so
+// no weight bytes cross PCIe); per layer the K and V caches int8 [max_positions][512]; the residual
+// rows x, the attention input / output rows and the FFN rows int8 [rows][width].
+//
+// One forward call over m tokens at start_pos, per layer:
+//   qkv   : RMSNorm of x in the prologue (each workgroup normalises the rows it needs in LDS), the
+//           three projections in one launch (blockIdx.y picks wq / wk / wv), k and v rows written
+//           straight into the caches at start_pos
+//   attn  : one workgroup per query row over cache rows 0..=start_pos + r
+//   wo    : requant, then saturating add into x
+//   up    : RMSNorm prologue, requant, relu
+//   down  : requant, saturating add into x
+// then the head (RMSNorm of the last row, int32 logits) and, in evaluate, the sample kernel,
+// which leaves the next token in device memory for the next step's embedding: the decode loop
+// never waits for the host.  Up to kMvRows rows the projections run on the matvec kernel below
+// (one weight row per wave, the token rows in LDS); longer prompts run the int8 MFMA GEMM of
+// gemm.hip with the same fused epilogues, after a row RMSNorm kernel.
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "forward.h"
+#include "jero_common.h"
+#include "runtime.h"
+
+namespace jero {
+
+constexpr int kFwdDim = 512, kFwdFfn = 1024, kFwdLayers = 4, kFwdMats = 6;
+constexpr int kMvRows = 64;     // token rows of one matvec launch (LDS: m x K bytes, 64 KiB at most)
+constexpr int kMvWaves = 4;     // weight rows per matvec workgroup, one per wave
+constexpr int kAttChunk = 4096;  // cache positions whose weights one attention pass keeps in LDS
+constexpr int64_t kFwdMaxPositions = int64_t(1) << 22;
+
+// splitmix (src/forward.rs:326-332): one SplitMix64 output for state x.
+__host__ __device__ __forceinline__ uint64_t splitmix(uint64_t x) {
+  uint64_t z = x + 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// Element i of fill_small(seed, .) (src/forward.rs:335-343), in [-8, 7].
+__device__ __forceinline__ int small_of(uint64_t seed, uint64_t i) {
+  return int(splitmix(seed ^ (i * 0xA24BAED4963EE407ull)) & 0xFu) - 8;
+}
+
+// isqrt (src/forward.rs:747-758): Newton's iteration from x = v, y = ceil(v / 2), stopping when y
+// no longer decreases; floor((x + v / x) / 2) as the overflow-free midpoint.
+__device__ __forceinline__ uint32_t isqrt_u32(uint32_t v) {
+  if (v < 2) return v;
+  uint32_t x = v, y = v / 2 + (v & 1);
+  while (y < x) {
+    x = y;
+    const uint32_t b = v / x;
+    y = (x & b) + ((x ^ b) >> 1);
+  }
+  return x;
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_add_i(int v) {
+  return v + __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, false);
+}
+
+// Integer sum over the wave with DPP; the total lands in lane 63.
+__device__ __forceinline__ int wave_sum_last_i(int v) {
+  v = dpp_add_i<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add_i<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add_i<0x124, 0xF>(v);  // row_ror:4
+  v = dpp_add_i<0x128, 0xF>(v);  // row_ror:8
+  v = dpp_add_i<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+  v = dpp_add_i<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
+__device__ __forceinline__ int8_t clamp_i8(int v, int lo) { return int8_t(v < lo ? lo : v > 127 ? 127 : v); }
+
+// ForwardExec::rmsnorm (src/forward.rs:672-699) of one 512-byte row held by a wave, 8 bytes per
+// lane: rms = max(isqrt(sum v^2 / 512), 1), y = clamp(v * 48 / rms, -127, 127) (division
+// truncating toward zero).
+__device__ __forceinline__ void rmsnorm_lane(uint32_t (&v)[2]) {
+  int ss = dot4(v[0], v[0], dot4(v[1], v[1], 0));
+  ss = __builtin_amdgcn_readlane(wave_sum_last_i(ss), 63);
+  const int rms = max(int(isqrt_u32(uint32_t(ss) / kFwdDim)), 1);
+#pragma unroll
+  for (int d = 0; d < 2; d++) {
+    uint32_t o = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+      const int x = int(int8_t(byte_of(v[d], b)));
+      o |= uint32_t(uint8_t(clamp_i8(x * 48 / rms, -127))) << (8 * b);
+    }
+    v[d] = o;
+  }
+}
+
+// Up to three projections of one launch (same shape and shift); blockIdx.y picks one.
+struct MvProj {
+  const int8_t* w;
+  void* out;
+};
+struct MvArgs {
+  MvProj p[3];
+  const int8_t* x;  // token rows [m][K]
+  int m, N, shift;
+};
+
+// out[r][n] = EPI(sum_k x[r][k] w[n][k]) for r < m <= kMvRows: the m token rows (RMSNorm-ed if
+// NORM, K = 512) staged in LDS by the four waves, then one weight row per wave, K / 64 bytes per
+// lane, one DPP reduction per token row; lane 63 writes.
+template <int K, int EPI, bool NORM>
+__global__ void __launch_bounds__(kMvWaves * 64) fwd_matvec_kernel(MvArgs a) {
+  static_assert(K == kFwdDim || K == kFwdFfn, "row width");
+  static_assert(!NORM || K == kFwdDim, "RMSNorm rows are model rows");
+  constexpr int D = K / 256;  // dwords per lane
+  extern __shared__ uint32_t xs[];  // [m][K / 4]
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int r = wv; r < a.m; r += kMvWaves) {
+    uint32_t v[D];
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.x) + int64_t(r) * K + lane * 4 * D;
+    if constexpr (D == 2) {
+      const u32x2 t = ld2(src);
+      v[0] = t[0], v[1] = t[1];
+    } else {
+      const u32x4 t = ld4(src);
+      v[0] = t[0], v[1] = t[1], v[2] = t[2], v[3] = t[3];
+    }
+    if constexpr (NORM) rmsnorm_lane(v);
+#pragma unroll
+    for (int d = 0; d < D; d++) xs[r * (K / 4) + lane * D + d] = v[d];
+  }
+  __syncthreads();
+  const int n = blockIdx.x * kMvWaves + wv;
+  if (n >= a.N) return;
+  const MvProj p = a.p[blockIdx.y];
+  uint32_t w[D];
+  const uint8_t* wr = reinterpret_cast<const uint8_t*>(p.w) + int64_t(n) * K + lane * 4 * D;
+  if constexpr (D == 2) {
+    const u32x2 t = ld2(wr);
+    w[0] = t[0], w[1] = t[1];
+  } else {
+    const u32x4 t = ld4(wr);
+    w[0] = t[0], w[1] = t[1], w[2] = t[2], w[3] = t[3];
+  }
+  for (int r = 0; r < a.m; r++) {
+    int acc = 0;
+#pragma unroll
+    for (int d = 0; d < D; d++) acc = dot4(w[d], xs[r * (K / 4) + lane * D + d], acc);
+    acc = wave_sum_last_i(acc);
+    if (lane == 63) {
+      const int64_t o = int64_t(r) * a.N + n;
+      if constexpr (EPI == kI8OutI32) {
+        static_cast<int32_t*>(p.out)[o] = acc;
+      } else {
+        const int q = int(int32_t(uint32_t(acc) + (uint32_t(1) << (a.shift - 1))) >> a.shift);
+        const int8_t rq = clamp_i8(q, -127);
+        int8_t* dst = static_cast<int8_t*>(p.out) + o;
+        if constexpr (EPI == kI8OutRequant) *dst = rq;
+        else if constexpr (EPI == kI8OutRequantRelu) *dst = rq < 0 ? int8_t(0) : rq;
+        else *dst = clamp_i8(int(*dst) + int(rq), -128);
+      }
+    }
+  }
+}
+
+// RMSNorm of m rows (the MFMA path's projection input): one wave per row.
+__global__ void __launch_bounds__(64) fwd_rmsnorm_rows_kernel(const int8_t* __restrict__ x, int8_t* __restrict__ out) {
+  const int64_t r = blockIdx.x;
+  const int lane = threadIdx.x;
+  const u32x2 t = ld2(reinterpret_cast<const uint8_t*>(x) + r * kFwdDim + lane * 8);
+  uint32_t v[2] = {t[0], t[1]};
+  rmsnorm_lane(v);
+  *reinterpret_cast<u32x2*>(out + r * kFwdDim + lane * 8) = u32x2{v[0], v[1]};
+}
+
+// ForwardExec::attention (src/forward.rs:702-744) for query row r = blockIdx.x at position
+// start_pos + r over cache rows 0..=start_pos + r: w_t = clamp(q . k_t >> 10, 0, 127) + 1,
+// out = sum w_t v_t / sum w_t (int64, truncating).  Per pass of up to kAttChunk positions the
+// scores come first (16 lanes per key, 32 bytes each, four keys per wave at a time) into LDS
+// bytes, then each thread sums two of the 512 columns over the pass in int32 (exact:
+// 128 * 127 * kAttChunk < 2^31) and carries the passes in int64.
+__global__ void __launch_bounds__(256) fwd_attention_kernel(const int8_t* __restrict__ q, const int8_t* __restrict__ kc,
+                                                            const int8_t* __restrict__ vc, int64_t start_pos,
+                                                            int8_t* __restrict__ out) {
+  __shared__ uint8_t wts[kAttChunk];
+  const int r = blockIdx.x;
+  const int64_t npos = start_pos + r + 1;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4, sub = lane & 15;
+  const uint8_t* qr = reinterpret_cast<const uint8_t*>(q) + int64_t(r) * kFwdDim + sub * 32;
+  const u32x4 q0 = ld4(qr), q1 = ld4(qr + 16);
+  const int c2 = threadIdx.x * 2;
+  int64_t acc0 = 0, acc1 = 0, total = 0;
+  for (int64_t c0 = 0; c0 < npos; c0 += kAttChunk) {
+    const int cn = int(std::min<int64_t>(kAttChunk, npos - c0));
+    for (int j = wv * 4 + g; j < cn; j += 16) {
+      const uint8_t* kr = reinterpret_cast<const uint8_t*>(kc) + (c0 + j) * kFwdDim + sub * 32;
+      const u32x4 k0 = ld4(kr), k1 = ld4(kr + 16);
+      int s = 0;
+#pragma unroll
+      for (int d = 0; d < 4; d++) s = dot4(q0[d], k0[d], dot4(q1[d], k1[d], s));
+      s = group_sum_i<16>(s);
+      if (sub == 0) {
+        const int sh = s >> 10;
+        wts[j] = uint8_t((sh < 0 ? 0 : sh > 127 ? 127 : sh) + 1);
+      }
+    }
+    __syncthreads();
+    int a0 = 0, a1 = 0, tw = 0;
+    const uint8_t* vr = reinterpret_cast<const uint8_t*>(vc) + c0 * kFwdDim + c2;
+#pragma unroll 8
+    for (int j = 0; j < cn; j++) {
+      const int w = wts[j];
+      const uint32_t vv = *reinterpret_cast<const uint16_t*>(vr + int64_t(j) * kFwdDim);
+      a0 += w * int(int8_t(vv & 0xFFu));
+      a1 += w * int(int8_t(vv >> 8));
+      tw += w;
+    }
+    acc0 += a0, acc1 += a1, total += tw;
+    __syncthreads();
+  }
+  out[int64_t(r) * kFwdDim + c2] = int8_t(acc0 / total);
+  out[int64_t(r) * kFwdDim + c2 + 1] = int8_t(acc1 / total);
+}
+
+// embed (src/forward.rs:918-926) of token rows tok[0, m): fill_small(seed ^ token * 0x9E3779B9) * 8.
+__global__ void __launch_bounds__(256) fwd_embed_kernel(uint64_t seed, const uint32_t* __restrict__ tok,
+                                                        int8_t* __restrict__ x) {
+  const int64_t r = blockIdx.x;
+  const uint64_t s = seed ^ (uint64_t(tok[r]) * 0x9E3779B9ull);
+  for (int i = threadIdx.x; i < kFwdDim; i += blockDim.x) x[r * kFwdDim + i] = int8_t(small_of(s, uint64_t(i)) * 8);
+}
+
+// Matrix::random (src/forward.rs:364-377): fill_small(seed, n k) then zero padding rows.
+__global__ void __launch_bounds__(256) fwd_fill_kernel(uint64_t seed, int64_t valid, int64_t total,
+                                                       int8_t* __restrict__ w) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x)
+    w[i] = i < valid ? int8_t(small_of(seed, uint64_t(i))) : int8_t(0);
+}
+
+// ForwardModel::sample (src/forward.rs:978-986): the first index of the largest of logits
+// [0, max(vocab, 1)), written to *tok.
+__global__ void __launch_bounds__(256) fwd_sample_kernel(const int32_t* __restrict__ logits, int64_t vocab,
+                                                         uint32_t* __restrict__ tok) {
+  __shared__ int sv[256];
+  __shared__ int64_t si[256];
+  const int t = threadIdx.x;
+  const int64_t n = vocab > 1 ? vocab : 1;
+  int bv = INT32_MIN;
+  int64_t bi = -1;
+  for (int64_t i = t; i < n; i += 256) {
+    const int v = logits[i];
+    if (bi < 0 || v > bv) bv = v, bi = i;
+  }
+  sv[t] = bv, si[t] = bi;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (t < off) {
+      const int ov = sv[t + off];
+      const int64_t oi = si[t + off];
+      if (oi >= 0 && (si[t] < 0 || ov > sv[t] || (ov == sv[t] && oi < si[t]))) sv[t] = ov, si[t] = oi;
+    }
+    __syncthreads();
+  }
+  if (t == 0) *tok = uint32_t(si[0]);
+}
+
+}  // namespace jero
+
+using namespace jero;
+
+struct jero_forward_model {
+  int device = -1;
+  uint64_t seed = 0;
+  int64_t vocab = 0, head_rows = 0, cap = 0, len = 0;
+  int8_t* w[kFwdLayers][kFwdMats] = {};
+  int8_t* head = nullptr;
+  int8_t* kc[kFwdLayers] = {};
+  int8_t* vc[kFwdLayers] = {};
+  int8_t *x = nullptr, *h = nullptr, *q = nullptr, *att = nullptr, *up = nullptr;  // [cap] rows
+  int32_t* logits = nullptr;                                                        // [head_rows]
+  uint32_t* tokens = nullptr;  // [cap]: the call's token rows, or evaluate's generated tokens
+  std::vector<void*> owned;
+};
+
+namespace {
+
+const int64_t kMatRows[kFwdMats] = {kFwdDim, kFwdDim, kFwdDim, kFwdDim, kFwdFfn, kFwdDim};
+const int64_t kMatCols[kFwdMats] = {kFwdDim, kFwdDim, kFwdDim, kFwdDim, kFwdDim, kFwdFfn};
+int mat_shift(int which) { return which == 5 ? 7 : 6; }
+
+int fwd_alloc(jero_forward_model* f, size_t bytes, void** p) {
+  if (hipMalloc(p, bytes < 256 ? 256 : bytes) != hipSuccess)
+    return fail(JERO_ERR_INSUFFICIENT_MEMORY, "forward_model: hipMalloc of " + std::to_string(bytes) + " bytes failed");
+  f->owned.push_back(*p);
+  return JERO_OK;
+}
+
+void fwd_release(jero_forward_model* f) {
+  for (void* p : f->owned) (void)hipFree(p);
+  delete f;
+}
+
+int gen_matrix(uint64_t seed, int64_t n, int64_t k, int8_t* dst) {
+  const int64_t total = (n + 7) / 8 * 8 * k;
+  hipLaunchKernelGGL(fwd_fill_kernel, dim3(unsigned(std::min<int64_t>((total + 255) / 256, 4096))), dim3(256), 0, 0,
+                     seed, n * k, total, dst);
+  return check_launch("forward_model weights");
+}
+
+// m token rows x (m <= kMvRows) through up to three same-shaped projections.
+template <int K, int EPI, bool NORM>
+int mv(const MvArgs& a, int n_proj, hipStream_t s) {
+  const dim3 grid(unsigned((a.N + kMvWaves - 1) / kMvWaves), unsigned(n_proj));
+  hipLaunchKernelGGL((fwd_matvec_kernel<K, EPI, NORM>), grid, dim3(kMvWaves * 64), size_t(a.m) * K, s, a);
+  return check_launch("forward matvec");
+}
+
+MvArgs mv_args(const int8_t* x, int64_t m, int64_t N, int shift) {
+  MvArgs a{};
+  a.x = x;
+  a.m = int(m);
+  a.N = int(N);
+  a.shift = shift;
+  return a;
+}
+
+// ForwardModel::forward (src/forward.rs:930-976) over the m token rows already in f->tokens.
+int forward_rows(jero_forward_model* f, int64_t m, int64_t start_pos, int32_t* logits, hipStream_t s) {
+  const int64_t D = kFwdDim;
+  int rc;
+  hipLaunchKernelGGL(fwd_embed_kernel, dim3(unsigned(m)), dim3(256), 0, s, f->seed, f->tokens, f->x);
+  if ((rc = check_launch("forward embed"))) return rc;
+  const bool small = m <= kMvRows;
+  for (int l = 0; l < kFwdLayers; l++) {
+    int8_t* const* W = f->w[l];
+    int8_t* kdst = f->kc[l] + start_pos * D;
+    int8_t* vdst = f->vc[l] + start_pos * D;
+    if (small) {
+      MvArgs a = mv_args(f->x, m, D, 6);
+      a.p[0] = {W[0], f->q};
+      a.p[1] = {W[1], kdst};
+      a.p[2] = {W[2], vdst};
+      if ((rc = mv<kFwdDim, kI8OutRequant, true>(a, 3, s))) return rc;
+    } else {
+      hipLaunchKernelGGL(fwd_rmsnorm_rows_kernel, dim3(unsigned(m)), dim3(64), 0, s, f->x, f->h);
+      if ((rc = check_launch("forward rmsnorm")) ||
+          (rc = launch_gemm_i8_epi(kI8OutRequant, f->h, m, D, W[0], D, f->q, 6, s)) ||
+          (rc = launch_gemm_i8_epi(kI8OutRequant, f->h, m, D, W[1], D, kdst, 6, s)) ||
+          (rc = launch_gemm_i8_epi(kI8OutRequant, f->h, m, D, W[2], D, vdst, 6, s)))
+        return rc;
+    }
+    hipLaunchKernelGGL(fwd_attention_kernel, dim3(unsigned(m)), dim3(256), 0, s, f->q, f->kc[l], f->vc[l], start_pos,
+                       f->att);
+    if ((rc = check_launch("forward attention"))) return rc;
+    if (small) {
+      MvArgs a = mv_args(f->att, m, D, 6);
+      a.p[0] = {W[3], f->x};
+      if ((rc = mv<kFwdDim, kI8OutRequantSatAdd, false>(a, 1, s))) return rc;
+      a = mv_args(f->x, m, kFwdFfn, 6);
+      a.p[0] = {W[4], f->up};
+      if ((rc = mv<kFwdDim, kI8OutRequantRelu, true>(a, 1, s))) return rc;
+      a = mv_args(f->up, m, D, 7);
+      a.p[0] = {W[5], f->x};
+      if ((rc = mv<kFwdFfn, kI8OutRequantSatAdd, false>(a, 1, s))) return rc;
+    } else {
+      if ((rc = launch_gemm_i8_epi(kI8OutRequantSatAdd, f->att, m, D, W[3], D, f->x, 6, s))) return rc;
+      hipLaunchKernelGGL(fwd_rmsnorm_rows_kernel, dim3(unsigned(m)), dim3(64), 0, s, f->x, f->h);
+      if ((rc = check_launch("forward rmsnorm")) ||
+          (rc = launch_gemm_i8_epi(kI8OutRequantRelu, f->h, m, D, W[4], kFwdFfn, f->up, 6, s)) ||
+          (rc = launch_gemm_i8_epi(kI8OutRequantSatAdd, f->up, m, kFwdFfn, W[5], D, f->x, 7, s)))
+        return rc;
+    }
+  }
+  MvArgs a = mv_args(f->x + (m - 1) * D, 1, f->head_rows, 0);
+  a.p[0] = {f->head, logits};
+  return mv<kFwdDim, kI8OutI32, true>(a, 1, s);
+}
+
+int check_model(const jero_forward_model* f, const char* who) {
+  if (!f) return fail(JERO_ERR_INVALID_ARGUMENT, std::string(who) + ": null model");
+  int dev = -1;
+  int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (rc) return rc;
+  if (dev != f->device)
+    return fail(JERO_ERR_INVALID_ARGUMENT, std::string(who) + ": the model lives on device " +
+                                               std::to_string(f->device) + ", not the current one");
+  return JERO_OK;
+}
+
+}  // namespace
+
+extern "C" int jero_hip_forward_model_create(uint64_t seed, int64_t vocab, int64_t max_positions,
+                                             jero_forward_model** out) {
+  if (!out) return fail(JERO_ERR_INVALID_ARGUMENT, "forward_model_create: null pointer");
+  *out = nullptr;
+  if (vocab < 0 || vocab > (int64_t(1) << 24))
+    return fail(JERO_ERR_TENSOR_BOUNDS, "forward_model_create: vocab must be in 0..2^24");
+  if (max_positions < 1 || max_positions > kFwdMaxPositions)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "forward_model_create: max_positions must be in 1..2^22");
+  auto* f = new jero_forward_model();
+  int rc = check_hip(hipGetDevice(&f->device), "hipGetDevice");
+  if (rc) {
+    delete f;
+    return rc;
+  }
+  f->seed = seed;
+  f->vocab = vocab;
+  f->cap = max_positions;
+  f->head_rows = (std::max<int64_t>(vocab, 1) + 7) / 8 * 8;
+  const size_t cap = size_t(max_positions);
+  void* p;
+  for (int l = 0; l < kFwdLayers && !rc; l++) {
+    for (int j = 0; j < kFwdMats && !rc; j++)
+      if (!(rc = fwd_alloc(f, size_t(kMatRows[j] * kMatCols[j]), &p))) f->w[l][j] = static_cast<int8_t*>(p);
+    if (!rc && !(rc = fwd_alloc(f, cap * kFwdDim, &p))) f->kc[l] = static_cast<int8_t*>(p);
+    if (!rc && !(rc = fwd_alloc(f, cap * kFwdDim, &p))) f->vc[l] = static_cast<int8_t*>(p);
+  }
+  int8_t** rows[5] = {&f->x, &f->h, &f->q, &f->att, &f->up};
+  for (int i = 0; i < 5 && !rc; i++)
+    if (!(rc = fwd_alloc(f, cap * (i == 4 ? kFwdFfn : kFwdDim), &p))) *rows[i] = static_cast<int8_t*>(p);
+  if (!rc && !(rc = fwd_alloc(f, size_t(f->head_rows) * kFwdDim, &p))) f->head = static_cast<int8_t*>(p);
+  if (!rc && !(rc = fwd_alloc(f, size_t(f->head_rows) * sizeof(int32_t), &p))) f->logits = static_cast<int32_t*>(p);
+  if (!rc && !(rc = fwd_alloc(f, cap * sizeof(uint32_t), &p))) f->tokens = static_cast<uint32_t*>(p);
+  // ForwardModel::new (src/forward.rs:879-903): layer l's matrices from splitmix(seed ^ (16 l + j)),
+  // j = 1..6 for wq wk wv wo up down; the head from splitmix(seed ^ 0xFFFF), max(vocab, 1) rows.
+  for (int l = 0; l < kFwdLayers && !rc; l++)
+    for (int j = 0; j < kFwdMats && !rc; j++)
+      rc = gen_matrix(splitmix(seed ^ (uint64_t(l) * 16 + uint64_t(j) + 1)), kMatRows[j], kMatCols[j], f->w[l][j]);
+  if (!rc) rc = gen_matrix(splitmix(seed ^ 0xFFFFull), std::max<int64_t>(vocab, 1), kFwdDim, f->head);
+  if (!rc) rc = check_hip(hipDeviceSynchronize(), "forward_model_create");
+  if (rc) {
+    fwd_release(f);
+    return rc;
+  }
+  *out = f;
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_forward_model_destroy(jero_forward_model* f) {
+  if (!f) return JERO_OK;
+  (void)hipDeviceSynchronize();
+  fwd_release(f);
+  return JERO_OK;
+}
+
+extern "C" int64_t jero_hip_forward_model_head_rows(const jero_forward_model* f) { return f ? f->head_rows : -1; }
+
+extern "C" int64_t jero_hip_forward_model_positions(const jero_forward_model* f) { return f ? f->len : -1; }
+
+extern "C" int jero_hip_forward_model_reset(jero_forward_model* f) {
+  if (!f) return fail(JERO_ERR_INVALID_ARGUMENT, "forward_model_reset: null model");
+  f->len = 0;
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_forward_model_weight(const jero_forward_model* f, int layer, int which, const int8_t** w_dev,
+                                             int64_t* n, int64_t* k, int* shift) {
+  if (!f || !w_dev || !n || !k || !shift) return fail(JERO_ERR_INVALID_ARGUMENT, "forward_model_weight: null pointer");
+  if (layer == -1) {
+    *w_dev = f->head, *n = f->head_rows, *k = kFwdDim, *shift = 6;
+    return JERO_OK;
+  }
+  if (layer < 0 || layer >= kFwdLayers || which < 0 || which >= kFwdMats)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "forward_model_weight: layer must be -1 (head) or 0..3, which 0..5");
+  *w_dev = f->w[layer][which], *n = kMatRows[which], *k = kMatCols[which], *shift = mat_shift(which);
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_forward_model_forward(jero_forward_model* f, const uint32_t* tokens, int64_t m,
+                                              int64_t start_pos, int32_t* logits_dev, void* stream) {
+  int rc = check_model(f, "forward_model_forward");
+  if (rc) return rc;
+  if (!tokens || !logits_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "forward_model_forward: null pointer");
+  if (m < 1) return fail(JERO_ERR_TENSOR_BOUNDS, "forward_model_forward: no tokens");
+  if (start_pos != f->len)
+    return fail(JERO_ERR_INVALID_ARGUMENT, "forward_model_forward: start_pos " + std::to_string(start_pos) +
+                                               " is not the cached position count " + std::to_string(f->len));
+  if (m > f->cap - start_pos)
+    return fail(JERO_ERR_CONTEXT_LENGTH_EXCEEDED, "forward_model_forward: " + std::to_string(start_pos + m) +
+                                                      " positions exceed the capacity " + std::to_string(f->cap));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((rc = check_hip(hipMemcpyAsync(f->tokens, tokens, size_t(m) * sizeof(uint32_t), hipMemcpyHostToDevice, s),
+                      "forward tokens")) ||
+      (rc = forward_rows(f, m, start_pos, logits_dev, s)))
+    return rc;
+  f->len = start_pos + m;
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_forward_model_evaluate(jero_forward_model* f, const uint32_t* prompt, int64_t n,
+                                               int64_t max_tokens, uint32_t* generated, float* timing_ms,
+                                               void* stream) {
+  int rc = check_model(f, "forward_model_evaluate");
+  if (rc) return rc;
+  if (!prompt || (max_tokens > 0 && !generated))
+    return fail(JERO_ERR_INVALID_ARGUMENT, "forward_model_evaluate: null pointer");
+  if (n < 1) return fail(JERO_ERR_CAPABILITY_MISMATCH, "forward_model_evaluate: prompt token sequence cannot be empty");
+  if (max_tokens < 0) return fail(JERO_ERR_INVALID_ARGUMENT, "forward_model_evaluate: negative max_tokens");
+  const int64_t need = n + (max_tokens > 0 ? max_tokens - 1 : 0);
+  if (n > f->cap || need > f->cap)
+    return fail(JERO_ERR_CONTEXT_LENGTH_EXCEEDED, "forward_model_evaluate: " + std::to_string(need) +
+                                                      " positions exceed the capacity " + std::to_string(f->cap));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  hipEvent_t ev[3] = {};
+  for (int i = 0; i < 3 && !rc; i++) rc = check_hip(hipEventCreate(&ev[i]), "forward_model_evaluate events");
+  f->len = 0;
+  // Prefill: the prompt rows, then its sample lands in tokens[0]; decode step i embeds tokens[i-1]
+  // at position n + i - 1 and samples into tokens[i] (evaluate, src/forward.rs:1016-1038).
+  if (!rc) rc = check_hip(hipMemcpyAsync(f->tokens, prompt, size_t(n) * sizeof(uint32_t), hipMemcpyHostToDevice, s),
+                          "forward prompt");
+  if (!rc) rc = check_hip(hipEventRecord(ev[0], s), "event");
+  if (!rc) rc = forward_rows(f, n, 0, f->logits, s);
+  if (!rc && max_tokens > 0) {
+    hipLaunchKernelGGL(fwd_sample_kernel, dim3(1), dim3(256), 0, s, f->logits, f->vocab, f->tokens);
+    rc = check_launch("forward sample");
+  }
+  if (!rc) rc = check_hip(hipEventRecord(ev[1], s), "event");
+  uint32_t* const toks = f->tokens;
+  for (int64_t i = 1; i < max_tokens && !rc; i++) {
+    // The step's token row is tokens[i - 1]: point the embedding at it through f->tokens.
+    f->tokens = toks + (i - 1);
+    rc = forward_rows(f, 1, n + i - 1, f->logits, s);
+    f->tokens = toks;
+    if (!rc) {
+      hipLaunchKernelGGL(fwd_sample_kernel, dim3(1), dim3(256), 0, s, f->logits, f->vocab, toks + i);
+      rc = check_launch("forward sample");
+    }
+  }
+  f->tokens = toks;
+  if (!rc) rc = check_hip(hipEventRecord(ev[2], s), "event");
+  if (!rc && max_tokens > 0)
+    rc = check_hip(hipMemcpyAsync(generated, toks, size_t(max_tokens) * sizeof(uint32_t), hipMemcpyDeviceToHost, s),
+                   "forward generated");
+  if (!rc) rc = check_hip(hipStreamSynchronize(s), "forward_model_evaluate");
+  if (!rc && timing_ms) {
+    rc = check_hip(hipEventElapsedTime(&timing_ms[0], ev[0], ev[1]), "event time");
+    if (!rc) rc = check_hip(hipEventElapsedTime(&timing_ms[1], ev[1], ev[2]), "event time");
+  }
+  for (hipEvent_t e : ev)
+    if (e) (void)hipEventDestroy(e);
+  if (!rc) f->len = need;
+  return rc;
+}

@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <string>
 
+#include "forward.h"
 #include "gemv.h"
 #include "jero_common.h"
 #include "runtime.h"
@@ -283,7 +284,10 @@ __device__ __forceinline__ int8_t requant_i8(int32_t v, int shift) {
   return int8_t(r < -127 ? -127 : r > 127 ? 127 : r);
 }
 
-enum { kI8OutI32 = 0, kI8OutRequant = 1, kI8OutTiles = 2 };
+// kI8OutRequantRelu and kI8OutRequantSatAdd (forward.h) are the two fused epilogues of
+// ForwardModel::forward (src/forward.rs:963-968): max(requant, 0) for the up projection, and the
+// i8 saturating add of the requantized result into the residual rows (sat_add, :817-821) for wo
+// and down.
 
 __device__ __forceinline__ void i8_store(const u32x4 (&r)[8], int8_t (*dst)[kPlaneStride]) {
   const int t = threadIdx.x, rr = t >> 1, h = t & 1;
@@ -356,6 +360,13 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_i8_kernel(const int8_t* __r
             static_cast<int32_t*>(out)[int64_t(m) * N + n] = C[i][k][v];
           } else if constexpr (EPI == kI8OutRequant) {
             static_cast<int8_t*>(out)[int64_t(m) * N + n] = requant_i8(C[i][k][v], shift);
+          } else if constexpr (EPI == kI8OutRequantRelu) {
+            const int8_t r = requant_i8(C[i][k][v], shift);
+            static_cast<int8_t*>(out)[int64_t(m) * N + n] = r < 0 ? int8_t(0) : r;
+          } else if constexpr (EPI == kI8OutRequantSatAdd) {
+            int8_t* o = static_cast<int8_t*>(out) + int64_t(m) * N + n;
+            const int t = int(*o) + int(requant_i8(C[i][k][v], shift));
+            *o = int8_t(t < -128 ? -128 : t > 127 ? 127 : t);
           } else {
             const int64_t blk = int64_t(m / kTileRows) * (N / kTileRows) + n / kTileRows;
             static_cast<int32_t*>(out)[blk * kTileRows * kTileRows + (m % kTileRows) * kTileRows + n % kTileRows] =
@@ -430,6 +441,27 @@ static int launch_gemm_i8(const int8_t* x, int64_t m, int64_t k, const int8_t* w
   hipLaunchKernelGGL((gemm_i8_small_kernel<EPI>), dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, x, w, int(m),
                      int(n), int(k), out, shift);
   return check_launch("gemm i8 (small k)");
+}
+
+// The forward pass's projections: the MFMA kernel with one of the int8 epilogues.
+int launch_gemm_i8_epi(int epi, const int8_t* x, int64_t m, int64_t k, const int8_t* w, int64_t n, int8_t* out,
+                       int shift, hipStream_t s) {
+  int rc = check_i8_args(x, m, k, w, n, out, "gemm_i8 (forward)");
+  if (rc) return rc;
+  if (k % 16 || !aligned4(x) || !aligned4(w)) return fail(JERO_ERR_INVALID_ARGUMENT, "gemm_i8 (forward): k % 16");
+  const dim3 grid(unsigned(gemm_tiles(m, n))), block(kGemmThreads);
+  if (epi == kI8OutRequant)
+    hipLaunchKernelGGL((gemm_i8_kernel<false, kI8OutRequant>), grid, block, 0, s, x, w, int(m), int(n), int(k), out,
+                       shift);
+  else if (epi == kI8OutRequantRelu)
+    hipLaunchKernelGGL((gemm_i8_kernel<false, kI8OutRequantRelu>), grid, block, 0, s, x, w, int(m), int(n), int(k),
+                       out, shift);
+  else if (epi == kI8OutRequantSatAdd)
+    hipLaunchKernelGGL((gemm_i8_kernel<false, kI8OutRequantSatAdd>), grid, block, 0, s, x, w, int(m), int(n), int(k),
+                       out, shift);
+  else
+    return fail(JERO_ERR_INVALID_ARGUMENT, "gemm_i8 (forward): epilogue");
+  return check_launch("gemm i8 (forward)");
 }
 
 }  // namespace jero

@@ -85,6 +85,15 @@ _SIGS = {
     "jero_hip_model_set_position": (_I32, [_P, _I32, _I64, _P]),
     "jero_hip_decode_step": (_I32, [_P, _P]),
     "jero_hip_model_prefill": (_I32, [_P, _P, _I64, _I64, _P]),
+    "jero_hip_forward_model_create": (_I32, [C.c_uint64, _I64, _I64, C.POINTER(_P)]),
+    "jero_hip_forward_model_destroy": (_I32, [_P]),
+    "jero_hip_forward_model_head_rows": (_I64, [_P]),
+    "jero_hip_forward_model_positions": (_I64, [_P]),
+    "jero_hip_forward_model_reset": (_I32, [_P]),
+    "jero_hip_forward_model_weight": (_I32, [_P, _I32, _I32, C.POINTER(_P), C.POINTER(_I64), C.POINTER(_I64),
+                                             C.POINTER(C.c_int)]),
+    "jero_hip_forward_model_forward": (_I32, [_P, _P, _I64, _I64, _P, _P]),
+    "jero_hip_forward_model_evaluate": (_I32, [_P, _P, _I64, _I64, _P, _P, _P]),
     "jero_hip_gguf_open": (_I32, [C.c_char_p, C.POINTER(_P)]),
     "jero_hip_gguf_close": (None, [_P]),
     "jero_hip_gguf_info": (_I32, [_P, C.POINTER(_I64), C.POINTER(C.c_char_p)]),
@@ -516,6 +525,72 @@ def _memcpy(dst_ptr, src_ptr, nbytes):
     rc = _hip.hipMemcpy(C.c_void_p(dst_ptr), C.c_void_p(src_ptr), nbytes, 4)
     if rc != 0:
         raise K3Error(20, f"hipMemcpy failed ({rc})")
+
+
+class ForwardModel:
+    """The synthetic all-int8 transformer of src/forward.rs (ForwardModel::new, :879-903) on the
+    device: weights generated from (seed, vocab), a K/V cache of max_positions positions.
+    forward() mirrors ForwardModel::forward (:930-976) and evaluate() the token loop of
+    ForwardModel::evaluate (:995-1043)."""
+
+    DIM, FFN, LAYERS = 512, 1024, 4
+    NAMES = ("wq", "wk", "wv", "wo", "up", "down")
+
+    def __init__(self, seed, vocab, max_positions=64):
+        h = C.c_void_p()
+        check(lib().jero_hip_forward_model_create(C.c_uint64(seed), vocab, max_positions, C.byref(h)))
+        self.h = h
+        self.vocab = vocab
+        self.max_positions = max_positions
+        self.head_rows = int(lib().jero_hip_forward_model_head_rows(h))
+
+    def close(self):
+        if self.h:
+            lib().jero_hip_forward_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def positions(self):
+        """Positions in the K/V cache: the start_pos the next forward() must pass."""
+        return int(lib().jero_hip_forward_model_positions(self.h))
+
+    def reset(self):
+        check(lib().jero_hip_forward_model_reset(self.h))
+
+    def weight(self, layer, which=0):
+        """(device pointer, n, k, shift) of layer's matrix `which` (0..5: wq wk wv wo up down), or of
+        the LM head for layer -1."""
+        w, n, k, sh = C.c_void_p(), C.c_int64(), C.c_int64(), C.c_int()
+        check(lib().jero_hip_forward_model_weight(self.h, layer, which, C.byref(w), C.byref(n), C.byref(k),
+                                                  C.byref(sh)))
+        return w.value, n.value, k.value, sh.value
+
+    def forward(self, tokens, start_pos, logits, stream=None):
+        """One forward pass over host `tokens` at start_pos (== positions); logits: int32 device
+        tensor of head_rows values."""
+        import numpy as np
+        t = np.ascontiguousarray(tokens, np.uint32)
+        check(lib().jero_hip_forward_model_forward(self.h, C.c_void_p(t.ctypes.data), t.size, start_pos,
+                                                   _ptr(logits), _stream(stream)))
+
+    def evaluate(self, prompt, max_tokens, stream=None, timing=False):
+        """Prefill over prompt, then greedy decode until max_tokens tokens: the generated ids
+        (and, with timing, the (prefill_ms, decode_ms) the device took)."""
+        import numpy as np
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(max(max_tokens, 1), np.uint32)
+        ms = np.zeros(2, np.float32)
+        check(lib().jero_hip_forward_model_evaluate(self.h, C.c_void_p(p.ctypes.data), p.size, max_tokens,
+                                                    C.c_void_p(out.ctypes.data), C.c_void_p(ms.ctypes.data),
+                                                    _stream(stream)))
+        toks = [int(v) for v in out[:max_tokens]]
+        return (toks, (float(ms[0]), float(ms[1]))) if timing else toks
 
 
 class DecodeModel:

@@ -875,3 +875,322 @@ int jo_decode_step(const jo_model *M, float *kv, int32_t token, int64_t pos, flo
   free(x);
   return rc;
 }
+
+/* ------------------------------------------------------------------ synthetic int8 ForwardModel */
+
+/* splitmix (src/forward.rs:326-332): one SplitMix64 output for state x. */
+uint64_t jo_splitmix(uint64_t x) {
+  uint64_t z = x + 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+/* fill_small (src/forward.rs:335-343): out[i] = (splitmix(seed ^ i * C) & 15) - 8. */
+void jo_fill_small(uint64_t seed, int64_t len, int8_t *out) {
+  for (int64_t i = 0; i < len; i++)
+    out[i] = (int8_t)((int)(jo_splitmix(seed ^ ((uint64_t)i * 0xA24BAED4963EE407ull)) & 0xF) - 8);
+}
+
+/* isqrt (src/forward.rs:747-758): Newton's iteration from x = v, y = ceil(v / 2), stopping when y
+ * no longer decreases; the midpoint is floor((x + v / x) / 2) without overflow. */
+uint64_t jo_isqrt(uint64_t v) {
+  if (v < 2) return v;
+  uint64_t x = v, y = v / 2 + (v & 1);
+  while (y < x) {
+    x = y;
+    const uint64_t b = v / x;
+    y = (x & b) + ((x ^ b) >> 1);
+  }
+  return x;
+}
+
+/* ForwardExec::rmsnorm (src/forward.rs:672-699): per row, rms = max(isqrt(sum v^2 / DIM), 1),
+ * y = clamp(v * 48 / rms, -127, 127) with division truncating toward zero. */
+void jo_fwd_rmsnorm(const int8_t *x, int64_t m, int8_t *out) {
+  for (int64_t r = 0; r < m; r++) {
+    const int8_t *row = x + r * JO_FWD_DIM;
+    uint64_t ms = 0;
+    for (int i = 0; i < JO_FWD_DIM; i++) ms += (uint64_t)((int32_t)row[i] * (int32_t)row[i]);
+    uint64_t rq = jo_isqrt(ms / JO_FWD_DIM);
+    int32_t rms = rq > INT32_MAX ? INT32_MAX : (int32_t)rq;
+    if (rms < 1) rms = 1;
+    for (int i = 0; i < JO_FWD_DIM; i++) {
+      int32_t y = (int32_t)row[i] * 48 / rms;
+      out[r * JO_FWD_DIM + i] = (int8_t)(y < -127 ? -127 : y > 127 ? 127 : y);
+    }
+  }
+}
+
+/* ForwardExec::attention (src/forward.rs:702-744): query row r sits at position start_pos + r and
+ * attends to cache rows 0..=start_pos + r with integer weights w = clamp(q.k >> 10, 0, 127) + 1;
+ * out = sum(w v) / sum(w), int64 division truncating toward zero. */
+void jo_fwd_attention(const int8_t *q, const int8_t *k_cache, const int8_t *v_cache, int64_t m, int64_t start_pos,
+                      int8_t *out) {
+  int64_t acc[JO_FWD_DIM];
+  for (int64_t r = 0; r < m; r++) {
+    const int64_t pos = start_pos + r;
+    const int8_t *qrow = q + r * JO_FWD_DIM;
+    memset(acc, 0, sizeof acc);
+    int64_t total = 0;
+    for (int64_t t = 0; t <= pos; t++) {
+      const int8_t *krow = k_cache + t * JO_FWD_DIM, *vrow = v_cache + t * JO_FWD_DIM;
+      int32_t s = 0;
+      for (int i = 0; i < JO_FWD_DIM; i++) s += (int32_t)qrow[i] * (int32_t)krow[i];
+      int32_t sh = s >> 10;
+      const int64_t w = (int64_t)(sh < 0 ? 0 : sh > 127 ? 127 : sh) + 1;
+      total += w;
+      for (int i = 0; i < JO_FWD_DIM; i++) acc[i] += w * vrow[i];
+    }
+    for (int i = 0; i < JO_FWD_DIM; i++) out[r * JO_FWD_DIM + i] = (int8_t)(acc[i] / total);
+  }
+}
+
+/* requant (src/forward.rs:345-350) over a buffer; relu != 0 then clamps below at 0 (the up
+ * projection, :963-966). */
+static void fwd_requant(const int32_t *raw, int64_t n, int shift, int relu, int8_t *out) {
+  for (int64_t i = 0; i < n; i++) {
+    int32_t r = (int32_t)((uint32_t)raw[i] + (1u << (shift - 1))) >> shift;
+    r = r < -127 ? -127 : r > 127 ? 127 : r;
+    if (relu && r < 0) r = 0;
+    out[i] = (int8_t)r;
+  }
+}
+
+/* sat_add (src/forward.rs:817-821): i8 saturating add in place. */
+static void fwd_sat_add(int8_t *a, const int8_t *b, int64_t n) {
+  for (int64_t i = 0; i < n; i++) {
+    int s = (int)a[i] + (int)b[i];
+    a[i] = (int8_t)(s < -128 ? -128 : s > 127 ? 127 : s);
+  }
+}
+
+typedef struct jo_fwd_mat {
+  int64_t n, k; /* n padded to whole 8-row tiles (Matrix::random, src/forward.rs:364-377) */
+  int shift;
+  int8_t *rows;
+} jo_fwd_mat;
+
+struct jo_fwd_model {
+  uint64_t seed;
+  int64_t vocab, cap, len;
+  int threads;
+  jo_fwd_mat w[JO_FWD_LAYERS][6];
+  jo_fwd_mat head;
+  int8_t *kc[JO_FWD_LAYERS], *vc[JO_FWD_LAYERS];
+};
+
+static int fwd_mat(jo_fwd_mat *m, uint64_t seed, int64_t n, int64_t k, int shift) {
+  const int64_t n_pad = (n + 7) / 8 * 8;
+  m->n = n_pad;
+  m->k = k;
+  m->shift = shift;
+  m->rows = (int8_t *)calloc((size_t)(n_pad * k), 1);
+  if (!m->rows) return -1;
+  jo_fill_small(seed, n * k, m->rows);
+  return 0;
+}
+
+void jo_fwd_free(jo_fwd_model *f) {
+  if (!f) return;
+  for (int l = 0; l < JO_FWD_LAYERS; l++) {
+    for (int j = 0; j < 6; j++) free(f->w[l][j].rows);
+    free(f->kc[l]);
+    free(f->vc[l]);
+  }
+  free(f->head.rows);
+  free(f);
+}
+
+/* ForwardModel::new (src/forward.rs:879-903): layer l's matrices from seeds
+ * splitmix(seed ^ (16 l + 1..6)) in the order wq wk wv wo up down, shifts 6 (down: 7); the LM
+ * head from splitmix(seed ^ 0xFFFF) with max(vocab, 1) rows. */
+jo_fwd_model *jo_fwd_new(uint64_t seed, int64_t vocab, int64_t max_positions) {
+  if (vocab < 0 || max_positions < 1) return NULL;
+  jo_fwd_model *f = (jo_fwd_model *)calloc(1, sizeof *f);
+  if (!f) return NULL;
+  f->seed = seed;
+  f->vocab = vocab;
+  f->cap = max_positions;
+  f->threads = 1;
+  int bad = 0;
+  for (int l = 0; l < JO_FWD_LAYERS; l++) {
+    const uint64_t s = (uint64_t)l * 16;
+    const int64_t shape[6][2] = {{JO_FWD_DIM, JO_FWD_DIM}, {JO_FWD_DIM, JO_FWD_DIM}, {JO_FWD_DIM, JO_FWD_DIM},
+                                 {JO_FWD_DIM, JO_FWD_DIM}, {JO_FWD_FFN, JO_FWD_DIM}, {JO_FWD_DIM, JO_FWD_FFN}};
+    for (int j = 0; j < 6; j++)
+      bad |= fwd_mat(&f->w[l][j], jo_splitmix(seed ^ (s + 1 + (uint64_t)j)), shape[j][0], shape[j][1], j == 5 ? 7 : 6);
+    f->kc[l] = (int8_t *)malloc((size_t)(max_positions * JO_FWD_DIM));
+    f->vc[l] = (int8_t *)malloc((size_t)(max_positions * JO_FWD_DIM));
+    bad |= !f->kc[l] || !f->vc[l];
+  }
+  bad |= fwd_mat(&f->head, jo_splitmix(seed ^ 0xFFFFull), vocab > 1 ? vocab : 1, JO_FWD_DIM, 6);
+  if (bad) {
+    jo_fwd_free(f);
+    return NULL;
+  }
+  return f;
+}
+
+int64_t jo_fwd_head_rows(const jo_fwd_model *f) { return f->head.n; }
+int64_t jo_fwd_len(const jo_fwd_model *f) { return f->len; }
+void jo_fwd_reset(jo_fwd_model *f) { f->len = 0; }
+void jo_fwd_set_threads(jo_fwd_model *f, int threads) { f->threads = threads < 1 ? 1 : threads; }
+
+const int8_t *jo_fwd_weight(const jo_fwd_model *f, int layer, int which, int64_t *n, int64_t *k, int *shift) {
+  const jo_fwd_mat *m;
+  if (layer == -1) m = &f->head;
+  else if (layer >= 0 && layer < JO_FWD_LAYERS && which >= 0 && which < 6) m = &f->w[layer][which];
+  else return NULL;
+  *n = m->n;
+  *k = m->k;
+  *shift = m->shift;
+  return m->rows;
+}
+
+/* embed (src/forward.rs:918-926): fill_small(seed ^ token * 0x9E3779B9, DIM) * 8. */
+void jo_fwd_embed(uint64_t seed, uint32_t token, int8_t *out) {
+  jo_fill_small(seed ^ ((uint64_t)token * 0x9E3779B9ull), JO_FWD_DIM, out);
+  for (int i = 0; i < JO_FWD_DIM; i++) out[i] = (int8_t)(out[i] * 8);
+}
+
+/* Splits [0, n) into `threads` contiguous ranges run on their own threads (the checker's speed
+ * only: every range computes the same integers as a single pass). */
+typedef void (*fwd_range_fn)(void *ctx, int64_t lo, int64_t hi);
+typedef struct {
+  fwd_range_fn fn;
+  void *ctx;
+  int64_t lo, hi;
+} fwd_job;
+
+static void *fwd_worker(void *p) {
+  fwd_job *j = (fwd_job *)p;
+  j->fn(j->ctx, j->lo, j->hi);
+  return NULL;
+}
+
+static void fwd_par(int threads, int64_t n, fwd_range_fn fn, void *ctx) {
+  if (threads > 64) threads = 64;
+  if (threads > n) threads = (int)n;
+  if (threads <= 1) {
+    fn(ctx, 0, n);
+    return;
+  }
+  pthread_t th[64];
+  fwd_job jobs[64];
+  const int64_t chunk = (n + threads - 1) / threads;
+  for (int t = 0; t < threads; t++) {
+    jobs[t].fn = fn, jobs[t].ctx = ctx;
+    jobs[t].lo = t * chunk < n ? t * chunk : n;
+    jobs[t].hi = (t + 1) * chunk < n ? (t + 1) * chunk : n;
+  }
+  for (int t = 1; t < threads; t++) pthread_create(&th[t], NULL, fwd_worker, &jobs[t]);
+  fwd_worker(&jobs[0]);
+  for (int t = 1; t < threads; t++) pthread_join(th[t], NULL);
+}
+
+typedef struct {
+  const int8_t *x, *w;
+  int64_t m, n, k;
+  int32_t *out;
+} fwd_gemm_ctx;
+
+/* out[i][j] = sum_t x[i][t] w[j][t] for weight rows j in [lo, hi). */
+static void fwd_gemm_range(void *p, int64_t lo, int64_t hi) {
+  const fwd_gemm_ctx *c = (const fwd_gemm_ctx *)p;
+  for (int64_t j = lo; j < hi; j++) {
+    const int8_t *wr = c->w + j * c->k;
+    for (int64_t i = 0; i < c->m; i++) {
+      const int8_t *xr = c->x + i * c->k;
+      int32_t s = 0;
+      for (int64_t t = 0; t < c->k; t++) s += (int32_t)xr[t] * (int32_t)wr[t];
+      c->out[i * c->n + j] = s;
+    }
+  }
+}
+
+typedef struct {
+  const int8_t *q, *kc, *vc;
+  int64_t start_pos;
+  int8_t *out;
+} fwd_att_ctx;
+
+static void fwd_att_range(void *p, int64_t lo, int64_t hi) {
+  const fwd_att_ctx *c = (const fwd_att_ctx *)p;
+  jo_fwd_attention(c->q + lo * JO_FWD_DIM, c->kc, c->vc, hi - lo, c->start_pos + lo, c->out + lo * JO_FWD_DIM);
+}
+
+static void fwd_proj(const jo_fwd_mat *w, const int8_t *x, int64_t m, int relu, int32_t *raw, int8_t *out,
+                     int threads) {
+  fwd_gemm_ctx c = {x, w->rows, m, w->n, w->k, raw};
+  fwd_par(threads, w->n, fwd_gemm_range, &c);
+  fwd_requant(raw, m * w->n, w->shift, relu, out);
+}
+
+/* ForwardModel::forward (src/forward.rs:930-976): the tokens at positions start_pos.., which must
+ * equal the positions already cached; logits [head rows] of the last token. */
+int jo_fwd_forward(jo_fwd_model *f, const uint32_t *tokens, int64_t m, int64_t start_pos, int32_t *logits) {
+  if (m < 1 || start_pos != f->len || start_pos + m > f->cap) return -1;
+  const int64_t D = JO_FWD_DIM;
+  int8_t *x = (int8_t *)malloc((size_t)(m * D)), *h = (int8_t *)malloc((size_t)(m * D));
+  int8_t *q = (int8_t *)malloc((size_t)(m * D)), *a = (int8_t *)malloc((size_t)(m * D));
+  int8_t *o = (int8_t *)malloc((size_t)(m * D)), *up = (int8_t *)malloc((size_t)(m * JO_FWD_FFN));
+  int32_t *raw = (int32_t *)malloc((size_t)(m * JO_FWD_FFN) * sizeof(int32_t));
+  int rc = (x && h && q && a && o && up && raw) ? 0 : -2;
+  if (!rc) {
+    for (int64_t r = 0; r < m; r++) jo_fwd_embed(f->seed, tokens[r], x + r * D);
+    for (int l = 0; l < JO_FWD_LAYERS; l++) {
+      const jo_fwd_mat *W = f->w[l];
+      const int T = f->threads;
+      jo_fwd_rmsnorm(x, m, h);
+      fwd_proj(&W[0], h, m, 0, raw, q, T);
+      fwd_proj(&W[1], h, m, 0, raw, f->kc[l] + start_pos * D, T);
+      fwd_proj(&W[2], h, m, 0, raw, f->vc[l] + start_pos * D, T);
+      fwd_att_ctx ac = {q, f->kc[l], f->vc[l], start_pos, a};
+      fwd_par(T, m, fwd_att_range, &ac);
+      fwd_proj(&W[3], a, m, 0, raw, o, T);
+      fwd_sat_add(x, o, m * D);
+      jo_fwd_rmsnorm(x, m, h);
+      fwd_proj(&W[4], h, m, 1, raw, up, T);
+      fwd_proj(&W[5], up, m, 0, raw, o, T);
+      fwd_sat_add(x, o, m * D);
+    }
+    jo_fwd_rmsnorm(x + (m - 1) * D, 1, h);
+    fwd_gemm_ctx hc = {h, f->head.rows, 1, f->head.n, D, logits};
+    fwd_par(f->threads, f->head.n, fwd_gemm_range, &hc);
+    f->len = start_pos + m;
+  }
+  free(x), free(h), free(q), free(a), free(o), free(up), free(raw);
+  return rc;
+}
+
+/* ForwardModel::sample (src/forward.rs:978-986): the first index of the largest of the first
+ * vocab logits (0 when vocab <= 1). */
+uint32_t jo_fwd_sample(const int32_t *logits, int64_t vocab) {
+  int64_t best = 0;
+  for (int64_t i = 1; i < vocab; i++)
+    if (logits[i] > logits[best]) best = i;
+  return (uint32_t)best;
+}
+
+/* ForwardModel::evaluate's token loop (src/forward.rs:1000-1043): a fresh cache, the prompt's
+ * forward, then greedy steps until max_tokens tokens are generated. */
+int jo_fwd_evaluate(jo_fwd_model *f, const uint32_t *prompt, int64_t n, int64_t max_tokens, uint32_t *generated) {
+  if (n < 1 || max_tokens < 0) return -1;
+  if (n + (max_tokens > 0 ? max_tokens - 1 : 0) > f->cap) return -1;
+  int32_t *logits = (int32_t *)malloc((size_t)f->head.n * sizeof(int32_t));
+  if (!logits) return -2;
+  f->len = 0;
+  int rc = jo_fwd_forward(f, prompt, n, 0, logits);
+  if (!rc && max_tokens > 0) {
+    uint32_t tok = jo_fwd_sample(logits, f->vocab);
+    generated[0] = tok;
+    for (int64_t i = 1; i < max_tokens && !rc; i++) {
+      rc = jo_fwd_forward(f, &tok, 1, n + i - 1, logits);
+      tok = jo_fwd_sample(logits, f->vocab);
+      generated[i] = tok;
+    }
+  }
+  free(logits);
+  return rc;
+}

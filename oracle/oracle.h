@@ -33,6 +33,9 @@
  *   top-k routing       : reference KATs src/gemma.rs:1722-1740
  *   argmax              : reference KATs src/engine.rs:2677-2727
  *   int8 GEMM           : brute force integer matmul (numpy), exact
+ *   int8 ForwardModel   : SplitMix64's published first outputs, isqrt against math.isqrt,
+ *                         rmsnorm / attention closed forms, brute force numpy pieces, and the
+ *                         prefill == token-by-token invariant of the whole forward
  */
 #ifndef JERO_ORACLE_H
 #define JERO_ORACLE_H
@@ -177,6 +180,34 @@ int jo_decode_head(const jo_model *mdl, const float *x, float *logits, int threa
 /* kv: f32 [n_layers][2][kv_capacity][nkv*hd].  logits [vocab]. */
 int jo_decode_step(const jo_model *mdl, float *kv, int32_t token, int64_t pos, float *logits,
                    int threads);
+
+/* Synthetic all-int8 transformer of src/forward.rs (ForwardModel, :834-1075): DIM 512, FFN 1024,
+ * 4 layers (:124-128), one 512-wide attention head, exact integer arithmetic throughout. */
+#define JO_FWD_DIM 512
+#define JO_FWD_FFN 1024
+#define JO_FWD_LAYERS 4
+uint64_t jo_splitmix(uint64_t x);
+void jo_fill_small(uint64_t seed, int64_t len, int8_t *out);
+uint64_t jo_isqrt(uint64_t v);
+void jo_fwd_rmsnorm(const int8_t *x, int64_t m, int8_t *out);
+void jo_fwd_attention(const int8_t *q, const int8_t *k_cache, const int8_t *v_cache, int64_t m, int64_t start_pos,
+                      int8_t *out);
+void jo_fwd_embed(uint64_t seed, uint32_t token, int8_t *out);
+typedef struct jo_fwd_model jo_fwd_model;
+/* NULL on a bad argument or allocation failure; the cache holds max_positions positions. */
+jo_fwd_model *jo_fwd_new(uint64_t seed, int64_t vocab, int64_t max_positions);
+void jo_fwd_free(jo_fwd_model *f);
+int64_t jo_fwd_head_rows(const jo_fwd_model *f);
+int64_t jo_fwd_len(const jo_fwd_model *f);
+void jo_fwd_reset(jo_fwd_model *f);
+/* Worker threads of the forward's products and attention (1 by default). */
+void jo_fwd_set_threads(jo_fwd_model *f, int threads);
+/* layer 0..3 with which 0..5 = wq wk wv wo up down, or layer -1: the LM head. Row-major [n][k]. */
+const int8_t *jo_fwd_weight(const jo_fwd_model *f, int layer, int which, int64_t *n, int64_t *k, int *shift);
+/* 0, or -1 for m < 1, start_pos != cached positions or past the capacity. logits [head rows]. */
+int jo_fwd_forward(jo_fwd_model *f, const uint32_t *tokens, int64_t m, int64_t start_pos, int32_t *logits);
+uint32_t jo_fwd_sample(const int32_t *logits, int64_t vocab);
+int jo_fwd_evaluate(jo_fwd_model *f, const uint32_t *prompt, int64_t n, int64_t max_tokens, uint32_t *generated);
 
 #ifdef __cplusplus
 }

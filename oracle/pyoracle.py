@@ -55,6 +55,22 @@ def lib():
             "jo_decode_step": (I32, [P, P, I32, I64, P, I32]),
             "jo_decode_layer": (I32, [P, P, I64, P, I64, I32, P]),
             "jo_decode_head": (I32, [P, P, P, I32, P, P]),
+            "jo_splitmix": (C.c_uint64, [C.c_uint64]),
+            "jo_fill_small": (None, [C.c_uint64, I64, P]),
+            "jo_isqrt": (C.c_uint64, [C.c_uint64]),
+            "jo_fwd_rmsnorm": (None, [P, I64, P]),
+            "jo_fwd_attention": (None, [P, P, P, I64, I64, P]),
+            "jo_fwd_embed": (None, [C.c_uint64, C.c_uint32, P]),
+            "jo_fwd_new": (P, [C.c_uint64, I64, I64]),
+            "jo_fwd_free": (None, [P]),
+            "jo_fwd_head_rows": (I64, [P]),
+            "jo_fwd_len": (I64, [P]),
+            "jo_fwd_reset": (None, [P]),
+            "jo_fwd_set_threads": (None, [P, I32]),
+            "jo_fwd_weight": (P, [P, I32, I32, P, P, P]),
+            "jo_fwd_forward": (I32, [P, P, I64, I64, P]),
+            "jo_fwd_sample": (C.c_uint32, [P, I64]),
+            "jo_fwd_evaluate": (I32, [P, P, I64, I64, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -332,3 +348,102 @@ class DecodeModel:
         rc = lib().jo_decode_head(C.byref(self.model), _p(x), _p(logits), threads, _p(xn), _p(q8))
         assert rc == 0
         return logits, xn, q8
+
+
+# ---------------------------------------------------------------- synthetic int8 ForwardModel
+
+FWD_DIM, FWD_FFN, FWD_LAYERS = 512, 1024, 4
+FWD_NAMES = ("wq", "wk", "wv", "wo", "up", "down")
+
+
+def splitmix(x):
+    return int(lib().jo_splitmix(x))
+
+
+def fill_small(seed, n):
+    out = np.empty(n, np.int8)
+    lib().jo_fill_small(seed, n, _p(out))
+    return out
+
+
+def isqrt(v):
+    return int(lib().jo_isqrt(v))
+
+
+def fwd_rmsnorm(x):
+    x = np.ascontiguousarray(x, np.int8).reshape(-1, FWD_DIM)
+    out = np.empty_like(x)
+    lib().jo_fwd_rmsnorm(_p(x), x.shape[0], _p(out))
+    return out
+
+
+def fwd_attention(q, k_cache, v_cache, start_pos):
+    q = np.ascontiguousarray(q, np.int8).reshape(-1, FWD_DIM)
+    k_cache = np.ascontiguousarray(k_cache, np.int8)
+    v_cache = np.ascontiguousarray(v_cache, np.int8)
+    assert k_cache.size >= (start_pos + q.shape[0]) * FWD_DIM and v_cache.size == k_cache.size
+    out = np.empty_like(q)
+    lib().jo_fwd_attention(_p(q), _p(k_cache), _p(v_cache), q.shape[0], start_pos, _p(out))
+    return out
+
+
+def fwd_embed(seed, token):
+    out = np.empty(FWD_DIM, np.int8)
+    lib().jo_fwd_embed(seed, token, _p(out))
+    return out
+
+
+def fwd_sample(logits, vocab):
+    logits = np.ascontiguousarray(logits, np.int32)
+    return int(lib().jo_fwd_sample(_p(logits), vocab))
+
+
+class ForwardModel:
+    """ForwardModel (src/forward.rs:834-1075) on the CPU: weights from (seed, vocab), a cache of
+    max_positions positions."""
+
+    def __init__(self, seed, vocab, max_positions=64, threads=1):
+        self.h = lib().jo_fwd_new(seed, vocab, max_positions)
+        if not self.h:
+            raise ValueError("jo_fwd_new failed")
+        lib().jo_fwd_set_threads(self.h, threads)
+        self.vocab = vocab
+        self.head_rows = int(lib().jo_fwd_head_rows(self.h))
+
+    def close(self):
+        if self.h:
+            lib().jo_fwd_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def weight(self, layer, which=0):
+        n, k, sh = C.c_int64(), C.c_int64(), C.c_int()
+        ptr = lib().jo_fwd_weight(self.h, layer, which, C.byref(n), C.byref(k), C.byref(sh))
+        assert ptr
+        arr = np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_int8)), shape=(n.value * k.value,))
+        return arr.reshape(n.value, k.value).copy(), sh.value
+
+    @property
+    def length(self):
+        return int(lib().jo_fwd_len(self.h))
+
+    def reset(self):
+        lib().jo_fwd_reset(self.h)
+
+    def forward(self, tokens, start_pos):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.empty(self.head_rows, np.int32)
+        rc = lib().jo_fwd_forward(self.h, _p(t), t.size, start_pos, _p(logits))
+        if rc:
+            raise ValueError(f"jo_fwd_forward rc={rc}")
+        return logits
+
+    def evaluate(self, prompt, max_tokens):
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(max(max_tokens, 1), np.uint32)
+        rc = lib().jo_fwd_evaluate(self.h, _p(p), p.size, max_tokens, _p(out))
+        if rc:
+            raise ValueError(f"jo_fwd_evaluate rc={rc}")
+        return [int(v) for v in out[:max_tokens]]

@@ -30,8 +30,12 @@ Third and fourth parts: the Q4_K x Q8_K prefill GEMM (M=512, K=4096, N=14336) on
 TOP/s and fractions of the int8 peak, next to the oracle's per-token GEMV; and the Qwen3-MoE expert
 layer (H=2048, 128 experts, FFN 768, top-8) at 1 and 64 tokens, as GB/s over the routed experts.
 
+Fifth part ("forward_model"): the int8 ForwardModel matrix bench (prompt "hello world", vocab
+256, n_ctx 64: 53 greedy tokens) through jero_hip_forward_model_evaluate, as prefill ms and decode
+tokens/s, next to the oracle's scalar C evaluate of the same run (and whether its tokens agree).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-gemm]
-                       [--no-moe] [--copy-probe MB]
+                       [--no-moe] [--no-forward] [--copy-probe MB]
 """
 import argparse
 import json
@@ -428,6 +432,63 @@ def cpu_baseline(O, host_w, host_xq, budget_s=12.0):
     return per_step * done / el / 1e9, threads, done, el
 
 
+def fnv1a(text):
+    """The matrix bench's model seed: FNV-1a of the prompt text (src/bin/jero-diag/bench.rs:1142-1147)."""
+    h = 0xCBF29CE484222325
+    for b in text.encode():
+        h = ((h ^ b) * 0x100000001B3) & ((1 << 64) - 1)
+    return h
+
+
+FWD_PROMPT_TEXT, FWD_VOCAB, FWD_CTX = "hello world", 256, 64
+FWD_LAYER_MACS = 4 * (4 * 512 * 512 + 2 * 512 * 1024)  # ForwardModel::layer_macs_per_token
+
+
+def bench_forward_model(J, reps):
+    """The int8 ForwardModel's matrix bench (src/bin/jero-diag/bench.rs:1125-1148 -> evaluate): prompt
+    "hello world" as byte tokens, vocab 256, n_ctx 64, so 11 prompt tokens and 53 generated."""
+    import numpy as np
+    prompt = list(FWD_PROMPT_TEXT.encode())
+    max_tokens = min(128, FWD_CTX - len(prompt))
+    m = J.ForwardModel(fnv1a(FWD_PROMPT_TEXT), FWD_VOCAB, FWD_CTX)
+    toks, _ = m.evaluate(prompt, max_tokens, timing=True)  # warm-up
+    pre, dec, wall = [], [], []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        t, (p_ms, d_ms) = m.evaluate(prompt, max_tokens, timing=True)
+        wall.append(time.perf_counter() - t0)
+        assert t == toks, "ForwardModel evaluate is not deterministic"
+        pre.append(p_ms)
+        dec.append(d_ms)
+    m.close()
+    steps = max_tokens - 1
+    d_ms = float(np.median(dec))
+    macs = FWD_LAYER_MACS + FWD_VOCAB * 512
+    return {
+        "workload": "ForwardModel (4 layers, dim 512, FFN 1024, vocab 256), prompt 'hello world' (11 byte tokens), "
+                    f"{max_tokens} greedy tokens, n_ctx {FWD_CTX}",
+        "reps": reps,
+        "prefill_ms": round(float(np.median(pre)), 4),
+        "decode_ms": round(d_ms, 4),
+        "decode_tok_s": round(steps / (d_ms * 1e-3), 1),
+        "decode_us_per_token": round(d_ms * 1e3 / steps, 2),
+        "decode_gmac_s": round(macs * steps / (d_ms * 1e-3) / 1e9, 2),
+        "evaluate_wall_ms": round(float(np.median(wall)) * 1e3, 3),
+        "tokens": toks,
+    }, (prompt, max_tokens)
+
+
+def cpu_forward_baseline(O, prompt, max_tokens, budget_s=3.0):
+    """The oracle's ForwardModel evaluate (scalar C restatement, one thread) on the same workload."""
+    f = O.ForwardModel(fnv1a(FWD_PROMPT_TEXT), FWD_VOCAB, FWD_CTX, threads=1)
+    reps, toks, t0 = 0, None, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or reps == 0:
+        toks = f.evaluate(prompt, max_tokens)
+        reps += 1
+    el = time.perf_counter() - t0
+    return reps * max_tokens / el, reps, el, toks
+
+
 def measured_traffic():
     """HBM bytes per Q4_K GEMV launch (mean of the three shapes) from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE passes, each scaled by the counter's reading for a 512 MB copy; None if
@@ -449,6 +510,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-forward", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=50)
     ap.add_argument("--copy-probe", type=float, default=0.0,
                     help="also run one device copy of this many MB (PMC byte-counter calibration)")
@@ -597,6 +659,18 @@ def main():
         moe = bench_moe(torch, J, dev, stream, max(20, args.steps // 5))
         torch.cuda.empty_cache()
 
+    # ---- int8 ForwardModel matrix bench (extra)
+    fwd = None
+    if not args.no_forward:
+        fwd, (fprompt, fmax) = bench_forward_model(J, 20)
+        if not args.no_cpu:
+            import pyoracle as O
+            tps, reps, el, ctoks = cpu_forward_baseline(O, fprompt, fmax)
+            fwd["cpu_baseline"] = {"value": round(tps, 1), "unit": "generated tok/s (prefill included)", "cores": 1,
+                                   "kind": "port", "tokens_equal": ctoks == fwd["tokens"],
+                                   "sample": f"{reps} full evaluate runs, {el:.1f} s, scalar C restatement"}
+            fwd["evaluate_tok_s"] = round(fmax / (fwd["evaluate_wall_ms"] * 1e-3), 1)
+
     # ---- full decode step (extra)
     decode = None
     if not args.no_decode:
@@ -642,6 +716,7 @@ def main():
         "prefill_gemm": gemm,
         "moe": moe,
         "decode": decode,
+        "forward_model": fwd,
     }
     print(json.dumps(out))
 

@@ -14,13 +14,15 @@
 //   qkv   : RMSNorm of x in the prologue (each workgroup normalises the rows it needs in LDS), the
 //           three projections in one launch (blockIdx.y picks wq / wk / wv), k and v rows written
 //           straight into the caches at start_pos
-//   attn  : one workgroup per query row over cache rows 0..=start_pos + r
+//   attn  : one workgroup per query row over cache rows 0..=start_pos + r; a one-row step below
+//           kAttInMax positions computes it instead in the prologue of every wo workgroup (a
+//           launch saved for npos KiB of cache reads per workgroup)
 //   wo    : requant, then saturating add into x
 //   up    : RMSNorm prologue, requant, relu
 //   down  : requant, saturating add into x
-// then the head (RMSNorm of the last row, int32 logits) and, in evaluate, the sample kernel,
-// which leaves the next token in device memory for the next step's embedding: the decode loop
-// never waits for the host.  Up to kMvRows rows the projections run on the matvec kernel below
+// then the head (RMSNorm of the last row, int32 logits) and, in evaluate, one workgroup that
+// samples the next token and writes it and its embedding (the next step's input row) to device
+// memory: the decode loop never waits for the host.  Up to kMvRows rows the projections run on the matvec kernel below
 // (one weight row per wave, the token rows in LDS); longer prompts run the int8 MFMA GEMM of
 // gemm.hip with the same fused epilogues, after a row RMSNorm kernel.
 #include <algorithm>
@@ -37,6 +39,7 @@ constexpr int kFwdDim = 512, kFwdFfn = 1024, kFwdLayers = 4, kFwdMats = 6;
 constexpr int kMvRows = 64;     // token rows of one matvec launch (LDS: m x K bytes, 64 KiB at most)
 constexpr int kMvWaves = 4;     // weight rows per matvec workgroup, one per wave
 constexpr int kAttChunk = 4096;  // cache positions whose weights one attention pass keeps in LDS
+constexpr int64_t kAttInMax = 128;  // one-row steps below this position compute attention in wo
 constexpr int64_t kFwdMaxPositions = int64_t(1) << 22;
 
 // splitmix (src/forward.rs:326-332): one SplitMix64 output for state x.
@@ -50,19 +53,6 @@ __host__ __device__ __forceinline__ uint64_t splitmix(uint64_t x) {
 // Element i of fill_small(seed, .) (src/forward.rs:335-343), in [-8, 7].
 __device__ __forceinline__ int small_of(uint64_t seed, uint64_t i) {
   return int(splitmix(seed ^ (i * 0xA24BAED4963EE407ull)) & 0xFu) - 8;
-}
-
-// isqrt (src/forward.rs:747-758): Newton's iteration from x = v, y = ceil(v / 2), stopping when y
-// no longer decreases; floor((x + v / x) / 2) as the overflow-free midpoint.
-__device__ __forceinline__ uint32_t isqrt_u32(uint32_t v) {
-  if (v < 2) return v;
-  uint32_t x = v, y = v / 2 + (v & 1);
-  while (y < x) {
-    x = y;
-    const uint32_t b = v / x;
-    y = (x & b) + ((x ^ b) >> 1);
-  }
-  return x;
 }
 
 template <int CTRL, int ROW_MASK>
@@ -83,23 +73,143 @@ __device__ __forceinline__ int wave_sum_last_i(int v) {
 
 __device__ __forceinline__ int8_t clamp_i8(int v, int lo) { return int8_t(v < lo ? lo : v > 127 ? 127 : v); }
 
+// isqrt (src/forward.rs:747-758) is floor(sqrt(v)); for v < 2^24 the hardware square root is
+// within one of it, and one correction step each way makes it exact.
+__device__ __forceinline__ uint32_t floor_sqrt_u24(uint32_t v) {
+  uint32_t r = uint32_t(__builtin_amdgcn_sqrtf(float(v)));
+  if (r * r > v) r--;
+  if ((r + 1) * (r + 1) <= v) r++;
+  return r;
+}
+
 // ForwardExec::rmsnorm (src/forward.rs:672-699) of one 512-byte row held by a wave, 8 bytes per
 // lane: rms = max(isqrt(sum v^2 / 512), 1), y = clamp(v * 48 / rms, -127, 127) (division
-// truncating toward zero).
+// truncating toward zero).  |v * 48| <= 6144 and rms <= 128, so the quotient is the high word of
+// |v * 48| * ceil(2^32 / rms), exact (division by an invariant integer, Granlund & Montgomery
+// 1994: the error term stays below |v * 48| / 2^32 < 1 / rms).
 __device__ __forceinline__ void rmsnorm_lane(uint32_t (&v)[2]) {
   int ss = dot4(v[0], v[0], dot4(v[1], v[1], 0));
   ss = __builtin_amdgcn_readlane(wave_sum_last_i(ss), 63);
-  const int rms = max(int(isqrt_u32(uint32_t(ss) / kFwdDim)), 1);
+  const uint32_t rms = max(floor_sqrt_u24(uint32_t(ss) / kFwdDim), 1u);
+  const uint32_t mul = rms == 1 ? 0u : 0xFFFFFFFFu / rms + 1u;  // ceil(2^32 / rms) for rms > 1
 #pragma unroll
   for (int d = 0; d < 2; d++) {
     uint32_t o = 0;
 #pragma unroll
     for (int b = 0; b < 4; b++) {
-      const int x = int(int8_t(byte_of(v[d], b)));
-      o |= uint32_t(uint8_t(clamp_i8(x * 48 / rms, -127))) << (8 * b);
+      const int x = int(int8_t(byte_of(v[d], b))) * 48;
+      const uint32_t ax = uint32_t(x < 0 ? -x : x);
+      const int q = int(rms == 1 ? ax : __umulhi(ax, mul));
+      o |= uint32_t(uint8_t(clamp_i8(x < 0 ? -q : q, -127))) << (8 * b);
     }
     v[d] = o;
   }
+}
+
+// ForwardExec::attention (src/forward.rs:702-744) for one query row at position npos - 1 over
+// cache rows 0..npos-1, by the 256 threads of a workgroup: w_t = clamp(q . k_t >> 10, 0, 127) + 1,
+// out = sum w_t v_t / sum w_t (int64, truncating).  Positions go in blocks of 64 whose k and v
+// loads are all issued at once (one memory round trip per block): sixteen 16-lane groups score
+// four keys each (32 bytes per lane) into LDS bytes, then eight groups of 32 threads each weigh
+// every eighth value row, 16 columns per thread.  The int32 partials (exact: 128 * 127 * 4096 / 8
+// per group) meet in LDS every kAttChunk positions and carry in int64, two columns per thread.
+struct AttSmem {
+  uint8_t wts[2][64];
+  int part[8][kFwdDim];
+  int tw[8];
+};
+
+__device__ __forceinline__ void attend_row(const int8_t* __restrict__ q, const int8_t* __restrict__ kc,
+                                           const int8_t* __restrict__ vc, int64_t npos, int8_t* __restrict__ out,
+                                           AttSmem& S) {
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6, g = lane >> 4, sub = lane & 15;
+  const uint8_t* qr = reinterpret_cast<const uint8_t*>(q) + sub * 32;
+  const u32x4 q0 = ld4(qr), q1 = ld4(qr + 16);
+  const int grp = t >> 5, c16 = (t & 31) * 16, kj = wv * 4 + g;
+  int64_t acc0 = 0, acc1 = 0, total = 0;
+  int buf = 0;
+  for (int64_t c0 = 0; c0 < npos; c0 += kAttChunk) {
+    const int cn = int(std::min<int64_t>(kAttChunk, npos - c0));
+    const uint8_t* kb = reinterpret_cast<const uint8_t*>(kc) + c0 * kFwdDim + sub * 32;
+    const uint8_t* vb = reinterpret_cast<const uint8_t*>(vc) + c0 * kFwdDim + c16;
+    int a[16] = {}, tw = 0;
+    for (int b0 = 0; b0 < cn; b0 += 64) {
+      u32x4 k[4][2], v[8];  // positions past the pass read its last row, weighted 0
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const uint8_t* kr = kb + int64_t(min(b0 + kj + 16 * u, cn - 1)) * kFwdDim;
+        k[u][0] = ld4(kr), k[u][1] = ld4(kr + 16);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = ld4(vb + int64_t(min(b0 + grp + 8 * i, cn - 1)) * kFwdDim);
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        int sc = 0;
+#pragma unroll
+        for (int d = 0; d < 4; d++) sc = dot4(q0[d], k[u][0][d], dot4(q1[d], k[u][1][d], sc));
+        sc = group_sum_i<16>(sc);
+        const int sh = sc >> 10;
+        if (sub == 0) S.wts[buf][kj + 16 * u] = uint8_t((sh < 0 ? 0 : sh > 127 ? 127 : sh) + 1);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int j = grp + 8 * i;
+        const int w = b0 + j < cn ? int(S.wts[buf][j]) : 0;
+#pragma unroll
+        for (int b = 0; b < 16; b++) a[b] += w * int(int8_t(byte_of(v[i][b >> 2], b & 3)));
+        tw += w;
+      }
+      buf ^= 1;  // the next block's scores go to the other buffer: no second barrier
+    }
+#pragma unroll
+    for (int b = 0; b < 16; b += 4) *reinterpret_cast<int4*>(&S.part[grp][c16 + b]) = int4{a[b], a[b + 1], a[b + 2], a[b + 3]};
+    if ((t & 31) == 0) S.tw[grp] = tw;
+    __syncthreads();
+    int s0 = 0, s1 = 0, st = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int2 pr = *reinterpret_cast<const int2*>(&S.part[i][2 * t]);
+      s0 += pr.x, s1 += pr.y, st += S.tw[i];
+    }
+    acc0 += s0, acc1 += s1, total += st;
+    __syncthreads();
+  }
+  out[2 * t] = int8_t(acc0 / total);
+  out[2 * t + 1] = int8_t(acc1 / total);
+}
+
+// embed (src/forward.rs:918-926) of one token into a 512-byte row by the calling workgroup:
+// fill_small(seed ^ token * 0x9E3779B9) * 8.
+__device__ __forceinline__ void embed_row(uint64_t seed, uint32_t token, int8_t* __restrict__ x) {
+  const uint64_t s = seed ^ (uint64_t(token) * 0x9E3779B9ull);
+  for (int i = threadIdx.x; i < kFwdDim; i += blockDim.x) x[i] = int8_t(small_of(s, uint64_t(i)) * 8);
+}
+
+// ForwardModel::sample (src/forward.rs:978-986) by the calling workgroup of 256 threads: the
+// first index of the largest of logits[0, max(vocab, 1)), returned to every thread.
+__device__ __forceinline__ uint32_t sample_block(const int32_t* __restrict__ logits, int64_t vocab) {
+  __shared__ int sv[256];
+  __shared__ int64_t si[256];
+  const int t = threadIdx.x;
+  const int64_t n = vocab > 1 ? vocab : 1;
+  int bv = INT32_MIN;
+  int64_t bi = -1;
+  for (int64_t i = t; i < n; i += 256) {
+    const int v = logits[i];
+    if (bi < 0 || v > bv) bv = v, bi = i;
+  }
+  sv[t] = bv, si[t] = bi;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (t < off) {
+      const int ov = sv[t + off];
+      const int64_t oi = si[t + off];
+      if (oi >= 0 && (si[t] < 0 || ov > sv[t] || (ov == sv[t] && oi < si[t]))) sv[t] = ov, si[t] = oi;
+    }
+    __syncthreads();
+  }
+  return uint32_t(si[0]);
 }
 
 // Up to three projections of one launch (same shape and shift); blockIdx.y picks one.
@@ -111,45 +221,60 @@ struct MvArgs {
   MvProj p[3];
   const int8_t* x;  // token rows [m][K]
   int m, N, shift;
+  // ATT_IN (m == 1): the input row is the attention of q over the npos cache rows, computed by
+  // every workgroup for itself instead of read from x
+  const int8_t *q, *kc, *vc;
+  int64_t npos;
 };
 
-// out[r][n] = EPI(sum_k x[r][k] w[n][k]) for r < m <= kMvRows: the m token rows (RMSNorm-ed if
-// NORM, K = 512) staged in LDS by the four waves, then one weight row per wave, K / 64 bytes per
-// lane, one DPP reduction per token row; lane 63 writes.
-template <int K, int EPI, bool NORM>
+// out[r][n] = EPI(sum_k x[r][k] w[n][k]) for r < m <= kMvRows: each wave's weight row (K / 64
+// bytes per lane) is loaded first, while the four waves stage the m token rows (RMSNorm-ed if
+// NORM, K = 512) in LDS; then one DPP reduction per token row, lane 63 writes.  ATT_IN (one row,
+// a short context): the workgroup computes the attention row itself into LDS (attend_row), so
+// that attention and the wo projection share one launch; the cache rows it reads are the
+// previous launch's output and small (npos * 1 KiB per workgroup).
+template <int K, int EPI, bool NORM, bool ATT_IN>
 __global__ void __launch_bounds__(kMvWaves * 64) fwd_matvec_kernel(MvArgs a) {
   static_assert(K == kFwdDim || K == kFwdFfn, "row width");
   static_assert(!NORM || K == kFwdDim, "RMSNorm rows are model rows");
+  static_assert(!ATT_IN || (!NORM && K == kFwdDim), "attention rows are model rows");
   constexpr int D = K / 256;  // dwords per lane
   extern __shared__ uint32_t xs[];  // [m][K / 4]
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  for (int r = wv; r < a.m; r += kMvWaves) {
-    uint32_t v[D];
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.x) + int64_t(r) * K + lane * 4 * D;
-    if constexpr (D == 2) {
-      const u32x2 t = ld2(src);
-      v[0] = t[0], v[1] = t[1];
-    } else {
-      const u32x4 t = ld4(src);
-      v[0] = t[0], v[1] = t[1], v[2] = t[2], v[3] = t[3];
-    }
-    if constexpr (NORM) rmsnorm_lane(v);
-#pragma unroll
-    for (int d = 0; d < D; d++) xs[r * (K / 4) + lane * D + d] = v[d];
-  }
-  __syncthreads();
   const int n = blockIdx.x * kMvWaves + wv;
-  if (n >= a.N) return;
   const MvProj p = a.p[blockIdx.y];
   uint32_t w[D];
-  const uint8_t* wr = reinterpret_cast<const uint8_t*>(p.w) + int64_t(n) * K + lane * 4 * D;
-  if constexpr (D == 2) {
-    const u32x2 t = ld2(wr);
-    w[0] = t[0], w[1] = t[1];
-  } else {
-    const u32x4 t = ld4(wr);
-    w[0] = t[0], w[1] = t[1], w[2] = t[2], w[3] = t[3];
+  {
+    const uint8_t* wr = reinterpret_cast<const uint8_t*>(p.w) + int64_t(min(n, a.N - 1)) * K + lane * 4 * D;
+    if constexpr (D == 2) {
+      const u32x2 t = ld2(wr);
+      w[0] = t[0], w[1] = t[1];
+    } else {
+      const u32x4 t = ld4(wr);
+      w[0] = t[0], w[1] = t[1], w[2] = t[2], w[3] = t[3];
+    }
   }
+  if constexpr (ATT_IN) {
+    __shared__ AttSmem S;
+    attend_row(a.q, a.kc, a.vc, a.npos, reinterpret_cast<int8_t*>(xs), S);
+  } else {
+    for (int r = wv; r < a.m; r += kMvWaves) {
+      uint32_t v[D];
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(a.x) + int64_t(r) * K + lane * 4 * D;
+      if constexpr (D == 2) {
+        const u32x2 t = ld2(src);
+        v[0] = t[0], v[1] = t[1];
+      } else {
+        const u32x4 t = ld4(src);
+        v[0] = t[0], v[1] = t[1], v[2] = t[2], v[3] = t[3];
+      }
+      if constexpr (NORM) rmsnorm_lane(v);
+#pragma unroll
+      for (int d = 0; d < D; d++) xs[r * (K / 4) + lane * D + d] = v[d];
+    }
+  }
+  __syncthreads();
+  if (n >= a.N) return;
   for (int r = 0; r < a.m; r++) {
     int acc = 0;
 #pragma unroll
@@ -171,6 +296,16 @@ __global__ void __launch_bounds__(kMvWaves * 64) fwd_matvec_kernel(MvArgs a) {
   }
 }
 
+// The greedy token of the head's logits into *tok (sample_block) and its embedding into x, the
+// next step's input row: one workgroup.
+__global__ void __launch_bounds__(256) fwd_sample_embed_kernel(const int32_t* __restrict__ logits, int64_t vocab,
+                                                               uint32_t* __restrict__ tok, uint64_t seed,
+                                                               int8_t* __restrict__ x) {
+  const uint32_t t = sample_block(logits, vocab);
+  if (threadIdx.x == 0) *tok = t;
+  embed_row(seed, t, x);
+}
+
 // RMSNorm of m rows (the MFMA path's projection input): one wave per row.
 __global__ void __launch_bounds__(64) fwd_rmsnorm_rows_kernel(const int8_t* __restrict__ x, int8_t* __restrict__ out) {
   const int64_t r = blockIdx.x;
@@ -181,61 +316,19 @@ __global__ void __launch_bounds__(64) fwd_rmsnorm_rows_kernel(const int8_t* __re
   *reinterpret_cast<u32x2*>(out + r * kFwdDim + lane * 8) = u32x2{v[0], v[1]};
 }
 
-// ForwardExec::attention (src/forward.rs:702-744) for query row r = blockIdx.x at position
-// start_pos + r over cache rows 0..=start_pos + r: w_t = clamp(q . k_t >> 10, 0, 127) + 1,
-// out = sum w_t v_t / sum w_t (int64, truncating).  Per pass of up to kAttChunk positions the
-// scores come first (16 lanes per key, 32 bytes each, four keys per wave at a time) into LDS
-// bytes, then each thread sums two of the 512 columns over the pass in int32 (exact:
-// 128 * 127 * kAttChunk < 2^31) and carries the passes in int64.
+// Attention of query rows r = blockIdx.x at positions start_pos + r (the prefill's m rows).
 __global__ void __launch_bounds__(256) fwd_attention_kernel(const int8_t* __restrict__ q, const int8_t* __restrict__ kc,
                                                             const int8_t* __restrict__ vc, int64_t start_pos,
                                                             int8_t* __restrict__ out) {
-  __shared__ uint8_t wts[kAttChunk];
-  const int r = blockIdx.x;
-  const int64_t npos = start_pos + r + 1;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = lane >> 4, sub = lane & 15;
-  const uint8_t* qr = reinterpret_cast<const uint8_t*>(q) + int64_t(r) * kFwdDim + sub * 32;
-  const u32x4 q0 = ld4(qr), q1 = ld4(qr + 16);
-  const int c2 = threadIdx.x * 2;
-  int64_t acc0 = 0, acc1 = 0, total = 0;
-  for (int64_t c0 = 0; c0 < npos; c0 += kAttChunk) {
-    const int cn = int(std::min<int64_t>(kAttChunk, npos - c0));
-    for (int j = wv * 4 + g; j < cn; j += 16) {
-      const uint8_t* kr = reinterpret_cast<const uint8_t*>(kc) + (c0 + j) * kFwdDim + sub * 32;
-      const u32x4 k0 = ld4(kr), k1 = ld4(kr + 16);
-      int s = 0;
-#pragma unroll
-      for (int d = 0; d < 4; d++) s = dot4(q0[d], k0[d], dot4(q1[d], k1[d], s));
-      s = group_sum_i<16>(s);
-      if (sub == 0) {
-        const int sh = s >> 10;
-        wts[j] = uint8_t((sh < 0 ? 0 : sh > 127 ? 127 : sh) + 1);
-      }
-    }
-    __syncthreads();
-    int a0 = 0, a1 = 0, tw = 0;
-    const uint8_t* vr = reinterpret_cast<const uint8_t*>(vc) + c0 * kFwdDim + c2;
-#pragma unroll 8
-    for (int j = 0; j < cn; j++) {
-      const int w = wts[j];
-      const uint32_t vv = *reinterpret_cast<const uint16_t*>(vr + int64_t(j) * kFwdDim);
-      a0 += w * int(int8_t(vv & 0xFFu));
-      a1 += w * int(int8_t(vv >> 8));
-      tw += w;
-    }
-    acc0 += a0, acc1 += a1, total += tw;
-    __syncthreads();
-  }
-  out[int64_t(r) * kFwdDim + c2] = int8_t(acc0 / total);
-  out[int64_t(r) * kFwdDim + c2 + 1] = int8_t(acc1 / total);
+  __shared__ AttSmem S;
+  const int64_t r = blockIdx.x;
+  attend_row(q + r * kFwdDim, kc, vc, start_pos + r + 1, out + r * kFwdDim, S);
 }
 
-// embed (src/forward.rs:918-926) of token rows tok[0, m): fill_small(seed ^ token * 0x9E3779B9) * 8.
+// embed of token rows tok[0, m), one workgroup per row.
 __global__ void __launch_bounds__(256) fwd_embed_kernel(uint64_t seed, const uint32_t* __restrict__ tok,
                                                         int8_t* __restrict__ x) {
-  const int64_t r = blockIdx.x;
-  const uint64_t s = seed ^ (uint64_t(tok[r]) * 0x9E3779B9ull);
-  for (int i = threadIdx.x; i < kFwdDim; i += blockDim.x) x[r * kFwdDim + i] = int8_t(small_of(s, uint64_t(i)) * 8);
+  embed_row(seed, tok[blockIdx.x], x + int64_t(blockIdx.x) * kFwdDim);
 }
 
 // Matrix::random (src/forward.rs:364-377): fill_small(seed, n k) then zero padding rows.
@@ -243,33 +336,6 @@ __global__ void __launch_bounds__(256) fwd_fill_kernel(uint64_t seed, int64_t va
                                                        int8_t* __restrict__ w) {
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x)
     w[i] = i < valid ? int8_t(small_of(seed, uint64_t(i))) : int8_t(0);
-}
-
-// ForwardModel::sample (src/forward.rs:978-986): the first index of the largest of logits
-// [0, max(vocab, 1)), written to *tok.
-__global__ void __launch_bounds__(256) fwd_sample_kernel(const int32_t* __restrict__ logits, int64_t vocab,
-                                                         uint32_t* __restrict__ tok) {
-  __shared__ int sv[256];
-  __shared__ int64_t si[256];
-  const int t = threadIdx.x;
-  const int64_t n = vocab > 1 ? vocab : 1;
-  int bv = INT32_MIN;
-  int64_t bi = -1;
-  for (int64_t i = t; i < n; i += 256) {
-    const int v = logits[i];
-    if (bi < 0 || v > bv) bv = v, bi = i;
-  }
-  sv[t] = bv, si[t] = bi;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (t < off) {
-      const int ov = sv[t + off];
-      const int64_t oi = si[t + off];
-      if (oi >= 0 && (si[t] < 0 || ov > sv[t] || (ov == sv[t] && oi < si[t]))) sv[t] = ov, si[t] = oi;
-    }
-    __syncthreads();
-  }
-  if (t == 0) *tok = uint32_t(si[0]);
 }
 
 }  // namespace jero
@@ -316,10 +382,10 @@ int gen_matrix(uint64_t seed, int64_t n, int64_t k, int8_t* dst) {
 }
 
 // m token rows x (m <= kMvRows) through up to three same-shaped projections.
-template <int K, int EPI, bool NORM>
+template <int K, int EPI, bool NORM, bool ATT_IN = false>
 int mv(const MvArgs& a, int n_proj, hipStream_t s) {
   const dim3 grid(unsigned((a.N + kMvWaves - 1) / kMvWaves), unsigned(n_proj));
-  hipLaunchKernelGGL((fwd_matvec_kernel<K, EPI, NORM>), grid, dim3(kMvWaves * 64), size_t(a.m) * K, s, a);
+  hipLaunchKernelGGL((fwd_matvec_kernel<K, EPI, NORM, ATT_IN>), grid, dim3(kMvWaves * 64), size_t(a.m) * K, s, a);
   return check_launch("forward matvec");
 }
 
@@ -332,12 +398,18 @@ MvArgs mv_args(const int8_t* x, int64_t m, int64_t N, int shift) {
   return a;
 }
 
-// ForwardModel::forward (src/forward.rs:930-976) over the m token rows already in f->tokens.
-int forward_rows(jero_forward_model* f, int64_t m, int64_t start_pos, int32_t* logits, hipStream_t s) {
+int embed_tokens(jero_forward_model* f, int64_t m, hipStream_t s) {
+  hipLaunchKernelGGL(fwd_embed_kernel, dim3(unsigned(m)), dim3(256), 0, s, f->seed, f->tokens, f->x);
+  return check_launch("forward embed");
+}
+
+// ForwardModel::forward (src/forward.rs:930-976) over m token rows whose embeddings are in f->x.
+// sample_to: if set, the greedy token goes to *sample_to and its embedding into f->x's first row
+// (the next step's input).
+int forward_rows(jero_forward_model* f, int64_t m, int64_t start_pos, int32_t* logits, uint32_t* sample_to,
+                 hipStream_t s) {
   const int64_t D = kFwdDim;
   int rc;
-  hipLaunchKernelGGL(fwd_embed_kernel, dim3(unsigned(m)), dim3(256), 0, s, f->seed, f->tokens, f->x);
-  if ((rc = check_launch("forward embed"))) return rc;
   const bool small = m <= kMvRows;
   for (int l = 0; l < kFwdLayers; l++) {
     int8_t* const* W = f->w[l];
@@ -357,13 +429,22 @@ int forward_rows(jero_forward_model* f, int64_t m, int64_t start_pos, int32_t* l
           (rc = launch_gemm_i8_epi(kI8OutRequant, f->h, m, D, W[2], D, vdst, 6, s)))
         return rc;
     }
-    hipLaunchKernelGGL(fwd_attention_kernel, dim3(unsigned(m)), dim3(256), 0, s, f->q, f->kc[l], f->vc[l], start_pos,
-                       f->att);
-    if ((rc = check_launch("forward attention"))) return rc;
+    const bool att_in = m == 1 && start_pos < kAttInMax;
+    if (!att_in) {
+      hipLaunchKernelGGL(fwd_attention_kernel, dim3(unsigned(m)), dim3(256), 0, s, f->q, f->kc[l], f->vc[l],
+                         start_pos, f->att);
+      if ((rc = check_launch("forward attention"))) return rc;
+    }
     if (small) {
       MvArgs a = mv_args(f->att, m, D, 6);
       a.p[0] = {W[3], f->x};
-      if ((rc = mv<kFwdDim, kI8OutRequantSatAdd, false>(a, 1, s))) return rc;
+      if (att_in) {
+        a.q = f->q, a.kc = f->kc[l], a.vc = f->vc[l], a.npos = start_pos + 1;
+        rc = mv<kFwdDim, kI8OutRequantSatAdd, false, true>(a, 1, s);
+      } else {
+        rc = mv<kFwdDim, kI8OutRequantSatAdd, false>(a, 1, s);
+      }
+      if (rc) return rc;
       a = mv_args(f->x, m, kFwdFfn, 6);
       a.p[0] = {W[4], f->up};
       if ((rc = mv<kFwdDim, kI8OutRequantRelu, true>(a, 1, s))) return rc;
@@ -381,7 +462,9 @@ int forward_rows(jero_forward_model* f, int64_t m, int64_t start_pos, int32_t* l
   }
   MvArgs a = mv_args(f->x + (m - 1) * D, 1, f->head_rows, 0);
   a.p[0] = {f->head, logits};
-  return mv<kFwdDim, kI8OutI32, true>(a, 1, s);
+  if ((rc = mv<kFwdDim, kI8OutI32, true>(a, 1, s)) || !sample_to) return rc;
+  hipLaunchKernelGGL(fwd_sample_embed_kernel, dim3(1), dim3(256), 0, s, logits, f->vocab, sample_to, f->seed, f->x);
+  return check_launch("forward sample");
 }
 
 int check_model(const jero_forward_model* f, const char* who) {
@@ -489,7 +572,7 @@ extern "C" int jero_hip_forward_model_forward(jero_forward_model* f, const uint3
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if ((rc = check_hip(hipMemcpyAsync(f->tokens, tokens, size_t(m) * sizeof(uint32_t), hipMemcpyHostToDevice, s),
                       "forward tokens")) ||
-      (rc = forward_rows(f, m, start_pos, logits_dev, s)))
+      (rc = embed_tokens(f, m, s)) || (rc = forward_rows(f, m, start_pos, logits_dev, nullptr, s)))
     return rc;
   f->len = start_pos + m;
   return JERO_OK;
@@ -512,29 +595,17 @@ extern "C" int jero_hip_forward_model_evaluate(jero_forward_model* f, const uint
   hipEvent_t ev[3] = {};
   for (int i = 0; i < 3 && !rc; i++) rc = check_hip(hipEventCreate(&ev[i]), "forward_model_evaluate events");
   f->len = 0;
-  // Prefill: the prompt rows, then its sample lands in tokens[0]; decode step i embeds tokens[i-1]
+  // Prefill: the prompt rows, then its sample lands in tokens[0]; decode step i runs tokens[i-1]
   // at position n + i - 1 and samples into tokens[i] (evaluate, src/forward.rs:1016-1038).
   if (!rc) rc = check_hip(hipMemcpyAsync(f->tokens, prompt, size_t(n) * sizeof(uint32_t), hipMemcpyHostToDevice, s),
                           "forward prompt");
   if (!rc) rc = check_hip(hipEventRecord(ev[0], s), "event");
-  if (!rc) rc = forward_rows(f, n, 0, f->logits, s);
-  if (!rc && max_tokens > 0) {
-    hipLaunchKernelGGL(fwd_sample_kernel, dim3(1), dim3(256), 0, s, f->logits, f->vocab, f->tokens);
-    rc = check_launch("forward sample");
-  }
-  if (!rc) rc = check_hip(hipEventRecord(ev[1], s), "event");
+  if (!rc) rc = embed_tokens(f, n, s);
   uint32_t* const toks = f->tokens;
-  for (int64_t i = 1; i < max_tokens && !rc; i++) {
-    // The step's token row is tokens[i - 1]: point the embedding at it through f->tokens.
-    f->tokens = toks + (i - 1);
-    rc = forward_rows(f, 1, n + i - 1, f->logits, s);
-    f->tokens = toks;
-    if (!rc) {
-      hipLaunchKernelGGL(fwd_sample_kernel, dim3(1), dim3(256), 0, s, f->logits, f->vocab, toks + i);
-      rc = check_launch("forward sample");
-    }
-  }
-  f->tokens = toks;
+  if (!rc) rc = forward_rows(f, n, 0, f->logits, max_tokens > 0 ? toks : nullptr, s);
+  if (!rc) rc = check_hip(hipEventRecord(ev[1], s), "event");
+  // step i's input row (the embedding of tokens[i - 1]) was left in f->x by the previous head
+  for (int64_t i = 1; i < max_tokens && !rc; i++) rc = forward_rows(f, 1, n + i - 1, f->logits, toks + i, s);
   if (!rc) rc = check_hip(hipEventRecord(ev[2], s), "event");
   if (!rc && max_tokens > 0)
     rc = check_hip(hipMemcpyAsync(generated, toks, size_t(max_tokens) * sizeof(uint32_t), hipMemcpyDeviceToHost, s),

@@ -113,6 +113,11 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C jero-engine_amd`")
+        # torch first: it loads its HIP runtime into the global namespace, so the library's HIP
+        # calls bind to that same runtime and torch's device pointers and streams are valid in
+        # them (loaded alone first, the library would start a second runtime that then keeps
+        # torch from opening the GPU).
+        import torch  # noqa: F401
         L = C.CDLL(LIB_PATH)
         for name, (res, args) in _SIGS.items():
             fn = getattr(L, name, None)

@@ -20,9 +20,9 @@
 //   wo    : requant, then saturating add into x
 //   up    : RMSNorm prologue, requant, relu
 //   down  : requant, saturating add into x
-// then the head (RMSNorm of the last row, int32 logits) and, in evaluate, one workgroup that
-// samples the next token and writes it and its embedding (the next step's input row) to device
-// memory: the decode loop never waits for the host.  Up to kMvRows rows the projections run on the matvec kernel below
+// then the head (RMSNorm of the last row, int32 logits).  In evaluate, the next step's first launch
+// samples the greedy token from those logits and embeds it in every workgroup's prologue (one
+// workgroup also stores the token and the row): the decode loop never waits for the host.  Up to kMvRows rows the projections run on the matvec kernel below
 // (one weight row per wave, the token rows in LDS); longer prompts run the int8 MFMA GEMM of
 // gemm.hip with the same fused epilogues, after a row RMSNorm kernel.
 #include <algorithm>
@@ -69,6 +69,14 @@ __device__ __forceinline__ int wave_sum_last_i(int v) {
   v = dpp_add_i<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
   v = dpp_add_i<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
   return v;
+}
+
+// Integer sum over each 16-lane DPP row, in every lane of the row.
+__device__ __forceinline__ int row_sum_i(int v) {
+  v = dpp_add_i<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add_i<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add_i<0x124, 0xF>(v);  // row_ror:4
+  return dpp_add_i<0x128, 0xF>(v);  // row_ror:8
 }
 
 __device__ __forceinline__ int8_t clamp_i8(int v, int lo) { return int8_t(v < lo ? lo : v > 127 ? 127 : v); }
@@ -147,7 +155,7 @@ __device__ __forceinline__ void attend_row(const int8_t* __restrict__ q, const i
         int sc = 0;
 #pragma unroll
         for (int d = 0; d < 4; d++) sc = dot4(q0[d], k[u][0][d], dot4(q1[d], k[u][1][d], sc));
-        sc = group_sum_i<16>(sc);
+        sc = row_sum_i(sc);
         const int sh = sc >> 10;
         if (sub == 0) S.wts[buf][kj + 16 * u] = uint8_t((sh < 0 ? 0 : sh > 127 ? 127 : sh) + 1);
       }
@@ -175,8 +183,13 @@ __device__ __forceinline__ void attend_row(const int8_t* __restrict__ q, const i
     acc0 += s0, acc1 += s1, total += st;
     __syncthreads();
   }
-  out[2 * t] = int8_t(acc0 / total);
-  out[2 * t + 1] = int8_t(acc1 / total);
+  if (total <= INT32_MAX && acc0 >= -INT32_MAX && acc0 <= INT32_MAX && acc1 >= -INT32_MAX && acc1 <= INT32_MAX) {
+    out[2 * t] = int8_t(int(acc0) / int(total));  // the same truncating quotient in 32 bits
+    out[2 * t + 1] = int8_t(int(acc1) / int(total));
+  } else {
+    out[2 * t] = int8_t(acc0 / total);
+    out[2 * t + 1] = int8_t(acc1 / total);
+  }
 }
 
 // embed (src/forward.rs:918-926) of one token into a 512-byte row by the calling workgroup:
@@ -186,30 +199,45 @@ __device__ __forceinline__ void embed_row(uint64_t seed, uint32_t token, int8_t*
   for (int i = threadIdx.x; i < kFwdDim; i += blockDim.x) x[i] = int8_t(small_of(s, uint64_t(i)) * 8);
 }
 
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_min_i(int v) {
+  return min(v, __builtin_amdgcn_update_dpp(INT32_MAX, v, CTRL, ROW_MASK, 0xF, false));
+}
+
+// Whole-wave integer max / min with DPP, returned to every lane (read from lane 63).
+__device__ __forceinline__ int wave_max_i(int v) { return wave_max_i32_dpp(v); }
+__device__ __forceinline__ int wave_min_i(int v) {
+  v = dpp_min_i<0xB1, 0xF>(v);
+  v = dpp_min_i<0x4E, 0xF>(v);
+  v = dpp_min_i<0x124, 0xF>(v);
+  v = dpp_min_i<0x128, 0xF>(v);
+  v = dpp_min_i<0x142, 0xA>(v);
+  v = dpp_min_i<0x143, 0xC>(v);
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
 // ForwardModel::sample (src/forward.rs:978-986) by the calling workgroup of 256 threads: the
-// first index of the largest of logits[0, max(vocab, 1)), returned to every thread.
+// first index of the largest of logits[0, max(vocab, 1)), returned to every thread.  Each thread
+// keeps the first maximum of its strided share; per wave the largest value, then the smallest
+// index holding it; the four waves meet in LDS.
 __device__ __forceinline__ uint32_t sample_block(const int32_t* __restrict__ logits, int64_t vocab) {
-  __shared__ int sv[256];
-  __shared__ int64_t si[256];
-  const int t = threadIdx.x;
-  const int64_t n = vocab > 1 ? vocab : 1;
-  int bv = INT32_MIN;
-  int64_t bi = -1;
-  for (int64_t i = t; i < n; i += 256) {
+  __shared__ int sv[kMvWaves], si[kMvWaves];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int n = int(vocab > 1 ? vocab : 1);
+  int bv = INT32_MIN, bi = INT32_MAX;
+  for (int i = t; i < n; i += 256) {
     const int v = logits[i];
-    if (bi < 0 || v > bv) bv = v, bi = i;
+    if (bi == INT32_MAX || v > bv) bv = v, bi = i;
   }
-  sv[t] = bv, si[t] = bi;
+  const int wmax = wave_max_i(bi == INT32_MAX ? INT32_MIN : bv);
+  const int widx = wave_min_i(bi != INT32_MAX && bv == wmax ? bi : INT32_MAX);
+  if (lane == 0) sv[wv] = wmax, si[wv] = widx;
   __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (t < off) {
-      const int ov = sv[t + off];
-      const int64_t oi = si[t + off];
-      if (oi >= 0 && (si[t] < 0 || ov > sv[t] || (ov == sv[t] && oi < si[t]))) sv[t] = ov, si[t] = oi;
-    }
-    __syncthreads();
-  }
-  return uint32_t(si[0]);
+  int v = sv[0], idx = si[0];
+#pragma unroll
+  for (int w = 1; w < kMvWaves; w++)
+    if (si[w] != INT32_MAX && (idx == INT32_MAX || sv[w] > v || (sv[w] == v && si[w] < idx))) v = sv[w], idx = si[w];
+  return uint32_t(idx);
 }
 
 // Up to three projections of one launch (same shape and shift); blockIdx.y picks one.
@@ -217,46 +245,72 @@ struct MvProj {
   const int8_t* w;
   void* out;
 };
+// Where the matvec's input rows come from.
+enum { kInRows = 0, kInAttention = 1, kInSample = 2 };
 struct MvArgs {
   MvProj p[3];
-  const int8_t* x;  // token rows [m][K]
+  const int8_t* x;  // kInRows: token rows [m][K]; kInSample: where workgroup (0, 0) stores the row
   int m, N, shift;
-  // ATT_IN (m == 1): the input row is the attention of q over the npos cache rows, computed by
-  // every workgroup for itself instead of read from x
+  // kInAttention (m == 1): the attention of q over the npos cache rows, computed by every
+  // workgroup for itself
   const int8_t *q, *kc, *vc;
   int64_t npos;
+  // kInSample (m == 1): the embedding of the greedy token of the previous step's logits, computed
+  // by every workgroup for itself; workgroup (0, 0) also stores the token at *tok and the row at x
+  const int32_t* logits;
+  int64_t vocab;
+  uint32_t* tok;
+  uint64_t seed;
 };
 
-// out[r][n] = EPI(sum_k x[r][k] w[n][k]) for r < m <= kMvRows: each wave's weight row (K / 64
-// bytes per lane) is loaded first, while the four waves stage the m token rows (RMSNorm-ed if
-// NORM, K = 512) in LDS; then one DPP reduction per token row, lane 63 writes.  ATT_IN (one row,
-// a short context): the workgroup computes the attention row itself into LDS (attend_row), so
-// that attention and the wo projection share one launch; the cache rows it reads are the
-// previous launch's output and small (npos * 1 KiB per workgroup).
-template <int K, int EPI, bool NORM, bool ATT_IN>
+// out[r][n] = EPI(sum_k x[r][k] w[n][k]) for r < m <= kMvRows: each wave's R weight rows (K / 64
+// bytes per lane each) are loaded first, while the input rows are staged in LDS (RMSNorm-ed if
+// NORM, K = 512); then one DPP reduction per (weight row, token row), lane 63 writes.  The
+// one-row inputs kInAttention and kInSample are computed by each workgroup itself, so that
+// attention shares the wo launch and the sample the next step's first launch; every workgroup
+// repeats that small step (npos KiB of cache reads, or the scan of the logits) instead of a
+// launch boundary and a round trip through memory.
+template <int K, int EPI, bool NORM, int IN, int R>
 __global__ void __launch_bounds__(kMvWaves * 64) fwd_matvec_kernel(MvArgs a) {
   static_assert(K == kFwdDim || K == kFwdFfn, "row width");
   static_assert(!NORM || K == kFwdDim, "RMSNorm rows are model rows");
-  static_assert(!ATT_IN || (!NORM && K == kFwdDim), "attention rows are model rows");
+  static_assert(IN != kInAttention || (!NORM && K == kFwdDim), "attention rows are model rows");
+  static_assert(IN != kInSample || (NORM && K == kFwdDim), "the sampled row feeds a normed projection");
   constexpr int D = K / 256;  // dwords per lane
   extern __shared__ uint32_t xs[];  // [m][K / 4]
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int n = blockIdx.x * kMvWaves + wv;
+  const int n0 = (blockIdx.x * kMvWaves + wv) * R;
   const MvProj p = a.p[blockIdx.y];
-  uint32_t w[D];
-  {
-    const uint8_t* wr = reinterpret_cast<const uint8_t*>(p.w) + int64_t(min(n, a.N - 1)) * K + lane * 4 * D;
+  uint32_t w[R][D];
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const uint8_t* wr = reinterpret_cast<const uint8_t*>(p.w) + int64_t(min(n0 + i, a.N - 1)) * K + lane * 4 * D;
     if constexpr (D == 2) {
       const u32x2 t = ld2(wr);
-      w[0] = t[0], w[1] = t[1];
+      w[i][0] = t[0], w[i][1] = t[1];
     } else {
       const u32x4 t = ld4(wr);
-      w[0] = t[0], w[1] = t[1], w[2] = t[2], w[3] = t[3];
+      w[i][0] = t[0], w[i][1] = t[1], w[i][2] = t[2], w[i][3] = t[3];
     }
   }
-  if constexpr (ATT_IN) {
+  if constexpr (IN == kInAttention) {
     __shared__ AttSmem S;
     attend_row(a.q, a.kc, a.vc, a.npos, reinterpret_cast<int8_t*>(xs), S);
+  } else if constexpr (IN == kInSample) {
+    const uint32_t tok = sample_block(a.logits, a.vocab);
+    if (wv == 0) {
+      const uint64_t sd = a.seed ^ (uint64_t(tok) * 0x9E3779B9ull);
+      uint32_t v[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        v[e >> 2] |= uint32_t(uint8_t(int8_t(small_of(sd, uint64_t(lane * 8 + e)) * 8))) << (8 * (e & 3));
+      if (blockIdx.x == 0 && blockIdx.y == 0) {
+        *reinterpret_cast<u32x2*>(const_cast<int8_t*>(a.x) + lane * 8) = u32x2{v[0], v[1]};
+        if (lane == 0) *a.tok = tok;
+      }
+      rmsnorm_lane(v);
+      xs[lane * 2] = v[0], xs[lane * 2 + 1] = v[1];
+    }
   } else {
     for (int r = wv; r < a.m; r += kMvWaves) {
       uint32_t v[D];
@@ -274,36 +328,37 @@ __global__ void __launch_bounds__(kMvWaves * 64) fwd_matvec_kernel(MvArgs a) {
     }
   }
   __syncthreads();
-  if (n >= a.N) return;
-  for (int r = 0; r < a.m; r++) {
-    int acc = 0;
 #pragma unroll
-    for (int d = 0; d < D; d++) acc = dot4(w[d], xs[r * (K / 4) + lane * D + d], acc);
-    acc = wave_sum_last_i(acc);
-    if (lane == 63) {
-      const int64_t o = int64_t(r) * a.N + n;
-      if constexpr (EPI == kI8OutI32) {
-        static_cast<int32_t*>(p.out)[o] = acc;
-      } else {
-        const int q = int(int32_t(uint32_t(acc) + (uint32_t(1) << (a.shift - 1))) >> a.shift);
-        const int8_t rq = clamp_i8(q, -127);
-        int8_t* dst = static_cast<int8_t*>(p.out) + o;
-        if constexpr (EPI == kI8OutRequant) *dst = rq;
-        else if constexpr (EPI == kI8OutRequantRelu) *dst = rq < 0 ? int8_t(0) : rq;
-        else *dst = clamp_i8(int(*dst) + int(rq), -128);
+  for (int i = 0; i < R; i++) {
+    const int n = n0 + i;
+    if (n >= a.N) return;
+    for (int r = 0; r < a.m; r++) {
+      int acc = 0;
+#pragma unroll
+      for (int d = 0; d < D; d++) acc = dot4(w[i][d], xs[r * (K / 4) + lane * D + d], acc);
+      acc = wave_sum_last_i(acc);
+      if (lane == 63) {
+        const int64_t o = int64_t(r) * a.N + n;
+        if constexpr (EPI == kI8OutI32) {
+          static_cast<int32_t*>(p.out)[o] = acc;
+        } else {
+          const int q = int(int32_t(uint32_t(acc) + (uint32_t(1) << (a.shift - 1))) >> a.shift);
+          const int8_t rq = clamp_i8(q, -127);
+          int8_t* dst = static_cast<int8_t*>(p.out) + o;
+          if constexpr (EPI == kI8OutRequant) *dst = rq;
+          else if constexpr (EPI == kI8OutRequantRelu) *dst = rq < 0 ? int8_t(0) : rq;
+          else *dst = clamp_i8(int(*dst) + int(rq), -128);
+        }
       }
     }
   }
 }
 
-// The greedy token of the head's logits into *tok (sample_block) and its embedding into x, the
-// next step's input row: one workgroup.
-__global__ void __launch_bounds__(256) fwd_sample_embed_kernel(const int32_t* __restrict__ logits, int64_t vocab,
-                                                               uint32_t* __restrict__ tok, uint64_t seed,
-                                                               int8_t* __restrict__ x) {
+// The greedy token of the head's logits into *tok (sample_block): one workgroup.
+__global__ void __launch_bounds__(256) fwd_sample_kernel(const int32_t* __restrict__ logits, int64_t vocab,
+                                                         uint32_t* __restrict__ tok) {
   const uint32_t t = sample_block(logits, vocab);
   if (threadIdx.x == 0) *tok = t;
-  embed_row(seed, t, x);
 }
 
 // RMSNorm of m rows (the MFMA path's projection input): one wave per row.
@@ -354,6 +409,10 @@ struct jero_forward_model {
   int32_t* logits = nullptr;                                                        // [head_rows]
   uint32_t* tokens = nullptr;  // [cap]: the call's token rows, or evaluate's generated tokens
   std::vector<void*> owned;
+  // evaluate's decode steps as a HIP graph for one (prompt length, max_tokens), replayed on gs
+  hipStream_t gs = nullptr;
+  hipGraphExec_t graph = nullptr;
+  int64_t graph_n = -1, graph_max = -1;
 };
 
 namespace {
@@ -370,6 +429,8 @@ int fwd_alloc(jero_forward_model* f, size_t bytes, void** p) {
 }
 
 void fwd_release(jero_forward_model* f) {
+  if (f->graph) (void)hipGraphExecDestroy(f->graph);
+  if (f->gs) (void)hipStreamDestroy(f->gs);
   for (void* p : f->owned) (void)hipFree(p);
   delete f;
 }
@@ -381,11 +442,12 @@ int gen_matrix(uint64_t seed, int64_t n, int64_t k, int8_t* dst) {
   return check_launch("forward_model weights");
 }
 
-// m token rows x (m <= kMvRows) through up to three same-shaped projections.
-template <int K, int EPI, bool NORM, bool ATT_IN = false>
+// m token rows (m <= kMvRows) through up to three same-shaped projections, R weight rows a wave.
+template <int K, int EPI, bool NORM, int IN = kInRows, int R = 1>
 int mv(const MvArgs& a, int n_proj, hipStream_t s) {
-  const dim3 grid(unsigned((a.N + kMvWaves - 1) / kMvWaves), unsigned(n_proj));
-  hipLaunchKernelGGL((fwd_matvec_kernel<K, EPI, NORM, ATT_IN>), grid, dim3(kMvWaves * 64), size_t(a.m) * K, s, a);
+  const int per_wg = kMvWaves * R;
+  const dim3 grid(unsigned((a.N + per_wg - 1) / per_wg), unsigned(n_proj));
+  hipLaunchKernelGGL((fwd_matvec_kernel<K, EPI, NORM, IN, R>), grid, dim3(kMvWaves * 64), size_t(a.m) * K, s, a);
   return check_launch("forward matvec");
 }
 
@@ -403,10 +465,10 @@ int embed_tokens(jero_forward_model* f, int64_t m, hipStream_t s) {
   return check_launch("forward embed");
 }
 
-// ForwardModel::forward (src/forward.rs:930-976) over m token rows whose embeddings are in f->x.
-// sample_to: if set, the greedy token goes to *sample_to and its embedding into f->x's first row
-// (the next step's input).
-int forward_rows(jero_forward_model* f, int64_t m, int64_t start_pos, int32_t* logits, uint32_t* sample_to,
+// ForwardModel::forward (src/forward.rs:930-976) over m token rows whose embeddings are in f->x,
+// or, with sampled set (m == 1), over the greedy token of the previous step's logits in f->logits
+// (ForwardModel::sample, src/forward.rs:978-986), which goes to *sampled and its embedding to f->x.
+int forward_rows(jero_forward_model* f, int64_t m, int64_t start_pos, int32_t* logits, uint32_t* sampled,
                  hipStream_t s) {
   const int64_t D = kFwdDim;
   int rc;
@@ -420,7 +482,13 @@ int forward_rows(jero_forward_model* f, int64_t m, int64_t start_pos, int32_t* l
       a.p[0] = {W[0], f->q};
       a.p[1] = {W[1], kdst};
       a.p[2] = {W[2], vdst};
-      if ((rc = mv<kFwdDim, kI8OutRequant, true>(a, 3, s))) return rc;
+      if (l == 0 && sampled) {
+        a.logits = f->logits, a.vocab = f->vocab, a.tok = sampled, a.seed = f->seed;
+        rc = mv<kFwdDim, kI8OutRequant, true, kInSample>(a, 3, s);
+      } else {
+        rc = mv<kFwdDim, kI8OutRequant, true>(a, 3, s);
+      }
+      if (rc) return rc;
     } else {
       hipLaunchKernelGGL(fwd_rmsnorm_rows_kernel, dim3(unsigned(m)), dim3(64), 0, s, f->x, f->h);
       if ((rc = check_launch("forward rmsnorm")) ||
@@ -440,7 +508,7 @@ int forward_rows(jero_forward_model* f, int64_t m, int64_t start_pos, int32_t* l
       a.p[0] = {W[3], f->x};
       if (att_in) {
         a.q = f->q, a.kc = f->kc[l], a.vc = f->vc[l], a.npos = start_pos + 1;
-        rc = mv<kFwdDim, kI8OutRequantSatAdd, false, true>(a, 1, s);
+        rc = mv<kFwdDim, kI8OutRequantSatAdd, false, kInAttention>(a, 1, s);
       } else {
         rc = mv<kFwdDim, kI8OutRequantSatAdd, false>(a, 1, s);
       }
@@ -462,9 +530,37 @@ int forward_rows(jero_forward_model* f, int64_t m, int64_t start_pos, int32_t* l
   }
   MvArgs a = mv_args(f->x + (m - 1) * D, 1, f->head_rows, 0);
   a.p[0] = {f->head, logits};
-  if ((rc = mv<kFwdDim, kI8OutI32, true>(a, 1, s)) || !sample_to) return rc;
-  hipLaunchKernelGGL(fwd_sample_embed_kernel, dim3(1), dim3(256), 0, s, logits, f->vocab, sample_to, f->seed, f->x);
-  return check_launch("forward sample");
+  return mv<kFwdDim, kI8OutI32, true>(a, 1, s);
+}
+
+// Records evaluate's decode steps for a prompt of n tokens and max_tokens >= 1 generated ones into
+// f->graph: step i (1 <= i < max_tokens) samples tokens[i - 1] from the previous logits in its
+// first launch and runs it at position n + i - 1; then the last sample into tokens[max_tokens - 1].
+int capture_decode(jero_forward_model* f, int64_t n, int64_t max_tokens) {
+  if (f->graph) {
+    (void)hipGraphExecDestroy(f->graph);
+    f->graph = nullptr;
+  }
+  f->graph_n = f->graph_max = -1;
+  int rc = check_hip(hipStreamBeginCapture(f->gs, hipStreamCaptureModeThreadLocal), "forward capture");
+  if (rc) return rc;
+  uint32_t* const toks = f->tokens;
+  for (int64_t i = 1; i < max_tokens && !rc; i++) rc = forward_rows(f, 1, n + i - 1, f->logits, toks + i - 1, f->gs);
+  if (!rc) {
+    hipLaunchKernelGGL(fwd_sample_kernel, dim3(1), dim3(256), 0, f->gs, f->logits, f->vocab, toks + max_tokens - 1);
+    rc = check_launch("forward sample");
+  }
+  hipGraph_t g = nullptr;
+  const int rc_end = check_hip(hipStreamEndCapture(f->gs, &g), "forward capture end");
+  if (!rc) rc = rc_end;
+  if (!rc) rc = check_hip(hipGraphInstantiate(&f->graph, g, nullptr, nullptr, 0), "forward graph instantiate");
+  if (g) (void)hipGraphDestroy(g);
+  if (rc) {
+    f->graph = nullptr;
+    return rc;
+  }
+  f->graph_n = n, f->graph_max = max_tokens;
+  return JERO_OK;
 }
 
 int check_model(const jero_forward_model* f, const char* who) {
@@ -602,15 +698,22 @@ extern "C" int jero_hip_forward_model_evaluate(jero_forward_model* f, const uint
   if (!rc) rc = check_hip(hipEventRecord(ev[0], s), "event");
   if (!rc) rc = embed_tokens(f, n, s);
   uint32_t* const toks = f->tokens;
-  if (!rc) rc = forward_rows(f, n, 0, f->logits, max_tokens > 0 ? toks : nullptr, s);
+  if (!rc) rc = forward_rows(f, n, 0, f->logits, nullptr, s);
   if (!rc) rc = check_hip(hipEventRecord(ev[1], s), "event");
-  // step i's input row (the embedding of tokens[i - 1]) was left in f->x by the previous head
-  for (int64_t i = 1; i < max_tokens && !rc; i++) rc = forward_rows(f, 1, n + i - 1, f->logits, toks + i, s);
-  if (!rc) rc = check_hip(hipEventRecord(ev[2], s), "event");
+  // The decode steps run as one graph on the model's stream gs, after the prefill: the steps are
+  // the same launches for every evaluate of this (n, max_tokens), so they are captured once and
+  // replayed (the host then enqueues one graph instead of ~17 launches per token).
+  if (!rc && !f->gs) rc = check_hip(hipStreamCreateWithFlags(&f->gs, hipStreamNonBlocking), "forward stream");
+  if (!rc) rc = check_hip(hipStreamWaitEvent(f->gs, ev[1], 0), "forward stream order");
+  if (!rc && max_tokens > 0 && (f->graph_n != n || f->graph_max != max_tokens || !f->graph))
+    rc = capture_decode(f, n, max_tokens);
+  if (!rc && max_tokens > 0) rc = check_hip(hipGraphLaunch(f->graph, f->gs), "forward decode graph");
+  if (!rc) rc = check_hip(hipEventRecord(ev[2], f->gs), "event");
   if (!rc && max_tokens > 0)
-    rc = check_hip(hipMemcpyAsync(generated, toks, size_t(max_tokens) * sizeof(uint32_t), hipMemcpyDeviceToHost, s),
+    rc = check_hip(hipMemcpyAsync(generated, toks, size_t(max_tokens) * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                  f->gs),
                    "forward generated");
-  if (!rc) rc = check_hip(hipStreamSynchronize(s), "forward_model_evaluate");
+  if (!rc) rc = check_hip(hipStreamSynchronize(f->gs), "forward_model_evaluate");
   if (!rc && timing_ms) {
     rc = check_hip(hipEventElapsedTime(&timing_ms[0], ev[0], ev[1]), "event time");
     if (!rc) rc = check_hip(hipEventElapsedTime(&timing_ms[1], ev[1], ev[2]), "event time");

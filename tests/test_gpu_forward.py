@@ -104,8 +104,14 @@ def test_evaluate_matrix_bench_workload(dev):
     assert toks == O.ForwardModel(SEED, 256, 64).evaluate(PROMPT, 53)
     assert pre_ms > 0 and dec_ms > 0
     assert g.positions == len(PROMPT) + 52
-    # a second evaluate starts from an empty cache and repeats itself
+    # a second evaluate starts from an empty cache and repeats itself (the decode steps replay the
+    # graph recorded by the first); another shape records a new one, and the first comes back
     assert g.evaluate(PROMPT, 53) == toks
+    short = O.ForwardModel(SEED, 256, 64).evaluate(PROMPT[:5], 20)
+    assert g.evaluate(PROMPT[:5], 20) == short
+    assert g.evaluate(PROMPT[:5], 20) == short
+    assert g.evaluate(PROMPT, 53) == toks
+    assert g.evaluate(PROMPT, 1) == toks[:1]
     assert g.evaluate(PROMPT, 0) == [] and g.positions == len(PROMPT)
     g.close()
 

@@ -59,6 +59,25 @@ def test_isqrt_is_floor_sqrt():
         assert O.isqrt(v) == math.isqrt(v)
 
 
+def test_device_integer_shortcuts_are_exact():
+    """The device RMSNorm replaces isqrt's Newton loop and the per-element division by cheaper
+    exact forms; both claims are checked here over their whole domain."""
+    # floor(sqrt(v)) from any root within one of it, by one correction each way, over the mean
+    # squares a row can have (v <= 128^2) and well beyond
+    v = np.arange(0, 1 << 20, dtype=np.int64)
+    root = np.array([math.isqrt(int(x)) for x in v], np.int64)
+    for off in (-1, 0, 1):
+        r = np.maximum(root + off, 0)
+        r = np.where(r * r > v, r - 1, r)
+        r = np.where((r + 1) * (r + 1) <= v, r + 1, r)
+        assert (r == root).all(), off
+    # |a| / d for |a| <= 6144 = 128 * 48 and 2 <= d <= 128: the high word of |a| * ceil(2^32 / d)
+    a = np.arange(0, 6145, dtype=np.uint64)
+    for d in range(2, 129):
+        mul = np.uint64(0xFFFFFFFF // d + 1)
+        assert ((a * mul) >> np.uint64(32) == a // np.uint64(d)).all(), d
+
+
 # ---------------------------------------------------------------- rmsnorm
 
 def test_rmsnorm_closed_forms():

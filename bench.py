@@ -219,7 +219,8 @@ def bench_decode(torch, J, dev, stream, steps, warmup, keep_host):
     t_tok = s0.elapsed_time(e0) / 1e3 / steps
     tok, pos = m.read_token_pos()
     # prefill (extra): a 512-token prompt from position 0 through jero_hip_model_prefill, every
-    # projection a GEMM over the 512 rows; one warm call allocates the row buffers
+    # projection a GEMM over the 512 rows; one warm call allocates the row buffers and builds the
+    # int8 planes of the Q6_K tensors
     import numpy as np
     n_pf = 512
     prompt = np.random.default_rng(5).integers(0, spec["vocab"], n_pf).tolist()

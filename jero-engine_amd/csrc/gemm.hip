@@ -412,6 +412,225 @@ __global__ void __launch_bounds__(256) pack_tiles_kernel(const int8_t* __restric
   dst[o] = r < rows ? src[r * K + int64_t(kc) * kTileK + kk] : int8_t(0);
 }
 
+// ---------------------------------------------------------------- Q6_K x Q8_K on int8 MFMA
+
+int gemm_tiles(int64_t M, int64_t N);
+
+// A Q6_K weight is d * sc * (q6 - 32) with the sub-block scale sc an int8 and q6 in 0..63, so
+// w = sc * (q6 - 32) is an exact integer in [-4064, 4096]: w = 128 hi + lo with hi in [-32, 32]
+// and lo in [-64, 63] gives two int8 planes whose int8 products sum exactly (per 256-block
+// |sum hi q8| < 2^21, |sum lo q8| < 2^22, and 128 |sum hi q8| + |sum lo q8| < 2^31).  The planes are built once from the tensor (GGUF
+// Q6_K or the JERO_Q6_K_R device layout): hi [N][K] int8, lo [N][K] int8, then d [N][K / 256] f32.
+size_t q6k_planes_bytes(int64_t n_in, int64_t n_out) {
+  return size_t(2 * n_out * n_in) + size_t(4 * n_out * (n_in / 256));
+}
+
+// Byte `off` (0..209, GGUF block order: ql[128] qh[64] scales[16] d) of block (r, b).
+__device__ __forceinline__ uint8_t q6k_byte(const uint8_t* __restrict__ p, bool planar, int64_t N, int nb, int64_t r,
+                                            int b, int off) {
+  if (!planar) return p[(r * nb + b) * 210 + off];
+  const int U = 4 * nb;
+  const int64_t plane = N * int64_t(U) * 16;
+  const int64_t u0 = r * U + 4 * b;
+  if (off < 128) {  // ql: lo plane (bytes 0..31 of each 64), hi plane (32..63)
+    const int n = off >> 6, rem = off & 63, which = rem >> 5, j = (rem >> 4) & 1, i = rem & 15;
+    return p[which * plane + (u0 + 2 * n + j) * 16 + i];
+  }
+  if (off < 192) {  // qh
+    const int o = off - 128, n = o >> 5, j = (o >> 4) & 1, i = o & 15;
+    return p[2 * plane + (u0 + 2 * n + j) * 16 + i];
+  }
+  if (off < 208) {  // scales: byte 8 n + j + 2 k -> unit 2 n + j, byte k
+    const int o = off - 192, n = o >> 3, j = o & 1, k = (o & 7) >> 1;
+    return p[3 * plane + (u0 + 2 * n + j) * 4 + k];
+  }
+  return p[3 * plane + N * int64_t(U) * 4 + (r * nb + b) * 2 + (off - 208)];
+}
+
+// One thread per 4 consecutive weights of a block: w = sc * (q6 - 32) split into the planes (the
+// ggml Q6_K element order: element e of the block is pair half n = e / 128, l = e % 32, quarter
+// (e % 128) / 32: low or high nibble of ql[64 n + l (+ 32 for odd quarters)], 2 bits of
+// qh[32 n + l] at 2 * quarter, scale 8 n + l / 16 + 2 * quarter).
+__global__ void __launch_bounds__(256) q6k_planes_kernel(const uint8_t* __restrict__ src, int planar, int64_t N,
+                                                         int nb, int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                         float* __restrict__ dout) {
+  const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= N * nb * 64) return;
+  const int g = int(t & 63);
+  const int64_t rb = t >> 6, r = rb / nb;
+  const int b = int(rb % nb);
+  const int e0 = 4 * g, n = e0 >> 7, quarter = (e0 & 127) >> 5;
+  const int sc = int(int8_t(q6k_byte(src, planar, N, nb, r, b, 192 + 8 * n + (e0 & 31) / 16 + 2 * quarter)));
+  uint32_t ph = 0, pl = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int l = (e0 + k) & 31;
+    const uint32_t qlb = q6k_byte(src, planar, N, nb, r, b, 64 * n + l + (quarter & 1) * 32);
+    const uint32_t qhb = q6k_byte(src, planar, N, nb, r, b, 128 + 32 * n + l);
+    const int q6 = int(((quarter >= 2 ? qlb >> 4 : qlb) & 15u) | (((qhb >> (2 * quarter)) & 3u) << 4));
+    const int w = sc * (q6 - 32);
+    const int h = (w + 64) >> 7;
+    ph |= uint32_t(uint8_t(int8_t(h))) << (8 * k);
+    pl |= uint32_t(uint8_t(int8_t(w - 128 * h))) << (8 * k);
+  }
+  const int64_t K = int64_t(nb) * 256;
+  *reinterpret_cast<uint32_t*>(hi + r * K + int64_t(b) * 256 + e0) = ph;
+  *reinterpret_cast<uint32_t*>(lo + r * K + int64_t(b) * 256 + e0) = pl;
+  if (g == 0) {
+    const uint32_t dbits = uint32_t(q6k_byte(src, planar, N, nb, r, b, 208)) |
+                           (uint32_t(q6k_byte(src, planar, N, nb, r, b, 209)) << 8);
+    dout[r * nb + b] = float(__builtin_bit_cast(_Float16, uint16_t(dbits)));
+  }
+}
+
+struct __attribute__((aligned(16))) Q6pStage {
+  int8_t a[kGemmBM][kPlaneStride];  // q8 of the activation block
+  int8_t h[kGemmBN][kPlaneStride];  // hi plane of the weight block
+  int8_t l[kGemmBN][kPlaneStride];  // lo plane
+  float dx[kGemmBM];
+  float dw[kGemmBN];
+};
+
+// The block's registers of one thread: half of an activation row and of each plane's row.
+struct Q6pRegs {
+  u32x4 a[8], h[8], l[8];
+  float d;
+};
+
+__device__ __forceinline__ void q6p_load(Q6pRegs& R, const uint8_t* __restrict__ xq, int64_t xrb, int m0, int M,
+                                         const int8_t* __restrict__ hi, const int8_t* __restrict__ lo,
+                                         const float* __restrict__ dw, int n0, int N, int nb, int b) {
+  const int t = threadIdx.x, r = t >> 1, half = t & 1;
+  const int m = min(m0 + r, M - 1), n = min(n0 + r, N - 1);
+  const uint8_t* xa = xq + int64_t(m) * xrb + int64_t(b) * 292;
+  const int64_t woff = int64_t(n) * nb * 256 + int64_t(b) * 256 + 128 * half;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    R.a[i] = ld4(xa + 4 + 128 * half + 16 * i);
+    R.h[i] = ld4(reinterpret_cast<const uint8_t*>(hi + woff) + 16 * i);
+    R.l[i] = ld4(reinterpret_cast<const uint8_t*>(lo + woff) + 16 * i);
+  }
+  R.d = half == 0 ? __uint_as_float(ld1(xa)) : dw[int64_t(n) * nb + b];
+}
+
+__device__ __forceinline__ void q6p_store(const Q6pRegs& R, Q6pStage& S) {
+  const int t = threadIdx.x, r = t >> 1, half = t & 1;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    *reinterpret_cast<u32x4*>(&S.a[r][128 * half + 16 * i]) = R.a[i];
+    *reinterpret_cast<u32x4*>(&S.h[r][128 * half + 16 * i]) = R.h[i];
+    *reinterpret_cast<u32x4*>(&S.l[r][128 * half + 16 * i]) = R.l[i];
+  }
+  if (half == 0) S.dx[r] = R.d;
+  else S.dw[r] = R.d;
+}
+
+// Y[m][n] = sum_b dx[m, b] d[n, b] (128 (hi . q8) + lo . q8) over the 256-blocks b: the same
+// 128 x 128 tile, four waves and 32 x 32 x 32 int8 MFMAs as the int8 product, two planes per
+// K step; per block the two int32 sums meet exactly and are scaled into an f32 accumulator.
+// The next block's loads are in flight while the current one runs from LDS.
+__global__ void __launch_bounds__(kGemmThreads) gemm_q6k_planes_kernel(const uint8_t* __restrict__ xq, int64_t xrb,
+                                                                        const int8_t* __restrict__ hi,
+                                                                        const int8_t* __restrict__ lo,
+                                                                        const float* __restrict__ dw, int M, int N,
+                                                                        int nb, float* __restrict__ y) {
+  __shared__ Q6pStage S;
+  const int n_tiles_m = (M + kGemmBM - 1) / kGemmBM;
+  int tm, tn;
+  gemm_tile_of(blockIdx.x, gridDim.x, n_tiles_m, tm, tn);
+  const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+  v16i Ch[2][2], Cl[2][2];
+  float F[2][2][16];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) Ch[i][k][v] = 0, Cl[i][k][v] = 0, F[i][k][v] = 0.f;
+  Q6pRegs R;
+  q6p_load(R, xq, xrb, m0, M, hi, lo, dw, n0, N, nb, 0);
+  q6p_store(R, S);
+  __syncthreads();
+  for (int b = 0; b < nb; b++) {
+    const bool more = b + 1 < nb;
+    if (more) q6p_load(R, xq, xrb, m0, M, hi, lo, dw, n0, N, nb, b + 1);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      v4i af[2], bh[2], bl[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        af[i] = *reinterpret_cast<const v4i*>(&S.a[64 * wm + 32 * i + lr][32 * j + 16 * lh]);
+        bh[i] = *reinterpret_cast<const v4i*>(&S.h[64 * wn + 32 * i + lr][32 * j + 16 * lh]);
+        bl[i] = *reinterpret_cast<const v4i*>(&S.l[64 * wn + 32 * i + lr][32 * j + 16 * lh]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+          Ch[i][k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bh[k], Ch[i][k], 0, 0, 0);
+          Cl[i][k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bl[k], Cl[i][k], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const float dn = S.dw[64 * wn + 32 * k + lr];
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int ml = 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
+          const int tsum = Ch[i][k][v] * 128 + Cl[i][k][v];
+          F[i][k][v] = fmaf(float(tsum) * S.dx[ml], dn, F[i][k][v]);
+          Ch[i][k][v] = 0, Cl[i][k][v] = 0;
+        }
+      }
+    __syncthreads();
+    if (more) {
+      q6p_store(R, S);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int n = n0 + 64 * wn + 32 * k + lr;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int m = m0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
+        if (m < M && n < N) y[int64_t(m) * N + n] = F[i][k][v];
+      }
+    }
+}
+
+int launch_q6k_planes(int quant, const void* w, int64_t n_in, int64_t n_out, void* planes, hipStream_t s) {
+  if (quant != JERO_Q6_K && quant != JERO_Q6_K_R)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "q6k planes: weights must be Q6_K or Q6_K_R");
+  const int nb = int(n_in / 256);
+  int8_t* hi = static_cast<int8_t*>(planes);
+  int8_t* lo = hi + n_out * n_in;
+  float* d = reinterpret_cast<float*>(lo + n_out * n_in);
+  const int64_t threads = n_out * nb * 64;
+  hipLaunchKernelGGL(q6k_planes_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const uint8_t*>(w), quant == JERO_Q6_K_R ? 1 : 0, n_out, nb, hi, lo, d);
+  return check_launch("q6k planes");
+}
+
+int launch_gemm_q6k_planes(const void* planes, int64_t n_in, int64_t n_out, const void* xq, int64_t m, float* y,
+                           hipStream_t s) {
+  const int nb = int(n_in / 256);
+  const int8_t* hi = static_cast<const int8_t*>(planes);
+  const int8_t* lo = hi + n_out * n_in;
+  const float* d = reinterpret_cast<const float*>(lo + n_out * n_in);
+  hipLaunchKernelGGL(gemm_q6k_planes_kernel, dim3(unsigned(gemm_tiles(m, n_out))), dim3(kGemmThreads), 0, s,
+                     static_cast<const uint8_t*>(xq), row_bytes(JERO_Q8_K, n_in), hi, lo, d, int(m), int(n_out), nb,
+                     y);
+  return check_launch("gemm q6_k planes");
+}
+
 int gemm_tiles(int64_t M, int64_t N) { return int(((M + kGemmBM - 1) / kGemmBM) * ((N + kGemmBN - 1) / kGemmBN)); }
 
 // Shared argument checks of the int8 products: sizes within 32-bit tile indexing and no int32
@@ -471,9 +690,20 @@ using namespace jero;
 namespace jero {
 
 int launch_gemm(int quant, const void* w_dev, int64_t n_in, int64_t n_out, const void* xq_dev, int64_t m, float* y_dev,
-                hipStream_t s) {
+                hipStream_t s, const void* q6_planes) {
   const int act = act_format(quant);
   const int64_t xrb = row_bytes(act, n_in);
+  if ((quant == JERO_Q6_K || quant == JERO_Q6_K_R) && (q6_planes || m >= kQ6PlanesMinRows)) {
+    int rc = JERO_OK;
+    if (!q6_planes) {  // expanded into the library workspace for this call
+      void* ws = nullptr;
+      if ((rc = workspace(q6k_planes_bytes(n_in, n_out), &ws)) ||
+          (rc = launch_q6k_planes(quant, w_dev, n_in, n_out, ws, s)))
+        return rc;
+      q6_planes = ws;
+    }
+    return launch_gemm_q6k_planes(q6_planes, n_in, n_out, xq_dev, m, y_dev, s);
+  }
   if ((quant == JERO_Q4_K || quant == JERO_Q4_K_R) && n_out % kGemmBN == 0) {
     const int tiles = gemm_tiles(m, n_out);
     if (quant == JERO_Q4_K)

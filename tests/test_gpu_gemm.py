@@ -91,6 +91,45 @@ def test_gemm_q4k_prefill_shape_rows_equal_gemv(dev):
     assert rel_err(y[rows], ref) < REL_TOL
 
 
+@pytest.mark.parametrize("m,k,n", [(8, 256, 64), (37, 512, 96), (128, 1024, 384), (200, 4096, 130),
+                                   (513, 12288, 256)])
+def test_gemm_q6k_planes_matches_oracle(dev, m, k, n):
+    """Q6_K from 8 rows: the int8-MFMA kernel over the tensor's hi / lo planes (w = sc (q6 - 32)
+    = 128 hi + lo), on GGUF bytes and on the Q6_K_R device layout."""
+    print(f"gemm q6_k m={m} k={k} n={n}", flush=True)
+    w, xq, y, view = run_gemm(dev, J.Q6_K, m, k, n, 7000 + m + k + n)
+    ref = O.gemm(J.Q6_K, w, k, n, xq, m, threads=8)
+    assert np.all(np.isfinite(y))
+    assert rel_err(y, ref) < REL_TOL
+    yr = torch.full((m, n), float("nan"), device=dev)
+    J.gemm(J.repack(view), to_dev(xq, dev), m, yr)
+    torch.cuda.synchronize()
+    assert np.array_equal(yr.cpu().numpy(), y)
+
+
+def test_gemm_q6k_planes_extremes(dev):
+    """Sub-block scales at -128 and 127 with q6 at 0 and 63 (w = 4096 and 3937: the planes' hi
+    at its top), zero and tiny activation rows."""
+    m, k, n = 40, 1024, 128
+    w = rand_weights(J.Q6_K, n, k, 81).reshape(n * (k // 256), 210)
+    w[0::4, 192:208] = np.uint8(0x80)   # every scale -128
+    w[1::4, 192:208] = np.uint8(0x7F)   # every scale 127
+    w[0::8, :192] = 0x00                # q6 = 0
+    w[1::8, :192] = 0xFF                # q6 = 63
+    w = w.reshape(-1)
+    x = rand_act(k, 82, m=m)
+    x[3] = 0.0
+    x[7, :256] = 1e-30
+    xq = J.quantize_act(J.Q8_K, to_dev(x, dev))
+    view = J.TensorView("w", J.Q6_K, [k, n], to_dev(w, dev))
+    y = torch.empty((m, n), device=dev)
+    J.gemm(view, xq, m, y)
+    ref = O.gemm(J.Q6_K, w, k, n, xq.cpu().numpy(), m, threads=8)
+    y = y.cpu().numpy()
+    assert np.all(y[3] == 0.0)
+    assert rel_err(y, ref) < REL_TOL
+
+
 @pytest.mark.parametrize("quant,m,k,n", [(J.Q8_0, 5, 512, 96), (J.Q4_0, 3, 256, 40), (J.Q6_K, 4, 512, 64),
                                          (J.Q4_K, 3, 256, 100)])
 def test_gemm_row_path_formats(dev, quant, m, k, n):

@@ -491,65 +491,66 @@ struct __attribute__((aligned(16))) Q6pStage {
   float dw[kGemmBN];
 };
 
-// The block's registers of one thread: half of an activation row and of each plane's row.
+constexpr int kQ6pThreads = 512;  // 8 waves, two per SIMD
+
+// The block's registers of one thread: a quarter of an activation row and of each plane's row.
 struct Q6pRegs {
-  u32x4 a[8], h[8], l[8];
+  u32x4 a[4], h[4], l[4];
   float d;
 };
 
 __device__ __forceinline__ void q6p_load(Q6pRegs& R, const uint8_t* __restrict__ xq, int64_t xrb, int m0, int M,
                                          const int8_t* __restrict__ hi, const int8_t* __restrict__ lo,
                                          const float* __restrict__ dw, int n0, int N, int nb, int b) {
-  const int t = threadIdx.x, r = t >> 1, half = t & 1;
+  const int t = threadIdx.x, r = t >> 2, q = t & 3;
   const int m = min(m0 + r, M - 1), n = min(n0 + r, N - 1);
   const uint8_t* xa = xq + int64_t(m) * xrb + int64_t(b) * 292;
-  const int64_t woff = int64_t(n) * nb * 256 + int64_t(b) * 256 + 128 * half;
+  const int64_t woff = int64_t(n) * nb * 256 + int64_t(b) * 256 + 64 * q;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    R.a[i] = ld4(xa + 4 + 128 * half + 16 * i);
+  for (int i = 0; i < 4; i++) {
+    R.a[i] = ld4(xa + 4 + 64 * q + 16 * i);
     R.h[i] = ld4(reinterpret_cast<const uint8_t*>(hi + woff) + 16 * i);
     R.l[i] = ld4(reinterpret_cast<const uint8_t*>(lo + woff) + 16 * i);
   }
-  R.d = half == 0 ? __uint_as_float(ld1(xa)) : dw[int64_t(n) * nb + b];
+  R.d = q == 0 ? __uint_as_float(ld1(xa)) : dw[int64_t(n) * nb + b];
 }
 
 __device__ __forceinline__ void q6p_store(const Q6pRegs& R, Q6pStage& S) {
-  const int t = threadIdx.x, r = t >> 1, half = t & 1;
+  const int t = threadIdx.x, r = t >> 2, q = t & 3;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    *reinterpret_cast<u32x4*>(&S.a[r][128 * half + 16 * i]) = R.a[i];
-    *reinterpret_cast<u32x4*>(&S.h[r][128 * half + 16 * i]) = R.h[i];
-    *reinterpret_cast<u32x4*>(&S.l[r][128 * half + 16 * i]) = R.l[i];
+  for (int i = 0; i < 4; i++) {
+    *reinterpret_cast<u32x4*>(&S.a[r][64 * q + 16 * i]) = R.a[i];
+    *reinterpret_cast<u32x4*>(&S.h[r][64 * q + 16 * i]) = R.h[i];
+    *reinterpret_cast<u32x4*>(&S.l[r][64 * q + 16 * i]) = R.l[i];
   }
-  if (half == 0) S.dx[r] = R.d;
-  else S.dw[r] = R.d;
+  if (q == 0) S.dx[r] = R.d;
+  else if (q == 1) S.dw[r] = R.d;
 }
 
-// Y[m][n] = sum_b dx[m, b] d[n, b] (128 (hi . q8) + lo . q8) over the 256-blocks b: the same
-// 128 x 128 tile, four waves and 32 x 32 x 32 int8 MFMAs as the int8 product, two planes per
-// K step; per block the two int32 sums meet exactly and are scaled into an f32 accumulator.
-// The next block's loads are in flight while the current one runs from LDS.
-__global__ void __launch_bounds__(kGemmThreads) gemm_q6k_planes_kernel(const uint8_t* __restrict__ xq, int64_t xrb,
-                                                                        const int8_t* __restrict__ hi,
-                                                                        const int8_t* __restrict__ lo,
-                                                                        const float* __restrict__ dw, int M, int N,
-                                                                        int nb, float* __restrict__ y) {
+// Y[m][n] = sum_b dx[m, b] d[n, b] (128 (hi . q8) + lo . q8) over the 256-blocks b: a 128 x 128
+// tile per workgroup of eight waves (two per SIMD), each wave a 64 x 32 piece of two 32 x 32
+// tiles, 32 x 32 x 32 int8 MFMAs, one per plane per K step; per block the two int32 sums meet
+// exactly and are scaled into an f32 accumulator.  The next block's loads are in flight while
+// the current one runs from LDS.
+__global__ void __launch_bounds__(kQ6pThreads) gemm_q6k_planes_kernel(const uint8_t* __restrict__ xq, int64_t xrb,
+                                                                       const int8_t* __restrict__ hi,
+                                                                       const int8_t* __restrict__ lo,
+                                                                       const float* __restrict__ dw, int M, int N,
+                                                                       int nb, float* __restrict__ y) {
   __shared__ Q6pStage S;
   const int n_tiles_m = (M + kGemmBM - 1) / kGemmBM;
   int tm, tn;
   gemm_tile_of(blockIdx.x, gridDim.x, n_tiles_m, tm, tn);
   const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int wm = wv >> 1, wn = wv & 1;
+  const int wm = wv >> 2, wn = wv & 3;
   const int lr = lane & 31, lh = lane >> 5;
-  v16i Ch[2][2], Cl[2][2];
-  float F[2][2][16];
+  v16i Ch[2], Cl[2];
+  float F[2][16];
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int k = 0; k < 2; k++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) Ch[i][k][v] = 0, Cl[i][k][v] = 0, F[i][k][v] = 0.f;
+    for (int v = 0; v < 16; v++) Ch[i][v] = 0, Cl[i][v] = 0, F[i][v] = 0.f;
   Q6pRegs R;
   q6p_load(R, xq, xrb, m0, M, hi, lo, dw, n0, N, nb, 0);
   q6p_store(R, S);
@@ -559,33 +560,26 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q6k_planes_kernel(const uin
     if (more) q6p_load(R, xq, xrb, m0, M, hi, lo, dw, n0, N, nb, b + 1);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      v4i af[2], bh[2], bl[2];
+      v4i af[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) af[i] = *reinterpret_cast<const v4i*>(&S.a[64 * wm + 32 * i + lr][32 * j + 16 * lh]);
+      const v4i bh = *reinterpret_cast<const v4i*>(&S.h[32 * wn + lr][32 * j + 16 * lh]);
+      const v4i bl = *reinterpret_cast<const v4i*>(&S.l[32 * wn + lr][32 * j + 16 * lh]);
 #pragma unroll
       for (int i = 0; i < 2; i++) {
-        af[i] = *reinterpret_cast<const v4i*>(&S.a[64 * wm + 32 * i + lr][32 * j + 16 * lh]);
-        bh[i] = *reinterpret_cast<const v4i*>(&S.h[64 * wn + 32 * i + lr][32 * j + 16 * lh]);
-        bl[i] = *reinterpret_cast<const v4i*>(&S.l[64 * wn + 32 * i + lr][32 * j + 16 * lh]);
+        Ch[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bh, Ch[i], 0, 0, 0);
+        Cl[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bl, Cl[i], 0, 0, 0);
       }
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-          Ch[i][k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bh[k], Ch[i][k], 0, 0, 0);
-          Cl[i][k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bl[k], Cl[i][k], 0, 0, 0);
-        }
     }
+    const float dn = S.dw[32 * wn + lr];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int k = 0; k < 2; k++) {
-        const float dn = S.dw[64 * wn + 32 * k + lr];
-#pragma unroll
-        for (int v = 0; v < 16; v++) {
-          const int ml = 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
-          const int tsum = Ch[i][k][v] * 128 + Cl[i][k][v];
-          F[i][k][v] = fmaf(float(tsum) * S.dx[ml], dn, F[i][k][v]);
-          Ch[i][k][v] = 0, Cl[i][k][v] = 0;
-        }
+      for (int v = 0; v < 16; v++) {
+        const int ml = 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
+        const int tsum = Ch[i][v] * 128 + Cl[i][v];
+        F[i][v] = fmaf(float(tsum) * S.dx[ml], dn, F[i][v]);
+        Ch[i][v] = 0, Cl[i][v] = 0;
       }
     __syncthreads();
     if (more) {
@@ -593,16 +587,13 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_q6k_planes_kernel(const uin
       __syncthreads();
     }
   }
+  const int n = n0 + 32 * wn + lr;
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const int n = n0 + 64 * wn + 32 * k + lr;
-#pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
-        if (m < M && n < N) y[int64_t(m) * N + n] = F[i][k][v];
-      }
+    for (int v = 0; v < 16; v++) {
+      const int m = m0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
+      if (m < M && n < N) y[int64_t(m) * N + n] = F[i][v];
     }
 }
 
@@ -625,7 +616,7 @@ int launch_gemm_q6k_planes(const void* planes, int64_t n_in, int64_t n_out, cons
   const int8_t* hi = static_cast<const int8_t*>(planes);
   const int8_t* lo = hi + n_out * n_in;
   const float* d = reinterpret_cast<const float*>(lo + n_out * n_in);
-  hipLaunchKernelGGL(gemm_q6k_planes_kernel, dim3(unsigned(gemm_tiles(m, n_out))), dim3(kGemmThreads), 0, s,
+  hipLaunchKernelGGL(gemm_q6k_planes_kernel, dim3(unsigned(gemm_tiles(m, n_out))), dim3(kQ6pThreads), 0, s,
                      static_cast<const uint8_t*>(xq), row_bytes(JERO_Q8_K, n_in), hi, lo, d, int(m), int(n_out), nb,
                      y);
   return check_launch("gemm q6_k planes");

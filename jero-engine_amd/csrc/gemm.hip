@@ -483,74 +483,75 @@ __global__ void __launch_bounds__(256) q6k_planes_kernel(const uint8_t* __restri
   }
 }
 
+constexpr int kQ6pThreads = 512;  // 8 waves
+constexpr int kQ6pBN = 64;        // weight rows per tile
+
 struct __attribute__((aligned(16))) Q6pStage {
   int8_t a[kGemmBM][kPlaneStride];  // q8 of the activation block
-  int8_t h[kGemmBN][kPlaneStride];  // hi plane of the weight block
-  int8_t l[kGemmBN][kPlaneStride];  // lo plane
+  int8_t h[kQ6pBN][kPlaneStride];   // hi plane of the weight block
+  int8_t l[kQ6pBN][kPlaneStride];   // lo plane
   float dx[kGemmBM];
-  float dw[kGemmBN];
+  float dw[kQ6pBN];
 };
 
-constexpr int kQ6pThreads = 512;  // 8 waves, two per SIMD
-
-// The block's registers of one thread: a quarter of an activation row and of each plane's row.
+// The block's registers of one thread: a quarter of an activation row and a quarter of one
+// plane row (threads 0..255 the hi plane, 256..511 the lo plane).
 struct Q6pRegs {
-  u32x4 a[4], h[4], l[4];
-  float d;
+  u32x4 a[4], w[4];
+  float dx, dw;
 };
 
 __device__ __forceinline__ void q6p_load(Q6pRegs& R, const uint8_t* __restrict__ xq, int64_t xrb, int m0, int M,
                                          const int8_t* __restrict__ hi, const int8_t* __restrict__ lo,
                                          const float* __restrict__ dw, int n0, int N, int nb, int b) {
   const int t = threadIdx.x, r = t >> 2, q = t & 3;
-  const int m = min(m0 + r, M - 1), n = min(n0 + r, N - 1);
+  const int m = min(m0 + r, M - 1);
   const uint8_t* xa = xq + int64_t(m) * xrb + int64_t(b) * 292;
-  const int64_t woff = int64_t(n) * nb * 256 + int64_t(b) * 256 + 64 * q;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    R.a[i] = ld4(xa + 4 + 64 * q + 16 * i);
-    R.h[i] = ld4(reinterpret_cast<const uint8_t*>(hi + woff) + 16 * i);
-    R.l[i] = ld4(reinterpret_cast<const uint8_t*>(lo + woff) + 16 * i);
-  }
-  R.d = q == 0 ? __uint_as_float(ld1(xa)) : dw[int64_t(n) * nb + b];
+  for (int i = 0; i < 4; i++) R.a[i] = ld4(xa + 4 + 64 * q + 16 * i);
+  R.dx = __uint_as_float(ld1(xa));
+  const int wr = r & (kQ6pBN - 1), n = min(n0 + wr, N - 1);
+  const int8_t* plane = t < 256 ? hi : lo;
+  const uint8_t* wp = reinterpret_cast<const uint8_t*>(plane + int64_t(n) * nb * 256 + int64_t(b) * 256 + 64 * q);
+#pragma unroll
+  for (int i = 0; i < 4; i++) R.w[i] = ld4(wp + 16 * i);
+  R.dw = dw[int64_t(n) * nb + b];
 }
 
 __device__ __forceinline__ void q6p_store(const Q6pRegs& R, Q6pStage& S) {
-  const int t = threadIdx.x, r = t >> 2, q = t & 3;
+  const int t = threadIdx.x, r = t >> 2, q = t & 3, wr = r & (kQ6pBN - 1);
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     *reinterpret_cast<u32x4*>(&S.a[r][64 * q + 16 * i]) = R.a[i];
-    *reinterpret_cast<u32x4*>(&S.h[r][64 * q + 16 * i]) = R.h[i];
-    *reinterpret_cast<u32x4*>(&S.l[r][64 * q + 16 * i]) = R.l[i];
+    if (t < 256) *reinterpret_cast<u32x4*>(&S.h[wr][64 * q + 16 * i]) = R.w[i];
+    else *reinterpret_cast<u32x4*>(&S.l[wr][64 * q + 16 * i]) = R.w[i];
   }
-  if (q == 0) S.dx[r] = R.d;
-  else if (q == 1) S.dw[r] = R.d;
+  if (q == 0) S.dx[r] = R.dx;
+  if (q == 1 && t < 256) S.dw[wr] = R.dw;
 }
 
-// Y[m][n] = sum_b dx[m, b] d[n, b] (128 (hi . q8) + lo . q8) over the 256-blocks b: a 128 x 128
-// tile per workgroup of eight waves (two per SIMD), each wave a 64 x 32 piece of two 32 x 32
-// tiles, 32 x 32 x 32 int8 MFMAs, one per plane per K step; per block the two int32 sums meet
-// exactly and are scaled into an f32 accumulator.  The next block's loads are in flight while
-// the current one runs from LDS.
-__global__ void __launch_bounds__(kQ6pThreads) gemm_q6k_planes_kernel(const uint8_t* __restrict__ xq, int64_t xrb,
-                                                                       const int8_t* __restrict__ hi,
-                                                                       const int8_t* __restrict__ lo,
-                                                                       const float* __restrict__ dw, int M, int N,
-                                                                       int nb, float* __restrict__ y) {
+// Y[m][n] = sum_b dx[m, b] d[n, b] (128 (hi . q8) + lo . q8) over the 256-blocks b: a 128 x 64
+// tile per workgroup of eight waves, each wave one 32 x 32 tile, one 32 x 32 x 32 int8 MFMA per
+// plane per K step; per block the two int32 sums meet exactly and are scaled into an f32
+// accumulator.  The next block's loads are in flight while the current one runs from LDS; at
+// 70 KB of LDS two workgroups share a CU.
+__global__ void __launch_bounds__(kQ6pThreads, 2) gemm_q6k_planes_kernel(const uint8_t* __restrict__ xq, int64_t xrb,
+                                                                          const int8_t* __restrict__ hi,
+                                                                          const int8_t* __restrict__ lo,
+                                                                          const float* __restrict__ dw, int M, int N,
+                                                                          int nb, float* __restrict__ y) {
   __shared__ Q6pStage S;
   const int n_tiles_m = (M + kGemmBM - 1) / kGemmBM;
   int tm, tn;
   gemm_tile_of(blockIdx.x, gridDim.x, n_tiles_m, tm, tn);
-  const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
+  const int m0 = tm * kGemmBM, n0 = tn * kQ6pBN;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int wm = wv >> 2, wn = wv & 3;
+  const int wm = wv >> 1, wn = wv & 1;
   const int lr = lane & 31, lh = lane >> 5;
-  v16i Ch[2], Cl[2];
-  float F[2][16];
+  v16i Ch, Cl;
+  float F[16];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
-#pragma unroll
-    for (int v = 0; v < 16; v++) Ch[i][v] = 0, Cl[i][v] = 0, F[i][v] = 0.f;
+  for (int v = 0; v < 16; v++) Ch[v] = 0, Cl[v] = 0, F[v] = 0.f;
   Q6pRegs R;
   q6p_load(R, xq, xrb, m0, M, hi, lo, dw, n0, N, nb, 0);
   q6p_store(R, S);
@@ -560,27 +561,20 @@ __global__ void __launch_bounds__(kQ6pThreads) gemm_q6k_planes_kernel(const uint
     if (more) q6p_load(R, xq, xrb, m0, M, hi, lo, dw, n0, N, nb, b + 1);
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-      v4i af[2];
-#pragma unroll
-      for (int i = 0; i < 2; i++) af[i] = *reinterpret_cast<const v4i*>(&S.a[64 * wm + 32 * i + lr][32 * j + 16 * lh]);
+      const v4i af = *reinterpret_cast<const v4i*>(&S.a[32 * wm + lr][32 * j + 16 * lh]);
       const v4i bh = *reinterpret_cast<const v4i*>(&S.h[32 * wn + lr][32 * j + 16 * lh]);
       const v4i bl = *reinterpret_cast<const v4i*>(&S.l[32 * wn + lr][32 * j + 16 * lh]);
-#pragma unroll
-      for (int i = 0; i < 2; i++) {
-        Ch[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bh, Ch[i], 0, 0, 0);
-        Cl[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bl, Cl[i], 0, 0, 0);
-      }
+      Ch = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bh, Ch, 0, 0, 0);
+      Cl = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bl, Cl, 0, 0, 0);
     }
     const float dn = S.dw[32 * wn + lr];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int ml = 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
-        const int tsum = Ch[i][v] * 128 + Cl[i][v];
-        F[i][v] = fmaf(float(tsum) * S.dx[ml], dn, F[i][v]);
-        Ch[i][v] = 0, Cl[i][v] = 0;
-      }
+    for (int v = 0; v < 16; v++) {
+      const int ml = 32 * wm + 8 * (v >> 2) + 4 * lh + (v & 3);
+      const int tsum = Ch[v] * 128 + Cl[v];
+      F[v] = fmaf(float(tsum) * S.dx[ml], dn, F[v]);
+      Ch[v] = 0, Cl[v] = 0;
+    }
     __syncthreads();
     if (more) {
       q6p_store(R, S);
@@ -589,12 +583,10 @@ __global__ void __launch_bounds__(kQ6pThreads) gemm_q6k_planes_kernel(const uint
   }
   const int n = n0 + 32 * wn + lr;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int m = m0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
-      if (m < M && n < N) y[int64_t(m) * N + n] = F[i][v];
-    }
+  for (int v = 0; v < 16; v++) {
+    const int m = m0 + 32 * wm + 8 * (v >> 2) + 4 * lh + (v & 3);
+    if (m < M && n < N) y[int64_t(m) * N + n] = F[v];
+  }
 }
 
 int launch_q6k_planes(int quant, const void* w, int64_t n_in, int64_t n_out, void* planes, hipStream_t s) {
@@ -616,7 +608,8 @@ int launch_gemm_q6k_planes(const void* planes, int64_t n_in, int64_t n_out, cons
   const int8_t* hi = static_cast<const int8_t*>(planes);
   const int8_t* lo = hi + n_out * n_in;
   const float* d = reinterpret_cast<const float*>(lo + n_out * n_in);
-  hipLaunchKernelGGL(gemm_q6k_planes_kernel, dim3(unsigned(gemm_tiles(m, n_out))), dim3(kQ6pThreads), 0, s,
+  const int64_t tiles = ((m + kGemmBM - 1) / kGemmBM) * ((n_out + kQ6pBN - 1) / kQ6pBN);
+  hipLaunchKernelGGL(gemm_q6k_planes_kernel, dim3(unsigned(tiles)), dim3(kQ6pThreads), 0, s,
                      static_cast<const uint8_t*>(xq), row_bytes(JERO_Q8_K, n_in), hi, lo, d, int(m), int(n_out), nb,
                      y);
   return check_launch("gemm q6_k planes");

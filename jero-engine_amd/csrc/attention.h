@@ -39,6 +39,7 @@ struct AttnParams {
   // q_stride floats on, which attends to active + t slots, and whose partials start t * part_tok
   // (part_o) and t * part_tok_ml (part_ml) floats on; all zero for one query
   int64_t q_stride, part_tok, part_tok_ml;
+  int n_tok;  // queries of the batch (set by the launcher)
 };
 
 int attn_splits(int active, int hd);

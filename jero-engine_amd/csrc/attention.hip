@@ -435,28 +435,40 @@ __device__ __forceinline__ h4_t h4_of(uint32_t lo, uint32_t hi) {
 //   * Fused (decode step): the q heads are normalised and rotated once per workgroup into LDS (one
 //     wave per head); the workgroup holding the new slot does the same for k, attends to the new
 //     k and v rounded to f16 (the values the ring then holds) and appends them to the ring.
-template <int HD, int MAXG, bool FUSED>
+template <int HD, int MAXG, bool FUSED, bool BATCH = false>
 __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
-  {  // token of a batch of queries (zero offsets for one query)
-    const int t = blockIdx.z;
-    p.q += t * p.q_stride;
-    p.active += t;
-    p.part_o += t * p.part_tok;
-    p.part_ml += t * p.part_tok_ml;
+  static_assert(!(FUSED && BATCH), "the decode step attends one query");
+  // BATCH (a batch of consecutive queries, the prefill): the workgroup's 16 score columns are
+  // (token, head) pairs, tpw = 16 / group tokens of one kv head's group, so each K/V row loaded
+  // serves every one of them; column c is token c / group, head c % group, attending to its own
+  // first active + token slots.  Otherwise the columns are the group's heads of query blockIdx.z.
+  const int group = p.group;
+  int t0 = blockIdx.z, ntok = 1;
+  if constexpr (BATCH) {
+    const int tpw = 16 / group;
+    t0 = blockIdx.z * tpw;
+    ntok = min(tpw, p.n_tok - t0);
   }
+  p.q += t0 * p.q_stride;
+  p.active += t0;
+  p.part_o += t0 * p.part_tok;
+  p.part_ml += t0 * p.part_tok_ml;
+  const int ncol = BATCH ? ntok * group : group;  // valid score columns
+  auto ctok = [&](int c) { return BATCH ? c / group : 0; };
+  auto chead = [&](int c) { return BATCH ? c % group : c; };
   constexpr int NCH = HD / 32;  // 16-byte chunks per lane per row
   constexpr int NT = HD / 16;   // 16-dim MFMA tiles
   constexpr int NW = kAttnThreads / kWave;
   constexpr int CH = 16 * NW;   // slots per workgroup
+  constexpr int QC = BATCH ? 16 : MAXG;  // score columns with a q row
   static_assert(MAXG <= 16 && (HD == 64 || HD == 128), "tile shape");
   __shared__ __attribute__((aligned(16))) float s_q[16][HD];
   __shared__ __attribute__((aligned(16))) float s_kn[HD];
-  __shared__ float s_o[NW][MAXG][HD];
+  __shared__ float s_o[NW][QC][HD];
   __shared__ float s_m[NW][16], s_l[NW][16];
 
   const int split = blockIdx.x, kh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int group = p.group;
   const int64_t kvd = int64_t(p.nkv) * HD;
   const int S = gridDim.x;
   const int p0 = split * CH, w0 = p0 + wv * 16;
@@ -465,14 +477,15 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
   // 0. small loads first (they complete before the K/V loads issued after them)
   int64_t pos_pre = p.pos;
   if constexpr (FUSED) pos_pre = *(p.pos_dev ? p.pos_dev : reinterpret_cast<const int64_t*>(p.k));
-  // fused: wave w prepares heads w, w + NW, ... as one pair of dims per lane (lanes < HD / 2)
-  constexpr int HPW = (MAXG + NW - 1) / NW;
+  // wave w prepares columns w, w + NW, ... as one pair of dims per lane (lanes < HD / 2)
+  constexpr int HPW = (QC + NW - 1) / NW;
   const int pr = lane < HD / 2 ? lane : HD / 2 - 1;
   float2 qv[HPW];
 #pragma unroll
   for (int j = 0; j < HPW; j++) {
-    const int h = min(wv + NW * j, group - 1);
-    qv[j] = reinterpret_cast<const float2*>(p.q + (int64_t(kh) * group + h) * HD)[pr];
+    const int c = min(wv + NW * j, ncol - 1);
+    qv[j] = reinterpret_cast<const float2*>(p.q + int64_t(ctok(c)) * p.q_stride +
+                                            (int64_t(kh) * group + chead(c)) * HD)[pr];
   }
   float2 knv = make_float2(0.f, 0.f), qnw = knv, knw = knv, csv = knv;
   if constexpr (FUSED) {
@@ -482,7 +495,8 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
     csv = reinterpret_cast<const float2*>(p.rope_cs ? p.rope_cs : p.q)[pr];
   }
   // 1. K and V loads: slot w0 + col, chunks 4j + kq (clamped in-bounds; masked below)
-  const int bound = p.pos_dev ? int(p.capacity) : p.active;
+  const int act_hi = p.active + ntok - 1;  // slots the workgroup's last query attends to
+  const int bound = p.pos_dev ? int(p.capacity) : act_hi;
   const int pl = min(p0 + CH, bound);
   const int ps = min(w0 + col, pl - 1);
   const _Float16* kb = static_cast<const _Float16*>(p.k) + int64_t(kh) * HD + int64_t(ps) * kvd;
@@ -493,7 +507,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
 #pragma unroll
   for (int j = 0; j < NCH; j++) vr[j] = ld4(reinterpret_cast<const uint8_t*>(vb + 8 * (4 * j + kq)));
 
-  int active = p.active, slot = p.slot;
+  int active = act_hi, slot = p.slot;
   int64_t pos_now = p.pos;
   if (p.pos_dev) {
     pos_now = pos_pre;
@@ -501,10 +515,11 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
     active = int(pos_now + 1 < p.capacity ? pos_now + 1 : p.capacity);
   }
   if (p0 >= active) {  // empty split: contributes nothing to the merge
-    if (tid < group) {
-      const int h = kh * group + tid;
-      p.part_ml[(int64_t(h) * S + split) * 2 + 0] = -INFINITY;
-      p.part_ml[(int64_t(h) * S + split) * 2 + 1] = 0.f;
+    if (tid < ncol) {
+      const int h = kh * group + chead(tid);
+      float* ml = p.part_ml + int64_t(ctok(tid)) * p.part_tok_ml;
+      ml[(int64_t(h) * S + split) * 2 + 0] = -INFINITY;
+      ml[(int64_t(h) * S + split) * 2 + 1] = 0.f;
     }
     return;
   }
@@ -535,7 +550,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
     float2 x = qv[j];
     if constexpr (FUSED) x = norm_rope(x, p.q_norm != nullptr, qnw);
     if (h < 16 && lane < HD / 2) {
-      const bool real = h < group;
+      const bool real = h < ncol;
       reinterpret_cast<float2*>(s_q[h])[lane] = real ? make_float2(x.x * p.scale, x.y * p.scale) : make_float2(0.f, 0.f);
       if constexpr (FUSED) {
         if (real && split == 0 && p.tr_q) reinterpret_cast<float2*>(p.tr_q + (int64_t(kh) * group + h) * HD)[lane] = x;
@@ -605,9 +620,11 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
     sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qhi[i], sc, 0, 0, 0);
     sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qlo[i], sc, 0, 0, 0);
   }
+  // this lane's column attends to slots below lim (its token's count; none for an empty column)
+  const int lim = BATCH ? (col < ncol ? min(p1, p.active + ctok(col)) : 0) : p1;
   float s[4];
 #pragma unroll
-  for (int r = 0; r < 4; r++) s[r] = w0 + 4 * kq + r < p1 ? sc[r] : -INFINITY;
+  for (int r = 0; r < 4; r++) s[r] = w0 + 4 * kq + r < lim ? sc[r] : -INFINITY;
   // 5. the wave's softmax per head: the 4 lanes col, col + 16, col + 32, col + 48
   float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
   mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
@@ -664,7 +681,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int h = 4 * kq + r;
-      if (h < MAXG && h < group) s_o[wv][h][d] = o[i][r];
+      if (h < QC && h < ncol) s_o[wv][h][d] = o[i][r];
     }
   }
   if (lane < 16) {
@@ -672,8 +689,8 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
     s_l[wv][lane] = sum;
   }
   __syncthreads();
-  for (int idx = tid; idx < group * HD; idx += kAttnThreads) {
-    const int h = idx / HD, d = idx % HD;
+  for (int idx = tid; idx < ncol * HD; idx += kAttnThreads) {
+    const int h = idx / HD, d = idx % HD;  // h: the score column
     float M = s_m[0][h];
 #pragma unroll
     for (int w = 1; w < NW; w++) M = fmaxf(M, s_m[w][h]);
@@ -684,11 +701,11 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
       ov += wt * s_o[w][h][d];
       L += wt * s_l[w][h];
     }
-    const int64_t row = int64_t(kh * group + h) * S + split;
-    p.part_o[row * HD + d] = ov;
+    const int64_t row = int64_t(kh * group + chead(h)) * S + split;
+    p.part_o[int64_t(ctok(h)) * p.part_tok + row * HD + d] = ov;
     if (d == 0) {
-      p.part_ml[row * 2 + 0] = M;
-      p.part_ml[row * 2 + 1] = L;
+      p.part_ml[int64_t(ctok(h)) * p.part_tok_ml + row * 2 + 0] = M;
+      p.part_ml[int64_t(ctok(h)) * p.part_tok_ml + row * 2 + 1] = L;
     }
   }
 }
@@ -889,6 +906,12 @@ static void launch_partial(const AttnParams& p, int S, int T, hipStream_t s) {
 
 template <int HD, bool FUSED>
 static void launch_mfma(const AttnParams& p, int S, int T, hipStream_t s) {
+  if (!FUSED && T > 1) {  // a batch of queries: 16 / group tokens per workgroup
+    const int tpw = 16 / p.group;
+    hipLaunchKernelGGL((attn_mfma_kernel<HD, 16, false, true>), dim3(S, p.nkv, (T + tpw - 1) / tpw),
+                       dim3(kAttnThreads), 0, s, p);
+    return;
+  }
   const dim3 grid(S, p.nkv, T);
   if (p.group <= 1)
     hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, FUSED>), grid, dim3(kAttnThreads), 0, s, p);
@@ -918,6 +941,7 @@ static int attention_impl(AttnParams p, bool fused, int S, int T, float* out, in
   p.part_tok = T > 1 ? nq * S * p.hd : 0;
   p.part_tok_ml = T > 1 ? nq * S * 2 : 0;
   p.part_ml = p.part_o + int64_t(T) * nq * S * p.hd;
+  p.n_tok = T;
 #define JERO_ATTN_CASE(HDV)                                                                     \
   if (p.hd == HDV) {                                                                            \
     if (p.kv_dtype == JERO_KV_F16 && HDV >= 64) {                                               \

@@ -125,14 +125,20 @@ __device__ __forceinline__ uint32_t pk_mul(uint32_t x, uint32_t s) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
-template <bool PLANAR>
+// SPLIT: the grid holds two workgroups per tile, each over one half of the K blocks, adding its
+// partial tile into y (zeroed before the launch): two addends, so the sum is the same in either
+// order, bit for bit.
+template <bool PLANAR, bool SPLIT>
 __global__ void __launch_bounds__(kQ4Threads) gemm_q4k_kernel(const uint8_t* __restrict__ w, int64_t wrb,
                                                                const uint8_t* __restrict__ x, int64_t xrb, int M,
                                                                int N, int nb, float* __restrict__ y) {
   __shared__ Q4kStage S[2];
   const int n_tiles_m = (M + kGemmBM - 1) / kGemmBM;
   int tm, tn;
-  gemm_tile_of(blockIdx.x, gridDim.x, n_tiles_m, tm, tn);
+  const int half = SPLIT ? int(blockIdx.x & 1) : 0;
+  gemm_tile_of(SPLIT ? int(blockIdx.x >> 1) : int(blockIdx.x), SPLIT ? int(gridDim.x >> 1) : int(gridDim.x),
+               n_tiles_m, tm, tn);
+  const int b0 = SPLIT ? half * ((nb + 1) / 2) : 0, b1 = SPLIT ? (half ? nb : (nb + 1) / 2) : nb;
   const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int wm = wv >> 2, wn = wv & 3;  // wave tile: rows 64 wm .. +64, weight rows 32 wn .. +32
@@ -146,12 +152,12 @@ __global__ void __launch_bounds__(kQ4Threads) gemm_q4k_kernel(const uint8_t* __r
     for (int v = 0; v < 16; v++) acc[i][v] = 0.f;
 
   Q4kRegs R;
-  q4k_load<PLANAR>(R, x, xrb, m0, M, w, wrb, n0, 0, nb);
+  q4k_load<PLANAR>(R, x, xrb, m0, M, w, wrb, n0, b0, nb);
   q4k_store(R, S[0]);
   __syncthreads();
-  for (int b = 0; b < nb; b++) {
-    const Q4kStage& T = S[b & 1];
-    if (b + 1 < nb) q4k_load<PLANAR>(R, x, xrb, m0, M, w, wrb, n0, b + 1, nb);
+  for (int b = b0; b < b1; b++) {
+    const Q4kStage& T = S[(b - b0) & 1];
+    if (b + 1 < b1) q4k_load<PLANAR>(R, x, xrb, m0, M, w, wrb, n0, b + 1, nb);
     // this lane's weight row: header d, dmin and the 6-bit scales / mins (GGUF Q4_K packing)
     const u32x4 hd = *reinterpret_cast<const u32x4*>(&T.w[nl][0]);
     uint32_t scv[8], mvv[4];
@@ -229,7 +235,7 @@ __global__ void __launch_bounds__(kQ4Threads) gemm_q4k_kernel(const uint8_t* __r
       }
     }
     // stage b + 1 goes to the buffer every wave finished reading before the last barrier
-    if (b + 1 < nb) q4k_store(R, S[(b + 1) & 1]);
+    if (b + 1 < b1) q4k_store(R, S[(b + 1 - b0) & 1]);
     __syncthreads();
   }
   // store: for each v, the 32 lanes of a half-wave write 32 consecutive floats of one row
@@ -239,8 +245,16 @@ __global__ void __launch_bounds__(kQ4Threads) gemm_q4k_kernel(const uint8_t* __r
 #pragma unroll
     for (int v = 0; v < 16; v++) {
       const int m = m0 + 64 * wm + 32 * mt + 8 * (v >> 2) + 4 * lh + (v & 3);
-      if (m < M) y[int64_t(m) * N + n] = acc[mt][v];
+      if (m < M) {
+        if constexpr (SPLIT) atomicAdd(&y[int64_t(m) * N + n], acc[mt][v]);
+        else y[int64_t(m) * N + n] = acc[mt][v];
+      }
     }
+}
+
+__global__ void __launch_bounds__(256) zero_f32_kernel(float* __restrict__ y, int64_t n) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+    y[i] = 0.f;
 }
 
 // ---------------------------------------------------------------- int8 x int8 -> int32
@@ -690,14 +704,31 @@ int launch_gemm(int quant, const void* w_dev, int64_t n_in, int64_t n_out, const
   }
   if ((quant == JERO_Q4_K || quant == JERO_Q4_K_R) && n_out % kGemmBN == 0) {
     const int tiles = gemm_tiles(m, n_out);
-    if (quant == JERO_Q4_K)
-      hipLaunchKernelGGL(gemm_q4k_kernel<false>, dim3(unsigned(tiles)), dim3(kQ4Threads), 0, s,
-                         static_cast<const uint8_t*>(w_dev), row_bytes(quant, n_in),
-                         static_cast<const uint8_t*>(xq_dev), xrb, int(m), int(n_out), int(n_in / 256), y_dev);
-    else
-      hipLaunchKernelGGL(gemm_q4k_kernel<true>, dim3(unsigned(tiles)), dim3(kQ4Threads), 0, s,
-                         static_cast<const uint8_t*>(w_dev), row_bytes(quant, n_in),
-                         static_cast<const uint8_t*>(xq_dev), xrb, int(m), int(n_out), int(n_in / 256), y_dev);
+    const int nb = int(n_in / 256);
+    // at most half the CUs busy (one 115 KB workgroup per CU): two workgroups per tile, one per
+    // half of K, adding into a zeroed output
+    const bool split = nb >= 2 && 2 * tiles <= device_info().cus;
+    const uint8_t* wb = static_cast<const uint8_t*>(w_dev);
+    const uint8_t* xb = static_cast<const uint8_t*>(xq_dev);
+    const int64_t wrb = row_bytes(quant, n_in);
+    if (split) {
+      hipLaunchKernelGGL(zero_f32_kernel, dim3(unsigned(std::min<int64_t>((m * n_out + 255) / 256, 4096))), dim3(256),
+                         0, s, y_dev, m * n_out);
+      int rc = check_launch("gemm q4_k zero");
+      if (rc) return rc;
+      if (quant == JERO_Q4_K)
+        hipLaunchKernelGGL((gemm_q4k_kernel<false, true>), dim3(unsigned(2 * tiles)), dim3(kQ4Threads), 0, s, wb, wrb,
+                           xb, xrb, int(m), int(n_out), nb, y_dev);
+      else
+        hipLaunchKernelGGL((gemm_q4k_kernel<true, true>), dim3(unsigned(2 * tiles)), dim3(kQ4Threads), 0, s, wb, wrb,
+                           xb, xrb, int(m), int(n_out), nb, y_dev);
+    } else if (quant == JERO_Q4_K) {
+      hipLaunchKernelGGL((gemm_q4k_kernel<false, false>), dim3(unsigned(tiles)), dim3(kQ4Threads), 0, s, wb, wrb, xb,
+                         xrb, int(m), int(n_out), nb, y_dev);
+    } else {
+      hipLaunchKernelGGL((gemm_q4k_kernel<true, false>), dim3(unsigned(tiles)), dim3(kQ4Threads), 0, s, wb, wrb, xb,
+                         xrb, int(m), int(n_out), nb, y_dev);
+    }
     return check_launch("gemm q4_k");
   }
   // other formats and shapes: one GEMV per activation row (each row is matvec_any of x_m)

@@ -439,61 +439,82 @@ size_t q6k_planes_bytes(int64_t n_in, int64_t n_out) {
   return size_t(2 * n_out * n_in) + size_t(4 * n_out * (n_in / 256));
 }
 
-// Byte `off` (0..209, GGUF block order: ql[128] qh[64] scales[16] d) of block (r, b).
-__device__ __forceinline__ uint8_t q6k_byte(const uint8_t* __restrict__ p, bool planar, int64_t N, int nb, int64_t r,
-                                            int b, int off) {
-  if (!planar) return p[(r * nb + b) * 210 + off];
+// Address of byte `off` (0..209, GGUF block order: ql[128] qh[64] scales[16] d) of block
+// (r, b), in the GGUF bytes or the JERO_Q6_K_R planes.  A 16-byte run of ql or qh starting at a
+// multiple of 16 stays contiguous in both.
+__device__ __forceinline__ const uint8_t* q6k_at(const uint8_t* __restrict__ p, bool planar, int64_t N, int nb,
+                                                 int64_t r, int b, int off) {
+  if (!planar) return p + (r * nb + b) * 210 + off;
   const int U = 4 * nb;
   const int64_t plane = N * int64_t(U) * 16;
   const int64_t u0 = r * U + 4 * b;
   if (off < 128) {  // ql: lo plane (bytes 0..31 of each 64), hi plane (32..63)
     const int n = off >> 6, rem = off & 63, which = rem >> 5, j = (rem >> 4) & 1, i = rem & 15;
-    return p[which * plane + (u0 + 2 * n + j) * 16 + i];
+    return p + which * plane + (u0 + 2 * n + j) * 16 + i;
   }
   if (off < 192) {  // qh
     const int o = off - 128, n = o >> 5, j = (o >> 4) & 1, i = o & 15;
-    return p[2 * plane + (u0 + 2 * n + j) * 16 + i];
+    return p + 2 * plane + (u0 + 2 * n + j) * 16 + i;
   }
   if (off < 208) {  // scales: byte 8 n + j + 2 k -> unit 2 n + j, byte k
     const int o = off - 192, n = o >> 3, j = o & 1, k = (o & 7) >> 1;
-    return p[3 * plane + (u0 + 2 * n + j) * 4 + k];
+    return p + 3 * plane + (u0 + 2 * n + j) * 4 + k;
   }
-  return p[3 * plane + N * int64_t(U) * 4 + (r * nb + b) * 2 + (off - 208)];
+  return p + 3 * plane + N * int64_t(U) * 4 + (r * nb + b) * 2 + (off - 208);
 }
 
-// One thread per 4 consecutive weights of a block: w = sc * (q6 - 32) split into the planes (the
+// One thread per 16 consecutive weights of a block: w = sc * (q6 - 32) split into the planes (the
 // ggml Q6_K element order: element e of the block is pair half n = e / 128, l = e % 32, quarter
 // (e % 128) / 32: low or high nibble of ql[64 n + l (+ 32 for odd quarters)], 2 bits of
-// qh[32 n + l] at 2 * quarter, scale 8 n + l / 16 + 2 * quarter).
+// qh[32 n + l] at 2 * quarter, scale 8 n + l / 16 + 2 * quarter; the 16 weights share n, the
+// quarter and the scale, and read one 16-byte run of ql and one of qh).  GGUF blocks are only
+// 2-byte aligned, so their runs are read as bytes.
 __global__ void __launch_bounds__(256) q6k_planes_kernel(const uint8_t* __restrict__ src, int planar, int64_t N,
                                                          int nb, int8_t* __restrict__ hi, int8_t* __restrict__ lo,
                                                          float* __restrict__ dout) {
   const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= N * nb * 64) return;
-  const int g = int(t & 63);
-  const int64_t rb = t >> 6, r = rb / nb;
+  if (t >= N * nb * 16) return;
+  const int g = int(t & 15);
+  const int64_t rb = t >> 4, r = rb / nb;
   const int b = int(rb % nb);
-  const int e0 = 4 * g, n = e0 >> 7, quarter = (e0 & 127) >> 5;
-  const int sc = int(int8_t(q6k_byte(src, planar, N, nb, r, b, 192 + 8 * n + (e0 & 31) / 16 + 2 * quarter)));
-  uint32_t ph = 0, pl = 0;
+  const int e0 = 16 * g, n = e0 >> 7, quarter = (e0 & 127) >> 5, l0 = e0 & 31;
+  const int sc = int(int8_t(*q6k_at(src, planar, N, nb, r, b, 192 + 8 * n + l0 / 16 + 2 * quarter)));
+  const uint8_t* qlp = q6k_at(src, planar, N, nb, r, b, 64 * n + l0 + (quarter & 1) * 32);
+  const uint8_t* qhp = q6k_at(src, planar, N, nb, r, b, 128 + 32 * n + l0);
+  uint32_t ql[4], qh[4];
+  if (planar) {
+    const u32x4 a = ld4(qlp), c = ld4(qhp);
+    ql[0] = a.x, ql[1] = a.y, ql[2] = a.z, ql[3] = a.w;
+    qh[0] = c.x, qh[1] = c.y, qh[2] = c.z, qh[3] = c.w;
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      ql[k] = uint32_t(qlp[4 * k]) | (uint32_t(qlp[4 * k + 1]) << 8) | (uint32_t(qlp[4 * k + 2]) << 16) |
+              (uint32_t(qlp[4 * k + 3]) << 24);
+      qh[k] = uint32_t(qhp[4 * k]) | (uint32_t(qhp[4 * k + 1]) << 8) | (uint32_t(qhp[4 * k + 2]) << 16) |
+              (uint32_t(qhp[4 * k + 3]) << 24);
+    }
+  }
+  uint32_t ph[4], pl[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const int l = (e0 + k) & 31;
-    const uint32_t qlb = q6k_byte(src, planar, N, nb, r, b, 64 * n + l + (quarter & 1) * 32);
-    const uint32_t qhb = q6k_byte(src, planar, N, nb, r, b, 128 + 32 * n + l);
-    const int q6 = int(((quarter >= 2 ? qlb >> 4 : qlb) & 15u) | (((qhb >> (2 * quarter)) & 3u) << 4));
-    const int w = sc * (q6 - 32);
-    const int h = (w + 64) >> 7;
-    ph |= uint32_t(uint8_t(int8_t(h))) << (8 * k);
-    pl |= uint32_t(uint8_t(int8_t(w - 128 * h))) << (8 * k);
+    ph[k] = pl[k] = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const uint32_t qlb = byte_of(ql[k], e), qhb = byte_of(qh[k], e);
+      const int q6 = int(((quarter >= 2 ? qlb >> 4 : qlb) & 15u) | (((qhb >> (2 * quarter)) & 3u) << 4));
+      const int w = sc * (q6 - 32);
+      const int h = (w + 64) >> 7;
+      ph[k] |= uint32_t(uint8_t(int8_t(h))) << (8 * e);
+      pl[k] |= uint32_t(uint8_t(int8_t(w - 128 * h))) << (8 * e);
+    }
   }
-  const int64_t K = int64_t(nb) * 256;
-  *reinterpret_cast<uint32_t*>(hi + r * K + int64_t(b) * 256 + e0) = ph;
-  *reinterpret_cast<uint32_t*>(lo + r * K + int64_t(b) * 256 + e0) = pl;
+  const int64_t K = int64_t(nb) * 256, o = r * K + int64_t(b) * 256 + e0;
+  *reinterpret_cast<u32x4*>(hi + o) = u32x4{ph[0], ph[1], ph[2], ph[3]};
+  *reinterpret_cast<u32x4*>(lo + o) = u32x4{pl[0], pl[1], pl[2], pl[3]};
   if (g == 0) {
-    const uint32_t dbits = uint32_t(q6k_byte(src, planar, N, nb, r, b, 208)) |
-                           (uint32_t(q6k_byte(src, planar, N, nb, r, b, 209)) << 8);
-    dout[r * nb + b] = float(__builtin_bit_cast(_Float16, uint16_t(dbits)));
+    const uint8_t* dp = q6k_at(src, planar, N, nb, r, b, 208);
+    dout[r * nb + b] = float(__builtin_bit_cast(_Float16, uint16_t(uint32_t(dp[0]) | (uint32_t(dp[1]) << 8))));
   }
 }
 
@@ -610,7 +631,7 @@ int launch_q6k_planes(int quant, const void* w, int64_t n_in, int64_t n_out, voi
   int8_t* hi = static_cast<int8_t*>(planes);
   int8_t* lo = hi + n_out * n_in;
   float* d = reinterpret_cast<float*>(lo + n_out * n_in);
-  const int64_t threads = n_out * nb * 64;
+  const int64_t threads = n_out * nb * 16;
   hipLaunchKernelGGL(q6k_planes_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s,
                      static_cast<const uint8_t*>(w), quant == JERO_Q6_K_R ? 1 : 0, n_out, nb, hi, lo, d);
   return check_launch("q6k planes");

@@ -342,7 +342,9 @@ int jero_hip_model_status(jero_model *model, void *stream);
  * attention causal over the ring up to its own position -- and leave the state n decode steps
  * would leave: the n K/V rows in the ring, the last token's logits, its greedy next token and
  * position pos0 + n.  pos0 + n <= kv_capacity, else ContextLengthExceeded (as engine.rs:727
- * rejects a prompt past n_ctx).  Allocates its row buffers on first use (held by the model).
+ * rejects a prompt past n_ctx).  Allocates its row buffers on first use, and from prompts of 8
+ * tokens builds the exact int8 planes of each Q6_K tensor for the GEMM (2.3x the tensor's bytes);
+ * both are held by the model until jero_hip_model_destroy.
  * With a trace set (jero_hip_model_trace, n * jero_hip_model_trace_bytes bytes or more), token t's
  * trace in the decode step's layout lands at t * jero_hip_model_trace_bytes; the head's fields
  * only for the last token. */

@@ -134,8 +134,9 @@ int jero_hip_matvec_partials(int quant, const void *w_dev, size_t w_bytes, int64
  * &QuantizedActQ8) (src/weights.rs:1416-1426).  xq_dev: m rows of jero_hip_row_bytes(act, n_in)
  * bytes (jero_hip_quantize_act with m rows); y_dev: [m][n_out] f32.  Q4_K / Q4_K_R with n_out
  * a multiple of 128 run the int8-MFMA kernel; Q6_K / Q6_K_R from 8 rows run an int8-MFMA kernel
- * over the tensor's two exact int8 planes, built for the call in the library workspace (2 bytes
- * per weight); other formats and shapes run one GEMV per row. */
+ * over the tensor's two exact int8 planes, built for the call in the library-owned per-device
+ * workspace (2 bytes per weight), so such calls must not overlap on one device; other formats and
+ * shapes run one GEMV per row. */
 int jero_hip_gemm(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
                   const void *xq_dev, int64_t m, float *y_dev, void *stream);
 

@@ -47,6 +47,8 @@ typedef enum jero_quant {
   JERO_Q4_K_T = 113, /* stacked expert Q4_K re-laid out by jero_hip_repack_experts (16-row tiles) */
   JERO_Q6_K_R = 114, /* Q6_K bytes re-laid out by jero_hip_repack into aligned planes (same size) */
   JERO_Q6_K_T = 115, /* stacked expert Q6_K re-laid out by jero_hip_repack_experts (16-row tiles) */
+  JERO_Q4_K_G = 116, /* Q4_K bytes in the GEMM's fragment order, by jero_hip_repack_gemm (GEMM only) */
+  JERO_Q6_K_P = 117, /* Q6_K as exact int8 planes, by jero_hip_repack_gemm (GEMM only) */
   JERO_ACT_Q8 = 100 /* activation blocks for Q8_0 / Q4_0 weights: f32 d, i8 q[32] (36 B) */
 } jero_quant;
 
@@ -139,6 +141,22 @@ int jero_hip_matvec_partials(int quant, const void *w_dev, size_t w_bytes, int64
  * shapes run one GEMV per row. */
 int jero_hip_gemm(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
                   const void *xq_dev, int64_t m, float *y_dev, void *stream);
+
+/* Load-time re-layout of a Q4_K / Q6_K tensor (GGUF bytes or JERO_Q4_K_R / JERO_Q6_K_R) for
+ * jero_hip_gemm, the RepackedWeight role of repack_tensor_parallel (src/weights.rs:914-955) for
+ * the prefill.  Q4_K -> JERO_Q4_K_G: the same bytes regrouped per 32-row tile and 256-block in
+ * the order of the int8-MFMA fragments (the same size as the Q4_K tensor for n_out a multiple of
+ * 32).  Q6_K -> JERO_Q6_K_P: every weight as the exact integer sc*(q6-32) under the block's d,
+ * split into two int8 planes (128*hi + lo) in the fragment order, plus d as f32 (2 bytes per
+ * weight and 4 per 256-block of a row: about 2.3x the Q6_K bytes).  Rows are padded to a
+ * multiple of 32.  jero_hip_gemm_layout_bytes(quant, n_in, n_out) bytes (n_in a multiple of 256;
+ * 0 for other formats or shapes).  dst_dev (16-byte aligned, dst_bytes bytes) is then passed to
+ * jero_hip_gemm as *dst_quant with the same n_in and n_out and w_bytes = the layout's size, and
+ * computes what the source tensor computes (the GEMV of each activation row); the GEMV entry
+ * points reject these formats. */
+size_t jero_hip_gemm_layout_bytes(int quant, int64_t n_in, int64_t n_out);
+int jero_hip_repack_gemm(int quant, const void *src_dev, size_t src_bytes, int64_t n_in, int64_t n_out,
+                         void *dst_dev, size_t dst_bytes, int *dst_quant, void *stream);
 
 /* The exact integer product of ForwardExec::matmul (src/forward.rs:555-655) -> matmul_rows
  * (:763-811) -> gemm_i8_ime / gemm_i8_vector: out[m][n] = sum_k x[m][k] * w[n][k] in int32.

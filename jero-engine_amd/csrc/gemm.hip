@@ -426,18 +426,24 @@ __global__ void __launch_bounds__(256) pack_tiles_kernel(const int8_t* __restric
   dst[o] = r < rows ? src[r * K + int64_t(kc) * kTileK + kk] : int8_t(0);
 }
 
-// ---------------------------------------------------------------- Q6_K x Q8_K on int8 MFMA
+// ---------------------------------------------------------------- GEMM layouts: Q4_K_G and Q6_K_P
 
 int gemm_tiles(int64_t M, int64_t N);
 
-// A Q6_K weight is d * sc * (q6 - 32) with the sub-block scale sc an int8 and q6 in 0..63, so
-// w = sc * (q6 - 32) is an exact integer in [-4064, 4096]: w = 128 hi + lo with hi in [-32, 32]
-// and lo in [-64, 63] gives two int8 planes whose int8 products sum exactly (per 256-block
-// |sum hi q8| < 2^21, |sum lo q8| < 2^22, and 128 |sum hi q8| + |sum lo q8| < 2^31).  The planes are built once from the tensor (GGUF
-// Q6_K or the JERO_Q6_K_R device layout): hi [N][K] int8, lo [N][K] int8, then d [N][K / 256] f32.
-size_t q6k_planes_bytes(int64_t n_in, int64_t n_out) {
-  return size_t(2 * n_out * n_in) + size_t(4 * n_out * (n_in / 256));
-}
+// Two load-time layouts feed one kernel structure (a workgroup of four waves owns 64 tokens x 128
+// weight rows, each wave one 32-row tile, its weight fragments loaded straight into registers in
+// 1 KB runs, the activations shared through LDS):
+//   JERO_Q4_K_G: the Q4_K bytes regrouped per (32-row tile, block) in the order of the MFMA
+//     fragments, same size; the kernel expands each fragment in registers to the two exact int8
+//     planes of the sub-block scale sc = 8 a + b (a, b in 0..7): a * q4 and b * q4, both <= 105.
+//   JERO_Q6_K_P: a Q6_K weight is d * sc * (q6 - 32) with the int8 sub-block scale sc and q6 in
+//     0..63, so w = sc * (q6 - 32) is an exact integer in [-4064, 4096]; w = 128 hi + lo with
+//     hi = (w + 64) >> 7 in [-32, 32] and lo in [-64, 63] gives two int8 planes stored expanded
+//     (2 bytes per weight): 6-bit weights with signed int8 scales cost more to expand per use
+//     than to read.  Per 256-block the int8 products add up exactly: 128 (hi . q8) + (lo . q8) =
+//     w . q8 and |w . q8| <= 256 * 4096 * 128 < 2^31.
+// Both are built once per tensor (GGUF bytes or the _R device layouts) and rows past n_out are
+// zero (n_out is padded to a multiple of 32).
 
 // Address of byte `off` (0..209, GGUF block order: ql[128] qh[64] scales[16] d) of block
 // (r, b), in the GGUF bytes or the JERO_Q6_K_R planes.  A 16-byte run of ql or qh starting at a
@@ -463,191 +469,375 @@ __device__ __forceinline__ const uint8_t* q6k_at(const uint8_t* __restrict__ p, 
   return p + 3 * plane + N * int64_t(U) * 4 + (r * nb + b) * 2 + (off - 208);
 }
 
-// One thread per 16 consecutive weights of a block: w = sc * (q6 - 32) split into the planes (the
-// ggml Q6_K element order: element e of the block is pair half n = e / 128, l = e % 32, quarter
-// (e % 128) / 32: low or high nibble of ql[64 n + l (+ 32 for odd quarters)], 2 bits of
-// qh[32 n + l] at 2 * quarter, scale 8 n + l / 16 + 2 * quarter; the 16 weights share n, the
-// quarter and the scale, and read one 16-byte run of ql and one of qh).  GGUF blocks are only
-// 2-byte aligned, so their runs are read as bytes.
-__global__ void __launch_bounds__(256) q6k_planes_kernel(const uint8_t* __restrict__ src, int planar, int64_t N,
-                                                         int nb, int8_t* __restrict__ hi, int8_t* __restrict__ lo,
-                                                         float* __restrict__ dout) {
+// Scale and min of sub-block sb from a Q4_K block header h (d | dmin, then the 12 packed scale
+// bytes, GGUF packing): sub-blocks 0..3 in the low 6 bits of bytes sb and sb + 4, sub-blocks 4..7
+// from the nibbles of byte sb + 4 and the top bits of bytes sb - 4 and sb.
+__device__ __forceinline__ void q4k_scale_min_of(const u32x4& h, int sb, int& sc, int& m) {
+  const uint32_t jj = uint32_t(sb & 3);
+  const uint32_t a = byte_of(h.y, jj), bb = byte_of(h.z, jj), c = byte_of(h.w, jj);
+  sc = int(sb < 4 ? a & 63u : (c & 15u) | ((a >> 6) << 4));
+  m = int(sb < 4 ? bb & 63u : (c >> 4) | ((bb >> 6) << 4));
+}
+
+// ---- JERO_Q4_K_G.  A record (4608 bytes, one 32-row tile and one block):
+//   qs [4 pairs i][64 lanes][16 bytes]: lane (r, h) holds qs bytes 32 i + 16 h .. + 16 of row r of
+//     the tile: its low nibbles are elements 16 h .. + 16 of sub-block 2 i, its high nibbles the
+//     same elements of sub-block 2 i + 1 (one lane's B fragment of both, before scaling);
+//   headers [32 rows][16 bytes]: d, dmin and the 12 packed scale bytes of row r.
+constexpr int kQ4gRec = 4 * 1024 + 32 * 16;
+
+// ---- JERO_Q6_K_P.  A record (16 512 bytes, one 32-row tile and one block):
+//   planes [8 K steps s][2: hi, lo][64 lanes][16 bytes]: lane (r, h) holds row r of the tile at
+//     elements 32 s + 16 h .. + 16 of the block (the B operand of v_mfma_i32_32x32x32_i8);
+//   d [32] f32.
+constexpr int kQ6pPlanes = 8 * 2 * 64 * 16;
+constexpr int kQ6pRec = kQ6pPlanes + 32 * 4;
+
+static bool is_q4k(int quant) { return quant == JERO_Q4_K || quant == JERO_Q4_K_R; }
+static bool is_q6k(int quant) { return quant == JERO_Q6_K || quant == JERO_Q6_K_R; }
+
+size_t gemm_layout_bytes(int quant, int64_t n_in, int64_t n_out) {
+  if (!is_q4k(quant) && !is_q6k(quant)) return 0;
+  return size_t((n_out + 31) / 32) * size_t(n_in / 256) * size_t(is_q4k(quant) ? kQ4gRec : kQ6pRec);
+}
+
+// One thread per 16-byte piece of a Q4_K_G record (288 per record: 256 qs pieces, 32 headers).
+__global__ void __launch_bounds__(256) q4kg_kernel(const uint8_t* __restrict__ src, int planar, int64_t N,
+                                                   int64_t tiles, int nb, uint8_t* __restrict__ dst) {
   const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= N * nb * 16) return;
-  const int g = int(t & 15);
-  const int64_t rb = t >> 4, r = rb / nb;
-  const int b = int(rb % nb);
-  const int e0 = 16 * g, n = e0 >> 7, quarter = (e0 & 127) >> 5, l0 = e0 & 31;
-  const int sc = int(int8_t(*q6k_at(src, planar, N, nb, r, b, 192 + 8 * n + l0 / 16 + 2 * quarter)));
-  const uint8_t* qlp = q6k_at(src, planar, N, nb, r, b, 64 * n + l0 + (quarter & 1) * 32);
-  const uint8_t* qhp = q6k_at(src, planar, N, nb, r, b, 128 + 32 * n + l0);
-  uint32_t ql[4], qh[4];
-  if (planar) {
-    const u32x4 a = ld4(qlp), c = ld4(qhp);
-    ql[0] = a.x, ql[1] = a.y, ql[2] = a.z, ql[3] = a.w;
-    qh[0] = c.x, qh[1] = c.y, qh[2] = c.z, qh[3] = c.w;
+  if (t >= tiles * nb * 288) return;
+  const int c = int(t % 288);
+  const int64_t tb = t / 288;
+  const int b = int(tb % nb);
+  const int U = 4 * nb;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (c < 256) {  // qs piece p = 2 i + h of row r (Q4_K_R: run p & 1, unit 4 b + p / 2)
+    const int i = c >> 6, lane = c & 63, h = lane >> 5, p = 2 * i + h;
+    const int64_t r = (tb / nb) * 32 + (lane & 31);
+    if (r < N) {
+      const uint8_t* rp = src + r * int64_t(nb) * 144;
+      v = ld4(planar ? rp + (p & 1) * U * 16 + (4 * b + (p >> 1)) * 16 : rp + int64_t(b) * 144 + 16 + 16 * p);
+    }
   } else {
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      ql[k] = uint32_t(qlp[4 * k]) | (uint32_t(qlp[4 * k + 1]) << 8) | (uint32_t(qlp[4 * k + 2]) << 16) |
-              (uint32_t(qlp[4 * k + 3]) << 24);
-      qh[k] = uint32_t(qhp[4 * k]) | (uint32_t(qhp[4 * k + 1]) << 8) | (uint32_t(qhp[4 * k + 2]) << 16) |
-              (uint32_t(qhp[4 * k + 3]) << 24);
+    const int64_t r = (tb / nb) * 32 + (c - 256);
+    if (r < N) {
+      const uint8_t* rp = src + r * int64_t(nb) * 144;
+      v = ld4(planar ? rp + U * 32 + b * 16 : rp + int64_t(b) * 144);
     }
   }
-  uint32_t ph[4], pl[4];
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    ph[k] = pl[k] = 0;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const uint32_t qlb = byte_of(ql[k], e), qhb = byte_of(qh[k], e);
-      const int q6 = int(((quarter >= 2 ? qlb >> 4 : qlb) & 15u) | (((qhb >> (2 * quarter)) & 3u) << 4));
-      const int w = sc * (q6 - 32);
-      const int h = (w + 64) >> 7;
-      ph[k] |= uint32_t(uint8_t(int8_t(h))) << (8 * e);
-      pl[k] |= uint32_t(uint8_t(int8_t(w - 128 * h))) << (8 * e);
-    }
-  }
-  const int64_t K = int64_t(nb) * 256, o = r * K + int64_t(b) * 256 + e0;
-  *reinterpret_cast<u32x4*>(hi + o) = u32x4{ph[0], ph[1], ph[2], ph[3]};
-  *reinterpret_cast<u32x4*>(lo + o) = u32x4{pl[0], pl[1], pl[2], pl[3]};
-  if (g == 0) {
-    const uint8_t* dp = q6k_at(src, planar, N, nb, r, b, 208);
-    dout[r * nb + b] = float(__builtin_bit_cast(_Float16, uint16_t(uint32_t(dp[0]) | (uint32_t(dp[1]) << 8))));
-  }
+  *reinterpret_cast<u32x4*>(dst + tb * kQ4gRec + int64_t(c) * 16) = v;
 }
 
-constexpr int kQ6pThreads = 512;  // 8 waves
-constexpr int kQ6pBN = 64;        // weight rows per tile
+// One thread per Q6_K_P lane fragment: thread (tile, block b, K step s, lane (i, h)) expands the
+// 16 consecutive weights 16 g .. + 16, g = 2 s + h, of row 32 tile + i into its 16-byte piece of
+// each plane, so a wave writes 1 KB runs; the threads of step 0 and h = 0 also write the row's d.
+// The element order is ggml's: element 128 n + 32 k + l is the low (k < 2) or high nibble of
+// ql[64 n + l + 32 (k & 1)] with bits 2 k of qh[32 n + l], scale 8 n + l / 16 + 2 k.  GGUF Q6_K
+// blocks are only 2-byte aligned, so their runs are read as bytes.
+__global__ void __launch_bounds__(256) q6kp_kernel(const uint8_t* __restrict__ src, int planar, int64_t N,
+                                                   int64_t tiles, int nb, uint8_t* __restrict__ dst) {
+  const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= tiles * nb * 512) return;
+  const int lane = int(t & 63), s = int((t >> 6) & 7);
+  const int64_t tb = t >> 9;
+  const int64_t r = (tb / nb) * 32 + (lane & 31);
+  const int b = int(tb % nb), h = lane >> 5, g = 2 * s + h;
+  uint8_t* rec = dst + tb * int64_t(kQ6pRec);
+  uint32_t ph[4] = {0u, 0u, 0u, 0u}, pl[4] = {0u, 0u, 0u, 0u};
+  float d = 0.f;
+  if (r < N) {
+    const int e0 = 16 * g, n = e0 >> 7, quarter = (e0 & 127) >> 5, l0 = e0 & 31;
+    const int sc = int(int8_t(*q6k_at(src, planar, N, nb, r, b, 192 + 8 * n + l0 / 16 + 2 * quarter)));
+    const uint8_t* qlp = q6k_at(src, planar, N, nb, r, b, 64 * n + l0 + (quarter & 1) * 32);
+    const uint8_t* qhp = q6k_at(src, planar, N, nb, r, b, 128 + 32 * n + l0);
+    uint32_t ql[4], qh[4];
+    if (planar) {
+      const u32x4 a = ld4(qlp), c = ld4(qhp);
+      ql[0] = a.x, ql[1] = a.y, ql[2] = a.z, ql[3] = a.w;
+      qh[0] = c.x, qh[1] = c.y, qh[2] = c.z, qh[3] = c.w;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        ql[k] = uint32_t(qlp[4 * k]) | (uint32_t(qlp[4 * k + 1]) << 8) | (uint32_t(qlp[4 * k + 2]) << 16) |
+                (uint32_t(qlp[4 * k + 3]) << 24);
+        qh[k] = uint32_t(qhp[4 * k]) | (uint32_t(qhp[4 * k + 1]) << 8) | (uint32_t(qhp[4 * k + 2]) << 16) |
+                (uint32_t(qhp[4 * k + 3]) << 24);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t qlb = byte_of(ql[k], e), qhb = byte_of(qh[k], e);
+        const int q6 = int(((quarter >= 2 ? qlb >> 4 : qlb) & 15u) | (((qhb >> (2 * quarter)) & 3u) << 4));
+        const int w = sc * (q6 - 32);
+        const int hh = (w + 64) >> 7;
+        ph[k] |= uint32_t(uint8_t(int8_t(hh))) << (8 * e);
+        pl[k] |= uint32_t(uint8_t(int8_t(w - 128 * hh))) << (8 * e);
+      }
+    if (s == 0 && h == 0) {
+      const uint8_t* dp = q6k_at(src, planar, N, nb, r, b, 208);
+      d = float(__builtin_bit_cast(_Float16, uint16_t(uint32_t(dp[0]) | (uint32_t(dp[1]) << 8))));
+    }
+  }
+  *reinterpret_cast<u32x4*>(rec + ((2 * s) * 64 + lane) * 16) = u32x4{ph[0], ph[1], ph[2], ph[3]};
+  *reinterpret_cast<u32x4*>(rec + ((2 * s + 1) * 64 + lane) * 16) = u32x4{pl[0], pl[1], pl[2], pl[3]};
+  if (s == 0 && h == 0) reinterpret_cast<float*>(rec + kQ6pPlanes)[lane] = d;
+}
 
-struct __attribute__((aligned(16))) Q6pStage {
-  int8_t a[kGemmBM][kPlaneStride];  // q8 of the activation block
-  int8_t h[kQ6pBN][kPlaneStride];   // hi plane of the weight block
-  int8_t l[kQ6pBN][kPlaneStride];   // lo plane
-  float dx[kGemmBM];
-  float dw[kQ6pBN];
+constexpr int kGpThreads = 256;  // 4 waves, one 32-row weight tile each
+constexpr int kGpBM = 64;        // tokens per workgroup tile
+constexpr int kGpBN = 128;       // weight rows per workgroup tile
+
+// One block of the workgroup's 64 activation rows (the weights do not pass through LDS).
+struct __attribute__((aligned(16))) GpStage {
+  int8_t a[kGpBM][kPlaneStride];  // q8 (16-byte reads of 16 rows hit distinct banks)
+  _Float16 bs[kGpBM][16];         // Q4_K: the 16 bsums, as f16 (exact: |bsum| <= 2048)
+  float dx[kGpBM];
 };
 
-// The block's registers of one thread: a quarter of an activation row and a quarter of one
-// plane row (threads 0..255 the hi plane, 256..511 the lo plane).
-struct Q6pRegs {
-  u32x4 a[4], w[4];
-  float dx, dw;
+// A thread's share of one activation block: a quarter of row t / 4 (64 q8 bytes) and, by quarter,
+// the row's d (quarter 0) or half of its bsums (quarters 1, 2).
+struct GpAct {
+  u32x4 q[4];
+  u32x4 tail;
 };
 
-__device__ __forceinline__ void q6p_load(Q6pRegs& R, const uint8_t* __restrict__ xq, int64_t xrb, int m0, int M,
-                                         const int8_t* __restrict__ hi, const int8_t* __restrict__ lo,
-                                         const float* __restrict__ dw, int n0, int N, int nb, int b) {
+__device__ __forceinline__ void gp_load_act(GpAct& A, const uint8_t* __restrict__ xq, int64_t xrb, int m0, int M,
+                                            int b) {
   const int t = threadIdx.x, r = t >> 2, q = t & 3;
-  const int m = min(m0 + r, M - 1);
-  const uint8_t* xa = xq + int64_t(m) * xrb + int64_t(b) * 292;
+  const uint8_t* xa = xq + int64_t(min(m0 + r, M - 1)) * xrb + int64_t(b) * 292;
 #pragma unroll
-  for (int i = 0; i < 4; i++) R.a[i] = ld4(xa + 4 + 64 * q + 16 * i);
-  R.dx = __uint_as_float(ld1(xa));
-  const int wr = r & (kQ6pBN - 1), n = min(n0 + wr, N - 1);
-  const int8_t* plane = t < 256 ? hi : lo;
-  const uint8_t* wp = reinterpret_cast<const uint8_t*>(plane + int64_t(n) * nb * 256 + int64_t(b) * 256 + 64 * q);
-#pragma unroll
-  for (int i = 0; i < 4; i++) R.w[i] = ld4(wp + 16 * i);
-  R.dw = dw[int64_t(n) * nb + b];
+  for (int i = 0; i < 4; i++) A.q[i] = ld4(xa + 4 + 64 * q + 16 * i);
+  A.tail = ld4(xa + (q == 1 ? 260 : q == 2 ? 276 : 0));
 }
 
-__device__ __forceinline__ void q6p_store(const Q6pRegs& R, Q6pStage& S) {
-  const int t = threadIdx.x, r = t >> 2, q = t & 3, wr = r & (kQ6pBN - 1);
+template <bool BSUMS>
+__device__ __forceinline__ void gp_store_act(const GpAct& A, GpStage& S) {
+  const int t = threadIdx.x, r = t >> 2, q = t & 3;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    *reinterpret_cast<u32x4*>(&S.a[r][64 * q + 16 * i]) = R.a[i];
-    if (t < 256) *reinterpret_cast<u32x4*>(&S.h[wr][64 * q + 16 * i]) = R.w[i];
-    else *reinterpret_cast<u32x4*>(&S.l[wr][64 * q + 16 * i]) = R.w[i];
-  }
-  if (q == 0) S.dx[r] = R.dx;
-  if (q == 1 && t < 256) S.dw[wr] = R.dw;
-}
-
-// Y[m][n] = sum_b dx[m, b] d[n, b] (128 (hi . q8) + lo . q8) over the 256-blocks b: a 128 x 64
-// tile per workgroup of eight waves, each wave one 32 x 32 tile, one 32 x 32 x 32 int8 MFMA per
-// plane per K step; per block the two int32 sums meet exactly and are scaled into an f32
-// accumulator.  The next block's loads are in flight while the current one runs from LDS; at
-// 70 KB of LDS two workgroups share a CU.
-__global__ void __launch_bounds__(kQ6pThreads, 2) gemm_q6k_planes_kernel(const uint8_t* __restrict__ xq, int64_t xrb,
-                                                                          const int8_t* __restrict__ hi,
-                                                                          const int8_t* __restrict__ lo,
-                                                                          const float* __restrict__ dw, int M, int N,
-                                                                          int nb, float* __restrict__ y) {
-  __shared__ Q6pStage S;
-  const int n_tiles_m = (M + kGemmBM - 1) / kGemmBM;
-  int tm, tn;
-  gemm_tile_of(blockIdx.x, gridDim.x, n_tiles_m, tm, tn);
-  const int m0 = tm * kGemmBM, n0 = tn * kQ6pBN;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int wm = wv >> 1, wn = wv & 1;
-  const int lr = lane & 31, lh = lane >> 5;
-  v16i Ch, Cl;
-  float F[16];
+  for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(&S.a[r][64 * q + 16 * i]) = A.q[i];
+  if (q == 0) S.dx[r] = __uint_as_float(A.tail.x);
+  if constexpr (BSUMS) {
+    if (q == 1 || q == 2) {
+      const uint32_t bw[4] = {A.tail.x, A.tail.y, A.tail.z, A.tail.w};
+      uint32_t hw[4];
 #pragma unroll
-  for (int v = 0; v < 16; v++) Ch[v] = 0, Cl[v] = 0, F[v] = 0.f;
-  Q6pRegs R;
-  q6p_load(R, xq, xrb, m0, M, hi, lo, dw, n0, N, nb, 0);
-  q6p_store(R, S);
-  __syncthreads();
-  for (int b = 0; b < nb; b++) {
-    const bool more = b + 1 < nb;
-    if (more) q6p_load(R, xq, xrb, m0, M, hi, lo, dw, n0, N, nb, b + 1);
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const v4i af = *reinterpret_cast<const v4i*>(&S.a[32 * wm + lr][32 * j + 16 * lh]);
-      const v4i bh = *reinterpret_cast<const v4i*>(&S.h[32 * wn + lr][32 * j + 16 * lh]);
-      const v4i bl = *reinterpret_cast<const v4i*>(&S.l[32 * wn + lr][32 * j + 16 * lh]);
-      Ch = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bh, Ch, 0, 0, 0);
-      Cl = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bl, Cl, 0, 0, 0);
+      for (int i = 0; i < 4; i++)
+        hw[i] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(float(int16_t(bw[i] & 0xFFFFu))))) |
+                (uint32_t(__builtin_bit_cast(uint16_t, _Float16(float(int16_t(bw[i] >> 16))))) << 16);
+      *reinterpret_cast<u32x4*>(&S.bs[r][8 * (q - 1)]) = u32x4{hw[0], hw[1], hw[2], hw[3]};
     }
-    const float dn = S.dw[32 * wn + lr];
+  }
+}
+
+// Y[m][n] = sum_b dx[m,b] (d[n,b] T[m,n,b] - dmin[n,b] (m . bsums)[m,n,b]) over the 256-blocks
+// (Q6_K: no dmin term), row m of Y equal to the GEMV of x_m, with T the block's exact integer
+// sum of w . q8.  A workgroup of four waves owns a 64 (tokens) x 128 (weight rows) tile, each wave
+// the 64 tokens x one 32-row record tile (read by that wave only), as two 32-token MFMA halves.
+// Per block a wave loads its record into registers while the previous block runs (Q6_K_P: step
+// by step, each step's two 1 KB plane runs as soon as its MFMAs have read the registers), the
+// activations of the next block go through LDS (double-buffered, one barrier per block), and
+// the block's integer sums are scaled into f32 accumulators.  Q4_K_G: per K pair the lane's
+// fragment is expanded to the planes a * q4, b * q4 of both sub-blocks and T = 8 Ta + Tb; the
+// mins term is one v_mfma_f32_32x32x16_f16 over the 16 bsums (|bsum| <= 2048 and m <= 63 are
+// exact in f16, sums below 2^24).  Q6_K_P: T = 128 Th + Tl.  Two workgroups share a CU.  SPLIT:
+// two workgroups per tile, one per half of the blocks, adding into the zeroed output (two
+// addends: the same sum in either order).
+template <bool Q4, bool SPLIT>
+__global__ void __launch_bounds__(kGpThreads, 2) gemm_laid_kernel(const uint8_t* __restrict__ xq, int64_t xrb,
+                                                                   const uint8_t* __restrict__ wg, int M, int N,
+                                                                   int nb, float* __restrict__ y) {
+  __shared__ GpStage S[2];
+  constexpr int REC = Q4 ? kQ4gRec : kQ6pRec;
+  const int n_tiles_m = (M + kGpBM - 1) / kGpBM;
+  int tm, tn;
+  const int half = SPLIT ? int(blockIdx.x & 1) : 0;
+  gemm_tile_of(SPLIT ? int(blockIdx.x >> 1) : int(blockIdx.x), SPLIT ? int(gridDim.x >> 1) : int(gridDim.x),
+               n_tiles_m, tm, tn);
+  const int b0 = SPLIT ? half * ((nb + 1) / 2) : 0, b1 = SPLIT ? (half ? nb : (nb + 1) / 2) : nb;
+  const int m0 = tm * kGpBM;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lr = lane & 31, lh = lane >> 5;
+  // this wave's record tile (clamped: a tile past N computes rows that are never stored)
+  const int t32 = min(4 * tn + wv, (N + 31) / 32 - 1);
+  const uint8_t* wt = wg + int64_t(t32) * nb * REC;
+  const uint8_t* wl = wt + 16 * lane;                                  // this lane's fragments
+  const uint8_t* wr = wt + (Q4 ? 4096 + 16 * lr : kQ6pPlanes + 4 * lr);  // its row's header / d
+
+  float acc[2][16];
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-      const int ml = 32 * wm + 8 * (v >> 2) + 4 * lh + (v & 3);
-      const int tsum = Ch[v] * 128 + Cl[v];
-      F[v] = fmaf(float(tsum) * S.dx[ml], dn, F[v]);
-      Ch[v] = 0, Cl[v] = 0;
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[mt][v] = 0.f;
+
+  GpAct A;
+  constexpr int NW = Q4 ? 4 : 16;  // 16-byte fragment loads per lane and block
+  u32x4 W[NW];
+  u32x4 H = {0u, 0u, 0u, 0u};  // Q4_K_G: the row's header
+  float dq = 0.f;              // Q6_K_P: the row's d
+  auto load_w = [&](u32x4 (&Wd)[NW], int64_t o) {
+#pragma unroll
+    for (int i = 0; i < NW; i++) Wd[i] = ld4(wl + o + 1024 * i);
+  };
+  gp_load_act(A, xq, xrb, m0, M, b0);
+  load_w(W, int64_t(b0) * REC);
+  if constexpr (Q4) H = ld4(wr + int64_t(b0) * REC);
+  else dq = __uint_as_float(ld1(wr + int64_t(b0) * REC));
+  gp_store_act<Q4>(A, S[0]);
+  __syncthreads();
+  for (int b = b0; b < b1; b++) {
+    const GpStage& T = S[(b - b0) & 1];
+    const int bn = min(b + 1, b1 - 1);  // the last block reloads itself: every load unconditional
+    const int64_t on = int64_t(bn) * REC;
+    gp_load_act(A, xq, xrb, m0, M, bn);
+    float dw, dm = 0.f;
+    v8h mnf = {};
+    v16i Ch[2], Cl[2];  // Q4_K_G: the a and b planes; Q6_K_P: hi and lo
+    if constexpr (Q4) {
+      const u32x4 Wc[4] = {W[0], W[1], W[2], W[3]}, Hc = H;
+      load_w(W, on);
+      H = ld4(wr + on);
+      __builtin_amdgcn_sched_barrier(0);  // the next block's loads are issued here
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++) {  // the mins of this lane's half of the bsum groups
+        int s_, m_;
+        q4k_scale_min_of(Hc, 4 * lh + jj, s_, m_);
+        mnf[2 * jj] = mnf[2 * jj + 1] = _Float16(float(m_));
+      }
+      dw = float(__builtin_bit_cast(_Float16, uint16_t(Hc.x & 0xFFFFu)));
+      dm = float(__builtin_bit_cast(_Float16, uint16_t(Hc.x >> 16)));
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        int s0, s1, m_;
+        q4k_scale_min_of(Hc, 2 * i, s0, m_);
+        q4k_scale_min_of(Hc, 2 * i + 1, s1, m_);
+        const uint32_t raw[4] = {Wc[i].x, Wc[i].y, Wc[i].z, Wc[i].w};
+        v4i pa0, pb0, pa1, pb1;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t ql = raw[e] & 0x0F0F0F0Fu, qh = (raw[e] >> 4) & 0x0F0F0F0Fu;
+          pa0[e] = int(pk_mul(ql, uint32_t(s0) >> 3));
+          pb0[e] = int(pk_mul(ql, uint32_t(s0) & 7u));
+          pa1[e] = int(pk_mul(qh, uint32_t(s1) >> 3));
+          pb1[e] = int(pk_mul(qh, uint32_t(s1) & 7u));
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+          const v4i af0 = *reinterpret_cast<const v4i*>(&T.a[32 * mt + lr][64 * i + 16 * lh]);
+          const v4i af1 = *reinterpret_cast<const v4i*>(&T.a[32 * mt + lr][64 * i + 32 + 16 * lh]);
+          const v16i z = {};
+          Ch[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af0, pa0, i == 0 ? z : Ch[mt], 0, 0, 0);
+          Cl[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af0, pb0, i == 0 ? z : Cl[mt], 0, 0, 0);
+          Ch[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af1, pa1, Ch[mt], 0, 0, 0);
+          Cl[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af1, pb1, Cl[mt], 0, 0, 0);
+        }
+      }
+    } else {
+      __builtin_amdgcn_sched_barrier(0);  // the activation loads ahead of the weight loads
+      dw = dq;
+#pragma unroll
+      for (int s = 0; s < 8; s++) {
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+          const v4i af = *reinterpret_cast<const v4i*>(&T.a[32 * mt + lr][32 * s + 16 * lh]);
+          const v16i z = {};
+          Ch[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, __builtin_bit_cast(v4i, W[2 * s]), s == 0 ? z : Ch[mt],
+                                                         0, 0, 0);
+          Cl[mt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, __builtin_bit_cast(v4i, W[2 * s + 1]),
+                                                         s == 0 ? z : Cl[mt], 0, 0, 0);
+        }
+        W[2 * s] = ld4(wl + on + (2 * s) * 1024);
+        W[2 * s + 1] = ld4(wl + on + (2 * s + 1) * 1024);
+        // the step's loads are issued here: left to itself the scheduler sinks them all to the
+        // end of the block, and the next block's first MFMAs then wait for a full round trip
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      dq = __uint_as_float(ld1(wr + on));
+    }
+    // block b + 1 goes to the buffer every wave finished reading before the last barrier
+    gp_store_act<Q4>(A, S[(b - b0 + 1) & 1]);
+    // the block's scales: column n = lane % 32 of the tile, token rows 8 (v / 4) + 4 (lane / 32) + v % 4
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+      v16f Mn = {};
+      if constexpr (Q4) {
+        const v8h bsf = *reinterpret_cast<const v8h*>(&T.bs[32 * mt + lr][8 * lh]);
+        Mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(bsf, mnf, Mn, 0, 0, 0);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const float4 dx = *reinterpret_cast<const float4*>(&T.dx[32 * mt + 8 * g + 4 * lh]);
+        const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int v = 4 * g + e;
+          const float tv = float(Q4 ? (Ch[mt][v] << 3) + Cl[mt][v] : Ch[mt][v] * 128 + Cl[mt][v]);
+          acc[mt][v] = fmaf(dxv[e], Q4 ? dw * tv - dm * Mn[v] : dw * tv, acc[mt][v]);
+        }
+      }
     }
     __syncthreads();
-    if (more) {
-      q6p_store(R, S);
-      __syncthreads();
-    }
   }
-  const int n = n0 + 32 * wn + lr;
+  // store: for each v, the 32 lanes of a half-wave write 32 consecutive floats of one row
+  const int n = 32 * (4 * tn + wv) + lr;
 #pragma unroll
-  for (int v = 0; v < 16; v++) {
-    const int m = m0 + 32 * wm + 8 * (v >> 2) + 4 * lh + (v & 3);
-    if (m < M && n < N) y[int64_t(m) * N + n] = F[v];
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int m = m0 + 32 * mt + 8 * (v >> 2) + 4 * lh + (v & 3);
+      if (m < M && n < N) {
+        if constexpr (SPLIT) atomicAdd(&y[int64_t(m) * N + n], acc[mt][v]);
+        else y[int64_t(m) * N + n] = acc[mt][v];
+      }
+    }
+}
+
+int launch_gemm_layout(int quant, const void* w, int64_t n_in, int64_t n_out, void* dst, hipStream_t s) {
+  if (!is_q4k(quant) && !is_q6k(quant))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "gemm layout: weights must be Q4_K, Q4_K_R, Q6_K or Q6_K_R");
+  const int nb = int(n_in / 256);
+  const int64_t tiles = (n_out + 31) / 32;
+  const int planar = quant == JERO_Q4_K_R || quant == JERO_Q6_K_R;
+  const uint8_t* src = static_cast<const uint8_t*>(w);
+  uint8_t* d = static_cast<uint8_t*>(dst);
+  if (is_q4k(quant)) {
+    const int64_t threads = tiles * nb * 288;
+    hipLaunchKernelGGL(q4kg_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, src, planar, n_out, tiles,
+                       nb, d);
+  } else {
+    const int64_t threads = tiles * nb * 512;
+    hipLaunchKernelGGL(q6kp_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, src, planar, n_out, tiles,
+                       nb, d);
   }
+  return check_launch("gemm layout");
 }
 
-int launch_q6k_planes(int quant, const void* w, int64_t n_in, int64_t n_out, void* planes, hipStream_t s) {
-  if (quant != JERO_Q6_K && quant != JERO_Q6_K_R)
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, "q6k planes: weights must be Q6_K or Q6_K_R");
+int launch_gemm_laid(int laid, const void* w, int64_t n_in, int64_t n_out, const void* xq, int64_t m, float* y,
+                     hipStream_t s) {
   const int nb = int(n_in / 256);
-  int8_t* hi = static_cast<int8_t*>(planes);
-  int8_t* lo = hi + n_out * n_in;
-  float* d = reinterpret_cast<float*>(lo + n_out * n_in);
-  const int64_t threads = n_out * nb * 16;
-  hipLaunchKernelGGL(q6k_planes_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const uint8_t*>(w), quant == JERO_Q6_K_R ? 1 : 0, n_out, nb, hi, lo, d);
-  return check_launch("q6k planes");
-}
-
-int launch_gemm_q6k_planes(const void* planes, int64_t n_in, int64_t n_out, const void* xq, int64_t m, float* y,
-                           hipStream_t s) {
-  const int nb = int(n_in / 256);
-  const int8_t* hi = static_cast<const int8_t*>(planes);
-  const int8_t* lo = hi + n_out * n_in;
-  const float* d = reinterpret_cast<const float*>(lo + n_out * n_in);
-  const int64_t tiles = ((m + kGemmBM - 1) / kGemmBM) * ((n_out + kQ6pBN - 1) / kQ6pBN);
-  hipLaunchKernelGGL(gemm_q6k_planes_kernel, dim3(unsigned(tiles)), dim3(kQ6pThreads), 0, s,
-                     static_cast<const uint8_t*>(xq), row_bytes(JERO_Q8_K, n_in), hi, lo, d, int(m), int(n_out), nb,
-                     y);
-  return check_launch("gemm q6_k planes");
+  const int64_t tiles = ((m + kGpBM - 1) / kGpBM) * ((n_out + kGpBN - 1) / kGpBN);
+  // two workgroups per CU: a grid that fills at most half of that splits K in two
+  const bool split = nb >= 2 && tiles <= device_info().cus;
+  const uint8_t* xb = static_cast<const uint8_t*>(xq);
+  const uint8_t* wb = static_cast<const uint8_t*>(w);
+  const int64_t xrb = row_bytes(JERO_Q8_K, n_in);
+  const dim3 grid(unsigned(split ? 2 * tiles : tiles)), block(kGpThreads);
+  if (split) {
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(unsigned(std::min<int64_t>((m * n_out + 255) / 256, 4096))), dim3(256), 0,
+                       s, y, m * n_out);
+    int rc = check_launch("gemm zero");
+    if (rc) return rc;
+    if (laid == JERO_Q4_K_G)
+      hipLaunchKernelGGL((gemm_laid_kernel<true, true>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y);
+    else
+      hipLaunchKernelGGL((gemm_laid_kernel<false, true>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y);
+  } else if (laid == JERO_Q4_K_G) {
+    hipLaunchKernelGGL((gemm_laid_kernel<true, false>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y);
+  } else {
+    hipLaunchKernelGGL((gemm_laid_kernel<false, false>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y);
+  }
+  return check_launch(laid == JERO_Q4_K_G ? "gemm q4_k_g" : "gemm q6_k_p");
 }
 
 int gemm_tiles(int64_t M, int64_t N) { return int(((M + kGemmBM - 1) / kGemmBM) * ((N + kGemmBN - 1) / kGemmBN)); }
@@ -709,19 +899,18 @@ using namespace jero;
 namespace jero {
 
 int launch_gemm(int quant, const void* w_dev, int64_t n_in, int64_t n_out, const void* xq_dev, int64_t m, float* y_dev,
-                hipStream_t s, const void* q6_planes) {
+                hipStream_t s, const void* laid) {
   const int act = act_format(quant);
   const int64_t xrb = row_bytes(act, n_in);
-  if ((quant == JERO_Q6_K || quant == JERO_Q6_K_R) && (q6_planes || m >= kQ6PlanesMinRows)) {
-    int rc = JERO_OK;
-    if (!q6_planes) {  // expanded into the library workspace for this call
-      void* ws = nullptr;
-      if ((rc = workspace(q6k_planes_bytes(n_in, n_out), &ws)) ||
-          (rc = launch_q6k_planes(quant, w_dev, n_in, n_out, ws, s)))
-        return rc;
-      q6_planes = ws;
-    }
-    return launch_gemm_q6k_planes(q6_planes, n_in, n_out, xq_dev, m, y_dev, s);
+  if (quant == JERO_Q4_K_G || quant == JERO_Q6_K_P) return launch_gemm_laid(quant, w_dev, n_in, n_out, xq_dev, m, y_dev, s);
+  if ((is_q4k(quant) || is_q6k(quant)) && laid)
+    return launch_gemm_laid(is_q4k(quant) ? JERO_Q4_K_G : JERO_Q6_K_P, laid, n_in, n_out, xq_dev, m, y_dev, s);
+  if (is_q6k(quant) && m >= kLaidMinRows) {  // the Q6_K_P planes built into the library workspace for this call
+    void* ws = nullptr;
+    int rc = workspace(gemm_layout_bytes(quant, n_in, n_out), &ws);
+    if (!rc) rc = launch_gemm_layout(quant, w_dev, n_in, n_out, ws, s);
+    if (rc) return rc;
+    return launch_gemm_laid(JERO_Q6_K_P, ws, n_in, n_out, xq_dev, m, y_dev, s);
   }
   if ((quant == JERO_Q4_K || quant == JERO_Q4_K_R) && n_out % kGemmBN == 0) {
     const int tiles = gemm_tiles(m, n_out);
@@ -763,10 +952,46 @@ int launch_gemm(int quant, const void* w_dev, int64_t n_in, int64_t n_out, const
 
 }  // namespace jero
 
+extern "C" size_t jero_hip_gemm_layout_bytes(int quant, int64_t n_in, int64_t n_out) {
+  if (n_in <= 0 || n_out <= 0 || n_in % 256 || n_in > (int64_t(1) << 30) || n_out > (int64_t(1) << 30)) return 0;
+  return jero::gemm_layout_bytes(quant, n_in, n_out);
+}
+
+extern "C" int jero_hip_repack_gemm(int quant, const void* src_dev, size_t src_bytes, int64_t n_in, int64_t n_out,
+                                    void* dst_dev, size_t dst_bytes, int* dst_quant, void* stream) {
+  if (!jero::is_q4k(quant) && !jero::is_q6k(quant))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "repack_gemm: weights must be Q4_K, Q4_K_R, Q6_K or Q6_K_R");
+  if (!src_dev || !dst_dev || !dst_quant) return fail(JERO_ERR_INVALID_ARGUMENT, "repack_gemm: null pointer");
+  const size_t need = jero_hip_gemm_layout_bytes(quant, n_in, n_out);
+  if (!need) return fail(JERO_ERR_TENSOR_BOUNDS, "repack_gemm: n_in a multiple of 256, sizes within 2^30");
+  if (uint64_t(jero::row_bytes(quant, n_in)) * uint64_t(n_out) > src_bytes)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "repack_gemm: source holds fewer bytes than the shape");
+  if (dst_bytes < need)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "repack_gemm: destination holds " + std::to_string(dst_bytes) +
+                                            " bytes, the layout needs " + std::to_string(need));
+  if ((reinterpret_cast<uintptr_t>(src_dev) & 15u) || (reinterpret_cast<uintptr_t>(dst_dev) & 15u))
+    return fail(JERO_ERR_INVALID_ARGUMENT, "repack_gemm: source and destination must be 16-byte aligned");
+  const int rc = jero::launch_gemm_layout(quant, src_dev, n_in, n_out, dst_dev, static_cast<hipStream_t>(stream));
+  if (!rc) *dst_quant = jero::is_q4k(quant) ? JERO_Q4_K_G : JERO_Q6_K_P;
+  return rc;
+}
+
 extern "C" int jero_hip_gemm(int quant, const void* w_dev, size_t w_bytes, int64_t n_in, int64_t n_out,
                              const void* xq_dev, int64_t m, float* y_dev, void* stream) {
-  int rc = check_matvec_args(quant, w_dev, w_bytes, n_in, n_out, xq_dev, y_dev);
-  if (rc) return rc;
+  if (quant == JERO_Q4_K_G || quant == JERO_Q6_K_P) {
+    const int base = quant == JERO_Q4_K_G ? JERO_Q4_K : JERO_Q6_K;
+    if (!w_dev || !xq_dev || !y_dev) return fail(JERO_ERR_INVALID_ARGUMENT, "gemm: null pointer");
+    const size_t need = jero_hip_gemm_layout_bytes(base, n_in, n_out);
+    if (!need) return fail(JERO_ERR_TENSOR_BOUNDS, "gemm: the GEMM layouts need n_in a multiple of 256, sizes within 2^30");
+    if (w_bytes < need)
+      return fail(JERO_ERR_TENSOR_BOUNDS, "gemm: the layout holds " + std::to_string(w_bytes) +
+                                              " bytes, the shape needs " + std::to_string(need));
+    if ((reinterpret_cast<uintptr_t>(w_dev) & 15u) || !jero::aligned4(xq_dev) || !jero::aligned4(y_dev))
+      return fail(JERO_ERR_INVALID_ARGUMENT, "gemm: layout 16-byte aligned, activations and output 4-byte aligned");
+  } else {
+    int rc = check_matvec_args(quant, w_dev, w_bytes, n_in, n_out, xq_dev, y_dev);
+    if (rc) return rc;
+  }
   if (m <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "gemm: no activation rows");
   if (m > (int64_t(1) << 24) || n_out > (int64_t(1) << 30))
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "gemm: m or n_out beyond the 32-bit tile indexing");

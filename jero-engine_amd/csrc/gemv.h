@@ -23,17 +23,20 @@ int check_matvec_args(int quant, const void* w, size_t w_bytes, int64_t n_in, in
 // same matrix), so its weight loads may bypass the caches (non-temporal).
 int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, float* y, int32_t* part,
                   hipStream_t s, bool once = true);
-// Y[m][n_out] for m activation rows (jero_hip_gemm after its checks): the int8-MFMA kernel for
-// Q4_K and Q4_K_R with n_out a multiple of 128; for Q6_K and Q6_K_R from kQ6PlanesMinRows rows
-// (or whenever q6_planes is given) the int8-MFMA kernel over the tensor's two int8 planes
-// (q6_planes: built by launch_q6k_planes; null: built for this call in the library workspace);
-// one GEMV per row otherwise.
-constexpr int64_t kQ6PlanesMinRows = 8;
+// Y[m][n_out] for m activation rows (jero_hip_gemm after its checks): JERO_Q4_K_G / JERO_Q6_K_P
+// (w in that GEMM layout), or Q4_K / Q4_K_R / Q6_K / Q6_K_R with their GEMM layout given
+// (laid), run the int8-MFMA kernel over the layout; Q6_K / Q6_K_R from kLaidMinRows rows build
+// the Q6_K_P planes into the library workspace for the call; Q4_K / Q4_K_R with n_out a multiple
+// of 128 run the int8-MFMA kernel over the Q4_K bytes; one GEMV per row otherwise.
+constexpr int64_t kLaidMinRows = 8;
 int launch_gemm(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, int64_t m, float* y,
-                hipStream_t s, const void* q6_planes = nullptr);
-// The int8 planes of a Q6_K / Q6_K_R tensor for the MFMA GEMM (planes: q6k_planes_bytes bytes).
-size_t q6k_planes_bytes(int64_t n_in, int64_t n_out);
-int launch_q6k_planes(int quant, const void* w, int64_t n_in, int64_t n_out, void* planes, hipStream_t s);
+                hipStream_t s, const void* laid = nullptr);
+// The GEMM layout of a Q4_K / Q4_K_R tensor (JERO_Q4_K_G) or Q6_K / Q6_K_R tensor (JERO_Q6_K_P):
+// gemm_layout_bytes bytes, 16-byte aligned (0 for other formats); and the GEMM over it.
+size_t gemm_layout_bytes(int quant, int64_t n_in, int64_t n_out);
+int launch_gemm_layout(int quant, const void* w, int64_t n_in, int64_t n_out, void* dst, hipStream_t s);
+int launch_gemm_laid(int laid, const void* w, int64_t n_in, int64_t n_out, const void* xq, int64_t m, float* y,
+                     hipStream_t s);
 // Enqueues the Q4_K -> Q4_K_R or Q6_K -> Q6_K_R re-layout (dst: 16-byte aligned, same size).
 int launch_repack(int quant, const void* src, int64_t n_in, int64_t n_out, void* dst, int* dst_quant, hipStream_t s);
 int launch_repack_experts(int quant, const void* src, int64_t n_in, int64_t n_rows, void* dst, int* dst_quant,

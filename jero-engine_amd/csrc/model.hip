@@ -80,8 +80,8 @@ struct jero_model {
   uint8_t* trace = nullptr;  // debug trace buffer of the caller (jero_hip_model_trace), or null
   size_t trace_bytes = 0;
   jero::PrefillBufs pf;
-  // int8 planes of the Q6_K tensors for the prefill GEMM, built on first use (keyed by tensor)
-  std::map<const void*, void*> q6_planes;
+  // GEMM layouts of the Q4_K / Q6_K tensors for the prefill (Q4_K_G, Q6_K_P), built on first use
+  std::map<const void*, void*> laid;
 };
 
 namespace jero {
@@ -675,21 +675,22 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
 
 namespace jero {
 
-// The int8 planes of a Q6_K tensor for the prefill GEMM (null for other formats), built on the
-// stream at first use; weights cannot change after finalize, so they stay valid.
-static int q6_planes_of(jero_model* m, const DevTensor& w, hipStream_t s, const void** out) {
+// The GEMM layout of a Q4_K / Q6_K tensor for the prefill (JERO_Q4_K_G, the Q4_K bytes in the
+// MFMA fragment order; JERO_Q6_K_P, the exact int8 planes), null for other formats; built on
+// the stream at first use.  Weights cannot change after finalize, so it stays valid.
+static int laid_of(jero_model* m, const DevTensor& w, hipStream_t s, const void** out) {
   *out = nullptr;
-  if (w.quant != JERO_Q6_K && w.quant != JERO_Q6_K_R) return JERO_OK;
-  auto it = m->q6_planes.find(w.dev);
-  if (it != m->q6_planes.end()) {
+  if (w.quant != JERO_Q4_K && w.quant != JERO_Q4_K_R && w.quant != JERO_Q6_K && w.quant != JERO_Q6_K_R) return JERO_OK;
+  auto it = m->laid.find(w.dev);
+  if (it != m->laid.end()) {
     *out = it->second;
     return JERO_OK;
   }
   void* p = nullptr;
-  int rc = dev_alloc(m, q6k_planes_bytes(w.n_in, w.n_out), &p);
-  if (!rc) rc = launch_q6k_planes(w.quant, w.dev, w.n_in, w.n_out, p, s);
+  int rc = dev_alloc(m, gemm_layout_bytes(w.quant, w.n_in, w.n_out), &p);
+  if (!rc) rc = launch_gemm_layout(w.quant, w.dev, w.n_in, w.n_out, p, s);
   if (rc) return rc;
-  m->q6_planes[w.dev] = p;
+  m->laid[w.dev] = p;
   *out = p;
   return JERO_OK;
 }
@@ -798,9 +799,9 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
         have_fmt = fmt;
         if (trace_field >= 0 && (r = snap(fld(L, trace_field), b.XQ, size_t(xrb), size_t(xrb)))) return r;
       }
-      const void* planes = nullptr;
-      if (n >= kQ6PlanesMinRows && (r = q6_planes_of(m, w, s, &planes))) return r;
-      return launch_gemm(w.quant, w.dev, k, w.n_out, b.XQ, n, out, s, planes);
+      const void* laid = nullptr;
+      if (n >= kLaidMinRows && (r = laid_of(m, w, s, &laid))) return r;
+      return launch_gemm(w.quant, w.dev, k, w.n_out, b.XQ, n, out, s, laid);
     };
     if (!l.qkv_split) {
       const int64_t w1 = l.qkv.n_out;  // Q + 2 KV, or Q + KV with V apart

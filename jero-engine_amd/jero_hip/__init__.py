@@ -17,10 +17,11 @@ LIB_PATH = os.path.normpath(os.path.join(HERE, "..", "libjero_hip.so"))
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, Q8_K, ACT_Q8, Q4_K_R, Q6_K_R = 0, 1, 2, 8, 12, 14, 15, 100, 112, 114
 Q4_K_T, Q6_K_T = 113, 115  # stacked expert tensors in 16-row tiles (repack of a 3-D tensor)
+Q4_K_G, Q6_K_P = 116, 117  # GEMM layouts (repack_gemm)
 BF16 = 30
 Q4_K_M = Q4_K  # the reference's QuantType::Q4_K_M names the Q4_K block format
 QUANT_NAMES = {F32: "F32", F16: "F16", BF16: "BF16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K", Q8_K: "Q8_K",
-               ACT_Q8: "ACT_Q8", Q4_K_R: "Q4_K_R", Q6_K_R: "Q6_K_R"}
+               ACT_Q8: "ACT_Q8", Q4_K_R: "Q4_K_R", Q6_K_R: "Q6_K_R", Q4_K_G: "Q4_K_G", Q6_K_P: "Q6_K_P"}
 KV_F32, KV_F16 = 0, 1
 
 OK = 0
@@ -69,6 +70,8 @@ _SIGS = {
     "jero_hip_gemm_i8_tiles": (_I32, [_P, _I64, _P, _I64, _I64, _I64, _P, _P]),
     "jero_hip_dequantize_rows": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, _P]),
     "jero_hip_repack": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, C.POINTER(C.c_int), _P]),
+    "jero_hip_gemm_layout_bytes": (_SZ, [_I32, _I64, _I64]),
+    "jero_hip_repack_gemm": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _SZ, C.POINTER(C.c_int), _P]),
     "jero_hip_repack_experts": (_I32, [_I32, _P, _SZ, _I64, _I64, _I64, _P, C.POINTER(C.c_int), _P]),
     "jero_hip_gqa_attention": (_I32, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I64, _F, _P, _SZ, _P]),
     "jero_hip_moe_ffn": (_I32, [_P, _P, _I64, _I64, _I32, _I32, _P, _SZ, _I32, _P, _SZ, _I32, _P, _SZ, _I64, _I64,
@@ -438,6 +441,25 @@ def repack(weights, stream=None, experts=None):
     else:
         check(lib().jero_hip_repack(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in, rows,
                                     _ptr(dst), C.byref(q), _stream(stream)))
+    return TensorView(weights.name, q.value, weights.shape, dst)
+
+
+def gemm_layout_bytes(quant, n_in, n_out):
+    return lib().jero_hip_gemm_layout_bytes(quant, n_in, n_out)
+
+
+def repack_gemm(weights, stream=None):
+    """Load-time re-layout of a Q4_K / Q6_K tensor (GGUF or the _R layouts) for the prefill GEMM
+    (the RepackedWeight role, src/weights.rs:914-955): returns a TensorView of quant Q4_K_G (the
+    Q4_K bytes in the MFMA fragment order) or Q6_K_P (exact int8 planes) for gemm()."""
+    import torch
+    n = gemm_layout_bytes(weights.quant, weights.n_in, weights.n_out)
+    if n == 0:
+        raise K3Error(10, f"repack_gemm: no GEMM layout for quant {weights.quant} at {weights.shape}")
+    dst = torch.empty(n, dtype=torch.uint8, device=weights.data.device)
+    q = C.c_int(0)
+    check(lib().jero_hip_repack_gemm(weights.quant, _ptr(weights.data), weights.nbytes(), weights.n_in,
+                                     weights.n_out, _ptr(dst), n, C.byref(q), _stream(stream)))
     return TensorView(weights.name, q.value, weights.shape, dst)
 
 

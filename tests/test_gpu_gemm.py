@@ -130,6 +130,139 @@ def test_gemm_q6k_planes_extremes(dev):
     assert rel_err(y, ref) < REL_TOL
 
 
+def layout_numpy(quant, w, k, n):
+    """The records of jero_hip_repack_gemm restated in numpy from the GGUF bytes (the layouts its
+    header documents), rows padded to a multiple of 32 with zeros.  Q4_K_G: per (32-row tile,
+    block) the qs bytes 32 i + 16 h .. + 16 of row r at lane (r, h) of pair i, then the 32 block
+    headers.  Q6_K_P: w = sc (q6 - 32) = 128 hi + lo, the planes at lane (r, h) of K step s
+    (elements 32 s + 16 h .. + 16), then d as f32."""
+    nb = k // 256
+    tiles = (n + 31) // 32
+    if quant == J.Q4_K:
+        blk = np.zeros((tiles * 32, nb, 144), np.uint8)
+        blk[:n] = w.reshape(n, nb, 144)
+        out = np.zeros((tiles, nb, 4608), np.uint8)
+        for t in range(tiles):
+            for b in range(nb):
+                rows = blk[32 * t:32 * t + 32, b]
+                for i in range(4):
+                    for h in range(2):
+                        lanes = rows[:, 16 + 32 * i + 16 * h:16 + 32 * i + 16 * h + 16]  # [32 rows][16]
+                        o = (i * 64 + 32 * h) * 16
+                        out[t, b, o:o + 512] = lanes.reshape(-1)
+                out[t, b, 4096:] = rows[:, :16].reshape(-1)
+        return out.reshape(-1)
+    blk = w.reshape(n, nb, 210)
+    wint = np.zeros((tiles * 32, nb, 256), np.int64)
+    d = np.zeros((tiles * 32, nb), np.float32)
+    for r in range(n):
+        for b in range(nb):
+            x = blk[r, b]
+            ql, qh, scales = x[:128].astype(np.int64), x[128:192].astype(np.int64), x[192:208].view(np.int8)
+            d[r, b] = x[208:210].view(np.float16)[0]
+            for e in range(256):
+                hn, rem = e // 128, e % 128
+                kq, l = rem // 32, rem % 32
+                lo4 = (ql[64 * hn + l + 32 * (kq & 1)] >> (4 * (kq >> 1))) & 15
+                h2 = (qh[32 * hn + l] >> (2 * kq)) & 3
+                wint[r, b, e] = int(scales[8 * hn + l // 16 + 2 * kq]) * ((lo4 | (h2 << 4)) - 32)
+    hi = (wint + 64) >> 7
+    lo = wint - 128 * hi
+    out = np.zeros((tiles, nb, 16512), np.uint8)
+    for t in range(tiles):
+        for b in range(nb):
+            for s_ in range(8):
+                for p, plane in enumerate((hi, lo)):
+                    for h in range(2):
+                        e0 = 32 * s_ + 16 * h
+                        frag = np.ascontiguousarray(plane[32 * t:32 * t + 32, b, e0:e0 + 16]).astype(np.int8).view(np.uint8)
+                        o = ((2 * s_ + p) * 64 + 32 * h) * 16
+                        out[t, b, o:o + 512] = frag.reshape(-1)
+            out[t, b, 16384:] = np.ascontiguousarray(d[32 * t:32 * t + 32, b]).view(np.uint8)
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("quant", [J.Q4_K, J.Q6_K])
+def test_gemm_layout_bytes(dev, quant):
+    """The GEMM layouts of GGUF bytes and of the _R device layouts equal a numpy restatement of
+    the documented records byte for byte (rows past n_out zero)."""
+    k, n = 512, 40
+    w = rand_weights(quant, n, k, 8800 + quant)
+    view = J.TensorView("w", quant, [k, n], to_dev(w, dev))
+    ref = layout_numpy(quant, w, k, n)
+    for v in (view, J.repack(view)):
+        p = J.repack_gemm(v)
+        assert p.quant == (J.Q4_K_G if quant == J.Q4_K else J.Q6_K_P)
+        assert np.array_equal(p.data.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("quant", [J.Q4_K, J.Q6_K])
+@pytest.mark.parametrize("m,k,n", [(8, 256, 64), (37, 512, 96), (128, 1024, 384), (200, 4096, 130),
+                                   (513, 2048, 256), (257, 512, 8224)])
+def test_gemm_laid_matches_oracle(dev, quant, m, k, n):
+    """jero_hip_gemm over the GEMM layouts (Q4_K_G / Q6_K_P) against the oracle: ragged token
+    tiles, n_out past the last 32-row tile, one block (no K split), the two-way K split of small
+    grids and the unsplit grid (257 x 8224: 325 tiles of 64 x 128).  The layouts of the _R tensors give the
+    same bits."""
+    print(f"gemm laid quant={quant} m={m} k={k} n={n}", flush=True)
+    w = rand_weights(quant, n, k, 7300 + quant + m + n)
+    x = rand_act(k, 7301 + m, m=m)
+    xq = J.quantize_act(J.Q8_K, to_dev(x, dev))
+    view = J.TensorView("w", quant, [k, n], to_dev(w, dev))
+    y = torch.full((m, n), float("nan"), device=dev)
+    J.gemm(J.repack_gemm(view), xq, m, y)
+    yr = torch.full((m, n), float("nan"), device=dev)
+    J.gemm(J.repack_gemm(J.repack(view)), xq, m, yr)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    assert np.array_equal(yr.cpu().numpy(), y)
+    ref = O.gemm(quant, w, k, n, xq.cpu().numpy(), m, threads=8)
+    assert np.all(np.isfinite(y))
+    assert rel_err(y, ref) < REL_TOL
+
+
+def test_gemm_laid_q4k_extremes(dev):
+    """Q4_K_G at the top of the expanded planes (scale 63 = 8 * 7 + 7, nibble 15: 105 each),
+    zero scales and mins, zero and tiny activation rows."""
+    m, k, n = 64, 1024, 128
+    w = rand_weights(J.Q4_K, n, k, 77).reshape(n * (k // 256), 144)
+    w[0::3, 4:16] = 0xFF
+    w[1::3, 4:16] = 0x00
+    w[0::5, 16:] = 0xFF
+    w = w.reshape(-1)
+    x = rand_act(k, 78, m=m)
+    x[3] = 0.0
+    x[5, :256] = 1e-30
+    xq = J.quantize_act(J.Q8_K, to_dev(x, dev))
+    view = J.TensorView("w", J.Q4_K, [k, n], to_dev(w, dev))
+    y = torch.empty((m, n), device=dev)
+    J.gemm(J.repack_gemm(view), xq, m, y)
+    ref = O.gemm(J.Q4_K, w, k, n, xq.cpu().numpy(), m, threads=8)
+    y = y.cpu().numpy()
+    assert np.all(y[3] == 0.0)
+    assert rel_err(y, ref) < REL_TOL
+
+
+def test_gemm_layout_errors(dev):
+    w = to_dev(rand_weights(J.Q4_K, 64, 256, 3), dev)
+    assert J.gemm_layout_bytes(J.Q4_K, 256, 64) == 2 * 4608 == J.row_bytes(J.Q4_K, 256) * 64
+    assert J.gemm_layout_bytes(J.Q6_K, 512, 33) == 2 * 2 * 16512
+    assert J.gemm_layout_bytes(J.Q8_0, 256, 64) == 0 and J.gemm_layout_bytes(J.Q4_K, 100, 64) == 0
+    with pytest.raises(J.K3Error) as e:
+        J.repack_gemm(J.TensorView("w", J.Q8_0, [256, 64], w))
+    assert e.value.variant == "CapabilityMismatch"
+    p = J.repack_gemm(J.TensorView("w", J.Q4_K, [256, 64], w))
+    xq = J.quantize_act(J.Q8_K, to_dev(rand_act(256, 4, m=2), dev))
+    y = torch.empty((2, 64), device=dev)
+    short = J.TensorView("w", J.Q4_K_G, [256, 64], p.data[:-16])
+    with pytest.raises(J.K3Error) as e:
+        J.gemm(short, xq, 2, y)
+    assert e.value.variant == "TensorBoundsError"
+    with pytest.raises(J.K3Error) as e:
+        J.matvec(p, xq[:J.row_bytes(J.Q8_K, 256)], y[0])
+    assert e.value.variant == "CapabilityMismatch"
+
+
 @pytest.mark.parametrize("quant,m,k,n", [(J.Q8_0, 5, 512, 96), (J.Q4_0, 3, 256, 40), (J.Q6_K, 4, 512, 64),
                                          (J.Q4_K, 3, 256, 100)])
 def test_gemm_row_path_formats(dev, quant, m, k, n):

@@ -695,10 +695,9 @@ __global__ void __launch_bounds__(kGpThreads, 2) gemm_laid_kernel(const uint8_t*
     v8h mnf = {};
     v16i Ch[2], Cl[2];  // Q4_K_G: the a and b planes; Q6_K_P: hi and lo
     if constexpr (Q4) {
-      const u32x4 Wc[4] = {W[0], W[1], W[2], W[3]}, Hc = H;
-      load_w(W, on);
+      const u32x4 Hc = H;
       H = ld4(wr + on);
-      __builtin_amdgcn_sched_barrier(0);  // the next block's loads are issued here
+      __builtin_amdgcn_sched_barrier(0);  // the activation and header loads are issued here
 #pragma unroll
       for (int jj = 0; jj < 4; jj++) {  // the mins of this lane's half of the bsum groups
         int s_, m_;
@@ -712,7 +711,8 @@ __global__ void __launch_bounds__(kGpThreads, 2) gemm_laid_kernel(const uint8_t*
         int s0, s1, m_;
         q4k_scale_min_of(Hc, 2 * i, s0, m_);
         q4k_scale_min_of(Hc, 2 * i + 1, s1, m_);
-        const uint32_t raw[4] = {Wc[i].x, Wc[i].y, Wc[i].z, Wc[i].w};
+        const uint32_t raw[4] = {W[i].x, W[i].y, W[i].z, W[i].w};
+        W[i] = ld4(wl + on + 1024 * i);  // the next block's fragment, as soon as this one is read
         v4i pa0, pb0, pa1, pb1;
 #pragma unroll
         for (int e = 0; e < 4; e++) {

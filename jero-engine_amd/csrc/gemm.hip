@@ -433,9 +433,10 @@ int gemm_tiles(int64_t M, int64_t N);
 // Two load-time layouts feed one kernel structure (a workgroup of four waves owns 64 tokens x 128
 // weight rows, each wave one 32-row tile, its weight fragments loaded straight into registers in
 // 1 KB runs, the activations shared through LDS):
-//   JERO_Q4_K_G: the Q4_K bytes regrouped per (32-row tile, block) in the order of the MFMA
-//     fragments, same size; the kernel expands each fragment in registers to the two exact int8
-//     planes of the sub-block scale sc = 8 a + b (a, b in 0..7): a * q4 and b * q4, both <= 105.
+//   JERO_Q4_K_G: the Q4_K quants regrouped per (32-row tile, block) in the order of the MFMA
+//     fragments, with the block headers' 6-bit scales and mins unpacked to bytes (11 % more than
+//     the Q4_K bytes); the kernel expands each fragment in registers to the two exact int8 planes
+//     of the sub-block scale sc = 8 a + b (a, b in 0..7): a * q4 and b * q4, both <= 105.
 //   JERO_Q6_K_P: a Q6_K weight is d * sc * (q6 - 32) with the int8 sub-block scale sc and q6 in
 //     0..63, so w = sc * (q6 - 32) is an exact integer in [-4064, 4096]; w = 128 hi + lo with
 //     hi = (w + 64) >> 7 in [-32, 32] and lo in [-64, 63] gives two int8 planes stored expanded
@@ -479,12 +480,13 @@ __device__ __forceinline__ void q4k_scale_min_of(const u32x4& h, int sb, int& sc
   m = int(sb < 4 ? bb & 63u : (c >> 4) | ((bb >> 6) << 4));
 }
 
-// ---- JERO_Q4_K_G.  A record (4608 bytes, one 32-row tile and one block):
+// ---- JERO_Q4_K_G.  A record (5120 bytes, one 32-row tile and one block):
 //   qs [4 pairs i][64 lanes][16 bytes]: lane (r, h) holds qs bytes 32 i + 16 h .. + 16 of row r of
 //     the tile: its low nibbles are elements 16 h .. + 16 of sub-block 2 i, its high nibbles the
 //     same elements of sub-block 2 i + 1 (one lane's B fragment of both, before scaling);
-//   headers [32 rows][16 bytes]: d, dmin and the 12 packed scale bytes of row r.
-constexpr int kQ4gRec = 4 * 1024 + 32 * 16;
+//   headers [2 halves h][32 rows][16 bytes]: d and dmin (the block's f16 pair), the 8 sub-block
+//     scales as bytes, then the mins of sub-blocks 4 h .. 4 h + 3 as bytes (what lane (r, h) needs).
+constexpr int kQ4gRec = 4 * 1024 + 32 * 32;
 
 // ---- JERO_Q6_K_P.  A record (16 512 bytes, one 32-row tile and one block):
 //   planes [8 K steps s][2: hi, lo][64 lanes][16 bytes]: lane (r, h) holds row r of the tile at
@@ -501,13 +503,13 @@ size_t gemm_layout_bytes(int quant, int64_t n_in, int64_t n_out) {
   return size_t((n_out + 31) / 32) * size_t(n_in / 256) * size_t(is_q4k(quant) ? kQ4gRec : kQ6pRec);
 }
 
-// One thread per 16-byte piece of a Q4_K_G record (288 per record: 256 qs pieces, 32 headers).
+// One thread per 16-byte piece of a Q4_K_G record (320 per record: 256 qs pieces, 64 headers).
 __global__ void __launch_bounds__(256) q4kg_kernel(const uint8_t* __restrict__ src, int planar, int64_t N,
                                                    int64_t tiles, int nb, uint8_t* __restrict__ dst) {
   const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= tiles * nb * 288) return;
-  const int c = int(t % 288);
-  const int64_t tb = t / 288;
+  if (t >= tiles * nb * 320) return;
+  const int c = int(t % 320);
+  const int64_t tb = t / 320;
   const int b = int(tb % nb);
   const int U = 4 * nb;
   u32x4 v = {0u, 0u, 0u, 0u};
@@ -518,11 +520,21 @@ __global__ void __launch_bounds__(256) q4kg_kernel(const uint8_t* __restrict__ s
       const uint8_t* rp = src + r * int64_t(nb) * 144;
       v = ld4(planar ? rp + (p & 1) * U * 16 + (4 * b + (p >> 1)) * 16 : rp + int64_t(b) * 144 + 16 + 16 * p);
     }
-  } else {
-    const int64_t r = (tb / nb) * 32 + (c - 256);
+  } else {  // header half h of row r, at lane r + 32 h
+    const int h = (c - 256) >> 5;
+    const int64_t r = (tb / nb) * 32 + ((c - 256) & 31);
     if (r < N) {
       const uint8_t* rp = src + r * int64_t(nb) * 144;
-      v = ld4(planar ? rp + U * 32 + b * 16 : rp + int64_t(b) * 144);
+      const u32x4 hd = ld4(planar ? rp + U * 32 + b * 16 : rp + int64_t(b) * 144);
+      uint32_t sc[2] = {0u, 0u}, mn = 0u;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        int s_, m_;
+        q4k_scale_min_of(hd, j, s_, m_);
+        sc[j >> 2] |= uint32_t(s_) << (8 * (j & 3));
+        if ((j >> 2) == h) mn |= uint32_t(m_) << (8 * (j & 3));
+      }
+      v = u32x4{hd.x, sc[0], sc[1], mn};
     }
   }
   *reinterpret_cast<u32x4*>(dst + tb * kQ4gRec + int64_t(c) * 16) = v;
@@ -663,7 +675,7 @@ __global__ void __launch_bounds__(kGpThreads, 2) gemm_laid_kernel(const uint8_t*
   const int t32 = min(4 * tn + wv, (N + 31) / 32 - 1);
   const uint8_t* wt = wg + int64_t(t32) * nb * REC;
   const uint8_t* wl = wt + 16 * lane;                                  // this lane's fragments
-  const uint8_t* wr = wt + (Q4 ? 4096 + 16 * lr : kQ6pPlanes + 4 * lr);  // its row's header / d
+  const uint8_t* wr = wt + (Q4 ? 4096 + 16 * lane : kQ6pPlanes + 4 * lr);  // its row's header half / d
 
   float acc[2][16];
 #pragma unroll
@@ -699,28 +711,24 @@ __global__ void __launch_bounds__(kGpThreads, 2) gemm_laid_kernel(const uint8_t*
       H = ld4(wr + on);
       __builtin_amdgcn_sched_barrier(0);  // the activation and header loads are issued here
 #pragma unroll
-      for (int jj = 0; jj < 4; jj++) {  // the mins of this lane's half of the bsum groups
-        int s_, m_;
-        q4k_scale_min_of(Hc, 4 * lh + jj, s_, m_);
-        mnf[2 * jj] = mnf[2 * jj + 1] = _Float16(float(m_));
-      }
+      for (int jj = 0; jj < 4; jj++)  // the mins of this lane's half of the bsum groups
+        mnf[2 * jj] = mnf[2 * jj + 1] = _Float16(float(byte_of(Hc.w, jj)));
       dw = float(__builtin_bit_cast(_Float16, uint16_t(Hc.x & 0xFFFFu)));
       dm = float(__builtin_bit_cast(_Float16, uint16_t(Hc.x >> 16)));
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        int s0, s1, m_;
-        q4k_scale_min_of(Hc, 2 * i, s0, m_);
-        q4k_scale_min_of(Hc, 2 * i + 1, s1, m_);
+        const uint32_t sw = i < 2 ? Hc.y : Hc.z;
+        const uint32_t s0 = byte_of(sw, 2 * (i & 1)), s1 = byte_of(sw, 2 * (i & 1) + 1);
         const uint32_t raw[4] = {W[i].x, W[i].y, W[i].z, W[i].w};
         W[i] = ld4(wl + on + 1024 * i);  // the next block's fragment, as soon as this one is read
         v4i pa0, pb0, pa1, pb1;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const uint32_t ql = raw[e] & 0x0F0F0F0Fu, qh = (raw[e] >> 4) & 0x0F0F0F0Fu;
-          pa0[e] = int(pk_mul(ql, uint32_t(s0) >> 3));
-          pb0[e] = int(pk_mul(ql, uint32_t(s0) & 7u));
-          pa1[e] = int(pk_mul(qh, uint32_t(s1) >> 3));
-          pb1[e] = int(pk_mul(qh, uint32_t(s1) & 7u));
+          pa0[e] = int(pk_mul(ql, s0 >> 3));
+          pb0[e] = int(pk_mul(ql, s0 & 7u));
+          pa1[e] = int(pk_mul(qh, s1 >> 3));
+          pb1[e] = int(pk_mul(qh, s1 & 7u));
         }
 #pragma unroll
         for (int mt = 0; mt < 2; mt++) {
@@ -802,7 +810,7 @@ int launch_gemm_layout(int quant, const void* w, int64_t n_in, int64_t n_out, vo
   const uint8_t* src = static_cast<const uint8_t*>(w);
   uint8_t* d = static_cast<uint8_t*>(dst);
   if (is_q4k(quant)) {
-    const int64_t threads = tiles * nb * 288;
+    const int64_t threads = tiles * nb * 320;
     hipLaunchKernelGGL(q4kg_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, s, src, planar, n_out, tiles,
                        nb, d);
   } else {

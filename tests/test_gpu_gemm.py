@@ -133,15 +133,15 @@ def test_gemm_q6k_planes_extremes(dev):
 def layout_numpy(quant, w, k, n):
     """The records of jero_hip_repack_gemm restated in numpy from the GGUF bytes (the layouts its
     header documents), rows padded to a multiple of 32 with zeros.  Q4_K_G: per (32-row tile,
-    block) the qs bytes 32 i + 16 h .. + 16 of row r at lane (r, h) of pair i, then the 32 block
-    headers.  Q6_K_P: w = sc (q6 - 32) = 128 hi + lo, the planes at lane (r, h) of K step s
+    block) the qs bytes 32 i + 16 h .. + 16 of row r at lane (r, h) of pair i, then per half h and
+    row: d, dmin, the 8 unpacked 6-bit scales, the mins of sub-blocks 4 h .. 4 h + 3.  Q6_K_P: w = sc (q6 - 32) = 128 hi + lo, the planes at lane (r, h) of K step s
     (elements 32 s + 16 h .. + 16), then d as f32."""
     nb = k // 256
     tiles = (n + 31) // 32
     if quant == J.Q4_K:
         blk = np.zeros((tiles * 32, nb, 144), np.uint8)
         blk[:n] = w.reshape(n, nb, 144)
-        out = np.zeros((tiles, nb, 4608), np.uint8)
+        out = np.zeros((tiles, nb, 5120), np.uint8)
         for t in range(tiles):
             for b in range(nb):
                 rows = blk[32 * t:32 * t + 32, b]
@@ -150,7 +150,17 @@ def layout_numpy(quant, w, k, n):
                         lanes = rows[:, 16 + 32 * i + 16 * h:16 + 32 * i + 16 * h + 16]  # [32 rows][16]
                         o = (i * 64 + 32 * h) * 16
                         out[t, b, o:o + 512] = lanes.reshape(-1)
-                out[t, b, 4096:] = rows[:, :16].reshape(-1)
+                hdr = np.zeros((32, 2, 16), np.uint8)
+                for r in range(32):
+                    x = rows[r]
+                    sc8 = x[4:16].astype(np.int64)
+                    sc = [sc8[j] & 63 if j < 4 else (sc8[j + 4] & 15) | ((sc8[j - 4] >> 6) << 4) for j in range(8)]
+                    mn = [sc8[j + 4] & 63 if j < 4 else (sc8[j + 4] >> 4) | ((sc8[j] >> 6) << 4) for j in range(8)]
+                    for h in range(2):
+                        hdr[r, h, :4] = x[:4]
+                        hdr[r, h, 4:12] = sc
+                        hdr[r, h, 12:16] = mn[4 * h:4 * h + 4]
+                out[t, b, 4096:] = hdr.transpose(1, 0, 2).reshape(-1)  # [half][row][16]
         return out.reshape(-1)
     blk = w.reshape(n, nb, 210)
     wint = np.zeros((tiles * 32, nb, 256), np.int64)
@@ -245,7 +255,7 @@ def test_gemm_laid_q4k_extremes(dev):
 
 def test_gemm_layout_errors(dev):
     w = to_dev(rand_weights(J.Q4_K, 64, 256, 3), dev)
-    assert J.gemm_layout_bytes(J.Q4_K, 256, 64) == 2 * 4608 == J.row_bytes(J.Q4_K, 256) * 64
+    assert J.gemm_layout_bytes(J.Q4_K, 256, 64) == 2 * 5120
     assert J.gemm_layout_bytes(J.Q6_K, 512, 33) == 2 * 2 * 16512
     assert J.gemm_layout_bytes(J.Q8_0, 256, 64) == 0 and J.gemm_layout_bytes(J.Q4_K, 100, 64) == 0
     with pytest.raises(J.K3Error) as e:

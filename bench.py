@@ -256,7 +256,8 @@ GEMM_SHAPE = (512, 4096, 14336)  # (tokens M, n_in K, n_out N), Q4_K weights
 def bench_gemm(torch, J, dev, stream, steps, keep_host):
     """Prefill GEMM: Y[512, 14336] = X[512, 4096] (Q8_K) . W (Q4_K), int8 MFMA.  The weights are
     re-laid out once at load into the GEMM's fragment order (jero_hip_repack_gemm: Q4_K_G, the
-    same bytes, as the model's prefill holds them); the kernel over the GGUF bytes is timed too
+    quants regrouped and the scales unpacked, 160 bytes per 256-block against 144, as the model's
+    prefill holds them); the kernel over the GGUF bytes is timed too
     (`gguf`).  Weights rotate over 4 copies.  `mfma_issue_frac`: the MFMA work the kernel issues
     (two int8 planes of 2MNK ops each, plus the f16 mins product of 2MN*16 per block) over the
     time at peak."""
@@ -285,7 +286,7 @@ def bench_gemm(torch, J, dev, stream, steps, keep_host):
     t = timed(laid)
     tg = timed(views)
     res = {"workload": f"Q4_K x Q8_K prefill GEMM M={M} K={K} N={N}, int8 MFMA, weights in the GEMM layout "
-                       f"(Q4_K_G: the Q4_K bytes in MFMA fragment order, repacked once at load)",
+                       f"(Q4_K_G: the quants in MFMA fragment order, scales unpacked, repacked once at load)",
            "us": round(t * 1e6, 2), "tops": round(ops / t / 1e12, 1), "unit": "TOP/s", "peak": INT8_PEAK_TOPS,
            "frac_int8_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS, 4),
            "mfma_issue_frac": round(issued / t, 4), "tokens_per_s": round(M / t, 1),

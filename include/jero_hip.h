@@ -47,7 +47,7 @@ typedef enum jero_quant {
   JERO_Q4_K_T = 113, /* stacked expert Q4_K re-laid out by jero_hip_repack_experts (16-row tiles) */
   JERO_Q6_K_R = 114, /* Q6_K bytes re-laid out by jero_hip_repack into aligned planes (same size) */
   JERO_Q6_K_T = 115, /* stacked expert Q6_K re-laid out by jero_hip_repack_experts (16-row tiles) */
-  JERO_Q4_K_G = 116, /* Q4_K bytes in the GEMM's fragment order, by jero_hip_repack_gemm (GEMM only) */
+  JERO_Q4_K_G = 116, /* Q4_K in the GEMM's fragment order, by jero_hip_repack_gemm (GEMM only) */
   JERO_Q6_K_P = 117, /* Q6_K as exact int8 planes, by jero_hip_repack_gemm (GEMM only) */
   JERO_ACT_Q8 = 100 /* activation blocks for Q8_0 / Q4_0 weights: f32 d, i8 q[32] (36 B) */
 } jero_quant;
@@ -144,9 +144,9 @@ int jero_hip_gemm(int quant, const void *w_dev, size_t w_bytes, int64_t n_in, in
 
 /* Load-time re-layout of a Q4_K / Q6_K tensor (GGUF bytes or JERO_Q4_K_R / JERO_Q6_K_R) for
  * jero_hip_gemm, the RepackedWeight role of repack_tensor_parallel (src/weights.rs:914-955) for
- * the prefill.  Q4_K -> JERO_Q4_K_G: the same bytes regrouped per 32-row tile and 256-block in
- * the order of the int8-MFMA fragments (the same size as the Q4_K tensor for n_out a multiple of
- * 32).  Q6_K -> JERO_Q6_K_P: every weight as the exact integer sc*(q6-32) under the block's d,
+ * the prefill.  Q4_K -> JERO_Q4_K_G: the quants regrouped per 32-row tile and 256-block in the
+ * order of the int8-MFMA fragments, with each block's 6-bit scales and mins unpacked to bytes
+ * (160 bytes per 256-block of a row against Q4_K's 144).  Q6_K -> JERO_Q6_K_P: every weight as the exact integer sc*(q6-32) under the block's d,
  * split into two int8 planes (128*hi + lo) in the fragment order, plus d as f32 (2 bytes per
  * weight and 4 per 256-block of a row: about 2.3x the Q6_K bytes).  Rows are padded to a
  * multiple of 32.  jero_hip_gemm_layout_bytes(quant, n_in, n_out) bytes (n_in a multiple of 256;
@@ -362,8 +362,8 @@ int jero_hip_model_status(jero_model *model, void *stream);
  * would leave: the n K/V rows in the ring, the last token's logits, its greedy next token and
  * position pos0 + n.  pos0 + n <= kv_capacity, else ContextLengthExceeded (as engine.rs:727
  * rejects a prompt past n_ctx).  Allocates its row buffers on first use, and from prompts of 8
- * tokens builds the exact int8 planes of each Q6_K tensor for the GEMM (2.3x the tensor's bytes);
- * both are held by the model until jero_hip_model_destroy.
+ * tokens builds the GEMM layout of each Q4_K and Q6_K tensor (jero_hip_repack_gemm's: 1.11x the
+ * Q4_K and 2.3x the Q6_K bytes); both are held by the model until jero_hip_model_destroy.
  * With a trace set (jero_hip_model_trace, n * jero_hip_model_trace_bytes bytes or more), token t's
  * trace in the decode step's layout lands at t * jero_hip_model_trace_bytes; the head's fields
  * only for the last token. */

@@ -451,7 +451,7 @@ def gemm_layout_bytes(quant, n_in, n_out):
 def repack_gemm(weights, stream=None):
     """Load-time re-layout of a Q4_K / Q6_K tensor (GGUF or the _R layouts) for the prefill GEMM
     (the RepackedWeight role, src/weights.rs:914-955): returns a TensorView of quant Q4_K_G (the
-    Q4_K bytes in the MFMA fragment order) or Q6_K_P (exact int8 planes) for gemm()."""
+    Q4_K quants in the MFMA fragment order, scales unpacked) or Q6_K_P (exact int8 planes) for gemm()."""
     import torch
     n = gemm_layout_bytes(weights.quant, weights.n_in, weights.n_out)
     if n == 0:

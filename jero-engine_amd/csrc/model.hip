@@ -780,17 +780,43 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
   if ((rc = launch_embed_rows(m->tok_embd.quant, m->tok_embd.dev, row_bytes(m->tok_embd.quant, H), int(H), b.tok, n,
                               b.X, s)))
     return rc;
+  // the residual of the last projection, added to X by the next row step (null: none pending)
+  const float* pending = nullptr;
+  auto q8k_input = [](const DevTensor& w) { return !w.present() || act_format(w.quant) == JERO_Q8_K; };
   for (int64_t L = 0; L < c.n_layers; L++) {
     const LayerW& l = m->layers[size_t(L)];
     const float* anw = static_cast<const float*>(l.attn_norm.dev);
-    if ((rc = snap(fld(L, TraceLayout::kXIn), b.X, 4 * H, 4 * H))) return rc;
-    // attention sublayer: RMSNorm rows -> Q, K, V rows
-    if ((rc = launch_rmsnorm_rows(b.X, n, H, anw, eps_attn, b.XN, s))) return rc;
-    if ((rc = snap(fld(L, TraceLayout::kXnAttn), b.XN, 4 * H, 4 * H))) return rc;
-    float *qp, *kp, *vp;
-    int64_t qs, ks, vs;
     int64_t xrb = 0;
     int have_fmt = -1;
+    // X += the pending residual, then RMSNorm rows: fused with the Q8_K quantization when every
+    // projection of the sublayer reads Q8_K (XN then only for the trace), else apart (the
+    // projections quantize XN themselves)
+    auto norm_step = [&](const float* nw, float eps, bool all_q8k, int f_xin, int f_xn, int f_q8) -> int {
+      int r = JERO_OK;
+      if (all_q8k && H % 256 == 0 && H <= 8192) {
+        if ((r = launch_add_rmsnorm_q8k_rows(b.X, pending, n, H, nw, eps, m->trace ? b.XN : nullptr, b.XQ, s)))
+          return r;
+        have_fmt = JERO_Q8_K;
+        xrb = row_bytes(JERO_Q8_K, H);
+        pending = nullptr;
+        if ((r = snap(fld(L, f_xin), b.X, 4 * H, 4 * H)) || (r = snap(fld(L, f_xn), b.XN, 4 * H, 4 * H)))
+          return r;
+        return snap(fld(L, f_q8), b.XQ, size_t(xrb), size_t(xrb));
+      }
+      if (pending && (r = launch_add_rows(b.X, pending, n * H, s))) return r;
+      pending = nullptr;
+      have_fmt = -1;
+      if ((r = snap(fld(L, f_xin), b.X, 4 * H, 4 * H)) || (r = launch_rmsnorm_rows(b.X, n, H, nw, eps, b.XN, s)))
+        return r;
+      return snap(fld(L, f_xn), b.XN, 4 * H, 4 * H);
+    };
+    // attention sublayer: RMSNorm rows -> Q, K, V rows
+    const bool attn_q8k = l.qkv_split ? q8k_input(l.wq) && q8k_input(l.wk) && q8k_input(l.wv)
+                                      : q8k_input(l.qkv) && (!l.v_separate || q8k_input(l.wv));
+    if ((rc = norm_step(anw, eps_attn, attn_q8k, TraceLayout::kXIn, TraceLayout::kXnAttn, TraceLayout::kQ8Attn)))
+      return rc;
+    float *qp, *kp, *vp;
+    int64_t qs, ks, vs;
     auto project = [&](const DevTensor& w, const float* in, int64_t k, float* out, int trace_field) -> int {
       const int fmt = act_format(w.quant);
       int r = JERO_OK;
@@ -861,25 +887,29 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
       if ((rc = launch_attention_tokens(p, int(nt), qs, b.ATT + t0 * Q, Q, s))) return rc;
     }
     if ((rc = snap(fld(L, TraceLayout::kAttn), b.ATT, 4 * Q, 4 * Q))) return rc;
-    // output projection + residual
+    // output projection; its residual is added by the FFN's row step
     have_fmt = -1;
     if (l.wo.present()) {
-      if ((rc = project(l.wo, b.ATT, Q, b.T, TraceLayout::kQ8Wo)) || (rc = launch_add_rows(b.X, b.T, n * H, s)))
-        return rc;
+      if ((rc = project(l.wo, b.ATT, Q, b.T, TraceLayout::kQ8Wo))) return rc;
+      pending = b.T;
     } else if ((rc = launch_det_proj(b.ATT, Q, nullptr, 0.f, 0.25f, b.X, H, true, s, n, Q, H))) {
       return rc;
     }
-    if ((rc = snap(fld(L, TraceLayout::kXMid), b.X, 4 * H, 4 * H))) return rc;
-    // FFN: RMSNorm rows -> gate | up -> SwiGLU -> down + residual
+    // FFN: (residual +) RMSNorm rows -> gate | up -> SwiGLU -> down + residual
     const float* fnw = static_cast<const float*>(l.ffn_norm.dev);
-    if ((rc = launch_rmsnorm_rows(b.X, n, H, fnw, eps_ffn, b.XN, s))) return rc;
-    if ((rc = snap(fld(L, TraceLayout::kXnFfn), b.XN, 4 * H, 4 * H))) return rc;
-    have_fmt = -1;
+    const bool ffn_q8k = l.gu_split ? q8k_input(l.gate) && q8k_input(l.up) : q8k_input(l.gate_up);
+    if ((rc = norm_step(fnw, eps_ffn, ffn_q8k, TraceLayout::kXMid, TraceLayout::kXnFfn, TraceLayout::kQ8Ffn)))
+      return rc;
+    // SwiGLU fused with the Q8_K quantization when down reads Q8_K (act then only for the trace)
+    const bool act_q8k = l.down.present() && act_format(l.down.quant) == JERO_Q8_K && F % 256 == 0;
+    auto swiglu = [&](const float* g, int64_t gst, const float* u, int64_t ust) -> int {
+      if (!act_q8k) return launch_swiglu_rows(g, gst, u, ust, b.ACT, n, F, s);
+      return launch_swiglu_q8k_rows(g, gst, u, ust, m->trace ? b.ACT : nullptr, n, F, b.XQ, s);
+    };
     const size_t fg = fld(L, TraceLayout::kGu);
     if (!l.gu_split) {
       if ((rc = project(l.gate_up, b.XN, H, b.GU, TraceLayout::kQ8Ffn)) ||
-          (rc = launch_swiglu_rows(b.GU, 2 * F, b.GU + F, 2 * F, b.ACT, n, F, s)) ||
-          (rc = snap(fg, b.GU, 8 * F, 8 * F)))
+          (rc = swiglu(b.GU, 2 * F, b.GU + F, 2 * F)) || (rc = snap(fg, b.GU, 8 * F, 8 * F)))
         return rc;
     } else {
       float* g2[2] = {b.GU, b.GU + n * F};
@@ -895,19 +925,25 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
         }
         if (rc) return rc;
       }
-      if ((rc = launch_swiglu_rows(g2[0], F, g2[1], F, b.ACT, n, F, s)) || (rc = snap(fg, g2[0], 4 * F, 4 * F)) ||
+      if ((rc = swiglu(g2[0], F, g2[1], F)) || (rc = snap(fg, g2[0], 4 * F, 4 * F)) ||
           (rc = snap(fg + 4 * F, g2[1], 4 * F, 4 * F)))
         return rc;
     }
     if ((rc = snap(fld(L, TraceLayout::kAct), b.ACT, 4 * F, 4 * F))) return rc;
     have_fmt = -1;
+    if (act_q8k) {  // the SwiGLU step left the Q8_K rows in XQ
+      have_fmt = JERO_Q8_K;
+      xrb = row_bytes(JERO_Q8_K, F);
+      if ((rc = snap(fld(L, TraceLayout::kQ8Down), b.XQ, size_t(xrb), size_t(xrb)))) return rc;
+    }
     if (l.down.present()) {
-      if ((rc = project(l.down, b.ACT, F, b.T, TraceLayout::kQ8Down)) || (rc = launch_add_rows(b.X, b.T, n * H, s)))
-        return rc;
+      if ((rc = project(l.down, b.ACT, F, b.T, TraceLayout::kQ8Down))) return rc;
+      pending = b.T;  // added by the next layer's row step
     } else if ((rc = launch_det_proj(b.ACT, F, nullptr, 0.f, 0.125f, b.X, H, true, s, n, F, H))) {
       return rc;
     }
   }
+  if (pending && (rc = launch_add_rows(b.X, pending, n * H, s))) return rc;
   // every token's final hidden state and RoPE table; the head on the last token only
   if ((rc = snap(tl.x_final, b.X, 4 * H, 4 * H)) || (rc = snap(tl.rope_cs, b.RC, 4 * size_t(c.head_dim), 4 * size_t(c.head_dim))))
     return rc;

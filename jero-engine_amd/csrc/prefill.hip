@@ -114,6 +114,67 @@ __global__ void __launch_bounds__(256) swiglu_rows_kernel(const float* __restric
   act[t * F + i] = gv / (1.0f + expf(-gv)) * uv;
 }
 
+// The fused row step before a projection over Q8_K activations, one workgroup per row t:
+// X[t] += D[t] when D is given (the previous projection's residual, written back), XN[t] =
+// RMSNorm(X[t]) * w as rmsnorm_rows_kernel computes it (the same per-thread strided sums, so the
+// same bits), XN[t] also stored when XN is given, and Q[t] = the Q8_K blocks of XN[t] as
+// quant_q8k_kernel makes them (a wave per 256-block from LDS).  H a multiple of 256, at most
+// kFusedMaxH.
+constexpr int kFusedMaxH = 8192;
+__global__ void __launch_bounds__(256) add_rmsnorm_q8k_rows_kernel(float* __restrict__ X, const float* __restrict__ D,
+                                                                   int64_t H, const float* __restrict__ w, float eps,
+                                                                   float* __restrict__ XN, uint8_t* __restrict__ Q) {
+  __shared__ float s_tmp[4];
+  __shared__ __attribute__((aligned(16))) float s_xn[kFusedMaxH];
+  float* x = X + int64_t(blockIdx.x) * H;
+  const float* d = D ? D + int64_t(blockIdx.x) * H : nullptr;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < H; i += 256) {
+    float v = x[i];
+    if (d) {
+      v += d[i];
+      x[i] = v;
+    }
+    s_xn[i] = v;
+    ss += v * v;
+  }
+  ss = block_sum256(ss, s_tmp);
+  const float inv = 1.0f / sqrtf(ss / float(H) + eps);
+  float* y = XN ? XN + int64_t(blockIdx.x) * H : nullptr;
+  for (int64_t i = threadIdx.x; i < H; i += 256) {
+    const float v = s_xn[i] * inv * w[i];
+    s_xn[i] = v;
+    if (y) y[i] = v;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  uint8_t* q = Q + int64_t(blockIdx.x) * (H / 256) * 292;
+  for (int64_t j = wv; j < H / 256; j += 4) {
+    const float4 v = reinterpret_cast<const float4*>(s_xn + 256 * j)[lane];
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    q8k_block_wave(e, lane, q + j * 292);
+  }
+}
+
+// act[t] = silu(g[t]) * u[t] as swiglu_rows_kernel computes it, stored when act is given, and its
+// Q8_K blocks: a wave per 256-block (4 elements per lane), grid (ceil(F / 1024), n).
+__global__ void __launch_bounds__(256) swiglu_q8k_rows_kernel(const float* __restrict__ g, int64_t g_stride,
+                                                              const float* __restrict__ u, int64_t u_stride,
+                                                              float* __restrict__ act, int64_t F,
+                                                              uint8_t* __restrict__ Q) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t j = int64_t(blockIdx.x) * 4 + wv, t = blockIdx.y;
+  if (j >= F / 256) return;
+  const float4 gv = reinterpret_cast<const float4*>(g + t * g_stride + 256 * j)[lane];
+  const float4 uv = reinterpret_cast<const float4*>(u + t * u_stride + 256 * j)[lane];
+  const float ga[4] = {gv.x, gv.y, gv.z, gv.w}, ua[4] = {uv.x, uv.y, uv.z, uv.w};
+  float e[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) e[i] = ga[i] / (1.0f + expf(-ga[i])) * ua[i];
+  if (act) reinterpret_cast<float4*>(act + t * F + 256 * j)[lane] = make_float4(e[0], e[1], e[2], e[3]);
+  q8k_block_wave(e, lane, Q + (t * (F / 256) + j) * 292);
+}
+
 // x[i] += d[i] (the residual of Wo and down).
 __global__ void __launch_bounds__(256) add_rows_kernel(float* __restrict__ x, const float* __restrict__ d, int64_t n) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -155,6 +216,23 @@ int launch_swiglu_rows(const float* g, int64_t g_stride, const float* u, int64_t
   hipLaunchKernelGGL(swiglu_rows_kernel, dim3(unsigned((F + 255) / 256), unsigned(n)), dim3(256), 0, s, g, g_stride,
                      u, u_stride, act, F);
   return check_launch("prefill swiglu");
+}
+
+int launch_add_rmsnorm_q8k_rows(float* X, const float* D, int64_t n, int64_t H, const float* w, float eps, float* XN,
+                                void* Q, hipStream_t s) {
+  if (H % 256 || H > kFusedMaxH) return fail(JERO_ERR_CAPABILITY_MISMATCH, "prefill: fused RMSNorm rows need H % 256 == 0, H <= 8192");
+  hipLaunchKernelGGL(add_rmsnorm_q8k_rows_kernel, dim3(unsigned(n)), dim3(256), 0, s, X, D, H, w, eps, XN,
+                     static_cast<uint8_t*>(Q));
+  return check_launch("prefill rmsnorm + q8_k");
+}
+
+int launch_swiglu_q8k_rows(const float* g, int64_t g_stride, const float* u, int64_t u_stride, float* act, int64_t n,
+                           int64_t F, void* Q, hipStream_t s) {
+  if (F % 256 || (g_stride | u_stride) % 4)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "prefill: fused SwiGLU rows need F % 256 == 0");
+  hipLaunchKernelGGL(swiglu_q8k_rows_kernel, dim3(unsigned((F / 256 + 3) / 4), unsigned(n)), dim3(256), 0, s, g,
+                     g_stride, u, u_stride, act, F, static_cast<uint8_t*>(Q));
+  return check_launch("prefill swiglu + q8_k");
 }
 
 int launch_add_rows(float* x, const float* d, int64_t count, hipStream_t s) {

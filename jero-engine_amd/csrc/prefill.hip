@@ -127,24 +127,48 @@ __global__ void __launch_bounds__(256) add_rmsnorm_q8k_rows_kernel(float* __rest
   __shared__ float s_tmp[4];
   __shared__ __attribute__((aligned(16))) float s_xn[kFusedMaxH];
   float* x = X + int64_t(blockIdx.x) * H;
-  const float* d = D ? D + int64_t(blockIdx.x) * H : nullptr;
+  const float* d = D ? D + int64_t(blockIdx.x) * H : x;
+  const int per = int(H / 256);  // elements per thread: i = threadIdx.x + 256 k
   float ss = 0.f;
-  for (int64_t i = threadIdx.x; i < H; i += 256) {
-    float v = x[i];
-    if (d) {
-      v += d[i];
-      x[i] = v;
+  // eight elements' loads in flight per batch, then the sums in the same order as the plain loop
+  for (int k0 = 0; k0 < per; k0 += 8) {
+    float v[8], e[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int64_t i = threadIdx.x + 256 * int64_t(min(k0 + k, per - 1));
+      v[k] = x[i];
+      e[k] = d[i];
     }
-    s_xn[i] = v;
-    ss += v * v;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      if (k0 + k < per) {
+        const int64_t i = threadIdx.x + 256 * int64_t(k0 + k);
+        float u = v[k];
+        if (D) {
+          u += e[k];
+          x[i] = u;
+        }
+        s_xn[i] = u;
+        ss += u * u;
+      }
+    }
   }
   ss = block_sum256(ss, s_tmp);
   const float inv = 1.0f / sqrtf(ss / float(H) + eps);
   float* y = XN ? XN + int64_t(blockIdx.x) * H : nullptr;
-  for (int64_t i = threadIdx.x; i < H; i += 256) {
-    const float v = s_xn[i] * inv * w[i];
-    s_xn[i] = v;
-    if (y) y[i] = v;
+  for (int k0 = 0; k0 < per; k0 += 8) {
+    float wk[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) wk[k] = w[threadIdx.x + 256 * int64_t(min(k0 + k, per - 1))];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      if (k0 + k < per) {
+        const int64_t i = threadIdx.x + 256 * int64_t(k0 + k);
+        const float u = s_xn[i] * inv * wk[k];
+        s_xn[i] = u;
+        if (y) y[i] = u;
+      }
+    }
   }
   __syncthreads();
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;

@@ -659,7 +659,8 @@ __device__ __forceinline__ void gp_store_act(const GpAct& A, GpStage& S) {
 template <bool Q4, bool SPLIT>
 __global__ void __launch_bounds__(kGpThreads, 2) gemm_laid_kernel(const uint8_t* __restrict__ xq, int64_t xrb,
                                                                    const uint8_t* __restrict__ wg, int M, int N,
-                                                                   int nb, float* __restrict__ y) {
+                                                                   int nb, float* __restrict__ y,
+                                                                   float* __restrict__ y2) {
   __shared__ GpStage S[2];
   constexpr int REC = Q4 ? kQ4gRec : kQ6pRec;
   const int n_tiles_m = (M + kGpBM - 1) / kGpBM;
@@ -795,8 +796,12 @@ __global__ void __launch_bounds__(kGpThreads, 2) gemm_laid_kernel(const uint8_t*
     for (int v = 0; v < 16; v++) {
       const int m = m0 + 32 * mt + 8 * (v >> 2) + 4 * lh + (v & 3);
       if (m < M && n < N) {
-        if constexpr (SPLIT) atomicAdd(&y[int64_t(m) * N + n], acc[mt][v]);
-        else y[int64_t(m) * N + n] = acc[mt][v];
+        if constexpr (SPLIT) {
+          if (y2) (half ? y2 : y)[int64_t(m) * N + n] = acc[mt][v];
+          else atomicAdd(&y[int64_t(m) * N + n], acc[mt][v]);
+        } else {
+          y[int64_t(m) * N + n] = acc[mt][v];
+        }
       }
     }
 }
@@ -822,28 +827,31 @@ int launch_gemm_layout(int quant, const void* w, int64_t n_in, int64_t n_out, vo
 }
 
 int launch_gemm_laid(int laid, const void* w, int64_t n_in, int64_t n_out, const void* xq, int64_t m, float* y,
-                     hipStream_t s) {
+                     hipStream_t s, float* y2, bool* split_out) {
   const int nb = int(n_in / 256);
   const int64_t tiles = ((m + kGpBM - 1) / kGpBM) * ((n_out + kGpBN - 1) / kGpBN);
   // two workgroups per CU: a grid that fills at most half of that splits K in two
   const bool split = nb >= 2 && tiles <= device_info().cus;
+  if (split_out) *split_out = split && y2;
   const uint8_t* xb = static_cast<const uint8_t*>(xq);
   const uint8_t* wb = static_cast<const uint8_t*>(w);
   const int64_t xrb = row_bytes(JERO_Q8_K, n_in);
   const dim3 grid(unsigned(split ? 2 * tiles : tiles)), block(kGpThreads);
   if (split) {
-    hipLaunchKernelGGL(zero_f32_kernel, dim3(unsigned(std::min<int64_t>((m * n_out + 255) / 256, 4096))), dim3(256), 0,
-                       s, y, m * n_out);
-    int rc = check_launch("gemm zero");
-    if (rc) return rc;
+    if (!y2) {  // both halves add into the zeroed output
+      hipLaunchKernelGGL(zero_f32_kernel, dim3(unsigned(std::min<int64_t>((m * n_out + 255) / 256, 4096))), dim3(256),
+                         0, s, y, m * n_out);
+      int rc = check_launch("gemm zero");
+      if (rc) return rc;
+    }
     if (laid == JERO_Q4_K_G)
-      hipLaunchKernelGGL((gemm_laid_kernel<true, true>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y);
+      hipLaunchKernelGGL((gemm_laid_kernel<true, true>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y, y2);
     else
-      hipLaunchKernelGGL((gemm_laid_kernel<false, true>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y);
+      hipLaunchKernelGGL((gemm_laid_kernel<false, true>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y, y2);
   } else if (laid == JERO_Q4_K_G) {
-    hipLaunchKernelGGL((gemm_laid_kernel<true, false>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y);
+    hipLaunchKernelGGL((gemm_laid_kernel<true, false>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y, y2);
   } else {
-    hipLaunchKernelGGL((gemm_laid_kernel<false, false>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y);
+    hipLaunchKernelGGL((gemm_laid_kernel<false, false>), grid, block, 0, s, xb, xrb, wb, int(m), int(n_out), nb, y, y2);
   }
   return check_launch(laid == JERO_Q4_K_G ? "gemm q4_k_g" : "gemm q6_k_p");
 }
@@ -907,12 +915,14 @@ using namespace jero;
 namespace jero {
 
 int launch_gemm(int quant, const void* w_dev, int64_t n_in, int64_t n_out, const void* xq_dev, int64_t m, float* y_dev,
-                hipStream_t s, const void* laid) {
+                hipStream_t s, const void* laid, float* y2, bool* split_out) {
+  if (split_out) *split_out = false;
   const int act = act_format(quant);
   const int64_t xrb = row_bytes(act, n_in);
   if (quant == JERO_Q4_K_G || quant == JERO_Q6_K_P) return launch_gemm_laid(quant, w_dev, n_in, n_out, xq_dev, m, y_dev, s);
   if ((is_q4k(quant) || is_q6k(quant)) && laid)
-    return launch_gemm_laid(is_q4k(quant) ? JERO_Q4_K_G : JERO_Q6_K_P, laid, n_in, n_out, xq_dev, m, y_dev, s);
+    return launch_gemm_laid(is_q4k(quant) ? JERO_Q4_K_G : JERO_Q6_K_P, laid, n_in, n_out, xq_dev, m, y_dev, s, y2,
+                            split_out);
   if (is_q6k(quant) && m >= kLaidMinRows) {  // the Q6_K_P planes built into the library workspace for this call
     void* ws = nullptr;
     int rc = workspace(gemm_layout_bytes(quant, n_in, n_out), &ws);

@@ -27,16 +27,19 @@ int launch_matvec(int quant, const void* w, int64_t n_in, int64_t n_out, const v
 // (w in that GEMM layout), or Q4_K / Q4_K_R / Q6_K / Q6_K_R with their GEMM layout given
 // (laid), run the int8-MFMA kernel over the layout; Q6_K / Q6_K_R from kLaidMinRows rows build
 // the Q6_K_P planes into the library workspace for the call; Q4_K / Q4_K_R with n_out a multiple
-// of 128 run the int8-MFMA kernel over the Q4_K bytes; one GEMV per row otherwise.
+// of 128 run the int8-MFMA kernel over the Q4_K bytes; one GEMV per row otherwise.  With y2 given,
+// a layout GEMM whose grid splits K in two writes one half's sums to y and the other's to y2
+// (*split_out true; the product is y + y2, the same bits as the one-output form) instead of adding
+// both into a zeroed y.
 constexpr int64_t kLaidMinRows = 8;
 int launch_gemm(int quant, const void* w, int64_t n_in, int64_t n_out, const void* xq, int64_t m, float* y,
-                hipStream_t s, const void* laid = nullptr);
+                hipStream_t s, const void* laid = nullptr, float* y2 = nullptr, bool* split_out = nullptr);
 // The GEMM layout of a Q4_K / Q4_K_R tensor (JERO_Q4_K_G) or Q6_K / Q6_K_R tensor (JERO_Q6_K_P):
 // gemm_layout_bytes bytes, 16-byte aligned (0 for other formats); and the GEMM over it.
 size_t gemm_layout_bytes(int quant, int64_t n_in, int64_t n_out);
 int launch_gemm_layout(int quant, const void* w, int64_t n_in, int64_t n_out, void* dst, hipStream_t s);
 int launch_gemm_laid(int laid, const void* w, int64_t n_in, int64_t n_out, const void* xq, int64_t m, float* y,
-                     hipStream_t s);
+                     hipStream_t s, float* y2 = nullptr, bool* split_out = nullptr);
 // Enqueues the Q4_K -> Q4_K_R or Q6_K -> Q6_K_R re-layout (dst: 16-byte aligned, same size).
 int launch_repack(int quant, const void* src, int64_t n_in, int64_t n_out, void* dst, int* dst_quant, hipStream_t s);
 int launch_repack_experts(int quant, const void* src, int64_t n_in, int64_t n_rows, void* dst, int* dst_quant,

@@ -52,8 +52,8 @@ struct PrefillBufs {
   int64_t rows = 0;
   size_t ws_bytes = 0;
   int32_t* tok = nullptr;
-  float *X = nullptr, *XN = nullptr, *T = nullptr, *QKV = nullptr, *ATT = nullptr, *GU = nullptr, *ACT = nullptr,
-        *RC = nullptr, *ws = nullptr;
+  float *X = nullptr, *XN = nullptr, *T = nullptr, *T2 = nullptr, *QKV = nullptr, *ATT = nullptr, *GU = nullptr,
+        *ACT = nullptr, *RC = nullptr, *ws = nullptr;
   uint8_t* XQ = nullptr;
 };
 
@@ -707,7 +707,7 @@ static int prefill_buffers(jero_model* m, int64_t n, int64_t pos0) {
   if (n <= b.rows && ws <= b.ws_bytes) return JERO_OK;
   const int64_t rows = std::max(n, b.rows);
   for (void* p : {static_cast<void*>(b.tok), static_cast<void*>(b.X), static_cast<void*>(b.XN),
-                  static_cast<void*>(b.T), static_cast<void*>(b.QKV), static_cast<void*>(b.ATT),
+                  static_cast<void*>(b.T), static_cast<void*>(b.T2), static_cast<void*>(b.QKV), static_cast<void*>(b.ATT),
                   static_cast<void*>(b.GU), static_cast<void*>(b.ACT), static_cast<void*>(b.RC),
                   static_cast<void*>(b.ws), static_cast<void*>(b.XQ)})
     if (p) dev_free(m, p);
@@ -724,6 +724,7 @@ static int prefill_buffers(jero_model* m, int64_t n, int64_t pos0) {
   if ((rc = dev_alloc(m, sizeof(int32_t) * size_t(rows), &p))) return rc;
   b.tok = static_cast<int32_t*>(p);
   if ((rc = f32(rows * H, &b.X)) || (rc = f32(rows * H, &b.XN)) || (rc = f32(rows * H, &b.T)) ||
+      (rc = f32(rows * H, &b.T2)) ||
       (rc = f32(rows * (Q + 2 * KV), &b.QKV)) || (rc = f32(rows * Q, &b.ATT)) || (rc = f32(rows * 2 * F, &b.GU)) ||
       (rc = f32(rows * F, &b.ACT)) || (rc = f32(rows * c.head_dim, &b.RC)))
     return rc;
@@ -780,8 +781,10 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
   if ((rc = launch_embed_rows(m->tok_embd.quant, m->tok_embd.dev, row_bytes(m->tok_embd.quant, H), int(H), b.tok, n,
                               b.X, s)))
     return rc;
-  // the residual of the last projection, added to X by the next row step (null: none pending)
+  // the residual of the last projection, added to X by the next row step (null: none pending);
+  // pending2: the second K half of a split projection (the residual is pending + pending2)
   const float* pending = nullptr;
+  const float* pending2 = nullptr;
   auto q8k_input = [](const DevTensor& w) { return !w.present() || act_format(w.quant) == JERO_Q8_K; };
   for (int64_t L = 0; L < c.n_layers; L++) {
     const LayerW& l = m->layers[size_t(L)];
@@ -794,17 +797,19 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
     auto norm_step = [&](const float* nw, float eps, bool all_q8k, int f_xin, int f_xn, int f_q8) -> int {
       int r = JERO_OK;
       if (all_q8k && H % 256 == 0 && H <= 8192) {
-        if ((r = launch_add_rmsnorm_q8k_rows(b.X, pending, n, H, nw, eps, m->trace ? b.XN : nullptr, b.XQ, s)))
+        if ((r = launch_add_rmsnorm_q8k_rows(b.X, pending, pending2, n, H, nw, eps, m->trace ? b.XN : nullptr, b.XQ,
+                                             s)))
           return r;
         have_fmt = JERO_Q8_K;
         xrb = row_bytes(JERO_Q8_K, H);
-        pending = nullptr;
+        pending = pending2 = nullptr;
         if ((r = snap(fld(L, f_xin), b.X, 4 * H, 4 * H)) || (r = snap(fld(L, f_xn), b.XN, 4 * H, 4 * H)))
           return r;
         return snap(fld(L, f_q8), b.XQ, size_t(xrb), size_t(xrb));
       }
+      if (pending2 && (r = launch_add_rows(b.T, pending2, n * H, s))) return r;  // pending is b.T
       if (pending && (r = launch_add_rows(b.X, pending, n * H, s))) return r;
-      pending = nullptr;
+      pending = pending2 = nullptr;
       have_fmt = -1;
       if ((r = snap(fld(L, f_xin), b.X, 4 * H, 4 * H)) || (r = launch_rmsnorm_rows(b.X, n, H, nw, eps, b.XN, s)))
         return r;
@@ -817,7 +822,9 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
       return rc;
     float *qp, *kp, *vp;
     int64_t qs, ks, vs;
-    auto project = [&](const DevTensor& w, const float* in, int64_t k, float* out, int trace_field) -> int {
+    // split: a projection into b.T whose split-K halves may land in b.T and b.T2 (then *split)
+    auto project = [&](const DevTensor& w, const float* in, int64_t k, float* out, int trace_field,
+                       bool* split = nullptr) -> int {
       const int fmt = act_format(w.quant);
       int r = JERO_OK;
       if (fmt != have_fmt) {
@@ -827,7 +834,7 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
       }
       const void* laid = nullptr;
       if (n >= kLaidMinRows && (r = laid_of(m, w, s, &laid))) return r;
-      return launch_gemm(w.quant, w.dev, k, w.n_out, b.XQ, n, out, s, laid);
+      return launch_gemm(w.quant, w.dev, k, w.n_out, b.XQ, n, out, s, laid, split ? b.T2 : nullptr, split);
     };
     if (!l.qkv_split) {
       const int64_t w1 = l.qkv.n_out;  // Q + 2 KV, or Q + KV with V apart
@@ -890,8 +897,10 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
     // output projection; its residual is added by the FFN's row step
     have_fmt = -1;
     if (l.wo.present()) {
-      if ((rc = project(l.wo, b.ATT, Q, b.T, TraceLayout::kQ8Wo))) return rc;
+      bool split = false;
+      if ((rc = project(l.wo, b.ATT, Q, b.T, TraceLayout::kQ8Wo, &split))) return rc;
       pending = b.T;
+      pending2 = split ? b.T2 : nullptr;
     } else if ((rc = launch_det_proj(b.ATT, Q, nullptr, 0.f, 0.25f, b.X, H, true, s, n, Q, H))) {
       return rc;
     }
@@ -937,12 +946,15 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
       if ((rc = snap(fld(L, TraceLayout::kQ8Down), b.XQ, size_t(xrb), size_t(xrb)))) return rc;
     }
     if (l.down.present()) {
-      if ((rc = project(l.down, b.ACT, F, b.T, TraceLayout::kQ8Down))) return rc;
+      bool split = false;
+      if ((rc = project(l.down, b.ACT, F, b.T, TraceLayout::kQ8Down, &split))) return rc;
       pending = b.T;  // added by the next layer's row step
+      pending2 = split ? b.T2 : nullptr;
     } else if ((rc = launch_det_proj(b.ACT, F, nullptr, 0.f, 0.125f, b.X, H, true, s, n, F, H))) {
       return rc;
     }
   }
+  if (pending2 && (rc = launch_add_rows(b.T, pending2, n * H, s))) return rc;
   if (pending && (rc = launch_add_rows(b.X, pending, n * H, s))) return rc;
   // every token's final hidden state and RoPE table; the head on the last token only
   if ((rc = snap(tl.x_final, b.X, 4 * H, 4 * H)) || (rc = snap(tl.rope_cs, b.RC, 4 * size_t(c.head_dim), 4 * size_t(c.head_dim))))

@@ -23,11 +23,12 @@ int launch_swiglu_rows(const float* g, int64_t g_stride, const float* u, int64_t
                        int64_t F, hipStream_t s);
 // x[i] += d[i], i < count.
 int launch_add_rows(float* x, const float* d, int64_t count, hipStream_t s);
-// Per row t < n: X[t] += D[t] (when D is given), then the Q8_K blocks of RMSNorm(X[t]) * w into
-// Q (rows of H / 256 blocks), bit for bit what launch_add_rows, launch_rmsnorm_rows and
-// launch_quantize_act make; XN[t] (when given) receives the normalised row.  H % 256 == 0, H <= 8192.
-int launch_add_rmsnorm_q8k_rows(float* X, const float* D, int64_t n, int64_t H, const float* w, float eps, float* XN,
-                                void* Q, hipStream_t s);
+// Per row t < n: X[t] += D[t] (+ D2[t], summed first, when given) when D is given, then the Q8_K
+// blocks of RMSNorm(X[t]) * w into Q (rows of H / 256 blocks), bit for bit what launch_add_rows,
+// launch_rmsnorm_rows and launch_quantize_act make; XN[t] (when given) receives the normalised
+// row.  H % 256 == 0, H <= 8192.
+int launch_add_rmsnorm_q8k_rows(float* X, const float* D, const float* D2, int64_t n, int64_t H, const float* w,
+                                float eps, float* XN, void* Q, hipStream_t s);
 // The Q8_K blocks of act[t] = silu(g[t]) * u[t] into Q, bit for bit what launch_swiglu_rows and
 // launch_quantize_act make; act (when given) receives the f32 rows.  F % 256 == 0.
 int launch_swiglu_q8k_rows(const float* g, int64_t g_stride, const float* u, int64_t u_stride, float* act, int64_t n,

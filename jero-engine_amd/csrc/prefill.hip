@@ -115,29 +115,33 @@ __global__ void __launch_bounds__(256) swiglu_rows_kernel(const float* __restric
 }
 
 // The fused row step before a projection over Q8_K activations, one workgroup per row t:
-// X[t] += D[t] when D is given (the previous projection's residual, written back), XN[t] =
+// X[t] += D[t] (+ D2[t], added to D[t] first: the two K halves of a split projection) when D is
+// given (the previous projection's residual, written back), XN[t] =
 // RMSNorm(X[t]) * w as rmsnorm_rows_kernel computes it (the same per-thread strided sums, so the
 // same bits), XN[t] also stored when XN is given, and Q[t] = the Q8_K blocks of XN[t] as
 // quant_q8k_kernel makes them (a wave per 256-block from LDS).  H a multiple of 256, at most
 // kFusedMaxH.
 constexpr int kFusedMaxH = 8192;
 __global__ void __launch_bounds__(256) add_rmsnorm_q8k_rows_kernel(float* __restrict__ X, const float* __restrict__ D,
-                                                                   int64_t H, const float* __restrict__ w, float eps,
+                                                                   const float* __restrict__ D2, int64_t H,
+                                                                   const float* __restrict__ w, float eps,
                                                                    float* __restrict__ XN, uint8_t* __restrict__ Q) {
   __shared__ float s_tmp[4];
   __shared__ __attribute__((aligned(16))) float s_xn[kFusedMaxH];
   float* x = X + int64_t(blockIdx.x) * H;
   const float* d = D ? D + int64_t(blockIdx.x) * H : x;
+  const float* d2 = D2 ? D2 + int64_t(blockIdx.x) * H : x;
   const int per = int(H / 256);  // elements per thread: i = threadIdx.x + 256 k
   float ss = 0.f;
   // eight elements' loads in flight per batch, then the sums in the same order as the plain loop
   for (int k0 = 0; k0 < per; k0 += 8) {
-    float v[8], e[8];
+    float v[8], e[8], e2[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
       const int64_t i = threadIdx.x + 256 * int64_t(min(k0 + k, per - 1));
       v[k] = x[i];
       e[k] = d[i];
+      e2[k] = d2[i];
     }
 #pragma unroll
     for (int k = 0; k < 8; k++) {
@@ -145,7 +149,7 @@ __global__ void __launch_bounds__(256) add_rmsnorm_q8k_rows_kernel(float* __rest
         const int64_t i = threadIdx.x + 256 * int64_t(k0 + k);
         float u = v[k];
         if (D) {
-          u += e[k];
+          u += D2 ? e[k] + e2[k] : e[k];
           x[i] = u;
         }
         s_xn[i] = u;
@@ -242,10 +246,10 @@ int launch_swiglu_rows(const float* g, int64_t g_stride, const float* u, int64_t
   return check_launch("prefill swiglu");
 }
 
-int launch_add_rmsnorm_q8k_rows(float* X, const float* D, int64_t n, int64_t H, const float* w, float eps, float* XN,
-                                void* Q, hipStream_t s) {
+int launch_add_rmsnorm_q8k_rows(float* X, const float* D, const float* D2, int64_t n, int64_t H, const float* w,
+                                float eps, float* XN, void* Q, hipStream_t s) {
   if (H % 256 || H > kFusedMaxH) return fail(JERO_ERR_CAPABILITY_MISMATCH, "prefill: fused RMSNorm rows need H % 256 == 0, H <= 8192");
-  hipLaunchKernelGGL(add_rmsnorm_q8k_rows_kernel, dim3(unsigned(n)), dim3(256), 0, s, X, D, H, w, eps, XN,
+  hipLaunchKernelGGL(add_rmsnorm_q8k_rows_kernel, dim3(unsigned(n)), dim3(256), 0, s, X, D, D2, H, w, eps, XN,
                      static_cast<uint8_t*>(Q));
   return check_launch("prefill rmsnorm + q8_k");
 }

@@ -435,32 +435,22 @@ __device__ __forceinline__ h4_t h4_of(uint32_t lo, uint32_t hi) {
 //   * Fused (decode step): the q heads are normalised and rotated once per workgroup into LDS (one
 //     wave per head); the workgroup holding the new slot does the same for k, attends to the new
 //     k and v rounded to f16 (the values the ring then holds) and appends them to the ring.
-template <int HD, int MAXG, bool FUSED, bool BATCH = false>
+template <int HD, int MAXG, bool FUSED>
 __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
-  static_assert(!(FUSED && BATCH), "the decode step attends one query");
-  // BATCH (a batch of consecutive queries, the prefill): the workgroup's 16 score columns are
-  // (token, head) pairs, tpw = 16 / group tokens of one kv head's group, so each K/V row loaded
-  // serves every one of them; column c is token c / group, head c % group, attending to its own
-  // first active + token slots.  Otherwise the columns are the group's heads of query blockIdx.z.
+  // the score columns are the group's heads of query blockIdx.z (a batch of queries: one query
+  // per grid z, each attending to its own first active + z slots)
   const int group = p.group;
-  int t0 = blockIdx.z, ntok = 1;
-  if constexpr (BATCH) {
-    const int tpw = 16 / group;
-    t0 = blockIdx.z * tpw;
-    ntok = min(tpw, p.n_tok - t0);
-  }
+  const int t0 = blockIdx.z;
   p.q += t0 * p.q_stride;
   p.active += t0;
   p.part_o += t0 * p.part_tok;
   p.part_ml += t0 * p.part_tok_ml;
-  const int ncol = BATCH ? ntok * group : group;  // valid score columns
-  auto ctok = [&](int c) { return BATCH ? c / group : 0; };
-  auto chead = [&](int c) { return BATCH ? c % group : c; };
+  const int ncol = group;  // valid score columns
   constexpr int NCH = HD / 32;  // 16-byte chunks per lane per row
   constexpr int NT = HD / 16;   // 16-dim MFMA tiles
   constexpr int NW = kAttnThreads / kWave;
   constexpr int CH = 16 * NW;   // slots per workgroup
-  constexpr int QC = BATCH ? 16 : MAXG;  // score columns with a q row
+  constexpr int QC = MAXG;      // score columns with a q row
   static_assert(MAXG <= 16 && (HD == 64 || HD == 128), "tile shape");
   __shared__ __attribute__((aligned(16))) float s_q[16][HD];
   __shared__ __attribute__((aligned(16))) float s_kn[HD];
@@ -484,8 +474,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
 #pragma unroll
   for (int j = 0; j < HPW; j++) {
     const int c = min(wv + NW * j, ncol - 1);
-    qv[j] = reinterpret_cast<const float2*>(p.q + int64_t(ctok(c)) * p.q_stride +
-                                            (int64_t(kh) * group + chead(c)) * HD)[pr];
+    qv[j] = reinterpret_cast<const float2*>(p.q + (int64_t(kh) * group + c) * HD)[pr];
   }
   float2 knv = make_float2(0.f, 0.f), qnw = knv, knw = knv, csv = knv;
   if constexpr (FUSED) {
@@ -495,7 +484,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
     csv = reinterpret_cast<const float2*>(p.rope_cs ? p.rope_cs : p.q)[pr];
   }
   // 1. K and V loads: slot w0 + col, chunks 4j + kq (clamped in-bounds; masked below)
-  const int act_hi = p.active + ntok - 1;  // slots the workgroup's last query attends to
+  const int act_hi = p.active;  // slots the query attends to
   const int bound = p.pos_dev ? int(p.capacity) : act_hi;
   const int pl = min(p0 + CH, bound);
   const int ps = min(w0 + col, pl - 1);
@@ -516,8 +505,8 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
   }
   if (p0 >= active) {  // empty split: contributes nothing to the merge
     if (tid < ncol) {
-      const int h = kh * group + chead(tid);
-      float* ml = p.part_ml + int64_t(ctok(tid)) * p.part_tok_ml;
+      const int h = kh * group + tid;
+      float* ml = p.part_ml;
       ml[(int64_t(h) * S + split) * 2 + 0] = -INFINITY;
       ml[(int64_t(h) * S + split) * 2 + 1] = 0.f;
     }
@@ -621,7 +610,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
     sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qlo[i], sc, 0, 0, 0);
   }
   // this lane's column attends to slots below lim (its token's count; none for an empty column)
-  const int lim = BATCH ? (col < ncol ? min(p1, p.active + ctok(col)) : 0) : p1;
+  const int lim = p1;
   float s[4];
 #pragma unroll
   for (int r = 0; r < 4; r++) s[r] = w0 + 4 * kq + r < lim ? sc[r] : -INFINITY;
@@ -701,12 +690,164 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
       ov += wt * s_o[w][h][d];
       L += wt * s_l[w][h];
     }
-    const int64_t row = int64_t(kh * group + chead(h)) * S + split;
-    p.part_o[int64_t(ctok(h)) * p.part_tok + row * HD + d] = ov;
+    const int64_t row = int64_t(kh * group + h) * S + split;
+    p.part_o[row * HD + d] = ov;
     if (d == 0) {
-      p.part_ml[int64_t(ctok(h)) * p.part_tok_ml + row * 2 + 0] = M;
-      p.part_ml[int64_t(ctok(h)) * p.part_tok_ml + row * 2 + 1] = L;
+      p.part_ml[row * 2 + 0] = M;
+      p.part_ml[row * 2 + 1] = L;
     }
+  }
+}
+
+// A batch of consecutive queries (the prefill) over f16 rings: grid (S, nkv, ceil(T / (NW tpw)))
+// with tpw = 16 / group tokens per wave.  The workgroup stages its 64 ring slots' K and V rows in
+// LDS once (slots past the last token's limit: V zero, a slot there may hold anything); wave w
+// owns the 16 score columns (token, head) of its tpw tokens, all heads of the group, and runs the
+// four 16-slot chunks through an online softmax, so a K/V row serves NW * tpw tokens.  Per
+// chunk: S^T = K q on v_mfma_f32_16x16x16_f16 (q split into f16 hi + lo, as in attn_mfma_kernel),
+// the running max and sum per column over the 4 lanes that hold it, the accumulators rescaled,
+// P V with V^T through the identity MFMA.  Each wave then writes its columns' (m, l, o) partials
+// in attn_mfma_kernel's layout, which the merge kernel combines.
+template <int HD>
+__global__ void __launch_bounds__(kAttnThreads) attn_prefill_kernel(AttnParams p) {
+  constexpr int NCH = HD / 32, NT = HD / 16, NW = kAttnThreads / kWave, CH = 16 * NW;
+  constexpr int KS = 2 * HD + 16;  // LDS bytes per staged row: the f16 row and 16 bytes of padding
+  __shared__ __attribute__((aligned(16))) uint8_t s_k[CH * KS];
+  __shared__ __attribute__((aligned(16))) uint8_t s_v[CH * KS];
+  const int group = p.group, tpw = 16 / group;
+  const int split = blockIdx.x, kh = blockIdx.y, S = gridDim.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int col = lane & 15, kq = lane >> 4;
+  const int64_t kvd = int64_t(p.nkv) * HD;
+  const int p0 = split * CH;
+  const int tg0 = blockIdx.z * NW * tpw;                    // the workgroup's first token
+  const int tg_last = min(tg0 + NW * tpw, p.n_tok) - 1;      // and its last
+  const int pl = min(p0 + CH, p.active + tg_last);           // slots any of its tokens attends to
+  const int tw0 = tg0 + wv * tpw;                            // this wave's first token
+  const int ncol = max(0, min(tpw, p.n_tok - tw0)) * group;  // this wave's valid columns
+  // 1. K and V rows of slots p0 .. p0 + 63: row r = tid / 4, a quarter of it per thread
+  {
+    const int r = tid >> 2, qq = tid & 3;
+    const int ps = max(0, min(p0 + r, pl - 1));
+    const uint8_t* kb = static_cast<const uint8_t*>(p.k) + (int64_t(ps) * kvd + int64_t(kh) * HD) * 2 + qq * (HD / 2);
+    const uint8_t* vb = static_cast<const uint8_t*>(p.v) + (int64_t(ps) * kvd + int64_t(kh) * HD) * 2 + qq * (HD / 2);
+    u32x4 kr[HD / 32], vr[HD / 32];
+#pragma unroll
+    for (int j = 0; j < HD / 32; j++) kr[j] = ld4(kb + 16 * j);
+#pragma unroll
+    for (int j = 0; j < HD / 32; j++) vr[j] = ld4(vb + 16 * j);
+    const bool vz = p0 + r >= pl;
+#pragma unroll
+    for (int j = 0; j < HD / 32; j++) {
+      *reinterpret_cast<u32x4*>(s_k + r * KS + qq * (HD / 2) + 16 * j) = kr[j];
+      *reinterpret_cast<u32x4*>(s_v + r * KS + qq * (HD / 2) + 16 * j) = vz ? u32x4{0u, 0u, 0u, 0u} : vr[j];
+    }
+  }
+  // 2. this lane's q fragments for column col (token tw0 + col / group, head col % group), scaled
+  const bool cvalid = col < ncol;
+  const int ctl = cvalid ? col / group : 0, chd = cvalid ? col % group : 0;
+  // (a wave past the last token reads the last token's row and uses none of it)
+  const float* qrow = p.q + int64_t(min(tw0 + ctl, p.n_tok - 1)) * p.q_stride + (int64_t(kh) * group + chd) * HD;
+  h4_t qhi[NT], qlo[NT];
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    const int d = 8 * (4 * (i / 2) + kq) + 4 * (i % 2);
+    const float4 q = *reinterpret_cast<const float4*>(qrow + d);
+    const float qa[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const float v = cvalid ? qa[t] * p.scale : 0.f;
+      const _Float16 hi = _Float16(v);
+      qhi[i][t] = hi;
+      qlo[i][t] = _Float16(v - float(hi));
+    }
+  }
+  // the column's slot limit (its token's causal bound, within the staged range)
+  const int lim = cvalid ? min(pl, p.active + tw0 + ctl) : 0;
+  lds_barrier();
+  float m = -INFINITY, l = 0.f;
+  f4_t o[NT];
+#pragma unroll
+  for (int i = 0; i < NT; i++) o[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+  h4_t ident;
+#pragma unroll
+  for (int t = 0; t < 4; t++) ident[t] = _Float16(4 * kq + t == col ? 1.0f : 0.0f);
+  for (int cc = 0; cc < NW; cc++) {
+    const int c0 = p0 + 16 * cc;
+    if (c0 >= pl) break;  // uniform: no slot of this chunk is attended by any token
+    // scores: lane holds column col, slots c0 + 4 kq + r
+    f4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+      const u32x4 c = *reinterpret_cast<const u32x4*>(s_k + (16 * cc + col) * KS + 16 * (4 * j + kq));
+      const h4_t a0 = h4_of(c.x, c.y), a1 = h4_of(c.z, c.w);
+      sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, qhi[2 * j], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, qlo[2 * j], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, qhi[2 * j + 1], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, qlo[2 * j + 1], sc, 0, 0, 0);
+    }
+    float s[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) s[r] = c0 + 4 * kq + r < lim ? sc[r] : -INFINITY;
+    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float mn = fmaxf(m, mx);
+    const float alpha = mn == -INFINITY ? 1.f : exp_fast(m - mn);
+    float e[4], sum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      e[r] = mn == -INFINITY ? 0.f : exp_fast(s[r] - mn);
+      sum += e[r];
+    }
+    sum += __shfl_xor(sum, 16, kWave);
+    sum += __shfl_xor(sum, 32, kWave);
+    l = l * alpha + sum;
+    m = mn;
+    // the accumulators hold columns 4 kq + r: their factors from the lanes of those columns
+    float ar[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) ar[r] = __shfl(alpha, 4 * kq + r, kWave);
+    h4_t phi, plo;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const _Float16 hi = _Float16(e[r]);
+      phi[r] = hi;
+      plo[r] = _Float16(e[r] - float(hi));
+    }
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+      const u32x4 c = *reinterpret_cast<const u32x4*>(s_v + (16 * cc + col) * KS + 16 * (4 * j + kq));
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int i = 2 * j + h;
+        const h4_t a = h ? h4_of(c.z, c.w) : h4_of(c.x, c.y);
+        const f4_t vt = __builtin_amdgcn_mfma_f32_16x16x16f16(a, ident, f4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        h4_t b;
+#pragma unroll
+        for (int t = 0; t < 4; t++) b[t] = _Float16(vt[t]);  // exact: the values are f16
+#pragma unroll
+        for (int r = 0; r < 4; r++) o[i][r] *= ar[r];
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, b, o[i], 0, 0, 0);
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, b, o[i], 0, 0, 0);
+      }
+    }
+  }
+  // 3. partials: o[i][r] is column 4 kq + r at dim 8 (4 (i / 2) + col / 4) + 4 (i % 2) + col % 4
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int c = 4 * kq + r;
+    if (c < ncol) {
+      const int tl = c / group, h = c % group;
+      float* po = p.part_o + int64_t(tw0 + tl) * p.part_tok + (int64_t(kh * group + h) * S + split) * HD;
+#pragma unroll
+      for (int i = 0; i < NT; i++) po[8 * (4 * (i / 2) + (col >> 2)) + 4 * (i & 1) + (col & 3)] = o[i][r];
+    }
+  }
+  if (kq == 0 && cvalid) {
+    float* ml = p.part_ml + int64_t(tw0 + ctl) * p.part_tok_ml + (int64_t(kh * group + chd) * S + split) * 2;
+    ml[0] = m;
+    ml[1] = l;
   }
 }
 
@@ -906,10 +1047,9 @@ static void launch_partial(const AttnParams& p, int S, int T, hipStream_t s) {
 
 template <int HD, bool FUSED>
 static void launch_mfma(const AttnParams& p, int S, int T, hipStream_t s) {
-  if (!FUSED && T > 1) {  // a batch of queries: 16 / group tokens per workgroup
-    const int tpw = 16 / p.group;
-    hipLaunchKernelGGL((attn_mfma_kernel<HD, 16, false, true>), dim3(S, p.nkv, (T + tpw - 1) / tpw),
-                       dim3(kAttnThreads), 0, s, p);
+  if (!FUSED && T > 1) {  // a batch of queries: 16 / group tokens per wave
+    const int tpg = (kAttnThreads / kWave) * (16 / p.group);
+    hipLaunchKernelGGL((attn_prefill_kernel<HD>), dim3(S, p.nkv, (T + tpg - 1) / tpg), dim3(kAttnThreads), 0, s, p);
     return;
   }
   const dim3 grid(S, p.nkv, T);

@@ -23,6 +23,7 @@ SMALL = dict(hidden=512, ffn=1024, n_layers=3, vocab=1000, nq=8, nkv=2, hd=64, e
 @pytest.mark.parametrize("mix,kv_name,qk_norm,cap,pos0,n", [
     ("q4_k_m", "f16", True, 400, 0, 17),       # Q4_K_R rows through the int8-MFMA GEMM, Q6_K rows per token
     ("q4_k_m", "f32", True, 400, 37, 300),     # a prompt longer than one attention batch, after a filled ring
+    ("q4_k_m", "f16", True, 400, 37, 300),     # the same on the f16 ring (the batched MFMA attention kernel)
     ("q8_0", "f16", False, 128, 5, 40),         # Q8_0 rows (GEMV per row), no QK-norm
     ("q4_k_m", "f16", True, 64, 0, 1)])         # a one-token prompt
 def test_prefill_matches_oracle(dev, mix, kv_name, qk_norm, cap, pos0, n):

@@ -1075,8 +1075,68 @@ static void launch_combine(const AttnParams& p, int S, int T, float* out, int64_
                        p.part_tok_ml, out_stride);
 }
 
+// The merge of a batch of queries fused with the Q8_K quantization of their attention rows (the
+// output projection's input): one workgroup per token; thread t combines 16 consecutive dims of
+// one head over the head's S splits (weights exp(m_s - M) over the splits that saw a slot;
+// splits with l = 0 never wrote their rows and are selected out), the row goes through LDS, and
+// a wave per 256-block quantizes it as quant_q8k_kernel does.  out (when given) receives the f32
+// row.  nq * HD a multiple of 256, at most kMergeQ8kMax.
+constexpr int kMergeQ8kMax = 8192;
+template <int HD>
+__global__ void __launch_bounds__(256) attn_merge_q8k_kernel(const float* __restrict__ part_o,
+                                                             const float* __restrict__ part_ml, int S, int nq,
+                                                             int64_t tok_o, int64_t tok_ml, float* __restrict__ out,
+                                                             int64_t out_stride, uint8_t* __restrict__ Q) {
+  __shared__ __attribute__((aligned(16))) float s_row[kMergeQ8kMax];
+  const int t = blockIdx.x, row_len = nq * HD;
+  part_o += int64_t(t) * tok_o;
+  part_ml += int64_t(t) * tok_ml;
+  for (int base = threadIdx.x * 16; base < row_len; base += 256 * 16) {
+    const int h = base / HD, d0 = base - h * HD;
+    const float2* ml = reinterpret_cast<const float2*>(part_ml) + int64_t(h) * S;
+    float M = -INFINITY;
+    for (int sp = 0; sp < S; sp++) {
+      const float2 e = ml[sp];
+      if (e.y > 0.f) M = fmaxf(M, e.x);
+    }
+    float acc[16], L = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) acc[k] = 0.f;
+    for (int sp = 0; sp < S; sp++) {
+      const float2 e = ml[sp];
+      const bool use = e.y > 0.f;
+      const float w = use ? exp_fast(e.x - M) : 0.f;
+      L += w * e.y;
+      const float4* o = reinterpret_cast<const float4*>(part_o + (int64_t(h) * S + sp) * HD + d0);
+      float4 v[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) v[k] = o[k];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        acc[4 * k] += use ? w * v[k].x : 0.f;
+        acc[4 * k + 1] += use ? w * v[k].y : 0.f;
+        acc[4 * k + 2] += use ? w * v[k].z : 0.f;
+        acc[4 * k + 3] += use ? w * v[k].w : 0.f;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) s_row[base + k] = acc[k] / L;
+  }
+  __syncthreads();
+  if (out)
+    for (int i = threadIdx.x; i < row_len; i += 256) out[int64_t(t) * out_stride + i] = s_row[i];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  uint8_t* q = Q + int64_t(t) * (row_len / 256) * 292;
+  for (int j = wv; j < row_len / 256; j += 4) {
+    const float4 v = reinterpret_cast<const float4*>(s_row + 256 * j)[lane];
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    q8k_block_wave(e, lane, q + int64_t(j) * 292);
+  }
+}
+
 // The split-K partial kernel over S splits for T queries, then the merge.
-static int attention_impl(AttnParams p, bool fused, int S, int T, float* out, int64_t out_stride, hipStream_t s) {
+static int attention_impl(AttnParams p, bool fused, int S, int T, float* out, int64_t out_stride, hipStream_t s,
+                          void* q8k = nullptr) {
   const int64_t nq = int64_t(p.nkv) * p.group;
   p.part_tok = T > 1 ? nq * S * p.hd : 0;
   p.part_tok_ml = T > 1 ? nq * S * 2 : 0;
@@ -1100,6 +1160,16 @@ static int attention_impl(AttnParams p, bool fused, int S, int T, float* out, in
 #undef JERO_ATTN_CASE
   int rc = check_launch("attention partial");
   if (rc) return rc;
+  if (q8k) {  // the merge writes the rows' Q8_K blocks (and the f32 rows when out is given)
+    const int nq32 = int(nq);
+    if (p.hd == 64)
+      hipLaunchKernelGGL(attn_merge_q8k_kernel<64>, dim3(unsigned(T)), dim3(256), 0, s, p.part_o, p.part_ml, S, nq32,
+                         p.part_tok, p.part_tok_ml, out, out_stride, static_cast<uint8_t*>(q8k));
+    else
+      hipLaunchKernelGGL(attn_merge_q8k_kernel<128>, dim3(unsigned(T)), dim3(256), 0, s, p.part_o, p.part_ml, S, nq32,
+                         p.part_tok, p.part_tok_ml, out, out_stride, static_cast<uint8_t*>(q8k));
+    return check_launch("attention merge + q8_k");
+  }
   if (p.hd == 32) launch_combine<32>(p, S, T, out, out_stride, s);
   else if (p.hd == 64) launch_combine<64>(p, S, T, out, out_stride, s);
   else launch_combine<128>(p, S, T, out, out_stride, s);
@@ -1111,11 +1181,17 @@ int launch_attention(const AttnParams& p, bool fused, float* out, hipStream_t s)
 }
 
 int launch_attention_tokens(const AttnParams& p0, int n_tok, int64_t q_stride, float* out, int64_t out_stride,
-                            hipStream_t s) {
+                            hipStream_t s, void* q8k) {
   if (n_tok <= 0 || n_tok > 65535) return fail(JERO_ERR_TENSOR_BOUNDS, "attention: query batch of 1..65535 tokens");
   AttnParams p = p0;
   p.q_stride = q_stride;
-  return attention_impl(p, false, attn_splits(p.active + n_tok - 1, p.hd), n_tok, out, out_stride, s);
+  if (q8k && !attn_merge_q8k_ok(p.nkv * p.group, p.hd, n_tok))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: no Q8_K merge for this shape");
+  return attention_impl(p, false, attn_splits(p.active + n_tok - 1, p.hd), n_tok, out, out_stride, s, q8k);
+}
+
+bool attn_merge_q8k_ok(int nq, int hd, int n_tok) {
+  return n_tok > 1 && (hd == 64 || hd == 128) && (int64_t(nq) * hd) % 256 == 0 && int64_t(nq) * hd <= kMergeQ8kMax;
 }
 
 static_assert(int64_t(kMaxSplits) * attn_chunk(64) == JERO_MAX_ATTENTION_POSITIONS, "attention position limit");

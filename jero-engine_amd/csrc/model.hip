@@ -877,6 +877,11 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
     if ((rc = snap(fld(L, TraceLayout::kQRope), qp, 4 * qs, 4 * Q)) ||
         (rc = snap(fld(L, TraceLayout::kKRope), kp, 4 * ks, 4 * KV)))
       return rc;
+    // the merge of each batch writes the Q8_K rows of Wo's input itself when Wo reads Q8_K and no
+    // batch holds a single token (the f32 rows then only for the trace)
+    const int64_t rbq = row_bytes(JERO_Q8_K, Q);
+    const bool att_q8k = l.wo.present() && act_format(l.wo.quant) == JERO_Q8_K && n > 1 &&
+                         n % kPrefillAttnTokens != 1 && attn_merge_q8k_ok(int(c.n_heads_q), int(c.head_dim), 2);
     for (int64_t t0 = 0; t0 < n; t0 += kPrefillAttnTokens) {
       const int64_t nt = std::min(kPrefillAttnTokens, n - t0);
       AttnParams p{};
@@ -891,11 +896,18 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
       p.scale = 1.0f / sqrtf(float(c.head_dim));
       p.part_o = b.ws;
       p.slot = -1;
-      if ((rc = launch_attention_tokens(p, int(nt), qs, b.ATT + t0 * Q, Q, s))) return rc;
+      if ((rc = launch_attention_tokens(p, int(nt), qs, !att_q8k || m->trace ? b.ATT + t0 * Q : nullptr, Q, s,
+                                        att_q8k ? b.XQ + t0 * rbq : nullptr)))
+        return rc;
     }
     if ((rc = snap(fld(L, TraceLayout::kAttn), b.ATT, 4 * Q, 4 * Q))) return rc;
     // output projection; its residual is added by the FFN's row step
     have_fmt = -1;
+    if (att_q8k) {
+      have_fmt = JERO_Q8_K;
+      xrb = rbq;
+      if ((rc = snap(fld(L, TraceLayout::kQ8Wo), b.XQ, size_t(rbq), size_t(rbq)))) return rc;
+    }
     if (l.wo.present()) {
       bool split = false;
       if ((rc = project(l.wo, b.ATT, Q, b.T, TraceLayout::kQ8Wo, &split))) return rc;

@@ -45,6 +45,23 @@ def test_prefill_matches_oracle(dev, mix, kv_name, qk_norm, cap, pos0, n):
     m.close()
 
 
+@pytest.mark.parametrize("nq,nkv,hd", [(16, 2, 64), (4, 4, 64), (4, 2, 128)])
+def test_prefill_group_sizes(dev, nq, nkv, hd):
+    """The batched attention kernel gives each wave 16 / group tokens: groups of 8, 1 and 2 (head_dim
+    64 and 128), f16 ring, 40 prompt tokens after 37 filled slots (crossing a 64-slot split)."""
+    print(f"prefill nq={nq} nkv={nkv} hd={hd}", flush=True)
+    spec = dict(SMALL, nq=nq, nkv=nkv, hd=hd, n_layers=2)
+    cap, pos0, n = 128, 37, 40
+    t = MS.build(spec, seed=29)
+    m = make_gpu_model(spec, t, cap, J.KV_F16, True)
+    om = O.DecodeModel(spec, MS.oracle_tensors(t), cap)
+    kv = prefill_kv(m, om, spec, cap, pos0, 31, dev, True)
+    tokens = np.random.default_rng(nq * 10 + nkv).integers(0, spec["vocab"], size=n).tolist()
+    gtok, _ = DP.run_prefill_traced(m, om, t, spec, kv, cap, pos0, tokens, True, dev, True)
+    DP.run_traced(m, om, t, spec, kv, cap, pos0 + n, 2, True, dev, gtok, True)
+    m.close()
+
+
 def test_prefill_matches_decode_steps_8b_layer_shape(dev):
     """Two layers of the Qwen3-8B shape, f16 ring: a 24-token prompt after 4000 filled slots."""
     spec = dict(hidden=4096, ffn=12288, n_layers=2, vocab=151936, nq=32, nkv=8, hd=128, eps=1e-6, theta=1e6)

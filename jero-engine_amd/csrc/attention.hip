@@ -27,6 +27,7 @@ constexpr int kAttnThreads = 256;
 // were 17 % slower).  The 16-byte K/V tiling needs at least 64 positions at head_dim 32.
 __host__ __device__ constexpr int attn_chunk(int /*hd*/) { return 64; }
 constexpr int kMaxGroup = 8;    // q heads per kv head
+constexpr int kFlashThreads = 512;  // the prefill's flash kernel: 8 waves
 
 template <typename T>
 __device__ __forceinline__ void widen16(const u32x4 v, float* out);
@@ -412,6 +413,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_partial_kernel(AttnParams p
 
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ h4_t h4_of(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(h4_t, (uint64_t(hi) << 32) | lo);
@@ -699,155 +701,210 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
   }
 }
 
-// A batch of consecutive queries (the prefill) over f16 rings: grid (S, nkv, ceil(T / (NW tpw)))
-// with tpw = 16 / group tokens per wave.  The workgroup stages its 64 ring slots' K and V rows in
-// LDS once (slots past the last token's limit: V zero, a slot there may hold anything); wave w
-// owns the 16 score columns (token, head) of its tpw tokens, all heads of the group, and runs the
-// four 16-slot chunks through an online softmax, so a K/V row serves NW * tpw tokens.  Per
-// chunk: S^T = K q on v_mfma_f32_16x16x16_f16 (q split into f16 hi + lo, as in attn_mfma_kernel),
-// the running max and sum per column over the 4 lanes that hold it, the accumulators rescaled,
-// P V with V^T through the identity MFMA.  Each wave then writes its columns' (m, l, o) partials
-// in attn_mfma_kernel's layout, which the merge kernel combines.
+// Causal attention of a batch of consecutive queries (the prefill) over an f16 ring, flash
+// style: grid (ceil(T / (4 tpw)), nkv) with tpw = 16 / group tokens per column set, the token
+// blocks with the longest causal ranges first.  Eight waves: column set w % 4 holds the 16 score
+// columns (token, head) of its tpw tokens, all heads of the group, and waves w and w + 4 share
+// them, taking alternate 64-slot runs.  The workgroup walks the slots its tokens attend to
+// (query t of the batch: the first active + t slots) 128 at a time, stages their K and V rows in
+// LDS (V zero past the last attended slot; the next 128 rows are loaded into registers while
+// the current ones are used; V transposed, [dim][slot]), and each wave takes its run's four
+// 16-slot chunks through an online softmax (running max and sum per column over the 4 lanes
+// that hold it, the accumulators rescaled per chunk).  The two waves' states of a column are
+// merged through LDS at the end.  Per chunk: S^T = K q on v_mfma_f32_16x16x32_f16
+// (q split into f16 hi + lo, one accumulator each), P V on v_mfma_f32_16x16x16_f16 with the
+// B operand read straight from V^T (P split likewise).  No split partials: the rows
+// o / l go through LDS and are written as f32 rows (out, when given) and, when q8k is given, as
+// the Q8_K blocks of Wo's input (group * HD a multiple of 256: the group's heads fill whole
+// blocks), quantized from the same f32 values.
 template <int HD>
-__global__ void __launch_bounds__(kAttnThreads) attn_prefill_kernel(AttnParams p) {
-  constexpr int NCH = HD / 32, NT = HD / 16, NW = kAttnThreads / kWave, CH = 16 * NW;
-  constexpr int KS = 2 * HD + 16;  // LDS bytes per staged row: the f16 row and 16 bytes of padding
-  __shared__ __attribute__((aligned(16))) uint8_t s_k[CH * KS];
-  __shared__ __attribute__((aligned(16))) uint8_t s_v[CH * KS];
+__global__ void __launch_bounds__(kFlashThreads) attn_flash_kernel(AttnParams p, float* __restrict__ out,
+                                                                   int64_t out_stride, uint8_t* __restrict__ q8k) {
+  constexpr int NCH = HD / 32, NT = HD / 16, NCS = 4, CH = 64, RS = 2 * CH;
+  constexpr int NW = kFlashThreads / kWave;
+  constexpr int KS = 2 * HD + 16;  // LDS bytes per staged K row: the f16 row and 16 bytes of padding
+  constexpr int VTS = RS + 8;      // f16 per row of V^T (one row per dim)
+  // K rows, then V^T.  After the runs: the second waves' partial states at the start, the
+  // workgroup's output rows ((64 / group) * group * HD floats = 256 HD bytes) after RS K rows
+  __shared__ __attribute__((aligned(16))) uint8_t s_kv[RS * KS + HD * VTS * 2];
+  constexpr int PO_BYTES = NCS * NT * 4 * 64 * 4 + NCS * 16 * 2 * 4;
+  static_assert(PO_BYTES <= RS * KS && RS * KS + 256 * HD <= RS * KS + HD * VTS * 2, "merge areas fit the staging");
+  uint8_t* const s_k = s_kv;
+  _Float16* const s_vt = reinterpret_cast<_Float16*>(s_kv + RS * KS);
   const int group = p.group, tpw = 16 / group;
-  const int split = blockIdx.x, kh = blockIdx.y, S = gridDim.x;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int kh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, cs = wv & 3, rp = wv >> 2;
   const int col = lane & 15, kq = lane >> 4;
   const int64_t kvd = int64_t(p.nkv) * HD;
-  const int p0 = split * CH;
-  const int tg0 = blockIdx.z * NW * tpw;                    // the workgroup's first token
-  const int tg_last = min(tg0 + NW * tpw, p.n_tok) - 1;      // and its last
-  const int pl = min(p0 + CH, p.active + tg_last);           // slots any of its tokens attends to
-  const int tw0 = tg0 + wv * tpw;                            // this wave's first token
-  const int ncol = max(0, min(tpw, p.n_tok - tw0)) * group;  // this wave's valid columns
-  // 1. K and V rows of slots p0 .. p0 + 63: row r = tid / 4, a quarter of it per thread
-  {
-    const int r = tid >> 2, qq = tid & 3;
-    const int ps = max(0, min(p0 + r, pl - 1));
-    const uint8_t* kb = static_cast<const uint8_t*>(p.k) + (int64_t(ps) * kvd + int64_t(kh) * HD) * 2 + qq * (HD / 2);
-    const uint8_t* vb = static_cast<const uint8_t*>(p.v) + (int64_t(ps) * kvd + int64_t(kh) * HD) * 2 + qq * (HD / 2);
-    u32x4 kr[HD / 32], vr[HD / 32];
+  const int tg0 = int(gridDim.x - 1 - blockIdx.x) * NCS * tpw;  // the workgroup's first token
+  const int ntl = min(NCS * tpw, p.n_tok - tg0);                 // and its token count
+  const int pl = p.active + tg0 + ntl - 1;                       // slots any of its tokens attends to
+  const int nstep = (pl + RS - 1) / RS;
+  const int tw0 = tg0 + cs * tpw;                                // this wave's first token
+  const int ncol = max(0, min(tpw, p.n_tok - tw0)) * group;      // this wave's valid columns
+  // staging: row r = tid / 4 of the 128 slots, a quarter of it per thread
+  const int r = tid >> 2, qq = tid & 3;
+  const uint8_t* const kb = static_cast<const uint8_t*>(p.k) + int64_t(kh) * HD * 2 + qq * (HD / 2);
+  const uint8_t* const vb = static_cast<const uint8_t*>(p.v) + int64_t(kh) * HD * 2 + qq * (HD / 2);
+  u32x4 kr[HD / 32], vr[HD / 32];
+  auto load_step = [&](int st) {
+    const int64_t o = int64_t(min(st * RS + r, pl - 1)) * kvd * 2;
 #pragma unroll
-    for (int j = 0; j < HD / 32; j++) kr[j] = ld4(kb + 16 * j);
+    for (int j = 0; j < HD / 32; j++) kr[j] = ld4(kb + o + 16 * j);
 #pragma unroll
-    for (int j = 0; j < HD / 32; j++) vr[j] = ld4(vb + 16 * j);
-    const bool vz = p0 + r >= pl;
-#pragma unroll
-    for (int j = 0; j < HD / 32; j++) {
-      *reinterpret_cast<u32x4*>(s_k + r * KS + qq * (HD / 2) + 16 * j) = kr[j];
-      *reinterpret_cast<u32x4*>(s_v + r * KS + qq * (HD / 2) + 16 * j) = vz ? u32x4{0u, 0u, 0u, 0u} : vr[j];
-    }
-  }
-  // 2. this lane's q fragments for column col (token tw0 + col / group, head col % group), scaled
+    for (int j = 0; j < HD / 32; j++) vr[j] = ld4(vb + o + 16 * j);
+  };
+  load_step(0);
+  // this lane's q fragments for column col (token tw0 + col / group, head col % group), scaled
   const bool cvalid = col < ncol;
   const int ctl = cvalid ? col / group : 0, chd = cvalid ? col % group : 0;
   // (a wave past the last token reads the last token's row and uses none of it)
   const float* qrow = p.q + int64_t(min(tw0 + ctl, p.n_tok - 1)) * p.q_stride + (int64_t(kh) * group + chd) * HD;
-  h4_t qhi[NT], qlo[NT];
+  h8_t qhi[NCH], qlo[NCH];  // dims 32 j + 8 kq .. + 8, the K-row fragment's dims
 #pragma unroll
-  for (int i = 0; i < NT; i++) {
-    const int d = 8 * (4 * (i / 2) + kq) + 4 * (i % 2);
-    const float4 q = *reinterpret_cast<const float4*>(qrow + d);
-    const float qa[4] = {q.x, q.y, q.z, q.w};
+  for (int j = 0; j < NCH; j++) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const float v = cvalid ? qa[t] * p.scale : 0.f;
-      const _Float16 hi = _Float16(v);
-      qhi[i][t] = hi;
-      qlo[i][t] = _Float16(v - float(hi));
+    for (int h = 0; h < 2; h++) {
+      const float4 q = *reinterpret_cast<const float4*>(qrow + 32 * j + 8 * kq + 4 * h);
+      const float qa[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const float v = cvalid ? qa[t] * p.scale : 0.f;
+        const _Float16 hi = _Float16(v);
+        qhi[j][4 * h + t] = hi;
+        qlo[j][4 * h + t] = _Float16(v - float(hi));
+      }
     }
   }
-  // the column's slot limit (its token's causal bound, within the staged range)
-  const int lim = cvalid ? min(pl, p.active + tw0 + ctl) : 0;
-  lds_barrier();
+  const int lim = cvalid ? p.active + tw0 + ctl : 0;  // the column's slots: [0, lim)
   float m = -INFINITY, l = 0.f;
   f4_t o[NT];
 #pragma unroll
   for (int i = 0; i < NT; i++) o[i] = f4_t{0.f, 0.f, 0.f, 0.f};
-  h4_t ident;
+  for (int st = 0; st < nstep; st++) {
+    const int p0 = st * RS + rp * CH;  // this wave's run
+    if (st) lds_barrier();             // every wave is done with the previous rows
+    const bool vz = st * RS + r >= pl;
 #pragma unroll
-  for (int t = 0; t < 4; t++) ident[t] = _Float16(4 * kq + t == col ? 1.0f : 0.0f);
-  for (int cc = 0; cc < NW; cc++) {
-    const int c0 = p0 + 16 * cc;
-    if (c0 >= pl) break;  // uniform: no slot of this chunk is attended by any token
-    // scores: lane holds column col, slots c0 + 4 kq + r
-    f4_t sc = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < HD / 32; j++) {
+      *reinterpret_cast<u32x4*>(s_k + r * KS + qq * (HD / 2) + 16 * j) = kr[j];
+      const uint32_t w[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
 #pragma unroll
-    for (int j = 0; j < NCH; j++) {
-      const u32x4 c = *reinterpret_cast<const u32x4*>(s_k + (16 * cc + col) * KS + 16 * (4 * j + kq));
-      const h4_t a0 = h4_of(c.x, c.y), a1 = h4_of(c.z, c.w);
-      sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, qhi[2 * j], sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, qlo[2 * j], sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, qhi[2 * j + 1], sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, qlo[2 * j + 1], sc, 0, 0, 0);
+      for (int t = 0; t < 8; t++) {  // dim qq HD / 4 + 8 j + t of slot r
+        const uint16_t h = vz ? uint16_t(0) : uint16_t(w[t / 2] >> (16 * (t % 2)));
+        s_vt[(qq * (HD / 4) + 8 * j + t) * VTS + r] = __builtin_bit_cast(_Float16, h);
+      }
     }
-    float s[4];
+    load_step(min(st + 1, nstep - 1));  // the next rows (the last step reloads itself: no branch)
+    lds_barrier();
+    for (int cc = 0; cc < 4; cc++) {
+      const int c0 = p0 + 16 * cc;
+      if (c0 >= pl) break;  // uniform in the wave: no slot of this chunk is attended by any token
+      // scores: lane holds column col, slots c0 + 4 kq + r
+      f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; r++) s[r] = c0 + 4 * kq + r < lim ? sc[r] : -INFINITY;
-    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float mn = fmaxf(m, mx);
-    const float alpha = mn == -INFINITY ? 1.f : exp_fast(m - mn);
-    float e[4], sum = 0.f;
+      for (int j = 0; j < NCH; j++) {
+        const h8_t a = __builtin_bit_cast(h8_t, *reinterpret_cast<const u32x4*>(s_k + (rp * CH + 16 * cc + col) * KS +
+                                                                                16 * (4 * j + kq)));
+        sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qhi[j], sh, 0, 0, 0);
+        sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qlo[j], sl, 0, 0, 0);
+      }
+      float s[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      e[r] = mn == -INFINITY ? 0.f : exp_fast(s[r] - mn);
-      sum += e[r];
-    }
-    sum += __shfl_xor(sum, 16, kWave);
-    sum += __shfl_xor(sum, 32, kWave);
-    l = l * alpha + sum;
-    m = mn;
-    // the accumulators hold columns 4 kq + r: their factors from the lanes of those columns
-    float ar[4];
+      for (int rr = 0; rr < 4; rr++) s[rr] = c0 + 4 * kq + rr < lim ? sh[rr] + sl[rr] : -INFINITY;
+      float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float mn = fmaxf(m, mx);
+      const float alpha = mn == -INFINITY ? 1.f : exp_fast(m - mn);
+      float e[4], sum = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; r++) ar[r] = __shfl(alpha, 4 * kq + r, kWave);
-    h4_t phi, plo;
+      for (int rr = 0; rr < 4; rr++) {
+        e[rr] = mn == -INFINITY ? 0.f : exp_fast(s[rr] - mn);
+        sum += e[rr];
+      }
+      sum += __shfl_xor(sum, 16, kWave);
+      sum += __shfl_xor(sum, 32, kWave);
+      l = l * alpha + sum;
+      m = mn;
+      // the accumulators hold columns 4 kq + rr: their factors from the lanes of those columns
+      float ar[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const _Float16 hi = _Float16(e[r]);
-      phi[r] = hi;
-      plo[r] = _Float16(e[r] - float(hi));
-    }
+      for (int rr = 0; rr < 4; rr++) ar[rr] = __shfl(alpha, 4 * kq + rr, kWave);
+      h4_t phi, plo;
 #pragma unroll
-    for (int j = 0; j < NCH; j++) {
-      const u32x4 c = *reinterpret_cast<const u32x4*>(s_v + (16 * cc + col) * KS + 16 * (4 * j + kq));
+      for (int rr = 0; rr < 4; rr++) {
+        const _Float16 hi = _Float16(e[rr]);
+        phi[rr] = hi;
+        plo[rr] = _Float16(e[rr] - float(hi));
+      }
+      // o[i]: columns 4 kq + rr, dim 16 i + col; B = V[slots c0 + 4 kq ..][dim 16 i + col] from V^T
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int i = 2 * j + h;
-        const h4_t a = h ? h4_of(c.z, c.w) : h4_of(c.x, c.y);
-        const f4_t vt = __builtin_amdgcn_mfma_f32_16x16x16f16(a, ident, f4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        h4_t b;
+      for (int i = 0; i < NT; i++) {
+        const h4_t bv = *reinterpret_cast<const h4_t*>(s_vt + (16 * i + col) * VTS + rp * CH + 16 * cc + 4 * kq);
 #pragma unroll
-        for (int t = 0; t < 4; t++) b[t] = _Float16(vt[t]);  // exact: the values are f16
-#pragma unroll
-        for (int r = 0; r < 4; r++) o[i][r] *= ar[r];
-        o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, b, o[i], 0, 0, 0);
-        o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, b, o[i], 0, 0, 0);
+        for (int rr = 0; rr < 4; rr++) o[i][rr] *= ar[rr];
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, bv, o[i], 0, 0, 0);
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, bv, o[i], 0, 0, 0);
       }
     }
   }
-  // 3. partials: o[i][r] is column 4 kq + r at dim 8 (4 (i / 2) + col / 4) + 4 (i % 2) + col % 4
+  // merge the two waves of each column set; o[i][rr] is column 4 kq + rr at dim 16 i + col
+  float* const s_po = reinterpret_cast<float*>(s_kv);  // [set][i][rr][lane]
+  float* const s_pml = s_po + NCS * NT * 4 * 64;       // [set][column][m, l]
+  const int rowlen = group * HD;
+  float* const s_row = reinterpret_cast<float*>(s_kv + RS * KS);  // [token of the workgroup][group * HD]
+  lds_barrier();  // every wave is done with the staged rows
+  if (rp == 1) {
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int c = 4 * kq + r;
-    if (c < ncol) {
-      const int tl = c / group, h = c % group;
-      float* po = p.part_o + int64_t(tw0 + tl) * p.part_tok + (int64_t(kh * group + h) * S + split) * HD;
+    for (int i = 0; i < NT; i++)
 #pragma unroll
-      for (int i = 0; i < NT; i++) po[8 * (4 * (i / 2) + (col >> 2)) + 4 * (i & 1) + (col & 3)] = o[i][r];
+      for (int rr = 0; rr < 4; rr++) s_po[((cs * NT + i) * 4 + rr) * 64 + lane] = o[i][rr];
+    if (kq == 0) {
+      s_pml[(cs * 16 + col) * 2] = m;
+      s_pml[(cs * 16 + col) * 2 + 1] = l;
     }
   }
-  if (kq == 0 && cvalid) {
-    float* ml = p.part_ml + int64_t(tw0 + ctl) * p.part_tok_ml + (int64_t(kh * group + chd) * S + split) * 2;
-    ml[0] = m;
-    ml[1] = l;
+  lds_barrier();
+  if (rp == 0) {
+    const float m1 = s_pml[(cs * 16 + col) * 2], l1 = s_pml[(cs * 16 + col) * 2 + 1];
+    const float M = fmaxf(m, m1);
+    const float a0 = m == -INFINITY ? 0.f : exp_fast(m - M), a1 = m1 == -INFINITY ? 0.f : exp_fast(m1 - M);
+    const float lt = l * a0 + l1 * a1;
+    float f0[4], f1[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+      const float li = __shfl(lt, 4 * kq + rr, kWave);
+      f0[rr] = __shfl(a0, 4 * kq + rr, kWave) / li;
+      f1[rr] = __shfl(a1, 4 * kq + rr, kWave) / li;
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+      const int c = 4 * kq + rr;
+      if (c < ncol) {
+        float* dst = s_row + (cs * tpw + c / group) * rowlen + (c % group) * HD;
+#pragma unroll
+        for (int i = 0; i < NT; i++)
+          dst[16 * i + col] = o[i][rr] * f0[rr] + s_po[((cs * NT + i) * 4 + rr) * 64 + lane] * f1[rr];
+      }
+    }
+  }
+  lds_barrier();
+  if (out)
+    for (int idx = 4 * tid; idx < ntl * rowlen; idx += 4 * kFlashThreads) {
+      const int tl = idx / rowlen, e = idx - tl * rowlen;
+      *reinterpret_cast<float4*>(out + int64_t(tg0 + tl) * out_stride + int64_t(kh) * rowlen + e) =
+          *reinterpret_cast<const float4*>(s_row + idx);
+    }
+  if (q8k) {
+    const int bpt = rowlen / 256;                      // the group's Q8_K blocks per token
+    const int64_t rbq = int64_t(p.nkv) * bpt * 292;    // bytes of a token's Q8_K row
+    for (int jb = wv; jb < ntl * bpt; jb += NW) {
+      const int tl = jb / bpt, j = jb - tl * bpt;
+      const float4 v = reinterpret_cast<const float4*>(s_row + tl * rowlen + 256 * j)[lane];
+      const float ev[4] = {v.x, v.y, v.z, v.w};
+      q8k_block_wave(ev, lane, q8k + int64_t(tg0 + tl) * rbq + (int64_t(kh) * bpt + j) * 292);
+    }
   }
 }
 
@@ -1047,11 +1104,6 @@ static void launch_partial(const AttnParams& p, int S, int T, hipStream_t s) {
 
 template <int HD, bool FUSED>
 static void launch_mfma(const AttnParams& p, int S, int T, hipStream_t s) {
-  if (!FUSED && T > 1) {  // a batch of queries: 16 / group tokens per wave
-    const int tpg = (kAttnThreads / kWave) * (16 / p.group);
-    hipLaunchKernelGGL((attn_prefill_kernel<HD>), dim3(S, p.nkv, (T + tpg - 1) / tpg), dim3(kAttnThreads), 0, s, p);
-    return;
-  }
   const dim3 grid(S, p.nkv, T);
   if (p.group <= 1)
     hipLaunchKernelGGL((attn_mfma_kernel<HD, 1, FUSED>), grid, dim3(kAttnThreads), 0, s, p);
@@ -1075,68 +1127,8 @@ static void launch_combine(const AttnParams& p, int S, int T, float* out, int64_
                        p.part_tok_ml, out_stride);
 }
 
-// The merge of a batch of queries fused with the Q8_K quantization of their attention rows (the
-// output projection's input): one workgroup per token; thread t combines 16 consecutive dims of
-// one head over the head's S splits (weights exp(m_s - M) over the splits that saw a slot;
-// splits with l = 0 never wrote their rows and are selected out), the row goes through LDS, and
-// a wave per 256-block quantizes it as quant_q8k_kernel does.  out (when given) receives the f32
-// row.  nq * HD a multiple of 256, at most kMergeQ8kMax.
-constexpr int kMergeQ8kMax = 8192;
-template <int HD>
-__global__ void __launch_bounds__(256) attn_merge_q8k_kernel(const float* __restrict__ part_o,
-                                                             const float* __restrict__ part_ml, int S, int nq,
-                                                             int64_t tok_o, int64_t tok_ml, float* __restrict__ out,
-                                                             int64_t out_stride, uint8_t* __restrict__ Q) {
-  __shared__ __attribute__((aligned(16))) float s_row[kMergeQ8kMax];
-  const int t = blockIdx.x, row_len = nq * HD;
-  part_o += int64_t(t) * tok_o;
-  part_ml += int64_t(t) * tok_ml;
-  for (int base = threadIdx.x * 16; base < row_len; base += 256 * 16) {
-    const int h = base / HD, d0 = base - h * HD;
-    const float2* ml = reinterpret_cast<const float2*>(part_ml) + int64_t(h) * S;
-    float M = -INFINITY;
-    for (int sp = 0; sp < S; sp++) {
-      const float2 e = ml[sp];
-      if (e.y > 0.f) M = fmaxf(M, e.x);
-    }
-    float acc[16], L = 0.f;
-#pragma unroll
-    for (int k = 0; k < 16; k++) acc[k] = 0.f;
-    for (int sp = 0; sp < S; sp++) {
-      const float2 e = ml[sp];
-      const bool use = e.y > 0.f;
-      const float w = use ? exp_fast(e.x - M) : 0.f;
-      L += w * e.y;
-      const float4* o = reinterpret_cast<const float4*>(part_o + (int64_t(h) * S + sp) * HD + d0);
-      float4 v[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) v[k] = o[k];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        acc[4 * k] += use ? w * v[k].x : 0.f;
-        acc[4 * k + 1] += use ? w * v[k].y : 0.f;
-        acc[4 * k + 2] += use ? w * v[k].z : 0.f;
-        acc[4 * k + 3] += use ? w * v[k].w : 0.f;
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < 16; k++) s_row[base + k] = acc[k] / L;
-  }
-  __syncthreads();
-  if (out)
-    for (int i = threadIdx.x; i < row_len; i += 256) out[int64_t(t) * out_stride + i] = s_row[i];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  uint8_t* q = Q + int64_t(t) * (row_len / 256) * 292;
-  for (int j = wv; j < row_len / 256; j += 4) {
-    const float4 v = reinterpret_cast<const float4*>(s_row + 256 * j)[lane];
-    const float e[4] = {v.x, v.y, v.z, v.w};
-    q8k_block_wave(e, lane, q + int64_t(j) * 292);
-  }
-}
-
 // The split-K partial kernel over S splits for T queries, then the merge.
-static int attention_impl(AttnParams p, bool fused, int S, int T, float* out, int64_t out_stride, hipStream_t s,
-                          void* q8k = nullptr) {
+static int attention_impl(AttnParams p, bool fused, int S, int T, float* out, int64_t out_stride, hipStream_t s) {
   const int64_t nq = int64_t(p.nkv) * p.group;
   p.part_tok = T > 1 ? nq * S * p.hd : 0;
   p.part_tok_ml = T > 1 ? nq * S * 2 : 0;
@@ -1160,16 +1152,6 @@ static int attention_impl(AttnParams p, bool fused, int S, int T, float* out, in
 #undef JERO_ATTN_CASE
   int rc = check_launch("attention partial");
   if (rc) return rc;
-  if (q8k) {  // the merge writes the rows' Q8_K blocks (and the f32 rows when out is given)
-    const int nq32 = int(nq);
-    if (p.hd == 64)
-      hipLaunchKernelGGL(attn_merge_q8k_kernel<64>, dim3(unsigned(T)), dim3(256), 0, s, p.part_o, p.part_ml, S, nq32,
-                         p.part_tok, p.part_tok_ml, out, out_stride, static_cast<uint8_t*>(q8k));
-    else
-      hipLaunchKernelGGL(attn_merge_q8k_kernel<128>, dim3(unsigned(T)), dim3(256), 0, s, p.part_o, p.part_ml, S, nq32,
-                         p.part_tok, p.part_tok_ml, out, out_stride, static_cast<uint8_t*>(q8k));
-    return check_launch("attention merge + q8_k");
-  }
   if (p.hd == 32) launch_combine<32>(p, S, T, out, out_stride, s);
   else if (p.hd == 64) launch_combine<64>(p, S, T, out, out_stride, s);
   else launch_combine<128>(p, S, T, out, out_stride, s);
@@ -1180,18 +1162,33 @@ int launch_attention(const AttnParams& p, bool fused, float* out, hipStream_t s)
   return attention_impl(p, fused, attn_splits(p.pos_dev ? int(p.capacity) : p.active, p.hd), 1, out, 0, s);
 }
 
+bool attn_flash_ok(int kv_dtype, int hd, int n_tok) {
+  return kv_dtype == JERO_KV_F16 && (hd == 64 || hd == 128) && n_tok > 1;
+}
+
+bool attn_flash_q8k_ok(int group, int hd) { return (hd == 64 || hd == 128) && (group * hd) % 256 == 0; }
+
 int launch_attention_tokens(const AttnParams& p0, int n_tok, int64_t q_stride, float* out, int64_t out_stride,
                             hipStream_t s, void* q8k) {
   if (n_tok <= 0 || n_tok > 65535) return fail(JERO_ERR_TENSOR_BOUNDS, "attention: query batch of 1..65535 tokens");
   AttnParams p = p0;
   p.q_stride = q_stride;
-  if (q8k && !attn_merge_q8k_ok(p.nkv * p.group, p.hd, n_tok))
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: no Q8_K merge for this shape");
-  return attention_impl(p, false, attn_splits(p.active + n_tok - 1, p.hd), n_tok, out, out_stride, s, q8k);
-}
-
-bool attn_merge_q8k_ok(int nq, int hd, int n_tok) {
-  return n_tok > 1 && (hd == 64 || hd == 128) && (int64_t(nq) * hd) % 256 == 0 && int64_t(nq) * hd <= kMergeQ8kMax;
+  p.n_tok = n_tok;
+  if (attn_flash_ok(p.kv_dtype, p.hd, n_tok)) {
+    if (q8k && !attn_flash_q8k_ok(p.group, p.hd))
+      return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: no Q8_K rows for this head group");
+    if (!out && !q8k) return fail(JERO_ERR_INVALID_ARGUMENT, "attention: no output");
+    if (out && ((reinterpret_cast<uintptr_t>(out) & 15u) || out_stride % 4))
+      return fail(JERO_ERR_INVALID_ARGUMENT, "attention: output rows must be 16-byte aligned");
+    const int tpg = 4 * (16 / p.group);  // four column sets of 16 / group tokens
+    const dim3 grid(unsigned((n_tok + tpg - 1) / tpg), unsigned(p.nkv));
+    uint8_t* q = static_cast<uint8_t*>(q8k);
+    if (p.hd == 64) hipLaunchKernelGGL(attn_flash_kernel<64>, grid, dim3(kFlashThreads), 0, s, p, out, out_stride, q);
+    else hipLaunchKernelGGL(attn_flash_kernel<128>, grid, dim3(kFlashThreads), 0, s, p, out, out_stride, q);
+    return check_launch("attention flash");
+  }
+  if (q8k) return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: Q8_K rows need an f16 ring, head_dim 64 or 128");
+  return attention_impl(p, false, attn_splits(p.active + n_tok - 1, p.hd), n_tok, out, out_stride, s);
 }
 
 static_assert(int64_t(kMaxSplits) * attn_chunk(64) == JERO_MAX_ATTENTION_POSITIONS, "attention position limit");

@@ -877,13 +877,16 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
     if ((rc = snap(fld(L, TraceLayout::kQRope), qp, 4 * qs, 4 * Q)) ||
         (rc = snap(fld(L, TraceLayout::kKRope), kp, 4 * ks, 4 * KV)))
       return rc;
-    // the merge of each batch writes the Q8_K rows of Wo's input itself when Wo reads Q8_K and no
-    // batch holds a single token (the f32 rows then only for the trace)
+    // on an f16 ring (head_dim 64 or 128) the flash kernel takes up to 65535 queries per launch
+    // and writes the Q8_K rows of Wo's input itself when Wo reads Q8_K, the group's heads fill
+    // whole 256-blocks and no batch holds a single token (the f32 rows then only for the trace)
     const int64_t rbq = row_bytes(JERO_Q8_K, Q);
-    const bool att_q8k = l.wo.present() && act_format(l.wo.quant) == JERO_Q8_K && n > 1 &&
-                         n % kPrefillAttnTokens != 1 && attn_merge_q8k_ok(int(c.n_heads_q), int(c.head_dim), 2);
-    for (int64_t t0 = 0; t0 < n; t0 += kPrefillAttnTokens) {
-      const int64_t nt = std::min(kPrefillAttnTokens, n - t0);
+    const bool flash = attn_flash_ok(c.kv_dtype, int(c.head_dim), int(std::min<int64_t>(n, 2)));
+    const int64_t batch = flash ? 65535 : kPrefillAttnTokens;
+    const bool att_q8k = flash && l.wo.present() && act_format(l.wo.quant) == JERO_Q8_K && n % batch != 1 &&
+                         attn_flash_q8k_ok(int(c.n_heads_q / c.n_heads_kv), int(c.head_dim));
+    for (int64_t t0 = 0; t0 < n; t0 += batch) {
+      const int64_t nt = std::min(batch, n - t0);
       AttnParams p{};
       p.q = qp + t0 * qs;
       p.k = base;

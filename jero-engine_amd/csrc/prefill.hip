@@ -184,6 +184,62 @@ __global__ void __launch_bounds__(256) add_rmsnorm_q8k_rows_kernel(float* __rest
   }
 }
 
+// add_rmsnorm_q8k_rows_kernel at H = 256 PER: the same element mapping, sums and products (the
+// same bits), with every load of the row (X, D, D2 and the weights) issued before the first use,
+// so a row costs one round trip instead of one per batch of eight.
+template <int PER>
+__global__ void __launch_bounds__(256) add_rmsnorm_q8k_rows_fixed_kernel(float* __restrict__ X,
+                                                                         const float* __restrict__ D,
+                                                                         const float* __restrict__ D2,
+                                                                         const float* __restrict__ w, float eps,
+                                                                         float* __restrict__ XN,
+                                                                         uint8_t* __restrict__ Q) {
+  constexpr int H = 256 * PER;
+  __shared__ float s_tmp[4];
+  __shared__ __attribute__((aligned(16))) float s_xn[H];
+  float* x = X + int64_t(blockIdx.x) * H;
+  const float* d = D ? D + int64_t(blockIdx.x) * H : x;
+  const float* d2 = D2 ? D2 + int64_t(blockIdx.x) * H : x;
+  float v[PER], e[PER], e2[PER], wk[PER];
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int i = threadIdx.x + 256 * k;
+    v[k] = x[i];
+    e[k] = d[i];
+    e2[k] = d2[i];
+    wk[k] = w[i];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    float u = v[k];
+    if (D) {
+      u += D2 ? e[k] + e2[k] : e[k];
+      x[threadIdx.x + 256 * k] = u;
+    }
+    v[k] = u;
+    ss += u * u;
+  }
+  ss = block_sum256(ss, s_tmp);
+  const float inv = 1.0f / sqrtf(ss / float(H) + eps);
+  float* y = XN ? XN + int64_t(blockIdx.x) * H : nullptr;
+#pragma unroll
+  for (int k = 0; k < PER; k++) {
+    const int i = threadIdx.x + 256 * k;
+    const float u = v[k] * inv * wk[k];
+    s_xn[i] = u;
+    if (y) y[i] = u;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  uint8_t* q = Q + int64_t(blockIdx.x) * PER * 292;
+  for (int j = wv; j < PER; j += 4) {
+    const float4 f = reinterpret_cast<const float4*>(s_xn + 256 * j)[lane];
+    const float ev[4] = {f.x, f.y, f.z, f.w};
+    q8k_block_wave(ev, lane, q + j * 292);
+  }
+}
+
 // act[t] = silu(g[t]) * u[t] as swiglu_rows_kernel computes it, stored when act is given, and its
 // Q8_K blocks: a wave per 256-block (4 elements per lane), grid (ceil(F / 1024), n).
 __global__ void __launch_bounds__(256) swiglu_q8k_rows_kernel(const float* __restrict__ g, int64_t g_stride,
@@ -249,8 +305,17 @@ int launch_swiglu_rows(const float* g, int64_t g_stride, const float* u, int64_t
 int launch_add_rmsnorm_q8k_rows(float* X, const float* D, const float* D2, int64_t n, int64_t H, const float* w,
                                 float eps, float* XN, void* Q, hipStream_t s) {
   if (H % 256 || H > kFusedMaxH) return fail(JERO_ERR_CAPABILITY_MISMATCH, "prefill: fused RMSNorm rows need H % 256 == 0, H <= 8192");
-  hipLaunchKernelGGL(add_rmsnorm_q8k_rows_kernel, dim3(unsigned(n)), dim3(256), 0, s, X, D, D2, H, w, eps, XN,
-                     static_cast<uint8_t*>(Q));
+  uint8_t* q = static_cast<uint8_t*>(Q);
+  const dim3 grid{unsigned(n)}, block{256u};
+  switch (H / 256) {  // the hidden sizes of the Qwen3 family (and 512): one round trip per row
+    case 2: hipLaunchKernelGGL(add_rmsnorm_q8k_rows_fixed_kernel<2>, grid, block, 0, s, X, D, D2, w, eps, XN, q); break;
+    case 4: hipLaunchKernelGGL(add_rmsnorm_q8k_rows_fixed_kernel<4>, grid, block, 0, s, X, D, D2, w, eps, XN, q); break;
+    case 8: hipLaunchKernelGGL(add_rmsnorm_q8k_rows_fixed_kernel<8>, grid, block, 0, s, X, D, D2, w, eps, XN, q); break;
+    case 10: hipLaunchKernelGGL(add_rmsnorm_q8k_rows_fixed_kernel<10>, grid, block, 0, s, X, D, D2, w, eps, XN, q); break;
+    case 16: hipLaunchKernelGGL(add_rmsnorm_q8k_rows_fixed_kernel<16>, grid, block, 0, s, X, D, D2, w, eps, XN, q); break;
+    case 20: hipLaunchKernelGGL(add_rmsnorm_q8k_rows_fixed_kernel<20>, grid, block, 0, s, X, D, D2, w, eps, XN, q); break;
+    default: hipLaunchKernelGGL(add_rmsnorm_q8k_rows_kernel, grid, block, 0, s, X, D, D2, H, w, eps, XN, q);
+  }
   return check_launch("prefill rmsnorm + q8_k");
 }
 

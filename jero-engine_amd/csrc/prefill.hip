@@ -44,11 +44,13 @@ __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(const float* __restri
   for (int64_t i = threadIdx.x; i < H; i += 256) y[i] = x[i] * inv * w[i];
 }
 
-// One wave per (token t = blockIdx.x, head y = blockIdx.y): y < nq a q head, y < nq + nkv a k
-// head (both: per-head RMSNorm when a norm is given, then RoPE at position pos0 + t with the
-// decode step's table cos / sin of pos / theta^(2i / hd), written back in place; k also into its
-// ring slot), otherwise a v head (into its ring slot).  Lane l < hd / 2 holds pair (2l, 2l + 1).
-// Token t's table also goes to rope_cs[t][hd] (the trace of its step).
+// One wave per token t = blockIdx.x and kRopeRowsPerWave head rows y from kRopeRowsPerWave *
+// blockIdx.y on, their loads issued together: y < nq a q head, y < nq + nkv a k head (both:
+// per-head RMSNorm when a norm is given, then RoPE at position pos0 + t with the decode step's
+// table cos / sin of pos / theta^(2i / hd), written back in place; k also into its ring slot),
+// otherwise a v head (into its ring slot).  Lane l < hd / 2 holds pair (2l, 2l + 1).  Token t's
+// table also goes to rope_cs[t][hd] (the trace of its step).
+constexpr int kRopeRowsPerWave = 4;
 template <typename KV>
 __global__ void __launch_bounds__(64) qk_rope_rows_kernel(float* __restrict__ q, int64_t q_stride, float* __restrict__ k,
                                                           int64_t k_stride, const float* __restrict__ v,
@@ -58,47 +60,60 @@ __global__ void __launch_bounds__(64) qk_rope_rows_kernel(float* __restrict__ q,
                                                           float theta, float* __restrict__ rope_cs,
                                                           KV* __restrict__ k_ring, KV* __restrict__ v_ring,
                                                           int64_t capacity) {
-  const int t = blockIdx.x, y = blockIdx.y, lane = threadIdx.x;
+  const int t = blockIdx.x, lane = threadIdx.x, ny = nq + 2 * nkv, y0 = kRopeRowsPerWave * int(blockIdx.y);
   const int64_t pos = pos0 + t;
   const int64_t slot = pos % capacity;
   const int64_t kvd = int64_t(nkv) * hd;
   const bool on = lane < hd / 2;
   const int pr = on ? lane : hd / 2 - 1;
-  if (y >= nq + nkv) {  // v head: ring append only
-    const int h = y - nq - nkv;
-    const float2 x = reinterpret_cast<const float2*>(v + t * v_stride + int64_t(h) * hd)[pr];
-    if (on) {
-      KV* dst = v_ring + slot * kvd + int64_t(h) * hd + 2 * lane;
-      dst[0] = KV(x.x);
-      dst[1] = KV(x.y);
-    }
-    return;
+  // every row's loads first (rows past the last repeat it and are not used)
+  float2 x[kRopeRowsPerWave], g[kRopeRowsPerWave];
+#pragma unroll
+  for (int j = 0; j < kRopeRowsPerWave; j++) {
+    const int y = min(y0 + j, ny - 1);
+    const float* row = y < nq ? q + t * q_stride + int64_t(y) * hd
+                       : y < nq + nkv ? k + t * k_stride + int64_t(y - nq) * hd
+                                      : v + t * v_stride + int64_t(y - nq - nkv) * hd;
+    const float* nw = y < nq ? q_norm : y < nq + nkv ? k_norm : nullptr;
+    x[j] = reinterpret_cast<const float2*>(row)[pr];
+    g[j] = reinterpret_cast<const float2*>(nw ? nw : row)[pr];
   }
   const float expo = float(2 * pr) / float(hd);
   float sn, cn;
   sincosf(float(pos) / powf(theta, expo), &sn, &cn);
-  if (y == 0 && on) {
+  if (y0 == 0 && on) {
     rope_cs[int64_t(t) * hd + 2 * lane] = cn;
     rope_cs[int64_t(t) * hd + 2 * lane + 1] = sn;
   }
-  const bool isq = y < nq;
-  float* row = isq ? q + t * q_stride + int64_t(y) * hd : k + t * k_stride + int64_t(y - nq) * hd;
-  const float* nw = isq ? q_norm : k_norm;
-  float2 x = reinterpret_cast<const float2*>(row)[pr];
-  if (nw) {
-    const float ss = wave_sum_dpp(on ? x.x * x.x + x.y * x.y : 0.f);
-    const float inv = 1.0f / sqrtf(ss / float(hd) + eps);
-    const float2 g = reinterpret_cast<const float2*>(nw)[pr];
-    x.x = x.x * inv * g.x;
-    x.y = x.y * inv * g.y;
-  }
-  const float2 r = make_float2(x.x * cn - x.y * sn, x.x * sn + x.y * cn);
-  if (on) {
-    reinterpret_cast<float2*>(row)[lane] = r;
-    if (!isq) {
-      KV* dst = k_ring + slot * kvd + int64_t(y - nq) * hd + 2 * lane;
-      dst[0] = KV(r.x);
-      dst[1] = KV(r.y);
+#pragma unroll
+  for (int j = 0; j < kRopeRowsPerWave; j++) {
+    const int y = y0 + j;
+    if (y >= ny) break;  // uniform
+    if (y >= nq + nkv) {  // v head: ring append only
+      if (on) {
+        KV* dst = v_ring + slot * kvd + int64_t(y - nq - nkv) * hd + 2 * lane;
+        dst[0] = KV(x[j].x);
+        dst[1] = KV(x[j].y);
+      }
+      continue;
+    }
+    const bool isq = y < nq;
+    float2 xv = x[j];
+    if (isq ? q_norm : k_norm) {
+      const float ss = wave_sum_dpp(on ? xv.x * xv.x + xv.y * xv.y : 0.f);
+      const float inv = 1.0f / sqrtf(ss / float(hd) + eps);
+      xv.x = xv.x * inv * g[j].x;
+      xv.y = xv.y * inv * g[j].y;
+    }
+    const float2 r = make_float2(xv.x * cn - xv.y * sn, xv.x * sn + xv.y * cn);
+    if (on) {
+      float* row = isq ? q + t * q_stride + int64_t(y) * hd : k + t * k_stride + int64_t(y - nq) * hd;
+      reinterpret_cast<float2*>(row)[lane] = r;
+      if (!isq) {
+        KV* dst = k_ring + slot * kvd + int64_t(y - nq) * hd + 2 * lane;
+        dst[0] = KV(r.x);
+        dst[1] = KV(r.y);
+      }
     }
   }
 }
@@ -283,7 +298,7 @@ int launch_qk_rope_rows(float* q, int64_t q_stride, float* k, int64_t k_stride, 
                         int64_t n, int nq, int nkv, int hd, const float* q_norm, const float* k_norm, float eps,
                         int64_t pos0, float theta, float* rope_cs, void* k_ring, void* v_ring, bool kv_f16,
                         int64_t capacity, hipStream_t s) {
-  const dim3 grid(unsigned(n), unsigned(nq + 2 * nkv));
+  const dim3 grid(unsigned(n), unsigned((nq + 2 * nkv + kRopeRowsPerWave - 1) / kRopeRowsPerWave));
   if (kv_f16)
     hipLaunchKernelGGL(qk_rope_rows_kernel<_Float16>, grid, dim3(64), 0, s, q, q_stride, k, k_stride, v, v_stride, nq,
                        nkv, hd, q_norm, k_norm, eps, pos0, theta, rope_cs, static_cast<_Float16*>(k_ring),

@@ -742,17 +742,19 @@ __global__ void __launch_bounds__(kFlashThreads) attn_flash_kernel(AttnParams p,
   const int nstep = (pl + RS - 1) / RS;
   const int tw0 = tg0 + cs * tpw;                                // this wave's first token
   const int ncol = max(0, min(tpw, p.n_tok - tw0)) * group;      // this wave's valid columns
-  // staging: row r = tid / 4 of the 128 slots, a quarter of it per thread
+  // staging: row r = tid / 4 of the 128 slots, a quarter of it per thread (K: dims qq HD / 4 + 8 j
+  // + t; V: the 16-byte chunks 4 j + qq, dims 8 (4 j + qq) + t, so that the transposed stores of
+  // the four quarters fall in different banks)
   const int r = tid >> 2, qq = tid & 3;
   const uint8_t* const kb = static_cast<const uint8_t*>(p.k) + int64_t(kh) * HD * 2 + qq * (HD / 2);
-  const uint8_t* const vb = static_cast<const uint8_t*>(p.v) + int64_t(kh) * HD * 2 + qq * (HD / 2);
+  const uint8_t* const vb = static_cast<const uint8_t*>(p.v) + int64_t(kh) * HD * 2 + 16 * qq;
   u32x4 kr[HD / 32], vr[HD / 32];
   auto load_step = [&](int st) {
     const int64_t o = int64_t(min(st * RS + r, pl - 1)) * kvd * 2;
 #pragma unroll
     for (int j = 0; j < HD / 32; j++) kr[j] = ld4(kb + o + 16 * j);
 #pragma unroll
-    for (int j = 0; j < HD / 32; j++) vr[j] = ld4(vb + o + 16 * j);
+    for (int j = 0; j < HD / 32; j++) vr[j] = ld4(vb + o + 64 * j);
   };
   load_step(0);
   // this lane's q fragments for column col (token tw0 + col / group, head col % group), scaled
@@ -785,15 +787,24 @@ __global__ void __launch_bounds__(kFlashThreads) attn_flash_kernel(AttnParams p,
     const int p0 = st * RS + rp * CH;  // this wave's run
     if (st) lds_barrier();             // every wave is done with the previous rows
     const bool vz = st * RS + r >= pl;
+    // V^T in dwords of two slots: rows r and r ^ 1 (lanes 4 apart) swap halves of their chunk,
+    // the even row then stores dims 0..3 of the chunk for both slots, the odd row dims 4..7
+    const bool odd = r & 1;
+    uint32_t* const s_vt32 = reinterpret_cast<uint32_t*>(s_vt);
 #pragma unroll
     for (int j = 0; j < HD / 32; j++) {
       *reinterpret_cast<u32x4*>(s_k + r * KS + qq * (HD / 2) + 16 * j) = kr[j];
-      const uint32_t w[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
-#pragma unroll
-      for (int t = 0; t < 8; t++) {  // dim qq HD / 4 + 8 j + t of slot r
-        const uint16_t h = vz ? uint16_t(0) : uint16_t(w[t / 2] >> (16 * (t % 2)));
-        s_vt[(qq * (HD / 4) + 8 * j + t) * VTS + r] = __builtin_bit_cast(_Float16, h);
-      }
+      const u32x4 vv = vz ? u32x4{0u, 0u, 0u, 0u} : vr[j];
+      const uint32_t r0 = __shfl_xor(odd ? vv.x : vv.z, 4, kWave), r1 = __shfl_xor(odd ? vv.y : vv.w, 4, kWave);
+      const uint32_t a0 = odd ? vv.z : vv.x, a1 = odd ? vv.w : vv.y;  // this row's four dims
+      // dword (slot even, slot odd): the even row's f16 in the low half
+      const uint32_t lo0 = odd ? r0 : a0, hi0 = odd ? a0 : r0, lo1 = odd ? r1 : a1, hi1 = odd ? a1 : r1;
+      const int d0 = 8 * (4 * j + qq) + (odd ? 4 : 0);
+      uint32_t* dst = s_vt32 + (d0 * VTS + (r & ~1)) / 2;
+      dst[0] = (lo0 & 0xFFFFu) | (hi0 << 16);
+      dst[VTS / 2] = (lo0 >> 16) | (hi0 & 0xFFFF0000u);
+      dst[VTS] = (lo1 & 0xFFFFu) | (hi1 << 16);
+      dst[3 * (VTS / 2)] = (lo1 >> 16) | (hi1 & 0xFFFF0000u);
     }
     load_step(min(st + 1, nstep - 1));  // the next rows (the last step reloads itself: no branch)
     lds_barrier();

@@ -701,7 +701,9 @@ constexpr int64_t kPrefillAttnTokens = 256;
 static int prefill_buffers(jero_model* m, int64_t n, int64_t pos0) {
   const auto& c = m->cfg;
   const int64_t H = c.hidden, F = c.ffn, Q = q_dim(c), KV = kv_dim(c);
-  const int64_t tq = std::min(n, kPrefillAttnTokens);
+  // the split attention path's partials (f32 ring, head_dim 32, or a batch of one query): the
+  // flash kernel needs none and leaves at most a trailing one-query batch to the split path
+  const int64_t tq = attn_flash_ok(c.kv_dtype, int(c.head_dim), 2) ? 1 : std::min(n, kPrefillAttnTokens);
   const size_t ws = size_t(tq) * attn_workspace_bytes(c.n_heads_q, c.head_dim, int(pos0 + n));
   PrefillBufs& b = m->pf;
   if (n <= b.rows && ws <= b.ws_bytes) return JERO_OK;

@@ -824,6 +824,7 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
       return rc;
     float *qp, *kp, *vp;
     int64_t qs, ks, vs;
+    bool vsplit = false;  // V's split-K halves in vp and b.T2 (added by the QK-norm / RoPE step)
     // split: a projection into b.T whose split-K halves may land in b.T and b.T2 (then *split)
     auto project = [&](const DevTensor& w, const float* in, int64_t k, float* out, int trace_field,
                        bool* split = nullptr) -> int {
@@ -844,7 +845,7 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
       if ((rc = project(l.qkv, b.XN, H, b.QKV, TraceLayout::kQ8Attn))) return rc;
       if (l.v_separate) {
         vp = b.QKV + n * w1, vs = KV;
-        if ((rc = project(l.wv, b.XN, H, vp, -1))) return rc;
+        if ((rc = project(l.wv, b.XN, H, vp, -1, &vsplit))) return rc;
       } else {
         vp = b.QKV + Q + KV, vs = w1;
       }
@@ -865,13 +866,15 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
         if (rc) return rc;
       }
     }
+    if (vsplit && m->trace && (rc = launch_add_rows(vp, b.T2, n * KV, s))) return rc;  // the trace's V rows
+    const float* v2 = vsplit && !m->trace ? b.T2 : nullptr;
     const size_t fq = fld(L, TraceLayout::kQkv);
     if ((rc = snap(fq, qp, 4 * qs, 4 * Q)) || (rc = snap(fq + 4 * Q, kp, 4 * ks, 4 * KV)) ||
         (rc = snap(fq + 4 * (Q + KV), vp, 4 * vs, 4 * KV)))
       return rc;
     // QK-norm, RoPE, the K/V rows into the ring, causal attention of every token
     uint8_t* base = static_cast<uint8_t*>(m->kv) + size_t(L) * 2 * ring;
-    if ((rc = launch_qk_rope_rows(qp, qs, kp, ks, vp, vs, n, c.n_heads_q, c.n_heads_kv, c.head_dim,
+    if ((rc = launch_qk_rope_rows(qp, qs, kp, ks, vp, vs, v2, n, c.n_heads_q, c.n_heads_kv, c.head_dim,
                                   c.qk_norm ? static_cast<const float*>(l.q_norm.dev) : nullptr,
                                   c.qk_norm ? static_cast<const float*>(l.k_norm.dev) : nullptr, eps_attn, pos0,
                                   c.rope_theta, b.RC, base, base + ring, c.kv_dtype == JERO_KV_F16, c.kv_capacity, s)))

@@ -12,10 +12,11 @@ int launch_embed_rows(int quant, const void* w, int64_t rb, int H, const int32_t
 // XN[t] = RMSNorm(X[t]) * w, rows of H floats.
 int launch_rmsnorm_rows(const float* X, int64_t n, int64_t H, const float* w, float eps, float* XN, hipStream_t s);
 // Per token t < n (position pos0 + t): QK-norm (when given) and RoPE of its q heads (row t at q +
-// t q_stride) and k heads (k + t k_stride), in place, the k and v heads (v + t v_stride) appended
-// to ring slot (pos0 + t) % capacity, and the RoPE table of the token into rope_cs[t][hd].
+// t q_stride) and k heads (k + t k_stride), in place, the k and v heads (v + t v_stride, plus v2 +
+// t v_stride when v2 is given: the second K half of a split V projection) appended to ring slot
+// (pos0 + t) % capacity, and the RoPE table of the token into rope_cs[t][hd].
 int launch_qk_rope_rows(float* q, int64_t q_stride, float* k, int64_t k_stride, const float* v, int64_t v_stride,
-                        int64_t n, int nq, int nkv, int hd, const float* q_norm, const float* k_norm, float eps,
+                        const float* v2, int64_t n, int nq, int nkv, int hd, const float* q_norm, const float* k_norm, float eps,
                         int64_t pos0, float theta, float* rope_cs, void* k_ring, void* v_ring, bool kv_f16,
                         int64_t capacity, hipStream_t s);
 // act[t][i] = silu(g[t][i]) * u[t][i], act rows of F floats.

@@ -54,7 +54,8 @@ constexpr int kRopeRowsPerWave = 4;
 template <typename KV>
 __global__ void __launch_bounds__(64) qk_rope_rows_kernel(float* __restrict__ q, int64_t q_stride, float* __restrict__ k,
                                                           int64_t k_stride, const float* __restrict__ v,
-                                                          int64_t v_stride, int nq, int nkv, int hd,
+                                                          int64_t v_stride, const float* __restrict__ v2, int nq,
+                                                          int nkv, int hd,
                                                           const float* __restrict__ q_norm,
                                                           const float* __restrict__ k_norm, float eps, int64_t pos0,
                                                           float theta, float* __restrict__ rope_cs,
@@ -67,16 +68,19 @@ __global__ void __launch_bounds__(64) qk_rope_rows_kernel(float* __restrict__ q,
   const bool on = lane < hd / 2;
   const int pr = on ? lane : hd / 2 - 1;
   // every row's loads first (rows past the last repeat it and are not used)
-  float2 x[kRopeRowsPerWave], g[kRopeRowsPerWave];
+  float2 x[kRopeRowsPerWave], g[kRopeRowsPerWave], x2[kRopeRowsPerWave];
 #pragma unroll
   for (int j = 0; j < kRopeRowsPerWave; j++) {
     const int y = min(y0 + j, ny - 1);
+    const bool isv = y >= nq + nkv;
     const float* row = y < nq ? q + t * q_stride + int64_t(y) * hd
-                       : y < nq + nkv ? k + t * k_stride + int64_t(y - nq) * hd
-                                      : v + t * v_stride + int64_t(y - nq - nkv) * hd;
-    const float* nw = y < nq ? q_norm : y < nq + nkv ? k_norm : nullptr;
+                       : !isv ? k + t * k_stride + int64_t(y - nq) * hd
+                              : v + t * v_stride + int64_t(y - nq - nkv) * hd;
+    const float* nw = y < nq ? q_norm : !isv ? k_norm : nullptr;
+    const float* row2 = isv && v2 ? v2 + t * v_stride + int64_t(y - nq - nkv) * hd : row;
     x[j] = reinterpret_cast<const float2*>(row)[pr];
     g[j] = reinterpret_cast<const float2*>(nw ? nw : row)[pr];
+    x2[j] = reinterpret_cast<const float2*>(row2)[pr];
   }
   const float expo = float(2 * pr) / float(hd);
   float sn, cn;
@@ -89,11 +93,12 @@ __global__ void __launch_bounds__(64) qk_rope_rows_kernel(float* __restrict__ q,
   for (int j = 0; j < kRopeRowsPerWave; j++) {
     const int y = y0 + j;
     if (y >= ny) break;  // uniform
-    if (y >= nq + nkv) {  // v head: ring append only
+    if (y >= nq + nkv) {  // v head: ring append only (the two halves' sum, when split)
       if (on) {
+        const float2 xv = v2 ? make_float2(x[j].x + x2[j].x, x[j].y + x2[j].y) : x[j];
         KV* dst = v_ring + slot * kvd + int64_t(y - nq - nkv) * hd + 2 * lane;
-        dst[0] = KV(x[j].x);
-        dst[1] = KV(x[j].y);
+        dst[0] = KV(xv.x);
+        dst[1] = KV(xv.y);
       }
       continue;
     }
@@ -295,16 +300,16 @@ int launch_rmsnorm_rows(const float* X, int64_t n, int64_t H, const float* w, fl
 }
 
 int launch_qk_rope_rows(float* q, int64_t q_stride, float* k, int64_t k_stride, const float* v, int64_t v_stride,
-                        int64_t n, int nq, int nkv, int hd, const float* q_norm, const float* k_norm, float eps,
+                        const float* v2, int64_t n, int nq, int nkv, int hd, const float* q_norm, const float* k_norm, float eps,
                         int64_t pos0, float theta, float* rope_cs, void* k_ring, void* v_ring, bool kv_f16,
                         int64_t capacity, hipStream_t s) {
   const dim3 grid(unsigned(n), unsigned((nq + 2 * nkv + kRopeRowsPerWave - 1) / kRopeRowsPerWave));
   if (kv_f16)
-    hipLaunchKernelGGL(qk_rope_rows_kernel<_Float16>, grid, dim3(64), 0, s, q, q_stride, k, k_stride, v, v_stride, nq,
+    hipLaunchKernelGGL(qk_rope_rows_kernel<_Float16>, grid, dim3(64), 0, s, q, q_stride, k, k_stride, v, v_stride, v2, nq,
                        nkv, hd, q_norm, k_norm, eps, pos0, theta, rope_cs, static_cast<_Float16*>(k_ring),
                        static_cast<_Float16*>(v_ring), capacity);
   else
-    hipLaunchKernelGGL(qk_rope_rows_kernel<float>, grid, dim3(64), 0, s, q, q_stride, k, k_stride, v, v_stride, nq,
+    hipLaunchKernelGGL(qk_rope_rows_kernel<float>, grid, dim3(64), 0, s, q, q_stride, k, k_stride, v, v_stride, v2, nq,
                        nkv, hd, q_norm, k_norm, eps, pos0, theta, rope_cs, static_cast<float*>(k_ring),
                        static_cast<float*>(v_ring), capacity);
   return check_launch("prefill qk-norm / rope");

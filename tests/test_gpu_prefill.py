@@ -62,6 +62,48 @@ def test_prefill_group_sizes(dev, nq, nkv, hd):
     m.close()
 
 
+@pytest.mark.parametrize("kv_name,n", [("f16", 300), ("f16", 17), ("f32", 300)])
+def test_prefill_untraced_matches_traced(dev, kv_name, n):
+    """The prefill without a trace -- the path bench.py times: attention writes only Wo's Q8_K
+    rows, no normalised rows are stored, a split V projection's two K halves are added by the
+    QK-norm / RoPE step -- leaves the same KV rings, logits and next token, bit for bit, as the
+    traced prefill that the other tests hold to the oracle (layer 0 of the mix has a Q6_K attn_v,
+    projected apart and split in K)."""
+    print(f"prefill untraced vs traced kv={kv_name} n={n}", flush=True)
+    spec = SMALL
+    cap = 400
+    t = MS.build(spec, seed=11)
+    kv_dtype, es = (J.KV_F16, 2) if kv_name == "f16" else (J.KV_F32, 4)
+    tokens = np.random.default_rng(n).integers(0, spec["vocab"], size=n).tolist()
+    ring_bytes = cap * spec["nkv"] * spec["hd"] * es
+    outs = []
+    for traced in (True, False):
+        m = make_gpu_model(spec, t, cap, kv_dtype, True)
+        if traced:
+            _, _, _, total = m.trace_layout()
+            buf = torch.zeros(n * total, dtype=torch.uint8, device=dev)
+            m.set_trace(buf)
+        m.prefill(tokens, 0)
+        m.status()
+        if traced:
+            m.set_trace(None)
+        logits = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
+        m.read_logits(logits)
+        rings = []
+        for layer in range(spec["n_layers"]):
+            for ptr in m.kv_ptrs(layer):
+                r = torch.empty(ring_bytes, dtype=torch.uint8, device=dev)
+                J._memcpy(r.data_ptr(), ptr, ring_bytes)
+                rings.append(r.cpu().numpy())
+        outs.append((logits.cpu().numpy(), rings, m.read_token_pos()))
+        m.close()
+    (la, ra, ta), (lb, rb, tb) = outs
+    assert ta == tb == (ta[0], n)
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    for x, y in zip(ra, rb):
+        assert np.array_equal(x, y)
+
+
 def test_prefill_matches_decode_steps_8b_layer_shape(dev):
     """Two layers of the Qwen3-8B shape, f16 ring: a 24-token prompt after 4000 filled slots."""
     spec = dict(hidden=4096, ffn=12288, n_layers=2, vocab=151936, nq=32, nkv=8, hd=128, eps=1e-6, theta=1e6)

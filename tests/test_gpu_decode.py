@@ -301,6 +301,36 @@ def test_decode_graph_replay_matches_eager(dev):
         _ = torch.randn(1000, device=dev).sum().item()  # unrelated eager work between replays
 
 
+def test_decode_untraced_matches_traced(dev):
+    """Decode steps without a trace (the path bench.py replays as a graph, itself equal to eager
+    steps above) give the same logits and tokens, bit for bit, as traced steps, which the parity
+    tests hold to the oracle."""
+    print("decode untraced vs traced", flush=True)
+    spec = dict(QWEN_SMALL, n_layers=2)
+    t = MS.build(spec, seed=6)
+    cap = 256
+    a = make_gpu_model(spec, t, cap, J.KV_F16, True)
+    b = make_gpu_model(spec, t, cap, J.KV_F16, True)
+    _, _, _, total = a.trace_layout()
+    buf = torch.zeros(total, dtype=torch.uint8, device=dev)
+    a.set_trace(buf)
+    a.set_position(7, 0)
+    b.set_position(7, 0)
+    la = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
+    lb = torch.empty_like(la)
+    for i in range(4):
+        a.decode_step()
+        b.decode_step()
+        torch.cuda.synchronize()
+        a.read_logits(la)
+        b.read_logits(lb)
+        assert torch.equal(la, lb), i
+        assert a.read_token_pos() == b.read_token_pos(), i
+    a.set_trace(None)
+    a.close()
+    b.close()
+
+
 def test_model_errors(dev):
     m = J.DecodeModel(512, 1024, 1, 100, 8, 2, 64, 1e-6, 1e6, 64)
     with pytest.raises(J.K3Error) as ei:

@@ -708,12 +708,13 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
 // them, taking alternate 64-slot runs.  The workgroup walks the slots its tokens attend to
 // (query t of the batch: the first active + t slots) 128 at a time, stages their K and V rows in
 // LDS (V zero past the last attended slot; the next 128 rows are loaded into registers while
-// the current ones are used; V transposed, [dim][slot]), and each wave takes its run's four
-// 16-slot chunks through an online softmax (running max and sum per column over the 4 lanes
-// that hold it, the accumulators rescaled per chunk).  The two waves' states of a column are
-// merged through LDS at the end.  Per chunk: S^T = K q on v_mfma_f32_16x16x32_f16
-// (q split into f16 hi + lo, one accumulator each), P V on v_mfma_f32_16x16x16_f16 with the
-// B operand read straight from V^T (P split likewise).  No split partials: the rows
+// the current ones are used; V transposed, [dim][slot]), and each wave takes its run 32 slots
+// at a time through an online softmax (running max and sum per column over the 4 lanes that
+// hold it, the accumulators rescaled per 32 slots).  The two waves' states of a column are
+// merged through LDS at the end.  Per 32 slots: S^T = K q for two 16-slot chunks on
+// v_mfma_f32_16x16x32_f16 (q split into f16 hi + lo, one accumulator each), P V on the same
+// MFMA with K = the lane's 8 slots of both chunks, the B operand read straight from V^T (P
+// split likewise).  No split partials: the rows
 // o / l go through LDS and are written as f32 rows (out, when given) and, when q8k is given, as
 // the Q8_K blocks of Wo's input (group * HD a multiple of 256: the group's heads fill whole
 // blocks), quantized from the same f32 values.
@@ -808,30 +809,38 @@ __global__ void __launch_bounds__(kFlashThreads) attn_flash_kernel(AttnParams p,
     }
     load_step(min(st + 1, nstep - 1));  // the next rows (the last step reloads itself: no branch)
     lds_barrier();
-    for (int cc = 0; cc < 4; cc++) {
-      const int c0 = p0 + 16 * cc;
-      if (c0 >= pl) break;  // uniform in the wave: no slot of this chunk is attended by any token
-      // scores: lane holds column col, slots c0 + 4 kq + r
-      f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
+    for (int cp = 0; cp < 2; cp++) {  // 32 slots at a time: chunks A (c0 ..) and B (c0 + 16 ..)
+      const int c0 = p0 + 32 * cp, sr = rp * CH + 32 * cp;  // sr: the staged row of slot c0
+      if (c0 >= pl) break;  // uniform in the wave: no slot of these chunks is attended by any token
+      // scores: lane holds column col, slots c0 + 4 kq + r (A) and c0 + 16 + 4 kq + r (B)
+      f4_t ha = {0.f, 0.f, 0.f, 0.f}, la = ha, hb = ha, lb = ha;
 #pragma unroll
       for (int j = 0; j < NCH; j++) {
-        const h8_t a = __builtin_bit_cast(h8_t, *reinterpret_cast<const u32x4*>(s_k + (rp * CH + 16 * cc + col) * KS +
-                                                                                16 * (4 * j + kq)));
-        sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qhi[j], sh, 0, 0, 0);
-        sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qlo[j], sl, 0, 0, 0);
+        const h8_t ka = __builtin_bit_cast(h8_t, *reinterpret_cast<const u32x4*>(s_k + (sr + col) * KS + 16 * (4 * j + kq)));
+        const h8_t kb8 = __builtin_bit_cast(h8_t, *reinterpret_cast<const u32x4*>(s_k + (sr + 16 + col) * KS +
+                                                                                  16 * (4 * j + kq)));
+        ha = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi[j], ha, 0, 0, 0);
+        la = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo[j], la, 0, 0, 0);
+        hb = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb8, qhi[j], hb, 0, 0, 0);
+        lb = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb8, qlo[j], lb, 0, 0, 0);
       }
-      float s[4];
+      float s8[8];
 #pragma unroll
-      for (int rr = 0; rr < 4; rr++) s[rr] = c0 + 4 * kq + rr < lim ? sh[rr] + sl[rr] : -INFINITY;
-      float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      for (int rr = 0; rr < 4; rr++) {
+        s8[rr] = c0 + 4 * kq + rr < lim ? ha[rr] + la[rr] : -INFINITY;
+        s8[4 + rr] = c0 + 16 + 4 * kq + rr < lim ? hb[rr] + lb[rr] : -INFINITY;
+      }
+      float mx = s8[0];
+#pragma unroll
+      for (int rr = 1; rr < 8; rr++) mx = fmaxf(mx, s8[rr]);
       mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
       mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
       const float mn = fmaxf(m, mx);
       const float alpha = mn == -INFINITY ? 1.f : exp_fast(m - mn);
-      float e[4], sum = 0.f;
+      float e[8], sum = 0.f;
 #pragma unroll
-      for (int rr = 0; rr < 4; rr++) {
-        e[rr] = mn == -INFINITY ? 0.f : exp_fast(s[rr] - mn);
+      for (int rr = 0; rr < 8; rr++) {
+        e[rr] = mn == -INFINITY ? 0.f : exp_fast(s8[rr] - mn);
         sum += e[rr];
       }
       sum += __shfl_xor(sum, 16, kWave);
@@ -842,21 +851,24 @@ __global__ void __launch_bounds__(kFlashThreads) attn_flash_kernel(AttnParams p,
       float ar[4];
 #pragma unroll
       for (int rr = 0; rr < 4; rr++) ar[rr] = __shfl(alpha, 4 * kq + rr, kWave);
-      h4_t phi, plo;
+      // P as the A operand of a K = 32 MFMA: the lane's 8 K elements are its 8 slots above, and the
+      // B operand (V) holds the same 8 slots for dim 16 i + col
+      h8_t phi, plo;
 #pragma unroll
-      for (int rr = 0; rr < 4; rr++) {
+      for (int rr = 0; rr < 8; rr++) {
         const _Float16 hi = _Float16(e[rr]);
         phi[rr] = hi;
         plo[rr] = _Float16(e[rr] - float(hi));
       }
-      // o[i]: columns 4 kq + rr, dim 16 i + col; B = V[slots c0 + 4 kq ..][dim 16 i + col] from V^T
 #pragma unroll
       for (int i = 0; i < NT; i++) {
-        const h4_t bv = *reinterpret_cast<const h4_t*>(s_vt + (16 * i + col) * VTS + rp * CH + 16 * cc + 4 * kq);
+        const _Float16* vrow = s_vt + (16 * i + col) * VTS + sr + 4 * kq;
+        const h4_t va = *reinterpret_cast<const h4_t*>(vrow), vb4 = *reinterpret_cast<const h4_t*>(vrow + 16);
+        const h8_t bv = {va[0], va[1], va[2], va[3], vb4[0], vb4[1], vb4[2], vb4[3]};
 #pragma unroll
         for (int rr = 0; rr < 4; rr++) o[i][rr] *= ar[rr];
-        o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, bv, o[i], 0, 0, 0);
-        o[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, bv, o[i], 0, 0, 0);
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(phi, bv, o[i], 0, 0, 0);
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo, bv, o[i], 0, 0, 0);
       }
     }
   }

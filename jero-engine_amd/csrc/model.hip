@@ -82,6 +82,9 @@ struct jero_model {
   jero::PrefillBufs pf;
   // GEMM layouts of the Q4_K / Q6_K tensors for the prefill (Q4_K_G, Q6_K_P), built on first use
   std::map<const void*, void*> laid;
+  // the prefill's second stream (default priority) and its fork / join events, made on first use
+  hipStream_t side = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 };
 
 namespace jero {
@@ -346,6 +349,9 @@ extern "C" int jero_hip_model_destroy(jero_model* m) {
   (void)hipDeviceSynchronize();
   for (void* q : m->owned)
     if (q) (void)hipFree(q);
+  if (m->ev_fork) (void)hipEventDestroy(m->ev_fork);
+  if (m->ev_join) (void)hipEventDestroy(m->ev_join);
+  if (m->side) (void)hipStreamDestroy(m->side);
   delete m;
   return JERO_OK;
 }
@@ -698,6 +704,25 @@ static int laid_of(jero_model* m, const DevTensor& w, hipStream_t s, const void*
 // Attention queries per launch of the batched prefill: bounds its split workspace.
 constexpr int64_t kPrefillAttnTokens = 256;
 
+// Work on the model's second stream after everything enqueued on s so far.
+static int fork_side(jero_model* m, hipStream_t s) {
+  if (!m->side &&
+      (hipStreamCreateWithFlags(&m->side, hipStreamNonBlocking) != hipSuccess ||
+       hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming) != hipSuccess ||
+       hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming) != hipSuccess))
+    return fail(JERO_ERR_DEVICE, "prefill: cannot create the second stream");
+  if (hipEventRecord(m->ev_fork, s) != hipSuccess || hipStreamWaitEvent(m->side, m->ev_fork, 0) != hipSuccess)
+    return fail(JERO_ERR_DEVICE, "prefill: stream fork failed");
+  return JERO_OK;
+}
+
+// s waits for what was enqueued on the second stream.
+static int join_side(jero_model* m, hipStream_t s) {
+  if (hipEventRecord(m->ev_join, m->side) != hipSuccess || hipStreamWaitEvent(s, m->ev_join, 0) != hipSuccess)
+    return fail(JERO_ERR_DEVICE, "prefill: stream join failed");
+  return JERO_OK;
+}
+
 static int prefill_buffers(jero_model* m, int64_t n, int64_t pos0) {
   const auto& c = m->cfg;
   const int64_t H = c.hidden, F = c.ffn, Q = q_dim(c), KV = kv_dim(c);
@@ -842,8 +867,20 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
     if (!l.qkv_split) {
       const int64_t w1 = l.qkv.n_out;  // Q + 2 KV, or Q + KV with V apart
       qp = b.QKV, qs = w1, kp = b.QKV + Q, ks = w1;
+      // V apart (a Q6_K attn_v) runs on the second stream beside Q|K when both read the Q8_K rows
+      // already built: its few workgroups fill the CUs the Q|K GEMM leaves idle
+      const bool vside = l.v_separate && attn_q8k && have_fmt == JERO_Q8_K && n >= kLaidMinRows;
+      if (vside) {
+        vp = b.QKV + n * w1, vs = KV;
+        const void* laid_v = nullptr;
+        if ((rc = laid_of(m, l.wv, s, &laid_v)) || (rc = fork_side(m, s)) ||
+            (rc = launch_gemm(l.wv.quant, l.wv.dev, H, l.wv.n_out, b.XQ, n, vp, m->side, laid_v, b.T2, &vsplit)))
+          return rc;
+      }
       if ((rc = project(l.qkv, b.XN, H, b.QKV, TraceLayout::kQ8Attn))) return rc;
-      if (l.v_separate) {
+      if (vside) {
+        if ((rc = join_side(m, s))) return rc;
+      } else if (l.v_separate) {
         vp = b.QKV + n * w1, vs = KV;
         if ((rc = project(l.wv, b.XN, H, vp, -1, &vsplit))) return rc;
       } else {

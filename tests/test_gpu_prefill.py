@@ -45,10 +45,12 @@ def test_prefill_matches_oracle(dev, mix, kv_name, qk_norm, cap, pos0, n):
     m.close()
 
 
-@pytest.mark.parametrize("nq,nkv,hd", [(16, 2, 64), (4, 4, 64), (4, 2, 128)])
+@pytest.mark.parametrize("nq,nkv,hd", [(16, 2, 64), (4, 4, 64), (4, 2, 128), (12, 4, 64), (6, 2, 128)])
 def test_prefill_group_sizes(dev, nq, nkv, hd):
-    """The batched attention kernel gives each wave 16 / group tokens: groups of 8, 1 and 2 (head_dim
-    64 and 128), f16 ring, 40 prompt tokens after 37 filled slots (crossing a 64-slot split)."""
+    """The flash attention kernel gives each column set 16 / group tokens: groups of 8, 1, 2 and 3
+    (15 of the 16 columns used; the group's rows fill no whole 256-block, so the output projection
+    quantizes the f32 rows), head_dim 64 and 128, f16 ring, 40 prompt tokens after 37 filled
+    slots (crossing a 64-slot run)."""
     print(f"prefill nq={nq} nkv={nkv} hd={hd}", flush=True)
     spec = dict(SMALL, nq=nq, nkv=nkv, hd=hd, n_layers=2)
     cap, pos0, n = 128, 37, 40

@@ -261,22 +261,34 @@ __global__ void __launch_bounds__(256) add_rmsnorm_q8k_rows_fixed_kernel(float* 
 }
 
 // act[t] = silu(g[t]) * u[t] as swiglu_rows_kernel computes it, stored when act is given, and its
-// Q8_K blocks: a wave per 256-block (4 elements per lane), grid (ceil(F / 1024), n).
+// Q8_K blocks: a wave per kSwigluBlocksPerWave 256-blocks (4 elements per lane), their loads issued
+// together, grid (ceil(F / (1024 kSwigluBlocksPerWave)), n).
+constexpr int kSwigluBlocksPerWave = 2;
 __global__ void __launch_bounds__(256) swiglu_q8k_rows_kernel(const float* __restrict__ g, int64_t g_stride,
                                                               const float* __restrict__ u, int64_t u_stride,
                                                               float* __restrict__ act, int64_t F,
                                                               uint8_t* __restrict__ Q) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int64_t j = int64_t(blockIdx.x) * 4 + wv, t = blockIdx.y;
-  if (j >= F / 256) return;
-  const float4 gv = reinterpret_cast<const float4*>(g + t * g_stride + 256 * j)[lane];
-  const float4 uv = reinterpret_cast<const float4*>(u + t * u_stride + 256 * j)[lane];
-  const float ga[4] = {gv.x, gv.y, gv.z, gv.w}, ua[4] = {uv.x, uv.y, uv.z, uv.w};
-  float e[4];
+  const int64_t nblk = F / 256, j0 = (int64_t(blockIdx.x) * 4 + wv) * kSwigluBlocksPerWave, t = blockIdx.y;
+  if (j0 >= nblk) return;
+  float4 gv[kSwigluBlocksPerWave], uv[kSwigluBlocksPerWave];
 #pragma unroll
-  for (int i = 0; i < 4; i++) e[i] = ga[i] / (1.0f + expf(-ga[i])) * ua[i];
-  if (act) reinterpret_cast<float4*>(act + t * F + 256 * j)[lane] = make_float4(e[0], e[1], e[2], e[3]);
-  q8k_block_wave(e, lane, Q + (t * (F / 256) + j) * 292);
+  for (int b = 0; b < kSwigluBlocksPerWave; b++) {  // a block past the last repeats it, unused
+    const int64_t j = min(j0 + b, nblk - 1);
+    gv[b] = reinterpret_cast<const float4*>(g + t * g_stride + 256 * j)[lane];
+    uv[b] = reinterpret_cast<const float4*>(u + t * u_stride + 256 * j)[lane];
+  }
+#pragma unroll
+  for (int b = 0; b < kSwigluBlocksPerWave; b++) {
+    const int64_t j = j0 + b;
+    if (j >= nblk) break;  // uniform
+    const float ga[4] = {gv[b].x, gv[b].y, gv[b].z, gv[b].w}, ua[4] = {uv[b].x, uv[b].y, uv[b].z, uv[b].w};
+    float e[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) e[i] = ga[i] / (1.0f + expf(-ga[i])) * ua[i];
+    if (act) reinterpret_cast<float4*>(act + t * F + 256 * j)[lane] = make_float4(e[0], e[1], e[2], e[3]);
+    q8k_block_wave(e, lane, Q + (t * nblk + j) * 292);
+  }
 }
 
 // x[i] += d[i] (the residual of Wo and down).
@@ -343,7 +355,8 @@ int launch_swiglu_q8k_rows(const float* g, int64_t g_stride, const float* u, int
                            int64_t F, void* Q, hipStream_t s) {
   if (F % 256 || (g_stride | u_stride) % 4)
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "prefill: fused SwiGLU rows need F % 256 == 0");
-  hipLaunchKernelGGL(swiglu_q8k_rows_kernel, dim3(unsigned((F / 256 + 3) / 4), unsigned(n)), dim3(256), 0, s, g,
+  const int64_t per_wg = 4 * kSwigluBlocksPerWave;
+  hipLaunchKernelGGL(swiglu_q8k_rows_kernel, dim3(unsigned((F / 256 + per_wg - 1) / per_wg), unsigned(n)), dim3(256), 0, s, g,
                      g_stride, u, u_stride, act, F, static_cast<uint8_t*>(Q));
   return check_launch("prefill swiglu + q8_k");
 }

@@ -726,7 +726,8 @@ __global__ void __launch_bounds__(kFlashThreads) attn_flash_kernel(AttnParams p,
   constexpr int KS = 2 * HD + 16;  // LDS bytes per staged K row: the f16 row and 16 bytes of padding
   constexpr int VTS = RS + 8;      // f16 per row of V^T (one row per dim)
   // K rows, then V^T.  After the runs: the second waves' partial states at the start, the
-  // workgroup's output rows ((64 / group) * group * HD floats = 256 HD bytes) after RS K rows
+  // workgroup's output rows (4 (16 / group) tokens of group * HD floats: at most 256 HD bytes)
+  // after RS K rows
   __shared__ __attribute__((aligned(16))) uint8_t s_kv[RS * KS + HD * VTS * 2];
   constexpr int PO_BYTES = NCS * NT * 4 * 64 * 4 + NCS * 16 * 2 * 4;
   static_assert(PO_BYTES <= RS * KS && RS * KS + 256 * HD <= RS * KS + HD * VTS * 2, "merge areas fit the staging");
@@ -745,7 +746,7 @@ __global__ void __launch_bounds__(kFlashThreads) attn_flash_kernel(AttnParams p,
   const int ncol = max(0, min(tpw, p.n_tok - tw0)) * group;      // this wave's valid columns
   // staging: row r = tid / 4 of the 128 slots, a quarter of it per thread (K: dims qq HD / 4 + 8 j
   // + t; V: the 16-byte chunks 4 j + qq, dims 8 (4 j + qq) + t, so that the transposed stores of
-  // the four quarters fall in different banks)
+  // the four quarters meet at most two to a bank)
   const int r = tid >> 2, qq = tid & 3;
   const uint8_t* const kb = static_cast<const uint8_t*>(p.k) + int64_t(kh) * HD * 2 + qq * (HD / 2);
   const uint8_t* const vb = static_cast<const uint8_t*>(p.v) + int64_t(kh) * HD * 2 + 16 * qq;

@@ -331,6 +331,43 @@ def test_decode_untraced_matches_traced(dev):
     b.close()
 
 
+def test_decode_untraced_matches_traced_8b_layer_shape(dev):
+    """The same at the timed layer shape: two layers of the Qwen3-8B shape (the fused Q|K|V,
+    the Q|K + Q6_K V launch, gate|up SwiGLU, both down formats, the LM head over 151936 rows),
+    f16 ring of 4096 slots filled to 4094, three steps (the last one wraps the ring)."""
+    print("decode untraced vs traced, qwen3-8b layer shape", flush=True)
+    spec = dict(QWEN3_8B, n_layers=2)
+    cap = 4096
+    t = MS.build(spec, seed=66)
+    a = make_gpu_model(spec, t, cap, J.KV_F16, True)
+    b = make_gpu_model(spec, t, cap, J.KV_F16, True)
+    kvd = spec["nkv"] * spec["hd"]
+    rng = np.random.default_rng(67)
+    for L in range(spec["n_layers"]):
+        k = torch.from_numpy(rng.standard_normal((cap, kvd)).astype(np.float16)).to(dev)
+        v = torch.from_numpy(rng.standard_normal((cap, kvd)).astype(np.float16)).to(dev)
+        a.write_kv(L, k, v)
+        b.write_kv(L, k, v)
+    _, _, _, total = a.trace_layout()
+    buf = torch.zeros(total, dtype=torch.uint8, device=dev)
+    a.set_trace(buf)
+    a.set_position(11, 4094)
+    b.set_position(11, 4094)
+    la = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
+    lb = torch.empty_like(la)
+    for i in range(3):
+        a.decode_step()
+        b.decode_step()
+        torch.cuda.synchronize()
+        a.read_logits(la)
+        b.read_logits(lb)
+        assert torch.equal(la, lb), i
+        assert a.read_token_pos() == b.read_token_pos(), i
+    a.set_trace(None)
+    a.close()
+    b.close()
+
+
 def test_model_errors(dev):
     m = J.DecodeModel(512, 1024, 1, 100, 8, 2, 64, 1e-6, 1e6, 64)
     with pytest.raises(J.K3Error) as ei:

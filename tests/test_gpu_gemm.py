@@ -231,6 +231,41 @@ def test_gemm_laid_matches_oracle(dev, quant, m, k, n):
     assert rel_err(y, ref) < REL_TOL
 
 
+@pytest.mark.parametrize("quant,m,k,n", [
+    (J.Q4_K, 512, 4096, 14336),   # the timed prefill GEMM: 8 x 112 tiles, 896 workgroups, unsplit
+    (J.Q4_K, 512, 4096, 24576),   # the 8B prefill's gate|up: 1536 workgroups
+    (J.Q4_K, 512, 4096, 5120),    # Q|K of the Q6_K-attn_v layers: 320 workgroups
+    (J.Q4_K, 512, 4096, 4096),    # Wo: 256 tiles, K split in two
+    (J.Q4_K, 512, 12288, 4096),   # Q4_K ffn_down, K split
+    (J.Q6_K, 512, 4096, 14336),   # the timed shape over Q6_K_P
+    (J.Q6_K, 512, 12288, 4096),   # Q6_K ffn_down, K split
+    (J.Q6_K, 512, 4096, 1024)])   # Q6_K attn_v, K split
+def test_gemm_laid_prefill_shapes(dev, quant, m, k, n):
+    """jero_hip_gemm over the GEMM layouts at the sizes bench.py and the 8B prefill run (the
+    grids whose workgroup-to-tile remap and K split the small cases above do not reach): every
+    row equals the GPU GEMV of that token row (bit-exact in its int32 partials against the
+    oracle) within 1e-5, and 8 rows spread over the token tiles match the oracle within 1e-5."""
+    print(f"gemm laid prefill shape quant={quant} m={m} k={k} n={n}", flush=True)
+    w = rand_weights(quant, n, k, 9300 + quant + n + k)
+    x = rand_act(k, 9301 + n + k, m=m)
+    xqd = J.quantize_act(J.Q8_K, to_dev(x, dev))
+    view = J.TensorView("w", quant, [k, n], to_dev(w, dev))
+    y = torch.full((m, n), float("nan"), device=dev)
+    J.gemm(J.repack_gemm(view), xqd, m, y)
+    rb = J.row_bytes(J.Q8_K, k)
+    g = torch.full((m, n), float("nan"), device=dev)
+    for r in range(m):
+        J.matvec(view, xqd[r * rb:(r + 1) * rb], g[r])
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    assert np.all(np.isfinite(y))
+    assert rel_err(y, g.cpu().numpy()) < REL_TOL
+    xq = xqd.cpu().numpy()
+    rows = [0, 63, 64, 200, 255, 256, 383, 511]
+    ref = np.stack([O.matvec(quant, w, k, n, xq[r * rb:(r + 1) * rb], threads=8) for r in rows])
+    assert rel_err(y[rows], ref) < REL_TOL
+
+
 def test_gemm_laid_q4k_extremes(dev):
     """Q4_K_G at the top of the expanded planes (scale 63 = 8 * 7 + 7, nibble 15: 105 each),
     zero scales and mins, zero and tiny activation rows."""

@@ -120,6 +120,74 @@ def test_prefill_matches_decode_steps_8b_layer_shape(dev):
     m.close()
 
 
+QWEN3_8B_2L = dict(hidden=4096, ffn=12288, n_layers=2, vocab=151936, nq=32, nkv=8, hd=128, eps=1e-6, theta=1e6)
+
+
+@pytest.mark.timeout(900)
+def test_prefill_8b_layer_shape_512_tokens(dev):
+    """The prefill bench.py times -- a 512-token prompt from position 0 into an f16 ring of 4096
+    slots -- on two layers of the Qwen3-8B shape: at 512 rows the Q|K (320 workgroups) and
+    gate|up (1536) GEMMs run unsplit with the workgroup-to-tile remap, Wo and ffn_down split K, the
+    Q6_K attn_v of layer 0 runs on the second stream, and the flash attention kernel covers 512
+    queries.  Every one of the 512 prompt tokens is held to the decode bars (every layer
+    teacher-forced, its hidden state within 1e-3 end to end, the last token's logits within 1e-3)."""
+    spec = QWEN3_8B_2L
+    cap, pos0, n = 4096, 0, 512
+    print("prefill qwen3-8b layer shape, 512 tokens from position 0", flush=True)
+    t = MS.build(spec, seed=51)
+    m = make_gpu_model(spec, t, cap, J.KV_F16, True)
+    om = O.DecodeModel(spec, MS.oracle_tensors(t), cap)
+    kv = prefill_kv(m, om, spec, cap, pos0, 53, dev)
+    tokens = np.random.default_rng(57).integers(0, spec["vocab"], size=n).tolist()
+    gtok, res = DP.run_prefill_traced(m, om, t, spec, kv, cap, pos0, tokens, True, dev)
+    print(f"  tie flips over the prompt {sum(r[0] for r in res)}, worst error {max(r[1] for r in res):.2e}",
+          flush=True)
+    DP.run_traced(m, om, t, spec, kv, cap, pos0 + n, 1, True, dev, gtok)
+    m.close()
+
+
+@pytest.mark.timeout(600)
+def test_prefill_untraced_matches_traced_8b_layer_shape(dev):
+    """The untraced prefill (the timed path) equals the traced one bit for bit at the timed size:
+    two layers of the 8B shape, 512 tokens from position 0, f16 ring of 4096 slots (rings,
+    logits, next token)."""
+    print("prefill untraced vs traced, qwen3-8b layer shape, 512 tokens", flush=True)
+    spec = QWEN3_8B_2L
+    cap, n = 4096, 512
+    t = MS.build(spec, seed=61)
+    tokens = np.random.default_rng(62).integers(0, spec["vocab"], size=n).tolist()
+    ring_bytes = cap * spec["nkv"] * spec["hd"] * 2
+    outs = []
+    for traced in (True, False):
+        m = make_gpu_model(spec, t, cap, J.KV_F16, True)
+        buf = None
+        if traced:
+            _, _, _, total = m.trace_layout()
+            buf = torch.zeros(n * total, dtype=torch.uint8, device=dev)
+            m.set_trace(buf)
+        m.prefill(tokens, 0)
+        m.status()
+        if traced:
+            m.set_trace(None)
+            del buf
+        logits = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
+        m.read_logits(logits)
+        rings = []
+        for layer in range(spec["n_layers"]):
+            for ptr in m.kv_ptrs(layer):
+                r = torch.empty(ring_bytes, dtype=torch.uint8, device=dev)
+                J._memcpy(r.data_ptr(), ptr, ring_bytes)
+                rings.append(r.cpu().numpy())
+        outs.append((logits.cpu().numpy(), rings, m.read_token_pos()))
+        m.close()
+        torch.cuda.empty_cache()
+    (la, ra, ta), (lb, rb, tb) = outs
+    assert ta == tb == (ta[0], n)
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    for x, y in zip(ra, rb):
+        assert np.array_equal(x, y)
+
+
 def test_prefill_errors(dev):
     spec = SMALL
     t = MS.build(spec, seed=2)

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import jero_hip as J
-from qdata import rand_act, rand_weights
+from qdata import rand_act, rand_float_weights, rand_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -19,16 +19,20 @@ def call(fn, quant, w, n_in, n_out, x, y, *extra):
                C.c_void_p(y.data_ptr()), *extra, J._stream()))
 
 
-@pytest.mark.parametrize("quant", [J.Q4_K, J.Q6_K, J.Q8_0, J.Q4_0])
+@pytest.mark.parametrize("quant", [J.Q4_K, J.Q6_K, J.Q8_0, J.Q4_0, J.F32, J.F16, J.BF16])
 def test_noalloc_matches_vec_dot(dev, quant):
+    """The quantized formats stage the activation in the static array; F32 / F16 / BF16 rows take
+    the f32 input unstaged (their own branch of the entry point)."""
     print(f"vec_dot_noalloc quant={quant}", flush=True)
     lib = J.lib()
+    floats = quant in (J.F32, J.F16, J.BF16)
     for i, (n_in, n_out) in enumerate(((8192, 3000), (1024, 77))):  # second call smaller
-        w = torch.from_numpy(rand_weights(quant, n_out, n_in, 300 + i)).to(dev)
+        gen = rand_float_weights if floats else rand_weights
+        w = torch.from_numpy(gen(quant, n_out, n_in, 300 + i)).to(dev)
         x = torch.from_numpy(rand_act(n_in, 310 + i)).to(dev)
         y0 = torch.empty(n_out, dtype=torch.float32, device=dev)
         y1 = torch.full((n_out,), float("nan"), dtype=torch.float32, device=dev)
-        ws = torch.empty(J.row_bytes(J.act_format(quant), n_in), dtype=torch.uint8, device=dev)
+        ws = torch.empty(4 * n_in if floats else J.row_bytes(J.act_format(quant), n_in), dtype=torch.uint8, device=dev)
         call(lib.jero_hip_vec_dot, quant, w, n_in, n_out, x, y0, C.c_void_p(ws.data_ptr()), ws.numel())
         call(lib.jero_hip_vec_dot_noalloc, quant, w, n_in, n_out, x, y1)
         torch.cuda.synchronize()

@@ -310,10 +310,28 @@ int jero_hip_dequantize_rows(int quant, const void *w_dev, size_t w_bytes, int64
  * Qwen3Recipe::decode_step (:1441-1460) and sample_greedy_argmax (src/engine.rs:1873-1895).
  * Tensors are given by GGUF name (ModelWeights::tensor): token_embd.weight, output.weight,
  * output_norm.weight, blk.N.{attn_norm, attn_q, attn_k, attn_v, attn_output, attn_q_norm,
- * attn_k_norm, ffn_norm, ffn_gate, ffn_up, ffn_down}.weight; norms F32, matrices in
- * Q8_0/Q4_0/Q4_K/Q6_K with GGUF shape [n_in, n_out] (rows of up to 54592 elements for Q8_0/Q4_0,
- * 53760 for Q4_K/Q6_K: the activation of a row is held in LDS), token_embd also F32/F16/BF16.  The KV arena is one device buffer of
- * [n_layers][K ring, V ring][kv_capacity][n_heads_kv * head_dim] (the recipes' flat layout). */
+ * attn_k_norm, ffn_norm, ffn_gate, ffn_up, ffn_down}.weight; projections in Q8_0/Q4_0/Q4_K/Q6_K
+ * with GGUF shape [n_in, n_out] (rows of up to 54592 elements for Q8_0/Q4_0, 53760 for Q4_K/Q6_K:
+ * the activation of a row is held in LDS).  Norms, the embedding and the head may also be
+ * F32/F16/BF16 and of any shape, and any of them may be absent; they are read as the reference
+ * reads them:
+ *   norms  read_f32_weight_or_default (src/qwen_deepseek.rs:491-519): absent -> all 1.0; F32 ->
+ *          the stored values with 1.0 for a non-finite one or past the tensor's end; another
+ *          format with at least len elements -> its first len elements dequantized (1.0 if they
+ *          are not whole blocks); fewer -> all 1.0;
+ *   token_embd  embed_token (:558-582): rows of `hidden` elements (num_elements / hidden of
+ *          them); a token past them (or with no token_embd) embeds as the deterministic row
+ *          ((token % 31) * 0.05 + 0.25) + (i % 7) * 0.01;
+ *   head   project_lm_head (:584-632): output.weight, else token_embd.weight (ModelWeights' tied
+ *          fallback, src/weights.rs:1110-1126); jero_hip_model_logits_len logits
+ *          (infer_logits_buffer_len, src/engine.rs:1781-1792: the head's rows when they exceed
+ *          vocab by at most 1024 and are a multiple of 64, else vocab); a [hidden, rows] head
+ *          gives the first min(logits, rows) of them and xn[i % hidden] * 0.05 past them; a head
+ *          of logits * hidden elements in another shape is read as rows of hidden; with no
+ *          usable head every logit is tanh(sum(xn) / 16) + xn[i % hidden] * 0.1 + (i % 13) * 0.01
+ *          (xn the final RMSNorm's output).  The greedy token is the argmax over all logits.
+ * The KV arena is one device buffer of [n_layers][K ring, V ring][kv_capacity][n_heads_kv *
+ * head_dim] (the recipes' flat layout). */
 typedef struct jero_model_config {
   int64_t hidden, ffn, n_layers, vocab;
   int n_heads_q, n_heads_kv, head_dim;
@@ -332,8 +350,8 @@ int jero_hip_model_destroy(jero_model *model);
  * (src/gemma.rs:841-860) ignores it: the step then takes that projection's fallback. */
 int jero_hip_model_set_tensor(jero_model *model, const char *name, int quant, const void *src, size_t nbytes,
                               int64_t n_in, int64_t n_out, int src_on_device);
-/* Checks the required tensors (embedding, head, norms) are present and builds the device layout
- * (fused Q|K|V and gate|up rows, Q6_K_R planes).  Required before the first decode step.  A
+/* Builds the device layout (norm weights as f32 vectors, fused Q|K|V and gate|up rows, Q4_K_R /
+ * Q6_K_R planes, the LM head).  Required before the first decode step.  A
  * projection left out takes project_or_deterministic_slice's fallback (src/gemma.rs:841-860):
  * out[i] = in[i % in_len] * scale with the Qwen3 call sites' scales (Q 0.5, K 0.25, V 0.125 of the
  * normalised input, src/qwen_deepseek.rs:1011-1031; Wo 0.25 of the attention output, :1086-1092;
@@ -342,9 +360,13 @@ int jero_hip_model_set_tensor(jero_model *model, const char *name, int quant, co
 int jero_hip_model_finalize(jero_model *model);
 /* Device addresses of layer `layer`'s K and V rings (to pre-fill or inspect the cache). */
 int jero_hip_model_kv(jero_model *model, int64_t layer, void **k_ring_dev, void **v_ring_dev);
-/* Device addresses of the current token, the position and the last step's logits [vocab]. */
+/* Device addresses of the current token, the position and the last step's logits
+ * [jero_hip_model_logits_len]. */
 int jero_hip_model_state(jero_model *model, int32_t **token_dev, int64_t **pos_dev, float **logits_dev);
-/* Enqueues: token and position of the next decode step. */
+/* Logits per step once finalized (infer_logits_buffer_len, src/engine.rs:1781-1792), vocab before;
+ * -1 for a null model. */
+int64_t jero_hip_model_logits_len(const jero_model *model);
+/* Enqueues: token (>= 0; embed_token takes any id) and position of the next decode step. */
 int jero_hip_model_set_position(jero_model *model, int32_t token, int64_t pos, void *stream);
 /* Enqueues one decode step at the device position: writes logits, replaces the token with the
  * greedy next token and advances the position.  Enqueues kernels only (graph-capturable).

@@ -50,9 +50,26 @@ int launch_dgemv_dual(int quant1, int quant2, const DGemvArgs& a, hipStream_t s)
 // dgemv_long_max_k run the long-row variant.
 int dgemv_max_k(int quant);
 int dgemv_long_max_k(int quant);
-// hidden = embedding row of *token; also the step's RoPE table rope_cs[hd/2][cos, sin].
-int launch_embed(int quant, const void* w, int64_t rb, int H, int64_t vocab, const int32_t* token, float* out,
+// hidden = embed_token(*token): a row of the `rows` rows of rb bytes at w (null: no token_embd), or
+// the deterministic row of a token past them; also the step's RoPE table rope_cs[hd/2][cos, sin].
+int launch_embed(int quant, const void* w, int64_t rb, int H, int64_t rows, const int32_t* token, float* out,
                  const int64_t* pos, float theta, int hd, float* rope_cs, hipStream_t s);
+// read_f32_weight_or_default (src/qwen_deepseek.rs:491-519) of a norm weight into out[len] (raw
+// null: absent; deq: dequantize the first len elements of a non-F32 tensor).
+int launch_norm_weight(int quant, const void* raw, int64_t n_el, int64_t len, bool deq, float* out, hipStream_t s);
+// xn[H] = RMSNorm(x) * nw for an LM head read with an f32 input.
+int launch_head_norm(const float* x, const float* nw, float eps, int64_t H, float* xn, hipStream_t s);
+// project_lm_head's logits [start, L) that no head row gives (src/qwen_deepseek.rs:584-632): mode 0
+// rows past the head's `start` rows (xn[i % H] * 0.05), mode 1 no usable head (start 0; tanh of
+// the sum of xn / 16 + xn[i % H] * 0.1 + (i % 13) * 0.01).  head_tail_blocks(start, L) workgroups,
+// each writing its argmax partial at pv / pi (unless null).
+constexpr int64_t kHeadTailRows = 4096;
+int head_tail_blocks(int64_t start, int64_t L);
+int launch_head_tail(const float* x, const float* nw, float eps, int64_t H, int mode, int64_t start, int64_t L,
+                     float* logits, float* pv, int64_t* pi, float* tr_xn, hipStream_t s);
+// Per-workgroup (max, first index) partials of x[n] into pv / pi; returns their count (argmax_partials(n)),
+// or -1 on a launch error.
+int launch_argmax_partials(const float* x, int64_t n, float* pv, int64_t* pi, hipStream_t s);
 // The greedy token from the head's per-workgroup partials; all-NaN logits set the sticky *status
 // (token -1, position kept) instead of producing a token.
 int launch_argmax_final(const float* v, const int64_t* idx, int n, int32_t* token, int64_t* pos, int32_t* status,

@@ -424,12 +424,13 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_dual_kernel(DGemvArgs a)
 
 // ---------------------------------------------------------------- small kernels
 
-// hidden = dequantize_token_row(token_embd, *token) (embed_token, src/qwen_deepseek.rs:558-582)
-// A token outside the vocabulary (the greedy token of all-NaN logits is -1) embeds as zeros.
+// hidden = embed_token(*token) (src/qwen_deepseek.rs:558-582): row *token of token_embd's `rows`,
+// or the deterministic row of a token past them (embed_value); -1 (the greedy token of all-NaN
+// logits) embeds as zeros.
 // Block 0 also writes the step's RoPE table: (cos, sin) of pos / theta^(2i/hd), the f32 angle
 // of the reference's apply_rope_inplace (src/qwen_deepseek.rs:1056-1071).
 __global__ void __launch_bounds__(256) embed_kernel(int quant, const uint8_t* __restrict__ w, int64_t rb, int H,
-                                                    int64_t vocab, const int32_t* __restrict__ token,
+                                                    int64_t rows, const int32_t* __restrict__ token,
                                                     float* __restrict__ out, const int64_t* __restrict__ pos,
                                                     float theta, int hd, float* __restrict__ rope_cs) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -442,8 +443,7 @@ __global__ void __launch_bounds__(256) embed_kernel(int quant, const uint8_t* __
     rope_cs[2 * threadIdx.x + 1] = sn;
   }
   if (i >= H) return;
-  const int64_t t = *token;
-  out[i] = (t >= 0 && t < vocab) ? dequant_elem(quant, w + t * rb, i) : 0.0f;
+  out[i] = embed_value(quant, w, rb, rows, *token, i);
 }
 
 // (max, first index) merge of sample_greedy_argmax (src/engine.rs:1873-1895): NaN never wins,
@@ -835,10 +835,10 @@ int dgemv_max_k(int quant) {
                                                     : 256 * (kDecodeThreads / kWave) * kDecodeMaxActBlocks;
 }
 
-int launch_embed(int quant, const void* w, int64_t rb, int H, int64_t vocab, const int32_t* token, float* out,
+int launch_embed(int quant, const void* w, int64_t rb, int H, int64_t rows, const int32_t* token, float* out,
                  const int64_t* pos, float theta, int hd, float* rope_cs, hipStream_t s) {
   hipLaunchKernelGGL(embed_kernel, dim3(unsigned((H + 255) / 256)), dim3(256), 0, s, quant,
-                     static_cast<const uint8_t*>(w), rb, H, vocab, token, out, pos, theta, hd, rope_cs);
+                     static_cast<const uint8_t*>(w), rb, H, rows, token, out, pos, theta, hd, rope_cs);
   return check_launch("embed");
 }
 
@@ -896,6 +896,123 @@ __global__ void __launch_bounds__(256) swiglu_kernel(const float* __restrict__ g
   if (i >= F) return;
   const float gv = gu[i], uv = gu[F + i];
   act[i] = gv / (1.0f + expf(-gv)) * uv;
+}
+
+// read_f32_weight_or_default (src/qwen_deepseek.rs:491-519) of a norm weight, out[len]: raw null
+// (the tensor is absent) gives all ones; F32 keeps each finite stored value and gives 1.0 for a
+// non-finite one and past the tensor's n_el elements; another format dequantizes its first len
+// elements (row 0) when deq is set (at least len elements, len a whole number of blocks), else
+// all ones.
+__global__ void __launch_bounds__(256) norm_weight_kernel(int quant, const uint8_t* __restrict__ raw, int64_t n_el,
+                                                           int64_t len, int deq, float* __restrict__ out) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= len) return;
+  float v = 1.0f;
+  if (raw != nullptr) {
+    if (quant == JERO_F32) {
+      if (i < n_el) {
+        const float r = reinterpret_cast<const float*>(raw)[i];
+        if (isfinite(r)) v = r;
+      }
+    } else if (deq) {
+      v = dequant_elem(quant, raw, i);
+    }
+  }
+  out[i] = v;
+}
+
+// The LM head's final RMSNorm of x into xn [H] (xn = x * (1 / sqrt(mean(x^2) + eps)) * nw, the
+// head GEMV prologue's formula), for heads whose GEMV takes an f32 input (F32 / F16 / BF16 rows).
+__global__ void __launch_bounds__(1024) head_norm_kernel(const float* __restrict__ x, const float* __restrict__ nw,
+                                                          float eps, int64_t H, float* __restrict__ xn) {
+  __shared__ float s_tmp[16];
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < H; i += blockDim.x) ss += x[i] * x[i];
+  ss = block_sum(ss, s_tmp);
+  const float inv = 1.0f / sqrtf(ss / float(H) + eps);
+  for (int64_t i = threadIdx.x; i < H; i += blockDim.x) xn[i] = x[i] * inv * nw[i];
+}
+
+// project_lm_head's logits that no head row gives (src/qwen_deepseek.rs:584-632), from the final
+// hidden state x with xn = RMSNorm(x) * nw recomputed per workgroup:
+//   mode 0, rows past a head of `start` rows (:614-616): logits[i] = xn[i % H] * 0.05;
+//   mode 1, no usable head (:626-631): logits[i] = tanh(sum(xn) / 16) + xn[i % H] * 0.1 + (i % 13) * 0.01,
+//   each operation rounded on its own as the reference computes it.
+// Workgroup b covers [start + b kHeadTailRows, ...) and writes its (max, first index) at pv / pi[b]
+// (pv null: none); workgroup 0 also writes xn to tr_xn (the trace's head input) when given.
+__global__ void __launch_bounds__(256) head_tail_kernel(const float* __restrict__ x, const float* __restrict__ nw,
+                                                         float eps, int64_t H, int mode, int64_t start, int64_t L,
+                                                         float* __restrict__ logits, float* __restrict__ pv,
+                                                         int64_t* __restrict__ pi, float* __restrict__ tr_xn) {
+#pragma clang fp contract(off)
+  __shared__ float s_tmp[4];
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < H; i += blockDim.x) ss += x[i] * x[i];
+  ss = block_sum(ss, s_tmp);
+  const float inv = 1.0f / sqrtf(ss / float(H) + eps);
+  float base = 0.f;
+  if (mode == 1) {
+    float sx = 0.f;
+    for (int64_t i = threadIdx.x; i < H; i += blockDim.x) sx += x[i] * inv * nw[i];
+    __syncthreads();  // every wave has read s_tmp before it is reused
+    sx = block_sum(sx, s_tmp);
+    base = tanhf(sx / 16.0f);
+  }
+  if (tr_xn != nullptr && blockIdx.x == 0)
+    for (int64_t i = threadIdx.x; i < H; i += blockDim.x) tr_xn[i] = x[i] * inv * nw[i];
+  const int64_t b0 = start + int64_t(blockIdx.x) * kHeadTailRows;
+  const int64_t b1 = b0 + kHeadTailRows < L ? b0 + kHeadTailRows : L;
+  float bv = -INFINITY;
+  int64_t bi = -1;
+  for (int64_t i = b0 + threadIdx.x; i < b1; i += blockDim.x) {  // ascending per thread
+    const int64_t j = i % H;
+    const float xn = x[j] * inv * nw[j];
+    const float v = mode == 0 ? xn * 0.05f : (base + xn * 0.1f) + float(i % 13) * 0.01f;  // no contraction
+    logits[i] = v;
+    if (!isnan(v) && (bi < 0 || v > bv)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  argmax_block(bv, bi);
+  if (threadIdx.x == 0 && pv != nullptr) {
+    pv[blockIdx.x] = bv;
+    pi[blockIdx.x] = bi;
+  }
+}
+
+int launch_norm_weight(int quant, const void* raw, int64_t n_el, int64_t len, bool deq, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(norm_weight_kernel, dim3(unsigned((len + 255) / 256)), dim3(256), 0, s, quant,
+                     static_cast<const uint8_t*>(raw), n_el, len, deq ? 1 : 0, out);
+  return check_launch("norm weight");
+}
+
+int launch_head_norm(const float* x, const float* nw, float eps, int64_t H, float* xn, hipStream_t s) {
+  hipLaunchKernelGGL(head_norm_kernel, dim3(1), dim3(1024), 0, s, x, nw, eps, H, xn);
+  return check_launch("head norm");
+}
+
+int head_tail_blocks(int64_t start, int64_t L) {
+  return L > start ? int((L - start + kHeadTailRows - 1) / kHeadTailRows) : 0;
+}
+
+int launch_head_tail(const float* x, const float* nw, float eps, int64_t H, int mode, int64_t start, int64_t L,
+                     float* logits, float* pv, int64_t* pi, float* tr_xn, hipStream_t s) {
+  const int nb = head_tail_blocks(start, L);
+  if (nb == 0) return JERO_OK;
+  hipLaunchKernelGGL(head_tail_kernel, dim3(unsigned(nb)), dim3(256), 0, s, x, nw, eps, H, mode, start, L, logits, pv,
+                     pi, tr_xn);
+  return check_launch("head tail");
+}
+
+int launch_argmax_partials(const float* x, int64_t n, float* pv, int64_t* pi, hipStream_t s) {
+  const int nb = argmax_partials(n);
+  if (nb > 0) {
+    const int64_t chunk = (n + nb - 1) / nb;
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(unsigned(nb)), dim3(1024), 0, s, x, n, chunk, pv, pi);
+    if (check_launch("argmax partials")) return -1;
+  }
+  return nb;
 }
 
 int launch_det_proj(const float* x, int64_t len, const float* norm_w, float eps, float scale, float* y,

@@ -57,6 +57,22 @@ __device__ __forceinline__ float dequant_elem(int quant, const uint8_t* __restri
   }
 }
 
+// embed_token (src/qwen_deepseek.rs:558-582), element i of the embedding of token t: row t of the
+// token_embd tensor (rows of `rb` bytes, `rows` of them; w null when absent) when it has that row,
+// else the deterministic row ((t % 31) * 0.05 + 0.25) + (i % 7) * 0.01 in f32, each operation
+// rounded on its own as the reference computes it: contraction into fused multiply-adds is off
+// for these operators (the pragma reaches only operators written in this function, not those
+// inside __fmul_rn / __fadd_rn, which the compiler would still fuse).  t < 0 marks no token
+// (the greedy token of a step that failed closed) and embeds as zeros.
+__device__ __forceinline__ float embed_value(int quant, const uint8_t* __restrict__ w, int64_t rb, int64_t rows,
+                                             int64_t t, int64_t i) {
+#pragma clang fp contract(off)
+  if (t < 0) return 0.0f;
+  if (t < rows) return dequant_elem(quant, w + t * rb, i);
+  const float seed = float(uint32_t(t) % 31u) * 0.05f + 0.25f;
+  const float off = float(i % 7) * 0.01f;
+  return seed + off;
+}
 
 int launch_dequant_rows(int quant, const void* w, int64_t n_in, int64_t row0, int64_t n_rows, float* out,
                         hipStream_t s);

@@ -62,6 +62,14 @@ struct PrefillBufs {
 struct jero_model {
   jero_model_config cfg{};
   jero::DevTensor tok_embd, output, output_norm;
+  // The LM head as the step runs it (set by finalize; project_lm_head, src/qwen_deepseek.rs:584-632):
+  // head_mode says how, `head` is the tensor read as [hidden, head_rows] rows (output.weight, or a
+  // copy of token_embd.weight when output.weight is absent), logits_len = infer_logits_buffer_len.
+  int head_mode = 0;
+  jero::DevTensor head;
+  int64_t head_rows = 0, logits_len = 0;
+  int64_t embd_rows = 0;  // rows of `hidden` elements in token_embd.weight (0: absent)
+  float* head_xn = nullptr;  // the normalised head input of an f32-input (F32 / F16 / BF16) head
   std::vector<jero::LayerW> layers;
   bool finalized = false;
   // device state
@@ -227,6 +235,14 @@ static int repack_planar(jero_model* m, DevTensor& t) {
 
 constexpr int kArgmaxSlots = 4096;
 
+// How the LM head runs (chosen at finalize):
+//   kHeadFused  a quantized GEMV over all logits_len rows, argmax in its epilogue;
+//   kHeadTail   a quantized GEMV over head_rows < logits_len rows, then the 0.05 slice for the rest;
+//   kHeadFloat  an F32 / F16 / BF16 head: RMSNorm, the float GEMV over head_rows, the slice for any
+//               rest, then an argmax over all logits;
+//   kHeadNone   no usable head: the tanh fallback for every logit.
+enum { kHeadFused = 0, kHeadTail = 1, kHeadFloat = 2, kHeadNone = 3 };
+
 // Byte offsets of the debug trace of one decode step (the layout include/jero_hip.h documents):
 // per layer the fields below in this order, each starting on a 16-byte boundary, then the
 // head's fields.  act_bytes(n) is the larger of the Q8_K and ACT_Q8 block sizes of n elements.
@@ -267,7 +283,7 @@ static TraceLayout trace_layout(const jero_model_config& c) {
 
 static int gemv(jero_model* m, const DevTensor& w, const float* x, const float* norm, float eps, int out_mode,
                 float* y, int64_t half, hipStream_t s, int* blocks = nullptr, float* tr_xn = nullptr,
-                uint8_t* tr_q8 = nullptr, float* tr_gu = nullptr) {
+                uint8_t* tr_q8 = nullptr, float* tr_gu = nullptr, int max_blocks = kArgmaxSlots) {
   DGemvArgs a{};
   a.w = static_cast<const uint8_t*>(w.dev);
   a.rb = row_bytes(w.quant, w.n_in);
@@ -281,7 +297,7 @@ static int gemv(jero_model* m, const DevTensor& w, const float* x, const float* 
   a.half = half;
   a.amax_v = m->amax_v;
   a.amax_i = m->amax_i;
-  a.max_blocks = kArgmaxSlots;  // one argmax partial slot per workgroup
+  a.max_blocks = max_blocks;  // one argmax partial slot per workgroup
   a.tr_xn = tr_xn;
   a.tr_q8 = tr_q8;
   a.tr_gu = tr_gu;
@@ -370,25 +386,31 @@ extern "C" int jero_hip_model_set_tensor(jero_model* m, const char* name, int qu
     *slot = DevTensor{};
     return JERO_OK;
   }
-  if (n_in != ein || n_out != eout)
+  const bool norm = is_norm(name);
+  const bool embd = std::string(name) == "token_embd.weight";
+  const bool head = std::string(name) == "output.weight";
+  const bool float_w = quant == JERO_F32 || quant == JERO_F16 || quant == JERO_BF16;
+  // Norms, the embedding and the head are read the way the reference reads them, whatever their
+  // shape (read_f32_weight_or_default, embed_token, project_lm_head); the projections must have
+  // their layer shape.
+  if (n_in <= 0 || n_out <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, std::string("set_tensor: '") + name + "' is empty");
+  if (!norm && !embd && !head && (n_in != ein || n_out != eout))
     return fail(JERO_ERR_TENSOR_BOUNDS, std::string("set_tensor: '") + name + "' has shape [" + std::to_string(n_in) +
                                             ", " + std::to_string(n_out) + "], expected [" + std::to_string(ein) +
                                             ", " + std::to_string(eout) + "]");
-  const bool norm = is_norm(name);
-  if (norm && quant != JERO_F32)
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string("set_tensor: norm '") + name + "' must be F32");
-  const bool embd = std::string(name) == "token_embd.weight";
-  const bool float_w = quant == JERO_F32 || quant == JERO_F16 || quant == JERO_BF16;
-  if (!norm && (!is_weight_quant(quant) || (float_w && !embd)))
+  if (!is_weight_quant(quant) || (float_w && !norm && !embd && !head))
     return fail(JERO_ERR_CAPABILITY_MISMATCH,
                 std::string("set_tensor: '") + name + "' quantization " + std::to_string(quant) +
-                    " unsupported by the decode step (projections: Q8_0, Q4_0, Q4_K, Q6_K; the embedding also F32, "
-                    "F16, BF16)");
+                    " unsupported by the decode step (projections: Q8_0, Q4_0, Q4_K, Q6_K; norms, the embedding "
+                    "and the head also F32, F16, BF16)");
   const int64_t rb = row_bytes(quant, n_in);
   if (rb < 0 || size_t(rb) * size_t(n_out) != nbytes)
     return fail(JERO_ERR_TENSOR_BOUNDS, std::string("set_tensor: '") + name + "' byte size " + std::to_string(nbytes) +
                                             " does not match its shape");
-  if (!norm && !embd && n_in > dgemv_long_max_k(quant))
+  if (embd && row_bytes(quant, m->cfg.hidden) < 0)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string("set_tensor: token_embd.weight rows of ") +
+                                                  std::to_string(m->cfg.hidden) + " elements are not whole blocks");
+  if (!norm && !embd && !head && n_in > dgemv_long_max_k(quant))
     return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string("set_tensor: '") + name + "' rows of " +
                                                   std::to_string(n_in) + " elements exceed the decode limit " +
                                                   std::to_string(dgemv_long_max_k(quant)));
@@ -407,22 +429,31 @@ extern "C" int jero_hip_model_finalize(jero_model* m) {
   if (!m) return fail(JERO_ERR_INVALID_ARGUMENT, "finalize: null model");
   if (m->finalized) return JERO_OK;
   const auto& c = m->cfg;
-  auto need = [&](const DevTensor& t, const std::string& n) -> int {
-    if (!t.present()) return fail(JERO_ERR_CAPABILITY_MISMATCH, "finalize: tensor '" + n + "' missing");
+  const int64_t H = c.hidden;
+  int rc;
+  // Norm weights as read_f32_weight_or_default reads them (src/qwen_deepseek.rs:491-519): an
+  // absent one is all ones, F32 values that are not finite become 1.0, other formats are
+  // dequantized from their first len elements (when they hold whole blocks of them); each
+  // becomes an f32 vector of len.
+  auto norm_weight = [&](DevTensor& t, int64_t len) -> int {
+    void* p = nullptr;
+    int r = dev_alloc(m, sizeof(float) * size_t(len), &p);
+    if (r) return r;
+    const int64_t n_el = t.present() ? t.n_in * t.n_out : 0;
+    const bool deq = t.present() && t.quant != JERO_F32 && n_el >= len && row_bytes(t.quant, len) >= 0;
+    if ((r = launch_norm_weight(t.quant, t.dev, n_el, len, deq, static_cast<float*>(p), nullptr)) ||
+        (r = check_hip(hipDeviceSynchronize(), "norm weight")))
+      return r;
+    if (t.dev) dev_free(m, t.dev);
+    t = {JERO_F32, p, sizeof(float) * size_t(len), len, 1};
     return JERO_OK;
   };
-  int rc;
-  if ((rc = need(m->tok_embd, "token_embd.weight")) || (rc = need(m->output, "output.weight")) ||
-      (rc = need(m->output_norm, "output_norm.weight")))
-    return rc;
+  if ((rc = norm_weight(m->output_norm, H))) return rc;
   for (int64_t L = 0; L < c.n_layers; L++) {
     LayerW& l = m->layers[size_t(L)];
-    const std::string p = "blk." + std::to_string(L) + ".";
-    // the projections may be absent (project_or_deterministic_slice's fallback); the norms may not
-    if ((rc = need(l.attn_norm, p + "attn_norm.weight")) || (rc = need(l.ffn_norm, p + "ffn_norm.weight")))
-      return rc;
-    if (c.qk_norm && ((rc = need(l.q_norm, p + "attn_q_norm.weight")) || (rc = need(l.k_norm, p + "attn_k_norm.weight"))))
-      return rc;
+    if ((rc = norm_weight(l.attn_norm, H)) || (rc = norm_weight(l.ffn_norm, H))) return rc;
+    if (c.qk_norm && ((rc = norm_weight(l.q_norm, c.head_dim)) || (rc = norm_weight(l.k_norm, c.head_dim)))) return rc;
+    // the projections may be absent (project_or_deterministic_slice's fallback)
     l.qkv_split = !l.wq.present() || !l.wk.present() || !l.wv.present() || l.wq.quant != l.wk.quant;
     l.gu_split = !l.gate.present() || !l.up.present() || l.gate.quant != l.up.quant;
     if (l.qkv_split) {
@@ -453,7 +484,63 @@ extern "C" int jero_hip_model_finalize(jero_model* m) {
     if (l.wo.present() && (rc = repack_planar(m, l.wo))) return rc;
     if (l.down.present() && (rc = repack_planar(m, l.down))) return rc;
   }
-  if ((rc = repack_planar(m, m->output))) return rc;
+  // embed_token's rows (num_elements / hidden) and the LM head of project_lm_head
+  // (src/qwen_deepseek.rs:584-632): output.weight, else token_embd.weight (ModelWeights' tied
+  // fallback, src/weights.rs:1110-1126), with logits_len = infer_logits_buffer_len
+  // (src/engine.rs:1781-1792): the head's rows when they exceed vocab by at most 1024 and are a
+  // multiple of 64.
+  m->embd_rows = m->tok_embd.present() ? m->tok_embd.n_in * m->tok_embd.n_out / H : 0;
+  const bool tied = !m->output.present() && m->tok_embd.present();
+  const DevTensor* src = m->output.present() ? &m->output : tied ? &m->tok_embd : nullptr;
+  int64_t Ln = c.vocab;
+  if (src && src->n_out > c.vocab && src->n_out % 64 == 0 && src->n_out - c.vocab <= 1024) Ln = src->n_out;
+  if (Ln > int64_t(kArgmaxSlots) * kHeadTailRows)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "finalize: " + std::to_string(Ln) + " logits exceed the head's limit");
+  m->logits_len = Ln;
+  if (Ln > c.vocab) {
+    void* p = nullptr;
+    if ((rc = dev_alloc(m, sizeof(float) * size_t(Ln), &p))) return rc;
+    dev_free(m, m->logits);
+    m->logits = static_cast<float*>(p);
+  }
+  DevTensor hd{};
+  int64_t rows = 0;
+  if (src && src->n_in == H) {  // [hidden, rows]: its first min(logits_len, rows) rows (:607-618)
+    hd = *src;
+    rows = std::min(Ln, src->n_out);
+  } else if (src && src->n_in * src->n_out == Ln * H && row_bytes(src->quant, H) >= 0) {
+    hd = *src;  // logits_len * hidden elements in another shape: rows of hidden (:620-623)
+    hd.n_in = H;
+    hd.n_out = Ln;
+    rows = Ln;
+  }
+  m->head_rows = rows;
+  const bool float_head = hd.present() && (hd.quant == JERO_F32 || hd.quant == JERO_F16 || hd.quant == JERO_BF16);
+  if (!hd.present()) {
+    m->head_mode = kHeadNone;
+  } else if (float_head) {
+    m->head_mode = kHeadFloat;  // read in place (the embedding's own bytes when tied)
+    m->head = hd;
+    void* p = nullptr;
+    if ((rc = dev_alloc(m, sizeof(float) * size_t(H), &p))) return rc;
+    m->head_xn = static_cast<float*>(p);
+  } else {
+    if (H > dgemv_long_max_k(hd.quant))
+      return fail(JERO_ERR_CAPABILITY_MISMATCH, "finalize: head rows of " + std::to_string(H) +
+                                                    " elements exceed the decode limit");
+    if (tied) {  // the head's own copy: the embedding keeps its GGUF layout, the head goes planar
+      void* p = nullptr;
+      if ((rc = dev_alloc(m, hd.bytes, &p)) ||
+          (rc = check_hip(hipMemcpy(p, hd.dev, hd.bytes, hipMemcpyDeviceToDevice), "head copy")))
+        return rc;
+      hd.dev = p;
+    } else {
+      m->output = DevTensor{};  // the head owns output.weight's buffer from here on
+    }
+    m->head = hd;
+    if ((rc = repack_planar(m, m->head))) return rc;
+    m->head_mode = rows < Ln ? kHeadTail : kHeadFused;
+  }
   m->finalized = true;
   return JERO_OK;
 }
@@ -479,10 +566,14 @@ extern "C" int jero_hip_model_state(jero_model* m, int32_t** token_dev, int64_t*
 
 extern "C" int jero_hip_model_set_position(jero_model* m, int32_t token, int64_t pos, void* stream) {
   if (!m) return fail(JERO_ERR_INVALID_ARGUMENT, "set_position: null model");
-  if (token < 0 || token >= m->cfg.vocab)
-    return fail(JERO_ERR_TENSOR_BOUNDS, "set_position: token " + std::to_string(token) + " outside the vocabulary");
+  if (token < 0) return fail(JERO_ERR_TENSOR_BOUNDS, "set_position: negative token " + std::to_string(token));
   if (pos < 0) return fail(JERO_ERR_CONTEXT_LENGTH_EXCEEDED, "set_position: negative position");
   return launch_set_state(m->token, m->pos, m->status, token, pos, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t jero_hip_model_logits_len(const jero_model* m) {
+  if (!m) return -1;
+  return m->finalized ? m->logits_len : m->cfg.vocab;
 }
 
 extern "C" int64_t jero_hip_model_trace_bytes(const jero_model* m) {
@@ -519,6 +610,55 @@ extern "C" int jero_hip_model_status(jero_model* m, void* stream) {
   return JERO_OK;
 }
 
+namespace jero {
+
+// Final RMSNorm, project_lm_head (src/qwen_deepseek.rs:584-632) and the greedy token
+// (sample_greedy_argmax, src/engine.rs:1873-1895) from the hidden state x [hidden] on the device,
+// as finalize chose to run the head; tr_xn / tr_q8: the trace's head fields (or null).
+static int head_step(jero_model* m, const float* x, hipStream_t s, float* tr_xn, uint8_t* tr_q8) {
+  const auto& c = m->cfg;
+  const int64_t H = c.hidden, Ln = m->logits_len;
+  const float eps = c.rms_eps > 1e-6f ? c.rms_eps : 1e-6f;  // rms_eps.max(1e-6), :1250
+  const float* nw = static_cast<const float*>(m->output_norm.dev);
+  int nb = 0, rc = JERO_OK;
+  switch (m->head_mode) {
+    case kHeadFused:
+    case kHeadTail: {
+      const int tb = m->head_mode == kHeadTail ? head_tail_blocks(m->head_rows, Ln) : 0;
+      DevTensor h = m->head;
+      h.n_out = m->head_rows;
+      if ((rc = gemv(m, h, x, nw, eps, kOutArgmax, m->logits, 0, s, &nb, tr_xn, tr_q8, nullptr, kArgmaxSlots - tb)))
+        return rc;
+      if (tb > 0) {  // the rows past the head: its argmax partials follow the GEMV's
+        if ((rc = launch_head_tail(x, nw, eps, H, 0, m->head_rows, Ln, m->logits, m->amax_v + nb, m->amax_i + nb,
+                                   nullptr, s)))
+          return rc;
+        nb += tb;
+      }
+      break;
+    }
+    case kHeadFloat: {
+      if ((rc = launch_head_norm(x, nw, eps, H, m->head_xn, s))) return rc;
+      if (tr_xn && (rc = check_hip(hipMemcpyAsync(tr_xn, m->head_xn, sizeof(float) * size_t(H),
+                                                  hipMemcpyDeviceToDevice, s),
+                                   "head trace copy")))
+        return rc;
+      if ((rc = launch_matvec_float(m->head.quant, m->head.dev, H, m->head_rows, m->head_xn, m->logits, s)) ||
+          (rc = launch_head_tail(x, nw, eps, H, 0, m->head_rows, Ln, m->logits, nullptr, nullptr, nullptr, s)))
+        return rc;
+      nb = launch_argmax_partials(m->logits, Ln, m->amax_v, m->amax_i, s);
+      if (nb < 0) return JERO_ERR_DEVICE;
+      break;
+    }
+    default:  // no usable head: the tanh fallback for every logit
+      if ((rc = launch_head_tail(x, nw, eps, H, 1, 0, Ln, m->logits, m->amax_v, m->amax_i, tr_xn, s))) return rc;
+      nb = head_tail_blocks(0, Ln);
+  }
+  return launch_argmax_final(m->amax_v, m->amax_i, nb, m->token, m->pos, m->status, s);
+}
+
+}  // namespace jero
+
 extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
   if (!m) return fail(JERO_ERR_INVALID_ARGUMENT, "decode_step: null model");
   if (!m->finalized) return fail(JERO_ERR_INVALID_ARGUMENT, "decode_step: call jero_hip_model_finalize first");
@@ -528,7 +668,7 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
   const float eps_attn = c.rms_eps;
   const float eps_ffn = c.rms_eps > 1e-6f ? c.rms_eps : 1e-6f;  // rms_eps.max(1e-6), :1250
   int rc = launch_embed(m->tok_embd.quant, m->tok_embd.dev, row_bytes(m->tok_embd.quant, c.hidden), int(c.hidden),
-                        c.vocab, m->token, m->hidden, m->pos, c.rope_theta, c.head_dim, m->rope_cs, s);
+                        m->embd_rows, m->token, m->hidden, m->pos, c.rope_theta, c.head_dim, m->rope_cs, s);
   if (rc) return rc;
   const size_t es = c.kv_dtype == JERO_KV_F16 ? 2 : 4;
   const size_t ring = size_t(c.kv_capacity) * size_t(KV) * es;
@@ -669,14 +809,10 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
     if (rc) return rc;
   }
   // final norm -> LM head -> greedy token
-  int head_blocks = 0;
   uint8_t* tr_tail = m->trace;
   if (tr_tail && (rc = snap(tr_tail + tl.x_final, m->hidden, 4 * size_t(c.hidden)))) return rc;
-  rc = gemv(m, m->output, m->hidden, static_cast<const float*>(m->output_norm.dev), eps_ffn, kOutArgmax, m->logits, 0,
-            s, &head_blocks, tr_tail ? reinterpret_cast<float*>(tr_tail + tl.xn_head) : nullptr,
-            tr_tail ? tr_tail + tl.q8_head : nullptr);
-  if (rc) return rc;
-  return launch_argmax_final(m->amax_v, m->amax_i, head_blocks, m->token, m->pos, m->status, s);
+  return head_step(m, m->hidden, s, tr_tail ? reinterpret_cast<float*>(tr_tail + tl.xn_head) : nullptr,
+                   tr_tail ? tr_tail + tl.q8_head : nullptr);
 }
 
 namespace jero {
@@ -776,8 +912,7 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
                                                       std::to_string(pos0 + n - 1) + " exceed the ring of " +
                                                       std::to_string(c.kv_capacity));
   for (int64_t t = 0; t < n; t++)
-    if (tokens[t] < 0 || tokens[t] >= c.vocab)
-      return fail(JERO_ERR_TENSOR_BOUNDS, "prefill: token " + std::to_string(tokens[t]) + " outside the vocabulary");
+    if (tokens[t] < 0) return fail(JERO_ERR_TENSOR_BOUNDS, "prefill: negative token " + std::to_string(tokens[t]));
   const TraceLayout tl = trace_layout(c);
   if (m->trace && m->trace_bytes < size_t(n) * tl.total)
     return fail(JERO_ERR_TENSOR_BOUNDS, "prefill: the trace buffer holds fewer than " + std::to_string(n) + " steps");
@@ -805,8 +940,8 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
     *xrb = row_bytes(fmt, k);
     return launch_quantize_act(fmt, x, n, k, b.XQ, s);
   };
-  if ((rc = launch_embed_rows(m->tok_embd.quant, m->tok_embd.dev, row_bytes(m->tok_embd.quant, H), int(H), b.tok, n,
-                              b.X, s)))
+  if ((rc = launch_embed_rows(m->tok_embd.quant, m->tok_embd.dev, row_bytes(m->tok_embd.quant, H), m->embd_rows, int(H),
+                              b.tok, n, b.X, s)))
     return rc;
   // the residual of the last projection, added to X by the next row step (null: none pending);
   // pending2: the second K half of a split projection (the residual is pending + pending2)
@@ -1018,10 +1153,6 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
     return rc;
   if ((rc = launch_set_state(m->token, m->pos, m->status, tokens[n - 1], pos0 + n - 1, s))) return rc;
   uint8_t* tr_last = m->trace ? m->trace + size_t(n - 1) * tl.total : nullptr;
-  int head_blocks = 0;
-  rc = gemv(m, m->output, b.X + (n - 1) * H, static_cast<const float*>(m->output_norm.dev), eps_ffn, kOutArgmax,
-            m->logits, 0, s, &head_blocks, tr_last ? reinterpret_cast<float*>(tr_last + tl.xn_head) : nullptr,
-            tr_last ? tr_last + tl.q8_head : nullptr);
-  if (rc) return rc;
-  return launch_argmax_final(m->amax_v, m->amax_i, head_blocks, m->token, m->pos, m->status, s);
+  return head_step(m, b.X + (n - 1) * H, s, tr_last ? reinterpret_cast<float*>(tr_last + tl.xn_head) : nullptr,
+                   tr_last ? tr_last + tl.q8_head : nullptr);
 }

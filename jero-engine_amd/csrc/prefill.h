@@ -6,9 +6,10 @@
 
 namespace jero {
 
-// X[t] = embedding row of tokens[t] (device array), t < n.
-int launch_embed_rows(int quant, const void* w, int64_t rb, int H, const int32_t* tokens, int64_t n, float* X,
-                      hipStream_t s);
+// X[t] = embed_token(tokens[t]) (device array), t < n: a row of the `rows` rows of rb bytes at w,
+// or the deterministic row of a token past them.
+int launch_embed_rows(int quant, const void* w, int64_t rb, int64_t rows, int H, const int32_t* tokens, int64_t n,
+                      float* X, hipStream_t s);
 // XN[t] = RMSNorm(X[t]) * w, rows of H floats.
 int launch_rmsnorm_rows(const float* X, int64_t n, int64_t H, const float* w, float eps, float* XN, hipStream_t s);
 // Per token t < n (position pos0 + t): QK-norm (when given) and RoPE of its q heads (row t at q +

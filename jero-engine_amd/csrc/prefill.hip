@@ -14,12 +14,14 @@ namespace jero {
 
 namespace {
 
-// X[t][i] = embedding row tokens[t]; grid (ceil(H / 256), n).
-__global__ void __launch_bounds__(256) embed_rows_kernel(int quant, const uint8_t* __restrict__ w, int64_t rb, int H,
-                                                         const int32_t* __restrict__ tokens, float* __restrict__ X) {
+// X[t][i] = embed_token(tokens[t]) (a row of token_embd's `rows`, or the deterministic row);
+// grid (ceil(H / 256), n).
+__global__ void __launch_bounds__(256) embed_rows_kernel(int quant, const uint8_t* __restrict__ w, int64_t rb, int64_t rows,
+                                                         int H, const int32_t* __restrict__ tokens,
+                                                         float* __restrict__ X) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= H) return;
-  X[int64_t(blockIdx.y) * H + i] = dequant_elem(quant, w + int64_t(tokens[blockIdx.y]) * rb, i);
+  X[int64_t(blockIdx.y) * H + i] = embed_value(quant, w, rb, rows, tokens[blockIdx.y], i);
 }
 
 __device__ __forceinline__ float block_sum256(float v, float* s_tmp) {
@@ -299,10 +301,11 @@ __global__ void __launch_bounds__(256) add_rows_kernel(float* __restrict__ x, co
 
 }  // namespace
 
-int launch_embed_rows(int quant, const void* w, int64_t rb, int H, const int32_t* tokens, int64_t n, float* X,
+int launch_embed_rows(int quant, const void* w, int64_t rb, int64_t rows, int H, const int32_t* tokens, int64_t n,
+                      float* X,
                       hipStream_t s) {
   hipLaunchKernelGGL(embed_rows_kernel, dim3(unsigned((H + 255) / 256), unsigned(n)), dim3(256), 0, s, quant,
-                     static_cast<const uint8_t*>(w), rb, H, tokens, X);
+                     static_cast<const uint8_t*>(w), rb, rows, H, tokens, X);
   return check_launch("prefill embed");
 }
 

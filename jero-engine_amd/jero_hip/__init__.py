@@ -60,6 +60,7 @@ _SIGS = {
     "jero_hip_model_status": (_I32, [_P, _P]),
     "jero_hip_model_trace": (_I32, [_P, _P, _SZ]),
     "jero_hip_model_trace_bytes": (_I64, [_P]),
+    "jero_hip_model_logits_len": (_I64, [_P]),
     "jero_hip_sync": (_I32, [_P]),
     "jero_hip_gemm": (_I32, [_I32, _P, _SZ, _I64, _I64, _P, _I64, _P, _P]),
     "jero_hip_gemm_i8": (_I32, [_P, _I64, _I64, _P, _I64, _P, _P]),
@@ -657,9 +658,16 @@ class DecodeModel:
             per = ["attn_norm", "ffn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up",
                    "ffn_down"] + (["attn_q_norm", "attn_k_norm"] if hp["qk_norm"] else [])
             names += [f"blk.{i}.{b}.weight" for i in range(hp["n_layers"]) for b in per]
+            present = set(g.tensor_names())
             for name in names:
+                # an absent tensor takes the reference's default (norms 1.0, the projections'
+                # deterministic slice, the tied head, embed_token's deterministic row)
+                if name not in present:
+                    continue
                 t = g.tensor(name)
-                n_out = t["dims"][1] if t["n_dims"] > 1 else 1
+                n_out = 1
+                for d in t["dims"][1:t["n_dims"]]:
+                    n_out *= d
                 check(lib().jero_hip_model_set_tensor(m.h, name.encode(), t["quant"], C.c_void_p(t["host"]),
                                                       t["nbytes"], t["dims"][0], n_out, 0))
             m.finalize()
@@ -764,9 +772,17 @@ class DecodeModel:
         (all-NaN logits), as the reference's engine fails closed (src/engine.rs:636-641)."""
         check(lib().jero_hip_model_status(self.h, _stream(stream)))
 
+    def logits_len(self):
+        """Logits per step: infer_logits_buffer_len once finalized (jero_hip_model_logits_len)."""
+        return int(lib().jero_hip_model_logits_len(self.h))
+
     def read_logits(self, out):
+        """Copies the last step's logits into the float32 device tensor `out` (at least
+        logits_len() long; its first logits_len() values are written)."""
+        n = self.logits_len()
+        assert out.numel() >= n, f"logits buffer of {out.numel()} values, the model writes {n}"
         _, _, lp = self.state_ptrs()
-        _memcpy(out.data_ptr(), lp, self.cfg.vocab * 4)
+        _memcpy(out.data_ptr(), lp, n * 4)
         return out
 
     def read_token_pos(self):

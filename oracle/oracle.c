@@ -851,25 +851,83 @@ int jo_decode_layer(const jo_model *M, float *kv, int64_t L, float *x, int64_t p
   return rc;
 }
 
-int jo_decode_head(const jo_model *M, const float *x, float *logits, int threads, float *xn_head, void *q8_head) {
+void jo_read_f32_weight_or_default(int quant, const void *data, int64_t n_elements, int64_t len, float def,
+                                   float *out) {
+  for (int64_t i = 0; i < len; i++) out[i] = def;
+  if (!data || len <= 0) return;
+  if (quant == JO_F32) { /* :499-509: stored finite values, `def` elsewhere */
+    const uint8_t *raw = (const uint8_t *)data;
+    for (int64_t i = 0; i < len && i < n_elements; i++) {
+      float v = rdf32(raw + 4 * i);
+      if (isfinite(v)) out[i] = v;
+    }
+    return;
+  }
+  if (n_elements < len) return; /* :510 */
+  float *deq = (float *)malloc((size_t)len * 4);
+  if (!deq) return;
+  if (jo_dequantize_row(quant, data, len, deq) == 0) memcpy(out, deq, (size_t)len * 4); /* row 0, :511-514 */
+  free(deq);
+}
+
+int64_t jo_logits_len(int64_t vocab, int has_head, int64_t head_rows) {
+  if (has_head && head_rows > vocab && head_rows % 64 == 0 && head_rows - vocab <= 1024) return head_rows;
+  return vocab;
+}
+
+/* The reference rounds each f32 operation of the deterministic rows on its own: no contraction
+ * into fused multiply-adds here (nor in jo_decode_head's fallback). */
+__attribute__((optimize("fp-contract=off"))) int jo_embed_token(const jo_model *M, uint32_t token, float *x) {
   const int64_t H = M->hidden;
+  if (M->tok_embd.data && (int64_t)token < M->embd_rows)
+    return jo_dequantize_row(M->tok_embd.quant,
+                             (const uint8_t *)M->tok_embd.data + (int64_t)token * jo_row_bytes(M->tok_embd.quant, H), H,
+                             x);
+  const float seed = (float)(token % 31u) * 0.05f + 0.25f; /* :574-580 */
+  for (int64_t i = 0; i < H; i++) x[i] = seed + (float)(i % 7) * 0.01f;
+  return 0;
+}
+
+static int64_t model_logits_len(const jo_model *M) { return M->logits_len > 0 ? M->logits_len : M->vocab; }
+
+__attribute__((optimize("fp-contract=off"))) int jo_decode_head(const jo_model *M, const float *x, float *logits,
+                                                                int threads, float *xn_head, void *q8_head) {
+  const int64_t H = M->hidden, L = model_logits_len(M);
   const float eps = M->eps > 1e-6f ? M->eps : 1e-6f; /* :1305-1306 */
   float *xn = (float *)malloc((size_t)H * 4);
   if (!xn) return -1;
   jo_rmsnorm(xn, x, M->output_norm, H, eps);
   if (xn_head) memcpy(xn_head, xn, (size_t)H * 4);
-  int rc = jo_matvec_q(M->output.quant, M->output.data, H, M->vocab, xn, logits, threads, q8_head);
+  int rc = 0;
+  const int64_t rows = M->output.data ? M->out_rows : 0;
+  if (rows > 0 && M->out_in == H) {
+    /* the head's first min(L, rows) rows (slice_rows), the rest a slice of xn (:607-618) */
+    const int64_t target = L < rows ? L : rows;
+    rc = jo_matvec_q(M->output.quant, M->output.data, H, target, xn, logits, threads, q8_head);
+    for (int64_t i = target; i < L; i++) logits[i] = xn[i % H] * 0.05f;
+  } else if (rows > 0 && M->out_in * rows == L * H) {
+    /* the same elements read as L rows of H (:620-623) */
+    rc = jo_matvec_q(M->output.quant, M->output.data, H, L, xn, logits, threads, q8_head);
+  } else {
+    /* no usable head (:626-631): the sum in element order, as the iterator sums it */
+    float sum = 0.0f;
+    for (int64_t i = 0; i < H; i++) sum += xn[i];
+    const float base = tanhf(sum / 16.0f);
+    for (int64_t i = 0; i < L; i++) {
+      const float t = base + xn[i % H] * 0.1f;
+      logits[i] = t + (float)(i % 13) * 0.01f;
+    }
+  }
   free(xn);
   return rc;
 }
 
 int jo_decode_step(const jo_model *M, float *kv, int32_t token, int64_t pos, float *logits, int threads) {
   const int64_t H = M->hidden;
-  if (token < 0 || token >= M->vocab || M->kv_capacity <= 0) return -1;
+  if (token < 0 || M->kv_capacity <= 0) return -1;
   float *x = (float *)malloc((size_t)H * 4);
   if (!x) return -1;
-  int rc = jo_dequantize_row(M->tok_embd.quant,
-                             (const uint8_t *)M->tok_embd.data + token * jo_row_bytes(M->tok_embd.quant, H), H, x);
+  int rc = jo_embed_token(M, (uint32_t)token, x);
   for (int64_t L = 0; L < M->n_layers && !rc; L++) rc = jo_decode_layer(M, kv, L, x, pos, threads, NULL);
   if (!rc) rc = jo_decode_head(M, x, logits, threads, NULL, NULL);
   free(x);

@@ -146,7 +146,28 @@ typedef struct jo_model {
   const float *output_norm;
   const jo_layer *layers;
   int kv_f16; /* nonzero: the rings hold f16 values (each new K/V row rounded before it is attended) */
+  /* Embedding and LM head as ModelWeights presents them (src/weights.rs:1097-1144):
+   *   embd_rows   rows of `hidden` elements in tok_embd (num_elements / hidden; 0: no token_embd)
+   *   out_in, out_rows   the head tensor's shape [out_in, out_rows] (`output`: output.weight, or
+   *               token_embd.weight when output.weight is absent; out_rows 0: no head at all)
+   *   logits_len  infer_logits_buffer_len (jo_logits_len) */
+  int64_t embd_rows, out_in, out_rows, logits_len;
 } jo_model;
+
+/* read_f32_weight_or_default (src/qwen_deepseek.rs:491-519): out[len] = the weight's first len
+ * values -- data NULL (absent): all `def`; F32: each of the n_elements stored values that is
+ * finite, `def` for a non-finite value and past the tensor's end; another format with at least
+ * len elements: row 0 (the first len elements) dequantized, all `def` if that fails (len not a
+ * whole number of blocks, an unsupported format); fewer elements: all `def`. */
+void jo_read_f32_weight_or_default(int quant, const void *data, int64_t n_elements, int64_t len, float def,
+                                   float *out);
+/* infer_logits_buffer_len (src/engine.rs:1781-1792): the head's rows when it has more than
+ * vocab, a multiple of 64, at most 1024 past vocab; else vocab. */
+int64_t jo_logits_len(int64_t vocab, int has_head, int64_t head_rows);
+/* embed_token (src/qwen_deepseek.rs:558-582): row `token` of tok_embd dequantized when the
+ * tensor has that row; else (token_embd absent or too short) the deterministic row
+ * x[i] = ((token % 31) * 0.05 + 0.25) + (i % 7) * 0.01 in f32. */
+int jo_embed_token(const jo_model *mdl, uint32_t token, float *x);
 
 /* Intermediate values of one layer of the decode step (every pointer optional):
  *   xn_attn  rmsnorm(x) * attn_norm, the f32 input of the Q|K|V projections [hidden]
@@ -174,10 +195,13 @@ typedef struct jo_layer_trace {
  * in, the layer's output out (in place); writes K/V of `pos` into layer L's rings of kv. */
 int jo_decode_layer(const jo_model *mdl, float *kv, int64_t layer, float *x, int64_t pos, int threads,
                     const jo_layer_trace *tr);
-/* Final RMSNorm and LM head (:1305-1312): logits [vocab] from the last hidden state; xn_head /
- * q8_head (optional) receive the normalised input and its activation blocks. */
+/* Final RMSNorm and project_lm_head (:1305-1312, :584-632): logits [logits_len] from the last
+ * hidden state.  A head of shape [hidden, rows]: its first min(logits_len, rows) rows, the rest
+ * xn[i % hidden] * 0.05; a head of logits_len * hidden elements in another shape: its rows of
+ * `hidden` elements; no usable head: tanh(sum(xn) / 16) + xn[i % hidden] * 0.1 + (i % 13) * 0.01.
+ * xn_head / q8_head (optional) receive the normalised input and its activation blocks. */
 int jo_decode_head(const jo_model *mdl, const float *x, float *logits, int threads, float *xn_head, void *q8_head);
-/* kv: f32 [n_layers][2][kv_capacity][nkv*hd].  logits [vocab]. */
+/* kv: f32 [n_layers][2][kv_capacity][nkv*hd].  logits [logits_len].  token >= 0 (embed_token). */
 int jo_decode_step(const jo_model *mdl, float *kv, int32_t token, int64_t pos, float *logits,
                    int threads);
 

@@ -55,6 +55,9 @@ def lib():
             "jo_decode_step": (I32, [P, P, I32, I64, P, I32]),
             "jo_decode_layer": (I32, [P, P, I64, P, I64, I32, P]),
             "jo_decode_head": (I32, [P, P, P, I32, P, P]),
+            "jo_read_f32_weight_or_default": (None, [I32, P, I64, I64, F, P]),
+            "jo_logits_len": (I64, [I64, I32, I64]),
+            "jo_embed_token": (I32, [P, C.c_uint32, P]),
             "jo_splitmix": (C.c_uint64, [C.c_uint64]),
             "jo_fill_small": (None, [C.c_uint64, I64, P]),
             "jo_isqrt": (C.c_uint64, [C.c_uint64]),
@@ -249,7 +252,8 @@ class JoModel(C.Structure):
     _fields_ = [("hidden", C.c_int64), ("ffn", C.c_int64), ("n_layers", C.c_int64), ("vocab", C.c_int64),
                 ("nq", C.c_int), ("nkv", C.c_int), ("hd", C.c_int), ("eps", C.c_float), ("theta", C.c_float),
                 ("kv_capacity", C.c_int64), ("tok_embd", JoTensor), ("output", JoTensor),
-                ("output_norm", C.c_void_p), ("layers", C.c_void_p), ("kv_f16", C.c_int)]
+                ("output_norm", C.c_void_p), ("layers", C.c_void_p), ("kv_f16", C.c_int),
+                ("embd_rows", C.c_int64), ("out_in", C.c_int64), ("out_rows", C.c_int64), ("logits_len", C.c_int64)]
 
 
 class JoLayerTrace(C.Structure):
@@ -261,40 +265,96 @@ def act_row_bytes(weight_quant, k):
     return row_bytes(lib().jo_act_format(weight_quant), k)
 
 
-class DecodeModel:
-    """Holds a jo_model over numpy-owned tensors (see tests/model_spec.py for the dict layout)."""
+def _elements(quant, arr, dims=None):
+    """Element count of a tensor given as (quant, array[, n_in, n_out])."""
+    if dims is not None:
+        return int(dims[0]) * int(dims[1])
+    a = np.asarray(arr)
+    if quant == F32 and a.dtype == np.float32:
+        return a.size
+    be, bb = int(lib().jo_block_elems(quant)), int(lib().jo_block_bytes(quant))
+    return a.nbytes // bb * be
 
-    def __init__(self, spec, tensors, kv_capacity):
+
+def read_f32_weight_or_default(quant, arr, n_elements, length, default=1.0):
+    """jo_read_f32_weight_or_default: arr None for an absent tensor."""
+    out = np.empty(length, np.float32)
+    if arr is None:
+        lib().jo_read_f32_weight_or_default(quant, None, 0, length, default, _p(out))
+        return out
+    a = np.ascontiguousarray(arr)
+    lib().jo_read_f32_weight_or_default(quant, a.ctypes.data, n_elements, length, default, _p(out))
+    return out
+
+
+def logits_len(vocab, head_rows):
+    """jo_logits_len (infer_logits_buffer_len); head_rows None: no head tensor."""
+    return int(lib().jo_logits_len(vocab, 0 if head_rows is None else 1, 0 if head_rows is None else head_rows))
+
+
+class DecodeModel:
+    """Holds a jo_model over numpy-owned tensors (see tests/model_spec.py for the dict layout).
+    tensors: {name: (quant, array) or (quant, array, n_in, n_out)}.  Norm weights go through
+    read_f32_weight_or_default (absent: ones); qk_norm (default: whether blk.0's q-norm weight is
+    given) applies QK-norm with such weights.  The head is output.weight, else token_embd.weight
+    (ModelWeights' tied fallback), else none; logits are infer_logits_buffer_len long."""
+
+    def __init__(self, spec, tensors, kv_capacity, qk_norm=None):
         self._keep = []
         s = spec
         nl = s["n_layers"]
+        H, hd = s["hidden"], s["hd"]
         self.layers = (JoLayer * nl)()
+        if qk_norm is None:
+            qk_norm = "blk.0.attn_q_norm.weight" in tensors
+
+        def dims(name):
+            v = tensors[name]
+            return (v[2], v[3]) if len(v) >= 4 else None
 
         def t(name):
             if name not in tensors:  # a projection left out: the deterministic slice (gemma.rs:841-860)
                 return JoTensor(0, None)
-            quant, arr = tensors[name]
+            quant, arr = tensors[name][:2]
             arr = np.ascontiguousarray(arr)
             self._keep.append(arr)
             return JoTensor(quant, arr.ctypes.data)
 
-        def f(name):
-            if name not in tensors:
+        def f(name, length, need=True):
+            if not need:
                 return None
-            arr = np.ascontiguousarray(tensors[name][1], dtype=np.float32)
+            if name not in tensors:
+                arr = read_f32_weight_or_default(F32, None, 0, length)
+            else:
+                quant, a = tensors[name][:2]
+                arr = read_f32_weight_or_default(quant, a, _elements(quant, a, dims(name)), length)
             self._keep.append(arr)
             return arr.ctypes.data
 
         for L in range(nl):
             p = f"blk.{L}."
-            self.layers[L] = JoLayer(f(p + "attn_norm.weight"), f(p + "ffn_norm.weight"),
-                                     f(p + "attn_q_norm.weight"), f(p + "attn_k_norm.weight"),
+            self.layers[L] = JoLayer(f(p + "attn_norm.weight", H), f(p + "ffn_norm.weight", H),
+                                     f(p + "attn_q_norm.weight", hd, qk_norm), f(p + "attn_k_norm.weight", hd, qk_norm),
                                      t(p + "attn_q.weight"), t(p + "attn_k.weight"), t(p + "attn_v.weight"),
                                      t(p + "attn_output.weight"), t(p + "ffn_gate.weight"), t(p + "ffn_up.weight"),
                                      t(p + "ffn_down.weight"))
+        embd_rows = 0
+        if "token_embd.weight" in tensors:
+            q, a = tensors["token_embd.weight"][:2]
+            embd_rows = _elements(q, a, dims("token_embd.weight")) // H
+        head = "output.weight" if "output.weight" in tensors else (
+            "token_embd.weight" if "token_embd.weight" in tensors else None)
+        out_in = out_rows = 0
+        if head is not None:
+            q, a = tensors[head][:2]
+            dm = dims(head)
+            out_in, out_rows = dm if dm is not None else (H, _elements(q, a) // H)
+        self.logits_len = logits_len(s["vocab"], None if head is None else out_rows)
         self.model = JoModel(s["hidden"], s["ffn"], nl, s["vocab"], s["nq"], s["nkv"], s["hd"], s["eps"],
-                             s["theta"], kv_capacity, t("token_embd.weight"), t("output.weight"),
-                             f("output_norm.weight"), C.cast(self.layers, C.c_void_p))
+                             s["theta"], kv_capacity, t("token_embd.weight"),
+                             t(head) if head is not None else JoTensor(0, None),
+                             f("output_norm.weight", H), C.cast(self.layers, C.c_void_p), 0,
+                             embd_rows, out_in, out_rows, self.logits_len)
         self.kv_capacity = kv_capacity
         self.kvd = s["nkv"] * s["hd"]
         self.spec = s
@@ -303,17 +363,15 @@ class DecodeModel:
         return np.zeros((self.spec["n_layers"], 2, self.kv_capacity, self.kvd), np.float32)
 
     def step(self, kv, token, pos, threads=1):
-        logits = np.empty(self.spec["vocab"], np.float32)
+        logits = np.empty(self.logits_len, np.float32)
         rc = lib().jo_decode_step(C.byref(self.model), _p(kv), token, pos, _p(logits), threads)
         assert rc == 0
         return logits
 
     def embed(self, token):
-        H = self.spec["hidden"]
-        q = self.model.tok_embd.quant
-        rb = row_bytes(q, H)
-        raw = (C.c_uint8 * rb).from_address(self.model.tok_embd.data + token * rb)
-        return dequantize(q, np.frombuffer(raw, np.uint8), 1, H)[0]
+        x = np.empty(self.spec["hidden"], np.float32)
+        assert lib().jo_embed_token(C.byref(self.model), token, _p(x)) == 0
+        return x
 
     def layer(self, kv, L, x, pos, threads=1, trace=True):
         """jo_decode_layer: returns (x_out, trace dict of the layer's intermediate values)."""
@@ -342,7 +400,7 @@ class DecodeModel:
         """jo_decode_head: (logits, xn_head, q8_head)."""
         s = self.spec
         x = np.ascontiguousarray(x, np.float32)
-        logits = np.empty(s["vocab"], np.float32)
+        logits = np.empty(self.logits_len, np.float32)
         xn = np.empty(s["hidden"], np.float32)
         q8 = np.empty(act_row_bytes(self.model.output.quant, s["hidden"]), np.uint8)
         rc = lib().jo_decode_head(C.byref(self.model), _p(x), _p(logits), threads, _p(xn), _p(q8))

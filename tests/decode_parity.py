@@ -193,15 +193,79 @@ def check_layer(t, spec, D, L, pos, x_next, ring_k, ring_v, kv_f16, qk_norm=True
     return err
 
 
-def check_head(t, spec, Dh, logits, token, threads=16):
-    """Final RMSNorm, LM-head activation blocks and GEMV, and the greedy token from the device's
-    own logits."""
+def resolve_norms(t, spec, qk_norm=True):
+    """t with every norm weight replaced by the f32 vector the reference reads for it
+    (read_f32_weight_or_default through the oracle: absent -> ones, non-finite F32 values -> 1.0,
+    other formats dequantized), so that the checks below can use t[name][1] as the weight."""
+    H, hd = spec["hidden"], spec["hd"]
+    out = dict(t)
+    names = [("output_norm.weight", H)]
+    for L in range(spec["n_layers"]):
+        names += [(f"blk.{L}.attn_norm.weight", H), (f"blk.{L}.ffn_norm.weight", H)]
+        if qk_norm:
+            names += [(f"blk.{L}.attn_q_norm.weight", hd), (f"blk.{L}.attn_k_norm.weight", hd)]
+    for name, n in names:
+        if name in t:
+            q, a = t[name][:2]
+            dims = t[name][2:4] if len(t[name]) >= 4 else None
+            v = O.read_f32_weight_or_default(q, a, O._elements(q, a, dims), n)
+        else:
+            v = O.read_f32_weight_or_default(O.F32, None, 0, n)
+        out[name] = (O.F32, v, n, 1)
+    return out
+
+
+def head_spec(t, spec):
+    """project_lm_head's head (src/qwen_deepseek.rs:584-632): (tensor name or None -- output.weight,
+    else token_embd.weight --, its n_in, its rows, the rows its GEMV gives, logits_len)."""
     H, V = spec["hidden"], spec["vocab"]
-    xn = O.rmsnorm(Dh["x_final"], t["output_norm.weight"][1], max(spec["eps"], 1e-6))
-    err = {"norm": rel(Dh["xn_head"], xn)}
-    oq = t["output.weight"][0]
-    check_q8("head input", act_fmt(oq), Dh["xn_head"], Dh["q8_head"])
-    ref = _mv(t, "output.weight", q8_bytes(act_fmt(oq), H, Dh["q8_head"]), threads)
+    name = "output.weight" if "output.weight" in t else ("token_embd.weight" if "token_embd.weight" in t else None)
+    if name is None:
+        return None, 0, 0, 0, O.logits_len(V, None)
+    n_in, rows = t[name][2], t[name][3]
+    L = O.logits_len(V, rows)
+    if n_in == H:
+        return name, n_in, rows, min(L, rows), L
+    if n_in * rows == L * H:
+        return name, n_in, rows, L, L
+    return None, n_in, rows, 0, L
+
+
+def oracle_head_on(om, t, spec, x, hq, threads):
+    """The oracle's project_lm_head from the hidden state x (jo_decode_head), with its head GEMV, if
+    any, recomputed over the activation blocks hq (the device's, once accounted for) instead of
+    the oracle's own; hq None keeps the oracle's (an f32-input head)."""
+    ref, xn, _ = om.head(x, threads)
+    name, _, _, target, _ = head_spec(t, spec)
+    if name is not None and target > 0 and hq is not None:
+        q, arr = t[name][:2]
+        ref = ref.copy()
+        ref[:target] = O.matvec(q, arr, spec["hidden"], target, hq, threads=threads)
+    return ref, xn
+
+
+def check_head(t, spec, Dh, logits, token, threads=16, om=None):
+    """Final RMSNorm, LM-head activation blocks and GEMV, and the greedy token from the device's
+    own logits.  With om (the oracle model), any head project_lm_head takes: the rows past the
+    head (xn * 0.05), a head read as rows of hidden, the tanh fallback, an f32-input head."""
+    H = spec["hidden"]
+    if om is None:
+        xn = O.rmsnorm(Dh["x_final"], t["output_norm.weight"][1], max(spec["eps"], 1e-6))
+        err = {"norm": rel(Dh["xn_head"], xn)}
+        oq = t["output.weight"][0]
+        check_q8("head input", act_fmt(oq), Dh["xn_head"], Dh["q8_head"])
+        ref = _mv(t, "output.weight", q8_bytes(act_fmt(oq), H, Dh["q8_head"]), threads)
+    else:
+        name, _, _, target, L = head_spec(t, spec)
+        logits = logits[:L]
+        quantized = name is not None and target > 0 and t[name][0] not in (O.F32, O.F16, O.BF16)
+        hq = None
+        if quantized:
+            fq = act_fmt(t[name][0])
+            check_q8("head input", fq, Dh["xn_head"], Dh["q8_head"])
+            hq = q8_bytes(fq, H, Dh["q8_head"])
+        ref, xn = oracle_head_on(om, t, spec, Dh["x_final"], hq, threads)
+        err = {"norm": rel(Dh["xn_head"], xn)}
     err["gemv"] = rel(logits, ref)
     want = O.argmax(logits)
     assert token == (-1 if want is None else want), (token, want)
@@ -300,15 +364,22 @@ def _adopt(stats, tag, fmt, n, x_or, dev_q8, dev_x):
     return q8_bytes(fmt, n, dev_q8)
 
 
-def oracle_step_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True, threads=16, dev_rows=None):
+def oracle_step_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True, threads=16, dev_rows=None,
+                         om=None):
     """The step's layers (oracle_layers_adopting), then the head adopting the device's head input
-    bytes the same way.  Returns (logits, FlipStats, f16 flips)."""
+    bytes the same way (om given: any head, oracle_head_on).  Returns (logits, FlipStats, f16 flips)."""
     x, st, f16_flips = oracle_layers_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm, threads, dev_rows)
     eps_ffn = max(spec["eps"], 1e-6)
     xn = O.rmsnorm(x, t["output_norm.weight"][1], eps_ffn)
-    fh = act_fmt(t["output.weight"][0])
-    hq = _adopt(st, "head input", fh, spec["hidden"], xn, dev_head["q8_head"], dev_head["xn_head"])
-    return _mv(t, "output.weight", hq, threads), st, f16_flips
+    if om is None:
+        fh = act_fmt(t["output.weight"][0])
+        hq = _adopt(st, "head input", fh, spec["hidden"], xn, dev_head["q8_head"], dev_head["xn_head"])
+        return _mv(t, "output.weight", hq, threads), st, f16_flips
+    name, _, _, target, _ = head_spec(t, spec)
+    hq = None
+    if name is not None and target > 0 and t[name][0] not in (O.F32, O.F16, O.BF16):
+        hq = _adopt(st, "head input", act_fmt(t[name][0]), spec["hidden"], xn, dev_head["q8_head"], dev_head["xn_head"])
+    return oracle_head_on(om, t, spec, x, hq, threads)[0], st, f16_flips
 
 
 def oracle_layers_adopting(t, spec, kv, pos, x, dev_layers, dev_head, qk_norm=True, threads=16, dev_rows=None):
@@ -401,12 +472,13 @@ def run_traced(m, om, t, spec, kv, cap, pos0, steps, kv_f16, dev, tok, qk_norm=T
     The oracle follows the device's tokens.  Returns per-step (tie flips, logits error with
     adoption, logits error and cosine of the plain free-running oracle)."""
     import torch
+    t = resolve_norms(t, spec, qk_norm)
     L_n = spec["n_layers"]
     kvd = spec["nkv"] * spec["hd"]
     _, _, _, total = m.trace_layout()
     buf = torch.zeros(total, dtype=torch.uint8, device=dev)
     m.set_trace(buf)
-    logits = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
+    logits = torch.empty(m.logits_len(), dtype=torch.float32, device=dev)
     m.set_position(tok, pos0)
     kv_free = kv.copy()
     om.model.kv_f16 = 1 if kv_f16 else 0  # the plain oracle's rings hold what the device's hold
@@ -434,10 +506,10 @@ def run_traced(m, om, t, spec, kv, cap, pos0, steps, kv_f16, dev, tok, qk_norm=T
                 e = check_layer(t, spec, dl[L], L, pos, x_next, rk, rv, kv_f16, qk_norm, threads, dh["rope_cs"])
                 for k_, v_ in e.items():
                     worst[k_] = max(worst.get(k_, 0.0), v_)
-            eh = check_head(t, spec, dh, got, gtok, threads)
+            eh = check_head(t, spec, dh, got, gtok, threads, om)
             worst["head_gemv"] = eh["gemv"]
             ref, st, f16_flips = oracle_step_adopting(t, spec, kv, pos, x0, dl, dh, qk_norm, threads,
-                                                      dev_rows if kv_f16 else None)
+                                                      dev_rows if kv_f16 else None, om)
             free = om.step(kv_free, tok, pos, threads=threads)
             err, cs = rel(got, ref), cosine(got, ref)
             ferr, fcs = rel(got, free), cosine(got, free)
@@ -470,6 +542,7 @@ def run_prefill_traced(m, om, t, spec, kv, cap, pos0, tokens, kv_f16, dev, qk_no
     1e-3 and, on the last token, the head checks and the logits within 1e-3.  kv: the oracle's f32
     rings, advanced in step.  Returns (greedy token, per-token (tie flips, hidden/logits error))."""
     import torch
+    t = resolve_norms(t, spec, qk_norm)
     L_n = spec["n_layers"]
     kvd = spec["nkv"] * spec["hd"]
     n = len(tokens)
@@ -481,7 +554,7 @@ def run_prefill_traced(m, om, t, spec, kv, cap, pos0, tokens, kv_f16, dev, qk_no
         m.status()
     finally:
         m.set_trace(None)
-    logits = torch.empty(spec["vocab"], dtype=torch.float32, device=dev)
+    logits = torch.empty(m.logits_len(), dtype=torch.float32, device=dev)
     m.read_logits(logits)
     got = logits.cpu().numpy()
     gtok, gpos = m.read_token_pos()
@@ -505,10 +578,10 @@ def run_prefill_traced(m, om, t, spec, kv, cap, pos0, tokens, kv_f16, dev, qk_no
                 worst[k_] = max(worst.get(k_, 0.0), v_)
         last = i == n - 1
         if last:
-            eh = check_head(t, spec, dh, got, gtok, threads)
+            eh = check_head(t, spec, dh, got, gtok, threads, om)
             worst["head_gemv"] = eh["gemv"]
             ref, st, f16_flips = oracle_step_adopting(t, spec, kv, pos, x0, dl, dh, qk_norm, threads,
-                                                      dev_rows if kv_f16 else None)
+                                                      dev_rows if kv_f16 else None, om)
             err = rel(got, ref)
         else:
             xo, st, f16_flips = oracle_layers_adopting(t, spec, kv, pos, x0, dl, dh, qk_norm, threads,

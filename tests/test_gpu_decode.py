@@ -105,15 +105,15 @@ def test_golden_llama_traced_against_oracle(dev):
     m.close()
 
 
-def write_model_gguf(path, arch, spec, tensors):
+def write_model_gguf(path, arch, spec, tensors, extra_kvs=()):
     """A GGUF v3 file holding `tensors` ({name: (quant, bytes, n_in, n_out)}) and the spec's
-    hyperparameters under {arch}.* keys."""
+    hyperparameters under {arch}.* keys (plus extra_kvs)."""
     import gguf_writer as W
     kvs = [(f"{arch}.block_count", W.U32, spec["n_layers"]), (f"{arch}.embedding_length", W.U32, spec["hidden"]),
            (f"{arch}.feed_forward_length", W.U32, spec["ffn"]), (f"{arch}.attention.head_count", W.U32, spec["nq"]),
            (f"{arch}.attention.head_count_kv", W.U32, spec["nkv"]),
            (f"{arch}.attention.key_length", W.U32, spec["hd"]), (f"{arch}.rope.freq_base", W.F32, spec["theta"]),
-           (f"{arch}.attention.layer_norm_rms_epsilon", W.F32, spec["eps"])]
+           (f"{arch}.attention.layer_norm_rms_epsilon", W.F32, spec["eps"])] + list(extra_kvs)
     ts = [(n, q, (n_in, n_out) if n_out > 1 else (n_in,), W.as_bytes(a)) for n, (q, a, n_in, n_out) in tensors.items()]
     path.write_bytes(W.gguf_bytes(arch, kvs, ts))
 
@@ -377,11 +377,24 @@ def test_model_errors(dev):
         m.set_tensor("blk.7.attn_q.weight", J.Q4_K, np.zeros(512 * 2 * 144, np.uint8), 512, 512)
     assert ei.value.variant == "CapabilityMismatch"
     with pytest.raises(J.K3Error) as ei:
-        m.finalize()
-    assert ei.value.variant == "CapabilityMismatch" and "missing" in str(ei.value)
-    with pytest.raises(J.K3Error) as ei:
-        m.decode_step()
+        m.decode_step()  # before finalize
     assert ei.value.variant == "InvalidArgument"
+    with pytest.raises(J.K3Error) as ei:  # a format the step cannot read
+        m.set_tensor("blk.0.attn_norm.weight", 15, np.zeros(292, np.uint8), 256, 1)
+    assert ei.value.variant == "CapabilityMismatch"
+    with pytest.raises(J.K3Error) as ei:  # hidden not a multiple of 32
+        J.DecodeModel(500, 1024, 1, 100, 4, 2, 64, 1e-6, 1e6, 64)
+    assert ei.value.variant == "TensorBoundsError"
+    with pytest.raises(J.K3Error) as ei:
+        m.set_position(-2, 0)
+    assert ei.value.variant == "TensorBoundsError"
+    # every tensor absent is a model too (the reference's defaults throughout): it decodes
+    m.finalize()
+    assert m.logits_len() == 100
+    m.set_position(7, 0)
+    m.decode_step()
+    m.status()
+    assert m.read_token_pos()[1] == 1
     with pytest.raises(J.K3Error) as ei:
         J.DecodeModel(512, 1024, 1, 100, 8, 3, 64, 1e-6, 1e6, 64)
     assert ei.value.variant == "TensorBoundsError"

@@ -195,8 +195,8 @@ def test_prefill_errors(dev):
     with pytest.raises(J.K3Error) as ei:
         m.prefill(list(range(20)), 13)  # positions 13 .. 32 past the 32-slot ring
     assert ei.value.variant == "ContextLengthExceeded"
-    with pytest.raises(J.K3Error) as ei:
-        m.prefill([1, 2, spec["vocab"]], 0)
+    with pytest.raises(J.K3Error) as ei:  # a token id beyond the vocabulary embeds (embed_token); a negative one is no id
+        m.prefill([1, 2, -1], 0)
     assert ei.value.variant == "TensorBoundsError"
     with pytest.raises(J.K3Error) as ei:
         m.prefill([], 0)

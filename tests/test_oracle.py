@@ -483,3 +483,182 @@ def test_f16_ring_mode_rounds_the_new_row_before_attending():
     # layer 0's rows come from the same input; later layers see the rounded attention
     assert np.array_equal(kv16[0, :, 0], kv32[0, :, 0].astype(np.float16).astype(np.float32))
     assert not np.array_equal(l16, l32)
+
+
+# ---------------------------------------------------------------- weight helpers, embedding, LM head
+
+def _q8_0_blocks(d, q):
+    """Q8_0 bytes of blocks with f16 scale d and int8 quants q [nb][32]."""
+    q = np.asarray(q, np.int8).reshape(-1, 32)
+    out = np.zeros((q.shape[0], 34), np.uint8)
+    out[:, 0:2] = np.asarray([d] * q.shape[0], np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = q.view(np.uint8)
+    return out.reshape(-1)
+
+
+def test_read_f32_weight_or_default_cases():
+    """read_f32_weight_or_default (src/qwen_deepseek.rs:491-519), case by case."""
+    ones = np.ones(8, np.float32)
+    assert np.array_equal(O.read_f32_weight_or_default(O.F32, None, 0, 8), ones)  # absent
+    v = np.array([0.5, np.nan, -2.0, np.inf, -np.inf, 3.0, 0.0, -0.0], np.float32)
+    got = O.read_f32_weight_or_default(O.F32, v, 8, 8)
+    assert np.array_equal(got, np.array([0.5, 1, -2, 1, 1, 3, 0, 0], np.float32))  # non-finite -> 1.0
+    assert np.signbit(got[7])  # -0.0 is finite and kept
+    short = O.read_f32_weight_or_default(O.F32, v[:3], 3, 8)  # past the tensor's end -> 1.0
+    assert np.array_equal(short, np.array([0.5, 1, -2, 1, 1, 1, 1, 1], np.float32))
+    assert np.array_equal(O.read_f32_weight_or_default(O.F32, v, 8, 2), np.array([0.5, 1], np.float32))
+    h = np.array([0.25, np.nan, -1.5, 65504.0], np.float16)  # F16: dequantized, NaN kept
+    got = O.read_f32_weight_or_default(O.F16, h.view(np.uint8), 4, 4)
+    assert np.array_equal(got[[0, 2, 3]], np.array([0.25, -1.5, 65504.0], np.float32)) and np.isnan(got[1])
+    assert np.array_equal(O.read_f32_weight_or_default(O.F16, h.view(np.uint8), 4, 6), np.ones(6, np.float32))
+    q = np.arange(-32, 32)  # Q8_0, d = 0.5: w = q / 2 exactly; row 0 = the first len elements
+    blk = _q8_0_blocks(0.5, q)
+    assert np.array_equal(O.read_f32_weight_or_default(O.Q8_0, blk, 64, 64), (q / 2).astype(np.float32))
+    assert np.array_equal(O.read_f32_weight_or_default(O.Q8_0, blk, 64, 32), (q[:32] / 2).astype(np.float32))
+    w = rand_weights(O.Q4_K, 1, 256, 5)  # 128 of a Q4_K block's 256 elements: not whole blocks -> 1.0
+    assert np.array_equal(O.read_f32_weight_or_default(O.Q4_K, w, 256, 128), np.ones(128, np.float32))
+
+
+def test_logits_len_rule():
+    """infer_logits_buffer_len (src/engine.rs:1781-1792)."""
+    assert O.logits_len(192, 256) == 256          # 64 rows of padding, rows % 64 == 0
+    assert O.logits_len(1024, 2048) == 2048       # 1024 rows of padding: the limit
+    assert O.logits_len(1000, 2048) == 1000       # 1048 rows: too many
+    assert O.logits_len(200, 232) == 200          # rows % 64 != 0
+    assert O.logits_len(200, 200) == 200 and O.logits_len(200, 150) == 200
+    assert O.logits_len(200, None) == 200
+
+
+HEAD_SPEC = dict(hidden=128, ffn=256, n_layers=1, vocab=300, nq=2, nkv=1, hd=64, eps=1e-5, theta=1e4)
+
+
+def _head_model(tensors_extra, drop=()):
+    """A Q8_0 model of HEAD_SPEC with the head / embedding replaced or dropped."""
+    from qdata import rand_weights as rw
+    H, V = HEAD_SPEC["hidden"], HEAD_SPEC["vocab"]
+    t = {"token_embd.weight": (O.Q8_0, rw(O.Q8_0, V, H, 1), H, V),
+         "output.weight": (O.Q8_0, rw(O.Q8_0, V, H, 2), H, V),
+         "output_norm.weight": (O.F32, (1 + 0.1 * rand_act(H, 3)).astype(np.float32), H, 1)}
+    t.update(tensors_extra)
+    for k in drop:
+        t.pop(k, None)
+    return O.DecodeModel(HEAD_SPEC, t, 8), t
+
+
+def test_lm_head_padded_rows_and_slices():
+    """project_lm_head (src/qwen_deepseek.rs:584-632) with infer_logits_buffer_len: a head padded
+    by 64 zero rows (vocab 300 -> 364 is not a multiple of 64, so vocab 320) gives 384 logits whose
+    first 320 equal the unpadded head's and the rest exactly 0; a head of 100 rows gives the full
+    head's first 100 logits, then xn[i % hidden] * 0.05 (i past hidden wraps); the same elements
+    as [2 hidden, rows / 2] are read as rows of hidden."""
+    from qdata import rand_weights as rw
+    H = HEAD_SPEC["hidden"]
+    spec_v = dict(HEAD_SPEC, vocab=320)
+    full = rw(O.Q8_0, 320, H, 2)
+    rb = O.row_bytes(O.Q8_0, H)
+    x = rand_act(H, 9)
+    base = dict(token_embd=(O.Q8_0, rw(O.Q8_0, 320, H, 1), H, 320), norm=(O.F32, np.ones(H, np.float32), H, 1))
+
+    def model(spec, head):
+        t = {"token_embd.weight": base["token_embd"], "output_norm.weight": base["norm"]}
+        if head is not None:
+            t["output.weight"] = head
+        return O.DecodeModel(spec, t, 8)
+
+    ref, xn, _ = model(spec_v, (O.Q8_0, full, H, 320)).head(x)
+    padded = np.concatenate([full, _q8_0_blocks(0.0, np.zeros((64 * H // 32, 32)))])
+    pm = model(spec_v, (O.Q8_0, padded, H, 384))
+    assert pm.logits_len == 384
+    lp, _, _ = pm.head(x)
+    assert np.array_equal(lp[:320], ref) and np.all(lp[320:] == 0.0)
+    sm = model(spec_v, (O.Q8_0, full[:100 * rb], H, 100))
+    ls, xs, _ = sm.head(x)
+    assert sm.logits_len == 320 and np.array_equal(ls[:100], ref[:100])
+    idx = np.arange(100, 320)
+    assert np.array_equal(ls[100:], (xs[idx % H] * np.float32(0.05)).astype(np.float32))
+    assert not np.array_equal(ls[100:], (xs[(idx - 100) % H] * np.float32(0.05)).astype(np.float32))
+    rm = model(spec_v, (O.Q8_0, full, 2 * H, 160))  # same bytes, another shape
+    lr, _, _ = rm.head(x)
+    assert np.array_equal(lr, ref)
+
+
+def test_lm_head_without_head_is_the_tanh_fallback():
+    """No output.weight and no token_embd.weight (src/qwen_deepseek.rs:626-631): a zero hidden state
+    normalises to zero, so logit i is exactly (i % 13) * 0.01; a constant one gives
+    tanh(hidden * xn / 16) + xn * 0.1 + (i % 13) * 0.01 with xn = c / sqrt(c^2 + eps)."""
+    H, V = HEAD_SPEC["hidden"], HEAD_SPEC["vocab"]
+    om, _ = _head_model({"output_norm.weight": (O.F32, np.ones(H, np.float32), H, 1)},
+                        drop=("output.weight", "token_embd.weight"))
+    assert om.logits_len == V
+    l0, _, _ = om.head(np.zeros(H, np.float32))
+    assert np.array_equal(l0, (np.arange(V) % 13).astype(np.float32) * np.float32(0.01))
+    c = 0.75
+    lc, xn, _ = om.head(np.full(H, c, np.float32))
+    x64 = c / math.sqrt(c * c + 1e-5)
+    want = math.tanh(H * x64 / 16) + 0.1 * x64 + (np.arange(V) % 13) * 0.01
+    assert np.max(np.abs(lc - want)) < 2e-6
+
+
+def test_embed_token_rows_and_deterministic_row():
+    """embed_token (src/qwen_deepseek.rs:558-582): a token with a row dequantizes it; a token past
+    the rows, or any token without token_embd, gives ((t % 31) * 0.05 + 0.25) + (i % 7) * 0.01."""
+    H, V = HEAD_SPEC["hidden"], HEAD_SPEC["vocab"]
+    om, t = _head_model({})
+    e = om.embed(7)
+    rb = O.row_bytes(O.Q8_0, H)
+    assert np.array_equal(e, O.dequantize(O.Q8_0, t["token_embd.weight"][1][7 * rb:8 * rb], 1, H)[0])
+
+    def det(tok):
+        seed = np.float32(tok % 31) * np.float32(0.05) + np.float32(0.25)
+        off = (np.arange(H) % 7).astype(np.float32) * np.float32(0.01)  # f32 products, one rounding each
+        assert off.dtype == np.float32
+        return (seed + off).astype(np.float32)
+
+    for tok in list(range(V, V + 31)) + [12345, 2 ** 31 - 1]:  # every residue mod 31
+        assert np.array_equal(om.embed(tok), det(tok)), tok
+    none, _ = _head_model({}, drop=("token_embd.weight",))
+    assert np.array_equal(none.embed(3), det(3))
+    assert np.abs(det(31) - det(0)).max() == 0.0 and det(1)[0] == np.float32(0.3)
+
+
+def test_absent_and_nonfinite_norms_in_the_decode_step():
+    """read_f32_weight_or_default in execute_token_standard_with_hidden: absent norms give the logits
+    of all-ones F32 norms, an F16 norm those of its f32 values, NaN / inf entries those of 1.0 in
+    their place (bitwise, over two steps); a tied model (no output.weight) those of output.weight =
+    token_embd.weight."""
+    import model_spec as MS
+    spec = dict(hidden=256, ffn=512, n_layers=2, vocab=40, nq=4, nkv=2, hd=64, eps=1e-6, theta=1e6)
+    t = MS.build(spec, seed=8)
+    norms = [k for k in t if k.endswith("norm.weight")]
+
+    def run(tensors, qk_norm=True):
+        om = O.DecodeModel(spec, tensors, 8, qk_norm=qk_norm)
+        kv, out, tok = om.new_kv(), [], 3
+        for pos in range(2):
+            lg = om.step(kv, tok, pos, threads=2)
+            out.append(lg)
+            tok = int(np.argmax(lg))
+        return np.stack(out)
+
+    ones = {k: (O.F32, np.ones(v[2], np.float32), v[2], 1) if k in norms else v for k, v in t.items()}
+    absent = {k: v for k, v in t.items() if k not in norms}
+    assert np.array_equal(run(absent), run(ones))
+    f16 = dict(t)
+    f32_of_f16 = dict(t)
+    for k in ("blk.0.attn_norm.weight", "blk.1.attn_k_norm.weight", "output_norm.weight"):
+        h = t[k][1].astype(np.float16)
+        f16[k] = (O.F16, h.view(np.uint8), t[k][2], 1)
+        f32_of_f16[k] = (O.F32, h.astype(np.float32), t[k][2], 1)
+    assert np.array_equal(run(f16), run(f32_of_f16))
+    bad, fixed = dict(t), dict(t)
+    w = t["blk.1.ffn_norm.weight"][1].copy()
+    w[[3, 17, 200]] = [np.nan, np.inf, -np.inf]
+    wf = w.copy()
+    wf[[3, 17, 200]] = 1.0
+    bad["blk.1.ffn_norm.weight"] = (O.F32, w, w.size, 1)
+    fixed["blk.1.ffn_norm.weight"] = (O.F32, wf, wf.size, 1)
+    assert np.array_equal(run(bad), run(fixed))
+    assert not np.array_equal(run(fixed), run(t))
+    tied = {k: v for k, v in t.items() if k != "output.weight"}
+    tied_explicit = dict(tied, **{"output.weight": t["token_embd.weight"]})
+    assert np.array_equal(run(tied), run(tied_explicit))

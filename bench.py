@@ -52,6 +52,7 @@ HEAD = (4096, 151936)  # Q6_K output head
 ROTATE_BYTES = 768e6
 QWEN3_8B = dict(hidden=4096, ffn=12288, n_layers=36, vocab=151936, nq=32, nkv=8, hd=128, eps=1e-6, theta=1e6)
 KV_CAP = 4096
+PF_REPS = 15
 
 
 def synth_weights(torch, J, quant, n_in, n_out, copies, dev, seed):
@@ -95,8 +96,12 @@ def q8_0_weights(torch, n_in, n_out, copies, dev, seed):
     return [mats[c % len(mats)].clone() for c in range(copies)]
 
 
-def time_graph(torch, fn, steps, warmup, stream):
-    """Captures `fn` (one step) `steps` times in a graph; returns (seconds per step)."""
+def time_graph(torch, fn, steps, warmup, stream, span=1):
+    """Captures `fn` (one step) max(steps, span) times in a graph and times one replay after a
+    warm one; returns seconds per step.  `span` is the number of steps after which the rotated
+    weight copies repeat, so a graph of at least that many steps never replays a copy that the
+    previous replay left in the Infinity Cache."""
+    n = max(steps, span)
     with torch.cuda.stream(stream):
         for _ in range(max(warmup, 1)):
             fn()
@@ -104,7 +109,7 @@ def time_graph(torch, fn, steps, warmup, stream):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         with torch.cuda.graph(g, stream=stream):
-            for _ in range(steps):
+            for _ in range(n):
                 fn()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):  # graph replays run on the current stream
@@ -114,7 +119,7 @@ def time_graph(torch, fn, steps, warmup, stream):
         g.replay()
         e.record(stream)
     e.synchronize()
-    return s.elapsed_time(e) / 1e3 / steps
+    return s.elapsed_time(e) / 1e3 / n
 
 
 def time_graph_dist(torch, fn, chunk, reps, stream):
@@ -220,20 +225,25 @@ def bench_decode(torch, J, dev, stream, steps, warmup, keep_host):
     tok, pos = m.read_token_pos()
     # prefill (extra): a 512-token prompt from position 0 through jero_hip_model_prefill, every
     # projection a GEMM over the 512 rows; one warm call allocates the row buffers and builds the
-    # int8 planes of the Q6_K tensors
+    # int8 planes of the Q6_K tensors.  The prompt sits in pinned host memory (its 2 KB upload is
+    # an asynchronous copy inside each call); events around each of PF_REPS back-to-back calls
     import numpy as np
     n_pf = 512
-    prompt = np.random.default_rng(5).integers(0, spec["vocab"], n_pf).tolist()
+    prompt = torch.tensor(np.random.default_rng(5).integers(0, spec["vocab"], n_pf), dtype=torch.int32).pin_memory()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(PF_REPS + 1)]
+    host_s = []
     with torch.cuda.stream(stream):
         m.prefill(prompt, 0, stream=stream)
         stream.synchronize()
-        s1, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s1.record(stream)
-        for _ in range(3):
+        ev[0].record(stream)
+        for r in range(PF_REPS):
+            h0 = time.perf_counter()
             m.prefill(prompt, 0, stream=stream)
-        e1.record(stream)
-    e1.synchronize()
-    t_pf = s1.elapsed_time(e1) / 1e3 / 3
+            host_s.append(time.perf_counter() - h0)
+            ev[r + 1].record(stream)
+    ev[-1].synchronize()
+    pf = np.array([ev[r].elapsed_time(ev[r + 1]) for r in range(PF_REPS)])  # ms per call
+    t_pf = float(np.median(pf)) * 1e-3
     kv_bytes = spec["n_layers"] * 2 * KV_CAP * kvd * 2
     res = {"workload": "Qwen3-8B-shape Q4_K_M batch-1 greedy decode, 36 layers, f16 KV ring 4096 slots full",
            "tok_s": round(1.0 / t_tok, 1), "ms_per_token": round(t_tok * 1e3, 4), "steps": steps,
@@ -242,8 +252,13 @@ def bench_decode(torch, J, dev, stream, steps, warmup, keep_host):
            "frac_weights_kv_roofline": round((weight_bytes + kv_bytes) / t_tok / 1e9 / HBM_PEAK_GBS, 4),
            "last_token": tok, "position": pos, "graph": "one decode step captured, replayed per token",
            "prefill": {"tokens": n_pf, "ms": round(t_pf * 1e3, 3), "tok_s": round(n_pf / t_pf, 1),
+                       "ms_p10": round(float(np.percentile(pf, 10)), 3), "ms_p90": round(float(np.percentile(pf, 90)), 3),
+                       "ms_min": round(float(pf.min()), 3), "ms_max": round(float(pf.max()), 3), "calls": PF_REPS,
+                       "host_enqueue_ms": round(float(np.median(host_s)) * 1e3, 3),
                        "what": "jero_hip_model_prefill of a 512-token prompt from position 0 (GEMMs over the "
-                               "token rows, causal attention), eager, events around 3 calls"}}
+                               "token rows, causal attention), eager, prompt in pinned host memory; median of "
+                               "per-call events over back-to-back calls (ms); host_enqueue_ms: the host's time "
+                               "to enqueue one call"}}
     m.close()
     return res, host, host_kv
 
@@ -251,6 +266,7 @@ def bench_decode(torch, J, dev, stream, steps, warmup, keep_host):
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 GEMM_SHAPE = (512, 4096, 14336)  # (tokens M, n_in K, n_out N), Q4_K weights
+GEMM_ROTATE_BYTES = 512 * 10 ** 6
 
 
 def bench_gemm(torch, J, dev, stream, steps, keep_host):
@@ -258,11 +274,13 @@ def bench_gemm(torch, J, dev, stream, steps, keep_host):
     re-laid out once at load into the GEMM's fragment order (jero_hip_repack_gemm: Q4_K_G, the
     quants regrouped and the scales unpacked, 160 bytes per 256-block against 144, as the model's
     prefill holds them); the kernel over the GGUF bytes is timed too
-    (`gguf`).  Weights rotate over 4 copies.  `mfma_issue_frac`: the MFMA work the kernel issues
+    (`gguf`).  Weights rotate over copies of >= 512 MB in all (14 of 36.7 MB in the GGUF layout,
+    40.8 MB in the GEMM layout), every graph spanning all of them.  `mfma_issue_frac`: the MFMA work the kernel issues
     (two int8 planes of 2MNK ops each, plus the f16 mins product of 2MN*16 per block) over the
     time at peak."""
     M, K, N = GEMM_SHAPE
-    copies = 4
+    nbytes = J.row_bytes(J.Q4_K, K) * N
+    copies = -(-GEMM_ROTATE_BYTES // nbytes)
     buf = synth_weights(torch, J, J.Q4_K, K, N, copies, dev, 3000)
     views = [J.TensorView("ffn_up", J.Q4_K, [K, N], buf[c]) for c in range(copies)]
     laid = [J.repack_gemm(v) for v in views]
@@ -281,17 +299,20 @@ def bench_gemm(torch, J, dev, stream, steps, keep_host):
             J.gemm(vs[cnt[0] % copies], xq, M, y, stream=stream)
             cnt[0] += 1
 
-        return time_graph(torch, one, steps, 3, stream)
+        return time_graph(torch, one, steps, 3, stream, span=copies)
 
     t = timed(laid)
     tg = timed(views)
+    laid_bytes = sum(v.nbytes() for v in laid)
     res = {"workload": f"Q4_K x Q8_K prefill GEMM M={M} K={K} N={N}, int8 MFMA, weights in the GEMM layout "
                        f"(Q4_K_G: the quants in MFMA fragment order, scales unpacked, repacked once at load)",
            "us": round(t * 1e6, 2), "tops": round(ops / t / 1e12, 1), "unit": "TOP/s", "peak": INT8_PEAK_TOPS,
            "frac_int8_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS, 4),
            "mfma_issue_frac": round(issued / t, 4), "tokens_per_s": round(M / t, 1),
+           "rotation_bytes": laid_bytes, "graph_launches": max(steps, copies),
            "gguf": {"what": "the same GEMM over the GGUF Q4_K bytes (no repack)", "us": round(tg * 1e6, 2),
-                    "tops": round(ops / tg / 1e12, 1), "frac_int8_peak": round(ops / tg / 1e12 / INT8_PEAK_TOPS, 4)}}
+                    "tops": round(ops / tg / 1e12, 1), "frac_int8_peak": round(ops / tg / 1e12 / INT8_PEAK_TOPS, 4),
+                    "rotation_bytes": copies * nbytes}}
     host = None
     if keep_host:
         host = (buf[0].cpu().numpy(), xq.cpu().numpy())
@@ -320,9 +341,13 @@ MOE = dict(hidden=2048, experts=128, ffn=768, top_k=8)
 
 def bench_moe(torch, J, dev, stream, steps):
     """Qwen3-MoE expert layer: H=2048, 128 experts of FFN 768 (gate/up Q4_K, down Q6_K, repacked
-    at load time), router logits N(0,1), top-8; T=1 (decode) and T=64.  Two weight copies and 8
-    logit sets rotate, so the experts read differ between launches.  Algorithmic bytes: the
-    distinct routed experts' weights (3.06 MB each) + activations."""
+    at load time), top-8; T=1 (decode) and T=64.  Two weight copies (392 MB of experts each).
+    T=1: router logits N(0,1) with +16 on 8 experts of a random permutation, 16 logit sets that
+    route the token to each of the 128 experts once, so 32 calls (16 sets x 2 copies) read all
+    784 MB of expert bytes once and no call re-reads what an earlier one left in the Infinity
+    Cache.  T=64: 8 sets of N(0,1) logits (each call routes to ~126 of the 128 experts), copies
+    alternating.  Every graph spans 32 calls.  Algorithmic bytes: the distinct routed experts'
+    weights (3.06 MB each) + activations."""
     H, E, F, k = MOE["hidden"], MOE["experts"], MOE["ffn"], MOE["top_k"]
     copies = 2
     gate = synth_weights(torch, J, J.Q4_K, H, E * F, copies, dev, 3100)
@@ -336,9 +361,19 @@ def bench_moe(torch, J, dev, stream, steps):
     g = torch.Generator(device=dev)
     g.manual_seed(3103)
     out = {}
+    sets = E // k  # T=1 logit sets: each expert the top-8 of exactly one
+    span = sets * copies
     for T in (1, 64):
         x = torch.randn(T, H, generator=g, device=dev)
-        logits = [torch.randn(T, E, generator=g, device=dev) for _ in range(8)]
+        if T == 1:
+            perm = torch.randperm(E, generator=g, device=dev)
+            logits = []
+            for i in range(sets):
+                lg = torch.randn(T, E, generator=g, device=dev)
+                lg[:, perm[i * k:(i + 1) * k]] += 16.0
+                logits.append(lg)
+        else:
+            logits = [torch.randn(T, E, generator=g, device=dev) for _ in range(8)]
         y = torch.empty(T, H, device=dev)
         ws = torch.empty(J.lib().jero_hip_moe_workspace_bytes(T, E, k, H, F), dtype=torch.uint8, device=dev)
         cnt = [0]
@@ -346,18 +381,24 @@ def bench_moe(torch, J, dev, stream, steps):
 
         def one():
             c = cnt[0]
-            sel, _ = J.dispatch_qwen3_moe_ffn(y, x, logits[c % 8], k, gv[c % copies], uv[c % copies],
-                                             dv[c % copies], workspace=ws, stream=stream)
-            if len(sels) < 8:
-                sels.append(sel)
+            # T=1: all 16 sets on one copy, then on the other; T=64: copies alternate
+            cp = (c // sets) % copies if T == 1 else c % copies
+            sel, _ = J.dispatch_qwen3_moe_ffn(y, x, logits[c % len(logits)], k, gv[cp], uv[cp], dv[cp],
+                                             workspace=ws, stream=stream)
+            if len(sels) < span:
+                sels.append((cp, sel))
             cnt[0] += 1
 
-        t = time_graph(torch, one, steps, 1, stream)
-        distinct = sum(len(set(s.cpu().numpy().reshape(-1).tolist())) for s in sels[:8]) / len(sels[:8])
+        t = time_graph(torch, one, steps, 1, stream, span=span)
+        per_call = [set(s.cpu().numpy().reshape(-1).tolist()) for _, s in sels]
+        distinct = sum(len(u) for u in per_call) / len(per_call)
+        rotation = sum(len(set().union(*[u for (cp, _), u in zip(sels, per_call) if cp == c]))
+                       for c in range(copies)) * per_expert
         algo = distinct * per_expert + T * H * 4 * 2 + T * E * 4
         out[f"T{T}"] = {"us": round(t * 1e6, 2), "distinct_experts": round(distinct, 1),
                         "bytes": int(algo), "GB_s": round(algo / t / 1e9, 1),
-                        "frac_hbm": round(algo / t / 1e9 / HBM_PEAK_GBS, 4)}
+                        "frac_hbm": round(algo / t / 1e9 / HBM_PEAK_GBS, 4),
+                        "rotation_bytes": int(rotation), "graph_launches": max(steps, span)}
     out["workload"] = "Qwen3-MoE expert layer H=2048, E=128, F=768, top-8, gate/up Q4_K, down Q6_K"
     out["weight_layout"] = "Q4_K_T / Q6_K_T (16-row tiles; load-time repack of the GGUF expert tensors)"
     del gate, up, down, gv, uv, dv
@@ -387,12 +428,13 @@ def bench_q8_0(torch, J, dev, stream, steps, warmup, keep_host):
         J.read_probe(bufs[cnt[0] % copies], sink, stream=stream)
         cnt[0] += 1
 
-    t = time_graph(torch, one, steps, warmup, stream)
-    tc = time_graph(torch, probe, steps, warmup, stream)
+    t = time_graph(torch, one, steps, warmup, stream, span=copies)
+    tc = time_graph(torch, probe, steps, warmup, stream, span=copies)
     algo = nbytes + J.row_bytes(J.ACT_Q8, n_in) + 4 * n_out
     res = {"workload": "Q8_0 x Q8_0 GEMV 4096x4096, batch 1", "us": round(t * 1e6, 3),
            "GB_s": round(algo / t / 1e9, 1), "bytes": algo, "frac_hbm": round(algo / t / 1e9 / HBM_PEAK_GBS, 4),
-           "read_ceiling_us": round(tc * 1e6, 3), "gemv_over_ceiling": round(tc / t, 4)}
+           "read_ceiling_us": round(tc * 1e6, 3), "gemv_over_ceiling": round(tc / t, 4),
+           "rotation_bytes": copies * nbytes}
     host = (bufs[0].cpu().numpy(), xq.cpu().numpy()) if keep_host else None
     del bufs, views
     return res, host
@@ -493,14 +535,18 @@ def bench_forward_model(J, reps):
 
 
 def cpu_forward_baseline(O, prompt, max_tokens, budget_s=3.0):
-    """The oracle's ForwardModel evaluate (scalar C restatement, one thread) on the same workload."""
-    f = O.ForwardModel(fnv1a(FWD_PROMPT_TEXT), FWD_VOCAB, FWD_CTX, threads=1)
+    """The oracle's ForwardModel evaluate (scalar C restatement) on the same workload, every
+    projection, attention and head split over a persistent pool of all host cores (the
+    reference's WorkerPool under its Spin profile)."""
+    threads = len(os.sched_getaffinity(0))
+    f = O.ForwardModel(fnv1a(FWD_PROMPT_TEXT), FWD_VOCAB, FWD_CTX, threads=threads)
     reps, toks, t0 = 0, None, time.perf_counter()
     while time.perf_counter() - t0 < budget_s or reps == 0:
         toks = f.evaluate(prompt, max_tokens)
         reps += 1
     el = time.perf_counter() - t0
-    return reps * max_tokens / el, reps, el, toks
+    f.close()
+    return reps * max_tokens / el, reps, el, toks, threads
 
 
 def measured_traffic():
@@ -513,6 +559,126 @@ def measured_traffic():
             return json.load(f)["q4k_gemv_traffic_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def kernel_short_name(name):
+    """`void ns::kern<T, 4>(args...)` -> `ns::kern<T, 4>` (the name up to its argument list)."""
+    name = name.strip()
+    if name.startswith("_Z"):  # a mangled name (some counter rows carry one)
+        import subprocess
+        try:
+            name = subprocess.run(["c++filt", name], capture_output=True, text=True, check=True).stdout.strip()
+        except (OSError, subprocess.CalledProcessError):
+            return name
+    name = name.replace("(anonymous namespace)", "{anon}")
+    if name.startswith("void "):
+        name = name[5:]
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return name[:i]
+    return name
+
+
+def read_profile_csv(dirs, suffix):
+    """Rows of every rocprofv3 `*<suffix>` CSV file under `dirs` (recursive)."""
+    import csv
+    import glob
+    rows = []
+    for d in dirs:
+        for path in sorted(glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True)):
+            with open(path, newline="") as f:
+                rows += list(csv.DictReader(f))
+    return rows
+
+
+def summarize_profiles(dirs, match, step_end, last, out):
+    """Markdown summary of rocprofv3 CSV output (--output-format csv) under `dirs`: per (kernel,
+    grid) launch counts and mean / median duration from *_kernel_trace.csv; per (kernel, grid)
+    counter means per dispatch (and per wave for SQ_INSTS_* given SQ_WAVES) from
+    *_counter_collection.csv; with `step_end`, the wall time and kernel-time sum of the last
+    `last` steps, a step being the dispatches after one `step_end` kernel up to the next."""
+    import numpy as np
+    w = out.write
+    trace = [r for r in read_profile_csv(dirs, "_kernel_trace.csv") if match in r["Kernel_Name"]]
+    if trace:
+        groups = {}
+        for r in trace:
+            grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            groups.setdefault((kernel_short_name(r["Kernel_Name"]), grid), []).append(dur)
+        w("| kernel | grid | launches | mean ns | median ns | min ns | total us |\n|---|---|---|---|---|---|---|\n")
+        for (k, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+            a = np.array(d, np.float64)
+            w(f"| `{k}` | {grid} | {len(d)} | {a.mean():.0f} | {np.median(a):.0f} | {a.min():.0f} | "
+              f"{a.sum() / 1e3:.1f} |\n")
+        if step_end:
+            ev = sorted(trace, key=lambda r: int(r["Start_Timestamp"]))
+            ends = [i for i, r in enumerate(ev) if step_end in r["Kernel_Name"]]
+            walls, sums, counts = [], [], []
+            for a, b in zip(ends[:-1], ends[1:]):
+                step = ev[a + 1:b + 1]
+                walls.append(int(step[-1]["End_Timestamp"]) - int(step[0]["Start_Timestamp"]))
+                sums.append(sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in step))
+                counts.append(len(step))
+            walls, sums, counts = walls[-last:], sums[-last:], counts[-last:]
+            if walls:
+                w(f"\nLast {len(walls)} steps ending in `{step_end}` ({counts[-1]} kernels per step): wall "
+                  f"mean {np.mean(walls) / 1e3:.1f} us (min {min(walls) / 1e3:.1f}, max {max(walls) / 1e3:.1f}); "
+                  f"kernel-time sum mean {np.mean(sums) / 1e3:.1f} us\n")
+    pmc = [r for r in read_profile_csv(dirs, "_counter_collection.csv") if match in r["Kernel_Name"]]
+    if pmc:
+        vals = {}
+        for r in pmc:
+            key = (kernel_short_name(r["Kernel_Name"]), int(r["Grid_Size"]))
+            vals.setdefault(key, {}).setdefault(r["Counter_Name"], {}).setdefault(r["Dispatch_Id"], 0.0)
+            vals[key][r["Counter_Name"]][r["Dispatch_Id"]] += float(r["Counter_Value"])
+        names = sorted({c for v in vals.values() for c in v})
+        w("\n| kernel | grid | dispatches | " + " | ".join(names) + " |\n|---|---|---|" + "---|" * len(names) + "\n")
+        for (k, grid), cs in sorted(vals.items()):
+            disp = max(len(d) for d in cs.values())
+            means = {c: float(np.mean(list(d.values()))) for c, d in cs.items()}
+            waves = means.get("SQ_WAVES")
+            cells = []
+            for c in names:
+                if c not in means:
+                    cells.append("")
+                elif c.startswith("SQ_INSTS_") and waves:
+                    cells.append(f"{means[c] / waves:.1f}/wave")
+                else:
+                    cells.append(f"{means[c]:.4g}")
+            w(f"| `{k}` | {grid} | {disp} | " + " | ".join(cells) + " |\n")
+
+
+def traffic_summary(fetch_dirs, write_dirs, match, copy_bytes):
+    """HBM bytes per dispatch from a FETCH_SIZE pass and a WRITE_SIZE pass (KiB per dispatch),
+    each scaled by what the counter reads for the torch copy of `copy_bytes` bytes in the same
+    run (--copy-probe): {(kernel, grid): (fetch KiB, write KiB, bytes)} and the two factors."""
+    import numpy as np
+
+    def means(dirs, counter):
+        out, copy = {}, []
+        for r in read_profile_csv(dirs, "_counter_collection.csv"):
+            if r["Counter_Name"] != counter:
+                continue
+            v = float(r["Counter_Value"])
+            if "copyBuffer" in r["Kernel_Name"] and v * 1024 > 0.4 * copy_bytes:
+                copy.append(v)
+            elif match in r["Kernel_Name"]:
+                out.setdefault((kernel_short_name(r["Kernel_Name"]), int(r["Grid_Size"])), []).append(v)
+        return {k: float(np.mean(v)) for k, v in out.items()}, (float(np.mean(copy)) if copy else None)
+
+    fetch, fcopy = means(fetch_dirs, "FETCH_SIZE")
+    write, wcopy = means(write_dirs, "WRITE_SIZE")
+    if not fcopy or not wcopy:
+        raise SystemExit("traffic: no copy-probe dispatch in the counter passes (run bench.py with --copy-probe)")
+    ff, wf = copy_bytes / (fcopy * 1024), copy_bytes / (wcopy * 1024)
+    res = {k: (fetch[k], write.get(k, 0.0), fetch[k] * 1024 * ff + write.get(k, 0.0) * 1024 * wf) for k in fetch}
+    return res, ff, wf
 
 
 def main():
@@ -528,7 +694,25 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=50)
     ap.add_argument("--copy-probe", type=float, default=0.0,
                     help="also run one device copy of this many MB (PMC byte-counter calibration)")
+    ap.add_argument("--summarize", nargs="+", metavar="DIR",
+                    help="print a markdown summary of rocprofv3 CSV output under DIR(s) and exit (no GPU)")
+    ap.add_argument("--match", default="jero", help="--summarize: kernels whose name contains this")
+    ap.add_argument("--step-end", default=None, help="--summarize: kernel that ends one step (per-step wall times)")
+    ap.add_argument("--last", type=int, default=16, help="--summarize: steps to average with --step-end")
+    ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print HBM bytes per dispatch from a FETCH_SIZE and a WRITE_SIZE pass run with "
+                         "--copy-probe MB (give the same MB) and exit (no GPU)")
     args = ap.parse_args()
+    if args.summarize:
+        summarize_profiles(args.summarize, args.match, args.step_end, args.last, sys.stdout)
+        return
+    if args.traffic:
+        res, ff, wf = traffic_summary([args.traffic[0]], [args.traffic[1]], args.match, args.copy_probe * 1e6)
+        print(f"copy probe factors: fetch {ff:.4f}, write {wf:.4f}")
+        print("| kernel | grid | FETCH_SIZE KiB | WRITE_SIZE KiB | bytes |\n|---|---|---|---|---|")
+        for (k, grid), (fk, wk, b) in sorted(res.items()):
+            print(f"| `{k}` | {grid} | {fk:.1f} | {wk:.1f} | {b:.0f} |")
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
@@ -551,9 +735,10 @@ def main():
 
     # ---- Q4_K decode shapes: the GGUF tensors re-laid out once at load (Q4_K -> Q4_K_R, the
     # layout the decode step runs on); the GGUF-layout kernel is timed too (per_shape_gguf)
-    bufs, xqs, ys, views, raw_views, algo = [], [], [], [], [], []
+    bufs, xqs, ys, views, raw_views, algo, wbytes = [], [], [], [], [], [], []
     for i, (n_in, n_out) in enumerate(SHAPES):
         nbytes = J.row_bytes(J.Q4_K, n_in) * n_out
+        wbytes.append(nbytes)
         copies = max(2, int(np.ceil(ROTATE_BYTES / nbytes)))
         buf = synth_weights(torch, J, J.Q4_K, n_in, n_out, copies, dev, 1000 + i)
         bufs.append(buf)
@@ -574,11 +759,12 @@ def main():
             J.matvec(vv[c % len(vv)], xqs[i], ys[i], stream=stream)
         counter[0] += 1
 
-    t_step = time_graph(torch, step, args.steps, args.warmup, stream)
+    max_copies = max(len(v) for v in views)
+    t_step = time_graph(torch, step, args.steps, args.warmup, stream, span=max_copies)
     step_bytes = sum(algo)
     value = step_bytes / t_step / 1e9
-    max_copies = max(len(v) for v in views)
     step_dist = time_graph_dist(torch, step, max_copies, 21, stream)
+    rotation = {f"{n_in}x{n_out}": len(views[i]) * wbytes[i] for i, (n_in, n_out) in enumerate(SHAPES)}
 
     # per-shape kernel averages (same method, one shape per graph), planar and GGUF layouts
     per_shape, per_shape_gguf = {}, {}
@@ -591,10 +777,12 @@ def main():
                 J.matvec(vv[cnt[0] % len(vv)], xqs[i], ys[i], stream=stream)
                 cnt[0] += 1
 
-            t = time_graph(torch, one, args.steps, args.warmup, stream)
+            nc = len(vlist[i])
+            t = time_graph(torch, one, args.steps, args.warmup, stream, span=nc)
             table[f"{n_in}x{n_out}"] = {"us": round(t * 1e6, 3), "GB_s": round(algo[i] / t / 1e9, 1),
-                                        "bytes": algo[i],
-                                        "dist": time_graph_dist(torch, one, len(vlist[i]), 21, stream)}
+                                        "bytes": algo[i], "rotation_bytes": nc * wbytes[i],
+                                        "graph_launches": max(args.steps, nc),
+                                        "dist": time_graph_dist(torch, one, nc, 21, stream)}
     # pure-read ceiling: one launch per shape reading the same rotated buffers and nothing else
     sink = torch.zeros(256, dtype=torch.int32, device=dev)
     ceiling = {}
@@ -606,7 +794,7 @@ def main():
             J.read_probe(vv[cnt[0] % len(vv)].data, sink, stream=stream)
             cnt[0] += 1
 
-        tc = time_graph(torch, probe, args.steps, args.warmup, stream)
+        tc = time_graph(torch, probe, args.steps, args.warmup, stream, span=len(views[i]))
         key = f"{n_in}x{n_out}"
         per_shape[key]["read_ceiling_us"] = round(tc * 1e6, 3)
         per_shape[key]["gemv_over_ceiling"] = round(tc * 1e6 / per_shape[key]["us"], 4)
@@ -632,7 +820,7 @@ def main():
     th = time_graph(torch, head_step, max(10, args.steps // 10), 2, stream)
     h_algo = hbytes + J.row_bytes(J.Q8_K, n_in) + 4 * n_out
     head = {"shape": "Q6_K 4096x151936 (planar device layout)", "us": round(th * 1e6, 2), "GB_s": round(h_algo / th / 1e9, 1),
-            "frac_hbm": round(h_algo / th / 1e9 / HBM_PEAK_GBS, 4)}
+            "frac_hbm": round(h_algo / th / 1e9 / HBM_PEAK_GBS, 4), "rotation_bytes": 2 * hbytes}
     del hv
 
     # ---- Q8_0 4096x4096 (the reference's CPU-runnable case; extra)
@@ -679,10 +867,11 @@ def main():
         fwd, (fprompt, fmax) = bench_forward_model(J, 20)
         if not args.no_cpu:
             import pyoracle as O
-            tps, reps, el, ctoks = cpu_forward_baseline(O, fprompt, fmax)
-            fwd["cpu_baseline"] = {"value": round(tps, 1), "unit": "generated tok/s (prefill included)", "cores": 1,
-                                   "kind": "port", "tokens_equal": ctoks == fwd["tokens"],
-                                   "sample": f"{reps} full evaluate runs, {el:.1f} s, scalar C restatement"}
+            tps, reps, el, ctoks, fthreads = cpu_forward_baseline(O, fprompt, fmax)
+            fwd["cpu_baseline"] = {"value": round(tps, 1), "unit": "generated tok/s (prefill included)",
+                                   "cores": fthreads, "kind": "port", "tokens_equal": ctoks == fwd["tokens"],
+                                   "sample": f"{reps} full evaluate runs, {el:.1f} s, scalar C restatement, "
+                                             f"persistent spin pool of {fthreads} threads"}
             fwd["evaluate_tok_s"] = round(fmax / (fwd["evaluate_wall_ms"] * 1e-3), 1)
 
     # ---- full decode step (extra)
@@ -715,7 +904,8 @@ def main():
         "data": "synthetic: random-init Q4_K weights (uniform payload, N(0,0.02)-scale fields), N(0,1) activations",
         "config": {"workload": "Q4_K x Q8_K decode GEMV, batch 1: 4096->4096, 4096->12288, 12288->4096",
                    "weight_layout": "Q4_K_R (GGUF Q4_K bytes re-laid out once at load by jero_hip_repack)",
-                   "rotated_weight_bytes": int(ROTATE_BYTES), "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+                   "rotation_bytes": rotation,
+                   "graph_steps": max(args.steps, max_copies), "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,

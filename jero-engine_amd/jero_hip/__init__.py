@@ -714,6 +714,12 @@ class DecodeModel:
         (jero_hip_model_prefill): leaves the last token's logits, the greedy next token and
         position pos0 + len(tokens)."""
         import numpy as np
+        if hasattr(tokens, "data_ptr"):  # an int32 torch tensor in host memory (pinned: the upload is asynchronous)
+            import torch
+            if tokens.dtype != torch.int32 or tokens.device.type != "cpu" or not tokens.is_contiguous():
+                raise K3Error(21, "prefill: a tensor of tokens must be contiguous int32 in host memory")
+            check(lib().jero_hip_model_prefill(self.h, tokens.data_ptr(), tokens.numel(), pos0, _stream(stream)))
+            return
         t = np.ascontiguousarray(np.asarray(tokens, np.int32))
         check(lib().jero_hip_model_prefill(self.h, t.ctypes.data, t.size, pos0, _stream(stream)))
 

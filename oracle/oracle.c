@@ -11,6 +11,7 @@
 
 #include <math.h>
 #include <pthread.h>
+#include <sched.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -1029,14 +1030,19 @@ typedef struct jo_fwd_mat {
   int8_t *rows;
 } jo_fwd_mat;
 
+typedef struct fwd_pool fwd_pool;
+
 struct jo_fwd_model {
   uint64_t seed;
   int64_t vocab, cap, len;
   int threads;
+  fwd_pool *pool; /* threads - 1 persistent workers (NULL: one thread) */
   jo_fwd_mat w[JO_FWD_LAYERS][6];
   jo_fwd_mat head;
   int8_t *kc[JO_FWD_LAYERS], *vc[JO_FWD_LAYERS];
 };
+
+static void fwd_pool_free(fwd_pool *p);
 
 static int fwd_mat(jo_fwd_mat *m, uint64_t seed, int64_t n, int64_t k, int shift) {
   const int64_t n_pad = (n + 7) / 8 * 8;
@@ -1057,6 +1063,7 @@ void jo_fwd_free(jo_fwd_model *f) {
     free(f->vc[l]);
   }
   free(f->head.rows);
+  fwd_pool_free(f->pool);
   free(f);
 }
 
@@ -1093,7 +1100,6 @@ jo_fwd_model *jo_fwd_new(uint64_t seed, int64_t vocab, int64_t max_positions) {
 int64_t jo_fwd_head_rows(const jo_fwd_model *f) { return f->head.n; }
 int64_t jo_fwd_len(const jo_fwd_model *f) { return f->len; }
 void jo_fwd_reset(jo_fwd_model *f) { f->len = 0; }
-void jo_fwd_set_threads(jo_fwd_model *f, int threads) { f->threads = threads < 1 ? 1 : threads; }
 
 const int8_t *jo_fwd_weight(const jo_fwd_model *f, int layer, int which, int64_t *n, int64_t *k, int *shift) {
   const jo_fwd_mat *m;
@@ -1112,39 +1118,103 @@ void jo_fwd_embed(uint64_t seed, uint32_t token, int8_t *out) {
   for (int i = 0; i < JO_FWD_DIM; i++) out[i] = (int8_t)(out[i] * 8);
 }
 
-/* Splits [0, n) into `threads` contiguous ranges run on their own threads (the checker's speed
- * only: every range computes the same integers as a single pass). */
+/* Splits [0, n) into contiguous ranges, one per thread (the checker's speed only: every range
+ * computes the same integers as a single pass).  The threads are a persistent pool whose workers
+ * spin on a job generation counter, as the reference's WorkerPool does under its default Spin
+ * coordination profile (src/affinity.rs:1991-2030); a worker that finds no job for a while yields
+ * its core between polls. */
 typedef void (*fwd_range_fn)(void *ctx, int64_t lo, int64_t hi);
+
+#define FWD_MAX_THREADS 64
+
 typedef struct {
+  fwd_pool *pool;
+  int idx; /* range idx + 1 of a job (range 0 is the caller's) */
+} fwd_worker_arg;
+
+struct fwd_pool {
+  int workers;
+  pthread_t th[FWD_MAX_THREADS - 1];
+  fwd_worker_arg args[FWD_MAX_THREADS - 1];
+  uint64_t gen;  /* incremented (release) once a job's fields are written */
+  int stop;
+  int remaining; /* workers that have not finished the current job */
   fwd_range_fn fn;
   void *ctx;
-  int64_t lo, hi;
-} fwd_job;
+  int64_t n;
+  int parts;
+};
 
-static void *fwd_worker(void *p) {
-  fwd_job *j = (fwd_job *)p;
-  j->fn(j->ctx, j->lo, j->hi);
-  return NULL;
+static void fwd_range_of(int64_t n, int parts, int part, int64_t *lo, int64_t *hi) {
+  const int64_t chunk = (n + parts - 1) / parts;
+  *lo = part * chunk < n ? part * chunk : n;
+  *hi = (part + 1) * chunk < n ? (part + 1) * chunk : n;
 }
 
-static void fwd_par(int threads, int64_t n, fwd_range_fn fn, void *ctx) {
-  if (threads > 64) threads = 64;
-  if (threads > n) threads = (int)n;
-  if (threads <= 1) {
+static void *fwd_pool_worker(void *arg) {
+  fwd_worker_arg *a = (fwd_worker_arg *)arg;
+  fwd_pool *p = a->pool;
+  uint64_t seen = 0;
+  for (;;) {
+    uint64_t g;
+    long idle = 0;
+    while ((g = __atomic_load_n(&p->gen, __ATOMIC_ACQUIRE)) == seen) {
+      if (__atomic_load_n(&p->stop, __ATOMIC_ACQUIRE)) return NULL;
+      if (++idle > (1L << 16)) sched_yield();
+    }
+    seen = g;
+    if (a->idx < p->parts) {
+      int64_t lo, hi;
+      fwd_range_of(p->n, p->parts, a->idx, &lo, &hi);
+      if (lo < hi) p->fn(p->ctx, lo, hi);
+    }
+    __atomic_sub_fetch(&p->remaining, 1, __ATOMIC_RELEASE);
+  }
+}
+
+static void fwd_pool_free(fwd_pool *p) {
+  if (!p) return;
+  __atomic_store_n(&p->stop, 1, __ATOMIC_RELEASE);
+  for (int t = 0; t < p->workers; t++) pthread_join(p->th[t], NULL);
+  free(p);
+}
+
+static fwd_pool *fwd_pool_new(int threads) {
+  fwd_pool *p = (fwd_pool *)calloc(1, sizeof *p);
+  if (!p) return NULL;
+  for (int t = 0; t < threads - 1; t++) {
+    p->args[t].pool = p;
+    p->args[t].idx = t + 1;
+    if (pthread_create(&p->th[t], NULL, fwd_pool_worker, &p->args[t])) break;
+    p->workers++;
+  }
+  return p;
+}
+
+void jo_fwd_set_threads(jo_fwd_model *f, int threads) {
+  if (threads < 1) threads = 1;
+  if (threads > FWD_MAX_THREADS) threads = FWD_MAX_THREADS;
+  fwd_pool_free(f->pool);
+  f->pool = threads > 1 ? fwd_pool_new(threads) : NULL;
+  f->threads = f->pool ? f->pool->workers + 1 : 1;
+}
+
+static void fwd_par(const jo_fwd_model *f, int64_t n, fwd_range_fn fn, void *ctx) {
+  fwd_pool *p = f->pool;
+  int parts = p ? p->workers + 1 : 1;
+  if (parts > n) parts = (int)n;
+  if (parts <= 1) {
     fn(ctx, 0, n);
     return;
   }
-  pthread_t th[64];
-  fwd_job jobs[64];
-  const int64_t chunk = (n + threads - 1) / threads;
-  for (int t = 0; t < threads; t++) {
-    jobs[t].fn = fn, jobs[t].ctx = ctx;
-    jobs[t].lo = t * chunk < n ? t * chunk : n;
-    jobs[t].hi = (t + 1) * chunk < n ? (t + 1) * chunk : n;
+  p->fn = fn, p->ctx = ctx, p->n = n, p->parts = parts;
+  __atomic_store_n(&p->remaining, p->workers, __ATOMIC_RELAXED);
+  __atomic_add_fetch(&p->gen, 1, __ATOMIC_RELEASE);
+  int64_t lo, hi;
+  fwd_range_of(n, parts, 0, &lo, &hi);
+  fn(ctx, lo, hi);
+  while (__atomic_load_n(&p->remaining, __ATOMIC_ACQUIRE) != 0) {
   }
-  for (int t = 1; t < threads; t++) pthread_create(&th[t], NULL, fwd_worker, &jobs[t]);
-  fwd_worker(&jobs[0]);
-  for (int t = 1; t < threads; t++) pthread_join(th[t], NULL);
 }
 
 typedef struct {
@@ -1178,10 +1248,10 @@ static void fwd_att_range(void *p, int64_t lo, int64_t hi) {
   jo_fwd_attention(c->q + lo * JO_FWD_DIM, c->kc, c->vc, hi - lo, c->start_pos + lo, c->out + lo * JO_FWD_DIM);
 }
 
-static void fwd_proj(const jo_fwd_mat *w, const int8_t *x, int64_t m, int relu, int32_t *raw, int8_t *out,
-                     int threads) {
+static void fwd_proj(const jo_fwd_model *f, const jo_fwd_mat *w, const int8_t *x, int64_t m, int relu, int32_t *raw,
+                     int8_t *out) {
   fwd_gemm_ctx c = {x, w->rows, m, w->n, w->k, raw};
-  fwd_par(threads, w->n, fwd_gemm_range, &c);
+  fwd_par(f, w->n, fwd_gemm_range, &c);
   fwd_requant(raw, m * w->n, w->shift, relu, out);
 }
 
@@ -1199,23 +1269,22 @@ int jo_fwd_forward(jo_fwd_model *f, const uint32_t *tokens, int64_t m, int64_t s
     for (int64_t r = 0; r < m; r++) jo_fwd_embed(f->seed, tokens[r], x + r * D);
     for (int l = 0; l < JO_FWD_LAYERS; l++) {
       const jo_fwd_mat *W = f->w[l];
-      const int T = f->threads;
       jo_fwd_rmsnorm(x, m, h);
-      fwd_proj(&W[0], h, m, 0, raw, q, T);
-      fwd_proj(&W[1], h, m, 0, raw, f->kc[l] + start_pos * D, T);
-      fwd_proj(&W[2], h, m, 0, raw, f->vc[l] + start_pos * D, T);
+      fwd_proj(f, &W[0], h, m, 0, raw, q);
+      fwd_proj(f, &W[1], h, m, 0, raw, f->kc[l] + start_pos * D);
+      fwd_proj(f, &W[2], h, m, 0, raw, f->vc[l] + start_pos * D);
       fwd_att_ctx ac = {q, f->kc[l], f->vc[l], start_pos, a};
-      fwd_par(T, m, fwd_att_range, &ac);
-      fwd_proj(&W[3], a, m, 0, raw, o, T);
+      fwd_par(f, m, fwd_att_range, &ac);
+      fwd_proj(f, &W[3], a, m, 0, raw, o);
       fwd_sat_add(x, o, m * D);
       jo_fwd_rmsnorm(x, m, h);
-      fwd_proj(&W[4], h, m, 1, raw, up, T);
-      fwd_proj(&W[5], up, m, 0, raw, o, T);
+      fwd_proj(f, &W[4], h, m, 1, raw, up);
+      fwd_proj(f, &W[5], up, m, 0, raw, o);
       fwd_sat_add(x, o, m * D);
     }
     jo_fwd_rmsnorm(x + (m - 1) * D, 1, h);
     fwd_gemm_ctx hc = {h, f->head.rows, 1, f->head.n, D, logits};
-    fwd_par(f->threads, f->head.n, fwd_gemm_range, &hc);
+    fwd_par(f, f->head.n, fwd_gemm_range, &hc);
     f->len = start_pos + m;
   }
   free(x), free(h), free(q), free(a), free(o), free(up), free(raw);

@@ -214,6 +214,23 @@ def test_prompt_forward_equals_token_by_token():
     assert (c.forward(prompt[3:], 3) == whole).all()
 
 
+@pytest.mark.parametrize("threads", [2, 5, 16])
+def test_pooled_threads_equal_one_thread(threads):
+    """The persistent worker pool splits every projection, the attention rows and the head over
+    `threads` ranges (more threads than rows of a 3-token prompt's attention included): prompt
+    logits, decode logits and a 40-token evaluate equal the one-thread run's."""
+    seed, prompt = fnv1a("hello world"), [104, 101, 108]
+    one = O.ForwardModel(seed, 256, 64)
+    many = O.ForwardModel(seed, 256, 64, threads=threads)
+    assert (one.forward(prompt, 0) == many.forward(prompt, 0)).all()
+    for i, t in enumerate([7, 255, 0]):
+        assert (one.forward([t], 3 + i) == many.forward([t], 3 + i)).all()
+    one.reset(), many.reset()
+    assert one.evaluate(list(b"hello world"), 40) == many.evaluate(list(b"hello world"), 40)
+    many.close()
+    many.close()
+
+
 def test_forward_rejects_wrong_start_and_capacity():
     f = O.ForwardModel(1, 16, 4)
     with pytest.raises(ValueError):

@@ -86,6 +86,14 @@ int jero_hip_weights_release_all(void);
  * its own bytes.  The owner of an mmaped weight file calls it before unmapping (munmap of
  * LockedModelWeights, src/weights.rs:729-734); jero_hip_gguf_close does so itself. */
 int jero_hip_weights_release(const void *host, size_t nbytes);
+/* n host tensors of nbytes each (per-expert tensors blk.L.ffn_*_exps.{e}.weight, looked up by
+ * slice_or_lookup_expert, src/qwen_deepseek.rs:729-746) registered as ONE stacked device tensor,
+ * expert e at *dev_out + e * nbytes, the layout of a stacked [n_in, rows, n] tensor, so the routed
+ * expert kernels take them as they take a stacked tensor.  Registering the same n tensors again
+ * returns the same address; each host range is then also registered on its own (lookup and
+ * release find it).  Some of the ranges registered otherwise (apart, or in another stack):
+ * TensorBoundsError. */
+int jero_hip_weights_register_stacked(const void *const *hosts, size_t nbytes, int64_t n, const void **dev_out);
 /* Waits for the work enqueued on `stream`. */
 int jero_hip_sync(void *stream);
 
@@ -288,6 +296,43 @@ int jero_hip_moe_ffn(const float *x_dev, const float *router_logits_dev, int64_t
                      int64_t hidden, int64_t ffn, float *y_dev, int32_t *sel_idx_dev, float *sel_w_dev,
                      void *workspace_dev, size_t workspace_bytes, void *stream);
 size_t jero_hip_moe_workspace_bytes(int64_t n_tokens, int64_t n_experts, int top_k, int64_t hidden, int64_t ffn);
+/* jero_hip_moe_ffn with y_dev holding, on entry, values the routed sum is added onto, in the
+ * reference's order: y[t][i] = ((y[t][i] + w[t][0] * e_0[i]) + w[t][1] * e_1[i]) + ...  -- the
+ * shared expert's output that dispatch_qwen3_moe_ffn adds first (src/qwen_deepseek.rs:860-871,
+ * 925-936).  Same arguments, limits and workspace as jero_hip_moe_ffn. */
+int jero_hip_moe_ffn_acc(const float *x_dev, const float *router_logits_dev, int64_t n_tokens, int64_t n_experts,
+                         int top_k, int gate_quant, const void *gate_dev, size_t gate_bytes, int up_quant,
+                         const void *up_dev, size_t up_bytes, int down_quant, const void *down_dev,
+                         size_t down_bytes, int64_t hidden, int64_t ffn, float *y_dev, int32_t *sel_idx_dev,
+                         float *sel_w_dev, void *workspace_dev, size_t workspace_bytes, void *stream);
+
+/* A weight tensor as the reference's ModelWeights hands it out: format, device bytes (NULL: the
+ * model has no such tensor) and TensorView::num_elements. */
+typedef struct jero_hip_tensor {
+  int quant;
+  const void *dev;
+  size_t bytes;
+  int64_t n_elements;
+} jero_hip_tensor;
+
+/* The dense SwiGLU FFNs of dispatch_qwen3_moe_ffn on one token row x_dev[hidden] (16-byte aligned):
+ *   r = down(silu(gate x) * up x),   y_dev[hidden] = (accumulate ? y_dev : 0) + r.
+ * JERO_FFN_SHARED_EXPERT -- run_single_swiglu_expert (src/qwen_deepseek.rs:748-771) of the shared
+ *   expert blk.L.ffn_{gate,up,down}_shexp (:860-871): F = gate.n_elements / hidden when that
+ *   divides, else max(ffn, 4); gate and up give their first F rows of hidden, down H rows of F
+ *   (matvec_any); each tensor must be present and hold them (TensorBoundsError).
+ * JERO_FFN_DENSE -- run_dense_swiglu_ffn (:696-727), the layer's FFN when it has no router (:873-880):
+ *   F = max(ffn, 4); each of blk.L.ffn_{gate,up,down} is project_or_deterministic_slice
+ *   (src/gemma.rs:841-860): its GEMV when present with exactly out_len * in_len elements, else
+ *   in[i % in_len] * scale (gate 0.5, up 0.25, down 0.125).
+ * Formats: those of jero_hip_vec_dot.  Workspace: jero_hip_swiglu_ffn_workspace_bytes(hidden, F)
+ * bytes with F as above, 256-byte aligned (NULL: library-owned, calls must not overlap on one
+ * device). */
+enum { JERO_FFN_SHARED_EXPERT = 0, JERO_FFN_DENSE = 1 };
+int jero_hip_swiglu_ffn(int mode, const float *x_dev, int64_t hidden, int64_t ffn, const jero_hip_tensor *gate,
+                        const jero_hip_tensor *up, const jero_hip_tensor *down, int accumulate, float *y_dev,
+                        void *workspace_dev, size_t workspace_bytes, void *stream);
+size_t jero_hip_swiglu_ffn_workspace_bytes(int64_t hidden, int64_t ffn);
 /* Debug view of a workspace after jero_hip_moe_ffn returned and its stream was synchronized, for
  * the per-expert parity tests (no counterpart in the reference, where the expert's SwiGLU
  * vector is a local of run_single_swiglu_expert, src/qwen_deepseek.rs:748-771): *act_dev holds the

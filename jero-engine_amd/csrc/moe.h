@@ -46,6 +46,8 @@ struct MoeArgs {
   const void* down;  // stacked [E][hidden rows][ffn]
   int64_t hidden, ffn;
   float* y;          // [T][hidden]
+  bool accumulate;   // y += the routed sum (y holds the values to add onto) instead of y =, in the
+                     // reference's order: ((y + w0 e0) + w1 e1) + ...
   int32_t* sel_idx;  // [T][k]
   float* sel_w;      // [T][k]
   // workspace carve-out (set by launch_moe)

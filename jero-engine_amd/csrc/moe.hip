@@ -585,7 +585,7 @@ __global__ void __launch_bounds__(256) moe1_down_kernel(const uint8_t* __restric
                                                         int U, int H, const float* __restrict__ act, int ffn,
                                                         int64_t aq_rb, int k, const int32_t* __restrict__ sel_idx,
                                                         const float* __restrict__ sel_w, float* __restrict__ y, int RW,
-                                                        int upg) {
+                                                        int upg, int accumulate) {
   using Ut = Unit<F>;
   using W = typename Ut::W;
   constexpr int G = kWave / LPR;
@@ -653,9 +653,10 @@ __global__ void __launch_bounds__(256) moe1_down_kernel(const uint8_t* __restric
   }
   lds_barrier();
   for (int r = threadIdx.x; r < RW; r += 256) {
-    float acc = 0.f;
+    if (hbase + r >= H) continue;
+    float acc = accumulate ? y[hbase + r] : 0.f;
     for (int j = 0; j < k; j++) acc += s_w[j] * s_dot[j * RW + r];
-    if (hbase + r < H) y[hbase + r] = acc;
+    y[hbase + r] = acc;
   }
 }
 
@@ -1089,11 +1090,11 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU)) moe_mfma_kernel(cons
 
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ yd, const float* __restrict__ w,
                                                           const int32_t* __restrict__ inv, int T, int k, int H,
-                                                          float* __restrict__ y) {
+                                                          float* __restrict__ y, int accumulate) {
   const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= int64_t(T) * H) return;
   const int t = int(idx / H), h = int(idx % H);
-  float acc = 0.f;
+  float acc = accumulate ? y[idx] : 0.f;
   for (int j = 0; j < k; j++) acc += w[t * k + j] * yd[int64_t(inv[t * k + j]) * H + h];
   y[idx] = acc;
 }
@@ -1193,7 +1194,7 @@ void down1_one(const MoeArgs& a, hipStream_t s) {
   const size_t lds = size_t(a.top_k) * size_t(arb) + sizeof(float) * size_t(a.top_k) * RW;
   hipLaunchKernelGGL((moe1_down_kernel<F, LPR, UPL>), dim3(unsigned((a.hidden + RW - 1) / RW)), dim3(256), lds, s,
                      static_cast<const uint8_t*>(a.down), a.E * a.hidden, row_bytes(F, a.ffn), U, int(a.hidden), a.act,
-                     int(a.ffn), arb, a.top_k, a.sel_idx, a.sel_w, a.y, RW, upg);
+                     int(a.ffn), arb, a.top_k, a.sel_idx, a.sel_w, a.y, RW, upg, int(a.accumulate));
 }
 
 template <int F>
@@ -1396,7 +1397,7 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   }
   const int64_t total = a.T * a.hidden;
   hipLaunchKernelGGL(moe_combine_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, a.yd, a.sel_w, L.inv,
-                     int(a.T), a.top_k, int(a.hidden), a.y);
+                     int(a.T), a.top_k, int(a.hidden), a.y, int(a.accumulate));
   return check_launch("moe combine");
 }
 
@@ -1427,13 +1428,14 @@ int check_moe_args(const MoeArgs& a, size_t gate_bytes, size_t up_bytes, size_t 
 
 using namespace jero;
 
-extern "C" int jero_hip_moe_ffn(const float* x_dev, const float* router_logits_dev, int64_t n_tokens,
-                                int64_t n_experts, int top_k, int gate_quant, const void* gate_dev, size_t gate_bytes,
-                                int up_quant, const void* up_dev, size_t up_bytes, int down_quant,
-                                const void* down_dev, size_t down_bytes, int64_t hidden, int64_t ffn, float* y_dev,
-                                int32_t* sel_idx_dev, float* sel_w_dev, void* workspace_dev, size_t workspace_bytes,
-                                void* stream) {
+namespace {
+int moe_entry(const float* x_dev, const float* router_logits_dev, int64_t n_tokens, int64_t n_experts, int top_k,
+              int gate_quant, const void* gate_dev, size_t gate_bytes, int up_quant, const void* up_dev,
+              size_t up_bytes, int down_quant, const void* down_dev, size_t down_bytes, int64_t hidden, int64_t ffn,
+              float* y_dev, int32_t* sel_idx_dev, float* sel_w_dev, void* workspace_dev, size_t workspace_bytes,
+              void* stream, bool accumulate) {
   MoeArgs a{};
+  a.accumulate = accumulate;
   a.x = x_dev;
   a.logits = router_logits_dev;
   a.T = n_tokens;
@@ -1465,6 +1467,29 @@ extern "C" int jero_hip_moe_ffn(const float* x_dev, const float* router_logits_d
     if (rc) return rc;
   }
   return launch_moe(a, ws, static_cast<hipStream_t>(stream));
+}
+}  // namespace
+
+extern "C" int jero_hip_moe_ffn(const float* x_dev, const float* router_logits_dev, int64_t n_tokens,
+                                int64_t n_experts, int top_k, int gate_quant, const void* gate_dev, size_t gate_bytes,
+                                int up_quant, const void* up_dev, size_t up_bytes, int down_quant,
+                                const void* down_dev, size_t down_bytes, int64_t hidden, int64_t ffn, float* y_dev,
+                                int32_t* sel_idx_dev, float* sel_w_dev, void* workspace_dev, size_t workspace_bytes,
+                                void* stream) {
+  return moe_entry(x_dev, router_logits_dev, n_tokens, n_experts, top_k, gate_quant, gate_dev, gate_bytes, up_quant,
+                   up_dev, up_bytes, down_quant, down_dev, down_bytes, hidden, ffn, y_dev, sel_idx_dev, sel_w_dev,
+                   workspace_dev, workspace_bytes, stream, false);
+}
+
+extern "C" int jero_hip_moe_ffn_acc(const float* x_dev, const float* router_logits_dev, int64_t n_tokens,
+                                    int64_t n_experts, int top_k, int gate_quant, const void* gate_dev,
+                                    size_t gate_bytes, int up_quant, const void* up_dev, size_t up_bytes,
+                                    int down_quant, const void* down_dev, size_t down_bytes, int64_t hidden,
+                                    int64_t ffn, float* y_dev, int32_t* sel_idx_dev, float* sel_w_dev,
+                                    void* workspace_dev, size_t workspace_bytes, void* stream) {
+  return moe_entry(x_dev, router_logits_dev, n_tokens, n_experts, top_k, gate_quant, gate_dev, gate_bytes, up_quant,
+                   up_dev, up_bytes, down_quant, down_dev, down_bytes, hidden, ffn, y_dev, sel_idx_dev, sel_w_dev,
+                   workspace_dev, workspace_bytes, stream, true);
 }
 
 extern "C" int jero_hip_moe_trace_view(void* workspace_dev, int64_t n_tokens, int64_t n_experts, int top_k,

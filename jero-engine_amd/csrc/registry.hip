@@ -8,6 +8,7 @@
 // matching device address, so a binding can hand the GPU the view the reference's callers pass.
 #include <algorithm>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -22,7 +23,15 @@ struct Region {
   size_t nbytes;
   int device;
   void* dev;
+  // the device allocation holding dev: one per tensor, or one per stack of tensors
+  // (jero_hip_weights_register_stacked), freed with the last region that holds it
+  std::shared_ptr<void> mem;
 };
+
+std::shared_ptr<void> own(void* dev) {
+  return std::shared_ptr<void>(dev, [](void* q) { (void)hipFree(q); });
+}
+
 
 std::mutex g_mu;
 // keyed by (device, host start address)
@@ -40,6 +49,17 @@ const Region* find_region(int device, uintptr_t p, size_t n, uintptr_t* start) {
   if (p < s || p + n > s + it->second.nbytes) return nullptr;
   *start = s;
   return &it->second;
+}
+
+// Does [p, p + n) overlap a registered range of `device`?  (g_mu held)
+bool overlaps(int device, uintptr_t p, size_t n) {
+  auto it = g_regions.lower_bound({device, p});
+  if (it != g_regions.end() && it->first.first == device && it->first.second < p + n) return true;
+  if (it != g_regions.begin()) {
+    auto pr = std::prev(it);
+    if (pr->first.first == device && pr->first.second + pr->second.nbytes > p) return true;
+  }
+  return false;
 }
 
 }  // namespace
@@ -61,14 +81,8 @@ extern "C" int jero_hip_weights_register(const void* host, size_t nbytes, const 
     return JERO_OK;
   }
   // a new range must not overlap an existing one partially
-  auto it = g_regions.lower_bound({device, p});
-  if (it != g_regions.end() && it->first.first == device && it->first.second < p + nbytes)
+  if (overlaps(device, p, nbytes))
     return fail(JERO_ERR_TENSOR_BOUNDS, "weights_register: range overlaps a registered tensor");
-  if (it != g_regions.begin()) {
-    auto pr = std::prev(it);
-    if (pr->first.first == device && pr->first.second + pr->second.nbytes > p)
-      return fail(JERO_ERR_TENSOR_BOUNDS, "weights_register: range overlaps a registered tensor");
-  }
   void* dev = nullptr;
   if (hipMalloc(&dev, nbytes) != hipSuccess) {
     (void)hipGetLastError();
@@ -80,7 +94,68 @@ extern "C" int jero_hip_weights_register(const void* host, size_t nbytes, const 
     (void)hipFree(dev);
     return rc;
   }
-  g_regions[{device, p}] = Region{nbytes, device, dev};
+  g_regions[{device, p}] = Region{nbytes, device, dev, own(dev)};
+  *dev_out = dev;
+  return JERO_OK;
+}
+
+extern "C" int jero_hip_weights_register_stacked(const void* const* hosts, size_t nbytes, int64_t n,
+                                                 const void** dev_out) {
+  if (!hosts || !dev_out) return fail(JERO_ERR_INVALID_ARGUMENT, "weights_register_stacked: null pointer");
+  if (nbytes == 0 || n <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "weights_register_stacked: empty tensors");
+  for (int64_t e = 0; e < n; e++)
+    if (!hosts[e]) return fail(JERO_ERR_INVALID_ARGUMENT, "weights_register_stacked: null tensor " + std::to_string(e));
+  int device = 0;
+  int rc = current_device(&device);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lock(g_mu);
+  // registered before as this same stack: every tensor at its place in one allocation
+  int64_t found = 0;
+  const Region* first = nullptr;
+  bool same_stack = true;
+  for (int64_t e = 0; e < n; e++) {
+    const uintptr_t p = reinterpret_cast<uintptr_t>(hosts[e]);
+    uintptr_t start = 0;
+    const Region* r = find_region(device, p, nbytes, &start);
+    if (!r) {
+      if (overlaps(device, p, nbytes)) same_stack = false;
+      continue;
+    }
+    found++;
+    if (e == 0) first = r;
+    if (start != p || r->nbytes != nbytes || !first ||
+        static_cast<const uint8_t*>(r->dev) != static_cast<const uint8_t*>(first->dev) + size_t(e) * nbytes ||
+        r->mem != first->mem)
+      same_stack = false;
+  }
+  if (found == n && same_stack) {
+    *dev_out = first->dev;
+    return JERO_OK;
+  }
+  if (found > 0 || !same_stack)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "weights_register_stacked: some of the tensors are registered apart");
+  for (int64_t e = 0; e < n; e++)
+    for (int64_t f = e + 1; f < n; f++) {
+      const uintptr_t a = reinterpret_cast<uintptr_t>(hosts[e]), b = reinterpret_cast<uintptr_t>(hosts[f]);
+      if (a < b + nbytes && b < a + nbytes)
+        return fail(JERO_ERR_TENSOR_BOUNDS, "weights_register_stacked: tensors " + std::to_string(e) + " and " +
+                                                std::to_string(f) + " overlap");
+    }
+  void* dev = nullptr;
+  if (hipMalloc(&dev, nbytes * size_t(n)) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(JERO_ERR_INSUFFICIENT_MEMORY, "weights_register_stacked: no device memory for " +
+                                                  std::to_string(nbytes * size_t(n)) + " bytes");
+  }
+  std::shared_ptr<void> mem = own(dev);
+  for (int64_t e = 0; e < n; e++) {
+    rc = check_hip(hipMemcpy(static_cast<uint8_t*>(dev) + size_t(e) * nbytes, hosts[e], nbytes, hipMemcpyHostToDevice),
+                   "weights_register_stacked upload");
+    if (rc) return rc;  // mem frees the allocation
+  }
+  for (int64_t e = 0; e < n; e++)
+    g_regions[{device, reinterpret_cast<uintptr_t>(hosts[e])}] =
+        Region{nbytes, device, static_cast<uint8_t*>(dev) + size_t(e) * nbytes, mem};
   *dev_out = dev;
   return JERO_OK;
 }
@@ -108,8 +183,7 @@ extern "C" int jero_hip_weights_release_all(void) {
   std::lock_guard<std::mutex> lock(g_mu);
   for (auto it = g_regions.begin(); it != g_regions.end();) {
     if (it->first.first == device) {
-      (void)hipFree(it->second.dev);
-      it = g_regions.erase(it);
+      it = g_regions.erase(it);  // the last region of an allocation frees it
     } else {
       ++it;
     }
@@ -140,8 +214,7 @@ extern "C" int jero_hip_weights_release(const void* host, size_t nbytes) {
       if (rc) return rc;
       synced.push_back(d);
     }
-    (void)hipFree(it->second.dev);
-    it = g_regions.erase(it);
+    it = g_regions.erase(it);  // the last region of an allocation frees it
   }
   return JERO_OK;
 }

@@ -78,6 +78,11 @@ _SIGS = {
     "jero_hip_moe_ffn": (_I32, [_P, _P, _I64, _I64, _I32, _I32, _P, _SZ, _I32, _P, _SZ, _I32, _P, _SZ, _I64, _I64,
                                 _P, _P, _P, _P, _SZ, _P]),
     "jero_hip_moe_workspace_bytes": (_SZ, [_I64, _I64, _I32, _I64, _I64]),
+    "jero_hip_moe_ffn_acc": (_I32, [_P, _P, _I64, _I64, _I32, _I32, _P, _SZ, _I32, _P, _SZ, _I32, _P, _SZ, _I64,
+                                    _I64, _P, _P, _P, _P, _SZ, _P]),
+    "jero_hip_swiglu_ffn": (_I32, [_I32, _P, _I64, _I64, _P, _P, _P, _I32, _P, _P, _SZ, _P]),
+    "jero_hip_swiglu_ffn_workspace_bytes": (_SZ, [_I64, _I64]),
+    "jero_hip_weights_register_stacked": (_I32, [C.POINTER(_P), _SZ, _I64, C.POINTER(_P)]),
     "jero_hip_moe_trace_view": (_I32, [_P, _I64, _I64, _I32, _I64, _I64, C.POINTER(_P), C.POINTER(_P),
                                        C.POINTER(C.c_int)]),
     "jero_hip_model_create": (_I32, [_P, C.POINTER(_P)]),
@@ -476,10 +481,12 @@ def gqa_causal_attention_f32(out, q, k, v, n_heads_q, n_heads_kv, head_dim, seq_
     return out
 
 
-def dispatch_qwen3_moe_ffn(out, norm_ffn_in, router_logits, top_k, gate, up, down, workspace=None, stream=None):
-    """dispatch_qwen3_moe_ffn (src/qwen_deepseek.rs:847-951) from router logits.
-    gate/up/down: stacked TensorViews with shape [n_in, rows_per_expert, n_experts].
-    Returns (sel_idx [T, k] int32, sel_w [T, k] f32) device tensors."""
+def dispatch_qwen3_moe_ffn(out, norm_ffn_in, router_logits, top_k, gate, up, down, workspace=None, stream=None,
+                           accumulate=False):
+    """The routed experts of dispatch_qwen3_moe_ffn (src/qwen_deepseek.rs:847-951) from router
+    logits.  gate/up/down: stacked TensorViews with shape [n_in, rows_per_expert, n_experts].
+    accumulate: the routed sum is added onto out (jero_hip_moe_ffn_acc).  Returns (sel_idx [T, k]
+    int32, sel_w [T, k] f32) device tensors."""
     import torch
     T = router_logits.shape[0] if router_logits.dim() == 2 else 1
     E = router_logits.shape[-1]
@@ -489,11 +496,122 @@ def dispatch_qwen3_moe_ffn(out, norm_ffn_in, router_logits, top_k, gate, up, dow
     if workspace is None:
         need = lib().jero_hip_moe_workspace_bytes(T, E, top_k, hidden, ffn)
         workspace = torch.empty(need, dtype=torch.uint8, device=out.device)
-    check(lib().jero_hip_moe_ffn(_ptr(norm_ffn_in), _ptr(router_logits), T, E, top_k, gate.quant, _ptr(gate.data),
-                                 gate.nbytes(), up.quant, _ptr(up.data), up.nbytes(), down.quant, _ptr(down.data),
-                                 down.nbytes(), hidden, ffn, _ptr(out), _ptr(sel_idx), _ptr(sel_w), _ptr(workspace),
-                                 workspace.numel(), _stream(stream)))
+    fn = lib().jero_hip_moe_ffn_acc if accumulate else lib().jero_hip_moe_ffn
+    check(fn(_ptr(norm_ffn_in), _ptr(router_logits), T, E, top_k, gate.quant, _ptr(gate.data), gate.nbytes(),
+             up.quant, _ptr(up.data), up.nbytes(), down.quant, _ptr(down.data), down.nbytes(), hidden, ffn, _ptr(out),
+             _ptr(sel_idx), _ptr(sel_w), _ptr(workspace), workspace.numel(), _stream(stream)))
     return sel_idx, sel_w
+
+
+class HipTensor(C.Structure):
+    """jero_hip_tensor."""
+    _fields_ = [("quant", C.c_int), ("dev", C.c_void_p), ("bytes", C.c_size_t), ("n_elements", C.c_int64)]
+
+    @classmethod
+    def of(cls, view):
+        if view is None:
+            return cls(0, None, 0, 0)
+        n = 1
+        for d in view.shape:
+            n *= d
+        return cls(view.quant, view.data.data_ptr(), view.nbytes(), n)
+
+
+FFN_SHARED_EXPERT, FFN_DENSE = 0, 1
+
+
+def swiglu_ffn(mode, out, x, ffn, gate, up, down, accumulate=False, workspace=None, stream=None):
+    """run_single_swiglu_expert (mode FFN_SHARED_EXPERT, src/qwen_deepseek.rs:748-771) or
+    run_dense_swiglu_ffn (FFN_DENSE, :696-727, each projection project_or_deterministic_slice; a
+    None tensor is absent) on one token row x [hidden]: out = (out if accumulate else 0) + r
+    (jero_hip_swiglu_ffn)."""
+    H = x.numel()
+    ws_p, ws_n = (_ptr(workspace), workspace.numel()) if workspace is not None else (None, 0)
+    g, u, d = HipTensor.of(gate), HipTensor.of(up), HipTensor.of(down)
+    check(lib().jero_hip_swiglu_ffn(mode, _ptr(x), H, ffn, C.byref(g), C.byref(u), C.byref(d), int(bool(accumulate)),
+                                    _ptr(out), ws_p, ws_n, _stream(stream)))
+    return out
+
+
+def weights_register_stacked(host_arrays):
+    """Device address of n equal-sized host buffers registered as one stacked tensor
+    (jero_hip_weights_register_stacked)."""
+    n = len(host_arrays)
+    if n == 0 or any(a.nbytes != host_arrays[0].nbytes for a in host_arrays):
+        raise K3Error(14, "weights_register_stacked: the tensors of a stack must all have the same size")
+    arr = (_P * n)(*[a.ctypes.data for a in host_arrays])
+    dev = _P()
+    check(lib().jero_hip_weights_register_stacked(arr, host_arrays[0].nbytes, n, C.byref(dev)))
+    return dev.value
+
+
+def _n_elements(view):
+    n = 1
+    for d in view.shape:
+        n *= d
+    return n
+
+
+def moe_layer(out, norm_ffn_in, layer, num_experts, top_k, expert_ffn_dim, use_shared_expert, weights, stream=None):
+    """dispatch_qwen3_moe_ffn (src/qwen_deepseek.rs:847-951) in full, on the device: `weights` maps
+    GGUF names to device TensorViews (ModelWeights).  out [hidden] = the shared expert (when
+    use_shared_expert and all three ffn_*_shexp tensors are present) + the routed experts over the
+    router ffn_gate_inp, or + the dense FFN (ffn_gate / ffn_up / ffn_down, each
+    project_or_deterministic_slice) when there is no router or no expert to route to.  The routed
+    experts come from the stacked ffn_*_exps tensors (3-D) or, for each of gate / up / down
+    apart, the per-expert tensors ffn_*_exps.{e} of every expert (slice_or_lookup_expert,
+    :729-746), stacked on the device.  Returns the selection [(expert, weight)] (empty after the
+    dense FFN).  Refused (CapabilityMismatch): exp_probs_b routing bias (DeepSeek's biased
+    selection, :909-918) and per-expert tensors missing for some experts (the reference would
+    skip those experts)."""
+    import torch
+    H = norm_ffn_in.numel()
+    name = lambda t: f"blk.{layer}.{t}.weight"
+    if f"blk.{layer}.exp_probs_b.bias" in weights:
+        raise K3Error(10, f"layer {layer}: exp_probs_b routing bias (biased expert selection) is not supported on the "
+                          "device")
+    shexp = [weights.get(name(t)) for t in ("ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp")]
+    shared = bool(use_shared_expert) and all(t is not None for t in shexp)
+    if shared:
+        swiglu_ffn(FFN_SHARED_EXPERT, out, norm_ffn_in, expert_ffn_dim, *shexp, accumulate=False, stream=stream)
+    router = weights.get(name("ffn_gate_inp"))
+    if num_experts == 0 or top_k == 0 or router is None:
+        swiglu_ffn(FFN_DENSE, out, norm_ffn_in, expert_ffn_dim, weights.get(name("ffn_gate")),
+                   weights.get(name("ffn_up")), weights.get(name("ffn_down")), accumulate=shared, stream=stream)
+        return []
+    re = _n_elements(router)
+    eff = min(re // H, num_experts) if re > 0 and re % H == 0 else num_experts
+    logits = torch.empty((1, eff), dtype=torch.float32, device=out.device)
+    matvec_any(logits.view(-1), router, norm_ffn_in, stream=stream)
+
+    def experts(kind):
+        st = weights.get(f"blk.{layer}.ffn_{kind}_exps.weight")
+        if st is not None and len(st.shape) == 3:
+            return TensorView(st.name, st.quant, [st.shape[0], _n_elements(st) // (st.shape[0] * eff), eff], st.data)
+        per = [weights.get(f"blk.{layer}.ffn_{kind}_exps.{e}.weight") for e in range(eff)]
+        missing = [e for e, t in enumerate(per) if t is None]
+        if missing:
+            raise K3Error(10, f"layer {layer}: no ffn_{kind}_exps tensor for experts {missing[:8]} (the device runs "
+                              "only complete expert sets)")
+        q, nb = per[0].quant, per[0].nbytes()
+        if any(t.quant != q or t.nbytes() != nb for t in per):
+            raise K3Error(10, f"layer {layer}: per-expert ffn_{kind}_exps tensors differ in format or size")
+        return TensorView(f"blk.{layer}.ffn_{kind}_exps", q, [per[0].shape[0], _n_elements(per[0]) // per[0].shape[0],
+                                                            eff], torch.cat([t.data.reshape(-1) for t in per]))
+
+    g, u, d = experts("gate"), experts("up"), experts("down")
+    k = min(top_k, eff)
+    g_rows = g.shape[1]  # run_single_swiglu_expert's eff_ffn of an expert slice (:757-762)
+    x2 = norm_ffn_in.view(1, H)
+    sel_idx, sel_w = dispatch_qwen3_moe_ffn(out.view(1, H), x2, logits, k, TensorView(g.name, g.quant, [H, g_rows, eff], g.data),
+                                            TensorView(u.name, u.quant, [H, g_rows, eff], u.data),
+                                            TensorView(d.name, d.quant, [g_rows, H, eff], d.data), stream=stream,
+                                            accumulate=shared)
+    if stream is not None:
+        stream.synchronize()
+    else:
+        torch.cuda.synchronize()
+    return list(zip(sel_idx.view(-1).tolist(), sel_w.view(-1).tolist()))
 
 
 def moe_workspace(n_tokens, n_experts, top_k, hidden, ffn, device="cuda"):

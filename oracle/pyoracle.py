@@ -236,6 +236,86 @@ def moe_ffn(router_logits, top_k, gate, up, down, gq, uq, dq, hidden, ffn, x, th
     return y, si, sw
 
 
+# ---- the whole MoE layer: dispatch_qwen3_moe_ffn (src/qwen_deepseek.rs:847-951) ----
+# `weights` maps GGUF names to (quant, data, dims): data the tensor's bytes (uint8) or f32 values,
+# dims its GGUF shape ([n_in, rows] or [n_in, rows, n_experts]).
+
+def _n_el(dims):
+    n = 1
+    for d in dims:
+        n *= d
+    return n
+
+
+def proj_or_det(w, x, out_len, scale):
+    """project_or_deterministic_slice (src/gemma.rs:841-860): the GEMV when the tensor is present
+    with exactly out_len * len(x) elements, else out[i] = x[i % len(x)] * scale."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if w is not None and _n_el(w[2]) == out_len * x.size:
+        return vec_dot(w[0], w[1], x.size, out_len, x)
+    return (x[np.arange(out_len) % x.size] * np.float32(scale)).astype(np.float32)
+
+
+def single_swiglu_expert(g, u, d, x, expert_ffn_dim):
+    """run_single_swiglu_expert (src/qwen_deepseek.rs:748-771): eff_ffn from the gate's element
+    count, then matvec_any of gate and up over x, SwiGLU, matvec_any of down."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    H, ge = x.size, _n_el(g[2])
+    F = ge // H if ge > 0 and ge % H == 0 else max(expert_ffn_dim, 4)
+    act = swiglu(vec_dot(g[0], g[1], H, F, x), vec_dot(u[0], u[1], H, F, x))
+    return vec_dot(d[0], d[1], F, H, act)
+
+
+def dense_swiglu_ffn(weights, layer, expert_ffn_dim, x):
+    """run_dense_swiglu_ffn (src/qwen_deepseek.rs:696-727)."""
+    F = max(expert_ffn_dim, 4)
+    name = lambda t: f"blk.{layer}.{t}.weight"
+    g = proj_or_det(weights.get(name("ffn_gate")), x, F, 0.5)
+    u = proj_or_det(weights.get(name("ffn_up")), x, F, 0.25)
+    return proj_or_det(weights.get(name("ffn_down")), swiglu(g, u), len(x), 0.125)
+
+
+def _expert_slice(weights, stacked, indexed, e, n):
+    """slice_or_lookup_expert (src/qwen_deepseek.rs:729-746): expert e of n equal parts of a 3-D
+    stacked tensor, else the per-expert tensor, else None."""
+    st = weights.get(stacked)
+    if st is not None and len(st[2]) == 3:
+        per = len(st[1]) // n
+        rows = _n_el(st[2]) // n // st[2][0]
+        return (st[0], st[1][e * per:(e + 1) * per], [st[2][0], rows])
+    return weights.get(indexed)
+
+
+def moe_layer(x, layer, num_experts, top_k, expert_ffn_dim, use_shared_expert, weights):
+    """dispatch_qwen3_moe_ffn (src/qwen_deepseek.rs:847-951) without the exp_probs_b bias: returns
+    (out [hidden] f32, [(expert, weight)])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    H = x.size
+    name = lambda t: f"blk.{layer}.{t}.weight"
+    out = np.zeros(H, np.float32)
+    sh = [weights.get(name(t)) for t in ("ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp")]
+    if use_shared_expert and all(t is not None for t in sh):
+        out += single_swiglu_expert(*sh, x, expert_ffn_dim)
+    router = weights.get(name("ffn_gate_inp"))
+    if num_experts == 0 or top_k == 0 or router is None:
+        out += dense_swiglu_ffn(weights, layer, expert_ffn_dim, x)
+        return out, []
+    re = _n_el(router[2])
+    eff = min(re // H, num_experts) if re > 0 and re % H == 0 else num_experts
+    logits = vec_dot(router[0], router[1], H, eff, x)
+    sel = select_top_k(logits, top_k, True)
+    ran = False
+    for e, w in sel:
+        parts = [_expert_slice(weights, f"blk.{layer}.ffn_{k}_exps.weight", f"blk.{layer}.ffn_{k}_exps.{e}.weight", e,
+                               eff) for k in ("gate", "up", "down")]
+        if all(p is not None for p in parts):
+            out += np.float32(w) * single_swiglu_expert(*parts, x, expert_ffn_dim)
+            ran = True
+    if not ran:
+        out += dense_swiglu_ffn(weights, layer, expert_ffn_dim, x)
+    return out, sel
+
+
 # ---- decode model (jo_model / jo_layer structs) ----
 
 class JoTensor(C.Structure):

@@ -662,3 +662,137 @@ def test_absent_and_nonfinite_norms_in_the_decode_step():
     tied = {k: v for k, v in t.items() if k != "output.weight"}
     tied_explicit = dict(tied, **{"output.weight": t["token_embd.weight"]})
     assert np.array_equal(run(tied), run(tied_explicit))
+
+
+def _one_hot_f32(rows, k, col_of, scale=1.0):
+    """F32 weight rows [rows][k] whose row i is scale * e_{col_of(i)}: an exact selection."""
+    w = np.zeros((rows, k), np.float32)
+    for i in range(rows):
+        w[i, col_of(i)] = scale
+    return w.reshape(-1)
+
+
+def _silu64(v):
+    return v / (1.0 + math.exp(-v))
+
+
+def test_single_swiglu_expert_selection_closed_form():
+    """run_single_swiglu_expert over one-hot F32 rows: out[h] = silu(x[p(r(h))]) * 2 x[q(r(h))],
+    with F taken from the gate's element count (48 rows, not the expert_ffn_dim of 5); distinct
+    permutations p, q, r make a swapped operand, a transposed matrix or a wrong F show."""
+    H, F = 32, 48
+    p = lambda i: (5 * i + 3) % H
+    q = lambda i: (7 * i + 1) % H
+    r = lambda h: (11 * h + 2) % F
+    x = rand_act(H, 3)
+    g = (O.F32, _one_hot_f32(F, H, p), [H, F])
+    u = (O.F32, _one_hot_f32(F, H, q, 2.0), [H, F])
+    d = (O.F32, _one_hot_f32(H, F, r), [F, H])
+    out = O.single_swiglu_expert(g, u, d, x, 5)
+    want = np.array([_silu64(float(x[p(r(h))])) * 2.0 * float(x[q(r(h))]) for h in range(H)])
+    np.testing.assert_allclose(out, want, rtol=2e-6, atol=1e-7)
+
+
+def test_dense_swiglu_ffn_deterministic_closed_form():
+    """run_dense_swiglu_ffn with no tensors, and with tensors of the wrong element count (both take
+    project_or_deterministic_slice's fallback): act[i] = silu(0.5 x[i % H]) * 0.25 x[i % H] over
+    F = max(ffn, 4), out[h] = act[h % F] * 0.125; a present tensor of the right size is used."""
+    H = 16
+    x = rand_act(H, 4)
+    for ffn, F in ((24, 24), (2, 4)):
+        act = [_silu64(0.5 * float(x[i % H])) * 0.25 * float(x[i % H]) for i in range(F)]
+        want = np.array([act[h % F] * 0.125 for h in range(H)])
+        out = O.dense_swiglu_ffn({}, 0, ffn, x)
+        np.testing.assert_allclose(out, want, rtol=2e-6, atol=1e-8)
+        bad = {"blk.0.ffn_gate.weight": (O.F32, np.ones(H * F + H, np.float32), [H, F + 1]),
+               "blk.0.ffn_down.weight": (O.F32, np.ones(7, np.float32), [7, 1])}
+        np.testing.assert_array_equal(O.dense_swiglu_ffn(bad, 0, ffn, x), out)
+    # a right-sized gate is used: one-hot rows picking x[(3 i) % H]
+    F = 24
+    good = {"blk.0.ffn_gate.weight": (O.F32, _one_hot_f32(F, H, lambda i: (3 * i) % H), [H, F])}
+    act = [_silu64(float(x[(3 * i) % H])) * 0.25 * float(x[i % H]) for i in range(F)]
+    want = np.array([act[h % F] * 0.125 for h in range(H)])
+    np.testing.assert_allclose(O.dense_swiglu_ffn(good, 0, F, x), want, rtol=2e-6, atol=1e-8)
+
+
+def _moe_weights(H, F, E, seed, shared=True, quant=O.Q4_K):
+    rng = np.random.default_rng(seed)
+    w = {}
+    g = rand_weights(quant, E * F, H, seed)
+    u = rand_weights(quant, E * F, H, seed + 1)
+    d = rand_weights(quant, E * H, F, seed + 2)
+    w["blk.0.ffn_gate_exps.weight"] = (quant, g, [H, F, E])
+    w["blk.0.ffn_up_exps.weight"] = (quant, u, [H, F, E])
+    w["blk.0.ffn_down_exps.weight"] = (quant, d, [F, H, E])
+    w["blk.0.ffn_gate_inp.weight"] = (O.F32, (rng.standard_normal(E * H) * 0.05).astype(np.float32), [H, E])
+    if shared:
+        w["blk.0.ffn_gate_shexp.weight"] = (quant, rand_weights(quant, F, H, seed + 5), [H, F])
+        w["blk.0.ffn_up_shexp.weight"] = (quant, rand_weights(quant, F, H, seed + 6), [H, F])
+        w["blk.0.ffn_down_shexp.weight"] = (quant, rand_weights(quant, H, F, seed + 7), [F, H])
+    return w
+
+
+def test_moe_layer_shared_expert_equal_to_every_routed_expert():
+    """With every routed expert and the shared expert the same tensors e, the layer is
+    (1 + sum of the normalised selection weights) * e(x) = 2 e(x); without the shared expert, e(x);
+    the selection is select_top_k of the router's logits (F32 rows with router row j = c_j e_0,
+    so logits c_j x[0])."""
+    H, F, E, k = 256, 256, 6, 3
+    x = rand_act(H, 9)
+    one = rand_weights(O.Q4_K, F, H, 11), rand_weights(O.Q4_K, F, H, 12), rand_weights(O.Q4_K, H, F, 13)
+    c = np.array([0.5, -2.0, 3.0, 1.0, 3.0, -1.0], np.float32)
+    router = np.zeros((E, H), np.float32)
+    router[:, 0] = c
+    w = {"blk.0.ffn_gate_inp.weight": (O.F32, router.reshape(-1), [H, E]),
+         "blk.0.ffn_gate_exps.weight": (O.Q4_K, np.tile(one[0], E), [H, F, E]),
+         "blk.0.ffn_up_exps.weight": (O.Q4_K, np.tile(one[1], E), [H, F, E]),
+         "blk.0.ffn_down_exps.weight": (O.Q4_K, np.tile(one[2], E), [F, H, E]),
+         "blk.0.ffn_gate_shexp.weight": (O.Q4_K, one[0], [H, F]),
+         "blk.0.ffn_up_shexp.weight": (O.Q4_K, one[1], [H, F]),
+         "blk.0.ffn_down_shexp.weight": (O.Q4_K, one[2], [F, H])}
+    e = O.single_swiglu_expert(w["blk.0.ffn_gate_shexp.weight"], w["blk.0.ffn_up_shexp.weight"],
+                               w["blk.0.ffn_down_shexp.weight"], x, F)
+    out, sel = O.moe_layer(x, 0, E, k, F, True, w)
+    assert [i for i, _ in sel] == [int(i) for i in np.lexsort((np.arange(E), -(c * x[0])))[:k]]
+    np.testing.assert_allclose(out, 2 * e, rtol=1e-6, atol=1e-6 * float(np.abs(e).max()))
+    out1, _ = O.moe_layer(x, 0, E, k, F, False, w)
+    np.testing.assert_allclose(out1, e, rtol=1e-6, atol=1e-6 * float(np.abs(e).max()))
+
+
+def test_moe_layer_indexed_experts_and_fallbacks():
+    """Per-expert tensors ffn_*_exps.{e} give the same bits as the stacked tensors; an expert
+    whose tensors are missing is skipped (the others keep their weights); with every selected
+    expert missing the dense FFN runs; with no router, shared expert + dense FFN."""
+    H, F, E, k = 256, 256, 5, 2
+    x = rand_act(H, 21)
+    w = _moe_weights(H, F, E, 30)
+    out, sel = O.moe_layer(x, 0, E, k, F, True, w)
+    ix = dict(w)
+    for kind in ("gate", "up", "down"):
+        q, data, dims = ix.pop(f"blk.0.ffn_{kind}_exps.weight")
+        per = len(data) // E
+        for e in range(E):
+            ix[f"blk.0.ffn_{kind}_exps.{e}.weight"] = (q, data[e * per:(e + 1) * per], dims[:2])
+    out_ix, sel_ix = O.moe_layer(x, 0, E, k, F, True, ix)
+    assert sel_ix == sel
+    np.testing.assert_array_equal(out_ix, out)
+    sh = O.single_swiglu_expert(w["blk.0.ffn_gate_shexp.weight"], w["blk.0.ffn_up_shexp.weight"],
+                                w["blk.0.ffn_down_shexp.weight"], x, F)
+    # the second selected expert missing: shared + w0 * e0 only
+    e0, e1 = sel[0][0], sel[1][0]
+    miss = {n: t for n, t in ix.items() if n != f"blk.0.ffn_up_exps.{e1}.weight"}
+    part = lambda e: [ix[f"blk.0.ffn_{kd}_exps.{e}.weight"] for kd in ("gate", "up", "down")]
+    want = np.zeros(H, np.float32)
+    want += sh
+    want += np.float32(sel[0][1]) * O.single_swiglu_expert(*part(e0), x, F)
+    np.testing.assert_array_equal(O.moe_layer(x, 0, E, k, F, True, miss)[0], want)
+    # both missing: shared + dense (deterministic here: no ffn_gate/up/down)
+    miss2 = {n: t for n, t in miss.items() if n != f"blk.0.ffn_down_exps.{e0}.weight"}
+    want = np.zeros(H, np.float32)
+    want += sh
+    want += O.dense_swiglu_ffn({}, 0, F, x)
+    np.testing.assert_array_equal(O.moe_layer(x, 0, E, k, F, True, miss2)[0], want)
+    # no router: shared + dense, no selection
+    nr = {n: t for n, t in w.items() if "gate_inp" not in n}
+    o, s = O.moe_layer(x, 0, E, k, F, True, nr)
+    assert s == [] and np.array_equal(o, want)

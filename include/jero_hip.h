@@ -268,7 +268,10 @@ int jero_hip_repack_experts(int quant, const void *src_dev, size_t src_bytes, in
  * each q head h, kv head h / (n_heads_q / n_heads_kv).  q_dev: [n_heads_q][head_dim] f32 (8-byte
  * aligned);
  * k_dev, v_dev: [seq_len][n_heads_kv * head_dim] of kv_dtype (16-byte aligned); out_dev:
- * [n_heads_q][head_dim] f32.  head_dim in {32, 64, 128}; at most 8 q heads per kv head.
+ * [n_heads_q][head_dim] f32.  head_dim: any even value up to 256 (even_head_dim,
+ * src/qwen_deepseek.rs:58-65, gives the recipes only even ones; 32, 64 and 128 run the head_dim-built
+ * kernels, the rest one q head per workgroup); above 256 or odd: CapabilityMismatch.  Any number of
+ * q heads per kv head.
  * seq_len <= JERO_MAX_ATTENTION_POSITIONS, else ContextLengthExceeded.  Workspace: n_heads_q * ceil(seq_len/64) * (head_dim + 2) floats, 16-byte
  * aligned (NULL: library-owned, calls must not overlap on one device). */
 #define JERO_MAX_ATTENTION_POSITIONS 131072
@@ -288,7 +291,10 @@ int jero_hip_gqa_attention(float *out_dev, const float *q_dev, const void *k_dev
  * GEMMs read fastest) or jero_hip_repack over all their rows (JERO_Q4_K_R / JERO_Q6_K_R); repacked
  * tensors 16-byte aligned.
  * Outputs y_dev [n_tokens][hidden], sel_idx_dev / sel_w_dev [n_tokens][top_k].
- * hidden <= 8192 for the gate/up pairing; top_k <= 16; n_experts <= 1024.  Workspace:
+ * Limits the reference does not have, refused with CapabilityMismatch: hidden <= 8192 (the gate/up
+ * rows' lane pairing), ffn <= 16384 (the down rows'), top_k <= 16 and n_experts <= 1024 (the
+ * routing kernels' per-lane columns); Qwen3-MoE (128 experts, top-8, hidden up to 4096, ffn 768 /
+ * 1536) and DeepSeek-style routers (256 experts, top-8) sit well inside them.  Workspace:
  * jero_hip_moe_workspace_bytes(...) bytes, 256-byte aligned (NULL: library-owned). */
 int jero_hip_moe_ffn(const float *x_dev, const float *router_logits_dev, int64_t n_tokens, int64_t n_experts,
                      int top_k, int gate_quant, const void *gate_dev, size_t gate_bytes, int up_quant,

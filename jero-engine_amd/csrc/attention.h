@@ -49,15 +49,16 @@ int check_attention_shape(int nq, int nkv, int hd, int64_t seq_len);
 int launch_attention(const AttnParams& p, bool fused, float* out, hipStream_t s);
 // Causal attention of n_tok consecutive queries (prefill): token t's q heads at p.q + t *
 // q_stride, attending to the first p.active + t slots of the rings; out row t at out + t *
-// out_stride.  f16 rings at head_dim 64 or 128 with more than one query (attn_flash_ok) run the
-// flash kernel, which needs no workspace; otherwise the split kernels need
+// out_stride.  f16 rings at head_dim 64 or 128, at most 8 q heads per kv head, with more than one
+// query (attn_flash_ok) run the flash kernel, which needs no workspace; otherwise the split kernels need
 // attn_workspace_bytes(nq, hd, p.active + n_tok - 1) * n_tok bytes at p.part_o.  With q8k given
 // (the flash kernel only, attn_flash_q8k_ok: group * hd a multiple of 256) each row's Q8_K
 // blocks are written at q8k + t * row_bytes(Q8_K, nq * hd), and the f32 rows only when out is
 // given.
 int launch_attention_tokens(const AttnParams& p, int n_tok, int64_t q_stride, float* out, int64_t out_stride,
                             hipStream_t s, void* q8k = nullptr);
-bool attn_flash_ok(int kv_dtype, int hd, int n_tok);
+bool attn_flash_ok(int kv_dtype, int hd, int n_tok, int group);
+bool attn_templated(int hd, int group);
 bool attn_flash_q8k_ok(int group, int hd);
 
 }  // namespace jero

@@ -1106,7 +1106,252 @@ __global__ void __launch_bounds__(256) attn_combine_small_kernel(const float* __
   }
 }
 
+// ---------------------------------------------------------------- any even head_dim up to 256
+// gqa_causal_attention_f32 takes any even head_dim (even_head_dim, src/qwen_deepseek.rs:58-65) and
+// any group size; the kernels above are built for head_dim 32 / 64 / 128 and up to 8 (16 on the
+// matrix cores) q heads per kv head.  The others run these two: a split-K partial with a runtime
+// head_dim and one q head per workgroup, and a merge with a runtime head_dim.  Workgroup (split s,
+// q head h, query z) owns slots [64 s, 64 s + 64), 16 per wave; lane l holds dims l, l + 64,
+// l + 128 and l + 192 (those below head_dim), so a slot's score is one whole-wave DPP sum.  Every
+// K / V load of the wave goes out before the first score.  Fused mode: the workgroup normalises and
+// rotates its q head (the RoPE partner of dim d, d ^ 1, sits one lane over) and, holding the new
+// slot, k; the workgroup of the group's first q head appends k and v to the ring.
+constexpr int kGenDims = 4;     // dims per lane: head_dim <= 256
+constexpr int kGenSlots = 16;   // slots per wave
+constexpr int kGenMaxHd = 64 * kGenDims;
+
+template <typename KV, bool FUSED>
+__global__ void __launch_bounds__(kAttnThreads) attn_generic_kernel(AttnParams p) {
+  const int t0 = blockIdx.z;
+  p.q += t0 * p.q_stride;
+  p.active += t0;
+  p.part_o += t0 * p.part_tok;
+  p.part_ml += t0 * p.part_tok_ml;
+  const int hd = p.hd, group = p.group;
+  const int split = blockIdx.x, h = blockIdx.y, kh = h / group;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int S = gridDim.x;
+  const int64_t kvd = int64_t(p.nkv) * hd;
+  constexpr int CH = kGenSlots * (kAttnThreads / kWave);
+  const int p0 = split * CH, w0 = p0 + wv * kGenSlots;
+  __shared__ float s_o[kAttnThreads / kWave][kGenMaxHd];
+  __shared__ float s_m[kAttnThreads / kWave], s_l[kAttnThreads / kWave];
+
+  // small loads first, then every K / V row of the wave (clamped in-bounds; masked below)
+  int64_t pos_now = p.pos;
+  if (p.pos_dev) pos_now = *p.pos_dev;
+  float q[kGenDims], kn[kGenDims], vn[kGenDims], qnw[kGenDims], knw[kGenDims];
+#pragma unroll
+  for (int t = 0; t < kGenDims; t++) {
+    const int d = min(lane + 64 * t, hd - 1);
+    q[t] = p.q[int64_t(h) * hd + d];
+    kn[t] = vn[t] = qnw[t] = knw[t] = 0.f;
+    if constexpr (FUSED) {
+      kn[t] = p.k_new[int64_t(kh) * hd + d];
+      vn[t] = p.v_new[int64_t(kh) * hd + d];
+      qnw[t] = p.q_norm ? p.q_norm[d] : 0.f;
+      knw[t] = p.k_norm ? p.k_norm[d] : 0.f;
+    }
+  }
+  const int bound = p.pos_dev ? int(p.capacity) : p.active;
+  const KV* kb = static_cast<const KV*>(p.k) + int64_t(kh) * hd;
+  const KV* vb = static_cast<const KV*>(p.v) + int64_t(kh) * hd;
+  KV kr[kGenSlots][kGenDims], vr[kGenSlots][kGenDims];
+#pragma unroll
+  for (int i = 0; i < kGenSlots; i++) {
+    const int64_t ps = min(w0 + i, bound - 1);
+#pragma unroll
+    for (int t = 0; t < kGenDims; t++) {
+      const int d = min(lane + 64 * t, hd - 1);
+      kr[i][t] = kb[ps * kvd + d];
+      vr[i][t] = vb[ps * kvd + d];
+    }
+  }
+  int active = p.active, slot = p.slot;
+  if (p.pos_dev) {
+    slot = int(pos_now % p.capacity);
+    active = int(pos_now + 1 < p.capacity ? pos_now + 1 : p.capacity);
+  }
+  float* ml = p.part_ml;
+  if (p0 >= active) {  // empty split: contributes nothing to the merge
+    if (threadIdx.x == 0) {
+      ml[(int64_t(h) * S + split) * 2 + 0] = -INFINITY;
+      ml[(int64_t(h) * S + split) * 2 + 1] = 0.f;
+    }
+    return;
+  }
+  const int p1 = min(p0 + CH, active);
+  const bool has_slot = FUSED && slot >= p0 && slot < p1;
+  if constexpr (FUSED) {
+    // per-head RMSNorm, then RoPE of the pair (2i, 2i + 1) = dims (d & ~1, d | 1)
+    float cs[kGenDims], sn[kGenDims];
+#pragma unroll
+    for (int t = 0; t < kGenDims; t++) {
+      const int i = min(lane + 64 * t, hd - 1) >> 1;
+      if (p.rope_cs) {
+        cs[t] = p.rope_cs[2 * i];
+        sn[t] = p.rope_cs[2 * i + 1];
+      } else {
+        sincosf(rope_angle(i, hd, pos_now, p.theta), &sn[t], &cs[t]);
+      }
+    }
+    auto norm_rope = [&](float (&x)[kGenDims], bool has_norm, const float (&nw)[kGenDims]) {
+      if (has_norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int t = 0; t < kGenDims; t++) ss += lane + 64 * t < hd ? x[t] * x[t] : 0.f;
+        ss = wave_sum_dpp(ss);
+        const float inv = 1.0f / sqrtf(ss / float(hd) + p.eps);
+#pragma unroll
+        for (int t = 0; t < kGenDims; t++) x[t] = x[t] * inv * nw[t];
+      }
+      const bool odd = lane & 1;
+#pragma unroll
+      for (int t = 0; t < kGenDims; t++) {
+        const float other = __shfl_xor(x[t], 1, kWave);
+        const float x0 = odd ? other : x[t], x1 = odd ? x[t] : other;
+        x[t] = odd ? x0 * sn[t] + x1 * cs[t] : x0 * cs[t] - x1 * sn[t];
+      }
+    };
+    norm_rope(q, p.q_norm != nullptr, qnw);
+    if (p.tr_q && split == 0 && wv == 0) {
+#pragma unroll
+      for (int t = 0; t < kGenDims; t++)
+        if (lane + 64 * t < hd) p.tr_q[int64_t(h) * hd + lane + 64 * t] = q[t];
+    }
+    if (has_slot) {
+      norm_rope(kn, p.k_norm != nullptr, knw);
+      if (p.tr_k && h == kh * group && wv == 0) {
+#pragma unroll
+        for (int t = 0; t < kGenDims; t++)
+          if (lane + 64 * t < hd) p.tr_k[int64_t(kh) * hd + lane + 64 * t] = kn[t];
+      }
+      // the ring holds the new k and v as KV values: attend to those
+#pragma unroll
+      for (int t = 0; t < kGenDims; t++) {
+        kn[t] = float(KV(kn[t]));
+        vn[t] = float(KV(vn[t]));
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kGenDims; t++) q[t] = lane + 64 * t < hd ? q[t] * p.scale : 0.f;
+
+  // scores, the wave's softmax over its slots, P V
+  float sc[kGenSlots];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kGenSlots; i++) {
+    const int pos = w0 + i;
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < kGenDims; t++) {
+      float kv = float(kr[i][t]);
+      if constexpr (FUSED) kv = pos == slot ? kn[t] : kv;
+      s += q[t] * kv;
+    }
+    s = wave_sum_dpp(s);
+    sc[i] = pos < p1 ? s : -INFINITY;
+    mx = fmaxf(mx, sc[i]);
+  }
+  float l = 0.f, acc[kGenDims];
+#pragma unroll
+  for (int t = 0; t < kGenDims; t++) acc[t] = 0.f;
+#pragma unroll
+  for (int i = 0; i < kGenSlots; i++) {
+    const int pos = w0 + i;
+    const float e = mx == -INFINITY ? 0.f : exp_fast(sc[i] - mx);
+    l += e;
+#pragma unroll
+    for (int t = 0; t < kGenDims; t++) {
+      float v = float(vr[i][t]);
+      if constexpr (FUSED) v = pos == slot ? vn[t] : v;
+      v = pos < p1 ? v : 0.f;  // a stale slot past the active range may hold anything
+      acc[t] += e * v;
+    }
+  }
+  // fused: the group's first q head's workgroup appends k and v to the ring
+  if constexpr (FUSED) {
+    if (has_slot && h == kh * group && wv == 0) {
+      KV* kw = static_cast<KV*>(p.k_write) + int64_t(slot) * kvd + int64_t(kh) * hd;
+      KV* vw = static_cast<KV*>(p.v_write) + int64_t(slot) * kvd + int64_t(kh) * hd;
+#pragma unroll
+      for (int t = 0; t < kGenDims; t++)
+        if (lane + 64 * t < hd) {
+          kw[lane + 64 * t] = KV(kn[t]);
+          vw[lane + 64 * t] = KV(vn[t]);
+        }
+    }
+  }
+  // merge of the four waves
+#pragma unroll
+  for (int t = 0; t < kGenDims; t++)
+    if (lane + 64 * t < hd) s_o[wv][lane + 64 * t] = acc[t];
+  if (lane == 0) {
+    s_m[wv] = mx;
+    s_l[wv] = l;
+  }
+  __syncthreads();
+  constexpr int NW = kAttnThreads / kWave;
+  for (int d = threadIdx.x; d < hd; d += kAttnThreads) {
+    float M = s_m[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) M = fmaxf(M, s_m[w]);
+    float o = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+      const float wt = s_m[w] == -INFINITY ? 0.f : exp_fast(s_m[w] - M);
+      o += wt * s_o[w][d];
+      L += wt * s_l[w];
+    }
+    const int64_t row = int64_t(h) * S + split;
+    p.part_o[row * hd + d] = o;
+    if (d == 0) {
+      ml[row * 2 + 0] = M;
+      ml[row * 2 + 1] = L;
+    }
+  }
+}
+
+// Merge of the generic kernel's splits, runtime head_dim: one workgroup per (q head, query).
+// Splits with l = 0 (empty) never wrote their rows and are left out by select.
+__global__ void __launch_bounds__(256) attn_combine_generic_kernel(const float* __restrict__ part_o,
+                                                                   const float* __restrict__ part_ml, int S, int hd,
+                                                                   float* __restrict__ out, int64_t tok_o,
+                                                                   int64_t tok_ml, int64_t tok_out) {
+  part_o += blockIdx.y * tok_o;
+  part_ml += blockIdx.y * tok_ml;
+  out += blockIdx.y * tok_out;
+  __shared__ float s_red[4];
+  const int h = blockIdx.x, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const float2* ml = reinterpret_cast<const float2*>(part_ml) + int64_t(h) * S;
+  float m = -INFINITY;
+  for (int s = threadIdx.x; s < S; s += 256) {
+    const float2 e = ml[s];
+    if (e.y > 0.f) m = fmaxf(m, e.x);
+  }
+  m = wave_max_dpp(m);
+  if (lane == 0) s_red[wv] = m;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  const float* po = part_o + int64_t(h) * S * hd;
+  for (int d = threadIdx.x; d < hd; d += 256) {
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < S; s++) {
+      const float2 e = ml[s];
+      const bool live = e.y > 0.f;
+      const float c = live ? exp_fast(e.x - M) : 0.f;
+      num += live ? c * po[int64_t(s) * hd + d] : 0.f;
+      den += c * e.y;
+    }
+    out[int64_t(h) * hd + d] = num / den;
+  }
+}
+
 int attn_splits(int active, int hd) { return (active + attn_chunk(hd) - 1) / attn_chunk(hd); }
+
+// head_dim and group sizes the head_dim-templated kernels take (the rest run the generic pair)
+bool attn_templated(int hd, int group) { return (hd == 32 || hd == 64 || hd == 128) && group <= kMaxGroup; }
 
 size_t attn_workspace_bytes(int nq, int hd, int active) {
   const size_t S = size_t(attn_splits(active, hd));
@@ -1158,6 +1403,21 @@ static int attention_impl(AttnParams p, bool fused, int S, int T, float* out, in
   p.part_tok_ml = T > 1 ? nq * S * 2 : 0;
   p.part_ml = p.part_o + int64_t(T) * nq * S * p.hd;
   p.n_tok = T;
+  if (!attn_templated(p.hd, p.group)) {  // any other even head_dim or group: one q head per workgroup
+    const dim3 grid(S, unsigned(nq), T);
+    if (p.kv_dtype == JERO_KV_F16) {
+      if (fused) hipLaunchKernelGGL((attn_generic_kernel<_Float16, true>), grid, dim3(kAttnThreads), 0, s, p);
+      else hipLaunchKernelGGL((attn_generic_kernel<_Float16, false>), grid, dim3(kAttnThreads), 0, s, p);
+    } else {
+      if (fused) hipLaunchKernelGGL((attn_generic_kernel<float, true>), grid, dim3(kAttnThreads), 0, s, p);
+      else hipLaunchKernelGGL((attn_generic_kernel<float, false>), grid, dim3(kAttnThreads), 0, s, p);
+    }
+    int rc = check_launch("attention partial");
+    if (rc) return rc;
+    hipLaunchKernelGGL(attn_combine_generic_kernel, dim3(unsigned(nq), T), dim3(256), 0, s, p.part_o, p.part_ml, S,
+                       p.hd, out, p.part_tok, p.part_tok_ml, out_stride);
+    return check_launch("attention combine");
+  }
 #define JERO_ATTN_CASE(HDV)                                                                     \
   if (p.hd == HDV) {                                                                            \
     if (p.kv_dtype == JERO_KV_F16 && HDV >= 64) {                                               \
@@ -1186,8 +1446,8 @@ int launch_attention(const AttnParams& p, bool fused, float* out, hipStream_t s)
   return attention_impl(p, fused, attn_splits(p.pos_dev ? int(p.capacity) : p.active, p.hd), 1, out, 0, s);
 }
 
-bool attn_flash_ok(int kv_dtype, int hd, int n_tok) {
-  return kv_dtype == JERO_KV_F16 && (hd == 64 || hd == 128) && n_tok > 1;
+bool attn_flash_ok(int kv_dtype, int hd, int n_tok, int group) {
+  return kv_dtype == JERO_KV_F16 && (hd == 64 || hd == 128) && n_tok > 1 && group <= kMaxGroup;
 }
 
 bool attn_flash_q8k_ok(int group, int hd) { return (hd == 64 || hd == 128) && (group * hd) % 256 == 0; }
@@ -1198,7 +1458,7 @@ int launch_attention_tokens(const AttnParams& p0, int n_tok, int64_t q_stride, f
   AttnParams p = p0;
   p.q_stride = q_stride;
   p.n_tok = n_tok;
-  if (attn_flash_ok(p.kv_dtype, p.hd, n_tok)) {
+  if (attn_flash_ok(p.kv_dtype, p.hd, n_tok, p.group)) {
     if (q8k && !attn_flash_q8k_ok(p.group, p.hd))
       return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: no Q8_K rows for this head group");
     if (!out && !q8k) return fail(JERO_ERR_INVALID_ARGUMENT, "attention: no output");
@@ -1221,11 +1481,9 @@ int check_attention_shape(int nq, int nkv, int hd, int64_t seq_len) {
   if (nq <= 0 || nkv <= 0 || hd <= 0 || seq_len <= 0)
     return fail(JERO_ERR_TENSOR_BOUNDS, "attention: empty heads or sequence");
   if (nq % nkv) return fail(JERO_ERR_TENSOR_BOUNDS, "attention: n_heads_q not a multiple of n_heads_kv");
-  if (nq / nkv > kMaxGroup)
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: more than " + std::to_string(kMaxGroup) +
-                                                  " q heads per kv head");
-  if (hd != 32 && hd != 64 && hd != 128)
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: head_dim " + std::to_string(hd) + " not in {32, 64, 128}");
+  if (hd % 2 || hd > kGenMaxHd)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "attention: head_dim " + std::to_string(hd) +
+                                                  " must be even and at most " + std::to_string(kGenMaxHd));
   if (seq_len > int64_t(kMaxSplits) * attn_chunk(hd))
     return fail(JERO_ERR_CONTEXT_LENGTH_EXCEEDED, "attention: more than " +
                                                       std::to_string(int64_t(kMaxSplits) * attn_chunk(hd)) + " positions");

@@ -864,7 +864,8 @@ static int prefill_buffers(jero_model* m, int64_t n, int64_t pos0) {
   const int64_t H = c.hidden, F = c.ffn, Q = q_dim(c), KV = kv_dim(c);
   // the split attention path's partials (f32 ring, head_dim 32, or a batch of one query): the
   // flash kernel needs none and leaves at most a trailing one-query batch to the split path
-  const int64_t tq = attn_flash_ok(c.kv_dtype, int(c.head_dim), 2) ? 1 : std::min(n, kPrefillAttnTokens);
+  const bool flash = attn_flash_ok(c.kv_dtype, int(c.head_dim), 2, c.n_heads_q / c.n_heads_kv);
+  const int64_t tq = flash ? 1 : std::min(n, kPrefillAttnTokens);
   const size_t ws = size_t(tq) * attn_workspace_bytes(c.n_heads_q, c.head_dim, int(pos0 + n));
   PrefillBufs& b = m->pf;
   if (n <= b.rows && ws <= b.ws_bytes) return JERO_OK;
@@ -1058,7 +1059,8 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
     // and writes the Q8_K rows of Wo's input itself when Wo reads Q8_K, the group's heads fill
     // whole 256-blocks and no batch holds a single token (the f32 rows then only for the trace)
     const int64_t rbq = row_bytes(JERO_Q8_K, Q);
-    const bool flash = attn_flash_ok(c.kv_dtype, int(c.head_dim), int(std::min<int64_t>(n, 2)));
+    const bool flash =
+        attn_flash_ok(c.kv_dtype, int(c.head_dim), int(std::min<int64_t>(n, 2)), c.n_heads_q / c.n_heads_kv);
     const int64_t batch = flash ? 65535 : kPrefillAttnTokens;
     const bool att_q8k = flash && l.wo.present() && act_format(l.wo.quant) == JERO_Q8_K && n % batch != 1 &&
                          attn_flash_q8k_ok(int(c.n_heads_q / c.n_heads_kv), int(c.head_dim));

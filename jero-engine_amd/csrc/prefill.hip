@@ -50,9 +50,11 @@ __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(const float* __restri
 // blockIdx.y on, their loads issued together: y < nq a q head, y < nq + nkv a k head (both:
 // per-head RMSNorm when a norm is given, then RoPE at position pos0 + t with the decode step's
 // table cos / sin of pos / theta^(2i / hd), written back in place; k also into its ring slot),
-// otherwise a v head (into its ring slot).  Lane l < hd / 2 holds pair (2l, 2l + 1).  Token t's
-// table also goes to rope_cs[t][hd] (the trace of its step).
+// otherwise a v head (into its ring slot).  Lane l holds pairs l and l + 64 (those below hd / 2:
+// head_dim up to 256), pair i being dims (2i, 2i + 1).  Token t's table also goes to rope_cs[t][hd]
+// (the trace of its step).
 constexpr int kRopeRowsPerWave = 4;
+constexpr int kRopePairsPerLane = 2;
 template <typename KV>
 __global__ void __launch_bounds__(64) qk_rope_rows_kernel(float* __restrict__ q, int64_t q_stride, float* __restrict__ k,
                                                           int64_t k_stride, const float* __restrict__ v,
@@ -67,10 +69,16 @@ __global__ void __launch_bounds__(64) qk_rope_rows_kernel(float* __restrict__ q,
   const int64_t pos = pos0 + t;
   const int64_t slot = pos % capacity;
   const int64_t kvd = int64_t(nkv) * hd;
-  const bool on = lane < hd / 2;
-  const int pr = on ? lane : hd / 2 - 1;
+  constexpr int PL = kRopePairsPerLane;
+  bool on[PL];
+  int pr[PL];
+#pragma unroll
+  for (int c = 0; c < PL; c++) {
+    on[c] = lane + 64 * c < hd / 2;
+    pr[c] = on[c] ? lane + 64 * c : hd / 2 - 1;
+  }
   // every row's loads first (rows past the last repeat it and are not used)
-  float2 x[kRopeRowsPerWave], g[kRopeRowsPerWave], x2[kRopeRowsPerWave];
+  float2 x[kRopeRowsPerWave][PL], g[kRopeRowsPerWave][PL], x2[kRopeRowsPerWave][PL];
 #pragma unroll
   for (int j = 0; j < kRopeRowsPerWave; j++) {
     const int y = min(y0 + j, ny - 1);
@@ -80,44 +88,62 @@ __global__ void __launch_bounds__(64) qk_rope_rows_kernel(float* __restrict__ q,
                               : v + t * v_stride + int64_t(y - nq - nkv) * hd;
     const float* nw = y < nq ? q_norm : !isv ? k_norm : nullptr;
     const float* row2 = isv && v2 ? v2 + t * v_stride + int64_t(y - nq - nkv) * hd : row;
-    x[j] = reinterpret_cast<const float2*>(row)[pr];
-    g[j] = reinterpret_cast<const float2*>(nw ? nw : row)[pr];
-    x2[j] = reinterpret_cast<const float2*>(row2)[pr];
+#pragma unroll
+    for (int c = 0; c < PL; c++) {
+      x[j][c] = reinterpret_cast<const float2*>(row)[pr[c]];
+      g[j][c] = reinterpret_cast<const float2*>(nw ? nw : row)[pr[c]];
+      x2[j][c] = reinterpret_cast<const float2*>(row2)[pr[c]];
+    }
   }
-  const float expo = float(2 * pr) / float(hd);
-  float sn, cn;
-  sincosf(float(pos) / powf(theta, expo), &sn, &cn);
-  if (y0 == 0 && on) {
-    rope_cs[int64_t(t) * hd + 2 * lane] = cn;
-    rope_cs[int64_t(t) * hd + 2 * lane + 1] = sn;
+  float sn[PL], cn[PL];
+#pragma unroll
+  for (int c = 0; c < PL; c++) {
+    const float expo = float(2 * pr[c]) / float(hd);
+    sincosf(float(pos) / powf(theta, expo), &sn[c], &cn[c]);
+    if (y0 == 0 && on[c]) {
+      rope_cs[int64_t(t) * hd + 2 * pr[c]] = cn[c];
+      rope_cs[int64_t(t) * hd + 2 * pr[c] + 1] = sn[c];
+    }
   }
 #pragma unroll
   for (int j = 0; j < kRopeRowsPerWave; j++) {
     const int y = y0 + j;
     if (y >= ny) break;  // uniform
     if (y >= nq + nkv) {  // v head: ring append only (the two halves' sum, when split)
-      if (on) {
-        const float2 xv = v2 ? make_float2(x[j].x + x2[j].x, x[j].y + x2[j].y) : x[j];
-        KV* dst = v_ring + slot * kvd + int64_t(y - nq - nkv) * hd + 2 * lane;
+#pragma unroll
+      for (int c = 0; c < PL; c++) {
+        if (!on[c]) continue;
+        const float2 xv = v2 ? make_float2(x[j][c].x + x2[j][c].x, x[j][c].y + x2[j][c].y) : x[j][c];
+        KV* dst = v_ring + slot * kvd + int64_t(y - nq - nkv) * hd + 2 * pr[c];
         dst[0] = KV(xv.x);
         dst[1] = KV(xv.y);
       }
       continue;
     }
     const bool isq = y < nq;
-    float2 xv = x[j];
+    float2 xv[PL];
+#pragma unroll
+    for (int c = 0; c < PL; c++) xv[c] = x[j][c];
     if (isq ? q_norm : k_norm) {
-      const float ss = wave_sum_dpp(on ? xv.x * xv.x + xv.y * xv.y : 0.f);
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < PL; c++) ss += on[c] ? xv[c].x * xv[c].x + xv[c].y * xv[c].y : 0.f;
+      ss = wave_sum_dpp(ss);
       const float inv = 1.0f / sqrtf(ss / float(hd) + eps);
-      xv.x = xv.x * inv * g[j].x;
-      xv.y = xv.y * inv * g[j].y;
+#pragma unroll
+      for (int c = 0; c < PL; c++) {
+        xv[c].x = xv[c].x * inv * g[j][c].x;
+        xv[c].y = xv[c].y * inv * g[j][c].y;
+      }
     }
-    const float2 r = make_float2(xv.x * cn - xv.y * sn, xv.x * sn + xv.y * cn);
-    if (on) {
+#pragma unroll
+    for (int c = 0; c < PL; c++) {
+      if (!on[c]) continue;
+      const float2 r = make_float2(xv[c].x * cn[c] - xv[c].y * sn[c], xv[c].x * sn[c] + xv[c].y * cn[c]);
       float* row = isq ? q + t * q_stride + int64_t(y) * hd : k + t * k_stride + int64_t(y - nq) * hd;
-      reinterpret_cast<float2*>(row)[lane] = r;
+      reinterpret_cast<float2*>(row)[pr[c]] = r;
       if (!isq) {
-        KV* dst = k_ring + slot * kvd + int64_t(y - nq) * hd + 2 * lane;
+        KV* dst = k_ring + slot * kvd + int64_t(y - nq) * hd + 2 * pr[c];
         dst[0] = KV(r.x);
         dst[1] = KV(r.y);
       }

@@ -27,8 +27,15 @@ CASES = [  # nq, nkv, hd, seq
 ]
 
 
+# head_dim outside {32, 64, 128} or more than 8 q heads per kv head: the generic kernels
+GENERIC_CASES = [
+    (4, 4, 48, 4), (8, 2, 80, 300), (12, 4, 96, 129), (16, 1, 256, 700), (32, 2, 32, 65), (64, 2, 128, 257),
+    (6, 3, 2, 70), (10, 5, 160, 64), (8, 8, 192, 4096), (3, 1, 256, 1), (48, 4, 64, 1000),
+]
+
+
 @pytest.mark.parametrize("kv", ["f32", "f16"])
-@pytest.mark.parametrize("nq,nkv,hd,seq", CASES)
+@pytest.mark.parametrize("nq,nkv,hd,seq", CASES + GENERIC_CASES)
 def test_gqa_attention_parity(dev, kv, nq, nkv, hd, seq):
     print(f"attention kv={kv} nq={nq} nkv={nkv} hd={hd} seq={seq}", flush=True)
     rng = np.random.default_rng(nq * 1000 + seq + hd)
@@ -52,9 +59,9 @@ def test_attention_shape_errors(dev):
     with pytest.raises(J.K3Error) as ei:
         J.gqa_causal_attention_f32(z, z, z, z, 6, 4, 32, 4, 1.0)
     assert ei.value.variant == "TensorBoundsError"
-    with pytest.raises(J.K3Error) as ei:
-        J.gqa_causal_attention_f32(z, z, z, z, 4, 4, 48, 4, 1.0)
+    with pytest.raises(J.K3Error) as ei:  # odd head_dim (even_head_dim never gives one)
+        J.gqa_causal_attention_f32(z, z, z, z, 4, 4, 47, 4, 1.0)
     assert ei.value.variant == "CapabilityMismatch"
-    with pytest.raises(J.K3Error) as ei:
-        J.gqa_causal_attention_f32(z, z, z, z, 32, 2, 32, 4, 1.0)
+    with pytest.raises(J.K3Error) as ei:  # above 256
+        J.gqa_causal_attention_f32(z, z, z, z, 1, 1, 258, 1, 1.0)
     assert ei.value.variant == "CapabilityMismatch"

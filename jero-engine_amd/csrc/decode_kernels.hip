@@ -84,11 +84,14 @@ __device__ __forceinline__ void pin_x(XRegs<ACT, XB, NORM>& X) {
   }
 }
 
-// Builds the activation blocks of x (or of rmsnorm(x) * nw) in LDS from the registers; tr_xn
-// (debug trace, or null) receives the f32 values that are quantized.
+// Builds the activation blocks of x (or of rmsnorm(x) * nw) in LDS from the registers and
+// returns the RMSNorm scale (1 without a norm).  It writes no global memory: a conditional store
+// here would leave the compiler unable to count the weight loads still in flight, so it would
+// make the first rows wait for loads issued after them (the trace is written afterwards,
+// trace_xn).
 template <int ACT, int XB, bool NORM>
-__device__ void build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps, int K, uint8_t* s_act, float* s_tmp,
-                              float* tr_xn) {
+__device__ float build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps, int K, uint8_t* s_act,
+                               float* s_tmp) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nwv = blockDim.x >> 6;
   float scale = 1.0f;
   if (has_norm) {
@@ -119,7 +122,6 @@ __device__ void build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps,
             e[3] = e[3] * scale * X.g[i].w;
           }
         }
-        if (tr_xn) reinterpret_cast<float4*>(tr_xn + b * 256)[lane] = make_float4(e[0], e[1], e[2], e[3]);
         q8k_block_wave(e, lane, s_act + b * 292);
       }
     } else {
@@ -130,7 +132,6 @@ __device__ void build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps,
         if constexpr (NORM) {
           if (has_norm) v = v * scale * X.g[i].x;
         }
-        if (tr_xn) tr_xn[b * 32 + l] = v;
         float a = fabsf(v);
 #pragma unroll
         for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, kWave));
@@ -143,6 +144,14 @@ __device__ void build_act_lds(XRegs<ACT, XB, NORM>& X, bool has_norm, float eps,
     }
   }
   lds_barrier();
+  return scale;
+}
+
+// Debug trace: the f32 values the prologue quantized, x[i] * scale * nw[i] (the same operations
+// in the same order as build_act_lds, so the same bits), or x itself without a norm.
+__device__ __forceinline__ void trace_xn(float* dst, const float* __restrict__ x, const float* __restrict__ nw,
+                                         bool has_norm, float scale, int K) {
+  for (int i = threadIdx.x; i < K; i += blockDim.x) dst[i] = has_norm ? x[i] * scale * nw[i] : x[i];
 }
 
 // Debug trace: the workgroup copies the activation blocks it built in LDS to global memory.
@@ -225,9 +234,8 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
   pin_x(X);
   // 2. activation blocks in LDS (every thread takes part)
   const bool tracing = blockIdx.x == 0 && a.tr_q8 != nullptr;
-  build_act_lds<ACT, XB, NORM>(X, NORM && a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp,
-                               tracing ? a.tr_xn : nullptr);
-  if (tracing) trace_act(a.tr_q8, s_act, int(ACT == JERO_Q8_K ? a.K / 256 * 292 : a.K / 32 * 36));
+  const bool has_norm = NORM && a.norm_w != nullptr;
+  const float xscale = build_act_lds<ACT, XB, NORM>(X, has_norm, a.eps, a.K, s_act, s_tmp);
   // The activation units stay in registers for all rows (re-reading them from LDS per row, to
   // fit two workgroups per CU on long rows, measured slower).
   typename Ut::Act act[UPL];
@@ -304,6 +312,12 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_kernel(DGemvArgs a) {
     load_rows(rg + 2 * stride, wa, ya);
     __builtin_amdgcn_sched_barrier(0);
     process(rg + stride, wb, yb);
+  }
+  // debug trace of the prologue (LDS is not written after it); stores before the rows would leave
+  // the compiler unable to count the weight loads still in flight
+  if (tracing) {
+    trace_act(a.tr_q8, s_act, int(ACT == JERO_Q8_K ? a.K / 256 * 292 : a.K / 32 * 36));
+    if (a.tr_xn) trace_xn(a.tr_xn, a.x, a.norm_w, has_norm, xscale, a.K);
   }
   if constexpr (OUT == kOutArgmax) {
     // (max, first index) over the workgroup's rows, NaN skipped
@@ -413,12 +427,15 @@ __global__ void __launch_bounds__(kDecodeThreads) dgemv_dual_kernel(DGemvArgs a)
   load_row_units<F1, UPL>(a.w, a.rb, a.U, N1, r1, c1);
   pin_x(X);
   const bool tracing = blockIdx.x == 0 && a.tr_q8 != nullptr;
-  build_act_lds<JERO_Q8_K, XB, true>(X, a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp, tracing ? a.tr_xn : nullptr);
-  if (tracing) trace_act(a.tr_q8, s_act, a.K / 256 * 292);
+  const float xscale = build_act_lds<JERO_Q8_K, XB, true>(X, a.norm_w != nullptr, a.eps, a.K, s_act, s_tmp);
   store_segment<F1, UPL>(a.w, a.rb, a.U, N1, r1, stride, s_act, a.y, c1);
   if (r2 + N1 < total) {
     load_row_units<F2, UPL>(a.w2, a.rb2, a.U, a.N2, r2, c2);
     store_segment<F2, UPL>(a.w2, a.rb2, a.U, a.N2, r2, stride, s_act, a.y + N1, c2);
+  }
+  if (tracing) {  // after the rows (see dgemv_kernel)
+    trace_act(a.tr_q8, s_act, a.K / 256 * 292);
+    if (a.tr_xn) trace_xn(a.tr_xn, a.x, a.norm_w, a.norm_w != nullptr, xscale, a.K);
   }
 }
 

@@ -34,8 +34,14 @@ Fifth part ("forward_model"): the int8 ForwardModel matrix bench (prompt "hello 
 256, n_ctx 64: 53 greedy tokens) through jero_hip_forward_model_evaluate, as prefill ms and decode
 tokens/s, next to the oracle's scalar C evaluate of the same run (and whether its tokens agree).
 
+Sixth part ("moe_decode"): the same decode step for a random-init Qwen3-30B-A3B-shaped model
+(48 layers, hidden 2048, 32/4 heads of 128, 128 experts of FFN 768, top-8, vocab 151936; Q4_K_M),
+as tokens/s and fractions of the HBM roofline over the bytes one token reads (attention, router,
+the 8 routed experts of every layer, head; + the KV ring), next to the oracle's step.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-gemm]
-                       [--no-moe] [--no-forward] [--copy-probe MB]
+                       [--no-moe] [--no-forward] [--no-dense-decode] [--no-moe-layer] [--copy-probe MB]
+(--no-decode and --no-moe each also skip moe_decode)
 """
 import argparse
 import json
@@ -261,6 +267,124 @@ def bench_decode(torch, J, dev, stream, steps, warmup, keep_host):
                                "to enqueue one call"}}
     m.close()
     return res, host, host_kv
+
+
+QWEN3_30B_A3B = dict(hidden=2048, ffn=6144, n_layers=48, vocab=151936, nq=32, nkv=4, hd=128, eps=1e-6, theta=1e6)
+QWEN3_30B_A3B_MOE = (128, 8, 768, False)  # (experts, top_k, expert FFN, shared expert)
+
+
+def moe_decode_tensors(spec, moe):
+    """(name, quant, dims) of the Q4_K_M Qwen3-MoE model: the Qwen3 attention of decode_tensors,
+    an F32 router [hidden, E] and stacked experts per layer (gate / up Q4_K [hidden, F, E], down
+    [F, hidden, E] Q6_K on the Q4_K_M rule's layers, else Q4_K)."""
+    E, _, F, _ = moe
+    H, L = spec["hidden"], spec["n_layers"]
+    hi = set(q6k_layers(L))
+    out = []
+    for name, quant, n_in, n_out in decode_tensors(spec):
+        if ".ffn_gate." in name or ".ffn_up." in name or ".ffn_down." in name:
+            continue
+        out.append((name, quant, (n_in, n_out) if n_out > 1 else (n_in,)))
+    for i in range(L):
+        p = f"blk.{i}."
+        out += [(p + "ffn_gate_inp.weight", 0, (H, E)), (p + "ffn_gate_exps.weight", 12, (H, F, E)),
+                (p + "ffn_up_exps.weight", 12, (H, F, E)), (p + "ffn_down_exps.weight", 14 if i in hi else 12, (F, H, E))]
+    return out
+
+
+def bench_moe_decode(torch, J, dev, stream, steps, warmup, keep_host):
+    """The batch-1 decode step of a random-init Qwen3-30B-A3B-shaped model (48 layers, hidden 2048,
+    32/4 heads of 128, 128 experts of FFN 768, top-8, vocab 151936) in Q4_K_M, f16 KV ring of 4096
+    slots pre-filled, greedy next token; one step captured in a HIP graph, each replay the next
+    token.  Algorithmic bytes per token: every attention / router / norm weight, the 8 routed
+    experts of every layer, the head, and the KV ring."""
+    import numpy as np
+    spec, moe = QWEN3_30B_A3B, QWEN3_30B_A3B_MOE
+    E, k, F, _ = moe
+    m = J.DecodeModel(spec["hidden"], spec["ffn"], spec["n_layers"], spec["vocab"], spec["nq"], spec["nkv"],
+                      spec["hd"], spec["eps"], spec["theta"], KV_CAP, J.KV_F16, True, moe=moe)
+    host = {}
+    dense_bytes, expert_bytes, total = 0, 0, 0
+    g = torch.Generator(device=dev)
+    g.manual_seed(4343)
+    for i, (name, quant, dims) in enumerate(moe_decode_tensors(spec, moe)):
+        n_in, n_out = dims[0], int(np.prod(dims[1:]))
+        if quant == 0:
+            t = (1.0 + 0.1 * torch.randn(n_in * n_out, generator=g, device=dev)).float() if n_out == 1 else \
+                (0.02 * torch.randn(n_in * n_out, generator=g, device=dev)).float()
+            nbytes = 4 * n_in * n_out
+        else:
+            t = synth_weights(torch, J, quant, n_in, n_out, 1, dev, 7000 + i)[0]
+            nbytes = t.numel()
+        total += nbytes
+        if "_exps." in name:
+            expert_bytes += nbytes // E * k  # the k routed experts of the layer
+        elif name != "token_embd.weight":
+            dense_bytes += nbytes
+        m.set_tensor(name, quant, t, n_in, n_out)
+        if keep_host:
+            host[name] = (quant, t.cpu().numpy(), list(dims))
+        del t
+    m.finalize()
+    kvd = spec["nkv"] * spec["hd"]
+    host_kv = np.empty((spec["n_layers"], 2, KV_CAP, kvd), np.float32) if keep_host else None
+    for L in range(spec["n_layers"]):
+        kk = torch.randn(KV_CAP, kvd, generator=g, device=dev).half()
+        vv = torch.randn(KV_CAP, kvd, generator=g, device=dev).half()
+        m.write_kv(L, kk, vv)
+        if keep_host:
+            host_kv[L, 0] = kk.float().cpu().numpy()
+            host_kv[L, 1] = vv.float().cpu().numpy()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        m.set_position(1, KV_CAP - 1, stream=stream)
+        for _ in range(max(1, warmup)):
+            m.decode_step(stream=stream)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            m.decode_step(stream=stream)
+        graph.replay()
+        stream.synchronize()
+        s0, e0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        e0.record(stream)
+    e0.synchronize()
+    t_tok = s0.elapsed_time(e0) / 1e3 / steps
+    tok, pos = m.read_token_pos()
+    m.close()
+    kv_bytes = spec["n_layers"] * 2 * KV_CAP * kvd * 2
+    wb = dense_bytes + expert_bytes
+    res = {"workload": "Qwen3-30B-A3B-shape Q4_K_M batch-1 greedy decode, 48 layers, 128 experts top-8, "
+                       "f16 KV ring 4096 slots full",
+           "tok_s": round(1.0 / t_tok, 1), "ms_per_token": round(t_tok * 1e3, 4), "steps": steps,
+           "model_bytes": total, "weight_bytes_per_token": wb, "kv_bytes_per_token": kv_bytes,
+           "frac_weight_roofline": round(wb / t_tok / 1e9 / HBM_PEAK_GBS, 4),
+           "frac_weights_kv_roofline": round((wb + kv_bytes) / t_tok / 1e9 / HBM_PEAK_GBS, 4),
+           "last_token": tok, "position": pos, "graph": "one decode step captured, replayed per token"}
+    return res, host, host_kv
+
+
+def cpu_moe_decode_baseline(O, host, host_kv, budget_s=10.0):
+    """The oracle's Qwen3-MoE decode step (the C attention sublayer and head, moe_layer's GEMVs;
+    pthreads over all host cores) on the same weights and KV values (widened to f32)."""
+    spec, moe = QWEN3_30B_A3B, QWEN3_30B_A3B_MOE
+    threads = len(os.sched_getaffinity(0))
+    om = O.DecodeModel(spec, {n: (q, a) for n, (q, a, _) in host.items()}, KV_CAP)
+    done, t0, tok = 0, time.perf_counter(), 1
+    pos = KV_CAP - 1
+    while True:
+        logits = om.moe_step(host_kv, tok, pos, moe, host, threads=threads)
+        tok = int(logits.argmax())
+        pos += 1
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return done / el, threads, done, el
 
 
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
@@ -630,6 +754,17 @@ def summarize_profiles(dirs, match, step_end, last, out):
                 w(f"\nLast {len(walls)} steps ending in `{step_end}` ({counts[-1]} kernels per step): wall "
                   f"mean {np.mean(walls) / 1e3:.1f} us (min {min(walls) / 1e3:.1f}, max {max(walls) / 1e3:.1f}); "
                   f"kernel-time sum mean {np.mean(sums) / 1e3:.1f} us\n")
+                per = {}
+                for a, b in list(zip(ends[:-1], ends[1:]))[-len(walls):]:
+                    for r in ev[a + 1:b + 1]:
+                        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+                        p = per.setdefault((kernel_short_name(r["Kernel_Name"]), grid), [0, 0])
+                        p[0] += 1
+                        p[1] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+                n = len(walls)
+                w("\n| kernel (per step) | grid | launches | us per step | mean us |\n|---|---|---|---|---|\n")
+                for (k, grid), (c, d) in sorted(per.items(), key=lambda kv: -kv[1][1]):
+                    w(f"| `{k}` | {grid} | {c / n:.0f} | {d / n / 1e3:.1f} | {d / c / 1e3:.2f} |\n")
     pmc = [r for r in read_profile_csv(dirs, "_counter_collection.csv") if match in r["Kernel_Name"]]
     if pmc:
         vals = {}
@@ -691,6 +826,8 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-forward", action="store_true")
+    ap.add_argument("--no-dense-decode", action="store_true", help="skip the Qwen3-8B decode (keep moe_decode)")
+    ap.add_argument("--no-moe-layer", action="store_true", help="skip the MoE layer part (keep moe_decode)")
     ap.add_argument("--decode-steps", type=int, default=50)
     ap.add_argument("--copy-probe", type=float, default=0.0,
                     help="also run one device copy of this many MB (PMC byte-counter calibration)")
@@ -857,7 +994,7 @@ def main():
 
     # ---- routed experts (extra)
     moe = None
-    if not args.no_moe:
+    if not args.no_moe and not args.no_moe_layer:
         moe = bench_moe(torch, J, dev, stream, max(20, args.steps // 5))
         torch.cuda.empty_cache()
 
@@ -876,9 +1013,9 @@ def main():
 
     # ---- full decode step (extra)
     decode = None
-    if not args.no_decode:
-        del bufs, views
-        torch.cuda.empty_cache()
+    del bufs, views
+    torch.cuda.empty_cache()
+    if not args.no_decode and not args.no_dense_decode:
         decode, host, host_kv = bench_decode(torch, J, dev, stream, args.decode_steps, 3, not args.no_cpu)
         if not args.no_cpu:
             import pyoracle as O
@@ -887,6 +1024,20 @@ def main():
                                       "sample": f"{reps} greedy steps of the same model from position {KV_CAP - 1}, "
                                                 f"{el:.1f} s, f32 KV ring"}
             del host, host_kv
+
+    # ---- Qwen3-MoE decode step (extra)
+    moe_decode = None
+    if not args.no_decode and not args.no_moe:
+        torch.cuda.empty_cache()
+        moe_decode, mhost, mkv = bench_moe_decode(torch, J, dev, stream, args.decode_steps, 3, not args.no_cpu)
+        torch.cuda.empty_cache()
+        if not args.no_cpu:
+            import pyoracle as O
+            tps, threads, reps, el = cpu_moe_decode_baseline(O, mhost, mkv)
+            moe_decode["cpu_baseline"] = {"value": round(tps, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+                                          "sample": f"{reps} greedy steps of the same model from position "
+                                                    f"{KV_CAP - 1}, {el:.1f} s, f32 KV ring"}
+            del mhost, mkv
 
     out = {
         "metric": "Q4_K GEMV GB/s (% HBM peak); decode tok/s, 8B-shape Q4_K_M, 1 GPU",
@@ -920,6 +1071,7 @@ def main():
         "prefill_gemm": gemm,
         "moe": moe,
         "decode": decode,
+        "moe_decode": moe_decode,
         "forward_model": fwd,
     }
     print(json.dumps(out))

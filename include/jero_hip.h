@@ -394,6 +394,23 @@ typedef struct jero_model_config {
 typedef struct jero_model jero_model;
 
 int jero_hip_model_create(const jero_model_config *cfg, jero_model **model);
+/* A Qwen3-MoE model (StandardExecSpec's `moe`, MoeDispatchSpec { num_experts, top_k,
+ * expert_ffn_dim, use_shared }, src/qwen_deepseek.rs:81-87, 1465-1487): every layer's FFN is then
+ * dispatch_qwen3_moe_ffn (:847-951, called at :1286-1300) instead of the dense SwiGLU FFN.  Call it
+ * after jero_hip_model_create and before any FFN tensor.  The model then also takes, per layer,
+ * blk.N.ffn_gate_inp.weight (the router, [hidden, E]), the stacked routed experts
+ * blk.N.ffn_{gate,up}_exps.weight ([hidden, F, E], n_out = F * E) and blk.N.ffn_down_exps.weight
+ * ([F, hidden, E]), and the shared expert blk.N.ffn_{gate,up,down}_shexp.weight; a layer's dense
+ * ffn_{gate,up,down}.weight have the expert FFN dimension (the fallback of a layer without router
+ * or experts, :873-880, 942-946).  The routed experts run jero_hip_moe_ffn's kernels (same formats
+ * and limits; Q4_K / Q6_K experts re-laid out at finalize as jero_hip_repack_experts does) on the
+ * router's eff_experts = min(its elements / hidden, num_experts) experts; the router and the shared
+ * expert take jero_hip_vec_dot's formats.  blk.N.exp_probs_b.bias (a routing bias) and an
+ * incomplete set of expert tensors make finalize return CapabilityMismatch.  The decode trace of
+ * such a layer holds xn_ffn (the FFN's normalised input) and, in gu, the router logits (when
+ * 2 * ffn >= E); its q8_ffn, act and q8_down are not written.  jero_hip_model_prefill runs the
+ * prompt as decode steps, the reference's own token loop. */
+int jero_hip_model_set_moe(jero_model *model, int64_t n_experts, int top_k, int64_t expert_ffn, int use_shared);
 int jero_hip_model_destroy(jero_model *model);
 /* Copies one tensor to the device (src host memory, or device memory if src_on_device).  A layer
  * projection (blk.N.attn_q/attn_k/attn_v/attn_output/ffn_gate/ffn_up/ffn_down.weight) whose

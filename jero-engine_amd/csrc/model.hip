@@ -21,6 +21,7 @@
 #include "attention.h"
 #include "decode.h"
 #include "gemv.h"
+#include "moe.h"
 #include "jero_common.h"
 #include "prefill.h"
 #include "quantize.h"
@@ -45,6 +46,13 @@ struct LayerW {
   // a projection tensor absent (or Q, K / gate, up in different formats): the present ones run
   // unfused, the absent ones as project_or_deterministic_slice's fallback
   bool qkv_split = false, gu_split = false;
+  // a model with an MoE spec (jero_hip_model_set_moe): dispatch_qwen3_moe_ffn's tensors
+  // (src/qwen_deepseek.rs:847-951) -- the router ffn_gate_inp, the stacked routed experts
+  // ffn_{gate,up,down}_exps, the shared expert ffn_{gate,up,down}_shexp; exp_probs_b is refused
+  DevTensor router, gate_exps, up_exps, down_exps, gate_shexp, up_shexp, down_shexp;
+  bool probs_bias = false;
+  bool routed = false;  // router and experts present: the routed path, else the dense fallback
+  int64_t n_experts = 0, exp_ffn = 0;  // the router's experts (eff_experts, :882-888), rows per expert
 };
 
 // Row buffers of the batched prefill, grown on demand (rows tokens at a time).
@@ -81,6 +89,17 @@ struct jero_model {
   int32_t* token = nullptr;
   int64_t* pos = nullptr;
   int32_t* status = nullptr;  // sticky: nonzero after a step whose logits held no argmax
+  // the MoE spec (MoeDispatchSpec, src/qwen_deepseek.rs:81-87): set by jero_hip_model_set_moe
+  // before the tensors; every layer's FFN is then dispatch_qwen3_moe_ffn (:1286-1300)
+  bool moe = false, moe_shared = false;
+  int64_t moe_experts = 0, moe_ffn = 0;
+  int moe_top_k = 0;
+  // its step buffers: RMSNorm(hidden) * ffn_norm, router logits, the shared expert's or dense
+  // FFN's output, the selections, a Q8 row of the router input, the workspaces
+  float *moe_xn = nullptr, *moe_logits = nullptr, *moe_y = nullptr, *moe_selw = nullptr;
+  int32_t* moe_sel = nullptr;
+  void *moe_xq = nullptr, *moe_ws = nullptr, *ffn_ws = nullptr;
+  size_t moe_ws_bytes = 0, ffn_ws_bytes = 0;
   float* rope_cs = nullptr;
   void* kv = nullptr;
   size_t kv_bytes = 0;
@@ -116,8 +135,11 @@ static int64_t q_dim(const jero_model_config& c) { return int64_t(c.n_heads_q) *
 static int64_t kv_dim(const jero_model_config& c) { return int64_t(c.n_heads_kv) * c.head_dim; }
 
 // Expected (n_in, n_out) of a named tensor; returns false if the name is unknown.
-static bool expected_shape(const jero_model_config& c, const std::string& base, int64_t& n_in, int64_t& n_out) {
-  const int64_t H = c.hidden, F = c.ffn, Q = q_dim(c), KV = kv_dim(c);
+// ffn: the dense FFN's rows (a model with an MoE spec runs its dense fallback with the expert
+// FFN dimension, src/qwen_deepseek.rs:873-880).
+static bool expected_shape(const jero_model_config& c, int64_t ffn, const std::string& base, int64_t& n_in,
+                           int64_t& n_out) {
+  const int64_t H = c.hidden, F = ffn, Q = q_dim(c), KV = kv_dim(c);
   static const std::map<std::string, int> kinds = {
       {"attn_norm.weight", 0}, {"ffn_norm.weight", 1}, {"attn_q_norm.weight", 2}, {"attn_k_norm.weight", 3},
       {"attn_q.weight", 4},    {"attn_k.weight", 5},   {"attn_v.weight", 6},      {"attn_output.weight", 7},
@@ -165,8 +187,20 @@ static DevTensor* find_slot(jero_model* m, const std::string& name, int64_t& n_i
   }
   if (L < 0 || L >= c.n_layers) return nullptr;
   std::string base = name.substr(dot + 1);
-  if (!expected_shape(c, base, n_in, n_out)) return nullptr;
   LayerW& l = m->layers[size_t(L)];
+  if (m->moe) {  // dispatch_qwen3_moe_ffn's tensors: shapes checked at finalize (n_in, n_out 0 here)
+    static const std::map<std::string, DevTensor LayerW::*> moe_slots = {
+        {"ffn_gate_inp.weight", &LayerW::router},     {"ffn_gate_exps.weight", &LayerW::gate_exps},
+        {"ffn_up_exps.weight", &LayerW::up_exps},     {"ffn_down_exps.weight", &LayerW::down_exps},
+        {"ffn_gate_shexp.weight", &LayerW::gate_shexp}, {"ffn_up_shexp.weight", &LayerW::up_shexp},
+        {"ffn_down_shexp.weight", &LayerW::down_shexp}};
+    auto it = moe_slots.find(base);
+    if (it != moe_slots.end()) {
+      n_in = n_out = 0;
+      return &(l.*(it->second));
+    }
+  }
+  if (!expected_shape(c, m->moe ? m->moe_ffn : c.ffn, base, n_in, n_out)) return nullptr;
   static const std::map<std::string, DevTensor LayerW::*> slots = {
       {"attn_norm.weight", &LayerW::attn_norm}, {"ffn_norm.weight", &LayerW::ffn_norm},
       {"attn_q_norm.weight", &LayerW::q_norm},  {"attn_k_norm.weight", &LayerW::k_norm},
@@ -377,8 +411,36 @@ extern "C" int jero_hip_model_set_tensor(jero_model* m, const char* name, int qu
   if (!m || !name || !src) return fail(JERO_ERR_INVALID_ARGUMENT, "set_tensor: null pointer");
   if (m->finalized) return fail(JERO_ERR_INVALID_ARGUMENT, "set_tensor: model already finalized");
   int64_t ein = 0, eout = 0;
+  const std::string nm(name);
+  static const std::string kProbsBias = ".exp_probs_b.bias";
+  if (m->moe && nm.rfind("blk.", 0) == 0 && nm.size() > kProbsBias.size() &&
+      nm.compare(nm.size() - kProbsBias.size(), kProbsBias.size(), kProbsBias) == 0) {
+    // select_experts_with_optional_bias's routing bias (DeepSeek; src/qwen_deepseek.rs:773-834):
+    // recorded so that finalize refuses the model
+    const int64_t L = std::atoll(nm.c_str() + 4);
+    if (L < 0 || L >= m->cfg.n_layers) return fail(JERO_ERR_CAPABILITY_MISMATCH, "set_tensor: unknown tensor '" + nm + "'");
+    m->layers[size_t(L)].probs_bias = true;
+    return JERO_OK;
+  }
   DevTensor* slot = find_slot(m, name, ein, eout);
   if (!slot) return fail(JERO_ERR_CAPABILITY_MISMATCH, std::string("set_tensor: unknown tensor '") + name + "'");
+  if (ein == 0) {  // an MoE tensor: any shape here, its bytes must match it
+    const int64_t rb = row_bytes(quant, n_in);
+    if (n_in <= 0 || n_out <= 0 || !is_weight_quant(quant))
+      return fail(JERO_ERR_TENSOR_BOUNDS, "set_tensor: '" + nm + "' is empty or of an unknown format");
+    if (rb < 0 || size_t(rb) * size_t(n_out) != nbytes)
+      return fail(JERO_ERR_TENSOR_BOUNDS, "set_tensor: '" + nm + "' byte size " + std::to_string(nbytes) +
+                                              " does not match its shape");
+    if (slot->dev) dev_free(m, slot->dev);
+    void* p = nullptr;
+    int rc = dev_alloc(m, nbytes, &p);
+    if (rc) return rc;
+    if ((rc = check_hip(hipMemcpy(p, src, nbytes, src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice),
+                        "set_tensor upload")))
+      return rc;
+    *slot = {quant, p, nbytes, n_in, n_out};
+    return JERO_OK;
+  }
   if (is_projection(name) && n_in * n_out != ein * eout) {
     // project_or_deterministic_slice (src/gemma.rs:841-860) uses a tensor only when its element count
     // is out_len * in_len; any other takes the deterministic fallback, as if it were absent
@@ -422,6 +484,198 @@ extern "C" int jero_hip_model_set_tensor(jero_model* m, const char* name, int qu
                  "set_tensor upload");
   if (rc) return rc;
   *slot = {quant, p, nbytes, n_in, n_out};
+  return JERO_OK;
+}
+
+namespace jero {
+
+static jero_hip_tensor view_of(const DevTensor& t) {
+  return jero_hip_tensor{t.quant, t.dev, t.bytes, t.present() ? t.n_in * t.n_out : 0};
+}
+
+// One layer of a model with an MoE spec, at finalize: dispatch_qwen3_moe_ffn's choices
+// (src/qwen_deepseek.rs:873-946) made once.  A router with experts takes the routed path: the
+// router's experts eff_experts = its elements / hidden (at most num_experts, :882-888), the stacked
+// gate / up / down tensors of that many experts re-laid out in 16-row tiles for the expert kernels.
+// Without a router (or with num_experts or top_k 0, or without expert tensors: ran_any_expert false)
+// the layer runs run_dense_swiglu_ffn with the expert FFN dimension (:873-880, :942-946).
+static int moe_layer_finalize(jero_model* m, int64_t L, LayerW& l) {
+  const int64_t H = m->cfg.hidden;
+  const std::string at = "finalize: layer " + std::to_string(L) + ": ";
+  if (l.probs_bias)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, at + "exp_probs_b.bias (the routing bias of "
+                                                   "select_experts_with_optional_bias) is not supported");
+  const int n_exp = int(l.gate_exps.present()) + int(l.up_exps.present()) + int(l.down_exps.present());
+  l.routed = m->moe_experts > 0 && m->moe_top_k > 0 && l.router.present() && n_exp == 3;
+  if (m->moe_experts > 0 && m->moe_top_k > 0 && l.router.present() && n_exp != 0 && n_exp != 3)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, at + "an incomplete set of ffn_{gate,up,down}_exps tensors");
+  if (!l.routed) return JERO_OK;
+  const int64_t re = l.router.n_in * l.router.n_out;
+  const int64_t E = (re > 0 && re % H == 0) ? std::min(re / H, m->moe_experts) : m->moe_experts;
+  if (E * H > re || !(is_float_weight(l.router.quant) || act_format(l.router.quant) >= 0))
+    return fail(JERO_ERR_TENSOR_BOUNDS, at + "the router does not hold " + std::to_string(E) + " rows of " +
+                                            std::to_string(H) + " elements in a GEMV format");
+  if (l.gate_exps.n_in != H || l.up_exps.n_in != H || l.gate_exps.n_out % E || l.gate_exps.n_out != l.up_exps.n_out)
+    return fail(JERO_ERR_TENSOR_BOUNDS, at + "ffn_gate_exps / ffn_up_exps must be [hidden, ffn, n_experts]");
+  const int64_t F = l.gate_exps.n_out / E;
+  if (l.down_exps.n_in != F || l.down_exps.n_out != H * E)
+    return fail(JERO_ERR_TENSOR_BOUNDS, at + "ffn_down_exps must be [ffn, hidden, n_experts]");
+  if (l.gate_exps.quant != l.up_exps.quant)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, at + "ffn_gate_exps and ffn_up_exps in different formats");
+  if (m->moe_top_k > E)
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, at + "top_k above the router's " + std::to_string(E) + " experts");
+  l.n_experts = E;
+  l.exp_ffn = F;
+  // the expert kernels read the 16-row tile layouts fastest (Q4_K_T / Q6_K_T, jero_hip_repack_experts)
+  for (DevTensor* t : {&l.gate_exps, &l.up_exps, &l.down_exps}) {
+    const int64_t rows_per = t->n_out / E;
+    if ((t->quant == JERO_Q4_K || t->quant == JERO_Q6_K) && rows_per % 16 == 0) {
+      void* p = nullptr;
+      int dq = -1;
+      int rc = dev_alloc(m, t->bytes, &p);
+      if (rc || (rc = launch_repack_experts(t->quant, t->dev, t->n_in, t->n_out, p, &dq, nullptr)) ||
+          (rc = check_hip(hipDeviceSynchronize(), "expert repack")))
+        return rc;
+      dev_free(m, t->dev);
+      t->dev = p;
+      t->quant = dq;
+    }
+  }
+  MoeArgs a{};
+  a.x = a.logits = reinterpret_cast<const float*>(l.router.dev);  // non-null stand-ins for the check
+  a.T = 1;
+  a.E = E;
+  a.top_k = m->moe_top_k;
+  a.gate_quant = l.gate_exps.quant;
+  a.up_quant = l.up_exps.quant;
+  a.down_quant = l.down_exps.quant;
+  a.gate = l.gate_exps.dev;
+  a.up = l.up_exps.dev;
+  a.down = l.down_exps.dev;
+  a.hidden = H;
+  a.ffn = F;
+  a.y = reinterpret_cast<float*>(l.router.dev);
+  a.sel_idx = reinterpret_cast<int32_t*>(l.router.dev);
+  a.sel_w = a.y;
+  const int rc = check_moe_args(a, l.gate_exps.bytes, l.up_exps.bytes, l.down_exps.bytes);
+  return rc ? fail(rc, at + jero_hip_last_error()) : JERO_OK;
+}
+
+// The step buffers of a model with an MoE spec (sized for its largest layer).
+static int moe_buffers(jero_model* m) {
+  const auto& c = m->cfg;
+  const int64_t H = c.hidden;
+  int64_t E = 1, F = 4;
+  for (const LayerW& l : m->layers) {
+    E = std::max(E, l.n_experts);
+    F = std::max(F, l.exp_ffn);
+  }
+  const int k = std::max(1, m->moe_top_k);
+  // the dense FFNs (the shared expert, the fallback): their row counts as jero_hip_swiglu_ffn takes them
+  int64_t Fd = std::max<int64_t>(m->moe_ffn, 4);
+  for (const LayerW& l : m->layers) {
+    const int64_t ge = l.gate_shexp.present() ? l.gate_shexp.n_in * l.gate_shexp.n_out : 0;
+    if (ge > 0 && ge % H == 0) Fd = std::max(Fd, ge / H);
+  }
+  m->moe_ws_bytes = moe_workspace_bytes(1, E, k, H, F);
+  m->ffn_ws_bytes = jero_hip_swiglu_ffn_workspace_bytes(H, Fd);
+  void* p = nullptr;
+  int rc;
+  if ((rc = dev_alloc(m, sizeof(float) * size_t(H), &p))) return rc;
+  m->moe_xn = static_cast<float*>(p);
+  if ((rc = dev_alloc(m, sizeof(float) * size_t(E), &p))) return rc;
+  m->moe_logits = static_cast<float*>(p);
+  if ((rc = dev_alloc(m, sizeof(float) * size_t(H), &p))) return rc;
+  m->moe_y = static_cast<float*>(p);
+  if ((rc = dev_alloc(m, sizeof(float) * size_t(k), &p))) return rc;
+  m->moe_selw = static_cast<float*>(p);
+  if ((rc = dev_alloc(m, sizeof(int32_t) * size_t(k), &p))) return rc;
+  m->moe_sel = static_cast<int32_t*>(p);
+  if ((rc = dev_alloc(m, size_t(H / 32 + 1) * 36 + size_t(H / 256 + 1) * 292, &m->moe_xq))) return rc;
+  if ((rc = dev_alloc(m, m->moe_ws_bytes, &m->moe_ws))) return rc;
+  return dev_alloc(m, m->ffn_ws_bytes, &m->ffn_ws);
+}
+
+// The FFN of layer L of a model with an MoE spec (src/qwen_deepseek.rs:1278-1303):
+// xn = rmsnorm(hidden) * ffn_norm, out = dispatch_qwen3_moe_ffn(xn) -- the shared expert first,
+// then either the routed sum added onto it in selection order or the dense fallback -- and
+// hidden += out.  The routed path adds out to hidden in its last kernel; the trace (when set)
+// gets xn and the router logits.
+static int moe_ffn_step(jero_model* m, const LayerW& l, float eps, hipStream_t s, float* tr_xn, float* tr_logits) {
+  const int64_t H = m->cfg.hidden;
+  int rc = launch_head_norm(m->hidden, static_cast<const float*>(l.ffn_norm.dev), eps, H, m->moe_xn, s);
+  if (rc) return rc;
+  const bool shared = m->moe_shared && l.gate_shexp.present() && l.up_shexp.present() && l.down_shexp.present();
+  if (shared) {  // :860-871
+    const jero_hip_tensor g = view_of(l.gate_shexp), u = view_of(l.up_shexp), d = view_of(l.down_shexp);
+    if ((rc = jero_hip_swiglu_ffn(JERO_FFN_SHARED_EXPERT, m->moe_xn, H, m->moe_ffn, &g, &u, &d, 0, m->moe_y, m->ffn_ws,
+                                  m->ffn_ws_bytes, s)))
+      return rc;
+  }
+  if (!l.routed) {  // run_dense_swiglu_ffn with the expert FFN dimension (:873-880, :942-946)
+    const jero_hip_tensor g = view_of(l.gate), u = view_of(l.up), d = view_of(l.down);
+    if ((rc = jero_hip_swiglu_ffn(JERO_FFN_DENSE, m->moe_xn, H, m->moe_ffn, &g, &u, &d, shared ? 1 : 0, m->moe_y,
+                                  m->ffn_ws, m->ffn_ws_bytes, s)))
+      return rc;
+    rc = launch_det_proj(m->moe_y, H, nullptr, 0.f, 1.0f, m->hidden, H, true, s);  // hidden += out (x * 1 exact)
+  } else {
+    // router logits (matvec_any over the router's eff_experts rows, :882-890)
+    const int E = int(l.n_experts);
+    if (is_float_weight(l.router.quant)) {
+      rc = launch_matvec_float(l.router.quant, l.router.dev, H, E, m->moe_xn, m->moe_logits, s);
+    } else if (!(rc = launch_quantize_act(act_format(l.router.quant), m->moe_xn, 1, H, m->moe_xq, s))) {
+      rc = launch_matvec(l.router.quant, l.router.dev, H, E, m->moe_xq, m->moe_logits, nullptr, s);
+    }
+    if (rc) return rc;
+    if (tr_logits && (rc = check_hip(hipMemcpyAsync(tr_logits, m->moe_logits, sizeof(float) * size_t(E),
+                                                    hipMemcpyDeviceToDevice, s), "decode trace copy")))
+      return rc;
+    // select_top_k_experts and the experts' SwiGLU, summed in selection order onto the shared
+    // expert's output (or zero) and that sum added to hidden (:890-938, :1301-1303)
+    MoeArgs a{};
+    a.x = m->moe_xn;
+    a.logits = m->moe_logits;
+    a.T = 1;
+    a.E = E;
+    a.top_k = m->moe_top_k;
+    a.gate_quant = l.gate_exps.quant;
+    a.up_quant = l.up_exps.quant;
+    a.down_quant = l.down_exps.quant;
+    a.gate = l.gate_exps.dev;
+    a.up = l.up_exps.dev;
+    a.down = l.down_exps.dev;
+    a.hidden = H;
+    a.ffn = l.exp_ffn;
+    a.y = m->moe_y;
+    a.accumulate = shared;
+    a.resid = m->hidden;
+    a.sel_idx = m->moe_sel;
+    a.sel_w = m->moe_selw;
+    rc = launch_moe(a, m->moe_ws, s);
+  }
+  if (rc) return rc;
+  if (tr_xn)
+    rc = check_hip(hipMemcpyAsync(tr_xn, m->moe_xn, sizeof(float) * size_t(H), hipMemcpyDeviceToDevice, s),
+                   "decode trace copy");
+  return rc;
+}
+
+}  // namespace jero
+
+extern "C" int jero_hip_model_set_moe(jero_model* m, int64_t n_experts, int top_k, int64_t expert_ffn,
+                                      int use_shared) {
+  if (!m) return fail(JERO_ERR_INVALID_ARGUMENT, "set_moe: null model");
+  if (m->finalized) return fail(JERO_ERR_INVALID_ARGUMENT, "set_moe: model already finalized");
+  if (n_experts < 0 || top_k < 0 || expert_ffn <= 0)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "set_moe: negative experts or top_k, or an empty expert FFN");
+  for (const LayerW& l : m->layers)
+    if (l.gate.present() || l.up.present() || l.down.present())
+      return fail(JERO_ERR_INVALID_ARGUMENT, "set_moe: call it before the FFN tensors are set");
+  m->moe = true;
+  m->moe_experts = n_experts;
+  m->moe_top_k = top_k;
+  m->moe_ffn = expert_ffn;
+  m->moe_shared = use_shared != 0;
   return JERO_OK;
 }
 
@@ -469,7 +723,9 @@ extern "C" int jero_hip_model_finalize(jero_model* m) {
       }
       if ((rc = repack_planar(m, l.qkv))) return rc;
     }
-    if (l.gu_split) {
+    if (m->moe) {  // the dense tensors, if any, serve the MoE dispatch's fallback in their GGUF layout
+      if ((rc = moe_layer_finalize(m, L, l))) return rc;
+    } else if (l.gu_split) {
       for (DevTensor* t : {&l.gate, &l.up})
         if (t->present() && (rc = repack_planar(m, *t))) return rc;
       if (!m->gu) {
@@ -482,8 +738,9 @@ extern "C" int jero_hip_model_finalize(jero_model* m) {
       if ((rc = repack_planar(m, l.gate_up))) return rc;
     }
     if (l.wo.present() && (rc = repack_planar(m, l.wo))) return rc;
-    if (l.down.present() && (rc = repack_planar(m, l.down))) return rc;
+    if (!m->moe && l.down.present() && (rc = repack_planar(m, l.down))) return rc;
   }
+  if (m->moe && (rc = moe_buffers(m))) return rc;
   // embed_token's rows (num_elements / hidden) and the LM head of project_lm_head
   // (src/qwen_deepseek.rs:584-632): output.weight, else token_embd.weight (ModelWeights' tied
   // fallback, src/weights.rs:1110-1126), with logits_len = infer_logits_buffer_len
@@ -776,6 +1033,11 @@ extern "C" int jero_hip_decode_step(jero_model* m, void* stream) {
     if (rc) return rc;
     if ((rc = snap(tr(L, TraceLayout::kXMid), m->hidden, 4 * size_t(c.hidden)))) return rc;
     // FFN: RMSNorm -> gate|up -> SwiGLU -> down + residual
+    if (m->moe) {  // dispatch_qwen3_moe_ffn (src/qwen_deepseek.rs:1286-1300)
+      float* tr_logits = m->trace && 2 * c.ffn >= l.n_experts ? trf(L, TraceLayout::kGu) : nullptr;
+      if ((rc = moe_ffn_step(m, l, eps_ffn, s, trf(L, TraceLayout::kXnFfn), tr_logits))) return rc;
+      continue;
+    }
     if (l.gu_split) {
       // gate and up apart (absent: fallback slices of the normalised input, scales 0.5 and 0.25,
       // run_dense_swiglu_ffn src/qwen_deepseek.rs:696-725), then SwiGLU
@@ -917,6 +1179,19 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
   const TraceLayout tl = trace_layout(c);
   if (m->trace && m->trace_bytes < size_t(n) * tl.total)
     return fail(JERO_ERR_TENSOR_BOUNDS, "prefill: the trace buffer holds fewer than " + std::to_string(n) + " steps");
+  if (m->moe) {
+    // a model with an MoE spec: run_prefill_with_hidden's own token loop (src/qwen_deepseek.rs:2298-2312),
+    // one decode step per prompt token (its trace at t * jero_hip_model_trace_bytes)
+    uint8_t* const trace0 = m->trace;
+    int rc = JERO_OK;
+    for (int64_t t = 0; t < n && !rc; t++) {
+      m->trace = trace0 ? trace0 + size_t(t) * tl.total : nullptr;
+      rc = launch_set_state(m->token, m->pos, m->status, tokens[t], pos0 + t, static_cast<hipStream_t>(stream));
+      if (!rc) rc = jero_hip_decode_step(m, stream);
+    }
+    m->trace = trace0;
+    return rc;
+  }
   int rc = prefill_buffers(m, n, pos0);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -48,6 +48,8 @@ struct MoeArgs {
   float* y;          // [T][hidden]
   bool accumulate;   // y += the routed sum (y holds the values to add onto) instead of y =, in the
                      // reference's order: ((y + w0 e0) + w1 e1) + ...
+  float* resid;      // null, or [T][hidden] the layer output is added to: resid += that sum (the
+                     // decode step's residual, src/qwen_deepseek.rs:1301-1303), y not written
   int32_t* sel_idx;  // [T][k]
   float* sel_w;      // [T][k]
   // workspace carve-out (set by launch_moe)

@@ -585,7 +585,7 @@ __global__ void __launch_bounds__(256) moe1_down_kernel(const uint8_t* __restric
                                                         int U, int H, const float* __restrict__ act, int ffn,
                                                         int64_t aq_rb, int k, const int32_t* __restrict__ sel_idx,
                                                         const float* __restrict__ sel_w, float* __restrict__ y, int RW,
-                                                        int upg, int accumulate) {
+                                                        int upg, int accumulate, float* __restrict__ resid) {
   using Ut = Unit<F>;
   using W = typename Ut::W;
   constexpr int G = kWave / LPR;
@@ -656,7 +656,8 @@ __global__ void __launch_bounds__(256) moe1_down_kernel(const uint8_t* __restric
     if (hbase + r >= H) continue;
     float acc = accumulate ? y[hbase + r] : 0.f;
     for (int j = 0; j < k; j++) acc += s_w[j] * s_dot[j * RW + r];
-    y[hbase + r] = acc;
+    if (resid) resid[hbase + r] += acc;
+    else y[hbase + r] = acc;
   }
 }
 
@@ -1090,13 +1091,15 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU)) moe_mfma_kernel(cons
 
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ yd, const float* __restrict__ w,
                                                           const int32_t* __restrict__ inv, int T, int k, int H,
-                                                          float* __restrict__ y, int accumulate) {
+                                                          float* __restrict__ y, int accumulate,
+                                                          float* __restrict__ resid) {
   const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= int64_t(T) * H) return;
   const int t = int(idx / H), h = int(idx % H);
   float acc = accumulate ? y[idx] : 0.f;
   for (int j = 0; j < k; j++) acc += w[t * k + j] * yd[int64_t(inv[t * k + j]) * H + h];
-  y[idx] = acc;
+  if (resid) resid[idx] += acc;
+  else y[idx] = acc;
 }
 
 // ---------------------------------------------------------------- launch plumbing
@@ -1194,7 +1197,7 @@ void down1_one(const MoeArgs& a, hipStream_t s) {
   const size_t lds = size_t(a.top_k) * size_t(arb) + sizeof(float) * size_t(a.top_k) * RW;
   hipLaunchKernelGGL((moe1_down_kernel<F, LPR, UPL>), dim3(unsigned((a.hidden + RW - 1) / RW)), dim3(256), lds, s,
                      static_cast<const uint8_t*>(a.down), a.E * a.hidden, row_bytes(F, a.ffn), U, int(a.hidden), a.act,
-                     int(a.ffn), arb, a.top_k, a.sel_idx, a.sel_w, a.y, RW, upg, int(a.accumulate));
+                     int(a.ffn), arb, a.top_k, a.sel_idx, a.sel_w, a.y, RW, upg, int(a.accumulate), a.resid);
 }
 
 template <int F>
@@ -1397,7 +1400,7 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   }
   const int64_t total = a.T * a.hidden;
   hipLaunchKernelGGL(moe_combine_kernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, s, a.yd, a.sel_w, L.inv,
-                     int(a.T), a.top_k, int(a.hidden), a.y, int(a.accumulate));
+                     int(a.T), a.top_k, int(a.hidden), a.y, int(a.accumulate), a.resid);
   return check_launch("moe combine");
 }
 

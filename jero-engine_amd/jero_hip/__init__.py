@@ -86,6 +86,7 @@ _SIGS = {
     "jero_hip_moe_trace_view": (_I32, [_P, _I64, _I64, _I32, _I64, _I64, C.POINTER(_P), C.POINTER(_P),
                                        C.POINTER(C.c_int)]),
     "jero_hip_model_create": (_I32, [_P, C.POINTER(_P)]),
+    "jero_hip_model_set_moe": (_I32, [_P, _I64, _I32, _I64, _I32]),
     "jero_hip_model_destroy": (_I32, [_P]),
     "jero_hip_model_set_tensor": (_I32, [_P, C.c_char_p, _I32, _P, _SZ, _I64, _I64, _I32]),
     "jero_hip_model_finalize": (_I32, [_P]),
@@ -740,17 +741,22 @@ class ForwardModel:
 
 
 class DecodeModel:
-    """A device-resident dense decoder (Qwen3 / Llama layout): the ArchRecipe::decode_step path
-    of the reference (src/qwen_deepseek.rs:1441-1460) with ctx state (token, position, logits)
-    held on the device."""
+    """A device-resident decoder (Qwen3 / Llama layout, dense or, with moe, Qwen3-MoE): the
+    ArchRecipe::decode_step path of the reference (src/qwen_deepseek.rs:1441-1460) with ctx state
+    (token, position, logits) held on the device.  moe = (num_experts, top_k, expert_ffn_dim,
+    use_shared), the recipe's MoeDispatchSpec (jero_hip_model_set_moe)."""
 
     def __init__(self, hidden, ffn, n_layers, vocab, n_heads_q, n_heads_kv, head_dim, rms_eps, rope_theta,
-                 kv_capacity, kv_dtype=KV_F16, qk_norm=True):
+                 kv_capacity, kv_dtype=KV_F16, qk_norm=True, moe=None):
         self.cfg = ModelConfig(hidden, ffn, n_layers, vocab, n_heads_q, n_heads_kv, head_dim, rms_eps, rope_theta,
                                kv_capacity, kv_dtype, 1 if qk_norm else 0)
         h = C.c_void_p()
         check(lib().jero_hip_model_create(C.byref(self.cfg), C.byref(h)))
         self.h = h
+        self.moe = tuple(moe) if moe is not None else None
+        if moe is not None:
+            E, k, F, shared = moe
+            check(lib().jero_hip_model_set_moe(self.h, E, k, F, 1 if shared else 0))
 
     def close(self):
         if self.h:
@@ -771,12 +777,18 @@ class DecodeModel:
         try:
             hp = g.hyperparams()
             m = cls(hp["hidden"], hp["ffn"], hp["n_layers"], hp["vocab"], hp["n_heads_q"], hp["n_heads_kv"],
-                    hp["head_dim"], hp["rms_eps"], hp["rope_theta"], kv_capacity, kv_dtype, hp["qk_norm"])
+                    hp["head_dim"], hp["rms_eps"], hp["rope_theta"], kv_capacity, kv_dtype, hp["qk_norm"],
+                    hp.get("moe"))
             names = ["token_embd.weight", "output.weight", "output_norm.weight"]
             per = ["attn_norm", "ffn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up",
                    "ffn_down"] + (["attn_q_norm", "attn_k_norm"] if hp["qk_norm"] else [])
+            if hp.get("moe"):
+                per += ["ffn_gate_inp", "ffn_gate_exps", "ffn_up_exps", "ffn_down_exps", "ffn_gate_shexp",
+                        "ffn_up_shexp", "ffn_down_shexp"]
             names += [f"blk.{i}.{b}.weight" for i in range(hp["n_layers"]) for b in per]
             present = set(g.tensor_names())
+            if hp.get("moe"):  # the routing bias is refused at finalize (select_experts_with_optional_bias)
+                names += [n for n in present if n.endswith(".exp_probs_b.bias")]
             for name in names:
                 # an absent tensor takes the reference's default (norms 1.0, the projections'
                 # deterministic slice, the tied head, embed_token's deterministic row)
@@ -1032,9 +1044,24 @@ class GGUFFile:
         if not hd:
             k = self.tensor("blk.0.attn_k.weight")
             hd = k["dims"][1] // nkv if k["dims"][1] % nkv == 0 else hidden // nq
-        ffn = self.meta_int(f"{a}.feed_forward_length", 0) or self.tensor("blk.0.ffn_gate.weight")["dims"][1]
+        ffn = self.meta_int(f"{a}.feed_forward_length", 0)
+        if not ffn and "blk.0.ffn_gate.weight" in names:
+            ffn = self.tensor("blk.0.ffn_gate.weight")["dims"][1]
         vocab = self.meta_int(f"{a}.vocab_size", 0) or self.tensor("output.weight")["dims"][1]
         eps = self.meta_float(f"{a}.attention.layer_norm_rms_epsilon", 1e-6)
         theta = self.meta_float(f"{a}.rope.freq_base", 10000.0)
+        # MoE (GgufHyperparams' expert_count, expert_used_count, expert_feed_forward_length and
+        # expert_shared_count, src/capability.rs:58-65, 428-455): the Qwen3-MoE recipe's spec
+        moe = None
+        n_exp = self.meta_int(f"{a}.expert_count", 0)
+        if n_exp:
+            top_k = self.meta_int(f"{a}.expert_used_count", 0)
+            f_exp = self.meta_int(f"{a}.expert_feed_forward_length", 0) or \
+                self.meta_int(f"{a}.expert.feed_forward_length", 0)
+            if not f_exp and "blk.0.ffn_gate_exps.weight" in names:
+                f_exp = self.tensor("blk.0.ffn_gate_exps.weight")["dims"][1]
+            shared = self.meta_int(f"{a}.expert_shared_count", 0) or self.meta_int(f"{a}.expert.shared_count", 0)
+            moe = (n_exp, top_k, f_exp, shared > 0)
+        ffn = ffn or (moe[2] if moe else 0)
         return dict(hidden=hidden, ffn=ffn, n_layers=n_layers, vocab=vocab, n_heads_q=nq, n_heads_kv=nkv,
-                    head_dim=hd, rms_eps=eps, rope_theta=theta, qk_norm="blk.0.attn_q_norm.weight" in names)
+                    head_dim=hd, rms_eps=eps, rope_theta=theta, qk_norm="blk.0.attn_q_norm.weight" in names, moe=moe)

@@ -782,20 +782,22 @@ static int proj_or_det(const jo_tensor *w, int64_t in_len, int64_t out_len, cons
   return jo_matvec_q(w->quant, w->data, in_len, out_len, in, out, threads, q8_trace);
 }
 
-int jo_decode_layer(const jo_model *M, float *kv, int64_t L, float *x, int64_t pos, int threads,
-                    const jo_layer_trace *tr) {
-  const int64_t H = M->hidden, F = M->ffn, qd = (int64_t)M->nq * M->hd, kvd = (int64_t)M->nkv * M->hd;
+/* The attention sublayer of layer L (src/qwen_deepseek.rs:1262-1275 with
+ * run_dense_attention_sublayer_scaled :984-1097): x += Wo(attention(RMSNorm(x))); writes K/V of
+ * `pos` into layer L's rings. */
+int jo_decode_attn(const jo_model *M, float *kv, int64_t L, float *x, int64_t pos, int threads,
+                   const jo_layer_trace *tr) {
+  const int64_t H = M->hidden, qd = (int64_t)M->nq * M->hd, kvd = (int64_t)M->nkv * M->hd;
   const int64_t cap = M->kv_capacity;
-  /* the attention sublayer and QK-norm use rms_eps as given; the FFN norm rms_eps.max(1e-6) (:1251) */
-  const float eps_attn = M->eps, eps_ffn = M->eps > 1e-6f ? M->eps : 1e-6f;
+  /* the attention sublayer and QK-norm use rms_eps as given */
+  const float eps_attn = M->eps;
   static const jo_layer_trace none;
   if (!tr) tr = &none;
   if (L < 0 || L >= M->n_layers || cap <= 0 || pos < 0) return -1;
   const jo_layer *ly = &M->layers[L];
   float *xn = (float *)malloc((size_t)H * 4), *qkv = (float *)malloc((size_t)(qd + 2 * kvd) * 4);
   float *att = (float *)malloc((size_t)qd * 4), *proj = (float *)malloc((size_t)H * 4);
-  float *gu = (float *)malloc((size_t)F * 8), *a = (float *)malloc((size_t)F * 4);
-  int rc = (!xn || !qkv || !att || !proj || !gu || !a) ? -1 : 0;
+  int rc = (!xn || !qkv || !att || !proj) ? -1 : 0;
   float *q = qkv, *k = qkv + qd, *v = qkv + qd + kvd;
   if (!rc) {
     jo_rmsnorm(xn, x, ly->attn_norm, H, eps_attn);
@@ -830,6 +832,28 @@ int jo_decode_layer(const jo_model *M, float *kv, int64_t L, float *x, int64_t p
     rc |= proj_or_det(&ly->wo, qd, H, att, proj, 0.25f, threads, tr->q8_wo); /* :1086-1092 */
     for (int64_t i = 0; i < H; i++) x[i] += proj[i];
     if (tr->x_mid) memcpy(tr->x_mid, x, (size_t)H * 4);
+  }
+  free(xn);
+  free(qkv);
+  free(att);
+  free(proj);
+  return rc;
+}
+
+int jo_decode_layer(const jo_model *M, float *kv, int64_t L, float *x, int64_t pos, int threads,
+                    const jo_layer_trace *tr) {
+  const int64_t H = M->hidden, F = M->ffn;
+  /* the FFN norm uses rms_eps.max(1e-6) (:1251) */
+  const float eps_ffn = M->eps > 1e-6f ? M->eps : 1e-6f;
+  static const jo_layer_trace none;
+  if (!tr) tr = &none;
+  int rc = jo_decode_attn(M, kv, L, x, pos, threads, tr);
+  if (rc) return rc;
+  const jo_layer *ly = &M->layers[L];
+  float *xn = (float *)malloc((size_t)H * 4), *proj = (float *)malloc((size_t)H * 4);
+  float *gu = (float *)malloc((size_t)F * 8), *a = (float *)malloc((size_t)F * 4);
+  rc = (!xn || !proj || !gu || !a) ? -1 : 0;
+  if (!rc) {
     jo_rmsnorm(xn, x, ly->ffn_norm, H, eps_ffn);
     if (tr->xn_ffn) memcpy(tr->xn_ffn, xn, (size_t)H * 4);
     /* run_dense_swiglu_ffn (:696-725): gate 0.5, up 0.25, down 0.125 */
@@ -844,8 +868,6 @@ int jo_decode_layer(const jo_model *M, float *kv, int64_t L, float *x, int64_t p
     for (int64_t i = 0; i < H; i++) x[i] += proj[i];
   }
   free(xn);
-  free(qkv);
-  free(att);
   free(proj);
   free(gu);
   free(a);

@@ -190,6 +190,12 @@ typedef struct jo_layer_trace {
   void *q8_down;
 } jo_layer_trace;
 
+/* The attention sublayer of layer L (src/qwen_deepseek.rs:1262-1275, run_dense_attention_sublayer_scaled
+ * :984-1097): x += Wo(attention(RMSNorm(x))) in place; writes K/V of `pos` into layer L's rings;
+ * fills tr's fields up to x_mid.  A Qwen3-MoE layer's FFN (dispatch_qwen3_moe_ffn) follows it in
+ * pyoracle.moe_decode_step. */
+int jo_decode_attn(const jo_model *mdl, float *kv, int64_t layer, float *x, int64_t pos, int threads,
+                   const jo_layer_trace *tr);
 /* Layer L of execute_token_standard_with_hidden (src/qwen_deepseek.rs:1262-1302, with
  * run_dense_attention_sublayer_scaled :984-1097 and run_dense_swiglu_ffn :696-727): x [hidden]
  * in, the layer's output out (in place); writes K/V of `pos` into layer L's rings of kv. */

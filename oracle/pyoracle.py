@@ -54,6 +54,7 @@ def lib():
             "jo_moe_ffn": (I32, [P, I64, I64, I32, I32, P, I32, P, I32, P, I64, I64, P, P, P, P, I32]),
             "jo_decode_step": (I32, [P, P, I32, I64, P, I32]),
             "jo_decode_layer": (I32, [P, P, I64, P, I64, I32, P]),
+            "jo_decode_attn": (I32, [P, P, I64, P, I64, I32, P]),
             "jo_decode_head": (I32, [P, P, P, I32, P, P]),
             "jo_read_f32_weight_or_default": (None, [I32, P, I64, I64, F, P]),
             "jo_logits_len": (I64, [I64, I32, I64]),
@@ -247,32 +248,32 @@ def _n_el(dims):
     return n
 
 
-def proj_or_det(w, x, out_len, scale):
+def proj_or_det(w, x, out_len, scale, threads=1):
     """project_or_deterministic_slice (src/gemma.rs:841-860): the GEMV when the tensor is present
     with exactly out_len * len(x) elements, else out[i] = x[i % len(x)] * scale."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     if w is not None and _n_el(w[2]) == out_len * x.size:
-        return vec_dot(w[0], w[1], x.size, out_len, x)
+        return vec_dot(w[0], w[1], x.size, out_len, x, threads)
     return (x[np.arange(out_len) % x.size] * np.float32(scale)).astype(np.float32)
 
 
-def single_swiglu_expert(g, u, d, x, expert_ffn_dim):
+def single_swiglu_expert(g, u, d, x, expert_ffn_dim, threads=1):
     """run_single_swiglu_expert (src/qwen_deepseek.rs:748-771): eff_ffn from the gate's element
     count, then matvec_any of gate and up over x, SwiGLU, matvec_any of down."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     H, ge = x.size, _n_el(g[2])
     F = ge // H if ge > 0 and ge % H == 0 else max(expert_ffn_dim, 4)
-    act = swiglu(vec_dot(g[0], g[1], H, F, x), vec_dot(u[0], u[1], H, F, x))
-    return vec_dot(d[0], d[1], F, H, act)
+    act = swiglu(vec_dot(g[0], g[1], H, F, x, threads), vec_dot(u[0], u[1], H, F, x, threads))
+    return vec_dot(d[0], d[1], F, H, act, threads)
 
 
-def dense_swiglu_ffn(weights, layer, expert_ffn_dim, x):
+def dense_swiglu_ffn(weights, layer, expert_ffn_dim, x, threads=1):
     """run_dense_swiglu_ffn (src/qwen_deepseek.rs:696-727)."""
     F = max(expert_ffn_dim, 4)
     name = lambda t: f"blk.{layer}.{t}.weight"
-    g = proj_or_det(weights.get(name("ffn_gate")), x, F, 0.5)
-    u = proj_or_det(weights.get(name("ffn_up")), x, F, 0.25)
-    return proj_or_det(weights.get(name("ffn_down")), swiglu(g, u), len(x), 0.125)
+    g = proj_or_det(weights.get(name("ffn_gate")), x, F, 0.5, threads)
+    u = proj_or_det(weights.get(name("ffn_up")), x, F, 0.25, threads)
+    return proj_or_det(weights.get(name("ffn_down")), swiglu(g, u), len(x), 0.125, threads)
 
 
 def _expert_slice(weights, stacked, indexed, e, n):
@@ -286,7 +287,7 @@ def _expert_slice(weights, stacked, indexed, e, n):
     return weights.get(indexed)
 
 
-def moe_layer(x, layer, num_experts, top_k, expert_ffn_dim, use_shared_expert, weights):
+def moe_layer(x, layer, num_experts, top_k, expert_ffn_dim, use_shared_expert, weights, threads=1):
     """dispatch_qwen3_moe_ffn (src/qwen_deepseek.rs:847-951) without the exp_probs_b bias: returns
     (out [hidden] f32, [(expert, weight)])."""
     x = np.ascontiguousarray(x, dtype=np.float32)
@@ -295,24 +296,24 @@ def moe_layer(x, layer, num_experts, top_k, expert_ffn_dim, use_shared_expert, w
     out = np.zeros(H, np.float32)
     sh = [weights.get(name(t)) for t in ("ffn_gate_shexp", "ffn_up_shexp", "ffn_down_shexp")]
     if use_shared_expert and all(t is not None for t in sh):
-        out += single_swiglu_expert(*sh, x, expert_ffn_dim)
+        out += single_swiglu_expert(*sh, x, expert_ffn_dim, threads)
     router = weights.get(name("ffn_gate_inp"))
     if num_experts == 0 or top_k == 0 or router is None:
-        out += dense_swiglu_ffn(weights, layer, expert_ffn_dim, x)
+        out += dense_swiglu_ffn(weights, layer, expert_ffn_dim, x, threads)
         return out, []
     re = _n_el(router[2])
     eff = min(re // H, num_experts) if re > 0 and re % H == 0 else num_experts
-    logits = vec_dot(router[0], router[1], H, eff, x)
+    logits = vec_dot(router[0], router[1], H, eff, x, threads)
     sel = select_top_k(logits, top_k, True)
     ran = False
     for e, w in sel:
         parts = [_expert_slice(weights, f"blk.{layer}.ffn_{k}_exps.weight", f"blk.{layer}.ffn_{k}_exps.{e}.weight", e,
                                eff) for k in ("gate", "up", "down")]
         if all(p is not None for p in parts):
-            out += np.float32(w) * single_swiglu_expert(*parts, x, expert_ffn_dim)
+            out += np.float32(w) * single_swiglu_expert(*parts, x, expert_ffn_dim, threads)
             ran = True
     if not ran:
-        out += dense_swiglu_ffn(weights, layer, expert_ffn_dim, x)
+        out += dense_swiglu_ffn(weights, layer, expert_ffn_dim, x, threads)
     return out, sel
 
 
@@ -475,6 +476,42 @@ class DecodeModel:
                                    C.byref(tr) if tr is not None else None)
         assert rc == 0
         return x, out
+
+    def attn(self, kv, L, x, pos, threads=1):
+        """jo_decode_attn: the attention sublayer of layer L; returns x after its residual."""
+        x = np.array(x, np.float32, copy=True)
+        assert lib().jo_decode_attn(C.byref(self.model), _p(kv), L, _p(x), pos, threads, None) == 0
+        return x
+
+    def moe_step(self, kv, token, pos, moe, weights, threads=1, trace=None):
+        """execute_token_standard_with_hidden (src/qwen_deepseek.rs:1239-1314) for a model with a
+        MoE spec (Qwen3-MoE, :1286-1300): per layer the attention sublayer (jo_decode_attn), then
+        RMSNorm with ffn_norm (rms_eps.max(1e-6), :1250, :1278-1284), dispatch_qwen3_moe_ffn
+        (moe_layer) and the residual hidden += out (:1301-1303); then the head.  moe = (num_experts,
+        top_k, expert_ffn_dim, use_shared); weights {name: (quant, data, dims)} as moe_layer reads
+        them.  trace (a list, optional) receives per layer (x_mid, xn, router logits, out, sel)."""
+        s = self.spec
+        E, k, F, shared = moe
+        eps_ffn = max(s["eps"], 1e-6)
+        x = self.embed(token)
+        for L in range(s["n_layers"]):
+            x = self.attn(kv, L, x, pos, threads)
+            norm = weights.get(f"blk.{L}.ffn_norm.weight")
+            nw = read_f32_weight_or_default(norm[0], norm[1], _n_el(norm[2]), s["hidden"]) if norm is not None \
+                else np.ones(s["hidden"], np.float32)
+            xn = rmsnorm(x, nw, eps_ffn)
+            out, sel = moe_layer(xn, L, E, k, F, shared, weights, threads)
+            if trace is not None:
+                router = weights.get(f"blk.{L}.ffn_gate_inp.weight")
+                lg = None
+                if router is not None and E > 0 and k > 0:
+                    re = _n_el(router[2])
+                    H = s["hidden"]
+                    eff = min(re // H, E) if re > 0 and re % H == 0 else E
+                    lg = vec_dot(router[0], router[1], H, eff, xn)
+                trace.append((x.copy(), xn, lg, out, sel))
+            x = (x + out).astype(np.float32)
+        return self.head(x, threads)[0]
 
     def head(self, x, threads=1):
         """jo_decode_head: (logits, xn_head, q8_head)."""

@@ -48,7 +48,7 @@ def gguf_bytes(arch, kvs, tensors, alignment=32, version=3, offsets=None):
     data_start = (len(head) + alignment - 1) // alignment * alignment
     buf = bytearray(head.ljust(data_start, b"\0"))
     for (_, _, _, payload), off in zip(tensors, offs):
-        if off > 1 << 24:  # an overridden offset far past any data: the payload is left out
+        if offsets is not None and off > 1 << 24:  # an overridden offset far past any data: the payload is left out
             continue
         end = data_start + off + len(payload)
         if len(buf) < end:

@@ -1,4 +1,4 @@
-"""Random-init dense decoder weights (Qwen3 layout) for the decode parity tests.
+"""Random-init decoder weights (Qwen3 layout, dense or Qwen3-MoE) for the decode parity tests.
 
 Quantized matrices are uniform random payload bytes with N(0, 0.02)-scale fields (qdata);
 norm weights are 1 + 0.1 N(0, 1).  The Q4_K_M mix follows llama.cpp's public recipe:
@@ -45,6 +45,51 @@ def build(spec, seed=0, mix="q4_k_m"):
         mat(p + "ffn_up.weight", Q4_K, H, F)
         mat(p + "ffn_down.weight", Q6_K if i in hi else Q4_K, F, H)
     return t
+
+
+def build_moe(spec, moe, seed=0, router_layers=None, shared_quant=Q8_0):
+    """A Qwen3-MoE-shaped model (the Qwen3 attention of build, then per layer
+    dispatch_qwen3_moe_ffn's tensors): an F32 router [hidden, E] of N(0, 0.02) weights, the stacked
+    Q4_K gate / up experts [hidden, F, E] and Q6_K down experts [F, hidden, E], and, when moe's
+    use_shared is set, a shared expert of 2 F rows in shared_quant.  Layers not in router_layers
+    (all by default) have no router: they take run_dense_swiglu_ffn with [hidden, F] Q4_K
+    gate / up and Q6_K down.  moe = (E, top_k, F, use_shared).  Returns (tensors as build returns
+    them, {name: (quant, data, dims)} as pyoracle.moe_layer reads them)."""
+    from qdata import rand_float_weights
+    E, k, F, shared = moe
+    H, L = spec["hidden"], spec["n_layers"]
+    t = build(spec, seed)
+    for i in range(L):
+        for b in ("ffn_gate", "ffn_up", "ffn_down"):
+            del t[f"blk.{i}.{b}.weight"]
+    w = {}
+    s = [seed * 100 + 50]
+
+    def mat(name, quant, dims, rows, n_in, gen=rand_weights):
+        s[0] += 1
+        arr = gen(quant, rows, n_in, s[0])
+        n_out = int(np.prod(dims[1:]))
+        t[name] = (quant, arr, dims[0], n_out)
+        w[name] = (quant, arr, list(dims))
+
+    for i in range(L):
+        p = f"blk.{i}."
+        if router_layers is None or i in router_layers:
+            mat(p + "ffn_gate_inp.weight", F32, (H, E), E, H, rand_float_weights)
+            mat(p + "ffn_gate_exps.weight", Q4_K, (H, F, E), E * F, H)
+            mat(p + "ffn_up_exps.weight", Q4_K, (H, F, E), E * F, H)
+            mat(p + "ffn_down_exps.weight", Q6_K, (F, H, E), E * H, F)
+        else:
+            mat(p + "ffn_gate.weight", Q4_K, (H, F), F, H)
+            mat(p + "ffn_up.weight", Q4_K, (H, F), F, H)
+            mat(p + "ffn_down.weight", Q6_K, (F, H), H, F)
+        if shared:
+            mat(p + "ffn_gate_shexp.weight", shared_quant, (H, 2 * F), 2 * F, H)
+            mat(p + "ffn_up_shexp.weight", shared_quant, (H, 2 * F), 2 * F, H)
+            mat(p + "ffn_down_shexp.weight", shared_quant, (2 * F, H), H, 2 * F)
+        nq, nd = t[p + "ffn_norm.weight"][:2]
+        w[p + "ffn_norm.weight"] = (nq, nd, [H])
+    return t, w
 
 
 def oracle_tensors(t):

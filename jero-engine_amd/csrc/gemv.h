@@ -12,6 +12,12 @@ bool is_float_weight(int quant);
 // Enqueues y = W x for unquantized weight rows (any n_in).
 int launch_matvec_float(int quant, const void* w, int64_t n_in, int64_t n_out, const float* x, float* y,
                         hipStream_t s);
+// xn = RMSNorm(x) * nw (eps) and y = W xn over F32 rows in one launch, for inputs router_norm_fits
+// accepts (F32, n_in % 4 == 0 and <= kRouterMaxK, w / x / xn 16-byte aligned); xn is written too.
+constexpr int64_t kRouterMaxK = 8192;  // xn staged in 32 KB of LDS
+bool router_norm_fits(int quant, const void* w, int64_t n_in, const float* x, const float* xn);
+int launch_router_norm(const void* w, int64_t n_in, int64_t n_out, const float* x, const float* nw, float eps,
+                       float* xn, float* y, hipStream_t s);
 // Largest n_in the register-resident activation layout supports for a weight format (longer
 // rows run the K-looped kernel).
 int max_gemv_k(int quant);

@@ -114,7 +114,99 @@ void launch_fq(const uint8_t* w, int64_t K, int64_t N, const float* x, float* y,
   else launch_q<Q, false>(w, rb, K, N, x, y, s);
 }
 
+// The Qwen3-MoE FFN's first two steps in one launch (src/qwen_deepseek.rs:1278-1284, 882-892):
+// xn = x * (1 / sqrt(mean(x^2) + eps)) * nw, then the router logits y = W xn over F32 rows of
+// K elements (16-byte aligned, K % 4 == 0).  Every workgroup computes the norm itself (the same
+// per-thread sums in the same order, so every workgroup holds the same xn bits) into LDS; the
+// first also stores xn for the expert kernels.  Each lane's first weight pieces are loaded
+// before the norm, unconditionally (clamped), so the prologue overlaps the row fetch.
+constexpr int kRouterPieces = 8;  // pieces per lane in flight: one pass over a 2048-wide row at LPR 64
+
+template <int LPR>
+__global__ void __launch_bounds__(kFloatThreads) router_norm_kernel(const uint8_t* __restrict__ w, int64_t rb,
+                                                                    int64_t K, int64_t N, const float* __restrict__ x,
+                                                                    const float* __restrict__ nw, float eps,
+                                                                    float* __restrict__ xn, float* __restrict__ y) {
+  extern __shared__ float s_x[];  // K floats
+  __shared__ float s_tmp[kFloatThreads / kWave];
+  constexpr int G = kWave / LPR;
+  const int lane = threadIdx.x & 63, g = lane / LPR, c = lane % LPR;
+  const int64_t row = ((int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave) * G + g;
+  const int64_t rr = row < N ? row : N - 1;
+  const uint8_t* wr = w + rr * rb;
+  const int64_t pieces = K / 4;
+  u32x4 v[kRouterPieces];
+#pragma unroll
+  for (int i = 0; i < kRouterPieces; i++) {
+    const int64_t p = c + int64_t(LPR) * i;
+    v[i] = *reinterpret_cast<const u32x4*>(wr + 16 * (p < pieces ? p : pieces - 1));
+  }
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < K; i += blockDim.x) ss += x[i] * x[i];
+  ss = wave_sum_dpp(ss);
+  if (lane == 0) s_tmp[threadIdx.x >> 6] = ss;
+  lds_barrier();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < kFloatThreads / kWave; i++) t += s_tmp[i];
+  const float inv = 1.0f / sqrtf(t / float(K) + eps);
+  for (int64_t i = threadIdx.x; i < K; i += blockDim.x) {
+    const float e = x[i] * inv * nw[i];
+    s_x[i] = e;
+    if (blockIdx.x == 0) xn[i] = e;
+  }
+  lds_barrier();
+  float acc = 0.f;
+  for (int64_t p0 = c;; p0 += int64_t(LPR) * kRouterPieces) {
+#pragma unroll
+    for (int i = 0; i < kRouterPieces; i++) {
+      const int64_t p = p0 + int64_t(LPR) * i;
+      if (p < pieces) {
+        const float4 xv = *reinterpret_cast<const float4*>(s_x + 4 * p);
+        acc = fmaf(__uint_as_float(v[i].x), xv.x, acc);
+        acc = fmaf(__uint_as_float(v[i].y), xv.y, acc);
+        acc = fmaf(__uint_as_float(v[i].z), xv.z, acc);
+        acc = fmaf(__uint_as_float(v[i].w), xv.w, acc);
+      }
+    }
+    const int64_t next = p0 + int64_t(LPR) * kRouterPieces;
+    if (next - c >= pieces) break;  // uniform across the wave: every lane's chunk start is p0 - c apart
+#pragma unroll
+    for (int i = 0; i < kRouterPieces; i++) {
+      const int64_t p = next + int64_t(LPR) * i;
+      v[i] = *reinterpret_cast<const u32x4*>(wr + 16 * (p < pieces ? p : pieces - 1));
+    }
+  }
+  acc = group_sum_last<LPR>(acc);
+  if (c == LPR - 1 && row < N) y[row] = acc;
+}
+
 }  // namespace
+
+bool router_norm_fits(int quant, const void* w, int64_t n_in, const float* x, const float* xn) {
+  return quant == JERO_F32 && n_in % 4 == 0 && n_in >= 4 && n_in <= kRouterMaxK &&
+         (reinterpret_cast<uintptr_t>(w) & 15u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+         (reinterpret_cast<uintptr_t>(xn) & 15u) == 0;
+}
+
+int launch_router_norm(const void* w, int64_t n_in, int64_t n_out, const float* x, const float* nw, float eps,
+                       float* xn, float* y, hipStream_t s) {
+  if (!router_norm_fits(JERO_F32, w, n_in, x, xn) || n_out < 1)
+    return fail(JERO_ERR_INVALID_ARGUMENT, "router_norm: unsupported shape or alignment");
+  const uint8_t* wb = static_cast<const uint8_t*>(w);
+  const int64_t rb = 4 * n_in, pieces = n_in / 4;
+  const int lpr = pieces >= 64 ? 64 : pieces >= 32 ? 32 : pieces >= 16 ? 16 : 4;
+  const int64_t waves = (n_out + (kWave / lpr) - 1) / (kWave / lpr);
+  const dim3 grid(unsigned((waves + kFloatThreads / kWave - 1) / (kFloatThreads / kWave)));
+  const size_t lds = sizeof(float) * size_t(n_in);
+  switch (lpr) {
+    case 64: hipLaunchKernelGGL((router_norm_kernel<64>), grid, dim3(kFloatThreads), lds, s, wb, rb, n_in, n_out, x, nw, eps, xn, y); break;
+    case 32: hipLaunchKernelGGL((router_norm_kernel<32>), grid, dim3(kFloatThreads), lds, s, wb, rb, n_in, n_out, x, nw, eps, xn, y); break;
+    case 16: hipLaunchKernelGGL((router_norm_kernel<16>), grid, dim3(kFloatThreads), lds, s, wb, rb, n_in, n_out, x, nw, eps, xn, y); break;
+    default: hipLaunchKernelGGL((router_norm_kernel<4>), grid, dim3(kFloatThreads), lds, s, wb, rb, n_in, n_out, x, nw, eps, xn, y); break;
+  }
+  return check_launch("router (norm + F32 rows)");
+}
 
 bool is_float_weight(int quant) { return quant == JERO_F32 || quant == JERO_F16 || quant == JERO_BF16; }
 

@@ -603,7 +603,11 @@ static int moe_buffers(jero_model* m) {
 // gets xn and the router logits.
 static int moe_ffn_step(jero_model* m, const LayerW& l, float eps, hipStream_t s, float* tr_xn, float* tr_logits) {
   const int64_t H = m->cfg.hidden;
-  int rc = launch_head_norm(m->hidden, static_cast<const float*>(l.ffn_norm.dev), eps, H, m->moe_xn, s);
+  const float* nw = static_cast<const float*>(l.ffn_norm.dev);
+  // an F32 router computes the norm itself (one launch for both); otherwise the norm runs alone
+  const bool fused = l.routed && router_norm_fits(l.router.quant, l.router.dev, H, m->hidden, m->moe_xn);
+  int rc = fused ? launch_router_norm(l.router.dev, H, l.n_experts, m->hidden, nw, eps, m->moe_xn, m->moe_logits, s)
+                 : launch_head_norm(m->hidden, nw, eps, H, m->moe_xn, s);
   if (rc) return rc;
   const bool shared = m->moe_shared && l.gate_shexp.present() && l.up_shexp.present() && l.down_shexp.present();
   if (shared) {  // :860-871
@@ -621,9 +625,9 @@ static int moe_ffn_step(jero_model* m, const LayerW& l, float eps, hipStream_t s
   } else {
     // router logits (matvec_any over the router's eff_experts rows, :882-890)
     const int E = int(l.n_experts);
-    if (is_float_weight(l.router.quant)) {
+    if (!fused && is_float_weight(l.router.quant)) {
       rc = launch_matvec_float(l.router.quant, l.router.dev, H, E, m->moe_xn, m->moe_logits, s);
-    } else if (!(rc = launch_quantize_act(act_format(l.router.quant), m->moe_xn, 1, H, m->moe_xq, s))) {
+    } else if (!fused && !(rc = launch_quantize_act(act_format(l.router.quant), m->moe_xn, 1, H, m->moe_xq, s))) {
       rc = launch_matvec(l.router.quant, l.router.dev, H, E, m->moe_xq, m->moe_logits, nullptr, s);
     }
     if (rc) return rc;

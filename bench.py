@@ -355,6 +355,22 @@ def bench_moe_decode(torch, J, dev, stream, steps, warmup, keep_host):
     e0.synchronize()
     t_tok = s0.elapsed_time(e0) / 1e3 / steps
     tok, pos = m.read_token_pos()
+    # prefill (extra): a 512-token prompt from position 0, every layer's experts as GEMMs over the
+    # tokens each expert was routed (jero_hip_model_prefill's batched MoE pass); timed as the dense
+    # model's prefill is
+    n_pf = 512
+    prompt = torch.tensor(np.random.default_rng(6).integers(0, spec["vocab"], n_pf), dtype=torch.int32).pin_memory()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(PF_REPS + 1)]
+    with torch.cuda.stream(stream):
+        m.prefill(prompt, 0, stream=stream)
+        stream.synchronize()
+        ev[0].record(stream)
+        for r in range(PF_REPS):
+            m.prefill(prompt, 0, stream=stream)
+            ev[r + 1].record(stream)
+    ev[-1].synchronize()
+    pf = np.array([ev[r].elapsed_time(ev[r + 1]) for r in range(PF_REPS)])
+    t_pf = float(np.median(pf)) * 1e-3
     m.close()
     kv_bytes = spec["n_layers"] * 2 * KV_CAP * kvd * 2
     wb = dense_bytes + expert_bytes
@@ -364,7 +380,13 @@ def bench_moe_decode(torch, J, dev, stream, steps, warmup, keep_host):
            "model_bytes": total, "weight_bytes_per_token": wb, "kv_bytes_per_token": kv_bytes,
            "frac_weight_roofline": round(wb / t_tok / 1e9 / HBM_PEAK_GBS, 4),
            "frac_weights_kv_roofline": round((wb + kv_bytes) / t_tok / 1e9 / HBM_PEAK_GBS, 4),
-           "last_token": tok, "position": pos, "graph": "one decode step captured, replayed per token"}
+           "last_token": tok, "position": pos, "graph": "one decode step captured, replayed per token",
+           "prefill": {"tokens": n_pf, "ms": round(t_pf * 1e3, 3), "tok_s": round(n_pf / t_pf, 1),
+                       "ms_p10": round(float(np.percentile(pf, 10)), 3), "ms_p90": round(float(np.percentile(pf, 90)), 3),
+                       "calls": PF_REPS,
+                       "what": "jero_hip_model_prefill of a 512-token prompt from position 0 (attention and "
+                               "projections over the token rows, each layer's experts as GEMMs over the tokens "
+                               "routed to them), eager, prompt in pinned host memory; median of per-call events"}}
     return res, host, host_kv
 
 

@@ -409,7 +409,10 @@ int jero_hip_model_create(const jero_model_config *cfg, jero_model **model);
  * incomplete set of expert tensors make finalize return CapabilityMismatch.  The decode trace of
  * such a layer holds xn_ffn (the FFN's normalised input) and, in gu, the router logits (when
  * 2 * ffn >= E); its q8_ffn, act and q8_down are not written.  jero_hip_model_prefill runs the
- * prompt as decode steps, the reference's own token loop. */
+ * prompt's rows through each layer at once when every layer is routed over an F32 router and no
+ * shared expert runs (the Qwen3-MoE recipe's form): the router logits as one f32 MFMA product
+ * over the rows, the experts as GEMMs over the tokens routed to each; any other MoE model's
+ * prompt runs as decode steps, the reference's own token loop. */
 int jero_hip_model_set_moe(jero_model *model, int64_t n_experts, int top_k, int64_t expert_ffn, int use_shared);
 int jero_hip_model_destroy(jero_model *model);
 /* Copies one tensor to the device (src host memory, or device memory if src_on_device).  A layer

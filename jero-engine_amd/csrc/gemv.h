@@ -18,6 +18,10 @@ constexpr int64_t kRouterMaxK = 8192;  // xn staged in 32 KB of LDS
 bool router_norm_fits(int quant, const void* w, int64_t n_in, const float* x, const float* xn);
 int launch_router_norm(const void* w, int64_t n_in, int64_t n_out, const float* x, const float* nw, float eps,
                        float* xn, float* y, hipStream_t s);
+// Y[rows][n_out] = X[rows][n_in] W^T over F32 weight rows (n_out rows of n_in floats), one launch on
+// the f32 MFMA; n_in a multiple of 64, w and x 16-byte aligned.
+int launch_matmul_f32_rows(const void* w, int64_t n_in, int64_t n_out, const float* x, int64_t rows, float* y,
+                           hipStream_t s);
 // Largest n_in the register-resident activation layout supports for a weight format (longer
 // rows run the K-looped kernel).
 int max_gemv_k(int quant);

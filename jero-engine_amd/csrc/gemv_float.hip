@@ -181,7 +181,86 @@ __global__ void __launch_bounds__(kFloatThreads) router_norm_kernel(const uint8_
   if (c == LPR - 1 && row < N) y[row] = acc;
 }
 
+// Y[t][n] = sum_k X[t][k] W[n][k] over F32 rows: the router logits of a batch of token rows (the
+// batched prefill's form of matvec_f32 per token), on v_mfma_f32_16x16x4f32.  A workgroup owns one
+// 16 x 16 tile (16 rows t, 16 rows n); its four waves take the four quarters of K (whole 64-wide
+// chunks, the first waves one more when the chunk count is not a multiple of 4) and the tile is
+// their sum, wave 0 + 1 + 2 + 3 in that order through LDS.  In a step, lane l supplies
+// A[l % 16][l / 16] = X[t0 + l % 16][k] and B[l / 16][l % 16] = W[n0 + l % 16][k] with the same
+// k = c + 4 (l / 16) + s for both; the lane reads 16 bytes of each row per 16 k, four of them per
+// buffer, two buffers alternating.  D: lane l holds rows 4 (l / 16) + i of column l % 16.
+// K % 64 == 0; rows past T or N are read clamped and not stored.
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kRowsChunk = 64;
+
+__global__ void __launch_bounds__(256) matmul_f32_rows_kernel(const float* __restrict__ w, int64_t K, int64_t N,
+                                                              const float* __restrict__ x, int64_t T,
+                                                              float* __restrict__ y, int64_t tiles_n) {
+  __shared__ v4f s_part[3][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, r = lane & 15, q = lane >> 4;
+  const int64_t tt = int64_t(blockIdx.x) / tiles_n, tn = int64_t(blockIdx.x) - tt * tiles_n;
+  const int64_t chunks = K / kRowsChunk, per = chunks / 4, extra = chunks % 4;
+  const int64_t c_lo = (wv * per + min<int64_t>(wv, extra)) * kRowsChunk;
+  const int64_t c_hi = c_lo + (per + (wv < extra ? 1 : 0)) * kRowsChunk;  // this wave's K range
+  const float* xr = x + min(tt * 16 + r, T - 1) * K + 4 * q;
+  const float* wr = w + min(tn * 16 + r, N - 1) * K + 4 * q;
+  auto load = [&](float4 (&xa)[4], float4 (&wa)[4], int64_t c) {
+    c = min(c, K - kRowsChunk);  // past the end: the last chunk again (not used)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      xa[g] = *reinterpret_cast<const float4*>(xr + c + 16 * g);
+      wa[g] = *reinterpret_cast<const float4*>(wr + c + 16 * g);
+    }
+  };
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  auto steps = [&](const float4 (&xa)[4], const float4 (&wa)[4]) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[g].x, wa[g].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[g].y, wa[g].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[g].z, wa[g].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[g].w, wa[g].w, acc, 0, 0, 0);
+    }
+  };
+  if (c_lo < c_hi) {  // uniform over the wave
+    float4 xa[4], wa[4], xb[4], wb[4];
+    load(xa, wa, c_lo);
+    for (int64_t c = c_lo;; c += 2 * kRowsChunk) {
+      load(xb, wb, c + kRowsChunk);
+      steps(xa, wa);
+      if (c + kRowsChunk >= c_hi) break;
+      load(xa, wa, c + 2 * kRowsChunk);
+      steps(xb, wb);
+      if (c + 2 * kRowsChunk >= c_hi) break;
+    }
+  }
+  if (wv > 0) s_part[wv - 1][lane] = acc;
+  __syncthreads();
+  if (wv == 0) {
+#pragma unroll
+    for (int j = 0; j < 3; j++) acc += s_part[j][lane];
+    const int64_t n = tn * 16 + r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int64_t t = tt * 16 + 4 * q + i;
+      if (n < N && t < T) y[t * N + n] = acc[i];
+    }
+  }
+}
+
 }  // namespace
+
+int launch_matmul_f32_rows(const void* w, int64_t n_in, int64_t n_out, const float* x, int64_t rows, float* y,
+                           hipStream_t s) {
+  if (n_in < kRowsChunk || n_in % kRowsChunk != 0 || n_out < 1 || rows < 1)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "router rows: n_in must be a positive multiple of 64");
+  if ((reinterpret_cast<uintptr_t>(w) & 15u) || (reinterpret_cast<uintptr_t>(x) & 15u))
+    return fail(JERO_ERR_INVALID_ARGUMENT, "router rows: weights and rows must be 16-byte aligned");
+  const int64_t tiles_n = (n_out + 15) / 16, tiles = ((rows + 15) / 16) * tiles_n;
+  hipLaunchKernelGGL(matmul_f32_rows_kernel, dim3(unsigned(tiles)), dim3(256), 0, s,
+                     static_cast<const float*>(w), n_in, n_out, x, rows, y, tiles_n);
+  return check_launch("router rows (F32)");
+}
 
 bool router_norm_fits(int quant, const void* w, int64_t n_in, const float* x, const float* xn) {
   return quant == JERO_F32 && n_in % 4 == 0 && n_in >= 4 && n_in <= kRouterMaxK &&

@@ -63,6 +63,10 @@ struct PrefillBufs {
   float *X = nullptr, *XN = nullptr, *T = nullptr, *T2 = nullptr, *QKV = nullptr, *ATT = nullptr, *GU = nullptr,
         *ACT = nullptr, *RC = nullptr, *ws = nullptr;
   uint8_t* XQ = nullptr;
+  // the MoE FFN over token rows: router logits and selections of one chunk, its workspace
+  float *LG = nullptr, *SW = nullptr;
+  int32_t* SI = nullptr;
+  void* MWS = nullptr;
 };
 
 }  // namespace jero
@@ -1125,6 +1129,20 @@ static int join_side(jero_model* m, hipStream_t s) {
   return JERO_OK;
 }
 
+// Token rows per MoE launch of the batched prefill: the grouping step places at most
+// kRouteLdsPairs (token, slot) pairs.
+static int64_t moe_prefill_chunk(const jero_model* m) { return std::max<int64_t>(1, 8192 / std::max(1, m->moe_top_k)); }
+
+// Whether a model with an MoE spec prefills in batches of token rows: every layer routed over an
+// F32 router (the Qwen3-MoE GGUF form) and no shared expert to run; otherwise the token loop.
+static bool moe_prefill_batched(const jero_model* m) {
+  for (const LayerW& l : m->layers) {
+    if (!l.routed || l.router.quant != JERO_F32 || m->cfg.hidden % 64 != 0) return false;
+    if (m->moe_shared && l.gate_shexp.present() && l.up_shexp.present() && l.down_shexp.present()) return false;
+  }
+  return true;
+}
+
 static int prefill_buffers(jero_model* m, int64_t n, int64_t pos0) {
   const auto& c = m->cfg;
   const int64_t H = c.hidden, F = c.ffn, Q = q_dim(c), KV = kv_dim(c);
@@ -1139,7 +1157,8 @@ static int prefill_buffers(jero_model* m, int64_t n, int64_t pos0) {
   for (void* p : {static_cast<void*>(b.tok), static_cast<void*>(b.X), static_cast<void*>(b.XN),
                   static_cast<void*>(b.T), static_cast<void*>(b.T2), static_cast<void*>(b.QKV), static_cast<void*>(b.ATT),
                   static_cast<void*>(b.GU), static_cast<void*>(b.ACT), static_cast<void*>(b.RC),
-                  static_cast<void*>(b.ws), static_cast<void*>(b.XQ)})
+                  static_cast<void*>(b.ws), static_cast<void*>(b.XQ), static_cast<void*>(b.LG),
+                  static_cast<void*>(b.SW), static_cast<void*>(b.SI), b.MWS})
     if (p) dev_free(m, p);
   b = PrefillBufs{};
   auto act_row = [](int64_t k) { return std::max(k / 32 * 36, k / 256 * 292); };
@@ -1162,6 +1181,15 @@ static int prefill_buffers(jero_model* m, int64_t n, int64_t pos0) {
   b.ws = static_cast<float*>(p);
   if ((rc = dev_alloc(m, xq_row * size_t(rows), &p))) return rc;
   b.XQ = static_cast<uint8_t*>(p);
+  if (m->moe) {
+    const int64_t ch = std::min(rows, moe_prefill_chunk(m)), k = std::max(1, m->moe_top_k);
+    int64_t E = 1, Fe = 1;
+    for (const LayerW& l : m->layers) E = std::max(E, l.n_experts), Fe = std::max(Fe, l.exp_ffn);
+    if ((rc = f32(ch * E, &b.LG)) || (rc = f32(ch * k, &b.SW))) return rc;
+    if ((rc = dev_alloc(m, sizeof(int32_t) * size_t(ch * k), &p))) return rc;
+    b.SI = static_cast<int32_t*>(p);
+    if ((rc = dev_alloc(m, moe_workspace_bytes(ch, E, int(k), H, Fe), &b.MWS))) return rc;
+  }
   b.rows = rows;
   b.ws_bytes = ws;
   return JERO_OK;
@@ -1183,9 +1211,11 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
   const TraceLayout tl = trace_layout(c);
   if (m->trace && m->trace_bytes < size_t(n) * tl.total)
     return fail(JERO_ERR_TENSOR_BOUNDS, "prefill: the trace buffer holds fewer than " + std::to_string(n) + " steps");
-  if (m->moe) {
-    // a model with an MoE spec: run_prefill_with_hidden's own token loop (src/qwen_deepseek.rs:2298-2312),
-    // one decode step per prompt token (its trace at t * jero_hip_model_trace_bytes)
+  if (m->moe && !moe_prefill_batched(m)) {
+    // a model with an MoE spec that the batched pass does not take (a shared expert, a layer
+    // without a router or with a non-F32 one): run_prefill_with_hidden's own token loop
+    // (src/qwen_deepseek.rs:2298-2312), one decode step per prompt token (its trace at
+    // t * jero_hip_model_trace_bytes)
     uint8_t* const trace0 = m->trace;
     int rc = JERO_OK;
     for (int64_t t = 0; t < n && !rc; t++) {
@@ -1377,8 +1407,49 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
     } else if ((rc = launch_det_proj(b.ATT, Q, nullptr, 0.f, 0.25f, b.X, H, true, s, n, Q, H))) {
       return rc;
     }
-    // FFN: (residual +) RMSNorm rows -> gate | up -> SwiGLU -> down + residual
     const float* fnw = static_cast<const float*>(l.ffn_norm.dev);
+    if (m->moe) {
+      // dispatch_qwen3_moe_ffn over the token rows (src/qwen_deepseek.rs:1286-1300, 882-938):
+      // RMSNorm rows, the F32 router's logits rows, then the routed experts of every token (the
+      // expert GEMMs over the tokens each expert was given), each token's sum in selection order
+      // added to its hidden row
+      if ((rc = norm_step(fnw, eps_ffn, false, TraceLayout::kXMid, TraceLayout::kXnFfn, TraceLayout::kQ8Ffn)))
+        return rc;
+      const int64_t E = l.n_experts, chunk = moe_prefill_chunk(m);
+      for (int64_t t0 = 0; t0 < n; t0 += chunk) {
+        const int64_t nt = std::min(chunk, n - t0);
+        if ((rc = launch_matmul_f32_rows(l.router.dev, H, E, b.XN + t0 * H, nt, b.LG, s))) return rc;
+        if (m->trace && 2 * F >= E &&
+            (rc = check_hip(hipMemcpy2DAsync(m->trace + size_t(t0) * tl.total + fld(L, TraceLayout::kGu), tl.total,
+                                             b.LG, sizeof(float) * size_t(E), sizeof(float) * size_t(E), size_t(nt),
+                                             hipMemcpyDeviceToDevice, s),
+                            "prefill trace copy")))
+          return rc;
+        MoeArgs a{};
+        a.x = b.XN + t0 * H;
+        a.logits = b.LG;
+        a.T = nt;
+        a.E = E;
+        a.top_k = m->moe_top_k;
+        a.gate_quant = l.gate_exps.quant;
+        a.up_quant = l.up_exps.quant;
+        a.down_quant = l.down_exps.quant;
+        a.gate = l.gate_exps.dev;
+        a.up = l.up_exps.dev;
+        a.down = l.down_exps.dev;
+        a.hidden = H;
+        a.ffn = l.exp_ffn;
+        a.y = b.T;  // not written: the sums go to the hidden rows
+        a.accumulate = false;
+        a.resid = b.X + t0 * H;
+        a.sel_idx = b.SI;
+        a.sel_w = b.SW;
+        if ((rc = launch_moe(a, b.MWS, s))) return rc;
+      }
+      have_fmt = -1;
+      continue;
+    }
+    // FFN: (residual +) RMSNorm rows -> gate | up -> SwiGLU -> down + residual
     const bool ffn_q8k = l.gu_split ? q8k_input(l.gate) && q8k_input(l.up) : q8k_input(l.gate_up);
     if ((rc = norm_step(fnw, eps_ffn, ffn_q8k, TraceLayout::kXMid, TraceLayout::kXnFfn, TraceLayout::kQ8Ffn)))
       return rc;

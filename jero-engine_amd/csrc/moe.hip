@@ -33,7 +33,8 @@ namespace jero {
 constexpr int kRouteThreads = 1024;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 16;
-constexpr int kRouteLdsPairs = 8192;  // (token, slot) pairs grouped from LDS
+constexpr int kRouteLdsPairs = 8192;  // (token, slot) pairs grouped from LDS (keys hold 13 bits)
+constexpr int kGroupSortPairs = 1024;  // above this many pairs, grouping sorts instead of ranking
 
 // Routes token t in one wave (PER = expert columns per lane, E <= 64 * PER): f32 softmax over
 // all experts, top-k by (logit desc, index asc) with non-finite logits last, renormalised
@@ -192,7 +193,63 @@ __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, in
     }
   }
   __syncthreads();
-  if (in_lds) {
+  const int nt = n / k, words = (nt + 31) / 32;  // tokens (pairs t * k + j) and their bitmask words
+  if (in_lds && n > kGroupSortPairs && n % k == 0 && E * words <= kRouteLdsPairs / 2) {
+    // many pairs: token t's k selections are distinct experts, so pair (t, j)'s rank among its
+    // expert's pairs is the number of tokens before t that selected that expert; from per-expert
+    // token bitmasks and the prefix counts of their words (both in g.list), in one pass
+    uint32_t* bits = reinterpret_cast<uint32_t*>(g.list);
+    int* pre = g.list + E * words;
+    for (int i = threadIdx.x; i < E * words; i += kRouteThreads) bits[i] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kRouteThreads) {
+      const int t = i / k;
+      atomicOr(&bits[g.sel[i] * words + (t >> 5)], 1u << (t & 31));
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += kRouteThreads) {
+      int run = 0;
+      for (int w = 0; w < words; w++) {
+        pre[e * words + w] = run;
+        run += __popc(bits[e * words + w]);
+      }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kRouteThreads) {
+      const int t = i / k, e = g.sel[i], wd = e * words + (t >> 5);
+      const int q = g.off[e] + pre[wd] + __popc(bits[wd] & ((1u << (t & 31)) - 1u));
+      lists.entry[q] = i;
+      lists.inv[i] = q;
+      g.entry[q] = i;
+    }
+  } else if (in_lds && n > kGroupSortPairs) {
+    // many pairs: sort the unique keys (expert << 13 | pair) ascending in LDS (bitonic network,
+    // padded to a power of two): expert e's pairs land at [off[e], off[e] + count[e]) in
+    // ascending pair order, the placement below without its per-pair scan of the segment
+    int P = 1;
+    while (P < n) P <<= 1;
+    for (int i = threadIdx.x; i < P; i += kRouteThreads) g.list[i] = i < n ? (g.sel[i] << 13) | i : 0x7FFFFFFF;
+    __syncthreads();
+    for (int size = 2; size <= P; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int t = threadIdx.x; t < P / 2; t += kRouteThreads) {
+          const int lo = 2 * t - (t & (stride - 1)), hi = lo + stride;
+          const int a = g.list[lo], b = g.list[hi];
+          if ((a > b) == ((lo & size) == 0)) {
+            g.list[lo] = b;
+            g.list[hi] = a;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int q = threadIdx.x; q < n; q += kRouteThreads) {
+      const int i = g.list[q] & 8191;
+      lists.entry[q] = i;
+      lists.inv[i] = q;
+      g.entry[q] = i;
+    }
+  } else if (in_lds) {
     // stable placement in two parallel steps: each pair takes a slot of its expert's segment by
     // an LDS atomic, then its final place is its rank among the segment's pairs (pairs ascend)
     for (int i = threadIdx.x; i < n; i += kRouteThreads) {
@@ -208,6 +265,8 @@ __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, in
       lists.inv[i] = o + r;
       g.entry[o + r] = i;
     }
+  }
+  if (in_lds) {
     if (lists.pass) {
       // per pass of an expert: expert, first list position, count, and its tokens (the last
       // one repeated past the count)

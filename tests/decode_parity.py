@@ -123,11 +123,17 @@ def check_layer(t, spec, D, L, pos, x_next, ring_k, ring_v, kv_f16, qk_norm=True
     """Teacher-forced checks of layer L from its device trace D; x_next is the device's input to
     the next layer (or its final hidden state).  ring_k / ring_v: the layer's rings after the step
     as f32 [capacity][n_kv*hd].  Returns the largest error of each kind; raises on a breach."""
-    H, F = spec["hidden"], spec["ffn"]
+    err = check_attn(t, spec, D, L, pos, ring_k, ring_v, kv_f16, qk_norm, threads, rope_cs, final=False)
+    return check_layer_ffn(t, spec, D, L, x_next, err, threads)
+
+
+def check_attn(t, spec, D, L, pos, ring_k, ring_v, kv_f16, qk_norm=True, threads=16, rope_cs=None, final=True):
+    """The attention sublayer of check_layer (RMSNorm, Q|K|V, QK-norm and RoPE, the ring slot,
+    attention, Wo + residual into the trace's x_mid); with final, raises on a breach here."""
+    H = spec["hidden"]
     nq, nkv, hd = spec["nq"], spec["nkv"], spec["hd"]
     Q, KV = nq * hd, nkv * hd
     eps = spec["eps"]
-    eps_ffn = max(eps, 1e-6)
     p = f"blk.{L}."
     err = {}
     # attention RMSNorm and the Q|K|V activation blocks
@@ -170,6 +176,19 @@ def check_layer(t, spec, D, L, pos, x_next, ring_k, ring_v, kv_f16, qk_norm=True
     check_q8(f"layer {L} wo input", act_fmt(wq_), D["attn"], D["q8_wo"])
     g = _mv(t, p + "attn_output.weight", q8_bytes(act_fmt(wq_), Q, D["q8_wo"]), threads)
     err["gemv"] = max(err["gemv"], rel_resid(D["x_mid"], D["x_in"], g))
+    if final:
+        assert err["norm"] <= NORM_TOL, (L, err)
+        assert err["gemv"] <= GEMV_TOL, (L, err)
+        assert err["rope"] <= ROPE_TOL, (L, err)
+        assert err["attn"] <= ATTN_TOL, (L, err)
+    return err
+
+
+def check_layer_ffn(t, spec, D, L, x_next, err, threads=16):
+    """The dense FFN sublayer of check_layer, its errors added to err (check_attn's)."""
+    H, F = spec["hidden"], spec["ffn"]
+    eps_ffn = max(spec["eps"], 1e-6)
+    p = f"blk.{L}."
     # FFN RMSNorm, gate|up, SwiGLU
     xn = O.rmsnorm(D["x_mid"], t[p + "ffn_norm.weight"][1], eps_ffn)
     err["norm"] = max(err["norm"], rel(D["xn_ffn"], xn))

@@ -131,6 +131,16 @@ def test_moe_many_tokens_per_expert(dev):
     run_case(dev, 24, 3, 256, 768, 3, J.Q6_K, J.Q6_K, 44, repacked=True)
 
 
+@pytest.mark.parametrize("T,E,K", [(130, 16, 8), (300, 64, 4), (200, 700, 16)])
+def test_moe_grouping_paths(dev, T, E, K):
+    """More than 1024 (token, slot) pairs, past the grouping step's per-pair rank: placed from
+    per-expert token bitmasks when E * ceil(T / 32) words fit in LDS (the first two), else by
+    sorting the (expert, pair) keys (the third); the experts' GEMMs and the combine read the
+    lists, so the outputs check them."""
+    print(f"moe grouping T={T} E={E} k={K}", flush=True)
+    run_case(dev, T, E, 256, 256, K, J.Q4_K, J.Q6_K, 80 + T)
+
+
 @pytest.mark.parametrize("E,K", [(200, 6), (300, 8), (700, 16)])
 def test_moe_many_experts(dev, E, K):
     """Router widths above 128 experts (4, 8 and 16 expert columns per lane), top-k up to 16."""

@@ -14,14 +14,16 @@ struct MoeLists {
   int32_t* n_active;  // [1]
   int32_t* entry;     // [T*k] (token*k + slot), grouped by expert, ascending within an expert
   int32_t* inv;       // [T*k] list position of (token*k + slot)
-  int32_t* pass;      // [passes][kMoePassInts] per pass (up to kMoePassTokens of one expert's
+  int32_t* pass;      // [passes][4 + pass_tokens] per pass (up to pass_tokens of one expert's
                       // list entries, experts ascending): expert, first list position, count, 0,
                       // then the pass's tokens (or null: no pass descriptors)
+  int pass_tokens;    // kMoePassTokens or kMoePassTokensWide
   int32_t* ctr;       // [kMoeCtrInts]: the number of passes, then the work counters of the
                       // expert GEMMs, each on its own 128-byte line (with pass)
 };
 
-constexpr int kMoePassTokens = 8;
+constexpr int kMoePassTokens = 8;       // tokens per expert-GEMM pass
+constexpr int kMoePassTokensWide = 16;  // when the experts average at least that many tokens
 constexpr int kMoePassInts = 4 + kMoePassTokens;
 constexpr int kMoeCtrInts = 96;
 constexpr int kMoeCtrGateUp = 32, kMoeCtrDown = 64;  // counter offsets in ctr

@@ -139,6 +139,7 @@ __device__ __forceinline__ void group_init(GroupLds& g, int E) {
 // fits, else in sel_idx.  One workgroup of kRouteThreads threads; starts and ends with a barrier.
 __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, int n, int E, int k, MoeLists lists) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = kRouteThreads / 64;
+  const int PT = lists.pass_tokens == kMoePassTokensWide ? kMoePassTokensWide : kMoePassTokens;
   if (threadIdx.x < 4 && n + int(threadIdx.x) < kRouteLdsPairs + 4) g.sel[n + threadIdx.x] = -1;
   __syncthreads();
   const bool in_lds = n <= kRouteLdsPairs;
@@ -148,7 +149,7 @@ __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, in
     // exclusive scans of the counts (offsets), of the active flags (active list) and of the
     // pass counts, one thread per expert: wave scans, then the 16 wave totals
     const int e = threadIdx.x;
-    const int c = e < E ? g.count[e] : 0, f = c > 0 ? 1 : 0, np = (c + kMoePassTokens - 1) / kMoePassTokens;
+    const int c = e < E ? g.count[e] : 0, f = c > 0 ? 1 : 0, np = (c + PT - 1) / PT;
     int ic = c, jf = f, kp = np;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -269,20 +270,24 @@ __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, in
   if (in_lds) {
     if (lists.pass) {
       // per pass of an expert: expert, first list position, count, and its tokens (the last
-      // one repeated past the count)
+      // one repeated past the count); one thread per pass, whose expert is the last one with
+      // poff[e] <= pass (an expert with no pairs has the poff of the next, so is passed over)
       __syncthreads();
-      for (int e = threadIdx.x; e < E; e += kRouteThreads) {
-        const int o = g.off[e], c = g.count[e];
-        int32_t* pd = lists.pass + int64_t(g.poff[e]) * kMoePassInts;
-        for (int b = 0; b < c; b += kMoePassTokens, pd += kMoePassInts) {
-          const int m = min(kMoePassTokens, c - b);
-          pd[0] = e;
-          pd[1] = o + b;
-          pd[2] = m;
-          pd[3] = 0;
-#pragma unroll
-          for (int j = 0; j < kMoePassTokens; j++) pd[4 + j] = g.entry[o + b + min(j, m - 1)] / k;
+      const int passes = g.poff[E - 1] + (g.count[E - 1] + PT - 1) / PT;
+      for (int pi = threadIdx.x; pi < passes; pi += kRouteThreads) {
+        int lo = 0, hi = E - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (g.poff[mid] <= pi) lo = mid;
+          else hi = mid - 1;
         }
+        const int e = lo, o = g.off[e], b = (pi - g.poff[e]) * PT, m = min(PT, g.count[e] - b);
+        int32_t* pd = lists.pass + int64_t(pi) * (4 + PT);
+        pd[0] = e;
+        pd[1] = o + b;
+        pd[2] = m;
+        pd[3] = 0;
+        for (int j = 0; j < PT; j++) pd[4 + j] = g.entry[o + b + min(j, m - 1)] / k;
       }
     }
   } else {
@@ -744,8 +749,7 @@ __host__ __device__ inline int act_row_stride(int nb) {
   const int s = ((nb * 292 + 15) & ~15) + 16;
   return (s / 16) % 2 ? s : s + 16;
 }
-// Tokens staged per pass (NT = kMfmaTokens / TPT token tiles): a pass descriptor's worth.
-constexpr int kMfmaTokens = kMoePassTokens;
+// Tokens staged per pass (PT: NT = PT / TPT token tiles): a pass descriptor's worth.
 
 // The weights of block b (units 4b .. 4b + 3: one step) of one weight row for lane group kg, as
 // loaded.  A step takes a whole block so that every cache line it fetches is used up within
@@ -872,43 +876,46 @@ __device__ __forceinline__ void q4k_scale_min(const u32x4& h, int sb, int& sc, i
   m = int(sb < 4 ? bb & 63u : (c >> 4) | ((bb >> 6) << 4));
 }
 
-constexpr int kStageChunks = 8;  // Q8_K staging: 16-byte chunks per thread in its one batch
-constexpr int kStageBlocks = 8;  // f32 staging: 256-element blocks per wave in its one batch
+constexpr int kStageChunks = 8;  // Q8_K staging: 16-byte chunks per thread in one batch
+constexpr int kStageBlocks = 8;  // f32 staging: 256-element blocks per wave in one batch
 
-// Work items: (pass, row block) -- one pass descriptor's tokens (up to kMfmaTokens of one
-// expert) against 64 * tiles weight rows of that expert (tiles tiles of 16 per wave, one after
+// Work items: (pass, row block) -- one pass descriptor's tokens (up to PT of one expert) against 64 * tiles weight rows of that expert (tiles tiles of 16 per wave, one after
 // the other), numbered pass-major.  The grid is persistent (what fits on the GPU at once) and
 // each workgroup takes the next item from a counter until none is left.  The next item's number
 // is fetched while the current one runs.  Each tile's results go to LDS when its last block is
 // done and leave in one coalesced pass.  GU: gate (w0) and up (w1) rows from the tokens' Q8_K
 // rows, out = silu(gate) * up per (list entry, row); else down (w0) rows from the f32 act rows
 // (quantized here), out = the dot per (list entry, row).  An item makes two dependent trips to
-// memory before its first MFMA: the pass descriptor, then the activations (in one batch) with the
+// memory before its first MFMA: the pass descriptor, then the activations (batches of 8 rows) with the
 // first weights behind them; the load counter drains in order, so nothing small waits behind
 // weights.  R is a multiple of 64 * tiles: no row is clamped.
 // Workgroups per CU the register budget is cut for: three (168 VGPRs), except Q6_K gate/up, whose
-// two tensors' pieces need more registers than that without spilling.
-__host__ __device__ constexpr int mfma_min_wgs(int f, bool gu) { return gu && mfma_seg(f) == 4 ? 2 : 3; }
+// two tensors' pieces need more registers than that without spilling, and the 16-token passes
+// (twice the accumulators) of Q4_K gate/up and Q6_K down: two.  (Q6_K gate/up takes no 16-token
+// passes: they spill at any budget.)
+__host__ __device__ constexpr int mfma_min_wgs(int f, bool gu, int pt) {
+  return (gu && (mfma_seg(f) == 4 || pt > kMoePassTokens)) || (!gu && mfma_seg(f) == 4 && pt > kMoePassTokens) ? 2 : 3;
+}
 
-template <int F, bool GU>
-__global__ void __launch_bounds__(256, mfma_min_wgs(F, GU)) moe_mfma_kernel(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
+template <int F, bool GU, int PT>
+__global__ void __launch_bounds__(256, mfma_min_wgs(F, GU, PT)) moe_mfma_kernel(const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1,
                                                        int64_t n_rows, int64_t rb, int U, int R, int tiles,
                                                        const uint8_t* __restrict__ xq, int64_t xq_rb,
                                                        const float* __restrict__ act_in, MoeLists lists,
                                                        float* __restrict__ out, int wg_per_expert, int ctr_off) {
-  constexpr int SEG = mfma_seg(F), TPT = 16 / SEG, NT = kMfmaTokens / TPT, LT = 4 / SEG;
+  constexpr int SEG = mfma_seg(F), TPT = 16 / SEG, NT = PT / TPT, LT = 4 / SEG;
   constexpr int NW = GU ? 2 : 1;  // weight tensors per wave
   using Piece = MfmaPiece<F>;
   using Cur = typename Piece::Cur;
   extern __shared__ __attribute__((aligned(16))) uint8_t s_act[];
-  __shared__ int s_tok[kMfmaTokens];
+  __shared__ int s_tok[PT];
   __shared__ int s_item;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int c = lane & 15, kg = lane >> 4;
   const int nb = U / 4, stride = act_row_stride(nb);
-  const int zrow = kMfmaTokens * stride, dummy = zrow + stride;  // the zero row, then a dummy area
+  const int zrow = PT * stride, dummy = zrow + stride;  // the zero row, then a dummy area
   const int steps = tiles * nb;
-  float* s_out = reinterpret_cast<float*>(s_act + dummy + 304);  // [tiles][kMfmaTokens][64 rows]
+  float* s_out = reinterpret_cast<float*>(s_act + dummy + 304);  // [tiles][PT][64 rows]
   for (int i = threadIdx.x; i < stride / 16; i += 256) *reinterpret_cast<u32x4*>(s_act + zrow + 16 * i) = u32x4{};
   // the counter is bumped by atomicInc (with no wrap): the compiler turns a single-lane atomicAdd
   // into a wave-aggregated one whose result it waits for at once
@@ -922,16 +929,26 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU)) moe_mfma_kernel(cons
   const bool a_on = vr % SEG == kg_seg;
   const int a_lane = SEG == 2 ? 4 + 16 * kg : 4 + 32 * kg;  // the lane's K group in a unit's bytes
   const uint32_t nsh = (kg & 2) ? 4u : 0u;                    // its nibble: low for kg < 2
-  static_assert(kMoePassInts == 12, "a pass descriptor is three 16-byte loads");
+  static_assert(PT % 4 == 0, "a pass descriptor is 1 + PT / 4 16-byte loads");
   for (int item = s_item; item < n_items;) {  // item is uniform over the workgroup
     const int pi = item / wg_per_expert, part = item - pi * wg_per_expert;
     // the pass descriptor in one trip: expert, first list position, token count, 0, tokens
-    const uint8_t* pd = reinterpret_cast<const uint8_t*>(lists.pass) + int64_t(pi) * (kMoePassInts * 4);
-    u32x4 ph = ld4(pd), pt0 = ld4(pd + 16), pt1 = ld4(pd + 32);
-    pin(pt0);  // held in registers: else a thread's token is loaded again once the header is in
-    pin(pt1);
+    const uint8_t* pd = reinterpret_cast<const uint8_t*>(lists.pass) + int64_t(pi) * ((4 + PT) * 4);
+    u32x4 ph = ld4(pd), ptv[PT / 4];
+#pragma unroll
+    for (int i = 0; i < PT / 4; i++) {
+      ptv[i] = ld4(pd + 16 + 16 * i);
+      pin(ptv[i]);  // held in registers: else a thread's token is loaded again once the header is in
+    }
     const int e = int(ph.x), i0 = int(ph.y), nch = int(ph.z);
-    const uint32_t tj[kMfmaTokens] = {pt0.x, pt0.y, pt0.z, pt0.w, pt1.x, pt1.y, pt1.z, pt1.w};
+    uint32_t tj[PT];
+#pragma unroll
+    for (int i = 0; i < PT / 4; i++) {
+      tj[4 * i] = ptv[i].x;
+      tj[4 * i + 1] = ptv[i].y;
+      tj[4 * i + 2] = ptv[i].z;
+      tj[4 * i + 3] = ptv[i].w;
+    }
     const int row0 = (part * 4 + wv) * tiles * 16 + c;  // this lane's weight row (B column) in tile 0
     Cur cur[NW];
 #pragma unroll
@@ -950,7 +967,7 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU)) moe_mfma_kernel(cons
 #pragma unroll
       for (int q = 0; q < LT; q++) e_base[tl][q] = min(tl * TPT + kg * LT + q, nch - 1) * stride;
     }
-    if (threadIdx.x < kMfmaTokens) s_tok[threadIdx.x] = int(tj[threadIdx.x]);
+    if (threadIdx.x < PT) s_tok[threadIdx.x] = int(tj[threadIdx.x]);
     lds_barrier();  // s_tok
     // Q6_K: the block's sum over its 16 groups of scale x bsum, per (token, row), comes from one f16
     // MFMA (exact: |sum| < 2^23): K slot 4 kg' + t is group 8n + j + 2t of unit kg' = 2n + j (the
@@ -965,37 +982,46 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU)) moe_mfma_kernel(cons
     auto kloop = [&](auto nta) {
       constexpr int NTA = decltype(nta)::value;
       Piece pa[NW], pb[NW];
-      // staging in one batch: every load issued, then the first weights, then the LDS writes
-      // (out-of-range slots write a dummy area: no branch may skip a wait)
+      // staging in batches: a batch's loads all issued, (after the first batch's) the first
+      // weights, then the batch's LDS writes (out-of-range slots write a dummy area: no branch
+      // may skip a wait); one batch holds 8 Q8_K rows of up to 4096 or 8 f32 rows of up to 1024
       if constexpr (GU) {
         const int chunks = int(xq_rb / 16), total = nch * chunks;  // 16-byte chunks of a (padded) Q8_K row
-        u32x4 v[kStageChunks];
+        auto batch = [&](int base, bool first) {
+          u32x4 v[kStageChunks];
 #pragma unroll
-        for (int q = 0; q < kStageChunks; q++) {
-          const int idx = min(int(threadIdx.x) + 256 * q, total - 1), j = idx / chunks;
-          v[q] = ld4(xq + int64_t(s_tok[j]) * xq_rb + (idx - j * chunks) * 16);
-        }
-        load(0, pa);
+          for (int q = 0; q < kStageChunks; q++) {
+            const int idx = min(base + int(threadIdx.x) + 256 * q, total - 1), j = idx / chunks;
+            v[q] = ld4(xq + int64_t(s_tok[j]) * xq_rb + (idx - j * chunks) * 16);
+          }
+          if (first) load(0, pa);
 #pragma unroll
-        for (int q = 0; q < kStageChunks; q++) {
-          const int idx = int(threadIdx.x) + 256 * q, j = idx / chunks;
-          *reinterpret_cast<u32x4*>(s_act + (idx < total ? j * stride + (idx - j * chunks) * 16 : dummy)) = v[q];
-        }
+          for (int q = 0; q < kStageChunks; q++) {
+            const int idx = base + int(threadIdx.x) + 256 * q, j = idx / chunks;
+            *reinterpret_cast<u32x4*>(s_act + (idx < total ? j * stride + (idx - j * chunks) * 16 : dummy)) = v[q];
+          }
+        };
+        batch(0, true);
+        for (int base = 256 * kStageChunks; base < total; base += 256 * kStageChunks) batch(base, false);
       } else {
         const int cols = U * 64, total = nch * nb;
-        float4 v[kStageBlocks];
+        auto batch = [&](int base, bool first) {
+          float4 v[kStageBlocks];
 #pragma unroll
-        for (int q = 0; q < kStageBlocks; q++) {
-          const int b = min(wv + 4 * q, total - 1), j = b / nb, jb = b - j * nb;
-          v[q] = reinterpret_cast<const float4*>(act_in + int64_t(i0 + j) * cols + int64_t(jb) * 256)[lane];
-        }
-        load(0, pa);
+          for (int q = 0; q < kStageBlocks; q++) {
+            const int b = min(base + wv + 4 * q, total - 1), j = b / nb, jb = b - j * nb;
+            v[q] = reinterpret_cast<const float4*>(act_in + int64_t(i0 + j) * cols + int64_t(jb) * 256)[lane];
+          }
+          if (first) load(0, pa);
 #pragma unroll
-        for (int q = 0; q < kStageBlocks; q++) {
-          const int b = wv + 4 * q, j = b / nb, jb = b - j * nb;
-          const float ev[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
-          q8k_block_wave(ev, lane, s_act + (b < total ? j * stride + 292 * jb : dummy));
-        }
+          for (int q = 0; q < kStageBlocks; q++) {
+            const int b = base + wv + 4 * q, j = b / nb, jb = b - j * nb;
+            const float ev[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+            q8k_block_wave(ev, lane, s_act + (b < total ? j * stride + 292 * jb : dummy));
+          }
+        };
+        batch(0, true);
+        for (int base = 4 * kStageBlocks; base < total; base += 4 * kStageBlocks) batch(base, false);
       }
       lds_barrier();
       // the next item's number, fetched behind the first weights: its wait comes after the K loop
@@ -1115,8 +1141,8 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU)) moe_mfma_kernel(cons
               } else {
                 v = acc[0][tl][q];
               }
-              const int t_loc = tl * TPT + kg * LT + q;  // < kMfmaTokens
-              if (live) s_out[(tile * kMfmaTokens + t_loc) * 64 + 16 * wv + c] = v;
+              const int t_loc = tl * TPT + kg * LT + q;  // < PT
+              if (live) s_out[(tile * PT + t_loc) * 64 + 16 * wv + c] = v;
 #pragma unroll
               for (int t = 0; t < NW; t++) acc[t][tl][q] = 0.f;
             }
@@ -1143,7 +1169,7 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU)) moe_mfma_kernel(cons
     for (int idx = threadIdx.x; idx < tiles * nch * 64; idx += 256) {
       const int tile = idx / (nch * 64), rem = idx - tile * nch * 64, t = rem / 64, w = (rem / 16) & 3, cc = rem & 15;
       const int row = (part * 4 + w) * tiles * 16 + 16 * tile + cc;
-      out[int64_t(i0 + t) * R + row] = s_out[(tile * kMfmaTokens + t) * 64 + 16 * w + cc];
+      out[int64_t(i0 + t) * R + row] = s_out[(tile * PT + t) * 64 + 16 * w + cc];
     }
   }
 }
@@ -1163,8 +1189,14 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restric
 
 // ---------------------------------------------------------------- launch plumbing
 
-// Passes over n (token, slot) pairs among E experts: at most one partial pass per active expert.
-int64_t moe_max_passes(int64_t n, int64_t E) { return (n + (kMoePassTokens - 1) * std::min(n, E)) / kMoePassTokens; }
+// Passes of pt tokens over n (token, slot) pairs among E experts: at most one partial pass per
+// active expert.
+int64_t moe_max_passes(int64_t n, int64_t E, int pt) { return (n + (pt - 1) * std::min(n, E)) / pt; }
+// Descriptor ints for either pass size.
+int64_t moe_pass_area(int64_t n, int64_t E) {
+  return std::max(moe_max_passes(n, E, kMoePassTokens) * (4 + kMoePassTokens),
+                  moe_max_passes(n, E, kMoePassTokensWide) * (4 + kMoePassTokensWide));
+}
 
 // Bytes between the tokens' Q8_K rows in the workspace: a row rounded up to 16 bytes, so that the
 // expert GEMMs stage them in 16-byte pieces.
@@ -1290,23 +1322,37 @@ int mfma_tiles(bool gu, int64_t R) {
   return R % 128 == 0 ? 2 : 1;
 }
 
-template <int F, bool GU>
-void mfma_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
+size_t mfma_lds(int nb, int tiles, int pt) {
+  return size_t(pt + 1) * size_t(act_row_stride(nb)) + 304 +  // + zero row, dummy area
+         sizeof(float) * size_t(tiles) * size_t(pt) * 64;     // + the results
+}
+
+template <int F, bool GU, int PT>
+void mfma_one_pt(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
   const int64_t K = GU ? a.hidden : a.ffn, R = GU ? a.ffn : a.hidden;
   const int U = units_per_row(F, K), nb = U / 4, tiles = mfma_tiles(GU, R);
   const int wg_per_expert = int(R / (64 * tiles));
-  const size_t lds = size_t(kMfmaTokens + 1) * size_t(act_row_stride(nb)) + 304 +  // + zero row, dummy area
-                     sizeof(float) * size_t(tiles) * kMfmaTokens * 64;               // + the results
+  const size_t lds = mfma_lds(nb, tiles, PT);
   int fit = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, moe_mfma_kernel<F, GU>, 256, lds) != hipSuccess || fit < 1)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, moe_mfma_kernel<F, GU, PT>, 256, lds) != hipSuccess || fit < 1)
     fit = 1;
-  const int64_t items = moe_max_passes(a.T * a.top_k, a.E) * wg_per_expert;
+  const int64_t items = moe_max_passes(a.T * a.top_k, a.E, PT) * wg_per_expert;
   const int64_t grid = std::min<int64_t>(items, int64_t(std::min(fit, kMfmaWgPerCu)) * device_info().cus);
   const uint8_t* w0 = static_cast<const uint8_t*>(GU ? a.gate : a.down);
   const uint8_t* w1 = static_cast<const uint8_t*>(GU ? a.up : a.down);
-  hipLaunchKernelGGL((moe_mfma_kernel<F, GU>), dim3(unsigned(grid)), dim3(256), lds, s, w0, w1, a.E * R,
+  hipLaunchKernelGGL((moe_mfma_kernel<F, GU, PT>), dim3(unsigned(grid)), dim3(256), lds, s, w0, w1, a.E * R,
                      row_bytes(F, K), U, int(R), tiles, a.xq, moe_xq_rb(a.hidden), a.act, L, GU ? a.act : a.yd,
                      wg_per_expert, GU ? kMoeCtrGateUp : kMoeCtrDown);
+}
+
+template <int F, bool GU>
+void mfma_one(const MoeArgs& a, const MoeLists& L, hipStream_t s) {
+  if constexpr (GU && mfma_seg(F) == 4) {
+    mfma_one_pt<F, GU, kMoePassTokens>(a, L, s);  // launch_moe gives Q6_K gate/up no wide passes
+  } else {
+    if (L.pass_tokens == kMoePassTokensWide) mfma_one_pt<F, GU, kMoePassTokensWide>(a, L, s);
+    else mfma_one_pt<F, GU, kMoePassTokens>(a, L, s);
+  }
 }
 
 template <bool GU>
@@ -1331,7 +1377,7 @@ size_t moe_workspace_bytes(int64_t T, int64_t E, int top_k, int64_t hidden, int6
   add(sizeof(int32_t) * size_t(E));                        // active
   add(sizeof(int32_t));                                    // n_active
   add(sizeof(int32_t) * size_t(n) * 2);                    // entry, inv
-  add(sizeof(int32_t) * size_t(moe_max_passes(n, E)) * kMoePassInts);  // pass descriptors
+  add(sizeof(int32_t) * size_t(moe_pass_area(n, E)));  // pass descriptors
   add(sizeof(int32_t) * kMoeCtrInts);                                   // pass count, work counters
   add(sizeof(float) * size_t(n) * size_t(ffn));            // act
   add(sizeof(float) * size_t(n) * size_t(hidden));         // per-slot down outputs
@@ -1348,14 +1394,14 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   };
   const int64_t xq_rb = moe_xq_rb(a.hidden);
   a.xq = take(size_t(a.T) * size_t(xq_rb));
-  MoeLists L;
+  MoeLists L{};
   L.offset = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(a.E + 1)));
   L.active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(a.E)));
   L.n_active = reinterpret_cast<int32_t*>(take(sizeof(int32_t)));
   int32_t* ei = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(n) * 2));
   L.entry = ei;
   L.inv = ei + n;
-  int32_t* pass = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(moe_max_passes(n, a.E)) * kMoePassInts));
+  int32_t* pass = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(moe_pass_area(n, a.E))));
   int32_t* ctr = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * kMoeCtrInts));
   a.act = reinterpret_cast<float*>(take(sizeof(float) * size_t(a.ffn) * size_t(n)));
   a.yd = reinterpret_cast<float*>(take(sizeof(float) * size_t(n) * size_t(a.hidden)));
@@ -1365,9 +1411,16 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   // from the pass descriptors and work counters, written by the grouping step
   const bool mfma = a.T * a.top_k >= 2 * a.E && n <= kRouteLdsPairs && mfma_format(a.gate_quant) &&
                     mfma_format(a.down_quant) && a.hidden % 64 == 0 && a.ffn % 64 == 0 &&  // whole 64-row items
-                    kMfmaTokens * (xq_rb / 16) <= kStageChunks * 256 &&                      // one staging batch
-                    kMfmaTokens * (a.ffn / 256) <= 4 * kStageBlocks;
+                    kMoePassTokens * (xq_rb / 16) <= kStageChunks * 256 &&                   // a batch: 8 rows
+                    kMoePassTokens * (a.ffn / 256) <= 4 * kStageBlocks;
+  // passes of 16 tokens when the experts average at least 16 (each expert's weights are then read
+  // half as often) and the staged rows leave LDS for two workgroups per CU
+  const int64_t nb_gu = a.hidden / 256, nb_dn = a.ffn / 256;
+  const bool wide = mfma && a.T * a.top_k >= int64_t(kMoePassTokensWide) * a.E && mfma_seg(a.gate_quant) == 2 &&
+                    std::max(mfma_lds(int(nb_gu), mfma_tiles(true, a.ffn), kMoePassTokensWide),
+                             mfma_lds(int(nb_dn), mfma_tiles(false, a.hidden), kMoePassTokensWide)) <= 80 * 1024;
   L.pass = mfma ? pass : nullptr;
+  L.pass_tokens = wide ? kMoePassTokensWide : kMoePassTokens;
   L.ctr = ctr;
 
   // one token among at most 128 experts: two launches.  Gate/up routes and quantizes the token
@@ -1574,7 +1627,7 @@ extern "C" int jero_hip_moe_trace_view(void* workspace_dev, int64_t n_tokens, in
   take(sizeof(int32_t) * size_t(n_experts));
   take(sizeof(int32_t));
   int32_t* ei = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * size_t(n) * 2));
-  take(sizeof(int32_t) * size_t(moe_max_passes(n, n_experts)) * kMoePassInts);
+  take(sizeof(int32_t) * size_t(moe_pass_area(n, n_experts)));
   take(sizeof(int32_t) * kMoeCtrInts);
   *act_dev = reinterpret_cast<float*>(take(sizeof(float) * size_t(ffn) * size_t(n)));
   *pair_row_dev = ei + n;

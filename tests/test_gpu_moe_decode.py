@@ -205,7 +205,9 @@ def test_moe_decode_matches_oracle(dev, case):
 # name: (spec, moe, capacity, filled slots before the prompt, prompt tokens); the batched pass
 # (every layer routed over an F32 router, no shared expert): below 32 prompt tokens the experts
 # take the GEMV passes, from 32 (256 (token, slot) pairs over 128 experts) the MFMA expert GEMMs
+# in passes of 8 tokens, from 256 (16 per expert on average) in passes of 16
 PREFILL_CASES = {
+    "qwen3_30b_a3b_layers_288_tokens": (QWEN3_MOE, (128, 8, 768, False), 512, 16, 288),
     "qwen3_30b_a3b_layers_96_tokens": (QWEN3_MOE, (128, 8, 768, False), 256, 40, 96),
     "qwen3_30b_a3b_layers_9_tokens": (QWEN3_MOE, (128, 8, 768, False), 256, 0, 9),
     "256_experts_70_tokens": (SMALL, (256, 8, 256, False), 128, 20, 70),

@@ -742,15 +742,20 @@ def read_profile_csv(dirs, suffix):
     return rows
 
 
-def summarize_profiles(dirs, match, step_end, last, out):
+def summarize_profiles(dirs, match, step_end, last, out, until=None):
     """Markdown summary of rocprofv3 CSV output (--output-format csv) under `dirs`: per (kernel,
     grid) launch counts and mean / median duration from *_kernel_trace.csv; per (kernel, grid)
     counter means per dispatch (and per wave for SQ_INSTS_* given SQ_WAVES) from
     *_counter_collection.csv; with `step_end`, the wall time and kernel-time sum of the last
-    `last` steps, a step being the dispatches after one `step_end` kernel up to the next."""
+    `last` steps, a step being the dispatches after one `step_end` kernel up to the next; with
+    `until`, only the dispatches before the first kernel whose name contains it."""
     import numpy as np
     w = out.write
     trace = [r for r in read_profile_csv(dirs, "_kernel_trace.csv") if match in r["Kernel_Name"]]
+    if until:
+        trace.sort(key=lambda r: int(r["Start_Timestamp"]))
+        cut = next((i for i, r in enumerate(trace) if until in r["Kernel_Name"]), len(trace))
+        trace = trace[:cut]
     if trace:
         groups = {}
         for r in trace:
@@ -858,12 +863,13 @@ def main():
     ap.add_argument("--match", default="jero", help="--summarize: kernels whose name contains this")
     ap.add_argument("--step-end", default=None, help="--summarize: kernel that ends one step (per-step wall times)")
     ap.add_argument("--last", type=int, default=16, help="--summarize: steps to average with --step-end")
+    ap.add_argument("--until", default=None, help="--summarize: only dispatches before the first kernel named so")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print HBM bytes per dispatch from a FETCH_SIZE and a WRITE_SIZE pass run with "
                          "--copy-probe MB (give the same MB) and exit (no GPU)")
     args = ap.parse_args()
     if args.summarize:
-        summarize_profiles(args.summarize, args.match, args.step_end, args.last, sys.stdout)
+        summarize_profiles(args.summarize, args.match, args.step_end, args.last, sys.stdout, args.until)
         return
     if args.traffic:
         res, ff, wf = traffic_summary([args.traffic[0]], [args.traffic[1]], args.match, args.copy_probe * 1e6)

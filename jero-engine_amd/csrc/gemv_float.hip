@@ -118,11 +118,12 @@ void launch_fq(const uint8_t* w, int64_t K, int64_t N, const float* x, float* y,
 // xn = x * (1 / sqrt(mean(x^2) + eps)) * nw, then the router logits y = W xn over F32 rows of
 // K elements (16-byte aligned, K % 4 == 0).  Every workgroup computes the norm itself (the same
 // per-thread sums in the same order, so every workgroup holds the same xn bits) into LDS; the
-// first also stores xn for the expert kernels.  Each lane's first weight pieces are loaded
-// before the norm, unconditionally (clamped), so the prologue overlaps the row fetch.
+// first also stores xn for the expert kernels.  The thread's elements of x and of the norm
+// weights are loaded first, then each lane's first weight pieces, all unconditionally
+// (clamped), so the norm waits for one round trip and overlaps the row fetch.
 constexpr int kRouterPieces = 8;  // pieces per lane in flight: one pass over a 2048-wide row at LPR 64
 
-template <int LPR>
+template <int LPR, int PER>
 __global__ void __launch_bounds__(kFloatThreads) router_norm_kernel(const uint8_t* __restrict__ w, int64_t rb,
                                                                     int64_t K, int64_t N, const float* __restrict__ x,
                                                                     const float* __restrict__ nw, float eps,
@@ -134,6 +135,15 @@ __global__ void __launch_bounds__(kFloatThreads) router_norm_kernel(const uint8_
   const int64_t row = ((int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave) * G + g;
   const int64_t rr = row < N ? row : N - 1;
   const uint8_t* wr = w + rr * rb;
+  // the thread's elements i = tid + 256 j of x and of the norm weights, all loaded up front
+  // (clamped), before the weights: the norm waits for one round trip and not for the weights
+  float xv[PER], gv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int64_t i = min<int64_t>(threadIdx.x + int64_t(kFloatThreads) * j, K - 1);
+    xv[j] = x[i];
+    gv[j] = nw[i];
+  }
   const int64_t pieces = K / 4;
   u32x4 v[kRouterPieces];
 #pragma unroll
@@ -142,7 +152,9 @@ __global__ void __launch_bounds__(kFloatThreads) router_norm_kernel(const uint8_
     v[i] = *reinterpret_cast<const u32x4*>(wr + 16 * (p < pieces ? p : pieces - 1));
   }
   float ss = 0.f;
-  for (int64_t i = threadIdx.x; i < K; i += blockDim.x) ss += x[i] * x[i];
+#pragma unroll
+  for (int j = 0; j < PER; j++)
+    if (threadIdx.x + int64_t(kFloatThreads) * j < K) ss += xv[j] * xv[j];
   ss = wave_sum_dpp(ss);
   if (lane == 0) s_tmp[threadIdx.x >> 6] = ss;
   lds_barrier();
@@ -150,10 +162,14 @@ __global__ void __launch_bounds__(kFloatThreads) router_norm_kernel(const uint8_
 #pragma unroll
   for (int i = 0; i < kFloatThreads / kWave; i++) t += s_tmp[i];
   const float inv = 1.0f / sqrtf(t / float(K) + eps);
-  for (int64_t i = threadIdx.x; i < K; i += blockDim.x) {
-    const float e = x[i] * inv * nw[i];
-    s_x[i] = e;
-    if (blockIdx.x == 0) xn[i] = e;
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int64_t i = threadIdx.x + int64_t(kFloatThreads) * j;
+    if (i < K) {
+      const float e = xv[j] * inv * gv[j];
+      s_x[i] = e;
+      if (blockIdx.x == 0) xn[i] = e;
+    }
   }
   lds_barrier();
   float acc = 0.f;
@@ -278,12 +294,24 @@ int launch_router_norm(const void* w, int64_t n_in, int64_t n_out, const float* 
   const int64_t waves = (n_out + (kWave / lpr) - 1) / (kWave / lpr);
   const dim3 grid(unsigned((waves + kFloatThreads / kWave - 1) / (kFloatThreads / kWave)));
   const size_t lds = sizeof(float) * size_t(n_in);
+  const int per = int((n_in + kFloatThreads - 1) / kFloatThreads);  // elements per thread, <= 32
+#define JERO_ROUTER(L, P)                                                                                 \
+  hipLaunchKernelGGL((router_norm_kernel<L, P>), grid, dim3(kFloatThreads), lds, s, wb, rb, n_in, n_out, x, nw, \
+                     eps, xn, y)
+#define JERO_ROUTER_P(L)              \
+  do {                                \
+    if (per <= 8) JERO_ROUTER(L, 8);   \
+    else if (per <= 16) JERO_ROUTER(L, 16); \
+    else JERO_ROUTER(L, 32);          \
+  } while (0)
   switch (lpr) {
-    case 64: hipLaunchKernelGGL((router_norm_kernel<64>), grid, dim3(kFloatThreads), lds, s, wb, rb, n_in, n_out, x, nw, eps, xn, y); break;
-    case 32: hipLaunchKernelGGL((router_norm_kernel<32>), grid, dim3(kFloatThreads), lds, s, wb, rb, n_in, n_out, x, nw, eps, xn, y); break;
-    case 16: hipLaunchKernelGGL((router_norm_kernel<16>), grid, dim3(kFloatThreads), lds, s, wb, rb, n_in, n_out, x, nw, eps, xn, y); break;
-    default: hipLaunchKernelGGL((router_norm_kernel<4>), grid, dim3(kFloatThreads), lds, s, wb, rb, n_in, n_out, x, nw, eps, xn, y); break;
+    case 64: JERO_ROUTER_P(64); break;
+    case 32: JERO_ROUTER_P(32); break;
+    case 16: JERO_ROUTER_P(16); break;
+    default: JERO_ROUTER_P(4); break;
   }
+#undef JERO_ROUTER_P
+#undef JERO_ROUTER
   return check_launch("router (norm + F32 rows)");
 }
 

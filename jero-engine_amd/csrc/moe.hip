@@ -644,7 +644,12 @@ __device__ __forceinline__ int xcd_grouped(int b, int n, int m) {
 // k selected experts' down rows (units (slot j, row r), lane group per unit); the token's act rows
 // (act row j = selection j) are quantized to Q8_K in LDS.  The dots land in LDS and the workgroup
 // then writes y[h] = sum over j ascending of w_j * dot_j, the reference's combine order.
-template <int F, int LPR, int UPL>
+// PRE: the k act rows hold at most 4 * kDown1PreBlocks 256-blocks; each wave loads its blocks into
+// registers at entry, beside the selections (they do not depend on them), and quantizes them while
+// the first weights are in flight; else they are staged after the first weight loads.
+constexpr int kDown1PreBlocks = 8;
+
+template <int F, int LPR, int UPL, bool PRE>
 __global__ void __launch_bounds__(256) moe1_down_kernel(const uint8_t* __restrict__ down, int64_t n_rows, int64_t rb,
                                                         int U, int H, const float* __restrict__ act, int ffn,
                                                         int64_t aq_rb, int k, const int32_t* __restrict__ sel_idx,
@@ -664,6 +669,15 @@ __global__ void __launch_bounds__(256) moe1_down_kernel(const uint8_t* __restric
   const int share = kTiled && RW < 16 && 16 % RW == 0 ? 16 / RW : 1;
   const int hbase = xcd_grouped(int(blockIdx.x), int(gridDim.x), share) * RW, n_units = RW * k;
   float* s_dot = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(s_x) + int64_t(k) * aq_rb);
+  const int nbk = ffn / 256, total_blk = k * nbk;
+  float4 av[PRE ? kDown1PreBlocks : 1];
+  if constexpr (PRE) {  // unconditional (clamped) loads of the wave's act blocks
+#pragma unroll
+    for (int q = 0; q < kDown1PreBlocks; q++) {
+      const int b = min(wv + 4 * q, total_blk - 1), j = b / nbk, jb = b - j * nbk;
+      av[q] = reinterpret_cast<const float4*>(act + int64_t(j) * ffn + int64_t(jb) * 256)[lane];
+    }
+  }
   if (threadIdx.x < kMaxTopK) {
     const int j = min(int(threadIdx.x), k - 1);
     s_sel[threadIdx.x] = sel_idx[j];
@@ -705,7 +719,19 @@ __global__ void __launch_bounds__(256) moe1_down_kernel(const uint8_t* __restric
   };
   W wa[UPL], wb[UPL];
   load_unit_w(0, wa);  // in flight while the act rows are quantized
-  stage_quant_rows(reinterpret_cast<uint8_t*>(s_x), act, ffn, aq_rb, k, 0);
+  if constexpr (PRE) {
+    // blocks past the last one quantize into a dummy block after the dots (no branch skips a wait)
+    uint8_t* dummy = reinterpret_cast<uint8_t*>(s_dot + k * RW);
+#pragma unroll
+    for (int q = 0; q < kDown1PreBlocks; q++) {
+      const int b = wv + 4 * q, j = b / nbk, jb = b - j * nbk;
+      const float e[4] = {av[q].x, av[q].y, av[q].z, av[q].w};
+      q8k_block_wave(e, lane, b < total_blk ? reinterpret_cast<uint8_t*>(s_x) + int64_t(j) * aq_rb + 292 * jb : dummy);
+    }
+    lds_barrier();
+  } else {
+    stage_quant_rows(reinterpret_cast<uint8_t*>(s_x), act, ffn, aq_rb, k, 0);
+  }
   for (int i = 0;; i += 2) {  // upg is even: the loop's only exit is at the bottom
     load_unit_w(i + 1, wb);
     __builtin_amdgcn_sched_barrier(0);
@@ -1285,8 +1311,10 @@ void down1_one(const MoeArgs& a, hipStream_t s) {
   const int U = units_per_row(F, a.ffn), upg = 2;
   const int RW = std::max(1, 4 * G * upg / a.top_k);
   const int64_t arb = row_bytes(JERO_Q8_K, a.ffn);
-  const size_t lds = size_t(a.top_k) * size_t(arb) + sizeof(float) * size_t(a.top_k) * RW;
-  hipLaunchKernelGGL((moe1_down_kernel<F, LPR, UPL>), dim3(unsigned((a.hidden + RW - 1) / RW)), dim3(256), lds, s,
+  const size_t lds = size_t(a.top_k) * size_t(arb) + sizeof(float) * size_t(a.top_k) * RW + 292;  // + dummy block
+  const bool pre = a.top_k * (a.ffn / 256) <= 4 * kDown1PreBlocks;
+  hipLaunchKernelGGL((pre ? moe1_down_kernel<F, LPR, UPL, true> : moe1_down_kernel<F, LPR, UPL, false>),
+                     dim3(unsigned((a.hidden + RW - 1) / RW)), dim3(256), lds, s,
                      static_cast<const uint8_t*>(a.down), a.E * a.hidden, row_bytes(F, a.ffn), U, int(a.hidden), a.act,
                      int(a.ffn), arb, a.top_k, a.sel_idx, a.sel_w, a.y, RW, upg, int(a.accumulate), a.resid);
 }

@@ -455,7 +455,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
   constexpr int QC = MAXG;      // score columns with a q row
   static_assert(MAXG <= 16 && (HD == 64 || HD == 128), "tile shape");
   __shared__ __attribute__((aligned(16))) float s_q[16][HD];
-  __shared__ __attribute__((aligned(16))) float s_kn[HD];
+  __shared__ __attribute__((aligned(16))) float s_kn[HD], s_vn[HD];
   __shared__ float s_o[NW][QC][HD];
   __shared__ float s_m[NW][16], s_l[NW][16];
 
@@ -478,9 +478,10 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
     const int c = min(wv + NW * j, ncol - 1);
     qv[j] = reinterpret_cast<const float2*>(p.q + (int64_t(kh) * group + c) * HD)[pr];
   }
-  float2 knv = make_float2(0.f, 0.f), qnw = knv, knw = knv, csv = knv;
+  float2 knv = make_float2(0.f, 0.f), vnv = knv, qnw = knv, knw = knv, csv = knv;
   if constexpr (FUSED) {
     knv = reinterpret_cast<const float2*>(p.k_new + kh * HD)[pr];
+    vnv = reinterpret_cast<const float2*>(p.v_new + kh * HD)[pr];
     qnw = reinterpret_cast<const float2*>(p.q_norm ? p.q_norm : p.q)[pr];
     knw = reinterpret_cast<const float2*>(p.k_norm ? p.k_norm : p.q)[pr];
     csv = reinterpret_cast<const float2*>(p.rope_cs ? p.rope_cs : p.q)[pr];
@@ -535,27 +536,28 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
     }
     return make_float2(x.x * cs.x - x.y * cs.y, x.x * cs.y + x.y * cs.x);
   };
+  // (the debug trace of q and k is written at the end: a conditional store here would leave the
+  // compiler unable to count the K/V loads in flight, and the scores would wait for V as well)
+  float2 q_tr[HPW], k_tr = make_float2(0.f, 0.f);
 #pragma unroll
   for (int j = 0; j < HPW; j++) {
     const int h = wv + NW * j;
     float2 x = qv[j];
     if constexpr (FUSED) x = norm_rope(x, p.q_norm != nullptr, qnw);
+    q_tr[j] = x;
     if (h < 16 && lane < HD / 2) {
       const bool real = h < ncol;
       reinterpret_cast<float2*>(s_q[h])[lane] = real ? make_float2(x.x * p.scale, x.y * p.scale) : make_float2(0.f, 0.f);
-      if constexpr (FUSED) {
-        if (real && split == 0 && p.tr_q) reinterpret_cast<float2*>(p.tr_q + (int64_t(kh) * group + h) * HD)[lane] = x;
-      }
     }
   }
   for (int h = wv + NW * HPW; h < 16; h += NW)  // rows no wave prepared (MAXG < 16)
     if (lane < HD / 2) reinterpret_cast<float2*>(s_q[h])[lane] = make_float2(0.f, 0.f);
   if constexpr (FUSED) {
     if (has_slot && wv == 0) {
-      const float2 k = norm_rope(knv, p.k_norm != nullptr, knw);
+      k_tr = norm_rope(knv, p.k_norm != nullptr, knw);
       if (lane < HD / 2) {
-        reinterpret_cast<float2*>(s_kn)[lane] = k;
-        if (p.tr_k) reinterpret_cast<float2*>(p.tr_k + int64_t(kh) * HD)[lane] = k;
+        reinterpret_cast<float2*>(s_kn)[lane] = k_tr;
+        reinterpret_cast<float2*>(s_vn)[lane] = vnv;
       }
     }
   }
@@ -582,7 +584,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
 #pragma unroll
       for (int j = 0; j < NCH; j++) {
         const int d = 8 * (4 * j + kq);
-        const float* vn = p.v_new + int64_t(kh) * HD + d;
+        const float* vn = s_vn + d;  // the new v, loaded at entry (a load here would sit under a branch)
         uint32_t kw[4], vw[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -698,6 +700,17 @@ __global__ void __launch_bounds__(kAttnThreads) attn_mfma_kernel(AttnParams p) {
       p.part_ml[row * 2 + 0] = M;
       p.part_ml[row * 2 + 1] = L;
     }
+  }
+  if constexpr (FUSED) {  // debug trace: q after QK-norm and RoPE (split 0), the new k (its slot's workgroup)
+    if (split == 0 && p.tr_q != nullptr && lane < HD / 2) {
+#pragma unroll
+      for (int j = 0; j < HPW; j++) {
+        const int h = wv + NW * j;
+        if (h < 16 && h < ncol) reinterpret_cast<float2*>(p.tr_q + (int64_t(kh) * group + h) * HD)[lane] = q_tr[j];
+      }
+    }
+    if (has_slot && wv == 0 && p.tr_k != nullptr && lane < HD / 2)
+      reinterpret_cast<float2*>(p.tr_k + int64_t(kh) * HD)[lane] = k_tr;
   }
 }
 

@@ -71,12 +71,17 @@ def cosine(a, b):
 QWEN3_MOE = dict(hidden=2048, ffn=6144, n_layers=2, vocab=2000, nq=32, nkv=4, hd=128, eps=1e-6, theta=1e6)
 SMALL = dict(hidden=1024, ffn=512, n_layers=2, vocab=1000, nq=16, nkv=4, hd=64, eps=1e-6, theta=1e6)
 
-# name: (spec, moe (E, top_k, F, use_shared), router layers (None: all), capacity, prefill, steps)
+# name: (spec, moe (E, top_k, F, use_shared), router layers (None: all), capacity, prefill, steps,
+# build_moe's formats)
 CASES = {
-    "qwen3_30b_a3b_layers": (QWEN3_MOE, (128, 8, 768, False), None, 512, 500, 3),
-    "shared_expert": (SMALL, (16, 4, 256, True), None, 128, 60, 4),
-    "layer_without_router": (SMALL, (16, 4, 256, False), {0}, 128, 60, 4),
-    "256_experts": (SMALL, (256, 8, 256, False), None, 128, 0, 4),
+    "qwen3_30b_a3b_layers": (QWEN3_MOE, (128, 8, 768, False), None, 512, 500, 3, {}),
+    "shared_expert": (SMALL, (16, 4, 256, True), None, 128, 60, 4, {}),
+    "layer_without_router": (SMALL, (16, 4, 256, False), {0}, 128, 60, 4, {}),
+    "256_experts": (SMALL, (256, 8, 256, False), None, 128, 0, 4, {}),
+    # routers the F32 router-norm kernel does not take (F16 values; Q8_0 through the quantized
+    # activation and GEMV), and Q4_K down experts (the Q4_K_T down kernels)
+    "f16_router_q4k_down": (SMALL, (32, 4, 256, False), None, 128, 30, 3, dict(router_quant=J.F16, down_quant=J.Q4_K)),
+    "q8_0_router": (SMALL, (32, 4, 256, False), None, 128, 30, 3, dict(router_quant=J.Q8_0)),
 }
 
 
@@ -168,9 +173,9 @@ def check_logits(got, free, gtok, pos):
 
 @pytest.mark.parametrize("case", sorted(CASES))
 def test_moe_decode_matches_oracle(dev, case):
-    spec, moe, routers, cap, prefill, steps = CASES[case]
+    spec, moe, routers, cap, prefill, steps, fmts = CASES[case]
     print(f"moe decode {case}", flush=True)
-    t, w = MS.build_moe(spec, moe, seed=60 + sorted(CASES).index(case), router_layers=routers)
+    t, w = MS.build_moe(spec, moe, seed=60 + sorted(CASES).index(case), router_layers=routers, **fmts)
     m = make(spec, moe, t, cap)
     om = O.DecodeModel(spec, MS.oracle_tensors(t), cap)
     kv = prefill_rings(m, om, spec, cap, prefill, 3, dev)
@@ -264,12 +269,14 @@ def test_moe_prefill_matches_oracle(dev, case):
     m2.close()
 
 
-def test_moe_prefill_equals_decode_steps(dev):
-    """jero_hip_model_prefill of a MoE model that the batched pass does not take (here: a shared
-    expert) runs the reference's token loop: it leaves the state the same tokens' decode steps
-    leave, logits, token, position and rings bit for bit."""
-    spec, moe = SMALL, (16, 4, 256, True)
-    t, _ = MS.build_moe(spec, moe, seed=71)
+@pytest.mark.parametrize("what", ["shared_expert", "f16_router"])
+def test_moe_prefill_equals_decode_steps(dev, what):
+    """jero_hip_model_prefill of a MoE model that the batched pass does not take (a shared expert,
+    a router in another format than F32) runs the reference's token loop: it leaves the state the
+    same tokens' decode steps leave, logits, token, position and rings bit for bit."""
+    spec = SMALL
+    moe = (16, 4, 256, what == "shared_expert")
+    t, _ = MS.build_moe(spec, moe, seed=71, **({"router_quant": J.F16} if what == "f16_router" else {}))
     a, b = make(spec, moe, t, 128), make(spec, moe, t, 128)
     tokens = np.array([5, 17, 3, 99, 42, 7], np.int32)
     a.prefill(tokens, 10)

@@ -212,6 +212,8 @@ def test_moe_decode_matches_oracle(dev, case):
 # take the GEMV passes, from 32 (256 (token, slot) pairs over 128 experts) the MFMA expert GEMMs
 # in passes of 8 tokens, from 256 (16 per expert on average) in passes of 16
 PREFILL_CASES = {
+    # 1100 tokens at top-8: two routing chunks (8192 pairs each at most); sampled tokens checked
+    "chunked_1100_tokens": (SMALL, (16, 8, 256, False), 1152, 8, 1100, [0, 1, 700, 1022, 1023, 1024, 1025, 1099]),
     "qwen3_30b_a3b_layers_288_tokens": (QWEN3_MOE, (128, 8, 768, False), 512, 16, 288),
     "qwen3_30b_a3b_layers_96_tokens": (QWEN3_MOE, (128, 8, 768, False), 256, 40, 96),
     "qwen3_30b_a3b_layers_9_tokens": (QWEN3_MOE, (128, 8, 768, False), 256, 0, 9),
@@ -224,7 +226,8 @@ def test_moe_prefill_matches_oracle(dev, case):
     """The batched MoE prefill (the experts' GEMMs over the prompt rows) writes every prompt token's
     trace in the decode step's layout: each token is held to the decode step's teacher-forced
     bars, and the last token's logits to the free-running oracle's token loop."""
-    spec, moe, cap, pos0, n = PREFILL_CASES[case]
+    spec, moe, cap, pos0, n = PREFILL_CASES[case][:5]
+    sample = set(PREFILL_CASES[case][5]) if len(PREFILL_CASES[case]) > 5 else set(range(n))
     print(f"moe prefill {case}", flush=True)
     t, w = MS.build_moe(spec, moe, seed=80 + sorted(PREFILL_CASES).index(case))
     m = make(spec, moe, t, cap)
@@ -245,12 +248,13 @@ def test_moe_prefill_matches_oracle(dev, case):
     assert gpos == pos0 + n
     worst = dict(attn=0.0, gemv=0.0, xn=0.0, router=0.0, ffn=0.0, flips=0)
     for i in range(n):
-        dl, dh = m.read_trace(buf[i * total:])
-        wi = check_layers(m, dl, dh, t, w, spec, moe, pos0 + i, cap)
-        worst = {a: worst[a] + wi[a] if a == "flips" else max(worst[a], wi[a]) for a in worst}
+        if i in sample:
+            dl, dh = m.read_trace(buf[i * total:])
+            wi = check_layers(m, dl, dh, t, w, spec, moe, pos0 + i, cap)
+            worst = {a: worst[a] + wi[a] if a == "flips" else max(worst[a], wi[a]) for a in worst}
         free = om.moe_step(kv_free, int(tokens[i]), pos0 + i, moe, w)
     cs = check_logits(got, free, gtok, pos0 + n - 1)
-    print(f"  {n} tokens: teacher-forced max errors " + " ".join(f"{a} {b:.1e}" for a, b in worst.items()) +
+    print(f"  {n} tokens ({len(sample)} checked): teacher-forced max errors " + " ".join(f"{a} {b:.1e}" for a, b in worst.items()) +
           f" | last token against the free-running oracle: rel err {rel(got, free):.2e} cos {cs:.8f}", flush=True)
     m.set_trace(None)
     m.status()

@@ -503,6 +503,23 @@ static jero_hip_tensor view_of(const DevTensor& t) {
 // gate / up / down tensors of that many experts re-laid out in 16-row tiles for the expert kernels.
 // Without a router (or with num_experts or top_k 0, or without expert tensors: ran_any_expert false)
 // the layer runs run_dense_swiglu_ffn with the expert FFN dimension (:873-880, :942-946).
+// The launch arguments of layer l's routed experts (its router's E, top-k, the stacked expert
+// tensors as finalize left them); the caller sets the tokens, inputs and outputs.
+static MoeArgs moe_args_of(const jero_model* m, const LayerW& l) {
+  MoeArgs a{};
+  a.E = l.n_experts;
+  a.top_k = m->moe_top_k;
+  a.gate_quant = l.gate_exps.quant;
+  a.up_quant = l.up_exps.quant;
+  a.down_quant = l.down_exps.quant;
+  a.gate = l.gate_exps.dev;
+  a.up = l.up_exps.dev;
+  a.down = l.down_exps.dev;
+  a.hidden = m->cfg.hidden;
+  a.ffn = l.exp_ffn;
+  return a;
+}
+
 static int moe_layer_finalize(jero_model* m, int64_t L, LayerW& l) {
   const int64_t H = m->cfg.hidden;
   const std::string at = "finalize: layer " + std::to_string(L) + ": ";
@@ -545,19 +562,9 @@ static int moe_layer_finalize(jero_model* m, int64_t L, LayerW& l) {
       t->quant = dq;
     }
   }
-  MoeArgs a{};
+  MoeArgs a = moe_args_of(m, l);
   a.x = a.logits = reinterpret_cast<const float*>(l.router.dev);  // non-null stand-ins for the check
   a.T = 1;
-  a.E = E;
-  a.top_k = m->moe_top_k;
-  a.gate_quant = l.gate_exps.quant;
-  a.up_quant = l.up_exps.quant;
-  a.down_quant = l.down_exps.quant;
-  a.gate = l.gate_exps.dev;
-  a.up = l.up_exps.dev;
-  a.down = l.down_exps.dev;
-  a.hidden = H;
-  a.ffn = F;
   a.y = reinterpret_cast<float*>(l.router.dev);
   a.sel_idx = reinterpret_cast<int32_t*>(l.router.dev);
   a.sel_w = a.y;
@@ -627,33 +634,25 @@ static int moe_ffn_step(jero_model* m, const LayerW& l, float eps, hipStream_t s
       return rc;
     rc = launch_det_proj(m->moe_y, H, nullptr, 0.f, 1.0f, m->hidden, H, true, s);  // hidden += out (x * 1 exact)
   } else {
-    // router logits (matvec_any over the router's eff_experts rows, :882-890)
+    // router logits (matvec_any over the router's eff_experts rows, :882-890): the fused launch
+    // above wrote them; otherwise the GEMV of float rows, or of quantized rows over xn quantized
     const int E = int(l.n_experts);
-    if (!fused && is_float_weight(l.router.quant)) {
-      rc = launch_matvec_float(l.router.quant, l.router.dev, H, E, m->moe_xn, m->moe_logits, s);
-    } else if (!fused && !(rc = launch_quantize_act(act_format(l.router.quant), m->moe_xn, 1, H, m->moe_xq, s))) {
-      rc = launch_matvec(l.router.quant, l.router.dev, H, E, m->moe_xq, m->moe_logits, nullptr, s);
+    if (!fused) {
+      if (is_float_weight(l.router.quant))
+        rc = launch_matvec_float(l.router.quant, l.router.dev, H, E, m->moe_xn, m->moe_logits, s);
+      else if (!(rc = launch_quantize_act(act_format(l.router.quant), m->moe_xn, 1, H, m->moe_xq, s)))
+        rc = launch_matvec(l.router.quant, l.router.dev, H, E, m->moe_xq, m->moe_logits, nullptr, s);
+      if (rc) return rc;
     }
-    if (rc) return rc;
     if (tr_logits && (rc = check_hip(hipMemcpyAsync(tr_logits, m->moe_logits, sizeof(float) * size_t(E),
                                                     hipMemcpyDeviceToDevice, s), "decode trace copy")))
       return rc;
     // select_top_k_experts and the experts' SwiGLU, summed in selection order onto the shared
     // expert's output (or zero) and that sum added to hidden (:890-938, :1301-1303)
-    MoeArgs a{};
+    MoeArgs a = moe_args_of(m, l);
     a.x = m->moe_xn;
     a.logits = m->moe_logits;
     a.T = 1;
-    a.E = E;
-    a.top_k = m->moe_top_k;
-    a.gate_quant = l.gate_exps.quant;
-    a.up_quant = l.up_exps.quant;
-    a.down_quant = l.down_exps.quant;
-    a.gate = l.gate_exps.dev;
-    a.up = l.up_exps.dev;
-    a.down = l.down_exps.dev;
-    a.hidden = H;
-    a.ffn = l.exp_ffn;
     a.y = m->moe_y;
     a.accumulate = shared;
     a.resid = m->hidden;
@@ -1425,20 +1424,10 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
                                              hipMemcpyDeviceToDevice, s),
                             "prefill trace copy")))
           return rc;
-        MoeArgs a{};
+        MoeArgs a = moe_args_of(m, l);
         a.x = b.XN + t0 * H;
         a.logits = b.LG;
         a.T = nt;
-        a.E = E;
-        a.top_k = m->moe_top_k;
-        a.gate_quant = l.gate_exps.quant;
-        a.up_quant = l.up_exps.quant;
-        a.down_quant = l.down_exps.quant;
-        a.gate = l.gate_exps.dev;
-        a.up = l.up_exps.dev;
-        a.down = l.down_exps.dev;
-        a.hidden = H;
-        a.ffn = l.exp_ffn;
         a.y = b.T;  // not written: the sums go to the hidden rows
         a.accumulate = false;
         a.resid = b.X + t0 * H;
@@ -1446,7 +1435,6 @@ extern "C" int jero_hip_model_prefill(jero_model* m, const int32_t* tokens, int6
         a.sel_w = b.SW;
         if ((rc = launch_moe(a, b.MWS, s))) return rc;
       }
-      have_fmt = -1;
       continue;
     }
     // FFN: (residual +) RMSNorm rows -> gate | up -> SwiGLU -> down + residual

@@ -285,15 +285,20 @@ int jero_hip_gqa_attention(float *out_dev, const float *q_dev, const void *k_dev
  * run_single_swiglu_expert (:748-771) per selected expert:
  *   y[t] = sum_j w[t][j] * down_e(silu(gate_e x_t) * up_e x_t),  e = sel_idx[t][j].
  * x_dev [n_tokens][hidden] f32 (16-byte aligned); router_logits_dev [n_tokens][n_experts] f32;
- * gate/up: stacked [n_experts][ffn rows][hidden] in one K-quant; down: [n_experts][hidden rows][ffn]
- * in Q4_K or Q6_K (GGUF stacked [hidden, ffn, n_experts] tensors, expert e = rows e*ffn..), or the
- * same tensors after jero_hip_repack_experts (JERO_Q4_K_T / JERO_Q6_K_T, the layouts the expert
- * GEMMs read fastest) or jero_hip_repack over all their rows (JERO_Q4_K_R / JERO_Q6_K_R); repacked
- * tensors 16-byte aligned.
+ * gate/up: stacked [n_experts][ffn rows][hidden] in one format; down: [n_experts][hidden rows][ffn];
+ * each Q4_K, Q6_K, Q8_0 or Q4_0 (GGUF stacked [hidden, ffn, n_experts] tensors, expert e = rows
+ * e*ffn..), the K-quants also after jero_hip_repack_experts (JERO_Q4_K_T / JERO_Q6_K_T, the layouts
+ * the expert GEMMs read fastest) or jero_hip_repack over all their rows (JERO_Q4_K_R /
+ * JERO_Q6_K_R); repacked tensors 16-byte aligned.  Activations are quantized as matvec_any
+ * quantizes them for each format (Q8_K for the K-quants, ACT_Q8 for Q8_0 / Q4_0); the expert
+ * GEMMs on the matrix cores take the K-quants, the 32-element formats run the GEMV kernels at
+ * any token count.
  * Outputs y_dev [n_tokens][hidden], sel_idx_dev / sel_w_dev [n_tokens][top_k].
  * Limits the reference does not have, refused with CapabilityMismatch: hidden <= 8192 (the gate/up
- * rows' lane pairing), ffn <= 16384 (the down rows'), top_k <= 16 and n_experts <= 1024 (the
- * routing kernels' per-lane columns); Qwen3-MoE (128 experts, top-8, hidden up to 4096, ffn 768 /
+ * rows' lane pairing; 4096 for Q8_0 / Q4_0), ffn <= 16384 (the down rows'; 8192 for Q8_0 / Q4_0),
+ * top_k <= 16 and n_experts <= 1024 (the routing kernels' per-lane columns); hidden and ffn
+ * multiples of 256 whatever the format (TensorBoundsError; the activations are quantized in
+ * 256-element groups); Qwen3-MoE (128 experts, top-8, hidden up to 4096, ffn 768 /
  * 1536) and DeepSeek-style routers (256 experts, top-8) sit well inside them.  Workspace:
  * jero_hip_moe_workspace_bytes(...) bytes, 256-byte aligned (NULL: library-owned). */
 int jero_hip_moe_ffn(const float *x_dev, const float *router_logits_dev, int64_t n_tokens, int64_t n_experts,

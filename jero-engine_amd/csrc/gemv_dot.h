@@ -388,6 +388,11 @@ struct Unit<JERO_Q8_0> {
     float d = h2f(w.D[0] >> (8u * w.s));
     return d * A.dx * float(s);
   }
+
+  // the many-token form of the expert kernels: nothing to unpack ahead of the token loop
+  using Prep = W;
+  static __device__ __forceinline__ void prep(Prep& p, const W& w, int /*u*/) { p = w; }
+  static __device__ __forceinline__ float dot_prep(const Prep& p, const Act& A) { return dot(p, A, nullptr); }
 };
 
 // ---------------------------------------------------------------- Q4_0 x ACT_Q8
@@ -442,6 +447,10 @@ struct Unit<JERO_Q4_0> {
     float d = h2f(w.D[0] >> (8u * w.s));
     return d * A.dx * float(s);
   }
+
+  using Prep = W;
+  static __device__ __forceinline__ void prep(Prep& p, const W& w, int /*u*/) { p = w; }
+  static __device__ __forceinline__ float dot_prep(const Prep& p, const Act& A) { return dot(p, A, nullptr); }
 };
 
 // Units per row and partial sums per row of a weight format.  "Planar": a device layout read

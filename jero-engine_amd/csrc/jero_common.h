@@ -280,6 +280,25 @@ __device__ __forceinline__ void q8k_block_wave(const float e[4], int lane, uint8
   q8k_block_wave_split(e, lane, ob + 4, ob + 260, ob);
 }
 
+// The same 256 elements as eight ACT_Q8 blocks (the activations of Q8_0 / Q4_0 weights) at
+// ob + 36 j, block j from lanes 8j .. 8j + 7: f32 d = amax / 127, q = rint(x * (1 / d)) (0 for an
+// all-zero block), the operations of the ACT_Q8 quantizer kernel.  ob is 4-byte aligned.
+__device__ __forceinline__ void actq8_blocks_wave(const float e[4], int lane, uint8_t* ob) {
+  float a = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 4; t++) a = fmaxf(a, fabsf(e[t]));
+#pragma unroll
+  for (int off = 1; off < 8; off <<= 1) a = fmaxf(a, __shfl_xor(a, off, kWave));
+  const float d = a / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  uint32_t packed = 0;
+#pragma unroll
+  for (int t = 0; t < 4; t++) packed |= (uint32_t(int(__builtin_rintf(e[t] * id))) & 0xFFu) << (8 * t);
+  uint8_t* blk = ob + 36 * (lane >> 3);
+  *reinterpret_cast<uint32_t*>(blk + 4 + 4 * (lane & 7)) = packed;
+  if ((lane & 7) == 0) *reinterpret_cast<float*>(blk) = d;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));

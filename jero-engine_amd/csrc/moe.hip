@@ -36,6 +36,16 @@ constexpr int kMaxTopK = 16;
 constexpr int kRouteLdsPairs = 8192;  // (token, slot) pairs grouped from LDS (keys hold 13 bits)
 constexpr int kGroupSortPairs = 1024;  // above this many pairs, grouping sorts instead of ranking
 
+// Activations are quantized in 256-element groups, one wave per group (four consecutive elements
+// per lane), to the format of the weights they meet: one Q8_K block (292 bytes) for the K-quants,
+// eight ACT_Q8 blocks (288 bytes) for Q8_0 / Q4_0.  A row keeps the Q8_K row's stride either way.
+__host__ __device__ constexpr bool act_is_q8(int f) { return f == JERO_Q8_0 || f == JERO_Q4_0; }
+__host__ __device__ constexpr int act_group_bytes(bool aq8) { return aq8 ? 288 : 292; }
+__device__ __forceinline__ void act_group_wave(const float e[4], int lane, uint8_t* ob, bool aq8) {
+  if (aq8) actq8_blocks_wave(e, lane, ob);
+  else q8k_block_wave(e, lane, ob);
+}
+
 // Routes token t in one wave (PER = expert columns per lane, E <= 64 * PER): f32 softmax over
 // all experts, top-k by (logit desc, index asc) with non-finite logits last, renormalised
 // weights -> sel_idx / sel_w (and s_sel when given).
@@ -305,23 +315,24 @@ __device__ void group_pairs(GroupLds& g, const int32_t* __restrict__ sel_idx, in
   }
 }
 
-// Few tokens: one workgroup quantizes the hidden vectors to Q8_K (when xq is given; one wave per
-// 256-element block), routes (one wave per token) and groups.
+// Few tokens: one workgroup quantizes the hidden vectors (when xq is given; one wave per
+// 256-element group; aq8: the ACT_Q8 blocks of Q8_0 / Q4_0 gate/up weights, else Q8_K), routes
+// (one wave per token) and groups.
 template <int PER>
 __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits, int T, int E,
                                                                   int k, int32_t* __restrict__ sel_idx,
                                                                   float* __restrict__ sel_w, MoeLists lists,
                                                                   const float* __restrict__ x, int H,
-                                                                  uint8_t* __restrict__ xq, int64_t xq_rb) {
+                                                                  uint8_t* __restrict__ xq, int64_t xq_rb, int aq8) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = kRouteThreads / 64;
   __shared__ GroupLds g;
   if (xq) {
-    const int bpr = H / 256, nblk = T * bpr;
+    const int bpr = H / 256, nblk = T * bpr, gb = act_group_bytes(aq8);
     for (int blk = wv; blk < nblk; blk += nw) {
       const int t = blk / bpr, j = blk - t * bpr;
       const float4 v = reinterpret_cast<const float4*>(x + int64_t(t) * H + int64_t(j) * 256)[lane];
       const float e[4] = {v.x, v.y, v.z, v.w};
-      q8k_block_wave(e, lane, xq + int64_t(t) * xq_rb + int64_t(j) * 292);
+      act_group_wave(e, lane, xq + int64_t(t) * xq_rb + int64_t(j) * gb, aq8);
     }
   }
   group_init(g, E);
@@ -329,22 +340,22 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
   group_pairs(g, sel_idx, T * k, E, k, lists);
 }
 
-// Many tokens, first step: workgroups [0, n_quant_wg) quantize the hidden vectors to Q8_K (one
-// wave per 256-element block), the others route one token per wave.  Spreading the routing over
+// Many tokens, first step: workgroups [0, n_quant_wg) quantize the hidden vectors (one wave per
+// 256-element group, in the format aq8 names as above), the others route one token per wave.  Spreading the routing over
 // many CUs matters: a single workgroup is bound by one CU's VALU issue at a few dozen tokens.
 template <int PER>
 __global__ void __launch_bounds__(256) moe_prep_kernel(const float* __restrict__ logits, int T, int E, int k,
                                                        int32_t* __restrict__ sel_idx, float* __restrict__ sel_w,
                                                        const float* __restrict__ x, int H, uint8_t* __restrict__ xq,
-                                                       int64_t xq_rb, int n_quant_wg) {
+                                                       int64_t xq_rb, int n_quant_wg, int aq8) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   if (int(blockIdx.x) < n_quant_wg) {
-    const int bpr = H / 256, nblk = T * bpr;
+    const int bpr = H / 256, nblk = T * bpr, gb = act_group_bytes(aq8);
     for (int blk = int(blockIdx.x) * 4 + wv; blk < nblk; blk += n_quant_wg * 4) {
       const int t = blk / bpr, j = blk - t * bpr;
       const float4 v = reinterpret_cast<const float4*>(x + int64_t(t) * H + int64_t(j) * 256)[lane];
       const float e[4] = {v.x, v.y, v.z, v.w};
-      q8k_block_wave(e, lane, xq + int64_t(t) * xq_rb + int64_t(j) * 292);
+      act_group_wave(e, lane, xq + int64_t(t) * xq_rb + int64_t(j) * gb, aq8);
     }
   } else {
     const int t = (int(blockIdx.x) - n_quant_wg) * 4 + wv;
@@ -374,6 +385,7 @@ __device__ __forceinline__ void vm_settle() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // Makes v opaque to the optimizer at this point (it waits for v's load here): a value picked by
 // lane from loaded registers is otherwise turned back into a load of its own, a second trip.
 __device__ __forceinline__ void pin(u32x4& v) { asm volatile("" : "+v"(v)); }
+
 
 // Unit u of row `row` of a stacked expert tensor of n_rows rows: GGUF bytes (rb per row) or a
 // planar layout (Q4_K_R / Q6_K_R, as written by jero_hip_repack over all n_rows rows).
@@ -411,11 +423,11 @@ __device__ __forceinline__ void stage_rows(uint32_t* __restrict__ dst, const uin
   lds_barrier();
 }
 
-// Quantizes n consecutive f32 rows (src rows row0 .. row0 + n, `cols` floats each) to Q8_K rows of
-// `qrb` bytes in LDS, one wave per 256-element block; each wave loads four blocks before
-// quantizing them.  Ends with a barrier on LDS traffic.
+// Quantizes n consecutive f32 rows (src rows row0 .. row0 + n, `cols` floats each) to activation
+// rows of `qrb` bytes in LDS (aq8: ACT_Q8, else Q8_K), one wave per 256-element group; each wave
+// loads four groups before quantizing them.  Ends with a barrier on LDS traffic.
 __device__ __forceinline__ void stage_quant_rows(uint8_t* __restrict__ dst, const float* __restrict__ src, int cols,
-                                                 int64_t qrb, int n, int row0) {
+                                                 int64_t qrb, int n, int row0, bool aq8) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = int(blockDim.x) >> 6;
   const int bpr = cols / 256, total = n * bpr;
   for (int b0 = wv; b0 < total; b0 += 4 * nw) {
@@ -431,7 +443,7 @@ __device__ __forceinline__ void stage_quant_rows(uint8_t* __restrict__ dst, cons
       if (b < total) {
         const int j = b / bpr, jb = b - j * bpr;
         const float e[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
-        q8k_block_wave(e, lane, dst + int64_t(j) * qrb + int64_t(jb) * 292);
+        act_group_wave(e, lane, dst + int64_t(j) * qrb + int64_t(jb) * act_group_bytes(aq8), aq8);
       }
     }
   }
@@ -476,7 +488,7 @@ __global__ void __launch_bounds__(256) moe_gate_up_kernel(const uint8_t* __restr
       for (int blk = wv - 1; blk < one.H / 256; blk += 3) {
         const float4 v = reinterpret_cast<const float4*>(one.x + int64_t(blk) * 256)[lane];
         const float ev[4] = {v.x, v.y, v.z, v.w};
-        q8k_block_wave(ev, lane, reinterpret_cast<uint8_t*>(s_x) + blk * 292);
+        act_group_wave(ev, lane, reinterpret_cast<uint8_t*>(s_x) + blk * act_group_bytes(act_is_q8(F)), act_is_q8(F));
       }
     }
     __syncthreads();
@@ -610,7 +622,7 @@ __global__ void __launch_bounds__(256) moe_down_kernel(const uint8_t* __restrict
     const int nch = min(chunk, cnt - base);
     load_row(0, wa);  // in flight while the activations are staged
     lds_barrier();    // the previous pass's readers are done
-    stage_quant_rows(reinterpret_cast<uint8_t*>(s_x), act, ffn, aq_rb, nch, i0 + base);
+    stage_quant_rows(reinterpret_cast<uint8_t*>(s_x), act, ffn, aq_rb, nch, i0 + base, act_is_q8(F));
     for (int it = 0;; it += 2) {  // rpw is even, as ppw in gate/up
       load_row(it + 1, wb);
       __builtin_amdgcn_sched_barrier(0);
@@ -726,11 +738,14 @@ __global__ void __launch_bounds__(256) moe1_down_kernel(const uint8_t* __restric
     for (int q = 0; q < kDown1PreBlocks; q++) {
       const int b = wv + 4 * q, j = b / nbk, jb = b - j * nbk;
       const float e[4] = {av[q].x, av[q].y, av[q].z, av[q].w};
-      q8k_block_wave(e, lane, b < total_blk ? reinterpret_cast<uint8_t*>(s_x) + int64_t(j) * aq_rb + 292 * jb : dummy);
+      act_group_wave(e, lane,
+                     b < total_blk ? reinterpret_cast<uint8_t*>(s_x) + int64_t(j) * aq_rb + act_group_bytes(act_is_q8(F)) * jb
+                                   : dummy,
+                     act_is_q8(F));
     }
     lds_barrier();
   } else {
-    stage_quant_rows(reinterpret_cast<uint8_t*>(s_x), act, ffn, aq_rb, k, 0);
+    stage_quant_rows(reinterpret_cast<uint8_t*>(s_x), act, ffn, aq_rb, k, 0, act_is_q8(F));
   }
   for (int i = 0;; i += 2) {  // upg is even: the loop's only exit is at the bottom
     load_unit_w(i + 1, wb);
@@ -1267,8 +1282,9 @@ int gate_up_fmt(const MoeArgs& a, const MoeLists& L, hipStream_t s, const MoeSin
         gate_up_one<F, 32, 4, SPER>(a, L, one, s);
         return JERO_OK;
       }
-      return fail(JERO_ERR_CAPABILITY_MISMATCH,
-                  "moe: hidden " + std::to_string(a.hidden) + " above the gate/up pairing limit (8192 for K-quants)");
+      return fail(JERO_ERR_CAPABILITY_MISMATCH, "moe: hidden " + std::to_string(a.hidden) +
+                                                    " above the gate/up pairing limit (8192 for K-quants, 4096 for "
+                                                    "Q8_0 / Q4_0)");
   }
 }
 
@@ -1463,6 +1479,8 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
       case JERO_Q4_K_T: rc = gate_up_fmt<JERO_Q4_K_T, 2>(a, L, s, one); break;
       case JERO_Q6_K_T: rc = gate_up_fmt<JERO_Q6_K_T, 2>(a, L, s, one); break;
       case JERO_Q6_K: rc = gate_up_fmt<JERO_Q6_K, 2>(a, L, s, one); break;
+      case JERO_Q8_0: rc = gate_up_fmt<JERO_Q8_0, 2>(a, L, s, one); break;
+      case JERO_Q4_0: rc = gate_up_fmt<JERO_Q4_0, 2>(a, L, s, one); break;
       default: rc = gate_up_fmt<JERO_Q6_K_R, 2>(a, L, s, one); break;
     }
     if (rc) return rc;
@@ -1474,6 +1492,8 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
       case JERO_Q4_K_T: rc = down1_fmt<JERO_Q4_K_T>(a, s); break;
       case JERO_Q6_K_T: rc = down1_fmt<JERO_Q6_K_T>(a, s); break;
       case JERO_Q6_K: rc = down1_fmt<JERO_Q6_K>(a, s); break;
+      case JERO_Q8_0: rc = down1_fmt<JERO_Q8_0>(a, s); break;
+      case JERO_Q4_0: rc = down1_fmt<JERO_Q4_0>(a, s); break;
       default: rc = down1_fmt<JERO_Q6_K_R>(a, s); break;
     }
     if (rc) return rc;
@@ -1486,14 +1506,15 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
   const int per = a.E <= 128 ? 2 : a.E <= 256 ? 4 : a.E <= 512 ? 8 : 16;
   const int n_quant_wg = int(std::min<int64_t>(1024, (a.T * (a.hidden / 256) + 3) / 4));
   const unsigned prep_grid = unsigned(n_quant_wg + (a.T + 3) / 4);
+  const int aq8 = act_is_q8(a.gate_quant);  // the hidden rows' activation format: the gate/up weights'
 #define JERO_ROUTE(P)                                                                                            \
   do {                                                                                                           \
     if (single)                                                                                                  \
       hipLaunchKernelGGL(moe_route_kernel<P>, dim3(1), dim3(kRouteThreads), 0, s, a.logits, int(a.T), int(a.E),  \
-                         a.top_k, a.sel_idx, a.sel_w, L, a.x, int(a.hidden), a.xq, xq_rb);                      \
+                         a.top_k, a.sel_idx, a.sel_w, L, a.x, int(a.hidden), a.xq, xq_rb, aq8);                 \
     else                                                                                                         \
       hipLaunchKernelGGL(moe_prep_kernel<P>, dim3(prep_grid), dim3(256), 0, s, a.logits, int(a.T), int(a.E),     \
-                         a.top_k, a.sel_idx, a.sel_w, a.x, int(a.hidden), a.xq, xq_rb, n_quant_wg);             \
+                         a.top_k, a.sel_idx, a.sel_w, a.x, int(a.hidden), a.xq, xq_rb, n_quant_wg, aq8);        \
   } while (0)
   if (per == 2) JERO_ROUTE(2);
   else if (per == 4) JERO_ROUTE(4);
@@ -1521,6 +1542,8 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
     case JERO_Q4_K_T: rc = gate_up_fmt<JERO_Q4_K_T>(a, L, s); break;
     case JERO_Q6_K_T: rc = gate_up_fmt<JERO_Q6_K_T>(a, L, s); break;
     case JERO_Q6_K: rc = gate_up_fmt<JERO_Q6_K>(a, L, s); break;
+    case JERO_Q8_0: rc = gate_up_fmt<JERO_Q8_0>(a, L, s); break;
+    case JERO_Q4_0: rc = gate_up_fmt<JERO_Q4_0>(a, L, s); break;
     default: rc = gate_up_fmt<JERO_Q6_K_R>(a, L, s); break;
   }
   if (rc) return rc;
@@ -1532,6 +1555,8 @@ int launch_moe(MoeArgs a, void* ws, hipStream_t s) {
     case JERO_Q4_K_T: rc = down_fmt<JERO_Q4_K_T>(a, L, s); break;
     case JERO_Q6_K_T: rc = down_fmt<JERO_Q6_K_T>(a, L, s); break;
     case JERO_Q6_K: rc = down_fmt<JERO_Q6_K>(a, L, s); break;
+    case JERO_Q8_0: rc = down_fmt<JERO_Q8_0>(a, L, s); break;
+    case JERO_Q4_0: rc = down_fmt<JERO_Q4_0>(a, L, s); break;
     default: rc = down_fmt<JERO_Q6_K_R>(a, L, s); break;
   }
   if (rc) return rc;
@@ -1551,11 +1576,14 @@ int check_moe_args(const MoeArgs& a, size_t gate_bytes, size_t up_bytes, size_t 
   if (a.T <= 0 || a.hidden <= 0 || a.ffn <= 0) return fail(JERO_ERR_TENSOR_BOUNDS, "moe: empty input");
   if (a.top_k > a.E || a.top_k > kMaxTopK || a.E > kMaxExperts)
     return fail(JERO_ERR_CAPABILITY_MISMATCH, "moe: top_k must be <= min(n_experts, 16), n_experts <= 1024");
-  if (a.gate_quant != a.up_quant || !is_kquant(a.gate_quant) || !is_kquant(a.down_quant))
-    return fail(JERO_ERR_CAPABILITY_MISMATCH, "moe: gate/up must share a K-quant format; down Q4_K or Q6_K (GGUF, "
-                                              "repacked _R or tiled _T layouts)");
+  auto expert_format = [](int f) { return is_kquant(f) || act_is_q8(f); };
+  if (a.gate_quant != a.up_quant || !expert_format(a.gate_quant) || !expert_format(a.down_quant))
+    return fail(JERO_ERR_CAPABILITY_MISMATCH, "moe: gate/up must share one format; gate/up and down each Q4_K or "
+                                              "Q6_K (GGUF, repacked _R or tiled _T layouts), Q8_0 or Q4_0");
   int64_t rg = row_bytes(a.gate_quant, a.hidden), rd = row_bytes(a.down_quant, a.ffn);
-  if (rg < 0 || rd < 0) return fail(JERO_ERR_TENSOR_BOUNDS, "moe: hidden/ffn not multiples of 256");
+  // (the activations are quantized in 256-element groups, whatever the format)
+  if (rg < 0 || rd < 0 || a.hidden % 256 || a.ffn % 256)
+    return fail(JERO_ERR_TENSOR_BOUNDS, "moe: hidden/ffn not multiples of 256");
   if (uint64_t(rg) * a.ffn * a.E > gate_bytes || uint64_t(rg) * a.ffn * a.E > up_bytes ||
       uint64_t(rd) * a.hidden * a.E > down_bytes)
     return fail(JERO_ERR_TENSOR_BOUNDS, "moe: stacked expert tensors smaller than [E][rows][cols]");

@@ -47,13 +47,15 @@ def build(spec, seed=0, mix="q4_k_m"):
     return t
 
 
-def build_moe(spec, moe, seed=0, router_layers=None, shared_quant=Q8_0, router_quant=F32, down_quant=Q6_K):
+def build_moe(spec, moe, seed=0, router_layers=None, shared_quant=Q8_0, router_quant=F32, down_quant=Q6_K,
+              gate_quant=Q4_K):
     """A Qwen3-MoE-shaped model (the Qwen3 attention of build, then per layer
     dispatch_qwen3_moe_ffn's tensors): a router [hidden, E] of N(0, 0.02) weights (router_quant:
-    F32, F16 or BF16 values, or a quantized format), the stacked Q4_K gate / up experts
-    [hidden, F, E] and down experts [F, hidden, E] in down_quant, and, when moe's use_shared is set,
+    F32, F16 or BF16 values, or a quantized format), the stacked gate / up experts [hidden, F, E]
+    in gate_quant and down experts [F, hidden, E] in down_quant, and, when moe's use_shared is set,
     a shared expert of 2 F rows in shared_quant.  Layers not in router_layers (all by default) have
-    no router: they take run_dense_swiglu_ffn with [hidden, F] Q4_K gate / up and down_quant down.
+    no router: they take run_dense_swiglu_ffn with [hidden, F] gate_quant gate / up and down_quant
+    down.
     moe = (E, top_k, F, use_shared).  Returns (tensors as build returns them,
     {name: (quant, data, dims)} as pyoracle.moe_layer reads them)."""
     from qdata import F16, BF16, rand_float_weights
@@ -78,12 +80,12 @@ def build_moe(spec, moe, seed=0, router_layers=None, shared_quant=Q8_0, router_q
         if router_layers is None or i in router_layers:
             float_router = router_quant in (F32, F16, BF16)
             mat(p + "ffn_gate_inp.weight", router_quant, (H, E), E, H, rand_float_weights if float_router else rand_weights)
-            mat(p + "ffn_gate_exps.weight", Q4_K, (H, F, E), E * F, H)
-            mat(p + "ffn_up_exps.weight", Q4_K, (H, F, E), E * F, H)
+            mat(p + "ffn_gate_exps.weight", gate_quant, (H, F, E), E * F, H)
+            mat(p + "ffn_up_exps.weight", gate_quant, (H, F, E), E * F, H)
             mat(p + "ffn_down_exps.weight", down_quant, (F, H, E), E * H, F)
         else:
-            mat(p + "ffn_gate.weight", Q4_K, (H, F), F, H)
-            mat(p + "ffn_up.weight", Q4_K, (H, F), F, H)
+            mat(p + "ffn_gate.weight", gate_quant, (H, F), F, H)
+            mat(p + "ffn_up.weight", gate_quant, (H, F), F, H)
             mat(p + "ffn_down.weight", down_quant, (F, H), H, F)
         if shared:
             mat(p + "ffn_gate_shexp.weight", shared_quant, (H, 2 * F), 2 * F, H)

@@ -4,7 +4,8 @@ Routing (selected experts and their order) must match exactly and the weights wi
 Outputs are checked per expert, as the decode step is (decode_parity): the oracle quantizes
 each token, runs each selected expert's gate/up from those (bit-identical) activation blocks and
 forms silu(g) * u; the device's f32 SwiGLU rows (jero_hip_moe_trace_view) must match within
-1e-5 of their rms, and the two rows' Q8_K quantizations may differ only by tie flips
+1e-5 of their rms, and the two rows' quantizations (Q8_K, or ACT_Q8 for Q8_0 / Q4_0 down
+experts) may differ only by tie flips
 (decode_parity.tie_flips: pre-rounding values within 0.05 quantum everywhere, each flip a +-1
 crossing of a rounding boundary between them).  The oracle then runs the expert's down
 projection on the device's activation blocks and combines the experts in selection order in
@@ -65,7 +66,7 @@ def check_experts(y, act, x, si, sw, gate, up, down, gq, dq, H, F):
     st = DP.FlipStats()
     act_err = 0.0
     for t in range(x.shape[0]):
-        xq = O.quantize_act(DP.Q8_K, x[t])
+        xq = O.quantize_act(DP.act_fmt(gq), x[t])
         ref = np.zeros(H, np.float32)
         for j, e in enumerate(si[t]):
             g = O.matvec(gq, gate[e * gb:(e + 1) * gb], H, F, xq)
@@ -73,8 +74,9 @@ def check_experts(y, act, x, si, sw, gate, up, down, gq, dq, H, F):
             a_or = O.swiglu(g, u)
             a_dev = act[t, j]
             act_err = max(act_err, DP.rel(a_dev, a_or))
-            q_dev = O.quantize_act(DP.Q8_K, a_dev)
-            st.add(DP.tie_flips(f"token {t} slot {j}", DP.Q8_K, F, a_or, O.quantize_act(DP.Q8_K, a_or), a_dev, q_dev))
+            af = DP.act_fmt(dq)
+            q_dev = O.quantize_act(af, a_dev)
+            st.add(DP.tie_flips(f"token {t} slot {j}", af, F, a_or, O.quantize_act(af, a_or), a_dev, q_dev))
             ref += np.float32(sw[t, j]) * O.matvec(dq, down[e * db:(e + 1) * db], F, H, q_dev)
         err = DP.rel(y[t], ref)
         assert err <= MOE_TOL, (t, err)
@@ -129,6 +131,26 @@ def test_moe_many_tokens_per_expert(dev):
     run_case(dev, 40, 4, 512, 512, 2, J.Q4_K, J.Q6_K, 42, repacked=True)
     run_case(dev, 40, 4, 512, 512, 2, J.Q4_K, J.Q4_K, 43, repacked=True)
     run_case(dev, 24, 3, 256, 768, 3, J.Q6_K, J.Q6_K, 44, repacked=True)
+
+
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_moe_q8_0_and_q4_0_experts(dev, T):
+    """Experts in the 32-element formats, whose activations are ACT_Q8 blocks (the token rows
+    quantized by the routing step or by the one-token gate/up kernel, the SwiGLU rows by the down
+    kernels): Q8_0 throughout, Q4_0 throughout, and each beside a K-quant; one token, a few, and
+    ~20 tokens per expert (the GEMV kernels' token passes: these formats take no MFMA path)."""
+    print(f"moe q8_0 / q4_0 experts T={T}", flush=True)
+    run_case(dev, T, 8, 512, 512, 4, J.Q8_0, J.Q8_0, 1100 + T)
+    run_case(dev, T, 8, 512, 256, 4, J.Q4_0, J.Q4_0, 1110 + T)
+    run_case(dev, T, 8, 256, 512, 2, J.Q8_0, J.Q6_K, 1120 + T)
+    run_case(dev, T, 8, 256, 512, 2, J.Q4_K, J.Q4_0, 1130 + T)
+
+
+def test_moe_q8_0_qwen3_shape(dev):
+    """Hidden 2048 (two units per lane of a 32-lane row group), 128 experts of 768, top-8, Q8_0."""
+    print("moe qwen3 shape q8_0", flush=True)
+    run_case(dev, 1, 128, 2048, 768, 8, J.Q8_0, J.Q8_0, 1140)
+    run_case(dev, 64, 128, 2048, 768, 8, J.Q8_0, J.Q8_0, 1141)
 
 
 @pytest.mark.parametrize("T,E,K", [(130, 16, 8), (300, 64, 4), (200, 700, 16)])

@@ -11,8 +11,8 @@ Per step, every layer teacher-forced from the device's own trace:
     and the same top-k selection;
   * the FFN output (next layer input - mid state) against moe_layer on the device's normalised
     input within 1e-3 of max(|ref|, rms(ref)), the bar of tests/test_gpu_moe_layer.py (the two
-    sides quantize the SwiGLU rows to Q8_K separately: a value within float error of a rounding
-    boundary may round the other way);
+    sides quantize the SwiGLU rows (Q8_K, or ACT_Q8 for Q8_0 / Q4_0 down experts) separately: a
+    value within float error of a rounding boundary may round the other way);
 end to end, the logits against the oracle's free-running step: cosine >= 0.9999 (the reference's
 certification floor) and the greedy token equal when the top-2 gap exceeds 1e-2 of the rms.
 The batched prefill (expert GEMMs over the prompt rows) writes every prompt token's trace in the
@@ -82,19 +82,27 @@ CASES = {
     # activation and GEMV), and Q4_K down experts (the Q4_K_T down kernels)
     "f16_router_q4k_down": (SMALL, (32, 4, 256, False), None, 128, 30, 3, dict(router_quant=J.F16, down_quant=J.Q4_K)),
     "q8_0_router": (SMALL, (32, 4, 256, False), None, 128, 30, 3, dict(router_quant=J.Q8_0)),
+    # experts in the 32-element formats (ACT_Q8 activations): Q8_0 gate / up, Q4_0 down; and the
+    # Qwen3-30B-A3B layer shape with Q8_0 experts throughout
+    "q8_0_gate_up_q4_0_down": (SMALL, (32, 4, 256, False), None, 128, 30, 3,
+                               dict(gate_quant=J.Q8_0, down_quant=J.Q4_0)),
+    "qwen3_30b_a3b_layers_q8_0": (QWEN3_MOE, (128, 8, 768, False), None, 256, 100, 2,
+                                  dict(gate_quant=J.Q8_0, down_quant=J.Q8_0)),
 }
 
 
-def act_ties(act):
-    """Elements of an f32 row whose Q8_K rounding lies within float error of a tie (|q| within
-    1e-3 of k + 0.5, ggml's rule: iscale = -127 / the block's first largest-magnitude value), and
-    each element's block scale |d|: two correct computations of the row may round these apart."""
-    a = np.asarray(act, np.float64).reshape(-1, 256)
+def act_ties(act, fmt=DP.Q8_K):
+    """Elements of an f32 row whose activation rounding lies within float error of a tie (|q|
+    within 1e-3 of k + 0.5; Q8_K: ggml's rule, iscale = -127 / the block's first largest-magnitude
+    value over 256 elements; ACT_Q8: 1 / d = 127 / amax over 32), and each element's block scale
+    |d|: two correct computations of the row may round these apart."""
+    n = 256 if fmt == DP.Q8_K else 32
+    a = np.asarray(act, np.float64).reshape(-1, n)
     mx = a[np.arange(len(a)), np.argmax(np.abs(a), axis=1)]
     iscale = np.where(mx != 0, -127.0 / np.where(mx != 0, mx, 1.0), 0.0)
     y = np.abs(a * iscale[:, None])
     tie = (np.abs(y - np.floor(y) - 0.5) < 1e-3) & (mx != 0)[:, None]
-    return tie.reshape(-1), np.repeat(np.abs(mx) / 127.0, 256)
+    return tie.reshape(-1), np.repeat(np.abs(mx) / 127.0, n)
 
 
 def flip_bound(xn, L, moe, w, sel):
@@ -110,7 +118,7 @@ def flip_bound(xn, L, moe, w, sel):
         g, u, dn = parts
         Fe = O._n_el(g[2]) // H
         act = O.swiglu(O.vec_dot(g[0], g[1], H, Fe, xn), O.vec_dot(u[0], u[1], H, Fe, xn))
-        tie, d = act_ties(act)
+        tie, d = act_ties(act, DP.act_fmt(dn[0]))
         if tie.any():
             Dq = O.dequantize(dn[0], dn[1], H, Fe)
             bound += abs(we) * (np.abs(Dq[:, tie]).astype(np.float64) @ d[tie])
@@ -218,6 +226,9 @@ PREFILL_CASES = {
     "qwen3_30b_a3b_layers_96_tokens": (QWEN3_MOE, (128, 8, 768, False), 256, 40, 96),
     "qwen3_30b_a3b_layers_9_tokens": (QWEN3_MOE, (128, 8, 768, False), 256, 0, 9),
     "256_experts_70_tokens": (SMALL, (256, 8, 256, False), 128, 20, 70),
+    # Q8_0 gate / up and Q4_0 down experts: the GEMV passes at any token count
+    "q8_0_q4_0_experts_40_tokens": (SMALL, (16, 4, 256, False), 128, 12, 40, None,
+                                    dict(gate_quant=J.Q8_0, down_quant=J.Q4_0)),
 }
 
 
@@ -227,9 +238,11 @@ def test_moe_prefill_matches_oracle(dev, case):
     trace in the decode step's layout: each token is held to the decode step's teacher-forced
     bars, and the last token's logits to the free-running oracle's token loop."""
     spec, moe, cap, pos0, n = PREFILL_CASES[case][:5]
-    sample = set(PREFILL_CASES[case][5]) if len(PREFILL_CASES[case]) > 5 else set(range(n))
+    extra = PREFILL_CASES[case][5:]
+    sample = set(extra[0]) if extra and extra[0] is not None else set(range(n))
+    fmts = extra[1] if len(extra) > 1 else {}
     print(f"moe prefill {case}", flush=True)
-    t, w = MS.build_moe(spec, moe, seed=80 + sorted(PREFILL_CASES).index(case))
+    t, w = MS.build_moe(spec, moe, seed=80 + sorted(PREFILL_CASES).index(case), **fmts)
     m = make(spec, moe, t, cap)
     om = O.DecodeModel(spec, MS.oracle_tensors(t), cap)
     kv = prefill_rings(m, om, spec, cap, pos0, 5, dev)

@@ -767,18 +767,20 @@ __global__ void __launch_bounds__(256) moe1_down_kernel(const uint8_t* __restric
 }
 
 // ---------------------------------------------------------------- expert GEMMs on MFMA
-// Several tokens per expert: v_mfma_i32_16x16x64_i8 over one 64-weight unit at a time.  A unit
-// has SEG integer-scaled segments (Q4_K: 2 sub-blocks of 32 weights; Q6_K: 4 groups of 16).  The
-// 16 rows of the A operand are (token, segment) pairs, each holding its token's activations only
-// in the K range of its segment (zeros elsewhere), so one MFMA yields the exact integer partial
-// sum of every segment for TPT = 16 / SEG tokens and 16 weight rows (the B operand, columns).
-// Lane l supplies A row l % 16 and B column l % 16 over K [16 (l / 16), +16) and receives C rows
-// 4 (l / 16) .. +4 of column l % 16: all segments of 4 / SEG tokens for one weight row, so the
-// segment scales and mins come from the lane's own weight row and are applied in-lane, in
-// integers, over the block's four units; the block's float scales then apply once per block,
-// dx * (d * isum - dmin * msum) as the reference's block dot.  Activations are staged in LDS as
-// Q8_K rows (rows of 16-byte multiples, one more row of zeros for the A lanes outside their
-// segment).
+// Several tokens per expert: v_mfma_i32_16x16x64_i8 over one 64-weight unit at a time.  Lane l
+// supplies A row l % 16 and B column l % 16 (a weight row) over K [16 (l / 16), +16) and receives
+// C rows 4 (l / 16) .. +4 of column l % 16.  Two forms, both exact in integers per block:
+//   * Q4_K (plane form): the A rows are 16 tokens.  A lane's 16 weights of a unit lie in one
+//     sub-block, whose 6-bit scale splits as sc = 8a + b: the lane feeds the MFMA the planes
+//     a q4 and b q4 (<= 105), so 8 Ta + Tb over the block's four units is the block's sum of
+//     sc q4 q8 per (token, row), and the mins sum over the 16 bsums is one f16 MFMA.
+//   * Q6_K (segment form): a unit has 4 integer-scaled groups of 16.  The 16 A rows are (token,
+//     group) pairs, each holding its token's activations only in the K range of its group (zeros
+//     elsewhere), so one MFMA yields the exact integer sum of every group for 4 tokens; the group
+//     scales come from the lane's own weight row and are applied in-lane, in integers.
+// The block's float scales then apply once per block, dx * (d * isum - dmin * msum) as the
+// reference's block dot.  Activations are staged in LDS as Q8_K rows (rows of 16-byte multiples,
+// one more row of zeros for the A lanes outside their group).
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -932,10 +934,16 @@ constexpr int kStageBlocks = 8;  // f32 staging: 256-element blocks per wave in 
 // weights.  R is a multiple of 64 * tiles: no row is clamped.
 // Workgroups per CU the register budget is cut for: three (168 VGPRs), except Q6_K gate/up, whose
 // two tensors' pieces need more registers than that without spilling, and the 16-token passes
-// (twice the accumulators) of Q4_K gate/up and Q6_K down: two.  (Q6_K gate/up takes no 16-token
-// passes: they spill at any budget.)
+// (twice the accumulators) of Q6_K down: two.  (Q6_K gate/up takes no 16-token passes: they spill
+// at any budget.)  The Q4_K plane form holds one 16-token tile either way (160 VGPRs).
 __host__ __device__ constexpr int mfma_min_wgs(int f, bool gu, int pt) {
-  return (gu && (mfma_seg(f) == 4 || pt > kMoePassTokens)) || (!gu && mfma_seg(f) == 4 && pt > kMoePassTokens) ? 2 : 3;
+  return mfma_seg(f) == 4 && (gu || pt > kMoePassTokens) ? 2 : 3;
+}
+
+// Four bytes times s (<= 7) as two 16-bit lanes: no carry between bytes, each product <= 105.
+__device__ __forceinline__ uint32_t bytes_times(uint32_t x, uint32_t s) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, x) * u16x2{uint16_t(s), uint16_t(s)});
 }
 
 template <int F, bool GU, int PT>
@@ -944,7 +952,15 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU, PT)) moe_mfma_kernel(
                                                        const uint8_t* __restrict__ xq, int64_t xq_rb,
                                                        const float* __restrict__ act_in, MoeLists lists,
                                                        float* __restrict__ out, int wg_per_expert, int ctr_off) {
-  constexpr int SEG = mfma_seg(F), TPT = 16 / SEG, NT = PT / TPT, LT = 4 / SEG;
+  // Q4_K: the plane form.  A rows are 16 tokens over the whole K range; a lane's B bytes lie in
+  // one sub-block, whose scale sc = 8a + b splits them into the exact int8 planes a q4 and b q4
+  // (<= 105), so two MFMAs per unit sum the scales in and T = 8 Ta + Tb is the block's integer
+  // sum of sc q4 q8 per (token, row); the mins sum over the 16 bsums is one f16 MFMA (exact:
+  // |bsum| <= 2032, m <= 63, sums below 2^24).  The VALU only expands the planes and applies the
+  // block's float scales.  Q6_K: the segment form (below).
+  constexpr int SEG = mfma_seg(F);
+  constexpr bool PLANE = SEG == 2;
+  constexpr int TPT = PLANE ? 16 : 16 / SEG, NT = PLANE ? (PT + 15) / 16 : PT / TPT, LT = PLANE ? 4 : 4 / SEG;
   constexpr int NW = GU ? 2 : 1;  // weight tensors per wave
   using Piece = MfmaPiece<F>;
   using Cur = typename Piece::Cur;
@@ -966,8 +982,8 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU, PT)) moe_mfma_kernel(
   __syncthreads();
   const uint8_t* wt[2] = {w0, GU ? w1 : w0};
   // A operand lanes: virtual row vr = (token, segment); K group kg belongs to segment kg / (4 / SEG)
-  const int vr = lane & 15, a_tok = vr / SEG, kg_seg = kg / (4 / SEG);
-  const bool a_on = vr % SEG == kg_seg;
+  const int vr = lane & 15, a_tok = PLANE ? vr : vr / SEG, kg_seg = kg / (4 / SEG);
+  const bool a_on = PLANE || vr % SEG == kg_seg;
   const int a_lane = SEG == 2 ? 4 + 16 * kg : 4 + 32 * kg;  // the lane's K group in a unit's bytes
   const uint32_t nsh = (kg & 2) ? 4u : 0u;                    // its nibble: low for kg < 2
   static_assert(PT % 4 == 0, "a pass descriptor is 1 + PT / 4 16-byte loads");
@@ -1001,10 +1017,11 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU, PT)) moe_mfma_kernel(
       for (int t = 0; t < NW; t++) Piece::load(p[t], cur[t], tile, sc - tile * nb);
     };
     // the lane's LDS rows: its A row's token (or the zero row), and the tokens of its C rows
-    int a_base[NT], e_base[NT][LT];
+    int a_base[NT], e_base[NT][LT], r_base[NT];
 #pragma unroll
     for (int tl = 0; tl < NT; tl++) {
-      a_base[tl] = (a_on ? min(tl * TPT + a_tok, nch - 1) * stride : zrow) + a_lane;
+      r_base[tl] = min(tl * TPT + a_tok, nch - 1) * stride;  // the A row's token (plane form: its bsums)
+      a_base[tl] = (a_on ? r_base[tl] : zrow) + a_lane;
 #pragma unroll
       for (int q = 0; q < LT; q++) e_base[tl][q] = min(tl * TPT + kg * LT + q, nch - 1) * stride;
     }
@@ -1080,65 +1097,104 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU, PT)) moe_mfma_kernel(
       auto process = [&](int s_, Piece (&p)[NW]) {
         const bool live = s_ < steps;
         const int sc_ = min(s_, steps - 1), tile = sc_ / nb, b = sc_ - tile * nb, bo = 292 * b;
-        int isum[NW][NT][LT], msum[NW][NT][LT];  // the block's integer sums (msum: Q4_K mins)
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        if constexpr (PLANE) {
+          v4i Ca[NW][NTA], Cb[NW][NTA];  // the a and b planes' integer sums over the block
 #pragma unroll
-        for (int x = 0; x < 4; x++) {
-          v4i A[NTA];
+          for (int x = 0; x < 4; x++) {
+            v4i A[NTA];
+#pragma unroll
+            for (int tl = 0; tl < NTA; tl++) {
+              const uint32_t* ap = reinterpret_cast<const uint32_t*>(s_act + a_base[tl] + bo + 64 * x);  // 4-byte aligned
+              A[tl] = v4i{int(ap[0]), int(ap[1]), int(ap[2]), int(ap[3])};
+            }
+#pragma unroll
+            for (int t = 0; t < NW; t++) {
+              // B: this lane's 16 weights of unit x (sub-block 2x + kg / 2) times a and b
+              int sc, mn;
+              q4k_scale_min(p[t].h, 2 * x + (kg >> 1), sc, mn);
+              const uint32_t sa = uint32_t(sc) >> 3, sb = uint32_t(sc) & 7u;
+              const u32x4 q = p[t].q[x];
+              const uint32_t qd[4] = {q.x, q.y, q.z, q.w};
+              v4i Ba, Bb;
+#pragma unroll
+              for (int w = 0; w < 4; w++) {
+                const uint32_t nib = (qd[w] >> nsh) & 0x0F0F0F0Fu;
+                Ba[w] = int(bytes_times(nib, sa));
+                Bb[w] = int(bytes_times(nib, sb));
+              }
+#pragma unroll
+              for (int tl = 0; tl < NTA; tl++) {
+                Ca[t][tl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tl], Ba, x == 0 ? v4i{0, 0, 0, 0} : Ca[t][tl], 0, 0, 0);
+                Cb[t][tl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tl], Bb, x == 0 ? v4i{0, 0, 0, 0} : Cb[t][tl], 0, 0, 0);
+              }
+            }
+          }
+          // the mins: A row = the A token's 16 bsums (this lane: 4 kg .. 4 kg + 3), B column = the
+          // lane's weight row, K slot k taking the min of sub-block k / 2
+          h4 Ab[NTA];
 #pragma unroll
           for (int tl = 0; tl < NTA; tl++) {
-            const int xo = SEG == 2 ? 64 * x : 128 * (x >> 1) + 16 * (x & 1);
-            const uint32_t* ap = reinterpret_cast<const uint32_t*>(s_act + a_base[tl] + bo + xo);  // 4-byte aligned
-            A[tl] = v4i{int(ap[0]), int(ap[1]), int(ap[2]), int(ap[3])};
+            const uint32_t* bp = reinterpret_cast<const uint32_t*>(s_act + r_base[tl] + bo + 260 + 8 * kg);
+            const uint32_t b0 = bp[0], b1 = bp[1];
+            Ab[tl] = h4{_Float16(int(int16_t(b0 & 0xFFFFu))), _Float16(int(int16_t(b0 >> 16))),
+                        _Float16(int(int16_t(b1 & 0xFFFFu))), _Float16(int(int16_t(b1 >> 16)))};
           }
 #pragma unroll
           for (int t = 0; t < NW; t++) {
-            // B: this lane's weight row over K group kg, as non-negative int8
-            v4i B;
-            int sc[SEG], mn[SEG];
-            if constexpr (SEG == 2) {
-              const u32x4 q = p[t].q[x];
-              const uint32_t qd[4] = {q.x, q.y, q.z, q.w};
+            int s0, m0, s1, m1;
+            q4k_scale_min(p[t].h, 2 * kg, s0, m0);
+            q4k_scale_min(p[t].h, 2 * kg + 1, s1, m1);
+            const h4 Bm = h4{_Float16(m0), _Float16(m0), _Float16(m1), _Float16(m1)};
+            const float dw = h2f(p[t].h.x), dm = h2f(p[t].h.x >> 16);
 #pragma unroll
-              for (int w = 0; w < 4; w++) B[w] = int((qd[w] >> nsh) & 0x0F0F0F0Fu);
+            for (int tl = 0; tl < NTA; tl++) {
+              const f4 Mn = __builtin_amdgcn_mfma_f32_16x16x16f16(Ab[tl], Bm, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+              // the block's float scales, once per (tensor, token): dx (d sum sc S - dmin sum m bsum)
 #pragma unroll
-              for (int sg = 0; sg < 2; sg++) q4k_scale_min(p[t].h, 2 * x + sg, sc[sg], mn[sg]);
-            } else {
+              for (int q = 0; q < LT; q++) {
+                const float dx = *reinterpret_cast<const float*>(s_act + e_base[tl][q] + bo);
+                const int T = (Ca[t][tl][q] << 3) + Cb[t][tl][q];
+                const float term = dx * (dw * float(T) - dm * Mn[q]);
+                acc[t][tl][q] += live ? term : 0.f;
+              }
+            }
+          }
+        } else {  // Q6_K: segment rows (token, group of 16) and the per-group scales in integers
+          int isum[NW][NT];  // the block's integer sums
+#pragma unroll
+          for (int x = 0; x < 4; x++) {
+            v4i A[NTA];
+#pragma unroll
+            for (int tl = 0; tl < NTA; tl++) {
+              const int xo = 128 * (x >> 1) + 16 * (x & 1);
+              const uint32_t* ap = reinterpret_cast<const uint32_t*>(s_act + a_base[tl] + bo + xo);  // 4-byte aligned
+              A[tl] = v4i{int(ap[0]), int(ap[1]), int(ap[2]), int(ap[3])};
+            }
+#pragma unroll
+            for (int t = 0; t < NW; t++) {
+              // B: this lane's weight row over K group kg, as non-negative int8
+              v4i B;
               const uint32_t xd[4] = {p[t].x[x].x, p[t].x[x].y, p[t].x[x].z, p[t].x[x].w};
               const uint32_t hd[4] = {p[t].qh[x].x, p[t].qh[x].y, p[t].qh[x].z, p[t].qh[x].w};
 #pragma unroll
               for (int w = 0; w < 4; w++)
-                B[w] = int(((xd[w] >> nsh) & 0x0F0F0F0Fu) |
-                           (__builtin_amdgcn_alignbit(hd[w], hd[w], qh_rot) & 0x30303030u));
+                B[w] = int(((xd[w] >> nsh) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(hd[w], hd[w], qh_rot) & 0x30303030u));
               const uint32_t scd[4] = {p[t].sc.x, p[t].sc.y, p[t].sc.z, p[t].sc.w};
+              int sc[4];
 #pragma unroll
               for (int g = 0; g < 4; g++) sc[g] = int(int8_t(scd[x] >> (8 * g)));
-            }
 #pragma unroll
-            for (int tl = 0; tl < NTA; tl++) {
-              const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tl], B, v4i{0, 0, 0, 0}, 0, 0, 0);
+              for (int tl = 0; tl < NTA; tl++) {
+                const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tl], B, v4i{0, 0, 0, 0}, 0, 0, 0);
+                int is = 0;  // the q6 offset of 32 is taken off once per block, below
 #pragma unroll
-              for (int q = 0; q < LT; q++) {
-                if constexpr (SEG == 2) {
-                  const int16_t* bs = reinterpret_cast<const int16_t*>(s_act + e_base[tl][q] + bo + 260);
-                  const int bsa = int(bs[4 * x]) + int(bs[4 * x + 1]), bsb = int(bs[4 * x + 2]) + int(bs[4 * x + 3]);
-                  // 24-bit products: |C| < 2^16 for a 32-weight sub-block, scales and mins < 64
-                  const int is = __mul24(sc[0], C[SEG * q]) + __mul24(sc[1], C[SEG * q + 1]);
-                  const int ms = __mul24(mn[0], bsa) + __mul24(mn[1], bsb);
-                  isum[t][tl][q] = x == 0 ? is : isum[t][tl][q] + is;
-                  msum[t][tl][q] = x == 0 ? ms : msum[t][tl][q] + ms;
-                } else {
-                  int is = 0;  // the q6 offset of 32 is taken off once per block, below
-#pragma unroll
-                  for (int g = 0; g < 4; g++) is += __mul24(sc[g], C[g]);  // |C| < 2^17
-                  isum[t][tl][q] = x == 0 ? is : isum[t][tl][q] + is;
-                }
+                for (int g = 0; g < 4; g++) is += __mul24(sc[g], C[g]);  // |C| < 2^17
+                isum[t][tl] = x == 0 ? is : isum[t][tl] + is;
               }
             }
           }
-        }
-        if constexpr (SEG == 4) {
-          typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-          typedef float f4 __attribute__((ext_vector_type(4)));
           const uint32_t* bp = reinterpret_cast<const uint32_t*>(s_act + fb_base + bo);
           h4 Ab;
 #pragma unroll
@@ -1150,26 +1206,20 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU, PT)) moe_mfma_kernel(
             h4 Bb;
 #pragma unroll
             for (int t4 = 0; t4 < 4; t4++) Bb[t4] = _Float16(int(int8_t(sdw >> (8 * t4))));
-            const f4 Cb = __builtin_amdgcn_mfma_f32_16x16x16f16(Ab, Bb, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            const f4 Cs = __builtin_amdgcn_mfma_f32_16x16x16f16(Ab, Bb, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-            for (int tl = 0; tl < NTA; tl++) isum[t][tl][0] -= 32 * int(Cb[tl]);
+            for (int tl = 0; tl < NTA; tl++) isum[t][tl] -= 32 * int(Cs[tl]);
           }
-        }
-        // the block's float scales, once per (tensor, token)
+          // the block's float scales, once per (tensor, token)
 #pragma unroll
-        for (int t = 0; t < NW; t++)
+          for (int t = 0; t < NW; t++)
 #pragma unroll
-          for (int tl = 0; tl < NTA; tl++)
-#pragma unroll
-            for (int q = 0; q < LT; q++) {
-              const float dx = *reinterpret_cast<const float*>(s_act + e_base[tl][q] + bo);
-              float term;
-              if constexpr (SEG == 2)
-                term = dx * (h2f(p[t].h.x) * float(isum[t][tl][q]) - h2f(p[t].h.x >> 16) * float(msum[t][tl][q]));
-              else
-                term = dx * (h2f(p[t].dw >> p[t].dsh) * float(isum[t][tl][q]));
-              acc[t][tl][q] += live ? term : 0.f;
+            for (int tl = 0; tl < NTA; tl++) {
+              const float dx = *reinterpret_cast<const float*>(s_act + e_base[tl][0] + bo);
+              const float term = dx * (h2f(p[t].dw >> p[t].dsh) * float(isum[t][tl]));
+              acc[t][tl][0] += live ? term : 0.f;
             }
+        }
         if (b == nb - 1) {  // the tile's last block: its results to LDS, accumulators reset
 #pragma unroll
           for (int tl = 0; tl < NTA; tl++)
@@ -1182,8 +1232,8 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU, PT)) moe_mfma_kernel(
               } else {
                 v = acc[0][tl][q];
               }
-              const int t_loc = tl * TPT + kg * LT + q;  // < PT
-              if (live) s_out[(tile * PT + t_loc) * 64 + 16 * wv + c] = v;
+              const int t_loc = tl * TPT + kg * LT + q;  // past PT: a plane-form tile's rows of no token
+              if (live && t_loc < PT) s_out[(tile * PT + t_loc) * 64 + 16 * wv + c] = v;
 #pragma unroll
               for (int t = 0; t < NW; t++) acc[t][tl][q] = 0.f;
             }

@@ -770,14 +770,16 @@ __global__ void __launch_bounds__(256) moe1_down_kernel(const uint8_t* __restric
 // Several tokens per expert: v_mfma_i32_16x16x64_i8 over one 64-weight unit at a time.  Lane l
 // supplies A row l % 16 and B column l % 16 (a weight row) over K [16 (l / 16), +16) and receives
 // C rows 4 (l / 16) .. +4 of column l % 16.  Two forms, both exact in integers per block:
-//   * Q4_K (plane form): the A rows are 16 tokens.  A lane's 16 weights of a unit lie in one
+//   * Q4_K in 16-token passes (plane form): the A rows are 16 tokens.  A lane's 16 weights of a unit lie in one
 //     sub-block, whose 6-bit scale splits as sc = 8a + b: the lane feeds the MFMA the planes
 //     a q4 and b q4 (<= 105), so 8 Ta + Tb over the block's four units is the block's sum of
 //     sc q4 q8 per (token, row), and the mins sum over the 16 bsums is one f16 MFMA.
-//   * Q6_K (segment form): a unit has 4 integer-scaled groups of 16.  The 16 A rows are (token,
-//     group) pairs, each holding its token's activations only in the K range of its group (zeros
-//     elsewhere), so one MFMA yields the exact integer sum of every group for 4 tokens; the group
-//     scales come from the lane's own weight row and are applied in-lane, in integers.
+//   * Q6_K, and Q4_K in 8-token passes (segment form): a unit has SEG integer-scaled segments
+//     (Q4_K: 2 sub-blocks of 32; Q6_K: 4 groups of 16).  The 16 A rows are (token, segment)
+//     pairs, each holding its token's activations only in the K range of its segment (zeros
+//     elsewhere), so one MFMA yields the exact integer sum of every segment for 16 / SEG tokens;
+//     the segment scales (and Q4_K mins) come from the lane's own weight row and are applied
+//     in-lane, in integers.
 // The block's float scales then apply once per block, dx * (d * isum - dmin * msum) as the
 // reference's block dot.  Activations are staged in LDS as Q8_K rows (rows of 16-byte multiples,
 // one more row of zeros for the A lanes outside their group).
@@ -935,7 +937,7 @@ constexpr int kStageBlocks = 8;  // f32 staging: 256-element blocks per wave in 
 // Workgroups per CU the register budget is cut for: three (168 VGPRs), except Q6_K gate/up, whose
 // two tensors' pieces need more registers than that without spilling, and the 16-token passes
 // (twice the accumulators) of Q6_K down: two.  (Q6_K gate/up takes no 16-token passes: they spill
-// at any budget.)  The Q4_K plane form holds one 16-token tile either way (160 VGPRs).
+// at any budget.)  Q4_K's 16-token passes take the plane form, one tile in 160 VGPRs.
 __host__ __device__ constexpr int mfma_min_wgs(int f, bool gu, int pt) {
   return mfma_seg(f) == 4 && (gu || pt > kMoePassTokens) ? 2 : 3;
 }
@@ -952,14 +954,15 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU, PT)) moe_mfma_kernel(
                                                        const uint8_t* __restrict__ xq, int64_t xq_rb,
                                                        const float* __restrict__ act_in, MoeLists lists,
                                                        float* __restrict__ out, int wg_per_expert, int ctr_off) {
-  // Q4_K: the plane form.  A rows are 16 tokens over the whole K range; a lane's B bytes lie in
-  // one sub-block, whose scale sc = 8a + b splits them into the exact int8 planes a q4 and b q4
-  // (<= 105), so two MFMAs per unit sum the scales in and T = 8 Ta + Tb is the block's integer
-  // sum of sc q4 q8 per (token, row); the mins sum over the 16 bsums is one f16 MFMA (exact:
-  // |bsum| <= 2032, m <= 63, sums below 2^24).  The VALU only expands the planes and applies the
-  // block's float scales.  Q6_K: the segment form (below).
+  // Q4_K in 16-token passes: the plane form.  A rows are 16 tokens over the whole K range; a
+  // lane's B bytes lie in one sub-block, whose scale sc = 8a + b splits them into the exact int8
+  // planes a q4 and b q4 (<= 105), so two MFMAs per unit sum the scales in and T = 8 Ta + Tb is
+  // the block's integer sum of sc q4 q8 per (token, row); the mins sum over the 16 bsums is one
+  // f16 MFMA (exact: |bsum| <= 2032, m <= 63, sums below 2^24).  The VALU only expands the planes
+  // and applies the block's float scales.  Q6_K, and Q4_K in 8-token passes (which would leave
+  // half of a 16-token tile empty): the segment form (below).
   constexpr int SEG = mfma_seg(F);
-  constexpr bool PLANE = SEG == 2;
+  constexpr bool PLANE = SEG == 2 && PT > kMoePassTokens;
   constexpr int TPT = PLANE ? 16 : 16 / SEG, NT = PLANE ? (PT + 15) / 16 : PT / TPT, LT = PLANE ? 4 : 4 / SEG;
   constexpr int NW = GU ? 2 : 1;  // weight tensors per wave
   using Piece = MfmaPiece<F>;
@@ -1161,14 +1164,14 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU, PT)) moe_mfma_kernel(
               }
             }
           }
-        } else {  // Q6_K: segment rows (token, group of 16) and the per-group scales in integers
-          int isum[NW][NT];  // the block's integer sums
+        } else {  // the segment form: (token, segment) rows, the segment scales in integers
+          int isum[NW][NT][LT], msum[NW][NT][LT];  // the block's integer sums (msum: Q4_K mins)
 #pragma unroll
           for (int x = 0; x < 4; x++) {
             v4i A[NTA];
 #pragma unroll
             for (int tl = 0; tl < NTA; tl++) {
-              const int xo = 128 * (x >> 1) + 16 * (x & 1);
+              const int xo = SEG == 2 ? 64 * x : 128 * (x >> 1) + 16 * (x & 1);
               const uint32_t* ap = reinterpret_cast<const uint32_t*>(s_act + a_base[tl] + bo + xo);  // 4-byte aligned
               A[tl] = v4i{int(ap[0]), int(ap[1]), int(ap[2]), int(ap[3])};
             }
@@ -1176,49 +1179,80 @@ __global__ void __launch_bounds__(256, mfma_min_wgs(F, GU, PT)) moe_mfma_kernel(
             for (int t = 0; t < NW; t++) {
               // B: this lane's weight row over K group kg, as non-negative int8
               v4i B;
-              const uint32_t xd[4] = {p[t].x[x].x, p[t].x[x].y, p[t].x[x].z, p[t].x[x].w};
-              const uint32_t hd[4] = {p[t].qh[x].x, p[t].qh[x].y, p[t].qh[x].z, p[t].qh[x].w};
+              int sc[SEG], mn[SEG];
+              if constexpr (SEG == 2) {
+                const u32x4 q = p[t].q[x];
+                const uint32_t qd[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-              for (int w = 0; w < 4; w++)
-                B[w] = int(((xd[w] >> nsh) & 0x0F0F0F0Fu) | (__builtin_amdgcn_alignbit(hd[w], hd[w], qh_rot) & 0x30303030u));
-              const uint32_t scd[4] = {p[t].sc.x, p[t].sc.y, p[t].sc.z, p[t].sc.w};
-              int sc[4];
+                for (int w = 0; w < 4; w++) B[w] = int((qd[w] >> nsh) & 0x0F0F0F0Fu);
 #pragma unroll
-              for (int g = 0; g < 4; g++) sc[g] = int(int8_t(scd[x] >> (8 * g)));
+                for (int sg = 0; sg < 2; sg++) q4k_scale_min(p[t].h, 2 * x + sg, sc[sg], mn[sg]);
+              } else {
+                const uint32_t xd[4] = {p[t].x[x].x, p[t].x[x].y, p[t].x[x].z, p[t].x[x].w};
+                const uint32_t hd[4] = {p[t].qh[x].x, p[t].qh[x].y, p[t].qh[x].z, p[t].qh[x].w};
+#pragma unroll
+                for (int w = 0; w < 4; w++)
+                  B[w] = int(((xd[w] >> nsh) & 0x0F0F0F0Fu) |
+                             (__builtin_amdgcn_alignbit(hd[w], hd[w], qh_rot) & 0x30303030u));
+                const uint32_t scd[4] = {p[t].sc.x, p[t].sc.y, p[t].sc.z, p[t].sc.w};
+#pragma unroll
+                for (int g = 0; g < 4; g++) sc[g] = int(int8_t(scd[x] >> (8 * g)));
+              }
 #pragma unroll
               for (int tl = 0; tl < NTA; tl++) {
                 const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tl], B, v4i{0, 0, 0, 0}, 0, 0, 0);
-                int is = 0;  // the q6 offset of 32 is taken off once per block, below
 #pragma unroll
-                for (int g = 0; g < 4; g++) is += __mul24(sc[g], C[g]);  // |C| < 2^17
-                isum[t][tl] = x == 0 ? is : isum[t][tl] + is;
+                for (int q = 0; q < LT; q++) {
+                  if constexpr (SEG == 2) {
+                    const int16_t* bs = reinterpret_cast<const int16_t*>(s_act + e_base[tl][q] + bo + 260);
+                    const int bsa = int(bs[4 * x]) + int(bs[4 * x + 1]), bsb = int(bs[4 * x + 2]) + int(bs[4 * x + 3]);
+                    // 24-bit products: |C| < 2^16 for a 32-weight sub-block, scales and mins < 64
+                    const int is = __mul24(sc[0], C[SEG * q]) + __mul24(sc[1], C[SEG * q + 1]);
+                    const int ms = __mul24(mn[0], bsa) + __mul24(mn[1], bsb);
+                    isum[t][tl][q] = x == 0 ? is : isum[t][tl][q] + is;
+                    msum[t][tl][q] = x == 0 ? ms : msum[t][tl][q] + ms;
+                  } else {
+                    int is = 0;  // the q6 offset of 32 is taken off once per block, below
+#pragma unroll
+                    for (int g = 0; g < 4; g++) is += __mul24(sc[g], C[g]);  // |C| < 2^17
+                    isum[t][tl][q] = x == 0 ? is : isum[t][tl][q] + is;
+                  }
+                }
               }
             }
           }
-          const uint32_t* bp = reinterpret_cast<const uint32_t*>(s_act + fb_base + bo);
-          h4 Ab;
+          if constexpr (SEG == 4) {
+            const uint32_t* bp = reinterpret_cast<const uint32_t*>(s_act + fb_base + bo);
+            h4 Ab;
 #pragma unroll
-          for (int t4 = 0; t4 < 4; t4++) Ab[t4] = _Float16(int(int16_t(bp[t4] >> fb_sh)));
+            for (int t4 = 0; t4 < 4; t4++) Ab[t4] = _Float16(int(int16_t(bp[t4] >> fb_sh)));
 #pragma unroll
-          for (int t = 0; t < NW; t++) {
-            pin(p[t].sc);  // in registers already: else the lane's pick becomes a load of its own
-            const uint32_t sdw = kg == 0 ? p[t].sc.x : kg == 1 ? p[t].sc.y : kg == 2 ? p[t].sc.z : p[t].sc.w;
-            h4 Bb;
+            for (int t = 0; t < NW; t++) {
+              pin(p[t].sc);  // in registers already: else the lane's pick becomes a load of its own
+              const uint32_t sdw = kg == 0 ? p[t].sc.x : kg == 1 ? p[t].sc.y : kg == 2 ? p[t].sc.z : p[t].sc.w;
+              h4 Bb;
 #pragma unroll
-            for (int t4 = 0; t4 < 4; t4++) Bb[t4] = _Float16(int(int8_t(sdw >> (8 * t4))));
-            const f4 Cs = __builtin_amdgcn_mfma_f32_16x16x16f16(Ab, Bb, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+              for (int t4 = 0; t4 < 4; t4++) Bb[t4] = _Float16(int(int8_t(sdw >> (8 * t4))));
+              const f4 Cb = __builtin_amdgcn_mfma_f32_16x16x16f16(Ab, Bb, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-            for (int tl = 0; tl < NTA; tl++) isum[t][tl] -= 32 * int(Cs[tl]);
+              for (int tl = 0; tl < NTA; tl++) isum[t][tl][0] -= 32 * int(Cb[tl]);
+            }
           }
           // the block's float scales, once per (tensor, token)
 #pragma unroll
           for (int t = 0; t < NW; t++)
 #pragma unroll
-            for (int tl = 0; tl < NTA; tl++) {
-              const float dx = *reinterpret_cast<const float*>(s_act + e_base[tl][0] + bo);
-              const float term = dx * (h2f(p[t].dw >> p[t].dsh) * float(isum[t][tl]));
-              acc[t][tl][0] += live ? term : 0.f;
-            }
+            for (int tl = 0; tl < NTA; tl++)
+#pragma unroll
+              for (int q = 0; q < LT; q++) {
+                const float dx = *reinterpret_cast<const float*>(s_act + e_base[tl][q] + bo);
+                float term;
+                if constexpr (SEG == 2)
+                  term = dx * (h2f(p[t].h.x) * float(isum[t][tl][q]) - h2f(p[t].h.x >> 16) * float(msum[t][tl][q]));
+                else
+                  term = dx * (h2f(p[t].dw >> p[t].dsh) * float(isum[t][tl][q]));
+                acc[t][tl][q] += live ? term : 0.f;
+              }
         }
         if (b == nb - 1) {  // the tile's last block: its results to LDS, accumulators reset
 #pragma unroll
